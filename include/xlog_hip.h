@@ -1,0 +1,219 @@
+/*
+ * xlog_hip.h — C ABI of the MI355X (gfx950) relational core for XLOG's
+ * semi-naive Datalog fixpoint.
+ *
+ * The entry points mirror the inherent methods of the reference's operator
+ * provider `xlog_cuda::CudaKernelProvider` (crates/xlog-cuda/src/provider/mod.rs:1139)
+ * that the runtime executor (crates/xlog-runtime/src/executor/) calls; each
+ * declaration cites the reference method it replaces.
+ *
+ * Conventions
+ *   - Relations are device-resident, u32 columns, arity 1..4.  They are opaque
+ *     handles owned by the library; operators borrow inputs (const) and return
+ *     new owned relations (reference: every provider op returns a fresh
+ *     CudaBuffer, e.g. relational.rs:2219, filter.rs:1927-1933).  Free with
+ *     xlog_hip_rel_free().
+ *   - Order is lexicographic over columns (col 0 most significant), unsigned per
+ *     column; equality is bytewise (kernels/dedup.cu:293-345,398-404).
+ *   - Every call returns an xlog_hip_status; on failure the message is
+ *     available from xlog_hip_last_error() (thread-local).  No exceptions
+ *     cross the ABI.  Errors fail closed like XlogError::Kernel.
+ *   - A context owns one HIP stream on one device.  Calls on one context are
+ *     stream-ordered; a context must not be used from two threads at once.
+ *   - Row counts are uint64_t: the reference's u32 row and 4 GiB column caps
+ *     (relational.rs:317-323,773-794,4550-4555) are lifted; results are equal
+ *     wherever the reference succeeds.
+ */
+#ifndef XLOG_HIP_H
+#define XLOG_HIP_H
+
+#include <stdint.h>
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    XLOG_HIP_OK = 0,
+    XLOG_HIP_INVALID_ARG = 1,
+    XLOG_HIP_TYPE_MISMATCH = 2,
+    XLOG_HIP_CAPACITY_OVERFLOW = 3,
+    XLOG_HIP_ITERATION_LIMIT = 4,
+    XLOG_HIP_OOM = 5,
+    XLOG_HIP_DEVICE_ERROR = 6,
+    XLOG_HIP_UNSUPPORTED = 7
+} xlog_hip_status;
+
+typedef struct xlog_hip_ctx xlog_hip_ctx;
+typedef struct xlog_hip_rel xlog_hip_rel;
+
+/* join kinds (reference JoinType, relational.rs:2926); only INNER is on the path */
+#define XLOG_HIP_JOIN_INNER 0
+#define XLOG_HIP_JOIN_SEMI 1
+#define XLOG_HIP_JOIN_ANTI 2
+
+/* ---- library / context ------------------------------------------------- */
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *xlog_hip_last_error(void);
+/* Library version string. */
+const char *xlog_hip_version(void);
+
+/* Create a context on `device` with its own stream
+ * (reference: CudaKernelProvider::new, provider/mod.rs:1139-1242). */
+xlog_hip_status xlog_hip_ctx_create(int device, xlog_hip_ctx **out);
+void xlog_hip_ctx_destroy(xlog_hip_ctx *ctx);
+/* Wait for all work of the context (reference: device().synchronize(), executor/mod.rs:1463). */
+xlog_hip_status xlog_hip_synchronize(xlog_hip_ctx *ctx);
+/* The context's hipStream_t, for callers that order their own work after it. */
+void *xlog_hip_stream(xlog_hip_ctx *ctx);
+/* Bytes held by live relations and scratch / peak (reference: memory().allocated_bytes(), memory.rs:57-148). */
+xlog_hip_status xlog_hip_memory_stats(xlog_hip_ctx *ctx, uint64_t *in_use, uint64_t *peak, uint64_t *cached);
+/* Return cached device blocks to the driver. */
+xlog_hip_status xlog_hip_trim(xlog_hip_ctx *ctx);
+
+/* ---- relations (CudaBuffer counterpart, memory.rs:1758-1930) ------------- */
+
+/* Empty relation of the given arity (reference: create_empty_buffer, provider/mod.rs:3018). */
+xlog_hip_status xlog_hip_rel_create_empty(xlog_hip_ctx *ctx, uint32_t arity, xlog_hip_rel **out);
+/* Upload host u32 columns (reference: create_buffer_from_slices, provider/io.rs:75). */
+xlog_hip_status xlog_hip_rel_from_host_columns(xlog_hip_ctx *ctx, const uint32_t *const *cols, uint32_t arity,
+                                               uint64_t rows, xlog_hip_rel **out);
+/* Copy device-resident u32 columns into a new relation (no host round trip). */
+xlog_hip_status xlog_hip_rel_from_device_columns(xlog_hip_ctx *ctx, const uint32_t *const *dev_cols,
+                                                 uint32_t arity, uint64_t rows, xlog_hip_rel **out);
+/* Upload host packed keys (arity 2: (c0 << 32) | c1; arity 1: c0). */
+xlog_hip_status xlog_hip_rel_from_host_packed(xlog_hip_ctx *ctx, const uint64_t *keys, uint32_t arity,
+                                              uint64_t rows, xlog_hip_rel **out);
+/* Download column `col` into host[0..rows) (reference: download_column::<u32>, provider/transfer.rs:22). */
+xlog_hip_status xlog_hip_rel_download_column(xlog_hip_ctx *ctx, const xlog_hip_rel *rel, uint32_t col,
+                                             uint32_t *host, uint64_t host_cap);
+/* Download packed keys of an arity<=2 relation into host[0..rows). */
+xlog_hip_status xlog_hip_rel_download_packed(xlog_hip_ctx *ctx, const xlog_hip_rel *rel, uint64_t *host,
+                                             uint64_t host_cap);
+/* Logical row count (reference: device_row_count, provider/mod.rs:2823-2830). */
+xlog_hip_status xlog_hip_rel_num_rows(const xlog_hip_rel *rel, uint64_t *rows);
+xlog_hip_status xlog_hip_rel_arity(const xlog_hip_rel *rel, uint32_t *arity);
+/* 1 if the relation is certified sorted by all columns and unique
+ * (reference: the canonical-set certificate, memory.rs:1771-1773). */
+xlog_hip_status xlog_hip_rel_is_canonical(const xlog_hip_rel *rel, int *canonical);
+/* Device pointer to the packed key words (word 0 or 1) of a relation, for zero-copy consumers. */
+xlog_hip_status xlog_hip_rel_device_words(const xlog_hip_rel *rel, uint32_t word, const uint64_t **dev);
+/* Deep copy (reference: clone_buffer, relational.rs:6113). */
+xlog_hip_status xlog_hip_rel_clone(xlog_hip_ctx *ctx, const xlog_hip_rel *in, xlog_hip_rel **out);
+void xlog_hip_rel_free(xlog_hip_rel *rel);
+
+/* ---- operators (CudaKernelProvider inherent methods) --------------------- */
+
+/* Stable sort by key columns, listed most significant first; rows with equal
+ * keys keep their input order (reference: sort, relational.rs:1881-2220). */
+xlog_hip_status xlog_hip_sort(xlog_hip_ctx *ctx, const xlog_hip_rel *in, const uint32_t *key_cols,
+                              uint32_t n_keys, xlog_hip_rel **out);
+/* Keep the first row of every group of rows equal on key_cols, output sorted
+ * by key_cols (reference: dedup, relational.rs:238-275). */
+xlog_hip_status xlog_hip_dedup(xlog_hip_ctx *ctx, const xlog_hip_rel *in, const uint32_t *key_cols,
+                               uint32_t n_keys, xlog_hip_rel **out);
+/* Full-row set: sort by every column, drop duplicate rows
+ * (reference: dedup_full_row / dedup_full_row_deterministic, relational.rs:1458,1558-1677). */
+xlog_hip_status xlog_hip_dedup_full_row(xlog_hip_ctx *ctx, const xlog_hip_rel *in, xlog_hip_rel **out);
+/* Set union, canonical output (reference: union_gpu, relational.rs:822-824). */
+xlog_hip_status xlog_hip_union(xlog_hip_ctx *ctx, const xlog_hip_rel *a, const xlog_hip_rel *b,
+                               xlog_hip_rel **out);
+/* Set union of many (reference: union_many_gpu, relational.rs:859-971). */
+xlog_hip_status xlog_hip_union_many(xlog_hip_ctx *ctx, const xlog_hip_rel *const *ins, uint32_t n_ins,
+                                    xlog_hip_rel **out);
+/* Set difference dedup(a) \ b, canonical output
+ * (reference: diff_gpu / diff_full_row, relational.rs:1102-1147,1489). */
+xlog_hip_status xlog_hip_diff(xlog_hip_ctx *ctx, const xlog_hip_rel *a, const xlog_hip_rel *b,
+                              xlog_hip_rel **out);
+/* Equi-join on one key column per side.  INNER output = left columns ++
+ * right columns (arity_l + arity_r <= 4), one row per matching pair, row
+ * order unspecified (reference: hash_join_v2, relational.rs:2926-2992,4417-4625).
+ * SEMI / ANTI output the left rows with / without a match. */
+xlog_hip_status xlog_hip_hash_join(xlog_hip_ctx *ctx, const xlog_hip_rel *left, const xlog_hip_rel *right,
+                                   uint32_t left_key, uint32_t right_key, int join_type, xlog_hip_rel **out);
+/* Inner join on one u32 key column, left ++ right columns, for inputs sorted
+ * on their key (reference: sort_merge_join_v2_inner_u32_1key, relational.rs:3401-3728). */
+xlog_hip_status xlog_hip_sort_merge_join(xlog_hip_ctx *ctx, const xlog_hip_rel *left, const xlog_hip_rel *right,
+                                         uint32_t left_key, uint32_t right_key, xlog_hip_rel **out);
+/* Fused join + projection: ChainJoin = Project(Join) (crates/xlog-logic/src/promote.rs:1020-1060,
+ * expression.rs:779-834).  out_cols index the concatenated row (left ++ right);
+ * the output has n_out (1 or 2) columns, bag semantics. */
+xlog_hip_status xlog_hip_join_project(xlog_hip_ctx *ctx, const xlog_hip_rel *left, const xlog_hip_rel *right,
+                                      uint32_t left_key, uint32_t right_key, const uint32_t *out_cols,
+                                      uint32_t n_out, xlog_hip_rel **out);
+/* Column projection, bag semantics (reference: extract_column + combine_columns,
+ * relational.rs:6196, provider/arithmetic.rs:1056). */
+xlog_hip_status xlog_hip_project(xlog_hip_ctx *ctx, const xlog_hip_rel *in, const uint32_t *cols, uint32_t n_cols,
+                                 xlog_hip_rel **out);
+/* Non-decreasing check of one column (reference: is_sorted_ascending_u32, relational.rs:3258). */
+xlog_hip_status xlog_hip_is_sorted(xlog_hip_ctx *ctx, const xlog_hip_rel *rel, uint32_t col, int *sorted);
+/* In-place exclusive scan of a device u32 array; *total receives the sum
+ * (reference: exclusive_scan_u32_inplace, provider/mod.rs:2177). */
+xlog_hip_status xlog_hip_exclusive_scan_u32(xlog_hip_ctx *ctx, uint32_t *dev, uint64_t n, uint64_t *total);
+/* Keep rows whose device u8 mask is non-zero, input order
+ * (reference: compact_buffer_by_device_mask_device_count, provider/filter.rs:1820-1935). */
+xlog_hip_status xlog_hip_compact(xlog_hip_ctx *ctx, const xlog_hip_rel *in, const uint8_t *dev_mask,
+                                 xlog_hip_rel **out);
+
+/* ---- fixpoint driver (Executor::execute_recursive_scc, recursive.rs:447-957) ---- */
+
+/* Program plan: int32 array
+ *   [n_rules, then per rule: head_pred, hv0, hv1, n_body, (pred, v0, v1) * n_body]
+ * over arity-2 predicates 0..n_preds-1; variables are small ints.  Bodies are
+ * chains: each atom after the first shares exactly one variable with the
+ * running binding, which keeps at most two live variables
+ * (left-deep lowering, crates/xlog-logic/src/lower.rs:1795-1850).
+ * rels[p] supplies every predicate (EDB facts; IDB initial contents, may be
+ * empty).  On success out[p] receives a new canonical relation for every IDB
+ * predicate (NULL for EDB ones). */
+typedef struct {
+    uint64_t iterations;      /* loop iterations incl. the final empty one (recursive.rs:619-620,860-865) */
+    uint64_t max_iterations;  /* limit; 0 = 1,000,000 (config.rs:164) */
+    uint64_t *delta_sizes;    /* optional: [0] seed delta, [k] total |delta| after iteration k */
+    uint64_t delta_cap;       /* entries available in delta_sizes */
+    uint64_t route;           /* XLOG_HIP_ROUTE_* used for linear chain rules (in: request, out: taken) */
+    double wall_ms;           /* device wall time of the fixpoint */
+} xlog_hip_fixpoint_stats;
+
+#define XLOG_HIP_ROUTE_AUTO 0
+#define XLOG_HIP_ROUTE_JOIN 1   /* join -> sort -> dedup -> diff -> merge */
+#define XLOG_HIP_ROUTE_BITMAP 2 /* dense factorized delta (fj_delta, provider/fj_delta.rs:117) */
+
+xlog_hip_status xlog_hip_fixpoint(xlog_hip_ctx *ctx, const int32_t *plan, uint32_t n_preds,
+                                  const xlog_hip_rel *const *rels, xlog_hip_rel **out,
+                                  xlog_hip_fixpoint_stats *stats);
+
+/* Transitive closure reach(X,Y) :- edge(X,Y). reach(X,Z) :- reach(X,Y), edge(Y,Z).
+ * Convenience over xlog_hip_fixpoint with the TC plan. */
+xlog_hip_status xlog_hip_fixpoint_tc(xlog_hip_ctx *ctx, const xlog_hip_rel *edge, xlog_hip_rel **reach,
+                                     xlog_hip_fixpoint_stats *stats);
+
+/* ---- kernel timing (diagnostics; no counterpart in the reference) ---------
+ * With profiling enabled every launch of the listed kernel kinds is bracketed
+ * by HIP events on the context stream.  profile_read synchronises and returns
+ * the number of launches, their summed duration and summed algorithmic bytes
+ * (the compulsory HBM bytes of the operation, e.g. 16 B per key per radix pass). */
+#define XLOG_HIP_KERNEL_SORT_PASS 0   /* onesweep digit pass */
+#define XLOG_HIP_KERNEL_SORT_HIST 1   /* 8-digit histogram */
+#define XLOG_HIP_KERNEL_SELECT 2      /* dedup / diff / compaction */
+#define XLOG_HIP_KERNEL_MERGE 3       /* merge-path merge */
+#define XLOG_HIP_KERNEL_PROBE_COUNT 4 /* join probe, count pass */
+#define XLOG_HIP_KERNEL_PROBE_EMIT 5  /* join probe, materialise pass */
+#define XLOG_HIP_KERNEL_TC_STEP 6     /* dense TC iteration */
+#define XLOG_HIP_KERNEL_TC_EMIT 7     /* dense TC final emit */
+#define XLOG_HIP_KERNEL_KINDS 8
+xlog_hip_status xlog_hip_profile_enable(xlog_hip_ctx *ctx, int on);
+xlog_hip_status xlog_hip_profile_reset(xlog_hip_ctx *ctx);
+xlog_hip_status xlog_hip_profile_read(xlog_hip_ctx *ctx, uint32_t kind, uint64_t *launches, double *total_ms,
+                                      double *algo_bytes);
+
+/* FNV-1a-64 over the little-endian bytes of the packed keys in row order
+ * (offset / prime as kernels/pack.cu:8-9); host-side, downloads the relation. */
+xlog_hip_status xlog_hip_rel_digest(xlog_hip_ctx *ctx, const xlog_hip_rel *rel, uint64_t *digest);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* XLOG_HIP_H */

@@ -1,0 +1,1467 @@
+// C ABI of libxlog_hip: context, relation handles, operators and the
+// semi-naive fixpoint driver.  Host code; the kernels live in sort.hip,
+// select.hip, join.hip and tc_bitmap.hip.
+#include "internal.hpp"
+
+#include <algorithm>
+#include <chrono>
+#include <cstring>
+#include <memory>
+
+namespace xh {
+
+// ---------------------------------------------------------------------------
+// errors
+// ---------------------------------------------------------------------------
+static thread_local std::string g_last_error;
+void set_error(const std::string &msg) { g_last_error = msg; }
+
+template <class F>
+static xlog_hip_status guarded(F &&f) {
+    try {
+        f();
+        g_last_error.clear();
+        return XLOG_HIP_OK;
+    } catch (const Error &e) {
+        g_last_error = e.msg;
+        return e.code;
+    } catch (const std::bad_alloc &) {
+        g_last_error = "host allocation failed";
+        return XLOG_HIP_OOM;
+    } catch (const std::exception &e) {
+        g_last_error = e.what();
+        return XLOG_HIP_DEVICE_ERROR;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// pool
+// ---------------------------------------------------------------------------
+size_t Pool::round_up(size_t b) {
+    if (b < 256) return 256;
+    // four size classes per power of two
+    int lg = 63 - __builtin_clzll(b);
+    size_t q = (lg >= 2) ? (size_t)1 << (lg - 2) : 1;
+    return (b + q - 1) / q * q;
+}
+void *Pool::alloc(size_t bytes) {
+    size_t sz = round_up(bytes);
+    auto it = free_.find(sz);
+    void *p = nullptr;
+    if (it != free_.end()) {
+        p = it->second;
+        free_.erase(it);
+        cached_ -= sz;
+    } else {
+        hipError_t e = hipMalloc(&p, sz);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            trim();
+            e = hipMalloc(&p, sz);
+            if (e != hipSuccess) {
+                (void)hipGetLastError();
+                throw Error{XLOG_HIP_OOM, "device allocation of " + std::to_string(sz) + " bytes failed"};
+            }
+        }
+    }
+    live_[p] = sz;
+    in_use_ += sz;
+    if (in_use_ > peak_) peak_ = in_use_;
+    return p;
+}
+void Pool::free(void *p) {
+    if (!p) return;
+    auto it = live_.find(p);
+    if (it == live_.end()) return;
+    size_t sz = it->second;
+    live_.erase(it);
+    in_use_ -= sz;
+    free_.emplace(sz, p);
+    cached_ += sz;
+}
+void Pool::trim() {
+    (void)hipDeviceSynchronize();
+    for (auto &kv : free_) (void)hipFree(kv.second);
+    free_.clear();
+    cached_ = 0;
+}
+Pool::~Pool() {
+    (void)hipDeviceSynchronize();
+    for (auto &kv : free_) (void)hipFree(kv.second);
+    for (auto &kv : live_) (void)hipFree(kv.first);
+}
+
+void Ctx::read_scalars(const void *dev, size_t count_u64) {
+    XH_CHECK_HIP(hipMemcpyAsync(host_scalars, dev, count_u64 * sizeof(uint64_t), hipMemcpyDeviceToHost, stream));
+    sync();
+}
+
+// ---------------------------------------------------------------------------
+// small kernels used only by the host layer
+// ---------------------------------------------------------------------------
+namespace {
+
+__global__ void k_widen(const uint32_t *__restrict__ c0, uint64_t n, uint64_t *__restrict__ out) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) out[i] = c0[i];
+}
+
+// value of column c (0..arity-1) of row i
+__device__ __forceinline__ uint32_t col_value(const uint64_t *w0, const uint64_t *w1, int arity, int c, uint64_t i) {
+    if (arity == 1) return (uint32_t)w0[i];
+    if (c == 0) return (uint32_t)(w0[i] >> 32);
+    if (c == 1) return (uint32_t)w0[i];
+    if (c == 2) return (uint32_t)(w1[i] >> 32);
+    return (uint32_t)w1[i];
+}
+
+struct ProjSpec {
+    int in_arity, out_arity;
+    int cols[4];
+};
+__global__ void k_project(const uint64_t *__restrict__ w0, const uint64_t *__restrict__ w1, uint64_t n, ProjSpec s,
+                          uint64_t *__restrict__ o0, uint64_t *__restrict__ o1) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        uint32_t v[4] = {0, 0, 0, 0};
+        for (int j = 0; j < s.out_arity; ++j) v[j] = col_value(w0, w1, s.in_arity, s.cols[j], i);
+        if (s.out_arity == 1) {
+            o0[i] = v[0];
+        } else {
+            o0[i] = ((uint64_t)v[0] << 32) | v[1];
+            if (s.out_arity == 3) o1[i] = (uint64_t)v[2] << 32;
+            if (s.out_arity == 4) o1[i] = ((uint64_t)v[2] << 32) | v[3];
+        }
+    }
+}
+
+__global__ void k_col_to_key(const uint64_t *__restrict__ w0, const uint64_t *__restrict__ w1, int arity, int c,
+                             const uint32_t *__restrict__ perm, uint64_t n, uint64_t *__restrict__ key) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        uint64_t r = perm ? perm[i] : i;
+        key[i] = (uint64_t)col_value(w0, w1, arity, c, r) << 32;
+    }
+}
+__global__ void k_iota(uint32_t *p, uint64_t n) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = (uint32_t)i;
+}
+__global__ void k_gather(const uint64_t *__restrict__ in, const uint32_t *__restrict__ perm, uint64_t n,
+                         uint64_t *__restrict__ out) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) out[i] = in[perm[i]];
+}
+// group-start flags over sorted rows for the given key columns
+__global__ void k_group_flags(const uint64_t *__restrict__ w0, const uint64_t *__restrict__ w1, int arity,
+                              ProjSpec keys, uint64_t n, uint8_t *__restrict__ flags) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        bool f = (i == 0);
+        if (!f)
+            for (int j = 0; j < keys.out_arity; ++j)
+                if (col_value(w0, w1, arity, keys.cols[j], i) != col_value(w0, w1, arity, keys.cols[j], i - 1)) f = true;
+        flags[i] = f;
+    }
+}
+__global__ void k_col_unsorted(const uint64_t *__restrict__ w0, const uint64_t *__restrict__ w1, int arity, int c,
+                               uint64_t n, uint32_t *flag) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i + 1 < n; i += stride)
+        if (col_value(w0, w1, arity, c, i) > col_value(w0, w1, arity, c, i + 1)) *flag = 1u;
+}
+__global__ void k_max_u32_of_packed(const uint64_t *__restrict__ k, uint64_t n, unsigned int *mx) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    unsigned int m = 0;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        uint64_t x = k[i];
+        unsigned a = (unsigned)(x >> 32), b = (unsigned)x;
+        m = max(m, max(a, b));
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = max(m, (unsigned)__shfl_xor((int)m, o, 64));
+    if ((threadIdx.x & 63) == 0) atomicMax(mx, m);
+}
+__global__ void k_u32_to_u64(const uint32_t *__restrict__ in, uint64_t n, uint64_t *__restrict__ out) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) out[i] = in[i];
+}
+__global__ void k_u64_to_u32(const uint64_t *__restrict__ in, uint64_t n, uint32_t *__restrict__ out) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) out[i] = (uint32_t)in[i];
+}
+
+}  // namespace
+
+// defined in join.hip / tc_bitmap.hip
+uint64_t join_probe_general(Ctx *ctx, const uint64_t *probe, uint64_t n, int pcol, const RunIndex &ix,
+                            const uint32_t *payload, int out_arity, const int oc[4], uint64_t **out0,
+                            uint64_t **out1);
+void join_match_flags(Ctx *ctx, const uint64_t *probe, uint64_t n, int pcol, const RunIndex &ix, int want,
+                      uint8_t *flags);
+void scan_u64_small(Ctx *ctx, uint64_t *a, uint64_t n, uint64_t *total);
+void tc_bitmap(Ctx *ctx, const uint64_t *edges, uint64_t m, uint32_t nv, uint64_t max_iter, uint64_t **out,
+               uint64_t *out_n, uint64_t *iterations, std::vector<uint64_t> &deltas);
+
+#define LAUNCH_1D(kern, n, ...)                                                                             \
+    do {                                                                                                    \
+        if ((n) > 0) {                                                                                      \
+            hipLaunchKernelGGL(kern, dim3(grid_for((n), 256, 16384)), dim3(256), 0, ctx->stream, __VA_ARGS__); \
+            XH_CHECK_HIP(hipGetLastError());                                                                \
+        }                                                                                                   \
+    } while (0)
+
+// ---------------------------------------------------------------------------
+// relations
+// ---------------------------------------------------------------------------
+xlog_hip_rel *rel_new(Ctx *ctx, uint32_t arity, uint64_t cap) {
+    XH_REQUIRE(arity >= 1 && arity <= 4, XLOG_HIP_INVALID_ARG, "relation arity must be 1..4");
+    std::unique_ptr<xlog_hip_rel> r(new xlog_hip_rel());
+    r->ctx = ctx;
+    r->arity = arity;
+    r->cap = cap;
+    if (cap) {
+        r->w[0] = static_cast<uint64_t *>(ctx->alloc(cap * sizeof(uint64_t)));
+        if (arity > 2) r->w[1] = static_cast<uint64_t *>(ctx->alloc(cap * sizeof(uint64_t)));
+    }
+    return r.release();
+}
+void rel_free(xlog_hip_rel *r) {
+    if (!r) return;
+    if (r->ctx) {
+        r->ctx->free(r->w[0]);
+        r->ctx->free(r->w[1]);
+    }
+    delete r;
+}
+// adopt device buffers (ownership moves to the relation)
+static xlog_hip_rel *rel_adopt(Ctx *ctx, uint32_t arity, uint64_t rows, uint64_t *w0, uint64_t *w1, uint32_t flags) {
+    xlog_hip_rel *r = new xlog_hip_rel();
+    r->ctx = ctx;
+    r->arity = arity;
+    r->rows = rows;
+    r->cap = rows;
+    r->w[0] = w0;
+    r->w[1] = w1;
+    r->flags = flags;
+    return r;
+}
+static void copy_d2d(Ctx *ctx, uint64_t *dst, const uint64_t *src, uint64_t n) {
+    if (n) XH_CHECK_HIP(hipMemcpyAsync(dst, src, n * sizeof(uint64_t), hipMemcpyDeviceToDevice, ctx->stream));
+}
+static xlog_hip_rel *rel_clone(Ctx *ctx, const xlog_hip_rel *in) {
+    xlog_hip_rel *r = rel_new(ctx, in->arity, in->rows);
+    r->rows = in->rows;
+    r->flags = in->flags;
+    copy_d2d(ctx, r->w[0], in->w[0], in->rows);
+    if (in->arity > 2) copy_d2d(ctx, r->w[1], in->w[1], in->rows);
+    return r;
+}
+
+static uint64_t read_count(Ctx *ctx, const uint64_t *d) {
+    ctx->read_scalars(d, 1);
+    return ctx->host_scalars[0];
+}
+
+// ---------------------------------------------------------------------------
+// sorting helpers
+// ---------------------------------------------------------------------------
+
+// Sort a u64 key array of any length; the result is returned in a buffer
+// owned by the caller (either `keys` itself or a new one).
+static uint64_t *sort_keys(Ctx *ctx, uint64_t *keys, uint64_t n, bool keys_owned, int *passes = nullptr) {
+    if (n < 2) {
+        if (keys_owned || n == 0) return keys;
+        uint64_t *c = static_cast<uint64_t *>(ctx->alloc(n * sizeof(uint64_t)));
+        copy_d2d(ctx, c, keys, n);
+        return c;
+    }
+    const uint64_t CHUNK = 1ull << 29;
+    if (n < (1ull << 30)) {
+        uint64_t *a = keys;
+        if (!keys_owned) {
+            a = static_cast<uint64_t *>(ctx->alloc(n * sizeof(uint64_t)));
+            copy_d2d(ctx, a, keys, n);
+        }
+        uint64_t *b = static_cast<uint64_t *>(ctx->alloc(n * sizeof(uint64_t)));
+        uint32_t *v0 = nullptr, *v1 = nullptr;
+        int p = radix_sort_u64(ctx, &a, &b, &v0, &v1, n);
+        if (passes) *passes = p;
+        ctx->free(b);
+        return a;
+    }
+    // chunked: sort pieces of 2^29 then merge pairwise
+    uint64_t *a = keys;
+    if (!keys_owned) {
+        a = static_cast<uint64_t *>(ctx->alloc(n * sizeof(uint64_t)));
+        copy_d2d(ctx, a, keys, n);
+    }
+    uint64_t *b = static_cast<uint64_t *>(ctx->alloc(n * sizeof(uint64_t)));
+    std::vector<std::pair<uint64_t, uint64_t>> runs;
+    for (uint64_t s = 0; s < n; s += CHUNK) {
+        uint64_t len = std::min(CHUNK, n - s);
+        uint64_t *ka = a + s, *kb = b + s;
+        uint32_t *v0 = nullptr, *v1 = nullptr;
+        radix_sort_u64(ctx, &ka, &kb, &v0, &v1, len);
+        if (ka != a + s) copy_d2d(ctx, a + s, ka, len);
+        runs.push_back({s, len});
+    }
+    uint64_t *src = a, *dst = b;
+    while (runs.size() > 1) {
+        std::vector<std::pair<uint64_t, uint64_t>> next;
+        for (size_t i = 0; i < runs.size(); i += 2) {
+            if (i + 1 < runs.size()) {
+                merge_sorted(ctx, src + runs[i].first, runs[i].second, src + runs[i + 1].first, runs[i + 1].second,
+                             dst + runs[i].first);
+                next.push_back({runs[i].first, runs[i].second + runs[i + 1].second});
+            } else {
+                copy_d2d(ctx, dst + runs[i].first, src + runs[i].first, runs[i].second);
+                next.push_back(runs[i]);
+            }
+        }
+        runs.swap(next);
+        std::swap(src, dst);
+    }
+    ctx->free(dst);
+    return src;
+}
+
+// sorted (any) keys -> unique keys in a new buffer; returns count
+static uint64_t unique_keys(Ctx *ctx, const uint64_t *sorted, uint64_t n, uint64_t **out) {
+    uint64_t *o = static_cast<uint64_t *>(ctx->alloc((n ? n : 1) * sizeof(uint64_t)));
+    Buf<uint64_t> cnt(ctx, 1);
+    select_unique(ctx, sorted, n, o, cnt.p);
+    *out = o;
+    return read_count(ctx, cnt.p);
+}
+
+// Canonical (sorted, unique) copy of the packed keys of an arity<=2 relation
+// or the relation's own buffer when it is already canonical (borrowed = true).
+struct Canon {
+    Ctx *ctx = nullptr;
+    const uint64_t *k = nullptr;
+    uint64_t n = 0;
+    uint64_t *owned = nullptr;
+    ~Canon() { if (owned && ctx) ctx->free(owned); }
+};
+static void canonical_keys(Ctx *ctx, const xlog_hip_rel *r, Canon &c) {
+    c.ctx = ctx;
+    if (r->flags & REL_CANONICAL) {
+        c.k = r->w[0];
+        c.n = r->rows;
+        return;
+    }
+    uint64_t *s = sort_keys(ctx, r->w[0], r->rows, false);
+    uint64_t *u;
+    c.n = unique_keys(ctx, s, r->rows, &u);
+    if (s != r->w[0]) ctx->free(s);
+    c.owned = u;
+    c.k = u;
+}
+
+// Stable permutation sorting rows of any arity by key_cols (most significant
+// first): LSD over the key columns, one stable 32-bit radix sort per column.
+static uint32_t *sort_perm(Ctx *ctx, const xlog_hip_rel *in, const std::vector<int> &cols) {
+    uint64_t n = in->rows;
+    XH_REQUIRE(n < (1ull << 30), XLOG_HIP_CAPACITY_OVERFLOW, "sort: keyed sort limited to 2^30 rows");
+    uint32_t *perm = static_cast<uint32_t *>(ctx->alloc(n * sizeof(uint32_t)));
+    uint32_t *perm2 = static_cast<uint32_t *>(ctx->alloc(n * sizeof(uint32_t)));
+    uint64_t *k0 = static_cast<uint64_t *>(ctx->alloc(n * sizeof(uint64_t)));
+    uint64_t *k1 = static_cast<uint64_t *>(ctx->alloc(n * sizeof(uint64_t)));
+    LAUNCH_1D(k_iota, n, perm, n);
+    for (int i = (int)cols.size() - 1; i >= 0; --i) {
+        LAUNCH_1D(k_col_to_key, n, in->w[0], in->w[1], (int)in->arity, cols[i], perm, n, k0);
+        uint64_t *ka = k0, *kb = k1;
+        uint32_t *va = perm, *vb = perm2;
+        radix_sort_u64(ctx, &ka, &kb, &va, &vb, n);
+        k0 = ka; k1 = kb;
+        perm = va; perm2 = vb;
+    }
+    ctx->free(perm2);
+    ctx->free(k0);
+    ctx->free(k1);
+    return perm;
+}
+
+static xlog_hip_rel *gather_rel(Ctx *ctx, const xlog_hip_rel *in, const uint32_t *perm) {
+    xlog_hip_rel *r = rel_new(ctx, in->arity, in->rows);
+    r->rows = in->rows;
+    uint64_t n = in->rows;
+    LAUNCH_1D(k_gather, n, in->w[0], perm, n, r->w[0]);
+    if (in->arity > 2) LAUNCH_1D(k_gather, n, in->w[1], perm, n, r->w[1]);
+    return r;
+}
+
+static bool is_full_key(const xlog_hip_rel *in, const std::vector<int> &cols) {
+    std::vector<int> uniq;
+    for (int c : cols)
+        if (std::find(uniq.begin(), uniq.end(), c) == uniq.end()) uniq.push_back(c);
+    if (uniq.size() != in->arity) return false;
+    for (size_t i = 0; i < uniq.size(); ++i)
+        if (uniq[i] != (int)i) return false;
+    return true;
+}
+
+static std::vector<int> check_cols(const xlog_hip_rel *in, const uint32_t *cols, uint32_t n) {
+    XH_REQUIRE(n == 0 || cols, XLOG_HIP_INVALID_ARG, "key column list is NULL");
+    std::vector<int> v;
+    for (uint32_t i = 0; i < n; ++i) {
+        XH_REQUIRE(cols[i] < in->arity, XLOG_HIP_INVALID_ARG,
+                   "key column " + std::to_string(cols[i]) + " out of range for arity " + std::to_string(in->arity));
+        v.push_back((int)cols[i]);
+    }
+    return v;
+}
+
+static xlog_hip_rel *op_sort(Ctx *ctx, const xlog_hip_rel *in, const std::vector<int> &cols) {
+    if (in->rows < 2 || cols.empty()) return rel_clone(ctx, in);
+    if (in->arity <= 2 && is_full_key(in, cols)) {
+        if (in->flags & REL_CANONICAL) return rel_clone(ctx, in);
+        uint64_t *s = sort_keys(ctx, in->w[0], in->rows, false);
+        return rel_adopt(ctx, in->arity, in->rows, s, nullptr, 0);
+    }
+    uint32_t *perm = sort_perm(ctx, in, cols);
+    xlog_hip_rel *r = gather_rel(ctx, in, perm);
+    ctx->free(perm);
+    return r;
+}
+
+static xlog_hip_rel *compact_rel(Ctx *ctx, const xlog_hip_rel *in, const uint8_t *flags) {
+    Buf<uint64_t> cnt(ctx, 1);
+    uint64_t *o0 = static_cast<uint64_t *>(ctx->alloc((in->rows ? in->rows : 1) * sizeof(uint64_t)));
+    select_flags(ctx, in->w[0], flags, in->rows, o0, cnt.p);
+    uint64_t *o1 = nullptr;
+    if (in->arity > 2) {
+        o1 = static_cast<uint64_t *>(ctx->alloc((in->rows ? in->rows : 1) * sizeof(uint64_t)));
+        Buf<uint64_t> cnt2(ctx, 1);
+        select_flags(ctx, in->w[1], flags, in->rows, o1, cnt2.p);
+    }
+    uint64_t n = read_count(ctx, cnt.p);
+    return rel_adopt(ctx, in->arity, n, o0, o1, 0);
+}
+
+static xlog_hip_rel *op_dedup_full(Ctx *ctx, const xlog_hip_rel *in) {
+    if (in->flags & REL_CANONICAL) return rel_clone(ctx, in);
+    if (in->arity <= 2) {
+        uint64_t *s = sort_keys(ctx, in->w[0], in->rows, false);
+        uint64_t *u;
+        uint64_t n = unique_keys(ctx, s, in->rows, &u);
+        if (s != in->w[0]) ctx->free(s);
+        return rel_adopt(ctx, in->arity, n, u, nullptr, REL_CANONICAL);
+    }
+    std::vector<int> all;
+    for (uint32_t c = 0; c < in->arity; ++c) all.push_back((int)c);
+    xlog_hip_rel *s = op_sort(ctx, in, all);
+    Buf<uint8_t> flags(ctx, s->rows ? s->rows : 1);
+    ProjSpec ks{(int)s->arity, (int)s->arity, {0, 1, 2, 3}};
+    LAUNCH_1D(k_group_flags, s->rows, s->w[0], s->w[1], (int)s->arity, ks, s->rows, flags.p);
+    xlog_hip_rel *r = compact_rel(ctx, s, flags.p);
+    rel_free(s);
+    r->flags = REL_CANONICAL;
+    return r;
+}
+
+static xlog_hip_rel *op_dedup(Ctx *ctx, const xlog_hip_rel *in, const std::vector<int> &cols) {
+    if (is_full_key(in, cols)) return op_dedup_full(ctx, in);
+    XH_REQUIRE(!cols.empty(), XLOG_HIP_INVALID_ARG, "dedup needs at least one key column");
+    xlog_hip_rel *s = op_sort(ctx, in, cols);
+    Buf<uint8_t> flags(ctx, s->rows ? s->rows : 1);
+    ProjSpec ks{(int)s->arity, (int)std::min<size_t>(cols.size(), 4), {0, 0, 0, 0}};
+    for (int j = 0; j < ks.out_arity; ++j) ks.cols[j] = cols[j];
+    LAUNCH_1D(k_group_flags, s->rows, s->w[0], s->w[1], (int)s->arity, ks, s->rows, flags.p);
+    xlog_hip_rel *r = compact_rel(ctx, s, flags.p);
+    rel_free(s);
+    return r;
+}
+
+static xlog_hip_rel *op_union_many(Ctx *ctx, const xlog_hip_rel *const *ins, uint32_t n) {
+    XH_REQUIRE(n >= 1 && ins, XLOG_HIP_INVALID_ARG, "union needs at least one input");
+    uint32_t arity = ins[0]->arity;
+    uint64_t total = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+        XH_REQUIRE(ins[i], XLOG_HIP_INVALID_ARG, "union input is NULL");
+        XH_REQUIRE(ins[i]->arity == arity, XLOG_HIP_TYPE_MISMATCH, "union inputs have different arity");
+        total += ins[i]->rows;
+    }
+    if (arity <= 2 && n == 2 && (ins[0]->flags & ins[1]->flags & REL_CANONICAL)) {
+        uint64_t *m = static_cast<uint64_t *>(ctx->alloc((total ? total : 1) * sizeof(uint64_t)));
+        merge_sorted(ctx, ins[0]->w[0], ins[0]->rows, ins[1]->w[0], ins[1]->rows, m);
+        uint64_t *u;
+        uint64_t cnt = unique_keys(ctx, m, total, &u);
+        ctx->free(m);
+        return rel_adopt(ctx, arity, cnt, u, nullptr, REL_CANONICAL);
+    }
+    xlog_hip_rel *cat = rel_new(ctx, arity, total);
+    cat->rows = total;
+    uint64_t off = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+        copy_d2d(ctx, cat->w[0] + off, ins[i]->w[0], ins[i]->rows);
+        if (arity > 2) copy_d2d(ctx, cat->w[1] + off, ins[i]->w[1], ins[i]->rows);
+        off += ins[i]->rows;
+    }
+    xlog_hip_rel *r = op_dedup_full(ctx, cat);
+    rel_free(cat);
+    return r;
+}
+
+static xlog_hip_rel *op_diff(Ctx *ctx, const xlog_hip_rel *a, const xlog_hip_rel *b) {
+    XH_REQUIRE(a->arity == b->arity, XLOG_HIP_TYPE_MISMATCH, "diff inputs have different arity");
+    XH_REQUIRE(a->arity <= 2, XLOG_HIP_UNSUPPORTED, "diff: arity above 2 is not supported");
+    Canon ca, cb;
+    canonical_keys(ctx, a, ca);
+    canonical_keys(ctx, b, cb);
+    uint64_t *o = static_cast<uint64_t *>(ctx->alloc((ca.n ? ca.n : 1) * sizeof(uint64_t)));
+    Buf<uint64_t> cnt(ctx, 1);
+    select_unique_diff(ctx, ca.k, ca.n, cb.k, cb.n, o, cnt.p);
+    uint64_t n = read_count(ctx, cnt.p);
+    return rel_adopt(ctx, a->arity, n, o, nullptr, REL_CANONICAL);
+}
+
+// Join index over one column of an arity<=2 relation: sorted (key, other)
+// pairs, run index and payload (= other column, key order).
+struct JoinIndex {
+    RunIndex ix;
+    Buf<uint32_t> payload;
+    uint64_t n = 0;
+};
+static void build_join_index(Ctx *ctx, const uint64_t *keys, uint64_t n, uint32_t arity, int col, bool canonical,
+                             JoinIndex &J) {
+    J.n = n;
+    uint64_t *sk = nullptr;
+    bool own = false;
+    if (arity == 1) {
+        // (c0 << 32) | 0
+        sk = static_cast<uint64_t *>(ctx->alloc((n ? n : 1) * sizeof(uint64_t)));
+        swap_words(ctx, keys, n, sk);
+        own = true;
+        sk = sort_keys(ctx, sk, n, true);
+    } else if (col == 0) {
+        if (canonical) sk = const_cast<uint64_t *>(keys);
+        else { sk = sort_keys(ctx, const_cast<uint64_t *>(keys), n, false); own = true; }
+    } else {
+        sk = static_cast<uint64_t *>(ctx->alloc((n ? n : 1) * sizeof(uint64_t)));
+        swap_words(ctx, keys, n, sk);
+        own = true;
+        sk = sort_keys(ctx, sk, n, true);
+    }
+    build_run_index(ctx, sk, n, J.ix);
+    J.payload = Buf<uint32_t>(ctx, n ? n : 1);
+    low_words(ctx, sk, n, J.payload.p);
+    if (own) ctx->free(sk);
+}
+
+// value-index of a relation column for the probe side: arity 1 stores c0 in
+// the low word (v1), arity 2 stores c0 high (v0) and c1 low (v1)
+static int probe_vidx(uint32_t arity, uint32_t c) { return arity == 1 ? 1 : (int)c; }
+
+static xlog_hip_rel *op_join(Ctx *ctx, const xlog_hip_rel *l, const xlog_hip_rel *r, uint32_t lk, uint32_t rk,
+                             int type, const std::vector<int> *out_cols) {
+    XH_REQUIRE(l && r, XLOG_HIP_INVALID_ARG, "join input is NULL");
+    XH_REQUIRE(lk < l->arity && rk < r->arity, XLOG_HIP_INVALID_ARG, "join key column out of range");
+    XH_REQUIRE(l->arity <= 2 && r->arity <= 2, XLOG_HIP_UNSUPPORTED, "join: input arity above 2 is not supported");
+    JoinIndex J;
+    build_join_index(ctx, r->w[0], r->rows, r->arity, (int)rk, (r->flags & REL_CANONICAL) != 0, J);
+    const int pcol = probe_vidx(l->arity, lk);
+    if (type == XLOG_HIP_JOIN_SEMI || type == XLOG_HIP_JOIN_ANTI) {
+        Buf<uint8_t> flags(ctx, l->rows ? l->rows : 1);
+        join_match_flags(ctx, l->w[0], l->rows, pcol, J.ix, type == XLOG_HIP_JOIN_SEMI, flags.p);
+        return compact_rel(ctx, l, flags.p);
+    }
+    XH_REQUIRE(type == XLOG_HIP_JOIN_INNER, XLOG_HIP_INVALID_ARG, "unknown join type");
+    // value index of every column of (left ++ right)
+    std::vector<int> vmap;
+    for (uint32_t c = 0; c < l->arity; ++c) vmap.push_back(probe_vidx(l->arity, c));
+    for (uint32_t c = 0; c < r->arity; ++c) vmap.push_back(c == rk ? 2 : 3);
+    std::vector<int> sel;
+    if (out_cols) {
+        for (int c : *out_cols) {
+            XH_REQUIRE(c >= 0 && c < (int)vmap.size(), XLOG_HIP_INVALID_ARG, "projection column out of range");
+            sel.push_back(vmap[c]);
+        }
+    } else {
+        sel = vmap;
+    }
+    XH_REQUIRE(!sel.empty() && sel.size() <= 4, XLOG_HIP_UNSUPPORTED, "join output arity must be 1..4");
+    int oc[4] = {0, 0, 0, 0};
+    for (size_t i = 0; i < sel.size(); ++i) oc[i] = sel[i];
+    uint64_t *o0 = nullptr, *o1 = nullptr;
+    uint64_t n = join_probe_general(ctx, l->w[0], l->rows, pcol, J.ix, J.payload.p, (int)sel.size(), oc, &o0, &o1);
+    if (n == 0) return rel_new(ctx, (uint32_t)sel.size(), 0);
+    return rel_adopt(ctx, (uint32_t)sel.size(), n, o0, o1, 0);
+}
+
+static xlog_hip_rel *op_project(Ctx *ctx, const xlog_hip_rel *in, const std::vector<int> &cols) {
+    XH_REQUIRE(!cols.empty() && cols.size() <= 4, XLOG_HIP_INVALID_ARG, "projection needs 1..4 columns");
+    xlog_hip_rel *r = rel_new(ctx, (uint32_t)cols.size(), in->rows);
+    r->rows = in->rows;
+    ProjSpec s{(int)in->arity, (int)cols.size(), {0, 0, 0, 0}};
+    for (size_t i = 0; i < cols.size(); ++i) s.cols[i] = cols[i];
+    LAUNCH_1D(k_project, in->rows, in->w[0], in->w[1], in->rows, s, r->w[0], r->w[1]);
+    return r;
+}
+
+// ---------------------------------------------------------------------------
+// semi-naive fixpoint driver (Executor::execute_recursive_scc,
+// crates/xlog-runtime/src/executor/recursive.rs:447-957)
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr int MAX_BODY = 4;
+struct Atom { int pred, v[2]; };
+struct Rule { int head, hv[2], nb; Atom b[MAX_BODY]; };
+
+std::vector<Rule> parse_plan(const int32_t *plan, uint32_t n_preds) {
+    XH_REQUIRE(plan, XLOG_HIP_INVALID_ARG, "plan is NULL");
+    int p = 0, nr = plan[p++];
+    XH_REQUIRE(nr >= 0 && nr <= 256, XLOG_HIP_INVALID_ARG, "plan: bad rule count");
+    std::vector<Rule> rules(nr);
+    for (int i = 0; i < nr; ++i) {
+        Rule &r = rules[i];
+        r.head = plan[p++]; r.hv[0] = plan[p++]; r.hv[1] = plan[p++]; r.nb = plan[p++];
+        XH_REQUIRE(r.head >= 0 && (uint32_t)r.head < n_preds, XLOG_HIP_INVALID_ARG, "plan: head predicate out of range");
+        XH_REQUIRE(r.nb >= 1 && r.nb <= MAX_BODY, XLOG_HIP_INVALID_ARG, "plan: body must have 1..4 atoms");
+        for (int j = 0; j < r.nb; ++j) {
+            r.b[j].pred = plan[p++]; r.b[j].v[0] = plan[p++]; r.b[j].v[1] = plan[p++];
+            XH_REQUIRE(r.b[j].pred >= 0 && (uint32_t)r.b[j].pred < n_preds, XLOG_HIP_INVALID_ARG,
+                       "plan: body predicate out of range");
+        }
+    }
+    return rules;
+}
+
+bool needed_later(const Rule &r, int from, int var) {
+    if (r.hv[0] == var || r.hv[1] == var) return true;
+    for (int j = from; j < r.nb; ++j)
+        if (r.b[j].v[0] == var || r.b[j].v[1] == var) return true;
+    return false;
+}
+
+// device-resident canonical packed relation
+struct DRel {
+    uint64_t *k = nullptr;
+    uint64_t n = 0;
+    bool owned = false;
+    uint64_t version = 0;
+};
+
+struct Driver {
+    Ctx *ctx;
+    std::vector<Rule> rules;
+    uint32_t n_preds;
+    std::vector<bool> idb;
+    std::vector<DRel> full, delta;
+    uint64_t version_counter = 1;
+    // join-index cache keyed by (relation buffer, column, version)
+    struct CacheKey {
+        const uint64_t *k; int col; uint64_t version;
+        bool operator<(const CacheKey &o) const {
+            return std::tie(k, col, version) < std::tie(o.k, o.col, o.version);
+        }
+    };
+    std::map<CacheKey, std::unique_ptr<JoinIndex>> cache;
+
+    ~Driver() {
+        cache.clear();
+        for (auto &r : full) if (r.owned) ctx->free(r.k);
+        for (auto &r : delta) if (r.owned) ctx->free(r.k);
+    }
+
+    const JoinIndex &index_of(const DRel &rel, int col) {
+        CacheKey key{rel.k, col, rel.version};
+        auto it = cache.find(key);
+        if (it != cache.end()) return *it->second;
+        std::unique_ptr<JoinIndex> J(new JoinIndex());
+        build_join_index(ctx, rel.k, rel.n, 2, col, true, *J);
+        auto &ref = *J;
+        cache[key] = std::move(J);
+        return ref;
+    }
+    void drop_index(const DRel &rel) {
+        for (auto it = cache.begin(); it != cache.end();)
+            if (it->first.k == rel.k) it = cache.erase(it); else ++it;
+    }
+
+    // Evaluate a rule body; rel[j] is the relation atom j reads.  Appends the
+    // head tuples (bag, packed) to `out` as owned device buffers.
+    void eval_body(const Rule &r, const DRel *const *rel, std::vector<std::pair<uint64_t *, uint64_t>> &out) {
+        const Atom &a0 = r.b[0];
+        XH_REQUIRE(a0.v[0] != a0.v[1], XLOG_HIP_UNSUPPORTED, "plan: repeated variable inside an atom");
+        bool k0 = needed_later(r, 1, a0.v[0]), k1 = needed_later(r, 1, a0.v[1]);
+        XH_REQUIRE(k0 && k1, XLOG_HIP_UNSUPPORTED, "plan: first atom must bind two live variables");
+        // binding: packed (vars[0], vars[1])
+        int vars[2] = {a0.v[0], a0.v[1]};
+        const uint64_t *bk = rel[0]->k;
+        uint64_t bn = rel[0]->n;
+        uint64_t *owned = nullptr;
+        if (bn == 0) return;
+        if (r.nb == 1) {
+            // head projection of a single atom
+            int h0 = (r.hv[0] == vars[0]) ? 0 : (r.hv[0] == vars[1] ? 1 : -1);
+            int h1 = (r.hv[1] == vars[0]) ? 0 : (r.hv[1] == vars[1] ? 1 : -1);
+            XH_REQUIRE(h0 >= 0 && h1 >= 0, XLOG_HIP_UNSUPPORTED, "plan: head variable not bound by the body");
+            uint64_t *o = static_cast<uint64_t *>(ctx->alloc(bn * sizeof(uint64_t)));
+            if (h0 == 0 && h1 == 1) copy_d2d(ctx, o, bk, bn);
+            else if (h0 == 1 && h1 == 0) swap_words(ctx, bk, bn, o);
+            else {
+                ProjSpec s{2, 2, {h0, h1, 0, 0}};
+                LAUNCH_1D(k_project, bn, bk, nullptr, bn, s, o, nullptr);
+            }
+            out.push_back({o, bn});
+            return;
+        }
+        for (int j = 1; j < r.nb; ++j) {
+            const Atom &a = r.b[j];
+            XH_REQUIRE(a.v[0] != a.v[1], XLOG_HIP_UNSUPPORTED, "plan: repeated variable inside an atom");
+            int bpos = -1, apos = -1, nshared = 0;
+            for (int x = 0; x < 2; ++x)
+                for (int y = 0; y < 2; ++y)
+                    if (vars[x] == a.v[y]) { bpos = x; apos = y; ++nshared; }
+            XH_REQUIRE(nshared == 1, XLOG_HIP_UNSUPPORTED, "plan: each atom must share exactly one variable");
+            int other = a.v[1 - apos];
+            // candidate values: v0 = binding var 0, v1 = binding var 1, v2 = shared, v3 = other
+            int cand_var[4] = {vars[0], vars[1], a.v[apos], other};
+            int sel[2], ns = 0;
+            bool last = (j == r.nb - 1);
+            if (last) {
+                for (int t = 0; t < 2; ++t) {
+                    int f = -1;
+                    for (int c = 0; c < 4; ++c) if (cand_var[c] == r.hv[t]) { f = c; break; }
+                    XH_REQUIRE(f >= 0, XLOG_HIP_UNSUPPORTED, "plan: head variable not bound by the body");
+                    sel[ns++] = f;
+                }
+            } else {
+                int seen[4] = {-1, -1, -1, -1}, nseen = 0;
+                for (int c = 0; c < 4; ++c) {
+                    int v = cand_var[c];
+                    bool dup = false;
+                    for (int q = 0; q < nseen; ++q) if (seen[q] == v) dup = true;
+                    if (dup) continue;
+                    seen[nseen++] = v;
+                    if (needed_later(r, j + 1, v)) {
+                        XH_REQUIRE(ns < 2, XLOG_HIP_UNSUPPORTED, "plan: more than two live variables");
+                        sel[ns++] = c;
+                    }
+                }
+                XH_REQUIRE(ns == 2, XLOG_HIP_UNSUPPORTED, "plan: intermediate binding must keep two variables");
+            }
+            const DRel &ar = *rel[j];
+            uint64_t *o = nullptr;
+            uint64_t on = 0;
+            if (ar.n != 0) {
+                const JoinIndex &J = index_of(ar, apos);
+                int oc[4] = {sel[0], sel[1], 0, 0};
+                on = join_probe_general(ctx, bk, bn, bpos, J.ix, J.payload.p, 2, oc, &o, nullptr);
+            }
+            if (owned) ctx->free(owned);
+            owned = o;
+            bk = o;
+            bn = on;
+            vars[0] = cand_var[sel[0]];
+            vars[1] = cand_var[sel[1]];
+            if (bn == 0) {
+                if (owned) ctx->free(owned);
+                return;
+            }
+        }
+        out.push_back({owned, bn});
+    }
+
+    // concat bags, sort, unique, minus full -> new canonical delta
+    DRel finalize(std::vector<std::pair<uint64_t *, uint64_t>> &bags, const DRel &against) {
+        uint64_t total = 0;
+        for (auto &b : bags) total += b.second;
+        DRel d;
+        if (total == 0) {
+            for (auto &b : bags) ctx->free(b.first);
+            bags.clear();
+            return d;
+        }
+        uint64_t *cat;
+        if (bags.size() == 1) {
+            cat = bags[0].first;
+        } else {
+            cat = static_cast<uint64_t *>(ctx->alloc(total * sizeof(uint64_t)));
+            uint64_t off = 0;
+            for (auto &b : bags) {
+                copy_d2d(ctx, cat + off, b.first, b.second);
+                off += b.second;
+                ctx->free(b.first);
+            }
+        }
+        bags.clear();
+        uint64_t *s = sort_keys(ctx, cat, total, true);
+        if (s != cat) ctx->free(cat);
+        uint64_t *o = static_cast<uint64_t *>(ctx->alloc(total * sizeof(uint64_t)));
+        Buf<uint64_t> cnt(ctx, 1);
+        select_unique_diff(ctx, s, total, against.k, against.n, o, cnt.p);
+        ctx->free(s);
+        d.n = read_count(ctx, cnt.p);
+        d.k = o;
+        d.owned = true;
+        d.version = version_counter++;
+        return d;
+    }
+
+    DRel merge(const DRel &a, const DRel &b) {
+        DRel m;
+        m.n = a.n + b.n;
+        m.k = static_cast<uint64_t *>(ctx->alloc((m.n ? m.n : 1) * sizeof(uint64_t)));
+        m.owned = true;
+        m.version = version_counter++;
+        merge_sorted(ctx, a.k, a.n, b.k, b.n, m.k);
+        return m;
+    }
+
+    void release(DRel &r) {
+        drop_index(r);
+        if (r.owned) ctx->free(r.k);
+        r = DRel();
+    }
+
+    uint64_t run(uint64_t max_iter, std::vector<uint64_t> &deltas) {
+        // seed: every rule once against the current store
+        std::vector<std::vector<std::pair<uint64_t *, uint64_t>>> derived(n_preds);
+        for (const Rule &r : rules) {
+            const DRel *rel[MAX_BODY];
+            for (int j = 0; j < r.nb; ++j) rel[j] = &full[r.b[j].pred];
+            eval_body(r, rel, derived[r.head]);
+        }
+        uint64_t seed = 0;
+        for (uint32_t p = 0; p < n_preds; ++p) {
+            if (!idb[p]) continue;
+            DRel d = finalize(derived[p], full[p]);  // full_new \ full_old
+            if (d.n) {
+                DRel m = merge(full[p], d);
+                release(full[p]);
+                full[p] = m;
+            }
+            delta[p] = d;
+            seed += d.n;
+        }
+        deltas.push_back(seed);
+        uint64_t it = 0;
+        while (it < max_iter) {
+            ++it;
+            std::vector<std::vector<std::pair<uint64_t *, uint64_t>>> raw(n_preds);
+            for (const Rule &r : rules) {
+                for (int occ = 0; occ < r.nb; ++occ) {
+                    int p = r.b[occ].pred;
+                    if (!idb[p] || delta[p].n == 0) continue;
+                    const DRel *rel[MAX_BODY];
+                    for (int j = 0; j < r.nb; ++j) {
+                        int q = r.b[j].pred;
+                        rel[j] = (j == occ) ? &delta[q] : &full[q];
+                    }
+                    eval_body(r, rel, raw[r.head]);
+                }
+            }
+            uint64_t total = 0;
+            for (uint32_t p = 0; p < n_preds; ++p) {
+                if (!idb[p]) continue;
+                DRel d = finalize(raw[p], full[p]);
+                release(delta[p]);
+                delta[p] = d;
+                total += d.n;
+            }
+            deltas.push_back(total);
+            if (total == 0) return it;
+            for (uint32_t p = 0; p < n_preds; ++p) {
+                if (!idb[p] || delta[p].n == 0) continue;
+                DRel m = merge(full[p], delta[p]);
+                release(full[p]);
+                full[p] = m;
+            }
+        }
+        throw Error{XLOG_HIP_ITERATION_LIMIT,
+                    "Recursive SCC iteration limit (" + std::to_string(max_iter) + ") exceeded"};
+    }
+};
+
+// TC plan shape: head(A,B) :- E(A,B).  head(A,C) :- head(A,B), E(B,C).
+bool tc_shape(const std::vector<Rule> &rules, int *edge_pred, int *head_pred) {
+    if (rules.size() != 2) return false;
+    const Rule *base = nullptr, *rec = nullptr;
+    for (const Rule &r : rules) (r.nb == 1 ? base : rec) = &r;
+    if (!base || !rec || rec->nb != 2 || base->head != rec->head) return false;
+    int E = base->b[0].pred, H = base->head;
+    if (E == H) return false;
+    if (!(base->hv[0] == base->b[0].v[0] && base->hv[1] == base->b[0].v[1] && base->hv[0] != base->hv[1])) return false;
+    const Atom &x = rec->b[0], &y = rec->b[1];
+    if (x.pred != H || y.pred != E) return false;
+    int A = x.v[0], B = x.v[1], C = y.v[1];
+    if (y.v[0] != B || A == B || B == C || A == C) return false;
+    return rec->hv[0] == A && rec->hv[1] == C;
+}
+
+}  // namespace
+
+// canonical keys of an input relation for the driver
+static DRel canon_drel(Ctx *ctx, const xlog_hip_rel *r) {
+    DRel d;
+    if (!r || r->rows == 0) return d;
+    XH_REQUIRE(r->arity == 2, XLOG_HIP_TYPE_MISMATCH, "fixpoint: every predicate must have arity 2");
+    if (r->flags & REL_CANONICAL) {
+        d.k = r->w[0];
+        d.n = r->rows;
+        d.owned = false;
+        return d;
+    }
+    uint64_t *s = sort_keys(ctx, r->w[0], r->rows, false);
+    uint64_t *u;
+    d.n = unique_keys(ctx, s, r->rows, &u);
+    if (s != r->w[0]) ctx->free(s);
+    d.k = u;
+    d.owned = true;
+    return d;
+}
+
+static void run_fixpoint(Ctx *ctx, const int32_t *plan, uint32_t n_preds, const xlog_hip_rel *const *rels,
+                         xlog_hip_rel **out, xlog_hip_fixpoint_stats *stats) {
+    XH_REQUIRE(n_preds >= 1 && n_preds <= 256, XLOG_HIP_INVALID_ARG, "n_preds must be 1..256");
+    XH_REQUIRE(rels && out, XLOG_HIP_INVALID_ARG, "rels / out is NULL");
+    std::vector<Rule> rules = parse_plan(plan, n_preds);
+    uint64_t max_iter = (stats && stats->max_iterations) ? stats->max_iterations : 1000000ull;
+    uint64_t route = stats ? stats->route : XLOG_HIP_ROUTE_AUTO;
+    for (uint32_t p = 0; p < n_preds; ++p) out[p] = nullptr;
+    for (uint32_t p = 0; p < n_preds; ++p)
+        XH_REQUIRE(!rels[p] || rels[p]->arity == 2, XLOG_HIP_TYPE_MISMATCH, "fixpoint: every predicate must have arity 2");
+    XH_CHECK_HIP(hipEventRecord(ctx->ev_a, ctx->stream));
+    std::vector<uint64_t> deltas;
+    uint64_t iterations = 0;
+
+    int E = -1, H = -1;
+    bool tc = tc_shape(rules, &E, &H);
+    if (tc) {
+        for (const Rule &r : rules) if (r.nb == 1) { E = r.b[0].pred; H = r.head; }
+    }
+    bool head_empty = tc && (!rels[H] || rels[H]->rows == 0);
+    uint32_t nv = 0;
+    DRel edges;
+    if (tc && head_empty && route != XLOG_HIP_ROUTE_JOIN) {
+        edges = canon_drel(ctx, rels[E]);
+        if (edges.n) {
+            Buf<unsigned int> mx(ctx, 1);
+            fill_u32(ctx, mx.p, 0u, 1);
+            LAUNCH_1D(k_max_u32_of_packed, edges.n, edges.k, edges.n, mx.p);
+            XH_CHECK_HIP(hipMemcpyAsync(ctx->host_scalars, mx.p, sizeof(unsigned int), hipMemcpyDeviceToHost, ctx->stream));
+            ctx->sync();
+            nv = *reinterpret_cast<uint32_t *>(ctx->host_scalars) + 1;
+        }
+    }
+    bool bitmap = tc && head_empty && route != XLOG_HIP_ROUTE_JOIN && (uint64_t)nv <= (1ull << 17);
+    XH_REQUIRE(!(route == XLOG_HIP_ROUTE_BITMAP && !bitmap), XLOG_HIP_UNSUPPORTED,
+               "bitmap route needs the transitive-closure plan, an empty head and a domain <= 2^17");
+    if (bitmap) {
+        uint64_t *res = nullptr, n = 0;
+        try {
+            tc_bitmap(ctx, edges.k, edges.n, nv, max_iter, &res, &n, &iterations, deltas);
+        } catch (...) {
+            if (edges.owned) ctx->free(edges.k);
+            if (stats) stats->iterations = deltas.empty() ? 0 : deltas.size() - 1;
+            throw;
+        }
+        if (edges.owned) ctx->free(edges.k);
+        out[H] = n ? rel_adopt(ctx, 2, n, res, nullptr, REL_CANONICAL) : rel_new(ctx, 2, 0);
+        out[H]->flags = REL_CANONICAL;
+        if (stats) stats->route = XLOG_HIP_ROUTE_BITMAP;
+    } else {
+        if (edges.owned) ctx->free(edges.k);
+        Driver drv{ctx, rules, n_preds, std::vector<bool>(n_preds, false), std::vector<DRel>(n_preds),
+                   std::vector<DRel>(n_preds)};
+        for (const Rule &r : rules) drv.idb[r.head] = true;
+        for (uint32_t p = 0; p < n_preds; ++p) {
+            drv.full[p] = canon_drel(ctx, rels[p]);
+            drv.full[p].version = drv.version_counter++;
+        }
+        try {
+            iterations = drv.run(max_iter, deltas);
+        } catch (const Error &) {
+            if (stats) stats->iterations = deltas.empty() ? 0 : deltas.size() - 1;
+            throw;
+        }
+        for (uint32_t p = 0; p < n_preds; ++p) {
+            if (!drv.idb[p]) continue;
+            DRel &f = drv.full[p];
+            drv.drop_index(f);
+            xlog_hip_rel *r;
+            if (f.n == 0) {
+                r = rel_new(ctx, 2, 0);
+            } else if (f.owned) {
+                r = rel_adopt(ctx, 2, f.n, f.k, nullptr, REL_CANONICAL);
+                f.owned = false;
+            } else {
+                r = rel_new(ctx, 2, f.n);
+                r->rows = f.n;
+                copy_d2d(ctx, r->w[0], f.k, f.n);
+            }
+            r->flags = REL_CANONICAL;
+            out[p] = r;
+        }
+        if (stats) stats->route = XLOG_HIP_ROUTE_JOIN;
+    }
+    XH_CHECK_HIP(hipEventRecord(ctx->ev_b, ctx->stream));
+    XH_CHECK_HIP(hipEventSynchronize(ctx->ev_b));
+    float ms = 0.f;
+    XH_CHECK_HIP(hipEventElapsedTime(&ms, ctx->ev_a, ctx->ev_b));
+    ctx->last_delta_sizes = deltas;
+    ctx->last_iterations = iterations;
+    if (stats) {
+        stats->iterations = iterations;
+        stats->wall_ms = ms;
+        if (stats->delta_sizes)
+            for (uint64_t i = 0; i < stats->delta_cap && i < deltas.size(); ++i) stats->delta_sizes[i] = deltas[i];
+    }
+}
+
+}  // namespace xh
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+using namespace xh;
+
+struct xlog_hip_ctx {
+    Ctx c;
+};
+
+static Ctx *C(xlog_hip_ctx *ctx) {
+    XH_REQUIRE(ctx, XLOG_HIP_INVALID_ARG, "context is NULL");
+    XH_CHECK_HIP(hipSetDevice(ctx->c.device));
+    return &ctx->c;
+}
+static void need_rel(const xlog_hip_rel *r, const char *what) {
+    XH_REQUIRE(r, XLOG_HIP_INVALID_ARG, std::string(what) + " is NULL");
+}
+
+extern "C" {
+
+const char *xlog_hip_last_error(void) { return g_last_error.c_str(); }
+const char *xlog_hip_version(void) { return "xlog_hip 0.1.0 (gfx950)"; }
+
+xlog_hip_status xlog_hip_ctx_create(int device, xlog_hip_ctx **out) {
+    return guarded([&] {
+        XH_REQUIRE(out, XLOG_HIP_INVALID_ARG, "out is NULL");
+        *out = nullptr;
+        int count = 0;
+        XH_CHECK_HIP(hipGetDeviceCount(&count));
+        XH_REQUIRE(device >= 0 && device < count, XLOG_HIP_INVALID_ARG, "device index out of range");
+        XH_CHECK_HIP(hipSetDevice(device));
+        std::unique_ptr<xlog_hip_ctx> h(new xlog_hip_ctx());
+        Ctx &c = h->c;
+        c.device = device;
+        hipDeviceProp_t prop;
+        XH_CHECK_HIP(hipGetDeviceProperties(&prop, device));
+        c.num_cus = prop.multiProcessorCount;
+        XH_CHECK_HIP(hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking));
+        c.pool = new Pool(device);
+        XH_CHECK_HIP(hipHostMalloc((void **)&c.host_scalars, 64 * sizeof(uint64_t), hipHostMallocDefault));
+        c.tickets = static_cast<unsigned long long *>(c.alloc(16 * sizeof(unsigned long long)));
+        fill_u64(&c, reinterpret_cast<uint64_t *>(c.tickets), 0ull, 16);
+        XH_CHECK_HIP(hipEventCreate(&c.ev_a));
+        XH_CHECK_HIP(hipEventCreate(&c.ev_b));
+        c.sync();
+        *out = h.release();
+    });
+}
+
+void xlog_hip_ctx_destroy(xlog_hip_ctx *ctx) {
+    if (!ctx) return;
+    Ctx &c = ctx->c;
+    (void)hipSetDevice(c.device);
+    (void)hipStreamSynchronize(c.stream);
+    sort_state_release(&c);
+    select_state_release(&c);
+    if (c.tickets) c.free(c.tickets);
+    delete c.pool;
+    if (c.host_scalars) (void)hipHostFree(c.host_scalars);
+    if (c.ev_a) (void)hipEventDestroy(c.ev_a);
+    if (c.ev_b) (void)hipEventDestroy(c.ev_b);
+    for (auto &r : c.prof_pending) {
+        (void)hipEventDestroy(r.a);
+        (void)hipEventDestroy(r.b);
+    }
+    for (hipEvent_t e : c.prof_events) (void)hipEventDestroy(e);
+    (void)hipStreamDestroy(c.stream);
+    delete ctx;
+}
+
+xlog_hip_status xlog_hip_synchronize(xlog_hip_ctx *ctx) { return guarded([&] { C(ctx)->sync(); }); }
+void *xlog_hip_stream(xlog_hip_ctx *ctx) { return ctx ? (void *)ctx->c.stream : nullptr; }
+
+xlog_hip_status xlog_hip_memory_stats(xlog_hip_ctx *ctx, uint64_t *in_use, uint64_t *peak, uint64_t *cached) {
+    return guarded([&] {
+        Ctx *c = C(ctx);
+        if (in_use) *in_use = c->pool->bytes_in_use();
+        if (peak) *peak = c->pool->peak_in_use();
+        if (cached) *cached = c->pool->bytes_cached();
+    });
+}
+xlog_hip_status xlog_hip_trim(xlog_hip_ctx *ctx) { return guarded([&] { C(ctx)->pool->trim(); }); }
+
+xlog_hip_status xlog_hip_rel_create_empty(xlog_hip_ctx *ctx, uint32_t arity, xlog_hip_rel **out) {
+    return guarded([&] {
+        XH_REQUIRE(out, XLOG_HIP_INVALID_ARG, "out is NULL");
+        *out = rel_new(C(ctx), arity, 0);
+        (*out)->flags = REL_CANONICAL;
+    });
+}
+
+xlog_hip_status xlog_hip_rel_from_host_columns(xlog_hip_ctx *ctx, const uint32_t *const *cols, uint32_t arity,
+                                               uint64_t rows, xlog_hip_rel **out) {
+    return guarded([&] {
+        Ctx *c = C(ctx);
+        XH_REQUIRE(out, XLOG_HIP_INVALID_ARG, "out is NULL");
+        XH_REQUIRE(arity >= 1 && arity <= 4, XLOG_HIP_INVALID_ARG, "relation arity must be 1..4");
+        XH_REQUIRE(rows == 0 || cols, XLOG_HIP_INVALID_ARG, "columns are NULL");
+        for (uint32_t i = 0; i < arity && rows; ++i) XH_REQUIRE(cols[i], XLOG_HIP_INVALID_ARG, "column pointer is NULL");
+        std::vector<uint64_t> h0(rows), h1(arity > 2 ? rows : 0);
+        for (uint64_t i = 0; i < rows; ++i) {
+            h0[i] = arity == 1 ? (uint64_t)cols[0][i] : (((uint64_t)cols[0][i] << 32) | cols[1][i]);
+            if (arity == 3) h1[i] = (uint64_t)cols[2][i] << 32;
+            if (arity == 4) h1[i] = ((uint64_t)cols[2][i] << 32) | cols[3][i];
+        }
+        xlog_hip_rel *r = rel_new(c, arity, rows);
+        r->rows = rows;
+        if (rows) {
+            XH_CHECK_HIP(hipMemcpyAsync(r->w[0], h0.data(), rows * 8, hipMemcpyHostToDevice, c->stream));
+            if (arity > 2) XH_CHECK_HIP(hipMemcpyAsync(r->w[1], h1.data(), rows * 8, hipMemcpyHostToDevice, c->stream));
+        }
+        c->sync();
+        *out = r;
+    });
+}
+
+xlog_hip_status xlog_hip_rel_from_device_columns(xlog_hip_ctx *ctx, const uint32_t *const *dev_cols, uint32_t arity,
+                                                 uint64_t rows, xlog_hip_rel **out) {
+    return guarded([&] {
+        Ctx *ctxp = C(ctx);
+        Ctx *ctx = ctxp;
+        XH_REQUIRE(out, XLOG_HIP_INVALID_ARG, "out is NULL");
+        XH_REQUIRE(arity >= 1 && arity <= 4, XLOG_HIP_INVALID_ARG, "relation arity must be 1..4");
+        XH_REQUIRE(rows == 0 || dev_cols, XLOG_HIP_INVALID_ARG, "columns are NULL");
+        xlog_hip_rel *r = rel_new(ctx, arity, rows);
+        r->rows = rows;
+        if (rows) {
+            if (arity == 1) LAUNCH_1D(k_widen, rows, dev_cols[0], rows, r->w[0]);
+            else pack_columns(ctx, dev_cols[0], dev_cols[1], rows, r->w[0]);
+            if (arity == 3) pack_columns(ctx, dev_cols[2], nullptr, rows, r->w[1]);
+            if (arity == 4) pack_columns(ctx, dev_cols[2], dev_cols[3], rows, r->w[1]);
+        }
+        *out = r;
+    });
+}
+
+xlog_hip_status xlog_hip_rel_from_host_packed(xlog_hip_ctx *ctx, const uint64_t *keys, uint32_t arity, uint64_t rows,
+                                              xlog_hip_rel **out) {
+    return guarded([&] {
+        Ctx *c = C(ctx);
+        XH_REQUIRE(out, XLOG_HIP_INVALID_ARG, "out is NULL");
+        XH_REQUIRE(arity == 1 || arity == 2, XLOG_HIP_INVALID_ARG, "packed upload supports arity 1 or 2");
+        XH_REQUIRE(rows == 0 || keys, XLOG_HIP_INVALID_ARG, "keys are NULL");
+        xlog_hip_rel *r = rel_new(c, arity, rows);
+        r->rows = rows;
+        if (rows) XH_CHECK_HIP(hipMemcpyAsync(r->w[0], keys, rows * 8, hipMemcpyHostToDevice, c->stream));
+        c->sync();
+        *out = r;
+    });
+}
+
+xlog_hip_status xlog_hip_rel_download_column(xlog_hip_ctx *ctx, const xlog_hip_rel *rel, uint32_t col, uint32_t *host,
+                                             uint64_t host_cap) {
+    return guarded([&] {
+        Ctx *ctxp = C(ctx);
+        Ctx *ctx = ctxp;
+        need_rel(rel, "relation");
+        XH_REQUIRE(col < rel->arity, XLOG_HIP_INVALID_ARG, "column out of range");
+        XH_REQUIRE(host_cap >= rel->rows, XLOG_HIP_CAPACITY_OVERFLOW, "host buffer too small");
+        if (!rel->rows) return;
+        XH_REQUIRE(host, XLOG_HIP_INVALID_ARG, "host buffer is NULL");
+        Buf<uint32_t> tmp(ctx, rel->rows);
+        if (rel->arity == 1) LAUNCH_1D(k_u64_to_u32, rel->rows, rel->w[0], rel->rows, tmp.p);
+        else {
+            const uint64_t *w = col < 2 ? rel->w[0] : rel->w[1];
+            unpack_column(ctx, w, (col % 2) == 0, rel->rows, tmp.p);
+        }
+        XH_CHECK_HIP(hipMemcpyAsync(host, tmp.p, rel->rows * 4, hipMemcpyDeviceToHost, ctx->stream));
+        ctx->sync();
+    });
+}
+
+xlog_hip_status xlog_hip_rel_download_packed(xlog_hip_ctx *ctx, const xlog_hip_rel *rel, uint64_t *host,
+                                             uint64_t host_cap) {
+    return guarded([&] {
+        Ctx *c = C(ctx);
+        need_rel(rel, "relation");
+        XH_REQUIRE(rel->arity <= 2, XLOG_HIP_INVALID_ARG, "packed download supports arity 1 or 2");
+        XH_REQUIRE(host_cap >= rel->rows, XLOG_HIP_CAPACITY_OVERFLOW, "host buffer too small");
+        if (!rel->rows) return;
+        XH_REQUIRE(host, XLOG_HIP_INVALID_ARG, "host buffer is NULL");
+        XH_CHECK_HIP(hipMemcpyAsync(host, rel->w[0], rel->rows * 8, hipMemcpyDeviceToHost, c->stream));
+        c->sync();
+    });
+}
+
+xlog_hip_status xlog_hip_rel_num_rows(const xlog_hip_rel *rel, uint64_t *rows) {
+    return guarded([&] {
+        need_rel(rel, "relation");
+        XH_REQUIRE(rows, XLOG_HIP_INVALID_ARG, "rows is NULL");
+        *rows = rel->rows;
+    });
+}
+xlog_hip_status xlog_hip_rel_arity(const xlog_hip_rel *rel, uint32_t *arity) {
+    return guarded([&] {
+        need_rel(rel, "relation");
+        XH_REQUIRE(arity, XLOG_HIP_INVALID_ARG, "arity is NULL");
+        *arity = rel->arity;
+    });
+}
+xlog_hip_status xlog_hip_rel_is_canonical(const xlog_hip_rel *rel, int *canonical) {
+    return guarded([&] {
+        need_rel(rel, "relation");
+        XH_REQUIRE(canonical, XLOG_HIP_INVALID_ARG, "canonical is NULL");
+        *canonical = (rel->flags & REL_CANONICAL) ? 1 : 0;
+    });
+}
+xlog_hip_status xlog_hip_rel_device_words(const xlog_hip_rel *rel, uint32_t word, const uint64_t **dev) {
+    return guarded([&] {
+        need_rel(rel, "relation");
+        XH_REQUIRE(dev, XLOG_HIP_INVALID_ARG, "dev is NULL");
+        XH_REQUIRE(word < (uint32_t)rel->nwords(), XLOG_HIP_INVALID_ARG, "word index out of range");
+        *dev = rel->w[word];
+    });
+}
+xlog_hip_status xlog_hip_rel_clone(xlog_hip_ctx *ctx, const xlog_hip_rel *in, xlog_hip_rel **out) {
+    return guarded([&] {
+        Ctx *c = C(ctx);
+        need_rel(in, "input");
+        XH_REQUIRE(out, XLOG_HIP_INVALID_ARG, "out is NULL");
+        *out = rel_clone(c, in);
+    });
+}
+void xlog_hip_rel_free(xlog_hip_rel *rel) {
+    if (rel && rel->ctx) (void)hipSetDevice(rel->ctx->device);
+    rel_free(rel);
+}
+
+#define OUT_GUARD XH_REQUIRE(out, XLOG_HIP_INVALID_ARG, "out is NULL"); *out = nullptr
+
+xlog_hip_status xlog_hip_sort(xlog_hip_ctx *ctx, const xlog_hip_rel *in, const uint32_t *key_cols, uint32_t n_keys,
+                              xlog_hip_rel **out) {
+    return guarded([&] {
+        Ctx *c = C(ctx);
+        OUT_GUARD;
+        need_rel(in, "input");
+        *out = op_sort(c, in, check_cols(in, key_cols, n_keys));
+    });
+}
+xlog_hip_status xlog_hip_dedup(xlog_hip_ctx *ctx, const xlog_hip_rel *in, const uint32_t *key_cols, uint32_t n_keys,
+                               xlog_hip_rel **out) {
+    return guarded([&] {
+        Ctx *c = C(ctx);
+        OUT_GUARD;
+        need_rel(in, "input");
+        *out = op_dedup(c, in, check_cols(in, key_cols, n_keys));
+    });
+}
+xlog_hip_status xlog_hip_dedup_full_row(xlog_hip_ctx *ctx, const xlog_hip_rel *in, xlog_hip_rel **out) {
+    return guarded([&] {
+        Ctx *c = C(ctx);
+        OUT_GUARD;
+        need_rel(in, "input");
+        *out = op_dedup_full(c, in);
+    });
+}
+xlog_hip_status xlog_hip_union(xlog_hip_ctx *ctx, const xlog_hip_rel *a, const xlog_hip_rel *b, xlog_hip_rel **out) {
+    return guarded([&] {
+        Ctx *c = C(ctx);
+        OUT_GUARD;
+        need_rel(a, "a");
+        need_rel(b, "b");
+        const xlog_hip_rel *ins[2] = {a, b};
+        *out = op_union_many(c, ins, 2);
+    });
+}
+xlog_hip_status xlog_hip_union_many(xlog_hip_ctx *ctx, const xlog_hip_rel *const *ins, uint32_t n_ins,
+                                    xlog_hip_rel **out) {
+    return guarded([&] {
+        Ctx *c = C(ctx);
+        OUT_GUARD;
+        *out = op_union_many(c, ins, n_ins);
+    });
+}
+xlog_hip_status xlog_hip_diff(xlog_hip_ctx *ctx, const xlog_hip_rel *a, const xlog_hip_rel *b, xlog_hip_rel **out) {
+    return guarded([&] {
+        Ctx *c = C(ctx);
+        OUT_GUARD;
+        need_rel(a, "a");
+        need_rel(b, "b");
+        *out = op_diff(c, a, b);
+    });
+}
+xlog_hip_status xlog_hip_hash_join(xlog_hip_ctx *ctx, const xlog_hip_rel *left, const xlog_hip_rel *right,
+                                   uint32_t left_key, uint32_t right_key, int join_type, xlog_hip_rel **out) {
+    return guarded([&] {
+        Ctx *c = C(ctx);
+        OUT_GUARD;
+        *out = op_join(c, left, right, left_key, right_key, join_type, nullptr);
+    });
+}
+xlog_hip_status xlog_hip_sort_merge_join(xlog_hip_ctx *ctx, const xlog_hip_rel *left, const xlog_hip_rel *right,
+                                         uint32_t left_key, uint32_t right_key, xlog_hip_rel **out) {
+    return guarded([&] {
+        Ctx *c = C(ctx);
+        OUT_GUARD;
+        *out = op_join(c, left, right, left_key, right_key, XLOG_HIP_JOIN_INNER, nullptr);
+    });
+}
+xlog_hip_status xlog_hip_join_project(xlog_hip_ctx *ctx, const xlog_hip_rel *left, const xlog_hip_rel *right,
+                                      uint32_t left_key, uint32_t right_key, const uint32_t *out_cols, uint32_t n_out,
+                                      xlog_hip_rel **out) {
+    return guarded([&] {
+        Ctx *c = C(ctx);
+        OUT_GUARD;
+        XH_REQUIRE(out_cols && n_out >= 1 && n_out <= 4, XLOG_HIP_INVALID_ARG, "out_cols must list 1..4 columns");
+        std::vector<int> oc(out_cols, out_cols + n_out);
+        *out = op_join(c, left, right, left_key, right_key, XLOG_HIP_JOIN_INNER, &oc);
+    });
+}
+xlog_hip_status xlog_hip_project(xlog_hip_ctx *ctx, const xlog_hip_rel *in, const uint32_t *cols, uint32_t n_cols,
+                                 xlog_hip_rel **out) {
+    return guarded([&] {
+        Ctx *c = C(ctx);
+        OUT_GUARD;
+        need_rel(in, "input");
+        *out = op_project(c, in, check_cols(in, cols, n_cols));
+    });
+}
+xlog_hip_status xlog_hip_is_sorted(xlog_hip_ctx *ctx, const xlog_hip_rel *rel, uint32_t col, int *sorted) {
+    return guarded([&] {
+        Ctx *ctxp = C(ctx);
+        Ctx *ctx = ctxp;
+        need_rel(rel, "relation");
+        XH_REQUIRE(sorted, XLOG_HIP_INVALID_ARG, "sorted is NULL");
+        XH_REQUIRE(col < rel->arity, XLOG_HIP_INVALID_ARG, "column out of range");
+        if (rel->rows < 2) { *sorted = 1; return; }
+        Buf<uint32_t> flag(ctx, 1);
+        fill_u32(ctx, flag.p, 0u, 1);
+        LAUNCH_1D(k_col_unsorted, rel->rows, rel->w[0], rel->w[1], (int)rel->arity, (int)col, rel->rows, flag.p);
+        uint32_t h = 0;
+        XH_CHECK_HIP(hipMemcpyAsync(&h, flag.p, 4, hipMemcpyDeviceToHost, ctx->stream));
+        ctx->sync();
+        *sorted = h == 0;
+    });
+}
+xlog_hip_status xlog_hip_exclusive_scan_u32(xlog_hip_ctx *ctx, uint32_t *dev, uint64_t n, uint64_t *total) {
+    return guarded([&] {
+        Ctx *ctxp = C(ctx);
+        Ctx *ctx = ctxp;
+        XH_REQUIRE(n == 0 || dev, XLOG_HIP_INVALID_ARG, "array is NULL");
+        if (n == 0) { if (total) *total = 0; return; }
+        Buf<uint64_t> tmp(ctx, n + 1);
+        LAUNCH_1D(k_u32_to_u64, n, dev, n, tmp.p);
+        scan_u64_small(ctx, tmp.p, n, tmp.p + n);
+        LAUNCH_1D(k_u64_to_u32, n, tmp.p, n, dev);
+        ctx->read_scalars(tmp.p + n, 1);
+        if (total) *total = ctx->host_scalars[0];
+    });
+}
+xlog_hip_status xlog_hip_compact(xlog_hip_ctx *ctx, const xlog_hip_rel *in, const uint8_t *dev_mask, xlog_hip_rel **out) {
+    return guarded([&] {
+        Ctx *c = C(ctx);
+        OUT_GUARD;
+        need_rel(in, "input");
+        XH_REQUIRE(in->rows == 0 || dev_mask, XLOG_HIP_INVALID_ARG, "mask is NULL");
+        *out = compact_rel(c, in, dev_mask);
+        if (in->flags & REL_CANONICAL) (*out)->flags = REL_CANONICAL;
+    });
+}
+
+xlog_hip_status xlog_hip_fixpoint(xlog_hip_ctx *ctx, const int32_t *plan, uint32_t n_preds,
+                                  const xlog_hip_rel *const *rels, xlog_hip_rel **out, xlog_hip_fixpoint_stats *stats) {
+    return guarded([&] { run_fixpoint(C(ctx), plan, n_preds, rels, out, stats); });
+}
+
+xlog_hip_status xlog_hip_fixpoint_tc(xlog_hip_ctx *ctx, const xlog_hip_rel *edge, xlog_hip_rel **reach,
+                                     xlog_hip_fixpoint_stats *stats) {
+    return guarded([&] {
+        Ctx *c = C(ctx);
+        need_rel(edge, "edge");
+        XH_REQUIRE(reach, XLOG_HIP_INVALID_ARG, "reach is NULL");
+        // preds: 0 = edge, 1 = reach ; vars X=0 Y=1 Z=2
+        static const int32_t plan[] = {2, 1, 0, 1, 1, 0, 0, 1, 1, 0, 2, 2, 1, 0, 1, 0, 1, 2};
+        const xlog_hip_rel *rels[2] = {edge, nullptr};
+        xlog_hip_rel *outs[2] = {nullptr, nullptr};
+        run_fixpoint(c, plan, 2, rels, outs, stats);
+        *reach = outs[1];
+    });
+}
+
+xlog_hip_status xlog_hip_rel_digest(xlog_hip_ctx *ctx, const xlog_hip_rel *rel, uint64_t *digest) {
+    return guarded([&] {
+        Ctx *c = C(ctx);
+        need_rel(rel, "relation");
+        XH_REQUIRE(digest, XLOG_HIP_INVALID_ARG, "digest is NULL");
+        XH_REQUIRE(rel->arity <= 2, XLOG_HIP_UNSUPPORTED, "digest supports arity 1 or 2");
+        std::vector<uint64_t> h(rel->rows);
+        if (rel->rows) {
+            XH_CHECK_HIP(hipMemcpyAsync(h.data(), rel->w[0], rel->rows * 8, hipMemcpyDeviceToHost, c->stream));
+            c->sync();
+        }
+        uint64_t x = 0xcbf29ce484222325ULL;
+        for (uint64_t k : h)
+            for (int b = 0; b < 8; ++b) { x ^= (k >> (8 * b)) & 255; x *= 0x100000001b3ULL; }
+        *digest = x;
+    });
+}
+
+}  // extern "C"
+
+// ---- kernel timing -----------------------------------------------------------
+void xh::Ctx::prof_resolve() {
+    if (prof_pending.empty()) return;
+    sync();
+    for (auto &r : prof_pending) {
+        float ms = 0.f;
+        XH_CHECK_HIP(hipEventElapsedTime(&ms, r.a, r.b));
+        if (r.kind >= 0 && r.kind < XLOG_HIP_KERNEL_KINDS) {
+            prof_ms[r.kind] += ms;
+            prof_bytes[r.kind] += r.bytes;
+            prof_launches[r.kind] += 1;
+        }
+        prof_events.push_back(r.a);
+        prof_events.push_back(r.b);
+    }
+    prof_pending.clear();
+}
+
+extern "C" {
+xlog_hip_status xlog_hip_profile_enable(xlog_hip_ctx *ctx, int on) {
+    return guarded([&] {
+        Ctx *c = C(ctx);
+        c->prof_resolve();
+        c->profiling = on != 0;
+    });
+}
+xlog_hip_status xlog_hip_profile_reset(xlog_hip_ctx *ctx) {
+    return guarded([&] {
+        Ctx *c = C(ctx);
+        c->prof_resolve();
+        for (int k = 0; k < XLOG_HIP_KERNEL_KINDS; ++k) {
+            c->prof_ms[k] = 0;
+            c->prof_bytes[k] = 0;
+            c->prof_launches[k] = 0;
+        }
+    });
+}
+xlog_hip_status xlog_hip_profile_read(xlog_hip_ctx *ctx, uint32_t kind, uint64_t *launches, double *total_ms,
+                                      double *algo_bytes) {
+    return guarded([&] {
+        Ctx *c = C(ctx);
+        XH_REQUIRE(kind < XLOG_HIP_KERNEL_KINDS, XLOG_HIP_INVALID_ARG, "unknown kernel kind");
+        c->prof_resolve();
+        if (launches) *launches = c->prof_launches[kind];
+        if (total_ms) *total_ms = c->prof_ms[kind];
+        if (algo_bytes) *algo_bytes = c->prof_bytes[kind];
+    });
+}
+}  // extern "C"

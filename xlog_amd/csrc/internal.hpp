@@ -1,0 +1,277 @@
+// Internal declarations shared by the HIP translation units of libxlog_hip.
+// Everything here is gfx950 (wave64) code; the public surface is the C ABI
+// declared in include/xlog_hip.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+#include <cstddef>
+#include <string>
+#include <vector>
+#include <map>
+#include <mutex>
+
+#include "../../include/xlog_hip.h"
+
+namespace xh {
+
+constexpr int WAVE = 64;
+
+// ---------------------------------------------------------------------------
+// error plumbing: every entry point returns a status and leaves a message in
+// a thread-local buffer readable through xlog_hip_last_error().
+// ---------------------------------------------------------------------------
+void set_error(const std::string &msg);
+struct Error {
+    xlog_hip_status code;
+    std::string msg;
+};
+
+#define XH_CHECK_HIP(expr)                                                          \
+    do {                                                                            \
+        hipError_t _e = (expr);                                                     \
+        if (_e != hipSuccess)                                                       \
+            throw ::xh::Error{XLOG_HIP_DEVICE_ERROR,                                \
+                              std::string(#expr) + ": " + hipGetErrorString(_e)};   \
+    } while (0)
+
+#define XH_REQUIRE(cond, code, msg)                                                 \
+    do {                                                                            \
+        if (!(cond)) throw ::xh::Error{code, msg};                                  \
+    } while (0)
+
+// ---------------------------------------------------------------------------
+// stream-ordered caching allocator.  All work of a context runs on its one
+// stream, so a block freed by one operation can be handed to the next one
+// without a synchronisation: the stream orders the reuse after the last use.
+// ---------------------------------------------------------------------------
+class Pool {
+  public:
+    explicit Pool(int device) : device_(device) {}
+    int device() const { return device_; }
+    ~Pool();
+    void *alloc(size_t bytes);
+    void free(void *p);
+    void trim();  // return cached blocks to the driver
+    size_t bytes_in_use() const { return in_use_; }
+    size_t bytes_cached() const { return cached_; }
+    size_t peak_in_use() const { return peak_; }
+
+  private:
+    static size_t round_up(size_t b);
+    int device_;
+    std::multimap<size_t, void *> free_;  // size class -> block
+    std::map<void *, size_t> live_;
+    size_t in_use_ = 0, cached_ = 0, peak_ = 0;
+};
+
+// RAII scratch buffer from the context pool
+struct Ctx;
+template <typename T>
+struct Buf {
+    Ctx *ctx = nullptr;
+    T *p = nullptr;
+    size_t n = 0;
+    Buf() = default;
+    Buf(Ctx *c, size_t count);
+    Buf(const Buf &) = delete;
+    Buf &operator=(const Buf &) = delete;
+    Buf(Buf &&o) noexcept : ctx(o.ctx), p(o.p), n(o.n) { o.p = nullptr; o.n = 0; }
+    Buf &operator=(Buf &&o) noexcept;
+    ~Buf();
+    T *release() { T *q = p; p = nullptr; n = 0; return q; }
+};
+
+// ---------------------------------------------------------------------------
+// context: one device, one stream, the pool and the small persistent device
+// state used by the single-pass (decoupled look-back) kernels.
+// ---------------------------------------------------------------------------
+struct Ctx {
+    int device = 0;
+    int num_cus = 0;
+    hipStream_t stream = nullptr;
+    Pool *pool = nullptr;
+    // pinned host staging for scalar read-backs
+    uint64_t *host_scalars = nullptr;  // 64 entries
+    // device scratch: ticket counters for tile ordering (monotone, never reset)
+    unsigned long long *tickets = nullptr;  // 16 counters
+    unsigned long long ticket_base[16] = {0};
+    hipEvent_t ev_a = nullptr, ev_b = nullptr;
+    // statistics of the last fixpoint / op (host side)
+    std::vector<uint64_t> last_delta_sizes;
+    uint64_t last_iterations = 0;
+    float last_kernel_ms = 0.f;
+
+    // per-kernel-kind timing with HIP events on `stream` (off unless enabled)
+    struct ProfRec {
+        int kind;
+        hipEvent_t a, b;
+        double bytes;
+    };
+    bool profiling = false;
+    std::vector<ProfRec> prof_pending;
+    std::vector<hipEvent_t> prof_events;
+    double prof_ms[XLOG_HIP_KERNEL_KINDS] = {0};
+    double prof_bytes[XLOG_HIP_KERNEL_KINDS] = {0};
+    uint64_t prof_launches[XLOG_HIP_KERNEL_KINDS] = {0};
+    hipEvent_t prof_event() {
+        if (!prof_events.empty()) {
+            hipEvent_t e = prof_events.back();
+            prof_events.pop_back();
+            return e;
+        }
+        hipEvent_t e;
+        XH_CHECK_HIP(hipEventCreate(&e));
+        return e;
+    }
+    void prof_resolve();  // synchronises, folds pending records into the totals
+
+    void *alloc(size_t bytes) { return pool->alloc(bytes); }
+    void free(void *p) { pool->free(p); }
+    // reserve `count` consecutive ticket values on counter `slot`; returns the
+    // base that the kernel subtracts from its atomicAdd result.
+    unsigned long long take_tickets(int slot, unsigned long long count) {
+        unsigned long long b = ticket_base[slot];
+        ticket_base[slot] += count;
+        return b;
+    }
+    void sync() { XH_CHECK_HIP(hipStreamSynchronize(stream)); }
+    // D2H of a few u64 scalars through pinned memory (synchronises)
+    void read_scalars(const void *dev, size_t count_u64);
+};
+
+// Brackets one launch with events when profiling is on.
+struct Prof {
+    Ctx *ctx;
+    Ctx::ProfRec rec;
+    bool on;
+    Prof(Ctx *c, int kind, double bytes) : ctx(c), on(c->profiling) {
+        if (!on) return;
+        rec.kind = kind;
+        rec.bytes = bytes;
+        rec.a = c->prof_event();
+        rec.b = c->prof_event();
+        XH_CHECK_HIP(hipEventRecord(rec.a, c->stream));
+    }
+    ~Prof() {
+        if (!on) return;
+        (void)hipEventRecord(rec.b, ctx->stream);
+        ctx->prof_pending.push_back(rec);
+    }
+};
+
+template <typename T>
+Buf<T>::Buf(Ctx *c, size_t count) : ctx(c), n(count) {
+    p = count ? static_cast<T *>(c->alloc(count * sizeof(T))) : nullptr;
+}
+template <typename T>
+Buf<T> &Buf<T>::operator=(Buf &&o) noexcept {
+    if (this != &o) {
+        if (p && ctx) ctx->free(p);
+        ctx = o.ctx; p = o.p; n = o.n;
+        o.p = nullptr; o.n = 0;
+    }
+    return *this;
+}
+template <typename T>
+Buf<T>::~Buf() {
+    if (p && ctx) ctx->free(p);
+}
+
+}  // namespace xh
+
+// ---------------------------------------------------------------------------
+// relation handle (the CudaBuffer counterpart).  Rows are stored as packed
+// u64 words, row-major within a word, word-major across words:
+//   arity 1: w[0][i] = c0
+//   arity 2: w[0][i] = (c0 << 32) | c1
+//   arity 3: w[0][i] = (c0 << 32) | c1, w[1][i] = c2 << 32
+//   arity 4: w[0][i] = (c0 << 32) | c1, w[1][i] = (c2 << 32) | c3
+// Unsigned u64 order over (w[0], w[1]) is the lexicographic unsigned column
+// order, and equal words are bytewise-equal rows.
+// ---------------------------------------------------------------------------
+struct xlog_hip_rel {
+    xh::Ctx *ctx = nullptr;
+    uint32_t arity = 0;
+    uint64_t rows = 0;
+    uint64_t cap = 0;
+    uint64_t *w[2] = {nullptr, nullptr};
+    uint32_t flags = 0;  // XLOG_HIP_REL_CANONICAL when sorted by all columns and unique
+    int nwords() const { return arity <= 2 ? 1 : 2; }
+};
+
+namespace xh {
+
+constexpr uint32_t REL_CANONICAL = 1u;
+
+xlog_hip_rel *rel_new(Ctx *ctx, uint32_t arity, uint64_t cap);
+void rel_free(xlog_hip_rel *r);
+
+// ---------------------------------------------------------------------------
+// device algorithm entry points (host wrappers around the kernels); all
+// stream-ordered on ctx->stream.
+// ---------------------------------------------------------------------------
+
+// LSD radix sort of u64 keys with an optional u32 payload.  On return *keys
+// (and *vals) point at whichever of the two buffers holds the result; the
+// other is scratch.  Digits that are constant over the input are skipped.
+// Returns the number of digit passes executed.
+int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **vals, uint32_t **vals_alt,
+                   uint64_t n);
+
+// Stream compaction family (single pass, decoupled look-back).  Each writes
+// the selected keys in input order to `out` and the count to *d_count
+// (device) ; returns nothing, the caller reads the count when it needs it.
+//   unique:      keep k[i] if i == 0 or k[i] != k[i-1]                 (sorted input)
+//   unique_diff: keep k[i] if unique and k[i] not in sorted b[0..nb)
+//   diff:        keep k[i] if k[i] not in sorted b[0..nb)
+void select_unique(Ctx *ctx, const uint64_t *k, uint64_t n, uint64_t *out, uint64_t *d_count);
+void select_unique_diff(Ctx *ctx, const uint64_t *k, uint64_t n, const uint64_t *b, uint64_t nb,
+                        uint64_t *out, uint64_t *d_count);
+void select_flags(Ctx *ctx, const uint64_t *k, const uint8_t *flags, uint64_t n, uint64_t *out,
+                  uint64_t *d_count);
+
+// Merge of two sorted arrays (stable, a before b on ties) into out[na+nb].
+void merge_sorted(Ctx *ctx, const uint64_t *a, uint64_t na, const uint64_t *b, uint64_t nb, uint64_t *out);
+
+// Sorted-run index over the high word of sorted packed keys (join build):
+// run_key[r], run_start[r] (run_start[nruns] = n) and an open-addressing
+// hash table mapping key -> run.
+struct RunIndex {
+    Buf<uint32_t> run_key;
+    Buf<uint64_t> run_start;
+    Buf<unsigned long long> table;  // (key << 32) | (run + 1), 0 = empty
+    uint64_t nruns = 0;
+    uint64_t table_mask = 0;
+};
+void build_run_index(Ctx *ctx, const uint64_t *sorted_keys, uint64_t n, RunIndex &ix);
+
+// Probe: for every packed probe row p[i], key = column `pcol` of the row
+// (0 = high word, 1 = low word); each match emits
+//   out = (sel(p, oc0) << 32) | sel(p, oc1)
+// where sel picks among (p.c0, p.c1, build.key, build.payload) by index 0..3.
+// Two launches: count (per-tile totals with look-back) and emit.  Returns the
+// number of output rows (one read-back).
+uint64_t join_probe_project(Ctx *ctx, const uint64_t *probe, uint64_t n, int pcol, const RunIndex &ix,
+                            const uint32_t *payload, int oc0, int oc1, uint64_t **out);
+
+// small helpers
+inline unsigned grid_for(uint64_t n, unsigned block, unsigned cap) {
+    uint64_t g = (n + block - 1) / block;
+    if (g < 1) g = 1;
+    if (g > cap) g = cap;
+    return (unsigned)g;
+}
+void fill_u32(Ctx *ctx, uint32_t *p, uint32_t v, uint64_t n);
+void select_runs(Ctx *ctx, const uint64_t *k, uint64_t n, uint32_t *run_key, uint64_t *run_start,
+                 uint64_t *d_count);
+void sort_state_release(Ctx *ctx);
+void select_state_release(Ctx *ctx);
+void fill_u64(Ctx *ctx, uint64_t *p, uint64_t v, uint64_t n);
+void pack_columns(Ctx *ctx, const uint32_t *c0, const uint32_t *c1, uint64_t n, uint64_t *out);
+void unpack_column(Ctx *ctx, const uint64_t *w, int hi, uint64_t n, uint32_t *out);
+void swap_words(Ctx *ctx, const uint64_t *in, uint64_t n, uint64_t *out);  // (c0,c1) -> (c1,c0)
+void low_words(Ctx *ctx, const uint64_t *in, uint64_t n, uint32_t *out);
+int is_sorted_u64(Ctx *ctx, const uint64_t *k, uint64_t n, int strict);
+
+}  // namespace xh

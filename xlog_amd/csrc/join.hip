@@ -1,0 +1,335 @@
+// Equi-join on one u32 key column for gfx950.
+//
+// Replaces the reference's bucketed-CSR hash join
+// (hash_join_v2 / build_hash_table_v2 / hash_join_probe_v2,
+//  crates/xlog-cuda/src/provider/relational.rs:2926-2992,4262-4625,
+//  kernels/join.cu:131-252; pack_and_hash_keys, pack.cu:144-214) with:
+//   build  - the build side arrives sorted by its key word (the high word of
+//            the packed row), so every distinct key is one contiguous run.
+//            One selection pass extracts (run key, run start); an
+//            open-addressing table in HBM (8-byte slots, linear probing,
+//            Fibonacci hashing, load <= 0.5) maps key -> run.  Keys are
+//            compared exactly, so colliding hashes cannot produce matches
+//            (join_collision_test.rs:19-194).
+//   probe  - two launches.  count: every probe row looks up its run and a
+//            tile total is written.  emit: after a scan of the tile totals,
+//            each wave expands its 64 rows' runs cooperatively: lane j of a
+//            round writes output j, j+64, ... of the wave, found by a
+//            64-entry binary search over the per-row prefix in LDS, so
+//            writes are contiguous across lanes and a hot key's long run is
+//            shared by all lanes instead of serialising one thread.
+//            The projection is fused into the emit.
+#include "internal.hpp"
+
+namespace xh {
+
+namespace {
+
+constexpr int JB = 256;      // block
+constexpr int JITEMS = 16;   // probe rows per thread
+constexpr int JWAVES = JB / WAVE;
+constexpr int JTILE = JB * JITEMS;
+
+__device__ __forceinline__ uint64_t hash_slot(uint32_t key, int bits) {
+    return (uint64_t)(((uint64_t)key * 0x9E3779B97F4A7C15ull) >> (64 - bits));
+}
+
+__global__ void k_insert(const uint32_t *__restrict__ run_key, uint64_t nruns, unsigned long long *table,
+                         uint64_t mask, int bits) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t r = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; r < nruns; r += stride) {
+        uint32_t key = run_key[r];
+        unsigned long long v = ((unsigned long long)key << 32) | (unsigned long long)(r + 1);
+        uint64_t h = hash_slot(key, bits);
+        for (;;) {
+            unsigned long long old = atomicCAS(&table[h], 0ull, v);
+            if (old == 0ull) break;
+            h = (h + 1) & mask;
+        }
+    }
+}
+
+__global__ void k_set_u64(uint64_t *p, uint64_t v) { *p = v; }
+
+__device__ __forceinline__ bool lookup_run(const unsigned long long *__restrict__ table, uint64_t mask, int bits,
+                                           uint32_t key, uint32_t *run) {
+    uint64_t h = hash_slot(key, bits);
+    for (;;) {
+        unsigned long long s = table[h];
+        if (s == 0ull) return false;
+        if ((uint32_t)(s >> 32) == key) {
+            *run = (uint32_t)s - 1u;
+            return true;
+        }
+        h = (h + 1) & mask;
+    }
+}
+
+struct ProbeArgs {
+    const uint64_t *probe;
+    uint64_t n;
+    int pcol;  // 0: key = high word of the probe row, 1: low word
+    const unsigned long long *table;
+    uint64_t mask;
+    int bits;
+    const uint64_t *run_start;
+    const uint32_t *payload;
+};
+
+__device__ __forceinline__ uint64_t probe_count(const ProbeArgs &a, uint64_t row, uint64_t *start) {
+    uint32_t key = a.pcol ? (uint32_t)row : (uint32_t)(row >> 32);
+    uint32_t run;
+    if (!lookup_run(a.table, a.mask, a.bits, key, &run)) {
+        *start = 0;
+        return 0;
+    }
+    uint64_t s = a.run_start[run];
+    *start = s;
+    return a.run_start[run + 1] - s;
+}
+
+__global__ __launch_bounds__(JB) void k_probe_count(ProbeArgs a, uint64_t *__restrict__ tile_cnt) {
+    __shared__ uint64_t s_part[JWAVES];
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
+    const uint64_t wbase = (uint64_t)blockIdx.x * JTILE + (uint64_t)wave * (JITEMS * WAVE);
+    uint64_t acc = 0;
+#pragma unroll 4
+    for (int r = 0; r < JITEMS; ++r) {
+        uint64_t idx = wbase + (uint64_t)r * WAVE + lane;
+        if (idx < a.n) {
+            uint64_t st;
+            acc += probe_count(a, a.probe[idx], &st);
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, WAVE);
+    if (lane == 0) s_part[wave] = acc;
+    __syncthreads();
+    if (tid == 0) {
+        uint64_t t = 0;
+        for (int w = 0; w < JWAVES; ++w) t += s_part[w];
+        tile_cnt[blockIdx.x] = t;
+    }
+}
+
+// single-block exclusive scan of a u64 array; total -> *total
+__global__ __launch_bounds__(1024) void k_scan_small(uint64_t *a, uint64_t n, uint64_t *total) {
+    __shared__ uint64_t s_w[16];
+    __shared__ uint64_t s_carry;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid == 0) s_carry = 0;
+    __syncthreads();
+    for (uint64_t base = 0; base < n; base += 1024) {
+        uint64_t i = base + tid;
+        uint64_t v = i < n ? a[i] : 0;
+        uint64_t x = v;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            uint64_t t = __shfl_up(x, o, 64);
+            if (lane >= o) x += t;
+        }
+        if (lane == 63) s_w[wave] = x;
+        __syncthreads();
+        uint64_t wpre = 0, tot = 0;
+        for (int w = 0; w < 16; ++w) {
+            if (w < wave) wpre += s_w[w];
+            tot += s_w[w];
+        }
+        uint64_t carry = s_carry;
+        if (i < n) a[i] = carry + wpre + x - v;
+        __syncthreads();
+        if (tid == 0) s_carry = carry + tot;
+        __syncthreads();
+    }
+    if (tid == 0) *total = s_carry;
+}
+
+// Output spec: up to 4 selected values among v0 = probe.c0, v1 = probe.c1,
+// v2 = build key, v3 = build payload, packed per the relation layout.
+struct OutSpec {
+    int arity;   // 1..4
+    int oc[4];
+};
+__device__ __forceinline__ void make_words(const OutSpec &o, const uint32_t v[4], uint64_t *w0, uint64_t *w1) {
+    if (o.arity == 1) {
+        *w0 = v[o.oc[0]];
+        *w1 = 0;
+        return;
+    }
+    *w0 = ((uint64_t)v[o.oc[0]] << 32) | v[o.oc[1]];
+    if (o.arity == 3) *w1 = (uint64_t)v[o.oc[2]] << 32;
+    else if (o.arity == 4) *w1 = ((uint64_t)v[o.oc[2]] << 32) | v[o.oc[3]];
+    else *w1 = 0;
+}
+
+__global__ __launch_bounds__(JB) void k_probe_emit(ProbeArgs a, const uint64_t *__restrict__ tile_off, OutSpec spec,
+                                                   uint64_t *__restrict__ out0, uint64_t *__restrict__ out1) {
+    __shared__ uint64_t s_wtot[JWAVES];
+    __shared__ uint64_t s_ex[JWAVES][WAVE + 1];
+    __shared__ uint64_t s_row[JWAVES][WAVE];
+    __shared__ uint64_t s_st[JWAVES][WAVE];
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
+    const uint64_t wbase = (uint64_t)blockIdx.x * JTILE + (uint64_t)wave * (JITEMS * WAVE);
+
+    // pass 1 over this wave's rows: total outputs of the wave
+    uint64_t acc = 0;
+#pragma unroll 4
+    for (int r = 0; r < JITEMS; ++r) {
+        uint64_t idx = wbase + (uint64_t)r * WAVE + lane;
+        if (idx < a.n) {
+            uint64_t st;
+            acc += probe_count(a, a.probe[idx], &st);
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, WAVE);
+    if (lane == 0) s_wtot[wave] = acc;
+    __syncthreads();
+    uint64_t base = tile_off[blockIdx.x];
+    for (int w = 0; w < wave; ++w) base += s_wtot[w];
+
+    // pass 2: expand round by round
+    for (int r = 0; r < JITEMS; ++r) {
+        uint64_t idx = wbase + (uint64_t)r * WAVE + lane;
+        uint64_t row = 0, st = 0, c = 0;
+        if (idx < a.n) {
+            row = a.probe[idx];
+            c = probe_count(a, row, &st);
+        }
+        uint64_t x = c;
+#pragma unroll
+        for (int o = 1; o < WAVE; o <<= 1) {
+            uint64_t t = __shfl_up(x, o, WAVE);
+            if (lane >= o) x += t;
+        }
+        uint64_t total = __shfl(x, WAVE - 1, WAVE);
+        if (total == 0) continue;
+        s_ex[wave][lane] = x - c;
+        s_row[wave][lane] = row;
+        s_st[wave][lane] = st;
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        for (uint64_t j = lane; j < total; j += WAVE) {
+            // largest s with ex[s] <= j
+            int lo = 0, hi = WAVE - 1;
+            while (lo < hi) {
+                int mid = (lo + hi + 1) >> 1;
+                if (s_ex[wave][mid] <= j) lo = mid; else hi = mid - 1;
+            }
+            uint64_t prow = s_row[wave][lo];
+            uint64_t bpos = s_st[wave][lo] + (j - s_ex[wave][lo]);
+            uint32_t v[4];
+            v[0] = (uint32_t)(prow >> 32);
+            v[1] = (uint32_t)prow;
+            v[2] = a.pcol ? (uint32_t)prow : (uint32_t)(prow >> 32);
+            v[3] = a.payload ? a.payload[bpos] : 0u;
+            uint64_t w0, w1;
+            make_words(spec, v, &w0, &w1);
+            out0[base + j] = w0;
+            if (out1) out1[base + j] = w1;
+        }
+        base += total;
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    }
+}
+
+// semi / anti: flag = key found (semi) or not found (anti)
+__global__ void k_match_flags(ProbeArgs a, int want, uint8_t *__restrict__ flags) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.n; i += stride) {
+        uint64_t row = a.probe[i];
+        uint32_t key = a.pcol ? (uint32_t)row : (uint32_t)(row >> 32);
+        uint32_t run;
+        bool hit = lookup_run(a.table, a.mask, a.bits, key, &run);
+        flags[i] = (uint8_t)(hit == (want != 0));
+    }
+}
+
+}  // namespace
+
+void build_run_index(Ctx *ctx, const uint64_t *sorted_keys, uint64_t n, RunIndex &ix) {
+    ix.run_key = Buf<uint32_t>(ctx, n ? n : 1);
+    ix.run_start = Buf<uint64_t>(ctx, n + 1);
+    Buf<uint64_t> cnt(ctx, 1);
+    select_runs(ctx, sorted_keys, n, ix.run_key.p, ix.run_start.p, cnt.p);
+    ctx->read_scalars(cnt.p, 1);
+    ix.nruns = ctx->host_scalars[0];
+    XH_REQUIRE(ix.nruns < 0xFFFFFFFFull, XLOG_HIP_CAPACITY_OVERFLOW, "join build: too many distinct keys");
+    hipLaunchKernelGGL(k_set_u64, dim3(1), dim3(1), 0, ctx->stream, ix.run_start.p + ix.nruns, n);
+    XH_CHECK_HIP(hipGetLastError());
+    int bits = 10;
+    while ((1ull << bits) < 2 * ix.nruns) ++bits;
+    uint64_t slots = 1ull << bits;
+    ix.table = Buf<unsigned long long>(ctx, slots);
+    ix.table_mask = slots - 1;
+    fill_u64(ctx, reinterpret_cast<uint64_t *>(ix.table.p), 0ull, slots);
+    if (ix.nruns)
+        hipLaunchKernelGGL(k_insert, dim3(grid_for(ix.nruns, 256, 16384)), dim3(256), 0, ctx->stream, ix.run_key.p,
+                           ix.nruns, ix.table.p, ix.table_mask, bits);
+    XH_CHECK_HIP(hipGetLastError());
+}
+
+static int table_bits(const RunIndex &ix) {
+    int bits = 0;
+    while ((1ull << bits) < ix.table_mask + 1) ++bits;
+    return bits;
+}
+
+uint64_t join_probe_general(Ctx *ctx, const uint64_t *probe, uint64_t n, int pcol, const RunIndex &ix,
+                            const uint32_t *payload, int out_arity, const int oc[4], uint64_t **out0,
+                            uint64_t **out1) {
+    *out0 = nullptr;
+    if (out1) *out1 = nullptr;
+    if (n == 0 || ix.nruns == 0) return 0;
+    ProbeArgs a{probe, n, pcol, ix.table.p, ix.table_mask, table_bits(ix), ix.run_start.p, payload};
+    uint64_t tiles = (n + JTILE - 1) / JTILE;
+    XH_REQUIRE(tiles < (1ull << 31), XLOG_HIP_CAPACITY_OVERFLOW, "join probe: input too large");
+    Buf<uint64_t> toff(ctx, tiles + 1);
+    {
+        Prof prof(ctx, XLOG_HIP_KERNEL_PROBE_COUNT, 8.0 * (double)n);
+        hipLaunchKernelGGL(k_probe_count, dim3((unsigned)tiles), dim3(JB), 0, ctx->stream, a, toff.p);
+        XH_CHECK_HIP(hipGetLastError());
+    }
+    hipLaunchKernelGGL(k_scan_small, dim3(1), dim3(1024), 0, ctx->stream, toff.p, tiles, toff.p + tiles);
+    XH_CHECK_HIP(hipGetLastError());
+    ctx->read_scalars(toff.p + tiles, 1);
+    uint64_t total = ctx->host_scalars[0];
+    if (total == 0) return 0;
+    uint64_t *o0 = static_cast<uint64_t *>(ctx->alloc(total * sizeof(uint64_t)));
+    uint64_t *o1 = (out_arity > 2) ? static_cast<uint64_t *>(ctx->alloc(total * sizeof(uint64_t))) : nullptr;
+    OutSpec spec{out_arity, {oc[0], oc[1], oc[2], oc[3]}};
+    {
+        // probe row 8 B + slot/run 16 B per probe row; payload 4 B + output 8 B per match
+        Prof prof(ctx, XLOG_HIP_KERNEL_PROBE_EMIT,
+                  24.0 * (double)n + (4.0 + 8.0 * (out_arity > 2 ? 2 : 1)) * (double)total);
+        hipLaunchKernelGGL(k_probe_emit, dim3((unsigned)tiles), dim3(JB), 0, ctx->stream, a, toff.p, spec, o0, o1);
+        XH_CHECK_HIP(hipGetLastError());
+    }
+    *out0 = o0;
+    if (out1) *out1 = o1;
+    return total;
+}
+
+uint64_t join_probe_project(Ctx *ctx, const uint64_t *probe, uint64_t n, int pcol, const RunIndex &ix,
+                            const uint32_t *payload, int oc0, int oc1, uint64_t **out) {
+    int oc[4] = {oc0, oc1, 0, 0};
+    return join_probe_general(ctx, probe, n, pcol, ix, payload, 2, oc, out, nullptr);
+}
+
+void join_match_flags(Ctx *ctx, const uint64_t *probe, uint64_t n, int pcol, const RunIndex &ix, int want,
+                      uint8_t *flags) {
+    if (n == 0) return;
+    ProbeArgs a{probe, n, pcol, ix.table.p, ix.table_mask, table_bits(ix), ix.run_start.p, nullptr};
+    hipLaunchKernelGGL(k_match_flags, dim3(grid_for(n, 256, 16384)), dim3(256), 0, ctx->stream, a, want, flags);
+    XH_CHECK_HIP(hipGetLastError());
+}
+
+}  // namespace xh
+
+namespace xh {
+void scan_u64_small(Ctx *ctx, uint64_t *a, uint64_t n, uint64_t *total) {
+    hipLaunchKernelGGL(k_scan_small, dim3(1), dim3(1024), 0, ctx->stream, a, n, total);
+    XH_CHECK_HIP(hipGetLastError());
+}
+}  // namespace xh

@@ -1,0 +1,404 @@
+// Stream compaction, adjacent-compare dedup, sorted set difference and
+// merge-path merge for gfx950.
+//
+// Replaces, on sorted packed u64 keys:
+//   - mark_unique_full_row_bytewise + scan + compact_bytes_by_mask
+//     (kernels/dedup.cu:306-345, scan.cu:133-270, filter.cu:902-942;
+//     relational.rs:1558-1677) with ONE pass: flags, per-tile count,
+//     decoupled look-back for the tile's output offset, ordered write;
+//   - diff_via_deterministic_set's binary-search mark + scan + compact
+//     (relational.rs:1311-1428, dedup.cu:515-565) with the same pass whose
+//     flag is "unique and not in B", where each tile first narrows B to the
+//     window spanned by its own first and last key;
+//   - union_gpu's concat + full re-sort (relational.rs:822-999) with a
+//     merge-path merge of the two sorted inputs.
+#include "internal.hpp"
+
+namespace xh {
+
+namespace {
+
+constexpr int SEL_BLOCK = 256;
+constexpr int SEL_ITEMS = 16;
+constexpr int SEL_WAVES = SEL_BLOCK / WAVE;
+constexpr int SEL_TILE = SEL_BLOCK * SEL_ITEMS;
+
+// look-back status word: [63:40] epoch, [39] inclusive, [38:0] value
+constexpr uint64_t LB_INC = 1ull << 39;
+constexpr uint64_t LB_VAL = LB_INC - 1;
+
+__device__ __forceinline__ uint64_t lb_load(const uint64_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void lb_store(uint64_t *p, uint64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+    return v;
+}
+
+// Exclusive prefix of the tile aggregates before `tile`, computed by one full
+// wave that inspects 64 predecessors at a time.
+__device__ uint64_t lookback_wave(const uint64_t *status, uint64_t tile, uint64_t epoch_tag, int lane) {
+    uint64_t prefix = 0;
+    int64_t j = (int64_t)tile - 1;
+    while (j >= 0) {
+        int64_t idx = j - lane;
+        bool ready, inc;
+        uint64_t val;
+        if (idx >= 0) {
+            uint64_t s = lb_load(status + idx);
+            ready = (s & ~(LB_INC | LB_VAL)) == epoch_tag;
+            inc = ready && (s & LB_INC);
+            val = ready ? (s & LB_VAL) : 0;
+        } else {
+            ready = true; inc = true; val = 0;
+        }
+        uint64_t inc_mask = __ballot(inc);
+        uint64_t nready = __ballot(!ready);
+        if (inc_mask) {
+            int f = __builtin_ctzll(inc_mask);
+            uint64_t upto = (f == 63) ? ~0ull : ((2ull << f) - 1ull);
+            if (nready & upto) continue;  // spin until the window up to the closest inclusive entry is ready
+            prefix += wave_sum_u64(lane <= f ? val : 0ull);
+            break;
+        }
+        if (nready) continue;
+        prefix += wave_sum_u64(val);
+        j -= WAVE;
+    }
+    return prefix;
+}
+
+// Generic single-pass selection.  Sel supplies:
+//   __device__ void setup(uint64_t tile_first_idx, uint64_t tile_last_idx, uint64_t *smem)  (thread 0)
+//   __device__ bool flag(uint64_t idx, uint64_t key, const uint64_t *smem)
+//   __device__ void emit(uint64_t pos, uint64_t idx, uint64_t key)
+template <class Sel>
+__global__ __launch_bounds__(SEL_BLOCK) void k_select(const uint64_t *__restrict__ in, uint64_t n, Sel sel,
+                                                      uint64_t *__restrict__ d_count, uint64_t *status,
+                                                      uint64_t epoch_tag, unsigned long long *ticket,
+                                                      unsigned long long ticket_base, uint64_t ntiles) {
+    __shared__ uint64_t s_tile;
+    __shared__ uint64_t s_prefix;
+    __shared__ uint32_t s_wc[SEL_WAVES];
+    __shared__ uint64_t s_sel[4];
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
+    if (tid == 0) {
+        uint64_t t = atomicAdd(ticket, 1ull) - ticket_base;
+        s_tile = t;
+        uint64_t first = t * SEL_TILE, last = first + SEL_TILE;
+        if (last > n) last = n;
+        sel.setup(first, last - 1, s_sel);
+    }
+    __syncthreads();
+    const uint64_t tile = s_tile;
+    const uint64_t wbase = tile * SEL_TILE + (uint64_t)wave * (SEL_ITEMS * WAVE);
+    const uint64_t lt_mask = (1ull << lane) - 1ull;
+    uint64_t k[SEL_ITEMS];
+    uint64_t fl = 0;  // bit r = flag of item r
+    uint32_t wc = 0;
+#pragma unroll
+    for (int r = 0; r < SEL_ITEMS; ++r) {
+        uint64_t idx = wbase + (uint64_t)r * WAVE + lane;
+        bool f = false;
+        if (idx < n) {
+            k[r] = in[idx];
+            f = sel.flag(idx, k[r], s_sel);
+        } else {
+            k[r] = 0;
+        }
+        if (f) fl |= 1ull << r;
+        wc += (uint32_t)__popcll(__ballot(f));
+    }
+    if (lane == 0) s_wc[wave] = wc;
+    __syncthreads();
+    uint64_t tile_cnt = 0, wpre = 0;
+#pragma unroll
+    for (int w = 0; w < SEL_WAVES; ++w) {
+        if (w < wave) wpre += s_wc[w];
+        tile_cnt += s_wc[w];
+    }
+    if (wave == 0) {
+        if (tid == 0) lb_store(status + tile, epoch_tag | (tile == 0 ? LB_INC : 0ull) | tile_cnt);
+        uint64_t prefix = tile ? lookback_wave(status, tile, epoch_tag, lane) : 0ull;
+        if (tid == 0) {
+            if (tile) lb_store(status + tile, epoch_tag | LB_INC | (prefix + tile_cnt));
+            s_prefix = prefix;
+            if (tile == ntiles - 1) *d_count = prefix + tile_cnt;
+        }
+    }
+    __syncthreads();
+    uint64_t pos = s_prefix + wpre;
+#pragma unroll
+    for (int r = 0; r < SEL_ITEMS; ++r) {
+        bool f = (fl >> r) & 1ull;
+        uint64_t m = __ballot(f);
+        if (f) sel.emit(pos + (uint64_t)__popcll(m & lt_mask), wbase + (uint64_t)r * WAVE + lane, k[r]);
+        pos += (uint64_t)__popcll(m);
+    }
+}
+
+__device__ __forceinline__ uint64_t lower_bound_u64(const uint64_t *a, uint64_t lo, uint64_t hi, uint64_t key) {
+    while (lo < hi) {
+        uint64_t mid = lo + ((hi - lo) >> 1);
+        if (a[mid] < key) lo = mid + 1; else hi = mid;
+    }
+    return lo;
+}
+__device__ __forceinline__ uint64_t upper_bound_u64(const uint64_t *a, uint64_t lo, uint64_t hi, uint64_t key) {
+    while (lo < hi) {
+        uint64_t mid = lo + ((hi - lo) >> 1);
+        if (a[mid] <= key) lo = mid + 1; else hi = mid;
+    }
+    return lo;
+}
+
+struct SelUnique {
+    const uint64_t *in;
+    uint64_t *out;
+    __device__ void setup(uint64_t, uint64_t, uint64_t *) const {}
+    __device__ bool flag(uint64_t idx, uint64_t key, const uint64_t *) const {
+        return idx == 0 || in[idx - 1] != key;
+    }
+    __device__ void emit(uint64_t pos, uint64_t, uint64_t key) const { out[pos] = key; }
+};
+
+// unique (optional) and not a member of sorted b
+template <bool UNIQ>
+struct SelDiff {
+    const uint64_t *in;
+    const uint64_t *b;
+    uint64_t nb;
+    uint64_t *out;
+    __device__ void setup(uint64_t first, uint64_t last, uint64_t *s) const {
+        s[0] = lower_bound_u64(b, 0, nb, in[first]);
+        s[1] = upper_bound_u64(b, s[0], nb, in[last]);
+    }
+    __device__ bool flag(uint64_t idx, uint64_t key, const uint64_t *s) const {
+        if (UNIQ && idx != 0 && in[idx - 1] == key) return false;
+        uint64_t p = lower_bound_u64(b, s[0], s[1], key);
+        return !(p < s[1] && b[p] == key);
+    }
+    __device__ void emit(uint64_t pos, uint64_t, uint64_t key) const { out[pos] = key; }
+};
+
+struct SelFlags {
+    const uint8_t *flags;
+    uint64_t *out;
+    __device__ void setup(uint64_t, uint64_t, uint64_t *) const {}
+    __device__ bool flag(uint64_t idx, uint64_t, const uint64_t *) const { return flags[idx] != 0; }
+    __device__ void emit(uint64_t pos, uint64_t, uint64_t key) const { out[pos] = key; }
+};
+
+// run starts of the high word (join build)
+struct SelRuns {
+    const uint64_t *in;
+    uint32_t *run_key;
+    uint64_t *run_start;
+    __device__ void setup(uint64_t, uint64_t, uint64_t *) const {}
+    __device__ bool flag(uint64_t idx, uint64_t key, const uint64_t *) const {
+        return idx == 0 || (in[idx - 1] >> 32) != (key >> 32);
+    }
+    __device__ void emit(uint64_t pos, uint64_t idx, uint64_t key) const {
+        run_key[pos] = (uint32_t)(key >> 32);
+        run_start[pos] = idx;
+    }
+};
+
+// ---- merge path -----------------------------------------------------------
+constexpr int MRG_BLOCK = 256;
+constexpr int MRG_ITEMS = 8;
+constexpr int MRG_TILE = MRG_BLOCK * MRG_ITEMS;
+
+// number of a-elements among the first d outputs of the stable merge (a first on ties)
+__device__ __forceinline__ uint64_t merge_path(const uint64_t *a, uint64_t na, const uint64_t *b, uint64_t nb,
+                                               uint64_t d) {
+    uint64_t lo = d > nb ? d - nb : 0, hi = d < na ? d : na;
+    while (lo < hi) {
+        uint64_t mid = lo + ((hi - lo) >> 1);
+        if (a[mid] <= b[d - 1 - mid]) lo = mid + 1; else hi = mid;
+    }
+    return lo;
+}
+
+__global__ __launch_bounds__(MRG_BLOCK) void k_merge(const uint64_t *__restrict__ a, uint64_t na,
+                                                     const uint64_t *__restrict__ b, uint64_t nb,
+                                                     uint64_t *__restrict__ out) {
+    __shared__ uint64_t s[MRG_TILE];
+    __shared__ uint64_t s_split[2];
+    const int tid = threadIdx.x;
+    const uint64_t total = na + nb;
+    const uint64_t d0 = (uint64_t)blockIdx.x * MRG_TILE;
+    const uint64_t d1 = (d0 + MRG_TILE < total) ? d0 + MRG_TILE : total;
+    if (tid < 2) s_split[tid] = merge_path(a, na, b, nb, tid == 0 ? d0 : d1);
+    __syncthreads();
+    const uint64_t a0 = s_split[0], a1 = s_split[1];
+    const uint32_t la = (uint32_t)(a1 - a0), len = (uint32_t)(d1 - d0), lb = len - la;
+    const uint64_t b0 = d0 - a0;
+    for (uint32_t i = tid; i < la; i += MRG_BLOCK) s[i] = a[a0 + i];
+    for (uint32_t i = tid; i < lb; i += MRG_BLOCK) s[la + i] = b[b0 + i];
+    __syncthreads();
+    const uint64_t *sa = s, *sb = s + la;
+    uint32_t td = tid * MRG_ITEMS;
+    uint64_t r[MRG_ITEMS];
+    uint32_t cnt = 0;
+    if (td < len) {
+        uint32_t ia = (uint32_t)merge_path(sa, la, sb, lb, td);
+        uint32_t ib = td - ia;
+#pragma unroll
+        for (int j = 0; j < MRG_ITEMS; ++j) {
+            if (td + j < len) {
+                bool take_a = ib >= lb || (ia < la && sa[ia] <= sb[ib]);
+                r[j] = take_a ? sa[ia] : sb[ib];
+                ia += take_a; ib += !take_a;
+                ++cnt;
+            }
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < MRG_ITEMS; ++j)
+        if ((uint32_t)j < cnt) s[td + j] = r[j];
+    __syncthreads();
+    for (uint32_t i = tid; i < len; i += MRG_BLOCK) out[d0 + i] = s[i];
+}
+
+// ---- helpers --------------------------------------------------------------
+__global__ void k_pack(const uint32_t *__restrict__ c0, const uint32_t *__restrict__ c1, uint64_t n,
+                       uint64_t *__restrict__ out) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        out[i] = ((uint64_t)c0[i] << 32) | (c1 ? c1[i] : 0u);
+}
+__global__ void k_unpack(const uint64_t *__restrict__ w, int hi, uint64_t n, uint32_t *__restrict__ out) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        out[i] = hi ? (uint32_t)(w[i] >> 32) : (uint32_t)w[i];
+}
+__global__ void k_swap(const uint64_t *__restrict__ in, uint64_t n, uint64_t *__restrict__ out) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        uint64_t k = in[i];
+        out[i] = (k << 32) | (k >> 32);
+    }
+}
+__global__ void k_unsorted(const uint64_t *__restrict__ k, uint64_t n, int strict, uint32_t *flag) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i + 1 < n; i += stride) {
+        bool bad = strict ? !(k[i] < k[i + 1]) : (k[i] > k[i + 1]);
+        if (bad) *flag = 1u;
+    }
+}
+
+}  // namespace
+
+// ---- host wrappers ----------------------------------------------------------
+
+struct SelectState {
+    uint64_t *status = nullptr;
+    uint64_t cap = 0;
+    uint64_t epoch = 0;
+};
+static std::map<Ctx *, SelectState> g_sel_state;
+static std::mutex g_sel_mu;
+
+void select_state_release(Ctx *ctx) {
+    std::lock_guard<std::mutex> g(g_sel_mu);
+    auto it = g_sel_state.find(ctx);
+    if (it == g_sel_state.end()) return;
+    if (it->second.status) ctx->free(it->second.status);
+    g_sel_state.erase(it);
+}
+
+// status buffer with >= tiles entries and a fresh epoch tag
+static uint64_t *select_status(Ctx *ctx, uint64_t tiles, uint64_t *epoch_tag) {
+    std::lock_guard<std::mutex> g(g_sel_mu);
+    SelectState &st = g_sel_state[ctx];
+    if (tiles > st.cap || st.epoch + 1 >= (1ull << 24)) {
+        uint64_t cap = tiles > st.cap ? (tiles < 4096 ? 4096 : tiles + tiles / 4) : st.cap;
+        if (st.status) ctx->free(st.status);
+        st.status = static_cast<uint64_t *>(ctx->alloc(cap * sizeof(uint64_t)));
+        fill_u64(ctx, st.status, 0ull, cap);
+        st.cap = cap;
+        st.epoch = 0;
+    }
+    st.epoch += 1;
+    *epoch_tag = st.epoch << 40;
+    return st.status;
+}
+
+template <class Sel>
+static void run_select(Ctx *ctx, const uint64_t *in, uint64_t n, const Sel &sel, uint64_t *d_count) {
+    if (n == 0) {
+        fill_u64(ctx, d_count, 0ull, 1);
+        return;
+    }
+    uint64_t tiles = (n + SEL_TILE - 1) / SEL_TILE;
+    XH_REQUIRE(tiles < (1ull << 31), XLOG_HIP_CAPACITY_OVERFLOW, "select: input too large");
+    uint64_t tag;
+    uint64_t *status = select_status(ctx, tiles, &tag);
+    unsigned long long tb = ctx->take_tickets(1, tiles);
+    Prof prof(ctx, XLOG_HIP_KERNEL_SELECT, 8.0 * (double)n);
+    hipLaunchKernelGGL(k_select<Sel>, dim3((unsigned)tiles), dim3(SEL_BLOCK), 0, ctx->stream, in, n, sel, d_count,
+                       status, tag, ctx->tickets + 1, tb, tiles);
+    XH_CHECK_HIP(hipGetLastError());
+}
+
+void select_unique(Ctx *ctx, const uint64_t *k, uint64_t n, uint64_t *out, uint64_t *d_count) {
+    run_select(ctx, k, n, SelUnique{k, out}, d_count);
+}
+void select_unique_diff(Ctx *ctx, const uint64_t *k, uint64_t n, const uint64_t *b, uint64_t nb, uint64_t *out,
+                        uint64_t *d_count) {
+    if (nb == 0) { select_unique(ctx, k, n, out, d_count); return; }
+    run_select(ctx, k, n, SelDiff<true>{k, b, nb, out}, d_count);
+}
+void select_flags(Ctx *ctx, const uint64_t *k, const uint8_t *flags, uint64_t n, uint64_t *out, uint64_t *d_count) {
+    run_select(ctx, k, n, SelFlags{flags, out}, d_count);
+}
+void select_runs(Ctx *ctx, const uint64_t *k, uint64_t n, uint32_t *run_key, uint64_t *run_start, uint64_t *d_count) {
+    run_select(ctx, k, n, SelRuns{k, run_key, run_start}, d_count);
+}
+
+void merge_sorted(Ctx *ctx, const uint64_t *a, uint64_t na, const uint64_t *b, uint64_t nb, uint64_t *out) {
+    uint64_t total = na + nb;
+    if (!total) return;
+    uint64_t tiles = (total + MRG_TILE - 1) / MRG_TILE;
+    XH_REQUIRE(tiles < (1ull << 31), XLOG_HIP_CAPACITY_OVERFLOW, "merge: input too large");
+    Prof prof(ctx, XLOG_HIP_KERNEL_MERGE, 16.0 * (double)total);
+    hipLaunchKernelGGL(k_merge, dim3((unsigned)tiles), dim3(MRG_BLOCK), 0, ctx->stream, a, na, b, nb, out);
+    XH_CHECK_HIP(hipGetLastError());
+}
+
+void pack_columns(Ctx *ctx, const uint32_t *c0, const uint32_t *c1, uint64_t n, uint64_t *out) {
+    if (!n) return;
+    hipLaunchKernelGGL(k_pack, dim3(grid_for(n, 256, 16384)), dim3(256), 0, ctx->stream, c0, c1, n, out);
+    XH_CHECK_HIP(hipGetLastError());
+}
+void unpack_column(Ctx *ctx, const uint64_t *w, int hi, uint64_t n, uint32_t *out) {
+    if (!n) return;
+    hipLaunchKernelGGL(k_unpack, dim3(grid_for(n, 256, 16384)), dim3(256), 0, ctx->stream, w, hi, n, out);
+    XH_CHECK_HIP(hipGetLastError());
+}
+void swap_words(Ctx *ctx, const uint64_t *in, uint64_t n, uint64_t *out) {
+    if (!n) return;
+    hipLaunchKernelGGL(k_swap, dim3(grid_for(n, 256, 16384)), dim3(256), 0, ctx->stream, in, n, out);
+    XH_CHECK_HIP(hipGetLastError());
+}
+void low_words(Ctx *ctx, const uint64_t *in, uint64_t n, uint32_t *out) { unpack_column(ctx, in, 0, n, out); }
+
+int is_sorted_u64(Ctx *ctx, const uint64_t *k, uint64_t n, int strict) {
+    if (n < 2) return 1;
+    Buf<uint32_t> flag(ctx, 2);
+    fill_u32(ctx, flag.p, 0u, 1);
+    hipLaunchKernelGGL(k_unsorted, dim3(grid_for(n, 256, 16384)), dim3(256), 0, ctx->stream, k, n, strict, flag.p);
+    XH_CHECK_HIP(hipGetLastError());
+    uint32_t h = 0;
+    XH_CHECK_HIP(hipMemcpyAsync(&h, flag.p, sizeof(uint32_t), hipMemcpyDeviceToHost, ctx->stream));
+    ctx->sync();
+    return h == 0;
+}
+
+}  // namespace xh

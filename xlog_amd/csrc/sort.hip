@@ -1,0 +1,322 @@
+// LSD radix sort of packed u64 tuple keys for gfx950.
+//
+// Replaces the reference's 4-bit, 8-passes-per-u32-column sort
+// (crates/xlog-cuda/src/provider/relational.rs:1881-2357, kernels/sort.cu:28-264)
+// with a onesweep design:
+//   1. k_hist8: one read of the keys builds all eight 256-bin digit
+//      histograms in LDS; a digit whose histogram has a single non-empty bin
+//      is constant over the input and its pass is skipped.
+//   2. k_onesweep, once per remaining digit: a tile of TILE keys is ranked
+//      per wave with 64-lane ballot matching (stable), the tile's 256 digit
+//      counts are published and the exclusive prefix over earlier tiles is
+//      obtained by decoupled look-back, the tile is reordered by digit in
+//      LDS and written out so that consecutive lanes write consecutive
+//      addresses of a digit run.
+// Each pass reads and writes every key exactly once (16 B per key, plus the
+// optional u32 payload).  Tiles are ordered by an atomic ticket, so a tile
+// only ever waits for tiles that are already running.
+#include "internal.hpp"
+
+namespace xh {
+
+namespace {
+
+constexpr int SORT_BLOCK = 256;
+constexpr int SORT_ITEMS = 16;
+constexpr int SORT_WAVES = SORT_BLOCK / WAVE;
+constexpr int SORT_TILE = SORT_BLOCK * SORT_ITEMS;  // 4096 keys
+constexpr uint32_t ST_AGG = 1u << 30;
+constexpr uint32_t ST_INC = 2u << 30;
+constexpr uint32_t ST_VAL = (1u << 30) - 1;
+
+__device__ __forceinline__ uint32_t ld_status(const uint32_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_status(uint32_t *p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__global__ __launch_bounds__(256) void k_hist8(const uint64_t *__restrict__ keys, uint64_t n,
+                                               uint32_t *__restrict__ ghist) {
+    // two copies per digit position halve same-address LDS atomic collisions
+    __shared__ uint32_t h[2][8][256];
+    uint32_t *hf = &h[0][0][0];
+    for (int i = threadIdx.x; i < 2 * 8 * 256; i += blockDim.x) hf[i] = 0;
+    __syncthreads();
+    const int copy = (threadIdx.x >> 6) & 1;
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        uint64_t k = keys[i];
+#pragma unroll
+        for (int d = 0; d < 8; ++d) atomicAdd(&h[copy][d][(k >> (8 * d)) & 255], 1u);
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < 8 * 256; i += blockDim.x) {
+        uint32_t c = hf[i] + hf[i + 8 * 256];
+        if (c) atomicAdd(&ghist[i], c);
+    }
+}
+
+// exclusive scan of each of the 8 histograms -> offsets[8][256]
+__global__ void k_digit_offsets(const uint32_t *__restrict__ ghist, uint32_t *__restrict__ off) {
+    int d = threadIdx.x;
+    if (d < 8) {
+        uint32_t acc = 0;
+        for (int b = 0; b < 256; ++b) {
+            uint32_t c = ghist[d * 256 + b];
+            off[d * 256 + b] = acc;
+            acc += c;
+        }
+    }
+}
+
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v, int lane) {
+#pragma unroll
+    for (int o = 1; o < WAVE; o <<= 1) {
+        uint32_t t = __shfl_up(v, o, WAVE);
+        if (lane >= o) v += t;
+    }
+    return v;
+}
+
+template <bool HAS_VAL>
+__global__ __launch_bounds__(SORT_BLOCK) void k_onesweep(
+    const uint64_t *__restrict__ kin, uint64_t *__restrict__ kout, const uint32_t *__restrict__ vin,
+    uint32_t *__restrict__ vout, uint64_t n, int shift, const uint32_t *__restrict__ digit_off,
+    uint32_t *status, uint32_t *status_next, unsigned long long *ticket, unsigned long long ticket_base) {
+    __shared__ uint32_t s_tile;
+    __shared__ uint32_t s_wcnt[SORT_WAVES][256];
+    __shared__ uint32_t s_tstart[256];
+    __shared__ uint32_t s_gbase[256];
+    __shared__ uint32_t s_wsum[SORT_WAVES];
+    __shared__ uint64_t s_keys[SORT_TILE];
+    __shared__ uint32_t s_vals[HAS_VAL ? SORT_TILE : 1];
+
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
+    if (tid == 0) s_tile = (uint32_t)(atomicAdd(ticket, 1ull) - ticket_base);
+    for (int i = tid; i < SORT_WAVES * 256; i += SORT_BLOCK) (&s_wcnt[0][0])[i] = 0;
+    __syncthreads();
+    const uint32_t tile = s_tile;
+    const uint64_t wbase = (uint64_t)tile * SORT_TILE + (uint64_t)wave * (SORT_ITEMS * WAVE);
+    const uint64_t lt_mask = (1ull << lane) - 1ull;
+
+    uint64_t k[SORT_ITEMS];
+    uint32_t v[SORT_ITEMS];
+    uint32_t rank[SORT_ITEMS];
+#pragma unroll
+    for (int r = 0; r < SORT_ITEMS; ++r) {
+        uint64_t idx = wbase + (uint64_t)r * WAVE + lane;
+        bool valid = idx < n;
+        k[r] = valid ? kin[idx] : 0ull;
+        if (HAS_VAL) v[r] = valid ? vin[idx] : 0u;
+    }
+#pragma unroll
+    for (int r = 0; r < SORT_ITEMS; ++r) {
+        uint64_t idx = wbase + (uint64_t)r * WAVE + lane;
+        bool valid = idx < n;
+        uint32_t d = (uint32_t)(k[r] >> shift) & 255u;
+        uint64_t peers = __ballot(valid);
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            bool bit = (d >> b) & 1u;
+            uint64_t m = __ballot(bit);
+            peers &= bit ? m : ~m;
+        }
+        uint32_t below = (uint32_t)__popcll(peers & lt_mask);
+        int leader = valid ? (int)__builtin_ctzll(peers) : lane;
+        uint32_t old = 0;
+        if (valid && below == 0) {
+            old = s_wcnt[wave][d];
+            s_wcnt[wave][d] = old + (uint32_t)__popcll(peers);
+        }
+        old = (uint32_t)__shfl((int)old, leader, WAVE);
+        rank[r] = old + below;
+    }
+    __syncthreads();
+
+    // per digit: totals and exclusive prefix over waves (thread = digit)
+    const int d = tid;  // SORT_BLOCK == 256
+    uint32_t cnt = 0;
+#pragma unroll
+    for (int w = 0; w < SORT_WAVES; ++w) {
+        uint32_t c = s_wcnt[w][d];
+        s_wcnt[w][d] = cnt;
+        cnt += c;
+    }
+    // publish this tile's aggregate (or inclusive prefix for tile 0)
+    uint32_t *my = status + (uint64_t)tile * 256 + d;
+    st_status(my, (tile == 0 ? ST_INC : ST_AGG) | cnt);
+
+    // tile-local exclusive scan over the 256 digits
+    uint32_t incl = wave_incl_scan(cnt, lane);
+    if (lane == WAVE - 1) s_wsum[wave] = incl;
+    __syncthreads();
+    uint32_t wpre = 0;
+#pragma unroll
+    for (int w = 0; w < SORT_WAVES; ++w)
+        if (w < wave) wpre += s_wsum[w];
+    const uint32_t tstart = wpre + incl - cnt;
+    s_tstart[d] = tstart;
+
+    // decoupled look-back over earlier tiles for this digit
+    uint32_t prefix = 0;
+    if (tile > 0) {
+        int64_t j = (int64_t)tile - 1;
+        for (;;) {
+            uint32_t s = ld_status(status + (uint64_t)j * 256 + d);
+            uint32_t flag = s & ~ST_VAL;
+            if (flag == 0) continue;  // predecessor not published yet
+            prefix += s & ST_VAL;
+            if (flag == ST_INC) break;
+            --j;
+        }
+        st_status(my, ST_INC | (prefix + cnt));
+    }
+    s_gbase[d] = digit_off[d] + prefix - tstart;
+    // the next pass uses the other status buffer: clear this tile's slot there
+    status_next[(uint64_t)tile * 256 + d] = 0u;
+    __syncthreads();
+
+    // reorder the tile by digit in LDS
+#pragma unroll
+    for (int r = 0; r < SORT_ITEMS; ++r) {
+        uint64_t idx = wbase + (uint64_t)r * WAVE + lane;
+        if (idx < n) {
+            uint32_t dd = (uint32_t)(k[r] >> shift) & 255u;
+            uint32_t pos = s_tstart[dd] + s_wcnt[wave][dd] + rank[r];
+            s_keys[pos] = k[r];
+            if (HAS_VAL) s_vals[pos] = v[r];
+        }
+    }
+    __syncthreads();
+    const uint64_t t0 = (uint64_t)tile * SORT_TILE;
+    const uint32_t tn = (uint32_t)((n - t0) < (uint64_t)SORT_TILE ? (n - t0) : (uint64_t)SORT_TILE);
+    for (uint32_t i = tid; i < tn; i += SORT_BLOCK) {
+        uint64_t key = s_keys[i];
+        uint32_t dd = (uint32_t)(key >> shift) & 255u;
+        uint32_t o = s_gbase[dd] + i;
+        kout[o] = key;
+        if (HAS_VAL) vout[o] = s_vals[i];
+    }
+}
+
+__global__ void k_fill_u32(uint32_t *p, uint32_t v, uint64_t n) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = v;
+}
+__global__ void k_fill_u64(uint64_t *p, uint64_t v, uint64_t n) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = v;
+}
+
+}  // namespace
+
+void fill_u64(Ctx *ctx, uint64_t *p, uint64_t v, uint64_t n) {
+    if (!n) return;
+    hipLaunchKernelGGL(k_fill_u64, dim3(grid_for(n, 256, 8192)), dim3(256), 0, ctx->stream, p, v, n);
+    XH_CHECK_HIP(hipGetLastError());
+}
+void fill_u32(Ctx *ctx, uint32_t *p, uint32_t v, uint64_t n) {
+    if (!n) return;
+    hipLaunchKernelGGL(k_fill_u32, dim3(grid_for(n, 256, 8192)), dim3(256), 0, ctx->stream, p, v, n);
+    XH_CHECK_HIP(hipGetLastError());
+}
+
+// Look-back status buffers for the sort passes, kept per context.  Invariant
+// tracked on the host: dirty[b] = number of leading tiles of buffer b that may
+// hold non-zero entries.
+struct SortState {
+    uint32_t *status[2] = {nullptr, nullptr};
+    uint64_t tiles_cap = 0;
+    uint64_t dirty[2] = {0, 0};
+    uint32_t *hist = nullptr;  // 8*256 counts + 8*256 offsets
+};
+static std::map<Ctx *, SortState> g_sort_state;
+static std::mutex g_sort_mu;
+
+void sort_state_release(Ctx *ctx) {
+    std::lock_guard<std::mutex> g(g_sort_mu);
+    auto it = g_sort_state.find(ctx);
+    if (it == g_sort_state.end()) return;
+    if (it->second.status[0]) ctx->free(it->second.status[0]);
+    if (it->second.status[1]) ctx->free(it->second.status[1]);
+    if (it->second.hist) ctx->free(it->second.hist);
+    g_sort_state.erase(it);
+}
+
+static SortState &sort_state(Ctx *ctx, uint64_t tiles) {
+    std::lock_guard<std::mutex> g(g_sort_mu);
+    SortState &st = g_sort_state[ctx];
+    if (!st.hist) st.hist = static_cast<uint32_t *>(ctx->alloc(2 * 8 * 256 * sizeof(uint32_t)));
+    if (tiles > st.tiles_cap) {
+        uint64_t cap = tiles < 1024 ? 1024 : tiles + tiles / 4;
+        for (int b = 0; b < 2; ++b) {
+            if (st.status[b]) ctx->free(st.status[b]);
+            st.status[b] = static_cast<uint32_t *>(ctx->alloc(cap * 256 * sizeof(uint32_t)));
+            fill_u32(ctx, st.status[b], 0u, cap * 256);
+            st.dirty[b] = 0;
+        }
+        st.tiles_cap = cap;
+    }
+    return st;
+}
+
+int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **vals, uint32_t **vals_alt,
+                   uint64_t n) {
+    if (n < 2) return 0;
+    XH_REQUIRE(n < (1ull << 30), XLOG_HIP_CAPACITY_OVERFLOW,
+               "radix sort: a single sort call is limited to 2^30 - 1 keys");
+    const bool has_val = vals && *vals;
+    const uint64_t tiles = (n + SORT_TILE - 1) / SORT_TILE;
+    SortState &st = sort_state(ctx, tiles);
+    uint32_t *hist = st.hist, *off = st.hist + 8 * 256;
+
+    fill_u32(ctx, hist, 0u, 8 * 256);
+    unsigned hg = grid_for(n, 256, (unsigned)ctx->num_cus * 4);
+    {
+        Prof prof(ctx, XLOG_HIP_KERNEL_SORT_HIST, 8.0 * (double)n);
+        hipLaunchKernelGGL(k_hist8, dim3(hg), dim3(256), 0, ctx->stream, *keys, n, hist);
+    }
+    XH_CHECK_HIP(hipGetLastError());
+    hipLaunchKernelGGL(k_digit_offsets, dim3(1), dim3(64), 0, ctx->stream, hist, off);
+    XH_CHECK_HIP(hipGetLastError());
+    // host copy of the histograms decides which digit passes are needed
+    uint32_t h_hist[8 * 256];
+    XH_CHECK_HIP(hipMemcpyAsync(h_hist, hist, sizeof(h_hist), hipMemcpyDeviceToHost, ctx->stream));
+    ctx->sync();
+
+    int passes = 0;
+    int cur = 0;  // status buffer for the next pass
+    if (st.dirty[0] == 0) cur = 0; else if (st.dirty[1] == 0) cur = 1; else cur = 0;
+    for (int dgt = 0; dgt < 8; ++dgt) {
+        bool trivial = false;
+        for (int b = 0; b < 256; ++b)
+            if (h_hist[dgt * 256 + b] == n) { trivial = true; break; }
+        if (trivial) continue;
+        int nxt = 1 - cur;
+        if (st.dirty[cur]) {  // make the buffer this pass reads clean
+            fill_u32(ctx, st.status[cur], 0u, st.dirty[cur] * 256);
+            st.dirty[cur] = 0;
+        }
+        unsigned long long tb = ctx->take_tickets(0, tiles);
+        Prof prof(ctx, XLOG_HIP_KERNEL_SORT_PASS, (has_val ? 24.0 : 16.0) * (double)n);
+        if (has_val)
+            hipLaunchKernelGGL(k_onesweep<true>, dim3((unsigned)tiles), dim3(SORT_BLOCK), 0, ctx->stream, *keys,
+                               *keys_alt, *vals, *vals_alt, n, 8 * dgt, off + dgt * 256, st.status[cur],
+                               st.status[nxt], ctx->tickets + 0, tb);
+        else
+            hipLaunchKernelGGL(k_onesweep<false>, dim3((unsigned)tiles), dim3(SORT_BLOCK), 0, ctx->stream, *keys,
+                               *keys_alt, nullptr, nullptr, n, 8 * dgt, off + dgt * 256, st.status[cur],
+                               st.status[nxt], ctx->tickets + 0, tb);
+        XH_CHECK_HIP(hipGetLastError());
+        st.dirty[cur] = tiles;
+        if (st.dirty[nxt] <= tiles) st.dirty[nxt] = 0;
+        std::swap(*keys, *keys_alt);
+        if (has_val) std::swap(*vals, *vals_alt);
+        cur = nxt;
+        ++passes;
+    }
+    return passes;
+}
+
+}  // namespace xh

@@ -1,0 +1,253 @@
+// Dense factorized transitive-closure step for gfx950.
+//
+// The reference's factorized delta (fj_delta_novel_u32_recorded,
+// crates/xlog-cuda/src/provider/fj_delta.rs:117-490; kernels wcoj.cu:3811-3946)
+// computes  novel[x] = (U_{y in delta[x]} edge[y]) \ R[x]  with a
+// domain x domain bitmap, capped at a 2^14..2^16 domain
+// (wcoj_dispatch.rs:176-186).  Here the whole fixpoint state lives in
+// bitmaps sized for the MI355X's HBM: R, delta and next-delta are V x V bit
+// matrices (V = 32,768 -> 128 MiB each), and a per-row "non-empty" flag lets
+// a block skip a row of an empty delta without touching its bitmap.
+//
+// One iteration = one launch of k_tc_step, one block per source row x:
+//   acc     = OR over set bits y of delta[x] of the adjacency list of y  (LDS)
+//   new     = acc & ~R[x];  R[x] |= new;  next[x] = new
+//   count  += popcount(new)          (the only value read back per iteration)
+// The final relation is emitted row by row in (x, z) order, so it is sorted
+// and unique by construction.
+#include "internal.hpp"
+
+namespace xh {
+
+namespace {
+
+constexpr int TB = 256;
+
+__global__ void k_edges_to_bits(const uint64_t *__restrict__ edges, uint64_t m, uint64_t words,
+                                uint64_t *__restrict__ R, uint64_t *__restrict__ D) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < m; i += stride) {
+        uint64_t e = edges[i];
+        uint32_t x = (uint32_t)(e >> 32), z = (uint32_t)e;
+        uint64_t off = (uint64_t)x * words + (z >> 6);
+        unsigned long long bit = 1ull << (z & 63);
+        atomicOr((unsigned long long *)&R[off], bit);
+        atomicOr((unsigned long long *)&D[off], bit);
+    }
+}
+
+// row_ptr[v] = first index of sorted unique edges with source >= v
+__global__ void k_row_ptr(const uint64_t *__restrict__ edges, uint64_t m, uint32_t nv, uint64_t *__restrict__ row_ptr) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t v = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; v <= nv; v += stride) {
+        uint64_t key = v << 32, lo = 0, hi = m;
+        while (lo < hi) {
+            uint64_t mid = (lo + hi) >> 1;
+            if (edges[mid] < key) lo = mid + 1; else hi = mid;
+        }
+        row_ptr[v] = lo;
+    }
+}
+
+__global__ void k_adj(const uint64_t *__restrict__ edges, uint64_t m, uint32_t *__restrict__ adj) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < m; i += stride) adj[i] = (uint32_t)edges[i];
+}
+
+__global__ void k_seed_nz(const uint64_t *__restrict__ row_ptr, uint32_t nv, uint8_t *__restrict__ nz) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t v = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; v < nv; v += stride)
+        nz[v] = row_ptr[v + 1] > row_ptr[v];
+}
+
+// Dynamic LDS: `words` u64 accumulator words for the row.
+__global__ __launch_bounds__(TB) void k_tc_step(uint32_t nv, uint64_t words, const uint64_t *__restrict__ row_ptr,
+                                                const uint32_t *__restrict__ adj, uint64_t *__restrict__ R,
+                                                const uint64_t *__restrict__ D, uint64_t *__restrict__ N,
+                                                const uint8_t *__restrict__ nz_cur, uint8_t *__restrict__ nz_next,
+                                                unsigned long long *__restrict__ count) {
+    extern __shared__ uint64_t s_acc[];
+    __shared__ unsigned long long s_cnt;
+    const uint32_t x = blockIdx.x;
+    const int tid = threadIdx.x;
+    if (!nz_cur[x]) {
+        if (tid == 0) nz_next[x] = 0;
+        return;
+    }
+    for (uint64_t w = tid; w < words; w += TB) s_acc[w] = 0ull;
+    if (tid == 0) s_cnt = 0;
+    __syncthreads();
+    const uint64_t *drow = D + (uint64_t)x * words;
+    for (uint64_t w = tid; w < words; w += TB) {
+        uint64_t bits = drow[w];
+        while (bits) {
+            int b = __builtin_ctzll(bits);
+            bits &= bits - 1;
+            uint32_t y = (uint32_t)(w * 64 + b);
+            for (uint64_t e = row_ptr[y], e1 = row_ptr[y + 1]; e < e1; ++e) {
+                uint32_t z = adj[e];
+                atomicOr((unsigned long long *)&s_acc[z >> 6], 1ull << (z & 63));
+            }
+        }
+    }
+    __syncthreads();
+    uint64_t *rrow = R + (uint64_t)x * words;
+    uint64_t *nrow = N + (uint64_t)x * words;
+    unsigned long long local = 0;
+    for (uint64_t w = tid; w < words; w += TB) {
+        uint64_t r = rrow[w];
+        uint64_t nw = s_acc[w] & ~r;
+        nrow[w] = nw;
+        if (nw) {
+            rrow[w] = r | nw;
+            local += (unsigned long long)__popcll(nw);
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) local += __shfl_xor(local, o, WAVE);
+    if ((tid & 63) == 0 && local) atomicAdd(&s_cnt, local);
+    __syncthreads();
+    if (tid == 0) {
+        nz_next[x] = s_cnt != 0;
+        if (s_cnt) {
+            atomicAdd(count, s_cnt);
+            atomicAdd(count + 1, 1ull);  // rows with a non-empty next delta
+        }
+    }
+}
+
+__global__ void k_set_ull(unsigned long long *p, unsigned long long v) { *p = v; }
+
+// per-row popcount of R
+__global__ __launch_bounds__(TB) void k_row_counts(const uint64_t *__restrict__ R, uint64_t words,
+                                                   uint64_t *__restrict__ cnt) {
+    __shared__ unsigned long long s;
+    const uint32_t x = blockIdx.x;
+    if (threadIdx.x == 0) s = 0;
+    __syncthreads();
+    unsigned long long local = 0;
+    for (uint64_t w = threadIdx.x; w < words; w += TB) local += __popcll(R[(uint64_t)x * words + w]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) local += __shfl_xor(local, o, WAVE);
+    if ((threadIdx.x & 63) == 0) atomicAdd(&s, local);
+    __syncthreads();
+    if (threadIdx.x == 0) cnt[x] = s;
+}
+
+// emit row x's set bits as (x << 32 | z) starting at off[x]
+__global__ __launch_bounds__(TB) void k_emit_rows(const uint64_t *__restrict__ R, uint64_t words,
+                                                  const uint64_t *__restrict__ off, uint64_t *__restrict__ out) {
+    __shared__ uint64_t s_part[TB / WAVE];
+    __shared__ uint64_t s_base;
+    const uint32_t x = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint64_t *row = R + (uint64_t)x * words;
+    if (tid == 0) s_base = off[x];
+    __syncthreads();
+    // chunks of TB words: each thread one word; block-exclusive scan of popcounts
+    for (uint64_t c0 = 0; c0 < words; c0 += TB) {
+        uint64_t w = c0 + tid;
+        uint64_t bits = w < words ? row[w] : 0ull;
+        uint64_t pc = (uint64_t)__popcll(bits), x_incl = pc;
+#pragma unroll
+        for (int o = 1; o < WAVE; o <<= 1) {
+            uint64_t t = __shfl_up(x_incl, o, WAVE);
+            if (lane >= o) x_incl += t;
+        }
+        if (lane == 63) s_part[wave] = x_incl;
+        __syncthreads();
+        uint64_t pre = 0, tot = 0;
+        for (int q = 0; q < TB / WAVE; ++q) {
+            if (q < wave) pre += s_part[q];
+            tot += s_part[q];
+        }
+        uint64_t pos = s_base + pre + x_incl - pc;
+        const uint64_t hi = (uint64_t)x << 32;
+        while (bits) {
+            int b = __builtin_ctzll(bits);
+            bits &= bits - 1;
+            out[pos++] = hi | (uint64_t)(w * 64 + b);
+        }
+        __syncthreads();
+        if (tid == 0) s_base += tot;
+        __syncthreads();
+    }
+}
+
+}  // namespace
+
+// scan helper from join.hip
+void scan_u64_small(Ctx *ctx, uint64_t *a, uint64_t n, uint64_t *total);
+
+// Dense transitive closure.  `edges` sorted unique packed (src, dst), all ids
+// < nv.  Returns the sorted closure in *out (count *out_n), the iteration
+// count and per-iteration delta sizes (index 0 = seed).
+void tc_bitmap(Ctx *ctx, const uint64_t *edges, uint64_t m, uint32_t nv, uint64_t max_iter, uint64_t **out,
+               uint64_t *out_n, uint64_t *iterations, std::vector<uint64_t> &deltas) {
+    deltas.clear();
+    const uint64_t words = ((uint64_t)nv + 63) / 64;
+    XH_REQUIRE(words * 8 <= 64 * 1024, XLOG_HIP_UNSUPPORTED, "tc bitmap: domain too large for an LDS row");
+    const uint64_t cells = (uint64_t)nv * words;
+    Buf<uint64_t> R(ctx, cells ? cells : 1), D0(ctx, cells ? cells : 1), D1(ctx, cells ? cells : 1);
+    Buf<uint64_t> row_ptr(ctx, (uint64_t)nv + 1);
+    Buf<uint32_t> adj(ctx, m ? m : 1);
+    Buf<uint8_t> nz0(ctx, nv ? nv : 1), nz1(ctx, nv ? nv : 1);
+    Buf<unsigned long long> cnt(ctx, 2);
+    fill_u64(ctx, R.p, 0ull, cells);
+    fill_u64(ctx, D0.p, 0ull, cells);
+    hipLaunchKernelGGL(k_row_ptr, dim3(grid_for((uint64_t)nv + 1, 256, 4096)), dim3(256), 0, ctx->stream, edges, m, nv,
+                       row_ptr.p);
+    if (m) {
+        hipLaunchKernelGGL(k_adj, dim3(grid_for(m, 256, 4096)), dim3(256), 0, ctx->stream, edges, m, adj.p);
+        hipLaunchKernelGGL(k_edges_to_bits, dim3(grid_for(m, 256, 4096)), dim3(256), 0, ctx->stream, edges, m, words,
+                           R.p, D0.p);
+    }
+    if (nv) hipLaunchKernelGGL(k_seed_nz, dim3(grid_for(nv, 256, 4096)), dim3(256), 0, ctx->stream, row_ptr.p, nv, nz0.p);
+    XH_CHECK_HIP(hipGetLastError());
+    deltas.push_back(m);  // seed: delta = R = edge
+    uint64_t *D = D0.p, *N = D1.p;
+    uint8_t *nzc = nz0.p, *nzn = nz1.p;
+    uint64_t it = 0, active_rows = nv;
+    bool converged = false;
+    const size_t lds = words * sizeof(uint64_t);
+    while (it < max_iter) {
+        ++it;
+        uint64_t dn = 0;
+        if (m && nv) {
+            fill_u64(ctx, reinterpret_cast<uint64_t *>(cnt.p), 0ull, 2);
+            {
+                // bitmap rows of delta and R read, R and next written (rows with an empty delta skip all four)
+                Prof prof(ctx, XLOG_HIP_KERNEL_TC_STEP, 32.0 * (double)words * (double)active_rows);
+                hipLaunchKernelGGL(k_tc_step, dim3(nv), dim3(TB), lds, ctx->stream, nv, words, row_ptr.p, adj.p, R.p,
+                                   D, N, nzc, nzn, cnt.p);
+                XH_CHECK_HIP(hipGetLastError());
+            }
+            ctx->read_scalars(cnt.p, 2);
+            dn = ctx->host_scalars[0];
+            active_rows = ctx->host_scalars[1];
+        }
+        deltas.push_back(dn);
+        if (dn == 0) {
+            converged = true;
+            break;
+        }
+        std::swap(D, N);
+        std::swap(nzc, nzn);
+    }
+    *iterations = it;
+    XH_REQUIRE(converged, XLOG_HIP_ITERATION_LIMIT, "Recursive SCC iteration limit exceeded");
+    // emit R
+    Buf<uint64_t> rc(ctx, (uint64_t)nv + 1);
+    if (nv) hipLaunchKernelGGL(k_row_counts, dim3(nv), dim3(TB), 0, ctx->stream, R.p, words, rc.p);
+    XH_CHECK_HIP(hipGetLastError());
+    scan_u64_small(ctx, rc.p, nv, rc.p + nv);
+    ctx->read_scalars(rc.p + nv, 1);
+    uint64_t total = ctx->host_scalars[0];
+    *out_n = total;
+    *out = total ? static_cast<uint64_t *>(ctx->alloc(total * sizeof(uint64_t))) : nullptr;
+    Prof prof(ctx, XLOG_HIP_KERNEL_TC_EMIT, 8.0 * (double)total + 8.0 * (double)cells);
+    if (total) hipLaunchKernelGGL(k_emit_rows, dim3(nv), dim3(TB), 0, ctx->stream, R.p, words, rc.p, *out);
+    XH_CHECK_HIP(hipGetLastError());
+}
+
+}  // namespace xh

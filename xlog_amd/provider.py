@@ -1,0 +1,481 @@
+"""Host-side mirror of the reference operator provider over the C ABI.
+
+`HipKernelProvider` exposes the inherent methods of
+`xlog_cuda::CudaKernelProvider` (crates/xlog-cuda/src/provider/mod.rs:1139) that
+the reference runtime calls on the semi-naive path, with the same names,
+argument meaning and error behaviour (a failed call raises `XlogError`, the
+counterpart of `XlogError::Kernel`, crates/xlog-core/src/error.rs).  Every
+operator is a call into libxlog_hip.so; there is no host fallback: if the
+library is missing the import of this module raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import weakref
+from pathlib import Path
+from typing import Iterable, Sequence
+
+import numpy as np
+
+_PKG = Path(__file__).resolve().parent
+_LIB_PATH = _PKG / "libxlog_hip.so"
+
+OK = 0
+STATUS_NAMES = {
+    0: "OK",
+    1: "INVALID_ARG",
+    2: "TYPE_MISMATCH",
+    3: "CAPACITY_OVERFLOW",
+    4: "ITERATION_LIMIT",
+    5: "OOM",
+    6: "DEVICE_ERROR",
+    7: "UNSUPPORTED",
+}
+JOIN_INNER, JOIN_SEMI, JOIN_ANTI = 0, 1, 2
+ROUTE_AUTO, ROUTE_JOIN, ROUTE_BITMAP = 0, 1, 2
+
+
+class XlogError(RuntimeError):
+    """Raised for every non-OK status of the C ABI."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"{STATUS_NAMES.get(status, status)}: {message}")
+        self.status = status
+        self.message = message
+
+
+class FixpointStats(C.Structure):
+    _fields_ = [
+        ("iterations", C.c_uint64),
+        ("max_iterations", C.c_uint64),
+        ("delta_sizes", C.POINTER(C.c_uint64)),
+        ("delta_cap", C.c_uint64),
+        ("route", C.c_uint64),
+        ("wall_ms", C.c_double),
+    ]
+
+
+def _load() -> C.CDLL:
+    if not _LIB_PATH.exists():
+        raise ImportError(
+            f"{_LIB_PATH} is not built; run `python xlog_amd/_build.py` (the HIP path has no fallback)"
+        )
+    lib = C.CDLL(str(_LIB_PATH))
+    P, U32, U64, I32 = C.c_void_p, C.c_uint32, C.c_uint64, C.c_int
+    PP = C.POINTER(C.c_void_p)
+    sig = {
+        "xlog_hip_last_error": (C.c_char_p, []),
+        "xlog_hip_version": (C.c_char_p, []),
+        "xlog_hip_ctx_create": (I32, [I32, PP]),
+        "xlog_hip_ctx_destroy": (None, [P]),
+        "xlog_hip_synchronize": (I32, [P]),
+        "xlog_hip_stream": (P, [P]),
+        "xlog_hip_memory_stats": (I32, [P, C.POINTER(U64), C.POINTER(U64), C.POINTER(U64)]),
+        "xlog_hip_trim": (I32, [P]),
+        "xlog_hip_rel_create_empty": (I32, [P, U32, PP]),
+        "xlog_hip_rel_from_host_columns": (I32, [P, PP, U32, U64, PP]),
+        "xlog_hip_rel_from_device_columns": (I32, [P, PP, U32, U64, PP]),
+        "xlog_hip_rel_from_host_packed": (I32, [P, P, U32, U64, PP]),
+        "xlog_hip_rel_download_column": (I32, [P, P, U32, P, U64]),
+        "xlog_hip_rel_download_packed": (I32, [P, P, P, U64]),
+        "xlog_hip_rel_num_rows": (I32, [P, C.POINTER(U64)]),
+        "xlog_hip_rel_arity": (I32, [P, C.POINTER(U32)]),
+        "xlog_hip_rel_is_canonical": (I32, [P, C.POINTER(I32)]),
+        "xlog_hip_rel_device_words": (I32, [P, U32, PP]),
+        "xlog_hip_rel_clone": (I32, [P, P, PP]),
+        "xlog_hip_rel_free": (None, [P]),
+        "xlog_hip_sort": (I32, [P, P, P, U32, PP]),
+        "xlog_hip_dedup": (I32, [P, P, P, U32, PP]),
+        "xlog_hip_dedup_full_row": (I32, [P, P, PP]),
+        "xlog_hip_union": (I32, [P, P, P, PP]),
+        "xlog_hip_union_many": (I32, [P, PP, U32, PP]),
+        "xlog_hip_diff": (I32, [P, P, P, PP]),
+        "xlog_hip_hash_join": (I32, [P, P, P, U32, U32, I32, PP]),
+        "xlog_hip_sort_merge_join": (I32, [P, P, P, U32, U32, PP]),
+        "xlog_hip_join_project": (I32, [P, P, P, U32, U32, P, U32, PP]),
+        "xlog_hip_project": (I32, [P, P, P, U32, PP]),
+        "xlog_hip_is_sorted": (I32, [P, P, U32, C.POINTER(I32)]),
+        "xlog_hip_exclusive_scan_u32": (I32, [P, P, U64, C.POINTER(U64)]),
+        "xlog_hip_compact": (I32, [P, P, P, PP]),
+        "xlog_hip_fixpoint": (I32, [P, P, U32, PP, PP, C.POINTER(FixpointStats)]),
+        "xlog_hip_fixpoint_tc": (I32, [P, P, PP, C.POINTER(FixpointStats)]),
+        "xlog_hip_rel_digest": (I32, [P, P, C.POINTER(U64)]),
+        "xlog_hip_profile_enable": (I32, [P, I32]),
+        "xlog_hip_profile_reset": (I32, [P]),
+        "xlog_hip_profile_read": (I32, [P, U32, C.POINTER(U64), C.POINTER(C.c_double), C.POINTER(C.c_double)]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(lib, name)
+        f.restype = res
+        f.argtypes = args
+    return lib
+
+
+_lib = _load()
+
+#: exported symbol names the C header declares (checked by the CPU test-suite)
+ABI_SYMBOLS = (
+    "xlog_hip_last_error", "xlog_hip_version", "xlog_hip_ctx_create", "xlog_hip_ctx_destroy",
+    "xlog_hip_synchronize", "xlog_hip_stream", "xlog_hip_memory_stats", "xlog_hip_trim",
+    "xlog_hip_rel_create_empty", "xlog_hip_rel_from_host_columns", "xlog_hip_rel_from_device_columns",
+    "xlog_hip_rel_from_host_packed", "xlog_hip_rel_download_column", "xlog_hip_rel_download_packed",
+    "xlog_hip_rel_num_rows", "xlog_hip_rel_arity", "xlog_hip_rel_is_canonical", "xlog_hip_rel_device_words",
+    "xlog_hip_rel_clone", "xlog_hip_rel_free", "xlog_hip_sort", "xlog_hip_dedup", "xlog_hip_dedup_full_row",
+    "xlog_hip_union", "xlog_hip_union_many", "xlog_hip_diff", "xlog_hip_hash_join",
+    "xlog_hip_sort_merge_join", "xlog_hip_join_project", "xlog_hip_project", "xlog_hip_is_sorted",
+    "xlog_hip_exclusive_scan_u32", "xlog_hip_compact", "xlog_hip_fixpoint", "xlog_hip_fixpoint_tc",
+    "xlog_hip_rel_digest", "xlog_hip_profile_enable", "xlog_hip_profile_reset", "xlog_hip_profile_read",
+)
+
+KERNEL_KINDS = {
+    "sort_pass": 0, "sort_hist": 1, "select": 2, "merge": 3, "probe_count": 4, "probe_emit": 5, "tc_step": 6,
+    "tc_emit": 7,
+}
+
+
+def library() -> C.CDLL:
+    return _lib
+
+
+def library_path() -> Path:
+    return _LIB_PATH
+
+
+def _check(status: int) -> None:
+    if status != OK:
+        msg = _lib.xlog_hip_last_error()
+        raise XlogError(status, msg.decode() if msg else "")
+
+
+def _u32_array(values: Iterable[int]):
+    vals = list(values)
+    return (C.c_uint32 * max(1, len(vals)))(*vals), len(vals)
+
+
+class Relation:
+    """Device-resident relation handle (the CudaBuffer counterpart,
+    crates/xlog-cuda/src/memory.rs:1758-1930).  Freed when garbage collected."""
+
+    __slots__ = ("_h", "_provider", "__weakref__")
+
+    def __init__(self, provider: "HipKernelProvider", handle: C.c_void_p):
+        self._provider = provider
+        self._h = handle
+
+    @property
+    def handle(self) -> C.c_void_p:
+        if not self._h:
+            raise XlogError(1, "relation already freed")
+        return self._h
+
+    def num_rows(self) -> int:
+        n = C.c_uint64()
+        _check(_lib.xlog_hip_rel_num_rows(self.handle, C.byref(n)))
+        return n.value
+
+    def __len__(self) -> int:
+        return self.num_rows()
+
+    @property
+    def arity(self) -> int:
+        a = C.c_uint32()
+        _check(_lib.xlog_hip_rel_arity(self.handle, C.byref(a)))
+        return a.value
+
+    def is_canonical(self) -> bool:
+        v = C.c_int()
+        _check(_lib.xlog_hip_rel_is_canonical(self.handle, C.byref(v)))
+        return bool(v.value)
+
+    def free(self) -> None:
+        if self._h:
+            _lib.xlog_hip_rel_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class HipKernelProvider:
+    """Operators over device relations on one MI355X (one context, one stream).
+
+    Method names follow `CudaKernelProvider` (relational.rs / io.rs / transfer.rs)."""
+
+    def __init__(self, device: int = 0):
+        self._ctx = None
+        self._live = weakref.WeakSet()
+        h = C.c_void_p()
+        _check(_lib.xlog_hip_ctx_create(device, C.byref(h)))
+        self._ctx = h
+        self.device = device
+
+    # -- lifecycle --------------------------------------------------------
+    def close(self) -> None:
+        if getattr(self, "_ctx", None):
+            # relations are context-owned device memory: release them first
+            for r in list(getattr(self, "_live", ())):
+                r.free()
+            _lib.xlog_hip_ctx_destroy(self._ctx)
+            self._ctx = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def ctx(self) -> C.c_void_p:
+        if not self._ctx:
+            raise XlogError(1, "provider closed")
+        return self._ctx
+
+    def synchronize(self) -> None:
+        _check(_lib.xlog_hip_synchronize(self.ctx))
+
+    def stream(self) -> int:
+        return _lib.xlog_hip_stream(self.ctx) or 0
+
+    def memory_stats(self) -> dict:
+        a, b, c = C.c_uint64(), C.c_uint64(), C.c_uint64()
+        _check(_lib.xlog_hip_memory_stats(self.ctx, C.byref(a), C.byref(b), C.byref(c)))
+        return {"in_use": a.value, "peak": b.value, "cached": c.value}
+
+    def trim(self) -> None:
+        _check(_lib.xlog_hip_trim(self.ctx))
+
+    # -- kernel timing (HIP events on the context stream) --------------------
+    def profile_enable(self, on: bool = True) -> None:
+        _check(_lib.xlog_hip_profile_enable(self.ctx, 1 if on else 0))
+
+    def profile_reset(self) -> None:
+        _check(_lib.xlog_hip_profile_reset(self.ctx))
+
+    def profile_read(self) -> dict:
+        out = {}
+        for name, kind in KERNEL_KINDS.items():
+            n, ms, b = C.c_uint64(), C.c_double(), C.c_double()
+            _check(_lib.xlog_hip_profile_read(self.ctx, kind, C.byref(n), C.byref(ms), C.byref(b)))
+            out[name] = {"launches": n.value, "total_ms": ms.value, "algo_bytes": b.value}
+        return out
+
+    def _rel(self, h: C.c_void_p) -> Relation:
+        r = Relation(self, h)
+        self._live.add(r)
+        return r
+
+    # -- buffers (provider/mod.rs:3018, io.rs:75, transfer.rs:22) ---------
+    def create_empty_buffer(self, arity: int) -> Relation:
+        h = C.c_void_p()
+        _check(_lib.xlog_hip_rel_create_empty(self.ctx, arity, C.byref(h)))
+        return self._rel(h)
+
+    def create_buffer_from_u32_columns(self, columns: Sequence[Sequence[int] | np.ndarray]) -> Relation:
+        cols = [np.ascontiguousarray(np.asarray(c, dtype=np.uint32)) for c in columns]
+        if not cols:
+            raise XlogError(1, "at least one column is required")
+        rows = len(cols[0])
+        if any(len(c) != rows for c in cols):
+            raise XlogError(1, "columns have different lengths")
+        ptrs = (C.c_void_p * len(cols))(*[c.ctypes.data for c in cols])
+        h = C.c_void_p()
+        _check(_lib.xlog_hip_rel_from_host_columns(self.ctx, ptrs, len(cols), rows, C.byref(h)))
+        return self._rel(h)
+
+    create_buffer_from_slices = create_buffer_from_u32_columns
+
+    def create_buffer_from_packed(self, keys: np.ndarray, arity: int = 2) -> Relation:
+        k = np.ascontiguousarray(np.asarray(keys, dtype=np.uint64))
+        h = C.c_void_p()
+        _check(_lib.xlog_hip_rel_from_host_packed(self.ctx, k.ctypes.data, arity, len(k), C.byref(h)))
+        return self._rel(h)
+
+    def create_buffer_from_device_columns(self, dev_ptrs: Sequence[int], rows: int) -> Relation:
+        ptrs = (C.c_void_p * len(dev_ptrs))(*dev_ptrs)
+        h = C.c_void_p()
+        _check(_lib.xlog_hip_rel_from_device_columns(self.ctx, ptrs, len(dev_ptrs), rows, C.byref(h)))
+        return self._rel(h)
+
+    def download_column(self, rel: Relation, col: int) -> np.ndarray:
+        n = rel.num_rows()
+        out = np.empty(n, dtype=np.uint32)
+        _check(_lib.xlog_hip_rel_download_column(self.ctx, rel.handle, col, out.ctypes.data if n else None, n))
+        return out
+
+    def download_packed(self, rel: Relation) -> np.ndarray:
+        n = rel.num_rows()
+        out = np.empty(n, dtype=np.uint64)
+        _check(_lib.xlog_hip_rel_download_packed(self.ctx, rel.handle, out.ctypes.data if n else None, n))
+        return out
+
+    def download_rows(self, rel: Relation) -> list[tuple[int, ...]]:
+        cols = [self.download_column(rel, c) for c in range(rel.arity)]
+        return list(zip(*[c.tolist() for c in cols]))
+
+    def device_row_count(self, rel: Relation) -> int:
+        return rel.num_rows()
+
+    def device_words(self, rel: Relation, word: int = 0) -> int:
+        p = C.c_void_p()
+        _check(_lib.xlog_hip_rel_device_words(rel.handle, word, C.byref(p)))
+        return p.value or 0
+
+    def clone_buffer(self, rel: Relation) -> Relation:
+        h = C.c_void_p()
+        _check(_lib.xlog_hip_rel_clone(self.ctx, rel.handle, C.byref(h)))
+        return self._rel(h)
+
+    def digest(self, rel: Relation) -> int:
+        d = C.c_uint64()
+        _check(_lib.xlog_hip_rel_digest(self.ctx, rel.handle, C.byref(d)))
+        return d.value
+
+    # -- operators (relational.rs) ------------------------------------------
+    def sort(self, rel: Relation, key_cols: Sequence[int]) -> Relation:
+        arr, n = _u32_array(key_cols)
+        h = C.c_void_p()
+        _check(_lib.xlog_hip_sort(self.ctx, rel.handle, arr, n, C.byref(h)))
+        return self._rel(h)
+
+    def dedup(self, rel: Relation, key_cols: Sequence[int]) -> Relation:
+        arr, n = _u32_array(key_cols)
+        h = C.c_void_p()
+        _check(_lib.xlog_hip_dedup(self.ctx, rel.handle, arr, n, C.byref(h)))
+        return self._rel(h)
+
+    def dedup_full_row(self, rel: Relation) -> Relation:
+        h = C.c_void_p()
+        _check(_lib.xlog_hip_dedup_full_row(self.ctx, rel.handle, C.byref(h)))
+        return self._rel(h)
+
+    def union_gpu(self, a: Relation, b: Relation) -> Relation:
+        h = C.c_void_p()
+        _check(_lib.xlog_hip_union(self.ctx, a.handle, b.handle, C.byref(h)))
+        return self._rel(h)
+
+    def union_many_gpu(self, rels: Sequence[Relation]) -> Relation:
+        arr = (C.c_void_p * max(1, len(rels)))(*[r.handle for r in rels])
+        h = C.c_void_p()
+        _check(_lib.xlog_hip_union_many(self.ctx, arr, len(rels), C.byref(h)))
+        return self._rel(h)
+
+    def diff_gpu(self, a: Relation, b: Relation) -> Relation:
+        h = C.c_void_p()
+        _check(_lib.xlog_hip_diff(self.ctx, a.handle, b.handle, C.byref(h)))
+        return self._rel(h)
+
+    diff_full_row = diff_gpu
+
+    def hash_join_v2(self, left: Relation, right: Relation, left_keys: Sequence[int], right_keys: Sequence[int],
+                     join_type: int = JOIN_INNER) -> Relation:
+        if len(left_keys) != 1 or len(right_keys) != 1:
+            raise XlogError(7, "joins on one key column per side are supported")
+        h = C.c_void_p()
+        _check(_lib.xlog_hip_hash_join(self.ctx, left.handle, right.handle, left_keys[0], right_keys[0],
+                                       join_type, C.byref(h)))
+        return self._rel(h)
+
+    def sort_merge_join_v2_inner_u32_1key(self, left: Relation, right: Relation, left_key: int,
+                                          right_key: int) -> Relation:
+        h = C.c_void_p()
+        _check(_lib.xlog_hip_sort_merge_join(self.ctx, left.handle, right.handle, left_key, right_key, C.byref(h)))
+        return self._rel(h)
+
+    def join_project(self, left: Relation, right: Relation, left_key: int, right_key: int,
+                     out_cols: Sequence[int]) -> Relation:
+        arr, n = _u32_array(out_cols)
+        h = C.c_void_p()
+        _check(_lib.xlog_hip_join_project(self.ctx, left.handle, right.handle, left_key, right_key, arr, n,
+                                          C.byref(h)))
+        return self._rel(h)
+
+    def project(self, rel: Relation, cols: Sequence[int]) -> Relation:
+        arr, n = _u32_array(cols)
+        h = C.c_void_p()
+        _check(_lib.xlog_hip_project(self.ctx, rel.handle, arr, n, C.byref(h)))
+        return self._rel(h)
+
+    def is_sorted_ascending_u32(self, rel: Relation, col: int) -> bool:
+        v = C.c_int()
+        _check(_lib.xlog_hip_is_sorted(self.ctx, rel.handle, col, C.byref(v)))
+        return bool(v.value)
+
+    def exclusive_scan_u32_inplace(self, dev_ptr: int, n: int) -> int:
+        t = C.c_uint64()
+        _check(_lib.xlog_hip_exclusive_scan_u32(self.ctx, C.c_void_p(dev_ptr), n, C.byref(t)))
+        return t.value
+
+    def compact_by_device_mask(self, rel: Relation, dev_mask_ptr: int) -> Relation:
+        h = C.c_void_p()
+        _check(_lib.xlog_hip_compact(self.ctx, rel.handle, C.c_void_p(dev_mask_ptr), C.byref(h)))
+        return self._rel(h)
+
+    # -- fixpoint (executor/recursive.rs:447-957) -----------------------------
+    def fixpoint(self, plan: Sequence[int], relations: Sequence[Relation | None], route: int = ROUTE_AUTO,
+                 max_iterations: int = 0, trace_cap: int = 4096):
+        """Run a plan (see include/xlog_hip.h) to fixpoint.
+
+        Returns (outputs, stats) where outputs[p] is the final relation of every
+        IDB predicate p (None for EDB ones) and stats is a dict with
+        iterations, delta_sizes (index 0 = seed), route and wall_ms."""
+        n = len(relations)
+        plan_arr = (C.c_int32 * len(plan))(*plan)
+        rels = (C.c_void_p * n)(*[r.handle if r is not None else None for r in relations])
+        outs = (C.c_void_p * n)()
+        trace = (C.c_uint64 * trace_cap)()
+        st = FixpointStats(0, max_iterations, trace, trace_cap, route, 0.0)
+        status = _lib.xlog_hip_fixpoint(self.ctx, plan_arr, n, rels, outs, C.byref(st))
+        stats = {"iterations": st.iterations, "route": int(st.route), "wall_ms": st.wall_ms}
+        if status != OK:
+            err = XlogError(status, (_lib.xlog_hip_last_error() or b"").decode())
+            err.stats = stats
+            raise err
+        stats["delta_sizes"] = [trace[i] for i in range(min(st.iterations + 1, trace_cap))]
+        out = [self._rel(C.c_void_p(outs[i])) if outs[i] else None for i in range(n)]
+        return out, stats
+
+
+# plans (int32 arrays, see include/xlog_hip.h)
+def tc_plan(edge: int = 0, reach: int = 1) -> list[int]:
+    """reach(X,Y) :- edge(X,Y).  reach(X,Z) :- reach(X,Y), edge(Y,Z).  (logic_bench.rs:102-110)"""
+    X, Y, Z = 0, 1, 2
+    return [2, reach, X, Y, 1, edge, X, Y, reach, X, Z, 2, reach, X, Y, edge, Y, Z]
+
+
+def andersen_plan(assign: int = 0, addr: int = 1, load: int = 2, store: int = 3, pts: int = 4) -> list[int]:
+    """Andersen points-to:
+         pointsTo(V,O) :- addressOf(V,O).
+         pointsTo(V,O) :- assign(V,W), pointsTo(W,O).
+         pointsTo(V,O) :- load(V,W), pointsTo(W,P), pointsTo(P,O).
+         pointsTo(P,O) :- store(V,W), pointsTo(V,P), pointsTo(W,O)."""
+    V, W, O, P = 0, 1, 2, 3
+    return [4,
+            pts, V, O, 1, addr, V, O,
+            pts, V, O, 2, assign, V, W, pts, W, O,
+            pts, V, O, 3, load, V, W, pts, W, P, pts, P, O,
+            pts, P, O, 3, store, V, W, pts, V, P, pts, W, O]
+
+
+def copy_points_to_plan(addr_of: int = 0, copy: int = 1, points_to: int = 2) -> list[int]:
+    """points_to(P,T) :- addr_of(P,T).  points_to(D,T) :- copy(D,S), points_to(S,T).
+    (examples/xlog/50-program-analysis/01_points_to_copy.xlog)"""
+    P, T, D, S = 0, 1, 2, 3
+    return [2, points_to, P, T, 1, addr_of, P, T, points_to, D, T, 2, copy, D, S, points_to, S, T]
+
+
+def pack(c0, c1) -> np.ndarray:
+    return (np.asarray(c0, dtype=np.uint64) << np.uint64(32)) | np.asarray(c1, dtype=np.uint64)
+
+
+def unpack(keys: np.ndarray):
+    k = np.asarray(keys, dtype=np.uint64)
+    return (k >> np.uint64(32)).astype(np.uint32), (k & np.uint64(0xFFFFFFFF)).astype(np.uint32)
