@@ -92,6 +92,18 @@ def make_workload(name: str, p):
         config = {"workload": f"{name}: semi-naive transitive closure, G(n,m) digraph", "vertices": cfg["n_vertices"],
                   "edges": cfg["n_edges"], "seed": datagen.seed_for(cid)}
         return step, None, "closure tuples", config, (src, dst), state
+    if name == "copy":
+        # calibration: k_project over 2^28 packed rows reads 8 B and writes 8 B per row
+        n = 1 << 28
+        K = p.create_buffer_from_packed(np.arange(n, dtype=np.uint64))
+        state = {}
+
+        def step():
+            o = p.project(K, [1, 0])
+            state["out_rows"] = o.num_rows()
+
+        config = {"workload": "copy: column swap of 2^28 packed rows (16 B/row), counter calibration", "rows": n}
+        return step, n, "rows", config, None, state
     if name == "c5":
         cfg = datagen.C5
         f = datagen.andersen(cfg["n_vars"], cfg["n_facts"], cfg["alpha"], datagen.seed_for(5))

@@ -18,8 +18,14 @@ namespace xh {
 
 namespace {
 
-constexpr int SEL_BLOCK = 256;
-constexpr int SEL_ITEMS = 16;
+#ifndef XH_SEL_BLOCK
+#define XH_SEL_BLOCK 512
+#endif
+#ifndef XH_SEL_ITEMS
+#define XH_SEL_ITEMS 16
+#endif
+constexpr int SEL_BLOCK = XH_SEL_BLOCK;
+constexpr int SEL_ITEMS = XH_SEL_ITEMS;
 constexpr int SEL_WAVES = SEL_BLOCK / WAVE;
 constexpr int SEL_TILE = SEL_BLOCK * SEL_ITEMS;
 
@@ -74,7 +80,8 @@ __device__ uint64_t lookback_wave(const uint64_t *status, uint64_t tile, uint64_
 
 // Generic single-pass selection.  Sel supplies:
 //   __device__ void setup(uint64_t tile_first_idx, uint64_t tile_last_idx, uint64_t *smem)  (thread 0)
-//   __device__ bool flag(uint64_t idx, uint64_t key, const uint64_t *smem)
+//   __device__ bool flag(uint64_t idx, uint64_t key, uint64_t prev_key, const uint64_t *smem)
+//        (prev_key = in[idx - 1], meaningful for idx > 0)
 //   __device__ void emit(uint64_t pos, uint64_t idx, uint64_t key)
 template <class Sel>
 __global__ __launch_bounds__(SEL_BLOCK) void k_select(const uint64_t *__restrict__ in, uint64_t n, Sel sel,
@@ -103,13 +110,18 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_select(const uint64_t *__restrict
 #pragma unroll
     for (int r = 0; r < SEL_ITEMS; ++r) {
         uint64_t idx = wbase + (uint64_t)r * WAVE + lane;
-        bool f = false;
-        if (idx < n) {
-            k[r] = in[idx];
-            f = sel.flag(idx, k[r], s_sel);
-        } else {
-            k[r] = 0;
-        }
+        k[r] = idx < n ? in[idx] : 0ull;
+    }
+    // predecessor of item r: lane-1 of the same round, lane 63 of the previous
+    // round for lane 0, one extra load for the wave's first item
+    uint64_t first_prev = (wbase > 0 && wbase <= n) ? in[wbase - 1] : 0ull;
+#pragma unroll
+    for (int r = 0; r < SEL_ITEMS; ++r) {
+        uint64_t idx = wbase + (uint64_t)r * WAVE + lane;
+        uint64_t up = __shfl_up(k[r], 1, WAVE);
+        uint64_t carry = (r > 0) ? __shfl(k[r > 0 ? r - 1 : 0], WAVE - 1, WAVE) : first_prev;
+        uint64_t prev = lane ? up : carry;
+        bool f = idx < n && sel.flag(idx, k[r], prev, s_sel);
         if (f) fl |= 1ull << r;
         wc += (uint32_t)__popcll(__ballot(f));
     }
@@ -160,8 +172,8 @@ struct SelUnique {
     const uint64_t *in;
     uint64_t *out;
     __device__ void setup(uint64_t, uint64_t, uint64_t *) const {}
-    __device__ bool flag(uint64_t idx, uint64_t key, const uint64_t *) const {
-        return idx == 0 || in[idx - 1] != key;
+    __device__ bool flag(uint64_t idx, uint64_t key, uint64_t prev, const uint64_t *) const {
+        return idx == 0 || prev != key;
     }
     __device__ void emit(uint64_t pos, uint64_t, uint64_t key) const { out[pos] = key; }
 };
@@ -177,8 +189,8 @@ struct SelDiff {
         s[0] = lower_bound_u64(b, 0, nb, in[first]);
         s[1] = upper_bound_u64(b, s[0], nb, in[last]);
     }
-    __device__ bool flag(uint64_t idx, uint64_t key, const uint64_t *s) const {
-        if (UNIQ && idx != 0 && in[idx - 1] == key) return false;
+    __device__ bool flag(uint64_t idx, uint64_t key, uint64_t prev, const uint64_t *s) const {
+        if (UNIQ && idx != 0 && prev == key) return false;
         uint64_t p = lower_bound_u64(b, s[0], s[1], key);
         return !(p < s[1] && b[p] == key);
     }
@@ -189,7 +201,7 @@ struct SelFlags {
     const uint8_t *flags;
     uint64_t *out;
     __device__ void setup(uint64_t, uint64_t, uint64_t *) const {}
-    __device__ bool flag(uint64_t idx, uint64_t, const uint64_t *) const { return flags[idx] != 0; }
+    __device__ bool flag(uint64_t idx, uint64_t, uint64_t, const uint64_t *) const { return flags[idx] != 0; }
     __device__ void emit(uint64_t pos, uint64_t, uint64_t key) const { out[pos] = key; }
 };
 
@@ -199,8 +211,8 @@ struct SelRuns {
     uint32_t *run_key;
     uint64_t *run_start;
     __device__ void setup(uint64_t, uint64_t, uint64_t *) const {}
-    __device__ bool flag(uint64_t idx, uint64_t key, const uint64_t *) const {
-        return idx == 0 || (in[idx - 1] >> 32) != (key >> 32);
+    __device__ bool flag(uint64_t idx, uint64_t key, uint64_t prev, const uint64_t *) const {
+        return idx == 0 || (prev >> 32) != (key >> 32);
     }
     __device__ void emit(uint64_t pos, uint64_t idx, uint64_t key) const {
         run_key[pos] = (uint32_t)(key >> 32);

@@ -21,10 +21,24 @@ namespace xh {
 
 namespace {
 
-constexpr int SORT_BLOCK = 256;
-constexpr int SORT_ITEMS = 16;
+// tile shape: SORT_BLOCK threads (>= 256; threads 0..255 own one digit each in
+// the counting phase) x SORT_ITEMS keys per thread
+#ifndef XH_SORT_BLOCK
+#define XH_SORT_BLOCK 512
+#endif
+#ifndef XH_SORT_DIRECT
+#define XH_SORT_DIRECT 0
+#endif
+#ifndef XH_SORT_ITEMS
+#define XH_SORT_ITEMS 16
+#endif
+constexpr int SORT_BLOCK = XH_SORT_BLOCK;
+constexpr int SORT_ITEMS = XH_SORT_ITEMS;
 constexpr int SORT_WAVES = SORT_BLOCK / WAVE;
-constexpr int SORT_TILE = SORT_BLOCK * SORT_ITEMS;  // 4096 keys
+constexpr int SORT_TILE = SORT_BLOCK * SORT_ITEMS;
+static_assert(SORT_BLOCK >= 256 && SORT_BLOCK % 256 == 0, "digit phase needs 256 threads");
+constexpr int HIST_SEG = 16;                // consecutive keys per thread (run-length aggregated)
+constexpr int HIST_TILE = 256 * HIST_SEG;   // keys staged in LDS per block iteration
 constexpr uint32_t ST_AGG = 1u << 30;
 constexpr uint32_t ST_INC = 2u << 30;
 constexpr uint32_t ST_VAL = (1u << 30) - 1;
@@ -38,21 +52,64 @@ __device__ __forceinline__ void st_status(uint32_t *p, uint32_t v) {
 
 __global__ __launch_bounds__(256) void k_hist8(const uint64_t *__restrict__ keys, uint64_t n,
                                                uint32_t *__restrict__ ghist) {
-    // two copies per digit position halve same-address LDS atomic collisions
-    __shared__ uint32_t h[2][8][256];
-    uint32_t *hf = &h[0][0][0];
-    for (int i = threadIdx.x; i < 2 * 8 * 256; i += blockDim.x) hf[i] = 0;
-    __syncthreads();
-    const int copy = (threadIdx.x >> 6) & 1;
-    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
-        uint64_t k = keys[i];
+    // A tile of HIST_TILE keys is loaded coalesced into LDS (split into padded
+    // low / high word arrays so that a lane stride of HIST_SEG keys is bank
+    // conflict free); each thread then walks HIST_SEG consecutive keys and
+    // adds run lengths of equal digits, so sorted-ish inputs (runs of equal
+    // high words, e.g. join output grouped by probe row) issue one LDS atomic
+    // per run instead of colliding on one counter.
+    __shared__ uint32_t h[8][256];
+    __shared__ uint32_t s_lo[HIST_TILE + HIST_TILE / HIST_SEG];
+    __shared__ uint32_t s_hi[HIST_TILE + HIST_TILE / HIST_SEG];
+    const int tid = threadIdx.x;
+    for (int i = tid; i < 8 * 256; i += blockDim.x) (&h[0][0])[i] = 0;
+    for (uint64_t t0 = (uint64_t)blockIdx.x * HIST_TILE; t0 < n; t0 += (uint64_t)gridDim.x * HIST_TILE) {
+        const uint32_t cnt = (n - t0) < (uint64_t)HIST_TILE ? (uint32_t)(n - t0) : (uint32_t)HIST_TILE;
+        __syncthreads();
 #pragma unroll
-        for (int d = 0; d < 8; ++d) atomicAdd(&h[copy][d][(k >> (8 * d)) & 255], 1u);
+        for (int r = 0; r < HIST_SEG; ++r) {
+            uint32_t j = r * 256 + tid;
+            if (j < cnt) {
+                uint64_t k = __builtin_nontemporal_load(keys + t0 + j);
+                uint32_t pj = j + (j / HIST_SEG);
+                s_lo[pj] = (uint32_t)k;
+                s_hi[pj] = (uint32_t)(k >> 32);
+            }
+        }
+        __syncthreads();
+        const uint32_t base = tid * HIST_SEG;
+        if (base < cnt) {
+            const uint32_t m = (cnt - base) < (uint32_t)HIST_SEG ? cnt - base : (uint32_t)HIST_SEG;
+            const uint32_t pb = base + tid;  // padded index of key `base`
+            uint32_t lo = s_lo[pb], hi = s_hi[pb];
+            uint32_t cur[8], run[8];
+#pragma unroll
+            for (int d = 0; d < 8; ++d) {
+                cur[d] = ((d < 4 ? lo : hi) >> (8 * (d & 3))) & 255u;
+                run[d] = 1;
+            }
+            for (uint32_t j = 1; j < m; ++j) {
+                lo = s_lo[pb + j];
+                hi = s_hi[pb + j];
+#pragma unroll
+                for (int d = 0; d < 8; ++d) {
+                    uint32_t dg = ((d < 4 ? lo : hi) >> (8 * (d & 3))) & 255u;
+                    if (dg == cur[d]) {
+                        ++run[d];
+                    } else {
+                        atomicAdd(&h[d][cur[d]], run[d]);
+                        cur[d] = dg;
+                        run[d] = 1;
+                    }
+                }
+            }
+#pragma unroll
+            for (int d = 0; d < 8; ++d) atomicAdd(&h[d][cur[d]], run[d]);
+        }
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < 8 * 256; i += blockDim.x) {
-        uint32_t c = hf[i] + hf[i + 8 * 256];
+    for (int i = tid; i < 8 * 256; i += blockDim.x) {
+        uint32_t c = (&h[0][0])[i];
         if (c) atomicAdd(&ghist[i], c);
     }
 }
@@ -89,8 +146,10 @@ __global__ __launch_bounds__(SORT_BLOCK) void k_onesweep(
     __shared__ uint32_t s_tstart[256];
     __shared__ uint32_t s_gbase[256];
     __shared__ uint32_t s_wsum[SORT_WAVES];
+#if !XH_SORT_DIRECT
     __shared__ uint64_t s_keys[SORT_TILE];
     __shared__ uint32_t s_vals[HAS_VAL ? SORT_TILE : 1];
+#endif
 
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
     if (tid == 0) s_tile = (uint32_t)(atomicAdd(ticket, 1ull) - ticket_base);
@@ -134,49 +193,67 @@ __global__ __launch_bounds__(SORT_BLOCK) void k_onesweep(
     }
     __syncthreads();
 
-    // per digit: totals and exclusive prefix over waves (thread = digit)
-    const int d = tid;  // SORT_BLOCK == 256
-    uint32_t cnt = 0;
-#pragma unroll
-    for (int w = 0; w < SORT_WAVES; ++w) {
-        uint32_t c = s_wcnt[w][d];
-        s_wcnt[w][d] = cnt;
-        cnt += c;
-    }
-    // publish this tile's aggregate (or inclusive prefix for tile 0)
+    // per digit (threads 0..255): totals and exclusive prefix over waves
+    const int d = tid;
+    const bool digit_thread = tid < 256;
+    uint32_t cnt = 0, incl = 0;
     uint32_t *my = status + (uint64_t)tile * 256 + d;
-    st_status(my, (tile == 0 ? ST_INC : ST_AGG) | cnt);
-
-    // tile-local exclusive scan over the 256 digits
-    uint32_t incl = wave_incl_scan(cnt, lane);
-    if (lane == WAVE - 1) s_wsum[wave] = incl;
-    __syncthreads();
-    uint32_t wpre = 0;
+    if (digit_thread) {
 #pragma unroll
-    for (int w = 0; w < SORT_WAVES; ++w)
-        if (w < wave) wpre += s_wsum[w];
-    const uint32_t tstart = wpre + incl - cnt;
-    s_tstart[d] = tstart;
-
-    // decoupled look-back over earlier tiles for this digit
-    uint32_t prefix = 0;
-    if (tile > 0) {
-        int64_t j = (int64_t)tile - 1;
-        for (;;) {
-            uint32_t s = ld_status(status + (uint64_t)j * 256 + d);
-            uint32_t flag = s & ~ST_VAL;
-            if (flag == 0) continue;  // predecessor not published yet
-            prefix += s & ST_VAL;
-            if (flag == ST_INC) break;
-            --j;
+        for (int w = 0; w < SORT_WAVES; ++w) {
+            uint32_t c = s_wcnt[w][d];
+            s_wcnt[w][d] = cnt;
+            cnt += c;
         }
-        st_status(my, ST_INC | (prefix + cnt));
+        // publish this tile's aggregate (or inclusive prefix for tile 0)
+        st_status(my, (tile == 0 ? ST_INC : ST_AGG) | cnt);
+        // tile-local exclusive scan over the 256 digits (waves 0..3)
+        incl = wave_incl_scan(cnt, lane);
+        if (lane == WAVE - 1) s_wsum[wave] = incl;
     }
-    s_gbase[d] = digit_off[d] + prefix - tstart;
-    // the next pass uses the other status buffer: clear this tile's slot there
-    status_next[(uint64_t)tile * 256 + d] = 0u;
+    __syncthreads();
+    if (digit_thread) {
+        uint32_t wpre = 0;
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+            if (w < wave) wpre += s_wsum[w];
+        const uint32_t tstart = wpre + incl - cnt;
+        s_tstart[d] = tstart;
+
+        // decoupled look-back over earlier tiles for this digit
+        uint32_t prefix = 0;
+        if (tile > 0) {
+            int64_t j = (int64_t)tile - 1;
+            for (;;) {
+                uint32_t s = ld_status(status + (uint64_t)j * 256 + d);
+                uint32_t flag = s & ~ST_VAL;
+                if (flag == 0) continue;  // predecessor not published yet
+                prefix += s & ST_VAL;
+                if (flag == ST_INC) break;
+                --j;
+            }
+            st_status(my, ST_INC | (prefix + cnt));
+        }
+        s_gbase[d] = digit_off[d] + prefix - tstart;
+        // the next pass uses the other status buffer: clear this tile's slot there
+        status_next[(uint64_t)tile * 256 + d] = 0u;
+    }
     __syncthreads();
 
+#if XH_SORT_DIRECT
+    // scatter straight from registers; the tile's keys of one digit still land
+    // in one contiguous range, so partial lines merge in L2
+#pragma unroll
+    for (int r = 0; r < SORT_ITEMS; ++r) {
+        uint64_t idx = wbase + (uint64_t)r * WAVE + lane;
+        if (idx < n) {
+            uint32_t dd = (uint32_t)(k[r] >> shift) & 255u;
+            uint32_t o = s_gbase[dd] + s_tstart[dd] + s_wcnt[wave][dd] + rank[r];
+            kout[o] = k[r];
+            if (HAS_VAL) vout[o] = v[r];
+        }
+    }
+#else
     // reorder the tile by digit in LDS
 #pragma unroll
     for (int r = 0; r < SORT_ITEMS; ++r) {
@@ -198,6 +275,7 @@ __global__ __launch_bounds__(SORT_BLOCK) void k_onesweep(
         kout[o] = key;
         if (HAS_VAL) vout[o] = s_vals[i];
     }
+#endif
 }
 
 __global__ void k_fill_u32(uint32_t *p, uint32_t v, uint64_t n) {
@@ -272,7 +350,7 @@ int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **va
     uint32_t *hist = st.hist, *off = st.hist + 8 * 256;
 
     fill_u32(ctx, hist, 0u, 8 * 256);
-    unsigned hg = grid_for(n, 256, (unsigned)ctx->num_cus * 4);
+    unsigned hg = grid_for(n, HIST_TILE, (unsigned)ctx->num_cus * 3);
     {
         Prof prof(ctx, XLOG_HIP_KERNEL_SORT_HIST, 8.0 * (double)n);
         hipLaunchKernelGGL(k_hist8, dim3(hg), dim3(256), 0, ctx->stream, *keys, n, hist);

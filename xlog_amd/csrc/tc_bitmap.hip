@@ -22,6 +22,8 @@ namespace xh {
 namespace {
 
 constexpr int TB = 256;
+constexpr int CHUNK_WORDS = 64;  // delta-row words compacted per round (<= 4096 set bits)
+constexpr int UNROLL = 4;        // adjacency lists loaded together per thread
 
 __global__ void k_edges_to_bits(const uint64_t *__restrict__ edges, uint64_t m, uint64_t words,
                                 uint64_t *__restrict__ R, uint64_t *__restrict__ D) {
@@ -68,29 +70,64 @@ __global__ __launch_bounds__(TB) void k_tc_step(uint32_t nv, uint64_t words, con
                                                 unsigned long long *__restrict__ count) {
     extern __shared__ uint64_t s_acc[];
     __shared__ unsigned long long s_cnt;
+    __shared__ uint64_t s_bits[CHUNK_WORDS];
+    __shared__ uint32_t s_woff[CHUNK_WORDS + 1];
+    __shared__ uint32_t s_y[CHUNK_WORDS * 64];
     const uint32_t x = blockIdx.x;
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
     if (!nz_cur[x]) {
         if (tid == 0) nz_next[x] = 0;
         return;
     }
     for (uint64_t w = tid; w < words; w += TB) s_acc[w] = 0ull;
     if (tid == 0) s_cnt = 0;
-    __syncthreads();
     const uint64_t *drow = D + (uint64_t)x * words;
-    for (uint64_t w = tid; w < words; w += TB) {
-        uint64_t bits = drow[w];
-        while (bits) {
-            int b = __builtin_ctzll(bits);
-            bits &= bits - 1;
-            uint32_t y = (uint32_t)(w * 64 + b);
-            for (uint64_t e = row_ptr[y], e1 = row_ptr[y + 1]; e < e1; ++e) {
-                uint32_t z = adj[e];
-                atomicOr((unsigned long long *)&s_acc[z >> 6], 1ull << (z & 63));
+    const uint64_t lt_mask = (1ull << lane) - 1ull;
+    // The delta row is consumed CHUNK_WORDS words at a time: its set bits y are
+    // compacted into s_y, then all threads expand adjacency lists of distinct
+    // y's (balanced regardless of where the bits sit), UNROLL lists in flight.
+    for (uint64_t c0 = 0; c0 < words; c0 += CHUNK_WORDS) {
+        if (wave == 0) {
+            uint64_t w = c0 + lane;
+            uint64_t bits = w < words ? drow[w] : 0ull;
+            uint32_t pc = (uint32_t)__popcll(bits), incl = pc;
+#pragma unroll
+            for (int o = 1; o < WAVE; o <<= 1) {
+                uint32_t t = __shfl_up(incl, o, WAVE);
+                if (lane >= o) incl += t;
+            }
+            s_bits[lane] = bits;
+            s_woff[lane] = incl - pc;
+            if (lane == WAVE - 1) s_woff[CHUNK_WORDS] = incl;
+        }
+        __syncthreads();
+        const uint32_t T = s_woff[CHUNK_WORDS];
+        if (T) {
+            for (int j = wave; j < CHUNK_WORDS; j += TB / WAVE) {
+                uint64_t bits = s_bits[j];
+                if ((bits >> lane) & 1ull)
+                    s_y[s_woff[j] + (uint32_t)__popcll(bits & lt_mask)] = (uint32_t)((c0 + j) * 64 + lane);
+            }
+            __syncthreads();
+            for (uint32_t q = tid; q < T; q += UNROLL * TB) {
+                uint64_t b[UNROLL], f[UNROLL];
+#pragma unroll
+                for (int u = 0; u < UNROLL; ++u) {
+                    uint32_t qq = q + u * TB;
+                    uint32_t y = qq < T ? s_y[qq] : 0u;
+                    b[u] = qq < T ? row_ptr[y] : 0ull;
+                    f[u] = qq < T ? row_ptr[y + 1] : 0ull;
+                }
+#pragma unroll
+                for (int u = 0; u < UNROLL; ++u)
+                    for (uint64_t e = b[u]; e < f[u]; ++e) {
+                        uint32_t z = adj[e];
+                        atomicOr((unsigned long long *)&s_acc[z >> 6], 1ull << (z & 63));
+                    }
             }
         }
+        __syncthreads();
     }
-    __syncthreads();
     uint64_t *rrow = R + (uint64_t)x * words;
     uint64_t *nrow = N + (uint64_t)x * words;
     unsigned long long local = 0;
@@ -139,6 +176,8 @@ __global__ __launch_bounds__(TB) void k_emit_rows(const uint64_t *__restrict__ R
                                                   const uint64_t *__restrict__ off, uint64_t *__restrict__ out) {
     __shared__ uint64_t s_part[TB / WAVE];
     __shared__ uint64_t s_base;
+    __shared__ uint64_t s_word[TB];
+    __shared__ uint64_t s_woff[TB];
     const uint32_t x = blockIdx.x;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint64_t *row = R + (uint64_t)x * words;
@@ -161,12 +200,19 @@ __global__ __launch_bounds__(TB) void k_emit_rows(const uint64_t *__restrict__ R
             if (q < wave) pre += s_part[q];
             tot += s_part[q];
         }
-        uint64_t pos = s_base + pre + x_incl - pc;
+        s_word[tid] = bits;
+        s_woff[tid] = s_base + pre + x_incl - pc;
+        __syncthreads();
+        // wave q writes words q*64 .. q*64+63 of the chunk, one word per step:
+        // lane b stores bit b, so a dense word is one contiguous 512-byte store
         const uint64_t hi = (uint64_t)x << 32;
-        while (bits) {
-            int b = __builtin_ctzll(bits);
-            bits &= bits - 1;
-            out[pos++] = hi | (uint64_t)(w * 64 + b);
+        const uint64_t lt_mask = (1ull << lane) - 1ull;
+        for (int j = 0; j < WAVE; ++j) {
+            const int t = wave * WAVE + j;
+            const uint64_t wb = s_word[t];
+            if (wb == 0ull) continue;
+            if ((wb >> lane) & 1ull)
+                out[s_woff[t] + (uint64_t)__popcll(wb & lt_mask)] = hi | (uint64_t)((c0 + t) * 64 + lane);
         }
         __syncthreads();
         if (tid == 0) s_base += tot;
