@@ -269,7 +269,10 @@ static uint64_t read_count(Ctx *ctx, const uint64_t *d) {
 
 // Sort a u64 key array of any length; the result is returned in a buffer
 // owned by the caller (either `keys` itself or a new one).
-static uint64_t *sort_keys(Ctx *ctx, uint64_t *keys, uint64_t n, bool keys_owned, int *passes = nullptr) {
+// digit_lo / digit_hi restrict the sort to 8-bit digits [lo, hi) (4..8 = by
+// the high word only, stable otherwise).
+static uint64_t *sort_keys(Ctx *ctx, uint64_t *keys, uint64_t n, bool keys_owned, int digit_lo = 0,
+                           int digit_hi = 8) {
     if (n < 2) {
         if (keys_owned || n == 0) return keys;
         uint64_t *c = static_cast<uint64_t *>(ctx->alloc(n * sizeof(uint64_t)));
@@ -278,18 +281,19 @@ static uint64_t *sort_keys(Ctx *ctx, uint64_t *keys, uint64_t n, bool keys_owned
     }
     const uint64_t CHUNK = 1ull << 29;
     if (n < (1ull << 30)) {
-        uint64_t *a = keys;
-        if (!keys_owned) {
-            a = static_cast<uint64_t *>(ctx->alloc(n * sizeof(uint64_t)));
-            copy_d2d(ctx, a, keys, n);
-        }
-        uint64_t *b = static_cast<uint64_t *>(ctx->alloc(n * sizeof(uint64_t)));
+        uint64_t *a = keys, *b = static_cast<uint64_t *>(ctx->alloc(n * sizeof(uint64_t)));
         uint32_t *v0 = nullptr, *v1 = nullptr;
-        int p = radix_sort_u64(ctx, &a, &b, &v0, &v1, n);
-        if (passes) *passes = p;
+        if (keys_owned) {
+            radix_sort_u64(ctx, &a, &b, &v0, &v1, n, digit_lo, digit_hi);
+        } else {
+            // the first pass reads the caller's keys; both ping-pong buffers are ours
+            a = static_cast<uint64_t *>(ctx->alloc(n * sizeof(uint64_t)));
+            radix_sort_u64(ctx, &a, &b, &v0, &v1, n, digit_lo, digit_hi, keys);
+        }
         ctx->free(b);
         return a;
     }
+    XH_REQUIRE(digit_lo == 0 && digit_hi == 8, XLOG_HIP_UNSUPPORTED, "partial-key sort above 2^30 keys");
     // chunked: sort pieces of 2^29 then merge pairwise
     uint64_t *a = keys;
     if (!keys_owned) {
@@ -529,20 +533,22 @@ static void build_join_index(Ctx *ctx, const uint64_t *keys, uint64_t n, uint32_
     J.n = n;
     uint64_t *sk = nullptr;
     bool own = false;
+    // only the key word needs ordering: runs of equal keys must be contiguous,
+    // the payload order inside a run is irrelevant (digits 4..7 only)
     if (arity == 1) {
         // (c0 << 32) | 0
         sk = static_cast<uint64_t *>(ctx->alloc((n ? n : 1) * sizeof(uint64_t)));
         swap_words(ctx, keys, n, sk);
         own = true;
-        sk = sort_keys(ctx, sk, n, true);
+        sk = sort_keys(ctx, sk, n, true, 4, 8);
     } else if (col == 0) {
         if (canonical) sk = const_cast<uint64_t *>(keys);
-        else { sk = sort_keys(ctx, const_cast<uint64_t *>(keys), n, false); own = true; }
+        else { sk = sort_keys(ctx, const_cast<uint64_t *>(keys), n, false, 4, 8); own = true; }
     } else {
         sk = static_cast<uint64_t *>(ctx->alloc((n ? n : 1) * sizeof(uint64_t)));
         swap_words(ctx, keys, n, sk);
         own = true;
-        sk = sort_keys(ctx, sk, n, true);
+        sk = sort_keys(ctx, sk, n, true, 4, 8);
     }
     build_run_index(ctx, sk, n, J.ix);
     J.payload = Buf<uint32_t>(ctx, n ? n : 1);

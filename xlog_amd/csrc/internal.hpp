@@ -212,12 +212,15 @@ void rel_free(xlog_hip_rel *r);
 // stream-ordered on ctx->stream.
 // ---------------------------------------------------------------------------
 
-// LSD radix sort of u64 keys with an optional u32 payload.  On return *keys
-// (and *vals) point at whichever of the two buffers holds the result; the
-// other is scratch.  Digits that are constant over the input are skipped.
-// Returns the number of digit passes executed.
+// LSD radix sort of u64 keys with an optional u32 payload, stable, over the
+// 8-bit digits [digit_lo, digit_hi) (0..8 = the whole key; 4..8 = the high
+// word only).  On return *keys (and *vals) point at whichever of the two
+// buffers holds the result; the other is scratch.  Digits that are constant
+// over the input are skipped.  Returns the number of digit passes executed.
+// With `src` (keys only) the first pass reads src and both buffers are
+// scratch, so an input that must not be modified is never copied first.
 int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **vals, uint32_t **vals_alt,
-                   uint64_t n);
+                   uint64_t n, int digit_lo = 0, int digit_hi = 8, const uint64_t *src = nullptr);
 
 // Stream compaction family (single pass, decoupled look-back).  Each writes
 // the selected keys in input order to `out` and the count to *d_count

@@ -21,22 +21,30 @@ namespace xh {
 
 namespace {
 
-// tile shape: SORT_BLOCK threads (>= 256; threads 0..255 own one digit each in
-// the counting phase) x SORT_ITEMS keys per thread
-#ifndef XH_SORT_BLOCK
-#define XH_SORT_BLOCK 512
+// Tile shapes: BLOCK threads (>= 256; threads 0..255 own one digit each in
+// the counting phase) x ITEMS keys per thread.  Measured on MI355X over 2^28
+// random keys: 512x16 (8192 keys, 74 KB LDS, 2 blocks per CU) beats 256x16,
+// 256x32, 768x16, 1024x8/12/16 and a direct (no LDS staging) scatter.
+// Key + payload sorts need LDS for the payload too, hence a smaller tile.
+#ifndef XH_SORT_BLOCK_K
+#define XH_SORT_BLOCK_K 512
+#endif
+#ifndef XH_SORT_ITEMS_K
+#define XH_SORT_ITEMS_K 16
+#endif
+#ifndef XH_SORT_BLOCK_V
+#define XH_SORT_BLOCK_V 256
+#endif
+#ifndef XH_SORT_ITEMS_V
+#define XH_SORT_ITEMS_V 16
 #endif
 #ifndef XH_SORT_DIRECT
 #define XH_SORT_DIRECT 0
 #endif
-#ifndef XH_SORT_ITEMS
-#define XH_SORT_ITEMS 16
-#endif
-constexpr int SORT_BLOCK = XH_SORT_BLOCK;
-constexpr int SORT_ITEMS = XH_SORT_ITEMS;
-constexpr int SORT_WAVES = SORT_BLOCK / WAVE;
-constexpr int SORT_TILE = SORT_BLOCK * SORT_ITEMS;
-static_assert(SORT_BLOCK >= 256 && SORT_BLOCK % 256 == 0, "digit phase needs 256 threads");
+constexpr int SORT_BLOCK_K = XH_SORT_BLOCK_K, SORT_ITEMS_K = XH_SORT_ITEMS_K;
+constexpr int SORT_BLOCK_V = XH_SORT_BLOCK_V, SORT_ITEMS_V = XH_SORT_ITEMS_V;
+static_assert(SORT_BLOCK_K >= 256 && SORT_BLOCK_K % 256 == 0 && SORT_BLOCK_V >= 256 && SORT_BLOCK_V % 256 == 0,
+              "digit phase needs 256 threads");
 constexpr int HIST_SEG = 16;                // consecutive keys per thread (run-length aggregated)
 constexpr int HIST_TILE = 256 * HIST_SEG;   // keys staged in LDS per block iteration
 constexpr uint32_t ST_AGG = 1u << 30;
@@ -63,18 +71,33 @@ __global__ __launch_bounds__(256) void k_hist8(const uint64_t *__restrict__ keys
     __shared__ uint32_t s_hi[HIST_TILE + HIST_TILE / HIST_SEG];
     const int tid = threadIdx.x;
     for (int i = tid; i < 8 * 256; i += blockDim.x) (&h[0][0])[i] = 0;
-    for (uint64_t t0 = (uint64_t)blockIdx.x * HIST_TILE; t0 < n; t0 += (uint64_t)gridDim.x * HIST_TILE) {
+    const uint64_t gstride = (uint64_t)gridDim.x * HIST_TILE;
+    // keys of the next tile are prefetched into registers while the current
+    // tile is counted from LDS
+    uint64_t pre[HIST_SEG];
+    uint64_t t0 = (uint64_t)blockIdx.x * HIST_TILE;
+#pragma unroll
+    for (int r = 0; r < HIST_SEG; ++r) {
+        uint64_t j = t0 + r * 256 + tid;
+        pre[r] = j < n ? __builtin_nontemporal_load(keys + j) : 0ull;
+    }
+    for (; t0 < n; t0 += gstride) {
         const uint32_t cnt = (n - t0) < (uint64_t)HIST_TILE ? (uint32_t)(n - t0) : (uint32_t)HIST_TILE;
         __syncthreads();
 #pragma unroll
         for (int r = 0; r < HIST_SEG; ++r) {
             uint32_t j = r * 256 + tid;
             if (j < cnt) {
-                uint64_t k = __builtin_nontemporal_load(keys + t0 + j);
                 uint32_t pj = j + (j / HIST_SEG);
-                s_lo[pj] = (uint32_t)k;
-                s_hi[pj] = (uint32_t)(k >> 32);
+                s_lo[pj] = (uint32_t)pre[r];
+                s_hi[pj] = (uint32_t)(pre[r] >> 32);
             }
+        }
+        const uint64_t t1 = t0 + gstride;
+#pragma unroll
+        for (int r = 0; r < HIST_SEG; ++r) {
+            uint64_t j = t1 + r * 256 + tid;
+            pre[r] = j < n ? __builtin_nontemporal_load(keys + j) : 0ull;
         }
         __syncthreads();
         const uint32_t base = tid * HIST_SEG;
@@ -136,41 +159,41 @@ __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v, int lane) {
     return v;
 }
 
-template <bool HAS_VAL>
-__global__ __launch_bounds__(SORT_BLOCK) void k_onesweep(
+template <bool HAS_VAL, int BLOCK, int ITEMS>
+__global__ __launch_bounds__(BLOCK) void k_onesweep(
     const uint64_t *__restrict__ kin, uint64_t *__restrict__ kout, const uint32_t *__restrict__ vin,
     uint32_t *__restrict__ vout, uint64_t n, int shift, const uint32_t *__restrict__ digit_off,
     uint32_t *status, uint32_t *status_next, unsigned long long *ticket, unsigned long long ticket_base) {
     __shared__ uint32_t s_tile;
-    __shared__ uint32_t s_wcnt[SORT_WAVES][256];
+    __shared__ uint32_t s_wcnt[(BLOCK / WAVE)][256];
     __shared__ uint32_t s_tstart[256];
     __shared__ uint32_t s_gbase[256];
-    __shared__ uint32_t s_wsum[SORT_WAVES];
+    __shared__ uint32_t s_wsum[(BLOCK / WAVE)];
 #if !XH_SORT_DIRECT
-    __shared__ uint64_t s_keys[SORT_TILE];
-    __shared__ uint32_t s_vals[HAS_VAL ? SORT_TILE : 1];
+    __shared__ uint64_t s_keys[(BLOCK * ITEMS)];
+    __shared__ uint32_t s_vals[HAS_VAL ? (BLOCK * ITEMS) : 1];
 #endif
 
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
     if (tid == 0) s_tile = (uint32_t)(atomicAdd(ticket, 1ull) - ticket_base);
-    for (int i = tid; i < SORT_WAVES * 256; i += SORT_BLOCK) (&s_wcnt[0][0])[i] = 0;
+    for (int i = tid; i < (BLOCK / WAVE) * 256; i += BLOCK) (&s_wcnt[0][0])[i] = 0;
     __syncthreads();
     const uint32_t tile = s_tile;
-    const uint64_t wbase = (uint64_t)tile * SORT_TILE + (uint64_t)wave * (SORT_ITEMS * WAVE);
+    const uint64_t wbase = (uint64_t)tile * (BLOCK * ITEMS) + (uint64_t)wave * (ITEMS * WAVE);
     const uint64_t lt_mask = (1ull << lane) - 1ull;
 
-    uint64_t k[SORT_ITEMS];
-    uint32_t v[SORT_ITEMS];
-    uint32_t rank[SORT_ITEMS];
+    uint64_t k[ITEMS];
+    uint32_t v[ITEMS];
+    uint32_t rank[ITEMS];
 #pragma unroll
-    for (int r = 0; r < SORT_ITEMS; ++r) {
+    for (int r = 0; r < ITEMS; ++r) {
         uint64_t idx = wbase + (uint64_t)r * WAVE + lane;
         bool valid = idx < n;
         k[r] = valid ? kin[idx] : 0ull;
         if (HAS_VAL) v[r] = valid ? vin[idx] : 0u;
     }
 #pragma unroll
-    for (int r = 0; r < SORT_ITEMS; ++r) {
+    for (int r = 0; r < ITEMS; ++r) {
         uint64_t idx = wbase + (uint64_t)r * WAVE + lane;
         bool valid = idx < n;
         uint32_t d = (uint32_t)(k[r] >> shift) & 255u;
@@ -200,7 +223,7 @@ __global__ __launch_bounds__(SORT_BLOCK) void k_onesweep(
     uint32_t *my = status + (uint64_t)tile * 256 + d;
     if (digit_thread) {
 #pragma unroll
-        for (int w = 0; w < SORT_WAVES; ++w) {
+        for (int w = 0; w < (BLOCK / WAVE); ++w) {
             uint32_t c = s_wcnt[w][d];
             s_wcnt[w][d] = cnt;
             cnt += c;
@@ -244,7 +267,7 @@ __global__ __launch_bounds__(SORT_BLOCK) void k_onesweep(
     // scatter straight from registers; the tile's keys of one digit still land
     // in one contiguous range, so partial lines merge in L2
 #pragma unroll
-    for (int r = 0; r < SORT_ITEMS; ++r) {
+    for (int r = 0; r < ITEMS; ++r) {
         uint64_t idx = wbase + (uint64_t)r * WAVE + lane;
         if (idx < n) {
             uint32_t dd = (uint32_t)(k[r] >> shift) & 255u;
@@ -256,7 +279,7 @@ __global__ __launch_bounds__(SORT_BLOCK) void k_onesweep(
 #else
     // reorder the tile by digit in LDS
 #pragma unroll
-    for (int r = 0; r < SORT_ITEMS; ++r) {
+    for (int r = 0; r < ITEMS; ++r) {
         uint64_t idx = wbase + (uint64_t)r * WAVE + lane;
         if (idx < n) {
             uint32_t dd = (uint32_t)(k[r] >> shift) & 255u;
@@ -266,9 +289,9 @@ __global__ __launch_bounds__(SORT_BLOCK) void k_onesweep(
         }
     }
     __syncthreads();
-    const uint64_t t0 = (uint64_t)tile * SORT_TILE;
-    const uint32_t tn = (uint32_t)((n - t0) < (uint64_t)SORT_TILE ? (n - t0) : (uint64_t)SORT_TILE);
-    for (uint32_t i = tid; i < tn; i += SORT_BLOCK) {
+    const uint64_t t0 = (uint64_t)tile * (BLOCK * ITEMS);
+    const uint32_t tn = (uint32_t)((n - t0) < (uint64_t)(BLOCK * ITEMS) ? (n - t0) : (uint64_t)(BLOCK * ITEMS));
+    for (uint32_t i = tid; i < tn; i += BLOCK) {
         uint64_t key = s_keys[i];
         uint32_t dd = (uint32_t)(key >> shift) & 255u;
         uint32_t o = s_gbase[dd] + i;
@@ -340,12 +363,17 @@ static SortState &sort_state(Ctx *ctx, uint64_t tiles) {
 }
 
 int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **vals, uint32_t **vals_alt,
-                   uint64_t n) {
-    if (n < 2) return 0;
+                   uint64_t n, int digit_lo, int digit_hi, const uint64_t *src) {
+    if (n < 2 || digit_lo >= digit_hi) {
+        if (src && n) XH_CHECK_HIP(hipMemcpyAsync(*keys, src, n * 8, hipMemcpyDeviceToDevice, ctx->stream));
+        return 0;
+    }
+    XH_REQUIRE(!(src && vals && *vals), XLOG_HIP_INVALID_ARG, "radix sort: a separate source is keys-only");
     XH_REQUIRE(n < (1ull << 30), XLOG_HIP_CAPACITY_OVERFLOW,
                "radix sort: a single sort call is limited to 2^30 - 1 keys");
     const bool has_val = vals && *vals;
-    const uint64_t tiles = (n + SORT_TILE - 1) / SORT_TILE;
+    const uint64_t tile_keys = has_val ? (uint64_t)SORT_BLOCK_V * SORT_ITEMS_V : (uint64_t)SORT_BLOCK_K * SORT_ITEMS_K;
+    const uint64_t tiles = (n + tile_keys - 1) / tile_keys;
     SortState &st = sort_state(ctx, tiles);
     uint32_t *hist = st.hist, *off = st.hist + 8 * 256;
 
@@ -353,7 +381,7 @@ int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **va
     unsigned hg = grid_for(n, HIST_TILE, (unsigned)ctx->num_cus * 3);
     {
         Prof prof(ctx, XLOG_HIP_KERNEL_SORT_HIST, 8.0 * (double)n);
-        hipLaunchKernelGGL(k_hist8, dim3(hg), dim3(256), 0, ctx->stream, *keys, n, hist);
+        hipLaunchKernelGGL(k_hist8, dim3(hg), dim3(256), 0, ctx->stream, src ? src : *keys, n, hist);
     }
     XH_CHECK_HIP(hipGetLastError());
     hipLaunchKernelGGL(k_digit_offsets, dim3(1), dim3(64), 0, ctx->stream, hist, off);
@@ -366,7 +394,7 @@ int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **va
     int passes = 0;
     int cur = 0;  // status buffer for the next pass
     if (st.dirty[0] == 0) cur = 0; else if (st.dirty[1] == 0) cur = 1; else cur = 0;
-    for (int dgt = 0; dgt < 8; ++dgt) {
+    for (int dgt = digit_lo; dgt < digit_hi; ++dgt) {
         bool trivial = false;
         for (int b = 0; b < 256; ++b)
             if (h_hist[dgt * 256 + b] == n) { trivial = true; break; }
@@ -379,13 +407,14 @@ int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **va
         unsigned long long tb = ctx->take_tickets(0, tiles);
         Prof prof(ctx, XLOG_HIP_KERNEL_SORT_PASS, (has_val ? 24.0 : 16.0) * (double)n);
         if (has_val)
-            hipLaunchKernelGGL(k_onesweep<true>, dim3((unsigned)tiles), dim3(SORT_BLOCK), 0, ctx->stream, *keys,
+            hipLaunchKernelGGL((k_onesweep<true, SORT_BLOCK_V, SORT_ITEMS_V>), dim3((unsigned)tiles), dim3(SORT_BLOCK_V), 0, ctx->stream, *keys,
                                *keys_alt, *vals, *vals_alt, n, 8 * dgt, off + dgt * 256, st.status[cur],
                                st.status[nxt], ctx->tickets + 0, tb);
         else
-            hipLaunchKernelGGL(k_onesweep<false>, dim3((unsigned)tiles), dim3(SORT_BLOCK), 0, ctx->stream, *keys,
-                               *keys_alt, nullptr, nullptr, n, 8 * dgt, off + dgt * 256, st.status[cur],
-                               st.status[nxt], ctx->tickets + 0, tb);
+            hipLaunchKernelGGL((k_onesweep<false, SORT_BLOCK_K, SORT_ITEMS_K>), dim3((unsigned)tiles),
+                               dim3(SORT_BLOCK_K), 0, ctx->stream, (passes == 0 && src) ? src : *keys, *keys_alt,
+                               nullptr, nullptr, n, 8 * dgt, off + dgt * 256, st.status[cur], st.status[nxt],
+                               ctx->tickets + 0, tb);
         XH_CHECK_HIP(hipGetLastError());
         st.dirty[cur] = tiles;
         if (st.dirty[nxt] <= tiles) st.dirty[nxt] = 0;
@@ -394,6 +423,7 @@ int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **va
         cur = nxt;
         ++passes;
     }
+    if (passes == 0 && src) XH_CHECK_HIP(hipMemcpyAsync(*keys, src, n * 8, hipMemcpyDeviceToDevice, ctx->stream));
     return passes;
 }
 
