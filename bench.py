@@ -30,6 +30,9 @@ import numpy as np  # noqa: E402
 
 METRIC = "semi-naive fixpoint wall time + join/sort tuples/s; % of HBM peak, 1 MI355X"
 HBM_PEAK_GBS = 8000.0
+# Measured HBM traffic / algorithmic bytes per launch from the rocprofv3 FETCH_SIZE + WRITE_SIZE runs of
+# profiles/c2_radix_probe_dedup_hbm_traffic.md (FETCH scaled x2, WRITE x1 by the copy calibration there).
+TRAFFIC_RATIO = {"sort_pass": 1.09, "probe_emit": 1.51, "select": 1.01}
 
 
 def log(msg: str) -> None:
@@ -206,8 +209,10 @@ def main() -> int:
     avg_ms = d["total_ms"] / max(1, d["launches"])
     bytes_per_launch = d["algo_bytes"] / max(1, d["launches"])
     achieved = (bytes_per_launch / (avg_ms / 1000.0)) / 1e9 if avg_ms > 0 else 0.0
+    traffic = TRAFFIC_RATIO.get(dname)
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": dname,
+                "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": round(traffic * bytes_per_launch) if traffic else None, "kernel": dname,
                 "launches_per_step": d["launches"] / max(1, args.steps), "avg_launch_ms": round(avg_ms, 4),
                 "algo_bytes_per_launch": bytes_per_launch}
     kernels = {k: {"launches": v["launches"], "total_ms": round(v["total_ms"], 3),

@@ -116,6 +116,27 @@ def test_andersen_small_vs_oracle(provider, n_vars, n_facts):
     assert st["delta_sizes"] == deltas_o
 
 
+def test_chunked_join_fold_parity(provider, monkeypatch):
+    """Join outputs above the chunk size are produced as sorted sets chunk by
+    chunk; forcing tiny chunks must not change any fixpoint result
+    (the reference's multi-chunk fold parity, set_ops_tests.rs:524-587)."""
+    p = provider
+    f = datagen.andersen(400, 1500, 1.5, datagen.seed_for(5))
+    rels = [pack(*f[k]) for k in ("assign", "addressOf", "load", "store")]
+    outs_o, it_o, deltas_o = oracle.seminaive(andersen_plan(), rels + [None])
+    src, dst = datagen.random_digraph(300, 1200, 11)
+    tc_o = oracle.bfs_tc(300, src, dst)
+    for chunk in ("1", "777", "100000"):
+        monkeypatch.setenv("XLOG_HIP_JOIN_CHUNK_ROWS", chunk)
+        dev = [p.create_buffer_from_packed(r) for r in rels] + [None]
+        outs, st = p.fixpoint(andersen_plan(), dev)
+        assert np.array_equal(p.download_packed(outs[4]), outs_o[4])
+        assert st["iterations"] == it_o and st["delta_sizes"] == deltas_o
+        e = p.create_buffer_from_u32_columns([src, dst])
+        o2, st2 = p.fixpoint(tc_plan(), [e, None], route=ROUTE_JOIN)
+        assert np.array_equal(p.download_packed(o2[1]), tc_o["relation"]) and st2["iterations"] == tc_o["iterations"]
+
+
 def test_iteration_limit_is_an_error(provider):
     src, dst = datagen.chain(20)
     e = provider.create_buffer_from_u32_columns([src, dst])

@@ -556,6 +556,75 @@ static void build_join_index(Ctx *ctx, const uint64_t *keys, uint64_t n, uint32_
     if (own) ctx->free(sk);
 }
 
+// Join step of a rule body with bounded memory.  A probe output of at most
+// kChunkRows rows is emitted whole (a bag).  A larger one is emitted in tile
+// ranges of at most kChunkRows rows; each range is sorted and deduplicated and
+// merged into the result, which is then a sorted set.  Rule bodies only feed
+// set operations (union, diff), so either form gives the same fixpoint, and
+// duplicate-heavy joins (points-to hubs) no longer materialise their bag.
+// XLOG_HIP_JOIN_CHUNK_ROWS overrides the chunk size (tests force multi-chunk
+// folds with it, like the reference's XLOG_UNION_CHUNK_BYTES, relational.rs:36-42).
+static uint64_t join_chunk_rows() {
+    const char *e = getenv("XLOG_HIP_JOIN_CHUNK_ROWS");
+    if (e && *e) {
+        unsigned long long v = strtoull(e, nullptr, 10);
+        if (v > 0) return v;
+    }
+    return 1ull << 28;
+}
+static uint64_t join_step(Ctx *ctx, const uint64_t *probe, uint64_t n, int pcol, const JoinIndex &J, const int oc[4],
+                          uint64_t **out) {
+    const uint64_t kChunkRows = join_chunk_rows();
+    ProbeJob job;
+    job.probe = probe;
+    job.n = n;
+    job.pcol = pcol;
+    job.ix = &J.ix;
+    job.payload = J.payload.p;
+    *out = nullptr;
+    uint64_t total = probe_prepare(ctx, job);
+    if (total == 0) return 0;
+    if (total <= kChunkRows) {
+        uint64_t *o = static_cast<uint64_t *>(ctx->alloc(total * sizeof(uint64_t)));
+        probe_emit_range(ctx, job, 0, job.tiles, total, 2, oc, o, nullptr);
+        *out = o;
+        return total;
+    }
+    std::vector<uint64_t> off = probe_tile_offsets(ctx, job);
+    uint64_t *acc = nullptr, acc_n = 0;
+    for (uint64_t t0 = 0; t0 < job.tiles;) {
+        uint64_t t1 = t0 + 1;
+        while (t1 < job.tiles && off[t1 + 1] - off[t0] <= kChunkRows) ++t1;
+        const uint64_t m = off[t1] - off[t0];
+        if (m) {
+            uint64_t *b = static_cast<uint64_t *>(ctx->alloc(m * sizeof(uint64_t)));
+            probe_emit_range(ctx, job, t0, t1, m, 2, oc, b, nullptr);
+            uint64_t *s = sort_keys(ctx, b, m, true);
+            if (s != b) ctx->free(b);
+            uint64_t *u;
+            uint64_t un = unique_keys(ctx, s, m, &u);
+            ctx->free(s);
+            if (!acc) {
+                acc = u;
+                acc_n = un;
+            } else {
+                uint64_t *mg = static_cast<uint64_t *>(ctx->alloc((acc_n + un) * sizeof(uint64_t)));
+                merge_sorted(ctx, acc, acc_n, u, un, mg);
+                ctx->free(acc);
+                ctx->free(u);
+                uint64_t *u2;
+                uint64_t n2 = unique_keys(ctx, mg, acc_n + un, &u2);
+                ctx->free(mg);
+                acc = u2;
+                acc_n = n2;
+            }
+        }
+        t0 = t1;
+    }
+    *out = acc;
+    return acc_n;
+}
+
 // value-index of a relation column for the probe side: arity 1 stores c0 in
 // the low word (v1), arity 2 stores c0 high (v0) and c1 low (v1)
 static int probe_vidx(uint32_t arity, uint32_t c) { return arity == 1 ? 1 : (int)c; }
@@ -756,7 +825,7 @@ struct Driver {
             if (ar.n != 0) {
                 const JoinIndex &J = index_of(ar, apos);
                 int oc[4] = {sel[0], sel[1], 0, 0};
-                on = join_probe_general(ctx, bk, bn, bpos, J.ix, J.payload.p, 2, oc, &o, nullptr);
+                on = join_step(ctx, bk, bn, bpos, J, oc, &o);
             }
             if (owned) ctx->free(owned);
             owned = o;

@@ -258,6 +258,24 @@ void build_run_index(Ctx *ctx, const uint64_t *sorted_keys, uint64_t n, RunIndex
 uint64_t join_probe_project(Ctx *ctx, const uint64_t *probe, uint64_t n, int pcol, const RunIndex &ix,
                             const uint32_t *payload, int oc0, int oc1, uint64_t **out);
 
+// Probe in pieces: a count pass over all probe tiles (tile offsets on the
+// device, total read back), then emits of tile ranges.  Tile t covers probe
+// rows [t * 4096, (t + 1) * 4096).
+struct ProbeJob {
+    const uint64_t *probe = nullptr;
+    uint64_t n = 0;
+    int pcol = 0;
+    const RunIndex *ix = nullptr;
+    const uint32_t *payload = nullptr;
+    Buf<uint64_t> toff;  // exclusive prefix of per-tile output counts; toff[tiles] = total
+    uint64_t tiles = 0, total = 0;
+};
+uint64_t probe_prepare(Ctx *ctx, ProbeJob &job);
+std::vector<uint64_t> probe_tile_offsets(Ctx *ctx, const ProbeJob &job);
+// writes the `rows` outputs of tiles [t0, t1) to out0 / out1 starting at index 0
+void probe_emit_range(Ctx *ctx, const ProbeJob &job, uint64_t t0, uint64_t t1, uint64_t rows, int out_arity,
+                      const int oc[4], uint64_t *out0, uint64_t *out1);
+
 // small helpers
 inline unsigned grid_for(uint64_t n, unsigned block, unsigned cap) {
     uint64_t g = (n + block - 1) / block;

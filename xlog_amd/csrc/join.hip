@@ -21,6 +21,8 @@
 //            The projection is fused into the emit.
 #include "internal.hpp"
 
+#include <algorithm>
+
 namespace xh {
 
 namespace {
@@ -162,14 +164,18 @@ __device__ __forceinline__ void make_words(const OutSpec &o, const uint32_t v[4]
     else *w1 = 0;
 }
 
-__global__ __launch_bounds__(JB) void k_probe_emit(ProbeArgs a, const uint64_t *__restrict__ tile_off, OutSpec spec,
-                                                   uint64_t *__restrict__ out0, uint64_t *__restrict__ out1) {
+// Emits the outputs of tiles [t0, t0 + gridDim.x); output index 0 is the
+// first output of tile t0.
+__global__ __launch_bounds__(JB) void k_probe_emit(ProbeArgs a, const uint64_t *__restrict__ tile_off, uint64_t t0,
+                                                   OutSpec spec, uint64_t *__restrict__ out0,
+                                                   uint64_t *__restrict__ out1) {
     __shared__ uint64_t s_wtot[JWAVES];
     __shared__ uint64_t s_ex[JWAVES][WAVE + 1];
     __shared__ uint64_t s_row[JWAVES][WAVE];
     __shared__ uint64_t s_st[JWAVES][WAVE];
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
-    const uint64_t wbase = (uint64_t)blockIdx.x * JTILE + (uint64_t)wave * (JITEMS * WAVE);
+    const uint64_t tile = t0 + blockIdx.x;
+    const uint64_t wbase = tile * JTILE + (uint64_t)wave * (JITEMS * WAVE);
 
     // pass 1 over this wave's rows: total outputs of the wave
     uint64_t acc = 0;
@@ -185,7 +191,7 @@ __global__ __launch_bounds__(JB) void k_probe_emit(ProbeArgs a, const uint64_t *
     for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, WAVE);
     if (lane == 0) s_wtot[wave] = acc;
     __syncthreads();
-    uint64_t base = tile_off[blockIdx.x];
+    uint64_t base = tile_off[tile] - tile_off[t0];
     for (int w = 0; w < wave; ++w) base += s_wtot[w];
 
     // pass 2: expand round by round
@@ -276,36 +282,72 @@ static int table_bits(const RunIndex &ix) {
     return bits;
 }
 
+static ProbeArgs probe_args(const ProbeJob &job) {
+    const RunIndex &ix = *job.ix;
+    return ProbeArgs{job.probe, job.n, job.pcol, ix.table.p, ix.table_mask, table_bits(ix), ix.run_start.p,
+                     job.payload};
+}
+
+uint64_t probe_prepare(Ctx *ctx, ProbeJob &job) {
+    job.tiles = (job.n + JTILE - 1) / JTILE;
+    job.total = 0;
+    if (job.n == 0 || job.ix->nruns == 0) return 0;
+    XH_REQUIRE(job.tiles < (1ull << 31), XLOG_HIP_CAPACITY_OVERFLOW, "join probe: input too large");
+    ProbeArgs a = probe_args(job);
+    job.toff = Buf<uint64_t>(ctx, job.tiles + 1);
+    {
+        Prof prof(ctx, XLOG_HIP_KERNEL_PROBE_COUNT, 8.0 * (double)job.n);
+        hipLaunchKernelGGL(k_probe_count, dim3((unsigned)job.tiles), dim3(JB), 0, ctx->stream, a, job.toff.p);
+        XH_CHECK_HIP(hipGetLastError());
+    }
+    hipLaunchKernelGGL(k_scan_small, dim3(1), dim3(1024), 0, ctx->stream, job.toff.p, job.tiles,
+                       job.toff.p + job.tiles);
+    XH_CHECK_HIP(hipGetLastError());
+    ctx->read_scalars(job.toff.p + job.tiles, 1);
+    job.total = ctx->host_scalars[0];
+    return job.total;
+}
+
+std::vector<uint64_t> probe_tile_offsets(Ctx *ctx, const ProbeJob &job) {
+    std::vector<uint64_t> h(job.tiles + 1, 0);
+    if (job.tiles) {
+        XH_CHECK_HIP(hipMemcpyAsync(h.data(), job.toff.p, (job.tiles + 1) * sizeof(uint64_t), hipMemcpyDeviceToHost,
+                                    ctx->stream));
+        ctx->sync();
+    }
+    return h;
+}
+
+void probe_emit_range(Ctx *ctx, const ProbeJob &job, uint64_t t0, uint64_t t1, uint64_t rows, int out_arity,
+                      const int oc[4], uint64_t *out0, uint64_t *out1) {
+    if (t1 <= t0) return;
+    ProbeArgs a = probe_args(job);
+    OutSpec spec{out_arity, {oc[0], oc[1], oc[2], oc[3]}};
+    uint64_t nprobe = std::min<uint64_t>(job.n, t1 * JTILE) - t0 * JTILE;
+    // probe row 8 B + slot/run 16 B per probe row; payload 4 B + output 8 B per match
+    Prof prof(ctx, XLOG_HIP_KERNEL_PROBE_EMIT,
+              24.0 * (double)nprobe + (4.0 + 8.0 * (out_arity > 2 ? 2 : 1)) * (double)rows);
+    hipLaunchKernelGGL(k_probe_emit, dim3((unsigned)(t1 - t0)), dim3(JB), 0, ctx->stream, a, job.toff.p, t0, spec,
+                       out0, out1);
+    XH_CHECK_HIP(hipGetLastError());
+}
+
 uint64_t join_probe_general(Ctx *ctx, const uint64_t *probe, uint64_t n, int pcol, const RunIndex &ix,
                             const uint32_t *payload, int out_arity, const int oc[4], uint64_t **out0,
                             uint64_t **out1) {
     *out0 = nullptr;
     if (out1) *out1 = nullptr;
-    if (n == 0 || ix.nruns == 0) return 0;
-    ProbeArgs a{probe, n, pcol, ix.table.p, ix.table_mask, table_bits(ix), ix.run_start.p, payload};
-    uint64_t tiles = (n + JTILE - 1) / JTILE;
-    XH_REQUIRE(tiles < (1ull << 31), XLOG_HIP_CAPACITY_OVERFLOW, "join probe: input too large");
-    Buf<uint64_t> toff(ctx, tiles + 1);
-    {
-        Prof prof(ctx, XLOG_HIP_KERNEL_PROBE_COUNT, 8.0 * (double)n);
-        hipLaunchKernelGGL(k_probe_count, dim3((unsigned)tiles), dim3(JB), 0, ctx->stream, a, toff.p);
-        XH_CHECK_HIP(hipGetLastError());
-    }
-    hipLaunchKernelGGL(k_scan_small, dim3(1), dim3(1024), 0, ctx->stream, toff.p, tiles, toff.p + tiles);
-    XH_CHECK_HIP(hipGetLastError());
-    ctx->read_scalars(toff.p + tiles, 1);
-    uint64_t total = ctx->host_scalars[0];
+    ProbeJob job;
+    job.probe = probe;
+    job.n = n;
+    job.pcol = pcol;
+    job.ix = &ix;
+    job.payload = payload;
+    uint64_t total = probe_prepare(ctx, job);
     if (total == 0) return 0;
     uint64_t *o0 = static_cast<uint64_t *>(ctx->alloc(total * sizeof(uint64_t)));
     uint64_t *o1 = (out_arity > 2) ? static_cast<uint64_t *>(ctx->alloc(total * sizeof(uint64_t))) : nullptr;
-    OutSpec spec{out_arity, {oc[0], oc[1], oc[2], oc[3]}};
-    {
-        // probe row 8 B + slot/run 16 B per probe row; payload 4 B + output 8 B per match
-        Prof prof(ctx, XLOG_HIP_KERNEL_PROBE_EMIT,
-                  24.0 * (double)n + (4.0 + 8.0 * (out_arity > 2 ? 2 : 1)) * (double)total);
-        hipLaunchKernelGGL(k_probe_emit, dim3((unsigned)tiles), dim3(JB), 0, ctx->stream, a, toff.p, spec, o0, o1);
-        XH_CHECK_HIP(hipGetLastError());
-    }
+    probe_emit_range(ctx, job, 0, job.tiles, total, out_arity, oc, o0, o1);
     *out0 = o0;
     if (out1) *out1 = o1;
     return total;
