@@ -43,7 +43,7 @@ def make_workload(name: str, p):
     """Returns (step_fn, units_per_step, unit_desc, config, checker_inputs)."""
     from xlog_amd import datagen, tc_plan, andersen_plan, pack
 
-    if name == "c2":
+    if name in ("c2", "c2u"):
         cfg = datagen.C2
         t = time.perf_counter()
         r_a, r_b, s_b, s_c = datagen.zipf_join(cfg["n_r"], cfg["n_s"], cfg["n_keys"], cfg["zipf_s"], datagen.seed_for(2))
@@ -52,14 +52,23 @@ def make_workload(name: str, p):
         S = p.create_buffer_from_u32_columns([s_b, s_c])
         state = {}
 
-        def step():
-            j = p.join_project(R, S, 1, 0, [0, 3])
-            d = p.dedup_full_row(j)
-            state["join_rows"] = j.num_rows()
-            state["out_rows"] = d.num_rows()
+        if name == "c2":
+            # fused operator: the join is emitted in (a, c) order, no sort of the 2^28-row output
+            def step():
+                d = p.join_project_dedup(R, S, 1, 0, [0, 3])
+                state["out_rows"] = d.num_rows()
+        else:
+            # unfused: join + project (bag of ~2^28 rows), then radix sort + unique
+            def step():
+                j = p.join_project(R, S, 1, 0, [0, 3])
+                d = p.dedup_full_row(j)
+                state["join_rows"] = j.num_rows()
+                state["out_rows"] = d.num_rows()
 
         units = cfg["n_r"] + cfg["n_s"]
-        config = {"workload": "c2: R(a,b) join S(b,c) on b, project (a,c), sort + dedup",
+        how = ("fused order-preserving join+project+dedup" if name == "c2"
+               else "join+project, then radix sort + unique of the join output")
+        config = {"workload": f"c2: R(a,b) join S(b,c) on b, project (a,c), sort + dedup ({how})",
                   "rows_r": cfg["n_r"], "rows_s": cfg["n_s"], "keys": cfg["n_keys"], "zipf_s_probe_side": cfg["zipf_s"],
                   "build_side_keys": "uniform", "seed": datagen.seed_for(2)}
         return step, units, "input tuples (|R|+|S|)", config, (r_a, r_b, s_b, s_c), state
@@ -129,7 +138,7 @@ def cpu_baseline(name: str, inputs, budget_s: float = 30.0):
     import oracle
     from xlog_amd import pack, tc_plan
 
-    if name == "c2":
+    if name in ("c2", "c2u"):
         r_a, r_b, s_b, s_c = inputs
         n_r = 1 << 22
         l = pack(r_a[:n_r], r_b[:n_r])

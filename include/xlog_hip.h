@@ -143,6 +143,14 @@ xlog_hip_status xlog_hip_sort_merge_join(xlog_hip_ctx *ctx, const xlog_hip_rel *
 xlog_hip_status xlog_hip_join_project(xlog_hip_ctx *ctx, const xlog_hip_rel *left, const xlog_hip_rel *right,
                                       uint32_t left_key, uint32_t right_key, const uint32_t *out_cols,
                                       uint32_t n_out, xlog_hip_rel **out);
+/* Canonical set of the projected join: dedup_full_row(project(join(left, right))).
+ * This is the ChainJoin -> Project -> dedup sequence of one rule contribution
+ * (promote.rs:1020-1060, expression.rs:779-834, relational.rs:1558-1677) as one
+ * operator; for output (left column, right non-key column) the join is emitted
+ * in output order and the full sort of the join output is avoided. */
+xlog_hip_status xlog_hip_join_project_dedup(xlog_hip_ctx *ctx, const xlog_hip_rel *left, const xlog_hip_rel *right,
+                                            uint32_t left_key, uint32_t right_key, const uint32_t *out_cols,
+                                            uint32_t n_out, xlog_hip_rel **out);
 /* Column projection, bag semantics (reference: extract_column + combine_columns,
  * relational.rs:6196, provider/arithmetic.rs:1056). */
 xlog_hip_status xlog_hip_project(xlog_hip_ctx *ctx, const xlog_hip_rel *in, const uint32_t *cols, uint32_t n_cols,

@@ -46,6 +46,11 @@ def test_c2_full_join_sort_dedup(provider):
     del j
     assert d.num_rows() == e["unique"]
     assert p.digest(d) == e["digest"]
+    del d
+    _note("c2 full: fused order-preserving join + project + dedup")
+    f = p.join_project_dedup(R, S, 1, 0, [0, 3])
+    assert f.num_rows() == e["unique"]
+    assert p.digest(f) == e["digest"]
 
 
 def test_c3_full_sort_dedup(provider):

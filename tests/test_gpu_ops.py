@@ -192,6 +192,32 @@ def test_join_project_random(provider, nl, nr, keys):
         assert rows == brute
 
 
+@pytest.mark.parametrize("nl,nr,lkeys,avals,seed", [
+    (0, 10, 5, 100, 1), (10, 0, 5, 100, 2), (1, 1, 1, 1, 3), (5000, 3000, 100, 50, 4),
+    (200000, 100000, 5000, 1 << 32, 5), (100000, 20000, 50, 7, 6), (300000, 50000, 3000, 2000, 7)])
+def test_join_project_dedup_ordered(provider, nl, nr, lkeys, avals, seed):
+    """The order-preserving fused join+project+dedup equals dedup(project(join)); small `avals`
+    forces many probe rows to share an output column (interleaved runs, including runs longer
+    than one LDS segment)."""
+    p = provider
+    _note(f"join_project_dedup nl={nl} nr={nr}")
+    rng = _rng(seed)
+    l = pack(rng.integers(0, avals, nl, dtype=np.uint64), rng.integers(0, lkeys, nl))
+    r = pack(rng.integers(0, lkeys, nr), rng.integers(0, 1 << 32, nr, dtype=np.uint64))
+    if nr > 10:
+        r[: nr // 10] = r[nr // 10: 2 * (nr // 10)]  # duplicate build rows
+    L, R = p.create_buffer_from_packed(l), p.create_buffer_from_packed(r)
+    exp = oracle.sort_dedup(oracle.join_project(l, r, 1, 0, 0, 3))
+    got = p.join_project_dedup(L, R, 1, 0, [0, 3])
+    assert got.is_canonical()
+    assert np.array_equal(p.download_packed(got), exp)
+    # the right key column 1 (payload = column 0) and the generic shapes
+    exp2 = oracle.sort_dedup(oracle.join_project(l, r, 1, 1, 0, 2))
+    assert np.array_equal(p.download_packed(p.join_project_dedup(L, R, 1, 1, [0, 2])), exp2)
+    exp3 = oracle.sort_dedup(oracle.join_project(l, r, 1, 0, 3, 0))
+    assert np.array_equal(p.download_packed(p.join_project_dedup(L, R, 1, 0, [3, 0])), exp3)
+
+
 def test_join_skewed_hot_key(provider):
     """One key holds most probe rows and a long build run (cooperative expansion)."""
     p = provider

@@ -529,12 +529,14 @@ struct JoinIndex {
     uint64_t n = 0;
 };
 static void build_join_index(Ctx *ctx, const uint64_t *keys, uint64_t n, uint32_t arity, int col, bool canonical,
-                             JoinIndex &J) {
+                             JoinIndex &J, bool payload_sorted = false) {
     J.n = n;
     uint64_t *sk = nullptr;
     bool own = false;
-    // only the key word needs ordering: runs of equal keys must be contiguous,
-    // the payload order inside a run is irrelevant (digits 4..7 only)
+    // Runs of equal keys must be contiguous; unless payload_sorted is asked
+    // for, the payload order inside a run is irrelevant and only the key word
+    // (digits 4..7) is sorted.
+    const int dlo = payload_sorted ? 0 : 4;
     if (arity == 1) {
         // (c0 << 32) | 0
         sk = static_cast<uint64_t *>(ctx->alloc((n ? n : 1) * sizeof(uint64_t)));
@@ -543,12 +545,12 @@ static void build_join_index(Ctx *ctx, const uint64_t *keys, uint64_t n, uint32_
         sk = sort_keys(ctx, sk, n, true, 4, 8);
     } else if (col == 0) {
         if (canonical) sk = const_cast<uint64_t *>(keys);
-        else { sk = sort_keys(ctx, const_cast<uint64_t *>(keys), n, false, 4, 8); own = true; }
+        else { sk = sort_keys(ctx, const_cast<uint64_t *>(keys), n, false, dlo, 8); own = true; }
     } else {
         sk = static_cast<uint64_t *>(ctx->alloc((n ? n : 1) * sizeof(uint64_t)));
         swap_words(ctx, keys, n, sk);
         own = true;
-        sk = sort_keys(ctx, sk, n, true, 4, 8);
+        sk = sort_keys(ctx, sk, n, true, dlo, 8);
     }
     build_run_index(ctx, sk, n, J.ix);
     J.payload = Buf<uint32_t>(ctx, n ? n : 1);
@@ -663,6 +665,83 @@ static xlog_hip_rel *op_join(Ctx *ctx, const xlog_hip_rel *l, const xlog_hip_rel
     uint64_t n = join_probe_general(ctx, l->w[0], l->rows, pcol, J.ix, J.payload.p, (int)sel.size(), oc, &o0, &o1);
     if (n == 0) return rel_new(ctx, (uint32_t)sel.size(), 0);
     return rel_adopt(ctx, (uint32_t)sel.size(), n, o0, o1, 0);
+}
+
+// Set of the projected join, canonical: dedup_full_row(project(join(l, r))).
+// When the output is (left column, right non-key column) the join is emitted
+// already ordered: the probe side is first sorted by its output column (key
+// word only) and the build runs are kept sorted by their payload, so each probe
+// row's outputs are ascending and rows come in output-column order.  Only
+// groups of probe rows that share the output column interleave; those runs
+// are sorted in place (LDS bitonic sort per run), then one unique pass.  This
+// replaces the radix sort of the whole join output.  Other shapes take the
+// join -> sort -> unique path.
+void left_keys(Ctx *ctx, const uint64_t *l, uint64_t n, int arity, int oc0, int jk, uint64_t *out);
+void group_head_flags(Ctx *ctx, const uint64_t *k, uint64_t n, uint8_t *flags);
+void sort_segments(Ctx *ctx, uint64_t *data, uint64_t n, const uint64_t *heads, uint64_t nh);
+
+static xlog_hip_rel *op_join_project_dedup(Ctx *ctx, const xlog_hip_rel *l, const xlog_hip_rel *r, uint32_t lk,
+                                           uint32_t rk, const std::vector<int> &out_cols) {
+    XH_REQUIRE(l && r, XLOG_HIP_INVALID_ARG, "join input is NULL");
+    XH_REQUIRE(lk < l->arity && rk < r->arity, XLOG_HIP_INVALID_ARG, "join key column out of range");
+    const bool ordered = l->arity <= 2 && r->arity == 2 && out_cols.size() == 2 && out_cols[0] >= 0 &&
+                         out_cols[0] < (int)l->arity && out_cols[1] == (int)l->arity + (1 - (int)rk);
+    if (!ordered) {
+        xlog_hip_rel *j = op_join(ctx, l, r, lk, rk, XLOG_HIP_JOIN_INNER, &out_cols);
+        xlog_hip_rel *d = nullptr;
+        try {
+            d = op_dedup_full(ctx, j);
+        } catch (...) {
+            rel_free(j);
+            throw;
+        }
+        rel_free(j);
+        return d;
+    }
+    const uint64_t n = l->rows;
+    if (n == 0 || r->rows == 0) {
+        xlog_hip_rel *e = rel_new(ctx, 2, 0);
+        e->flags = REL_CANONICAL;
+        return e;
+    }
+    // 1. probe keys (out column << 32 | join key), ordered by the out column
+    uint64_t *lkeys = static_cast<uint64_t *>(ctx->alloc(n * sizeof(uint64_t)));
+    left_keys(ctx, l->w[0], n, (int)l->arity, out_cols[0], (int)lk, lkeys);
+    lkeys = sort_keys(ctx, lkeys, n, true, 4, 8);
+    // 2. build index with payload-ordered runs
+    JoinIndex J;
+    build_join_index(ctx, r->w[0], r->rows, r->arity, (int)rk, (r->flags & REL_CANONICAL) != 0, J, true);
+    // 3. probe: v0 = out column (high word of the probe key), v3 = payload; pcol 1 = join key
+    const int oc[4] = {0, 3, 0, 0};
+    uint64_t *o = nullptr;
+    uint64_t m = 0;
+    try {
+        m = join_probe_general(ctx, lkeys, n, 1, J.ix, J.payload.p, 2, oc, &o, nullptr);
+        // 4. runs whose out column comes from several probe rows are interleaved: sort them
+        if (m) {
+            Buf<uint8_t> flags(ctx, n);
+            group_head_flags(ctx, lkeys, n, flags.p);
+            Buf<uint64_t> heads(ctx, n), cnt(ctx, 1);
+            select_flags(ctx, lkeys, flags.p, n, heads.p, cnt.p);
+            uint64_t nh = read_count(ctx, cnt.p);
+            sort_segments(ctx, o, m, heads.p, nh);
+        }
+    } catch (...) {
+        ctx->free(lkeys);
+        if (o) ctx->free(o);
+        throw;
+    }
+    ctx->free(lkeys);
+    if (!m) {
+        xlog_hip_rel *e = rel_new(ctx, 2, 0);
+        e->flags = REL_CANONICAL;
+        return e;
+    }
+    // 5. one unique pass
+    uint64_t *u;
+    uint64_t un = unique_keys(ctx, o, m, &u);
+    ctx->free(o);
+    return rel_adopt(ctx, 2, un, u, nullptr, REL_CANONICAL);
 }
 
 static xlog_hip_rel *op_project(Ctx *ctx, const xlog_hip_rel *in, const std::vector<int> &cols) {
@@ -1398,6 +1477,17 @@ xlog_hip_status xlog_hip_join_project(xlog_hip_ctx *ctx, const xlog_hip_rel *lef
         XH_REQUIRE(out_cols && n_out >= 1 && n_out <= 4, XLOG_HIP_INVALID_ARG, "out_cols must list 1..4 columns");
         std::vector<int> oc(out_cols, out_cols + n_out);
         *out = op_join(c, left, right, left_key, right_key, XLOG_HIP_JOIN_INNER, &oc);
+    });
+}
+xlog_hip_status xlog_hip_join_project_dedup(xlog_hip_ctx *ctx, const xlog_hip_rel *left, const xlog_hip_rel *right,
+                                            uint32_t left_key, uint32_t right_key, const uint32_t *out_cols,
+                                            uint32_t n_out, xlog_hip_rel **out) {
+    return guarded([&] {
+        Ctx *c = C(ctx);
+        OUT_GUARD;
+        XH_REQUIRE(out_cols && n_out >= 1 && n_out <= 4, XLOG_HIP_INVALID_ARG, "out_cols must list 1..4 columns");
+        std::vector<int> oc(out_cols, out_cols + n_out);
+        *out = op_join_project_dedup(c, left, right, left_key, right_key, oc);
     });
 }
 xlog_hip_status xlog_hip_project(xlog_hip_ctx *ctx, const xlog_hip_rel *in, const uint32_t *cols, uint32_t n_cols,

@@ -367,6 +367,148 @@ void join_match_flags(Ctx *ctx, const uint64_t *probe, uint64_t n, int pcol, con
     XH_CHECK_HIP(hipGetLastError());
 }
 
+// ---------------------------------------------------------------------------
+// Order-preserving join + project: helpers for emitting the projected join
+// already sorted by (left column, right payload).
+// ---------------------------------------------------------------------------
+namespace {
+
+__device__ __forceinline__ uint32_t packed_col(uint64_t row, int arity, int c) {
+    return arity == 1 ? (uint32_t)row : (c == 0 ? (uint32_t)(row >> 32) : (uint32_t)row);
+}
+
+__global__ void k_left_keys(const uint64_t *__restrict__ l, uint64_t n, int arity, int oc0, int jk,
+                            uint64_t *__restrict__ out) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        uint64_t r = l[i];
+        out[i] = ((uint64_t)packed_col(r, arity, oc0) << 32) | packed_col(r, arity, jk);
+    }
+}
+
+// first row of every group of >= 2 consecutive rows with the same high word
+__global__ void k_group_heads(const uint64_t *__restrict__ k, uint64_t n, uint8_t *__restrict__ flags) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        uint32_t h = (uint32_t)(k[i] >> 32);
+        bool next_same = i + 1 < n && (uint32_t)(k[i + 1] >> 32) == h;
+        bool prev_same = i > 0 && (uint32_t)(k[i - 1] >> 32) == h;
+        flags[i] = next_same && !prev_same;
+    }
+}
+
+// [start, end) of the run of high word hw in sorted out[0..n)
+__global__ void k_find_segments(const uint64_t *__restrict__ out, uint64_t n, const uint64_t *__restrict__ heads,
+                                uint64_t nh, uint64_t *__restrict__ seg) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nh; i += stride) {
+        uint32_t hw = (uint32_t)(heads[i] >> 32);
+        uint64_t lo = 0, hi = n;
+        while (lo < hi) {
+            uint64_t m = (lo + hi) >> 1;
+            if ((uint32_t)(out[m] >> 32) < hw) lo = m + 1; else hi = m;
+        }
+        uint64_t s = lo;
+        hi = n;
+        while (lo < hi) {
+            uint64_t m = (lo + hi) >> 1;
+            if ((uint32_t)(out[m] >> 32) <= hw) lo = m + 1; else hi = m;
+        }
+        seg[2 * i] = s;
+        seg[2 * i + 1] = lo - s;
+    }
+}
+
+constexpr int SEG_MAX = 4096;
+
+// One block per listed segment (length <= SEG_MAX): bitonic sort in LDS.
+__global__ __launch_bounds__(256) void k_segsort(uint64_t *__restrict__ data, const uint64_t *__restrict__ seg,
+                                                 const uint32_t *__restrict__ which) {
+    __shared__ uint64_t s[SEG_MAX];
+    const uint32_t q = which[blockIdx.x];
+    const uint64_t start = seg[2 * q], len = seg[2 * q + 1];
+    uint32_t m = 1;
+    while (m < len) m <<= 1;
+    for (uint32_t i = threadIdx.x; i < m; i += blockDim.x) s[i] = i < len ? data[start + i] : ~0ull;
+    __syncthreads();
+    for (uint32_t k = 2; k <= m; k <<= 1) {
+        for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+            for (uint32_t i = threadIdx.x; i < m; i += blockDim.x) {
+                uint32_t p = i ^ j;
+                if (p > i) {
+                    uint64_t a = s[i], b = s[p];
+                    bool up = (i & k) == 0;
+                    if ((a > b) == up) {
+                        s[i] = b;
+                        s[p] = a;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+    for (uint32_t i = threadIdx.x; i < len; i += blockDim.x) data[start + i] = s[i];
+}
+
+}  // namespace
+
+void left_keys(Ctx *ctx, const uint64_t *l, uint64_t n, int arity, int oc0, int jk, uint64_t *out) {
+    if (!n) return;
+    hipLaunchKernelGGL(k_left_keys, dim3(grid_for(n, 256, 16384)), dim3(256), 0, ctx->stream, l, n, arity, oc0, jk,
+                       out);
+    XH_CHECK_HIP(hipGetLastError());
+}
+
+void group_head_flags(Ctx *ctx, const uint64_t *k, uint64_t n, uint8_t *flags) {
+    if (!n) return;
+    hipLaunchKernelGGL(k_group_heads, dim3(grid_for(n, 256, 16384)), dim3(256), 0, ctx->stream, k, n, flags);
+    XH_CHECK_HIP(hipGetLastError());
+}
+
+// Sorts the runs of equal high word named by heads[0..nh) inside sorted-by-
+// high-word data[0..n).  Runs up to SEG_MAX keys are sorted in LDS, longer
+// ones by the radix sort on the slice.
+void sort_segments(Ctx *ctx, uint64_t *data, uint64_t n, const uint64_t *heads, uint64_t nh) {
+    if (!nh || !n) return;
+    Buf<uint64_t> seg(ctx, 2 * nh);
+    hipLaunchKernelGGL(k_find_segments, dim3(grid_for(nh, 256, 16384)), dim3(256), 0, ctx->stream, data, n, heads,
+                       nh, seg.p);
+    XH_CHECK_HIP(hipGetLastError());
+    std::vector<uint64_t> h(2 * nh);
+    XH_CHECK_HIP(hipMemcpyAsync(h.data(), seg.p, 2 * nh * sizeof(uint64_t), hipMemcpyDeviceToHost, ctx->stream));
+    ctx->sync();
+    std::vector<uint32_t> small;
+    std::vector<uint64_t> large;
+    small.reserve(nh);
+    for (uint64_t i = 0; i < nh; ++i) {
+        uint64_t len = h[2 * i + 1];
+        if (len < 2) continue;
+        if (len <= (uint64_t)SEG_MAX) small.push_back((uint32_t)i);
+        else large.push_back(i);
+    }
+    if (!small.empty()) {
+        Buf<uint32_t> which(ctx, small.size());
+        XH_CHECK_HIP(hipMemcpyAsync(which.p, small.data(), small.size() * sizeof(uint32_t), hipMemcpyHostToDevice,
+                                    ctx->stream));
+        for (size_t off = 0; off < small.size(); off += (1u << 30)) {
+            size_t cnt = std::min<size_t>(small.size() - off, 1u << 30);
+            hipLaunchKernelGGL(k_segsort, dim3((unsigned)cnt), dim3(256), 0, ctx->stream, data, seg.p, which.p + off);
+            XH_CHECK_HIP(hipGetLastError());
+        }
+        ctx->sync();  // `which` is a pageable-host-sourced buffer: keep it alive until the copy and launch finish
+    }
+    for (uint64_t i : large) {
+        uint64_t s = h[2 * i], len = h[2 * i + 1];
+        uint64_t *a = data + s;
+        uint64_t *b = static_cast<uint64_t *>(ctx->alloc(len * sizeof(uint64_t)));
+        uint64_t *k0 = a, *k1 = b;
+        uint32_t *v0 = nullptr, *v1 = nullptr;
+        radix_sort_u64(ctx, &k0, &k1, &v0, &v1, len, 0, 4);  // high words are equal inside the run
+        if (k0 != a) XH_CHECK_HIP(hipMemcpyAsync(a, k0, len * 8, hipMemcpyDeviceToDevice, ctx->stream));
+        ctx->free(b);
+    }
+}
+
 }  // namespace xh
 
 namespace xh {

@@ -93,6 +93,7 @@ def _load() -> C.CDLL:
         "xlog_hip_hash_join": (I32, [P, P, P, U32, U32, I32, PP]),
         "xlog_hip_sort_merge_join": (I32, [P, P, P, U32, U32, PP]),
         "xlog_hip_join_project": (I32, [P, P, P, U32, U32, P, U32, PP]),
+        "xlog_hip_join_project_dedup": (I32, [P, P, P, U32, U32, P, U32, PP]),
         "xlog_hip_project": (I32, [P, P, P, U32, PP]),
         "xlog_hip_is_sorted": (I32, [P, P, U32, C.POINTER(I32)]),
         "xlog_hip_exclusive_scan_u32": (I32, [P, P, U64, C.POINTER(U64)]),
@@ -122,7 +123,8 @@ ABI_SYMBOLS = (
     "xlog_hip_rel_num_rows", "xlog_hip_rel_arity", "xlog_hip_rel_is_canonical", "xlog_hip_rel_device_words",
     "xlog_hip_rel_clone", "xlog_hip_rel_free", "xlog_hip_sort", "xlog_hip_dedup", "xlog_hip_dedup_full_row",
     "xlog_hip_union", "xlog_hip_union_many", "xlog_hip_diff", "xlog_hip_hash_join",
-    "xlog_hip_sort_merge_join", "xlog_hip_join_project", "xlog_hip_project", "xlog_hip_is_sorted",
+    "xlog_hip_sort_merge_join", "xlog_hip_join_project", "xlog_hip_join_project_dedup", "xlog_hip_project",
+    "xlog_hip_is_sorted",
     "xlog_hip_exclusive_scan_u32", "xlog_hip_compact", "xlog_hip_fixpoint", "xlog_hip_fixpoint_tc",
     "xlog_hip_rel_digest", "xlog_hip_profile_enable", "xlog_hip_profile_reset", "xlog_hip_profile_read",
 )
@@ -396,6 +398,15 @@ class HipKernelProvider:
         h = C.c_void_p()
         _check(_lib.xlog_hip_join_project(self.ctx, left.handle, right.handle, left_key, right_key, arr, n,
                                           C.byref(h)))
+        return self._rel(h)
+
+    def join_project_dedup(self, left: Relation, right: Relation, left_key: int, right_key: int,
+                           out_cols: Sequence[int]) -> Relation:
+        """Canonical set of the projected join (one rule contribution, join -> project -> dedup)."""
+        arr, n = _u32_array(out_cols)
+        h = C.c_void_p()
+        _check(_lib.xlog_hip_join_project_dedup(self.ctx, left.handle, right.handle, left_key, right_key, arr, n,
+                                                C.byref(h)))
         return self._rel(h)
 
     def project(self, rel: Relation, cols: Sequence[int]) -> Relation:
