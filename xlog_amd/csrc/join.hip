@@ -90,19 +90,62 @@ __device__ __forceinline__ uint64_t probe_count(const ProbeArgs &a, uint64_t row
     return a.run_start[run + 1] - s;
 }
 
+// Lookups of N probe rows with their memory latencies overlapped: all first
+// slots are loaded together, the rare collision chains are walked after, then
+// all run bounds are loaded together.  cnt[i] = 0 for rows with idx >= n.
+template <int N>
+__device__ __forceinline__ void lookup_batch(const ProbeArgs &a, const uint64_t *rows, uint64_t wbase, int lane,
+                                             uint64_t *start, uint32_t *cnt) {
+    unsigned long long slot[N];
+    uint64_t h[N];
+    uint32_t key[N];
+#pragma unroll
+    for (int r = 0; r < N; ++r) {
+        key[r] = a.pcol ? (uint32_t)rows[r] : (uint32_t)(rows[r] >> 32);
+        h[r] = hash_slot(key[r], a.bits);
+        bool valid = wbase + (uint64_t)r * WAVE + lane < a.n;
+        slot[r] = valid ? a.table[h[r]] : 0ull;
+    }
+    uint32_t run[N];
+#pragma unroll
+    for (int r = 0; r < N; ++r) {
+        unsigned long long s = slot[r];
+        uint64_t hh = h[r];
+        while (s != 0ull && (uint32_t)(s >> 32) != key[r]) {
+            hh = (hh + 1) & a.mask;
+            s = a.table[hh];
+        }
+        run[r] = s ? (uint32_t)s - 1u : 0xFFFFFFFFu;
+    }
+    uint64_t b[N], e[N];
+#pragma unroll
+    for (int r = 0; r < N; ++r) {
+        b[r] = run[r] != 0xFFFFFFFFu ? a.run_start[run[r]] : 0ull;
+        e[r] = run[r] != 0xFFFFFFFFu ? a.run_start[run[r] + 1] : 0ull;
+    }
+#pragma unroll
+    for (int r = 0; r < N; ++r) {
+        start[r] = b[r];
+        cnt[r] = (uint32_t)(e[r] - b[r]);
+    }
+}
+
 __global__ __launch_bounds__(JB) void k_probe_count(ProbeArgs a, uint64_t *__restrict__ tile_cnt) {
     __shared__ uint64_t s_part[JWAVES];
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
     const uint64_t wbase = (uint64_t)blockIdx.x * JTILE + (uint64_t)wave * (JITEMS * WAVE);
-    uint64_t acc = 0;
-#pragma unroll 4
+    uint64_t rows[JITEMS];
+#pragma unroll
     for (int r = 0; r < JITEMS; ++r) {
         uint64_t idx = wbase + (uint64_t)r * WAVE + lane;
-        if (idx < a.n) {
-            uint64_t st;
-            acc += probe_count(a, a.probe[idx], &st);
-        }
+        rows[r] = idx < a.n ? a.probe[idx] : 0ull;
     }
+    uint64_t starts[JITEMS];
+    uint32_t cnts[JITEMS];
+    lookup_batch<JITEMS>(a, rows, wbase, lane, starts, cnts);
+    uint64_t acc = 0;
+#pragma unroll
+    for (int r = 0; r < JITEMS; ++r) acc += cnts[r];
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, WAVE);
     if (lane == 0) s_part[wave] = acc;
@@ -177,16 +220,19 @@ __global__ __launch_bounds__(JB) void k_probe_emit(ProbeArgs a, const uint64_t *
     const uint64_t tile = t0 + blockIdx.x;
     const uint64_t wbase = tile * JTILE + (uint64_t)wave * (JITEMS * WAVE);
 
-    // pass 1 over this wave's rows: total outputs of the wave
-    uint64_t acc = 0;
-#pragma unroll 4
+    // pass 1 over this wave's rows: all JITEMS lookups issued together (their
+    // latencies overlap) and kept in registers for the expansion
+    uint64_t rows[JITEMS], starts[JITEMS];
+    uint32_t cnts[JITEMS];
+#pragma unroll
     for (int r = 0; r < JITEMS; ++r) {
         uint64_t idx = wbase + (uint64_t)r * WAVE + lane;
-        if (idx < a.n) {
-            uint64_t st;
-            acc += probe_count(a, a.probe[idx], &st);
-        }
+        rows[r] = idx < a.n ? a.probe[idx] : 0ull;
     }
+    lookup_batch<JITEMS>(a, rows, wbase, lane, starts, cnts);
+    uint64_t acc = 0;
+#pragma unroll
+    for (int r = 0; r < JITEMS; ++r) acc += cnts[r];
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, WAVE);
     if (lane == 0) s_wtot[wave] = acc;
@@ -195,13 +241,9 @@ __global__ __launch_bounds__(JB) void k_probe_emit(ProbeArgs a, const uint64_t *
     for (int w = 0; w < wave; ++w) base += s_wtot[w];
 
     // pass 2: expand round by round
+#pragma unroll
     for (int r = 0; r < JITEMS; ++r) {
-        uint64_t idx = wbase + (uint64_t)r * WAVE + lane;
-        uint64_t row = 0, st = 0, c = 0;
-        if (idx < a.n) {
-            row = a.probe[idx];
-            c = probe_count(a, row, &st);
-        }
+        const uint64_t row = rows[r], st = starts[r], c = cnts[r];
         uint64_t x = c;
 #pragma unroll
         for (int o = 1; o < WAVE; o <<= 1) {
