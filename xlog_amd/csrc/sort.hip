@@ -41,6 +41,10 @@ namespace {
 #ifndef XH_SORT_DIRECT
 #define XH_SORT_DIRECT 0
 #endif
+#ifndef XH_SORT_LOOKBACK
+#define XH_SORT_LOOKBACK 4
+#endif
+constexpr int SORT_LOOKBACK = XH_SORT_LOOKBACK;
 constexpr int SORT_BLOCK_K = XH_SORT_BLOCK_K, SORT_ITEMS_K = XH_SORT_ITEMS_K;
 constexpr int SORT_BLOCK_V = XH_SORT_BLOCK_V, SORT_ITEMS_V = XH_SORT_ITEMS_V;
 static_assert(SORT_BLOCK_K >= 256 && SORT_BLOCK_K % 256 == 0 && SORT_BLOCK_V >= 256 && SORT_BLOCK_V % 256 == 0,
@@ -178,41 +182,71 @@ __global__ __launch_bounds__(BLOCK) void k_onesweep(
     if (tid == 0) s_tile = (uint32_t)(atomicAdd(ticket, 1ull) - ticket_base);
     for (int i = tid; i < (BLOCK / WAVE) * 256; i += BLOCK) (&s_wcnt[0][0])[i] = 0;
     __syncthreads();
-    const uint32_t tile = s_tile;
-    const uint64_t wbase = (uint64_t)tile * (BLOCK * ITEMS) + (uint64_t)wave * (ITEMS * WAVE);
-    const uint64_t lt_mask = (1ull << lane) - 1ull;
+    // the tile index is block-uniform: keep it (and every per-round bound
+    // derived from it) in scalar registers
+    const uint32_t tile = __builtin_amdgcn_readfirstlane(s_tile);
+    const uint64_t wbase = (uint64_t)tile * (BLOCK * ITEMS) + (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane(wave) * (ITEMS * WAVE);
+    // valid keys of this wave (0..ITEMS*WAVE) and of its round r (0..64)
+    const int32_t wleft = wbase >= n ? 0 : ((n - wbase) >= (uint64_t)(ITEMS * WAVE) ? ITEMS * WAVE : (int32_t)(n - wbase));
+    auto round_valid = [&](int r) -> uint32_t {
+        const int32_t rem = wleft - r * WAVE;
+        return rem <= 0 ? 0u : (rem >= WAVE ? (uint32_t)WAVE : (uint32_t)rem);
+    };
 
     uint64_t k[ITEMS];
     uint32_t v[ITEMS];
     uint32_t rank[ITEMS];
 #pragma unroll
     for (int r = 0; r < ITEMS; ++r) {
-        uint64_t idx = wbase + (uint64_t)r * WAVE + lane;
-        bool valid = idx < n;
+        const uint64_t idx = wbase + (uint64_t)r * WAVE + lane;
+        const bool valid = (uint32_t)lane < round_valid(r);
         k[r] = valid ? kin[idx] : 0ull;
         if (HAS_VAL) v[r] = valid ? vin[idx] : 0u;
     }
+    // Stable rank of each key among the wave's keys of equal digit, two rounds
+    // at a time so that the two ballot chains interleave.  A lane's peers are
+    // the lanes whose 8 digit bits all agree with its own; the lanes that
+    // disagree on bit b are ballot(bit b) ^ splat(own bit b), accumulated
+    // over the 8 bits as a mismatch mask (invalid lanes start mismatched).
+    static_assert(ITEMS % 2 == 0, "rounds are ranked in pairs");
+    const uint32_t lane_u = (uint32_t)lane;
 #pragma unroll
-    for (int r = 0; r < ITEMS; ++r) {
-        uint64_t idx = wbase + (uint64_t)r * WAVE + lane;
-        bool valid = idx < n;
-        uint32_t d = (uint32_t)(k[r] >> shift) & 255u;
-        uint64_t peers = __ballot(valid);
+    for (int r = 0; r < ITEMS; r += 2) {
+        uint32_t dg[2], mlo[2], mhi[2], nv[2];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            dg[q] = (uint32_t)(k[r + q] >> shift) & 255u;
+            nv[q] = round_valid(r + q);
+            const uint64_t vm = nv[q] >= (uint32_t)WAVE ? ~0ull : ((1ull << nv[q]) - 1ull);
+            mlo[q] = ~(uint32_t)vm;
+            mhi[q] = ~(uint32_t)(vm >> 32);
+        }
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
-            bool bit = (d >> b) & 1u;
-            uint64_t m = __ballot(bit);
-            peers &= bit ? m : ~m;
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                // s = 0 or ~0: bit b of the digit, sign-extended.  The empty
+                // asm keeps the ballot's compare on s itself (v_bfe + v_cmp)
+                // instead of a recomputed shift of the digit.
+                uint32_t s = (uint32_t)__builtin_amdgcn_sbfe((int32_t)dg[q], b, 1);
+                asm("" : "+v"(s));
+                const uint64_t m = __ballot(s != 0u);
+                mlo[q] |= (uint32_t)m ^ s;
+                mhi[q] |= (uint32_t)(m >> 32) ^ s;
+            }
         }
-        uint32_t below = (uint32_t)__popcll(peers & lt_mask);
-        int leader = valid ? (int)__builtin_ctzll(peers) : lane;
-        uint32_t old = 0;
-        if (valid && below == 0) {
-            old = s_wcnt[wave][d];
-            s_wcnt[wave][d] = old + (uint32_t)__popcll(peers);
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            // peers below = lanes below - mismatched lanes below
+            const uint32_t below =
+                lane_u - __builtin_amdgcn_mbcnt_hi(mhi[q], __builtin_amdgcn_mbcnt_lo(mlo[q], 0u));
+            // every peer reads the running count before the group's first lane
+            // bumps it: LDS operations of one wave complete in program order
+            const uint32_t old = s_wcnt[wave][dg[q]];
+            if (below == 0 && lane_u < nv[q])
+                s_wcnt[wave][dg[q]] = old + (uint32_t)WAVE - (uint32_t)(__popc(mlo[q]) + __popc(mhi[q]));
+            rank[r + q] = old + below;
         }
-        old = (uint32_t)__shfl((int)old, leader, WAVE);
-        rank[r] = old + below;
     }
     __syncthreads();
 
@@ -244,16 +278,32 @@ __global__ __launch_bounds__(BLOCK) void k_onesweep(
         s_tstart[d] = tstart;
 
         // decoupled look-back over earlier tiles for this digit
+        // (LOOKBACK predecessors are loaded at once; the walk consumes them in
+        // order and resumes at the first one not yet published)
         uint32_t prefix = 0;
         if (tile > 0) {
             int64_t j = (int64_t)tile - 1;
-            for (;;) {
-                uint32_t s = ld_status(status + (uint64_t)j * 256 + d);
-                uint32_t flag = s & ~ST_VAL;
-                if (flag == 0) continue;  // predecessor not published yet
-                prefix += s & ST_VAL;
-                if (flag == ST_INC) break;
-                --j;
+            bool done = false;
+            while (!done) {
+                uint32_t st[SORT_LOOKBACK];
+#pragma unroll
+                for (int q = 0; q < SORT_LOOKBACK; ++q)
+                    // tile 0 is inclusive, so the walk never passes it; the
+                    // guard only keeps the batch's loads in bounds
+                    st[q] = j - q >= 0 ? ld_status(status + (uint64_t)(j - q) * 256 + d) : ST_INC;
+                int used = 0;
+#pragma unroll
+                for (int q = 0; q < SORT_LOOKBACK; ++q) {
+                    const uint32_t flag = st[q] & ~ST_VAL;
+                    if (flag == 0) break;  // not published yet: reload from here
+                    prefix += st[q] & ST_VAL;
+                    used = q + 1;
+                    if (flag == ST_INC) {
+                        done = true;
+                        break;
+                    }
+                }
+                j -= used;
             }
             st_status(my, ST_INC | (prefix + cnt));
         }
