@@ -47,6 +47,8 @@ typedef enum {
 
 typedef struct xlog_hip_ctx xlog_hip_ctx;
 typedef struct xlog_hip_rel xlog_hip_rel;
+/* reusable join index over one key column of a relation (reference JoinIndexV2) */
+typedef struct xlog_hip_join_index xlog_hip_join_index;
 
 /* join kinds (reference JoinType, relational.rs:2926); only INNER is on the path */
 #define XLOG_HIP_JOIN_INNER 0
@@ -114,6 +116,11 @@ xlog_hip_status xlog_hip_sort(xlog_hip_ctx *ctx, const xlog_hip_rel *in, const u
  * by key_cols (reference: dedup, relational.rs:238-275). */
 xlog_hip_status xlog_hip_dedup(xlog_hip_ctx *ctx, const xlog_hip_rel *in, const uint32_t *key_cols,
                                uint32_t n_keys, xlog_hip_rel **out);
+/* Dedup of input already ordered on key_cols: the first row of every run of
+ * adjacent rows equal on key_cols, input order, no sort; a full-row key list
+ * on arity > 1 is the full-row dedup (reference: dedup_sorted, relational.rs:288-420). */
+xlog_hip_status xlog_hip_dedup_sorted(xlog_hip_ctx *ctx, const xlog_hip_rel *in, const uint32_t *key_cols,
+                                      uint32_t n_keys, xlog_hip_rel **out);
 /* Full-row set: sort by every column, drop duplicate rows
  * (reference: dedup_full_row / dedup_full_row_deterministic, relational.rs:1458,1558-1677). */
 xlog_hip_status xlog_hip_dedup_full_row(xlog_hip_ctx *ctx, const xlog_hip_rel *in, xlog_hip_rel **out);
@@ -133,6 +140,28 @@ xlog_hip_status xlog_hip_diff(xlog_hip_ctx *ctx, const xlog_hip_rel *a, const xl
  * SEMI / ANTI output the left rows with / without a match. */
 xlog_hip_status xlog_hip_hash_join(xlog_hip_ctx *ctx, const xlog_hip_rel *left, const xlog_hip_rel *right,
                                    uint32_t left_key, uint32_t right_key, int join_type, xlog_hip_rel **out);
+/* Join index over column right_key of `right`, reused across probes; fails
+ * on an empty relation like the reference (build_join_index_v2,
+ * relational.rs:3728-3880).  Free it with xlog_hip_join_index_free before its
+ * context is destroyed. */
+xlog_hip_status xlog_hip_join_index_build(xlog_hip_ctx *ctx, const xlog_hip_rel *right, uint32_t right_key,
+                                          xlog_hip_join_index **out);
+/* xlog_hip_hash_join against a prebuilt index of (right, right_key); the
+ * output is that of xlog_hip_hash_join.  max_output > 0 keeps at most that
+ * many INNER rows (reference: hash_join_v2_with_index, relational.rs:3882-4000;
+ * the reference keeps an unspecified subset, this keeps the first rows in
+ * probe-row order). */
+xlog_hip_status xlog_hip_hash_join_with_index(xlog_hip_ctx *ctx, const xlog_hip_rel *left, const xlog_hip_rel *right,
+                                              uint32_t left_key, uint32_t right_key, int join_type,
+                                              const xlog_hip_join_index *index, uint64_t max_output,
+                                              xlog_hip_rel **out);
+void xlog_hip_join_index_free(xlog_hip_join_index *index);
+/* Nested-loop inner join on one key column, left ++ right columns, rows in
+ * left-row-major then right-row order; CAPACITY_OVERFLOW when rows_l * rows_r
+ * > 4,000,000 (reference: nested_loop_join_v2_inner_u32_1key,
+ * relational.rs:3041-3255; NESTED_LOOP_TOTAL_THRESHOLD, provider/mod.rs:1030). */
+xlog_hip_status xlog_hip_nested_loop_join(xlog_hip_ctx *ctx, const xlog_hip_rel *left, const xlog_hip_rel *right,
+                                          uint32_t left_key, uint32_t right_key, xlog_hip_rel **out);
 /* Inner join on one u32 key column, left ++ right columns, for inputs sorted
  * on their key (reference: sort_merge_join_v2_inner_u32_1key, relational.rs:3401-3728). */
 xlog_hip_status xlog_hip_sort_merge_join(xlog_hip_ctx *ctx, const xlog_hip_rel *left, const xlog_hip_rel *right,
@@ -160,6 +189,23 @@ xlog_hip_status xlog_hip_is_sorted(xlog_hip_ctx *ctx, const xlog_hip_rel *rel, u
 /* In-place exclusive scan of a device u32 array; *total receives the sum
  * (reference: exclusive_scan_u32_inplace, provider/mod.rs:2177). */
 xlog_hip_status xlog_hip_exclusive_scan_u32(xlog_hip_ctx *ctx, uint32_t *dev, uint64_t n, uint64_t *total);
+/* Column roles of one factorized delta step (reference FjDeltaCols,
+ * provider/fj_delta.rs:50-84); each pair is {0, 1} in some order. */
+typedef struct {
+    uint32_t delta_carry; /* delta column carried into the head */
+    uint32_t delta_key;   /* delta column joined with edge column 0 */
+    uint32_t r_carry;     /* head / full column holding the carry */
+    uint32_t r_value;     /* head / full column holding edge column 1 */
+} xlog_hip_fj_delta_cols;
+/* One factorized semi-naive delta step over a dense domain:
+ *   { head(carry, value) : delta(carry, key), edge(key, value), head not in full }
+ * as a canonical (sorted, unique) arity-2 relation in full's column order.
+ * Every id must be < domain and 0 < domain <= 2^16, else INVALID_ARG
+ * (reference: fj_delta_novel_u32_recorded, provider/fj_delta.rs:117-490; the
+ * reference's launch stream is the context's stream here). */
+xlog_hip_status xlog_hip_fj_delta_novel(xlog_hip_ctx *ctx, const xlog_hip_rel *delta, const xlog_hip_rel *edge,
+                                        const xlog_hip_rel *full, const xlog_hip_fj_delta_cols *cols,
+                                        uint32_t domain, xlog_hip_rel **out);
 /* Keep rows whose device u8 mask is non-zero, input order
  * (reference: compact_buffer_by_device_mask_device_count, provider/filter.rs:1820-1935). */
 xlog_hip_status xlog_hip_compact(xlog_hip_ctx *ctx, const xlog_hip_rel *in, const uint8_t *dev_mask,

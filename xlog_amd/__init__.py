@@ -6,6 +6,9 @@ The product is libxlog_hip.so (HIP kernels + C ABI, include/xlog_hip.h);
 from .provider import (  # noqa: F401
     HipKernelProvider,
     Relation,
+    JoinIndex,
+    FjDeltaCols,
+    FJ_DELTA_CANONICAL,
     XlogError,
     JOIN_INNER,
     JOIN_SEMI,

@@ -268,7 +268,8 @@ static uint64_t read_count(Ctx *ctx, const uint64_t *d) {
 // ---------------------------------------------------------------------------
 
 // Sort a u64 key array of any length; the result is returned in a buffer
-// owned by the caller (either `keys` itself or a new one).
+// owned by the caller (either `keys` itself or a new one).  With keys_owned
+// the call consumes `keys`: it is either returned or freed.
 // digit_lo / digit_hi restrict the sort to 8-bit digits [lo, hi) (4..8 = by
 // the high word only, stable otherwise).
 static uint64_t *sort_keys(Ctx *ctx, uint64_t *keys, uint64_t n, bool keys_owned, int digit_lo = 0,
@@ -528,6 +529,15 @@ struct JoinIndex {
     Buf<uint32_t> payload;
     uint64_t n = 0;
 };
+}  // namespace xh
+// Reusable join index handle of the C ABI (one build, many probes).
+struct xlog_hip_join_index {
+    xh::Ctx *ctx = nullptr;
+    xh::JoinIndex J;
+    uint32_t arity = 0, key = 0;
+    uint64_t rows = 0;
+};
+namespace xh {
 static void build_join_index(Ctx *ctx, const uint64_t *keys, uint64_t n, uint32_t arity, int col, bool canonical,
                              JoinIndex &J, bool payload_sorted = false) {
     J.n = n;
@@ -601,8 +611,7 @@ static uint64_t join_step(Ctx *ctx, const uint64_t *probe, uint64_t n, int pcol,
         if (m) {
             uint64_t *b = static_cast<uint64_t *>(ctx->alloc(m * sizeof(uint64_t)));
             probe_emit_range(ctx, job, t0, t1, m, 2, oc, b, nullptr);
-            uint64_t *s = sort_keys(ctx, b, m, true);
-            if (s != b) ctx->free(b);
+            uint64_t *s = sort_keys(ctx, b, m, true);  // consumes b
             uint64_t *u;
             uint64_t un = unique_keys(ctx, s, m, &u);
             ctx->free(s);
@@ -631,13 +640,14 @@ static uint64_t join_step(Ctx *ctx, const uint64_t *probe, uint64_t n, int pcol,
 // the low word (v1), arity 2 stores c0 high (v0) and c1 low (v1)
 static int probe_vidx(uint32_t arity, uint32_t c) { return arity == 1 ? 1 : (int)c; }
 
-static xlog_hip_rel *op_join(Ctx *ctx, const xlog_hip_rel *l, const xlog_hip_rel *r, uint32_t lk, uint32_t rk,
-                             int type, const std::vector<int> *out_cols) {
-    XH_REQUIRE(l && r, XLOG_HIP_INVALID_ARG, "join input is NULL");
-    XH_REQUIRE(lk < l->arity && rk < r->arity, XLOG_HIP_INVALID_ARG, "join key column out of range");
-    XH_REQUIRE(l->arity <= 2 && r->arity <= 2, XLOG_HIP_UNSUPPORTED, "join: input arity above 2 is not supported");
-    JoinIndex J;
-    build_join_index(ctx, r->w[0], r->rows, r->arity, (int)rk, (r->flags & REL_CANONICAL) != 0, J);
+// Join of `l` against an index built over column rk of a relation of arity
+// r_arity.  max_output > 0 keeps the first max_output rows of the output
+// (row order: probe-row major).
+static xlog_hip_rel *op_join_indexed(Ctx *ctx, const xlog_hip_rel *l, uint32_t lk, const JoinIndex &J, uint32_t r_arity,
+                                     uint32_t rk, int type, const std::vector<int> *out_cols, uint64_t max_output = 0) {
+    XH_REQUIRE(lk < l->arity, XLOG_HIP_INVALID_ARG, "join key column out of range");
+    XH_REQUIRE(l->arity <= 2, XLOG_HIP_UNSUPPORTED, "join: input arity above 2 is not supported");
+    const uint32_t r_arity_ = r_arity;
     const int pcol = probe_vidx(l->arity, lk);
     if (type == XLOG_HIP_JOIN_SEMI || type == XLOG_HIP_JOIN_ANTI) {
         Buf<uint8_t> flags(ctx, l->rows ? l->rows : 1);
@@ -648,7 +658,7 @@ static xlog_hip_rel *op_join(Ctx *ctx, const xlog_hip_rel *l, const xlog_hip_rel
     // value index of every column of (left ++ right)
     std::vector<int> vmap;
     for (uint32_t c = 0; c < l->arity; ++c) vmap.push_back(probe_vidx(l->arity, c));
-    for (uint32_t c = 0; c < r->arity; ++c) vmap.push_back(c == rk ? 2 : 3);
+    for (uint32_t c = 0; c < r_arity_; ++c) vmap.push_back(c == rk ? 2 : 3);
     std::vector<int> sel;
     if (out_cols) {
         for (int c : *out_cols) {
@@ -664,7 +674,108 @@ static xlog_hip_rel *op_join(Ctx *ctx, const xlog_hip_rel *l, const xlog_hip_rel
     uint64_t *o0 = nullptr, *o1 = nullptr;
     uint64_t n = join_probe_general(ctx, l->w[0], l->rows, pcol, J.ix, J.payload.p, (int)sel.size(), oc, &o0, &o1);
     if (n == 0) return rel_new(ctx, (uint32_t)sel.size(), 0);
+    if (max_output && n > max_output) n = max_output;
     return rel_adopt(ctx, (uint32_t)sel.size(), n, o0, o1, 0);
+}
+
+static xlog_hip_rel *op_join(Ctx *ctx, const xlog_hip_rel *l, const xlog_hip_rel *r, uint32_t lk, uint32_t rk,
+                             int type, const std::vector<int> *out_cols) {
+    XH_REQUIRE(l && r, XLOG_HIP_INVALID_ARG, "join input is NULL");
+    XH_REQUIRE(lk < l->arity && rk < r->arity, XLOG_HIP_INVALID_ARG, "join key column out of range");
+    XH_REQUIRE(l->arity <= 2 && r->arity <= 2, XLOG_HIP_UNSUPPORTED, "join: input arity above 2 is not supported");
+    JoinIndex J;
+    build_join_index(ctx, r->w[0], r->rows, r->arity, (int)rk, (r->flags & REL_CANONICAL) != 0, J);
+    return op_join_indexed(ctx, l, lk, J, r->arity, rk, type, out_cols);
+}
+
+// Nested-loop inner join (reference nested_loop_join_v2_inner_u32_1key,
+// relational.rs:3041-3255): same output columns as the inner hash join, rows
+// in left-row-major, right-row order; refused above rows_l * rows_r =
+// 4,000,000 like the reference (NESTED_LOOP_TOTAL_THRESHOLD, provider/mod.rs:1030).
+static xlog_hip_rel *op_nested_loop_join(Ctx *ctx, const xlog_hip_rel *l, const xlog_hip_rel *r, uint32_t lk,
+                                         uint32_t rk) {
+    XH_REQUIRE(l && r, XLOG_HIP_INVALID_ARG, "join input is NULL");
+    XH_REQUIRE(lk < l->arity && rk < r->arity, XLOG_HIP_INVALID_ARG, "join key column out of range");
+    XH_REQUIRE(l->arity <= 2 && r->arity <= 2, XLOG_HIP_UNSUPPORTED, "join: input arity above 2 is not supported");
+    const uint32_t arity = l->arity + r->arity;
+    if (l->rows == 0 || r->rows == 0) return rel_new(ctx, arity, 0);
+    XH_REQUIRE(l->rows <= 4000000ull / r->rows, XLOG_HIP_CAPACITY_OVERFLOW,
+               "nested loop join: rows_l * rows_r exceeds 4000000");
+    uint64_t *o0, *o1;
+    const uint64_t n = nested_loop_join(ctx, l->w[0], l->rows, (int)l->arity, (int)lk, r->w[0], r->rows,
+                                        (int)r->arity, (int)rk, &o0, &o1);
+    if (n == 0) return rel_new(ctx, arity, 0);
+    return rel_adopt(ctx, arity, n, o0, o1, 0);
+}
+
+// Dedup of input ordered on the key columns (reference dedup_sorted,
+// relational.rs:288-420): full-row keys of arity > 1 take the full-row dedup;
+// otherwise the first row of every run of adjacent rows equal on the key
+// columns is kept, in input order, without sorting.
+static xlog_hip_rel *op_dedup_sorted(Ctx *ctx, const xlog_hip_rel *in, const std::vector<int> &cols) {
+    XH_REQUIRE(!cols.empty(), XLOG_HIP_INVALID_ARG, "dedup needs at least one key column");
+    if (in->arity > 1 && is_full_key(in, cols)) return op_dedup_full(ctx, in);
+    if (in->rows <= 1) return rel_clone(ctx, in);
+    std::vector<int> keys;  // distinct key columns (at most the arity, <= 4)
+    for (int c : cols)
+        if (std::find(keys.begin(), keys.end(), c) == keys.end()) keys.push_back(c);
+    Buf<uint8_t> flags(ctx, in->rows);
+    ProjSpec ks{(int)in->arity, (int)keys.size(), {0, 0, 0, 0}};
+    for (int j = 0; j < ks.out_arity; ++j) ks.cols[j] = keys[j];
+    LAUNCH_1D(k_group_flags, in->rows, in->w[0], in->w[1], (int)in->arity, ks, in->rows, flags.p);
+    xlog_hip_rel *r = compact_rel(ctx, in, flags.p);
+    if (in->flags & REL_CANONICAL) r->flags = REL_CANONICAL;  // a subset of a sorted set is one
+    return r;
+}
+
+// One factorized TC delta step (reference fj_delta_novel_u32_recorded,
+// crates/xlog-cuda/src/provider/fj_delta.rs:117-490): the set
+//   { head(carry, value) : delta(carry, key), edge(key, value), head not in full }
+// with the column roles of `cols`, output in full's column order (r_carry,
+// r_value), canonical.  Every id must be below `domain` <= 2^16.
+static xlog_hip_rel *op_fj_delta(Ctx *ctx, const xlog_hip_rel *delta, const xlog_hip_rel *edge,
+                                 const xlog_hip_rel *full, const xlog_hip_fj_delta_cols &c, uint32_t domain) {
+    XH_REQUIRE(delta && edge && full, XLOG_HIP_INVALID_ARG, "fj delta: input is NULL");
+    XH_REQUIRE(delta->arity == 2 && edge->arity == 2 && full->arity == 2, XLOG_HIP_INVALID_ARG,
+               "fj delta: delta, edge and full must be arity-2");
+    auto roles_ok = [](uint32_t a, uint32_t b) { return a < 2 && b < 2 && a != b; };
+    XH_REQUIRE(roles_ok(c.delta_carry, c.delta_key) && roles_ok(c.r_carry, c.r_value), XLOG_HIP_INVALID_ARG,
+               "fj delta: invalid column roles (arity-2 indices, pairwise distinct)");
+    XH_REQUIRE(domain > 0 && domain <= (1u << 16), XLOG_HIP_INVALID_ARG, "fj delta: domain outside (0, 2^16]");
+    if (delta->rows == 0 || edge->rows == 0) {
+        xlog_hip_rel *e = rel_new(ctx, 2, 0);
+        e->flags = REL_CANONICAL;
+        return e;
+    }
+    {  // every id below the domain (checked before any bitmap is touched)
+        Buf<unsigned int> mx(ctx, 1);
+        fill_u32(ctx, mx.p, 0u, 1);
+        const xlog_hip_rel *rs[3] = {delta, edge, full};
+        for (const xlog_hip_rel *r : rs)
+            if (r->rows) LAUNCH_1D(k_max_u32_of_packed, r->rows, r->w[0], r->rows, mx.p);
+        uint32_t h = 0;
+        XH_CHECK_HIP(hipMemcpyAsync(&h, mx.p, 4, hipMemcpyDeviceToHost, ctx->stream));
+        ctx->sync();
+        XH_REQUIRE(h < domain, XLOG_HIP_INVALID_ARG,
+                   "fj delta: id " + std::to_string(h) + " outside the domain " + std::to_string(domain));
+    }
+    Canon ce;  // edge as sorted unique (key << 32) | value
+    canonical_keys(ctx, edge, ce);
+    uint64_t *o = nullptr;
+    const uint64_t n = fj_delta_step(ctx, delta->w[0], delta->rows, c.delta_carry == 0 ? 1 : 0, ce.k, ce.n,
+                                     full->w[0], full->rows, c.r_carry == 0 ? 1 : 0, domain, &o);
+    if (n == 0) {
+        xlog_hip_rel *e = rel_new(ctx, 2, 0);
+        e->flags = REL_CANONICAL;
+        return e;
+    }
+    if (c.r_carry == 1) {  // head column order (value, carry): swap and re-sort
+        uint64_t *sw = static_cast<uint64_t *>(ctx->alloc(n * sizeof(uint64_t)));
+        swap_words(ctx, o, n, sw);
+        ctx->free(o);
+        o = sort_keys(ctx, sw, n, true);  // consumes sw
+    }
+    return rel_adopt(ctx, 2, n, o, nullptr, REL_CANONICAL);
 }
 
 // Set of the projected join, canonical: dedup_full_row(project(join(l, r))).
@@ -943,8 +1054,7 @@ struct Driver {
             }
         }
         bags.clear();
-        uint64_t *s = sort_keys(ctx, cat, total, true);
-        if (s != cat) ctx->free(cat);
+        uint64_t *s = sort_keys(ctx, cat, total, true);  // consumes cat
         uint64_t *o = static_cast<uint64_t *>(ctx->alloc(total * sizeof(uint64_t)));
         Buf<uint64_t> cnt(ctx, 1);
         select_unique_diff(ctx, s, total, against.k, against.n, o, cnt.p);
@@ -1458,6 +1568,74 @@ xlog_hip_status xlog_hip_hash_join(xlog_hip_ctx *ctx, const xlog_hip_rel *left, 
         Ctx *c = C(ctx);
         OUT_GUARD;
         *out = op_join(c, left, right, left_key, right_key, join_type, nullptr);
+    });
+}
+xlog_hip_status xlog_hip_join_index_build(xlog_hip_ctx *ctx, const xlog_hip_rel *right, uint32_t right_key,
+                                          xlog_hip_join_index **out) {
+    return guarded([&] {
+        Ctx *c = C(ctx);
+        OUT_GUARD;
+        need_rel(right, "right");
+        XH_REQUIRE(right_key < right->arity, XLOG_HIP_INVALID_ARG, "right key column out of range");
+        XH_REQUIRE(right->arity <= 2, XLOG_HIP_UNSUPPORTED, "join: input arity above 2 is not supported");
+        XH_REQUIRE(right->rows > 0, XLOG_HIP_INVALID_ARG, "cannot build a join index for an empty relation");
+        auto *ix = new xlog_hip_join_index;
+        ix->ctx = c;
+        ix->arity = right->arity;
+        ix->key = right_key;
+        ix->rows = right->rows;
+        try {
+            build_join_index(c, right->w[0], right->rows, right->arity, (int)right_key,
+                             (right->flags & REL_CANONICAL) != 0, ix->J);
+        } catch (...) {
+            delete ix;
+            throw;
+        }
+        *out = ix;
+    });
+}
+xlog_hip_status xlog_hip_hash_join_with_index(xlog_hip_ctx *ctx, const xlog_hip_rel *left, const xlog_hip_rel *right,
+                                              uint32_t left_key, uint32_t right_key, int join_type,
+                                              const xlog_hip_join_index *index, uint64_t max_output,
+                                              xlog_hip_rel **out) {
+    return guarded([&] {
+        Ctx *c = C(ctx);
+        OUT_GUARD;
+        need_rel(left, "left");
+        need_rel(right, "right");
+        XH_REQUIRE(index, XLOG_HIP_INVALID_ARG, "join index is NULL");
+        XH_REQUIRE(index->ctx == c, XLOG_HIP_INVALID_ARG, "join index belongs to another context");
+        XH_REQUIRE(index->arity == right->arity && index->key == right_key && index->rows == right->rows,
+                   XLOG_HIP_INVALID_ARG, "join index was not built over this right relation and key");
+        *out = op_join_indexed(c, left, left_key, index->J, right->arity, right_key, join_type, nullptr, max_output);
+    });
+}
+void xlog_hip_join_index_free(xlog_hip_join_index *index) { delete index; }
+xlog_hip_status xlog_hip_nested_loop_join(xlog_hip_ctx *ctx, const xlog_hip_rel *left, const xlog_hip_rel *right,
+                                          uint32_t left_key, uint32_t right_key, xlog_hip_rel **out) {
+    return guarded([&] {
+        Ctx *c = C(ctx);
+        OUT_GUARD;
+        *out = op_nested_loop_join(c, left, right, left_key, right_key);
+    });
+}
+xlog_hip_status xlog_hip_dedup_sorted(xlog_hip_ctx *ctx, const xlog_hip_rel *in, const uint32_t *key_cols,
+                                      uint32_t n_keys, xlog_hip_rel **out) {
+    return guarded([&] {
+        Ctx *c = C(ctx);
+        OUT_GUARD;
+        need_rel(in, "input");
+        *out = op_dedup_sorted(c, in, check_cols(in, key_cols, n_keys));
+    });
+}
+xlog_hip_status xlog_hip_fj_delta_novel(xlog_hip_ctx *ctx, const xlog_hip_rel *delta, const xlog_hip_rel *edge,
+                                        const xlog_hip_rel *full, const xlog_hip_fj_delta_cols *cols, uint32_t domain,
+                                        xlog_hip_rel **out) {
+    return guarded([&] {
+        Ctx *c = C(ctx);
+        OUT_GUARD;
+        XH_REQUIRE(cols, XLOG_HIP_INVALID_ARG, "column roles are NULL");
+        *out = op_fj_delta(c, delta, edge, full, *cols, domain);
     });
 }
 xlog_hip_status xlog_hip_sort_merge_join(xlog_hip_ctx *ctx, const xlog_hip_rel *left, const xlog_hip_rel *right,

@@ -276,6 +276,22 @@ std::vector<uint64_t> probe_tile_offsets(Ctx *ctx, const ProbeJob &job);
 void probe_emit_range(Ctx *ctx, const ProbeJob &job, uint64_t t0, uint64_t t1, uint64_t rows, int out_arity,
                       const int oc[4], uint64_t *out0, uint64_t *out1);
 
+// Nested-loop inner join of packed arity-1/2 relations on one key column,
+// output (left columns ++ right columns) in left-row-major, right-row order.
+// Returns the row count; out1 is set when the output arity exceeds 2.
+uint64_t nested_loop_join(Ctx *ctx, const uint64_t *l, uint64_t nl, int la, int lk, const uint64_t *r, uint64_t nr,
+                          int ra, int rk, uint64_t **out0, uint64_t **out1);
+void scan_u64_small(Ctx *ctx, uint64_t *a, uint64_t n, uint64_t *total);
+
+// One factorized TC delta step over a dense domain (ids < domain): the set
+// {(x, z) : (x, y) in delta, (y, z) in edge, (x, z) not in full} as sorted
+// unique packed (x << 32) | z rows.  delta and full are given as packed rows
+// with the x column in the high (x_hi = 1) or low word; edge is sorted unique
+// (y << 32) | z.  Returns the row count.
+uint64_t fj_delta_step(Ctx *ctx, const uint64_t *delta, uint64_t nd, int delta_x_hi, const uint64_t *edge,
+                       uint64_t ne, const uint64_t *full, uint64_t nf, int full_x_hi, uint32_t domain,
+                       uint64_t **out);
+
 // small helpers
 inline unsigned grid_for(uint64_t n, unsigned block, unsigned cap) {
     uint64_t g = (n + block - 1) / block;

@@ -554,6 +554,78 @@ void sort_segments(Ctx *ctx, uint64_t *data, uint64_t n, const uint64_t *heads, 
 }  // namespace xh
 
 namespace xh {
+namespace {
+
+// Nested-loop inner join on one key column.  One wave per left row; the
+// lanes stride the right rows 64 at a time and a ballot per step gives the
+// matches, so every left row's outputs come in right-row order.  The count
+// launch (emit == 0) writes per-left-row match counts; the emit launch reads
+// their exclusive prefix and writes (left columns ++ right columns).
+constexpr int NLJ_WAVES = 4;
+__global__ __launch_bounds__(NLJ_WAVES * WAVE) void k_nlj(const uint64_t *__restrict__ l, uint64_t nl, int la, int lk,
+                                                         const uint64_t *__restrict__ r, uint64_t nr, int ra, int rk,
+                                                         uint64_t *__restrict__ cnt_off, int emit, OutSpec spec,
+                                                         uint64_t *__restrict__ out0, uint64_t *__restrict__ out1) {
+    const int lane = threadIdx.x & (WAVE - 1);
+    const uint64_t row = (uint64_t)blockIdx.x * NLJ_WAVES + (threadIdx.x >> 6);
+    if (row >= nl) return;
+    const uint64_t lw = l[row];
+    const uint32_t lc0 = packed_col(lw, la, 0), lc1 = la == 2 ? packed_col(lw, la, 1) : 0u;
+    const uint32_t key = lk == 0 ? lc0 : lc1;
+    const uint64_t lt_mask = (1ull << lane) - 1ull;
+    uint64_t o = emit ? cnt_off[row] : 0ull;
+    for (uint64_t b = 0; b < nr; b += WAVE) {
+        const uint64_t j = b + (uint64_t)lane;
+        uint32_t rc0 = 0, rc1 = 0;
+        bool m = false;
+        if (j < nr) {
+            const uint64_t rw = r[j];
+            rc0 = packed_col(rw, ra, 0);
+            rc1 = ra == 2 ? packed_col(rw, ra, 1) : 0u;
+            m = (rk == 0 ? rc0 : rc1) == key;
+        }
+        const uint64_t bal = __ballot(m);
+        if (emit && m) {
+            const uint64_t pos = o + (uint64_t)__popcll(bal & lt_mask);
+            const uint32_t v[4] = {lc0, lc1, rc0, rc1};
+            uint64_t w0, w1;
+            make_words(spec, v, &w0, &w1);
+            out0[pos] = w0;
+            if (out1) out1[pos] = w1;
+        }
+        o += (uint64_t)__popcll(bal);
+    }
+    if (!emit && lane == 0) cnt_off[row] = o;
+}
+
+}  // namespace
+
+uint64_t nested_loop_join(Ctx *ctx, const uint64_t *l, uint64_t nl, int la, int lk, const uint64_t *r, uint64_t nr,
+                          int ra, int rk, uint64_t **out0, uint64_t **out1) {
+    *out0 = *out1 = nullptr;
+    if (nl == 0 || nr == 0) return 0;
+    Buf<uint64_t> off(ctx, nl + 1);
+    OutSpec spec{la + ra, {0, 1, 2, 3}};
+    if (la == 1) {  // v = {l.c0, l.c1, r.c0, r.c1}: output = left columns ++ right columns
+        spec.oc[1] = 2;
+        spec.oc[2] = 3;
+    }
+    const unsigned grid = (unsigned)((nl + NLJ_WAVES - 1) / NLJ_WAVES);
+    hipLaunchKernelGGL(k_nlj, dim3(grid), dim3(NLJ_WAVES * WAVE), 0, ctx->stream, l, nl, la, lk, r, nr, ra, rk, off.p,
+                       0, spec, nullptr, nullptr);
+    XH_CHECK_HIP(hipGetLastError());
+    scan_u64_small(ctx, off.p, nl, off.p + nl);
+    ctx->read_scalars(off.p + nl, 1);
+    const uint64_t total = ctx->host_scalars[0];
+    if (total == 0) return 0;
+    *out0 = static_cast<uint64_t *>(ctx->alloc(total * sizeof(uint64_t)));
+    if (spec.arity > 2) *out1 = static_cast<uint64_t *>(ctx->alloc(total * sizeof(uint64_t)));
+    hipLaunchKernelGGL(k_nlj, dim3(grid), dim3(NLJ_WAVES * WAVE), 0, ctx->stream, l, nl, la, lk, r, nr, ra, rk, off.p,
+                       1, spec, *out0, *out1);
+    XH_CHECK_HIP(hipGetLastError());
+    return total;
+}
+
 void scan_u64_small(Ctx *ctx, uint64_t *a, uint64_t n, uint64_t *total) {
     hipLaunchKernelGGL(k_scan_small, dim3(1), dim3(1024), 0, ctx->stream, a, n, total);
     XH_CHECK_HIP(hipGetLastError());

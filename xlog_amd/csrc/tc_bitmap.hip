@@ -155,6 +155,22 @@ __global__ __launch_bounds__(TB) void k_tc_step(uint32_t nv, uint64_t words, con
 
 __global__ void k_set_ull(unsigned long long *p, unsigned long long v) { *p = v; }
 
+// Bit (x, z) of a domain x domain bitmap for every packed pair row; x is the
+// high word when x_hi, else the low word.  Rows outside the domain are
+// skipped (callers reject them before the launch).
+__global__ void k_pairs_to_bits(const uint64_t *__restrict__ rows, uint64_t n, int x_hi, uint32_t domain,
+                                uint64_t words, uint64_t *__restrict__ B, uint8_t *__restrict__ nz) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const uint64_t e = rows[i];
+        const uint32_t x = x_hi ? (uint32_t)(e >> 32) : (uint32_t)e;
+        const uint32_t z = x_hi ? (uint32_t)e : (uint32_t)(e >> 32);
+        if (x >= domain || z >= domain) continue;
+        atomicOr((unsigned long long *)&B[(uint64_t)x * words + (z >> 6)], 1ull << (z & 63));
+        if (nz) nz[x] = 1;
+    }
+}
+
 // per-row popcount of R
 __global__ __launch_bounds__(TB) void k_row_counts(const uint64_t *__restrict__ R, uint64_t words,
                                                    uint64_t *__restrict__ cnt) {
@@ -221,6 +237,59 @@ __global__ __launch_bounds__(TB) void k_emit_rows(const uint64_t *__restrict__ R
 }
 
 }  // namespace
+
+// One factorized delta step (the reference's fj_delta_novel_u32_recorded,
+// crates/xlog-cuda/src/provider/fj_delta.rs:117-490): bitmaps of full R and
+// of delta over the domain, one k_tc_step (novel = (U_{y in delta[x]}
+// edge[y]) & ~R[x]), then the novel bitmap emitted row by row, which gives
+// sorted unique (x, z) rows.
+uint64_t fj_delta_step(Ctx *ctx, const uint64_t *delta, uint64_t nd, int delta_x_hi, const uint64_t *edge,
+                       uint64_t ne, const uint64_t *full, uint64_t nf, int full_x_hi, uint32_t domain,
+                       uint64_t **out) {
+    *out = nullptr;
+    if (nd == 0 || ne == 0 || domain == 0) return 0;
+    const uint64_t words = ((uint64_t)domain + 63) / 64;
+    XH_REQUIRE(words * 8 <= 64 * 1024, XLOG_HIP_UNSUPPORTED, "fj delta: domain too large for an LDS row");
+    const uint64_t cells = (uint64_t)domain * words;
+    Buf<uint64_t> R(ctx, cells), D(ctx, cells), N(ctx, cells);
+    Buf<uint64_t> row_ptr(ctx, (uint64_t)domain + 1);
+    Buf<uint32_t> adj(ctx, ne);
+    const uint64_t nz_bytes = ((uint64_t)domain + 3) / 4 * 4;
+    Buf<uint8_t> nz(ctx, nz_bytes), nz_next(ctx, nz_bytes);
+    Buf<unsigned long long> cnt(ctx, 2);
+    fill_u64(ctx, R.p, 0ull, cells);
+    fill_u64(ctx, D.p, 0ull, cells);
+    fill_u64(ctx, N.p, 0ull, cells);
+    fill_u64(ctx, reinterpret_cast<uint64_t *>(cnt.p), 0ull, 2);
+    fill_u32(ctx, reinterpret_cast<uint32_t *>(nz.p), 0u, nz_bytes / 4);
+    if (nf)
+        hipLaunchKernelGGL(k_pairs_to_bits, dim3(grid_for(nf, 256, 4096)), dim3(256), 0, ctx->stream, full, nf,
+                           full_x_hi, domain, words, R.p, nullptr);
+    hipLaunchKernelGGL(k_pairs_to_bits, dim3(grid_for(nd, 256, 4096)), dim3(256), 0, ctx->stream, delta, nd,
+                       delta_x_hi, domain, words, D.p, nz.p);
+    hipLaunchKernelGGL(k_row_ptr, dim3(grid_for((uint64_t)domain + 1, 256, 4096)), dim3(256), 0, ctx->stream, edge,
+                       ne, domain, row_ptr.p);
+    hipLaunchKernelGGL(k_adj, dim3(grid_for(ne, 256, 4096)), dim3(256), 0, ctx->stream, edge, ne, adj.p);
+    XH_CHECK_HIP(hipGetLastError());
+    {
+        Prof prof(ctx, XLOG_HIP_KERNEL_TC_STEP, 32.0 * (double)cells);
+        hipLaunchKernelGGL(k_tc_step, dim3(domain), dim3(TB), words * sizeof(uint64_t), ctx->stream, domain, words,
+                           row_ptr.p, adj.p, R.p, D.p, N.p, nz.p, nz_next.p, cnt.p);
+        XH_CHECK_HIP(hipGetLastError());
+    }
+    Buf<uint64_t> rc(ctx, (uint64_t)domain + 1);
+    hipLaunchKernelGGL(k_row_counts, dim3(domain), dim3(TB), 0, ctx->stream, N.p, words, rc.p);
+    XH_CHECK_HIP(hipGetLastError());
+    scan_u64_small(ctx, rc.p, domain, rc.p + domain);
+    ctx->read_scalars(rc.p + domain, 1);
+    const uint64_t total = ctx->host_scalars[0];
+    if (total == 0) return 0;
+    *out = static_cast<uint64_t *>(ctx->alloc(total * sizeof(uint64_t)));
+    Prof prof(ctx, XLOG_HIP_KERNEL_TC_EMIT, 8.0 * (double)total + 8.0 * (double)cells);
+    hipLaunchKernelGGL(k_emit_rows, dim3(domain), dim3(TB), 0, ctx->stream, N.p, words, rc.p, *out);
+    XH_CHECK_HIP(hipGetLastError());
+    return total;
+}
 
 // scan helper from join.hip
 void scan_u64_small(Ctx *ctx, uint64_t *a, uint64_t n, uint64_t *total);

@@ -13,7 +13,7 @@ from __future__ import annotations
 import ctypes as C
 import weakref
 from pathlib import Path
-from typing import Iterable, Sequence
+from typing import Iterable, Optional, Sequence
 
 import numpy as np
 
@@ -55,6 +55,22 @@ class FixpointStats(C.Structure):
     ]
 
 
+class FjDeltaCols(C.Structure):
+    """Column roles of one factorized delta step (reference FjDeltaCols,
+    crates/xlog-cuda/src/provider/fj_delta.rs:50-84)."""
+
+    _fields_ = [
+        ("delta_carry", C.c_uint32),
+        ("delta_key", C.c_uint32),
+        ("r_carry", C.c_uint32),
+        ("r_value", C.c_uint32),
+    ]
+
+
+#: right-linear TC orientation: delta (x, y), head (x, z)
+FJ_DELTA_CANONICAL = (0, 1, 0, 1)
+
+
 def _load() -> C.CDLL:
     if not _LIB_PATH.exists():
         raise ImportError(
@@ -87,6 +103,12 @@ def _load() -> C.CDLL:
         "xlog_hip_sort": (I32, [P, P, P, U32, PP]),
         "xlog_hip_dedup": (I32, [P, P, P, U32, PP]),
         "xlog_hip_dedup_full_row": (I32, [P, P, PP]),
+        "xlog_hip_dedup_sorted": (I32, [P, P, P, U32, PP]),
+        "xlog_hip_join_index_build": (I32, [P, P, U32, PP]),
+        "xlog_hip_hash_join_with_index": (I32, [P, P, P, U32, U32, I32, P, U64, PP]),
+        "xlog_hip_join_index_free": (None, [P]),
+        "xlog_hip_nested_loop_join": (I32, [P, P, P, U32, U32, PP]),
+        "xlog_hip_fj_delta_novel": (I32, [P, P, P, P, C.POINTER(FjDeltaCols), U32, PP]),
         "xlog_hip_union": (I32, [P, P, P, PP]),
         "xlog_hip_union_many": (I32, [P, PP, U32, PP]),
         "xlog_hip_diff": (I32, [P, P, P, PP]),
@@ -122,6 +144,8 @@ ABI_SYMBOLS = (
     "xlog_hip_rel_from_host_packed", "xlog_hip_rel_download_column", "xlog_hip_rel_download_packed",
     "xlog_hip_rel_num_rows", "xlog_hip_rel_arity", "xlog_hip_rel_is_canonical", "xlog_hip_rel_device_words",
     "xlog_hip_rel_clone", "xlog_hip_rel_free", "xlog_hip_sort", "xlog_hip_dedup", "xlog_hip_dedup_full_row",
+    "xlog_hip_dedup_sorted", "xlog_hip_join_index_build", "xlog_hip_hash_join_with_index",
+    "xlog_hip_join_index_free", "xlog_hip_nested_loop_join", "xlog_hip_fj_delta_novel",
     "xlog_hip_union", "xlog_hip_union_many", "xlog_hip_diff", "xlog_hip_hash_join",
     "xlog_hip_sort_merge_join", "xlog_hip_join_project", "xlog_hip_join_project_dedup", "xlog_hip_project",
     "xlog_hip_is_sorted",
@@ -192,6 +216,35 @@ class Relation:
     def free(self) -> None:
         if self._h:
             _lib.xlog_hip_rel_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class JoinIndex:
+    """Reusable join index over one key column (the JoinIndexV2 counterpart,
+    relational.rs:3728).  Freed when garbage collected or when its provider closes."""
+
+    __slots__ = ("_h", "_provider", "right_key", "__weakref__")
+
+    def __init__(self, provider: "HipKernelProvider", handle: C.c_void_p, right_key: int):
+        self._provider = provider
+        self._h = handle
+        self.right_key = right_key
+
+    @property
+    def handle(self) -> C.c_void_p:
+        if not self._h:
+            raise XlogError(1, "join index already freed")
+        return self._h
+
+    def free(self) -> None:
+        if self._h:
+            _lib.xlog_hip_join_index_free(self._h)
             self._h = None
 
     def __del__(self):
@@ -354,6 +407,13 @@ class HipKernelProvider:
         _check(_lib.xlog_hip_dedup(self.ctx, rel.handle, arr, n, C.byref(h)))
         return self._rel(h)
 
+    def dedup_sorted(self, rel: Relation, key_cols: Sequence[int]) -> Relation:
+        """First row of every run of adjacent rows equal on key_cols (input already ordered)."""
+        arr, n = _u32_array(key_cols)
+        h = C.c_void_p()
+        _check(_lib.xlog_hip_dedup_sorted(self.ctx, rel.handle, arr, n, C.byref(h)))
+        return self._rel(h)
+
     def dedup_full_row(self, rel: Relation) -> Relation:
         h = C.c_void_p()
         _check(_lib.xlog_hip_dedup_full_row(self.ctx, rel.handle, C.byref(h)))
@@ -384,6 +444,44 @@ class HipKernelProvider:
         h = C.c_void_p()
         _check(_lib.xlog_hip_hash_join(self.ctx, left.handle, right.handle, left_keys[0], right_keys[0],
                                        join_type, C.byref(h)))
+        return self._rel(h)
+
+    def build_join_index_v2(self, right: Relation, right_keys: Sequence[int]) -> JoinIndex:
+        if len(right_keys) != 1:
+            raise XlogError(7, "joins on one key column per side are supported")
+        h = C.c_void_p()
+        _check(_lib.xlog_hip_join_index_build(self.ctx, right.handle, right_keys[0], C.byref(h)))
+        ix = JoinIndex(self, h, right_keys[0])
+        self._live.add(ix)
+        return ix
+
+    def hash_join_v2_with_index(self, left: Relation, right: Relation, left_keys: Sequence[int],
+                                right_keys: Sequence[int], join_type: int, index: JoinIndex,
+                                max_output: Optional[int] = None) -> Relation:
+        if len(left_keys) != 1 or len(right_keys) != 1:
+            raise XlogError(7, "joins on one key column per side are supported")
+        h = C.c_void_p()
+        _check(_lib.xlog_hip_hash_join_with_index(self.ctx, left.handle, right.handle, left_keys[0], right_keys[0],
+                                                  join_type, index.handle, max_output or 0, C.byref(h)))
+        return self._rel(h)
+
+    def nested_loop_join_v2_inner_u32_1key(self, left: Relation, right: Relation, left_key: int,
+                                           right_key: int) -> Relation:
+        h = C.c_void_p()
+        _check(_lib.xlog_hip_nested_loop_join(self.ctx, left.handle, right.handle, left_key, right_key,
+                                              C.byref(h)))
+        return self._rel(h)
+
+    def fj_delta_novel_u32_recorded(self, delta: Relation, edge: Relation, full_r: Relation,
+                                    cols: Sequence[int] = FJ_DELTA_CANONICAL, domain: int = 1 << 16) -> Relation:
+        """One factorized TC delta step: novel head tuples of delta x edge not in full_r (canonical).
+
+        cols = (delta_carry, delta_key, r_carry, r_value); the reference's launch stream is the
+        provider's stream."""
+        roles = FjDeltaCols(*cols)
+        h = C.c_void_p()
+        _check(_lib.xlog_hip_fj_delta_novel(self.ctx, delta.handle, edge.handle, full_r.handle, C.byref(roles),
+                                            domain, C.byref(h)))
         return self._rel(h)
 
     def sort_merge_join_v2_inner_u32_1key(self, left: Relation, right: Relation, left_key: int,
