@@ -216,6 +216,10 @@ def test_join_project_dedup_ordered(provider, nl, nr, lkeys, avals, seed):
     assert np.array_equal(p.download_packed(p.join_project_dedup(L, R, 1, 1, [0, 2])), exp2)
     exp3 = oracle.sort_dedup(oracle.join_project(l, r, 1, 0, 3, 0))
     assert np.array_equal(p.download_packed(p.join_project_dedup(L, R, 1, 0, [3, 0])), exp3)
+    # a canonical build side (already a sorted set) takes the index without re-sorting
+    Rc = p.dedup_full_row(R)
+    got_c = p.join_project_dedup(L, Rc, 1, 0, [0, 3])
+    assert got_c.is_canonical() and np.array_equal(p.download_packed(got_c), exp)
 
 
 def test_join_skewed_hot_key(provider):

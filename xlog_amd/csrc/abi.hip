@@ -147,6 +147,10 @@ __global__ void k_iota(uint32_t *p, uint64_t n) {
     uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = (uint32_t)i;
 }
+__global__ void k_iota64(uint64_t *p, uint64_t n) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = i;
+}
 __global__ void k_gather(const uint64_t *__restrict__ in, const uint32_t *__restrict__ perm, uint64_t n,
                          uint64_t *__restrict__ out) {
     uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
@@ -538,8 +542,12 @@ struct xlog_hip_join_index {
     uint64_t rows = 0;
 };
 namespace xh {
+// payload_sorted: the payload order inside a run is ascending; unique_rows
+// (implies payload_sorted): duplicate (key, payload) rows are dropped, so a
+// run's payloads are distinct (set-semantics callers only).
 static void build_join_index(Ctx *ctx, const uint64_t *keys, uint64_t n, uint32_t arity, int col, bool canonical,
-                             JoinIndex &J, bool payload_sorted = false) {
+                             JoinIndex &J, bool payload_sorted = false, bool unique_rows = false) {
+    if (unique_rows) payload_sorted = true;
     J.n = n;
     uint64_t *sk = nullptr;
     bool own = false;
@@ -561,6 +569,15 @@ static void build_join_index(Ctx *ctx, const uint64_t *keys, uint64_t n, uint32_
         swap_words(ctx, keys, n, sk);
         own = true;
         sk = sort_keys(ctx, sk, n, true, dlo, 8);
+    }
+    if (unique_rows && n > 1 && !(canonical && col == 0 && arity == 2)) {
+        uint64_t *u;
+        const uint64_t un = unique_keys(ctx, sk, n, &u);
+        if (own) ctx->free(sk);
+        sk = u;
+        own = true;
+        n = un;
+        J.n = un;
     }
     build_run_index(ctx, sk, n, J.ix);
     J.payload = Buf<uint32_t>(ctx, n ? n : 1);
@@ -788,8 +805,11 @@ static xlog_hip_rel *op_fj_delta(Ctx *ctx, const xlog_hip_rel *delta, const xlog
 // replaces the radix sort of the whole join output.  Other shapes take the
 // join -> sort -> unique path.
 void left_keys(Ctx *ctx, const uint64_t *l, uint64_t n, int arity, int oc0, int jk, uint64_t *out);
-void group_head_flags(Ctx *ctx, const uint64_t *k, uint64_t n, uint8_t *flags);
 void sort_segments(Ctx *ctx, uint64_t *data, uint64_t n, const uint64_t *heads, uint64_t nh);
+void group_marks(Ctx *ctx, const uint64_t *k, uint64_t n, uint8_t *head, uint8_t *member, int32_t *gsel);
+void group_heads_select(Ctx *ctx, const uint64_t *head_pos, uint64_t nh, int32_t *gsel);
+void group_segments(Ctx *ctx, const uint64_t *sorted, uint64_t n, const uint64_t *head_keys, uint64_t nh,
+                    uint64_t *seg);
 
 static xlog_hip_rel *op_join_project_dedup(Ctx *ctx, const xlog_hip_rel *l, const xlog_hip_rel *r, uint32_t lk,
                                            uint32_t rk, const std::vector<int> &out_cols) {
@@ -819,40 +839,82 @@ static xlog_hip_rel *op_join_project_dedup(Ctx *ctx, const xlog_hip_rel *l, cons
     uint64_t *lkeys = static_cast<uint64_t *>(ctx->alloc(n * sizeof(uint64_t)));
     left_keys(ctx, l->w[0], n, (int)l->arity, out_cols[0], (int)lk, lkeys);
     lkeys = sort_keys(ctx, lkeys, n, true, 4, 8);
-    // 2. build index with payload-ordered runs
+    Buf<uint64_t> lk_buf;  // owns lkeys from here on
+    lk_buf.ctx = ctx;
+    lk_buf.p = lkeys;
+    // 2. build index whose runs hold distinct, ascending payloads: a probe
+    //    row alone with its out column then emits sorted, unique outputs
     JoinIndex J;
-    build_join_index(ctx, r->w[0], r->rows, r->arity, (int)rk, (r->flags & REL_CANONICAL) != 0, J, true);
-    // 3. probe: v0 = out column (high word of the probe key), v3 = payload; pcol 1 = join key
-    const int oc[4] = {0, 3, 0, 0};
-    uint64_t *o = nullptr;
-    uint64_t m = 0;
-    try {
-        m = join_probe_general(ctx, lkeys, n, 1, J.ix, J.payload.p, 2, oc, &o, nullptr);
-        // 4. runs whose out column comes from several probe rows are interleaved: sort them
-        if (m) {
-            Buf<uint8_t> flags(ctx, n);
-            group_head_flags(ctx, lkeys, n, flags.p);
-            Buf<uint64_t> heads(ctx, n), cnt(ctx, 1);
-            select_flags(ctx, lkeys, flags.p, n, heads.p, cnt.p);
-            uint64_t nh = read_count(ctx, cnt.p);
-            sort_segments(ctx, o, m, heads.p, nh);
+    build_join_index(ctx, r->w[0], r->rows, r->arity, (int)rk, (r->flags & REL_CANONICAL) != 0, J, true, true);
+    // 3. probe rows sharing their out column (groups) can emit the same
+    //    output twice and interleave: their outputs are produced on the side
+    //    (probe, sort inside each group, unique) and copied into place by the
+    //    main emit through the group selector
+    Buf<uint8_t> head(ctx, n), member(ctx, n);
+    Buf<int32_t> gsel(ctx, n);
+    group_marks(ctx, lkeys, n, head.p, member.p, gsel.p);
+    Buf<uint64_t> cnt(ctx, 2);
+    Buf<uint64_t> mkeys(ctx, n);
+    select_flags(ctx, lkeys, member.p, n, mkeys.p, cnt.p);
+    const uint64_t nm = read_count(ctx, cnt.p);
+    const int oc[4] = {0, 3, 0, 0};  // v0 = out column (probe high word), v3 = payload
+    Buf<uint64_t> gseg, gsrc_buf;
+    if (nm) {
+        Buf<uint64_t> hkeys(ctx, n), hpos(ctx, n), iota(ctx, n);
+        LAUNCH_1D(k_iota64, n, iota.p, n);
+        select_flags(ctx, lkeys, head.p, n, hkeys.p, cnt.p);
+        select_flags(ctx, iota.p, head.p, n, hpos.p, cnt.p + 1);
+        ctx->read_scalars(cnt.p, 2);
+        const uint64_t nh = ctx->host_scalars[0];
+        uint64_t *bag = nullptr;
+        const uint64_t m2 = join_probe_general(ctx, mkeys.p, nm, 1, J.ix, J.payload.p, 2, oc, &bag, nullptr);
+        uint64_t *u2 = nullptr, nu2 = 0;
+        if (m2) {
+            try {
+                sort_segments(ctx, bag, m2, hkeys.p, nh);
+                nu2 = unique_keys(ctx, bag, m2, &u2);
+            } catch (...) {
+                ctx->free(bag);
+                throw;
+            }
+            ctx->free(bag);
         }
-    } catch (...) {
-        ctx->free(lkeys);
-        if (o) ctx->free(o);
-        throw;
+        gsrc_buf.ctx = ctx;
+        gsrc_buf.p = u2;
+        gseg = Buf<uint64_t>(ctx, 2 * nh);
+        if (nu2) {
+            group_segments(ctx, u2, nu2, hkeys.p, nh, gseg.p);
+        } else {
+            fill_u64(ctx, gseg.p, 0ull, 2 * nh);
+        }
+        group_heads_select(ctx, hpos.p, nh, gsel.p);
     }
-    ctx->free(lkeys);
-    if (!m) {
+    // 4. the main probe: count, scan, emit into the final buffer
+    ProbeJob job;
+    job.probe = lkeys;
+    job.n = n;
+    job.pcol = 1;
+    job.ix = &J.ix;
+    job.payload = J.payload.p;
+    if (nm) {
+        job.gsel = gsel.p;
+        job.gseg = gseg.p;
+        job.gsrc = gsrc_buf.p;
+    }
+    const uint64_t total = probe_prepare(ctx, job);
+    if (!total) {
         xlog_hip_rel *e = rel_new(ctx, 2, 0);
         e->flags = REL_CANONICAL;
         return e;
     }
-    // 5. one unique pass
-    uint64_t *u;
-    uint64_t un = unique_keys(ctx, o, m, &u);
-    ctx->free(o);
-    return rel_adopt(ctx, 2, un, u, nullptr, REL_CANONICAL);
+    uint64_t *o = static_cast<uint64_t *>(ctx->alloc(total * sizeof(uint64_t)));
+    try {
+        probe_emit_range(ctx, job, 0, job.tiles, total, 2, oc, o, nullptr);
+    } catch (...) {
+        ctx->free(o);
+        throw;
+    }
+    return rel_adopt(ctx, 2, total, o, nullptr, REL_CANONICAL);
 }
 
 static xlog_hip_rel *op_project(Ctx *ctx, const xlog_hip_rel *in, const std::vector<int> &cols) {

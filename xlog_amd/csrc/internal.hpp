@@ -260,15 +260,22 @@ uint64_t join_probe_project(Ctx *ctx, const uint64_t *probe, uint64_t n, int pco
 
 // Probe in pieces: a count pass over all probe tiles (tile offsets on the
 // device, total read back), then emits of tile ranges.  Tile t covers probe
-// rows [t * 4096, (t + 1) * 4096).
+// rows [t * 256 * items, (t + 1) * 256 * items).
 struct ProbeJob {
     const uint64_t *probe = nullptr;
     uint64_t n = 0;
     int pcol = 0;
     const RunIndex *ix = nullptr;
     const uint32_t *payload = nullptr;
+    // Optional row groups, for 2-column outputs: gsel[i] = -1 plain row, -2
+    // a row with no output, g >= 0 a row whose outputs are the finished words
+    // gsrc[gseg[2g] .. gseg[2g] + gseg[2g + 1]) instead of its matches.
+    const int32_t *gsel = nullptr;
+    const uint64_t *gseg = nullptr;  // (start, count) per group
+    const uint64_t *gsrc = nullptr;
     Buf<uint64_t> toff;  // exclusive prefix of per-tile output counts; toff[tiles] = total
     uint64_t tiles = 0, total = 0;
+    int items = 16;      // probe rows per thread (set by probe_prepare); a tile is 256 * items rows
 };
 uint64_t probe_prepare(Ctx *ctx, ProbeJob &job);
 std::vector<uint64_t> probe_tile_offsets(Ctx *ctx, const ProbeJob &job);

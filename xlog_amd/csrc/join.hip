@@ -28,9 +28,13 @@ namespace xh {
 namespace {
 
 constexpr int JB = 256;      // block
-constexpr int JITEMS = 16;   // probe rows per thread
+// probe rows per thread: JITEMS for large probes, JITEMS_SMALL (more,
+// smaller tiles) when fewer rows than JSMALL_ROWS leave the GPU under-filled
+constexpr int JITEMS = 16;
+constexpr int JITEMS_SMALL = 2;
+constexpr uint64_t JSMALL_ROWS = 4ull << 20;
 constexpr int JWAVES = JB / WAVE;
-constexpr int JTILE = JB * JITEMS;
+constexpr uint64_t tile_rows(int items) { return (uint64_t)JB * items; }
 
 __device__ __forceinline__ uint64_t hash_slot(uint32_t key, int bits) {
     return (uint64_t)(((uint64_t)key * 0x9E3779B97F4A7C15ull) >> (64 - bits));
@@ -76,7 +80,15 @@ struct ProbeArgs {
     int bits;
     const uint64_t *run_start;
     const uint32_t *payload;
+    // optional row groups (see ProbeJob): gsel[i] = -1 plain row, -2 row
+    // without output, g >= 0 row whose outputs are gsrc[gseg[2g] ..
+    // gseg[2g] + gseg[2g + 1]) (finished output words)
+    const int32_t *gsel;
+    const uint64_t *gseg;
+    const uint64_t *gsrc;
 };
+// set in a row's start when its outputs come from gsrc
+constexpr uint64_t GROUP_BIT = 1ull << 63;
 
 __device__ __forceinline__ uint64_t probe_count(const ProbeArgs &a, uint64_t row, uint64_t *start) {
     uint32_t key = a.pcol ? (uint32_t)row : (uint32_t)(row >> 32);
@@ -118,34 +130,49 @@ __device__ __forceinline__ void lookup_batch(const ProbeArgs &a, const uint64_t 
         run[r] = s ? (uint32_t)s - 1u : 0xFFFFFFFFu;
     }
     uint64_t b[N], e[N];
+    int32_t g[N];
 #pragma unroll
     for (int r = 0; r < N; ++r) {
         b[r] = run[r] != 0xFFFFFFFFu ? a.run_start[run[r]] : 0ull;
         e[r] = run[r] != 0xFFFFFFFFu ? a.run_start[run[r] + 1] : 0ull;
+        // group selectors travel with the run bounds (no extra round trip)
+        const uint64_t idx = wbase + (uint64_t)r * WAVE + lane;
+        g[r] = (a.gsel && idx < a.n) ? a.gsel[idx] : -1;
     }
 #pragma unroll
     for (int r = 0; r < N; ++r) {
         start[r] = b[r];
         cnt[r] = (uint32_t)(e[r] - b[r]);
     }
+    if (a.gsel) {
+#pragma unroll
+        for (int r = 0; r < N; ++r) {
+            if (g[r] == -2) cnt[r] = 0;
+            if (g[r] >= 0) {
+                start[r] = a.gseg[2 * g[r]] | GROUP_BIT;
+                cnt[r] = (uint32_t)a.gseg[2 * g[r] + 1];
+            }
+        }
+    }
 }
 
+template <int ITEMS>
 __global__ __launch_bounds__(JB) void k_probe_count(ProbeArgs a, uint64_t *__restrict__ tile_cnt) {
     __shared__ uint64_t s_part[JWAVES];
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
-    const uint64_t wbase = (uint64_t)blockIdx.x * JTILE + (uint64_t)wave * (JITEMS * WAVE);
-    uint64_t rows[JITEMS];
+    const uint64_t wbase = (uint64_t)blockIdx.x * tile_rows(ITEMS) + (uint64_t)wave * (ITEMS * WAVE);
+    uint64_t rows[ITEMS];
 #pragma unroll
-    for (int r = 0; r < JITEMS; ++r) {
+    for (int r = 0; r < ITEMS; ++r) {
         uint64_t idx = wbase + (uint64_t)r * WAVE + lane;
         rows[r] = idx < a.n ? a.probe[idx] : 0ull;
     }
-    uint64_t starts[JITEMS];
-    uint32_t cnts[JITEMS];
-    lookup_batch<JITEMS>(a, rows, wbase, lane, starts, cnts);
+    uint64_t starts[ITEMS];
+    uint32_t cnts[ITEMS];
+    lookup_batch<ITEMS>(a, rows, wbase, lane, starts, cnts);
     uint64_t acc = 0;
 #pragma unroll
-    for (int r = 0; r < JITEMS; ++r) acc += cnts[r];
+    for (int r = 0; r < ITEMS; ++r) acc += cnts[r];
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, WAVE);
     if (lane == 0) s_part[wave] = acc;
@@ -209,6 +236,7 @@ __device__ __forceinline__ void make_words(const OutSpec &o, const uint32_t v[4]
 
 // Emits the outputs of tiles [t0, t0 + gridDim.x); output index 0 is the
 // first output of tile t0.
+template <int ITEMS>
 __global__ __launch_bounds__(JB) void k_probe_emit(ProbeArgs a, const uint64_t *__restrict__ tile_off, uint64_t t0,
                                                    OutSpec spec, uint64_t *__restrict__ out0,
                                                    uint64_t *__restrict__ out1) {
@@ -218,21 +246,21 @@ __global__ __launch_bounds__(JB) void k_probe_emit(ProbeArgs a, const uint64_t *
     __shared__ uint64_t s_st[JWAVES][WAVE];
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
     const uint64_t tile = t0 + blockIdx.x;
-    const uint64_t wbase = tile * JTILE + (uint64_t)wave * (JITEMS * WAVE);
+    const uint64_t wbase = tile * tile_rows(ITEMS) + (uint64_t)wave * (ITEMS * WAVE);
 
-    // pass 1 over this wave's rows: all JITEMS lookups issued together (their
+    // pass 1 over this wave's rows: all ITEMS lookups issued together (their
     // latencies overlap) and kept in registers for the expansion
-    uint64_t rows[JITEMS], starts[JITEMS];
-    uint32_t cnts[JITEMS];
+    uint64_t rows[ITEMS], starts[ITEMS];
+    uint32_t cnts[ITEMS];
 #pragma unroll
-    for (int r = 0; r < JITEMS; ++r) {
+    for (int r = 0; r < ITEMS; ++r) {
         uint64_t idx = wbase + (uint64_t)r * WAVE + lane;
         rows[r] = idx < a.n ? a.probe[idx] : 0ull;
     }
-    lookup_batch<JITEMS>(a, rows, wbase, lane, starts, cnts);
+    lookup_batch<ITEMS>(a, rows, wbase, lane, starts, cnts);
     uint64_t acc = 0;
 #pragma unroll
-    for (int r = 0; r < JITEMS; ++r) acc += cnts[r];
+    for (int r = 0; r < ITEMS; ++r) acc += cnts[r];
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, WAVE);
     if (lane == 0) s_wtot[wave] = acc;
@@ -242,7 +270,7 @@ __global__ __launch_bounds__(JB) void k_probe_emit(ProbeArgs a, const uint64_t *
 
     // pass 2: expand round by round
 #pragma unroll
-    for (int r = 0; r < JITEMS; ++r) {
+    for (int r = 0; r < ITEMS; ++r) {
         const uint64_t row = rows[r], st = starts[r], c = cnts[r];
         uint64_t x = c;
 #pragma unroll
@@ -266,13 +294,18 @@ __global__ __launch_bounds__(JB) void k_probe_emit(ProbeArgs a, const uint64_t *
             }
             uint64_t prow = s_row[wave][lo];
             uint64_t bpos = s_st[wave][lo] + (j - s_ex[wave][lo]);
-            uint32_t v[4];
-            v[0] = (uint32_t)(prow >> 32);
-            v[1] = (uint32_t)prow;
-            v[2] = a.pcol ? (uint32_t)prow : (uint32_t)(prow >> 32);
-            v[3] = a.payload ? a.payload[bpos] : 0u;
             uint64_t w0, w1;
-            make_words(spec, v, &w0, &w1);
+            if (bpos & GROUP_BIT) {
+                w0 = a.gsrc[bpos & ~GROUP_BIT];
+                w1 = 0;
+            } else {
+                uint32_t v[4];
+                v[0] = (uint32_t)(prow >> 32);
+                v[1] = (uint32_t)prow;
+                v[2] = a.pcol ? (uint32_t)prow : (uint32_t)(prow >> 32);
+                v[3] = a.payload ? a.payload[bpos] : 0u;
+                make_words(spec, v, &w0, &w1);
+            }
             out0[base + j] = w0;
             if (out1) out1[base + j] = w1;
         }
@@ -327,11 +360,12 @@ static int table_bits(const RunIndex &ix) {
 static ProbeArgs probe_args(const ProbeJob &job) {
     const RunIndex &ix = *job.ix;
     return ProbeArgs{job.probe, job.n, job.pcol, ix.table.p, ix.table_mask, table_bits(ix), ix.run_start.p,
-                     job.payload};
+                     job.payload, job.gsel, job.gseg, job.gsrc};
 }
 
 uint64_t probe_prepare(Ctx *ctx, ProbeJob &job) {
-    job.tiles = (job.n + JTILE - 1) / JTILE;
+    job.items = job.n >= JSMALL_ROWS ? JITEMS : JITEMS_SMALL;
+    job.tiles = (job.n + tile_rows(job.items) - 1) / tile_rows(job.items);
     job.total = 0;
     if (job.n == 0 || job.ix->nruns == 0) return 0;
     XH_REQUIRE(job.tiles < (1ull << 31), XLOG_HIP_CAPACITY_OVERFLOW, "join probe: input too large");
@@ -339,7 +373,12 @@ uint64_t probe_prepare(Ctx *ctx, ProbeJob &job) {
     job.toff = Buf<uint64_t>(ctx, job.tiles + 1);
     {
         Prof prof(ctx, XLOG_HIP_KERNEL_PROBE_COUNT, 8.0 * (double)job.n);
-        hipLaunchKernelGGL(k_probe_count, dim3((unsigned)job.tiles), dim3(JB), 0, ctx->stream, a, job.toff.p);
+        if (job.items == JITEMS)
+            hipLaunchKernelGGL(k_probe_count<JITEMS>, dim3((unsigned)job.tiles), dim3(JB), 0, ctx->stream, a,
+                               job.toff.p);
+        else
+            hipLaunchKernelGGL(k_probe_count<JITEMS_SMALL>, dim3((unsigned)job.tiles), dim3(JB), 0, ctx->stream, a,
+                               job.toff.p);
         XH_CHECK_HIP(hipGetLastError());
     }
     hipLaunchKernelGGL(k_scan_small, dim3(1), dim3(1024), 0, ctx->stream, job.toff.p, job.tiles,
@@ -365,12 +404,17 @@ void probe_emit_range(Ctx *ctx, const ProbeJob &job, uint64_t t0, uint64_t t1, u
     if (t1 <= t0) return;
     ProbeArgs a = probe_args(job);
     OutSpec spec{out_arity, {oc[0], oc[1], oc[2], oc[3]}};
-    uint64_t nprobe = std::min<uint64_t>(job.n, t1 * JTILE) - t0 * JTILE;
+    const uint64_t tr = tile_rows(job.items);
+    uint64_t nprobe = std::min<uint64_t>(job.n, t1 * tr) - t0 * tr;
     // probe row 8 B + slot/run 16 B per probe row; payload 4 B + output 8 B per match
     Prof prof(ctx, XLOG_HIP_KERNEL_PROBE_EMIT,
               24.0 * (double)nprobe + (4.0 + 8.0 * (out_arity > 2 ? 2 : 1)) * (double)rows);
-    hipLaunchKernelGGL(k_probe_emit, dim3((unsigned)(t1 - t0)), dim3(JB), 0, ctx->stream, a, job.toff.p, t0, spec,
-                       out0, out1);
+    if (job.items == JITEMS)
+        hipLaunchKernelGGL(k_probe_emit<JITEMS>, dim3((unsigned)(t1 - t0)), dim3(JB), 0, ctx->stream, a, job.toff.p,
+                           t0, spec, out0, out1);
+    else
+        hipLaunchKernelGGL(k_probe_emit<JITEMS_SMALL>, dim3((unsigned)(t1 - t0)), dim3(JB), 0, ctx->stream, a,
+                           job.toff.p, t0, spec, out0, out1);
     XH_CHECK_HIP(hipGetLastError());
 }
 
@@ -404,7 +448,8 @@ uint64_t join_probe_project(Ctx *ctx, const uint64_t *probe, uint64_t n, int pco
 void join_match_flags(Ctx *ctx, const uint64_t *probe, uint64_t n, int pcol, const RunIndex &ix, int want,
                       uint8_t *flags) {
     if (n == 0) return;
-    ProbeArgs a{probe, n, pcol, ix.table.p, ix.table_mask, table_bits(ix), ix.run_start.p, nullptr};
+    ProbeArgs a{probe, n, pcol, ix.table.p, ix.table_mask, table_bits(ix), ix.run_start.p, nullptr,
+                nullptr, nullptr, nullptr};
     hipLaunchKernelGGL(k_match_flags, dim3(grid_for(n, 256, 16384)), dim3(256), 0, ctx->stream, a, want, flags);
     XH_CHECK_HIP(hipGetLastError());
 }
@@ -463,6 +508,34 @@ __global__ void k_find_segments(const uint64_t *__restrict__ out, uint64_t n, co
 
 constexpr int SEG_MAX = 4096;
 
+// One wave per listed segment of at most 64 keys: bitonic sort across the
+// lanes (one key per lane, padding keys sort last).
+constexpr int SEGW_WAVES = 4;
+__global__ __launch_bounds__(SEGW_WAVES * WAVE) void k_segsort_wave(uint64_t *__restrict__ data,
+                                                                   const uint64_t *__restrict__ seg,
+                                                                   const uint32_t *__restrict__ which, uint32_t nw) {
+    const uint32_t w = blockIdx.x * SEGW_WAVES + (threadIdx.x >> 6);
+    if (w >= nw) return;
+    const int lane = threadIdx.x & (WAVE - 1);
+    const uint32_t q = which[w];
+    const uint64_t start = seg[2 * q], len = seg[2 * q + 1];
+    uint64_t x = (uint64_t)lane < len ? data[start + lane] : ~0ull;
+#pragma unroll
+    for (int k = 2; k <= WAVE; k <<= 1) {
+#pragma unroll
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            const uint64_t y = ((uint64_t)(uint32_t)__shfl_xor((int)(uint32_t)(x >> 32), j, WAVE) << 32) |
+                               (uint32_t)__shfl_xor((int)(uint32_t)x, j, WAVE);
+            // the lower lane of the pair keeps the smaller key in an ascending
+            // block (bit k of the lane clear), the larger one otherwise
+            const bool lower = (lane & j) == 0, asc = (lane & k) == 0;
+            const uint64_t lo = x < y ? x : y, hi = x < y ? y : x;
+            x = (lower == asc) ? lo : hi;
+        }
+    }
+    if ((uint64_t)lane < len) data[start + lane] = x;
+}
+
 // One block per listed segment (length <= SEG_MAX): bitonic sort in LDS.
 __global__ __launch_bounds__(256) void k_segsort(uint64_t *__restrict__ data, const uint64_t *__restrict__ seg,
                                                  const uint32_t *__restrict__ which) {
@@ -507,9 +580,50 @@ void group_head_flags(Ctx *ctx, const uint64_t *k, uint64_t n, uint8_t *flags) {
     XH_CHECK_HIP(hipGetLastError());
 }
 
+// Per row of keys sorted by their high word: head[i] = first row of a run
+// of >= 2 rows with equal high words, member[i] = row of such a run,
+// gsel[i] = -2 for members and -1 otherwise (heads are set later).
+__global__ void k_group_marks(const uint64_t *__restrict__ k, uint64_t n, uint8_t *__restrict__ head,
+                              uint8_t *__restrict__ member, int32_t *__restrict__ gsel) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const uint32_t h = (uint32_t)(k[i] >> 32);
+        const bool next_same = i + 1 < n && (uint32_t)(k[i + 1] >> 32) == h;
+        const bool prev_same = i > 0 && (uint32_t)(k[i - 1] >> 32) == h;
+        head[i] = next_same && !prev_same;
+        member[i] = next_same || prev_same;
+        gsel[i] = (next_same || prev_same) ? -2 : -1;
+    }
+}
+__global__ void k_group_heads_sel(const uint64_t *__restrict__ pos, uint64_t nh, int32_t *__restrict__ gsel) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t g = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; g < nh; g += stride) gsel[pos[g]] = (int32_t)g;
+}
+
+void group_marks(Ctx *ctx, const uint64_t *k, uint64_t n, uint8_t *head, uint8_t *member, int32_t *gsel) {
+    if (!n) return;
+    hipLaunchKernelGGL(k_group_marks, dim3(grid_for(n, 256, 16384)), dim3(256), 0, ctx->stream, k, n, head, member,
+                       gsel);
+    XH_CHECK_HIP(hipGetLastError());
+}
+void group_heads_select(Ctx *ctx, const uint64_t *head_pos, uint64_t nh, int32_t *gsel) {
+    if (!nh) return;
+    XH_REQUIRE(nh < (1ull << 31), XLOG_HIP_CAPACITY_OVERFLOW, "join: too many row groups");
+    hipLaunchKernelGGL(k_group_heads_sel, dim3(grid_for(nh, 256, 16384)), dim3(256), 0, ctx->stream, head_pos, nh,
+                       gsel);
+    XH_CHECK_HIP(hipGetLastError());
+}
+void group_segments(Ctx *ctx, const uint64_t *sorted, uint64_t n, const uint64_t *head_keys, uint64_t nh,
+                    uint64_t *seg) {
+    if (!nh) return;
+    hipLaunchKernelGGL(k_find_segments, dim3(grid_for(nh, 256, 16384)), dim3(256), 0, ctx->stream, sorted, n,
+                       head_keys, nh, seg);
+    XH_CHECK_HIP(hipGetLastError());
+}
+
 // Sorts the runs of equal high word named by heads[0..nh) inside sorted-by-
-// high-word data[0..n).  Runs up to SEG_MAX keys are sorted in LDS, longer
-// ones by the radix sort on the slice.
+// high-word data[0..n).  Runs of up to one wave are sorted in registers, up
+// to SEG_MAX keys in LDS, longer ones by the radix sort on the slice.
 void sort_segments(Ctx *ctx, uint64_t *data, uint64_t n, const uint64_t *heads, uint64_t nh) {
     if (!nh || !n) return;
     Buf<uint64_t> seg(ctx, 2 * nh);
@@ -519,14 +633,26 @@ void sort_segments(Ctx *ctx, uint64_t *data, uint64_t n, const uint64_t *heads, 
     std::vector<uint64_t> h(2 * nh);
     XH_CHECK_HIP(hipMemcpyAsync(h.data(), seg.p, 2 * nh * sizeof(uint64_t), hipMemcpyDeviceToHost, ctx->stream));
     ctx->sync();
-    std::vector<uint32_t> small;
+    std::vector<uint32_t> tiny, small;
     std::vector<uint64_t> large;
-    small.reserve(nh);
+    tiny.reserve(nh);
     for (uint64_t i = 0; i < nh; ++i) {
         uint64_t len = h[2 * i + 1];
         if (len < 2) continue;
-        if (len <= (uint64_t)SEG_MAX) small.push_back((uint32_t)i);
+        if (len <= (uint64_t)WAVE) tiny.push_back((uint32_t)i);
+        else if (len <= (uint64_t)SEG_MAX) small.push_back((uint32_t)i);
         else large.push_back(i);
+    }
+    if (!tiny.empty()) {
+        XH_REQUIRE(tiny.size() < (1ull << 32), XLOG_HIP_CAPACITY_OVERFLOW, "segment sort: too many segments");
+        Buf<uint32_t> which(ctx, tiny.size());
+        XH_CHECK_HIP(hipMemcpyAsync(which.p, tiny.data(), tiny.size() * sizeof(uint32_t), hipMemcpyHostToDevice,
+                                    ctx->stream));
+        const uint32_t nw = (uint32_t)tiny.size();
+        hipLaunchKernelGGL(k_segsort_wave, dim3((nw + SEGW_WAVES - 1) / SEGW_WAVES), dim3(SEGW_WAVES * WAVE), 0,
+                           ctx->stream, data, seg.p, which.p, nw);
+        XH_CHECK_HIP(hipGetLastError());
+        ctx->sync();  // `tiny` is pageable host memory: keep it alive until the copy has run
     }
     if (!small.empty()) {
         Buf<uint32_t> which(ctx, small.size());
