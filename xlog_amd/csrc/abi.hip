@@ -806,8 +806,8 @@ static xlog_hip_rel *op_fj_delta(Ctx *ctx, const xlog_hip_rel *delta, const xlog
 // join -> sort -> unique path.
 void left_keys(Ctx *ctx, const uint64_t *l, uint64_t n, int arity, int oc0, int jk, uint64_t *out);
 void sort_segments(Ctx *ctx, uint64_t *data, uint64_t n, const uint64_t *heads, uint64_t nh);
-void group_marks(Ctx *ctx, const uint64_t *k, uint64_t n, uint8_t *head, uint8_t *member, int32_t *gsel);
-void group_heads_select(Ctx *ctx, const uint64_t *head_pos, uint64_t nh, int32_t *gsel);
+uint64_t group_rows(Ctx *ctx, const uint64_t *k, uint64_t n, int32_t *gsel, uint64_t *mkeys, uint64_t *hkeys,
+                    uint64_t *nh);
 void group_segments(Ctx *ctx, const uint64_t *sorted, uint64_t n, const uint64_t *head_keys, uint64_t nh,
                     uint64_t *seg);
 
@@ -850,22 +850,13 @@ static xlog_hip_rel *op_join_project_dedup(Ctx *ctx, const xlog_hip_rel *l, cons
     //    output twice and interleave: their outputs are produced on the side
     //    (probe, sort inside each group, unique) and copied into place by the
     //    main emit through the group selector
-    Buf<uint8_t> head(ctx, n), member(ctx, n);
     Buf<int32_t> gsel(ctx, n);
-    group_marks(ctx, lkeys, n, head.p, member.p, gsel.p);
-    Buf<uint64_t> cnt(ctx, 2);
-    Buf<uint64_t> mkeys(ctx, n);
-    select_flags(ctx, lkeys, member.p, n, mkeys.p, cnt.p);
-    const uint64_t nm = read_count(ctx, cnt.p);
+    Buf<uint64_t> mkeys(ctx, n), hkeys(ctx, n);
+    uint64_t nh = 0;
+    const uint64_t nm = group_rows(ctx, lkeys, n, gsel.p, mkeys.p, hkeys.p, &nh);
     const int oc[4] = {0, 3, 0, 0};  // v0 = out column (probe high word), v3 = payload
     Buf<uint64_t> gseg, gsrc_buf;
     if (nm) {
-        Buf<uint64_t> hkeys(ctx, n), hpos(ctx, n), iota(ctx, n);
-        LAUNCH_1D(k_iota64, n, iota.p, n);
-        select_flags(ctx, lkeys, head.p, n, hkeys.p, cnt.p);
-        select_flags(ctx, iota.p, head.p, n, hpos.p, cnt.p + 1);
-        ctx->read_scalars(cnt.p, 2);
-        const uint64_t nh = ctx->host_scalars[0];
         uint64_t *bag = nullptr;
         const uint64_t m2 = join_probe_general(ctx, mkeys.p, nm, 1, J.ix, J.payload.p, 2, oc, &bag, nullptr);
         uint64_t *u2 = nullptr, nu2 = 0;
@@ -887,7 +878,6 @@ static xlog_hip_rel *op_join_project_dedup(Ctx *ctx, const xlog_hip_rel *l, cons
         } else {
             fill_u64(ctx, gseg.p, 0ull, 2 * nh);
         }
-        group_heads_select(ctx, hpos.p, nh, gsel.p);
     }
     // 4. the main probe: count, scan, emit into the final buffer
     ProbeJob job;

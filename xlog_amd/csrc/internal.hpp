@@ -238,12 +238,10 @@ void select_flags(Ctx *ctx, const uint64_t *k, const uint8_t *flags, uint64_t n,
 void merge_sorted(Ctx *ctx, const uint64_t *a, uint64_t na, const uint64_t *b, uint64_t nb, uint64_t *out);
 
 // Sorted-run index over the high word of sorted packed keys (join build):
-// run_key[r], run_start[r] (run_start[nruns] = n) and an open-addressing
-// hash table mapping key -> run.
+// an open-addressing hash table of 16-byte slots mapping key -> (run start,
+// run length) in the sorted keys.
 struct RunIndex {
-    Buf<uint32_t> run_key;
-    Buf<uint64_t> run_start;
-    Buf<unsigned long long> table;  // (key << 32) | (run + 1), 0 = empty
+    Buf<unsigned long long> table;  // per slot: (key << 32) | run length (0 = empty), run start
     uint64_t nruns = 0;
     uint64_t table_mask = 0;
 };
@@ -309,6 +307,13 @@ inline unsigned grid_for(uint64_t n, unsigned block, unsigned cap) {
 void fill_u32(Ctx *ctx, uint32_t *p, uint32_t v, uint64_t n);
 void select_runs(Ctx *ctx, const uint64_t *k, uint64_t n, uint32_t *run_key, uint64_t *run_start,
                  uint64_t *d_count);
+// Keys sorted by their high word: rows sharing it with a neighbour (key,
+// position), then among those the group heads (key; gsel[position] = group
+// number).
+void select_group_members(Ctx *ctx, const uint64_t *k, uint64_t n, uint64_t *mkeys, uint64_t *mpos,
+                          uint64_t *d_count);
+void select_group_heads(Ctx *ctx, const uint64_t *mkeys, uint64_t nm, const uint64_t *mpos, uint64_t *hkeys,
+                        int32_t *gsel, uint64_t *d_count);
 void sort_state_release(Ctx *ctx);
 void select_state_release(Ctx *ctx);
 void fill_u64(Ctx *ctx, uint64_t *p, uint64_t v, uint64_t n);

@@ -7,10 +7,11 @@
 //   build  - the build side arrives sorted by its key word (the high word of
 //            the packed row), so every distinct key is one contiguous run.
 //            One selection pass extracts (run key, run start); an
-//            open-addressing table in HBM (8-byte slots, linear probing,
-//            Fibonacci hashing, load <= 0.5) maps key -> run.  Keys are
-//            compared exactly, so colliding hashes cannot produce matches
-//            (join_collision_test.rs:19-194).
+//            open-addressing table in HBM (16-byte slots holding key, run
+//            length and run start, linear probing, Fibonacci hashing,
+//            load <= 0.5) maps key -> run, so a probe row reads one slot and
+//            then its run.  Keys are compared exactly, so colliding hashes
+//            cannot produce matches (join_collision_test.rs:19-194).
 //   probe  - two launches.  count: every probe row looks up its run and a
 //            tile total is written.  emit: after a scan of the tile totals,
 //            each wave expands its 64 rows' runs cooperatively: lane j of a
@@ -40,16 +41,27 @@ __device__ __forceinline__ uint64_t hash_slot(uint32_t key, int bits) {
     return (uint64_t)(((uint64_t)key * 0x9E3779B97F4A7C15ull) >> (64 - bits));
 }
 
-__global__ void k_insert(const uint32_t *__restrict__ run_key, uint64_t nruns, unsigned long long *table,
-                         uint64_t mask, int bits) {
+// Slot h = table[2h .. 2h+1]: (key << 32) | run length (0 = empty slot; a
+// run is never empty), then the run start.
+typedef unsigned long long u64x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ u64x2 load_slot(const unsigned long long *table, uint64_t h) {
+    return *reinterpret_cast<const u64x2 *>(table + 2 * h);
+}
+
+__global__ void k_insert(const uint32_t *__restrict__ run_key, const uint64_t *__restrict__ run_start, uint64_t nruns,
+                         unsigned long long *table, uint64_t mask, int bits) {
     uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
     for (uint64_t r = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; r < nruns; r += stride) {
-        uint32_t key = run_key[r];
-        unsigned long long v = ((unsigned long long)key << 32) | (unsigned long long)(r + 1);
+        const uint32_t key = run_key[r];
+        const uint64_t st = run_start[r], len = run_start[r + 1] - st;
+        const unsigned long long v = ((unsigned long long)key << 32) | (unsigned long long)len;
         uint64_t h = hash_slot(key, bits);
         for (;;) {
-            unsigned long long old = atomicCAS(&table[h], 0ull, v);
-            if (old == 0ull) break;
+            unsigned long long old = atomicCAS(&table[2 * h], 0ull, v);
+            if (old == 0ull) {
+                table[2 * h + 1] = st;  // read only by later launches
+                break;
+            }
             h = (h + 1) & mask;
         }
     }
@@ -58,13 +70,14 @@ __global__ void k_insert(const uint32_t *__restrict__ run_key, uint64_t nruns, u
 __global__ void k_set_u64(uint64_t *p, uint64_t v) { *p = v; }
 
 __device__ __forceinline__ bool lookup_run(const unsigned long long *__restrict__ table, uint64_t mask, int bits,
-                                           uint32_t key, uint32_t *run) {
+                                           uint32_t key, uint64_t *start, uint32_t *len) {
     uint64_t h = hash_slot(key, bits);
     for (;;) {
-        unsigned long long s = table[h];
-        if (s == 0ull) return false;
-        if ((uint32_t)(s >> 32) == key) {
-            *run = (uint32_t)s - 1u;
+        const u64x2 s = load_slot(table, h);
+        if (s.x == 0ull) return false;
+        if ((uint32_t)(s.x >> 32) == key) {
+            *start = s.y;
+            *len = (uint32_t)s.x;
             return true;
         }
         h = (h + 1) & mask;
@@ -75,10 +88,9 @@ struct ProbeArgs {
     const uint64_t *probe;
     uint64_t n;
     int pcol;  // 0: key = high word of the probe row, 1: low word
-    const unsigned long long *table;
+    const unsigned long long *table;  // 16-byte slots (load_slot)
     uint64_t mask;
     int bits;
-    const uint64_t *run_start;
     const uint32_t *payload;
     // optional row groups (see ProbeJob): gsel[i] = -1 plain row, -2 row
     // without output, g >= 0 row whose outputs are gsrc[gseg[2g] ..
@@ -90,67 +102,47 @@ struct ProbeArgs {
 // set in a row's start when its outputs come from gsrc
 constexpr uint64_t GROUP_BIT = 1ull << 63;
 
-__device__ __forceinline__ uint64_t probe_count(const ProbeArgs &a, uint64_t row, uint64_t *start) {
-    uint32_t key = a.pcol ? (uint32_t)row : (uint32_t)(row >> 32);
-    uint32_t run;
-    if (!lookup_run(a.table, a.mask, a.bits, key, &run)) {
-        *start = 0;
-        return 0;
-    }
-    uint64_t s = a.run_start[run];
-    *start = s;
-    return a.run_start[run + 1] - s;
-}
-
 // Lookups of N probe rows with their memory latencies overlapped: all first
-// slots are loaded together, the rare collision chains are walked after, then
-// all run bounds are loaded together.  cnt[i] = 0 for rows with idx >= n.
+// slots (and group selectors) are loaded together, the rare collision chains
+// are walked after.  cnt[i] = 0 for rows with idx >= n.
 template <int N>
 __device__ __forceinline__ void lookup_batch(const ProbeArgs &a, const uint64_t *rows, uint64_t wbase, int lane,
                                              uint64_t *start, uint32_t *cnt) {
-    unsigned long long slot[N];
-    uint64_t h[N];
-    uint32_t key[N];
+    // chunks of at most 8 rows keep the in-flight 16-byte slots within the
+    // register budget of 4 waves per SIMD
+    constexpr int C = N < 8 ? N : 8;
+    static_assert(N % C == 0, "lookup chunking");
 #pragma unroll
-    for (int r = 0; r < N; ++r) {
-        key[r] = a.pcol ? (uint32_t)rows[r] : (uint32_t)(rows[r] >> 32);
-        h[r] = hash_slot(key[r], a.bits);
-        bool valid = wbase + (uint64_t)r * WAVE + lane < a.n;
-        slot[r] = valid ? a.table[h[r]] : 0ull;
-    }
-    uint32_t run[N];
+    for (int c0 = 0; c0 < N; c0 += C) {
+        u64x2 slot[C];
+        int32_t g[C];
 #pragma unroll
-    for (int r = 0; r < N; ++r) {
-        unsigned long long s = slot[r];
-        uint64_t hh = h[r];
-        while (s != 0ull && (uint32_t)(s >> 32) != key[r]) {
-            hh = (hh + 1) & a.mask;
-            s = a.table[hh];
+        for (int q = 0; q < C; ++q) {
+            const int r = c0 + q;
+            const uint32_t key = a.pcol ? (uint32_t)rows[r] : (uint32_t)(rows[r] >> 32);
+            const uint64_t idx = wbase + (uint64_t)r * WAVE + lane;
+            const bool valid = idx < a.n;
+            slot[q] = valid ? load_slot(a.table, hash_slot(key, a.bits)) : u64x2{0ull, 0ull};
+            g[q] = (a.gsel && valid) ? a.gsel[idx] : -1;
         }
-        run[r] = s ? (uint32_t)s - 1u : 0xFFFFFFFFu;
-    }
-    uint64_t b[N], e[N];
-    int32_t g[N];
 #pragma unroll
-    for (int r = 0; r < N; ++r) {
-        b[r] = run[r] != 0xFFFFFFFFu ? a.run_start[run[r]] : 0ull;
-        e[r] = run[r] != 0xFFFFFFFFu ? a.run_start[run[r] + 1] : 0ull;
-        // group selectors travel with the run bounds (no extra round trip)
-        const uint64_t idx = wbase + (uint64_t)r * WAVE + lane;
-        g[r] = (a.gsel && idx < a.n) ? a.gsel[idx] : -1;
-    }
-#pragma unroll
-    for (int r = 0; r < N; ++r) {
-        start[r] = b[r];
-        cnt[r] = (uint32_t)(e[r] - b[r]);
-    }
-    if (a.gsel) {
-#pragma unroll
-        for (int r = 0; r < N; ++r) {
-            if (g[r] == -2) cnt[r] = 0;
-            if (g[r] >= 0) {
-                start[r] = a.gseg[2 * g[r]] | GROUP_BIT;
-                cnt[r] = (uint32_t)a.gseg[2 * g[r] + 1];
+        for (int q = 0; q < C; ++q) {
+            const int r = c0 + q;
+            const uint32_t key = a.pcol ? (uint32_t)rows[r] : (uint32_t)(rows[r] >> 32);
+            u64x2 s = slot[q];
+            if (s.x != 0ull && (uint32_t)(s.x >> 32) != key) {  // rare: walk the collision chain
+                uint64_t hh = hash_slot(key, a.bits);
+                do {
+                    hh = (hh + 1) & a.mask;
+                    s = load_slot(a.table, hh);
+                } while (s.x != 0ull && (uint32_t)(s.x >> 32) != key);
+            }
+            start[r] = s.x ? s.y : 0ull;
+            cnt[r] = (uint32_t)s.x;  // 0 when the key has no run (empty slot)
+            if (g[q] == -2) cnt[r] = 0;
+            if (g[q] >= 0) {
+                start[r] = a.gseg[2 * g[q]] | GROUP_BIT;
+                cnt[r] = (uint32_t)a.gseg[2 * g[q] + 1];
             }
         }
     }
@@ -321,8 +313,9 @@ __global__ void k_match_flags(ProbeArgs a, int want, uint8_t *__restrict__ flags
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.n; i += stride) {
         uint64_t row = a.probe[i];
         uint32_t key = a.pcol ? (uint32_t)row : (uint32_t)(row >> 32);
-        uint32_t run;
-        bool hit = lookup_run(a.table, a.mask, a.bits, key, &run);
+        uint64_t st;
+        uint32_t len;
+        bool hit = lookup_run(a.table, a.mask, a.bits, key, &st, &len);
         flags[i] = (uint8_t)(hit == (want != 0));
     }
 }
@@ -330,24 +323,25 @@ __global__ void k_match_flags(ProbeArgs a, int want, uint8_t *__restrict__ flags
 }  // namespace
 
 void build_run_index(Ctx *ctx, const uint64_t *sorted_keys, uint64_t n, RunIndex &ix) {
-    ix.run_key = Buf<uint32_t>(ctx, n ? n : 1);
-    ix.run_start = Buf<uint64_t>(ctx, n + 1);
+    XH_REQUIRE(n < (1ull << 32), XLOG_HIP_CAPACITY_OVERFLOW, "join build: more than 2^32 - 1 rows");
+    Buf<uint32_t> run_key(ctx, n ? n : 1);
+    Buf<uint64_t> run_start(ctx, n + 1);
     Buf<uint64_t> cnt(ctx, 1);
-    select_runs(ctx, sorted_keys, n, ix.run_key.p, ix.run_start.p, cnt.p);
+    select_runs(ctx, sorted_keys, n, run_key.p, run_start.p, cnt.p);
     ctx->read_scalars(cnt.p, 1);
     ix.nruns = ctx->host_scalars[0];
     XH_REQUIRE(ix.nruns < 0xFFFFFFFFull, XLOG_HIP_CAPACITY_OVERFLOW, "join build: too many distinct keys");
-    hipLaunchKernelGGL(k_set_u64, dim3(1), dim3(1), 0, ctx->stream, ix.run_start.p + ix.nruns, n);
+    hipLaunchKernelGGL(k_set_u64, dim3(1), dim3(1), 0, ctx->stream, run_start.p + ix.nruns, n);
     XH_CHECK_HIP(hipGetLastError());
     int bits = 10;
     while ((1ull << bits) < 2 * ix.nruns) ++bits;
     uint64_t slots = 1ull << bits;
-    ix.table = Buf<unsigned long long>(ctx, slots);
+    ix.table = Buf<unsigned long long>(ctx, 2 * slots);
     ix.table_mask = slots - 1;
-    fill_u64(ctx, reinterpret_cast<uint64_t *>(ix.table.p), 0ull, slots);
+    fill_u64(ctx, reinterpret_cast<uint64_t *>(ix.table.p), 0ull, 2 * slots);
     if (ix.nruns)
-        hipLaunchKernelGGL(k_insert, dim3(grid_for(ix.nruns, 256, 16384)), dim3(256), 0, ctx->stream, ix.run_key.p,
-                           ix.nruns, ix.table.p, ix.table_mask, bits);
+        hipLaunchKernelGGL(k_insert, dim3(grid_for(ix.nruns, 256, 16384)), dim3(256), 0, ctx->stream, run_key.p,
+                           run_start.p, ix.nruns, ix.table.p, ix.table_mask, bits);
     XH_CHECK_HIP(hipGetLastError());
 }
 
@@ -359,8 +353,8 @@ static int table_bits(const RunIndex &ix) {
 
 static ProbeArgs probe_args(const ProbeJob &job) {
     const RunIndex &ix = *job.ix;
-    return ProbeArgs{job.probe, job.n, job.pcol, ix.table.p, ix.table_mask, table_bits(ix), ix.run_start.p,
-                     job.payload, job.gsel, job.gseg, job.gsrc};
+    return ProbeArgs{job.probe, job.n, job.pcol, ix.table.p, ix.table_mask, table_bits(ix), job.payload, job.gsel,
+                     job.gseg, job.gsrc};
 }
 
 uint64_t probe_prepare(Ctx *ctx, ProbeJob &job) {
@@ -448,8 +442,7 @@ uint64_t join_probe_project(Ctx *ctx, const uint64_t *probe, uint64_t n, int pco
 void join_match_flags(Ctx *ctx, const uint64_t *probe, uint64_t n, int pcol, const RunIndex &ix, int want,
                       uint8_t *flags) {
     if (n == 0) return;
-    ProbeArgs a{probe, n, pcol, ix.table.p, ix.table_mask, table_bits(ix), ix.run_start.p, nullptr,
-                nullptr, nullptr, nullptr};
+    ProbeArgs a{probe, n, pcol, ix.table.p, ix.table_mask, table_bits(ix), nullptr, nullptr, nullptr, nullptr};
     hipLaunchKernelGGL(k_match_flags, dim3(grid_for(n, 256, 16384)), dim3(256), 0, ctx->stream, a, want, flags);
     XH_CHECK_HIP(hipGetLastError());
 }
@@ -580,38 +573,32 @@ void group_head_flags(Ctx *ctx, const uint64_t *k, uint64_t n, uint8_t *flags) {
     XH_CHECK_HIP(hipGetLastError());
 }
 
-// Per row of keys sorted by their high word: head[i] = first row of a run
-// of >= 2 rows with equal high words, member[i] = row of such a run,
-// gsel[i] = -2 for members and -1 otherwise (heads are set later).
-__global__ void k_group_marks(const uint64_t *__restrict__ k, uint64_t n, uint8_t *__restrict__ head,
-                              uint8_t *__restrict__ member, int32_t *__restrict__ gsel) {
+__global__ void k_mark_members(const uint64_t *__restrict__ pos, uint64_t nm, int32_t *__restrict__ gsel) {
     uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
-        const uint32_t h = (uint32_t)(k[i] >> 32);
-        const bool next_same = i + 1 < n && (uint32_t)(k[i + 1] >> 32) == h;
-        const bool prev_same = i > 0 && (uint32_t)(k[i - 1] >> 32) == h;
-        head[i] = next_same && !prev_same;
-        member[i] = next_same || prev_same;
-        gsel[i] = (next_same || prev_same) ? -2 : -1;
-    }
-}
-__global__ void k_group_heads_sel(const uint64_t *__restrict__ pos, uint64_t nh, int32_t *__restrict__ gsel) {
-    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-    for (uint64_t g = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; g < nh; g += stride) gsel[pos[g]] = (int32_t)g;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nm; i += stride) gsel[pos[i]] = -2;
 }
 
-void group_marks(Ctx *ctx, const uint64_t *k, uint64_t n, uint8_t *head, uint8_t *member, int32_t *gsel) {
-    if (!n) return;
-    hipLaunchKernelGGL(k_group_marks, dim3(grid_for(n, 256, 16384)), dim3(256), 0, ctx->stream, k, n, head, member,
-                       gsel);
+// Row groups of probe keys sorted by their high word (the out column): rows
+// that share it with a neighbour.  gsel[n] receives -1 for lone rows, -2 for
+// group members and, at each group's first row, the group number; mkeys /
+// hkeys (n entries each) receive the members' and the heads' keys.  Returns
+// the member count; *nh the group count.
+uint64_t group_rows(Ctx *ctx, const uint64_t *k, uint64_t n, int32_t *gsel, uint64_t *mkeys, uint64_t *hkeys,
+                    uint64_t *nh) {
+    *nh = 0;
+    if (!n) return 0;
+    fill_u32(ctx, reinterpret_cast<uint32_t *>(gsel), 0xFFFFFFFFu, n);
+    Buf<uint64_t> mpos(ctx, n), cnt(ctx, 1);
+    select_group_members(ctx, k, n, mkeys, mpos.p, cnt.p);
+    ctx->read_scalars(cnt.p, 1);
+    const uint64_t nm = ctx->host_scalars[0];
+    if (!nm) return 0;
+    hipLaunchKernelGGL(k_mark_members, dim3(grid_for(nm, 256, 16384)), dim3(256), 0, ctx->stream, mpos.p, nm, gsel);
     XH_CHECK_HIP(hipGetLastError());
-}
-void group_heads_select(Ctx *ctx, const uint64_t *head_pos, uint64_t nh, int32_t *gsel) {
-    if (!nh) return;
-    XH_REQUIRE(nh < (1ull << 31), XLOG_HIP_CAPACITY_OVERFLOW, "join: too many row groups");
-    hipLaunchKernelGGL(k_group_heads_sel, dim3(grid_for(nh, 256, 16384)), dim3(256), 0, ctx->stream, head_pos, nh,
-                       gsel);
-    XH_CHECK_HIP(hipGetLastError());
+    select_group_heads(ctx, mkeys, nm, mpos.p, hkeys, gsel, cnt.p);
+    ctx->read_scalars(cnt.p, 1);
+    *nh = ctx->host_scalars[0];
+    return nm;
 }
 void group_segments(Ctx *ctx, const uint64_t *sorted, uint64_t n, const uint64_t *head_keys, uint64_t nh,
                     uint64_t *seg) {

@@ -206,6 +206,38 @@ struct SelFlags {
 };
 
 // run starts of the high word (join build)
+// Rows of keys sorted by their high word that share it with a neighbour
+// (groups of >= 2 rows): key and position.
+struct SelGroupMembers {
+    const uint64_t *in;
+    uint64_t n;
+    uint64_t *out_key, *out_pos;
+    __device__ void setup(uint64_t, uint64_t, uint64_t *) const {}
+    __device__ bool flag(uint64_t idx, uint64_t key, uint64_t prev, const uint64_t *) const {
+        const uint32_t h = (uint32_t)(key >> 32);
+        return (idx > 0 && (uint32_t)(prev >> 32) == h) || (idx + 1 < n && (uint32_t)(in[idx + 1] >> 32) == h);
+    }
+    __device__ void emit(uint64_t pos, uint64_t idx, uint64_t key) const {
+        out_key[pos] = key;
+        out_pos[pos] = idx;
+    }
+};
+// Group heads among the member rows above: the head key and, at the head's
+// original row, its group number in the row-group selector.
+struct SelGroupHeads {
+    const uint64_t *mpos;
+    uint64_t *out_key;
+    int32_t *gsel;
+    __device__ void setup(uint64_t, uint64_t, uint64_t *) const {}
+    __device__ bool flag(uint64_t idx, uint64_t key, uint64_t prev, const uint64_t *) const {
+        return idx == 0 || (uint32_t)(prev >> 32) != (uint32_t)(key >> 32);
+    }
+    __device__ void emit(uint64_t pos, uint64_t idx, uint64_t key) const {
+        out_key[pos] = key;
+        gsel[mpos[idx]] = (int32_t)pos;
+    }
+};
+
 struct SelRuns {
     const uint64_t *in;
     uint32_t *run_key;
@@ -369,6 +401,15 @@ void select_unique_diff(Ctx *ctx, const uint64_t *k, uint64_t n, const uint64_t 
 }
 void select_flags(Ctx *ctx, const uint64_t *k, const uint8_t *flags, uint64_t n, uint64_t *out, uint64_t *d_count) {
     run_select(ctx, k, n, SelFlags{flags, out}, d_count);
+}
+void select_group_members(Ctx *ctx, const uint64_t *k, uint64_t n, uint64_t *mkeys, uint64_t *mpos,
+                          uint64_t *d_count) {
+    run_select(ctx, k, n, SelGroupMembers{k, n, mkeys, mpos}, d_count);
+}
+void select_group_heads(Ctx *ctx, const uint64_t *mkeys, uint64_t nm, const uint64_t *mpos, uint64_t *hkeys,
+                        int32_t *gsel, uint64_t *d_count) {
+    XH_REQUIRE(nm < (1ull << 31), XLOG_HIP_CAPACITY_OVERFLOW, "join: too many grouped probe rows");
+    run_select(ctx, mkeys, nm, SelGroupHeads{mpos, hkeys, gsel}, d_count);
 }
 void select_runs(Ctx *ctx, const uint64_t *k, uint64_t n, uint32_t *run_key, uint64_t *run_start, uint64_t *d_count) {
     run_select(ctx, k, n, SelRuns{k, run_key, run_start}, d_count);
