@@ -29,11 +29,19 @@ namespace xh {
 namespace {
 
 constexpr int JB = 256;      // block
-// probe rows per thread: JITEMS for large probes, JITEMS_SMALL (more,
-// smaller tiles) when fewer rows than JSMALL_ROWS leave the GPU under-filled
-constexpr int JITEMS = 16;
-constexpr int JITEMS_SMALL = 2;
-constexpr uint64_t JSMALL_ROWS = 4ull << 20;
+// Probe rows per thread (a tile is JB * JITEMS rows) and outputs per lane
+// per expansion step of the emit.  Measured on MI355X over the C2 join
+// (2^24 probe rows, 2.7e8 outputs): (rows, unroll) = (2, 4) 1.01 ms per emit,
+// (4, 4) 1.03, (8, 4) 1.14, (16, 1) 1.42 -- small tiles with several payload
+// loads in flight per lane beat deep per-thread lookup batches.
+#ifndef XH_JITEMS
+#define XH_JITEMS 2
+#endif
+#ifndef XH_EMIT_UNROLL
+#define XH_EMIT_UNROLL 4
+#endif
+constexpr int JITEMS = XH_JITEMS;
+constexpr int EMIT_UNROLL = XH_EMIT_UNROLL;
 constexpr int JWAVES = JB / WAVE;
 constexpr uint64_t tile_rows(int items) { return (uint64_t)JB * items; }
 
@@ -277,29 +285,47 @@ __global__ __launch_bounds__(JB) void k_probe_emit(ProbeArgs a, const uint64_t *
         s_st[wave][lane] = st;
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        for (uint64_t j = lane; j < total; j += WAVE) {
-            // largest s with ex[s] <= j
-            int lo = 0, hi = WAVE - 1;
-            while (lo < hi) {
-                int mid = (lo + hi + 1) >> 1;
-                if (s_ex[wave][mid] <= j) lo = mid; else hi = mid - 1;
+        // EMIT_UNROLL outputs per lane per step, so that their payload loads
+        // are in flight together
+        for (uint64_t j0 = lane; j0 < total; j0 += EMIT_UNROLL * WAVE) {
+            uint64_t prow[EMIT_UNROLL], bpos[EMIT_UNROLL];
+            uint32_t pay[EMIT_UNROLL];
+            uint64_t gw[EMIT_UNROLL];
+#pragma unroll
+            for (int u = 0; u < EMIT_UNROLL; ++u) {
+                const uint64_t j = j0 + (uint64_t)u * WAVE;
+                // largest s with ex[s] <= j
+                int lo = 0, hi = WAVE - 1;
+                while (lo < hi) {
+                    int mid = (lo + hi + 1) >> 1;
+                    if (s_ex[wave][mid] <= j) lo = mid; else hi = mid - 1;
+                }
+                prow[u] = s_row[wave][lo];
+                bpos[u] = s_st[wave][lo] + (j - s_ex[wave][lo]);
+                const bool live = j < total;
+                const bool grp = (bpos[u] & GROUP_BIT) != 0;
+                pay[u] = (live && !grp && a.payload) ? a.payload[bpos[u]] : 0u;
+                gw[u] = (live && grp) ? a.gsrc[bpos[u] & ~GROUP_BIT] : 0ull;
             }
-            uint64_t prow = s_row[wave][lo];
-            uint64_t bpos = s_st[wave][lo] + (j - s_ex[wave][lo]);
-            uint64_t w0, w1;
-            if (bpos & GROUP_BIT) {
-                w0 = a.gsrc[bpos & ~GROUP_BIT];
-                w1 = 0;
-            } else {
-                uint32_t v[4];
-                v[0] = (uint32_t)(prow >> 32);
-                v[1] = (uint32_t)prow;
-                v[2] = a.pcol ? (uint32_t)prow : (uint32_t)(prow >> 32);
-                v[3] = a.payload ? a.payload[bpos] : 0u;
-                make_words(spec, v, &w0, &w1);
+#pragma unroll
+            for (int u = 0; u < EMIT_UNROLL; ++u) {
+                const uint64_t j = j0 + (uint64_t)u * WAVE;
+                if (j >= total) break;
+                uint64_t w0, w1;
+                if (bpos[u] & GROUP_BIT) {
+                    w0 = gw[u];
+                    w1 = 0;
+                } else {
+                    uint32_t v[4];
+                    v[0] = (uint32_t)(prow[u] >> 32);
+                    v[1] = (uint32_t)prow[u];
+                    v[2] = a.pcol ? (uint32_t)prow[u] : (uint32_t)(prow[u] >> 32);
+                    v[3] = pay[u];
+                    make_words(spec, v, &w0, &w1);
+                }
+                out0[base + j] = w0;
+                if (out1) out1[base + j] = w1;
             }
-            out0[base + j] = w0;
-            if (out1) out1[base + j] = w1;
         }
         base += total;
         __builtin_amdgcn_wave_barrier();
@@ -358,7 +384,7 @@ static ProbeArgs probe_args(const ProbeJob &job) {
 }
 
 uint64_t probe_prepare(Ctx *ctx, ProbeJob &job) {
-    job.items = job.n >= JSMALL_ROWS ? JITEMS : JITEMS_SMALL;
+    job.items = JITEMS;
     job.tiles = (job.n + tile_rows(job.items) - 1) / tile_rows(job.items);
     job.total = 0;
     if (job.n == 0 || job.ix->nruns == 0) return 0;
@@ -367,12 +393,8 @@ uint64_t probe_prepare(Ctx *ctx, ProbeJob &job) {
     job.toff = Buf<uint64_t>(ctx, job.tiles + 1);
     {
         Prof prof(ctx, XLOG_HIP_KERNEL_PROBE_COUNT, 8.0 * (double)job.n);
-        if (job.items == JITEMS)
-            hipLaunchKernelGGL(k_probe_count<JITEMS>, dim3((unsigned)job.tiles), dim3(JB), 0, ctx->stream, a,
-                               job.toff.p);
-        else
-            hipLaunchKernelGGL(k_probe_count<JITEMS_SMALL>, dim3((unsigned)job.tiles), dim3(JB), 0, ctx->stream, a,
-                               job.toff.p);
+        hipLaunchKernelGGL(k_probe_count<JITEMS>, dim3((unsigned)job.tiles), dim3(JB), 0, ctx->stream, a,
+                           job.toff.p);
         XH_CHECK_HIP(hipGetLastError());
     }
     hipLaunchKernelGGL(k_scan_small, dim3(1), dim3(1024), 0, ctx->stream, job.toff.p, job.tiles,
@@ -403,12 +425,8 @@ void probe_emit_range(Ctx *ctx, const ProbeJob &job, uint64_t t0, uint64_t t1, u
     // probe row 8 B + slot/run 16 B per probe row; payload 4 B + output 8 B per match
     Prof prof(ctx, XLOG_HIP_KERNEL_PROBE_EMIT,
               24.0 * (double)nprobe + (4.0 + 8.0 * (out_arity > 2 ? 2 : 1)) * (double)rows);
-    if (job.items == JITEMS)
-        hipLaunchKernelGGL(k_probe_emit<JITEMS>, dim3((unsigned)(t1 - t0)), dim3(JB), 0, ctx->stream, a, job.toff.p,
-                           t0, spec, out0, out1);
-    else
-        hipLaunchKernelGGL(k_probe_emit<JITEMS_SMALL>, dim3((unsigned)(t1 - t0)), dim3(JB), 0, ctx->stream, a,
-                           job.toff.p, t0, spec, out0, out1);
+    hipLaunchKernelGGL(k_probe_emit<JITEMS>, dim3((unsigned)(t1 - t0)), dim3(JB), 0, ctx->stream, a, job.toff.p, t0,
+                       spec, out0, out1);
     XH_CHECK_HIP(hipGetLastError());
 }
 
