@@ -5,8 +5,11 @@
 Default workload is BASELINE.json configs[1] (C2): R(a,b) |><| S(b,c) on b,
 2^24 rows each, b Zipf(1.1) over 2^20 keys on the probe side and uniform on the
 build side; project (a,c), sort and dedup.  One step = the whole hot path on
-inputs already resident in HBM: join+project (build index, count, emit),
-radix sort of the ~2^28 outputs, adjacent-compare dedup.
+inputs already resident in HBM, as one fused join+project+dedup call: probe
+keys radix sorted by a, build index over the sorted unique (b,c) rows, count
+and emit of the ~2^28 outputs directly in (a,c) order (rows sharing their a
+value are finished on the side).  `c2u` runs the unfused join -> radix sort ->
+dedup sequence of the same step.
 
 Prints one JSON line.  `value` is input tuples/s (|R| + |S|) / step time, the
 reference's join-throughput definition (docs/guides/benchmarking.mdx:250-253).
@@ -31,8 +34,9 @@ import numpy as np  # noqa: E402
 METRIC = "semi-naive fixpoint wall time + join/sort tuples/s; % of HBM peak, 1 MI355X"
 HBM_PEAK_GBS = 8000.0
 # Measured HBM traffic / algorithmic bytes per launch from the rocprofv3 FETCH_SIZE + WRITE_SIZE runs of
-# profiles/c2_radix_probe_dedup_hbm_traffic.md (FETCH scaled x2, WRITE x1 by the copy calibration there).
-TRAFFIC_RATIO = {"sort_pass": 1.09, "probe_emit": 1.51, "select": 1.01}
+# profiles/c2_radix_probe_dedup_hbm_traffic.md (FETCH scaled x2, WRITE x1 by the copy calibration there):
+# radix pass x1.10 (2^24 keys; x1.09 at 2^28), probe emit x1.08, selections x1.01.
+TRAFFIC_RATIO = {"sort_pass": 1.10, "probe_emit": 1.08, "select": 1.01}
 
 
 def log(msg: str) -> None:
@@ -117,7 +121,9 @@ def make_workload(name: str, p):
         config = {"workload": "copy: column swap of 2^28 packed rows (16 B/row), counter calibration", "rows": n}
         return step, n, "rows", config, None, state
     if name == "c5":
-        cfg = datagen.C5
+        # BASELINE's literal C5 (500,000 variables) grows |pointsTo| like V^2 (~10^10 tuples, past the
+        # reference's u32 row cap): the bench runs the same generator at 10,000 variables / 40,000 facts
+        cfg = dict(datagen.C5, n_vars=10_000, n_facts=40_000)
         f = datagen.andersen(cfg["n_vars"], cfg["n_facts"], cfg["alpha"], datagen.seed_for(5))
         rels = [p.create_buffer_from_u32_columns(list(f[k])) for k in ("assign", "addressOf", "load", "store")]
         state = {}
@@ -128,7 +134,8 @@ def make_workload(name: str, p):
             state["iterations"] = st["iterations"]
             state["delta_sizes"] = st["delta_sizes"]
 
-        config = {"workload": "c5: Andersen points-to, 4 rules", **cfg, "seed": datagen.seed_for(5)}
+        config = {"workload": "c5 scaled: Andersen points-to, 4 rules (literal size infeasible, see DESIGN)", **cfg,
+                  "seed": datagen.seed_for(5)}
         return step, None, "pointsTo tuples", config, f, state
     raise SystemExit(f"unknown workload {name}")
 
@@ -157,6 +164,17 @@ def cpu_baseline(name: str, inputs, budget_s: float = 30.0):
         dt = time.perf_counter() - t
         return {"value": n / dt, "unit": "tuples/s", "cores": 1, "kind": "port",
                 "sample": f"first {n} of {len(keys)} tuples, sort + dedup -> {len(u)} in {dt:.2f}s"}
+    if name == "c5":
+        # the semi-naive oracle on the 5,000-variable instance of the same generator
+        from xlog_amd import andersen_plan, datagen
+        f = datagen.andersen(5000, 20000, 1.5, datagen.seed_for(5))
+        rels = [pack(*f[k]) for k in ("assign", "addressOf", "load", "store")] + [None]
+        t = time.perf_counter()
+        outs, it, _ = oracle.seminaive(andersen_plan(), rels)
+        dt = time.perf_counter() - t
+        return {"value": len(outs[4]) / dt, "unit": "pointsTo tuples/s", "cores": 1, "kind": "port",
+                "sample": f"5,000 variables / 20,000 facts (the bench runs 10,000 / 40,000): "
+                          f"{len(outs[4])} tuples, {it} iterations in {dt:.2f}s"}
     if name in ("c1", "c4"):
         src, dst = inputs
         t = time.perf_counter()

@@ -76,6 +76,13 @@ __global__ void k_insert(const uint32_t *__restrict__ run_key, const uint64_t *_
 }
 
 __global__ void k_set_u64(uint64_t *p, uint64_t v) { *p = v; }
+__global__ void k_max_run_len(const uint64_t *__restrict__ run_start, uint64_t nruns, unsigned long long *mx) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    unsigned long long m = 0;
+    for (uint64_t r = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; r < nruns; r += stride)
+        m = max(m, (unsigned long long)(run_start[r + 1] - run_start[r]));
+    atomicMax(mx, m);
+}
 
 __device__ __forceinline__ bool lookup_run(const unsigned long long *__restrict__ table, uint64_t mask, int bits,
                                            uint32_t key, uint64_t *start, uint32_t *len) {
@@ -349,7 +356,6 @@ __global__ void k_match_flags(ProbeArgs a, int want, uint8_t *__restrict__ flags
 }  // namespace
 
 void build_run_index(Ctx *ctx, const uint64_t *sorted_keys, uint64_t n, RunIndex &ix) {
-    XH_REQUIRE(n < (1ull << 32), XLOG_HIP_CAPACITY_OVERFLOW, "join build: more than 2^32 - 1 rows");
     Buf<uint32_t> run_key(ctx, n ? n : 1);
     Buf<uint64_t> run_start(ctx, n + 1);
     Buf<uint64_t> cnt(ctx, 1);
@@ -358,6 +364,16 @@ void build_run_index(Ctx *ctx, const uint64_t *sorted_keys, uint64_t n, RunIndex
     ix.nruns = ctx->host_scalars[0];
     XH_REQUIRE(ix.nruns < 0xFFFFFFFFull, XLOG_HIP_CAPACITY_OVERFLOW, "join build: too many distinct keys");
     hipLaunchKernelGGL(k_set_u64, dim3(1), dim3(1), 0, ctx->stream, run_start.p + ix.nruns, n);
+    if (n >= (1ull << 32) && ix.nruns) {  // a slot holds a 32-bit run length
+        Buf<unsigned long long> mx(ctx, 1);
+        fill_u64(ctx, reinterpret_cast<uint64_t *>(mx.p), 0ull, 1);
+        hipLaunchKernelGGL(k_max_run_len, dim3(grid_for(ix.nruns, 256, 16384)), dim3(256), 0, ctx->stream,
+                           run_start.p, ix.nruns, mx.p);
+        XH_CHECK_HIP(hipGetLastError());
+        ctx->read_scalars(mx.p, 1);
+        XH_REQUIRE(ctx->host_scalars[0] < (1ull << 32), XLOG_HIP_CAPACITY_OVERFLOW,
+                   "join build: a key with 2^32 or more rows");
+    }
     XH_CHECK_HIP(hipGetLastError());
     int bits = 10;
     while ((1ull << bits) < 2 * ix.nruns) ++bits;
