@@ -141,55 +141,84 @@ def make_workload(name: str, p):
 
 
 def cpu_baseline(name: str, inputs, budget_s: float = 30.0):
-    """CPU oracle (single-threaded C, oracle/oracle.c) on a bounded sample."""
+    """CPU oracle (C, oracle/oracle.c) on this host: `value` with every OpenMP thread
+    (OMP_NUM_THREADS, or the host's cores) on the workload or a bounded sample of it, and
+    `single_thread` on a smaller sample, both stated."""
     import oracle
     from xlog_amd import pack, tc_plan
 
+    threads = oracle.max_threads()
+
+    def timed(fn, t, warmup=False):
+        # warmup: one untimed call first, so multi-GB first-touch page faults are not timed
+        # (the GPU side is timed after warm-up steps as well)
+        oracle.set_threads(t)
+        try:
+            if warmup:
+                fn()
+            t0 = time.perf_counter()
+            res = fn()
+            return res, time.perf_counter() - t0
+        finally:
+            oracle.set_threads(1)
+
+    def entry(value, unit, cores, sample):
+        return {"value": value, "unit": unit, "cores": cores, "kind": "port", "sample": sample}
+
     if name in ("c2", "c2u"):
         r_a, r_b, s_b, s_c = inputs
-        n_r = 1 << 22
-        l = pack(r_a[:n_r], r_b[:n_r])
         r = pack(s_b, s_c)
-        t = time.perf_counter()
-        out = oracle.sort_dedup(oracle.join_project(l, r, 1, 0, 0, 3))
-        dt = time.perf_counter() - t
-        return {"value": (n_r + len(r)) / dt, "unit": "tuples/s", "cores": 1, "kind": "port",
-                "sample": f"first {n_r} rows of R (of {len(r_a)}) joined with all {len(r)} rows of S, "
-                          f"project + sort + dedup -> {len(out)} tuples in {dt:.2f}s"}
+        l_all = pack(r_a, r_b)
+        n_r = 1 << 22
+
+        def run(l):
+            return oracle.sort_dedup(oracle.join_project(l, r, 1, 0, 0, 3))
+        out, dt = timed(lambda: run(l_all), threads, warmup=True)
+        out1, dt1 = timed(lambda: run(l_all[:n_r]), 1, warmup=True)
+        res = entry((len(l_all) + len(r)) / dt, "tuples/s", threads,
+                    f"full config: R join S, project + sort + dedup -> {len(out)} tuples in {dt:.2f}s "
+                    f"(after one untimed run)")
+        res["single_thread"] = entry((n_r + len(r)) / dt1, "tuples/s", 1,
+                                     f"first {n_r} rows of R with all of S -> {len(out1)} tuples in {dt1:.2f}s")
+        return res
     if name == "c3":
         (keys,) = inputs
-        n = 1 << 25
-        t = time.perf_counter()
-        u = oracle.sort_dedup(keys[:n])
-        dt = time.perf_counter() - t
-        return {"value": n / dt, "unit": "tuples/s", "cores": 1, "kind": "port",
-                "sample": f"first {n} of {len(keys)} tuples, sort + dedup -> {len(u)} in {dt:.2f}s"}
+        n1 = 1 << 25
+        u, dt = timed(lambda: oracle.sort_dedup(keys), threads, warmup=True)
+        u1, dt1 = timed(lambda: oracle.sort_dedup(keys[:n1]), 1, warmup=True)
+        res = entry(len(keys) / dt, "tuples/s", threads, f"full config: sort + dedup of {len(keys)} -> {len(u)} in {dt:.2f}s")
+        res["single_thread"] = entry(n1 / dt1, "tuples/s", 1, f"first {n1} tuples -> {len(u1)} in {dt1:.2f}s")
+        return res
     if name == "c5":
         # the semi-naive oracle on the 5,000-variable instance of the same generator
         from xlog_amd import andersen_plan, datagen
         f = datagen.andersen(5000, 20000, 1.5, datagen.seed_for(5))
         rels = [pack(*f[k]) for k in ("assign", "addressOf", "load", "store")] + [None]
-        t = time.perf_counter()
-        outs, it, _ = oracle.seminaive(andersen_plan(), rels)
-        dt = time.perf_counter() - t
-        return {"value": len(outs[4]) / dt, "unit": "pointsTo tuples/s", "cores": 1, "kind": "port",
-                "sample": f"5,000 variables / 20,000 facts (the bench runs 10,000 / 40,000): "
-                          f"{len(outs[4])} tuples, {it} iterations in {dt:.2f}s"}
-    if name in ("c1", "c4"):
+        (outs, it, _), dt = timed(lambda: oracle.seminaive(andersen_plan(), rels), threads)
+        (outs1, _, _), dt1 = timed(lambda: oracle.seminaive(andersen_plan(), rels), 1)
+        smp = f"5,000 variables / 20,000 facts (the bench runs 10,000 / 40,000): {len(outs[4])} tuples, {it} iterations"
+        res = entry(len(outs[4]) / dt, "pointsTo tuples/s", threads, f"{smp} in {dt:.2f}s")
+        res["single_thread"] = entry(len(outs1[4]) / dt1, "pointsTo tuples/s", 1, f"same instance in {dt1:.2f}s")
+        return res
+    if name == "c1":
         src, dst = inputs
-        t = time.perf_counter()
-        outs, it, _ = oracle.seminaive(tc_plan(), [pack(src, dst), None]) if name == "c1" else (None, None, None)
-        if name == "c4":
-            # the semi-naive oracle over ~10^9 tuples takes far longer than the budget:
-            # time the BFS closed form on a bounded set of sources instead
-            res = oracle.bfs_tc(32768, src, dst, want_relation=False)
-            dt = time.perf_counter() - t
-            return {"value": res["total"] / dt, "unit": "tuples/s", "cores": 1, "kind": "port",
-                    "sample": f"BFS-layer closure from all sources (closed form, not the semi-naive loop): "
-                              f"{res['total']} tuples in {dt:.2f}s"}
-        dt = time.perf_counter() - t
-        return {"value": len(outs[1]) / dt, "unit": "tuples/s", "cores": 1, "kind": "port",
-                "sample": f"full config, semi-naive oracle: {len(outs[1])} tuples, {it} iterations in {dt:.2f}s"}
+        (outs, it, _), dt = timed(lambda: oracle.seminaive(tc_plan(), [pack(src, dst), None]), threads)
+        (outs1, _, _), dt1 = timed(lambda: oracle.seminaive(tc_plan(), [pack(src, dst), None]), 1)
+        res = entry(len(outs[1]) / dt, "tuples/s", threads,
+                    f"full config, semi-naive oracle: {len(outs[1])} tuples, {it} iterations in {dt:.2f}s")
+        res["single_thread"] = entry(len(outs1[1]) / dt1, "tuples/s", 1, f"same in {dt1:.2f}s")
+        return res
+    if name == "c4":
+        src, dst = inputs
+        # the semi-naive oracle over ~10^9 tuples takes far longer than the budget:
+        # time the BFS closed form (closure size from every source) instead
+        res_mt, dt = timed(lambda: oracle.bfs_tc(32768, src, dst, want_relation=False, digest=False), threads)
+        res_1, dt1 = timed(lambda: oracle.bfs_tc(32768, src, dst, want_relation=False, digest=False), 1)
+        res = entry(res_mt["total"] / dt, "tuples/s", threads,
+                    f"BFS-layer closure from all sources (closed form, not the semi-naive loop): "
+                    f"{res_mt['total']} tuples in {dt:.2f}s")
+        res["single_thread"] = entry(res_1["total"] / dt1, "tuples/s", 1, f"same in {dt1:.2f}s")
+        return res
     return None
 
 

@@ -64,6 +64,10 @@ def _load() -> C.CDLL:
     lib.or_naive.restype = I
     lib.or_bfs_tc.argtypes = [C.c_uint32, P, P, U64, P, U64, P, C.POINTER(U64), C.POINTER(U64)]
     lib.or_bfs_tc.restype = C.c_int64
+    lib.or_set_threads.argtypes = [I]
+    lib.or_set_threads.restype = I
+    lib.or_max_threads.argtypes = []
+    lib.or_max_threads.restype = I
     return lib
 
 
@@ -180,22 +184,36 @@ def naive(plan, relations, max_rounds: int = 1_000_000):
     return outs, it
 
 
-def bfs_tc(n_vertices: int, src, dst, want_relation: bool = True, max_dist: int = 4096):
-    """Closed-form TC by BFS from every source.  Returns dict(iterations, total, digest,
-    dist_count (index d = #pairs at shortest distance d), relation (sorted) or None)."""
+def set_threads(n: int) -> int:
+    """Threads of the parallel sort / join probe / BFS paths (1 = single-threaded); returns the value set."""
+    return int(_lib.or_set_threads(int(n)))
+
+
+def max_threads() -> int:
+    """OpenMP's default thread count (OMP_NUM_THREADS or the host's cores)."""
+    return int(_lib.or_max_threads())
+
+
+def bfs_tc(n_vertices: int, src, dst, want_relation: bool = True, max_dist: int = 4096, digest: bool = True):
+    """Closed-form TC by BFS from every source.  Returns dict(iterations, total, digest (None when not
+    asked for), dist_count (index d = #pairs at shortest distance d), relation (sorted) or None)."""
     src = np.ascontiguousarray(np.asarray(src, np.uint32))
     dst = np.ascontiguousarray(np.asarray(dst, np.uint32))
     dist = np.zeros(max_dist, np.uint64)
-    total, digest = C.c_uint64(), C.c_uint64()
+    total, digest_v = C.c_uint64(), C.c_uint64()
     out = None
     if want_relation:
         # first pass for the size
-        _lib.or_bfs_tc(n_vertices, _p(src), _p(dst), len(src), None, 0, None, C.byref(total), C.byref(digest))
+        _lib.or_bfs_tc(n_vertices, _p(src), _p(dst), len(src), None, 0, None, C.byref(total), C.byref(digest_v))
         out = np.empty(max(1, total.value), np.uint64)
+    # the digest needs the rows in source order: with digest=False and no relation the parallel path
+    # (counts only) runs when set_threads(n > 1) is in effect
     it = _lib.or_bfs_tc(n_vertices, _p(src), _p(dst), len(src), dist.ctypes.data, max_dist,
-                        out.ctypes.data if out is not None else None, C.byref(total), C.byref(digest))
+                        out.ctypes.data if out is not None else None, C.byref(total),
+                        C.byref(digest_v) if (digest or want_relation) else None)
     if it < 0:
         raise MemoryError("or_bfs_tc")
     rel = out[: total.value].copy() if out is not None else None
-    return {"iterations": int(it), "total": int(total.value), "digest": int(digest.value),
+    return {"iterations": int(it), "total": int(total.value),
+            "digest": int(digest_v.value) if (digest or want_relation) else None,
             "dist_count": dist, "relation": rel}

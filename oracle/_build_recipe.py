@@ -14,7 +14,7 @@ LIB = DIR / "liboracle.so"
 
 def build() -> Path:
     tmp = LIB.with_suffix(".so.tmp")
-    cmd = ["gcc", "-O2", "-fPIC", "-shared", "-Wall", "-Wextra", "-Wno-unused-parameter", "-o", str(tmp),
+    cmd = ["gcc", "-O2", "-fopenmp", "-fPIC", "-shared", "-Wall", "-Wextra", "-Wno-unused-parameter", "-o", str(tmp),
            str(DIR / "oracle.c")]
     r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     if r.returncode != 0:

@@ -24,19 +24,113 @@
  * Independent cross-checks live beside it: a BFS-layer transitive closure
  * (iteration count = max finite shortest-path length) and a naive fixpoint
  * (R <- R U T(R) until stable).
+ *
+ * or_set_threads(t > 1) switches the sort, the join probe and the BFS to
+ * OpenMP versions (used for the multi-core CPU baseline).  They produce the
+ * same results as the single-threaded code, which stays the pinned reference
+ * for them (tests/test_oracle.py compares both).
  */
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
 #include <stdio.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+static int g_threads = 1;
+/* threads for the parallel paths (1 = the single-threaded code) */
+int or_set_threads(int t) {
+#ifdef _OPENMP
+    g_threads = t > 1 ? t : 1;
+#else
+    (void)t;
+    g_threads = 1;
+#endif
+    return g_threads;
+}
+int or_max_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
 
 /* ------------------------------------------------------------------------ */
 /* sorted-vector primitives                                                  */
 /* ------------------------------------------------------------------------ */
 
+static int sort_u64_serial(uint64_t *a, uint64_t n);
+#ifdef _OPENMP
+/* Parallel form: one stable counting pass on the most significant digit that
+ * varies (every thread counts its contiguous chunk, offsets digit-major then
+ * thread-minor, every thread scatters its chunk in order), then the 256
+ * buckets -- whose keys agree on that digit and every digit above it -- are
+ * sorted independently by the serial LSD sort, buckets spread over the
+ * threads.  The result is the sorted array, as from the serial sort. */
+static int sort_u64_mt(uint64_t *a, uint64_t n, int T) {
+    uint64_t orv = 0, andv = ~0ull;
+    for (uint64_t i = 0; i < n; ++i) { orv |= a[i]; andv &= a[i]; }
+    uint64_t diff = orv ^ andv;  /* bits that vary */
+    if (!diff) return 0;
+    int D = 7;
+    while (D > 0 && !((diff >> (8 * D)) & 255)) --D;
+    uint64_t *tmp = (uint64_t *)malloc(n * sizeof(uint64_t));
+    uint64_t *cnt = (uint64_t *)calloc((size_t)T * 256, sizeof(uint64_t));
+    uint64_t bstart[257];
+    if (!tmp || !cnt) { free(tmp); free(cnt); return -2; }
+    const int sh = 8 * D;
+    int rc = 0;
+    #pragma omp parallel num_threads(T)
+    {
+        const int t = omp_get_thread_num();
+        const uint64_t lo = n * (uint64_t)t / (uint64_t)T, hi = n * (uint64_t)(t + 1) / (uint64_t)T;
+        uint64_t *c = cnt + (size_t)t * 256;
+        for (uint64_t i = lo; i < hi; ++i) c[(a[i] >> sh) & 255]++;
+        #pragma omp barrier
+        #pragma omp single
+        {
+            uint64_t acc = 0;
+            for (int b = 0; b < 256; ++b) {
+                bstart[b] = acc;
+                for (int u = 0; u < T; ++u) {
+                    uint64_t v = cnt[(size_t)u * 256 + b];
+                    cnt[(size_t)u * 256 + b] = acc;
+                    acc += v;
+                }
+            }
+            bstart[256] = acc;
+        }
+        for (uint64_t i = lo; i < hi; ++i) {
+            uint64_t k = a[i];
+            tmp[c[(k >> sh) & 255]++] = k;
+        }
+        #pragma omp barrier
+        #pragma omp for schedule(dynamic, 1)
+        for (int b = 0; b < 256; ++b) {
+            if (sort_u64_serial(tmp + bstart[b], bstart[b + 1] - bstart[b])) {
+                #pragma omp atomic write
+                rc = -2;
+            }
+            memcpy(a + bstart[b], tmp + bstart[b], (bstart[b + 1] - bstart[b]) * sizeof(uint64_t));
+        }
+    }
+    free(tmp); free(cnt);
+    return rc;
+}
+#endif
+
 /* LSD radix sort of u64 keys, 8-bit digits, digits that are constant over
  * the whole input are skipped.  Stable (a textbook counting sort per pass). */
 int or_sort_u64(uint64_t *a, uint64_t n) {
+    if (n < 2) return 0;
+#ifdef _OPENMP
+    if (g_threads > 1 && n >= (1u << 16)) return sort_u64_mt(a, n, g_threads);
+#endif
+    return sort_u64_serial(a, n);
+}
+static int sort_u64_serial(uint64_t *a, uint64_t n) {
     if (n < 2) return 0;
     uint64_t *tmp = (uint64_t *)malloc(n * sizeof(uint64_t));
     if (!tmp) return -2;
@@ -151,6 +245,59 @@ static int join_project(const uint64_t *l, uint64_t nl, const uint64_t *r, uint6
     for (uint64_t i = 0; i < nr; ++i)  /* (key, other column) */
         idx[i] = ((uint64_t)col_of(r[i], rk) << 32) | col_of(r[i], 1 - rk);
     if (or_sort_u64(idx, nr)) { free(idx); return -2; }
+#ifdef _OPENMP
+    if (g_threads > 1 && nl >= (1u << 14)) {
+        /* two passes over contiguous chunks of L (count, then write at the
+         * chunk's offset): the same bag in the same order as below.  The run
+         * start of every L row is kept from the first pass. */
+        const int T = g_threads;
+        uint64_t *off = (uint64_t *)calloc((size_t)T + 1, sizeof(uint64_t));
+        uint64_t *lo_of = (uint64_t *)malloc(nl * sizeof(uint64_t));
+        uint32_t *cnt_of = (uint32_t *)malloc(nl * sizeof(uint32_t));
+        if (!off || !lo_of || !cnt_of) { free(off); free(lo_of); free(cnt_of); free(idx); return -2; }
+        #pragma omp parallel num_threads(T)
+        {
+            const int t = omp_get_thread_num();
+            const uint64_t lo = nl * (uint64_t)t / (uint64_t)T, hi = nl * (uint64_t)(t + 1) / (uint64_t)T;
+            uint64_t c = 0;
+            for (uint64_t i = lo; i < hi; ++i) {
+                uint32_t key = col_of(l[i], lk);
+                uint64_t a = 0, b = nr;
+                while (a < b) { uint64_t m = (a + b) / 2; if ((uint32_t)(idx[m] >> 32) < key) a = m + 1; else b = m; }
+                uint64_t e = a;
+                while (e < nr && (uint32_t)(idx[e] >> 32) == key) ++e;
+                lo_of[i] = a;
+                cnt_of[i] = (uint32_t)(e - a);
+                c += e - a;
+            }
+            off[t + 1] = c;
+        }
+        for (int t = 0; t < T; ++t) off[t + 1] += off[t];
+        const uint64_t base = out->n;
+        if (vec_reserve(out, base + off[T])) { free(off); free(lo_of); free(cnt_of); free(idx); return -2; }
+        #pragma omp parallel num_threads(T)
+        {
+            const int t = omp_get_thread_num();
+            const uint64_t lo = nl * (uint64_t)t / (uint64_t)T, hi = nl * (uint64_t)(t + 1) / (uint64_t)T;
+            uint64_t w = base + off[t];
+            for (uint64_t i = lo; i < hi; ++i) {
+                const uint32_t key = col_of(l[i], lk);
+                for (uint64_t j = lo_of[i], e = lo_of[i] + cnt_of[i]; j < e; ++j) {
+                    uint32_t row[4];
+                    row[0] = (uint32_t)(l[i] >> 32); row[1] = (uint32_t)l[i];
+                    row[2 + rk] = key; row[3 - rk] = (uint32_t)idx[j];
+                    out->v[w++] = ((uint64_t)row[out_cols[0]] << 32) | row[out_cols[1]];
+                }
+            }
+        }
+        free(lo_of);
+        free(cnt_of);
+        out->n = base + off[T];
+        free(off);
+        free(idx);
+        return 0;
+    }
+#endif
     for (uint64_t i = 0; i < nl; ++i) {
         uint32_t key = col_of(l[i], lk);
         uint64_t lo = 0, hi = nr;
@@ -527,6 +674,51 @@ int64_t or_bfs_tc(uint32_t n_vertices, const uint32_t *src, const uint32_t *dst,
     free(fill);
     int64_t maxd = 0;
     uint64_t tot = 0, h = 0xcbf29ce484222325ULL;
+#ifdef _OPENMP
+    if (g_threads > 1 && !out && !digest) {
+        /* counts only: sources in parallel, each thread with its own BFS state */
+        const int T = g_threads;
+        uint64_t *dc = dist_count ? (uint64_t *)calloc((size_t)T * max_dist, sizeof(uint64_t)) : NULL;
+        #pragma omp parallel num_threads(T) reduction(+ : tot) reduction(max : maxd)
+        {
+            const int t = omp_get_thread_num();
+            int32_t *dl = (int32_t *)malloc((size_t)(n_vertices ? n_vertices : 1) * sizeof(int32_t));
+            uint32_t *ql = (uint32_t *)malloc((size_t)(n_vertices ? n_vertices : 1) * sizeof(uint32_t));
+            uint64_t *mydc = dc ? dc + (size_t)t * max_dist : NULL;
+            #pragma omp for schedule(dynamic, 64)
+            for (uint32_t x = 0; x < n_vertices; ++x) {
+                for (uint32_t v = 0; v < n_vertices; ++v) dl[v] = -1;
+                uint64_t qh = 0, qt = 0;
+                for (uint64_t e = deg[x]; e < deg[x + 1]; ++e) {
+                    uint32_t z = adj[e];
+                    if (dl[z] < 0) { dl[z] = 1; ql[qt++] = z; }
+                }
+                while (qh < qt) {
+                    uint32_t y = ql[qh++];
+                    for (uint64_t e = deg[y]; e < deg[y + 1]; ++e) {
+                        uint32_t z = adj[e];
+                        if (dl[z] < 0) { dl[z] = dl[y] + 1; ql[qt++] = z; }
+                    }
+                }
+                for (uint64_t i = 0; i < qt; ++i) {
+                    int32_t dz = dl[ql[i]];
+                    if (dz > maxd) maxd = dz;
+                    if (mydc && (uint64_t)dz < max_dist) mydc[dz]++;
+                }
+                tot += qt;
+            }
+            free(dl); free(ql);
+        }
+        if (dc) {
+            for (int t = 0; t < T; ++t)
+                for (uint64_t d = 0; d < max_dist; ++d) dist_count[d] += dc[(size_t)t * max_dist + d];
+            free(dc);
+        }
+        free(deg); free(adj); free(dist); free(queue); free(row);
+        if (total) *total = tot;
+        return maxd == 0 ? 1 : maxd;
+    }
+#endif
     for (uint32_t x = 0; x < n_vertices; ++x) {
         for (uint32_t v = 0; v < n_vertices; ++v) dist[v] = -1;
         uint64_t qh = 0, qt = 0, nrow = 0;

@@ -235,3 +235,37 @@ def test_planted_mistake_is_caught():
     outs, it, _ = oracle.seminaive(wrong, [pack(src, dst), None])
     b = oracle.bfs_tc(60, src, dst)
     assert not np.array_equal(outs[1], b["relation"])
+
+
+# ---- the multi-threaded paths (CPU baseline) against the single-threaded ones --
+def test_parallel_paths_match_serial():
+    """or_set_threads(t > 1) switches the sort, join probe and BFS to OpenMP versions; they must give
+    exactly the single-threaded results (which the tests above pin)."""
+    rng = np.random.default_rng(2024)
+    keys = rng.integers(0, 1 << 64, 400_000, dtype=np.uint64)
+    keys[::7] = keys[1::7][: len(keys[::7])]  # duplicates
+    l = pack(rng.integers(0, 1 << 31, 60_000, dtype=np.uint64), rng.integers(0, 5_000, 60_000, dtype=np.uint64))
+    r = pack(rng.integers(0, 5_000, 50_000, dtype=np.uint64), rng.integers(0, 1 << 31, 50_000, dtype=np.uint64))
+    src, dst = datagen.random_digraph(1200, 5000, datagen.seed_for(1))
+    f = datagen.andersen(1500, 6000, 1.5, datagen.seed_for(5))
+    rels = [pack(*f[k]) for k in ("assign", "addressOf", "load", "store")] + [None]
+    tc_rel = [pack(src, dst), None]
+
+    def run():
+        return (oracle.sort_dedup(keys.copy()), oracle.join_project(l, r, 1, 0, 0, 3),
+                oracle.seminaive(tc_plan(), tc_rel), oracle.seminaive(andersen_plan(), rels),
+                oracle.bfs_tc(1200, src, dst, want_relation=False, digest=False))
+
+    serial = run()
+    try:
+        assert oracle.set_threads(4) == 4
+        par = run()
+    finally:
+        oracle.set_threads(1)
+    assert np.array_equal(serial[0], par[0])
+    assert np.array_equal(serial[1], par[1])  # same bag, same order
+    for s_, p_ in ((serial[2], par[2]), (serial[3], par[3])):
+        assert s_[1:] == p_[1:]
+        assert all((a is None and b is None) or np.array_equal(a, b) for a, b in zip(s_[0], p_[0]))
+    assert serial[4]["total"] == par[4]["total"] and serial[4]["iterations"] == par[4]["iterations"]
+    assert np.array_equal(serial[4]["dist_count"], par[4]["dist_count"])
