@@ -257,7 +257,10 @@ xlog_hip_status xlog_hip_fixpoint_tc(xlog_hip_ctx *ctx, const xlog_hip_rel *edge
 #define XLOG_HIP_KERNEL_PROBE_EMIT 5  /* join probe, materialise pass */
 #define XLOG_HIP_KERNEL_TC_STEP 6     /* dense TC iteration */
 #define XLOG_HIP_KERNEL_TC_EMIT 7     /* dense TC final emit */
-#define XLOG_HIP_KERNEL_KINDS 8
+#define XLOG_HIP_KERNEL_CHAIN_PRODUCT 8  /* dense chain-rule boolean product */
+#define XLOG_HIP_KERNEL_CHAIN_FINALIZE 9 /* dense chain-rule delta / merge */
+#define XLOG_HIP_KERNEL_CHAIN_EMIT 10    /* dense chain-rule final emit */
+#define XLOG_HIP_KERNEL_KINDS 11
 xlog_hip_status xlog_hip_profile_enable(xlog_hip_ctx *ctx, int on);
 xlog_hip_status xlog_hip_profile_reset(xlog_hip_ctx *ctx);
 xlog_hip_status xlog_hip_profile_read(xlog_hip_ctx *ctx, uint32_t kind, uint64_t *launches, double *total_ms,

@@ -95,12 +95,16 @@ def test_c4_full_transitive_closure(provider, route):
     assert p.digest(R) == e["digest"]
 
 
-def test_c5_scaled_andersen_fixture(provider):
-    e = FX["c5_5000_20000"]
+@pytest.mark.parametrize("route", [ROUTE_BITMAP, ROUTE_JOIN])
+@pytest.mark.parametrize("fixture", ["c5_2000_8000", "c5_5000_20000"])
+def test_c5_scaled_andersen_fixture(provider, fixture, route):
+    e = FX[fixture]
     f = datagen.andersen(e["n_vars"], e["n_facts"], e["alpha"], datagen.seed_for(5))
     p = provider
     rels = [p.create_buffer_from_u32_columns(list(f[k])) for k in ("assign", "addressOf", "load", "store")]
-    outs, st = p.fixpoint(andersen_plan(), rels + [None])
+    _note(f"{fixture}: fixpoint route={route}")
+    outs, st = p.fixpoint(andersen_plan(), rels + [None], route=route)
+    assert st["route"] == route
     assert outs[4].num_rows() == e["tuples"]
     assert st["iterations"] == e["iterations"]
     assert st["delta_sizes"] == e["delta_sizes"]

@@ -129,7 +129,7 @@ def test_chunked_join_fold_parity(provider, monkeypatch):
     for chunk in ("1", "777", "100000"):
         monkeypatch.setenv("XLOG_HIP_JOIN_CHUNK_ROWS", chunk)
         dev = [p.create_buffer_from_packed(r) for r in rels] + [None]
-        outs, st = p.fixpoint(andersen_plan(), dev)
+        outs, st = p.fixpoint(andersen_plan(), dev, route=ROUTE_JOIN)
         assert np.array_equal(p.download_packed(outs[4]), outs_o[4])
         assert st["iterations"] == it_o and st["delta_sizes"] == deltas_o
         e = p.create_buffer_from_u32_columns([src, dst])

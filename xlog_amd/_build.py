@@ -19,7 +19,7 @@ CSRC = PKG / "csrc"
 BUILD = ROOT / "_build" / "xlog_amd"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-HIP_SOURCES = ["sort.hip", "select.hip", "join.hip", "tc_bitmap.hip", "abi.hip"]
+HIP_SOURCES = ["sort.hip", "select.hip", "join.hip", "tc_bitmap.hip", "chain_bitmap.hip", "abi.hip"]
 HIP_FLAGS = [
     "--offload-arch=gfx950",
     "-O3",

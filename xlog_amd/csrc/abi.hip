@@ -1209,6 +1209,44 @@ bool tc_shape(const std::vector<Rule> &rules, int *edge_pred, int *head_pred) {
     return rec->hv[0] == A && rec->hv[1] == C;
 }
 
+// Chain plans: in every rule the body atoms form a simple path from the first
+// head variable to the second (each atom read forward or backward), e.g.
+// Andersen's  pointsTo(P,O) :- store(V,W), pointsTo(V,P), pointsTo(W,O)  is
+// P -pointsTo^T-> V -store-> W -pointsTo-> O.
+bool chain_shape(const std::vector<Rule> &rules, std::vector<ChainRule> &out) {
+    out.clear();
+    for (const Rule &r : rules) {
+        if (r.hv[0] == r.hv[1]) return false;
+        ChainRule c;
+        c.head = r.head;
+        bool used[MAX_BODY] = {false, false, false, false};
+        int cur = r.hv[0];
+        std::vector<int> seen{cur};
+        for (int step = 0; step < r.nb; ++step) {
+            int pick = -1;
+            bool back = false;
+            for (int j = 0; j < r.nb; ++j) {
+                const Atom &a = r.b[j];
+                if (a.v[0] == a.v[1]) return false;
+                if (used[j] || (a.v[0] != cur && a.v[1] != cur)) continue;
+                if (pick >= 0) return false;  // the path branches
+                pick = j;
+                back = a.v[1] == cur;
+            }
+            if (pick < 0) return false;
+            used[pick] = true;
+            cur = back ? r.b[pick].v[0] : r.b[pick].v[1];
+            for (int v : seen)
+                if (v == cur) return false;
+            seen.push_back(cur);
+            c.path.push_back(ChainAtom{r.b[pick].pred, back});
+        }
+        if (cur != r.hv[1]) return false;
+        out.push_back(c);
+    }
+    return !out.empty();
+}
+
 }  // namespace
 
 // canonical keys of an input relation for the driver
@@ -1229,6 +1267,89 @@ static DRel canon_drel(Ctx *ctx, const xlog_hip_rel *r) {
     d.k = u;
     d.owned = true;
     return d;
+}
+
+// The dense chain route (chain_fixpoint) when the plan is made of chain rules
+// over at most 2^17 ids whose bit matrices fit in half the free device
+// memory; false (nothing done) when the join route should run instead, an
+// error when the bitmap route was requested and cannot run.  Consumes `edges`
+// (the canonical edge list of the transitive-closure check, if any).
+static bool run_chain_route(Ctx *ctx, const std::vector<Rule> &rules, uint32_t n_preds,
+                            const xlog_hip_rel *const *rels, uint64_t route, uint64_t max_iter, xlog_hip_rel **out,
+                            uint64_t *iterations, std::vector<uint64_t> &deltas, xlog_hip_fixpoint_stats *stats,
+                            DRel &edges) {
+    if (edges.owned) ctx->free(edges.k);
+    edges = DRel();
+    std::vector<ChainRule> chains;
+    bool chain = route != XLOG_HIP_ROUTE_JOIN && chain_shape(rules, chains);
+    XH_REQUIRE(chain || route != XLOG_HIP_ROUTE_BITMAP, XLOG_HIP_UNSUPPORTED,
+               "bitmap route needs chain rules (body atoms forming a path between the head variables)");
+    if (!chain) return false;
+    std::vector<char> idb(n_preds, 0);
+    for (const Rule &r : rules) idb[r.head] = 1;
+    std::vector<DRel> canon(n_preds);
+    std::vector<uint64_t *> res;
+    auto release = [&]() {
+        for (auto &d : canon)
+            if (d.owned) ctx->free(d.k);
+        canon.clear();
+        for (uint64_t *q : res)
+            if (q) ctx->free(q);
+        res.clear();
+    };
+    try {
+        for (uint32_t p = 0; p < n_preds; ++p) canon[p] = canon_drel(ctx, rels[p]);
+        uint64_t any = 0;
+        Buf<unsigned int> mx(ctx, 1);
+        fill_u32(ctx, mx.p, 0u, 1);
+        for (uint32_t p = 0; p < n_preds; ++p)
+            if (canon[p].n) {
+                any += canon[p].n;
+                LAUNCH_1D(k_max_u32_of_packed, canon[p].n, canon[p].k, canon[p].n, mx.p);
+            }
+        uint64_t domain = 0;
+        if (any) {
+            XH_CHECK_HIP(hipMemcpyAsync(ctx->host_scalars, mx.p, sizeof(unsigned int), hipMemcpyDeviceToHost,
+                                        ctx->stream));
+            ctx->sync();
+            domain = (uint64_t)*reinterpret_cast<uint32_t *>(ctx->host_scalars) + 1;
+        }
+        size_t free_b = 0, total_b = 0;
+        XH_CHECK_HIP(hipMemGetInfo(&free_b, &total_b));
+        const bool fits = domain >= 1 && domain <= (1ull << 17) &&
+                          chain_fixpoint_bytes(chains, idb, (uint32_t)domain) <= (uint64_t)free_b / 2;
+        XH_REQUIRE(fits || route != XLOG_HIP_ROUTE_BITMAP, XLOG_HIP_UNSUPPORTED,
+                   "bitmap route needs 1..2^17 ids and room for the bit matrices");
+        if (!fits) {
+            release();
+            return false;
+        }
+        std::vector<const uint64_t *> keys(n_preds);
+        std::vector<uint64_t> rows(n_preds), res_n;
+        for (uint32_t p = 0; p < n_preds; ++p) {
+            keys[p] = canon[p].k;
+            rows[p] = canon[p].n;
+        }
+        chain_fixpoint(ctx, chains, n_preds, idb, keys, rows, (uint32_t)domain, max_iter, res, res_n, iterations,
+                       deltas);
+        for (uint32_t p = 0; p < n_preds; ++p) {
+            if (!idb[p]) continue;
+            out[p] = res_n[p] ? rel_adopt(ctx, 2, res_n[p], res[p], nullptr, REL_CANONICAL) : rel_new(ctx, 2, 0);
+            res[p] = nullptr;
+            out[p]->flags = REL_CANONICAL;
+        }
+    } catch (...) {
+        release();
+        for (uint32_t p = 0; p < n_preds; ++p)
+            if (out[p]) {
+                rel_free(out[p]);
+                out[p] = nullptr;
+            }
+        if (stats) stats->iterations = deltas.empty() ? 0 : deltas.size() - 1;
+        throw;
+    }
+    release();
+    return true;
 }
 
 static void run_fixpoint(Ctx *ctx, const int32_t *plan, uint32_t n_preds, const xlog_hip_rel *const *rels,
@@ -1265,8 +1386,6 @@ static void run_fixpoint(Ctx *ctx, const int32_t *plan, uint32_t n_preds, const 
         }
     }
     bool bitmap = tc && head_empty && route != XLOG_HIP_ROUTE_JOIN && (uint64_t)nv <= (1ull << 17);
-    XH_REQUIRE(!(route == XLOG_HIP_ROUTE_BITMAP && !bitmap), XLOG_HIP_UNSUPPORTED,
-               "bitmap route needs the transitive-closure plan, an empty head and a domain <= 2^17");
     if (bitmap) {
         uint64_t *res = nullptr, n = 0;
         try {
@@ -1280,8 +1399,10 @@ static void run_fixpoint(Ctx *ctx, const int32_t *plan, uint32_t n_preds, const 
         out[H] = n ? rel_adopt(ctx, 2, n, res, nullptr, REL_CANONICAL) : rel_new(ctx, 2, 0);
         out[H]->flags = REL_CANONICAL;
         if (stats) stats->route = XLOG_HIP_ROUTE_BITMAP;
+    } else if (run_chain_route(ctx, rules, n_preds, rels, route, max_iter, out, &iterations, deltas, stats,
+                               edges)) {
+        if (stats) stats->route = XLOG_HIP_ROUTE_BITMAP;
     } else {
-        if (edges.owned) ctx->free(edges.k);
         Driver drv{ctx, rules, n_preds, std::vector<bool>(n_preds, false), std::vector<DRel>(n_preds),
                    std::vector<DRel>(n_preds)};
         for (const Rule &r : rules) drv.idb[r.head] = true;

@@ -1,0 +1,608 @@
+// Dense-domain semi-naive fixpoint for programs whose rules are chains of
+// binary relations, for gfx950.
+//
+// The reference evaluates every recursive rule with the join route
+// (Executor::execute_recursive_scc, crates/xlog-runtime/src/executor/
+// recursive.rs:447-957) and keeps a dense factorized delta only for the
+// transitive-closure shape (fj_delta_novel_u32_recorded, crates/xlog-cuda/src/
+// provider/fj_delta.rs:117-490).  Here any rule
+//     head(v0, vk) :- a1(v0, v1), a2(v1, v2), ..., ak(v_{k-1}, vk)
+// (atoms in any order, each read forward or with its columns swapped) is a
+// chain of boolean products over the id domain, so a whole program of such
+// rules (transitive closure, Andersen points-to, same-generation ...) runs
+// with every relation as a domain x domain bit matrix resident in HBM:
+//
+//   IDB predicate  : R (full), D (delta), C (candidates), and R^T / D^T when
+//                    some rule reads it backward; each with a row mask (bit x
+//                    set iff row x is non-empty) so empty rows are skipped.
+//   EDB predicate  : CSR (row_ptr, adj), forward and / or transposed.
+//
+// One product  out[x] = OR_{y in left[x], right[y] != 0} right[y]  is one
+// launch of k_chain_product (a block per row x).  A chain of k atoms is k-1
+// products evaluated left to right into two ping-pong temporaries; the last
+// product ORs into the head's candidate matrix.  Per iteration, for every
+// rule and every IDB occurrence whose delta is non-empty, the chain runs with
+// the delta at that occurrence and the full relation elsewhere -- the same
+// variants as the join route -- then k_chain_finalize per IDB predicate does
+//   D = C & ~R;  R |= D;  C = 0   (+ scatter of D into R^T and D^T)
+// and counts |D|; the counts are the only values read back.  Results leave
+// the device once, at convergence, as canonical rows (bitmap_emit).
+#include "internal.hpp"
+
+namespace xh {
+
+namespace {
+
+constexpr int PTB = 512;           // product block: 8 waves
+constexpr int PNW = PTB / WAVE;
+constexpr int LCHUNK_WORDS = 64;   // left-row bitmap words compacted per round (<= 4096 ids)
+constexpr int FTB = 256;           // finalize / row-op block
+constexpr uint32_t MAX_DOMAIN = 1u << 17;
+
+// One operand of a product: a bitmap (bits != null) or a CSR (row_ptr, adj);
+// mask bit x is set iff row x is non-empty (exact for CSR and for R / D / C /
+// R^T / D^T; for product temporaries rows without their bit hold garbage and
+// are never read).
+struct Operand {
+    const uint64_t *bits;
+    const uint64_t *row_ptr;
+    const uint32_t *adj;
+    const uint64_t *mask;
+};
+
+__device__ __forceinline__ bool bit_of(const uint64_t *m, uint32_t x) { return (m[x >> 6] >> (x & 63)) & 1ull; }
+
+__device__ __forceinline__ void set_bit(uint64_t *m, uint32_t x) {
+    const uint64_t b = 1ull << (x & 63);
+    // a stale read only costs a redundant atomic
+    if (!(m[x >> 6] & b)) atomicOr((unsigned long long *)&m[x >> 6], (unsigned long long)b);
+}
+
+// out[x] (= or |=) OR over the left row's ids y whose right row is non-empty
+// of right[y].  Left CSR rows are consumed PTB entries per round, left bitmap
+// rows LCHUNK_WORDS words per round; each round's ids are compacted into
+// s_y.  A bitmap right row is read in 64-word stripes, one coalesced 512-byte
+// load per id per stripe (a lane per word), by waves that split the stripes
+// and, when there are fewer stripes than waves, the ids; a CSR right row is
+// expanded by threads over ids with LDS atomics.  The row accumulates in LDS.
+template <bool LCSR, bool RCSR, bool ACC>
+__global__ __launch_bounds__(PTB) void k_chain_product(uint32_t words, Operand L, Operand R, uint64_t *__restrict__ O,
+                                                       uint64_t *__restrict__ omask,
+                                                       unsigned long long *__restrict__ work) {
+    extern __shared__ uint64_t s_acc[];  // words
+    __shared__ uint32_t s_y[LCHUNK_WORDS * 64];
+    __shared__ uint64_t s_bits[LCHUNK_WORDS];
+    __shared__ uint32_t s_woff[LCHUNK_WORDS + 1];
+    __shared__ uint32_t s_any;
+    const uint32_t x = blockIdx.x;
+    if (!bit_of(L.mask, x)) return;  // block-uniform
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
+    for (uint32_t w = tid; w < words; w += PTB) s_acc[w] = 0ull;
+    if (tid == 0) s_any = 0u;
+    __syncthreads();
+    uint64_t lbeg = 0, lend = words;
+    if (LCSR) {
+        lbeg = L.row_ptr[x];
+        lend = L.row_ptr[x + 1];
+    }
+    const uint64_t step = LCSR ? (uint64_t)PTB : (uint64_t)LCHUNK_WORDS;
+    const uint64_t lt_mask = (1ull << lane) - 1ull;
+    const uint32_t ns = (words + 63) / 64;
+    uint64_t total_y = 0;
+    for (uint64_t c0 = lbeg; c0 < lend; c0 += step) {
+        if (LCSR) {
+            const uint64_t e = c0 + tid;
+            const uint32_t y = e < lend ? L.adj[e] : 0u;
+            const bool keep = e < lend && bit_of(R.mask, y);
+            const uint64_t bal = __ballot(keep);
+            if (lane == 0) s_woff[wave] = (uint32_t)__popcll(bal);
+            __syncthreads();
+            if (tid == 0) {
+                uint32_t run = 0;
+                for (int q = 0; q < PNW; ++q) {
+                    const uint32_t c = s_woff[q];
+                    s_woff[q] = run;
+                    run += c;
+                }
+                s_woff[LCHUNK_WORDS] = run;
+            }
+            __syncthreads();
+            if (keep) s_y[s_woff[wave] + (uint32_t)__popcll(bal & lt_mask)] = y;
+        } else {
+            if (wave == 0) {
+                const uint64_t w = c0 + lane;
+                const uint64_t bits = w < words ? L.bits[(uint64_t)x * words + w] & R.mask[w] : 0ull;
+                const uint32_t pc = (uint32_t)__popcll(bits);
+                uint32_t incl = pc;
+#pragma unroll
+                for (int o = 1; o < WAVE; o <<= 1) {
+                    const uint32_t t = __shfl_up(incl, o, WAVE);
+                    if (lane >= o) incl += t;
+                }
+                s_bits[lane] = bits;
+                s_woff[lane] = incl - pc;
+                if (lane == WAVE - 1) s_woff[LCHUNK_WORDS] = incl;
+            }
+            __syncthreads();
+            if (s_woff[LCHUNK_WORDS])
+                for (int j = wave; j < LCHUNK_WORDS; j += PNW) {
+                    const uint64_t bits = s_bits[j];
+                    if ((bits >> lane) & 1ull)
+                        s_y[s_woff[j] + (uint32_t)__popcll(bits & lt_mask)] = (uint32_t)((c0 + j) * 64 + lane);
+                }
+        }
+        __syncthreads();
+        const uint32_t T = s_woff[LCHUNK_WORDS];
+        total_y += T;
+        if (T) {
+            if (RCSR) {
+                for (uint32_t q = tid; q < T; q += PTB) {
+                    const uint32_t y = s_y[q];
+                    const uint64_t b = R.row_ptr[y], f = R.row_ptr[y + 1];
+                    for (uint64_t e = b; e < f; ++e) {
+                        const uint32_t z = R.adj[e];
+                        atomicOr((unsigned long long *)&s_acc[z >> 6], 1ull << (z & 63));
+                    }
+                }
+            } else {
+                // waves split stripes; with fewer stripes than waves, G waves
+                // share a stripe and take every G-th id
+                uint32_t s0, sstep, g, G;
+                if (ns >= (uint32_t)PNW) {
+                    s0 = wave; sstep = PNW; g = 0; G = 1;
+                } else {
+                    G = PNW / ns; g = wave / ns; sstep = ns;
+                    s0 = g < G ? wave % ns : ns;
+                }
+                for (uint32_t s = s0; s < ns; s += sstep) {
+                    const uint32_t w = s * 64 + lane;
+                    const bool ok = w < words;
+                    const uint64_t *col = R.bits + w;
+                    uint64_t a0 = 0ull, a1 = 0ull;
+                    uint32_t j = g;
+                    if (ok) {
+                        for (; j + 3 * G < T; j += 4 * G) {
+                            const uint64_t v0 = col[(uint64_t)s_y[j] * words];
+                            const uint64_t v1 = col[(uint64_t)s_y[j + G] * words];
+                            const uint64_t v2 = col[(uint64_t)s_y[j + 2 * G] * words];
+                            const uint64_t v3 = col[(uint64_t)s_y[j + 3 * G] * words];
+                            a0 |= v0 | v1;
+                            a1 |= v2 | v3;
+                        }
+                        for (; j < T; j += G) a0 |= col[(uint64_t)s_y[j] * words];
+                        a0 |= a1;
+                        if (a0) atomicOr((unsigned long long *)&s_acc[w], a0);
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+    uint64_t *orow = O + (uint64_t)x * words;
+    bool any = false;
+    for (uint32_t w = tid; w < words; w += PTB) {
+        const uint64_t a = s_acc[w];
+        if (ACC) {
+            if (a) orow[w] |= a;
+        } else {
+            orow[w] = a;
+        }
+        any |= a != 0ull;
+    }
+    if (__ballot(any) != 0ull && lane == 0) s_any = 1u;
+    __syncthreads();
+    if (tid == 0) {
+        if (s_any) set_bit(omask, x);
+        if (work) atomicAdd(work, (unsigned long long)total_y);
+    }
+}
+
+// C[x] |= B[x] for the rows of B's mask (a one-atom chain over an IDB operand)
+__global__ __launch_bounds__(FTB) void k_or_rows(uint32_t words, const uint64_t *__restrict__ B,
+                                                 const uint64_t *__restrict__ bmask, uint64_t *__restrict__ C,
+                                                 uint64_t *__restrict__ cmask) {
+    __shared__ uint32_t s_any;
+    const uint32_t x = blockIdx.x;
+    if (!bit_of(bmask, x)) return;
+    if (threadIdx.x == 0) s_any = 0u;
+    __syncthreads();
+    bool any = false;
+    for (uint32_t w = threadIdx.x; w < words; w += FTB) {
+        const uint64_t b = B[(uint64_t)x * words + w];
+        if (b) {
+            C[(uint64_t)x * words + w] |= b;
+            any = true;
+        }
+    }
+    if (__ballot(any) != 0ull && (threadIdx.x & 63) == 0) s_any = 1u;
+    __syncthreads();
+    if (threadIdx.x == 0 && s_any) set_bit(cmask, x);
+}
+
+// bit (x, z) of B for every packed row (x the high word when x_hi, else the low)
+__global__ void k_pairs_bits_mask(const uint64_t *__restrict__ rows, uint64_t n, int x_hi, uint32_t words,
+                                  uint64_t *__restrict__ B, uint64_t *__restrict__ mask) {
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const uint64_t e = rows[i];
+        const uint32_t x = x_hi ? (uint32_t)(e >> 32) : (uint32_t)e;
+        const uint32_t z = x_hi ? (uint32_t)e : (uint32_t)(e >> 32);
+        atomicOr((unsigned long long *)&B[(uint64_t)x * words + (z >> 6)], 1ull << (z & 63));
+        set_bit(mask, x);
+    }
+}
+
+// mask of the non-empty CSR rows, one mask word per thread
+__global__ void k_csr_mask(const uint64_t *__restrict__ row_ptr, uint32_t nv, uint32_t words,
+                           uint64_t *__restrict__ mask) {
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t w = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; w < words; w += stride) {
+        uint64_t m = 0ull;
+        for (uint32_t b = 0; b < 64; ++b) {
+            const uint64_t v = w * 64 + b;
+            if (v < nv && row_ptr[v + 1] > row_ptr[v]) m |= 1ull << b;
+        }
+        mask[w] = m;
+    }
+}
+
+// zero the rows of B whose mask bit is set
+__global__ __launch_bounds__(FTB) void k_clear_rows(uint32_t words, uint64_t *__restrict__ B,
+                                                    const uint64_t *__restrict__ mask) {
+    const uint32_t x = blockIdx.x;
+    if (!bit_of(mask, x)) return;
+    for (uint32_t w = threadIdx.x; w < words; w += FTB) B[(uint64_t)x * words + w] = 0ull;
+}
+
+// Per row x with candidates or an old delta row:
+//   D[x] = C[x] & ~R[x];  R[x] |= D[x];  C[x] = 0
+// sets the new delta / full row-mask bits, adds |D[x]| to *count and, with
+// TRANS, ORs every new (x, z) into R^T and D^T as (z, x).
+template <bool TRANS>
+__global__ __launch_bounds__(FTB) void k_chain_finalize(uint32_t domain, uint32_t words, uint64_t *__restrict__ C,
+                                                        const uint64_t *__restrict__ cmask, uint64_t *__restrict__ Rb,
+                                                        uint64_t *__restrict__ rmask, uint64_t *__restrict__ Db,
+                                                        const uint64_t *__restrict__ dmask_old,
+                                                        uint64_t *__restrict__ dmask_new, uint64_t *__restrict__ RT,
+                                                        uint64_t *__restrict__ rtmask, uint64_t *__restrict__ DT,
+                                                        uint64_t *__restrict__ dtmask,
+                                                        unsigned long long *__restrict__ count) {
+    __shared__ unsigned long long s_cnt;
+    const uint32_t x = blockIdx.x;
+    const bool c_on = bit_of(cmask, x), d_on = bit_of(dmask_old, x);
+    if (!c_on && !d_on) return;
+    if (threadIdx.x == 0) s_cnt = 0ull;
+    __syncthreads();
+    uint64_t *crow = C + (uint64_t)x * words, *rrow = Rb + (uint64_t)x * words, *drow = Db + (uint64_t)x * words;
+    unsigned long long local = 0ull;
+    const uint64_t xbit = 1ull << (x & 63);
+    for (uint32_t w = threadIdx.x; w < words; w += FTB) {
+        uint64_t nw = 0ull;
+        if (c_on) {
+            const uint64_t c = crow[w];
+            if (c) {
+                const uint64_t r = rrow[w];
+                nw = c & ~r;
+                if (nw) rrow[w] = r | nw;
+                crow[w] = 0ull;
+            }
+        }
+        if (d_on || nw) drow[w] = nw;
+        if (nw) {
+            local += (unsigned long long)__popcll(nw);
+            if (TRANS) {
+                uint64_t b = nw;
+                while (b) {
+                    const uint32_t z = w * 64 + (uint32_t)__builtin_ctzll(b);
+                    b &= b - 1ull;
+                    if (z >= domain) break;  // (no id reaches the domain; keeps the scatter in bounds)
+                    const uint64_t off = (uint64_t)z * words + (x >> 6);
+                    atomicOr((unsigned long long *)&RT[off], (unsigned long long)xbit);
+                    atomicOr((unsigned long long *)&DT[off], (unsigned long long)xbit);
+                    set_bit(rtmask, z);
+                    set_bit(dtmask, z);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) local += __shfl_xor(local, o, WAVE);
+    if ((threadIdx.x & 63) == 0 && local) atomicAdd(&s_cnt, local);
+    __syncthreads();
+    if (threadIdx.x == 0 && s_cnt) {
+        set_bit(dmask_new, x);
+        set_bit(rmask, x);
+        atomicAdd(count, s_cnt);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+struct BitRel {  // an IDB predicate
+    Buf<uint64_t> R, D, C, RT, DT;
+    Buf<uint64_t> rmask, dmask[2], cmask, rtmask, dtmask;
+    int dcur = 0;
+    bool trans = false;
+    uint64_t rcount = 0, dcount = 0;
+};
+struct CsrRel {  // an EDB predicate in one direction
+    Buf<uint64_t> row_ptr, mask, pairs_t;
+    Buf<uint32_t> adj;
+    bool built = false;
+};
+
+struct ChainRun {
+    Ctx *ctx;
+    const std::vector<ChainRule> &rules;
+    uint32_t n_preds, domain, words;
+    uint64_t cells;
+    const std::vector<char> &idb;
+    const std::vector<const uint64_t *> &keys;
+    const std::vector<uint64_t> &rows;
+    std::vector<BitRel> bit;       // by predicate (IDB only)
+    std::vector<CsrRel> csr[2];    // by predicate: forward, backward (EDB only)
+    Buf<uint64_t> T[2], TM[2];
+    Buf<unsigned long long> counts;
+    std::vector<int> idb_list;
+
+    void fill0(Buf<uint64_t> &b, uint64_t n) { fill_u64(ctx, b.p, 0ull, n); }
+
+    void setup() {
+        bit.resize(n_preds);
+        csr[0].resize(n_preds);
+        csr[1].resize(n_preds);
+        size_t max_len = 0;
+        for (const ChainRule &r : rules) {
+            max_len = std::max(max_len, r.path.size());
+            for (const ChainAtom &a : r.path) {
+                if (idb[a.pred]) {
+                    if (a.backward) bit[a.pred].trans = true;
+                } else if (rows[a.pred]) {
+                    csr[a.backward ? 1 : 0][a.pred].built = true;  // built below
+                }
+            }
+        }
+        for (uint32_t p = 0; p < n_preds; ++p) {
+            if (!idb[p]) continue;
+            idb_list.push_back((int)p);
+            BitRel &b = bit[p];
+            b.R = Buf<uint64_t>(ctx, cells); fill0(b.R, cells);
+            b.D = Buf<uint64_t>(ctx, cells); fill0(b.D, cells);
+            b.C = Buf<uint64_t>(ctx, cells); fill0(b.C, cells);
+            b.rmask = Buf<uint64_t>(ctx, words); fill0(b.rmask, words);
+            b.dmask[0] = Buf<uint64_t>(ctx, words); fill0(b.dmask[0], words);
+            b.dmask[1] = Buf<uint64_t>(ctx, words); fill0(b.dmask[1], words);
+            b.cmask = Buf<uint64_t>(ctx, words); fill0(b.cmask, words);
+            if (b.trans) {
+                b.RT = Buf<uint64_t>(ctx, cells); fill0(b.RT, cells);
+                b.DT = Buf<uint64_t>(ctx, cells); fill0(b.DT, cells);
+                b.rtmask = Buf<uint64_t>(ctx, words); fill0(b.rtmask, words);
+                b.dtmask = Buf<uint64_t>(ctx, words); fill0(b.dtmask, words);
+            }
+            if (rows[p]) {  // initial contents of the head relation
+                hipLaunchKernelGGL(k_pairs_bits_mask, dim3(grid_for(rows[p], 256, 4096)), dim3(256), 0, ctx->stream,
+                                   keys[p], rows[p], 1, words, b.R.p, b.rmask.p);
+                if (b.trans)
+                    hipLaunchKernelGGL(k_pairs_bits_mask, dim3(grid_for(rows[p], 256, 4096)), dim3(256), 0,
+                                       ctx->stream, keys[p], rows[p], 0, words, b.RT.p, b.rtmask.p);
+                XH_CHECK_HIP(hipGetLastError());
+                b.rcount = rows[p];
+            }
+        }
+        for (int dir = 0; dir < 2; ++dir)
+            for (uint32_t p = 0; p < n_preds; ++p) {
+                CsrRel &c = csr[dir][p];
+                if (!c.built) continue;
+                const uint64_t *pairs = keys[p];
+                const uint64_t m = rows[p];
+                if (dir == 1) {  // transposed: swap the columns and re-sort (rows stay unique)
+                    c.pairs_t = Buf<uint64_t>(ctx, m);
+                    Buf<uint64_t> alt(ctx, m);
+                    swap_words(ctx, keys[p], m, c.pairs_t.p);
+                    uint64_t *a = c.pairs_t.p, *b = alt.p;
+                    radix_sort_u64(ctx, &a, &b, nullptr, nullptr, m);
+                    if (a != c.pairs_t.p) std::swap(c.pairs_t.p, alt.p);
+                    pairs = c.pairs_t.p;
+                }
+                c.row_ptr = Buf<uint64_t>(ctx, (uint64_t)domain + 1);
+                c.adj = Buf<uint32_t>(ctx, m);
+                c.mask = Buf<uint64_t>(ctx, words);
+                pairs_csr(ctx, pairs, m, domain, c.row_ptr.p, c.adj.p);
+                hipLaunchKernelGGL(k_csr_mask, dim3(grid_for(words, 256, 1024)), dim3(256), 0, ctx->stream,
+                                   c.row_ptr.p, domain, words, c.mask.p);
+                XH_CHECK_HIP(hipGetLastError());
+            }
+        if (max_len >= 3) {
+            T[0] = Buf<uint64_t>(ctx, cells);
+            TM[0] = Buf<uint64_t>(ctx, words);
+        }
+        if (max_len >= 4) {
+            T[1] = Buf<uint64_t>(ctx, cells);
+            TM[1] = Buf<uint64_t>(ctx, words);
+        }
+        counts = Buf<unsigned long long>(ctx, n_preds);
+    }
+
+    // operand for atom a reading the delta (use_delta) or the full relation;
+    // false when it is known to be empty
+    bool operand(const ChainAtom &a, bool use_delta, Operand &op) {
+        op = Operand{nullptr, nullptr, nullptr, nullptr};
+        if (idb[a.pred]) {
+            BitRel &b = bit[a.pred];
+            if ((use_delta ? b.dcount : b.rcount) == 0) return false;
+            if (!a.backward) {
+                op.bits = use_delta ? b.D.p : b.R.p;
+                op.mask = use_delta ? b.dmask[b.dcur].p : b.rmask.p;
+            } else {
+                op.bits = use_delta ? b.DT.p : b.RT.p;
+                op.mask = use_delta ? b.dtmask.p : b.rtmask.p;
+            }
+            return true;
+        }
+        if (rows[a.pred] == 0) return false;
+        CsrRel &c = csr[a.backward ? 1 : 0][a.pred];
+        op.row_ptr = c.row_ptr.p;
+        op.adj = c.adj.p;
+        op.mask = c.mask.p;
+        return true;
+    }
+
+    template <bool LCSR, bool RCSR, bool ACC>
+    void launch(const Operand &l, const Operand &r, uint64_t *o, uint64_t *om) {
+        hipLaunchKernelGGL((k_chain_product<LCSR, RCSR, ACC>), dim3(domain), dim3(PTB), words * sizeof(uint64_t),
+                           ctx->stream, words, l, r, o, om, nullptr);
+    }
+    void product(const Operand &l, const Operand &r, bool acc, uint64_t *o, uint64_t *om) {
+        Prof prof(ctx, XLOG_HIP_KERNEL_CHAIN_PRODUCT, 0.0);
+        const bool lc = l.bits == nullptr, rc = r.bits == nullptr;
+        if (acc) {
+            if (lc && rc) launch<true, true, true>(l, r, o, om);
+            else if (lc) launch<true, false, true>(l, r, o, om);
+            else if (rc) launch<false, true, true>(l, r, o, om);
+            else launch<false, false, true>(l, r, o, om);
+        } else {
+            if (lc && rc) launch<true, true, false>(l, r, o, om);
+            else if (lc) launch<true, false, false>(l, r, o, om);
+            else if (rc) launch<false, true, false>(l, r, o, om);
+            else launch<false, false, false>(l, r, o, om);
+        }
+        XH_CHECK_HIP(hipGetLastError());
+    }
+
+    // candidates of rule r with the delta at atom `delta_at` (-1: none)
+    void eval_chain(const ChainRule &r, int delta_at) {
+        const size_t k = r.path.size();
+        Operand ops[8];
+        for (size_t j = 0; j < k; ++j)
+            if (!operand(r.path[j], (int)j == delta_at, ops[j])) return;
+        BitRel &H = bit[r.head];
+        if (k == 1) {
+            const ChainAtom &a = r.path[0];
+            if (idb[a.pred]) {
+                hipLaunchKernelGGL(k_or_rows, dim3(domain), dim3(FTB), 0, ctx->stream, words, ops[0].bits,
+                                   ops[0].mask, H.C.p, H.cmask.p);
+            } else {
+                hipLaunchKernelGGL(k_pairs_bits_mask, dim3(grid_for(rows[a.pred], 256, 4096)), dim3(256), 0,
+                                   ctx->stream, keys[a.pred], rows[a.pred], a.backward ? 0 : 1, words, H.C.p,
+                                   H.cmask.p);
+            }
+            XH_CHECK_HIP(hipGetLastError());
+            return;
+        }
+        Operand left = ops[0];
+        for (size_t j = 1; j < k; ++j) {
+            const bool last = j + 1 == k;
+            uint64_t *o = last ? H.C.p : T[(j - 1) & 1].p;
+            uint64_t *om = last ? H.cmask.p : TM[(j - 1) & 1].p;
+            if (!last) fill_u64(ctx, om, 0ull, words);
+            product(left, ops[j], last, o, om);
+            left = Operand{o, nullptr, nullptr, om};
+        }
+    }
+
+    // new deltas of every IDB predicate from its candidates; returns their total
+    uint64_t finalize_all() {
+        fill_u64(ctx, reinterpret_cast<uint64_t *>(counts.p), 0ull, n_preds);
+        for (int p : idb_list) {
+            BitRel &b = bit[p];
+            if (b.trans) {  // D^T is rebuilt from the new delta
+                hipLaunchKernelGGL(k_clear_rows, dim3(domain), dim3(FTB), 0, ctx->stream, words, b.DT.p, b.dtmask.p);
+                fill_u64(ctx, b.dtmask.p, 0ull, words);
+            }
+            uint64_t *dnew = b.dmask[b.dcur ^ 1].p;
+            fill_u64(ctx, dnew, 0ull, words);
+            Prof prof(ctx, XLOG_HIP_KERNEL_CHAIN_FINALIZE, 0.0);
+            if (b.trans)
+                hipLaunchKernelGGL(k_chain_finalize<true>, dim3(domain), dim3(FTB), 0, ctx->stream, domain, words, b.C.p,
+                                   b.cmask.p, b.R.p, b.rmask.p, b.D.p, b.dmask[b.dcur].p, dnew, b.RT.p, b.rtmask.p,
+                                   b.DT.p, b.dtmask.p, counts.p + p);
+            else
+                hipLaunchKernelGGL(k_chain_finalize<false>, dim3(domain), dim3(FTB), 0, ctx->stream, domain, words, b.C.p,
+                                   b.cmask.p, b.R.p, b.rmask.p, b.D.p, b.dmask[b.dcur].p, dnew, nullptr, nullptr,
+                                   nullptr, nullptr, counts.p + p);
+            XH_CHECK_HIP(hipGetLastError());
+            fill_u64(ctx, b.cmask.p, 0ull, words);
+            b.dcur ^= 1;
+        }
+        // one read-back of every predicate's delta size
+        std::vector<uint64_t> host(n_preds);
+        XH_CHECK_HIP(hipMemcpyAsync(host.data(), counts.p, n_preds * sizeof(uint64_t), hipMemcpyDeviceToHost,
+                                    ctx->stream));
+        ctx->sync();
+        uint64_t total = 0;
+        for (int p : idb_list) {
+            bit[p].dcount = host[p];
+            bit[p].rcount += host[p];
+            total += host[p];
+        }
+        return total;
+    }
+};
+
+}  // namespace
+
+uint64_t chain_fixpoint_bytes(const std::vector<ChainRule> &rules, const std::vector<char> &idb, uint32_t domain) {
+    const uint64_t words = ((uint64_t)domain + 63) / 64, cells = (uint64_t)domain * words;
+    std::vector<char> trans(idb.size(), 0);
+    size_t max_len = 0;
+    for (const ChainRule &r : rules) {
+        max_len = std::max(max_len, r.path.size());
+        for (const ChainAtom &a : r.path)
+            if (idb[a.pred] && a.backward) trans[a.pred] = 1;
+    }
+    uint64_t mats = (max_len >= 3) + (max_len >= 4);
+    for (size_t p = 0; p < idb.size(); ++p)
+        if (idb[p]) mats += trans[p] ? 5 : 3;
+    return mats * cells * 8;
+}
+
+void chain_fixpoint(Ctx *ctx, const std::vector<ChainRule> &rules, uint32_t n_preds, const std::vector<char> &idb,
+                    const std::vector<const uint64_t *> &keys, const std::vector<uint64_t> &rows, uint32_t domain,
+                    uint64_t max_iter, std::vector<uint64_t *> &out, std::vector<uint64_t> &out_n,
+                    uint64_t *iterations, std::vector<uint64_t> &deltas) {
+    XH_REQUIRE(domain >= 1 && domain <= MAX_DOMAIN, XLOG_HIP_UNSUPPORTED, "chain bitmap: domain must be 1..2^17");
+    for (const ChainRule &r : rules)
+        XH_REQUIRE(!r.path.empty() && r.path.size() <= 8 && idb[r.head], XLOG_HIP_INVALID_ARG,
+                   "chain bitmap: bad rule");
+    deltas.clear();
+    out.assign(n_preds, nullptr);
+    out_n.assign(n_preds, 0);
+    const uint32_t words = (domain + 63) / 64;
+    ChainRun run{ctx, rules, n_preds, domain, words, (uint64_t)domain * words, idb, keys, rows};
+    run.setup();
+    // seed: every rule once against the initial relations
+    for (const ChainRule &r : rules) run.eval_chain(r, -1);
+    deltas.push_back(run.finalize_all());
+    uint64_t it = 0;
+    bool converged = false;
+    while (it < max_iter) {
+        ++it;
+        for (const ChainRule &r : rules)
+            for (size_t j = 0; j < r.path.size(); ++j) {
+                const int p = r.path[j].pred;
+                if (!idb[p] || run.bit[p].dcount == 0) continue;
+                run.eval_chain(r, (int)j);
+            }
+        const uint64_t total = run.finalize_all();
+        deltas.push_back(total);
+        if (total == 0) {
+            converged = true;
+            break;
+        }
+    }
+    *iterations = it;
+    XH_REQUIRE(converged, XLOG_HIP_ITERATION_LIMIT,
+               "Recursive SCC iteration limit (" + std::to_string(max_iter) + ") exceeded");
+    // release the working matrices before the results are materialised
+    for (int p : run.idb_list) {
+        BitRel &b = run.bit[p];
+        b.D = Buf<uint64_t>(); b.C = Buf<uint64_t>(); b.RT = Buf<uint64_t>(); b.DT = Buf<uint64_t>();
+    }
+    run.T[0] = Buf<uint64_t>();
+    run.T[1] = Buf<uint64_t>();
+    for (int p : run.idb_list)
+        out_n[p] = bitmap_emit(ctx, run.bit[p].R.p, domain, words, &out[p], XLOG_HIP_KERNEL_CHAIN_EMIT);
+}
+
+}  // namespace xh

@@ -297,6 +297,30 @@ uint64_t fj_delta_step(Ctx *ctx, const uint64_t *delta, uint64_t nd, int delta_x
                        uint64_t ne, const uint64_t *full, uint64_t nf, int full_x_hi, uint32_t domain,
                        uint64_t **out);
 
+// CSR of sorted unique packed (src << 32) | dst rows with ids < nv
+// (row_ptr: nv + 1 entries, adj: m entries).
+void pairs_csr(Ctx *ctx, const uint64_t *pairs, uint64_t m, uint32_t nv, uint64_t *row_ptr, uint32_t *adj);
+// Set bits of an nv x words bitmap as sorted packed (x << 32) | z rows in a
+// new pool buffer *out; returns the row count.
+uint64_t bitmap_emit(Ctx *ctx, const uint64_t *bits, uint32_t nv, uint64_t words, uint64_t **out, int prof_kind);
+
+// Dense-domain fixpoint of a program whose rules are chains of binary
+// relations: rule r derives head(v0, vk) from path[0](v0, v1), ...,
+// path[k-1](v_{k-1}, v_k), atom j read forward or, when backward, with its
+// columns swapped.  keys[p] / rows[p] are the canonical packed rows of every
+// predicate (idb[p] marks rule heads; their rows are the initial contents),
+// every id < domain.  Semi-naive iteration with the seed / delta-variant /
+// iteration-count semantics of the join route; results are canonical packed
+// rows per IDB predicate in out / out_n.
+struct ChainAtom { int pred; bool backward; };
+struct ChainRule { int head; std::vector<ChainAtom> path; };
+void chain_fixpoint(Ctx *ctx, const std::vector<ChainRule> &rules, uint32_t n_preds, const std::vector<char> &idb,
+                    const std::vector<const uint64_t *> &keys, const std::vector<uint64_t> &rows, uint32_t domain,
+                    uint64_t max_iter, std::vector<uint64_t *> &out, std::vector<uint64_t> &out_n,
+                    uint64_t *iterations, std::vector<uint64_t> &deltas);
+// Bytes of device memory chain_fixpoint keeps for its bitmaps.
+uint64_t chain_fixpoint_bytes(const std::vector<ChainRule> &rules, const std::vector<char> &idb, uint32_t domain);
+
 // small helpers
 inline unsigned grid_for(uint64_t n, unsigned block, unsigned cap) {
     uint64_t g = (n + block - 1) / block;

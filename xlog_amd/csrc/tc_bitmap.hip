@@ -277,22 +277,36 @@ uint64_t fj_delta_step(Ctx *ctx, const uint64_t *delta, uint64_t nd, int delta_x
                            row_ptr.p, adj.p, R.p, D.p, N.p, nz.p, nz_next.p, cnt.p);
         XH_CHECK_HIP(hipGetLastError());
     }
-    Buf<uint64_t> rc(ctx, (uint64_t)domain + 1);
-    hipLaunchKernelGGL(k_row_counts, dim3(domain), dim3(TB), 0, ctx->stream, N.p, words, rc.p);
+    return bitmap_emit(ctx, N.p, domain, words, out, XLOG_HIP_KERNEL_TC_EMIT);
+}
+
+// CSR of sorted unique packed (src << 32) | dst rows with every id < nv:
+// row_ptr[v] .. row_ptr[v + 1] index the destinations of v in adj.
+void pairs_csr(Ctx *ctx, const uint64_t *pairs, uint64_t m, uint32_t nv, uint64_t *row_ptr, uint32_t *adj) {
+    hipLaunchKernelGGL(k_row_ptr, dim3(grid_for((uint64_t)nv + 1, 256, 4096)), dim3(256), 0, ctx->stream, pairs, m, nv,
+                       row_ptr);
+    if (m) hipLaunchKernelGGL(k_adj, dim3(grid_for(m, 256, 4096)), dim3(256), 0, ctx->stream, pairs, m, adj);
     XH_CHECK_HIP(hipGetLastError());
-    scan_u64_small(ctx, rc.p, domain, rc.p + domain);
-    ctx->read_scalars(rc.p + domain, 1);
+}
+
+// The set bits of an nv x words bitmap as sorted packed (x << 32) | z rows
+// (row counts, a scan, then one block per row writing at its offset).
+uint64_t bitmap_emit(Ctx *ctx, const uint64_t *bits, uint32_t nv, uint64_t words, uint64_t **out, int prof_kind) {
+    *out = nullptr;
+    if (nv == 0) return 0;
+    Buf<uint64_t> rc(ctx, (uint64_t)nv + 1);
+    hipLaunchKernelGGL(k_row_counts, dim3(nv), dim3(TB), 0, ctx->stream, bits, words, rc.p);
+    XH_CHECK_HIP(hipGetLastError());
+    scan_u64_small(ctx, rc.p, nv, rc.p + nv);
+    ctx->read_scalars(rc.p + nv, 1);
     const uint64_t total = ctx->host_scalars[0];
     if (total == 0) return 0;
     *out = static_cast<uint64_t *>(ctx->alloc(total * sizeof(uint64_t)));
-    Prof prof(ctx, XLOG_HIP_KERNEL_TC_EMIT, 8.0 * (double)total + 8.0 * (double)cells);
-    hipLaunchKernelGGL(k_emit_rows, dim3(domain), dim3(TB), 0, ctx->stream, N.p, words, rc.p, *out);
+    Prof prof(ctx, prof_kind, 8.0 * (double)total + 8.0 * (double)nv * (double)words);
+    hipLaunchKernelGGL(k_emit_rows, dim3(nv), dim3(TB), 0, ctx->stream, bits, words, rc.p, *out);
     XH_CHECK_HIP(hipGetLastError());
     return total;
 }
-
-// scan helper from join.hip
-void scan_u64_small(Ctx *ctx, uint64_t *a, uint64_t n, uint64_t *total);
 
 // Dense transitive closure.  `edges` sorted unique packed (src, dst), all ids
 // < nv.  Returns the sorted closure in *out (count *out_n), the iteration
@@ -351,18 +365,7 @@ void tc_bitmap(Ctx *ctx, const uint64_t *edges, uint64_t m, uint32_t nv, uint64_
     }
     *iterations = it;
     XH_REQUIRE(converged, XLOG_HIP_ITERATION_LIMIT, "Recursive SCC iteration limit exceeded");
-    // emit R
-    Buf<uint64_t> rc(ctx, (uint64_t)nv + 1);
-    if (nv) hipLaunchKernelGGL(k_row_counts, dim3(nv), dim3(TB), 0, ctx->stream, R.p, words, rc.p);
-    XH_CHECK_HIP(hipGetLastError());
-    scan_u64_small(ctx, rc.p, nv, rc.p + nv);
-    ctx->read_scalars(rc.p + nv, 1);
-    uint64_t total = ctx->host_scalars[0];
-    *out_n = total;
-    *out = total ? static_cast<uint64_t *>(ctx->alloc(total * sizeof(uint64_t))) : nullptr;
-    Prof prof(ctx, XLOG_HIP_KERNEL_TC_EMIT, 8.0 * (double)total + 8.0 * (double)cells);
-    if (total) hipLaunchKernelGGL(k_emit_rows, dim3(nv), dim3(TB), 0, ctx->stream, R.p, words, rc.p, *out);
-    XH_CHECK_HIP(hipGetLastError());
+    *out_n = bitmap_emit(ctx, R.p, nv, words, out, XLOG_HIP_KERNEL_TC_EMIT);
 }
 
 }  // namespace xh
