@@ -1509,6 +1509,7 @@ void xlog_hip_ctx_destroy(xlog_hip_ctx *ctx) {
     sort_state_release(&c);
     select_state_release(&c);
     if (c.tickets) c.free(c.tickets);
+    if (c.prof_work) c.free(c.prof_work);
     delete c.pool;
     if (c.host_scalars) (void)hipHostFree(c.host_scalars);
     if (c.ev_a) (void)hipEventDestroy(c.ev_a);
@@ -1933,15 +1934,34 @@ xlog_hip_status xlog_hip_rel_digest(xlog_hip_ctx *ctx, const xlog_hip_rel *rel, 
 }  // extern "C"
 
 // ---- kernel timing -----------------------------------------------------------
+unsigned long long *xh::Prof::work(double bytes_per_unit) {
+    if (!on) return nullptr;
+    if (!ctx->prof_work) {
+        ctx->prof_work = static_cast<unsigned long long *>(ctx->alloc(Ctx::PROF_WORK_SLOTS * sizeof(uint64_t)));
+        fill_u64(ctx, reinterpret_cast<uint64_t *>(ctx->prof_work), 0ull, Ctx::PROF_WORK_SLOTS);
+    }
+    if (ctx->prof_work_next >= Ctx::PROF_WORK_SLOTS) return nullptr;
+    rec.work_slot = ctx->prof_work_next++;
+    rec.bytes_per_work = bytes_per_unit;
+    return ctx->prof_work + rec.work_slot;
+}
+
 void xh::Ctx::prof_resolve() {
     if (prof_pending.empty()) return;
     sync();
+    std::vector<uint64_t> work;
+    if (prof_work_next > 0) {
+        work.resize(prof_work_next);
+        XH_CHECK_HIP(hipMemcpy(work.data(), prof_work, prof_work_next * sizeof(uint64_t), hipMemcpyDeviceToHost));
+        fill_u64(this, reinterpret_cast<uint64_t *>(prof_work), 0ull, prof_work_next);
+        prof_work_next = 0;
+    }
     for (auto &r : prof_pending) {
         float ms = 0.f;
         XH_CHECK_HIP(hipEventElapsedTime(&ms, r.a, r.b));
         if (r.kind >= 0 && r.kind < XLOG_HIP_KERNEL_KINDS) {
             prof_ms[r.kind] += ms;
-            prof_bytes[r.kind] += r.bytes;
+            prof_bytes[r.kind] += r.bytes + (r.work_slot >= 0 ? r.bytes_per_work * (double)work[r.work_slot] : 0.0);
             prof_launches[r.kind] += 1;
         }
         prof_events.push_back(r.a);

@@ -23,8 +23,11 @@
 // product ORs into the head's candidate matrix.  Per iteration, for every
 // rule and every IDB occurrence whose delta is non-empty, the chain runs with
 // the delta at that occurrence and the full relation elsewhere -- the same
-// variants as the join route -- then k_chain_finalize per IDB predicate does
-//   D = C & ~R;  R |= D;  C = 0   (+ scatter of D into R^T and D^T)
+// variants as the join route, IDB atoms before the delta reading R minus D
+// (P) -- then k_chain_finalize per IDB predicate does
+//   P |= D;  D = C & ~R;  R |= D;  C = 0
+// and, for predicates read backward, k_transpose_delta rebuilds D^T and
+// updates R^T and P^T from 64 x 64 bit tiles of the changed row blocks.
 // and counts |D|; the counts are the only values read back.  Results leave
 // the device once, at convergence, as canonical rows (bitmap_emit).
 #include "internal.hpp"
@@ -37,6 +40,10 @@ constexpr int PTB = 512;           // product block: 8 waves
 constexpr int PNW = PTB / WAVE;
 constexpr int LCHUNK_WORDS = 64;   // left-row bitmap words compacted per round (<= 4096 ids)
 constexpr int FTB = 256;           // finalize / row-op block
+#ifndef XH_GATHER_UNROLL
+#define XH_GATHER_UNROLL 8
+#endif
+constexpr int GATHER_UNROLL = XH_GATHER_UNROLL;  // right-row loads in flight per wave
 constexpr uint32_t MAX_DOMAIN = 1u << 17;
 
 // One operand of a product: a bitmap (bits != null) or a CSR (row_ptr, adj);
@@ -74,11 +81,15 @@ __global__ __launch_bounds__(PTB) void k_chain_product(uint32_t words, Operand L
     __shared__ uint64_t s_bits[LCHUNK_WORDS];
     __shared__ uint32_t s_woff[LCHUNK_WORDS + 1];
     __shared__ uint32_t s_any;
+    __shared__ unsigned long long s_moved;
     const uint32_t x = blockIdx.x;
     if (!bit_of(L.mask, x)) return;  // block-uniform
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
     for (uint32_t w = tid; w < words; w += PTB) s_acc[w] = 0ull;
-    if (tid == 0) s_any = 0u;
+    if (tid == 0) {
+        s_any = 0u;
+        s_moved = 0ull;
+    }
     __syncthreads();
     uint64_t lbeg = 0, lend = words;
     if (LCSR) {
@@ -88,7 +99,8 @@ __global__ __launch_bounds__(PTB) void k_chain_product(uint32_t words, Operand L
     const uint64_t step = LCSR ? (uint64_t)PTB : (uint64_t)LCHUNK_WORDS;
     const uint64_t lt_mask = (1ull << lane) - 1ull;
     const uint32_t ns = (words + 63) / 64;
-    uint64_t total_y = 0;
+    // bytes this block reads and writes (left row, gathered right rows, output row), for profiling
+    uint64_t moved = (LCSR ? 4ull * (lend - lbeg) : 8ull * words) + 8ull * words, adj_bytes = 0;
     for (uint64_t c0 = lbeg; c0 < lend; c0 += step) {
         if (LCSR) {
             const uint64_t e = c0 + tid;
@@ -133,46 +145,46 @@ __global__ __launch_bounds__(PTB) void k_chain_product(uint32_t words, Operand L
         }
         __syncthreads();
         const uint32_t T = s_woff[LCHUNK_WORDS];
-        total_y += T;
         if (T) {
             if (RCSR) {
+                moved += 16ull * T;
                 for (uint32_t q = tid; q < T; q += PTB) {
                     const uint32_t y = s_y[q];
                     const uint64_t b = R.row_ptr[y], f = R.row_ptr[y + 1];
+                    adj_bytes += 4ull * (f - b);
                     for (uint64_t e = b; e < f; ++e) {
                         const uint32_t z = R.adj[e];
                         atomicOr((unsigned long long *)&s_acc[z >> 6], 1ull << (z & 63));
                     }
                 }
             } else {
-                // waves split stripes; with fewer stripes than waves, G waves
-                // share a stripe and take every G-th id
-                uint32_t s0, sstep, g, G;
-                if (ns >= (uint32_t)PNW) {
-                    s0 = wave; sstep = PNW; g = 0; G = 1;
-                } else {
-                    G = PNW / ns; g = wave / ns; sstep = ns;
-                    s0 = g < G ? wave % ns : ns;
-                }
-                for (uint32_t s = s0; s < ns; s += sstep) {
+                moved += 8ull * words * T;
+                // The round's (stripe, id) pairs, stripe-major, split into equal
+                // contiguous ranges, one per wave: a wave ORs each run of ids
+                // of one stripe in registers (GATHER_UNROLL row loads in
+                // flight, a lane per word) and folds the run into LDS.
+                const uint32_t N = ns * T, per = (N + PNW - 1) / PNW;
+                uint32_t i = wave * per;
+                const uint32_t iend = min(N, i + per);
+                while (i < iend) {
+                    const uint32_t s = i / T, j0 = i - s * T;
+                    const uint32_t j1 = min(T, j0 + (iend - i));
                     const uint32_t w = s * 64 + lane;
-                    const bool ok = w < words;
-                    const uint64_t *col = R.bits + w;
-                    uint64_t a0 = 0ull, a1 = 0ull;
-                    uint32_t j = g;
-                    if (ok) {
-                        for (; j + 3 * G < T; j += 4 * G) {
-                            const uint64_t v0 = col[(uint64_t)s_y[j] * words];
-                            const uint64_t v1 = col[(uint64_t)s_y[j + G] * words];
-                            const uint64_t v2 = col[(uint64_t)s_y[j + 2 * G] * words];
-                            const uint64_t v3 = col[(uint64_t)s_y[j + 3 * G] * words];
-                            a0 |= v0 | v1;
-                            a1 |= v2 | v3;
+                    if (w < words) {
+                        const uint64_t *col = R.bits + w;
+                        uint64_t acc = 0ull;
+                        uint32_t j = j0;
+                        for (; j + GATHER_UNROLL <= j1; j += GATHER_UNROLL) {
+                            uint64_t v[GATHER_UNROLL];
+#pragma unroll
+                            for (int u = 0; u < GATHER_UNROLL; ++u) v[u] = col[(uint64_t)s_y[j + u] * words];
+#pragma unroll
+                            for (int u = 0; u < GATHER_UNROLL; ++u) acc |= v[u];
                         }
-                        for (; j < T; j += G) a0 |= col[(uint64_t)s_y[j] * words];
-                        a0 |= a1;
-                        if (a0) atomicOr((unsigned long long *)&s_acc[w], a0);
+                        for (; j < j1; ++j) acc |= col[(uint64_t)s_y[j] * words];
+                        if (acc) atomicOr((unsigned long long *)&s_acc[w], acc);
                     }
+                    i += j1 - j0;
                 }
             }
         }
@@ -190,10 +202,11 @@ __global__ __launch_bounds__(PTB) void k_chain_product(uint32_t words, Operand L
         any |= a != 0ull;
     }
     if (__ballot(any) != 0ull && lane == 0) s_any = 1u;
+    if (RCSR && work && adj_bytes) atomicAdd(&s_moved, (unsigned long long)adj_bytes);
     __syncthreads();
     if (tid == 0) {
         if (s_any) set_bit(omask, x);
-        if (work) atomicAdd(work, (unsigned long long)total_y);
+        if (work) atomicAdd(work, (unsigned long long)moved + s_moved);
     }
 }
 
@@ -246,36 +259,32 @@ __global__ void k_csr_mask(const uint64_t *__restrict__ row_ptr, uint32_t nv, ui
     }
 }
 
-// zero the rows of B whose mask bit is set
-__global__ __launch_bounds__(FTB) void k_clear_rows(uint32_t words, uint64_t *__restrict__ B,
-                                                    const uint64_t *__restrict__ mask) {
-    const uint32_t x = blockIdx.x;
-    if (!bit_of(mask, x)) return;
-    for (uint32_t w = threadIdx.x; w < words; w += FTB) B[(uint64_t)x * words + w] = 0ull;
-}
+struct FinalizeArgs {
+    uint64_t *C;
+    const uint64_t *cmask;
+    uint64_t *R, *rmask;
+    uint64_t *D;
+    const uint64_t *dmask_old;
+    uint64_t *dmask_new;
+    uint64_t *P, *pmask;  // R minus D (null when no rule reads it forward)
+    unsigned long long *count;
+};
 
 // Per row x with candidates or an old delta row:
-//   D[x] = C[x] & ~R[x];  R[x] |= D[x];  C[x] = 0
-// sets the new delta / full row-mask bits, adds |D[x]| to *count and, with
-// TRANS, ORs every new (x, z) into R^T and D^T as (z, x).
-template <bool TRANS>
-__global__ __launch_bounds__(FTB) void k_chain_finalize(uint32_t domain, uint32_t words, uint64_t *__restrict__ C,
-                                                        const uint64_t *__restrict__ cmask, uint64_t *__restrict__ Rb,
-                                                        uint64_t *__restrict__ rmask, uint64_t *__restrict__ Db,
-                                                        const uint64_t *__restrict__ dmask_old,
-                                                        uint64_t *__restrict__ dmask_new, uint64_t *__restrict__ RT,
-                                                        uint64_t *__restrict__ rtmask, uint64_t *__restrict__ DT,
-                                                        uint64_t *__restrict__ dtmask,
-                                                        unsigned long long *__restrict__ count) {
+//   P[x] |= D[x];  D[x] = C[x] & ~R[x];  R[x] |= D[x];  C[x] = 0
+// (so that afterwards P = R minus the new D), sets the new delta / full
+// row-mask bits and adds |D[x]| to *count.
+template <bool PREV>
+__global__ __launch_bounds__(FTB) void k_chain_finalize(uint32_t words, FinalizeArgs a) {
     __shared__ unsigned long long s_cnt;
     const uint32_t x = blockIdx.x;
-    const bool c_on = bit_of(cmask, x), d_on = bit_of(dmask_old, x);
+    const bool c_on = bit_of(a.cmask, x), d_on = bit_of(a.dmask_old, x);
     if (!c_on && !d_on) return;
     if (threadIdx.x == 0) s_cnt = 0ull;
     __syncthreads();
-    uint64_t *crow = C + (uint64_t)x * words, *rrow = Rb + (uint64_t)x * words, *drow = Db + (uint64_t)x * words;
+    const uint64_t base = (uint64_t)x * words;
+    uint64_t *crow = a.C + base, *rrow = a.R + base, *drow = a.D + base;
     unsigned long long local = 0ull;
-    const uint64_t xbit = 1ull << (x & 63);
     for (uint32_t w = threadIdx.x; w < words; w += FTB) {
         uint64_t nw = 0ull;
         if (c_on) {
@@ -287,32 +296,93 @@ __global__ __launch_bounds__(FTB) void k_chain_finalize(uint32_t domain, uint32_
                 crow[w] = 0ull;
             }
         }
-        if (d_on || nw) drow[w] = nw;
-        if (nw) {
-            local += (unsigned long long)__popcll(nw);
-            if (TRANS) {
-                uint64_t b = nw;
-                while (b) {
-                    const uint32_t z = w * 64 + (uint32_t)__builtin_ctzll(b);
-                    b &= b - 1ull;
-                    if (z >= domain) break;  // (no id reaches the domain; keeps the scatter in bounds)
-                    const uint64_t off = (uint64_t)z * words + (x >> 6);
-                    atomicOr((unsigned long long *)&RT[off], (unsigned long long)xbit);
-                    atomicOr((unsigned long long *)&DT[off], (unsigned long long)xbit);
-                    set_bit(rtmask, z);
-                    set_bit(dtmask, z);
-                }
+        if (d_on) {
+            if (PREV) {
+                const uint64_t old = drow[w];
+                if (old) a.P[base + w] |= old;
             }
+            drow[w] = nw;
+        } else if (nw) {
+            drow[w] = nw;
         }
+        local += (unsigned long long)__popcll(nw);
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) local += __shfl_xor(local, o, WAVE);
     if ((threadIdx.x & 63) == 0 && local) atomicAdd(&s_cnt, local);
     __syncthreads();
-    if (threadIdx.x == 0 && s_cnt) {
-        set_bit(dmask_new, x);
-        set_bit(rmask, x);
-        atomicAdd(count, s_cnt);
+    if (threadIdx.x == 0) {
+        if (PREV && d_on) set_bit(a.pmask, x);  // the old delta row was non-empty
+        if (s_cnt) {
+            set_bit(a.dmask_new, x);
+            set_bit(a.rmask, x);
+            atomicAdd(a.count, s_cnt);
+        }
+    }
+}
+
+// 64 x 64 bit transpose across a wave: lane l holds row l on entry (bit c =
+// column c) and column l on exit (bit r = row r).  Step s swaps the s x s
+// off-diagonal blocks of every 2s x 2s block.
+__device__ __forceinline__ uint64_t wave_transpose64(uint64_t w, int lane) {
+    const uint64_t m[6] = {0x00000000FFFFFFFFull, 0x0000FFFF0000FFFFull, 0x00FF00FF00FF00FFull,
+                           0x0F0F0F0F0F0F0F0Full, 0x3333333333333333ull, 0x5555555555555555ull};
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+        const int s = 32 >> k;
+        const uint64_t p = __shfl_xor(w, s, WAVE);
+        w = (lane & s) ? ((w & ~m[k]) | ((p & ~m[k]) >> s)) : ((w & m[k]) | ((p & m[k]) << s));
+    }
+    return w;
+}
+
+constexpr int TT_WAVES = 4;  // transpose block: one 64-row block of D per wave
+constexpr int TT_COLS = 8;   // word columns per wave (64-byte runs per lane, merged rows on the write side)
+
+// Transposes after a finalize, for every 64-row block I of D where the old
+// or the new delta has rows (elsewhere nothing changed): per word column J,
+//   D^T[z][I] = column z of D's (I, J) tile;  P^T[z][I] = R^T[z][I] (R minus
+//   the new D, transposed);  R^T[z][I] |= D^T[z][I].
+// D^T's row mask is rebuilt (zeroed by the caller); R^T's and P^T's only
+// grow, as R does.
+__global__ __launch_bounds__(TT_WAVES * WAVE) void k_transpose_delta(
+    uint32_t domain, uint32_t words, const uint64_t *__restrict__ D, const uint64_t *__restrict__ dmask_old,
+    const uint64_t *__restrict__ dmask_new, uint64_t *__restrict__ DT, uint64_t *__restrict__ dtmask,
+    uint64_t *__restrict__ RT, uint64_t *__restrict__ rtmask, uint64_t *__restrict__ PT,
+    uint64_t *__restrict__ ptmask) {
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
+    const uint32_t I = blockIdx.y * TT_WAVES + wave;
+    if (I >= words) return;                              // wave-uniform
+    if ((dmask_old[I] | dmask_new[I]) == 0ull) return;  // wave-uniform
+    const uint32_t J0 = blockIdx.x * TT_COLS;
+    const uint32_t row = I * 64 + lane;
+    uint64_t v[TT_COLS];
+#pragma unroll
+    for (int j = 0; j < TT_COLS; ++j)
+        v[j] = (row < domain && J0 + j < words) ? D[(uint64_t)row * words + J0 + j] : 0ull;
+#pragma unroll
+    for (int j = 0; j < TT_COLS; ++j) {
+        const uint32_t J = J0 + j;
+        if (J >= words) break;  // wave-uniform
+        const uint64_t t = wave_transpose64(v[j], lane);
+        const uint32_t z = J * 64 + lane;
+        bool nd = false, np = false, nr = false;
+        if (z < domain) {
+            const uint64_t off = (uint64_t)z * words + I;
+            const uint64_t r = RT[off];
+            DT[off] = t;
+            if (PT) PT[off] = r;
+            if (t) RT[off] = r | t;
+            nd = t != 0ull;
+            np = r != 0ull;
+            nr = (r | t) != 0ull;
+        }
+        const uint64_t bd = __ballot(nd), bp = __ballot(np), br = __ballot(nr);
+        if (lane == 0) {
+            if (bd) atomicOr((unsigned long long *)&dtmask[J], (unsigned long long)bd);
+            if (PT && bp && (ptmask[J] & bp) != bp) atomicOr((unsigned long long *)&ptmask[J], (unsigned long long)bp);
+            if (br && (rtmask[J] & br) != br) atomicOr((unsigned long long *)&rtmask[J], (unsigned long long)br);
+        }
     }
 }
 
@@ -320,10 +390,11 @@ __global__ __launch_bounds__(FTB) void k_chain_finalize(uint32_t domain, uint32_
 // host side
 // ---------------------------------------------------------------------------
 struct BitRel {  // an IDB predicate
-    Buf<uint64_t> R, D, C, RT, DT;
-    Buf<uint64_t> rmask, dmask[2], cmask, rtmask, dtmask;
+    Buf<uint64_t> R, D, C, RT, DT, P, PT;
+    Buf<uint64_t> rmask, dmask[2], cmask, rtmask, dtmask, pmask, ptmask;
     int dcur = 0;
-    bool trans = false;
+    bool trans = false;         // some rule reads it backward
+    bool prev = false, prev_t = false;  // R minus D read forward / backward
     uint64_t rcount = 0, dcount = 0;
 };
 struct CsrRel {  // an EDB predicate in one direction
@@ -355,9 +426,13 @@ struct ChainRun {
         size_t max_len = 0;
         for (const ChainRule &r : rules) {
             max_len = std::max(max_len, r.path.size());
-            for (const ChainAtom &a : r.path) {
+            for (size_t j = 0; j < r.path.size(); ++j) {
+                const ChainAtom &a = r.path[j];
                 if (idb[a.pred]) {
                     if (a.backward) bit[a.pred].trans = true;
+                    // an IDB atom with a later IDB atom reads R minus D when the delta sits there
+                    for (size_t k = j + 1; k < r.path.size(); ++k)
+                        if (idb[r.path[k].pred]) (a.backward ? bit[a.pred].prev_t : bit[a.pred].prev) = true;
                 } else if (rows[a.pred]) {
                     csr[a.backward ? 1 : 0][a.pred].built = true;  // built below
                 }
@@ -380,12 +455,27 @@ struct ChainRun {
                 b.rtmask = Buf<uint64_t>(ctx, words); fill0(b.rtmask, words);
                 b.dtmask = Buf<uint64_t>(ctx, words); fill0(b.dtmask, words);
             }
-            if (rows[p]) {  // initial contents of the head relation
-                hipLaunchKernelGGL(k_pairs_bits_mask, dim3(grid_for(rows[p], 256, 4096)), dim3(256), 0, ctx->stream,
-                                   keys[p], rows[p], 1, words, b.R.p, b.rmask.p);
+            if (b.prev) {
+                b.P = Buf<uint64_t>(ctx, cells); fill0(b.P, cells);
+                b.pmask = Buf<uint64_t>(ctx, words); fill0(b.pmask, words);
+            }
+            if (b.prev_t) {
+                b.PT = Buf<uint64_t>(ctx, cells); fill0(b.PT, cells);
+                b.ptmask = Buf<uint64_t>(ctx, words); fill0(b.ptmask, words);
+            }
+            if (rows[p]) {  // initial contents of the head relation (also R minus D: D starts empty)
+                const unsigned g = grid_for(rows[p], 256, 4096);
+                hipLaunchKernelGGL(k_pairs_bits_mask, dim3(g), dim3(256), 0, ctx->stream, keys[p], rows[p], 1, words,
+                                   b.R.p, b.rmask.p);
                 if (b.trans)
-                    hipLaunchKernelGGL(k_pairs_bits_mask, dim3(grid_for(rows[p], 256, 4096)), dim3(256), 0,
-                                       ctx->stream, keys[p], rows[p], 0, words, b.RT.p, b.rtmask.p);
+                    hipLaunchKernelGGL(k_pairs_bits_mask, dim3(g), dim3(256), 0, ctx->stream, keys[p], rows[p], 0,
+                                       words, b.RT.p, b.rtmask.p);
+                if (b.prev)
+                    hipLaunchKernelGGL(k_pairs_bits_mask, dim3(g), dim3(256), 0, ctx->stream, keys[p], rows[p], 1,
+                                       words, b.P.p, b.pmask.p);
+                if (b.prev_t)
+                    hipLaunchKernelGGL(k_pairs_bits_mask, dim3(g), dim3(256), 0, ctx->stream, keys[p], rows[p], 0,
+                                       words, b.PT.p, b.ptmask.p);
                 XH_CHECK_HIP(hipGetLastError());
                 b.rcount = rows[p];
             }
@@ -424,19 +514,20 @@ struct ChainRun {
         counts = Buf<unsigned long long>(ctx, n_preds);
     }
 
-    // operand for atom a reading the delta (use_delta) or the full relation;
-    // false when it is known to be empty
-    bool operand(const ChainAtom &a, bool use_delta, Operand &op) {
+    enum Use { FULL, DELTA, PREV };  // R, D, or R minus D
+    // operand for atom a; false when it is known to be empty
+    bool operand(const ChainAtom &a, Use use, Operand &op) {
         op = Operand{nullptr, nullptr, nullptr, nullptr};
         if (idb[a.pred]) {
             BitRel &b = bit[a.pred];
-            if ((use_delta ? b.dcount : b.rcount) == 0) return false;
+            const uint64_t n = use == FULL ? b.rcount : (use == DELTA ? b.dcount : b.rcount - b.dcount);
+            if (n == 0) return false;
             if (!a.backward) {
-                op.bits = use_delta ? b.D.p : b.R.p;
-                op.mask = use_delta ? b.dmask[b.dcur].p : b.rmask.p;
+                op.bits = use == FULL ? b.R.p : (use == DELTA ? b.D.p : b.P.p);
+                op.mask = use == FULL ? b.rmask.p : (use == DELTA ? b.dmask[b.dcur].p : b.pmask.p);
             } else {
-                op.bits = use_delta ? b.DT.p : b.RT.p;
-                op.mask = use_delta ? b.dtmask.p : b.rtmask.p;
+                op.bits = use == FULL ? b.RT.p : (use == DELTA ? b.DT.p : b.PT.p);
+                op.mask = use == FULL ? b.rtmask.p : (use == DELTA ? b.dtmask.p : b.ptmask.p);
             }
             return true;
         }
@@ -449,33 +540,41 @@ struct ChainRun {
     }
 
     template <bool LCSR, bool RCSR, bool ACC>
-    void launch(const Operand &l, const Operand &r, uint64_t *o, uint64_t *om) {
+    void launch(const Operand &l, const Operand &r, uint64_t *o, uint64_t *om, unsigned long long *work) {
         hipLaunchKernelGGL((k_chain_product<LCSR, RCSR, ACC>), dim3(domain), dim3(PTB), words * sizeof(uint64_t),
-                           ctx->stream, words, l, r, o, om, nullptr);
+                           ctx->stream, words, l, r, o, om, work);
     }
     void product(const Operand &l, const Operand &r, bool acc, uint64_t *o, uint64_t *om) {
+        // algorithmic bytes: the rows each active block reads and writes, counted on the device
         Prof prof(ctx, XLOG_HIP_KERNEL_CHAIN_PRODUCT, 0.0);
+        unsigned long long *w = prof.work(1.0);
         const bool lc = l.bits == nullptr, rc = r.bits == nullptr;
         if (acc) {
-            if (lc && rc) launch<true, true, true>(l, r, o, om);
-            else if (lc) launch<true, false, true>(l, r, o, om);
-            else if (rc) launch<false, true, true>(l, r, o, om);
-            else launch<false, false, true>(l, r, o, om);
+            if (lc && rc) launch<true, true, true>(l, r, o, om, w);
+            else if (lc) launch<true, false, true>(l, r, o, om, w);
+            else if (rc) launch<false, true, true>(l, r, o, om, w);
+            else launch<false, false, true>(l, r, o, om, w);
         } else {
-            if (lc && rc) launch<true, true, false>(l, r, o, om);
-            else if (lc) launch<true, false, false>(l, r, o, om);
-            else if (rc) launch<false, true, false>(l, r, o, om);
-            else launch<false, false, false>(l, r, o, om);
+            if (lc && rc) launch<true, true, false>(l, r, o, om, w);
+            else if (lc) launch<true, false, false>(l, r, o, om, w);
+            else if (rc) launch<false, true, false>(l, r, o, om, w);
+            else launch<false, false, false>(l, r, o, om, w);
         }
         XH_CHECK_HIP(hipGetLastError());
     }
 
-    // candidates of rule r with the delta at atom `delta_at` (-1: none)
+    // Candidates of rule r with the delta at atom `delta_at` (-1: none, every
+    // atom full).  IDB atoms before the delta read R minus D and those after
+    // it R: over all delta positions this covers each derivation with at
+    // least one delta atom exactly once (at its first one), the same union as
+    // delta-at-one-position, full-elsewhere, with smaller left operands.
     void eval_chain(const ChainRule &r, int delta_at) {
         const size_t k = r.path.size();
         Operand ops[8];
-        for (size_t j = 0; j < k; ++j)
-            if (!operand(r.path[j], (int)j == delta_at, ops[j])) return;
+        for (size_t j = 0; j < k; ++j) {
+            const Use use = (int)j == delta_at ? DELTA : ((int)j < delta_at ? PREV : FULL);
+            if (!operand(r.path[j], use, ops[j])) return;
+        }
         BitRel &H = bit[r.head];
         if (k == 1) {
             const ChainAtom &a = r.path[0];
@@ -490,15 +589,39 @@ struct ChainRun {
             XH_CHECK_HIP(hipGetLastError());
             return;
         }
-        Operand left = ops[0];
-        for (size_t j = 1; j < k; ++j) {
-            const bool last = j + 1 == k;
-            uint64_t *o = last ? H.C.p : T[(j - 1) & 1].p;
-            uint64_t *om = last ? H.cmask.p : TM[(j - 1) & 1].p;
-            if (!last) fill_u64(ctx, om, 0ull, words);
-            product(left, ops[j], last, o, om);
-            left = Operand{o, nullptr, nullptr, om};
+        if (!right_to_left(r)) {  // ((a1 a2) a3) ...
+            Operand left = ops[0];
+            for (size_t j = 1; j < k; ++j) {
+                const bool last = j + 1 == k;
+                uint64_t *o = last ? H.C.p : T[(j - 1) & 1].p;
+                uint64_t *om = last ? H.cmask.p : TM[(j - 1) & 1].p;
+                if (!last) fill_u64(ctx, om, 0ull, words);
+                product(left, ops[j], last, o, om);
+                left = Operand{o, nullptr, nullptr, om};
+            }
+        } else {  // a1 (a2 (a3 ...))
+            Operand right = ops[k - 1];
+            for (size_t j = k - 1; j-- > 0;) {
+                const bool last = j == 0;
+                const size_t t = (k - 2 - j) & 1;
+                uint64_t *o = last ? H.C.p : T[t].p;
+                uint64_t *om = last ? H.cmask.p : TM[t].p;
+                if (!last) fill_u64(ctx, om, 0ull, words);
+                product(ops[j], right, last, o, om);
+                right = Operand{o, nullptr, nullptr, om};
+            }
         }
+    }
+
+    // A product whose right operand is a CSR relation expands adjacency lists
+    // id by id (latency-bound); with a bitmap right operand every id is one
+    // coalesced row gather.  Left to right puts every EDB atom after the first
+    // on the right, right to left only the last one, so a chain with an EDB
+    // atom strictly inside runs right to left.
+    bool right_to_left(const ChainRule &r) const {
+        for (size_t j = 1; j + 1 < r.path.size(); ++j)
+            if (!idb[r.path[j].pred]) return true;
+        return false;
     }
 
     // new deltas of every IDB predicate from its candidates; returns their total
@@ -506,22 +629,27 @@ struct ChainRun {
         fill_u64(ctx, reinterpret_cast<uint64_t *>(counts.p), 0ull, n_preds);
         for (int p : idb_list) {
             BitRel &b = bit[p];
-            if (b.trans) {  // D^T is rebuilt from the new delta
-                hipLaunchKernelGGL(k_clear_rows, dim3(domain), dim3(FTB), 0, ctx->stream, words, b.DT.p, b.dtmask.p);
-                fill_u64(ctx, b.dtmask.p, 0ull, words);
-            }
             uint64_t *dnew = b.dmask[b.dcur ^ 1].p;
             fill_u64(ctx, dnew, 0ull, words);
-            Prof prof(ctx, XLOG_HIP_KERNEL_CHAIN_FINALIZE, 0.0);
-            if (b.trans)
-                hipLaunchKernelGGL(k_chain_finalize<true>, dim3(domain), dim3(FTB), 0, ctx->stream, domain, words, b.C.p,
-                                   b.cmask.p, b.R.p, b.rmask.p, b.D.p, b.dmask[b.dcur].p, dnew, b.RT.p, b.rtmask.p,
-                                   b.DT.p, b.dtmask.p, counts.p + p);
-            else
-                hipLaunchKernelGGL(k_chain_finalize<false>, dim3(domain), dim3(FTB), 0, ctx->stream, domain, words, b.C.p,
-                                   b.cmask.p, b.R.p, b.rmask.p, b.D.p, b.dmask[b.dcur].p, dnew, nullptr, nullptr,
-                                   nullptr, nullptr, counts.p + p);
-            XH_CHECK_HIP(hipGetLastError());
+            const FinalizeArgs fa{b.C.p, b.cmask.p, b.R.p, b.rmask.p, b.D.p, b.dmask[b.dcur].p, dnew, b.P.p,
+                                  b.pmask.p, counts.p + p};
+            {
+                Prof prof(ctx, XLOG_HIP_KERNEL_CHAIN_FINALIZE, 0.0);
+                if (b.prev)
+                    hipLaunchKernelGGL((k_chain_finalize<true>), dim3(domain), dim3(FTB), 0, ctx->stream, words, fa);
+                else
+                    hipLaunchKernelGGL((k_chain_finalize<false>), dim3(domain), dim3(FTB), 0, ctx->stream, words, fa);
+                XH_CHECK_HIP(hipGetLastError());
+            }
+            if (b.trans) {
+                fill_u64(ctx, b.dtmask.p, 0ull, words);
+                Prof prof(ctx, XLOG_HIP_KERNEL_CHAIN_FINALIZE, 0.0);
+                const dim3 g((words + TT_COLS - 1) / TT_COLS, (words + TT_WAVES - 1) / TT_WAVES);
+                hipLaunchKernelGGL(k_transpose_delta, g, dim3(TT_WAVES * WAVE), 0, ctx->stream, domain, words, b.D.p,
+                                   b.dmask[b.dcur].p, dnew, b.DT.p, b.dtmask.p, b.RT.p, b.rtmask.p, b.PT.p,
+                                   b.ptmask.p);
+                XH_CHECK_HIP(hipGetLastError());
+            }
             fill_u64(ctx, b.cmask.p, 0ull, words);
             b.dcur ^= 1;
         }
@@ -544,16 +672,21 @@ struct ChainRun {
 
 uint64_t chain_fixpoint_bytes(const std::vector<ChainRule> &rules, const std::vector<char> &idb, uint32_t domain) {
     const uint64_t words = ((uint64_t)domain + 63) / 64, cells = (uint64_t)domain * words;
-    std::vector<char> trans(idb.size(), 0);
+    std::vector<char> trans(idb.size(), 0), prev(idb.size(), 0), prev_t(idb.size(), 0);
     size_t max_len = 0;
     for (const ChainRule &r : rules) {
         max_len = std::max(max_len, r.path.size());
-        for (const ChainAtom &a : r.path)
-            if (idb[a.pred] && a.backward) trans[a.pred] = 1;
+        for (size_t j = 0; j < r.path.size(); ++j) {
+            const ChainAtom &a = r.path[j];
+            if (!idb[a.pred]) continue;
+            if (a.backward) trans[a.pred] = 1;
+            for (size_t k = j + 1; k < r.path.size(); ++k)
+                if (idb[r.path[k].pred]) (a.backward ? prev_t : prev)[a.pred] = 1;
+        }
     }
     uint64_t mats = (max_len >= 3) + (max_len >= 4);
     for (size_t p = 0; p < idb.size(); ++p)
-        if (idb[p]) mats += trans[p] ? 5 : 3;
+        if (idb[p]) mats += (trans[p] ? 5 : 3) + prev[p] + prev_t[p];
     return mats * cells * 8;
 }
 
@@ -598,6 +731,7 @@ void chain_fixpoint(Ctx *ctx, const std::vector<ChainRule> &rules, uint32_t n_pr
     for (int p : run.idb_list) {
         BitRel &b = run.bit[p];
         b.D = Buf<uint64_t>(); b.C = Buf<uint64_t>(); b.RT = Buf<uint64_t>(); b.DT = Buf<uint64_t>();
+        b.P = Buf<uint64_t>(); b.PT = Buf<uint64_t>();
     }
     run.T[0] = Buf<uint64_t>();
     run.T[1] = Buf<uint64_t>();

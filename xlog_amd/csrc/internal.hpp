@@ -107,6 +107,8 @@ struct Ctx {
         int kind;
         hipEvent_t a, b;
         double bytes;
+        int work_slot;         // device work counter of the launch (-1: none)
+        double bytes_per_work; // algorithmic bytes per counted work unit
     };
     bool profiling = false;
     std::vector<ProfRec> prof_pending;
@@ -125,6 +127,11 @@ struct Ctx {
         return e;
     }
     void prof_resolve();  // synchronises, folds pending records into the totals
+    // device counters that profiled launches add their work units to; read
+    // back and cleared by prof_resolve
+    static constexpr int PROF_WORK_SLOTS = 4096;
+    unsigned long long *prof_work = nullptr;
+    int prof_work_next = 0;
 
     void *alloc(size_t bytes) { return pool->alloc(bytes); }
     void free(void *p) { pool->free(p); }
@@ -149,10 +156,15 @@ struct Prof {
         if (!on) return;
         rec.kind = kind;
         rec.bytes = bytes;
+        rec.work_slot = -1;
+        rec.bytes_per_work = 0.0;
         rec.a = c->prof_event();
         rec.b = c->prof_event();
         XH_CHECK_HIP(hipEventRecord(rec.a, c->stream));
     }
+    // A zeroed device counter for the launch to add work units to (each worth
+    // bytes_per_unit algorithmic bytes), or null when not profiling.
+    unsigned long long *work(double bytes_per_unit);
     ~Prof() {
         if (!on) return;
         (void)hipEventRecord(rec.b, ctx->stream);
