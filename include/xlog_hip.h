@@ -215,25 +215,34 @@ xlog_hip_status xlog_hip_compact(xlog_hip_ctx *ctx, const xlog_hip_rel *in, cons
 
 /* Program plan: int32 array
  *   [n_rules, then per rule: head_pred, hv0, hv1, n_body, (pred, v0, v1) * n_body]
- * over arity-2 predicates 0..n_preds-1; variables are small ints.  Bodies are
- * chains: each atom after the first shares exactly one variable with the
- * running binding, which keeps at most two live variables
- * (left-deep lowering, crates/xlog-logic/src/lower.rs:1795-1850).
+ * over arity-2 predicates 0..n_preds-1; variables are small ints; 1..4 atoms
+ * per body.  The join route evaluates bodies left-deep in body order: each
+ * atom after the first shares exactly one variable with the running binding,
+ * which keeps at most two live variables (crates/xlog-logic/src/lower.rs:
+ * 1795-1850).  The bitmap route takes bodies whose atoms form a path from hv0
+ * to hv1 in any order (each atom read forward or with its columns swapped).
  * rels[p] supplies every predicate (EDB facts; IDB initial contents, may be
  * empty).  On success out[p] receives a new canonical relation for every IDB
- * predicate (NULL for EDB ones). */
+ * predicate (NULL for EDB ones).  Both routes give the same relations, the
+ * same iteration count and the same per-iteration delta sizes. */
 typedef struct {
     uint64_t iterations;      /* loop iterations incl. the final empty one (recursive.rs:619-620,860-865) */
     uint64_t max_iterations;  /* limit; 0 = 1,000,000 (config.rs:164) */
     uint64_t *delta_sizes;    /* optional: [0] seed delta, [k] total |delta| after iteration k */
     uint64_t delta_cap;       /* entries available in delta_sizes */
-    uint64_t route;           /* XLOG_HIP_ROUTE_* used for linear chain rules (in: request, out: taken) */
+    uint64_t route;           /* XLOG_HIP_ROUTE_* (in: request, out: taken) */
     double wall_ms;           /* device wall time of the fixpoint */
 } xlog_hip_fixpoint_stats;
 
+/* AUTO takes the bitmap route when every rule body is a path, there are at
+ * most 2^17 distinct ids (max id + 1) and the bit matrices fit in half the
+ * free device memory; the join route otherwise.  Requesting BITMAP for a plan
+ * or domain it cannot take is UNSUPPORTED. */
 #define XLOG_HIP_ROUTE_AUTO 0
 #define XLOG_HIP_ROUTE_JOIN 1   /* join -> sort -> dedup -> diff -> merge */
-#define XLOG_HIP_ROUTE_BITMAP 2 /* dense factorized delta (fj_delta, provider/fj_delta.rs:117) */
+#define XLOG_HIP_ROUTE_BITMAP 2 /* relations as domain x domain bit matrices, rule bodies as chains of
+                                   boolean products (the dense factorized delta of provider/fj_delta.rs:117
+                                   generalised from transitive closure to path-shaped bodies) */
 
 xlog_hip_status xlog_hip_fixpoint(xlog_hip_ctx *ctx, const int32_t *plan, uint32_t n_preds,
                                   const xlog_hip_rel *const *rels, xlog_hip_rel **out,
