@@ -88,6 +88,32 @@ xlog_hip_status xlog_hip_rel_from_device_columns(xlog_hip_ctx *ctx, const uint32
 /* Upload host packed keys (arity 2: (c0 << 32) | c1; arity 1: c0). */
 xlog_hip_status xlog_hip_rel_from_host_packed(xlog_hip_ctx *ctx, const uint64_t *keys, uint32_t arity,
                                               uint64_t rows, xlog_hip_rel **out);
+/* ---- Arrow IPC streams (RecordBatchStream: schema, one record batch, end marker) ----
+ * Relations travel as 1..4 UInt32 columns; another column type is TYPE_MISMATCH,
+ * compression, dictionaries and big-endian streams are UNSUPPORTED, a stream
+ * with no or several record batches is INVALID_ARG (as io.rs:721-737).  Values
+ * are taken as stored, validity bitmaps ignored (io.rs:651-653).  Written
+ * fields are non-nullable UInt32, named by `names` (NULL: "c0", "c1", ...). */
+/* Decode a stream held in host memory into arity x rows column-major u32 values
+ * in cols (cols NULL: only *arity and *rows); no device involved. */
+xlog_hip_status xlog_hip_arrow_ipc_decode_u32(const uint8_t *ipc, uint64_t len, uint32_t *arity, uint64_t *rows,
+                                              uint32_t *cols, uint64_t cols_cap);
+/* Encode host columns as a stream in a new buffer (*ipc, *len; free with xlog_hip_bytes_free). */
+xlog_hip_status xlog_hip_arrow_ipc_encode_u32(const uint32_t *const *cols, uint32_t arity, uint64_t rows,
+                                              const char *const *names, uint8_t **ipc, uint64_t *len);
+void xlog_hip_bytes_free(uint8_t *p);
+/* Relation from a stream in host memory; each column buffer is copied once to
+ * the device and packed there (reference: from_arrow_ipc_stream, provider/io.rs:716-739). */
+xlog_hip_status xlog_hip_rel_from_arrow_ipc(xlog_hip_ctx *ctx, const uint8_t *ipc, uint64_t len, xlog_hip_rel **out);
+/* Stream of a relation's columns (reference: to_arrow_ipc_stream, provider/io.rs:697-713). */
+xlog_hip_status xlog_hip_rel_to_arrow_ipc(xlog_hip_ctx *ctx, const xlog_hip_rel *rel, const char *const *names,
+                                          uint8_t **ipc, uint64_t *len);
+/* File forms; the file is memory-mapped and its column buffers uploaded from
+ * the mapping (reference: read_arrow_ipc_stream_file / write_arrow_ipc_stream_file,
+ * provider/io.rs:743-772). */
+xlog_hip_status xlog_hip_read_arrow_ipc_stream_file(xlog_hip_ctx *ctx, const char *path, xlog_hip_rel **out);
+xlog_hip_status xlog_hip_write_arrow_ipc_stream_file(xlog_hip_ctx *ctx, const xlog_hip_rel *rel,
+                                                     const char *const *names, const char *path);
 /* Download column `col` into host[0..rows) (reference: download_column::<u32>, provider/transfer.rs:22). */
 xlog_hip_status xlog_hip_rel_download_column(xlog_hip_ctx *ctx, const xlog_hip_rel *rel, uint32_t col,
                                              uint32_t *host, uint64_t host_cap);

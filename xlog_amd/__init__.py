@@ -21,6 +21,8 @@ from .provider import (  # noqa: F401
     copy_points_to_plan,
     pack,
     unpack,
+    arrow_ipc_decode_u32,
+    arrow_ipc_encode_u32,
     library_path,
     ABI_SYMBOLS,
 )

@@ -19,7 +19,7 @@ CSRC = PKG / "csrc"
 BUILD = ROOT / "_build" / "xlog_amd"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-HIP_SOURCES = ["sort.hip", "select.hip", "join.hip", "tc_bitmap.hip", "chain_bitmap.hip", "abi.hip"]
+HIP_SOURCES = ["sort.hip", "select.hip", "join.hip", "tc_bitmap.hip", "chain_bitmap.hip", "arrow_ipc.cpp", "abi.hip"]
 HIP_FLAGS = [
     "--offload-arch=gfx950",
     "-O3",
@@ -59,7 +59,7 @@ def build_hip(jobs: int = 8) -> Path:
     BUILD.mkdir(parents=True, exist_ok=True)
 
     def compile_one(src: str) -> Path:
-        obj = BUILD / (src.replace(".hip", ".o"))
+        obj = BUILD / (src.rsplit(".", 1)[0] + ".o")
         _run([HIPCC, *HIP_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
         return obj
 

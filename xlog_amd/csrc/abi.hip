@@ -5,7 +5,14 @@
 
 #include <algorithm>
 #include <chrono>
+#include <cerrno>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
 #include <memory>
 
 namespace xh {
@@ -1470,6 +1477,66 @@ static void need_rel(const xlog_hip_rel *r, const char *what) {
     XH_REQUIRE(r, XLOG_HIP_INVALID_ARG, std::string(what) + " is NULL");
 }
 
+namespace xh {
+// Arrow IPC stream I/O helpers (provider/io.rs:697-773)
+namespace {
+// Device relation from UInt32 column buffers in host memory: each column is
+// copied once to a device staging buffer and packed there.
+xlog_hip_rel *rel_from_ipc(Ctx *ctx, const IpcColumns &ic) {
+    xlog_hip_rel *r = rel_new(ctx, ic.arity, ic.rows);
+    r->rows = ic.rows;
+    if (!ic.rows) return r;
+    try {
+        Buf<uint32_t> stage(ctx, (uint64_t)ic.arity * ic.rows);
+        const uint32_t *dc[4] = {nullptr, nullptr, nullptr, nullptr};
+        for (uint32_t c = 0; c < ic.arity; ++c) {
+            uint32_t *d = stage.p + (uint64_t)c * ic.rows;
+            XH_CHECK_HIP(hipMemcpyAsync(d, ic.cols[c], ic.rows * 4, hipMemcpyHostToDevice, ctx->stream));
+            dc[c] = d;
+        }
+        if (ic.arity == 1) LAUNCH_1D(k_widen, ic.rows, dc[0], ic.rows, r->w[0]);
+        else pack_columns(ctx, dc[0], dc[1], ic.rows, r->w[0]);
+        if (ic.arity == 3) pack_columns(ctx, dc[2], nullptr, ic.rows, r->w[1]);
+        if (ic.arity == 4) pack_columns(ctx, dc[2], dc[3], ic.rows, r->w[1]);
+        ctx->sync();  // the host bytes may go away after the call
+    } catch (...) {
+        rel_free(r);
+        throw;
+    }
+    return r;
+}
+
+// All columns of a relation, column-major in host memory
+std::vector<uint32_t> columns_to_host(Ctx *ctx, const xlog_hip_rel *rel) {
+    std::vector<uint32_t> h((uint64_t)rel->arity * rel->rows);
+    if (!rel->rows) return h;
+    Buf<uint32_t> tmp(ctx, (uint64_t)rel->arity * rel->rows);
+    for (uint32_t c = 0; c < rel->arity; ++c) {
+        uint32_t *d = tmp.p + (uint64_t)c * rel->rows;
+        if (rel->arity == 1) LAUNCH_1D(k_u64_to_u32, rel->rows, rel->w[0], rel->rows, d);
+        else unpack_column(ctx, c < 2 ? rel->w[0] : rel->w[1], (c % 2) == 0, rel->rows, d);
+    }
+    XH_CHECK_HIP(hipMemcpyAsync(h.data(), tmp.p, h.size() * 4, hipMemcpyDeviceToHost, ctx->stream));
+    ctx->sync();
+    return h;
+}
+
+std::vector<uint8_t> rel_to_ipc(Ctx *ctx, const xlog_hip_rel *rel, const char *const *names) {
+    const std::vector<uint32_t> h = columns_to_host(ctx, rel);
+    const uint32_t *cols[4] = {nullptr, nullptr, nullptr, nullptr};
+    for (uint32_t c = 0; c < rel->arity; ++c) cols[c] = h.data() + (uint64_t)c * rel->rows;
+    return ipc_encode_u32(cols, rel->arity, rel->rows, names);
+}
+
+uint8_t *to_malloc(const std::vector<uint8_t> &v) {
+    uint8_t *p = static_cast<uint8_t *>(malloc(v.size() ? v.size() : 1));
+    XH_REQUIRE(p, XLOG_HIP_OOM, "host allocation failed");
+    if (!v.empty()) memcpy(p, v.data(), v.size());
+    return p;
+}
+}  // namespace
+}  // namespace xh
+
 extern "C" {
 
 const char *xlog_hip_last_error(void) { return g_last_error.c_str(); }
@@ -1622,6 +1689,99 @@ xlog_hip_status xlog_hip_rel_download_column(xlog_hip_ctx *ctx, const xlog_hip_r
         }
         XH_CHECK_HIP(hipMemcpyAsync(host, tmp.p, rel->rows * 4, hipMemcpyDeviceToHost, ctx->stream));
         ctx->sync();
+    });
+}
+
+
+// ---- Arrow IPC stream I/O (provider/io.rs:697-773) ----------------------------
+xlog_hip_status xlog_hip_arrow_ipc_decode_u32(const uint8_t *ipc, uint64_t len, uint32_t *arity, uint64_t *rows,
+                                              uint32_t *cols, uint64_t cols_cap) {
+    return guarded([&] {
+        XH_REQUIRE(arity && rows, XLOG_HIP_INVALID_ARG, "arity / rows is NULL");
+        IpcColumns ic;
+        ipc_decode_u32(ipc, len, ic);
+        *arity = ic.arity;
+        *rows = ic.rows;
+        if (!cols) return;
+        XH_REQUIRE(cols_cap >= (uint64_t)ic.arity * ic.rows, XLOG_HIP_CAPACITY_OVERFLOW, "column buffer too small");
+        for (uint32_t c = 0; c < ic.arity; ++c) memcpy(cols + (uint64_t)c * ic.rows, ic.cols[c], ic.rows * 4);
+    });
+}
+
+xlog_hip_status xlog_hip_arrow_ipc_encode_u32(const uint32_t *const *cols, uint32_t arity, uint64_t rows,
+                                              const char *const *names, uint8_t **ipc, uint64_t *len) {
+    return guarded([&] {
+        XH_REQUIRE(ipc && len, XLOG_HIP_INVALID_ARG, "ipc / len is NULL");
+        const std::vector<uint8_t> v = ipc_encode_u32(cols, arity, rows, names);
+        *ipc = to_malloc(v);
+        *len = v.size();
+    });
+}
+
+void xlog_hip_bytes_free(uint8_t *p) { free(p); }
+
+xlog_hip_status xlog_hip_rel_from_arrow_ipc(xlog_hip_ctx *ctx, const uint8_t *ipc, uint64_t len, xlog_hip_rel **out) {
+    return guarded([&] {
+        XH_REQUIRE(out, XLOG_HIP_INVALID_ARG, "out is NULL");
+        IpcColumns ic;
+        ipc_decode_u32(ipc, len, ic);
+        *out = rel_from_ipc(C(ctx), ic);
+    });
+}
+
+xlog_hip_status xlog_hip_rel_to_arrow_ipc(xlog_hip_ctx *ctx, const xlog_hip_rel *rel, const char *const *names,
+                                          uint8_t **ipc, uint64_t *len) {
+    return guarded([&] {
+        need_rel(rel, "relation");
+        XH_REQUIRE(ipc && len, XLOG_HIP_INVALID_ARG, "ipc / len is NULL");
+        const std::vector<uint8_t> v = rel_to_ipc(C(ctx), rel, names);
+        *ipc = to_malloc(v);
+        *len = v.size();
+    });
+}
+
+xlog_hip_status xlog_hip_read_arrow_ipc_stream_file(xlog_hip_ctx *ctx, const char *path, xlog_hip_rel **out) {
+    return guarded([&] {
+        XH_REQUIRE(path && out, XLOG_HIP_INVALID_ARG, "path / out is NULL");
+        const std::string where = std::string("Failed to read Arrow IPC stream from ") + path + ": ";
+        const int fd = open(path, O_RDONLY);
+        XH_REQUIRE(fd >= 0, XLOG_HIP_INVALID_ARG, where + strerror(errno));
+        struct stat st;
+        if (fstat(fd, &st) != 0) {
+            const int e = errno;
+            close(fd);
+            throw Error{XLOG_HIP_INVALID_ARG, where + strerror(e)};
+        }
+        const uint64_t n = (uint64_t)st.st_size;
+        void *m = n ? mmap(nullptr, n, PROT_READ, MAP_PRIVATE, fd, 0) : nullptr;
+        close(fd);
+        XH_REQUIRE(n == 0 || m != MAP_FAILED, XLOG_HIP_INVALID_ARG, where + strerror(errno));
+        // the column buffers are uploaded straight from the mapping
+        try {
+            IpcColumns ic;
+            ipc_decode_u32(static_cast<const uint8_t *>(m), n, ic);
+            *out = rel_from_ipc(C(ctx), ic);
+        } catch (...) {
+            if (m) munmap(m, n);
+            throw;
+        }
+        if (m) munmap(m, n);
+    });
+}
+
+xlog_hip_status xlog_hip_write_arrow_ipc_stream_file(xlog_hip_ctx *ctx, const xlog_hip_rel *rel,
+                                                     const char *const *names, const char *path) {
+    return guarded([&] {
+        need_rel(rel, "relation");
+        XH_REQUIRE(path, XLOG_HIP_INVALID_ARG, "path is NULL");
+        const std::vector<uint8_t> v = rel_to_ipc(C(ctx), rel, names);
+        const std::string where = std::string("Failed to write Arrow IPC stream to ") + path + ": ";
+        FILE *f = fopen(path, "wb");
+        XH_REQUIRE(f, XLOG_HIP_INVALID_ARG, where + strerror(errno));
+        const bool wrote = v.empty() || fwrite(v.data(), 1, v.size(), f) == v.size();
+        const int e = errno;
+        const bool closed = fclose(f) == 0;
+        XH_REQUIRE(wrote && closed, XLOG_HIP_INVALID_ARG, where + strerror(wrote ? errno : e));
     });
 }
 

@@ -333,6 +333,20 @@ void chain_fixpoint(Ctx *ctx, const std::vector<ChainRule> &rules, uint32_t n_pr
 // Bytes of device memory chain_fixpoint keeps for its bitmaps.
 uint64_t chain_fixpoint_bytes(const std::vector<ChainRule> &rules, const std::vector<char> &idb, uint32_t domain);
 
+// Arrow IPC stream codec for relations of 1..4 UInt32 columns (arrow_ipc.cpp,
+// host code).  decode checks the stream and returns pointers to the column
+// value buffers inside it (one schema, exactly one record batch); encode
+// writes schema + one batch + end-of-stream.
+struct IpcColumns {
+    uint32_t arity = 0;
+    uint64_t rows = 0;
+    std::vector<const uint8_t *> cols;  // rows * 4 bytes each, possibly unaligned
+    std::vector<std::string> names;
+};
+void ipc_decode_u32(const uint8_t *stream, uint64_t len, IpcColumns &out);
+std::vector<uint8_t> ipc_encode_u32(const uint32_t *const *cols, uint32_t arity, uint64_t rows,
+                                    const char *const *names);
+
 // small helpers
 inline unsigned grid_for(uint64_t n, unsigned block, unsigned cap) {
     uint64_t g = (n + block - 1) / block;

@@ -126,6 +126,13 @@ def _load() -> C.CDLL:
         "xlog_hip_profile_enable": (I32, [P, I32]),
         "xlog_hip_profile_reset": (I32, [P]),
         "xlog_hip_profile_read": (I32, [P, U32, C.POINTER(U64), C.POINTER(C.c_double), C.POINTER(C.c_double)]),
+        "xlog_hip_arrow_ipc_decode_u32": (I32, [P, U64, C.POINTER(U32), C.POINTER(U64), P, U64]),
+        "xlog_hip_arrow_ipc_encode_u32": (I32, [PP, U32, U64, C.POINTER(C.c_char_p), PP, C.POINTER(U64)]),
+        "xlog_hip_bytes_free": (None, [P]),
+        "xlog_hip_rel_from_arrow_ipc": (I32, [P, P, U64, PP]),
+        "xlog_hip_rel_to_arrow_ipc": (I32, [P, P, C.POINTER(C.c_char_p), PP, C.POINTER(U64)]),
+        "xlog_hip_read_arrow_ipc_stream_file": (I32, [P, C.c_char_p, PP]),
+        "xlog_hip_write_arrow_ipc_stream_file": (I32, [P, P, C.POINTER(C.c_char_p), C.c_char_p]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -151,6 +158,9 @@ ABI_SYMBOLS = (
     "xlog_hip_is_sorted",
     "xlog_hip_exclusive_scan_u32", "xlog_hip_compact", "xlog_hip_fixpoint", "xlog_hip_fixpoint_tc",
     "xlog_hip_rel_digest", "xlog_hip_profile_enable", "xlog_hip_profile_reset", "xlog_hip_profile_read",
+    "xlog_hip_arrow_ipc_decode_u32", "xlog_hip_arrow_ipc_encode_u32", "xlog_hip_bytes_free",
+    "xlog_hip_rel_from_arrow_ipc", "xlog_hip_rel_to_arrow_ipc", "xlog_hip_read_arrow_ipc_stream_file",
+    "xlog_hip_write_arrow_ipc_stream_file",
 )
 
 KERNEL_KINDS = {
@@ -171,6 +181,44 @@ def _check(status: int) -> None:
     if status != OK:
         msg = _lib.xlog_hip_last_error()
         raise XlogError(status, msg.decode() if msg else "")
+
+
+def _names_arg(names: Sequence[str] | None, arity: int):
+    if names is None:
+        return None
+    if len(names) != arity:
+        raise XlogError(1, f"{len(names)} column names for {arity} columns")
+    return (C.c_char_p * arity)(*[n.encode() for n in names])
+
+
+def _take_bytes(ptr: C.c_void_p, n: int) -> bytes:
+    try:
+        return C.string_at(ptr, n) if n else b""
+    finally:
+        _lib.xlog_hip_bytes_free(ptr)
+
+
+def arrow_ipc_decode_u32(data: bytes) -> list[np.ndarray]:
+    """Host-only decode of an Arrow IPC stream of UInt32 columns (one record batch) into numpy columns."""
+    buf = np.frombuffer(data, dtype=np.uint8)
+    arity, rows = C.c_uint32(), C.c_uint64()
+    ptr = buf.ctypes.data if len(buf) else None
+    _check(_lib.xlog_hip_arrow_ipc_decode_u32(ptr, len(buf), C.byref(arity), C.byref(rows), None, 0))
+    out = np.empty((arity.value, rows.value), dtype=np.uint32)
+    _check(_lib.xlog_hip_arrow_ipc_decode_u32(ptr, len(buf), C.byref(arity), C.byref(rows),
+                                              out.ctypes.data if out.size else None, out.size))
+    return list(out)
+
+
+def arrow_ipc_encode_u32(columns: Sequence[np.ndarray], names: Sequence[str] | None = None) -> bytes:
+    """Host-only encode of UInt32 columns as an Arrow IPC stream (schema, one record batch, end marker)."""
+    cols = [np.ascontiguousarray(np.asarray(c, dtype=np.uint32)) for c in columns]
+    rows = len(cols[0]) if cols else 0
+    ptrs = (C.c_void_p * max(1, len(cols)))(*[c.ctypes.data for c in cols])
+    out, n = C.c_void_p(), C.c_uint64()
+    _check(_lib.xlog_hip_arrow_ipc_encode_u32(ptrs, len(cols), rows, _names_arg(names, len(cols)), C.byref(out),
+                                              C.byref(n)))
+    return _take_bytes(out, n.value)
 
 
 def _u32_array(values: Iterable[int]):
@@ -359,6 +407,29 @@ class HipKernelProvider:
         h = C.c_void_p()
         _check(_lib.xlog_hip_rel_from_device_columns(self.ctx, ptrs, len(dev_ptrs), rows, C.byref(h)))
         return self._rel(h)
+
+    # -- Arrow IPC streams (provider/io.rs:697-773) ---------------------
+    def from_arrow_ipc_stream(self, data: bytes) -> Relation:
+        buf = np.frombuffer(data, dtype=np.uint8)
+        h = C.c_void_p()
+        _check(_lib.xlog_hip_rel_from_arrow_ipc(self.ctx, buf.ctypes.data if len(buf) else None, len(buf),
+                                                C.byref(h)))
+        return self._rel(h)
+
+    def to_arrow_ipc_stream(self, rel: Relation, names: Sequence[str] | None = None) -> bytes:
+        out, n = C.c_void_p(), C.c_uint64()
+        _check(_lib.xlog_hip_rel_to_arrow_ipc(self.ctx, rel.handle, _names_arg(names, rel.arity), C.byref(out),
+                                              C.byref(n)))
+        return _take_bytes(out, n.value)
+
+    def read_arrow_ipc_stream_file(self, path: str | Path) -> Relation:
+        h = C.c_void_p()
+        _check(_lib.xlog_hip_read_arrow_ipc_stream_file(self.ctx, str(path).encode(), C.byref(h)))
+        return self._rel(h)
+
+    def write_arrow_ipc_stream_file(self, rel: Relation, path: str | Path, names: Sequence[str] | None = None) -> None:
+        _check(_lib.xlog_hip_write_arrow_ipc_stream_file(self.ctx, rel.handle, _names_arg(names, rel.arity),
+                                                         str(path).encode()))
 
     def download_column(self, rel: Relation, col: int) -> np.ndarray:
         n = rel.num_rows()
