@@ -65,6 +65,9 @@ const char *xlog_hip_version(void);
 /* Create a context on `device` with its own stream
  * (reference: CudaKernelProvider::new, provider/mod.rs:1139-1242). */
 xlog_hip_status xlog_hip_ctx_create(int device, xlog_hip_ctx **out);
+/* Destroy a context.  It releases the device memory of every relation and
+ * join index still alive on it: those handles must not be passed to any call
+ * afterwards, xlog_hip_rel_free / xlog_hip_join_index_free included. */
 void xlog_hip_ctx_destroy(xlog_hip_ctx *ctx);
 /* Wait for all work of the context (reference: device().synchronize(), executor/mod.rs:1463). */
 xlog_hip_status xlog_hip_synchronize(xlog_hip_ctx *ctx);

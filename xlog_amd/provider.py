@@ -262,8 +262,13 @@ class Relation:
         return bool(v.value)
 
     def free(self) -> None:
+        # After the provider's context is destroyed the device memory is already released and the
+        # handle must not reach the library again; that happens when the provider and its relations
+        # are collected in one batch (weak references are cleared before finalizers run, so close()
+        # cannot see them).
         if self._h:
-            _lib.xlog_hip_rel_free(self._h)
+            if self._provider._ctx is not None:
+                _lib.xlog_hip_rel_free(self._h)
             self._h = None
 
     def __del__(self):
@@ -292,7 +297,8 @@ class JoinIndex:
 
     def free(self) -> None:
         if self._h:
-            _lib.xlog_hip_join_index_free(self._h)
+            if self._provider._ctx is not None:  # see Relation.free
+                _lib.xlog_hip_join_index_free(self._h)
             self._h = None
 
     def __del__(self):
