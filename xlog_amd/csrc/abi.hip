@@ -211,8 +211,6 @@ uint64_t join_probe_general(Ctx *ctx, const uint64_t *probe, uint64_t n, int pco
 void join_match_flags(Ctx *ctx, const uint64_t *probe, uint64_t n, int pcol, const RunIndex &ix, int want,
                       uint8_t *flags);
 void scan_u64_small(Ctx *ctx, uint64_t *a, uint64_t n, uint64_t *total);
-void tc_bitmap(Ctx *ctx, const uint64_t *edges, uint64_t m, uint32_t nv, uint64_t max_iter, uint64_t **out,
-               uint64_t *out_n, uint64_t *iterations, std::vector<uint64_t> &deltas);
 
 #define LAUNCH_1D(kern, n, ...)                                                                             \
     do {                                                                                                    \
@@ -1394,9 +1392,31 @@ static void run_fixpoint(Ctx *ctx, const int32_t *plan, uint32_t n_preds, const 
     }
     bool bitmap = tc && head_empty && route != XLOG_HIP_ROUTE_JOIN && (uint64_t)nv <= (1ull << 17);
     if (bitmap) {
+        // With the head empty, Δ of iteration k is the set of pairs at shortest distance k + 1 whether the
+        // step is Δ ∘ edge (the plan as written) or edge ∘ Δ: a shortest path of length k + 2 splits off its
+        // last edge or its first edge, and every other derivation lies in R.  So the left-linear chain
+        //   reach(X,Z) :- edge(X,Y), reach(Y,Z)
+        // gives the same relation, iteration count and Δ sizes, and its product gathers whole Δ rows
+        // (CSR left, bitmap right) instead of expanding adjacency lists id by id.
         uint64_t *res = nullptr, n = 0;
         try {
-            tc_bitmap(ctx, edges.k, edges.n, nv, max_iter, &res, &n, &iterations, deltas);
+            if (nv == 0) {  // no edges: the seed and the one empty iteration
+                deltas.assign(2, 0);
+                iterations = 1;
+            } else {
+                std::vector<ChainRule> chains{ChainRule{H, {ChainAtom{E, false}}},
+                                              ChainRule{H, {ChainAtom{E, false}, ChainAtom{H, false}}}};
+                std::vector<char> idb(n_preds, 0);
+                idb[H] = 1;
+                std::vector<const uint64_t *> keys(n_preds, nullptr);
+                std::vector<uint64_t> rows(n_preds, 0), res_n;
+                keys[E] = edges.k;
+                rows[E] = edges.n;
+                std::vector<uint64_t *> r;
+                chain_fixpoint(ctx, chains, n_preds, idb, keys, rows, nv, max_iter, r, res_n, &iterations, deltas);
+                res = r[H];
+                n = res_n[H];
+            }
         } catch (...) {
             if (edges.owned) ctx->free(edges.k);
             if (stats) stats->iterations = deltas.empty() ? 0 : deltas.size() - 1;
@@ -2096,14 +2116,15 @@ xlog_hip_status xlog_hip_rel_digest(xlog_hip_ctx *ctx, const xlog_hip_rel *rel, 
 // ---- kernel timing -----------------------------------------------------------
 unsigned long long *xh::Prof::work(double bytes_per_unit) {
     if (!on) return nullptr;
+    constexpr uint64_t total = (uint64_t)Ctx::PROF_WORK_SLOTS * Ctx::PROF_WORK_SPREAD;
     if (!ctx->prof_work) {
-        ctx->prof_work = static_cast<unsigned long long *>(ctx->alloc(Ctx::PROF_WORK_SLOTS * sizeof(uint64_t)));
-        fill_u64(ctx, reinterpret_cast<uint64_t *>(ctx->prof_work), 0ull, Ctx::PROF_WORK_SLOTS);
+        ctx->prof_work = static_cast<unsigned long long *>(ctx->alloc(total * sizeof(uint64_t)));
+        fill_u64(ctx, reinterpret_cast<uint64_t *>(ctx->prof_work), 0ull, total);
     }
     if (ctx->prof_work_next >= Ctx::PROF_WORK_SLOTS) return nullptr;
     rec.work_slot = ctx->prof_work_next++;
     rec.bytes_per_work = bytes_per_unit;
-    return ctx->prof_work + rec.work_slot;
+    return ctx->prof_work + (uint64_t)rec.work_slot * Ctx::PROF_WORK_SPREAD;
 }
 
 void xh::Ctx::prof_resolve() {
@@ -2111,9 +2132,12 @@ void xh::Ctx::prof_resolve() {
     sync();
     std::vector<uint64_t> work;
     if (prof_work_next > 0) {
-        work.resize(prof_work_next);
-        XH_CHECK_HIP(hipMemcpy(work.data(), prof_work, prof_work_next * sizeof(uint64_t), hipMemcpyDeviceToHost));
-        fill_u64(this, reinterpret_cast<uint64_t *>(prof_work), 0ull, prof_work_next);
+        const uint64_t n = (uint64_t)prof_work_next * PROF_WORK_SPREAD;
+        std::vector<uint64_t> raw(n);
+        XH_CHECK_HIP(hipMemcpy(raw.data(), prof_work, n * sizeof(uint64_t), hipMemcpyDeviceToHost));
+        fill_u64(this, reinterpret_cast<uint64_t *>(prof_work), 0ull, n);
+        work.assign(prof_work_next, 0);
+        for (uint64_t i = 0; i < n; ++i) work[i / PROF_WORK_SPREAD] += raw[i];
         prof_work_next = 0;
     }
     for (auto &r : prof_pending) {

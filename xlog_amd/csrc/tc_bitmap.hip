@@ -1,20 +1,18 @@
-// Dense factorized transitive-closure step for gfx950.
+// Dense factorized transitive-closure step for gfx950, and the bitmap helpers
+// the dense fixpoint routes share.
 //
 // The reference's factorized delta (fj_delta_novel_u32_recorded,
 // crates/xlog-cuda/src/provider/fj_delta.rs:117-490; kernels wcoj.cu:3811-3946)
 // computes  novel[x] = (U_{y in delta[x]} edge[y]) \ R[x]  with a
 // domain x domain bitmap, capped at a 2^14..2^16 domain
-// (wcoj_dispatch.rs:176-186).  Here the whole fixpoint state lives in
-// bitmaps sized for the MI355X's HBM: R, delta and next-delta are V x V bit
-// matrices (V = 32,768 -> 128 MiB each), and a per-row "non-empty" flag lets
-// a block skip a row of an empty delta without touching its bitmap.
-//
-// One iteration = one launch of k_tc_step, one block per source row x:
+// (wcoj_dispatch.rs:176-186).  fj_delta_step keeps that one-step operator:
+// R, delta and the result are V x V bit matrices and k_tc_step handles one
+// source row x per block:
 //   acc     = OR over set bits y of delta[x] of the adjacency list of y  (LDS)
 //   new     = acc & ~R[x];  R[x] |= new;  next[x] = new
-//   count  += popcount(new)          (the only value read back per iteration)
-// The final relation is emitted row by row in (x, z) order, so it is sorted
-// and unique by construction.
+// The result is emitted row by row in (x, z) order, so it is sorted and unique
+// by construction.  (Inside the fixpoint, transitive closure runs on the chain
+// route of chain_bitmap.hip, which gathers delta rows instead.)
 #include "internal.hpp"
 
 namespace xh {
@@ -24,19 +22,6 @@ namespace {
 constexpr int TB = 256;
 constexpr int CHUNK_WORDS = 64;  // delta-row words compacted per round (<= 4096 set bits)
 constexpr int UNROLL = 4;        // adjacency lists loaded together per thread
-
-__global__ void k_edges_to_bits(const uint64_t *__restrict__ edges, uint64_t m, uint64_t words,
-                                uint64_t *__restrict__ R, uint64_t *__restrict__ D) {
-    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < m; i += stride) {
-        uint64_t e = edges[i];
-        uint32_t x = (uint32_t)(e >> 32), z = (uint32_t)e;
-        uint64_t off = (uint64_t)x * words + (z >> 6);
-        unsigned long long bit = 1ull << (z & 63);
-        atomicOr((unsigned long long *)&R[off], bit);
-        atomicOr((unsigned long long *)&D[off], bit);
-    }
-}
 
 // row_ptr[v] = first index of sorted unique edges with source >= v
 __global__ void k_row_ptr(const uint64_t *__restrict__ edges, uint64_t m, uint32_t nv, uint64_t *__restrict__ row_ptr) {
@@ -54,12 +39,6 @@ __global__ void k_row_ptr(const uint64_t *__restrict__ edges, uint64_t m, uint32
 __global__ void k_adj(const uint64_t *__restrict__ edges, uint64_t m, uint32_t *__restrict__ adj) {
     uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < m; i += stride) adj[i] = (uint32_t)edges[i];
-}
-
-__global__ void k_seed_nz(const uint64_t *__restrict__ row_ptr, uint32_t nv, uint8_t *__restrict__ nz) {
-    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-    for (uint64_t v = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; v < nv; v += stride)
-        nz[v] = row_ptr[v + 1] > row_ptr[v];
 }
 
 // Dynamic LDS: `words` u64 accumulator words for the row.
@@ -306,66 +285,6 @@ uint64_t bitmap_emit(Ctx *ctx, const uint64_t *bits, uint32_t nv, uint64_t words
     hipLaunchKernelGGL(k_emit_rows, dim3(nv), dim3(TB), 0, ctx->stream, bits, words, rc.p, *out);
     XH_CHECK_HIP(hipGetLastError());
     return total;
-}
-
-// Dense transitive closure.  `edges` sorted unique packed (src, dst), all ids
-// < nv.  Returns the sorted closure in *out (count *out_n), the iteration
-// count and per-iteration delta sizes (index 0 = seed).
-void tc_bitmap(Ctx *ctx, const uint64_t *edges, uint64_t m, uint32_t nv, uint64_t max_iter, uint64_t **out,
-               uint64_t *out_n, uint64_t *iterations, std::vector<uint64_t> &deltas) {
-    deltas.clear();
-    const uint64_t words = ((uint64_t)nv + 63) / 64;
-    XH_REQUIRE(words * 8 <= 64 * 1024, XLOG_HIP_UNSUPPORTED, "tc bitmap: domain too large for an LDS row");
-    const uint64_t cells = (uint64_t)nv * words;
-    Buf<uint64_t> R(ctx, cells ? cells : 1), D0(ctx, cells ? cells : 1), D1(ctx, cells ? cells : 1);
-    Buf<uint64_t> row_ptr(ctx, (uint64_t)nv + 1);
-    Buf<uint32_t> adj(ctx, m ? m : 1);
-    Buf<uint8_t> nz0(ctx, nv ? nv : 1), nz1(ctx, nv ? nv : 1);
-    Buf<unsigned long long> cnt(ctx, 2);
-    fill_u64(ctx, R.p, 0ull, cells);
-    fill_u64(ctx, D0.p, 0ull, cells);
-    hipLaunchKernelGGL(k_row_ptr, dim3(grid_for((uint64_t)nv + 1, 256, 4096)), dim3(256), 0, ctx->stream, edges, m, nv,
-                       row_ptr.p);
-    if (m) {
-        hipLaunchKernelGGL(k_adj, dim3(grid_for(m, 256, 4096)), dim3(256), 0, ctx->stream, edges, m, adj.p);
-        hipLaunchKernelGGL(k_edges_to_bits, dim3(grid_for(m, 256, 4096)), dim3(256), 0, ctx->stream, edges, m, words,
-                           R.p, D0.p);
-    }
-    if (nv) hipLaunchKernelGGL(k_seed_nz, dim3(grid_for(nv, 256, 4096)), dim3(256), 0, ctx->stream, row_ptr.p, nv, nz0.p);
-    XH_CHECK_HIP(hipGetLastError());
-    deltas.push_back(m);  // seed: delta = R = edge
-    uint64_t *D = D0.p, *N = D1.p;
-    uint8_t *nzc = nz0.p, *nzn = nz1.p;
-    uint64_t it = 0, active_rows = nv;
-    bool converged = false;
-    const size_t lds = words * sizeof(uint64_t);
-    while (it < max_iter) {
-        ++it;
-        uint64_t dn = 0;
-        if (m && nv) {
-            fill_u64(ctx, reinterpret_cast<uint64_t *>(cnt.p), 0ull, 2);
-            {
-                // bitmap rows of delta and R read, R and next written (rows with an empty delta skip all four)
-                Prof prof(ctx, XLOG_HIP_KERNEL_TC_STEP, 32.0 * (double)words * (double)active_rows);
-                hipLaunchKernelGGL(k_tc_step, dim3(nv), dim3(TB), lds, ctx->stream, nv, words, row_ptr.p, adj.p, R.p,
-                                   D, N, nzc, nzn, cnt.p);
-                XH_CHECK_HIP(hipGetLastError());
-            }
-            ctx->read_scalars(cnt.p, 2);
-            dn = ctx->host_scalars[0];
-            active_rows = ctx->host_scalars[1];
-        }
-        deltas.push_back(dn);
-        if (dn == 0) {
-            converged = true;
-            break;
-        }
-        std::swap(D, N);
-        std::swap(nzc, nzn);
-    }
-    *iterations = it;
-    XH_REQUIRE(converged, XLOG_HIP_ITERATION_LIMIT, "Recursive SCC iteration limit exceeded");
-    *out_n = bitmap_emit(ctx, R.p, nv, words, out, XLOG_HIP_KERNEL_TC_EMIT);
 }
 
 }  // namespace xh
