@@ -276,6 +276,10 @@ __global__ __launch_bounds__(BLOCK) void k_onesweep(
             if (w < wave) wpre += s_wsum[w];
         const uint32_t tstart = wpre + incl - cnt;
         s_tstart[d] = tstart;
+        // fold the digit's tile start into the per-wave bases: the reorder
+        // then reads one LDS word per key instead of two
+#pragma unroll
+        for (int w = 0; w < (BLOCK / WAVE); ++w) s_wcnt[w][d] += tstart;
 
         // decoupled look-back over earlier tiles for this digit
         // (LOOKBACK predecessors are loaded at once; the walk consumes them in
@@ -333,7 +337,7 @@ __global__ __launch_bounds__(BLOCK) void k_onesweep(
         uint64_t idx = wbase + (uint64_t)r * WAVE + lane;
         if (idx < n) {
             uint32_t dd = (uint32_t)(k[r] >> shift) & 255u;
-            uint32_t pos = s_tstart[dd] + s_wcnt[wave][dd] + rank[r];
+            uint32_t pos = s_wcnt[wave][dd] + rank[r];
             s_keys[pos] = k[r];
             if (HAS_VAL) s_vals[pos] = v[r];
         }
