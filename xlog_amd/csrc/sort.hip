@@ -325,7 +325,7 @@ __global__ __launch_bounds__(BLOCK) void k_onesweep(
         uint64_t idx = wbase + (uint64_t)r * WAVE + lane;
         if (idx < n) {
             uint32_t dd = (uint32_t)(k[r] >> shift) & 255u;
-            uint32_t o = s_gbase[dd] + s_tstart[dd] + s_wcnt[wave][dd] + rank[r];
+            uint32_t o = s_gbase[dd] + s_wcnt[wave][dd] + rank[r];  // the bases include the tile start
             kout[o] = k[r];
             if (HAS_VAL) vout[o] = v[r];
         }
