@@ -317,6 +317,16 @@ __global__ __launch_bounds__(FTB) void k_clear_rows(uint32_t words, uint64_t *__
     for (uint32_t w = threadIdx.x; w < words; w += FTB) B[(uint64_t)x * words + w] = 0ull;
 }
 
+// totals[i] = sum of the SPREAD partial counts of entry i (iterations x predicates)
+__global__ void k_sum_counts(const unsigned long long *__restrict__ parts, uint32_t n,
+                             unsigned long long *__restrict__ totals) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    unsigned long long t = 0;
+    for (int q = 0; q < SPREAD; ++q) t += parts[(uint64_t)i * SPREAD + q];
+    totals[i] = t;
+}
+
 // C[x] |= B[x] for the rows of B's mask (a one-atom chain over an IDB operand)
 __global__ __launch_bounds__(FTB) void k_or_rows(uint32_t words, const uint64_t *__restrict__ B,
                                                  const uint64_t *__restrict__ bmask, uint64_t *__restrict__ C,
@@ -521,7 +531,12 @@ struct ChainRun {
     std::vector<BitRel> bit;       // by predicate (IDB only)
     std::vector<CsrRel> csr[2];    // by predicate: forward, backward (EDB only)
     Buf<uint64_t> T[2], TM[2];
-    Buf<unsigned long long> counts;
+    // partial delta counts: CHUNK iterations x predicates x SPREAD, and their sums
+    static constexpr int CHUNK = 8;
+    Buf<unsigned long long> counts, totals;
+    int slot = 0;             // iteration slot of the chunk being queued
+    bool speculative = false; // delta sizes of the queued iterations are not known yet
+    unsigned long long *cnt_of(int p) { return counts.p + ((uint64_t)slot * n_preds + p) * SPREAD; }
     std::vector<int> idb_list;
 
     void fill0(Buf<uint64_t> &b, uint64_t n) { fill_u64(ctx, b.p, 0ull, n); }
@@ -618,7 +633,8 @@ struct ChainRun {
             T[1] = Buf<uint64_t>(ctx, cells);
             TM[1] = Buf<uint64_t>(ctx, words);
         }
-        counts = Buf<unsigned long long>(ctx, (uint64_t)n_preds * SPREAD);
+        counts = Buf<unsigned long long>(ctx, (uint64_t)CHUNK * n_preds * SPREAD);
+        totals = Buf<unsigned long long>(ctx, (uint64_t)CHUNK * n_preds);
     }
 
     enum Use { FULL, DELTA, PREV };  // R, D, or R minus D
@@ -628,7 +644,7 @@ struct ChainRun {
         if (idb[a.pred]) {
             BitRel &b = bit[a.pred];
             const uint64_t n = use == FULL ? b.rcount : (use == DELTA ? b.dcount : b.rcount - b.dcount);
-            if (n == 0) return false;
+            if (n == 0 && !speculative) return false;  // (queued iterations: the masks skip empty rows)
             if (!a.backward) {
                 op.bits = use == FULL ? b.R.p : (use == DELTA ? b.D.p : b.P.p);
                 op.mask = use == FULL ? b.rmask.p : (use == DELTA ? b.dmask[b.dcur].p : b.pmask.p);
@@ -706,7 +722,7 @@ struct ChainRun {
         }
         // the last product ORs into the candidates, or, fused, writes the new delta into them
         const int last_mode = fused ? OUT_FUSED : OUT_OR;
-        const FusedArgs fz{H.R.p, H.rmask.p, H.dmask[H.dcur ^ 1].p, counts.p + (uint64_t)r.head * SPREAD};
+        const FusedArgs fz{H.R.p, H.rmask.p, H.dmask[H.dcur ^ 1].p, cnt_of(r.head)};
         uint64_t *last_mask = fused ? H.dmask[H.dcur ^ 1].p : H.cmask.p;
         if (!right_to_left(r)) {  // ((a1 a2) a3) ...
             Operand left = ops[0];
@@ -737,6 +753,21 @@ struct ChainRun {
     // left operand, and nothing else of the head is read or kept: no other
     // atom of the head in the body (the product updates R in place), no
     // transposes and no R-minus-delta copy to maintain.
+    // Every IDB head has exactly one IDB occurrence over its rules, and that
+    // variant can take the fused product.
+    bool all_fused() const {
+        std::vector<int> occ(n_preds, 0);
+        for (const ChainRule &r : rules)
+            for (size_t j = 0; j < r.path.size(); ++j)
+                if (idb[r.path[j].pred]) ++occ[r.head];
+        for (const ChainRule &r : rules)
+            for (size_t j = 0; j < r.path.size(); ++j)
+                if (idb[r.path[j].pred] && (occ[r.head] != 1 || !can_fuse(r, (int)j))) return false;
+        for (int p : idb_list)
+            if (occ[p] != 1) return false;
+        return true;
+    }
+
     bool can_fuse(const ChainRule &r, int delta_at) const {
         const BitRel &H = bit[r.head];
         if (H.trans || H.prev || r.path.size() < 2) return false;
@@ -763,14 +794,14 @@ struct ChainRun {
     // Before an iteration's products: clear the counts and, for every head
     // whose delta a fused product writes, the new delta's row mask.
     void begin_iteration(const std::vector<char> &fused) {
-        fill_u64(ctx, reinterpret_cast<uint64_t *>(counts.p), 0ull, (uint64_t)n_preds * SPREAD);
+        fill_u64(ctx, reinterpret_cast<uint64_t *>(cnt_of(0)), 0ull, (uint64_t)n_preds * SPREAD);
         for (int p : idb_list)
             if (fused[p]) fill_u64(ctx, bit[p].dmask[bit[p].dcur ^ 1].p, 0ull, words);
     }
 
     // New deltas of every IDB predicate from its candidates (or, for fused
     // heads, already in the candidate matrix); returns their total.
-    uint64_t finalize_all(const std::vector<char> &fused) {
+    void finalize_all(const std::vector<char> &fused) {
         for (int p : idb_list) {
             BitRel &b = bit[p];
             uint64_t *dnew = b.dmask[b.dcur ^ 1].p;
@@ -785,7 +816,7 @@ struct ChainRun {
             }
             fill_u64(ctx, dnew, 0ull, words);
             const FinalizeArgs fa{b.C.p, b.cmask.p, b.R.p, b.rmask.p, b.D.p, b.dmask[b.dcur].p, dnew, b.P.p,
-                                  b.pmask.p, counts.p + (uint64_t)p * SPREAD};
+                                  b.pmask.p, cnt_of(p)};
             {
                 Prof prof(ctx, XLOG_HIP_KERNEL_CHAIN_FINALIZE, 0.0);
                 if (b.prev)
@@ -806,15 +837,30 @@ struct ChainRun {
             fill_u64(ctx, b.cmask.p, 0ull, words);
             b.dcur ^= 1;
         }
-        // one read-back of every predicate's delta size (SPREAD partial counts each)
-        std::vector<uint64_t> host((uint64_t)n_preds * SPREAD);
-        XH_CHECK_HIP(hipMemcpyAsync(host.data(), counts.p, host.size() * sizeof(uint64_t), hipMemcpyDeviceToHost,
-                                    ctx->stream));
-        ctx->sync();
+    }
+
+    // Sums and reads back the delta sizes of the `queued` iterations (one
+    // copy, pinned staging when it fits) into sizes[i * n_preds + p].
+    void read_counts(int queued, std::vector<uint64_t> &sizes) {
+        const uint32_t n = (uint32_t)queued * n_preds;
+        hipLaunchKernelGGL(k_sum_counts, dim3((n + 255) / 256), dim3(256), 0, ctx->stream, counts.p, n, totals.p);
+        XH_CHECK_HIP(hipGetLastError());
+        sizes.resize(n);
+        if (n <= 64) {
+            ctx->read_scalars(totals.p, n);
+            for (uint32_t i = 0; i < n; ++i) sizes[i] = ctx->host_scalars[i];
+        } else {
+            XH_CHECK_HIP(hipMemcpyAsync(sizes.data(), totals.p, n * sizeof(uint64_t), hipMemcpyDeviceToHost,
+                                        ctx->stream));
+            ctx->sync();
+        }
+    }
+
+    // Applies iteration i's delta sizes; returns their total.
+    uint64_t take_counts(const std::vector<uint64_t> &sizes, int i) {
         uint64_t total = 0;
         for (int p : idb_list) {
-            uint64_t n = 0;
-            for (int q = 0; q < SPREAD; ++q) n += host[(uint64_t)p * SPREAD + q];
+            const uint64_t n = sizes[(uint64_t)i * n_preds + p];
             bit[p].dcount = n;
             bit[p].rcount += n;
             total += n;
@@ -861,37 +907,54 @@ void chain_fixpoint(Ctx *ctx, const std::vector<ChainRule> &rules, uint32_t n_pr
     run.setup();
     // seed: every rule once against the initial relations
     const std::vector<char> none(n_preds, 0);
+    std::vector<uint64_t> sizes;
     run.begin_iteration(none);
     for (const ChainRule &r : rules) run.eval_chain(r, -1);
-    deltas.push_back(run.finalize_all(none));
+    run.finalize_all(none);
+    run.read_counts(1, sizes);
+    deltas.push_back(run.take_counts(sizes, 0));
+    // When every head takes one fused variant per iteration (transitive
+    // closure), CHUNK iterations are queued per read-back: an iteration after
+    // the fixpoint finds every delta row empty, derives nothing and counts 0,
+    // so the queued iterations past it change no relation and are not reported.
+    const bool chunked = run.all_fused();
     uint64_t it = 0;
     bool converged = false;
     std::vector<int> nvar(n_preds);
     std::vector<char> fused(n_preds);
-    while (it < max_iter) {
-        ++it;
-        // the variants of this iteration; a head with exactly one may take the fused product
-        std::fill(nvar.begin(), nvar.end(), 0);
-        std::fill(fused.begin(), fused.end(), 0);
-        for (const ChainRule &r : rules)
-            for (size_t j = 0; j < r.path.size(); ++j)
-                if (idb[r.path[j].pred] && run.bit[r.path[j].pred].dcount) ++nvar[r.head];
-        for (const ChainRule &r : rules)
-            for (size_t j = 0; j < r.path.size(); ++j)
-                if (idb[r.path[j].pred] && run.bit[r.path[j].pred].dcount && nvar[r.head] == 1)
-                    fused[r.head] = run.can_fuse(r, (int)j);
-        run.begin_iteration(fused);
-        for (const ChainRule &r : rules)
-            for (size_t j = 0; j < r.path.size(); ++j) {
-                const int p = r.path[j].pred;
-                if (!idb[p] || run.bit[p].dcount == 0) continue;
-                run.eval_chain(r, (int)j, fused[r.head] != 0);
+    while (it < max_iter && !converged) {
+        const int queue = chunked ? (int)std::min<uint64_t>(ChainRun::CHUNK, max_iter - it) : 1;
+        for (int k = 0; k < queue; ++k) {
+            run.slot = k;
+            run.speculative = k > 0;
+            if (k == 0) {
+                // the variants of this iteration; a head with exactly one may take the fused product
+                std::fill(nvar.begin(), nvar.end(), 0);
+                std::fill(fused.begin(), fused.end(), 0);
+                for (const ChainRule &r : rules)
+                    for (size_t j = 0; j < r.path.size(); ++j)
+                        if (idb[r.path[j].pred] && run.bit[r.path[j].pred].dcount) ++nvar[r.head];
+                for (const ChainRule &r : rules)
+                    for (size_t j = 0; j < r.path.size(); ++j)
+                        if (idb[r.path[j].pred] && run.bit[r.path[j].pred].dcount && nvar[r.head] == 1)
+                            fused[r.head] = run.can_fuse(r, (int)j);
             }
-        const uint64_t total = run.finalize_all(fused);
-        deltas.push_back(total);
-        if (total == 0) {
-            converged = true;
-            break;
+            run.begin_iteration(fused);
+            for (const ChainRule &r : rules)
+                for (size_t j = 0; j < r.path.size(); ++j) {
+                    const int p = r.path[j].pred;
+                    if (!idb[p] || (!run.speculative && run.bit[p].dcount == 0)) continue;
+                    run.eval_chain(r, (int)j, fused[r.head] != 0);
+                }
+            run.finalize_all(fused);
+        }
+        run.read_counts(queue, sizes);
+        run.speculative = false;
+        for (int k = 0; k < queue && !converged; ++k) {
+            ++it;
+            const uint64_t total = run.take_counts(sizes, k);
+            deltas.push_back(total);
+            converged = total == 0;
         }
     }
     *iterations = it;
