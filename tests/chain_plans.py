@@ -37,6 +37,15 @@ def parity_plan(edge=0, odd=1, even=2):
             odd, X, Z, 2, even, X, Y, edge, Y, Z]
 
 
+def parity_left_plan(edge=0, odd=1, even=2):
+    """The same walks with the IDB atom last: odd(X,Y) :- edge(X,Y).  even(X,Z) :- edge(X,Y), odd(Y,Z).
+    odd(X,Z) :- edge(X,Y), even(Y,Z).  Every variant is a CSR-left product and each head has one, so every
+    iteration is fused; the two deltas alternate between empty and non-empty."""
+    return [3, odd, X, Y, 1, edge, X, Y,
+            even, X, Z, 2, edge, X, Y, odd, Y, Z,
+            odd, X, Z, 2, edge, X, Y, even, Y, Z]
+
+
 def symmetric_plan(edge=0, sym=1):
     """sym(X,Y) :- edge(Y,X).  sym(X,Y) :- sym(Y,X).  sym(X,Z) :- sym(X,Y), edge(Y,Z)."""
     return [3, sym, X, Y, 1, edge, Y, X,

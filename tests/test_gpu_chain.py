@@ -78,6 +78,7 @@ def test_same_generation(provider, n, seed):
 def test_parity_mutual_recursion(provider, n, m, seed):
     s, d = _graph(n, m, seed)
     _parity(provider, "parity", cp.parity_plan(), [pack(s, d), None, None], [1, 2])
+    _parity(provider, "parity left-linear", cp.parity_left_plan(), [pack(s, d), None, None], [1, 2])
 
 
 @pytest.mark.parametrize("n,m,seed", [(150, 200, 9), (1500, 2200, 10)])

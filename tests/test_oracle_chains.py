@@ -95,6 +95,14 @@ def test_parity_mutual_recursion(n, m, seed):
     _check(cp.parity_plan(), [pack(s, d), None, None], [1, 2], _kleene(step, [np.zeros_like(E)] * 2))
 
 
+@pytest.mark.parametrize("n,m,seed", [(30, 45, 5), (90, 160, 6)])
+def test_parity_left_linear(n, m, seed):
+    s, d = _graph(n, m, seed)
+    E = _mat(n, s, d)
+    step = lambda R: (E | _mm(E, R[1]), _mm(E, R[0]))  # (odd, even)
+    _check(cp.parity_left_plan(), [pack(s, d), None, None], [1, 2], _kleene(step, [np.zeros_like(E)] * 2))
+
+
 @pytest.mark.parametrize("n,m,seed", [(30, 40, 7), (100, 150, 8)])
 def test_symmetric_closure(n, m, seed):
     s, d = _graph(n, m, seed)

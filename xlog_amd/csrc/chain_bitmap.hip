@@ -39,7 +39,7 @@ namespace {
 constexpr int PTB = 512;           // product block: 8 waves
 constexpr int PNW = PTB / WAVE;
 constexpr int LCHUNK_WORDS = 64;   // left-row bitmap words compacted per round (<= 4096 ids)
-constexpr int FTB = 256;           // finalize / row-op block
+constexpr int FTB = 256;           // row-op block
 #ifndef XH_GATHER_UNROLL
 #define XH_GATHER_UNROLL 8
 #endif
@@ -215,97 +215,195 @@ __global__ __launch_bounds__(PTB) void k_chain_product(uint32_t words, Operand L
 }
 
 // Output of a fused product: the new delta is written straight into the
-// (all-zero) candidate matrix, R is updated and the delta counted, so no
-// separate finalize pass touches the row again.
+// candidate matrix, R is updated and the delta counted, so no separate
+// finalize pass touches the row again.  With full_rows every row the product
+// reaches is written whole (zero words included), so the matrix needs no
+// clearing beforehand: its other rows keep stale bits under a clear mask bit.
+// `zero` (when set) is a row mask of zero_words words that the launch clears
+// on the side: the next iteration's delta mask, read by nothing in this one.
 struct FusedArgs {
     uint64_t *R, *rmask;
-    uint64_t *dmask_new;
     unsigned long long *count;
+    uint32_t full_rows;
+    uint64_t *zero;
+    uint32_t zero_words;
 };
 
-constexpr int GW = 4;           // k_csr_gather: rows (waves) per block
+constexpr int GW = 4;           // k_csr_gather: waves per block
 constexpr int GWORDS = 8;       // words per lane per stripe group (a group = 512 words)
+#ifndef XH_GATHER_NR
+#define XH_GATHER_NR 2
+#endif
+#ifndef XH_GATHER_WAVES
+#define XH_GATHER_WAVES 8192
+#endif
+constexpr int GNR = XH_GATHER_NR;  // right rows gathered per round (GNR x GWORDS loads in flight per lane)
+constexpr uint32_t GATHER_WAVES = XH_GATHER_WAVES;  // waves per launch the row batches aim at
+constexpr uint32_t GATHER_MAX_BATCH = 32;            // rows per wave batch (a power of two <= 32)
 
 enum { OUT_ASSIGN = 0, OUT_OR = 1, OUT_FUSED = 2 };
 
+// rows per wave of the row-batched kernels: a power of two (so a batch never
+// straddles a row-mask word) large enough to keep the launch near GATHER_WAVES waves
+inline uint32_t row_batch(uint32_t domain) {
+    uint32_t batch = 1;
+    while (batch < GATHER_MAX_BATCH && (uint64_t)domain > (uint64_t)GATHER_WAVES * batch) batch *= 2;
+    return batch;
+}
+
+// atomically m |= bits << x, bits covering rows x .. x + 63 (two words at most)
+__device__ __forceinline__ void or_bits(uint64_t *m, uint32_t x, uint64_t bits) {
+    const uint32_t sh = x & 63;
+    if (bits << sh) atomicOr((unsigned long long *)&m[x >> 6], (unsigned long long)(bits << sh));
+    if (sh && (bits >> (64 - sh))) atomicOr((unsigned long long *)&m[(x >> 6) + 1], (unsigned long long)(bits >> (64 - sh)));
+}
+
 // The fused last product of a variant with a CSR left operand (short rows:
-// EDB relations) and a bitmap right operand, one wave per output row x, no
-// LDS and no block barriers.  The row's ids y whose right row is non-empty
-// come 64 at a time from a ballot; each right row is gathered as 8 coalesced
-// loads per lane (words g0 + lane + 64k of a 512-word stripe group), two rows
-// in flight, into registers; then new = acc & ~R[x], R[x] |= new, O[x] = new
-// (O is the zeroed candidate matrix becoming the next delta), counted.
+// EDB relations) and a bitmap right operand.  A wave owns `batch` consecutive
+// output rows: their row offsets come in one load (a lane per row), their
+// adjacency and the right operand's row-mask bits 64 edges at a time (a lane
+// per edge), so the dependent loads before any gather are paid once per batch,
+// not per row.  Per row x, the ids y of x's edges whose right row is non-empty
+// come from a ballot over the loaded edges; R[x] and the right rows are then
+// loaded in one round (8 coalesced loads per lane per row: words
+// g0 + lane + 64k of a 512-word stripe group; GNR right rows at a time) and
+// new = acc & ~R[x], R[x] |= new, O[x] = new (O is the candidate matrix
+// becoming the next delta: all zero, or written whole when fz.full_rows),
+// counted.  A row with no such id is left alone.
+// The rows that received bits are OR-ed into the output and R row masks once
+// per batch, and the counts once per block.
 // (For the non-fused products of short left rows the block-per-row
 // k_chain_product measured faster: 4.3 against 6.8 ms per C5 fixpoint.)
-__global__ __launch_bounds__(GW * WAVE) void k_csr_gather_fused(uint32_t domain, uint32_t words, Operand L, Operand Rt,
-                                                          uint64_t *__restrict__ O, uint64_t *__restrict__ omask,
-                                                          FusedArgs fz, unsigned long long *__restrict__ work) {
+__global__ __launch_bounds__(GW * WAVE) void k_csr_gather_fused(uint32_t domain, uint32_t words, uint32_t batch,
+                                                          Operand L, Operand Rt, uint64_t *__restrict__ O,
+                                                          uint64_t *__restrict__ omask, FusedArgs fz,
+                                                          unsigned long long *__restrict__ work) {
+    __shared__ unsigned long long s_cnt[GW], s_work[GW];
     const int lane = threadIdx.x & (WAVE - 1);
-    const uint32_t x = blockIdx.x * GW + (threadIdx.x >> 6);
-    if (x >= domain || !bit_of(L.mask, x)) return;  // wave-uniform
-    const uint64_t beg = L.row_ptr[x], end = L.row_ptr[x + 1];
-    uint64_t *orow = O + (uint64_t)x * words;
-    bool any = false;
-    unsigned long long cnt = 0, gathered = 0;
-    for (uint32_t g0 = 0; g0 < words; g0 += GWORDS * WAVE) {
-        uint64_t acc[GWORDS];
-#pragma unroll
-        for (int k = 0; k < GWORDS; ++k) acc[k] = 0ull;
-        for (uint64_t c0 = beg; c0 < end; c0 += WAVE) {
+    const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    unsigned long long cnt = 0, moved = 0;  // per lane
+    if (fz.zero)
+        for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < fz.zero_words; i += gridDim.x * blockDim.x)
+            fz.zero[i] = 0ull;
+    const uint64_t x0 = ((uint64_t)blockIdx.x * GW + wave) * batch;
+    if (x0 < domain) {
+        const uint32_t nr = (uint32_t)(domain - x0 < batch ? domain - x0 : batch);
+        const uint64_t rp = (uint32_t)lane <= nr ? L.row_ptr[x0 + lane] : 0ull;
+        const uint64_t ebeg = __shfl(rp, 0, WAVE), eend = __shfl(rp, (int)nr, WAVE);
+        if (lane == 0) moved += 4ull * (eend - ebeg);
+        // the loaded edge chunk: edges c0 + lane, their ids and whether their right row is non-empty
+        uint64_t c0 = ebeg;
+        uint32_t y = 0;
+        bool keep = false;
+        {
             const uint64_t e = c0 + lane;
-            const uint32_t y = e < end ? L.adj[e] : 0u;
-            uint64_t bal = __ballot(e < end && bit_of(Rt.mask, y));
-            gathered += (unsigned long long)__popcll(bal);
-            while (bal) {  // wave-uniform: the kept ids, two rows at a time
-                const int s0 = __builtin_ctzll(bal);
-                bal &= bal - 1ull;
-                const uint32_t y0 = (uint32_t)__shfl((int)y, s0, WAVE);
-                int s1 = -1;
-                if (bal) {
-                    s1 = __builtin_ctzll(bal);
-                    bal &= bal - 1ull;
+            y = e < eend ? L.adj[e] : 0u;
+            keep = e < eend && bit_of(Rt.mask, y);
+        }
+        uint64_t rows_set = 0;  // bit r: row x0 + r received new bits
+        for (uint32_t r = 0; r < nr; ++r) {
+            const uint64_t rb = __shfl(rp, (int)r, WAVE), re = __shfl(rp, (int)r + 1, WAVE);
+            if (rb == re) continue;  // wave-uniform
+            const uint64_t x = x0 + r;
+            uint64_t *orow = O + x * words;
+            uint64_t *rrow = fz.R + x * words;
+            bool any = false;
+            for (uint32_t g0 = 0; g0 < words; g0 += GWORDS * WAVE) {
+                uint64_t acc[GWORDS], rv[GWORDS];
+#pragma unroll
+                for (int k = 0; k < GWORDS; ++k) acc[k] = rv[k] = 0ull;
+                bool have_r = false;
+                unsigned long long gathered = 0;
+                for (uint64_t pos = rb; pos < re;) {  // wave-uniform walk over the row's edges
+                    if (pos < c0 || pos >= c0 + WAVE) {
+                        c0 = pos;
+                        const uint64_t e = c0 + lane;
+                        y = e < eend ? L.adj[e] : 0u;
+                        keep = e < eend && bit_of(Rt.mask, y);
+                    }
+                    const uint64_t lim = re < c0 + WAVE ? re : c0 + WAVE;
+                    const uint64_t e = c0 + lane;
+                    uint64_t bal = __ballot(keep && e >= pos && e < lim);
+                    pos = lim;
+                    if (!bal) continue;
+                    gathered += (unsigned long long)__popcll(bal);
+                    if (!have_r) {  // R[x]'s group, loaded with the first right rows
+                        have_r = true;
+#pragma unroll
+                        for (int k = 0; k < GWORDS; ++k) {
+                            const uint32_t w = g0 + lane + 64u * k;
+                            rv[k] = w < words ? rrow[w] : 0ull;
+                        }
+                    }
+                    while (bal) {  // GNR right rows at a time
+                        uint32_t ys[GNR];
+                        bool ok[GNR];
+#pragma unroll
+                        for (int j = 0; j < GNR; ++j) {
+                            ok[j] = bal != 0ull;
+                            const int s = ok[j] ? __builtin_ctzll(bal) : 0;
+                            bal &= bal - 1ull;
+                            ys[j] = (uint32_t)__shfl((int)y, s, WAVE);
+                        }
+                        uint64_t v[GNR][GWORDS];
+#pragma unroll
+                        for (int j = 0; j < GNR; ++j) {
+                            const uint64_t *src = Rt.bits + (uint64_t)ys[j] * words + g0 + lane;
+#pragma unroll
+                            for (int k = 0; k < GWORDS; ++k)
+                                v[j][k] = (ok[j] && g0 + lane + 64u * k < words) ? src[64 * k] : 0ull;
+                        }
+#pragma unroll
+                        for (int j = 0; j < GNR; ++j)
+#pragma unroll
+                            for (int k = 0; k < GWORDS; ++k) acc[k] |= v[j][k];
+                    }
                 }
-                const uint32_t y1 = (uint32_t)__shfl((int)y, s1 < 0 ? s0 : s1, WAVE);
-                const uint64_t *r0 = Rt.bits + (uint64_t)y0 * words + g0 + lane;
-                const uint64_t *r1 = Rt.bits + (uint64_t)y1 * words + g0 + lane;
-                uint64_t v0[GWORDS], v1[GWORDS];
+                if (!have_r) continue;  // no id of this row has a non-empty right row
+                const uint32_t gw = words - g0 < GWORDS * WAVE ? words - g0 : GWORDS * WAVE;
+                if (lane == 0) moved += 8ull * gw * (gathered + 1);  // the right rows and R[x]
 #pragma unroll
                 for (int k = 0; k < GWORDS; ++k) {
-                    const bool ok = g0 + lane + 64u * k < words;
-                    v0[k] = ok ? r0[64 * k] : 0ull;
-                    v1[k] = (ok && s1 >= 0) ? r1[64 * k] : 0ull;
+                    const uint32_t w = g0 + lane + 64u * k;
+                    const uint64_t nw = acc[k] & ~rv[k];
+                    if (w < words && nw) {
+                        rrow[w] = rv[k] | nw;
+                        orow[w] = nw;
+                        cnt += (unsigned long long)__popcll(nw);
+                        moved += 16ull;  // the R and O words written
+                        any = true;
+                    } else if (w < words && fz.full_rows) {
+                        orow[w] = 0ull;
+                        moved += 8ull;
+                    }
                 }
-#pragma unroll
-                for (int k = 0; k < GWORDS; ++k) acc[k] |= v0[k] | v1[k];
             }
+            if (__ballot(any) != 0ull) rows_set |= 1ull << r;
         }
-#pragma unroll
-        for (int k = 0; k < GWORDS; ++k) {
-            const uint32_t w = g0 + lane + 64u * k;
-            if (w >= words) continue;
-            const uint64_t a = acc[k];
-            if (a) {
-                uint64_t *rr = fz.R + (uint64_t)x * words + w;
-                const uint64_t r = *rr, nw = a & ~r;
-                if (nw) {
-                    *rr = r | nw;
-                    orow[w] = nw;
-                    cnt += (unsigned long long)__popcll(nw);
-                    any = true;
-                }
-            }
+        if (lane == 0 && rows_set) {
+            or_bits(omask, (uint32_t)x0, rows_set);
+            or_bits(fz.rmask, (uint32_t)x0, rows_set);
         }
     }
-    const bool wave_any = __ballot(any) != 0ull;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) cnt += __shfl_xor(cnt, o, WAVE);
+    for (int o = 32; o > 0; o >>= 1) {
+        cnt += __shfl_xor(cnt, o, WAVE);
+        moved += __shfl_xor(moved, o, WAVE);
+    }
     if (lane == 0) {
-        if (wave_any) {
-            set_bit(omask, x);
-            set_bit(fz.rmask, x);
+        s_cnt[wave] = cnt;
+        s_work[wave] = moved;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long c = 0, m = 0;
+#pragma unroll
+        for (int i = 0; i < GW; ++i) {
+            c += s_cnt[i];
+            m += s_work[i];
         }
-        if (cnt) atomicAdd(&fz.count[blockIdx.x & (SPREAD - 1)], cnt);
-        if (work) atomicAdd(&work[blockIdx.x & (SPREAD - 1)], 4ull * (end - beg) + 8ull * words * (gathered + 1));
+        if (c) atomicAdd(&fz.count[blockIdx.x & (SPREAD - 1)], c);
+        if (work && m) atomicAdd(&work[blockIdx.x & (SPREAD - 1)], m);
     }
 }
 
@@ -390,51 +488,80 @@ struct FinalizeArgs {
 // Per row x with candidates or an old delta row:
 //   P[x] |= D[x];  D[x] = C[x] & ~R[x];  R[x] |= D[x];  C[x] = 0
 // (so that afterwards P = R minus the new D), sets the new delta / full
-// row-mask bits and adds |D[x]| to *count.
+// row-mask bits and adds |D[x]| to the count.  A wave owns `batch` rows (a
+// power of two, so their mask bits share one word, read once): per active
+// row, C, the old D and P words come in one round of loads (8 per lane per
+// 512-word group), R under the non-zero C words in a second, then the stores.
+// Row-mask bits are OR-ed once per batch, the count once per block.
 template <bool PREV>
-__global__ __launch_bounds__(FTB) void k_chain_finalize(uint32_t words, FinalizeArgs a) {
-    __shared__ unsigned long long s_cnt;
-    const uint32_t x = blockIdx.x;
-    const bool c_on = bit_of(a.cmask, x), d_on = bit_of(a.dmask_old, x);
-    if (!c_on && !d_on) return;
-    if (threadIdx.x == 0) s_cnt = 0ull;
-    __syncthreads();
-    const uint64_t base = (uint64_t)x * words;
-    uint64_t *crow = a.C + base, *rrow = a.R + base, *drow = a.D + base;
-    unsigned long long local = 0ull;
-    for (uint32_t w = threadIdx.x; w < words; w += FTB) {
-        uint64_t nw = 0ull;
-        if (c_on) {
-            const uint64_t c = crow[w];
-            if (c) {
-                const uint64_t r = rrow[w];
-                nw = c & ~r;
-                if (nw) rrow[w] = r | nw;
-                crow[w] = 0ull;
+__global__ __launch_bounds__(GW * WAVE) void k_chain_finalize(uint32_t domain, uint32_t words, uint32_t batch,
+                                                              FinalizeArgs a) {
+    __shared__ unsigned long long s_cnt[GW];
+    const int lane = threadIdx.x & (WAVE - 1);
+    const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    unsigned long long cnt = 0;  // per lane
+    const uint32_t x0 = (blockIdx.x * GW + wave) * batch;
+    if (x0 < domain) {
+        const uint32_t nr = domain - x0 < batch ? domain - x0 : batch;
+        const uint64_t rows = nr == 64 ? ~0ull : (1ull << nr) - 1ull;
+        const uint64_t cm = (a.cmask[x0 >> 6] >> (x0 & 63)) & rows, dm = (a.dmask_old[x0 >> 6] >> (x0 & 63)) & rows;
+        uint64_t active = cm | dm, dset = 0;
+        while (active) {  // wave-uniform
+            const int r = __builtin_ctzll(active);
+            active &= active - 1ull;
+            const bool c_on = (cm >> r) & 1ull, d_on = (dm >> r) & 1ull;
+            const uint64_t base = (uint64_t)(x0 + r) * words;
+            uint64_t *crow = a.C + base, *rrow = a.R + base, *drow = a.D + base;
+            bool any = false;
+            for (uint32_t g0 = 0; g0 < words; g0 += GWORDS * WAVE) {
+                uint64_t cv[GWORDS], dv[GWORDS], pv[GWORDS], rv[GWORDS];
+#pragma unroll
+                for (int k = 0; k < GWORDS; ++k) {
+                    const uint32_t w = g0 + lane + 64u * k;
+                    const bool in = w < words;
+                    cv[k] = in && c_on ? crow[w] : 0ull;
+                    dv[k] = PREV && in && d_on ? drow[w] : 0ull;
+                    pv[k] = PREV && in && d_on ? a.P[base + w] : 0ull;
+                }
+#pragma unroll
+                for (int k = 0; k < GWORDS; ++k) {
+                    const uint32_t w = g0 + lane + 64u * k;
+                    rv[k] = cv[k] ? rrow[w] : 0ull;
+                }
+#pragma unroll
+                for (int k = 0; k < GWORDS; ++k) {
+                    const uint32_t w = g0 + lane + 64u * k;
+                    if (w >= words) continue;
+                    const uint64_t nw = cv[k] & ~rv[k];
+                    if (cv[k]) {
+                        if (nw) rrow[w] = rv[k] | nw;
+                        crow[w] = 0ull;
+                    }
+                    if (PREV && dv[k] && (pv[k] | dv[k]) != pv[k]) a.P[base + w] = pv[k] | dv[k];
+                    if (d_on || nw) drow[w] = nw;
+                    cnt += (unsigned long long)__popcll(nw);
+                    any |= nw != 0ull;
+                }
             }
+            if (__ballot(any) != 0ull) dset |= 1ull << r;
         }
-        if (d_on) {
-            if (PREV) {
-                const uint64_t old = drow[w];
-                if (old) a.P[base + w] |= old;
+        if (lane == 0) {
+            if (dset) {
+                or_bits(a.dmask_new, x0, dset);
+                or_bits(a.rmask, x0, dset);
             }
-            drow[w] = nw;
-        } else if (nw) {
-            drow[w] = nw;
+            if (PREV && dm) or_bits(a.pmask, x0, dm);  // the old delta rows were non-empty
         }
-        local += (unsigned long long)__popcll(nw);
     }
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) local += __shfl_xor(local, o, WAVE);
-    if ((threadIdx.x & 63) == 0 && local) atomicAdd(&s_cnt, local);
+    for (int o = 32; o > 0; o >>= 1) cnt += __shfl_xor(cnt, o, WAVE);
+    if (lane == 0) s_cnt[wave] = cnt;
     __syncthreads();
     if (threadIdx.x == 0) {
-        if (PREV && d_on) set_bit(a.pmask, x);  // the old delta row was non-empty
-        if (s_cnt) {
-            set_bit(a.dmask_new, x);
-            set_bit(a.rmask, x);
-            atomicAdd(&a.count[blockIdx.x & (SPREAD - 1)], s_cnt);
-        }
+        unsigned long long c = 0;
+#pragma unroll
+        for (int i = 0; i < GW; ++i) c += s_cnt[i];
+        if (c) atomicAdd(&a.count[blockIdx.x & (SPREAD - 1)], c);
     }
 }
 
@@ -510,6 +637,10 @@ struct BitRel {  // an IDB predicate
     Buf<uint64_t> R, D, C, RT, DT, P, PT;
     Buf<uint64_t> rmask, dmask[2], cmask, rtmask, dtmask, pmask, ptmask;
     int dcur = 0;
+    // when every iteration is fused: a third delta mask, cleared by the fused
+    // product while the other two are read and written (spare_zeroed: it was)
+    Buf<uint64_t> dspare;
+    bool spare_zeroed = false;
     bool trans = false;         // some rule reads it backward
     bool prev = false, prev_t = false;  // R minus D read forward / backward
     uint64_t rcount = 0, dcount = 0;
@@ -536,6 +667,9 @@ struct ChainRun {
     Buf<unsigned long long> counts, totals;
     int slot = 0;             // iteration slot of the chunk being queued
     bool speculative = false; // delta sizes of the queued iterations are not known yet
+    // every iteration after the seed is fused for every head: the fused
+    // products write whole rows, and retired delta rows need no clearing
+    bool no_clear = false;
     unsigned long long *cnt_of(int p) { return counts.p + ((uint64_t)slot * n_preds + p) * SPREAD; }
     std::vector<int> idb_list;
 
@@ -674,9 +808,11 @@ struct ChainRun {
         unsigned long long *w = prof.work(1.0);
         const bool lc = l.bits == nullptr, rc = r.bits == nullptr, acc = mode != OUT_ASSIGN;
         XH_REQUIRE(mode != OUT_FUSED || (lc && !rc), XLOG_HIP_INVALID_ARG, "chain bitmap: fused product needs a CSR left");
-        if (mode == OUT_FUSED) {  // a wave per row
-            hipLaunchKernelGGL(k_csr_gather_fused, dim3((domain + GW - 1) / GW), dim3(GW * WAVE), 0, ctx->stream,
-                               domain, words, l, r, o, om, fz, w);
+        if (mode == OUT_FUSED) {  // a wave per batch of rows
+            const uint32_t batch = row_batch(domain);
+            const uint32_t blocks = (domain + GW * batch - 1) / (GW * batch);
+            hipLaunchKernelGGL(k_csr_gather_fused, dim3(blocks), dim3(GW * WAVE), 0, ctx->stream,
+                               domain, words, batch, l, r, o, om, fz, w);
             XH_CHECK_HIP(hipGetLastError());
             return;
         }
@@ -722,7 +858,8 @@ struct ChainRun {
         }
         // the last product ORs into the candidates, or, fused, writes the new delta into them
         const int last_mode = fused ? OUT_FUSED : OUT_OR;
-        const FusedArgs fz{H.R.p, H.rmask.p, H.dmask[H.dcur ^ 1].p, cnt_of(r.head)};
+        const FusedArgs fz{H.R.p, H.rmask.p, cnt_of(r.head), no_clear ? 1u : 0u, no_clear ? H.dspare.p : nullptr,
+                           words};
         uint64_t *last_mask = fused ? H.dmask[H.dcur ^ 1].p : H.cmask.p;
         if (!right_to_left(r)) {  // ((a1 a2) a3) ...
             Operand left = ops[0];
@@ -746,6 +883,7 @@ struct ChainRun {
                 right = Operand{o, nullptr, nullptr, om};
             }
         }
+        if (fused && no_clear) H.spare_zeroed = true;
     }
 
     // The variant can write its head's new delta directly (OUT_FUSED) when it
@@ -791,12 +929,16 @@ struct ChainRun {
         return false;
     }
 
-    // Before an iteration's products: clear the counts and, for every head
-    // whose delta a fused product writes, the new delta's row mask.
+    // Before an iteration's products: clear the counts (of every queued
+    // iteration, at the first) and, for every head whose delta a fused product
+    // writes, the new delta's row mask (already clear when every iteration is
+    // fused: the previous product cleared it).
     void begin_iteration(const std::vector<char> &fused) {
-        fill_u64(ctx, reinterpret_cast<uint64_t *>(cnt_of(0)), 0ull, (uint64_t)n_preds * SPREAD);
-        for (int p : idb_list)
-            if (fused[p]) fill_u64(ctx, bit[p].dmask[bit[p].dcur ^ 1].p, 0ull, words);
+        if (slot == 0) fill_u64(ctx, reinterpret_cast<uint64_t *>(counts.p), 0ull, (uint64_t)CHUNK * n_preds * SPREAD);
+        for (int p : idb_list) {
+            bit[p].spare_zeroed = false;
+            if (fused[p] && !no_clear) fill_u64(ctx, bit[p].dmask[bit[p].dcur ^ 1].p, 0ull, words);
+        }
     }
 
     // New deltas of every IDB predicate from its candidates (or, for fused
@@ -807,11 +949,17 @@ struct ChainRun {
             uint64_t *dnew = b.dmask[b.dcur ^ 1].p;
             if (fused[p]) {
                 // the new delta is in C: retire the old delta rows, then swap the two matrices
-                hipLaunchKernelGGL(k_clear_rows, dim3(domain), dim3(FTB), 0, ctx->stream, words, b.D.p,
-                                   b.dmask[b.dcur].p);
-                XH_CHECK_HIP(hipGetLastError());
+                if (!no_clear) {
+                    hipLaunchKernelGGL(k_clear_rows, dim3(domain), dim3(FTB), 0, ctx->stream, words, b.D.p,
+                                       b.dmask[b.dcur].p);
+                    XH_CHECK_HIP(hipGetLastError());
+                }
                 std::swap(b.D.p, b.C.p);
                 b.dcur ^= 1;
+                if (no_clear) {  // the delta mask read this iteration becomes the spare, the cleared spare the next new one
+                    if (!b.spare_zeroed) fill0(b.dspare, words);
+                    std::swap(b.dmask[b.dcur ^ 1].p, b.dspare.p);
+                }
                 continue;
             }
             fill_u64(ctx, dnew, 0ull, words);
@@ -819,10 +967,13 @@ struct ChainRun {
                                   b.pmask.p, cnt_of(p)};
             {
                 Prof prof(ctx, XLOG_HIP_KERNEL_CHAIN_FINALIZE, 0.0);
+                const uint32_t batch = row_batch(domain), blocks = (domain + GW * batch - 1) / (GW * batch);
                 if (b.prev)
-                    hipLaunchKernelGGL((k_chain_finalize<true>), dim3(domain), dim3(FTB), 0, ctx->stream, words, fa);
+                    hipLaunchKernelGGL((k_chain_finalize<true>), dim3(blocks), dim3(GW * WAVE), 0, ctx->stream, domain,
+                                       words, batch, fa);
                 else
-                    hipLaunchKernelGGL((k_chain_finalize<false>), dim3(domain), dim3(FTB), 0, ctx->stream, words, fa);
+                    hipLaunchKernelGGL((k_chain_finalize<false>), dim3(blocks), dim3(GW * WAVE), 0, ctx->stream, domain,
+                                       words, batch, fa);
                 XH_CHECK_HIP(hipGetLastError());
             }
             if (b.trans) {
@@ -918,6 +1069,12 @@ void chain_fixpoint(Ctx *ctx, const std::vector<ChainRule> &rules, uint32_t n_pr
     // the fixpoint finds every delta row empty, derives nothing and counts 0,
     // so the queued iterations past it change no relation and are not reported.
     const bool chunked = run.all_fused();
+    run.no_clear = chunked;
+    if (chunked)
+        for (int p : run.idb_list) {
+            run.bit[p].dspare = Buf<uint64_t>(ctx, words);
+            run.fill0(run.bit[p].dspare, words);
+        }
     uint64_t it = 0;
     bool converged = false;
     std::vector<int> nvar(n_preds);
@@ -938,6 +1095,10 @@ void chain_fixpoint(Ctx *ctx, const std::vector<ChainRule> &rules, uint32_t n_pr
                     for (size_t j = 0; j < r.path.size(); ++j)
                         if (idb[r.path[j].pred] && run.bit[r.path[j].pred].dcount && nvar[r.head] == 1)
                             fused[r.head] = run.can_fuse(r, (int)j);
+                // every head's one variant is fusable: fused even when its input delta is empty now (its
+                // queued iterations may find one non-empty, and C is not kept clear for other products)
+                if (run.no_clear)
+                    for (int p : run.idb_list) fused[p] = 1;
             }
             run.begin_iteration(fused);
             for (const ChainRule &r : rules)
