@@ -10,7 +10,10 @@ from xlog_amd import JOIN_ANTI, JOIN_INNER, JOIN_SEMI, XlogError, pack, unpack
 
 pytestmark = pytest.mark.gpu
 
-SIZES = [0, 1, 2, 63, 64, 65, 255, 256, 4095, 4096, 4097, 8191, 70000, (1 << 20) + 17]
+# the last three span 129, 513 and 769 sort tiles of 8192 keys: tile chunks of
+# 2 and 8 per XCD, and a last group of blocks partly without a tile
+SIZES = [0, 1, 2, 63, 64, 65, 255, 256, 4095, 4096, 4097, 8191, 70000, (1 << 20) + 17, (1 << 22) + 3,
+         3 * (1 << 21) + 5]
 
 
 def _note(msg):
