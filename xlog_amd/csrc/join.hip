@@ -16,7 +16,7 @@
 //            tile total is written.  emit: after a scan of the tile totals,
 //            each wave expands its 64 rows' runs cooperatively: lane j of a
 //            round writes output j, j+64, ... of the wave, found by a
-//            64-entry binary search over the per-row prefix in LDS, so
+//            6-step binary lifting over the per-row prefix in LDS, so
 //            writes are contiguous across lanes and a hot key's long run is
 //            shared by all lanes instead of serialising one thread.
 //            The projection is fused into the emit.
@@ -298,17 +298,27 @@ __global__ __launch_bounds__(JB) void k_probe_emit(ProbeArgs a, const uint64_t *
             uint64_t prow[EMIT_UNROLL], bpos[EMIT_UNROLL];
             uint32_t pay[EMIT_UNROLL];
             uint64_t gw[EMIT_UNROLL];
+            // row of output j: the largest s with ex[s] <= j (ex[0] = 0 and ex
+            // is non-decreasing, so an empty row resolves to the next
+            // non-empty one), by binary lifting in 6 fixed steps; the
+            // EMIT_UNROLL searches advance level by level, so their LDS reads
+            // overlap instead of forming EMIT_UNROLL dependent chains
+            int lo[EMIT_UNROLL];
+#pragma unroll
+            for (int u = 0; u < EMIT_UNROLL; ++u) lo[u] = 0;
+#pragma unroll
+            for (int step = WAVE / 2; step > 0; step >>= 1) {
+#pragma unroll
+                for (int u = 0; u < EMIT_UNROLL; ++u) {
+                    const uint64_t j = j0 + (uint64_t)u * WAVE;
+                    lo[u] += s_ex[wave][lo[u] + step] <= j ? step : 0;  // lo[u] + step <= WAVE - 1
+                }
+            }
 #pragma unroll
             for (int u = 0; u < EMIT_UNROLL; ++u) {
                 const uint64_t j = j0 + (uint64_t)u * WAVE;
-                // largest s with ex[s] <= j
-                int lo = 0, hi = WAVE - 1;
-                while (lo < hi) {
-                    int mid = (lo + hi + 1) >> 1;
-                    if (s_ex[wave][mid] <= j) lo = mid; else hi = mid - 1;
-                }
-                prow[u] = s_row[wave][lo];
-                bpos[u] = s_st[wave][lo] + (j - s_ex[wave][lo]);
+                prow[u] = s_row[wave][lo[u]];
+                bpos[u] = s_st[wave][lo[u]] + (j - s_ex[wave][lo[u]]);
                 const bool live = j < total;
                 const bool grp = (bpos[u] & GROUP_BIT) != 0;
                 pay[u] = (live && !grp && a.payload) ? a.payload[bpos[u]] : 0u;
