@@ -191,8 +191,13 @@ void xlog_hip_join_index_free(xlog_hip_join_index *index);
  * relational.rs:3041-3255; NESTED_LOOP_TOTAL_THRESHOLD, provider/mod.rs:1030). */
 xlog_hip_status xlog_hip_nested_loop_join(xlog_hip_ctx *ctx, const xlog_hip_rel *left, const xlog_hip_rel *right,
                                           uint32_t left_key, uint32_t right_key, xlog_hip_rel **out);
-/* Inner join on one u32 key column, left ++ right columns, for inputs sorted
- * on their key (reference: sort_merge_join_v2_inner_u32_1key, relational.rs:3401-3728). */
+/* Sort-merge inner join on one u32 key column, left ++ right columns
+ * (reference: sort_merge_join_v2_inner_u32_1key, relational.rs:3401-3728).
+ * The reference requires both inputs sorted ascending on their key and at most
+ * 4,000,000 row pairs; here an input whose key column is not sorted is sorted
+ * first and there is no pair cap.  Left rows are matched to the right side's
+ * runs of equal keys along the merge path; rows come out in left key order,
+ * the right rows of a run in input order. */
 xlog_hip_status xlog_hip_sort_merge_join(xlog_hip_ctx *ctx, const xlog_hip_rel *left, const xlog_hip_rel *right,
                                          uint32_t left_key, uint32_t right_key, xlog_hip_rel **out);
 /* Fused join + projection: ChainJoin = Project(Join) (crates/xlog-logic/src/promote.rs:1020-1060,

@@ -710,6 +710,94 @@ static xlog_hip_rel *op_join(Ctx *ctx, const xlog_hip_rel *l, const xlog_hip_rel
     return op_join_indexed(ctx, l, lk, J, r->arity, rk, type, out_cols);
 }
 
+static bool column_sorted(Ctx *ctx, const xlog_hip_rel *rel, uint32_t col) {
+    if (rel->rows < 2) return true;
+    Buf<uint32_t> flag(ctx, 1);
+    fill_u32(ctx, flag.p, 0u, 1);
+    LAUNCH_1D(k_col_unsorted, rel->rows, rel->w[0], rel->w[1], (int)rel->arity, (int)col, rel->rows, flag.p);
+    uint32_t h = 0;
+    XH_CHECK_HIP(hipMemcpyAsync(&h, flag.p, 4, hipMemcpyDeviceToHost, ctx->stream));
+    ctx->sync();
+    return h == 0;
+}
+
+// Sort-merge inner join (reference sort_merge_join_v2_inner_u32_1key,
+// relational.rs:3401-3571): output columns left ++ right like the hash join.
+// The reference requires both sides sorted ascending on their key and at
+// most 4,000,000 row pairs; here a side whose key column is not sorted is
+// sorted (stably, key word only) and there is no pair cap.  The right side's
+// runs of equal keys are matched to the left rows along the merge path
+// (smj_lookup); the matches are expanded by the probe's count / emit.  Rows
+// come out left-row-major (in key order), right rows of a run in input order.
+static xlog_hip_rel *op_sort_merge_join(Ctx *ctx, const xlog_hip_rel *l, const xlog_hip_rel *r, uint32_t lk,
+                                        uint32_t rk) {
+    XH_REQUIRE(l && r, XLOG_HIP_INVALID_ARG, "join input is NULL");
+    XH_REQUIRE(lk < l->arity && rk < r->arity, XLOG_HIP_INVALID_ARG, "join key column out of range");
+    XH_REQUIRE(l->arity <= 2 && r->arity <= 2, XLOG_HIP_UNSUPPORTED, "join: input arity above 2 is not supported");
+    const uint32_t arity = l->arity + r->arity;
+    if (l->rows == 0 || r->rows == 0) return rel_new(ctx, arity, 0);
+    // right side as (key << 32) | other column, ordered by key
+    const uint64_t nr = r->rows;
+    uint64_t *rs = static_cast<uint64_t *>(ctx->alloc(nr * sizeof(uint64_t)));
+    if (r->arity == 2 && rk == 0) copy_d2d(ctx, rs, r->w[0], nr);
+    else swap_words(ctx, r->w[0], nr, rs);  // arity 1 keeps c0 in the low word
+    if (!column_sorted(ctx, r, rk)) rs = sort_keys(ctx, rs, nr, true, 4, 8);
+    JoinIndex J;  // runs and payload only; the sort-merge lookup needs no hash table
+    J.n = nr;
+    Buf<uint32_t> run_key(ctx, nr);
+    Buf<uint64_t> run_start(ctx, nr + 1);
+    {
+        Buf<uint64_t> cnt(ctx, 1);
+        select_runs(ctx, rs, nr, run_key.p, run_start.p, cnt.p);
+        J.ix.nruns = read_count(ctx, cnt.p);
+    }
+    fill_u64(ctx, run_start.p + J.ix.nruns, nr, 1);  // run_start[nruns] = end
+    J.payload = Buf<uint32_t>(ctx, nr);
+    low_words(ctx, rs, nr, J.payload.p);
+    ctx->free(rs);
+    // left side ordered by its key column (stable: key digits only)
+    const int pcol = probe_vidx(l->arity, lk);
+    uint64_t *ls = nullptr;
+    const uint64_t *probe = l->w[0];
+    if (!column_sorted(ctx, l, lk)) {
+        ls = static_cast<uint64_t *>(ctx->alloc(l->rows * sizeof(uint64_t)));
+        copy_d2d(ctx, ls, l->w[0], l->rows);
+        ls = sort_keys(ctx, ls, l->rows, true, pcol ? 0 : 4, pcol ? 4 : 8);
+        probe = ls;
+    }
+    Buf<uint64_t> pre_start(ctx, l->rows);
+    Buf<uint32_t> pre_cnt(ctx, l->rows);
+    {
+        Prof prof(ctx, XLOG_HIP_KERNEL_MERGE, 8.0 * (double)l->rows + 4.0 * (double)J.ix.nruns);
+        smj_lookup(ctx, probe, l->rows, pcol, run_key.p, run_start.p, J.ix.nruns, pre_start.p, pre_cnt.p);
+    }
+    std::vector<int> vmap;  // value index of every output column (left ++ right)
+    for (uint32_t c = 0; c < l->arity; ++c) vmap.push_back(probe_vidx(l->arity, c));
+    for (uint32_t c = 0; c < r->arity; ++c) vmap.push_back(c == rk ? 2 : 3);
+    int oc[4] = {0, 0, 0, 0};
+    for (size_t i = 0; i < vmap.size(); ++i) oc[i] = vmap[i];
+    ProbeJob job;
+    job.probe = probe;
+    job.n = l->rows;
+    job.pcol = pcol;
+    job.ix = &J.ix;
+    job.payload = J.payload.p;
+    job.pre_start = pre_start.p;
+    job.pre_cnt = pre_cnt.p;
+    const uint64_t total = probe_prepare(ctx, job);
+    xlog_hip_rel *out;
+    if (total == 0) {
+        out = rel_new(ctx, arity, 0);
+    } else {
+        uint64_t *o0 = static_cast<uint64_t *>(ctx->alloc(total * sizeof(uint64_t)));
+        uint64_t *o1 = arity > 2 ? static_cast<uint64_t *>(ctx->alloc(total * sizeof(uint64_t))) : nullptr;
+        probe_emit_range(ctx, job, 0, job.tiles, total, (int)arity, oc, o0, o1);
+        out = rel_adopt(ctx, arity, total, o0, o1, 0);
+    }
+    if (ls) ctx->free(ls);
+    return out;
+}
+
 // Nested-loop inner join (reference nested_loop_join_v2_inner_u32_1key,
 // relational.rs:3041-3255): same output columns as the inner hash join, rows
 // in left-row-major, right-row order; refused above rows_l * rows_r =
@@ -1997,7 +2085,7 @@ xlog_hip_status xlog_hip_sort_merge_join(xlog_hip_ctx *ctx, const xlog_hip_rel *
     return guarded([&] {
         Ctx *c = C(ctx);
         OUT_GUARD;
-        *out = op_join(c, left, right, left_key, right_key, XLOG_HIP_JOIN_INNER, nullptr);
+        *out = op_sort_merge_join(c, left, right, left_key, right_key);
     });
 }
 xlog_hip_status xlog_hip_join_project(xlog_hip_ctx *ctx, const xlog_hip_rel *left, const xlog_hip_rel *right,
@@ -2033,19 +2121,11 @@ xlog_hip_status xlog_hip_project(xlog_hip_ctx *ctx, const xlog_hip_rel *in, cons
 }
 xlog_hip_status xlog_hip_is_sorted(xlog_hip_ctx *ctx, const xlog_hip_rel *rel, uint32_t col, int *sorted) {
     return guarded([&] {
-        Ctx *ctxp = C(ctx);
-        Ctx *ctx = ctxp;
+        Ctx *c = C(ctx);
         need_rel(rel, "relation");
         XH_REQUIRE(sorted, XLOG_HIP_INVALID_ARG, "sorted is NULL");
         XH_REQUIRE(col < rel->arity, XLOG_HIP_INVALID_ARG, "column out of range");
-        if (rel->rows < 2) { *sorted = 1; return; }
-        Buf<uint32_t> flag(ctx, 1);
-        fill_u32(ctx, flag.p, 0u, 1);
-        LAUNCH_1D(k_col_unsorted, rel->rows, rel->w[0], rel->w[1], (int)rel->arity, (int)col, rel->rows, flag.p);
-        uint32_t h = 0;
-        XH_CHECK_HIP(hipMemcpyAsync(&h, flag.p, 4, hipMemcpyDeviceToHost, ctx->stream));
-        ctx->sync();
-        *sorted = h == 0;
+        *sorted = column_sorted(c, rel, col) ? 1 : 0;
     });
 }
 xlog_hip_status xlog_hip_exclusive_scan_u32(xlog_hip_ctx *ctx, uint32_t *dev, uint64_t n, uint64_t *total) {

@@ -262,6 +262,11 @@ struct RunIndex {
     uint64_t table_mask = 0;
 };
 void build_run_index(Ctx *ctx, const uint64_t *sorted_keys, uint64_t n, RunIndex &ix);
+// Merge-path lookup of the sort-merge join: for every row of l (sorted by the
+// key word pcol), the start and length of its run among the nr runs of
+// (run_key, run_start[0..nr]) (sorted, distinct keys); length 0 without one.
+void smj_lookup(Ctx *ctx, const uint64_t *l, uint64_t nl, int pcol, const uint32_t *run_key, const uint64_t *run_start,
+                uint64_t nr, uint64_t *start, uint32_t *cnt);
 
 // Probe: for every packed probe row p[i], key = column `pcol` of the row
 // (0 = high word, 1 = low word); each match emits
@@ -287,6 +292,10 @@ struct ProbeJob {
     const int32_t *gsel = nullptr;
     const uint64_t *gseg = nullptr;  // (start, count) per group
     const uint64_t *gsrc = nullptr;
+    // Optional precomputed lookups (sort-merge join): run start and length
+    // per probe row, used instead of the index's hash table.
+    const uint64_t *pre_start = nullptr;
+    const uint32_t *pre_cnt = nullptr;
     Buf<uint64_t> toff;  // exclusive prefix of per-tile output counts; toff[tiles] = total
     uint64_t tiles = 0, total = 0;
     int items = 16;      // probe rows per thread (set by probe_prepare); a tile is 256 * items rows

@@ -113,6 +113,10 @@ struct ProbeArgs {
     const int32_t *gsel;
     const uint64_t *gseg;
     const uint64_t *gsrc;
+    // optional precomputed lookups (sort-merge join): run start and length
+    // of every probe row; the table is not read when set
+    const uint64_t *pre_start;
+    const uint32_t *pre_cnt;
 };
 // set in a row's start when its outputs come from gsrc
 constexpr uint64_t GROUP_BIT = 1ull << 63;
@@ -127,6 +131,16 @@ __device__ __forceinline__ void lookup_batch(const ProbeArgs &a, const uint64_t 
     // register budget of 4 waves per SIMD
     constexpr int C = N < 8 ? N : 8;
     static_assert(N % C == 0, "lookup chunking");
+    if (a.pre_cnt) {  // block-uniform
+#pragma unroll
+        for (int r = 0; r < N; ++r) {
+            const uint64_t idx = wbase + (uint64_t)r * WAVE + lane;
+            const bool valid = idx < a.n;
+            start[r] = valid ? a.pre_start[idx] : 0ull;
+            cnt[r] = valid ? a.pre_cnt[idx] : 0u;
+        }
+        return;
+    }
 #pragma unroll
     for (int c0 = 0; c0 < N; c0 += C) {
         u64x2 slot[C];
@@ -350,6 +364,79 @@ __global__ __launch_bounds__(JB) void k_probe_emit(ProbeArgs a, const uint64_t *
     }
 }
 
+// Sort-merge join lookup (reference sort_merge_join_v2_inner_u32_1key,
+// relational.rs:3401-3571, kernels/join.cu:665-712, which binary-searches the
+// sorted right keys once per left row).  The left rows, sorted by key, are
+// merged with the sorted distinct run keys of the right side along the merge
+// path: a tile is 2048 consecutive items of the merged sequence, whatever mix
+// of left rows and runs they are, so every block does the same work however
+// the keys are skewed; runs go first on equal keys, so a left row's match is
+// the last run merged before it, when that run has the row's key.  Output per
+// left row: run start and length (0 without a match), for the probe's count
+// and emit, which spread each row's run over the lanes of a wave.
+constexpr int SMJ_BLOCK = 256, SMJ_ITEMS = 8, SMJ_TILE = SMJ_BLOCK * SMJ_ITEMS;
+
+// number of runs among the first d items of the merge (runs first on ties)
+template <typename RK, typename LK>
+__device__ __forceinline__ uint64_t smj_path(RK rkey, uint64_t nr, LK lkey, uint64_t nl, uint64_t d) {
+    uint64_t lo = d > nl ? d - nl : 0, hi = d < nr ? d : nr;
+    while (lo < hi) {
+        const uint64_t mid = (lo + hi) >> 1;
+        if (rkey(mid) <= lkey(d - mid - 1)) lo = mid + 1; else hi = mid;
+    }
+    return lo;
+}
+
+__global__ __launch_bounds__(SMJ_BLOCK) void k_smj_lookup(const uint64_t *__restrict__ l, uint64_t nl, int pcol,
+                                                          const uint32_t *__restrict__ run_key,
+                                                          const uint64_t *__restrict__ run_start, uint64_t nr,
+                                                          uint64_t *__restrict__ start, uint32_t *__restrict__ cnt) {
+    __shared__ uint32_t s_key[SMJ_TILE];  // the tile's runs, then its left rows
+    __shared__ uint64_t s_split[2];
+    const int tid = threadIdx.x;
+    auto lkey_g = [&](uint64_t i) { const uint64_t r = l[i]; return pcol ? (uint32_t)r : (uint32_t)(r >> 32); };
+    auto rkey_g = [&](uint64_t i) { return run_key[i]; };
+    const uint64_t total = nl + nr;
+    const uint64_t d0 = (uint64_t)blockIdx.x * SMJ_TILE;
+    const uint64_t d1 = d0 + SMJ_TILE < total ? d0 + SMJ_TILE : total;
+    if (tid < 2) s_split[tid] = smj_path(rkey_g, nr, lkey_g, nl, tid == 0 ? d0 : d1);
+    __syncthreads();
+    const uint64_t r0 = s_split[0], r1 = s_split[1];
+    const uint32_t len = (uint32_t)(d1 - d0), lr = (uint32_t)(r1 - r0), ll = len - lr;
+    const uint64_t l0 = d0 - r0;
+    for (uint32_t i = tid; i < lr; i += SMJ_BLOCK) s_key[i] = run_key[r0 + i];
+    for (uint32_t i = tid; i < ll; i += SMJ_BLOCK) s_key[lr + i] = lkey_g(l0 + i);
+    __syncthreads();
+    const uint32_t *sr = s_key, *sl = s_key + lr;
+    const uint32_t td = (uint32_t)tid * SMJ_ITEMS;
+    if (td >= len) return;
+    auto rkey_s = [&](uint64_t i) { return sr[i]; };
+    auto lkey_s = [&](uint64_t i) { return sl[i]; };
+    uint32_t ir = (uint32_t)smj_path(rkey_s, lr, lkey_s, ll, td);
+    uint32_t il = td - ir;
+    // the run merged last before this thread's first item
+    bool have = r0 + ir > 0;
+    uint64_t cur = have ? r0 + ir - 1 : 0;
+    uint32_t cur_key = have ? (ir > 0 ? sr[ir - 1] : run_key[r0 - 1]) : 0u;
+    const uint32_t end = td + SMJ_ITEMS < len ? td + SMJ_ITEMS : len;
+    for (uint32_t t = td; t < end; ++t) {
+        const bool take_r = il >= ll || (ir < lr && sr[ir] <= sl[il]);
+        if (take_r) {
+            cur = r0 + ir;
+            cur_key = sr[ir];
+            have = true;
+            ++ir;
+        } else {
+            const uint64_t row = l0 + il;
+            const bool hit = have && cur_key == sl[il];
+            const uint64_t st = hit ? run_start[cur] : 0ull;
+            start[row] = st;
+            cnt[row] = hit ? (uint32_t)(run_start[cur + 1] - st) : 0u;
+            ++il;
+        }
+    }
+}
+
 // semi / anti: flag = key found (semi) or not found (anti)
 __global__ void k_match_flags(ProbeArgs a, int want, uint8_t *__restrict__ flags) {
     uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
@@ -406,7 +493,7 @@ static int table_bits(const RunIndex &ix) {
 static ProbeArgs probe_args(const ProbeJob &job) {
     const RunIndex &ix = *job.ix;
     return ProbeArgs{job.probe, job.n, job.pcol, ix.table.p, ix.table_mask, table_bits(ix), job.payload, job.gsel,
-                     job.gseg, job.gsrc};
+                     job.gseg, job.gsrc, job.pre_start, job.pre_cnt};
 }
 
 uint64_t probe_prepare(Ctx *ctx, ProbeJob &job) {
@@ -486,8 +573,19 @@ uint64_t join_probe_project(Ctx *ctx, const uint64_t *probe, uint64_t n, int pco
 void join_match_flags(Ctx *ctx, const uint64_t *probe, uint64_t n, int pcol, const RunIndex &ix, int want,
                       uint8_t *flags) {
     if (n == 0) return;
-    ProbeArgs a{probe, n, pcol, ix.table.p, ix.table_mask, table_bits(ix), nullptr, nullptr, nullptr, nullptr};
+    ProbeArgs a{probe, n, pcol, ix.table.p, ix.table_mask, table_bits(ix), nullptr, nullptr, nullptr, nullptr,
+                nullptr, nullptr};
     hipLaunchKernelGGL(k_match_flags, dim3(grid_for(n, 256, 16384)), dim3(256), 0, ctx->stream, a, want, flags);
+    XH_CHECK_HIP(hipGetLastError());
+}
+
+void smj_lookup(Ctx *ctx, const uint64_t *l, uint64_t nl, int pcol, const uint32_t *run_key, const uint64_t *run_start,
+                uint64_t nr, uint64_t *start, uint32_t *cnt) {
+    if (nl == 0) return;
+    const uint64_t tiles = (nl + nr + SMJ_TILE - 1) / SMJ_TILE;
+    XH_REQUIRE(tiles < (1ull << 31), XLOG_HIP_CAPACITY_OVERFLOW, "sort-merge join: input too large");
+    hipLaunchKernelGGL(k_smj_lookup, dim3((unsigned)tiles), dim3(SMJ_BLOCK), 0, ctx->stream, l, nl, pcol, run_key,
+                       run_start, nr, start, cnt);
     XH_CHECK_HIP(hipGetLastError());
 }
 
