@@ -205,17 +205,23 @@ __global__ __launch_bounds__(JB) void k_probe_count(ProbeArgs a, uint64_t *__res
     }
 }
 
-// single-block exclusive scan of a u64 array; total -> *total
+// single-block exclusive scan of a u64 array; total -> *total.  Each round
+// covers 1024 x 16 elements: a thread sums 16 consecutive ones, the block
+// scans the 1024 sums, and the thread writes its 16 prefixes.
+constexpr int SCAN_SEG = 16;
 __global__ __launch_bounds__(1024) void k_scan_small(uint64_t *a, uint64_t n, uint64_t *total) {
     __shared__ uint64_t s_w[16];
-    __shared__ uint64_t s_carry;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (tid == 0) s_carry = 0;
-    __syncthreads();
-    for (uint64_t base = 0; base < n; base += 1024) {
-        uint64_t i = base + tid;
-        uint64_t v = i < n ? a[i] : 0;
-        uint64_t x = v;
+    uint64_t carry = 0;
+    for (uint64_t base = 0; base < n; base += 1024 * SCAN_SEG) {
+        const uint64_t i0 = base + (uint64_t)tid * SCAN_SEG;
+        uint64_t v[SCAN_SEG], sum = 0;
+#pragma unroll
+        for (int k = 0; k < SCAN_SEG; ++k) {
+            v[k] = i0 + k < n ? a[i0 + k] : 0ull;
+            sum += v[k];
+        }
+        uint64_t x = sum;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
             uint64_t t = __shfl_up(x, o, 64);
@@ -224,17 +230,21 @@ __global__ __launch_bounds__(1024) void k_scan_small(uint64_t *a, uint64_t n, ui
         if (lane == 63) s_w[wave] = x;
         __syncthreads();
         uint64_t wpre = 0, tot = 0;
+#pragma unroll
         for (int w = 0; w < 16; ++w) {
             if (w < wave) wpre += s_w[w];
             tot += s_w[w];
         }
-        uint64_t carry = s_carry;
-        if (i < n) a[i] = carry + wpre + x - v;
-        __syncthreads();
-        if (tid == 0) s_carry = carry + tot;
-        __syncthreads();
+        uint64_t run = carry + wpre + x - sum;
+#pragma unroll
+        for (int k = 0; k < SCAN_SEG; ++k) {
+            if (i0 + k < n) a[i0 + k] = run;
+            run += v[k];
+        }
+        carry += tot;
+        __syncthreads();  // s_w is rewritten by the next round
     }
-    if (tid == 0) *total = s_carry;
+    if (tid == 0) *total = carry;
 }
 
 // Output spec: up to 4 selected values among v0 = probe.c0, v1 = probe.c1,
@@ -620,9 +630,12 @@ __global__ void k_group_heads(const uint64_t *__restrict__ k, uint64_t n, uint8_
 }
 
 // [start, end) of the run of high word hw in sorted out[0..n)
+// seg[2i], seg[2i + 1] = start and length of head i's rows in out; *max_len
+// (when given) = the largest length
 __global__ void k_find_segments(const uint64_t *__restrict__ out, uint64_t n, const uint64_t *__restrict__ heads,
-                                uint64_t nh, uint64_t *__restrict__ seg) {
+                                uint64_t nh, uint64_t *__restrict__ seg, unsigned long long *max_len) {
     uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    unsigned long long mx = 0;
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nh; i += stride) {
         uint32_t hw = (uint32_t)(heads[i] >> 32);
         uint64_t lo = 0, hi = n;
@@ -638,22 +651,33 @@ __global__ void k_find_segments(const uint64_t *__restrict__ out, uint64_t n, co
         }
         seg[2 * i] = s;
         seg[2 * i + 1] = lo - s;
+        mx = lo - s > mx ? lo - s : mx;
+    }
+    if (max_len) {
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const unsigned long long t = __shfl_xor(mx, o, WAVE);
+            mx = t > mx ? t : mx;
+        }
+        if ((threadIdx.x & (WAVE - 1)) == 0 && mx) atomicMax(max_len, mx);
     }
 }
 
 constexpr int SEG_MAX = 4096;
 
-// One wave per listed segment of at most 64 keys: bitonic sort across the
-// lanes (one key per lane, padding keys sort last).
+// One wave per segment of 2..64 keys (segment w, or which[w] when a list is
+// given; other lengths are left alone): bitonic sort across the lanes (one key
+// per lane, padding keys sort last).
 constexpr int SEGW_WAVES = 4;
 __global__ __launch_bounds__(SEGW_WAVES * WAVE) void k_segsort_wave(uint64_t *__restrict__ data,
                                                                    const uint64_t *__restrict__ seg,
-                                                                   const uint32_t *__restrict__ which, uint32_t nw) {
-    const uint32_t w = blockIdx.x * SEGW_WAVES + (threadIdx.x >> 6);
+                                                                   const uint32_t *__restrict__ which, uint64_t nw) {
+    const uint64_t w = (uint64_t)blockIdx.x * SEGW_WAVES + (threadIdx.x >> 6);
     if (w >= nw) return;
     const int lane = threadIdx.x & (WAVE - 1);
-    const uint32_t q = which[w];
+    const uint64_t q = which ? which[w] : w;
     const uint64_t start = seg[2 * q], len = seg[2 * q + 1];
+    if (len < 2 || len > (uint64_t)WAVE) return;
     uint64_t x = (uint64_t)lane < len ? data[start + lane] : ~0ull;
 #pragma unroll
     for (int k = 2; k <= WAVE; k <<= 1) {
@@ -671,12 +695,14 @@ __global__ __launch_bounds__(SEGW_WAVES * WAVE) void k_segsort_wave(uint64_t *__
     if ((uint64_t)lane < len) data[start + lane] = x;
 }
 
-// One block per listed segment (length <= SEG_MAX): bitonic sort in LDS.
+// One block per segment of 65..SEG_MAX keys (segment blockIdx.x + first;
+// other lengths are left alone): bitonic sort in LDS.
 __global__ __launch_bounds__(256) void k_segsort(uint64_t *__restrict__ data, const uint64_t *__restrict__ seg,
-                                                 const uint32_t *__restrict__ which) {
+                                                 uint64_t first) {
     __shared__ uint64_t s[SEG_MAX];
-    const uint32_t q = which[blockIdx.x];
+    const uint64_t q = first + blockIdx.x;
     const uint64_t start = seg[2 * q], len = seg[2 * q + 1];
+    if (len <= (uint64_t)WAVE || len > (uint64_t)SEG_MAX) return;  // block-uniform
     uint32_t m = 1;
     while (m < len) m <<= 1;
     for (uint32_t i = threadIdx.x; i < m; i += blockDim.x) s[i] = i < len ? data[start + i] : ~0ull;
@@ -746,7 +772,7 @@ void group_segments(Ctx *ctx, const uint64_t *sorted, uint64_t n, const uint64_t
                     uint64_t *seg) {
     if (!nh) return;
     hipLaunchKernelGGL(k_find_segments, dim3(grid_for(nh, 256, 16384)), dim3(256), 0, ctx->stream, sorted, n,
-                       head_keys, nh, seg);
+                       head_keys, nh, seg, nullptr);
     XH_CHECK_HIP(hipGetLastError());
 }
 
@@ -756,51 +782,38 @@ void group_segments(Ctx *ctx, const uint64_t *sorted, uint64_t n, const uint64_t
 void sort_segments(Ctx *ctx, uint64_t *data, uint64_t n, const uint64_t *heads, uint64_t nh) {
     if (!nh || !n) return;
     Buf<uint64_t> seg(ctx, 2 * nh);
+    Buf<unsigned long long> mx(ctx, 1);
+    fill_u64(ctx, reinterpret_cast<uint64_t *>(mx.p), 0ull, 1);
     hipLaunchKernelGGL(k_find_segments, dim3(grid_for(nh, 256, 16384)), dim3(256), 0, ctx->stream, data, n, heads,
-                       nh, seg.p);
+                       nh, seg.p, mx.p);
     XH_CHECK_HIP(hipGetLastError());
+    // segments of up to 64 keys (the common case: probe rows sharing an out
+    // column) need no host round trip: one wave per segment, all segments
+    hipLaunchKernelGGL(k_segsort_wave, dim3((unsigned)((nh + SEGW_WAVES - 1) / SEGW_WAVES)), dim3(SEGW_WAVES * WAVE),
+                       0, ctx->stream, data, seg.p, nullptr, nh);
+    XH_CHECK_HIP(hipGetLastError());
+    ctx->read_scalars(mx.p, 1);
+    const uint64_t max_len = ctx->host_scalars[0];
+    if (max_len <= (uint64_t)WAVE) return;
+    for (uint64_t off = 0; off < nh; off += (1u << 30)) {
+        const uint64_t cnt = std::min<uint64_t>(nh - off, 1u << 30);
+        hipLaunchKernelGGL(k_segsort, dim3((unsigned)cnt), dim3(256), 0, ctx->stream, data, seg.p, off);
+        XH_CHECK_HIP(hipGetLastError());
+    }
+    if (max_len <= (uint64_t)SEG_MAX) return;
+    // longer segments: radix sort of the slice (low words; the high words are
+    // equal inside a segment)
     std::vector<uint64_t> h(2 * nh);
     XH_CHECK_HIP(hipMemcpyAsync(h.data(), seg.p, 2 * nh * sizeof(uint64_t), hipMemcpyDeviceToHost, ctx->stream));
     ctx->sync();
-    std::vector<uint32_t> tiny, small;
-    std::vector<uint64_t> large;
-    tiny.reserve(nh);
     for (uint64_t i = 0; i < nh; ++i) {
-        uint64_t len = h[2 * i + 1];
-        if (len < 2) continue;
-        if (len <= (uint64_t)WAVE) tiny.push_back((uint32_t)i);
-        else if (len <= (uint64_t)SEG_MAX) small.push_back((uint32_t)i);
-        else large.push_back(i);
-    }
-    if (!tiny.empty()) {
-        XH_REQUIRE(tiny.size() < (1ull << 32), XLOG_HIP_CAPACITY_OVERFLOW, "segment sort: too many segments");
-        Buf<uint32_t> which(ctx, tiny.size());
-        XH_CHECK_HIP(hipMemcpyAsync(which.p, tiny.data(), tiny.size() * sizeof(uint32_t), hipMemcpyHostToDevice,
-                                    ctx->stream));
-        const uint32_t nw = (uint32_t)tiny.size();
-        hipLaunchKernelGGL(k_segsort_wave, dim3((nw + SEGW_WAVES - 1) / SEGW_WAVES), dim3(SEGW_WAVES * WAVE), 0,
-                           ctx->stream, data, seg.p, which.p, nw);
-        XH_CHECK_HIP(hipGetLastError());
-        ctx->sync();  // `tiny` is pageable host memory: keep it alive until the copy has run
-    }
-    if (!small.empty()) {
-        Buf<uint32_t> which(ctx, small.size());
-        XH_CHECK_HIP(hipMemcpyAsync(which.p, small.data(), small.size() * sizeof(uint32_t), hipMemcpyHostToDevice,
-                                    ctx->stream));
-        for (size_t off = 0; off < small.size(); off += (1u << 30)) {
-            size_t cnt = std::min<size_t>(small.size() - off, 1u << 30);
-            hipLaunchKernelGGL(k_segsort, dim3((unsigned)cnt), dim3(256), 0, ctx->stream, data, seg.p, which.p + off);
-            XH_CHECK_HIP(hipGetLastError());
-        }
-        ctx->sync();  // `which` is a pageable-host-sourced buffer: keep it alive until the copy and launch finish
-    }
-    for (uint64_t i : large) {
-        uint64_t s = h[2 * i], len = h[2 * i + 1];
-        uint64_t *a = data + s;
+        const uint64_t st = h[2 * i], len = h[2 * i + 1];
+        if (len <= (uint64_t)SEG_MAX) continue;
+        uint64_t *a = data + st;
         uint64_t *b = static_cast<uint64_t *>(ctx->alloc(len * sizeof(uint64_t)));
         uint64_t *k0 = a, *k1 = b;
         uint32_t *v0 = nullptr, *v1 = nullptr;
-        radix_sort_u64(ctx, &k0, &k1, &v0, &v1, len, 0, 4);  // high words are equal inside the run
+        radix_sort_u64(ctx, &k0, &k1, &v0, &v1, len, 0, 4);
         if (k0 != a) XH_CHECK_HIP(hipMemcpyAsync(a, k0, len * 8, hipMemcpyDeviceToDevice, ctx->stream));
         ctx->free(b);
     }

@@ -3,9 +3,10 @@
 // Replaces the reference's 4-bit, 8-passes-per-u32-column sort
 // (crates/xlog-cuda/src/provider/relational.rs:1881-2357, kernels/sort.cu:28-264)
 // with a onesweep design:
-//   1. k_hist8: one read of the keys builds all eight 256-bin digit
-//      histograms in LDS; a digit whose histogram has a single non-empty bin
-//      is constant over the input and its pass is skipped.
+//   1. k_hist8: one read of the keys builds the 256-bin histograms of the
+//      digits the sort uses (all eight for a full-key sort); a digit whose
+//      histogram has a single non-empty bin is constant over the input and
+//      its pass is skipped.
 //   2. k_onesweep, once per remaining digit: a tile of TILE keys is ranked
 //      per wave with 64-lane ballot matching (stable), the tile's 256 digit
 //      counts are published and the exclusive prefix over earlier tiles is
@@ -60,8 +61,10 @@ __device__ __forceinline__ void st_status(uint32_t *p, uint32_t v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// ALL: every digit is counted (full-key sorts); otherwise only [dlo, dhi)
+template <bool ALL>
 __global__ __launch_bounds__(256) void k_hist8(const uint64_t *__restrict__ keys, uint64_t n,
-                                               uint32_t *__restrict__ ghist) {
+                                               uint32_t *__restrict__ ghist, int dlo, int dhi) {
     // A tile of HIST_TILE keys is loaded coalesced into LDS (split into padded
     // low / high word arrays so that a lane stride of HIST_SEG keys is bank
     // conflict free); each thread then walks HIST_SEG consecutive keys and
@@ -118,6 +121,7 @@ __global__ __launch_bounds__(256) void k_hist8(const uint64_t *__restrict__ keys
                 hi = s_hi[pb + j];
 #pragma unroll
                 for (int d = 0; d < 8; ++d) {
+                    if (!ALL && (d < dlo || d >= dhi)) continue;  // digits the caller does not sort on (uniform)
                     uint32_t dg = ((d < 4 ? lo : hi) >> (8 * (d & 3))) & 255u;
                     if (dg == cur[d]) {
                         ++run[d];
@@ -129,7 +133,8 @@ __global__ __launch_bounds__(256) void k_hist8(const uint64_t *__restrict__ keys
                 }
             }
 #pragma unroll
-            for (int d = 0; d < 8; ++d) atomicAdd(&h[d][cur[d]], run[d]);
+            for (int d = 0; d < 8; ++d)
+                if (ALL || (d >= dlo && d < dhi)) atomicAdd(&h[d][cur[d]], run[d]);
         }
     }
     __syncthreads();
@@ -471,8 +476,12 @@ int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **va
     fill_u32(ctx, hist, 0u, 8 * 256);
     unsigned hg = grid_for(n, HIST_TILE, (unsigned)ctx->num_cus * 3);
     {
-        Prof prof(ctx, XLOG_HIP_KERNEL_SORT_HIST, 8.0 * (double)n);
-        hipLaunchKernelGGL(k_hist8, dim3(hg), dim3(256), 0, ctx->stream, src ? src : *keys, n, hist);
+        Prof prof(ctx, XLOG_HIP_KERNEL_SORT_HIST, 8.0 * (double)n);  // reads every key once
+        if (digit_lo == 0 && digit_hi == 8)
+            hipLaunchKernelGGL(k_hist8<true>, dim3(hg), dim3(256), 0, ctx->stream, src ? src : *keys, n, hist, 0, 8);
+        else
+            hipLaunchKernelGGL(k_hist8<false>, dim3(hg), dim3(256), 0, ctx->stream, src ? src : *keys, n, hist,
+                               digit_lo, digit_hi);
     }
     XH_CHECK_HIP(hipGetLastError());
     hipLaunchKernelGGL(k_digit_offsets, dim3(1), dim3(64), 0, ctx->stream, hist, off);
