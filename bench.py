@@ -1,6 +1,6 @@
 """Benchmark of the semi-naive relational core on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c1|c3|c4|c5]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c2u|c1|c1j|c3|c4|c4j|c5|copy]
 
 Default workload is BASELINE.json configs[1] (C2): R(a,b) |><| S(b,c) on b,
 2^24 rows each, b Zipf(1.1) over 2^20 keys on the probe side and uniform on the
@@ -92,21 +92,26 @@ def make_workload(name: str, p):
         config = {"workload": "c3: radix sort + dedup of 2^28 packed u64 tuples, 30% exact duplicates",
                   "tuples": n, "seed": datagen.seed_for(3)}
         return step, n, "input tuples", config, (keys,), state
-    if name in ("c1", "c4"):
-        cfg = datagen.C1 if name == "c1" else datagen.C4
-        cid = 1 if name == "c1" else 4
+    if name in ("c1", "c4", "c1j", "c4j"):
+        # c1j / c4j: the same closure forced onto the join route (per iteration: delta join edge, radix
+        # sort, unique and not-in-R selection, merge into R) instead of the bitmap route AUTO picks
+        from xlog_amd import ROUTE_AUTO, ROUTE_JOIN
+        route = ROUTE_JOIN if name.endswith("j") else ROUTE_AUTO
+        cfg = datagen.C1 if name.startswith("c1") else datagen.C4
+        cid = 1 if name.startswith("c1") else 4
         src, dst = datagen.random_digraph(cfg["n_vertices"], cfg["n_edges"], datagen.seed_for(cid))
         E = p.create_buffer_from_u32_columns([src, dst])
         state = {}
 
         def step():
-            outs, st = p.fixpoint(tc_plan(), [E, None])
+            outs, st = p.fixpoint(tc_plan(), [E, None], route=route)
             state["out_rows"] = outs[1].num_rows()
             state["iterations"] = st["iterations"]
             state["delta_sizes"] = st["delta_sizes"]
             state["route"] = st["route"]
 
-        config = {"workload": f"{name}: semi-naive transitive closure, G(n,m) digraph", "vertices": cfg["n_vertices"],
+        config = {"workload": f"{name}: semi-naive transitive closure, G(n,m) digraph"
+                              + (" (join route)" if route == ROUTE_JOIN else ""), "vertices": cfg["n_vertices"],
                   "edges": cfg["n_edges"], "seed": datagen.seed_for(cid)}
         return step, None, "closure tuples", config, (src, dst), state
     if name == "copy":
@@ -214,7 +219,7 @@ def cpu_baseline(name: str, inputs, budget_s: float = 30.0):
         res = entry(len(outs[4]) / dt, "pointsTo tuples/s", threads, f"{smp} in {dt:.2f}s")
         res["single_thread"] = entry(len(outs1[4]) / dt1, "pointsTo tuples/s", 1, f"same instance in {dt1:.2f}s")
         return res
-    if name == "c1":
+    if name in ("c1", "c1j"):
         src, dst = inputs
         (outs, it, _), dt = timed(lambda: oracle.seminaive(tc_plan(), [pack(src, dst), None]), threads)
         (outs1, _, _), dt1 = timed(lambda: oracle.seminaive(tc_plan(), [pack(src, dst), None]), 1)
@@ -222,7 +227,7 @@ def cpu_baseline(name: str, inputs, budget_s: float = 30.0):
                     f"full config, semi-naive oracle: {len(outs[1])} tuples, {it} iterations in {dt:.2f}s")
         res["single_thread"] = entry(len(outs1[1]) / dt1, "tuples/s", 1, f"same in {dt1:.2f}s")
         return res
-    if name == "c4":
+    if name in ("c4", "c4j"):
         src, dst = inputs
         # the semi-naive oracle over ~10^9 tuples takes far longer than the budget:
         # time the BFS closed form (closure size from every source) instead

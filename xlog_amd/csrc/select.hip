@@ -78,8 +78,16 @@ __device__ uint64_t lookback_wave(const uint64_t *status, uint64_t tile, uint64_
     return prefix;
 }
 
+// Dynamic LDS of window selections (SelDiff): the tile's window of B.
+extern __shared__ uint64_t sel_window[];
+
 // Generic single-pass selection.  Sel supplies:
-//   __device__ void setup(uint64_t tile_first_idx, uint64_t tile_last_idx, uint64_t *smem)  (thread 0)
+//   static constexpr bool kWindow: false, or true for a selection that needs
+//        a window of a second sorted array (then setup runs on all lanes of
+//        wave 0 and stage on every thread, with barriers around both)
+//   __device__ void setup(uint64_t tile_first_idx, uint64_t tile_last_idx, uint64_t *smem, int lane)
+//        (thread 0 only unless kWindow)
+//   __device__ void stage(const uint64_t *smem, int tid)          (kWindow only)
 //   __device__ bool flag(uint64_t idx, uint64_t key, uint64_t prev_key, const uint64_t *smem)
 //        (prev_key = in[idx - 1], meaningful for idx > 0)
 //   __device__ void emit(uint64_t pos, uint64_t idx, uint64_t key)
@@ -96,12 +104,24 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_select(const uint64_t *__restrict
     if (tid == 0) {
         uint64_t t = atomicAdd(ticket, 1ull) - ticket_base;
         s_tile = t;
-        uint64_t first = t * SEL_TILE, last = first + SEL_TILE;
-        if (last > n) last = n;
-        sel.setup(first, last - 1, s_sel);
+        if constexpr (!Sel::kWindow) {
+            uint64_t first = t * SEL_TILE, last = first + SEL_TILE;
+            if (last > n) last = n;
+            sel.setup(first, last - 1, s_sel, 0);
+        }
     }
     __syncthreads();
     const uint64_t tile = s_tile;
+    if constexpr (Sel::kWindow) {
+        if (wave == 0) {
+            uint64_t first = tile * SEL_TILE, last = first + SEL_TILE;
+            if (last > n) last = n;
+            sel.setup(first, last - 1, s_sel, lane);
+        }
+        __syncthreads();
+        sel.stage(s_sel, tid);
+        __syncthreads();
+    }
     const uint64_t wbase = tile * SEL_TILE + (uint64_t)wave * (SEL_ITEMS * WAVE);
     const uint64_t lt_mask = (1ull << lane) - 1ull;
     uint64_t k[SEL_ITEMS];
@@ -171,26 +191,76 @@ __device__ __forceinline__ uint64_t upper_bound_u64(const uint64_t *a, uint64_t 
 struct SelUnique {
     const uint64_t *in;
     uint64_t *out;
-    __device__ void setup(uint64_t, uint64_t, uint64_t *) const {}
+    static constexpr bool kWindow = false;
+    __device__ void setup(uint64_t, uint64_t, uint64_t *, int) const {}
     __device__ bool flag(uint64_t idx, uint64_t key, uint64_t prev, const uint64_t *) const {
         return idx == 0 || prev != key;
     }
     __device__ void emit(uint64_t pos, uint64_t, uint64_t key) const { out[pos] = key; }
 };
 
-// unique (optional) and not a member of sorted b
+// First position p in a[lo, hi) with !(a[p] < key) (UPPER: !(a[p] <= key)),
+// by all 64 lanes of a wave: each round probes 64 evenly spaced positions and
+// keeps the segment where the predicate turns, so a search over 2^30 keys
+// takes 5 rounds of one load each instead of 30 dependent loads.
+template <bool UPPER>
+__device__ uint64_t wave_bound(const uint64_t *a, uint64_t lo, uint64_t hi, uint64_t key, int lane) {
+    auto before = [&](uint64_t v) { return UPPER ? v <= key : v < key; };
+    while (hi - lo > (uint64_t)WAVE) {
+        const uint64_t step = (hi - lo + WAVE - 1) / WAVE;
+        const uint64_t pr = lo + (uint64_t)lane * step;
+        const uint64_t m = __ballot(pr < hi && before(a[pr]));  // lanes 0..c-1 (monotone)
+        const int c = __popcll(m);
+        if (c == 0) return lo;
+        const uint64_t nlo = lo + (uint64_t)(c - 1) * step + 1;  // probe c-1 is before the bound
+        const uint64_t nhi = lo + (uint64_t)c * step;             // probe c (if any) is not
+        lo = nlo;
+        hi = nhi < hi ? nhi : hi;
+    }
+    const uint64_t pr = lo + (uint64_t)lane;
+    return lo + (uint64_t)__popcll(__ballot(pr < hi && before(a[pr])));
+}
+
+// unique (optional) and not a member of sorted b.  The tile's window of b
+// (from its first key's lower bound to its last key's upper bound) is found by
+// wave 0; a window of up to WIN_CAP keys is staged in LDS and each key is
+// looked up there in 13 fixed steps, a larger one is searched in HBM.
+constexpr uint32_t WIN_CAP = 8192;  // keys (64 KB of dynamic LDS)
 template <bool UNIQ>
 struct SelDiff {
+    static constexpr bool kWindow = true;
     const uint64_t *in;
     const uint64_t *b;
     uint64_t nb;
     uint64_t *out;
-    __device__ void setup(uint64_t first, uint64_t last, uint64_t *s) const {
-        s[0] = lower_bound_u64(b, 0, nb, in[first]);
-        s[1] = upper_bound_u64(b, s[0], nb, in[last]);
+    // s[0], s[1]: window [s0, s1) of b; s[2]: 1 when staged in LDS
+    __device__ void setup(uint64_t first, uint64_t last, uint64_t *s, int lane) const {
+        const uint64_t s0 = wave_bound<false>(b, 0, nb, in[first], lane);
+        const uint64_t s1 = wave_bound<true>(b, s0, nb, in[last], lane);
+        if (lane == 0) {
+            s[0] = s0;
+            s[1] = s1;
+            s[2] = s1 - s0 <= WIN_CAP ? 1u : 0u;
+        }
+    }
+    __device__ void stage(const uint64_t *s, int tid) const {
+        if (!s[2]) return;
+        const uint64_t s0 = s[0];
+        const uint32_t len = (uint32_t)(s[1] - s0);
+        for (uint32_t i = tid; i < len; i += SEL_BLOCK) sel_window[i] = b[s0 + i];
     }
     __device__ bool flag(uint64_t idx, uint64_t key, uint64_t prev, const uint64_t *s) const {
         if (UNIQ && idx != 0 && prev == key) return false;
+        if (s[2]) {
+            // elements of the window below key: binary lifting over <= WIN_CAP entries
+            const uint32_t len = (uint32_t)(s[1] - s[0]);
+            uint32_t pos = 0;
+#pragma unroll
+            for (uint32_t step = WIN_CAP / 2; step > 0; step >>= 1)
+                if (pos + step <= len && sel_window[pos + step - 1] < key) pos += step;
+            if (pos + 1 <= len && sel_window[pos] < key) ++pos;  // pos counts every entry < key
+            return !(pos < len && sel_window[pos] == key);
+        }
         uint64_t p = lower_bound_u64(b, s[0], s[1], key);
         return !(p < s[1] && b[p] == key);
     }
@@ -200,7 +270,8 @@ struct SelDiff {
 struct SelFlags {
     const uint8_t *flags;
     uint64_t *out;
-    __device__ void setup(uint64_t, uint64_t, uint64_t *) const {}
+    static constexpr bool kWindow = false;
+    __device__ void setup(uint64_t, uint64_t, uint64_t *, int) const {}
     __device__ bool flag(uint64_t idx, uint64_t, uint64_t, const uint64_t *) const { return flags[idx] != 0; }
     __device__ void emit(uint64_t pos, uint64_t, uint64_t key) const { out[pos] = key; }
 };
@@ -212,7 +283,8 @@ struct SelGroupMembers {
     const uint64_t *in;
     uint64_t n;
     uint64_t *out_key, *out_pos;
-    __device__ void setup(uint64_t, uint64_t, uint64_t *) const {}
+    static constexpr bool kWindow = false;
+    __device__ void setup(uint64_t, uint64_t, uint64_t *, int) const {}
     __device__ bool flag(uint64_t idx, uint64_t key, uint64_t prev, const uint64_t *) const {
         const uint32_t h = (uint32_t)(key >> 32);
         return (idx > 0 && (uint32_t)(prev >> 32) == h) || (idx + 1 < n && (uint32_t)(in[idx + 1] >> 32) == h);
@@ -228,7 +300,8 @@ struct SelGroupHeads {
     const uint64_t *mpos;
     uint64_t *out_key;
     int32_t *gsel;
-    __device__ void setup(uint64_t, uint64_t, uint64_t *) const {}
+    static constexpr bool kWindow = false;
+    __device__ void setup(uint64_t, uint64_t, uint64_t *, int) const {}
     __device__ bool flag(uint64_t idx, uint64_t key, uint64_t prev, const uint64_t *) const {
         return idx == 0 || (uint32_t)(prev >> 32) != (uint32_t)(key >> 32);
     }
@@ -242,7 +315,8 @@ struct SelRuns {
     const uint64_t *in;
     uint32_t *run_key;
     uint64_t *run_start;
-    __device__ void setup(uint64_t, uint64_t, uint64_t *) const {}
+    static constexpr bool kWindow = false;
+    __device__ void setup(uint64_t, uint64_t, uint64_t *, int) const {}
     __device__ bool flag(uint64_t idx, uint64_t key, uint64_t prev, const uint64_t *) const {
         return idx == 0 || (prev >> 32) != (key >> 32);
     }
@@ -386,7 +460,8 @@ static void run_select(Ctx *ctx, const uint64_t *in, uint64_t n, const Sel &sel,
     uint64_t *status = select_status(ctx, tiles, &tag);
     unsigned long long tb = ctx->take_tickets(1, tiles);
     Prof prof(ctx, XLOG_HIP_KERNEL_SELECT, 8.0 * (double)n);
-    hipLaunchKernelGGL(k_select<Sel>, dim3((unsigned)tiles), dim3(SEL_BLOCK), 0, ctx->stream, in, n, sel, d_count,
+    const size_t dyn = Sel::kWindow ? (size_t)WIN_CAP * sizeof(uint64_t) : 0;
+    hipLaunchKernelGGL(k_select<Sel>, dim3((unsigned)tiles), dim3(SEL_BLOCK), dyn, ctx->stream, in, n, sel, d_count,
                        status, tag, ctx->tickets + 1, tb, tiles);
     XH_CHECK_HIP(hipGetLastError());
 }
