@@ -738,32 +738,39 @@ static xlog_hip_rel *op_sort_merge_join(Ctx *ctx, const xlog_hip_rel *l, const x
     if (l->rows == 0 || r->rows == 0) return rel_new(ctx, arity, 0);
     // right side as (key << 32) | other column, ordered by key
     const uint64_t nr = r->rows;
-    uint64_t *rs = static_cast<uint64_t *>(ctx->alloc(nr * sizeof(uint64_t)));
-    if (r->arity == 2 && rk == 0) copy_d2d(ctx, rs, r->w[0], nr);
-    else swap_words(ctx, r->w[0], nr, rs);  // arity 1 keeps c0 in the low word
-    if (!column_sorted(ctx, r, rk)) rs = sort_keys(ctx, rs, nr, true, 4, 8);
+    // every buffer of this operator is owned by a Buf, so an error on the way frees them
+    auto adopt = [&](uint64_t *q, uint64_t count) {
+        Buf<uint64_t> b;
+        b.ctx = ctx;
+        b.p = q;
+        b.n = count;
+        return b;
+    };
+    Buf<uint64_t> rs(ctx, nr);
+    if (r->arity == 2 && rk == 0) copy_d2d(ctx, rs.p, r->w[0], nr);
+    else swap_words(ctx, r->w[0], nr, rs.p);  // arity 1 keeps c0 in the low word
+    if (!column_sorted(ctx, r, rk)) rs = adopt(sort_keys(ctx, rs.p, nr, false, 4, 8), nr);
     JoinIndex J;  // runs and payload only; the sort-merge lookup needs no hash table
     J.n = nr;
     Buf<uint32_t> run_key(ctx, nr);
     Buf<uint64_t> run_start(ctx, nr + 1);
     {
         Buf<uint64_t> cnt(ctx, 1);
-        select_runs(ctx, rs, nr, run_key.p, run_start.p, cnt.p);
+        select_runs(ctx, rs.p, nr, run_key.p, run_start.p, cnt.p);
         J.ix.nruns = read_count(ctx, cnt.p);
     }
     fill_u64(ctx, run_start.p + J.ix.nruns, nr, 1);  // run_start[nruns] = end
     J.payload = Buf<uint32_t>(ctx, nr);
-    low_words(ctx, rs, nr, J.payload.p);
-    ctx->free(rs);
+    low_words(ctx, rs.p, nr, J.payload.p);
+    rs = Buf<uint64_t>();
     // left side ordered by its key column (stable: key digits only)
     const int pcol = probe_vidx(l->arity, lk);
-    uint64_t *ls = nullptr;
+    Buf<uint64_t> ls;
     const uint64_t *probe = l->w[0];
     if (!column_sorted(ctx, l, lk)) {
-        ls = static_cast<uint64_t *>(ctx->alloc(l->rows * sizeof(uint64_t)));
-        copy_d2d(ctx, ls, l->w[0], l->rows);
-        ls = sort_keys(ctx, ls, l->rows, true, pcol ? 0 : 4, pcol ? 4 : 8);
-        probe = ls;
+        ls = adopt(sort_keys(ctx, const_cast<uint64_t *>(l->w[0]), l->rows, false, pcol ? 0 : 4, pcol ? 4 : 8),
+                   l->rows);
+        probe = ls.p;
     }
     Buf<uint64_t> pre_start(ctx, l->rows);
     Buf<uint32_t> pre_cnt(ctx, l->rows);
@@ -785,17 +792,10 @@ static xlog_hip_rel *op_sort_merge_join(Ctx *ctx, const xlog_hip_rel *l, const x
     job.pre_start = pre_start.p;
     job.pre_cnt = pre_cnt.p;
     const uint64_t total = probe_prepare(ctx, job);
-    xlog_hip_rel *out;
-    if (total == 0) {
-        out = rel_new(ctx, arity, 0);
-    } else {
-        uint64_t *o0 = static_cast<uint64_t *>(ctx->alloc(total * sizeof(uint64_t)));
-        uint64_t *o1 = arity > 2 ? static_cast<uint64_t *>(ctx->alloc(total * sizeof(uint64_t))) : nullptr;
-        probe_emit_range(ctx, job, 0, job.tiles, total, (int)arity, oc, o0, o1);
-        out = rel_adopt(ctx, arity, total, o0, o1, 0);
-    }
-    if (ls) ctx->free(ls);
-    return out;
+    if (total == 0) return rel_new(ctx, arity, 0);
+    Buf<uint64_t> o0(ctx, total), o1(ctx, arity > 2 ? total : 0);
+    probe_emit_range(ctx, job, 0, job.tiles, total, (int)arity, oc, o0.p, o1.p);
+    return rel_adopt(ctx, arity, total, o0.release(), o1.release(), 0);
 }
 
 // Nested-loop inner join (reference nested_loop_join_v2_inner_u32_1key,
