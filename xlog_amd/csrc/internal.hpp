@@ -296,6 +296,11 @@ struct ProbeJob {
     // per probe row, used instead of the index's hash table.
     const uint64_t *pre_start = nullptr;
     const uint32_t *pre_cnt = nullptr;
+    // probe_prepare records the count pass's lookups (12 B per probe row) and
+    // points pre_start / pre_cnt at them for the emit
+    bool record_lookups = true;
+    Buf<uint64_t> rec_start;
+    Buf<uint32_t> rec_cnt;
     Buf<uint64_t> toff;  // exclusive prefix of per-tile output counts; toff[tiles] = total
     uint64_t tiles = 0, total = 0;
     int items = 16;      // probe rows per thread (set by probe_prepare); a tile is 256 * items rows

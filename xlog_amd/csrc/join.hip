@@ -12,8 +12,9 @@
 //            load <= 0.5) maps key -> run, so a probe row reads one slot and
 //            then its run.  Keys are compared exactly, so colliding hashes
 //            cannot produce matches (join_collision_test.rs:19-194).
-//   probe  - two launches.  count: every probe row looks up its run and a
-//            tile total is written.  emit: after a scan of the tile totals,
+//   probe  - two launches.  count: every probe row looks up its run, records
+//            (run start, length) and a tile total is written.  emit: after a
+//            scan of the tile totals, reading the recorded runs,
 //            each wave expands its 64 rows' runs cooperatively: lane j of a
 //            round writes output j, j+64, ... of the wave, found by a
 //            6-step binary lifting over the per-row prefix in LDS, so
@@ -117,6 +118,10 @@ struct ProbeArgs {
     // of every probe row; the table is not read when set
     const uint64_t *pre_start;
     const uint32_t *pre_cnt;
+    // optional record of the count pass's lookups (read back by the emit as
+    // pre_start / pre_cnt)
+    uint64_t *rec_start;
+    uint32_t *rec_cnt;
 };
 // set in a row's start when its outputs come from gsrc
 constexpr uint64_t GROUP_BIT = 1ull << 63;
@@ -191,6 +196,16 @@ __global__ __launch_bounds__(JB) void k_probe_count(ProbeArgs a, uint64_t *__res
     uint64_t starts[ITEMS];
     uint32_t cnts[ITEMS];
     lookup_batch<ITEMS>(a, rows, wbase, lane, starts, cnts);
+    if (a.rec_cnt) {  // block-uniform
+#pragma unroll
+        for (int r = 0; r < ITEMS; ++r) {
+            const uint64_t idx = wbase + (uint64_t)r * WAVE + lane;
+            if (idx < a.n) {
+                a.rec_start[idx] = starts[r];
+                a.rec_cnt[idx] = cnts[r];
+            }
+        }
+    }
     uint64_t acc = 0;
 #pragma unroll
     for (int r = 0; r < ITEMS; ++r) acc += cnts[r];
@@ -503,7 +518,7 @@ static int table_bits(const RunIndex &ix) {
 static ProbeArgs probe_args(const ProbeJob &job) {
     const RunIndex &ix = *job.ix;
     return ProbeArgs{job.probe, job.n, job.pcol, ix.table.p, ix.table_mask, table_bits(ix), job.payload, job.gsel,
-                     job.gseg, job.gsrc, job.pre_start, job.pre_cnt};
+                     job.gseg, job.gsrc, job.pre_start, job.pre_cnt, nullptr, nullptr};
 }
 
 uint64_t probe_prepare(Ctx *ctx, ProbeJob &job) {
@@ -514,8 +529,17 @@ uint64_t probe_prepare(Ctx *ctx, ProbeJob &job) {
     XH_REQUIRE(job.tiles < (1ull << 31), XLOG_HIP_CAPACITY_OVERFLOW, "join probe: input too large");
     ProbeArgs a = probe_args(job);
     job.toff = Buf<uint64_t>(ctx, job.tiles + 1);
+    if (!job.pre_cnt && job.record_lookups) {
+        // the emit then reads each row's run from these arrays instead of
+        // repeating the hash-table lookup
+        job.rec_start = Buf<uint64_t>(ctx, job.n);
+        job.rec_cnt = Buf<uint32_t>(ctx, job.n);
+        a.rec_start = job.rec_start.p;
+        a.rec_cnt = job.rec_cnt.p;
+    }
     {
-        Prof prof(ctx, XLOG_HIP_KERNEL_PROBE_COUNT, 8.0 * (double)job.n);
+        // probe row + one 16-byte slot per row, + the 12-byte record when kept
+        Prof prof(ctx, XLOG_HIP_KERNEL_PROBE_COUNT, (a.rec_cnt ? 36.0 : (job.pre_cnt ? 20.0 : 24.0)) * (double)job.n);
         hipLaunchKernelGGL(k_probe_count<JITEMS>, dim3((unsigned)job.tiles), dim3(JB), 0, ctx->stream, a,
                            job.toff.p);
         XH_CHECK_HIP(hipGetLastError());
@@ -525,6 +549,10 @@ uint64_t probe_prepare(Ctx *ctx, ProbeJob &job) {
     XH_CHECK_HIP(hipGetLastError());
     ctx->read_scalars(job.toff.p + job.tiles, 1);
     job.total = ctx->host_scalars[0];
+    if (a.rec_cnt) {
+        job.pre_start = job.rec_start.p;
+        job.pre_cnt = job.rec_cnt.p;
+    }
     return job.total;
 }
 
@@ -545,9 +573,10 @@ void probe_emit_range(Ctx *ctx, const ProbeJob &job, uint64_t t0, uint64_t t1, u
     OutSpec spec{out_arity, {oc[0], oc[1], oc[2], oc[3]}};
     const uint64_t tr = tile_rows(job.items);
     uint64_t nprobe = std::min<uint64_t>(job.n, t1 * tr) - t0 * tr;
-    // probe row 8 B + slot/run 16 B per probe row; payload 4 B + output 8 B per match
+    // per probe row: the row (8 B) and its run, as a 16-byte slot or as the count
+    // pass's 12-byte record; per match: payload 4 B + output 8 B
     Prof prof(ctx, XLOG_HIP_KERNEL_PROBE_EMIT,
-              24.0 * (double)nprobe + (4.0 + 8.0 * (out_arity > 2 ? 2 : 1)) * (double)rows);
+              (job.pre_cnt ? 20.0 : 24.0) * (double)nprobe + (4.0 + 8.0 * (out_arity > 2 ? 2 : 1)) * (double)rows);
     hipLaunchKernelGGL(k_probe_emit<JITEMS>, dim3((unsigned)(t1 - t0)), dim3(JB), 0, ctx->stream, a, job.toff.p, t0,
                        spec, out0, out1);
     XH_CHECK_HIP(hipGetLastError());
@@ -584,7 +613,7 @@ void join_match_flags(Ctx *ctx, const uint64_t *probe, uint64_t n, int pcol, con
                       uint8_t *flags) {
     if (n == 0) return;
     ProbeArgs a{probe, n, pcol, ix.table.p, ix.table_mask, table_bits(ix), nullptr, nullptr, nullptr, nullptr,
-                nullptr, nullptr};
+                nullptr, nullptr, nullptr, nullptr};
     hipLaunchKernelGGL(k_match_flags, dim3(grid_for(n, 256, 16384)), dim3(256), 0, ctx->stream, a, want, flags);
     XH_CHECK_HIP(hipGetLastError());
 }
