@@ -99,6 +99,7 @@ Pool::~Pool() {
 }
 
 void Ctx::read_scalars(const void *dev, size_t count_u64) {
+    XH_REQUIRE(count_u64 <= HOST_STAGE_U64, XLOG_HIP_INVALID_ARG, "read_scalars: more than the pinned staging holds");
     XH_CHECK_HIP(hipMemcpyAsync(host_scalars, dev, count_u64 * sizeof(uint64_t), hipMemcpyDeviceToHost, stream));
     sync();
 }
@@ -1666,11 +1667,13 @@ xlog_hip_status xlog_hip_ctx_create(int device, xlog_hip_ctx **out) {
         c.num_cus = prop.multiProcessorCount;
         XH_CHECK_HIP(hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking));
         c.pool = new Pool(device);
-        XH_CHECK_HIP(hipHostMalloc((void **)&c.host_scalars, 64 * sizeof(uint64_t), hipHostMallocDefault));
+        XH_CHECK_HIP(hipHostMalloc((void **)&c.host_scalars, Ctx::HOST_STAGE_U64 * sizeof(uint64_t),
+                                   hipHostMallocDefault));
         c.tickets = static_cast<unsigned long long *>(c.alloc(16 * sizeof(unsigned long long)));
         fill_u64(&c, reinterpret_cast<uint64_t *>(c.tickets), 0ull, 16);
         XH_CHECK_HIP(hipEventCreate(&c.ev_a));
         XH_CHECK_HIP(hipEventCreate(&c.ev_b));
+        XH_CHECK_HIP(hipEventCreateWithFlags(&c.ev_sync, hipEventDisableTiming));
         c.sync();
         *out = h.release();
     });
@@ -1689,6 +1692,7 @@ void xlog_hip_ctx_destroy(xlog_hip_ctx *ctx) {
     if (c.host_scalars) (void)hipHostFree(c.host_scalars);
     if (c.ev_a) (void)hipEventDestroy(c.ev_a);
     if (c.ev_b) (void)hipEventDestroy(c.ev_b);
+    if (c.ev_sync) (void)hipEventDestroy(c.ev_sync);
     for (auto &r : c.prof_pending) {
         (void)hipEventDestroy(r.a);
         (void)hipEventDestroy(r.b);

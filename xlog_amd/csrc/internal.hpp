@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 #include <cstdint>
 #include <cstddef>
+#include <cstring>
 #include <string>
 #include <vector>
 #include <map>
@@ -92,11 +93,13 @@ struct Ctx {
     hipStream_t stream = nullptr;
     Pool *pool = nullptr;
     // pinned host staging for scalar read-backs
-    uint64_t *host_scalars = nullptr;  // 64 entries
+    static constexpr size_t HOST_STAGE_U64 = 2048;  // 16 KB: scalars, counts, the sort's 8 x 256 histogram
+    uint64_t *host_scalars = nullptr;  // HOST_STAGE_U64 entries
     // device scratch: ticket counters for tile ordering (monotone, never reset)
     unsigned long long *tickets = nullptr;  // 16 counters
     unsigned long long ticket_base[16] = {0};
     hipEvent_t ev_a = nullptr, ev_b = nullptr;
+    hipEvent_t ev_sync = nullptr;  // no timing; sync() polls it
     // statistics of the last fixpoint / op (host side)
     std::vector<uint64_t> last_delta_sizes;
     uint64_t last_iterations = 0;
@@ -146,7 +149,16 @@ struct Ctx {
         ticket_base[slot] += count;
         return b;
     }
-    void sync() { XH_CHECK_HIP(hipStreamSynchronize(stream)); }
+    // Waits for the stream by polling an event: a read-back is followed by a
+    // launch that depends on the value, and a blocking wait's wake-up adds tens
+    // of microseconds of idle device per read-back (the host core spins instead).
+    void sync() {
+        XH_CHECK_HIP(hipEventRecord(ev_sync, stream));
+        hipError_t e;
+        while ((e = hipEventQuery(ev_sync)) == hipErrorNotReady) {
+        }
+        XH_CHECK_HIP(e);
+    }
     // D2H of a few u64 scalars through pinned memory (synchronises)
     void read_scalars(const void *dev, size_t count_u64);
 };

@@ -488,8 +488,9 @@ int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **va
     XH_CHECK_HIP(hipGetLastError());
     // host copy of the histograms decides which digit passes are needed
     uint32_t h_hist[8 * 256];
-    XH_CHECK_HIP(hipMemcpyAsync(h_hist, hist, sizeof(h_hist), hipMemcpyDeviceToHost, ctx->stream));
-    ctx->sync();
+    constexpr size_t hist_words = sizeof(h_hist) / 8;  // the 8 KB histogram in u64 words of the pinned staging
+    ctx->read_scalars(hist, hist_words);
+    memcpy(h_hist, ctx->host_scalars, sizeof(h_hist));
 
     int passes = 0;
     int cur = 0;  // status buffer for the next pass
