@@ -19,6 +19,8 @@
 // for tiles of earlier-dispatched blocks.
 #include "internal.hpp"
 
+#include <atomic>
+
 namespace xh {
 
 namespace {
@@ -439,14 +441,15 @@ static SortState &sort_state(Ctx *ctx, uint64_t tiles) {
 // queried once per process): the tile order needs 8 * chunk of them.
 template <bool HAS_VAL, int BLOCK, int ITEMS>
 static uint32_t pass_capacity(Ctx *ctx) {
-    static int per_cu = 0;
-    if (per_cu == 0) {
-        int b = 0;
+    static std::atomic<int> per_cu{0};  // contexts on other threads may ask at the same time
+    int b = per_cu.load(std::memory_order_relaxed);
+    if (b == 0) {
         XH_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(
             &b, reinterpret_cast<const void *>(&k_onesweep<HAS_VAL, BLOCK, ITEMS>), BLOCK, 0));
-        per_cu = b > 0 ? b : 1;
+        if (b <= 0) b = 1;
+        per_cu.store(b, std::memory_order_relaxed);
     }
-    return (uint32_t)ctx->num_cus * (uint32_t)per_cu;
+    return (uint32_t)ctx->num_cus * (uint32_t)b;
 }
 
 int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **vals, uint32_t **vals_alt,
