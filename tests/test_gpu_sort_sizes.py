@@ -1,0 +1,82 @@
+"""GPU parity of the radix sort at every tile-order chunk size.
+
+The digit passes deal tiles to the XCDs in chunks of consecutive tiles
+(xlog_amd/csrc/sort.hip, chunk_tile): 8 tiles per chunk from 512 tiles up, and
+tiles / 64 below that, so sorts of 64-511 tiles run with chunks of 1..7 and a
+last group of blocks partly without a tile.  Keys-only sorts use 8192-key tiles;
+sorts that carry a row payload (the keyed sort of arity-3/4 rows, join index
+builds) use 4096-key tiles.  Every size here is checked against numpy: the full
+sort + dedup, a stable sort on one key column, and narrow keys whose constant
+digits are skipped."""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from xlog_amd import pack
+
+pytestmark = pytest.mark.gpu
+
+TILE_K = 8192  # keys-only tile
+
+
+def _note(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+# tile counts covering chunk = 1..8 (tiles // 64, capped at 8) with ragged last tiles
+TILES = [64, 130, 200, 260, 330, 400, 450, 511, 512, 700]
+
+
+@pytest.mark.parametrize("tiles", TILES)
+def test_sort_dedup_every_chunk(provider, tiles):
+    p = provider
+    n = tiles * TILE_K - (tiles * 37) % 5000  # ragged last tile
+    _note(f"sort sizes: tiles={tiles} n={n} chunk={min(8, max(1, (n + TILE_K - 1) // TILE_K // 64))}")
+    rng = np.random.default_rng(tiles)
+    keys = rng.integers(0, 1 << 64, size=n, dtype=np.uint64)
+    keys[rng.integers(0, n, size=n // 4)] = keys[rng.integers(0, n, size=n // 4)]
+    rel = p.create_buffer_from_packed(keys)
+    assert np.array_equal(p.download_packed(p.sort(rel, [0, 1])), np.sort(keys))
+    assert np.array_equal(p.download_packed(p.dedup_full_row(rel)), oracle.sort_dedup(keys))
+
+
+@pytest.mark.parametrize("tiles", [70, 150, 333])
+def test_stable_column_sort_every_chunk(provider, tiles):
+    """Sort by the second column only: a 4-digit pass range, stable (equal keys keep input order)."""
+    p = provider
+    n = tiles * TILE_K - 123
+    rng = np.random.default_rng(1000 + tiles)
+    c0 = np.arange(n, dtype=np.uint32)  # input order, to check stability
+    c1 = rng.integers(0, 5000, n, dtype=np.uint32)
+    rel = p.create_buffer_from_u32_columns([c0, c1])
+    got = p.download_packed(p.sort(rel, [1]))
+    order = np.argsort(c1, kind="stable")
+    assert np.array_equal(got, pack(c0[order], c1[order]))
+
+
+@pytest.mark.parametrize("tiles", [90, 260, 480])
+def test_narrow_keys_every_chunk(provider, tiles):
+    """Transitive-closure-shaped keys (both columns < 2^15): four of the eight digits are constant and skipped."""
+    p = provider
+    n = tiles * TILE_K - 777
+    rng = np.random.default_rng(2000 + tiles)
+    keys = pack(rng.integers(0, 1 << 15, n), rng.integers(0, 1 << 15, n))
+    rel = p.create_buffer_from_packed(keys)
+    assert np.array_equal(p.download_packed(p.dedup_full_row(rel)), oracle.sort_dedup(keys))
+
+
+@pytest.mark.parametrize("rows", [300_000, 1_100_000, 2_000_001])
+def test_payload_sort_every_chunk(provider, rows):
+    """Arity-4 rows sorted on two columns: the key + row-index (payload) sort with 4096-key tiles."""
+    p = provider
+    rng = np.random.default_rng(rows)
+    cols = [rng.integers(0, 50, rows, dtype=np.uint32) for _ in range(2)] + \
+           [rng.integers(0, 1 << 32, rows, dtype=np.uint64).astype(np.uint32) for _ in range(2)]
+    rel = p.create_buffer_from_u32_columns(cols)
+    out = p.sort(rel, [1, 0])
+    order = np.lexsort((cols[0], cols[1]))  # primary column 1, then column 0, stable
+    for c in range(4):
+        assert np.array_equal(p.download_column(out, c), cols[c][order])
