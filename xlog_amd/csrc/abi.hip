@@ -1674,6 +1674,7 @@ xlog_hip_status xlog_hip_ctx_create(int device, xlog_hip_ctx **out) {
         XH_CHECK_HIP(hipEventCreate(&c.ev_a));
         XH_CHECK_HIP(hipEventCreate(&c.ev_b));
         XH_CHECK_HIP(hipEventCreateWithFlags(&c.ev_sync, hipEventDisableTiming));
+        XH_CHECK_HIP(hipEventCreateWithFlags(&c.ev_read, hipEventDisableTiming));
         c.sync();
         *out = h.release();
     });
@@ -1693,6 +1694,7 @@ void xlog_hip_ctx_destroy(xlog_hip_ctx *ctx) {
     if (c.ev_a) (void)hipEventDestroy(c.ev_a);
     if (c.ev_b) (void)hipEventDestroy(c.ev_b);
     if (c.ev_sync) (void)hipEventDestroy(c.ev_sync);
+    if (c.ev_read) (void)hipEventDestroy(c.ev_read);
     for (auto &r : c.prof_pending) {
         (void)hipEventDestroy(r.a);
         (void)hipEventDestroy(r.b);

@@ -100,6 +100,7 @@ struct Ctx {
     unsigned long long ticket_base[16] = {0};
     hipEvent_t ev_a = nullptr, ev_b = nullptr;
     hipEvent_t ev_sync = nullptr;  // no timing; sync() polls it
+    hipEvent_t ev_read = nullptr;  // no timing; marks a read-back that later launches may overtake
     // statistics of the last fixpoint / op (host side)
     std::vector<uint64_t> last_delta_sizes;
     uint64_t last_iterations = 0;
@@ -152,12 +153,15 @@ struct Ctx {
     // Waits for the stream by polling an event: a read-back is followed by a
     // launch that depends on the value, and a blocking wait's wake-up adds tens
     // of microseconds of idle device per read-back (the host core spins instead).
-    void sync() {
-        XH_CHECK_HIP(hipEventRecord(ev_sync, stream));
+    void wait_event(hipEvent_t ev) {
         hipError_t e;
-        while ((e = hipEventQuery(ev_sync)) == hipErrorNotReady) {
+        while ((e = hipEventQuery(ev)) == hipErrorNotReady) {
         }
         XH_CHECK_HIP(e);
+    }
+    void sync() {
+        XH_CHECK_HIP(hipEventRecord(ev_sync, stream));
+        wait_event(ev_sync);
     }
     // D2H of a few u64 scalars through pinned memory (synchronises)
     void read_scalars(const void *dev, size_t count_u64);

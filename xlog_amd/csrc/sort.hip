@@ -489,20 +489,10 @@ int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **va
     XH_CHECK_HIP(hipGetLastError());
     hipLaunchKernelGGL(k_digit_offsets, dim3(1), dim3(64), 0, ctx->stream, hist, off);
     XH_CHECK_HIP(hipGetLastError());
-    // host copy of the histograms decides which digit passes are needed
-    uint32_t h_hist[8 * 256];
-    constexpr size_t hist_words = sizeof(h_hist) / 8;  // the 8 KB histogram in u64 words of the pinned staging
-    ctx->read_scalars(hist, hist_words);
-    memcpy(h_hist, ctx->host_scalars, sizeof(h_hist));
-
     int passes = 0;
     int cur = 0;  // status buffer for the next pass
     if (st.dirty[0] == 0) cur = 0; else if (st.dirty[1] == 0) cur = 1; else cur = 0;
-    for (int dgt = digit_lo; dgt < digit_hi; ++dgt) {
-        bool trivial = false;
-        for (int b = 0; b < 256; ++b)
-            if (h_hist[dgt * 256 + b] == n) { trivial = true; break; }
-        if (trivial) continue;
+    auto launch_pass = [&](int dgt) {
         int nxt = 1 - cur;
         if (st.dirty[cur]) {  // make the buffer this pass reads clean
             fill_u32(ctx, st.status[cur], 0u, st.dirty[cur] * 256);
@@ -524,6 +514,25 @@ int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **va
         if (has_val) std::swap(*vals, *vals_alt);
         cur = nxt;
         ++passes;
+    };
+    // The host copy of the histograms decides which digit passes are needed.
+    // The pass of the lowest digit is launched before waiting for it (a pass
+    // over a constant digit is a stable copy, so it is right either way): the
+    // device works on it while the host reads the histograms and queues the
+    // rest, instead of idling through the read-back.
+    uint32_t h_hist[8 * 256];
+    static_assert(sizeof(h_hist) <= Ctx::HOST_STAGE_U64 * sizeof(uint64_t), "histograms exceed the staging");
+    XH_CHECK_HIP(hipMemcpyAsync(ctx->host_scalars, hist, sizeof(h_hist), hipMemcpyDeviceToHost, ctx->stream));
+    XH_CHECK_HIP(hipEventRecord(ctx->ev_read, ctx->stream));
+    int first = digit_lo;
+    if (digit_hi - digit_lo >= 2) launch_pass(first++);
+    ctx->wait_event(ctx->ev_read);
+    memcpy(h_hist, ctx->host_scalars, sizeof(h_hist));
+    for (int dgt = first; dgt < digit_hi; ++dgt) {
+        bool trivial = false;
+        for (int b = 0; b < 256; ++b)
+            if (h_hist[dgt * 256 + b] == n) { trivial = true; break; }
+        if (!trivial) launch_pass(dgt);
     }
     if (passes == 0 && src) XH_CHECK_HIP(hipMemcpyAsync(*keys, src, n * 8, hipMemcpyDeviceToDevice, ctx->stream));
     return passes;
