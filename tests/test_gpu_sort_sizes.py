@@ -7,7 +7,8 @@ last group of blocks partly without a tile.  Keys-only sorts use 8192-key tiles;
 sorts that carry a row payload (the keyed sort of arity-3/4 rows, join index
 builds) use 4096-key tiles.  Every size here is checked against numpy: the full
 sort + dedup, a stable sort on one key column, and narrow keys whose constant
-digits are skipped."""
+digits are skipped, and sorts whose lowest digit (the pass queued before the
+histograms are read back) is constant."""
 import sys
 
 import numpy as np
@@ -80,3 +81,40 @@ def test_payload_sort_every_chunk(provider, rows):
     order = np.lexsort((cols[0], cols[1]))  # primary column 1, then column 0, stable
     for c in range(4):
         assert np.array_equal(p.download_column(out, c), cols[c][order])
+
+
+@pytest.mark.parametrize("n", [1000, 70_001, 300 * TILE_K + 5])
+def test_constant_lowest_digit(provider, n):
+    """Keys whose lowest byte is the same everywhere.  The lowest digit's pass is
+    queued before the histograms are read back, so here it runs as a stable copy
+    and the later digits must still give the exact order."""
+    p = provider
+    rng = np.random.default_rng(3000 + n)
+    keys = (rng.integers(0, 1 << 50, n, dtype=np.uint64) << np.uint64(8)) | np.uint64(0x5A)
+    keys[rng.integers(0, n, n // 3)] = keys[rng.integers(0, n, n // 3)]
+    rel = p.create_buffer_from_packed(keys)
+    assert np.array_equal(p.download_packed(p.sort(rel, [0, 1])), np.sort(keys))
+    assert np.array_equal(p.download_packed(p.dedup_full_row(rel)), oracle.sort_dedup(keys))
+
+
+@pytest.mark.parametrize("n", [2, 4097, 200 * TILE_K + 9])
+def test_all_keys_equal(provider, n):
+    """Every digit is constant: only the speculative pass runs, and it must leave the rows intact."""
+    p = provider
+    keys = np.full(n, 0x0123456789ABCDEF, dtype=np.uint64)
+    rel = p.create_buffer_from_packed(keys)
+    assert np.array_equal(p.download_packed(p.sort(rel, [0, 1])), keys)
+    assert np.array_equal(p.download_packed(p.dedup_full_row(rel)), keys[:1])
+
+
+@pytest.mark.parametrize("n", [5000, 150 * TILE_K - 17])
+def test_stable_sort_column_with_constant_low_byte(provider, n):
+    """Sort by a column whose values are multiples of 256: its lowest digit's pass is a stable copy."""
+    p = provider
+    rng = np.random.default_rng(4000 + n)
+    c0 = np.arange(n, dtype=np.uint32)
+    c1 = (rng.integers(0, 3000, n, dtype=np.uint32) * 256).astype(np.uint32)
+    rel = p.create_buffer_from_u32_columns([c0, c1])
+    got = p.download_packed(p.sort(rel, [1]))
+    order = np.argsort(c1, kind="stable")
+    assert np.array_equal(got, pack(c0[order], c1[order]))
