@@ -13,6 +13,7 @@
 //   - union_gpu's concat + full re-sort (relational.rs:822-999) with a
 //     merge-path merge of the two sorted inputs.
 #include "internal.hpp"
+#include <type_traits>
 
 namespace xh {
 
@@ -91,6 +92,13 @@ extern __shared__ uint64_t sel_window[];
 //   __device__ bool flag(uint64_t idx, uint64_t key, uint64_t prev_key, const uint64_t *smem)
 //        (prev_key = in[idx - 1], meaningful for idx > 0)
 //   __device__ void emit(uint64_t pos, uint64_t idx, uint64_t key)
+// A predicate that also reads the following row declares kNext = true and
+// provides flag_next(idx, key, prev, next); next is 0 past the last row.
+template <class S, class = void>
+struct sel_next : std::false_type {};
+template <class S>
+struct sel_next<S, std::void_t<decltype(S::kNext)>> : std::bool_constant<S::kNext> {};
+
 template <class Sel>
 __global__ __launch_bounds__(SEL_BLOCK) void k_select(const uint64_t *__restrict__ in, uint64_t n, Sel sel,
                                                       uint64_t *__restrict__ d_count, uint64_t *status,
@@ -135,13 +143,27 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_select(const uint64_t *__restrict
     // predecessor of item r: lane-1 of the same round, lane 63 of the previous
     // round for lane 0, one extra load for the wave's first item
     uint64_t first_prev = (wbase > 0 && wbase <= n) ? in[wbase - 1] : 0ull;
+    // successor likewise: lane+1 of the same round, lane 0 of the next round
+    // for lane 63, one extra load after the wave's last item
+    uint64_t last_next = 0;
+    if constexpr (sel_next<Sel>::value) {
+        const uint64_t e = wbase + (uint64_t)SEL_ITEMS * WAVE;
+        last_next = e < n ? in[e] : 0ull;
+    }
 #pragma unroll
     for (int r = 0; r < SEL_ITEMS; ++r) {
         uint64_t idx = wbase + (uint64_t)r * WAVE + lane;
         uint64_t up = __shfl_up(k[r], 1, WAVE);
         uint64_t carry = (r > 0) ? __shfl(k[r > 0 ? r - 1 : 0], WAVE - 1, WAVE) : first_prev;
         uint64_t prev = lane ? up : carry;
-        bool f = idx < n && sel.flag(idx, k[r], prev, s_sel);
+        bool f;
+        if constexpr (sel_next<Sel>::value) {
+            uint64_t down = __shfl_down(k[r], 1, WAVE);
+            uint64_t ncarry = (r + 1 < SEL_ITEMS) ? __shfl(k[r + 1 < SEL_ITEMS ? r + 1 : r], 0, WAVE) : last_next;
+            f = idx < n && sel.flag_next(idx, k[r], prev, lane < WAVE - 1 ? down : ncarry);
+        } else {
+            f = idx < n && sel.flag(idx, k[r], prev, s_sel);
+        }
         if (f) fl |= 1ull << r;
         wc += (uint32_t)__popcll(__ballot(f));
     }
@@ -284,10 +306,11 @@ struct SelGroupMembers {
     uint64_t n;
     uint64_t *out_key, *out_pos;
     static constexpr bool kWindow = false;
+    static constexpr bool kNext = true;
     __device__ void setup(uint64_t, uint64_t, uint64_t *, int) const {}
-    __device__ bool flag(uint64_t idx, uint64_t key, uint64_t prev, const uint64_t *) const {
+    __device__ bool flag_next(uint64_t idx, uint64_t key, uint64_t prev, uint64_t next) const {
         const uint32_t h = (uint32_t)(key >> 32);
-        return (idx > 0 && (uint32_t)(prev >> 32) == h) || (idx + 1 < n && (uint32_t)(in[idx + 1] >> 32) == h);
+        return (idx > 0 && (uint32_t)(prev >> 32) == h) || (idx + 1 < n && (uint32_t)(next >> 32) == h);
     }
     __device__ void emit(uint64_t pos, uint64_t idx, uint64_t key) const {
         out_key[pos] = key;
