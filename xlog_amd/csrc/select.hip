@@ -19,16 +19,29 @@ namespace xh {
 
 namespace {
 
+// Plain selections: 16 waves x 16 rows per lane, 16,384-row tiles (measured
+// against 256/512-thread blocks and 8-64 rows per lane).  Selections that
+// stage a window of a second array keep 8,192-row tiles, whose windows fit the
+// LDS cap more often.
 #ifndef XH_SEL_BLOCK
-#define XH_SEL_BLOCK 512
+#define XH_SEL_BLOCK 1024
+#endif
+#ifndef XH_SEL_WIN_BLOCK
+#define XH_SEL_WIN_BLOCK 512
 #endif
 #ifndef XH_SEL_ITEMS
 #define XH_SEL_ITEMS 16
 #endif
 constexpr int SEL_BLOCK = XH_SEL_BLOCK;
 constexpr int SEL_ITEMS = XH_SEL_ITEMS;
-constexpr int SEL_WAVES = SEL_BLOCK / WAVE;
-constexpr int SEL_TILE = SEL_BLOCK * SEL_ITEMS;
+constexpr int SEL_WIN_BLOCK = XH_SEL_WIN_BLOCK;
+// block, waves and tile rows of k_select<Sel>
+template <class Sel>
+struct SelShape {
+    static constexpr int block = Sel::kWindow ? SEL_WIN_BLOCK : SEL_BLOCK;
+    static constexpr int waves = block / WAVE;
+    static constexpr uint64_t tile = (uint64_t)block * SEL_ITEMS;
+};
 
 // look-back status word: [63:40] epoch, [39] inclusive, [38:0] value
 constexpr uint64_t LB_INC = 1ull << 39;
@@ -100,12 +113,14 @@ template <class S>
 struct sel_next<S, std::void_t<decltype(S::kNext)>> : std::bool_constant<S::kNext> {};
 
 template <class Sel>
-__global__ __launch_bounds__(SEL_BLOCK) void k_select(const uint64_t *__restrict__ in, uint64_t n, Sel sel,
+__global__ __launch_bounds__(SelShape<Sel>::block) void k_select(const uint64_t *__restrict__ in, uint64_t n, Sel sel,
                                                       uint64_t *__restrict__ d_count, uint64_t *status,
                                                       uint64_t epoch_tag, unsigned long long *ticket,
                                                       unsigned long long ticket_base, uint64_t ntiles) {
     __shared__ uint64_t s_tile;
     __shared__ uint64_t s_prefix;
+    constexpr int SEL_WAVES = SelShape<Sel>::waves;
+    constexpr uint64_t SEL_TILE = SelShape<Sel>::tile;
     __shared__ uint32_t s_wc[SEL_WAVES];
     __shared__ uint64_t s_sel[4];
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
@@ -269,7 +284,7 @@ struct SelDiff {
         if (!s[2]) return;
         const uint64_t s0 = s[0];
         const uint32_t len = (uint32_t)(s[1] - s0);
-        for (uint32_t i = tid; i < len; i += SEL_BLOCK) sel_window[i] = b[s0 + i];
+        for (uint32_t i = tid; i < len; i += SEL_WIN_BLOCK) sel_window[i] = b[s0 + i];
     }
     __device__ bool flag(uint64_t idx, uint64_t key, uint64_t prev, const uint64_t *s) const {
         if (UNIQ && idx != 0 && prev == key) return false;
@@ -477,14 +492,15 @@ static void run_select(Ctx *ctx, const uint64_t *in, uint64_t n, const Sel &sel,
         fill_u64(ctx, d_count, 0ull, 1);
         return;
     }
-    uint64_t tiles = (n + SEL_TILE - 1) / SEL_TILE;
+    constexpr uint64_t tile_rows = SelShape<Sel>::tile;
+    uint64_t tiles = (n + tile_rows - 1) / tile_rows;
     XH_REQUIRE(tiles < (1ull << 31), XLOG_HIP_CAPACITY_OVERFLOW, "select: input too large");
     uint64_t tag;
     uint64_t *status = select_status(ctx, tiles, &tag);
     unsigned long long tb = ctx->take_tickets(1, tiles);
     Prof prof(ctx, XLOG_HIP_KERNEL_SELECT, 8.0 * (double)n);
     const size_t dyn = Sel::kWindow ? (size_t)WIN_CAP * sizeof(uint64_t) : 0;
-    hipLaunchKernelGGL(k_select<Sel>, dim3((unsigned)tiles), dim3(SEL_BLOCK), dyn, ctx->stream, in, n, sel, d_count,
+    hipLaunchKernelGGL(k_select<Sel>, dim3((unsigned)tiles), dim3(SelShape<Sel>::block), dyn, ctx->stream, in, n, sel, d_count,
                        status, tag, ctx->tickets + 1, tb, tiles);
     XH_CHECK_HIP(hipGetLastError());
 }
