@@ -1,21 +1,25 @@
 """Benchmark of the semi-naive relational core on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c2u|c1|c1j|c3|c4|c4j|c5|copy]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c4|c1|c1j|c2|c2u|c3|c4j|c5|copy]
+                    [--no-extra] [--no-cpu-baseline]
 
-Default workload is BASELINE.json configs[1] (C2): R(a,b) |><| S(b,c) on b,
-2^24 rows each, b Zipf(1.1) over 2^20 keys on the probe side and uniform on the
-build side; project (a,c), sort and dedup.  One step = the whole hot path on
-inputs already resident in HBM, as one fused join+project+dedup call: probe
-keys radix sorted by a, build index over the sorted unique (b,c) rows, count
-and emit of the ~2^28 outputs directly in (a,c) order (rows sharing their a
-value are finished on the side).  `c2u` runs the unfused join -> radix sort ->
-dedup sequence of the same step.
+Default workload is BASELINE.json configs[3] (C4), the metric's lead quantity:
+the semi-naive transitive closure of a seeded G(32768, 98304) digraph, run to
+fixpoint on inputs already resident in HBM.  One step is one whole fixpoint,
+the emit of the ~9.5 x 10^8 sorted closure tuples included; `ms_per_step` is
+the fixpoint wall time and `value` is closure tuples per second of it.
 
-Prints one JSON line.  `value` is input tuples/s (|R| + |S|) / step time, the
-reference's join-throughput definition (docs/guides/benchmarking.mdx:250-253).
-The roofline object describes the kernel with the largest share of device time,
-timed live with HIP events on the library's stream; the cpu_baseline object is
-the CPU oracle (single thread) timed on a bounded sample of the same workload.
+With the default workload the same line carries the other configs under
+`configs` (c1: TC on G(1000, 5000); c2: R(a,b) join S(b,c), project, sort +
+dedup at 2^24 rows a side; c3: sort + dedup of 2^28 packed tuples; c5: Andersen
+points-to at 10,000 variables), each with its own timing, roofline and CPU
+baseline.  c1j / c4j force the join route, c2u the unfused join -> sort ->
+dedup sequence, copy is the counter calibration kernel.
+
+Every `roofline` object describes the kernel kind with the largest share of
+device time in the timed steps, timed live with HIP events on the library's
+stream (algorithmic bytes / average launch time).  `cpu_baseline` is the CPU
+oracle (oracle/oracle.c) with every host thread and single-threaded.
 """
 from __future__ import annotations
 
@@ -33,11 +37,6 @@ import numpy as np  # noqa: E402
 
 METRIC = "semi-naive fixpoint wall time + join/sort tuples/s; % of HBM peak, 1 MI355X"
 HBM_PEAK_GBS = 8000.0
-# Measured HBM traffic / algorithmic bytes per launch from the rocprofv3 FETCH_SIZE + WRITE_SIZE runs of
-# profiles/c2_radix_probe_dedup_hbm_traffic.md and profiles/c3_radix_pass_hbm_traffic.md (FETCH scaled x2,
-# WRITE x1 by the copy calibration there): radix pass x1.07 (2^24 keys; x1.06 at 2^28), probe emit x0.95
-# (hot payload runs re-read from L2), selections x1.01.
-TRAFFIC_RATIO = {"sort_pass": 1.07, "probe_emit": 0.95, "select": 1.01}
 
 
 def log(msg: str) -> None:
@@ -241,13 +240,67 @@ def cpu_baseline(name: str, inputs, budget_s: float = 30.0):
     return None
 
 
+def measure(name: str, p, steps: int, warmup: int, with_cpu: bool) -> dict:
+    """Warm-up, then `steps` timed steps of one workload with live kernel timing;
+    returns the per-config record (timing, roofline, kernels, result, CPU baseline)."""
+    step, units, unit_desc, config, inputs, state = make_workload(name, p)
+    log(f"workload {name}: warmup {warmup}")
+    for _ in range(warmup):
+        step()
+    p.synchronize()
+    p.profile_reset()
+    p.profile_enable(True)
+    log(f"workload {name}: timing {steps} steps")
+    p.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    p.synchronize()
+    t1 = time.perf_counter()
+    p.profile_enable(False)
+    prof = p.profile_read()
+    # the same-sample GPU figure accompanies the CPU baseline (and stays out of profiler runs without it)
+    same_sample = state.pop("_extra", None)
+    extra = same_sample() if (same_sample and with_cpu) else {}
+    ms = (t1 - t0) * 1000.0 / max(1, steps)
+    if units is None:
+        units = state.get("out_rows", 0)
+    value = units / (ms / 1000.0) if ms > 0 else 0.0
+
+    # dominant kernel: the kind with the largest share of device time in the timed steps
+    dname, d = max(prof.items(), key=lambda kv: kv[1]["total_ms"])
+    avg_ms = d["total_ms"] / max(1, d["launches"])
+    bytes_per_launch = d["algo_bytes"] / max(1, d["launches"])
+    achieved = (bytes_per_launch / (avg_ms / 1000.0)) / 1e9 if avg_ms > 0 else 0.0
+    # HBM traffic comes from rocprofv3 FETCH_SIZE / WRITE_SIZE runs kept under profiles/, not from this run
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": dname,
+                "launches_per_step": d["launches"] / max(1, steps), "avg_launch_ms": round(avg_ms, 4),
+                "algo_bytes_per_launch": bytes_per_launch}
+    kernels = {k: {"launches": v["launches"], "total_ms": round(v["total_ms"], 3),
+                   "algo_GBps": round(v["algo_bytes"] / (v["total_ms"] / 1000.0) / 1e9, 1) if v["total_ms"] else None}
+               for k, v in prof.items() if v["launches"]}
+    cpu = None
+    if with_cpu:
+        log(f"workload {name}: cpu baseline (oracle, bounded sample)")
+        cpu = cpu_baseline(name, inputs)
+    result = {k: v for k, v in state.items() if k != "delta_sizes"}
+    if "delta_sizes" in state:
+        result["delta_sizes"] = state["delta_sizes"]
+    result.update(extra)
+    return {"workload": name, "value": value, "unit": "tuples/s", "value_counts": unit_desc, "ms_per_step": ms,
+            "steps": steps, "warmup": warmup, "config": config, "roofline": roofline, "cpu_baseline": cpu,
+            "kernels": kernels, "result": result}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", default="c2")
+    ap.add_argument("--workload", default="c4")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="headline workload only (no per-config entries)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; --gpus above 1 is not supported "
@@ -257,73 +310,36 @@ def main() -> int:
     from xlog_amd import HipKernelProvider
 
     p = HipKernelProvider(0)
-    step, units, unit_desc, config, inputs, state = make_workload(args.workload, p)
-    log(f"workload {args.workload}: warmup {args.warmup}")
-    for _ in range(args.warmup):
-        step()
-    p.synchronize()
-    p.profile_reset()
-    p.profile_enable(True)
-    log(f"timing {args.steps} steps")
-    p.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    p.synchronize()
-    t1 = time.perf_counter()
-    p.profile_enable(False)
-    prof = p.profile_read()
-    # the same-sample GPU figure accompanies the CPU baseline (and stays out of profiler runs without it)
-    same_sample = state.pop("_extra", None)
-    extra = same_sample() if (same_sample and not args.no_cpu_baseline) else {}
-    ms = (t1 - t0) * 1000.0 / max(1, args.steps)
-    if units is None:
-        units = state.get("out_rows", 0)
-    value = units / (ms / 1000.0) if ms > 0 else 0.0
-
-    # dominant kernel
-    dom = max(prof.items(), key=lambda kv: kv[1]["total_ms"])
-    dname, d = dom
-    avg_ms = d["total_ms"] / max(1, d["launches"])
-    bytes_per_launch = d["algo_bytes"] / max(1, d["launches"])
-    achieved = (bytes_per_launch / (avg_ms / 1000.0)) / 1e9 if avg_ms > 0 else 0.0
-    traffic = TRAFFIC_RATIO.get(dname)
-    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4),
-                "traffic": round(traffic * bytes_per_launch) if traffic else None, "kernel": dname,
-                "launches_per_step": d["launches"] / max(1, args.steps), "avg_launch_ms": round(avg_ms, 4),
-                "algo_bytes_per_launch": bytes_per_launch}
-    kernels = {k: {"launches": v["launches"], "total_ms": round(v["total_ms"], 3),
-                   "algo_GBps": round(v["algo_bytes"] / (v["total_ms"] / 1000.0) / 1e9, 1) if v["total_ms"] else None}
-               for k, v in prof.items() if v["launches"]}
-
-    cpu = None
-    if not args.no_cpu_baseline:
-        log("cpu baseline (oracle, bounded sample)")
-        cpu = cpu_baseline(args.workload, inputs)
+    head = measure(args.workload, p, args.steps, args.warmup, not args.no_cpu_baseline)
+    p.trim()
+    extras = {}
+    if args.workload == "c4" and not args.no_extra:
+        # the other configs of BASELINE.json, each with its own timing and roofline (a few steps each)
+        for name, k, w in (("c1", 20, 3), ("c2", 10, 3), ("c3", 3, 1), ("c5", 5, 2)):
+            extras[name] = measure(name, p, k, w, not args.no_cpu_baseline)
+            p.trim()
 
     out = {
         "metric": METRIC,
-        "value": value,
+        "value": head["value"],
         "unit": "tuples/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": ms,
+        "ms_per_step": head["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "u64",
         "data": "synthetic (seeded generators, xlog_amd/csrc/datagen.c)",
-        "config": {**config, "value_counts": unit_desc, "parallelism": "single GPU"},
-        "roofline": roofline,
-        "cpu_baseline": cpu,
-        "kernels": kernels,
-        "result": {k: v for k, v in state.items() if k != "delta_sizes"},
+        "config": {**head["config"], "value_counts": head["value_counts"], "parallelism": "single GPU"},
+        "roofline": head["roofline"],
+        "cpu_baseline": head["cpu_baseline"],
+        "kernels": head["kernels"],
+        "result": head["result"],
     }
-    if "delta_sizes" in state:
-        out["result"]["delta_sizes"] = state["delta_sizes"]
-    out["result"].update(extra)
+    if extras:
+        out["configs"] = {k: {kk: vv for kk, vv in v.items() if kk != "workload"} for k, v in extras.items()}
     print(json.dumps(out))
     p.close()
     return 0

@@ -52,6 +52,8 @@ def _load() -> C.CDLL:
     lib.or_union_sorted.restype = U64
     lib.or_fnv1a64.argtypes = [P, U64]
     lib.or_fnv1a64.restype = U64
+    lib.or_fnv1a64_bytes.argtypes = [P, U64]
+    lib.or_fnv1a64_bytes.restype = U64
     lib.or_join_project.argtypes = [P, U64, P, U64, I, I, I, I, C.POINTER(P)]
     lib.or_join_project.restype = C.c_int64
     lib.or_join_count.argtypes = [P, U64, P, U64, I, I]
@@ -112,6 +114,12 @@ def union_sorted(a, b) -> np.ndarray:
 def fnv1a64(keys) -> int:
     a = _u64(keys)
     return int(_lib.or_fnv1a64(_p(a), len(a)))
+
+
+def fnv1a64_bytes(data: bytes) -> int:
+    """FNV-1a 64 of a byte string."""
+    buf = C.create_string_buffer(bytes(data), max(1, len(data)))
+    return int(_lib.or_fnv1a64_bytes(C.cast(buf, C.c_void_p), len(data)))
 
 
 def join_project(l, r, lk: int, rk: int, oc0: int, oc1: int) -> np.ndarray:

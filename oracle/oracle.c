@@ -206,6 +206,14 @@ uint64_t or_fnv1a64(const uint64_t *a, uint64_t n) {
     return h;
 }
 
+/* FNV-1a 64 over a byte string (the published function itself; the key form
+ * above is this function over the keys' little-endian bytes). */
+uint64_t or_fnv1a64_bytes(const uint8_t *p, uint64_t n) {
+    uint64_t h = 0xcbf29ce484222325ULL;
+    for (uint64_t i = 0; i < n; ++i) { h ^= p[i]; h *= 0x100000001b3ULL; }
+    return h;
+}
+
 /* ------------------------------------------------------------------------ */
 /* growable u64 vector                                                       */
 /* ------------------------------------------------------------------------ */

@@ -121,6 +121,31 @@ def test_smj_merge_path_shapes(provider, case):
         assert p.download_rows(out) == _expected(l_rows, r_rows, 0, 0)
 
 
+def _mix(w0, w1):
+    """64-bit row hash of two packed words (splitmix64 finaliser over w0 ^ rotated w1)."""
+    with np.errstate(over="ignore"):
+        x = w0 ^ ((w1 << np.uint64(29)) | (w1 >> np.uint64(35))) ^ (w1 * np.uint64(0x9E3779B97F4A7C15))
+        x = (x ^ (x >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        x = (x ^ (x >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        return x ^ (x >> np.uint64(31))
+
+
+def _host_join_words(lk_, lpay, rpay, rk_):
+    """Packed words of left(lk, lpay) join right(rpay, rk) on lk = rk, output
+    (lk, lpay, rpay, rk), built with numpy from the sorted right keys."""
+    order = np.argsort(rk_, kind="stable")
+    rks, rps = rk_[order], rpay[order]
+    lo = np.searchsorted(rks, lk_, side="left")
+    hi = np.searchsorted(rks, lk_, side="right")
+    cnt = (hi - lo).astype(np.int64)
+    li = np.repeat(np.arange(len(lk_)), cnt)
+    starts = np.repeat(lo - np.concatenate([[0], np.cumsum(cnt)[:-1]]), cnt)
+    ri = np.arange(len(li)) + starts
+    w0 = (lk_[li].astype(np.uint64) << np.uint64(32)) | lpay[li].astype(np.uint64)
+    w1 = (rps[ri].astype(np.uint64) << np.uint64(32)) | rks[ri].astype(np.uint64)
+    return w0, w1
+
+
 def test_smj_skewed_hot_key(provider):
     """A hot key with 3000 left x 2000 right rows among uniform keys: same multiset as the hash join
     (about 6.5e6 rows, 6e6 of them from the hot key)."""
@@ -141,13 +166,16 @@ def test_smj_skewed_hot_key(provider):
     sm = p.sort_merge_join_v2_inner_u32_1key(left, right, 0, 1)
     hj = p.hash_join_v2(left, right, [0], [1], JOIN_INNER)
     assert sm.num_rows() == expect_n == hj.num_rows()
-    # as multisets: compare the column arrays lexicographically sorted
-    def cols(rel):
+    # as multisets against a host join: rows are hashed from their packed words
+    # ((c0 << 32) | c1, (c2 << 32) | c3) and the sorted hash arrays compared
+    exp_rows = _host_join_words(lk_, lpay, rpay, rk_)
+
+    def row_hashes(rel):
         c = [p.download_column(rel, i).astype(np.uint64) for i in range(4)]
-        order = np.lexsort(c[::-1])
-        return [x[order] for x in c]
-    for a, b in zip(cols(sm), cols(hj)):
-        assert np.array_equal(a, b)
+        return _mix((c[0] << np.uint64(32)) | c[1], (c[2] << np.uint64(32)) | c[3])
+    want = np.sort(_mix(*exp_rows))
+    assert np.array_equal(np.sort(row_hashes(sm)), want)
+    assert np.array_equal(np.sort(row_hashes(hj)), want)
     # left rows come out in key order
     k0 = p.download_column(sm, 0)
     assert np.all(k0[1:] >= k0[:-1])

@@ -269,3 +269,27 @@ def test_parallel_paths_match_serial():
         assert all((a is None and b is None) or np.array_equal(a, b) for a, b in zip(s_[0], p_[0]))
     assert serial[4]["total"] == par[4]["total"] and serial[4]["iterations"] == par[4]["iterations"]
     assert np.array_equal(serial[4]["dist_count"], par[4]["dist_count"])
+
+
+# ---- FNV-1a-64, the digest of every fixture ------------------------------------
+@pytest.mark.parametrize("data,digest", [
+    # published FNV-1a 64-bit test vectors (the FNV reference test suite, isthe.com/chongo/tech/comp/fnv)
+    (b"", 0xCBF29CE484222325),
+    (b"a", 0xAF63DC4C8601EC8C),
+    (b"foobar", 0x85944171F73967E8),
+])
+def test_fnv1a64_published_vectors(data, digest):
+    assert oracle.fnv1a64_bytes(data) == digest
+
+
+def test_fnv1a64_keys_are_little_endian_bytes():
+    # the fixture digest is FNV-1a over the keys' little-endian bytes in row order
+    rng = np.random.default_rng(3)
+    for n in (0, 1, 2, 7, 1000):
+        keys = rng.integers(0, 1 << 64, size=n, dtype=np.uint64)
+        assert oracle.fnv1a64(keys) == oracle.fnv1a64_bytes(keys.astype("<u8").tobytes()), n
+    assert oracle.fnv1a64(np.zeros(0, np.uint64)) == 0xCBF29CE484222325
+    # one key's bytes in order: 0x0102030405060708 hashes the bytes 08 07 ... 01
+    k = np.array([0x0102030405060708], np.uint64)
+    assert oracle.fnv1a64(k) == oracle.fnv1a64_bytes(bytes([8, 7, 6, 5, 4, 3, 2, 1]))
+    assert oracle.fnv1a64(k) != oracle.fnv1a64_bytes(bytes([1, 2, 3, 4, 5, 6, 7, 8]))

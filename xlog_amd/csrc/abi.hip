@@ -114,41 +114,49 @@ __global__ void k_widen(const uint32_t *__restrict__ c0, uint64_t n, uint64_t *_
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) out[i] = c0[i];
 }
 
+// device view of a relation's words (or of any packed word arrays)
+struct RelView {
+    const uint64_t *w[MAX_WORDS];
+    int arity;
+};
+struct RelOut {
+    uint64_t *w[MAX_WORDS];
+};
 // value of column c (0..arity-1) of row i
-__device__ __forceinline__ uint32_t col_value(const uint64_t *w0, const uint64_t *w1, int arity, int c, uint64_t i) {
-    if (arity == 1) return (uint32_t)w0[i];
-    if (c == 0) return (uint32_t)(w0[i] >> 32);
-    if (c == 1) return (uint32_t)w0[i];
-    if (c == 2) return (uint32_t)(w1[i] >> 32);
-    return (uint32_t)w1[i];
+__device__ __forceinline__ uint32_t col_value(const RelView &v, int c, uint64_t i) {
+    if (v.arity == 1) return (uint32_t)v.w[0][i];
+    const uint64_t x = v.w[c >> 1][i];
+    return (c & 1) ? (uint32_t)x : (uint32_t)(x >> 32);
+}
+// packs out_arity column values into the words of one output row
+__device__ __forceinline__ void put_row(const RelOut &o, int out_arity, const uint32_t *v, uint64_t i) {
+    if (out_arity == 1) {
+        o.w[0][i] = v[0];
+        return;
+    }
+    for (int k = 0; 2 * k < out_arity; ++k)
+        o.w[k][i] = ((uint64_t)v[2 * k] << 32) | (2 * k + 1 < out_arity ? v[2 * k + 1] : 0u);
 }
 
 struct ProjSpec {
     int in_arity, out_arity;
-    int cols[4];
+    int cols[MAX_ARITY];
 };
-__global__ void k_project(const uint64_t *__restrict__ w0, const uint64_t *__restrict__ w1, uint64_t n, ProjSpec s,
-                          uint64_t *__restrict__ o0, uint64_t *__restrict__ o1) {
+__global__ void k_project(RelView in, uint64_t n, ProjSpec s, RelOut out) {
     uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
-        uint32_t v[4] = {0, 0, 0, 0};
-        for (int j = 0; j < s.out_arity; ++j) v[j] = col_value(w0, w1, s.in_arity, s.cols[j], i);
-        if (s.out_arity == 1) {
-            o0[i] = v[0];
-        } else {
-            o0[i] = ((uint64_t)v[0] << 32) | v[1];
-            if (s.out_arity == 3) o1[i] = (uint64_t)v[2] << 32;
-            if (s.out_arity == 4) o1[i] = ((uint64_t)v[2] << 32) | v[3];
-        }
+        uint32_t v[MAX_ARITY];
+        for (int j = 0; j < s.out_arity; ++j) v[j] = col_value(in, s.cols[j], i);
+        put_row(out, s.out_arity, v, i);
     }
 }
 
-__global__ void k_col_to_key(const uint64_t *__restrict__ w0, const uint64_t *__restrict__ w1, int arity, int c,
-                             const uint32_t *__restrict__ perm, uint64_t n, uint64_t *__restrict__ key) {
+__global__ void k_col_to_key(RelView in, int c, const uint32_t *__restrict__ perm, uint64_t n,
+                             uint64_t *__restrict__ key) {
     uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
         uint64_t r = perm ? perm[i] : i;
-        key[i] = (uint64_t)col_value(w0, w1, arity, c, r) << 32;
+        key[i] = (uint64_t)col_value(in, c, r) << 32;
     }
 }
 __global__ void k_iota(uint32_t *p, uint64_t n) {
@@ -165,22 +173,20 @@ __global__ void k_gather(const uint64_t *__restrict__ in, const uint32_t *__rest
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) out[i] = in[perm[i]];
 }
 // group-start flags over sorted rows for the given key columns
-__global__ void k_group_flags(const uint64_t *__restrict__ w0, const uint64_t *__restrict__ w1, int arity,
-                              ProjSpec keys, uint64_t n, uint8_t *__restrict__ flags) {
+__global__ void k_group_flags(RelView in, ProjSpec keys, uint64_t n, uint8_t *__restrict__ flags) {
     uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
         bool f = (i == 0);
         if (!f)
             for (int j = 0; j < keys.out_arity; ++j)
-                if (col_value(w0, w1, arity, keys.cols[j], i) != col_value(w0, w1, arity, keys.cols[j], i - 1)) f = true;
+                if (col_value(in, keys.cols[j], i) != col_value(in, keys.cols[j], i - 1)) f = true;
         flags[i] = f;
     }
 }
-__global__ void k_col_unsorted(const uint64_t *__restrict__ w0, const uint64_t *__restrict__ w1, int arity, int c,
-                               uint64_t n, uint32_t *flag) {
+__global__ void k_col_unsorted(RelView in, int c, uint64_t n, uint32_t *flag) {
     uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i + 1 < n; i += stride)
-        if (col_value(w0, w1, arity, c, i) > col_value(w0, w1, arity, c, i + 1)) *flag = 1u;
+        if (col_value(in, c, i) > col_value(in, c, i + 1)) *flag = 1u;
 }
 __global__ void k_max_u32_of_packed(const uint64_t *__restrict__ k, uint64_t n, unsigned int *mx) {
     uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
@@ -193,10 +199,6 @@ __global__ void k_max_u32_of_packed(const uint64_t *__restrict__ k, uint64_t n, 
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) m = max(m, (unsigned)__shfl_xor((int)m, o, 64));
     if ((threadIdx.x & 63) == 0) atomicMax(mx, m);
-}
-__global__ void k_u32_to_u64(const uint32_t *__restrict__ in, uint64_t n, uint64_t *__restrict__ out) {
-    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) out[i] = in[i];
 }
 __global__ void k_u64_to_u32(const uint64_t *__restrict__ in, uint64_t n, uint32_t *__restrict__ out) {
     uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
@@ -225,24 +227,34 @@ void scan_u64_small(Ctx *ctx, uint64_t *a, uint64_t n, uint64_t *total);
 // relations
 // ---------------------------------------------------------------------------
 xlog_hip_rel *rel_new(Ctx *ctx, uint32_t arity, uint64_t cap) {
-    XH_REQUIRE(arity >= 1 && arity <= 4, XLOG_HIP_INVALID_ARG, "relation arity must be 1..4");
+    XH_REQUIRE(arity >= 1 && arity <= MAX_ARITY, XLOG_HIP_INVALID_ARG, "relation arity must be 1..8");
     std::unique_ptr<xlog_hip_rel> r(new xlog_hip_rel());
     r->ctx = ctx;
     r->arity = arity;
     r->cap = cap;
     if (cap) {
-        r->w[0] = static_cast<uint64_t *>(ctx->alloc(cap * sizeof(uint64_t)));
-        if (arity > 2) r->w[1] = static_cast<uint64_t *>(ctx->alloc(cap * sizeof(uint64_t)));
+        try {
+            for (int k = 0; k < r->nwords(); ++k) r->w[k] = static_cast<uint64_t *>(ctx->alloc(cap * sizeof(uint64_t)));
+        } catch (...) {
+            for (int k = 0; k < MAX_WORDS; ++k) ctx->free(r->w[k]);
+            throw;
+        }
     }
     return r.release();
 }
 void rel_free(xlog_hip_rel *r) {
     if (!r) return;
-    if (r->ctx) {
-        r->ctx->free(r->w[0]);
-        r->ctx->free(r->w[1]);
-    }
+    if (r->ctx)
+        for (int k = 0; k < MAX_WORDS; ++k) r->ctx->free(r->w[k]);
     delete r;
+}
+static RelView view_of(const xlog_hip_rel *r) {
+    RelView v{{r->w[0], r->w[1], r->w[2], r->w[3]}, (int)r->arity};
+    return v;
+}
+static RelOut out_of(xlog_hip_rel *r) {
+    RelOut o{{r->w[0], r->w[1], r->w[2], r->w[3]}};
+    return o;
 }
 // adopt device buffers (ownership moves to the relation)
 static xlog_hip_rel *rel_adopt(Ctx *ctx, uint32_t arity, uint64_t rows, uint64_t *w0, uint64_t *w1, uint32_t flags) {
@@ -256,6 +268,23 @@ static xlog_hip_rel *rel_adopt(Ctx *ctx, uint32_t arity, uint64_t rows, uint64_t
     r->flags = flags;
     return r;
 }
+// packs device-resident u32 columns (arity 1..8) into the words of r
+static void pack_device_columns(Ctx *ctx, const uint32_t *const *cols, uint32_t arity, uint64_t rows, xlog_hip_rel *r) {
+    if (!rows) return;
+    if (arity == 1) {
+        LAUNCH_1D(k_widen, rows, cols[0], rows, r->w[0]);
+        return;
+    }
+    for (int k = 0; k < words_for(arity); ++k)
+        pack_columns(ctx, cols[2 * k], 2u * k + 1 < arity ? cols[2 * k + 1] : nullptr, rows, r->w[k]);
+}
+// adopt all words (ownership moves to the relation)
+static xlog_hip_rel *rel_adopt_words(Ctx *ctx, uint32_t arity, uint64_t rows, uint64_t *const *w, uint32_t flags) {
+    xlog_hip_rel *r = rel_adopt(ctx, arity, rows, w[0], w[1], flags);
+    r->w[2] = w[2];
+    r->w[3] = w[3];
+    return r;
+}
 static void copy_d2d(Ctx *ctx, uint64_t *dst, const uint64_t *src, uint64_t n) {
     if (n) XH_CHECK_HIP(hipMemcpyAsync(dst, src, n * sizeof(uint64_t), hipMemcpyDeviceToDevice, ctx->stream));
 }
@@ -263,8 +292,7 @@ static xlog_hip_rel *rel_clone(Ctx *ctx, const xlog_hip_rel *in) {
     xlog_hip_rel *r = rel_new(ctx, in->arity, in->rows);
     r->rows = in->rows;
     r->flags = in->flags;
-    copy_d2d(ctx, r->w[0], in->w[0], in->rows);
-    if (in->arity > 2) copy_d2d(ctx, r->w[1], in->w[1], in->rows);
+    for (int k = 0; k < in->nwords(); ++k) copy_d2d(ctx, r->w[k], in->w[k], in->rows);
     return r;
 }
 
@@ -385,10 +413,11 @@ static uint32_t *sort_perm(Ctx *ctx, const xlog_hip_rel *in, const std::vector<i
     uint64_t *k1 = static_cast<uint64_t *>(ctx->alloc(n * sizeof(uint64_t)));
     LAUNCH_1D(k_iota, n, perm, n);
     for (int i = (int)cols.size() - 1; i >= 0; --i) {
-        LAUNCH_1D(k_col_to_key, n, in->w[0], in->w[1], (int)in->arity, cols[i], perm, n, k0);
+        LAUNCH_1D(k_col_to_key, n, view_of(in), cols[i], perm, n, k0);
         uint64_t *ka = k0, *kb = k1;
         uint32_t *va = perm, *vb = perm2;
-        radix_sort_u64(ctx, &ka, &kb, &va, &vb, n);
+        // the column sits in the high word (low word zero): digits 4..8 only
+        radix_sort_u64(ctx, &ka, &kb, &va, &vb, n, 4, 8);
         k0 = ka; k1 = kb;
         perm = va; perm2 = vb;
     }
@@ -402,8 +431,7 @@ static xlog_hip_rel *gather_rel(Ctx *ctx, const xlog_hip_rel *in, const uint32_t
     xlog_hip_rel *r = rel_new(ctx, in->arity, in->rows);
     r->rows = in->rows;
     uint64_t n = in->rows;
-    LAUNCH_1D(k_gather, n, in->w[0], perm, n, r->w[0]);
-    if (in->arity > 2) LAUNCH_1D(k_gather, n, in->w[1], perm, n, r->w[1]);
+    for (int k = 0; k < in->nwords(); ++k) LAUNCH_1D(k_gather, n, in->w[k], perm, n, r->w[k]);
     return r;
 }
 
@@ -442,17 +470,15 @@ static xlog_hip_rel *op_sort(Ctx *ctx, const xlog_hip_rel *in, const std::vector
 }
 
 static xlog_hip_rel *compact_rel(Ctx *ctx, const xlog_hip_rel *in, const uint8_t *flags) {
-    Buf<uint64_t> cnt(ctx, 1);
-    uint64_t *o0 = static_cast<uint64_t *>(ctx->alloc((in->rows ? in->rows : 1) * sizeof(uint64_t)));
-    select_flags(ctx, in->w[0], flags, in->rows, o0, cnt.p);
-    uint64_t *o1 = nullptr;
-    if (in->arity > 2) {
-        o1 = static_cast<uint64_t *>(ctx->alloc((in->rows ? in->rows : 1) * sizeof(uint64_t)));
-        Buf<uint64_t> cnt2(ctx, 1);
-        select_flags(ctx, in->w[1], flags, in->rows, o1, cnt2.p);
+    Buf<uint64_t> cnt(ctx, in->nwords());
+    Buf<uint64_t> o[MAX_WORDS];
+    for (int k = 0; k < in->nwords(); ++k) {
+        o[k] = Buf<uint64_t>(ctx, in->rows ? in->rows : 1);
+        select_flags(ctx, in->w[k], flags, in->rows, o[k].p, cnt.p + k);
     }
     uint64_t n = read_count(ctx, cnt.p);
-    return rel_adopt(ctx, in->arity, n, o0, o1, 0);
+    uint64_t *w[MAX_WORDS] = {o[0].release(), o[1].release(), o[2].release(), o[3].release()};
+    return rel_adopt_words(ctx, in->arity, n, w, 0);
 }
 
 static xlog_hip_rel *op_dedup_full(Ctx *ctx, const xlog_hip_rel *in) {
@@ -468,8 +494,8 @@ static xlog_hip_rel *op_dedup_full(Ctx *ctx, const xlog_hip_rel *in) {
     for (uint32_t c = 0; c < in->arity; ++c) all.push_back((int)c);
     xlog_hip_rel *s = op_sort(ctx, in, all);
     Buf<uint8_t> flags(ctx, s->rows ? s->rows : 1);
-    ProjSpec ks{(int)s->arity, (int)s->arity, {0, 1, 2, 3}};
-    LAUNCH_1D(k_group_flags, s->rows, s->w[0], s->w[1], (int)s->arity, ks, s->rows, flags.p);
+    ProjSpec ks{(int)s->arity, (int)s->arity, {0, 1, 2, 3, 4, 5, 6, 7}};
+    LAUNCH_1D(k_group_flags, s->rows, view_of(s), ks, s->rows, flags.p);
     xlog_hip_rel *r = compact_rel(ctx, s, flags.p);
     rel_free(s);
     r->flags = REL_CANONICAL;
@@ -481,9 +507,12 @@ static xlog_hip_rel *op_dedup(Ctx *ctx, const xlog_hip_rel *in, const std::vecto
     XH_REQUIRE(!cols.empty(), XLOG_HIP_INVALID_ARG, "dedup needs at least one key column");
     xlog_hip_rel *s = op_sort(ctx, in, cols);
     Buf<uint8_t> flags(ctx, s->rows ? s->rows : 1);
-    ProjSpec ks{(int)s->arity, (int)std::min<size_t>(cols.size(), 4), {0, 0, 0, 0}};
-    for (int j = 0; j < ks.out_arity; ++j) ks.cols[j] = cols[j];
-    LAUNCH_1D(k_group_flags, s->rows, s->w[0], s->w[1], (int)s->arity, ks, s->rows, flags.p);
+    std::vector<int> keys;  // distinct key columns (at most the arity)
+    for (int c : cols)
+        if (std::find(keys.begin(), keys.end(), c) == keys.end()) keys.push_back(c);
+    ProjSpec ks{(int)s->arity, (int)keys.size(), {0, 0, 0, 0, 0, 0, 0, 0}};
+    for (int j = 0; j < ks.out_arity; ++j) ks.cols[j] = keys[j];
+    LAUNCH_1D(k_group_flags, s->rows, view_of(s), ks, s->rows, flags.p);
     xlog_hip_rel *r = compact_rel(ctx, s, flags.p);
     rel_free(s);
     return r;
@@ -510,8 +539,7 @@ static xlog_hip_rel *op_union_many(Ctx *ctx, const xlog_hip_rel *const *ins, uin
     cat->rows = total;
     uint64_t off = 0;
     for (uint32_t i = 0; i < n; ++i) {
-        copy_d2d(ctx, cat->w[0] + off, ins[i]->w[0], ins[i]->rows);
-        if (arity > 2) copy_d2d(ctx, cat->w[1] + off, ins[i]->w[1], ins[i]->rows);
+        for (int k = 0; k < cat->nwords(); ++k) copy_d2d(ctx, cat->w[k] + off, ins[i]->w[k], ins[i]->rows);
         off += ins[i]->rows;
     }
     xlog_hip_rel *r = op_dedup_full(ctx, cat);
@@ -715,7 +743,7 @@ static bool column_sorted(Ctx *ctx, const xlog_hip_rel *rel, uint32_t col) {
     if (rel->rows < 2) return true;
     Buf<uint32_t> flag(ctx, 1);
     fill_u32(ctx, flag.p, 0u, 1);
-    LAUNCH_1D(k_col_unsorted, rel->rows, rel->w[0], rel->w[1], (int)rel->arity, (int)col, rel->rows, flag.p);
+    LAUNCH_1D(k_col_unsorted, rel->rows, view_of(rel), (int)col, rel->rows, flag.p);
     uint32_t h = 0;
     XH_CHECK_HIP(hipMemcpyAsync(&h, flag.p, 4, hipMemcpyDeviceToHost, ctx->stream));
     ctx->sync();
@@ -831,9 +859,9 @@ static xlog_hip_rel *op_dedup_sorted(Ctx *ctx, const xlog_hip_rel *in, const std
     for (int c : cols)
         if (std::find(keys.begin(), keys.end(), c) == keys.end()) keys.push_back(c);
     Buf<uint8_t> flags(ctx, in->rows);
-    ProjSpec ks{(int)in->arity, (int)keys.size(), {0, 0, 0, 0}};
+    ProjSpec ks{(int)in->arity, (int)keys.size(), {0, 0, 0, 0, 0, 0, 0, 0}};
     for (int j = 0; j < ks.out_arity; ++j) ks.cols[j] = keys[j];
-    LAUNCH_1D(k_group_flags, in->rows, in->w[0], in->w[1], (int)in->arity, ks, in->rows, flags.p);
+    LAUNCH_1D(k_group_flags, in->rows, view_of(in), ks, in->rows, flags.p);
     xlog_hip_rel *r = compact_rel(ctx, in, flags.p);
     if (in->flags & REL_CANONICAL) r->flags = REL_CANONICAL;  // a subset of a sorted set is one
     return r;
@@ -1002,12 +1030,12 @@ static xlog_hip_rel *op_join_project_dedup(Ctx *ctx, const xlog_hip_rel *l, cons
 }
 
 static xlog_hip_rel *op_project(Ctx *ctx, const xlog_hip_rel *in, const std::vector<int> &cols) {
-    XH_REQUIRE(!cols.empty() && cols.size() <= 4, XLOG_HIP_INVALID_ARG, "projection needs 1..4 columns");
+    XH_REQUIRE(!cols.empty() && cols.size() <= MAX_ARITY, XLOG_HIP_INVALID_ARG, "projection needs 1..8 columns");
     xlog_hip_rel *r = rel_new(ctx, (uint32_t)cols.size(), in->rows);
     r->rows = in->rows;
-    ProjSpec s{(int)in->arity, (int)cols.size(), {0, 0, 0, 0}};
+    ProjSpec s{(int)in->arity, (int)cols.size(), {0, 0, 0, 0, 0, 0, 0, 0}};
     for (size_t i = 0; i < cols.size(); ++i) s.cols[i] = cols[i];
-    LAUNCH_1D(k_project, in->rows, in->w[0], in->w[1], in->rows, s, r->w[0], r->w[1]);
+    LAUNCH_1D(k_project, in->rows, view_of(in), in->rows, s, out_of(r));
     return r;
 }
 
@@ -1114,8 +1142,10 @@ struct Driver {
             if (h0 == 0 && h1 == 1) copy_d2d(ctx, o, bk, bn);
             else if (h0 == 1 && h1 == 0) swap_words(ctx, bk, bn, o);
             else {
-                ProjSpec s{2, 2, {h0, h1, 0, 0}};
-                LAUNCH_1D(k_project, bn, bk, nullptr, bn, s, o, nullptr);
+                ProjSpec s{2, 2, {h0, h1, 0, 0, 0, 0, 0, 0}};
+                RelView bv{{bk, nullptr, nullptr, nullptr}, 2};
+                RelOut bo{{o, nullptr, nullptr, nullptr}};
+                LAUNCH_1D(k_project, bn, bv, bn, s, bo);
             }
             out.push_back({o, bn});
             return;
@@ -1597,16 +1627,13 @@ xlog_hip_rel *rel_from_ipc(Ctx *ctx, const IpcColumns &ic) {
     if (!ic.rows) return r;
     try {
         Buf<uint32_t> stage(ctx, (uint64_t)ic.arity * ic.rows);
-        const uint32_t *dc[4] = {nullptr, nullptr, nullptr, nullptr};
+        const uint32_t *dc[MAX_ARITY] = {nullptr};
         for (uint32_t c = 0; c < ic.arity; ++c) {
             uint32_t *d = stage.p + (uint64_t)c * ic.rows;
             XH_CHECK_HIP(hipMemcpyAsync(d, ic.cols[c], ic.rows * 4, hipMemcpyHostToDevice, ctx->stream));
             dc[c] = d;
         }
-        if (ic.arity == 1) LAUNCH_1D(k_widen, ic.rows, dc[0], ic.rows, r->w[0]);
-        else pack_columns(ctx, dc[0], dc[1], ic.rows, r->w[0]);
-        if (ic.arity == 3) pack_columns(ctx, dc[2], nullptr, ic.rows, r->w[1]);
-        if (ic.arity == 4) pack_columns(ctx, dc[2], dc[3], ic.rows, r->w[1]);
+        pack_device_columns(ctx, dc, ic.arity, ic.rows, r);
         ctx->sync();  // the host bytes may go away after the call
     } catch (...) {
         rel_free(r);
@@ -1623,7 +1650,7 @@ std::vector<uint32_t> columns_to_host(Ctx *ctx, const xlog_hip_rel *rel) {
     for (uint32_t c = 0; c < rel->arity; ++c) {
         uint32_t *d = tmp.p + (uint64_t)c * rel->rows;
         if (rel->arity == 1) LAUNCH_1D(k_u64_to_u32, rel->rows, rel->w[0], rel->rows, d);
-        else unpack_column(ctx, c < 2 ? rel->w[0] : rel->w[1], (c % 2) == 0, rel->rows, d);
+        else unpack_column(ctx, rel->w[c / 2], (c % 2) == 0, rel->rows, d);
     }
     XH_CHECK_HIP(hipMemcpyAsync(h.data(), tmp.p, h.size() * 4, hipMemcpyDeviceToHost, ctx->stream));
     ctx->sync();
@@ -1730,23 +1757,26 @@ xlog_hip_status xlog_hip_rel_from_host_columns(xlog_hip_ctx *ctx, const uint32_t
     return guarded([&] {
         Ctx *c = C(ctx);
         XH_REQUIRE(out, XLOG_HIP_INVALID_ARG, "out is NULL");
-        XH_REQUIRE(arity >= 1 && arity <= 4, XLOG_HIP_INVALID_ARG, "relation arity must be 1..4");
+        XH_REQUIRE(arity >= 1 && arity <= MAX_ARITY, XLOG_HIP_INVALID_ARG, "relation arity must be 1..8");
         XH_REQUIRE(rows == 0 || cols, XLOG_HIP_INVALID_ARG, "columns are NULL");
         for (uint32_t i = 0; i < arity && rows; ++i) XH_REQUIRE(cols[i], XLOG_HIP_INVALID_ARG, "column pointer is NULL");
-        std::vector<uint64_t> h0(rows), h1(arity > 2 ? rows : 0);
+        const int nw = words_for(arity);
+        std::vector<std::vector<uint64_t>> h(nw, std::vector<uint64_t>(rows));
         for (uint64_t i = 0; i < rows; ++i) {
-            h0[i] = arity == 1 ? (uint64_t)cols[0][i] : (((uint64_t)cols[0][i] << 32) | cols[1][i]);
-            if (arity == 3) h1[i] = (uint64_t)cols[2][i] << 32;
-            if (arity == 4) h1[i] = ((uint64_t)cols[2][i] << 32) | cols[3][i];
+            if (arity == 1) {
+                h[0][i] = cols[0][i];
+                continue;
+            }
+            for (int k = 0; k < nw; ++k)
+                h[k][i] = ((uint64_t)cols[2 * k][i] << 32) | (2u * k + 1 < arity ? cols[2 * k + 1][i] : 0u);
         }
-        xlog_hip_rel *r = rel_new(c, arity, rows);
+        std::unique_ptr<xlog_hip_rel, void (*)(xlog_hip_rel *)> r(rel_new(c, arity, rows), rel_free);
         r->rows = rows;
-        if (rows) {
-            XH_CHECK_HIP(hipMemcpyAsync(r->w[0], h0.data(), rows * 8, hipMemcpyHostToDevice, c->stream));
-            if (arity > 2) XH_CHECK_HIP(hipMemcpyAsync(r->w[1], h1.data(), rows * 8, hipMemcpyHostToDevice, c->stream));
-        }
+        if (rows)
+            for (int k = 0; k < nw; ++k)
+                XH_CHECK_HIP(hipMemcpyAsync(r->w[k], h[k].data(), rows * 8, hipMemcpyHostToDevice, c->stream));
         c->sync();
-        *out = r;
+        *out = r.release();
     });
 }
 
@@ -1756,16 +1786,11 @@ xlog_hip_status xlog_hip_rel_from_device_columns(xlog_hip_ctx *ctx, const uint32
         Ctx *ctxp = C(ctx);
         Ctx *ctx = ctxp;
         XH_REQUIRE(out, XLOG_HIP_INVALID_ARG, "out is NULL");
-        XH_REQUIRE(arity >= 1 && arity <= 4, XLOG_HIP_INVALID_ARG, "relation arity must be 1..4");
+        XH_REQUIRE(arity >= 1 && arity <= MAX_ARITY, XLOG_HIP_INVALID_ARG, "relation arity must be 1..8");
         XH_REQUIRE(rows == 0 || dev_cols, XLOG_HIP_INVALID_ARG, "columns are NULL");
         xlog_hip_rel *r = rel_new(ctx, arity, rows);
         r->rows = rows;
-        if (rows) {
-            if (arity == 1) LAUNCH_1D(k_widen, rows, dev_cols[0], rows, r->w[0]);
-            else pack_columns(ctx, dev_cols[0], dev_cols[1], rows, r->w[0]);
-            if (arity == 3) pack_columns(ctx, dev_cols[2], nullptr, rows, r->w[1]);
-            if (arity == 4) pack_columns(ctx, dev_cols[2], dev_cols[3], rows, r->w[1]);
-        }
+        if (rows) pack_device_columns(ctx, dev_cols, arity, rows, r);
         *out = r;
     });
 }
@@ -1798,8 +1823,7 @@ xlog_hip_status xlog_hip_rel_download_column(xlog_hip_ctx *ctx, const xlog_hip_r
         Buf<uint32_t> tmp(ctx, rel->rows);
         if (rel->arity == 1) LAUNCH_1D(k_u64_to_u32, rel->rows, rel->w[0], rel->rows, tmp.p);
         else {
-            const uint64_t *w = col < 2 ? rel->w[0] : rel->w[1];
-            unpack_column(ctx, w, (col % 2) == 0, rel->rows, tmp.p);
+            unpack_column(ctx, rel->w[col / 2], (col % 2) == 0, rel->rows, tmp.p);
         }
         XH_CHECK_HIP(hipMemcpyAsync(host, tmp.p, rel->rows * 4, hipMemcpyDeviceToHost, ctx->stream));
         ctx->sync();
@@ -2140,11 +2164,9 @@ xlog_hip_status xlog_hip_exclusive_scan_u32(xlog_hip_ctx *ctx, uint32_t *dev, ui
         Ctx *ctx = ctxp;
         XH_REQUIRE(n == 0 || dev, XLOG_HIP_INVALID_ARG, "array is NULL");
         if (n == 0) { if (total) *total = 0; return; }
-        Buf<uint64_t> tmp(ctx, n + 1);
-        LAUNCH_1D(k_u32_to_u64, n, dev, n, tmp.p);
-        scan_u64_small(ctx, tmp.p, n, tmp.p + n);
-        LAUNCH_1D(k_u64_to_u32, n, tmp.p, n, dev);
-        ctx->read_scalars(tmp.p + n, 1);
+        Buf<unsigned long long> tot(ctx, 1);
+        scan_u32_inplace(ctx, dev, n, tot.p);
+        ctx->read_scalars(tot.p, 1);
         if (total) *total = ctx->host_scalars[0];
     });
 }

@@ -215,21 +215,26 @@ Buf<T>::~Buf() {
 // ---------------------------------------------------------------------------
 // relation handle (the CudaBuffer counterpart).  Rows are stored as packed
 // u64 words, row-major within a word, word-major across words:
-//   arity 1: w[0][i] = c0
-//   arity 2: w[0][i] = (c0 << 32) | c1
-//   arity 3: w[0][i] = (c0 << 32) | c1, w[1][i] = c2 << 32
-//   arity 4: w[0][i] = (c0 << 32) | c1, w[1][i] = (c2 << 32) | c3
-// Unsigned u64 order over (w[0], w[1]) is the lexicographic unsigned column
-// order, and equal words are bytewise-equal rows.
+//   arity 1:    w[0][i] = c0
+//   arity 2k:   w[j][i] = (c_{2j} << 32) | c_{2j+1}          (j < k)
+//   arity 2k+1: as 2k + 2 with the last column zero
+// e.g. arity 3: w[0][i] = (c0 << 32) | c1, w[1][i] = c2 << 32.  Arity is 1..8
+// (four words).  Unsigned u64 order over (w[0], w[1], ...) is the
+// lexicographic unsigned column order, and equal words are bytewise-equal rows.
 // ---------------------------------------------------------------------------
+namespace xh {
+constexpr uint32_t MAX_ARITY = 8;
+constexpr int MAX_WORDS = 4;
+inline int words_for(uint32_t arity) { return arity <= 2 ? 1 : (int)((arity + 1) / 2); }
+}  // namespace xh
 struct xlog_hip_rel {
     xh::Ctx *ctx = nullptr;
     uint32_t arity = 0;
     uint64_t rows = 0;
     uint64_t cap = 0;
-    uint64_t *w[2] = {nullptr, nullptr};
+    uint64_t *w[xh::MAX_WORDS] = {nullptr, nullptr, nullptr, nullptr};
     uint32_t flags = 0;  // XLOG_HIP_REL_CANONICAL when sorted by all columns and unique
-    int nwords() const { return arity <= 2 ? 1 : 2; }
+    int nwords() const { return xh::words_for(arity); }
 };
 
 namespace xh {
@@ -247,8 +252,10 @@ void rel_free(xlog_hip_rel *r);
 // LSD radix sort of u64 keys with an optional u32 payload, stable, over the
 // 8-bit digits [digit_lo, digit_hi) (0..8 = the whole key; 4..8 = the high
 // word only).  On return *keys (and *vals) point at whichever of the two
-// buffers holds the result; the other is scratch.  Digits that are constant
-// over the input are skipped.  Returns the number of digit passes executed.
+// buffers holds the result; the other is scratch.  The pass of the lowest
+// digit always runs (it is queued before the histograms are read back); every
+// higher digit that is constant over the input is skipped.  Returns the number
+// of digit passes executed.
 // With `src` (keys only) the first pass reads src and both buffers are
 // scratch, so an input that must not be modified is never copied first.
 int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **vals, uint32_t **vals_alt,
@@ -265,6 +272,10 @@ void select_unique_diff(Ctx *ctx, const uint64_t *k, uint64_t n, const uint64_t 
                         uint64_t *out, uint64_t *d_count);
 void select_flags(Ctx *ctx, const uint64_t *k, const uint8_t *flags, uint64_t n, uint64_t *out,
                   uint64_t *d_count);
+
+// In-place exclusive scan of u32 values (prefixes wrap modulo 2^32); the
+// exact u64 sum goes to *d_total (device).  One pass, decoupled look-back.
+void scan_u32_inplace(Ctx *ctx, uint32_t *a, uint64_t n, unsigned long long *d_total);
 
 // Merge of two sorted arrays (stable, a before b on ties) into out[na+nb].
 void merge_sorted(Ctx *ctx, const uint64_t *a, uint64_t na, const uint64_t *b, uint64_t nb, uint64_t *out);

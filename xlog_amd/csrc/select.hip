@@ -364,6 +364,99 @@ struct SelRuns {
     }
 };
 
+// ---- exclusive scan of u32, in place ----------------------------------------
+// One pass with decoupled look-back (replaces the reference's three-phase
+// recursive multiblock scan, scan.cu:133-270, provider/mod.rs:2192-2290).  A
+// thread owns SCAN_ITEMS consecutive values (16-byte loads when the array is
+// 16-byte aligned), scans them serially, the block scans the thread sums, and
+// the tile's prefix comes from the look-back over earlier tiles.  Prefixes are
+// u32 and wrap modulo 2^32 like the reference's u32 arithmetic; the exact u64
+// total is accumulated separately (one atomic per tile).
+constexpr int SCAN_BLOCK = 1024;
+constexpr int SCAN_ITEMS = 16;
+constexpr uint64_t SCAN_TILE = (uint64_t)SCAN_BLOCK * SCAN_ITEMS;
+
+template <bool VEC>
+__global__ __launch_bounds__(SCAN_BLOCK) void k_scan_u32(uint32_t *a, uint64_t n, uint64_t *status,
+                                                         uint64_t epoch_tag, unsigned long long *ticket,
+                                                         unsigned long long ticket_base,
+                                                         unsigned long long *d_total) {
+    __shared__ uint64_t s_tile;
+    __shared__ uint32_t s_prefix;
+    __shared__ uint32_t s_wsum[SCAN_BLOCK / WAVE];
+    __shared__ unsigned long long s_wsum64[SCAN_BLOCK / WAVE];
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
+    if (tid == 0) s_tile = atomicAdd(ticket, 1ull) - ticket_base;
+    __syncthreads();
+    const uint64_t tile = s_tile;
+    const uint64_t base = tile * SCAN_TILE + (uint64_t)tid * SCAN_ITEMS;
+    uint32_t v[SCAN_ITEMS];
+    if (VEC && base + SCAN_ITEMS <= n) {
+        const uint4 *q = reinterpret_cast<const uint4 *>(a + base);
+#pragma unroll
+        for (int k = 0; k < SCAN_ITEMS / 4; ++k) {
+            const uint4 x = q[k];
+            v[4 * k] = x.x; v[4 * k + 1] = x.y; v[4 * k + 2] = x.z; v[4 * k + 3] = x.w;
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < SCAN_ITEMS; ++k) v[k] = base + k < n ? a[base + k] : 0u;
+    }
+    uint32_t sum = 0;
+    unsigned long long sum64 = 0;
+#pragma unroll
+    for (int k = 0; k < SCAN_ITEMS; ++k) {
+        const uint32_t x = v[k];
+        v[k] = sum;  // thread-local exclusive prefix
+        sum += x;
+        sum64 += x;
+    }
+    // wave scan of the thread sums
+    uint32_t incl = sum;
+#pragma unroll
+    for (int o = 1; o < WAVE; o <<= 1) {
+        const uint32_t t = __shfl_up(incl, o, WAVE);
+        if (lane >= o) incl += t;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) sum64 += __shfl_xor(sum64, o, WAVE);
+    if (lane == WAVE - 1) s_wsum[wave] = incl;
+    if (lane == 0) s_wsum64[wave] = sum64;
+    __syncthreads();
+    uint32_t wpre = 0, tile_sum = 0;
+    unsigned long long tile_sum64 = 0;
+#pragma unroll
+    for (int w = 0; w < SCAN_BLOCK / WAVE; ++w) {
+        if (w < wave) wpre += s_wsum[w];
+        tile_sum += s_wsum[w];
+        tile_sum64 += s_wsum64[w];
+    }
+    if (wave == 0) {
+        if (tid == 0) {
+            lb_store(status + tile, epoch_tag | (tile == 0 ? LB_INC : 0ull) | tile_sum);
+            atomicAdd(d_total, tile_sum64);
+        }
+        // the look-back sums prefixes in u64; only their value modulo 2^32 is used
+        const uint64_t prefix = tile ? lookback_wave(status, tile, epoch_tag, lane) : 0ull;
+        if (tid == 0) {
+            if (tile) lb_store(status + tile, epoch_tag | LB_INC | (uint32_t)(prefix + tile_sum));
+            s_prefix = (uint32_t)prefix;
+        }
+    }
+    __syncthreads();
+    const uint32_t off = s_prefix + wpre + (incl - sum);
+    if (VEC && base + SCAN_ITEMS <= n) {
+        uint4 *q = reinterpret_cast<uint4 *>(a + base);
+#pragma unroll
+        for (int k = 0; k < SCAN_ITEMS / 4; ++k)
+            q[k] = make_uint4(off + v[4 * k], off + v[4 * k + 1], off + v[4 * k + 2], off + v[4 * k + 3]);
+    } else {
+#pragma unroll
+        for (int k = 0; k < SCAN_ITEMS; ++k)
+            if (base + k < n) a[base + k] = off + v[k];
+    }
+}
+
 // ---- merge path -----------------------------------------------------------
 constexpr int MRG_BLOCK = 256;
 constexpr int MRG_ITEMS = 8;
@@ -527,6 +620,24 @@ void select_group_heads(Ctx *ctx, const uint64_t *mkeys, uint64_t nm, const uint
 }
 void select_runs(Ctx *ctx, const uint64_t *k, uint64_t n, uint32_t *run_key, uint64_t *run_start, uint64_t *d_count) {
     run_select(ctx, k, n, SelRuns{k, run_key, run_start}, d_count);
+}
+
+void scan_u32_inplace(Ctx *ctx, uint32_t *a, uint64_t n, unsigned long long *d_total) {
+    fill_u64(ctx, reinterpret_cast<uint64_t *>(d_total), 0ull, 1);
+    if (n == 0) return;
+    const uint64_t tiles = (n + SCAN_TILE - 1) / SCAN_TILE;
+    XH_REQUIRE(tiles < (1ull << 31), XLOG_HIP_CAPACITY_OVERFLOW, "scan: input too large");
+    uint64_t tag;
+    uint64_t *status = select_status(ctx, tiles, &tag);
+    unsigned long long tb = ctx->take_tickets(1, tiles);
+    Prof prof(ctx, XLOG_HIP_KERNEL_SELECT, 8.0 * (double)n);  // reads and writes 4 B per value
+    if ((reinterpret_cast<uintptr_t>(a) & 15u) == 0)
+        hipLaunchKernelGGL(k_scan_u32<true>, dim3((unsigned)tiles), dim3(SCAN_BLOCK), 0, ctx->stream, a, n, status,
+                           tag, ctx->tickets + 1, tb, d_total);
+    else
+        hipLaunchKernelGGL(k_scan_u32<false>, dim3((unsigned)tiles), dim3(SCAN_BLOCK), 0, ctx->stream, a, n, status,
+                           tag, ctx->tickets + 1, tb, d_total);
+    XH_CHECK_HIP(hipGetLastError());
 }
 
 void merge_sorted(Ctx *ctx, const uint64_t *a, uint64_t na, const uint64_t *b, uint64_t nb, uint64_t *out) {

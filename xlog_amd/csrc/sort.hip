@@ -4,9 +4,10 @@
 // (crates/xlog-cuda/src/provider/relational.rs:1881-2357, kernels/sort.cu:28-264)
 // with a onesweep design:
 //   1. k_hist8: one read of the keys builds the 256-bin histograms of the
-//      digits the sort uses (all eight for a full-key sort); a digit whose
-//      histogram has a single non-empty bin is constant over the input and
-//      its pass is skipped.
+//      digits the sort uses (all eight for a full-key sort); a digit above
+//      the lowest whose histogram has a single non-empty bin is constant over
+//      the input and its pass is skipped (the lowest digit's pass is queued
+//      before the histograms reach the host, so it always runs).
 //   2. k_onesweep, once per remaining digit: a tile of TILE keys is ranked
 //      per wave with 64-lane ballot matching (stable), the tile's 256 digit
 //      counts are published and the exclusive prefix over earlier tiles is
