@@ -8,7 +8,7 @@
  * declaration cites the reference method it replaces.
  *
  * Conventions
- *   - Relations are device-resident, u32 columns, arity 1..4.  They are opaque
+ *   - Relations are device-resident, u32 columns, arity 1..8.  They are opaque
  *     handles owned by the library; operators borrow inputs (const) and return
  *     new owned relations (reference: every provider op returns a fresh
  *     CudaBuffer, e.g. relational.rs:2219, filter.rs:1927-1933).  Free with
@@ -164,11 +164,23 @@ xlog_hip_status xlog_hip_union_many(xlog_hip_ctx *ctx, const xlog_hip_rel *const
 xlog_hip_status xlog_hip_diff(xlog_hip_ctx *ctx, const xlog_hip_rel *a, const xlog_hip_rel *b,
                               xlog_hip_rel **out);
 /* Equi-join on one key column per side.  INNER output = left columns ++
- * right columns (arity_l + arity_r <= 4), one row per matching pair, row
+ * right columns (arity_l + arity_r <= 8), one row per matching pair, row
  * order unspecified (reference: hash_join_v2, relational.rs:2926-2992,4417-4625).
  * SEMI / ANTI output the left rows with / without a match. */
 xlog_hip_status xlog_hip_hash_join(xlog_hip_ctx *ctx, const xlog_hip_rel *left, const xlog_hip_rel *right,
                                    uint32_t left_key, uint32_t right_key, int join_type, xlog_hip_rel **out);
+/* Equi-join on n_keys key columns per side: left row i matches right row j
+ * when left[i][left_keys[t]] == right[j][right_keys[t]] for every t
+ * (reference: hash_join_v2(left, right, left_keys, right_keys, join_type),
+ * relational.rs:2926-2992, keys packed by pack_and_hash_keys, pack.cu:144-214).
+ * INNER output = left columns ++ right columns (arity_l + arity_r <= 8), rows
+ * in left-row order and, per left row, right-row order; SEMI / ANTI output the
+ * left rows with / without a match, in input order.  Each side holds fewer
+ * than 2^32 - 1 rows (CAPACITY_OVERFLOW otherwise, as the reference's u32 row
+ * indices). */
+xlog_hip_status xlog_hip_hash_join_keys(xlog_hip_ctx *ctx, const xlog_hip_rel *left, const xlog_hip_rel *right,
+                                        const uint32_t *left_keys, const uint32_t *right_keys, uint32_t n_keys,
+                                        int join_type, xlog_hip_rel **out);
 /* Join index over column right_key of `right`, reused across probes; fails
  * on an empty relation like the reference (build_join_index_v2,
  * relational.rs:3728-3880).  Free it with xlog_hip_join_index_free before its
@@ -266,6 +278,12 @@ typedef struct {
     uint64_t delta_cap;       /* entries available in delta_sizes */
     uint64_t route;           /* XLOG_HIP_ROUTE_* (in: request, out: taken) */
     double wall_ms;           /* device wall time of the fixpoint */
+    uint64_t max_join_rows;   /* in: 0 = no limit; otherwise a binary join of a rule body whose output
+                                 (a bag) would exceed it fails with CAPACITY_OVERFLOW before it is
+                                 materialised.  4294967295 reproduces the reference's u32 join-row
+                                 limit (relational.rs:4550-4555). */
+    uint64_t host_waits;      /* out: times the host waited for the device during the fixpoint
+                                 (each count or size read-back is one wait) */
 } xlog_hip_fixpoint_stats;
 
 /* AUTO takes the bitmap route when every rule body is a path, there are at

@@ -636,7 +636,7 @@ static uint64_t join_chunk_rows() {
     return 1ull << 28;
 }
 static uint64_t join_step(Ctx *ctx, const uint64_t *probe, uint64_t n, int pcol, const JoinIndex &J, const int oc[4],
-                          uint64_t **out) {
+                          uint64_t **out, uint64_t max_rows = 0) {
     const uint64_t kChunkRows = join_chunk_rows();
     ProbeJob job;
     job.probe = probe;
@@ -647,6 +647,11 @@ static uint64_t join_step(Ctx *ctx, const uint64_t *probe, uint64_t n, int pcol,
     *out = nullptr;
     uint64_t total = probe_prepare(ctx, job);
     if (total == 0) return 0;
+    // the bag size is known before anything is materialised (the reference
+    // refuses joins above its u32 row limit at the same point, relational.rs:4550-4555)
+    XH_REQUIRE(max_rows == 0 || total <= max_rows, XLOG_HIP_CAPACITY_OVERFLOW,
+               "Join produced " + std::to_string(total) + " rows which exceeds the row limit " +
+                   std::to_string(max_rows));
     if (total <= kChunkRows) {
         uint64_t *o = static_cast<uint64_t *>(ctx->alloc(total * sizeof(uint64_t)));
         probe_emit_range(ctx, job, 0, job.tiles, total, 2, oc, o, nullptr);
@@ -729,14 +734,178 @@ static xlog_hip_rel *op_join_indexed(Ctx *ctx, const xlog_hip_rel *l, uint32_t l
     return rel_adopt(ctx, (uint32_t)sel.size(), n, o0, o1, 0);
 }
 
+static xlog_hip_rel *op_join_keys(Ctx *ctx, const xlog_hip_rel *l, const xlog_hip_rel *r, const std::vector<int> &lk,
+                                  const std::vector<int> &rk, int type);
+static xlog_hip_rel *op_project(Ctx *ctx, const xlog_hip_rel *in, const std::vector<int> &cols);
+
 static xlog_hip_rel *op_join(Ctx *ctx, const xlog_hip_rel *l, const xlog_hip_rel *r, uint32_t lk, uint32_t rk,
                              int type, const std::vector<int> *out_cols) {
     XH_REQUIRE(l && r, XLOG_HIP_INVALID_ARG, "join input is NULL");
     XH_REQUIRE(lk < l->arity && rk < r->arity, XLOG_HIP_INVALID_ARG, "join key column out of range");
-    XH_REQUIRE(l->arity <= 2 && r->arity <= 2, XLOG_HIP_UNSUPPORTED, "join: input arity above 2 is not supported");
+    if (l->arity > 2 || r->arity > 2) {
+        // wider rows: the keyed join with one key column, then the projection
+        xlog_hip_rel *j = op_join_keys(ctx, l, r, {(int)lk}, {(int)rk}, type);
+        if (!out_cols || type != XLOG_HIP_JOIN_INNER) return j;
+        std::unique_ptr<xlog_hip_rel, void (*)(xlog_hip_rel *)> jg(j, rel_free);
+        return op_project(ctx, j, *out_cols);
+    }
     JoinIndex J;
     build_join_index(ctx, r->w[0], r->rows, r->arity, (int)rk, (r->flags & REL_CANONICAL) != 0, J);
     return op_join_indexed(ctx, l, lk, J, r->arity, rk, type, out_cols);
+}
+
+// ---------------------------------------------------------------------------
+// Equi-join on lists of key columns, inputs of any arity (reference
+// hash_join_v2 with key lists, relational.rs:2926-2992, whose keys are packed
+// row-major and hashed by pack_and_hash_keys, pack.cu:144-214).
+//
+// Instead of hashing variable-length packed key bytes, every key column is
+// folded into a dense u32 id: the first step keys each row by its first one or
+// two key columns as one u64, later steps by (previous id << 32) | next key
+// column; the id is the key's rank among the build side's sorted unique keys
+// (a left key absent from the build side gets KEY_NONE, which no build id
+// equals).  The equal-id join then runs on (id << 32) | row words through the
+// single-key run index and the wave-cooperative probe, which emit
+// (left row << 32) | right row in left-row-major, right-row order; a gather
+// writes the left ++ right columns.
+// ---------------------------------------------------------------------------
+namespace {
+constexpr uint32_t KEY_NONE = 0xFFFFFFFFu;
+
+// u64 key of one folding step: (hi << 32) | column c1, hi = prev[i] when given,
+// else column c0; c1 < 0 keys by hi alone
+__global__ void k_fold_key(RelView in, const uint32_t *__restrict__ prev, int c0, int c1, uint64_t n,
+                           uint64_t *__restrict__ out) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const uint64_t hi = prev ? (uint64_t)prev[i] : (uint64_t)col_value(in, c0, i);
+        out[i] = c1 < 0 ? hi : ((hi << 32) | col_value(in, c1, i));
+    }
+}
+// rank of each key among the sorted unique keys u[0..nu), KEY_NONE when absent
+__global__ void k_rank_ids(const uint64_t *__restrict__ keys, uint64_t n, const uint64_t *__restrict__ u, uint64_t nu,
+                           uint32_t *__restrict__ ids) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const uint64_t k = keys[i];
+        uint64_t lo = 0, hi = nu;
+        while (lo < hi) {
+            const uint64_t mid = lo + ((hi - lo) >> 1);
+            if (u[mid] < k) lo = mid + 1; else hi = mid;
+        }
+        ids[i] = (lo < nu && u[lo] == k) ? (uint32_t)lo : KEY_NONE;
+    }
+}
+// (id << 32) | row index
+__global__ void k_id_rows(const uint32_t *__restrict__ ids, uint64_t n, uint64_t *__restrict__ out) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        out[i] = ((uint64_t)ids[i] << 32) | (uint32_t)i;
+}
+__global__ void k_found_flags(const uint32_t *__restrict__ ids, uint64_t n, int want, uint8_t *__restrict__ flags) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        flags[i] = (ids[i] != KEY_NONE) == (want != 0);
+}
+// output row r = left row (pairs[r] >> 32) ++ right row (low word)
+__global__ void k_gather_pairs(RelView L, RelView R, const uint64_t *__restrict__ pairs, uint64_t n, RelOut out) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    const int arity = L.arity + R.arity;
+    for (uint64_t r = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; r < n; r += stride) {
+        const uint64_t pr = pairs[r];
+        const uint64_t i = pr >> 32, j = (uint32_t)pr;
+        uint32_t v[MAX_ARITY];
+        for (int c = 0; c < L.arity; ++c) v[c] = col_value(L, c, i);
+        for (int c = 0; c < R.arity; ++c) v[L.arity + c] = col_value(R, c, j);
+        put_row(out, arity, v, r);
+    }
+}
+}  // namespace
+
+static xlog_hip_rel *op_join_keys(Ctx *ctx, const xlog_hip_rel *l, const xlog_hip_rel *r, const std::vector<int> &lk,
+                                  const std::vector<int> &rk, int type) {
+    XH_REQUIRE(l && r, XLOG_HIP_INVALID_ARG, "join input is NULL");
+    XH_REQUIRE(!lk.empty() && lk.size() == rk.size(), XLOG_HIP_INVALID_ARG,
+               "join: key column lists must be non-empty and of equal length");
+    for (size_t t = 0; t < lk.size(); ++t)
+        XH_REQUIRE(lk[t] >= 0 && lk[t] < (int)l->arity && rk[t] >= 0 && rk[t] < (int)r->arity, XLOG_HIP_INVALID_ARG,
+                   "join key column out of range");
+    XH_REQUIRE(type == XLOG_HIP_JOIN_INNER || type == XLOG_HIP_JOIN_SEMI || type == XLOG_HIP_JOIN_ANTI,
+               XLOG_HIP_INVALID_ARG, "unknown join type");
+    const uint32_t arity = l->arity + r->arity;
+    XH_REQUIRE(type != XLOG_HIP_JOIN_INNER || arity <= MAX_ARITY, XLOG_HIP_UNSUPPORTED,
+               "join: output arity (left ++ right) above 8");
+    XH_REQUIRE(l->rows < KEY_NONE && r->rows < KEY_NONE, XLOG_HIP_CAPACITY_OVERFLOW,
+               "join: more than 2^32 - 2 rows on one side");
+    const uint64_t nl = l->rows, nr = r->rows;
+    if (nl == 0 || nr == 0) {
+        if (type == XLOG_HIP_JOIN_ANTI) return rel_clone(ctx, l);
+        return rel_new(ctx, type == XLOG_HIP_JOIN_INNER ? arity : l->arity, 0);
+    }
+    // fold the key columns into dense ids
+    Buf<uint32_t> rid(ctx, nr), lid(ctx, nl);
+    Buf<uint64_t> rkey(ctx, nr), lkey(ctx, nl);
+    const size_t nk = lk.size();
+    for (size_t t = 0; t < nk;) {
+        const bool first = t == 0;
+        int lc0 = -1, lc1, rc0 = -1, rc1;
+        if (first) {
+            lc0 = lk[0];
+            rc0 = rk[0];
+            lc1 = nk >= 2 ? lk[1] : -1;
+            rc1 = nk >= 2 ? rk[1] : -1;
+            t = nk >= 2 ? 2 : 1;
+        } else {
+            lc1 = lk[t];
+            rc1 = rk[t];
+            ++t;
+        }
+        LAUNCH_1D(k_fold_key, nr, view_of(r), first ? nullptr : rid.p, rc0, rc1, nr, rkey.p);
+        LAUNCH_1D(k_fold_key, nl, view_of(l), first ? nullptr : lid.p, lc0, lc1, nl, lkey.p);
+        uint64_t *s = sort_keys(ctx, rkey.p, nr, false);
+        uint64_t *u = nullptr;
+        uint64_t nu = 0;
+        try {
+            nu = unique_keys(ctx, s, nr, &u);
+        } catch (...) {
+            ctx->free(s);
+            throw;
+        }
+        ctx->free(s);
+        LAUNCH_1D(k_rank_ids, nr, rkey.p, nr, u, nu, rid.p);
+        LAUNCH_1D(k_rank_ids, nl, lkey.p, nl, u, nu, lid.p);
+        ctx->free(u);
+    }
+    rkey = Buf<uint64_t>();
+    if (type != XLOG_HIP_JOIN_INNER) {
+        Buf<uint8_t> flags(ctx, nl);
+        LAUNCH_1D(k_found_flags, nl, lid.p, nl, type == XLOG_HIP_JOIN_SEMI ? 1 : 0, flags.p);
+        xlog_hip_rel *o = compact_rel(ctx, l, flags.p);
+        if (l->flags & REL_CANONICAL) o->flags = REL_CANONICAL;  // a subset of a sorted set is one
+        return o;
+    }
+    // (id << 32) | row on both sides; the run index groups the build rows by id
+    // (stable, so a run lists its rows in input order)
+    Buf<uint64_t> rp(ctx, nr);
+    LAUNCH_1D(k_id_rows, nr, rid.p, nr, rp.p);
+    uint64_t *lp = lkey.p;  // reused: the left keys are no longer needed
+    LAUNCH_1D(k_id_rows, nl, lid.p, nl, lp);
+    rid = Buf<uint32_t>();
+    lid = Buf<uint32_t>();
+    JoinIndex J;
+    build_join_index(ctx, rp.p, nr, 2, 0, false, J);
+    rp = Buf<uint64_t>();
+    const int oc[4] = {1, 3, 0, 0};  // (left row << 32) | right row
+    uint64_t *pairs = nullptr;
+    const uint64_t n = join_probe_general(ctx, lp, nl, 0, J.ix, J.payload.p, 2, oc, &pairs, nullptr);
+    if (n == 0) return rel_new(ctx, arity, 0);
+    Buf<uint64_t> pb;
+    pb.ctx = ctx;
+    pb.p = pairs;
+    std::unique_ptr<xlog_hip_rel, void (*)(xlog_hip_rel *)> o(rel_new(ctx, arity, n), rel_free);
+    o->rows = n;
+    LAUNCH_1D(k_gather_pairs, n, view_of(l), view_of(r), pairs, n, out_of(o.get()));
+    return o.release();
 }
 
 static bool column_sorted(Ctx *ctx, const xlog_hip_rel *rel, uint32_t col) {
@@ -1090,6 +1259,7 @@ struct Driver {
     std::vector<bool> idb;
     std::vector<DRel> full, delta;
     uint64_t version_counter = 1;
+    uint64_t max_join_rows = 0;  // 0: no limit on a body join's bag size
     // join-index cache keyed by (relation buffer, column, version)
     struct CacheKey {
         const uint64_t *k; int col; uint64_t version;
@@ -1191,7 +1361,7 @@ struct Driver {
             if (ar.n != 0) {
                 const JoinIndex &J = index_of(ar, apos);
                 int oc[4] = {sel[0], sel[1], 0, 0};
-                on = join_step(ctx, bk, bn, bpos, J, oc, &o);
+                on = join_step(ctx, bk, bn, bpos, J, oc, &o, max_join_rows);
             }
             if (owned) ctx->free(owned);
             owned = o;
@@ -1476,8 +1646,8 @@ static bool run_chain_route(Ctx *ctx, const std::vector<Rule> &rules, uint32_t n
     return true;
 }
 
-static void run_fixpoint(Ctx *ctx, const int32_t *plan, uint32_t n_preds, const xlog_hip_rel *const *rels,
-                         xlog_hip_rel **out, xlog_hip_fixpoint_stats *stats) {
+static void run_fixpoint_impl(Ctx *ctx, const int32_t *plan, uint32_t n_preds, const xlog_hip_rel *const *rels,
+                              xlog_hip_rel **out, xlog_hip_fixpoint_stats *stats, std::vector<uint64_t> &deltas) {
     XH_REQUIRE(n_preds >= 1 && n_preds <= 256, XLOG_HIP_INVALID_ARG, "n_preds must be 1..256");
     XH_REQUIRE(rels && out, XLOG_HIP_INVALID_ARG, "rels / out is NULL");
     std::vector<Rule> rules = parse_plan(plan, n_preds);
@@ -1487,7 +1657,6 @@ static void run_fixpoint(Ctx *ctx, const int32_t *plan, uint32_t n_preds, const 
     for (uint32_t p = 0; p < n_preds; ++p)
         XH_REQUIRE(!rels[p] || rels[p]->arity == 2, XLOG_HIP_TYPE_MISMATCH, "fixpoint: every predicate must have arity 2");
     XH_CHECK_HIP(hipEventRecord(ctx->ev_a, ctx->stream));
-    std::vector<uint64_t> deltas;
     uint64_t iterations = 0;
 
     int E = -1, H = -1;
@@ -1552,6 +1721,7 @@ static void run_fixpoint(Ctx *ctx, const int32_t *plan, uint32_t n_preds, const 
         Driver drv{ctx, rules, n_preds, std::vector<bool>(n_preds, false), std::vector<DRel>(n_preds),
                    std::vector<DRel>(n_preds)};
         for (const Rule &r : rules) drv.idb[r.head] = true;
+        drv.max_join_rows = stats ? stats->max_join_rows : 0;
         for (uint32_t p = 0; p < n_preds; ++p) {
             drv.full[p] = canon_drel(ctx, rels[p]);
             drv.full[p].version = drv.version_counter++;
@@ -1594,6 +1764,26 @@ static void run_fixpoint(Ctx *ctx, const int32_t *plan, uint32_t n_preds, const 
         if (stats->delta_sizes)
             for (uint64_t i = 0; i < stats->delta_cap && i < deltas.size(); ++i) stats->delta_sizes[i] = deltas[i];
     }
+}
+
+// The fixpoint with its statistics: on failure too, the iterations and delta
+// sizes reached are reported, and host_waits counts the device waits.
+static void run_fixpoint(Ctx *ctx, const int32_t *plan, uint32_t n_preds, const xlog_hip_rel *const *rels,
+                         xlog_hip_rel **out, xlog_hip_fixpoint_stats *stats) {
+    const uint64_t waits0 = ctx->host_waits;
+    std::vector<uint64_t> deltas;
+    try {
+        run_fixpoint_impl(ctx, plan, n_preds, rels, out, stats, deltas);
+    } catch (...) {
+        if (stats) {
+            stats->iterations = deltas.empty() ? 0 : deltas.size() - 1;
+            if (stats->delta_sizes)
+                for (uint64_t i = 0; i < stats->delta_cap && i < deltas.size(); ++i) stats->delta_sizes[i] = deltas[i];
+            stats->host_waits = ctx->host_waits - waits0;
+        }
+        throw;
+    }
+    if (stats) stats->host_waits = ctx->host_waits - waits0;
 }
 
 }  // namespace xh
@@ -2040,6 +2230,26 @@ xlog_hip_status xlog_hip_hash_join(xlog_hip_ctx *ctx, const xlog_hip_rel *left, 
         Ctx *c = C(ctx);
         OUT_GUARD;
         *out = op_join(c, left, right, left_key, right_key, join_type, nullptr);
+    });
+}
+xlog_hip_status xlog_hip_hash_join_keys(xlog_hip_ctx *ctx, const xlog_hip_rel *left, const xlog_hip_rel *right,
+                                        const uint32_t *left_keys, const uint32_t *right_keys, uint32_t n_keys,
+                                        int join_type, xlog_hip_rel **out) {
+    return guarded([&] {
+        Ctx *c = C(ctx);
+        OUT_GUARD;
+        need_rel(left, "left");
+        need_rel(right, "right");
+        XH_REQUIRE(n_keys >= 1 && left_keys && right_keys, XLOG_HIP_INVALID_ARG, "key column lists are empty or NULL");
+        XH_REQUIRE(n_keys <= MAX_ARITY, XLOG_HIP_INVALID_ARG, "more key columns than columns");
+        std::vector<int> lk(left_keys, left_keys + n_keys), rk(right_keys, right_keys + n_keys);
+        for (uint32_t t = 0; t < n_keys; ++t)
+            XH_REQUIRE(left_keys[t] < left->arity && right_keys[t] < right->arity, XLOG_HIP_INVALID_ARG,
+                       "join key column out of range");
+        if (n_keys == 1 && left->arity <= 2 && right->arity <= 2)
+            *out = op_join(c, left, right, left_keys[0], right_keys[0], join_type, nullptr);
+        else
+            *out = op_join_keys(c, left, right, lk, rk, join_type);
     });
 }
 xlog_hip_status xlog_hip_join_index_build(xlog_hip_ctx *ctx, const xlog_hip_rel *right, uint32_t right_key,

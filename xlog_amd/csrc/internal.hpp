@@ -153,7 +153,9 @@ struct Ctx {
     // Waits for the stream by polling an event: a read-back is followed by a
     // launch that depends on the value, and a blocking wait's wake-up adds tens
     // of microseconds of idle device per read-back (the host core spins instead).
+    uint64_t host_waits = 0;  // waits for the device (read-backs, synchronisations)
     void wait_event(hipEvent_t ev) {
+        ++host_waits;
         hipError_t e;
         while ((e = hipEventQuery(ev)) == hipErrorNotReady) {
         }

@@ -52,6 +52,8 @@ class FixpointStats(C.Structure):
         ("delta_cap", C.c_uint64),
         ("route", C.c_uint64),
         ("wall_ms", C.c_double),
+        ("max_join_rows", C.c_uint64),
+        ("host_waits", C.c_uint64),
     ]
 
 
@@ -113,6 +115,7 @@ def _load() -> C.CDLL:
         "xlog_hip_union_many": (I32, [P, PP, U32, PP]),
         "xlog_hip_diff": (I32, [P, P, P, PP]),
         "xlog_hip_hash_join": (I32, [P, P, P, U32, U32, I32, PP]),
+        "xlog_hip_hash_join_keys": (I32, [P, P, P, P, P, U32, I32, PP]),
         "xlog_hip_sort_merge_join": (I32, [P, P, P, U32, U32, PP]),
         "xlog_hip_join_project": (I32, [P, P, P, U32, U32, P, U32, PP]),
         "xlog_hip_join_project_dedup": (I32, [P, P, P, U32, U32, P, U32, PP]),
@@ -153,7 +156,7 @@ ABI_SYMBOLS = (
     "xlog_hip_rel_clone", "xlog_hip_rel_free", "xlog_hip_sort", "xlog_hip_dedup", "xlog_hip_dedup_full_row",
     "xlog_hip_dedup_sorted", "xlog_hip_join_index_build", "xlog_hip_hash_join_with_index",
     "xlog_hip_join_index_free", "xlog_hip_nested_loop_join", "xlog_hip_fj_delta_novel",
-    "xlog_hip_union", "xlog_hip_union_many", "xlog_hip_diff", "xlog_hip_hash_join",
+    "xlog_hip_union", "xlog_hip_union_many", "xlog_hip_diff", "xlog_hip_hash_join", "xlog_hip_hash_join_keys",
     "xlog_hip_sort_merge_join", "xlog_hip_join_project", "xlog_hip_join_project_dedup", "xlog_hip_project",
     "xlog_hip_is_sorted",
     "xlog_hip_exclusive_scan_u32", "xlog_hip_compact", "xlog_hip_fixpoint", "xlog_hip_fixpoint_tc",
@@ -516,11 +519,14 @@ class HipKernelProvider:
 
     def hash_join_v2(self, left: Relation, right: Relation, left_keys: Sequence[int], right_keys: Sequence[int],
                      join_type: int = JOIN_INNER) -> Relation:
-        if len(left_keys) != 1 or len(right_keys) != 1:
-            raise XlogError(7, "joins on one key column per side are supported")
+        """Equi-join on key column lists (relational.rs:2926-2992); INNER output is
+        left columns ++ right columns, SEMI / ANTI the matching / unmatched left rows."""
+        if len(left_keys) != len(right_keys) or not left_keys:
+            raise XlogError(1, "key column lists must be non-empty and of equal length")
+        (lk, _), (rk, _) = _u32_array(left_keys), _u32_array(right_keys)
         h = C.c_void_p()
-        _check(_lib.xlog_hip_hash_join(self.ctx, left.handle, right.handle, left_keys[0], right_keys[0],
-                                       join_type, C.byref(h)))
+        _check(_lib.xlog_hip_hash_join_keys(self.ctx, left.handle, right.handle, lk, rk, len(left_keys),
+                                            join_type, C.byref(h)))
         return self._rel(h)
 
     def build_join_index_v2(self, right: Relation, right_keys: Sequence[int]) -> JoinIndex:
@@ -607,25 +613,30 @@ class HipKernelProvider:
 
     # -- fixpoint (executor/recursive.rs:447-957) -----------------------------
     def fixpoint(self, plan: Sequence[int], relations: Sequence[Relation | None], route: int = ROUTE_AUTO,
-                 max_iterations: int = 0, trace_cap: int = 4096):
+                 max_iterations: int = 0, trace_cap: int = 4096, max_join_rows: int = 0):
         """Run a plan (see include/xlog_hip.h) to fixpoint.
 
         Returns (outputs, stats) where outputs[p] is the final relation of every
         IDB predicate p (None for EDB ones) and stats is a dict with
-        iterations, delta_sizes (index 0 = seed), route and wall_ms."""
+        iterations, delta_sizes (index 0 = seed), route, wall_ms and host_waits.
+        max_join_rows > 0 fails a rule body's join whose output would exceed it
+        (CAPACITY_OVERFLOW; 2**32 - 1 is the reference's u32 limit).  On failure
+        the raised XlogError carries .stats with the iterations and delta sizes
+        reached."""
         n = len(relations)
         plan_arr = (C.c_int32 * len(plan))(*plan)
         rels = (C.c_void_p * n)(*[r.handle if r is not None else None for r in relations])
         outs = (C.c_void_p * n)()
         trace = (C.c_uint64 * trace_cap)()
-        st = FixpointStats(0, max_iterations, trace, trace_cap, route, 0.0)
+        st = FixpointStats(0, max_iterations, trace, trace_cap, route, 0.0, max_join_rows, 0)
         status = _lib.xlog_hip_fixpoint(self.ctx, plan_arr, n, rels, outs, C.byref(st))
-        stats = {"iterations": st.iterations, "route": int(st.route), "wall_ms": st.wall_ms}
+        stats = {"iterations": st.iterations, "route": int(st.route), "wall_ms": st.wall_ms,
+                 "host_waits": st.host_waits}
+        stats["delta_sizes"] = [trace[i] for i in range(min(st.iterations + 1, trace_cap))]
         if status != OK:
             err = XlogError(status, (_lib.xlog_hip_last_error() or b"").decode())
             err.stats = stats
             raise err
-        stats["delta_sizes"] = [trace[i] for i in range(min(st.iterations + 1, trace_cap))]
         out = [self._rel(C.c_void_p(outs[i])) if outs[i] else None for i in range(n)]
         return out, stats
 
