@@ -235,6 +235,15 @@ xlog_hip_status xlog_hip_is_sorted(xlog_hip_ctx *ctx, const xlog_hip_rel *rel, u
 /* In-place exclusive scan of a device u32 array; *total receives the sum
  * (reference: exclusive_scan_u32_inplace, provider/mod.rs:2177). */
 xlog_hip_status xlog_hip_exclusive_scan_u32(xlog_hip_ctx *ctx, uint32_t *dev, uint64_t n, uint64_t *total);
+/* xlog_hip_exclusive_scan_u32 without any device allocation.  No counterpart
+ * in the reference: it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Its scratch (ticket, total, look-back status) lives in a
+ * fixed device array of 2 MiB per GPU, held from library load to process
+ * exit; n above 2^32 is CAPACITY_OVERFLOW.  All calls on one GPU share that
+ * array: calls that overlap on one GPU (two contexts on two threads) race.
+ * Synchronises the context stream to read *total. */
+xlog_hip_status xlog_hip_exclusive_scan_u32_noalloc(xlog_hip_ctx *ctx, uint32_t *dev, uint64_t n, uint64_t *total);
 /* Column roles of one factorized delta step (reference FjDeltaCols,
  * provider/fj_delta.rs:50-84); each pair is {0, 1} in some order. */
 typedef struct {

@@ -1886,6 +1886,7 @@ xlog_hip_status xlog_hip_ctx_create(int device, xlog_hip_ctx **out) {
         c.pool = new Pool(device);
         XH_CHECK_HIP(hipHostMalloc((void **)&c.host_scalars, Ctx::HOST_STAGE_U64 * sizeof(uint64_t),
                                    hipHostMallocDefault));
+        scan_noalloc_init(device);  // the allocation-free scan's scratch on this device
         c.tickets = static_cast<unsigned long long *>(c.alloc(16 * sizeof(unsigned long long)));
         fill_u64(&c, reinterpret_cast<uint64_t *>(c.tickets), 0ull, 16);
         XH_CHECK_HIP(hipEventCreate(&c.ev_a));
@@ -2378,6 +2379,13 @@ xlog_hip_status xlog_hip_exclusive_scan_u32(xlog_hip_ctx *ctx, uint32_t *dev, ui
         scan_u32_inplace(ctx, dev, n, tot.p);
         ctx->read_scalars(tot.p, 1);
         if (total) *total = ctx->host_scalars[0];
+    });
+}
+xlog_hip_status xlog_hip_exclusive_scan_u32_noalloc(xlog_hip_ctx *ctx, uint32_t *dev, uint64_t n, uint64_t *total) {
+    return guarded([&] {
+        Ctx *c = C(ctx);
+        XH_REQUIRE(n == 0 || dev, XLOG_HIP_INVALID_ARG, "array is NULL");
+        scan_u32_inplace_noalloc(c, dev, n, total);
     });
 }
 xlog_hip_status xlog_hip_compact(xlog_hip_ctx *ctx, const xlog_hip_rel *in, const uint8_t *dev_mask, xlog_hip_rel **out) {

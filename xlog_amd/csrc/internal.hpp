@@ -278,6 +278,13 @@ void select_flags(Ctx *ctx, const uint64_t *k, const uint8_t *flags, uint64_t n,
 // In-place exclusive scan of u32 values (prefixes wrap modulo 2^32); the
 // exact u64 sum goes to *d_total (device).  One pass, decoupled look-back.
 void scan_u32_inplace(Ctx *ctx, uint32_t *a, uint64_t n, unsigned long long *d_total);
+// The same scan with its scratch (ticket, total, look-back status) in a
+// file-scope device array instead of pool memory: no device allocation.  At
+// most SCAN_NOALLOC_MAX values; the total is read back (synchronises).
+// scan_noalloc_init looks the array's address up on `device` (current).
+constexpr uint64_t SCAN_NOALLOC_MAX = 1ull << 32;
+void scan_noalloc_init(int device);
+void scan_u32_inplace_noalloc(Ctx *ctx, uint32_t *a, uint64_t n, uint64_t *total);
 
 // Merge of two sorted arrays (stable, a before b on ties) into out[na+nb].
 void merge_sorted(Ctx *ctx, const uint64_t *a, uint64_t na, const uint64_t *b, uint64_t nb, uint64_t *out);

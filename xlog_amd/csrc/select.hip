@@ -640,6 +640,64 @@ void scan_u32_inplace(Ctx *ctx, uint32_t *a, uint64_t n, unsigned long long *d_t
     XH_CHECK_HIP(hipGetLastError());
 }
 
+// ---- the scan without allocation ---------------------------------------------
+// Device scratch of the allocation-free scan: [0] tile ticket, [1] exact total,
+// [2 ..] one look-back status word per tile.  It is a file-scope device array,
+// so every GPU the library runs on holds its own copy from module load to
+// process exit; its device address differs per GPU and is looked up once per
+// device (scan_noalloc_init) with that device current.  The name `scratch` in
+// host code is a host-side stand-in, never a device address: host code uses the
+// looked-up pointer only.
+constexpr uint64_t SCAN_NOALLOC_TILES = SCAN_NOALLOC_MAX / SCAN_TILE + 1;
+static_assert(SCAN_NOALLOC_MAX % SCAN_TILE == 0, "whole tiles");
+static __device__ __align__(256) uint64_t scratch[2 + SCAN_NOALLOC_TILES];
+
+static std::mutex g_noalloc_mu;
+static uint64_t *g_noalloc_ptr[64] = {nullptr};
+
+void scan_noalloc_init(int device) {
+    XH_REQUIRE(device >= 0 && device < 64, XLOG_HIP_INVALID_ARG, "device index above 63");
+    std::lock_guard<std::mutex> g(g_noalloc_mu);
+    if (g_noalloc_ptr[device]) return;
+    void *p = nullptr;
+    XH_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    XH_REQUIRE(p, XLOG_HIP_DEVICE_ERROR, "scratch symbol has no device address");
+    g_noalloc_ptr[device] = static_cast<uint64_t *>(p);
+}
+
+void scan_u32_inplace_noalloc(Ctx *ctx, uint32_t *a, uint64_t n, uint64_t *total) {
+    XH_REQUIRE(n <= SCAN_NOALLOC_MAX, XLOG_HIP_CAPACITY_OVERFLOW,
+               "scan without allocation: n = " + std::to_string(n) + " exceeds the maximum " +
+                   std::to_string(SCAN_NOALLOC_MAX));
+    uint64_t *sp = nullptr;
+    {
+        std::lock_guard<std::mutex> g(g_noalloc_mu);
+        sp = (ctx->device >= 0 && ctx->device < 64) ? g_noalloc_ptr[ctx->device] : nullptr;
+    }
+    XH_REQUIRE(sp, XLOG_HIP_DEVICE_ERROR, "scan without allocation: scratch not set up for this device");
+    const uint64_t tiles = (n + SCAN_TILE - 1) / SCAN_TILE;
+    // the ticket, the total and the status words of this call's tiles start at
+    // zero (a kernel fill, no memset); status words carry a fixed epoch tag,
+    // so a zeroed word reads as "not yet published"
+    fill_u64(ctx, sp, 0ull, 2 + tiles);
+    if (n) {
+        unsigned long long *ticket = reinterpret_cast<unsigned long long *>(sp);
+        unsigned long long *d_total = reinterpret_cast<unsigned long long *>(sp + 1);
+        const uint64_t tag = 1ull << 40;
+        if ((reinterpret_cast<uintptr_t>(a) & 15u) == 0)
+            hipLaunchKernelGGL(k_scan_u32<true>, dim3((unsigned)tiles), dim3(SCAN_BLOCK), 0, ctx->stream, a, n,
+                               sp + 2, tag, ticket, 0ull, d_total);
+        else
+            hipLaunchKernelGGL(k_scan_u32<false>, dim3((unsigned)tiles), dim3(SCAN_BLOCK), 0, ctx->stream, a, n,
+                               sp + 2, tag, ticket, 0ull, d_total);
+        XH_CHECK_HIP(hipGetLastError());
+    }
+    // the total comes back through the context's pinned staging (no allocation)
+    XH_CHECK_HIP(hipMemcpyAsync(ctx->host_scalars, sp + 1, sizeof(uint64_t), hipMemcpyDeviceToHost, ctx->stream));
+    ctx->sync();
+    if (total) *total = ctx->host_scalars[0];
+}
+
 void merge_sorted(Ctx *ctx, const uint64_t *a, uint64_t na, const uint64_t *b, uint64_t nb, uint64_t *out) {
     uint64_t total = na + nb;
     if (!total) return;

@@ -122,6 +122,7 @@ def _load() -> C.CDLL:
         "xlog_hip_project": (I32, [P, P, P, U32, PP]),
         "xlog_hip_is_sorted": (I32, [P, P, U32, C.POINTER(I32)]),
         "xlog_hip_exclusive_scan_u32": (I32, [P, P, U64, C.POINTER(U64)]),
+        "xlog_hip_exclusive_scan_u32_noalloc": (I32, [P, P, U64, C.POINTER(U64)]),
         "xlog_hip_compact": (I32, [P, P, P, PP]),
         "xlog_hip_fixpoint": (I32, [P, P, U32, PP, PP, C.POINTER(FixpointStats)]),
         "xlog_hip_fixpoint_tc": (I32, [P, P, PP, C.POINTER(FixpointStats)]),
@@ -159,7 +160,7 @@ ABI_SYMBOLS = (
     "xlog_hip_union", "xlog_hip_union_many", "xlog_hip_diff", "xlog_hip_hash_join", "xlog_hip_hash_join_keys",
     "xlog_hip_sort_merge_join", "xlog_hip_join_project", "xlog_hip_join_project_dedup", "xlog_hip_project",
     "xlog_hip_is_sorted",
-    "xlog_hip_exclusive_scan_u32", "xlog_hip_compact", "xlog_hip_fixpoint", "xlog_hip_fixpoint_tc",
+    "xlog_hip_exclusive_scan_u32", "xlog_hip_exclusive_scan_u32_noalloc", "xlog_hip_compact", "xlog_hip_fixpoint", "xlog_hip_fixpoint_tc",
     "xlog_hip_rel_digest", "xlog_hip_profile_enable", "xlog_hip_profile_reset", "xlog_hip_profile_read",
     "xlog_hip_arrow_ipc_decode_u32", "xlog_hip_arrow_ipc_encode_u32", "xlog_hip_bytes_free",
     "xlog_hip_rel_from_arrow_ipc", "xlog_hip_rel_to_arrow_ipc", "xlog_hip_read_arrow_ipc_stream_file",
@@ -604,6 +605,13 @@ class HipKernelProvider:
     def exclusive_scan_u32_inplace(self, dev_ptr: int, n: int) -> int:
         t = C.c_uint64()
         _check(_lib.xlog_hip_exclusive_scan_u32(self.ctx, C.c_void_p(dev_ptr), n, C.byref(t)))
+        return t.value
+
+    def exclusive_scan_u32_inplace_noalloc(self, dev_ptr: int, n: int) -> int:
+        """exclusive_scan_u32_inplace without any device allocation (scratch in
+        a fixed device array; n <= 2^32; overlapping calls on one GPU race)."""
+        t = C.c_uint64()
+        _check(_lib.xlog_hip_exclusive_scan_u32_noalloc(self.ctx, C.c_void_p(dev_ptr), n, C.byref(t)))
         return t.value
 
     def compact_by_device_mask(self, rel: Relation, dev_mask_ptr: int) -> Relation:
