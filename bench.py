@@ -91,14 +91,24 @@ def make_workload(name: str, p):
         config = {"workload": "c3: radix sort + dedup of 2^28 packed u64 tuples, 30% exact duplicates",
                   "tuples": n, "seed": datagen.seed_for(3)}
         return step, n, "input tuples", config, (keys,), state
-    if name in ("c1", "c4", "c1j", "c4j"):
+    if name in ("c1", "c4", "c1j", "c4j", "c1h", "c4h", "tcs", "tcs_crit", "tcs_j"):
         # c1j / c4j: the same closure forced onto the join route (per iteration: delta join edge, radix
-        # sort, unique and not-in-R selection, merge into R) instead of the bitmap route AUTO picks
-        from xlog_amd import ROUTE_AUTO, ROUTE_JOIN
-        route = ROUTE_JOIN if name.endswith("j") else ROUTE_AUTO
-        cfg = datagen.C1 if name.startswith("c1") else datagen.C4
-        cid = 1 if name.startswith("c1") else 4
+        # sort, unique and not-in-R selection, merge into R); c1h / c4h onto the hash-set route (one fused
+        # expand + insert pass per iteration) instead of the bitmap route AUTO picks.  tcs / tcs_crit: G(2^20, m)
+        # digraphs with ids spread over the u32 range (beyond the bit-matrix domain: AUTO takes the hash
+        # route; tcs_j forces the join route)
+        from xlog_amd import ROUTE_AUTO, ROUTE_HASH, ROUTE_JOIN
+        route = {"j": ROUTE_JOIN, "h": ROUTE_HASH}.get(name[-1], ROUTE_AUTO)
+        if name.startswith("tcs"):
+            cfg = datagen.TCS_CRIT if name == "tcs_crit" else datagen.TCS
+            cid = 6
+        else:
+            cfg = datagen.C1 if name.startswith("c1") else datagen.C4
+            cid = 1 if name.startswith("c1") else 4
         src, dst = datagen.random_digraph(cfg["n_vertices"], cfg["n_edges"], datagen.seed_for(cid))
+        graph = (src, dst)  # the CPU baseline's BFS takes the dense ids (same closure up to relabelling)
+        if name.startswith("tcs"):
+            src, dst = datagen.sparse_ids(src), datagen.sparse_ids(dst)
         E = p.create_buffer_from_u32_columns([src, dst])
         state = {}
 
@@ -108,11 +118,13 @@ def make_workload(name: str, p):
             state["iterations"] = st["iterations"]
             state["delta_sizes"] = st["delta_sizes"]
             state["route"] = st["route"]
+            state["host_waits"] = st["host_waits"]
 
         config = {"workload": f"{name}: semi-naive transitive closure, G(n,m) digraph"
-                              + (" (join route)" if route == ROUTE_JOIN else ""), "vertices": cfg["n_vertices"],
-                  "edges": cfg["n_edges"], "seed": datagen.seed_for(cid)}
-        return step, None, "closure tuples", config, (src, dst), state
+                              + (" with ids spread over u32" if name.startswith("tcs") else "")
+                              + {ROUTE_JOIN: " (join route)", ROUTE_HASH: " (hash-set route)"}.get(route, ""),
+                  "vertices": cfg["n_vertices"], "edges": cfg["n_edges"], "seed": datagen.seed_for(cid)}
+        return step, None, "closure tuples", config, (graph, cfg["n_vertices"]), state
     if name == "copy":
         # calibration: k_project over 2^28 packed rows reads 8 B and writes 8 B per row
         n = 1 << 28
@@ -218,20 +230,24 @@ def cpu_baseline(name: str, inputs, budget_s: float = 30.0):
         res = entry(len(outs[4]) / dt, "pointsTo tuples/s", threads, f"{smp} in {dt:.2f}s")
         res["single_thread"] = entry(len(outs1[4]) / dt1, "pointsTo tuples/s", 1, f"same instance in {dt1:.2f}s")
         return res
-    if name in ("c1", "c1j"):
-        src, dst = inputs
+    if name in ("c1", "c1j", "c1h"):
+        (src, dst), _ = inputs
         (outs, it, _), dt = timed(lambda: oracle.seminaive(tc_plan(), [pack(src, dst), None]), threads)
         (outs1, _, _), dt1 = timed(lambda: oracle.seminaive(tc_plan(), [pack(src, dst), None]), 1)
         res = entry(len(outs[1]) / dt, "tuples/s", threads,
                     f"full config, semi-naive oracle: {len(outs[1])} tuples, {it} iterations in {dt:.2f}s")
         res["single_thread"] = entry(len(outs1[1]) / dt1, "tuples/s", 1, f"same in {dt1:.2f}s")
         return res
-    if name in ("c4", "c4j"):
-        src, dst = inputs
+    if name in ("c4", "c4j", "c4h") or name.startswith("tcs"):
+        (src, dst), nv = inputs
         # the semi-naive oracle over ~10^9 tuples takes far longer than the budget:
         # time the BFS closed form (closure size from every source) instead
-        res_mt, dt = timed(lambda: oracle.bfs_tc(32768, src, dst, want_relation=False, digest=False), threads)
-        res_1, dt1 = timed(lambda: oracle.bfs_tc(32768, src, dst, want_relation=False, digest=False), 1)
+        res_mt, dt = timed(lambda: oracle.bfs_tc(nv, src, dst, want_relation=False, digest=False), threads)
+        if name.startswith("tcs"):  # a 1-thread run of the whole closure would take minutes: report the threaded one
+            return entry(res_mt["total"] / dt, "tuples/s", threads,
+                         f"BFS-layer closure from all sources (closed form, not the semi-naive loop): "
+                         f"{res_mt['total']} tuples in {dt:.2f}s")
+        res_1, dt1 = timed(lambda: oracle.bfs_tc(nv, src, dst, want_relation=False, digest=False), 1)
         res = entry(res_mt["total"] / dt, "tuples/s", threads,
                     f"BFS-layer closure from all sources (closed form, not the semi-naive loop): "
                     f"{res_mt['total']} tuples in {dt:.2f}s")
@@ -293,6 +309,41 @@ def measure(name: str, p, steps: int, warmup: int, with_cpu: bool) -> dict:
             "kernels": kernels, "result": result}
 
 
+def run_c5full(p) -> dict:
+    """BASELINE's literal C5 (500,000 variables / 2,000,000 facts) on the join route with the reference's
+    u32 join-row limit (relational.rs:4550-4555): the outcome (converged, or the failure with the iteration
+    and the bag size that tripped it), plus the size of rule 2's first-iteration output, a lower bound of
+    |pointsTo| computed by the fused join+project+dedup."""
+    from xlog_amd import XlogError, andersen_plan, datagen
+
+    cfg = datagen.C5
+    t = time.perf_counter()
+    f = datagen.andersen(cfg["n_vars"], cfg["n_facts"], cfg["alpha"], datagen.seed_for(5))
+    log(f"c5full inputs generated in {time.perf_counter() - t:.1f}s")
+    rels = [p.create_buffer_from_u32_columns(list(f[k])) for k in ("assign", "addressOf", "load", "store")]
+    out = {"workload": "c5full: Andersen points-to at 500,000 variables / 2,000,000 facts (BASELINE configs[4])",
+           **cfg, "seed": datagen.seed_for(5), "max_join_rows": (1 << 32) - 1}
+    p.synchronize()
+    t0 = time.perf_counter()
+    try:
+        outs, st = p.fixpoint(andersen_plan(), rels + [None], max_join_rows=(1 << 32) - 1)
+        out.update(outcome="converged", tuples=outs[4].num_rows(), iterations=st["iterations"],
+                   delta_sizes=st["delta_sizes"], route=st["route"])
+    except XlogError as e:
+        st = getattr(e, "stats", {})
+        out.update(outcome=f"failed closed: status {e.status}", message=str(e),
+                   iterations_reached=st.get("iterations"), delta_sizes=st.get("delta_sizes"), route=st.get("route"))
+    p.synchronize()
+    out["seconds"] = time.perf_counter() - t0
+    # rule 2 of the first iteration alone: {(v, o) : assign(v, w), addressOf(w, o)} (the seed delta is addressOf)
+    t0 = time.perf_counter()
+    r2 = p.join_project_dedup(rels[0], rels[1], 1, 0, [0, 3])
+    p.synchronize()
+    out["rule2_first_iteration_tuples"] = r2.num_rows()
+    out["rule2_seconds"] = time.perf_counter() - t0
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -310,6 +361,10 @@ def main() -> int:
     from xlog_amd import HipKernelProvider
 
     p = HipKernelProvider(0)
+    if args.workload == "c5full":
+        print(json.dumps({"metric": METRIC, "value": None, "n_gpus": 1, "result": run_c5full(p)}))
+        p.close()
+        return 0
     head = measure(args.workload, p, args.steps, args.warmup, not args.no_cpu_baseline)
     p.trim()
     extras = {}

@@ -261,6 +261,15 @@ typedef struct {
 xlog_hip_status xlog_hip_fj_delta_novel(xlog_hip_ctx *ctx, const xlog_hip_rel *delta, const xlog_hip_rel *edge,
                                         const xlog_hip_rel *full, const xlog_hip_fj_delta_cols *cols,
                                         uint32_t domain, xlog_hip_rel **out);
+/* The same step over a device hash set, with no domain bound (reference:
+ * fj_delta_sparse_novel_u32_recorded, provider/fj_delta_sparse.rs:66).  The
+ * table holds 2 x (|full| + candidate tuples) slots; when that is above
+ * max_table_bytes (0: no budget) the call declines like the reference's
+ * Ok(None): it returns XLOG_HIP_OK with *out = NULL.  The output is canonical
+ * (the reference's is unordered). */
+xlog_hip_status xlog_hip_fj_delta_sparse_novel(xlog_hip_ctx *ctx, const xlog_hip_rel *delta, const xlog_hip_rel *edge,
+                                               const xlog_hip_rel *full, const xlog_hip_fj_delta_cols *cols,
+                                               uint64_t max_table_bytes, xlog_hip_rel **out);
 /* Keep rows whose device u8 mask is non-zero, input order
  * (reference: compact_buffer_by_device_mask_device_count, provider/filter.rs:1820-1935). */
 xlog_hip_status xlog_hip_compact(xlog_hip_ctx *ctx, const xlog_hip_rel *in, const uint8_t *dev_mask,
@@ -297,13 +306,18 @@ typedef struct {
 
 /* AUTO takes the bitmap route when every rule body is a path, there are at
  * most 2^17 distinct ids (max id + 1) and the bit matrices fit in half the
- * free device memory; the join route otherwise.  Requesting BITMAP for a plan
- * or domain it cannot take is UNSUPPORTED. */
+ * free device memory; the hash route for the transitive-closure plan with an
+ * empty head above 2^17 ids; the join route otherwise.  Requesting BITMAP or
+ * HASH for a plan or domain it cannot take is UNSUPPORTED. */
 #define XLOG_HIP_ROUTE_AUTO 0
 #define XLOG_HIP_ROUTE_JOIN 1   /* join -> sort -> dedup -> diff -> merge */
 #define XLOG_HIP_ROUTE_BITMAP 2 /* relations as domain x domain bit matrices, rule bodies as chains of
                                    boolean products (the dense factorized delta of provider/fj_delta.rs:117
                                    generalised from transitive closure to path-shaped bodies) */
+#define XLOG_HIP_ROUTE_HASH 3   /* transitive closure with R in a device hash set: each iteration is one
+                                   fused expand + insert pass (the sparse factorized delta of
+                                   provider/fj_delta_sparse.rs:66 with a persistent table); AUTO takes it
+                                   for the TC plan with an empty head above 2^17 ids */
 
 xlog_hip_status xlog_hip_fixpoint(xlog_hip_ctx *ctx, const int32_t *plan, uint32_t n_preds,
                                   const xlog_hip_rel *const *rels, xlog_hip_rel **out,
@@ -330,7 +344,8 @@ xlog_hip_status xlog_hip_fixpoint_tc(xlog_hip_ctx *ctx, const xlog_hip_rel *edge
 #define XLOG_HIP_KERNEL_CHAIN_PRODUCT 8  /* dense chain-rule boolean product */
 #define XLOG_HIP_KERNEL_CHAIN_FINALIZE 9 /* dense chain-rule delta / merge */
 #define XLOG_HIP_KERNEL_CHAIN_EMIT 10    /* dense chain-rule final emit */
-#define XLOG_HIP_KERNEL_KINDS 11
+#define XLOG_HIP_KERNEL_HASH_INSERT 11   /* sparse delta step: expand + hash-set insert */
+#define XLOG_HIP_KERNEL_KINDS 12
 xlog_hip_status xlog_hip_profile_enable(xlog_hip_ctx *ctx, int on);
 xlog_hip_status xlog_hip_profile_reset(xlog_hip_ctx *ctx);
 xlog_hip_status xlog_hip_profile_read(xlog_hip_ctx *ctx, uint32_t kind, uint64_t *launches, double *total_ms,

@@ -391,6 +391,101 @@ static int needed_later(const rule_t *r, int from_atom, int var) {
     return 0;
 }
 
+/* The last join of a body when its two output variables are a binding
+ * variable g (not the shared one) and the atom's new variable o: the set
+ * { (g, o) : binding (g, s), atom (s, o) } (with the columns of `nxt`'s
+ * order) without the bag.  Binding rows are grouped by g; per group the o's of
+ * every matching atom row are OR-ed into a bitset over o's domain and the set
+ * bits emitted, groups spread over the threads.  idx: the atom relation as
+ * sorted (shared << 32) | o.  Returns 1 when it ran, 0 when the domain is too
+ * large for per-thread bitsets (the caller then takes the bag path), <0 on
+ * OOM. */
+static int last_join_grouped(const binding_t *cur, int gpos, const uint64_t *idx, uint64_t nr, int atom_self,
+                             int g_first, vec64 *outv) {
+    uint32_t maxo = 0;
+    for (uint64_t i = 0; i < nr; ++i) if ((uint32_t)idx[i] > maxo) maxo = (uint32_t)idx[i];
+    const uint64_t D = (uint64_t)maxo + 1;
+    if (D > (1ull << 27)) return 0;
+    const uint64_t words = (D + 63) / 64, n = cur->rows.n;
+    uint64_t *gp = (uint64_t *)malloc((n ? n : 1) * sizeof(uint64_t));  /* (g << 32) | shared */
+    if (!gp) return -2;
+    for (uint64_t i = 0; i < n; ++i) {
+        const uint64_t row = cur->rows.v[i];
+        const uint32_t g = gpos ? (uint32_t)row : (uint32_t)(row >> 32);
+        const uint32_t s = gpos ? (uint32_t)(row >> 32) : (uint32_t)row;
+        gp[i] = ((uint64_t)g << 32) | s;
+    }
+    if (or_sort_u64(gp, n)) { free(gp); return -2; }
+    /* group starts */
+    uint64_t ng = 0;
+    uint64_t *gs = (uint64_t *)malloc((n + 1) * sizeof(uint64_t));
+    if (!gs) { free(gp); return -2; }
+    for (uint64_t i = 0; i < n; ++i)
+        if (i == 0 || (gp[i] >> 32) != (gp[i - 1] >> 32)) gs[ng++] = i;
+    gs[ng] = n;
+    int T = 1;
+#ifdef _OPENMP
+    T = g_threads > 1 ? g_threads : 1;
+#endif
+    vec64 *loc = (vec64 *)calloc((size_t)T, sizeof(vec64));
+    uint64_t **bits = (uint64_t **)calloc((size_t)T, sizeof(uint64_t *));
+    int err = (!loc || !bits);
+    for (int t = 0; t < T && !err; ++t)
+        if (!(bits[t] = (uint64_t *)calloc(words, sizeof(uint64_t)))) err = 1;
+    if (!err) {
+#ifdef _OPENMP
+        #pragma omp parallel for num_threads(T) schedule(dynamic, 8)
+#endif
+        for (int64_t q = 0; q < (int64_t)ng; ++q) {
+            int t = 0;
+#ifdef _OPENMP
+            t = omp_get_thread_num();
+#endif
+            uint64_t *b = bits[t];
+            const uint32_t g = (uint32_t)(gp[gs[q]] >> 32);
+            uint64_t wlo = words, whi = 0;  /* touched word range */
+            for (uint64_t i = gs[q]; i < gs[q + 1]; ++i) {
+                const uint32_t key = (uint32_t)gp[i];
+                uint64_t lo = 0, hi = nr;
+                while (lo < hi) { uint64_t m = (lo + hi) / 2; if ((uint32_t)(idx[m] >> 32) < key) lo = m + 1; else hi = m; }
+                for (uint64_t e = lo; e < nr && (uint32_t)(idx[e] >> 32) == key; ++e) {
+                    const uint32_t o = (uint32_t)idx[e];
+                    if (atom_self && o != key) continue;
+                    b[o >> 6] |= 1ull << (o & 63);
+                    if ((o >> 6) < wlo) wlo = o >> 6;
+                    if ((o >> 6) + 1 > whi) whi = (o >> 6) + 1;
+                }
+            }
+            for (uint64_t w = wlo; w < whi; ++w) {
+                uint64_t x = b[w];
+                b[w] = 0;
+                while (x) {
+                    const uint32_t o = (uint32_t)(w * 64 + (uint64_t)__builtin_ctzll(x));
+                    x &= x - 1;
+                    const uint64_t row = g_first ? (((uint64_t)g << 32) | o) : (((uint64_t)o << 32) | g);
+                    if (vec_push(&loc[t], row)) err = 1;
+                }
+            }
+        }
+    }
+    uint64_t total = 0;
+    for (int t = 0; t < T && !err; ++t) total += loc[t].n;
+    if (!err && vec_reserve(outv, outv->n + total)) err = 1;
+    for (int t = 0; t < T; ++t) {
+        if (!err) {
+            memcpy(outv->v + outv->n, loc[t].v, loc[t].n * sizeof(uint64_t));
+            outv->n += loc[t].n;
+        }
+        if (loc) vec_free(&loc[t]);
+        if (bits) free(bits[t]);
+    }
+    free(loc);
+    free(bits);
+    free(gs);
+    free(gp);
+    return err ? -2 : 1;
+}
+
 /* Evaluate one rule body with rel[j] the relation read by atom j.
  * Appends the projected head tuples (bag) to *out. */
 static int eval_body(const rule_t *r, const uint64_t *const *rel, const uint64_t *nrel, vec64 *out) {
@@ -443,6 +538,22 @@ static int eval_body(const rule_t *r, const uint64_t *const *rel, const uint64_t
         for (uint64_t i = 0; i < nr; ++i) idx[i] = ((uint64_t)col_of(rel[j][i], jk) << 32) | col_of(rel[j][i], 1 - jk);
         or_sort_u64(idx, nr);
         int atom_self = (a->v[0] == a->v[1]);
+        /* the last join with output (the binding's other variable, the atom's new variable): grouped, no bag */
+        if (j == r->nb - 1 && cur.nv == 2 && nxt.nv == 2 && other_is_new) {
+            const int gpos = 1 - bpos[0];
+            const int gv = cur.vars[gpos];
+            if ((nxt.vars[0] == gv && nxt.vars[1] == other) || (nxt.vars[1] == gv && nxt.vars[0] == other)) {
+                const int ran = last_join_grouped(&cur, gpos, idx, nr, atom_self, nxt.vars[0] == gv, &nxt.rows);
+                if (ran < 0) { free(idx); vec_free(&cur.rows); vec_free(&nxt.rows); return -2; }
+                if (ran == 1) {
+                    free(idx);
+                    vec_free(&cur.rows);
+                    nxt.rows.n = or_sort_dedup(nxt.rows.v, nxt.rows.n);
+                    cur = nxt;
+                    continue;
+                }
+            }
+        }
         /* column of 'other' check when it is an already-bound var (ns would be 2) handled above */
         for (uint64_t i = 0; i < cur.rows.n; ++i) {
             uint64_t row = cur.rows.v[i];
@@ -693,9 +804,9 @@ int64_t or_bfs_tc(uint32_t n_vertices, const uint32_t *src, const uint32_t *dst,
             int32_t *dl = (int32_t *)malloc((size_t)(n_vertices ? n_vertices : 1) * sizeof(int32_t));
             uint32_t *ql = (uint32_t *)malloc((size_t)(n_vertices ? n_vertices : 1) * sizeof(uint32_t));
             uint64_t *mydc = dc ? dc + (size_t)t * max_dist : NULL;
+            for (uint32_t v = 0; v < n_vertices; ++v) dl[v] = -1;
             #pragma omp for schedule(dynamic, 64)
             for (uint32_t x = 0; x < n_vertices; ++x) {
-                for (uint32_t v = 0; v < n_vertices; ++v) dl[v] = -1;
                 uint64_t qh = 0, qt = 0;
                 for (uint64_t e = deg[x]; e < deg[x + 1]; ++e) {
                     uint32_t z = adj[e];
@@ -712,6 +823,7 @@ int64_t or_bfs_tc(uint32_t n_vertices, const uint32_t *src, const uint32_t *dst,
                     int32_t dz = dl[ql[i]];
                     if (dz > maxd) maxd = dz;
                     if (mydc && (uint64_t)dz < max_dist) mydc[dz]++;
+                    dl[ql[i]] = -1;  /* only the visited vertices are reset */
                 }
                 tot += qt;
             }
@@ -727,8 +839,8 @@ int64_t or_bfs_tc(uint32_t n_vertices, const uint32_t *src, const uint32_t *dst,
         return maxd == 0 ? 1 : maxd;
     }
 #endif
+    for (uint32_t v = 0; v < n_vertices; ++v) dist[v] = -1;
     for (uint32_t x = 0; x < n_vertices; ++x) {
-        for (uint32_t v = 0; v < n_vertices; ++v) dist[v] = -1;
         uint64_t qh = 0, qt = 0, nrow = 0;
         /* x itself is not at distance 0 in the relation: only walks of length >= 1 count */
         for (uint64_t e = deg[x]; e < deg[x + 1]; ++e) {
@@ -742,12 +854,15 @@ int64_t or_bfs_tc(uint32_t n_vertices, const uint32_t *src, const uint32_t *dst,
                 if (dist[z] < 0) { dist[z] = dist[y] + 1; queue[qt++] = z; }
             }
         }
-        for (uint32_t z = 0; z < n_vertices; ++z) {
-            if (dist[z] < 0) continue;
+        /* the row of x in z order: the visited vertices, sorted; then reset them */
+        for (uint64_t i = 0; i < qt; ++i) {
+            const uint32_t z = queue[i];
             if (dist[z] > maxd) maxd = dist[z];
             if (dist_count && (uint64_t)dist[z] < max_dist) dist_count[dist[z]]++;
             row[nrow++] = ((uint64_t)x << 32) | z;
+            dist[z] = -1;
         }
+        sort_u64_serial(row, nrow);
         for (uint64_t i = 0; i < nrow; ++i) {
             uint64_t k = row[i];
             for (int b = 0; b < 8; ++b) { h ^= (k >> (8 * b)) & 255; h *= 0x100000001b3ULL; }

@@ -1,16 +1,18 @@
 // CPU model of the radix pass's tile order and decoupled look-back
 // (xlog_amd/csrc/sort.hip: chunk_tile, k_onesweep, radix_sort_u64's grid).
 //
-// Threads play workgroups.  Blocks are dispatched in index order into `cap`
-// slots (a slot frees when its block ends), block b runs tile
+// Threads play workgroups.  Blocks are dispatched into `cap` slots (a slot
+// frees when its block ends), in index order or, in mode "shuffled", in a
+// random order; a starting block takes the next ticket b and runs tile
 // ((b/8)/chunk*8 + b%8)*chunk + (b/8)%chunk, publishes its aggregate, walks
 // back over 4 predecessors per round until an inclusive prefix, and publishes
 // its own inclusive prefix.  Checked: every tile runs once, every exclusive
 // prefix is exact, and no run deadlocks (watchdog) when cap >= 8*chunk, the
-// condition the host sizes chunk for.  With cap below 8*chunk the same model
-// must be able to deadlock, which shows the watchdog detects it.
+// condition the host sizes chunk for, whatever the dispatch order.  With cap
+// below 8*chunk the same model must be able to deadlock, which shows the
+// watchdog detects it.
 //
-// usage: sort_schedule_sim <trials> <watchdog_seconds> <mode: ok|tight>
+// usage: sort_schedule_sim <trials> <watchdog_seconds> <mode: ok|tight|shuffled>
 // prints "runs R failures F hangs H"
 #include <atomic>
 #include <chrono>
@@ -19,6 +21,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <algorithm>
 #include <mutex>
 #include <random>
 #include <thread>
@@ -81,6 +84,7 @@ int main(int argc, char **argv) {
     const int trials = argc > 1 ? atoi(argv[1]) : 40;
     const int watchdog = argc > 2 ? atoi(argv[2]) : 10;
     const bool tight = argc > 3 && strcmp(argv[3], "tight") == 0;
+    const bool shuffled = argc > 3 && strcmp(argv[3], "shuffled") == 0;
     std::mt19937 rng(2024);
     int runs = 0, failures = 0, hangs = 0;
     for (int trial = 0; trial < trials; ++trial) {
@@ -98,6 +102,10 @@ int main(int argc, char **argv) {
         const uint32_t nchunks = (tiles + chunk - 1) / chunk;
         const uint32_t grid = 8 * ((nchunks + 7) / 8) * chunk;
         Run r(tiles, chunk);
+        std::vector<uint32_t> order(grid);  // dispatch order of the block indices
+        for (uint32_t b = 0; b < grid; ++b) order[b] = b;
+        if (shuffled) std::shuffle(order.begin(), order.end(), rng);
+        std::atomic<uint32_t> ticket{0};
         std::mutex mu;
         std::condition_variable cv;
         uint32_t running = 0;
@@ -117,8 +125,8 @@ int main(int argc, char **argv) {
             ++running;
             lk.unlock();
             th.emplace_back([&, b] {
-                std::mt19937 lr(b * 31u + (uint32_t)trial);
-                const uint32_t t = r.tile_of(b);
+                std::mt19937 lr(order[b] * 31u + (uint32_t)trial);
+                const uint32_t t = r.tile_of(ticket.fetch_add(1));  // the kernel's start-order ticket
                 if (t != NONE) r.process(t, lr);
                 std::lock_guard<std::mutex> g(mu);
                 --running;

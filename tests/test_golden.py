@@ -74,3 +74,40 @@ def test_full_size_input_digests(name):
     else:
         r_a, r_b, s_b, s_c = datagen.zipf_join(e["n_r"], e["n_s"], e["n_keys"], e["zipf_s"], datagen.seed_for(2))
         assert fnv_inputs(r_a, r_b, s_b, s_c) == e["input_digest"]
+
+
+@pytest.mark.parametrize("name", ["c5_10000_40000", "c5_20000_80000", "c5_40000_160000"])
+def test_c5_larger_input_digests(name):
+    """The larger Andersen fixtures pin the generator at their sizes (their outputs are
+    checked on the GPU against both routes; make_golden.py checked semi-naive = naive up
+    to 20,000 variables)."""
+    if name not in FX:
+        pytest.skip(f"{name} fixture not generated")
+    e = FX[name]
+    f = datagen.andersen(e["n_vars"], e["n_facts"], e["alpha"], datagen.seed_for(5))
+    assert fnv_inputs(*[x for k in ("assign", "addressOf", "load", "store") for x in f[k]]) == e["input_digest"]
+
+
+def test_c5_10000_fixture_reproduced():
+    # the instance bench.py times: the oracle (all host threads) reproduces the committed entry
+    e = FX["c5_10000_40000"]
+    f = datagen.andersen(e["n_vars"], e["n_facts"], e["alpha"], datagen.seed_for(5))
+    rels = [pack(*f[k]) for k in ("assign", "addressOf", "load", "store")]
+    oracle.set_threads(oracle.max_threads())
+    try:
+        outs, it, deltas = oracle.seminaive(andersen_plan(), rels + [None])
+    finally:
+        oracle.set_threads(1)
+    assert (len(outs[4]), it, deltas, oracle.fnv1a64(outs[4])) == (e["tuples"], e["iterations"], e["delta_sizes"],
+                                                                     e["digest"])
+
+
+@pytest.mark.parametrize("name,cfg", [("tcs", datagen.TCS), ("tcs_crit", datagen.TCS_CRIT)])
+def test_sparse_id_closure_inputs(name, cfg):
+    # G(2^20, m) digraphs with ids spread over the u32 range (datagen.sparse_ids)
+    e = FX[name]
+    src, dst = datagen.random_digraph(cfg["n_vertices"], cfg["n_edges"], datagen.seed_for(6))
+    s, d = datagen.sparse_ids(src), datagen.sparse_ids(dst)
+    assert int(max(s.max(), d.max())) + 1 > (1 << 17)  # beyond the dense domain
+    assert fnv_inputs(s, d) == e["input_digest"]
+    assert e["delta_sizes"][-1] == 0 and sum(e["delta_sizes"]) == e["tuples"]

@@ -95,11 +95,18 @@ def test_c4_full_transitive_closure(provider, route):
     assert p.digest(R) == e["digest"]
 
 
-@pytest.mark.parametrize("route", [ROUTE_BITMAP, ROUTE_JOIN])
-@pytest.mark.parametrize("fixture", ["c5_2000_8000", "c5_5000_20000"])
+@pytest.mark.parametrize("route,fixture", [
+    (ROUTE_BITMAP, "c5_2000_8000"), (ROUTE_JOIN, "c5_2000_8000"),
+    (ROUTE_BITMAP, "c5_5000_20000"), (ROUTE_JOIN, "c5_5000_20000"),
+    # the instance bench.py times (10,000 variables / 40,000 facts) and larger ones
+    (ROUTE_BITMAP, "c5_10000_40000"), (ROUTE_JOIN, "c5_10000_40000"),
+    (ROUTE_BITMAP, "c5_20000_80000"), (ROUTE_JOIN, "c5_20000_80000"),
+    (ROUTE_BITMAP, "c5_40000_160000"),
+])
 def test_c5_scaled_andersen_fixture(provider, fixture, route):
     e = FX[fixture]
     f = datagen.andersen(e["n_vars"], e["n_facts"], e["alpha"], datagen.seed_for(5))
+    assert _fnv_inputs(*[x for k in ("assign", "addressOf", "load", "store") for x in f[k]]) == e["input_digest"]
     p = provider
     rels = [p.create_buffer_from_u32_columns(list(f[k])) for k in ("assign", "addressOf", "load", "store")]
     _note(f"{fixture}: fixpoint route={route}")
@@ -109,6 +116,14 @@ def test_c5_scaled_andersen_fixture(provider, fixture, route):
     assert st["iterations"] == e["iterations"]
     assert st["delta_sizes"] == e["delta_sizes"]
     assert p.digest(outs[4]) == e["digest"]
+
+
+def _fnv_inputs(*arrays):
+    """Input digest of the fixtures (tests/golden/make_golden.py: fnv_inputs)."""
+    h = 0
+    for a in arrays:
+        h = ((h * 0x100000001B3) ^ oracle.fnv1a64(np.asarray(a).astype(np.uint64))) & ((1 << 64) - 1)
+    return h
 
 
 def test_c1_full_matches_committed_closure(provider):

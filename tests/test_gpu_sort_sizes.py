@@ -118,3 +118,24 @@ def test_stable_sort_column_with_constant_low_byte(provider, n):
     got = p.download_packed(p.sort(rel, [1]))
     order = np.argsort(c1, kind="stable")
     assert np.array_equal(got, pack(c0[order], c1[order]))
+
+
+@pytest.mark.parametrize("tiles", [1, 64, 260, 700, 2100])
+def test_ticketed_tile_order(provider, monkeypatch, tiles):
+    # XLOG_HIP_SORT_TICKETS=1: tiles numbered by start-order tickets (no in-order dispatch assumed)
+    p = provider
+    monkeypatch.setenv("XLOG_HIP_SORT_TICKETS", "1")
+    n = tiles * TILE_K - (tiles * 53) % 3000
+    _note(f"ticketed sort: tiles={tiles} n={n}")
+    rng = np.random.default_rng(1000 + tiles)
+    keys = rng.integers(0, 1 << 64, size=n, dtype=np.uint64)
+    keys[rng.integers(0, n, n // 4)] = keys[rng.integers(0, n, n // 4)]  # duplicates
+    d = p.dedup_full_row(p.create_buffer_from_packed(keys))
+    assert np.array_equal(p.download_packed(d), np.unique(keys))
+    # a stable keyed sort (payload passes) under the same order
+    c0 = rng.integers(0, 1000, size=min(n, 400_000), dtype=np.uint32)
+    c1 = np.arange(len(c0), dtype=np.uint32)
+    c2 = rng.integers(0, 7, size=len(c0), dtype=np.uint32)
+    s = p.sort(p.create_buffer_from_u32_columns([c0, c1, c2]), [2, 0])
+    order = np.lexsort((c0, c2))  # stable: by c2, then c0, ties in input order
+    assert np.array_equal(p.download_column(s, 1), c1[order])

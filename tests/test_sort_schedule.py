@@ -1,6 +1,7 @@
 """CPU check of the radix pass's tile order (xlog_amd/csrc/sort.hip, chunk_tile and
-radix_sort_u64's grid): a threaded model of in-order workgroup dispatch with the
-kernel's tile formula and decoupled look-back (tests/sim/sort_schedule_sim.cpp).
+radix_sort_u64's grid): a threaded model of workgroup dispatch (in index order and
+shuffled) with the kernel's start-order tickets, tile formula and decoupled look-back
+(tests/sim/sort_schedule_sim.cpp).
 
 With room for at least 8 * chunk blocks at once (the condition the host sizes
 chunk for) every tile must run exactly once with its exact exclusive prefix and
@@ -31,6 +32,12 @@ def _run(exe, trials, watchdog, mode):
 def test_tile_order_never_stalls_with_the_host_chunk(sim):
     res, out = _run(sim, 200, 30, "ok")
     assert res == {"runs": 200, "failures": 0, "hangs": 0}, out
+
+
+def test_tile_order_never_stalls_under_any_dispatch_order(sim):
+    # tiles come from start-order tickets, so a shuffled dispatch order changes nothing
+    res, out = _run(sim, 100, 30, "shuffled")
+    assert res == {"runs": 100, "failures": 0, "hangs": 0}, out
 
 
 def test_tile_order_can_stall_below_the_condition(sim):

@@ -16,6 +16,7 @@ from .provider import (  # noqa: F401
     ROUTE_AUTO,
     ROUTE_JOIN,
     ROUTE_BITMAP,
+    ROUTE_HASH,
     tc_plan,
     andersen_plan,
     copy_points_to_plan,

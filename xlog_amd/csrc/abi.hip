@@ -311,7 +311,7 @@ static uint64_t read_count(Ctx *ctx, const uint64_t *d) {
 // digit_lo / digit_hi restrict the sort to 8-bit digits [lo, hi) (4..8 = by
 // the high word only, stable otherwise).
 static uint64_t *sort_keys(Ctx *ctx, uint64_t *keys, uint64_t n, bool keys_owned, int digit_lo = 0,
-                           int digit_hi = 8) {
+                           int digit_hi = 8, uint32_t known_digits = 0) {
     if (n < 2) {
         if (keys_owned || n == 0) return keys;
         uint64_t *c = static_cast<uint64_t *>(ctx->alloc(n * sizeof(uint64_t)));
@@ -323,11 +323,11 @@ static uint64_t *sort_keys(Ctx *ctx, uint64_t *keys, uint64_t n, bool keys_owned
         uint64_t *a = keys, *b = static_cast<uint64_t *>(ctx->alloc(n * sizeof(uint64_t)));
         uint32_t *v0 = nullptr, *v1 = nullptr;
         if (keys_owned) {
-            radix_sort_u64(ctx, &a, &b, &v0, &v1, n, digit_lo, digit_hi);
+            radix_sort_u64(ctx, &a, &b, &v0, &v1, n, digit_lo, digit_hi, nullptr, known_digits);
         } else {
             // the first pass reads the caller's keys; both ping-pong buffers are ours
             a = static_cast<uint64_t *>(ctx->alloc(n * sizeof(uint64_t)));
-            radix_sort_u64(ctx, &a, &b, &v0, &v1, n, digit_lo, digit_hi, keys);
+            radix_sort_u64(ctx, &a, &b, &v0, &v1, n, digit_lo, digit_hi, keys, known_digits);
         }
         ctx->free(b);
         return a;
@@ -345,7 +345,7 @@ static uint64_t *sort_keys(Ctx *ctx, uint64_t *keys, uint64_t n, bool keys_owned
         uint64_t len = std::min(CHUNK, n - s);
         uint64_t *ka = a + s, *kb = b + s;
         uint32_t *v0 = nullptr, *v1 = nullptr;
-        radix_sort_u64(ctx, &ka, &kb, &v0, &v1, len);
+        radix_sort_u64(ctx, &ka, &kb, &v0, &v1, len, 0, 8, nullptr, known_digits);
         if (ka != a + s) copy_d2d(ctx, a + s, ka, len);
         runs.push_back({s, len});
     }
@@ -620,7 +620,8 @@ static void build_join_index(Ctx *ctx, const uint64_t *keys, uint64_t n, uint32_
 }
 
 // Join step of a rule body with bounded memory.  A probe output of at most
-// kChunkRows rows is emitted whole (a bag).  A larger one is emitted in tile
+// kChunkRows rows (default 2^30 - 1: 8 GiB of packed rows, one radix sort
+// call) is emitted whole (a bag).  A larger one is emitted in tile
 // ranges of at most kChunkRows rows; each range is sorted and deduplicated and
 // merged into the result, which is then a sorted set.  Rule bodies only feed
 // set operations (union, diff), so either form gives the same fixpoint, and
@@ -633,19 +634,15 @@ static uint64_t join_chunk_rows() {
         unsigned long long v = strtoull(e, nullptr, 10);
         if (v > 0) return v;
     }
-    return 1ull << 28;
+    return (1ull << 30) - 1;
 }
-static uint64_t join_step(Ctx *ctx, const uint64_t *probe, uint64_t n, int pcol, const JoinIndex &J, const int oc[4],
-                          uint64_t **out, uint64_t max_rows = 0) {
+// The emit side of a join step whose count pass has run (job.total known).
+// digits: the sort's known varying digits (0: from the histograms).
+static uint64_t join_emit(Ctx *ctx, ProbeJob &job, const int oc[4], uint64_t **out, uint64_t max_rows,
+                          uint32_t digits) {
     const uint64_t kChunkRows = join_chunk_rows();
-    ProbeJob job;
-    job.probe = probe;
-    job.n = n;
-    job.pcol = pcol;
-    job.ix = &J.ix;
-    job.payload = J.payload.p;
+    const uint64_t total = job.total;
     *out = nullptr;
-    uint64_t total = probe_prepare(ctx, job);
     if (total == 0) return 0;
     // the bag size is known before anything is materialised (the reference
     // refuses joins above its u32 row limit at the same point, relational.rs:4550-4555)
@@ -667,7 +664,7 @@ static uint64_t join_step(Ctx *ctx, const uint64_t *probe, uint64_t n, int pcol,
         if (m) {
             uint64_t *b = static_cast<uint64_t *>(ctx->alloc(m * sizeof(uint64_t)));
             probe_emit_range(ctx, job, t0, t1, m, 2, oc, b, nullptr);
-            uint64_t *s = sort_keys(ctx, b, m, true);  // consumes b
+            uint64_t *s = sort_keys(ctx, b, m, true, 0, 8, digits);  // consumes b
             uint64_t *u;
             uint64_t un = unique_keys(ctx, s, m, &u);
             ctx->free(s);
@@ -690,6 +687,18 @@ static uint64_t join_step(Ctx *ctx, const uint64_t *probe, uint64_t n, int pcol,
     }
     *out = acc;
     return acc_n;
+}
+static uint64_t join_step(Ctx *ctx, const uint64_t *probe, uint64_t n, int pcol, const JoinIndex &J, const int oc[4],
+                          uint64_t **out, uint64_t max_rows = 0, uint32_t digits = 0) {
+    ProbeJob job;
+    job.probe = probe;
+    job.n = n;
+    job.pcol = pcol;
+    job.ix = &J.ix;
+    job.payload = J.payload.p;
+    *out = nullptr;
+    if (probe_prepare(ctx, job) == 0) return 0;
+    return join_emit(ctx, job, oc, out, max_rows, digits);
 }
 
 // value-index of a relation column for the probe side: arity 1 stores c0 in
@@ -1086,6 +1095,67 @@ static xlog_hip_rel *op_fj_delta(Ctx *ctx, const xlog_hip_rel *delta, const xlog
     return rel_adopt(ctx, 2, n, o, nullptr, REL_CANONICAL);
 }
 
+// One sparse factorized delta step (reference fj_delta_sparse_novel_u32_recorded,
+// crates/xlog-cuda/src/provider/fj_delta_sparse.rs:66-490): the set
+//   { head(carry, value) : delta(carry, key), edge(key, value), head not in full }
+// with no domain bound, over a device hash set filled with `full`.  The
+// table is sized 2 x (|full| + candidates), the candidate count coming from
+// the probe's count pass (an upper bound of the distinct candidates, which the
+// reference estimates with a bitmap).  A table above max_table_bytes (when
+// non-zero) declines, like the reference's Ok(None): *declined is set and no
+// relation is returned.  The output is canonical in full's column order.
+static xlog_hip_rel *op_fj_delta_sparse(Ctx *ctx, const xlog_hip_rel *delta, const xlog_hip_rel *edge,
+                                        const xlog_hip_rel *full, const xlog_hip_fj_delta_cols &c,
+                                        uint64_t max_table_bytes, bool *declined) {
+    *declined = false;
+    XH_REQUIRE(delta && edge && full, XLOG_HIP_INVALID_ARG, "fj delta sparse: input is NULL");
+    XH_REQUIRE(delta->arity == 2 && edge->arity == 2 && full->arity == 2, XLOG_HIP_INVALID_ARG,
+               "fj delta sparse: delta, edge and full must be arity-2");
+    auto roles_ok = [](uint32_t a, uint32_t b) { return a < 2 && b < 2 && a != b; };
+    XH_REQUIRE(roles_ok(c.delta_carry, c.delta_key) && roles_ok(c.r_carry, c.r_value), XLOG_HIP_INVALID_ARG,
+               "fj delta sparse: invalid column roles (arity-2 indices, pairwise distinct)");
+    auto empty = [&]() {
+        xlog_hip_rel *e = rel_new(ctx, 2, 0);
+        e->flags = REL_CANONICAL;
+        return e;
+    };
+    if (delta->rows == 0 || edge->rows == 0) return empty();
+    Canon ce;  // edge as sorted unique (key << 32) | value: runs of values per key
+    canonical_keys(ctx, edge, ce);
+    JoinIndex J;
+    build_join_index(ctx, ce.k, ce.n, 2, 0, true, J);
+    ProbeJob job;  // count pass only: the number of candidate tuples
+    job.probe = delta->w[0];
+    job.n = delta->rows;
+    job.pcol = c.delta_key == 0 ? 0 : 1;
+    job.ix = &J.ix;
+    job.payload = J.payload.p;
+    job.record_lookups = false;
+    const uint64_t cand = probe_prepare(ctx, job);
+    if (cand == 0) return empty();
+    uint64_t slots = 1ull << 16;
+    while (slots < 2 * (full->rows + cand)) slots <<= 1;
+    if (max_table_bytes && slots * sizeof(uint64_t) > max_table_bytes) {
+        *declined = true;
+        return nullptr;
+    }
+    HashSet h;
+    hs_init(ctx, h, slots);
+    hs_insert_all(ctx, h, full->w[0], full->rows);
+    h.size = full->rows;
+    // the novel tuples number at most `cand`, so a limit of cand + 1 is never reached
+    Buf<uint64_t> novel(ctx, cand + 1 + HS_APPEND_SLACK);
+    hs_join_insert(ctx, h, delta->w[0], delta->rows, c.delta_key == 0 ? 1 : 0, c.r_carry == 0 ? 1 : 0, J.ix,
+                   J.payload.p, novel.p, cand + 1);
+    ctx->read_scalars(h.flags.p + 1, 2);
+    XH_REQUIRE(ctx->host_scalars[0] == 0, XLOG_HIP_DEVICE_ERROR, "fj delta sparse: table overflow");
+    const uint64_t n = ctx->host_scalars[1];
+    if (n == 0) return empty();
+    h = HashSet();
+    uint64_t *s = sort_keys(ctx, novel.p, n, false);
+    return rel_adopt(ctx, 2, n, s, nullptr, REL_CANONICAL);
+}
+
 // Set of the projected join, canonical: dedup_full_row(project(join(l, r))).
 // When the output is (left column, right non-key column) the join is emitted
 // already ordered: the probe side is first sorted by its output column (key
@@ -1260,6 +1330,7 @@ struct Driver {
     std::vector<DRel> full, delta;
     uint64_t version_counter = 1;
     uint64_t max_join_rows = 0;  // 0: no limit on a body join's bag size
+    uint32_t digits = 0;         // varying digits of packed tuples over the value domain (0: from the histograms)
     // join-index cache keyed by (relation buffer, column, version)
     struct CacheKey {
         const uint64_t *k; int col; uint64_t version;
@@ -1292,7 +1363,8 @@ struct Driver {
 
     // Evaluate a rule body; rel[j] is the relation atom j reads.  Appends the
     // head tuples (bag, packed) to `out` as owned device buffers.
-    void eval_body(const Rule &r, const DRel *const *rel, std::vector<std::pair<uint64_t *, uint64_t>> &out) {
+    void eval_body(const Rule &r, const DRel *const *rel, std::vector<std::pair<uint64_t *, uint64_t>> &out,
+                   ProbeJob *pre) {
         const Atom &a0 = r.b[0];
         XH_REQUIRE(a0.v[0] != a0.v[1], XLOG_HIP_UNSUPPORTED, "plan: repeated variable inside an atom");
         bool k0 = needed_later(r, 1, a0.v[0]), k1 = needed_later(r, 1, a0.v[1]);
@@ -1359,9 +1431,13 @@ struct Driver {
             uint64_t *o = nullptr;
             uint64_t on = 0;
             if (ar.n != 0) {
-                const JoinIndex &J = index_of(ar, apos);
                 int oc[4] = {sel[0], sel[1], 0, 0};
-                on = join_step(ctx, bk, bn, bpos, J, oc, &o, max_join_rows);
+                if (j == 1 && pre) {  // the count pass ran with the delta's count still on the device
+                    on = join_emit(ctx, *pre, oc, &o, max_join_rows, digits);
+                } else {
+                    const JoinIndex &J = index_of(ar, apos);
+                    on = join_step(ctx, bk, bn, bpos, J, oc, &o, max_join_rows, digits);
+                }
             }
             if (owned) ctx->free(owned);
             owned = o;
@@ -1377,8 +1453,10 @@ struct Driver {
         out.push_back({owned, bn});
     }
 
-    // concat bags, sort, unique, minus full -> new canonical delta
-    DRel finalize(std::vector<std::pair<uint64_t *, uint64_t>> &bags, const DRel &against) {
+    // concat bags, sort, unique, minus full -> new canonical delta.  The count
+    // stays on the device (cnt); d.n is the candidate total, a bound on it,
+    // until the caller reads the count back.
+    DRel finalize_async(std::vector<std::pair<uint64_t *, uint64_t>> &bags, const DRel &against, Buf<uint64_t> &cnt) {
         uint64_t total = 0;
         for (auto &b : bags) total += b.second;
         DRel d;
@@ -1400,15 +1478,21 @@ struct Driver {
             }
         }
         bags.clear();
-        uint64_t *s = sort_keys(ctx, cat, total, true);  // consumes cat
+        uint64_t *s = sort_keys(ctx, cat, total, true, 0, 8, digits);  // consumes cat
         uint64_t *o = static_cast<uint64_t *>(ctx->alloc(total * sizeof(uint64_t)));
-        Buf<uint64_t> cnt(ctx, 1);
+        cnt = Buf<uint64_t>(ctx, 1);
         select_unique_diff(ctx, s, total, against.k, against.n, o, cnt.p);
         ctx->free(s);
-        d.n = read_count(ctx, cnt.p);
+        d.n = total;
         d.k = o;
         d.owned = true;
         d.version = version_counter++;
+        return d;
+    }
+    DRel finalize(std::vector<std::pair<uint64_t *, uint64_t>> &bags, const DRel &against) {
+        Buf<uint64_t> cnt;
+        DRel d = finalize_async(bags, against, cnt);
+        if (d.k) d.n = read_count(ctx, cnt.p);
         return d;
     }
 
@@ -1428,13 +1512,31 @@ struct Driver {
         r = DRel();
     }
 
+    // The first join of a variant whose delta atom comes first and whose other
+    // atoms are all EDB (their indexes never change): its count pass can run
+    // as soon as the delta exists on the device, before its size is known, so
+    // the iteration needs one read-back (delta sizes and these totals together).
+    bool precountable(const Rule &r, int occ, int *bpos, int *apos) const {
+        if (occ != 0 || r.nb < 2 || !idb[r.b[0].pred]) return false;
+        for (int j = 1; j < r.nb; ++j)
+            if (idb[r.b[j].pred]) return false;
+        const Atom &a0 = r.b[0], &a1 = r.b[1];
+        if (a0.v[0] == a0.v[1] || a1.v[0] == a1.v[1]) return false;
+        if (!needed_later(r, 1, a0.v[0]) || !needed_later(r, 1, a0.v[1])) return false;
+        int ns = 0;
+        for (int x = 0; x < 2; ++x)
+            for (int y = 0; y < 2; ++y)
+                if (a0.v[x] == a1.v[y]) { *bpos = x; *apos = y; ++ns; }
+        return ns == 1;
+    }
+
     uint64_t run(uint64_t max_iter, std::vector<uint64_t> &deltas) {
         // seed: every rule once against the current store
         std::vector<std::vector<std::pair<uint64_t *, uint64_t>>> derived(n_preds);
         for (const Rule &r : rules) {
             const DRel *rel[MAX_BODY];
             for (int j = 0; j < r.nb; ++j) rel[j] = &full[r.b[j].pred];
-            eval_body(r, rel, derived[r.head]);
+            eval_body(r, rel, derived[r.head], nullptr);
         }
         uint64_t seed = 0;
         for (uint32_t p = 0; p < n_preds; ++p) {
@@ -1449,11 +1551,14 @@ struct Driver {
             seed += d.n;
         }
         deltas.push_back(seed);
+        // count jobs of the next iteration's pre-countable first joins, by (rule, occurrence)
+        std::map<std::pair<int, int>, std::unique_ptr<ProbeJob>> pre;
         uint64_t it = 0;
         while (it < max_iter) {
             ++it;
             std::vector<std::vector<std::pair<uint64_t *, uint64_t>>> raw(n_preds);
-            for (const Rule &r : rules) {
+            for (size_t ri = 0; ri < rules.size(); ++ri) {
+                const Rule &r = rules[ri];
                 for (int occ = 0; occ < r.nb; ++occ) {
                     int p = r.b[occ].pred;
                     if (!idb[p] || delta[p].n == 0) continue;
@@ -1462,16 +1567,56 @@ struct Driver {
                         int q = r.b[j].pred;
                         rel[j] = (j == occ) ? &delta[q] : &full[q];
                     }
-                    eval_body(r, rel, raw[r.head]);
+                    auto pj = pre.find({(int)ri, occ});
+                    eval_body(r, rel, raw[r.head], pj != pre.end() ? pj->second.get() : nullptr);
                 }
             }
-            uint64_t total = 0;
+            pre.clear();
+            // the new deltas, their counts on the device
+            std::vector<Buf<uint64_t>> cnt(n_preds);
             for (uint32_t p = 0; p < n_preds; ++p) {
                 if (!idb[p]) continue;
-                DRel d = finalize(raw[p], full[p]);
+                DRel d = finalize_async(raw[p], full[p], cnt[p]);
                 release(delta[p]);
                 delta[p] = d;
-                total += d.n;
+            }
+            // count passes of the next iteration's pre-countable first joins
+            for (size_t ri = 0; ri < rules.size(); ++ri) {
+                const Rule &r = rules[ri];
+                int bpos = 0, apos = 0;
+                if (!precountable(r, 0, &bpos, &apos)) continue;
+                const DRel &d = delta[r.b[0].pred];
+                if (!d.k || full[r.b[1].pred].n == 0) continue;
+                const JoinIndex &J = index_of(full[r.b[1].pred], apos);
+                std::unique_ptr<ProbeJob> job(new ProbeJob());
+                job->probe = d.k;
+                job->pcol = bpos;
+                job->ix = &J.ix;
+                job->payload = J.payload.p;
+                probe_prepare_deferred(ctx, *job, d.n, cnt[r.b[0].pred].p);
+                pre[{(int)ri, 0}] = std::move(job);
+            }
+            // one read-back: every delta size and every pre-counted total
+            std::vector<const uint64_t *> src;
+            for (uint32_t p = 0; p < n_preds; ++p)
+                if (idb[p] && delta[p].k) src.push_back(cnt[p].p);
+            for (auto &kv : pre) src.push_back(kv.second->toff.p + kv.second->tiles);
+            if (!src.empty()) {
+                XH_REQUIRE(src.size() <= Ctx::HOST_STAGE_U64, XLOG_HIP_UNSUPPORTED, "fixpoint: too many predicates");
+                Buf<uint64_t> gather(ctx, src.size());
+                for (size_t q = 0; q < src.size(); ++q) copy_d2d(ctx, gather.p + q, src[q], 1);
+                ctx->read_scalars(gather.p, src.size());
+            }
+            size_t q = 0;
+            uint64_t total = 0;
+            for (uint32_t p = 0; p < n_preds; ++p) {
+                if (!idb[p] || !delta[p].k) continue;
+                delta[p].n = ctx->host_scalars[q++];
+                total += delta[p].n;
+            }
+            for (auto &kv : pre) {
+                const int p0 = rules[kv.first.first].b[0].pred;
+                probe_finish(*kv.second, delta[p0].n, ctx->host_scalars[q++]);
             }
             deltas.push_back(total);
             if (total == 0) return it;
@@ -1646,6 +1791,106 @@ static bool run_chain_route(Ctx *ctx, const std::vector<Rule> &rules, uint32_t n
     return true;
 }
 
+// Transitive closure over the device hash set: the persistent-table form of
+// the reference's sparse factorized delta (fj_delta_sparse_novel_u32_recorded,
+// provider/fj_delta_sparse.rs:66) inside the semi-naive loop of
+// recursive.rs:447-957.  R is the set.  The seed is R = delta_0 = edge; every
+// iteration is one fused pass (expand delta (x, y) through the edges of y,
+// insert (x, z), append the inserted tuples as the next delta) and one
+// read-back of the appended count and the overflow flag.  The iteration count
+// includes the final empty iteration; R is sorted once at the end.
+// XLOG_HIP_HASH_SLOTS / XLOG_HIP_HASH_APPENDS override the initial table size
+// and the appends allowed per attempt (tests force the grow-and-rerun path).
+static uint64_t env_u64(const char *name, uint64_t dflt) {
+    const char *e = getenv(name);
+    if (e && *e) {
+        const unsigned long long v = strtoull(e, nullptr, 10);
+        if (v > 0) return v;
+    }
+    return dflt;
+}
+static void tc_fixpoint_hash(Ctx *ctx, const DRel &edges, uint64_t max_iter, uint64_t **res, uint64_t *res_n,
+                             uint64_t *iterations, std::vector<uint64_t> &deltas) {
+    *res = nullptr;
+    *res_n = 0;
+    deltas.push_back(edges.n);
+    uint64_t it = 0;
+    if (edges.n == 0) {  // the seed and the one empty iteration
+        deltas.push_back(0);
+        *iterations = 1;
+        return;
+    }
+    JoinIndex J;  // edges by source: runs of targets
+    build_join_index(ctx, edges.k, edges.n, 2, 0, true, J);
+    const uint64_t avg_deg = std::max<uint64_t>(1, (edges.n + J.ix.nruns - 1) / std::max<uint64_t>(1, J.ix.nruns));
+    HashSet h;
+    hs_init(ctx, h, env_u64("XLOG_HIP_HASH_SLOTS", std::max<uint64_t>(4 * edges.n, 1ull << 16)));
+    if (h.cap / 2 < edges.n) hs_grow(ctx, h, 4 * edges.n);
+    hs_insert_all(ctx, h, edges.k, edges.n);
+    h.size = edges.n;
+    const uint64_t min_want = env_u64("XLOG_HIP_HASH_APPENDS", 1ull << 20);
+    const uint64_t *cur = edges.k;
+    uint64_t ncur = edges.n;
+    Buf<uint64_t> bufs[2];
+    int nb = 0;
+    for (;;) {
+        XH_REQUIRE(it < max_iter, XLOG_HIP_ITERATION_LIMIT,
+                   "Recursive SCC iteration limit (" + std::to_string(max_iter) + ") exceeded");
+        ++it;
+        Buf<uint64_t> &out = bufs[nb];
+        fill_u64(ctx, h.flags.p + 1, 0ull, 2);  // overflow, appended count
+        // appends allowed per attempt: the expected candidate count (a bound on the novel ones)
+        uint64_t want = std::max<uint64_t>(min_want, ncur * avg_deg + ncur / 4);
+        if (min_want < (1ull << 20)) want = min_want;                          // forced small (tests)
+        uint64_t appended = 0;
+        for (;;) {
+            uint64_t room = h.cap / 2 > h.size + appended ? h.cap / 2 - h.size - appended : 0;
+            if (room < want) {
+                // 4x what this step needs: R keeps growing, and every rehash re-inserts all of it
+                hs_grow(ctx, h, 4 * (h.size + appended + want));
+                room = h.cap / 2 - h.size - appended;
+            }
+            const uint64_t limit = appended + std::min(want, room);
+            if (out.n < limit + HS_APPEND_SLACK) {  // keep the tuples appended by an earlier attempt
+                Buf<uint64_t> bigger(ctx, limit + HS_APPEND_SLACK);
+                if (appended) copy_d2d(ctx, bigger.p, out.p, appended);
+                out = std::move(bigger);
+            }
+            hs_join_insert(ctx, h, cur, ncur, 0, 1, J.ix, J.payload.p, out.p, limit);
+            ctx->read_scalars(h.flags.p + 1, 2);
+            const uint64_t overflow = ctx->host_scalars[0];
+            appended = ctx->host_scalars[1];
+            if (!overflow) break;
+            // the limit or a full table stopped the pass: grow and run it again; the tuples it inserted
+            // are found present and are not appended twice
+            fill_u64(ctx, h.flags.p + 1, 0ull, 1);
+            want *= 4;
+        }
+        h.size += appended;
+        deltas.push_back(appended);
+        if (appended == 0) break;
+        cur = out.p;
+        ncur = appended;
+        nb ^= 1;
+    }
+    *iterations = it;
+    bufs[0] = Buf<uint64_t>();
+    bufs[1] = Buf<uint64_t>();
+    uint64_t *all = static_cast<uint64_t *>(ctx->alloc(h.size * sizeof(uint64_t)));
+    uint64_t got = 0;
+    try {
+        got = hs_collect(ctx, h, all);
+        XH_REQUIRE(got == h.size, XLOG_HIP_DEVICE_ERROR,
+                   "hash set holds " + std::to_string(got) + " tuples, expected " + std::to_string(h.size));
+        h = HashSet();
+    } catch (...) {
+        ctx->free(all);
+        throw;
+    }
+    *res = sort_keys(ctx, all, got, true);  // consumes all
+    *res_n = got;
+}
+
 static void run_fixpoint_impl(Ctx *ctx, const int32_t *plan, uint32_t n_preds, const xlog_hip_rel *const *rels,
                               xlog_hip_rel **out, xlog_hip_fixpoint_stats *stats, std::vector<uint64_t> &deltas) {
     XH_REQUIRE(n_preds >= 1 && n_preds <= 256, XLOG_HIP_INVALID_ARG, "n_preds must be 1..256");
@@ -1665,7 +1910,9 @@ static void run_fixpoint_impl(Ctx *ctx, const int32_t *plan, uint32_t n_preds, c
         for (const Rule &r : rules) if (r.nb == 1) { E = r.b[0].pred; H = r.head; }
     }
     bool head_empty = tc && (!rels[H] || rels[H]->rows == 0);
-    uint32_t nv = 0;
+    XH_REQUIRE(route != XLOG_HIP_ROUTE_HASH || (tc && head_empty), XLOG_HIP_UNSUPPORTED,
+               "hash route needs the transitive-closure plan with an empty head");
+    uint64_t nv = 0;  // max id + 1 (up to 2^32)
     DRel edges;
     if (tc && head_empty && route != XLOG_HIP_ROUTE_JOIN) {
         edges = canon_drel(ctx, rels[E]);
@@ -1675,11 +1922,27 @@ static void run_fixpoint_impl(Ctx *ctx, const int32_t *plan, uint32_t n_preds, c
             LAUNCH_1D(k_max_u32_of_packed, edges.n, edges.k, edges.n, mx.p);
             XH_CHECK_HIP(hipMemcpyAsync(ctx->host_scalars, mx.p, sizeof(unsigned int), hipMemcpyDeviceToHost, ctx->stream));
             ctx->sync();
-            nv = *reinterpret_cast<uint32_t *>(ctx->host_scalars) + 1;
+            nv = (uint64_t)*reinterpret_cast<uint32_t *>(ctx->host_scalars) + 1;
         }
     }
-    bool bitmap = tc && head_empty && route != XLOG_HIP_ROUTE_JOIN && (uint64_t)nv <= (1ull << 17);
-    if (bitmap) {
+    const bool bitmap = tc && head_empty && route != XLOG_HIP_ROUTE_JOIN && route != XLOG_HIP_ROUTE_HASH &&
+                        nv <= (1ull << 17);
+    // above the dense domain (or when asked for) the closure runs over the device hash set
+    const bool hashset = tc && head_empty && !bitmap &&
+                         (route == XLOG_HIP_ROUTE_HASH || (route == XLOG_HIP_ROUTE_AUTO && nv > (1ull << 17)));
+    if (hashset) {
+        uint64_t *res = nullptr, n = 0;
+        try {
+            tc_fixpoint_hash(ctx, edges, max_iter, &res, &n, &iterations, deltas);
+        } catch (...) {
+            if (edges.owned) ctx->free(edges.k);
+            throw;
+        }
+        if (edges.owned) ctx->free(edges.k);
+        out[H] = n ? rel_adopt(ctx, 2, n, res, nullptr, REL_CANONICAL) : rel_new(ctx, 2, 0);
+        out[H]->flags = REL_CANONICAL;
+        if (stats) stats->route = XLOG_HIP_ROUTE_HASH;
+    } else if (bitmap) {
         // With the head empty, Δ of iteration k is the set of pairs at shortest distance k + 1 whether the
         // step is Δ ∘ edge (the plan as written) or edge ∘ Δ: a shortest path of length k + 2 splits off its
         // last edge or its first edge, and every other derivation lies in R.  So the left-linear chain
@@ -1701,7 +1964,8 @@ static void run_fixpoint_impl(Ctx *ctx, const int32_t *plan, uint32_t n_preds, c
                 keys[E] = edges.k;
                 rows[E] = edges.n;
                 std::vector<uint64_t *> r;
-                chain_fixpoint(ctx, chains, n_preds, idb, keys, rows, nv, max_iter, r, res_n, &iterations, deltas);
+                chain_fixpoint(ctx, chains, n_preds, idb, keys, rows, (uint32_t)nv, max_iter, r, res_n, &iterations,
+                               deltas);
                 res = r[H];
                 n = res_n[H];
             }
@@ -1725,6 +1989,19 @@ static void run_fixpoint_impl(Ctx *ctx, const int32_t *plan, uint32_t n_preds, c
         for (uint32_t p = 0; p < n_preds; ++p) {
             drv.full[p] = canon_drel(ctx, rels[p]);
             drv.full[p].version = drv.version_counter++;
+        }
+        {
+            // Every derived value comes from the inputs, so the largest input id bounds the digits a packed
+            // tuple can vary in: sorts inside the loop run those passes without reading histograms back.
+            Buf<unsigned int> mx(ctx, 1);
+            fill_u32(ctx, mx.p, 0u, 1);
+            for (uint32_t p = 0; p < n_preds; ++p)
+                if (drv.full[p].n) LAUNCH_1D(k_max_u32_of_packed, drv.full[p].n, drv.full[p].k, drv.full[p].n, mx.p);
+            ctx->read_scalars(mx.p, 1);
+            const uint32_t maxid = (uint32_t)ctx->host_scalars[0];
+            const int bits = maxid ? 32 - __builtin_clz(maxid) : 0;
+            const uint32_t nd = (uint32_t)(bits + 7) / 8;  // bytes per column
+            drv.digits = nd ? (((1u << nd) - 1u) | (((1u << nd) - 1u) << 4)) : 1u;
         }
         try {
             iterations = drv.run(max_iter, deltas);
@@ -2319,6 +2596,21 @@ xlog_hip_status xlog_hip_fj_delta_novel(xlog_hip_ctx *ctx, const xlog_hip_rel *d
         OUT_GUARD;
         XH_REQUIRE(cols, XLOG_HIP_INVALID_ARG, "column roles are NULL");
         *out = op_fj_delta(c, delta, edge, full, *cols, domain);
+    });
+}
+xlog_hip_status xlog_hip_fj_delta_sparse_novel(xlog_hip_ctx *ctx, const xlog_hip_rel *delta, const xlog_hip_rel *edge,
+                                               const xlog_hip_rel *full, const xlog_hip_fj_delta_cols *cols,
+                                               uint64_t max_table_bytes, xlog_hip_rel **out) {
+    return guarded([&] {
+        Ctx *c = C(ctx);
+        OUT_GUARD;
+        XH_REQUIRE(cols, XLOG_HIP_INVALID_ARG, "cols is NULL");
+        need_rel(delta, "delta");
+        need_rel(edge, "edge");
+        need_rel(full, "full");
+        bool declined = false;
+        xlog_hip_rel *r = op_fj_delta_sparse(c, delta, edge, full, *cols, max_table_bytes, &declined);
+        *out = declined ? nullptr : r;
     });
 }
 xlog_hip_status xlog_hip_sort_merge_join(xlog_hip_ctx *ctx, const xlog_hip_rel *left, const xlog_hip_rel *right,

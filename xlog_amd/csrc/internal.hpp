@@ -260,8 +260,13 @@ void rel_free(xlog_hip_rel *r);
 // of digit passes executed.
 // With `src` (keys only) the first pass reads src and both buffers are
 // scratch, so an input that must not be modified is never copied first.
+// With known_digits (a bitmask of digits that may vary, e.g. from the value
+// domain) the passes are exactly those digits of [digit_lo, digit_hi) and the
+// histograms are not read back (a known digit that turns out constant costs a
+// stable copy).
 int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **vals, uint32_t **vals_alt,
-                   uint64_t n, int digit_lo = 0, int digit_hi = 8, const uint64_t *src = nullptr);
+                   uint64_t n, int digit_lo = 0, int digit_hi = 8, const uint64_t *src = nullptr,
+                   uint32_t known_digits = 0);
 
 // Stream compaction family (single pass, decoupled look-back).  Each writes
 // the selected keys in input order to `out` and the count to *d_count
@@ -274,6 +279,8 @@ void select_unique_diff(Ctx *ctx, const uint64_t *k, uint64_t n, const uint64_t 
                         uint64_t *out, uint64_t *d_count);
 void select_flags(Ctx *ctx, const uint64_t *k, const uint8_t *flags, uint64_t n, uint64_t *out,
                   uint64_t *d_count);
+//   not_value:   keep k[i] if k[i] != v
+void select_not_value(Ctx *ctx, const uint64_t *k, uint64_t n, uint64_t v, uint64_t *out, uint64_t *d_count);
 
 // In-place exclusive scan of u32 values (prefixes wrap modulo 2^32); the
 // exact u64 sum goes to *d_total (device).  One pass, decoupled look-back.
@@ -342,10 +349,46 @@ struct ProbeJob {
     int items = 16;      // probe rows per thread (set by probe_prepare); a tile is 256 * items rows
 };
 uint64_t probe_prepare(Ctx *ctx, ProbeJob &job);
+// The count pass for a probe whose row count is on the device (*d_n <= n_bound),
+// with no read-back; the total lands at job.toff.p[job.tiles].  probe_finish
+// completes the job once the host has read the row count and the total.
+void probe_prepare_deferred(Ctx *ctx, ProbeJob &job, uint64_t n_bound, const uint64_t *d_n);
+void probe_finish(ProbeJob &job, uint64_t n, uint64_t total);
 std::vector<uint64_t> probe_tile_offsets(Ctx *ctx, const ProbeJob &job);
 // writes the `rows` outputs of tiles [t0, t1) to out0 / out1 starting at index 0
 void probe_emit_range(Ctx *ctx, const ProbeJob &job, uint64_t t0, uint64_t t1, uint64_t rows, int out_arity,
                       const int oc[4], uint64_t *out0, uint64_t *out1);
+
+// Device hash set of packed u64 tuples (hash_set.hip): open addressing,
+// linear probing, the all-ones key kept as a flag.  flags[0] = all-ones key
+// present, flags[1] = overflow of the last insert pass, flags[2] = tuples
+// appended by the last novel-insert pass (the host zeroes [1] and [2]).
+struct HashSet {
+    Buf<uint64_t> slots;
+    Buf<uint64_t> flags;
+    uint64_t cap = 0;   // slots, a power of two
+    int bits = 0;
+    uint64_t size = 0;  // tuples held (host bookkeeping)
+};
+void hs_init(Ctx *ctx, HashSet &h, uint64_t min_cap);
+// inserts keys without novelty bookkeeping (flags[1] set on a full table)
+void hs_insert_all(Ctx *ctx, HashSet &h, const uint64_t *keys, uint64_t n);
+// rehash into a table of at least min_cap slots
+void hs_grow(Ctx *ctx, HashSet &h, uint64_t min_cap);
+// One sparse factorized delta step: for every delta row (carry, key) and
+// every run entry of key in the index (values in payload), insert
+// head(carry, value) (carry in the high word when out_carry_hi); the inserted
+// tuples are appended to out at flags[2].  Once the appended count reaches
+// `limit` (or the table is full) flags[1] is set and the pass stops early; out
+// needs limit + HS_APPEND_SLACK entries.
+void hs_join_insert(Ctx *ctx, HashSet &h, const uint64_t *delta, uint64_t n, int key_hi, int out_carry_hi,
+                    const RunIndex &ix, const uint32_t *payload, uint64_t *out, uint64_t limit);
+// inserts keys[0..n) and appends the novel ones (same protocol)
+void hs_insert_novel(Ctx *ctx, HashSet &h, const uint64_t *keys, uint64_t n, uint64_t *out, uint64_t limit);
+// every tuple of the set, unordered, into out (h.size entries); returns the count
+uint64_t hs_collect(Ctx *ctx, const HashSet &h, uint64_t *out);
+// appends past `limit`: one 64-tuple chunk per wave of the insert grid
+constexpr uint64_t HS_APPEND_SLACK = 1ull << 21;
 
 // Nested-loop inner join of packed arity-1/2 relations on one key column,
 // output (left columns ++ right columns) in left-row-major, right-row order.

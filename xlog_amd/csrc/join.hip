@@ -122,6 +122,9 @@ struct ProbeArgs {
     // pre_start / pre_cnt)
     uint64_t *rec_start;
     uint32_t *rec_cnt;
+    // optional device-side row count (deferred count pass): when set, it
+    // replaces n, which is then only the bound the grid was sized for
+    const uint64_t *d_n;
 };
 // set in a row's start when its outputs come from gsrc
 constexpr uint64_t GROUP_BIT = 1ull << 63;
@@ -185,6 +188,7 @@ __device__ __forceinline__ void lookup_batch(const ProbeArgs &a, const uint64_t 
 template <int ITEMS>
 __global__ __launch_bounds__(JB) void k_probe_count(ProbeArgs a, uint64_t *__restrict__ tile_cnt) {
     __shared__ uint64_t s_part[JWAVES];
+    if (a.d_n) a.n = *a.d_n;  // tiles past the real rows count zero
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
     const uint64_t wbase = (uint64_t)blockIdx.x * tile_rows(ITEMS) + (uint64_t)wave * (ITEMS * WAVE);
     uint64_t rows[ITEMS];
@@ -554,6 +558,49 @@ uint64_t probe_prepare(Ctx *ctx, ProbeJob &job) {
         job.pre_cnt = job.rec_cnt.p;
     }
     return job.total;
+}
+
+// The count pass and the tile scan for a probe whose row count is still on
+// the device (*d_n <= n_bound): the grid, the tile offsets and the recorded
+// lookups are sized for n_bound; nothing is read back.  probe_finish then
+// takes the row count and the total (read back by the caller together with
+// whatever else it needs: d_total() points at the total).
+void probe_prepare_deferred(Ctx *ctx, ProbeJob &job, uint64_t n_bound, const uint64_t *d_n) {
+    job.items = JITEMS;
+    job.n = n_bound;
+    job.tiles = (n_bound + tile_rows(job.items) - 1) / tile_rows(job.items);
+    job.total = 0;
+    XH_REQUIRE(job.tiles < (1ull << 31), XLOG_HIP_CAPACITY_OVERFLOW, "join probe: input too large");
+    job.toff = Buf<uint64_t>(ctx, job.tiles + 1);
+    if (n_bound == 0 || job.ix->nruns == 0) {
+        fill_u64(ctx, job.toff.p, 0ull, job.tiles + 1);
+        return;
+    }
+    ProbeArgs a = probe_args(job);
+    a.d_n = d_n;
+    XH_REQUIRE(!job.pre_cnt && job.record_lookups, XLOG_HIP_INVALID_ARG, "deferred probe: recorded lookups only");
+    job.rec_start = Buf<uint64_t>(ctx, n_bound);
+    job.rec_cnt = Buf<uint32_t>(ctx, n_bound);
+    a.rec_start = job.rec_start.p;
+    a.rec_cnt = job.rec_cnt.p;
+    {
+        Prof prof(ctx, XLOG_HIP_KERNEL_PROBE_COUNT, 36.0 * (double)n_bound);
+        hipLaunchKernelGGL(k_probe_count<JITEMS>, dim3((unsigned)job.tiles), dim3(JB), 0, ctx->stream, a,
+                           job.toff.p);
+        XH_CHECK_HIP(hipGetLastError());
+    }
+    hipLaunchKernelGGL(k_scan_small, dim3(1), dim3(1024), 0, ctx->stream, job.toff.p, job.tiles,
+                       job.toff.p + job.tiles);
+    XH_CHECK_HIP(hipGetLastError());
+}
+void probe_finish(ProbeJob &job, uint64_t n, uint64_t total) {
+    job.n = n;
+    job.tiles = (n + tile_rows(job.items) - 1) / tile_rows(job.items);
+    job.total = total;
+    if (job.rec_cnt.p) {
+        job.pre_start = job.rec_start.p;
+        job.pre_cnt = job.rec_cnt.p;
+    }
 }
 
 std::vector<uint64_t> probe_tile_offsets(Ctx *ctx, const ProbeJob &job) {

@@ -304,6 +304,16 @@ struct SelDiff {
     __device__ void emit(uint64_t pos, uint64_t, uint64_t key) const { out[pos] = key; }
 };
 
+// keys different from one value (the occupied slots of a hash table)
+struct SelNotValue {
+    uint64_t v;
+    uint64_t *out;
+    static constexpr bool kWindow = false;
+    __device__ void setup(uint64_t, uint64_t, uint64_t *, int) const {}
+    __device__ bool flag(uint64_t, uint64_t key, uint64_t, const uint64_t *) const { return key != v; }
+    __device__ void emit(uint64_t pos, uint64_t, uint64_t key) const { out[pos] = key; }
+};
+
 struct SelFlags {
     const uint8_t *flags;
     uint64_t *out;
@@ -605,6 +615,9 @@ void select_unique_diff(Ctx *ctx, const uint64_t *k, uint64_t n, const uint64_t 
                         uint64_t *d_count) {
     if (nb == 0) { select_unique(ctx, k, n, out, d_count); return; }
     run_select(ctx, k, n, SelDiff<true>{k, b, nb, out}, d_count);
+}
+void select_not_value(Ctx *ctx, const uint64_t *k, uint64_t n, uint64_t v, uint64_t *out, uint64_t *d_count) {
+    run_select(ctx, k, n, SelNotValue{v, out}, d_count);
 }
 void select_flags(Ctx *ctx, const uint64_t *k, const uint8_t *flags, uint64_t n, uint64_t *out, uint64_t *d_count) {
     run_select(ctx, k, n, SelFlags{flags, out}, d_count);

@@ -174,12 +174,18 @@ __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v, int lane) {
 // one L2.  Workgroups are dispatched in index order, round-robin over the 8
 // XCDs, so tiles go out in chunks of `chunk` consecutive tiles: block b runs
 // tile ((j / chunk) * 8 + b % 8) * chunk + j % chunk with j = b / 8, i.e. chunk
-// k goes to the blocks with b % 8 == k % 8.  Within each group of 8 * chunk
-// blocks this is a permutation, and a tile waits only on tiles of its own or
-// earlier groups; with in-order dispatch and room for at least 8 * chunk blocks
-// at once (the host sizes chunk for that) the look-back always ends.  Measured
-// on MI355X against a ticket-ordered grid: 2^28 keys 1.16 -> 1.07 ms per pass,
-// 2^24 keys 0.087 -> 0.081 ms.
+// k goes to the blocks with b % 8 == k % 8 (one XCD).  Within each group of
+// 8 * chunk blocks this is a permutation, and a tile waits only on tiles of
+// its own or earlier groups.  The look-back therefore always ends under two
+// conditions: (1) workgroups start in index order, and (2) the device holds at
+// least 8 * chunk blocks of the pass at once (the host sizes chunk to 1/16 of
+// what it holds).  If either failed, a tile could wait on a tile whose block
+// cannot start, and the pass would never finish.  The ticketed order
+// (XLOG_HIP_SORT_TICKETS=1) numbers blocks by an atomic ticket taken at start
+// instead of their index, which removes condition (1) and keeps (2).  Measured
+// on MI355X: chunked by index 1.07 ms per 2^28-key pass (0.081 ms at 2^24),
+// chunked by ticket 1.21 ms (blocks start in a slightly different order on
+// each XCD, which breaks the chunk-to-XCD placement), plain ticket order 1.16 ms.
 constexpr uint32_t TILE_NONE = 0xFFFFFFFFu;
 
 __device__ __forceinline__ uint32_t chunk_tile(uint32_t b, uint32_t chunk, uint32_t tiles) {
@@ -192,8 +198,10 @@ template <bool HAS_VAL, int BLOCK, int ITEMS>
 __global__ __launch_bounds__(BLOCK) void k_onesweep(
     const uint64_t *__restrict__ kin, uint64_t *__restrict__ kout, const uint32_t *__restrict__ vin,
     uint32_t *__restrict__ vout, uint64_t n, uint32_t tiles, int shift, const uint32_t *__restrict__ digit_off,
-    uint32_t *status, uint32_t *status_next, uint32_t chunk) {
+    uint32_t *status, uint32_t *status_next, uint32_t chunk, unsigned long long *ticket,
+    unsigned long long ticket_base) {
     __shared__ uint32_t s_wcnt[(BLOCK / WAVE)][256];
+    __shared__ uint32_t s_ticket;
     __shared__ uint32_t s_gbase[256];
     __shared__ uint32_t s_wsum[(BLOCK / WAVE)];
     __shared__ uint64_t s_keys[(BLOCK * ITEMS)];
@@ -203,12 +211,17 @@ __global__ __launch_bounds__(BLOCK) void k_onesweep(
     const uint32_t lane_u = (uint32_t)lane;
     const int d = tid;
     const bool digit_thread = tid < 256;
-    // block-uniform, so it (and every per-round bound derived from it) stays
-    // in scalar registers
-    const uint32_t tile = chunk_tile(blockIdx.x, chunk, tiles);
-    if (tile == TILE_NONE) return;
+    // The tile comes from the block index (default: tiles stay on their XCD
+    // under in-order dispatch) or, in the ticketed order, from the block's
+    // start-order ticket, so that a tile only ever waits on tiles of blocks that
+    // started before it or belong to its own group of 8 * chunk tickets,
+    // whatever order the blocks are dispatched in.  Block-uniform, so it (and
+    // every per-round bound derived from it) stays in scalar registers.
+    if (ticket && tid == 0) s_ticket = (uint32_t)(atomicAdd(ticket, 1ull) - ticket_base);
     for (int i = tid; i < (BLOCK / WAVE) * 256; i += BLOCK) (&s_wcnt[0][0])[i] = 0;
     __syncthreads();
+    const uint32_t tile = chunk_tile(ticket ? __builtin_amdgcn_readfirstlane(s_ticket) : blockIdx.x, chunk, tiles);
+    if (tile == TILE_NONE) return;
     {  // one tile per block
         const uint64_t wbase =
             (uint64_t)tile * (BLOCK * ITEMS) + (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane(wave) * (ITEMS * WAVE);
@@ -453,8 +466,14 @@ static uint32_t pass_capacity(Ctx *ctx) {
     return (uint32_t)ctx->num_cus * (uint32_t)b;
 }
 
+// XLOG_HIP_SORT_TICKETS=1 selects the ticketed tile order (read at each sort).
+static bool sort_tickets() {
+    const char *e = getenv("XLOG_HIP_SORT_TICKETS");
+    return e && e[0] == '1';
+}
+
 int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **vals, uint32_t **vals_alt,
-                   uint64_t n, int digit_lo, int digit_hi, const uint64_t *src) {
+                   uint64_t n, int digit_lo, int digit_hi, const uint64_t *src, uint32_t known_digits) {
     if (n < 2 || digit_lo >= digit_hi) {
         if (src && n) XH_CHECK_HIP(hipMemcpyAsync(*keys, src, n * 8, hipMemcpyDeviceToDevice, ctx->stream));
         return 0;
@@ -500,14 +519,17 @@ int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **va
             st.dirty[cur] = 0;
         }
         Prof prof(ctx, XLOG_HIP_KERNEL_SORT_PASS, (has_val ? 24.0 : 16.0) * (double)n);
+        unsigned long long *tk = sort_tickets() ? ctx->tickets + 2 : nullptr;
+        const unsigned long long tb = tk ? ctx->take_tickets(2, grid) : 0ull;
         if (has_val)
             hipLaunchKernelGGL((k_onesweep<true, SORT_BLOCK_V, SORT_ITEMS_V>), dim3(grid), dim3(SORT_BLOCK_V), 0,
                                ctx->stream, *keys, *keys_alt, *vals, *vals_alt, n, (uint32_t)tiles, 8 * dgt,
-                               off + dgt * 256, st.status[cur], st.status[nxt], chunk);
+                               off + dgt * 256, st.status[cur], st.status[nxt], chunk, tk, tb);
         else
             hipLaunchKernelGGL((k_onesweep<false, SORT_BLOCK_K, SORT_ITEMS_K>), dim3(grid), dim3(SORT_BLOCK_K), 0,
                                ctx->stream, (passes == 0 && src) ? src : *keys, *keys_alt, nullptr, nullptr, n,
-                               (uint32_t)tiles, 8 * dgt, off + dgt * 256, st.status[cur], st.status[nxt], chunk);
+                               (uint32_t)tiles, 8 * dgt, off + dgt * 256, st.status[cur], st.status[nxt], chunk,
+                               tk, tb);
         XH_CHECK_HIP(hipGetLastError());
         st.dirty[cur] = tiles;
         if (st.dirty[nxt] <= tiles) st.dirty[nxt] = 0;
@@ -516,6 +538,12 @@ int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **va
         cur = nxt;
         ++passes;
     };
+    if (known_digits) {  // the caller knows which digits may vary: no read-back
+        for (int dgt = digit_lo; dgt < digit_hi; ++dgt)
+            if ((known_digits >> dgt) & 1u) launch_pass(dgt);
+        if (passes == 0 && src) XH_CHECK_HIP(hipMemcpyAsync(*keys, src, n * 8, hipMemcpyDeviceToDevice, ctx->stream));
+        return passes;
+    }
     // The host copy of the histograms decides which digit passes are needed.
     // The pass of the lowest digit is launched before waiting for it (a pass
     // over a constant digit is a stable copy, so it is right either way): the

@@ -125,8 +125,23 @@ def andersen(n_vars: int, n_facts: int, alpha: float, seed: int):
 
 
 # ---- the five configurations (BASELINE.json "configs") ----------------------
+# Vertex ids spread over the whole u32 range (id v -> (v * A + B) mod 2^32, A odd,
+# so a bijection; B puts vertex 7 on 0xFFFFFFFF, the all-ones id): graphs whose
+# max id + 1 is ~2^32, beyond any dense bit-matrix domain.
+SPARSE_ID_MUL = 2654435761
+SPARSE_ID_ADD = (0xFFFFFFFF - 7 * SPARSE_ID_MUL) % (1 << 32)
+
+
+def sparse_ids(v) -> np.ndarray:
+    v = np.asarray(v, dtype=np.uint64)
+    return ((v * np.uint64(SPARSE_ID_MUL) + np.uint64(SPARSE_ID_ADD)) & np.uint64(0xFFFFFFFF)).astype(np.uint32)
+
+
 C1 = dict(n_vertices=1000, n_edges=5000)
 C2 = dict(n_r=1 << 24, n_s=1 << 24, n_keys=1 << 20, zipf_s=1.1)
 C3 = dict(n=1 << 28)
 C4 = dict(n_vertices=32768, n_edges=3 * 32768)
 C5 = dict(n_vars=500_000, n_facts=2_000_000, alpha=1.5)
+# transitive closure above the dense domain: G(2^20, m) digraphs with sparse ids (seed_for(6))
+TCS = dict(n_vertices=1 << 20, n_edges=int(0.9 * (1 << 20)))      # subcritical: ~9.4M tuples, 64 iterations
+TCS_CRIT = dict(n_vertices=1 << 20, n_edges=1 << 20)              # critical: ~2.6e8 tuples, 418 iterations

@@ -32,7 +32,7 @@ STATUS_NAMES = {
     7: "UNSUPPORTED",
 }
 JOIN_INNER, JOIN_SEMI, JOIN_ANTI = 0, 1, 2
-ROUTE_AUTO, ROUTE_JOIN, ROUTE_BITMAP = 0, 1, 2
+ROUTE_AUTO, ROUTE_JOIN, ROUTE_BITMAP, ROUTE_HASH = 0, 1, 2, 3
 
 
 class XlogError(RuntimeError):
@@ -111,6 +111,7 @@ def _load() -> C.CDLL:
         "xlog_hip_join_index_free": (None, [P]),
         "xlog_hip_nested_loop_join": (I32, [P, P, P, U32, U32, PP]),
         "xlog_hip_fj_delta_novel": (I32, [P, P, P, P, C.POINTER(FjDeltaCols), U32, PP]),
+        "xlog_hip_fj_delta_sparse_novel": (I32, [P, P, P, P, C.POINTER(FjDeltaCols), U64, PP]),
         "xlog_hip_union": (I32, [P, P, P, PP]),
         "xlog_hip_union_many": (I32, [P, PP, U32, PP]),
         "xlog_hip_diff": (I32, [P, P, P, PP]),
@@ -156,7 +157,7 @@ ABI_SYMBOLS = (
     "xlog_hip_rel_num_rows", "xlog_hip_rel_arity", "xlog_hip_rel_is_canonical", "xlog_hip_rel_device_words",
     "xlog_hip_rel_clone", "xlog_hip_rel_free", "xlog_hip_sort", "xlog_hip_dedup", "xlog_hip_dedup_full_row",
     "xlog_hip_dedup_sorted", "xlog_hip_join_index_build", "xlog_hip_hash_join_with_index",
-    "xlog_hip_join_index_free", "xlog_hip_nested_loop_join", "xlog_hip_fj_delta_novel",
+    "xlog_hip_join_index_free", "xlog_hip_nested_loop_join", "xlog_hip_fj_delta_novel", "xlog_hip_fj_delta_sparse_novel",
     "xlog_hip_union", "xlog_hip_union_many", "xlog_hip_diff", "xlog_hip_hash_join", "xlog_hip_hash_join_keys",
     "xlog_hip_sort_merge_join", "xlog_hip_join_project", "xlog_hip_join_project_dedup", "xlog_hip_project",
     "xlog_hip_is_sorted",
@@ -169,7 +170,7 @@ ABI_SYMBOLS = (
 
 KERNEL_KINDS = {
     "sort_pass": 0, "sort_hist": 1, "select": 2, "merge": 3, "probe_count": 4, "probe_emit": 5, "tc_step": 6,
-    "tc_emit": 7, "chain_product": 8, "chain_finalize": 9, "chain_emit": 10,
+    "tc_emit": 7, "chain_product": 8, "chain_finalize": 9, "chain_emit": 10, "hash_insert": 11,
 }
 
 
@@ -567,6 +568,17 @@ class HipKernelProvider:
         _check(_lib.xlog_hip_fj_delta_novel(self.ctx, delta.handle, edge.handle, full_r.handle, C.byref(roles),
                                             domain, C.byref(h)))
         return self._rel(h)
+
+    def fj_delta_sparse_novel_u32_recorded(self, delta: Relation, edge: Relation, full_r: Relation,
+                                           cols: Sequence[int] = FJ_DELTA_CANONICAL,
+                                           max_table_bytes: int = 0) -> Optional[Relation]:
+        """The factorized delta step over a device hash set, no domain bound
+        (fj_delta_sparse.rs:66); None when the table would exceed max_table_bytes."""
+        roles = FjDeltaCols(*cols)
+        h = C.c_void_p()
+        _check(_lib.xlog_hip_fj_delta_sparse_novel(self.ctx, delta.handle, edge.handle, full_r.handle,
+                                                   C.byref(roles), max_table_bytes, C.byref(h)))
+        return self._rel(h) if h.value else None
 
     def sort_merge_join_v2_inner_u32_1key(self, left: Relation, right: Relation, left_key: int,
                                           right_key: int) -> Relation:
