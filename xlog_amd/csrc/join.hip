@@ -125,6 +125,8 @@ struct ProbeArgs {
     // optional device-side row count (deferred count pass): when set, it
     // replaces n, which is then only the bound the grid was sized for
     const uint64_t *d_n;
+    // optional profiling counter: the deferred count pass adds its real row count
+    unsigned long long *work;
 };
 // set in a row's start when its outputs come from gsrc
 constexpr uint64_t GROUP_BIT = 1ull << 63;
@@ -188,8 +190,16 @@ __device__ __forceinline__ void lookup_batch(const ProbeArgs &a, const uint64_t 
 template <int ITEMS>
 __global__ __launch_bounds__(JB) void k_probe_count(ProbeArgs a, uint64_t *__restrict__ tile_cnt) {
     __shared__ uint64_t s_part[JWAVES];
-    if (a.d_n) a.n = *a.d_n;  // tiles past the real rows count zero
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
+    if (a.d_n) {
+        // deferred count: the grid covers a bound; tiles past the real rows count zero
+        a.n = *a.d_n;
+        if (a.work && blockIdx.x == 0 && tid == 0) atomicAdd(a.work, (unsigned long long)a.n);
+        if ((uint64_t)blockIdx.x * tile_rows(ITEMS) >= a.n) {
+            if (tid == 0) tile_cnt[blockIdx.x] = 0;
+            return;
+        }
+    }
     const uint64_t wbase = (uint64_t)blockIdx.x * tile_rows(ITEMS) + (uint64_t)wave * (ITEMS * WAVE);
     uint64_t rows[ITEMS];
 #pragma unroll
@@ -226,11 +236,15 @@ __global__ __launch_bounds__(JB) void k_probe_count(ProbeArgs a, uint64_t *__res
 
 // single-block exclusive scan of a u64 array; total -> *total.  Each round
 // covers 1024 x 16 elements: a thread sums 16 consecutive ones, the block
-// scans the 1024 sums, and the thread writes its 16 prefixes.
+// scans the 1024 sums, and the thread writes its 16 prefixes.  With d_rows
+// set, only the first ceil(*d_rows / rows_per) elements are scanned (the
+// tiles of a deferred count whose grid covers a bound).
 constexpr int SCAN_SEG = 16;
-__global__ __launch_bounds__(1024) void k_scan_small(uint64_t *a, uint64_t n, uint64_t *total) {
+__global__ __launch_bounds__(1024) void k_scan_small(uint64_t *a, uint64_t n, uint64_t *total,
+                                                      const uint64_t *d_rows, uint64_t rows_per) {
     __shared__ uint64_t s_w[16];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (d_rows) n = std::min<uint64_t>(n, (*d_rows + rows_per - 1) / rows_per);
     uint64_t carry = 0;
     for (uint64_t base = 0; base < n; base += 1024 * SCAN_SEG) {
         const uint64_t i0 = base + (uint64_t)tid * SCAN_SEG;
@@ -549,7 +563,7 @@ uint64_t probe_prepare(Ctx *ctx, ProbeJob &job) {
         XH_CHECK_HIP(hipGetLastError());
     }
     hipLaunchKernelGGL(k_scan_small, dim3(1), dim3(1024), 0, ctx->stream, job.toff.p, job.tiles,
-                       job.toff.p + job.tiles);
+                       job.toff.p + job.tiles, nullptr, 0ull);
     XH_CHECK_HIP(hipGetLastError());
     ctx->read_scalars(job.toff.p + job.tiles, 1);
     job.total = ctx->host_scalars[0];
@@ -584,13 +598,14 @@ void probe_prepare_deferred(Ctx *ctx, ProbeJob &job, uint64_t n_bound, const uin
     a.rec_start = job.rec_start.p;
     a.rec_cnt = job.rec_cnt.p;
     {
-        Prof prof(ctx, XLOG_HIP_KERNEL_PROBE_COUNT, 36.0 * (double)n_bound);
+        Prof prof(ctx, XLOG_HIP_KERNEL_PROBE_COUNT, 0.0);
+        a.work = prof.work(36.0);  // 36 B per real row, counted on the device
         hipLaunchKernelGGL(k_probe_count<JITEMS>, dim3((unsigned)job.tiles), dim3(JB), 0, ctx->stream, a,
                            job.toff.p);
         XH_CHECK_HIP(hipGetLastError());
     }
     hipLaunchKernelGGL(k_scan_small, dim3(1), dim3(1024), 0, ctx->stream, job.toff.p, job.tiles,
-                       job.toff.p + job.tiles);
+                       job.toff.p + job.tiles, d_n, tile_rows(job.items));
     XH_CHECK_HIP(hipGetLastError());
 }
 void probe_finish(ProbeJob &job, uint64_t n, uint64_t total) {
@@ -971,7 +986,7 @@ uint64_t nested_loop_join(Ctx *ctx, const uint64_t *l, uint64_t nl, int la, int 
 }
 
 void scan_u64_small(Ctx *ctx, uint64_t *a, uint64_t n, uint64_t *total) {
-    hipLaunchKernelGGL(k_scan_small, dim3(1), dim3(1024), 0, ctx->stream, a, n, total);
+    hipLaunchKernelGGL(k_scan_small, dim3(1), dim3(1024), 0, ctx->stream, a, n, total, nullptr, 0ull);
     XH_CHECK_HIP(hipGetLastError());
 }
 }  // namespace xh
