@@ -1,6 +1,7 @@
 """Benchmark of the semi-naive relational core on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c4|c1|c1j|c2|c2u|c3|c4j|c5|copy]
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+                    [--workload c4|c1|c1j|c1h|c2|c2u|c3|c4j|c4h|c5|tcs|tcs_crit|tcs_j|copy|c5full]
                     [--no-extra] [--no-cpu-baseline]
 
 Default workload is BASELINE.json configs[3] (C4), the metric's lead quantity:
@@ -13,8 +14,13 @@ With the default workload the same line carries the other configs under
 `configs` (c1: TC on G(1000, 5000); c2: R(a,b) join S(b,c), project, sort +
 dedup at 2^24 rows a side; c3: sort + dedup of 2^28 packed tuples; c5: Andersen
 points-to at 10,000 variables), each with its own timing, roofline and CPU
-baseline.  c1j / c4j force the join route, c2u the unfused join -> sort ->
-dedup sequence, copy is the counter calibration kernel.
+baseline.  c1j / c4j force the join route and c1h / c4h the hash-set route;
+tcs / tcs_crit are closures over 2^20 vertices whose ids are spread over u32
+(the hash-set route, AUTO's choice there) and tcs_j is tcs on the join route;
+c2u is the unfused join -> sort -> dedup sequence; copy is the counter
+calibration kernel; c5full runs C5 at its stated 500,000 variables once and
+reports its outcome (the library fails closed at the reference's 2^32-1 join
+row limit).
 
 Every `roofline` object describes the kernel kind with the largest share of
 device time in the timed steps, timed live with HIP events on the library's
