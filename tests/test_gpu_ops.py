@@ -225,6 +225,28 @@ def test_join_project_dedup_ordered(provider, nl, nr, lkeys, avals, seed):
     assert got_c.is_canonical() and np.array_equal(p.download_packed(got_c), exp)
 
 
+@pytest.mark.parametrize("all_unmatched", [False, True])
+def test_join_project_dedup_groups_without_outputs(provider, all_unmatched):
+    """Probe rows sharing their output column whose keys match nothing: groups with no outputs (some
+    groups, or every group, so that the side probe emits nothing), next to lone rows that match."""
+    p = provider
+    rng = _rng(31 if all_unmatched else 32)
+    n = 40000
+    a = np.arange(n, dtype=np.uint64)
+    grouped = a < 20000
+    a[grouped] = a[grouped] // 4  # groups of 4 rows sharing their out column
+    a[~grouped] += 1 << 20
+    key = rng.integers(0, 100, n).astype(np.uint64)
+    unmatched = grouped if all_unmatched else grouped & ((a % 2) == 1)
+    key[unmatched] = (1 << 30) + np.arange(int(unmatched.sum()), dtype=np.uint64)
+    l = pack(a, key)
+    r = pack(rng.integers(0, 100, 3000), rng.integers(0, 1 << 32, 3000, dtype=np.uint64))
+    exp = oracle.sort_dedup(oracle.join_project(l, r, 1, 0, 0, 3))
+    got = p.join_project_dedup(p.create_buffer_from_packed(l), p.create_buffer_from_packed(r), 1, 0, [0, 3])
+    assert got.is_canonical()
+    assert np.array_equal(p.download_packed(got), exp)
+
+
 def test_join_skewed_hot_key(provider):
     """One key holds most probe rows and a long build run (cooperative expansion)."""
     p = provider

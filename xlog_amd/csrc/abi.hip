@@ -1166,11 +1166,20 @@ static xlog_hip_rel *op_fj_delta_sparse(Ctx *ctx, const xlog_hip_rel *delta, con
 // replaces the radix sort of the whole join output.  Other shapes take the
 // join -> sort -> unique path.
 void left_keys(Ctx *ctx, const uint64_t *l, uint64_t n, int arity, int oc0, int jk, uint64_t *out);
-void sort_segments(Ctx *ctx, uint64_t *data, uint64_t n, const uint64_t *heads, uint64_t nh);
-uint64_t group_rows(Ctx *ctx, const uint64_t *k, uint64_t n, int32_t *gsel, uint64_t *mkeys, uint64_t *hkeys,
-                    uint64_t *nh);
+void group_rows_async(Ctx *ctx, const uint64_t *k, uint64_t n, int32_t *gsel, uint64_t *mkeys, uint64_t *mpos,
+                      uint64_t *hkeys, uint64_t *hpos, uint64_t *d_nm, uint64_t *d_nh);
 void group_segments(Ctx *ctx, const uint64_t *sorted, uint64_t n, const uint64_t *head_keys, uint64_t nh,
-                    uint64_t *seg);
+                    uint64_t *seg, const uint64_t *d_n);
+void sort_segments_async(Ctx *ctx, uint64_t *data, uint64_t n, const uint64_t *heads, uint64_t nh, uint64_t *seg,
+                         unsigned long long *d_max);
+void sort_segments_long(Ctx *ctx, uint64_t *data, const uint64_t *seg, uint64_t nh, uint64_t max_len);
+
+namespace {
+__global__ void k_gather_u64(const uint64_t *a, const uint64_t *b, uint64_t *out) {
+    out[0] = *a;
+    out[1] = *b;
+}
+}  // namespace
 
 static xlog_hip_rel *op_join_project_dedup(Ctx *ctx, const xlog_hip_rel *l, const xlog_hip_rel *r, uint32_t lk,
                                            uint32_t rk, const std::vector<int> &out_cols) {
@@ -1190,74 +1199,152 @@ static xlog_hip_rel *op_join_project_dedup(Ctx *ctx, const xlog_hip_rel *l, cons
         rel_free(j);
         return d;
     }
-    const uint64_t n = l->rows;
-    if (n == 0 || r->rows == 0) {
+    const uint64_t n = l->rows, nr = r->rows;
+    auto empty = [&]() {
         xlog_hip_rel *e = rel_new(ctx, 2, 0);
         e->flags = REL_CANONICAL;
         return e;
-    }
+    };
+    if (n == 0 || nr == 0) return empty();
+    // The host waits three times: for the build side's and the groups' sizes,
+    // for the side probe's size (while the device runs the main count pass),
+    // and for the output size (plus the sorts' histogram read-backs, which
+    // their first digit pass overlaps).
     // 1. probe keys (out column << 32 | join key), ordered by the out column
-    uint64_t *lkeys = static_cast<uint64_t *>(ctx->alloc(n * sizeof(uint64_t)));
-    left_keys(ctx, l->w[0], n, (int)l->arity, out_cols[0], (int)lk, lkeys);
-    lkeys = sort_keys(ctx, lkeys, n, true, 4, 8);
-    Buf<uint64_t> lk_buf;  // owns lkeys from here on
+    Buf<uint64_t> lk_buf;  // owns the sorted probe keys
     lk_buf.ctx = ctx;
-    lk_buf.p = lkeys;
-    // 2. build index whose runs hold distinct, ascending payloads: a probe
-    //    row alone with its out column then emits sorted, unique outputs
+    if (l->arity == 2 && out_cols[0] == 0 && lk == 1) {
+        // the rows are already (out column << 32 | join key): the sort reads them directly
+        lk_buf.p = sort_keys(ctx, l->w[0], n, false, 4, 8);
+    } else {
+        lk_buf.p = static_cast<uint64_t *>(ctx->alloc(n * sizeof(uint64_t)));
+        left_keys(ctx, l->w[0], n, (int)l->arity, out_cols[0], (int)lk, lk_buf.p);
+        lk_buf.p = sort_keys(ctx, lk_buf.p, n, true, 4, 8);
+    }
+    const uint64_t *lkeys = lk_buf.p;
+    // 2. build rows as (key << 32 | payload), sorted and unique, so that a probe
+    //    row alone with its out column emits sorted, unique outputs
+    Buf<uint64_t> sk_buf;
+    sk_buf.ctx = ctx;
+    const uint64_t *sk;
+    const bool canon = rk == 0 && (r->flags & REL_CANONICAL) != 0;
+    if (canon) {
+        sk = r->w[0];
+    } else if (rk == 0) {
+        sk_buf.p = sort_keys(ctx, r->w[0], nr, false, 0, 8);
+        sk = sk_buf.p;
+    } else {
+        uint64_t *sw = static_cast<uint64_t *>(ctx->alloc(nr * sizeof(uint64_t)));
+        sk_buf.p = sw;
+        swap_words(ctx, r->w[0], nr, sw);
+        sk_buf.p = sort_keys(ctx, sw, nr, true, 0, 8);
+        sk = sk_buf.p;
+    }
+    Buf<uint64_t> cnt(ctx, 4);  // unique build rows, runs, group members, groups
+    Buf<uint64_t> ub;
     JoinIndex J;
-    build_join_index(ctx, r->w[0], r->rows, r->arity, (int)rk, (r->flags & REL_CANONICAL) != 0, J, true, true);
+    J.payload = Buf<uint32_t>(ctx, nr);
+    const uint64_t *bk = sk, *d_un = nullptr;
+    if (!canon && nr > 1) {
+        ub = Buf<uint64_t>(ctx, nr);
+        select_unique_low(ctx, sk, nr, ub.p, J.payload.p, cnt.p);  // the payloads come with the unique rows
+        bk = ub.p;
+        d_un = cnt.p;
+    } else {
+        low_words(ctx, bk, nr, J.payload.p);
+    }
+    RunScratch rs;
+    build_run_index_async(ctx, bk, nr, d_un, rs, cnt.p + 1);
     // 3. probe rows sharing their out column (groups) can emit the same
     //    output twice and interleave: their outputs are produced on the side
     //    (probe, sort inside each group, unique) and copied into place by the
     //    main emit through the group selector
     Buf<int32_t> gsel(ctx, n);
-    Buf<uint64_t> mkeys(ctx, n), hkeys(ctx, n);
-    uint64_t nh = 0;
-    const uint64_t nm = group_rows(ctx, lkeys, n, gsel.p, mkeys.p, hkeys.p, &nh);
+    Buf<uint64_t> mkeys(ctx, n), mpos(ctx, n), hkeys(ctx, n), hpos(ctx, n);
+    group_rows_async(ctx, lkeys, n, gsel.p, mkeys.p, mpos.p, hkeys.p, hpos.p, cnt.p + 2, cnt.p + 3);
+    ctx->read_scalars(cnt.p, 4);
+    const uint64_t un = d_un ? ctx->host_scalars[0] : nr, nruns = ctx->host_scalars[1];
+    const uint64_t nm = ctx->host_scalars[2], nh = ctx->host_scalars[3];
+    J.n = un;
+    build_run_index_finish(ctx, rs, nruns, un, J.ix);
+    sk_buf = Buf<uint64_t>();
+    ub = Buf<uint64_t>();
+    mpos = Buf<uint64_t>();
+    // 4. the side probe's count, then the main count pass (group heads count
+    //    zero until their groups are known); the side total comes back while
+    //    the main count runs
     const int oc[4] = {0, 3, 0, 0};  // v0 = out column (probe high word), v3 = payload
-    Buf<uint64_t> gseg, gsrc_buf;
+    ProbeJob side;
     if (nm) {
-        uint64_t *bag = nullptr;
-        const uint64_t m2 = join_probe_general(ctx, mkeys.p, nm, 1, J.ix, J.payload.p, 2, oc, &bag, nullptr);
-        uint64_t *u2 = nullptr, nu2 = 0;
-        if (m2) {
-            try {
-                sort_segments(ctx, bag, m2, hkeys.p, nh);
-                nu2 = unique_keys(ctx, bag, m2, &u2);
-            } catch (...) {
-                ctx->free(bag);
-                throw;
-            }
-            ctx->free(bag);
-        }
-        gsrc_buf.ctx = ctx;
-        gsrc_buf.p = u2;
-        gseg = Buf<uint64_t>(ctx, 2 * nh);
-        if (nu2) {
-            group_segments(ctx, u2, nu2, hkeys.p, nh, gseg.p);
-        } else {
-            fill_u64(ctx, gseg.p, 0ull, 2 * nh);
-        }
+        side.probe = mkeys.p;
+        side.n = nm;
+        side.pcol = 1;
+        side.ix = &J.ix;
+        side.payload = J.payload.p;
+        probe_count_only(ctx, side);
+        probe_scan_async(ctx, side);
+        XH_CHECK_HIP(hipMemcpyAsync(ctx->host_scalars, side.toff.p + side.tiles, sizeof(uint64_t),
+                                    hipMemcpyDeviceToHost, ctx->stream));
+        XH_CHECK_HIP(hipEventRecord(ctx->ev_read, ctx->stream));
     }
-    // 4. the main probe: count, scan, emit into the final buffer
     ProbeJob job;
     job.probe = lkeys;
     job.n = n;
     job.pcol = 1;
     job.ix = &J.ix;
     job.payload = J.payload.p;
+    if (nm) job.gsel = gsel.p;  // gseg unset: heads deferred
+    probe_count_only(ctx, job);
+    // 5. group outputs: emit, sort inside each group, unique; each head then
+    //    gets its group's unique words and count
+    Buf<uint64_t> gseg, bag, seg, u2, nu2(ctx, 1);
+    Buf<unsigned long long> mx(ctx, 1);
+    uint64_t m2 = 0;
     if (nm) {
-        job.gsel = gsel.p;
+        ctx->wait_event(ctx->ev_read);
+        m2 = ctx->host_scalars[0];
+        probe_finish(side, nm, m2);
+        gseg = Buf<uint64_t>(ctx, 2 * nh);
+        if (m2) {
+            bag = Buf<uint64_t>(ctx, m2);
+            probe_emit_range(ctx, side, 0, side.tiles, m2, 2, oc, bag.p, nullptr);
+            seg = Buf<uint64_t>(ctx, 2 * nh);
+            sort_segments_async(ctx, bag.p, m2, hkeys.p, nh, seg.p, mx.p);
+            u2 = Buf<uint64_t>(ctx, m2);
+            select_unique(ctx, bag.p, m2, u2.p, nu2.p);
+            group_segments(ctx, u2.p, m2, hkeys.p, nh, gseg.p, nu2.p);
+        } else {
+            fill_u64(ctx, gseg.p, 0ull, 2 * nh);
+        }
+        probe_group_fixup(ctx, job, hpos.p, gseg.p, nh);
+    }
+    if (!nm || !m2) fill_u64(ctx, reinterpret_cast<uint64_t *>(mx.p), 0ull, 1);
+    probe_scan_async(ctx, job);
+    Buf<uint64_t> g2(ctx, 2);
+    hipLaunchKernelGGL(k_gather_u64, dim3(1), dim3(1), 0, ctx->stream, job.toff.p + job.tiles,
+                       reinterpret_cast<const uint64_t *>(mx.p), g2.p);
+    XH_CHECK_HIP(hipGetLastError());
+    ctx->read_scalars(g2.p, 2);
+    uint64_t total = ctx->host_scalars[0];
+    const uint64_t max_len = ctx->host_scalars[1];
+    if (max_len > (uint64_t)WAVE) {
+        // rare: a group with more than 64 outputs needs the block / radix
+        // segment sorts; its unique words and the counts are then redone
+        sort_segments_long(ctx, bag.p, seg.p, nh, max_len);
+        select_unique(ctx, bag.p, m2, u2.p, nu2.p);
+        group_segments(ctx, u2.p, m2, hkeys.p, nh, gseg.p, nu2.p);
+        probe_count_only(ctx, job);
+        probe_group_fixup(ctx, job, hpos.p, gseg.p, nh);
+        probe_scan_async(ctx, job);
+        ctx->read_scalars(job.toff.p + job.tiles, 1);
+        total = ctx->host_scalars[0];
+    }
+    probe_finish(job, n, total);
+    if (nm) {
         job.gseg = gseg.p;
-        job.gsrc = gsrc_buf.p;
+        job.gsrc = u2.p;
     }
-    const uint64_t total = probe_prepare(ctx, job);
-    if (!total) {
-        xlog_hip_rel *e = rel_new(ctx, 2, 0);
-        e->flags = REL_CANONICAL;
-        return e;
-    }
+    if (!total) return empty();
     uint64_t *o = static_cast<uint64_t *>(ctx->alloc(total * sizeof(uint64_t)));
     try {
         probe_emit_range(ctx, job, 0, job.tiles, total, 2, oc, o, nullptr);

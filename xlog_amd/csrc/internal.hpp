@@ -271,10 +271,15 @@ int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **va
 // Stream compaction family (single pass, decoupled look-back).  Each writes
 // the selected keys in input order to `out` and the count to *d_count
 // (device) ; returns nothing, the caller reads the count when it needs it.
+// Where a d_n argument is taken and set, the input's row count is *d_n on the
+// device and n only the bound the launch is sized for.
 //   unique:      keep k[i] if i == 0 or k[i] != k[i-1]                 (sorted input)
 //   unique_diff: keep k[i] if unique and k[i] not in sorted b[0..nb)
 //   diff:        keep k[i] if k[i] not in sorted b[0..nb)
-void select_unique(Ctx *ctx, const uint64_t *k, uint64_t n, uint64_t *out, uint64_t *d_count);
+void select_unique(Ctx *ctx, const uint64_t *k, uint64_t n, uint64_t *out, uint64_t *d_count,
+                   const uint64_t *d_n = nullptr);
+//   unique_low:  unique, and the low word of each selected key to low[]
+void select_unique_low(Ctx *ctx, const uint64_t *k, uint64_t n, uint64_t *out, uint32_t *low, uint64_t *d_count);
 void select_unique_diff(Ctx *ctx, const uint64_t *k, uint64_t n, const uint64_t *b, uint64_t nb,
                         uint64_t *out, uint64_t *d_count);
 void select_flags(Ctx *ctx, const uint64_t *k, const uint8_t *flags, uint64_t n, uint64_t *out,
@@ -305,6 +310,16 @@ struct RunIndex {
     uint64_t table_mask = 0;
 };
 void build_run_index(Ctx *ctx, const uint64_t *sorted_keys, uint64_t n, RunIndex &ix);
+// The same in two steps around one read-back: the runs of sorted_keys[0, n)
+// with n = *d_n when d_n is set (n_bound sizes the buffers), run count to
+// *d_nruns; then the table, once the run count and n are known.
+struct RunScratch {
+    Buf<uint32_t> run_key;
+    Buf<uint64_t> run_start;
+};
+void build_run_index_async(Ctx *ctx, const uint64_t *sorted_keys, uint64_t n_bound, const uint64_t *d_n,
+                           RunScratch &rs, uint64_t *d_nruns);
+void build_run_index_finish(Ctx *ctx, RunScratch &rs, uint64_t nruns, uint64_t n, RunIndex &ix);
 // Merge-path lookup of the sort-merge join: for every row of l (sorted by the
 // key word pcol), the start and length of its run among the nr runs of
 // (run_key, run_start[0..nr]) (sorted, distinct keys); length 0 without one.
@@ -354,6 +369,13 @@ uint64_t probe_prepare(Ctx *ctx, ProbeJob &job);
 // completes the job once the host has read the row count and the total.
 void probe_prepare_deferred(Ctx *ctx, ProbeJob &job, uint64_t n_bound, const uint64_t *d_n);
 void probe_finish(ProbeJob &job, uint64_t n, uint64_t total);
+// The count pass alone, lookups recorded, no scan and no read-back; with gsel
+// set and gseg null the group heads count zero until probe_group_fixup gives
+// each head (row hpos[g]) its group's finished words gseg[2g], gseg[2g + 1].
+// probe_scan_async then leaves the total at job.toff.p[job.tiles].
+void probe_count_only(Ctx *ctx, ProbeJob &job);
+void probe_group_fixup(Ctx *ctx, ProbeJob &job, const uint64_t *hpos, const uint64_t *gseg, uint64_t nh);
+void probe_scan_async(Ctx *ctx, ProbeJob &job);
 std::vector<uint64_t> probe_tile_offsets(Ctx *ctx, const ProbeJob &job);
 // writes the `rows` outputs of tiles [t0, t1) to out0 / out1 starting at index 0
 void probe_emit_range(Ctx *ctx, const ProbeJob &job, uint64_t t0, uint64_t t1, uint64_t rows, int out_arity,
@@ -453,16 +475,21 @@ inline unsigned grid_for(uint64_t n, unsigned block, unsigned cap) {
 }
 void fill_u32(Ctx *ctx, uint32_t *p, uint32_t v, uint64_t n);
 void select_runs(Ctx *ctx, const uint64_t *k, uint64_t n, uint32_t *run_key, uint64_t *run_start,
-                 uint64_t *d_count);
+                 uint64_t *d_count, const uint64_t *d_n = nullptr);
 // Keys sorted by their high word: rows sharing it with a neighbour (key,
 // position), then among those the group heads (key; gsel[position] = group
-// number).
+// number; hpos, when set, receives each head's position).
 void select_group_members(Ctx *ctx, const uint64_t *k, uint64_t n, uint64_t *mkeys, uint64_t *mpos,
                           uint64_t *d_count);
 void select_group_heads(Ctx *ctx, const uint64_t *mkeys, uint64_t nm, const uint64_t *mpos, uint64_t *hkeys,
-                        int32_t *gsel, uint64_t *d_count);
+                        int32_t *gsel, uint64_t *d_count, const uint64_t *d_n = nullptr, uint64_t *hpos = nullptr);
 void sort_state_release(Ctx *ctx);
 void select_state_release(Ctx *ctx);
+// Exclusive scan of u64 counts in place, one pass; the exact total goes to
+// *d_total (device).  The prefixes are exact while the total is below
+// SCAN64_EXACT; a caller checks the total before using them.
+constexpr uint64_t SCAN64_EXACT = 1ull << 39;
+void scan_u64_inplace(Ctx *ctx, uint64_t *a, uint64_t n, uint64_t *d_total);
 void fill_u64(Ctx *ctx, uint64_t *p, uint64_t v, uint64_t n);
 void pack_columns(Ctx *ctx, const uint32_t *c0, const uint32_t *c1, uint64_t n, uint64_t *out);
 void unpack_column(Ctx *ctx, const uint64_t *w, int hi, uint64_t n, uint32_t *out);

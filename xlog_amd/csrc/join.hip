@@ -180,8 +180,10 @@ __device__ __forceinline__ void lookup_batch(const ProbeArgs &a, const uint64_t 
             cnt[r] = (uint32_t)s.x;  // 0 when the key has no run (empty slot)
             if (g[q] == -2) cnt[r] = 0;
             if (g[q] >= 0) {
-                start[r] = a.gseg[2 * g[q]] | GROUP_BIT;
-                cnt[r] = (uint32_t)a.gseg[2 * g[q] + 1];
+                // without gseg the group outputs are not known yet: the head
+                // counts zero here and k_group_fixup adds its group later
+                start[r] = a.gseg ? (a.gseg[2 * g[q]] | GROUP_BIT) : 0ull;
+                cnt[r] = a.gseg ? (uint32_t)a.gseg[2 * g[q] + 1] : 0u;
             }
         }
     }
@@ -236,15 +238,11 @@ __global__ __launch_bounds__(JB) void k_probe_count(ProbeArgs a, uint64_t *__res
 
 // single-block exclusive scan of a u64 array; total -> *total.  Each round
 // covers 1024 x 16 elements: a thread sums 16 consecutive ones, the block
-// scans the 1024 sums, and the thread writes its 16 prefixes.  With d_rows
-// set, only the first ceil(*d_rows / rows_per) elements are scanned (the
-// tiles of a deferred count whose grid covers a bound).
+// scans the 1024 sums, and the thread writes its 16 prefixes.
 constexpr int SCAN_SEG = 16;
-__global__ __launch_bounds__(1024) void k_scan_small(uint64_t *a, uint64_t n, uint64_t *total,
-                                                      const uint64_t *d_rows, uint64_t rows_per) {
+__global__ __launch_bounds__(1024) void k_scan_small(uint64_t *a, uint64_t n, uint64_t *total) {
     __shared__ uint64_t s_w[16];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (d_rows) n = std::min<uint64_t>(n, (*d_rows + rows_per - 1) / rows_per);
     uint64_t carry = 0;
     for (uint64_t base = 0; base < n; base += 1024 * SCAN_SEG) {
         const uint64_t i0 = base + (uint64_t)tid * SCAN_SEG;
@@ -495,20 +493,25 @@ __global__ void k_match_flags(ProbeArgs a, int want, uint8_t *__restrict__ flags
 
 }  // namespace
 
-void build_run_index(Ctx *ctx, const uint64_t *sorted_keys, uint64_t n, RunIndex &ix) {
-    Buf<uint32_t> run_key(ctx, n ? n : 1);
-    Buf<uint64_t> run_start(ctx, n + 1);
-    Buf<uint64_t> cnt(ctx, 1);
-    select_runs(ctx, sorted_keys, n, run_key.p, run_start.p, cnt.p);
-    ctx->read_scalars(cnt.p, 1);
-    ix.nruns = ctx->host_scalars[0];
+// Runs of the high word of sorted keys [0, n), n = *d_n when d_n is set
+// (then n_bound sizes the buffers): key and start per run, the run count to
+// *d_nruns.  build_run_index_finish builds the table once the host knows the
+// run count and n.
+void build_run_index_async(Ctx *ctx, const uint64_t *sorted_keys, uint64_t n_bound, const uint64_t *d_n,
+                           RunScratch &rs, uint64_t *d_nruns) {
+    rs.run_key = Buf<uint32_t>(ctx, n_bound ? n_bound : 1);
+    rs.run_start = Buf<uint64_t>(ctx, n_bound + 1);
+    select_runs(ctx, sorted_keys, n_bound, rs.run_key.p, rs.run_start.p, d_nruns, d_n);
+}
+void build_run_index_finish(Ctx *ctx, RunScratch &rs, uint64_t nruns, uint64_t n, RunIndex &ix) {
+    ix.nruns = nruns;
     XH_REQUIRE(ix.nruns < 0xFFFFFFFFull, XLOG_HIP_CAPACITY_OVERFLOW, "join build: too many distinct keys");
-    hipLaunchKernelGGL(k_set_u64, dim3(1), dim3(1), 0, ctx->stream, run_start.p + ix.nruns, n);
+    hipLaunchKernelGGL(k_set_u64, dim3(1), dim3(1), 0, ctx->stream, rs.run_start.p + ix.nruns, n);
     if (n >= (1ull << 32) && ix.nruns) {  // a slot holds a 32-bit run length
         Buf<unsigned long long> mx(ctx, 1);
         fill_u64(ctx, reinterpret_cast<uint64_t *>(mx.p), 0ull, 1);
         hipLaunchKernelGGL(k_max_run_len, dim3(grid_for(ix.nruns, 256, 16384)), dim3(256), 0, ctx->stream,
-                           run_start.p, ix.nruns, mx.p);
+                           rs.run_start.p, ix.nruns, mx.p);
         XH_CHECK_HIP(hipGetLastError());
         ctx->read_scalars(mx.p, 1);
         XH_REQUIRE(ctx->host_scalars[0] < (1ull << 32), XLOG_HIP_CAPACITY_OVERFLOW,
@@ -522,9 +525,16 @@ void build_run_index(Ctx *ctx, const uint64_t *sorted_keys, uint64_t n, RunIndex
     ix.table_mask = slots - 1;
     fill_u64(ctx, reinterpret_cast<uint64_t *>(ix.table.p), 0ull, 2 * slots);
     if (ix.nruns)
-        hipLaunchKernelGGL(k_insert, dim3(grid_for(ix.nruns, 256, 16384)), dim3(256), 0, ctx->stream, run_key.p,
-                           run_start.p, ix.nruns, ix.table.p, ix.table_mask, bits);
+        hipLaunchKernelGGL(k_insert, dim3(grid_for(ix.nruns, 256, 16384)), dim3(256), 0, ctx->stream, rs.run_key.p,
+                           rs.run_start.p, ix.nruns, ix.table.p, ix.table_mask, bits);
     XH_CHECK_HIP(hipGetLastError());
+}
+void build_run_index(Ctx *ctx, const uint64_t *sorted_keys, uint64_t n, RunIndex &ix) {
+    RunScratch rs;
+    Buf<uint64_t> cnt(ctx, 1);
+    build_run_index_async(ctx, sorted_keys, n, nullptr, rs, cnt.p);
+    ctx->read_scalars(cnt.p, 1);
+    build_run_index_finish(ctx, rs, ctx->host_scalars[0], n, ix);
 }
 
 static int table_bits(const RunIndex &ix) {
@@ -562,11 +572,11 @@ uint64_t probe_prepare(Ctx *ctx, ProbeJob &job) {
                            job.toff.p);
         XH_CHECK_HIP(hipGetLastError());
     }
-    hipLaunchKernelGGL(k_scan_small, dim3(1), dim3(1024), 0, ctx->stream, job.toff.p, job.tiles,
-                       job.toff.p + job.tiles, nullptr, 0ull);
-    XH_CHECK_HIP(hipGetLastError());
+    scan_u64_inplace(ctx, job.toff.p, job.tiles, job.toff.p + job.tiles);
     ctx->read_scalars(job.toff.p + job.tiles, 1);
     job.total = ctx->host_scalars[0];
+    XH_REQUIRE(job.total < SCAN64_EXACT, XLOG_HIP_CAPACITY_OVERFLOW,
+               "join probe: " + std::to_string(job.total) + " output rows");
     if (a.rec_cnt) {
         job.pre_start = job.rec_start.p;
         job.pre_cnt = job.rec_cnt.p;
@@ -604,11 +614,11 @@ void probe_prepare_deferred(Ctx *ctx, ProbeJob &job, uint64_t n_bound, const uin
                            job.toff.p);
         XH_CHECK_HIP(hipGetLastError());
     }
-    hipLaunchKernelGGL(k_scan_small, dim3(1), dim3(1024), 0, ctx->stream, job.toff.p, job.tiles,
-                       job.toff.p + job.tiles, d_n, tile_rows(job.items));
-    XH_CHECK_HIP(hipGetLastError());
+    // tiles past the real rows hold zero counts
+    scan_u64_inplace(ctx, job.toff.p, job.tiles, job.toff.p + job.tiles);
 }
 void probe_finish(ProbeJob &job, uint64_t n, uint64_t total) {
+    XH_REQUIRE(total < SCAN64_EXACT, XLOG_HIP_CAPACITY_OVERFLOW, "join probe: " + std::to_string(total) + " output rows");
     job.n = n;
     job.tiles = (n + tile_rows(job.items) - 1) / tile_rows(job.items);
     job.total = total;
@@ -616,6 +626,66 @@ void probe_finish(ProbeJob &job, uint64_t n, uint64_t total) {
         job.pre_start = job.rec_start.p;
         job.pre_cnt = job.rec_cnt.p;
     }
+}
+
+// The count pass alone (tile counts in job.toff[0..tiles), lookups recorded),
+// for a caller that adds to the counts before probe_scan_async.  With gsel
+// set and gseg null, group heads count zero (see k_group_fixup).
+void probe_count_only(Ctx *ctx, ProbeJob &job) {
+    job.items = JITEMS;
+    job.tiles = (job.n + tile_rows(job.items) - 1) / tile_rows(job.items);
+    job.total = 0;
+    XH_REQUIRE(job.tiles < (1ull << 31), XLOG_HIP_CAPACITY_OVERFLOW, "join probe: input too large");
+    XH_REQUIRE(job.record_lookups && !job.pre_cnt, XLOG_HIP_INVALID_ARG, "count-only probe: recorded lookups only");
+    job.toff = Buf<uint64_t>(ctx, job.tiles + 1);
+    if (job.n == 0) return;
+    if (job.ix->nruns == 0) {
+        fill_u64(ctx, job.toff.p, 0ull, job.tiles + 1);
+        job.rec_start = Buf<uint64_t>(ctx, job.n);
+        job.rec_cnt = Buf<uint32_t>(ctx, job.n);
+        fill_u64(ctx, job.rec_start.p, 0ull, job.n);
+        fill_u32(ctx, job.rec_cnt.p, 0u, job.n);
+        return;
+    }
+    ProbeArgs a = probe_args(job);
+    job.rec_start = Buf<uint64_t>(ctx, job.n);
+    job.rec_cnt = Buf<uint32_t>(ctx, job.n);
+    a.rec_start = job.rec_start.p;
+    a.rec_cnt = job.rec_cnt.p;
+    Prof prof(ctx, XLOG_HIP_KERNEL_PROBE_COUNT, 36.0 * (double)job.n);
+    hipLaunchKernelGGL(k_probe_count<JITEMS>, dim3((unsigned)job.tiles), dim3(JB), 0, ctx->stream, a, job.toff.p);
+    XH_CHECK_HIP(hipGetLastError());
+}
+
+namespace {
+// Group heads of a count pass run without gseg: each head's recorded run
+// becomes its group's finished words and its tile count grows by their number.
+__global__ void k_group_fixup(const uint64_t *__restrict__ hpos, const uint64_t *__restrict__ gseg, uint64_t nh,
+                              uint64_t *__restrict__ rec_start, uint32_t *__restrict__ rec_cnt,
+                              unsigned long long *tile_cnt, uint64_t rows_per_tile) {
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t g = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; g < nh; g += stride) {
+        const uint64_t p = hpos[g], st = gseg[2 * g], c = gseg[2 * g + 1];
+        rec_start[p] = st | GROUP_BIT;
+        rec_cnt[p] = (uint32_t)c;
+        if (c) atomicAdd(tile_cnt + p / rows_per_tile, (unsigned long long)c);
+    }
+}
+}  // namespace
+
+void probe_group_fixup(Ctx *ctx, ProbeJob &job, const uint64_t *hpos, const uint64_t *gseg, uint64_t nh) {
+    if (!nh || !job.n) return;
+    hipLaunchKernelGGL(k_group_fixup, dim3(grid_for(nh, 256, 4096)), dim3(256), 0, ctx->stream, hpos, gseg, nh,
+                       job.rec_start.p, job.rec_cnt.p, reinterpret_cast<unsigned long long *>(job.toff.p),
+                       tile_rows(job.items));
+    XH_CHECK_HIP(hipGetLastError());
+}
+
+// The tile scan of a count-only probe; the total lands at job.toff.p[job.tiles]
+// (finish with probe_finish once the host has read it).
+void probe_scan_async(Ctx *ctx, ProbeJob &job) {
+    if (!job.n) return;
+    scan_u64_inplace(ctx, job.toff.p, job.tiles, job.toff.p + job.tiles);
 }
 
 std::vector<uint64_t> probe_tile_offsets(Ctx *ctx, const ProbeJob &job) {
@@ -724,7 +794,9 @@ __global__ void k_group_heads(const uint64_t *__restrict__ k, uint64_t n, uint8_
 // seg[2i], seg[2i + 1] = start and length of head i's rows in out; *max_len
 // (when given) = the largest length
 __global__ void k_find_segments(const uint64_t *__restrict__ out, uint64_t n, const uint64_t *__restrict__ heads,
-                                uint64_t nh, uint64_t *__restrict__ seg, unsigned long long *max_len) {
+                                uint64_t nh, uint64_t *__restrict__ seg, unsigned long long *max_len,
+                                const uint64_t *d_n) {
+    if (d_n) n = *d_n;  // the data length on the device
     uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
     unsigned long long mx = 0;
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nh; i += stride) {
@@ -832,7 +904,9 @@ void group_head_flags(Ctx *ctx, const uint64_t *k, uint64_t n, uint8_t *flags) {
     XH_CHECK_HIP(hipGetLastError());
 }
 
-__global__ void k_mark_members(const uint64_t *__restrict__ pos, uint64_t nm, int32_t *__restrict__ gsel) {
+__global__ void k_mark_members(const uint64_t *__restrict__ pos, uint64_t nm, int32_t *__restrict__ gsel,
+                               const uint64_t *d_nm) {
+    if (d_nm) nm = *d_nm;
     uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nm; i += stride) gsel[pos[i]] = -2;
 }
@@ -840,62 +914,62 @@ __global__ void k_mark_members(const uint64_t *__restrict__ pos, uint64_t nm, in
 // Row groups of probe keys sorted by their high word (the out column): rows
 // that share it with a neighbour.  gsel[n] receives -1 for lone rows, -2 for
 // group members and, at each group's first row, the group number; mkeys /
-// hkeys (n entries each) receive the members' and the heads' keys.  Returns
-// the member count; *nh the group count.
-uint64_t group_rows(Ctx *ctx, const uint64_t *k, uint64_t n, int32_t *gsel, uint64_t *mkeys, uint64_t *hkeys,
-                    uint64_t *nh) {
-    *nh = 0;
-    if (!n) return 0;
+// mpos (n entries each) receive the members' keys and rows, hkeys / hpos (n
+// entries each, hpos optional) the heads' keys and rows; the member count
+// goes to *d_nm and the group count to *d_nh, on the device.
+void group_rows_async(Ctx *ctx, const uint64_t *k, uint64_t n, int32_t *gsel, uint64_t *mkeys, uint64_t *mpos,
+                      uint64_t *hkeys, uint64_t *hpos, uint64_t *d_nm, uint64_t *d_nh) {
+    if (!n) {
+        fill_u64(ctx, d_nm, 0ull, 1);
+        fill_u64(ctx, d_nh, 0ull, 1);
+        return;
+    }
     fill_u32(ctx, reinterpret_cast<uint32_t *>(gsel), 0xFFFFFFFFu, n);
-    Buf<uint64_t> mpos(ctx, n), cnt(ctx, 1);
-    select_group_members(ctx, k, n, mkeys, mpos.p, cnt.p);
-    ctx->read_scalars(cnt.p, 1);
-    const uint64_t nm = ctx->host_scalars[0];
-    if (!nm) return 0;
-    hipLaunchKernelGGL(k_mark_members, dim3(grid_for(nm, 256, 16384)), dim3(256), 0, ctx->stream, mpos.p, nm, gsel);
+    select_group_members(ctx, k, n, mkeys, mpos, d_nm);
+    hipLaunchKernelGGL(k_mark_members, dim3(grid_for(n, 256, (unsigned)ctx->num_cus * 4)), dim3(256), 0, ctx->stream,
+                       mpos, n, gsel, d_nm);
     XH_CHECK_HIP(hipGetLastError());
-    select_group_heads(ctx, mkeys, nm, mpos.p, hkeys, gsel, cnt.p);
-    ctx->read_scalars(cnt.p, 1);
-    *nh = ctx->host_scalars[0];
-    return nm;
+    select_group_heads(ctx, mkeys, n, mpos, hkeys, gsel, d_nh, d_nm, hpos);
 }
 void group_segments(Ctx *ctx, const uint64_t *sorted, uint64_t n, const uint64_t *head_keys, uint64_t nh,
-                    uint64_t *seg) {
+                    uint64_t *seg, const uint64_t *d_n) {
     if (!nh) return;
     hipLaunchKernelGGL(k_find_segments, dim3(grid_for(nh, 256, 16384)), dim3(256), 0, ctx->stream, sorted, n,
-                       head_keys, nh, seg, nullptr);
+                       head_keys, nh, seg, nullptr, d_n);
     XH_CHECK_HIP(hipGetLastError());
 }
 
 // Sorts the runs of equal high word named by heads[0..nh) inside sorted-by-
 // high-word data[0..n).  Runs of up to one wave are sorted in registers, up
-// to SEG_MAX keys in LDS, longer ones by the radix sort on the slice.
-void sort_segments(Ctx *ctx, uint64_t *data, uint64_t n, const uint64_t *heads, uint64_t nh) {
+// to SEG_MAX keys in LDS, longer ones by the radix sort on the slice.  The
+// async part finds the runs (seg: 2 * nh entries) and sorts those of up to one
+// wave, with the longest run's length in *d_max; sort_segments_long sorts the
+// longer ones once the host knows that length.
+void sort_segments_async(Ctx *ctx, uint64_t *data, uint64_t n, const uint64_t *heads, uint64_t nh, uint64_t *seg,
+                         unsigned long long *d_max) {
+    fill_u64(ctx, reinterpret_cast<uint64_t *>(d_max), 0ull, 1);
     if (!nh || !n) return;
-    Buf<uint64_t> seg(ctx, 2 * nh);
-    Buf<unsigned long long> mx(ctx, 1);
-    fill_u64(ctx, reinterpret_cast<uint64_t *>(mx.p), 0ull, 1);
     hipLaunchKernelGGL(k_find_segments, dim3(grid_for(nh, 256, 16384)), dim3(256), 0, ctx->stream, data, n, heads,
-                       nh, seg.p, mx.p);
+                       nh, seg, d_max, nullptr);
     XH_CHECK_HIP(hipGetLastError());
     // segments of up to 64 keys (the common case: probe rows sharing an out
     // column) need no host round trip: one wave per segment, all segments
     hipLaunchKernelGGL(k_segsort_wave, dim3((unsigned)((nh + SEGW_WAVES - 1) / SEGW_WAVES)), dim3(SEGW_WAVES * WAVE),
-                       0, ctx->stream, data, seg.p, nullptr, nh);
+                       0, ctx->stream, data, seg, nullptr, nh);
     XH_CHECK_HIP(hipGetLastError());
-    ctx->read_scalars(mx.p, 1);
-    const uint64_t max_len = ctx->host_scalars[0];
+}
+void sort_segments_long(Ctx *ctx, uint64_t *data, const uint64_t *seg, uint64_t nh, uint64_t max_len) {
     if (max_len <= (uint64_t)WAVE) return;
     for (uint64_t off = 0; off < nh; off += (1u << 30)) {
         const uint64_t cnt = std::min<uint64_t>(nh - off, 1u << 30);
-        hipLaunchKernelGGL(k_segsort, dim3((unsigned)cnt), dim3(256), 0, ctx->stream, data, seg.p, off);
+        hipLaunchKernelGGL(k_segsort, dim3((unsigned)cnt), dim3(256), 0, ctx->stream, data, seg, off);
         XH_CHECK_HIP(hipGetLastError());
     }
     if (max_len <= (uint64_t)SEG_MAX) return;
     // longer segments: radix sort of the slice (low words; the high words are
     // equal inside a segment)
     std::vector<uint64_t> h(2 * nh);
-    XH_CHECK_HIP(hipMemcpyAsync(h.data(), seg.p, 2 * nh * sizeof(uint64_t), hipMemcpyDeviceToHost, ctx->stream));
+    XH_CHECK_HIP(hipMemcpyAsync(h.data(), seg, 2 * nh * sizeof(uint64_t), hipMemcpyDeviceToHost, ctx->stream));
     ctx->sync();
     for (uint64_t i = 0; i < nh; ++i) {
         const uint64_t st = h[2 * i], len = h[2 * i + 1];
@@ -909,7 +983,6 @@ void sort_segments(Ctx *ctx, uint64_t *data, uint64_t n, const uint64_t *heads, 
         ctx->free(b);
     }
 }
-
 }  // namespace xh
 
 namespace xh {
@@ -986,7 +1059,7 @@ uint64_t nested_loop_join(Ctx *ctx, const uint64_t *l, uint64_t nl, int la, int 
 }
 
 void scan_u64_small(Ctx *ctx, uint64_t *a, uint64_t n, uint64_t *total) {
-    hipLaunchKernelGGL(k_scan_small, dim3(1), dim3(1024), 0, ctx->stream, a, n, total, nullptr, 0ull);
+    hipLaunchKernelGGL(k_scan_small, dim3(1), dim3(1024), 0, ctx->stream, a, n, total);
     XH_CHECK_HIP(hipGetLastError());
 }
 }  // namespace xh

@@ -116,7 +116,8 @@ template <class Sel>
 __global__ __launch_bounds__(SelShape<Sel>::block) void k_select(const uint64_t *__restrict__ in, uint64_t n, Sel sel,
                                                       uint64_t *__restrict__ d_count, uint64_t *status,
                                                       uint64_t epoch_tag, unsigned long long *ticket,
-                                                      unsigned long long ticket_base, uint64_t ntiles) {
+                                                      unsigned long long ticket_base, uint64_t ntiles,
+                                                      const uint64_t *d_n) {
     __shared__ uint64_t s_tile;
     __shared__ uint64_t s_prefix;
     constexpr int SEL_WAVES = SelShape<Sel>::waves;
@@ -124,13 +125,16 @@ __global__ __launch_bounds__(SelShape<Sel>::block) void k_select(const uint64_t 
     __shared__ uint32_t s_wc[SEL_WAVES];
     __shared__ uint64_t s_sel[4];
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
+    // a row count still on the device replaces the bound the grid was sized
+    // for; tiles past it select nothing but keep the look-back chain
+    if (d_n) n = *d_n < n ? *d_n : n;
     if (tid == 0) {
         uint64_t t = atomicAdd(ticket, 1ull) - ticket_base;
         s_tile = t;
         if constexpr (!Sel::kWindow) {
             uint64_t first = t * SEL_TILE, last = first + SEL_TILE;
             if (last > n) last = n;
-            sel.setup(first, last - 1, s_sel, 0);
+            if (first < last) sel.setup(first, last - 1, s_sel, 0);
         }
     }
     __syncthreads();
@@ -234,6 +238,22 @@ struct SelUnique {
         return idx == 0 || prev != key;
     }
     __device__ void emit(uint64_t pos, uint64_t, uint64_t key) const { out[pos] = key; }
+};
+
+// unique rows and, beside them, their low words (a join build's payloads)
+struct SelUniqueLow {
+    const uint64_t *in;
+    uint64_t *out;
+    uint32_t *low;
+    static constexpr bool kWindow = false;
+    __device__ void setup(uint64_t, uint64_t, uint64_t *, int) const {}
+    __device__ bool flag(uint64_t idx, uint64_t key, uint64_t prev, const uint64_t *) const {
+        return idx == 0 || prev != key;
+    }
+    __device__ void emit(uint64_t pos, uint64_t, uint64_t key) const {
+        out[pos] = key;
+        low[pos] = (uint32_t)key;
+    }
 };
 
 // First position p in a[lo, hi) with !(a[p] < key) (UPPER: !(a[p] <= key)),
@@ -348,6 +368,7 @@ struct SelGroupHeads {
     const uint64_t *mpos;
     uint64_t *out_key;
     int32_t *gsel;
+    uint64_t *out_pos;  // optional: the head's original row
     static constexpr bool kWindow = false;
     __device__ void setup(uint64_t, uint64_t, uint64_t *, int) const {}
     __device__ bool flag(uint64_t idx, uint64_t key, uint64_t prev, const uint64_t *) const {
@@ -355,7 +376,9 @@ struct SelGroupHeads {
     }
     __device__ void emit(uint64_t pos, uint64_t idx, uint64_t key) const {
         out_key[pos] = key;
-        gsel[mpos[idx]] = (int32_t)pos;
+        const uint64_t p = mpos[idx];
+        gsel[p] = (int32_t)pos;
+        if (out_pos) out_pos[pos] = p;
     }
 };
 
@@ -465,6 +488,69 @@ __global__ __launch_bounds__(SCAN_BLOCK) void k_scan_u32(uint32_t *a, uint64_t n
         for (int k = 0; k < SCAN_ITEMS; ++k)
             if (base + k < n) a[base + k] = off + v[k];
     }
+}
+
+// ---- exclusive scan of u64 counts, in place --------------------------------
+// The probe's per-tile output counts.  Same single pass as k_scan_u32; the
+// look-back words carry 39-bit values, and the exact u64 total is added up
+// separately (one atomic per tile): a caller whose total reaches 2^39 must not
+// use the prefixes (no bag that large fits a device anyway).
+constexpr int SCAN64_BLOCK = 1024;
+constexpr int SCAN64_ITEMS = 8;
+constexpr uint64_t SCAN64_TILE = (uint64_t)SCAN64_BLOCK * SCAN64_ITEMS;
+
+__global__ __launch_bounds__(SCAN64_BLOCK) void k_scan_u64(uint64_t *a, uint64_t n, uint64_t *status,
+                                                           uint64_t epoch_tag, unsigned long long *ticket,
+                                                           unsigned long long ticket_base,
+                                                           unsigned long long *d_total) {
+    __shared__ uint64_t s_tile;
+    __shared__ uint64_t s_prefix;
+    __shared__ uint64_t s_wsum[SCAN64_BLOCK / WAVE];
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
+    if (tid == 0) s_tile = atomicAdd(ticket, 1ull) - ticket_base;
+    __syncthreads();
+    const uint64_t tile = s_tile;
+    const uint64_t base = tile * SCAN64_TILE + (uint64_t)tid * SCAN64_ITEMS;
+    uint64_t v[SCAN64_ITEMS];
+#pragma unroll
+    for (int k = 0; k < SCAN64_ITEMS; ++k) v[k] = base + k < n ? a[base + k] : 0ull;
+    uint64_t sum = 0;
+#pragma unroll
+    for (int k = 0; k < SCAN64_ITEMS; ++k) {
+        const uint64_t x = v[k];
+        v[k] = sum;
+        sum += x;
+    }
+    uint64_t incl = sum;
+#pragma unroll
+    for (int o = 1; o < WAVE; o <<= 1) {
+        const uint64_t t = __shfl_up(incl, o, WAVE);
+        if (lane >= o) incl += t;
+    }
+    if (lane == WAVE - 1) s_wsum[wave] = incl;
+    __syncthreads();
+    uint64_t wpre = 0, tile_sum = 0;
+#pragma unroll
+    for (int w = 0; w < SCAN64_BLOCK / WAVE; ++w) {
+        if (w < wave) wpre += s_wsum[w];
+        tile_sum += s_wsum[w];
+    }
+    if (wave == 0) {
+        if (tid == 0) {
+            lb_store(status + tile, epoch_tag | (tile == 0 ? LB_INC : 0ull) | (tile_sum & LB_VAL));
+            if (tile_sum) atomicAdd(d_total, (unsigned long long)tile_sum);
+        }
+        const uint64_t prefix = tile ? lookback_wave(status, tile, epoch_tag, lane) : 0ull;
+        if (tid == 0) {
+            if (tile) lb_store(status + tile, epoch_tag | LB_INC | ((prefix + tile_sum) & LB_VAL));
+            s_prefix = prefix;
+        }
+    }
+    __syncthreads();
+    const uint64_t off = s_prefix + wpre + (incl - sum);
+#pragma unroll
+    for (int k = 0; k < SCAN64_ITEMS; ++k)
+        if (base + k < n) a[base + k] = off + v[k];
 }
 
 // ---- merge path -----------------------------------------------------------
@@ -589,8 +675,12 @@ static uint64_t *select_status(Ctx *ctx, uint64_t tiles, uint64_t *epoch_tag) {
     return st.status;
 }
 
+// d_n (optional, not for window selections): the row count on the device,
+// at most n, which is then only the bound the grid is sized for
 template <class Sel>
-static void run_select(Ctx *ctx, const uint64_t *in, uint64_t n, const Sel &sel, uint64_t *d_count) {
+static void run_select(Ctx *ctx, const uint64_t *in, uint64_t n, const Sel &sel, uint64_t *d_count,
+                       const uint64_t *d_n = nullptr) {
+    XH_REQUIRE(!(d_n && Sel::kWindow), XLOG_HIP_INVALID_ARG, "select: a device row count needs a plain selection");
     if (n == 0) {
         fill_u64(ctx, d_count, 0ull, 1);
         return;
@@ -604,12 +694,15 @@ static void run_select(Ctx *ctx, const uint64_t *in, uint64_t n, const Sel &sel,
     Prof prof(ctx, XLOG_HIP_KERNEL_SELECT, 8.0 * (double)n);
     const size_t dyn = Sel::kWindow ? (size_t)WIN_CAP * sizeof(uint64_t) : 0;
     hipLaunchKernelGGL(k_select<Sel>, dim3((unsigned)tiles), dim3(SelShape<Sel>::block), dyn, ctx->stream, in, n, sel, d_count,
-                       status, tag, ctx->tickets + 1, tb, tiles);
+                       status, tag, ctx->tickets + 1, tb, tiles, d_n);
     XH_CHECK_HIP(hipGetLastError());
 }
 
-void select_unique(Ctx *ctx, const uint64_t *k, uint64_t n, uint64_t *out, uint64_t *d_count) {
-    run_select(ctx, k, n, SelUnique{k, out}, d_count);
+void select_unique(Ctx *ctx, const uint64_t *k, uint64_t n, uint64_t *out, uint64_t *d_count, const uint64_t *d_n) {
+    run_select(ctx, k, n, SelUnique{k, out}, d_count, d_n);
+}
+void select_unique_low(Ctx *ctx, const uint64_t *k, uint64_t n, uint64_t *out, uint32_t *low, uint64_t *d_count) {
+    run_select(ctx, k, n, SelUniqueLow{k, out, low}, d_count);
 }
 void select_unique_diff(Ctx *ctx, const uint64_t *k, uint64_t n, const uint64_t *b, uint64_t nb, uint64_t *out,
                         uint64_t *d_count) {
@@ -627,12 +720,26 @@ void select_group_members(Ctx *ctx, const uint64_t *k, uint64_t n, uint64_t *mke
     run_select(ctx, k, n, SelGroupMembers{k, n, mkeys, mpos}, d_count);
 }
 void select_group_heads(Ctx *ctx, const uint64_t *mkeys, uint64_t nm, const uint64_t *mpos, uint64_t *hkeys,
-                        int32_t *gsel, uint64_t *d_count) {
+                        int32_t *gsel, uint64_t *d_count, const uint64_t *d_n, uint64_t *hpos) {
     XH_REQUIRE(nm < (1ull << 31), XLOG_HIP_CAPACITY_OVERFLOW, "join: too many grouped probe rows");
-    run_select(ctx, mkeys, nm, SelGroupHeads{mpos, hkeys, gsel}, d_count);
+    run_select(ctx, mkeys, nm, SelGroupHeads{mpos, hkeys, gsel, hpos}, d_count, d_n);
 }
-void select_runs(Ctx *ctx, const uint64_t *k, uint64_t n, uint32_t *run_key, uint64_t *run_start, uint64_t *d_count) {
-    run_select(ctx, k, n, SelRuns{k, run_key, run_start}, d_count);
+void select_runs(Ctx *ctx, const uint64_t *k, uint64_t n, uint32_t *run_key, uint64_t *run_start, uint64_t *d_count,
+                 const uint64_t *d_n) {
+    run_select(ctx, k, n, SelRuns{k, run_key, run_start}, d_count, d_n);
+}
+
+void scan_u64_inplace(Ctx *ctx, uint64_t *a, uint64_t n, uint64_t *d_total) {
+    fill_u64(ctx, d_total, 0ull, 1);
+    if (n == 0) return;
+    const uint64_t tiles = (n + SCAN64_TILE - 1) / SCAN64_TILE;
+    XH_REQUIRE(tiles < (1ull << 31), XLOG_HIP_CAPACITY_OVERFLOW, "scan: input too large");
+    uint64_t tag;
+    uint64_t *status = select_status(ctx, tiles, &tag);
+    unsigned long long tb = ctx->take_tickets(1, tiles);
+    hipLaunchKernelGGL(k_scan_u64, dim3((unsigned)tiles), dim3(SCAN64_BLOCK), 0, ctx->stream, a, n, status, tag,
+                       ctx->tickets + 1, tb, reinterpret_cast<unsigned long long *>(d_total));
+    XH_CHECK_HIP(hipGetLastError());
 }
 
 void scan_u32_inplace(Ctx *ctx, uint32_t *a, uint64_t n, unsigned long long *d_total) {

@@ -51,8 +51,6 @@ constexpr int SORT_BLOCK_K = XH_SORT_BLOCK_K, SORT_ITEMS_K = XH_SORT_ITEMS_K;
 constexpr int SORT_BLOCK_V = XH_SORT_BLOCK_V, SORT_ITEMS_V = XH_SORT_ITEMS_V;
 static_assert(SORT_BLOCK_K >= 256 && SORT_BLOCK_K % 256 == 0 && SORT_BLOCK_V >= 256 && SORT_BLOCK_V % 256 == 0,
               "digit phase needs 256 threads");
-constexpr int HIST_SEG = 16;                // consecutive keys per thread (run-length aggregated)
-constexpr int HIST_TILE = 256 * HIST_SEG;   // keys staged in LDS per block iteration
 constexpr uint32_t ST_AGG = 1u << 30;
 constexpr uint32_t ST_INC = 2u << 30;
 constexpr uint32_t ST_VAL = (1u << 30) - 1;
@@ -64,85 +62,86 @@ __device__ __forceinline__ void st_status(uint32_t *p, uint32_t v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// ALL: every digit is counted (full-key sorts); otherwise only [dlo, dhi)
-template <bool ALL>
-__global__ __launch_bounds__(256) void k_hist8(const uint64_t *__restrict__ keys, uint64_t n,
-                                               uint32_t *__restrict__ ghist, int dlo, int dhi) {
-    // A tile of HIST_TILE keys is loaded coalesced into LDS (split into padded
-    // low / high word arrays so that a lane stride of HIST_SEG keys is bank
-    // conflict free); each thread then walks HIST_SEG consecutive keys and
-    // adds run lengths of equal digits, so sorted-ish inputs (runs of equal
-    // high words, e.g. join output grouped by probe row) issue one LDS atomic
-    // per run instead of colliding on one counter.
-    __shared__ uint32_t h[8][256];
-    __shared__ uint32_t s_lo[HIST_TILE + HIST_TILE / HIST_SEG];
-    __shared__ uint32_t s_hi[HIST_TILE + HIST_TILE / HIST_SEG];
-    const int tid = threadIdx.x;
-    for (int i = tid; i < 8 * 256; i += blockDim.x) (&h[0][0])[i] = 0;
-    const uint64_t gstride = (uint64_t)gridDim.x * HIST_TILE;
-    // keys of the next tile are prefetched into registers while the current
-    // tile is counted from LDS
-    uint64_t pre[HIST_SEG];
-    uint64_t t0 = (uint64_t)blockIdx.x * HIST_TILE;
+// Histograms of the digits [dlo, dhi) in one read of the keys.  A block of
+// HIST_BLOCK threads reads HIST_ITEMS keys per thread per round, coalesced
+// (key base + r * HIST_BLOCK + tid), with the next round's loads in flight,
+// and adds every counted digit to LDS counters held in HIST_COPIES interleaved
+// copies (lane l adds to copy l % HIST_COPIES), so that the random bins of one
+// instruction's lanes spread over more LDS banks: bank conflicts, not the
+// loads, bound a single-copy histogram of random keys (measured on MI355X over
+// 2^28 random keys: 0.54 ms with one copy, 0.47-0.51 ms with four; a plain
+// read of the keys takes 0.30 ms).  A digit that has one value in all of a
+// wave's keys of the round (the constant digits of a narrow domain, the high
+// words of a run of equal keys) is added once by the wave's first lane
+// instead of by every lane on one counter.
+constexpr int HIST_BLOCK = 512, HIST_ITEMS = 8, HIST_COPIES = 4;
+__global__ __launch_bounds__(HIST_BLOCK) void k_hist8(const uint64_t *__restrict__ keys, uint64_t n,
+                                                      uint32_t *__restrict__ ghist, int dlo, int dhi) {
+    __shared__ uint32_t h[8 * 256 * HIST_COPIES];
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
+    for (int i = tid; i < 8 * 256 * HIST_COPIES; i += HIST_BLOCK) h[i] = 0;
+    __syncthreads();
+    uint32_t *hs = h + (lane % HIST_COPIES);
+    const uint32_t counted = (0xFFu >> (8 - dhi)) & ~((1u << dlo) - 1u);  // digits [dlo, dhi)
+    const uint64_t round = (uint64_t)HIST_BLOCK * HIST_ITEMS, gstride = (uint64_t)gridDim.x * round;
+    uint64_t pre[HIST_ITEMS];
+    uint64_t t0 = (uint64_t)blockIdx.x * round;
 #pragma unroll
-    for (int r = 0; r < HIST_SEG; ++r) {
-        uint64_t j = t0 + r * 256 + tid;
+    for (int r = 0; r < HIST_ITEMS; ++r) {
+        const uint64_t j = t0 + (uint64_t)r * HIST_BLOCK + tid;
         pre[r] = j < n ? __builtin_nontemporal_load(keys + j) : 0ull;
     }
     for (; t0 < n; t0 += gstride) {
-        const uint32_t cnt = (n - t0) < (uint64_t)HIST_TILE ? (uint32_t)(n - t0) : (uint32_t)HIST_TILE;
-        __syncthreads();
+        uint64_t k[HIST_ITEMS];
 #pragma unroll
-        for (int r = 0; r < HIST_SEG; ++r) {
-            uint32_t j = r * 256 + tid;
-            if (j < cnt) {
-                uint32_t pj = j + (j / HIST_SEG);
-                s_lo[pj] = (uint32_t)pre[r];
-                s_hi[pj] = (uint32_t)(pre[r] >> 32);
-            }
-        }
+        for (int r = 0; r < HIST_ITEMS; ++r) k[r] = pre[r];
         const uint64_t t1 = t0 + gstride;
 #pragma unroll
-        for (int r = 0; r < HIST_SEG; ++r) {
-            uint64_t j = t1 + r * 256 + tid;
+        for (int r = 0; r < HIST_ITEMS; ++r) {
+            const uint64_t j = t1 + (uint64_t)r * HIST_BLOCK + tid;
             pre[r] = j < n ? __builtin_nontemporal_load(keys + j) : 0ull;
         }
-        __syncthreads();
-        const uint32_t base = tid * HIST_SEG;
-        if (base < cnt) {
-            const uint32_t m = (cnt - base) < (uint32_t)HIST_SEG ? cnt - base : (uint32_t)HIST_SEG;
-            const uint32_t pb = base + tid;  // padded index of key `base`
-            uint32_t lo = s_lo[pb], hi = s_hi[pb];
-            uint32_t cur[8], run[8];
+        // the wave's valid keys in this round (scalar) and the digits on which
+        // some valid key differs from the first lane's first key
+        const uint64_t wb = t0 + (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane(wave) * WAVE;
+        uint32_t wtot = 0;
 #pragma unroll
-            for (int d = 0; d < 8; ++d) {
-                cur[d] = ((d < 4 ? lo : hi) >> (8 * (d & 3))) & 255u;
-                run[d] = 1;
+        for (int r = 0; r < HIST_ITEMS; ++r) {
+            const uint64_t b = wb + (uint64_t)r * HIST_BLOCK;
+            wtot += b >= n ? 0u : (n - b >= (uint64_t)WAVE ? (uint32_t)WAVE : (uint32_t)(n - b));
+        }
+        if (wtot == 0) continue;  // wave-uniform: past the end
+        const uint64_t k0 = (uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)k[0]) |
+                            ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(k[0] >> 32)) << 32);
+        uint64_t x = 0;
+#pragma unroll
+        for (int r = 0; r < HIST_ITEMS; ++r) {
+            const uint64_t j = t0 + (uint64_t)r * HIST_BLOCK + tid;
+            x |= j < n ? k[r] ^ k0 : 0ull;
+        }
+        uint32_t varying = 0;
+#pragma unroll
+        for (int d = 0; d < 8; ++d) varying |= (__ballot(((x >> (8 * d)) & 255u) != 0) ? 1u : 0u) << d;
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+            if (!((counted >> d) & 1u)) continue;
+            if (!((varying >> d) & 1u)) {
+                if (lane == 0) atomicAdd(&hs[(d * 256 + (uint32_t)((k0 >> (8 * d)) & 255u)) * HIST_COPIES], wtot);
+                continue;
             }
-            for (uint32_t j = 1; j < m; ++j) {
-                lo = s_lo[pb + j];
-                hi = s_hi[pb + j];
 #pragma unroll
-                for (int d = 0; d < 8; ++d) {
-                    if (!ALL && (d < dlo || d >= dhi)) continue;  // digits the caller does not sort on (uniform)
-                    uint32_t dg = ((d < 4 ? lo : hi) >> (8 * (d & 3))) & 255u;
-                    if (dg == cur[d]) {
-                        ++run[d];
-                    } else {
-                        atomicAdd(&h[d][cur[d]], run[d]);
-                        cur[d] = dg;
-                        run[d] = 1;
-                    }
-                }
+            for (int r = 0; r < HIST_ITEMS; ++r) {
+                const uint64_t j = t0 + (uint64_t)r * HIST_BLOCK + tid;
+                if (j < n) atomicAdd(&hs[(d * 256 + (uint32_t)((k[r] >> (8 * d)) & 255u)) * HIST_COPIES], 1u);
             }
-#pragma unroll
-            for (int d = 0; d < 8; ++d)
-                if (ALL || (d >= dlo && d < dhi)) atomicAdd(&h[d][cur[d]], run[d]);
         }
     }
     __syncthreads();
-    for (int i = tid; i < 8 * 256; i += blockDim.x) {
-        uint32_t c = (&h[0][0])[i];
+    for (int i = tid; i < 8 * 256; i += HIST_BLOCK) {
+        if (!((counted >> (i >> 8)) & 1u)) continue;
+        uint32_t c = 0;
+#pragma unroll
+        for (int q = 0; q < HIST_COPIES; ++q) c += h[i * HIST_COPIES + q];
         if (c) atomicAdd(&ghist[i], c);
     }
 }
@@ -497,14 +496,14 @@ int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **va
     const unsigned grid = (unsigned)(8 * ((nchunks + 7) / 8) * chunk);  // blocks past the last tile exit
 
     fill_u32(ctx, hist, 0u, 8 * 256);
-    unsigned hg = grid_for(n, HIST_TILE, (unsigned)ctx->num_cus * 3);
     {
         Prof prof(ctx, XLOG_HIP_KERNEL_SORT_HIST, 8.0 * (double)n);  // reads every key once
-        if (digit_lo == 0 && digit_hi == 8)
-            hipLaunchKernelGGL(k_hist8<true>, dim3(hg), dim3(256), 0, ctx->stream, src ? src : *keys, n, hist, 0, 8);
-        else
-            hipLaunchKernelGGL(k_hist8<false>, dim3(hg), dim3(256), 0, ctx->stream, src ? src : *keys, n, hist,
-                               digit_lo, digit_hi);
+        // at least 4 rounds per block: every block ends with up to 2048 device-scope atomics, which cost more
+        // than the counting when blocks have little to count (2^24 keys: 62 us with one round per block, 47 us
+        // with 4, 60 us with 16)
+        const unsigned hg = grid_for(n, (unsigned)(HIST_BLOCK * HIST_ITEMS) * 4, (unsigned)ctx->num_cus * 8);
+        hipLaunchKernelGGL(k_hist8, dim3(hg), dim3(HIST_BLOCK), 0, ctx->stream, src ? src : *keys, n, hist, digit_lo,
+                           digit_hi);
     }
     XH_CHECK_HIP(hipGetLastError());
     hipLaunchKernelGGL(k_digit_offsets, dim3(1), dim3(64), 0, ctx->stream, hist, off);
