@@ -1224,23 +1224,29 @@ static xlog_hip_rel *op_join_project_dedup(Ctx *ctx, const xlog_hip_rel *l, cons
     const uint64_t *lkeys = lk_buf.p;
     // 2. build rows as (key << 32 | payload), sorted and unique, so that a probe
     //    row alone with its out column emits sorted, unique outputs
-    Buf<uint64_t> sk_buf;
-    sk_buf.ctx = ctx;
+    //    (the key word's radix passes, then each run of equal keys sorted by
+    //    payload in one pass; a run of more than 256 rows makes the build
+    //    rows take the payload's radix passes too, after the first read-back)
+    Buf<uint64_t> cnt(ctx, 5);  // unique build rows, runs, group members, groups, long run
+    Buf<uint64_t> kw_buf, sk_buf;
+    kw_buf.ctx = sk_buf.ctx = ctx;
     const uint64_t *sk;
     const bool canon = rk == 0 && (r->flags & REL_CANONICAL) != 0;
     if (canon) {
         sk = r->w[0];
-    } else if (rk == 0) {
-        sk_buf.p = sort_keys(ctx, r->w[0], nr, false, 0, 8);
-        sk = sk_buf.p;
+        fill_u64(ctx, cnt.p + 4, 0ull, 1);
     } else {
-        uint64_t *sw = static_cast<uint64_t *>(ctx->alloc(nr * sizeof(uint64_t)));
-        sk_buf.p = sw;
-        swap_words(ctx, r->w[0], nr, sw);
-        sk_buf.p = sort_keys(ctx, sw, nr, true, 0, 8);
+        if (rk == 0) {
+            kw_buf.p = sort_keys(ctx, r->w[0], nr, false, 4, 8);
+        } else {
+            kw_buf.p = static_cast<uint64_t *>(ctx->alloc(nr * sizeof(uint64_t)));
+            swap_words(ctx, r->w[0], nr, kw_buf.p);
+            kw_buf.p = sort_keys(ctx, kw_buf.p, nr, true, 4, 8);
+        }
+        sk_buf = Buf<uint64_t>(ctx, nr);
+        sort_short_runs(ctx, kw_buf.p, nr, sk_buf.p, cnt.p + 4);
         sk = sk_buf.p;
     }
-    Buf<uint64_t> cnt(ctx, 4);  // unique build rows, runs, group members, groups
     Buf<uint64_t> ub;
     JoinIndex J;
     J.payload = Buf<uint32_t>(ctx, nr);
@@ -1262,9 +1268,20 @@ static xlog_hip_rel *op_join_project_dedup(Ctx *ctx, const xlog_hip_rel *l, cons
     Buf<int32_t> gsel(ctx, n);
     Buf<uint64_t> mkeys(ctx, n), mpos(ctx, n), hkeys(ctx, n), hpos(ctx, n);
     group_rows_async(ctx, lkeys, n, gsel.p, mkeys.p, mpos.p, hkeys.p, hpos.p, cnt.p + 2, cnt.p + 3);
-    ctx->read_scalars(cnt.p, 4);
-    const uint64_t un = d_un ? ctx->host_scalars[0] : nr, nruns = ctx->host_scalars[1];
+    ctx->read_scalars(cnt.p, 5);
+    uint64_t un = d_un ? ctx->host_scalars[0] : nr, nruns = ctx->host_scalars[1];
     const uint64_t nm = ctx->host_scalars[2], nh = ctx->host_scalars[3];
+    if (ctx->host_scalars[4]) {  // a long run: the full sort of the build rows
+        sk_buf = Buf<uint64_t>();
+        sk_buf.ctx = ctx;
+        sk_buf.p = sort_keys(ctx, kw_buf.p, nr, false, 0, 8);
+        select_unique_low(ctx, sk_buf.p, nr, ub.p, J.payload.p, cnt.p);
+        build_run_index_async(ctx, ub.p, nr, cnt.p, rs, cnt.p + 1);
+        ctx->read_scalars(cnt.p, 2);
+        un = ctx->host_scalars[0];
+        nruns = ctx->host_scalars[1];
+    }
+    kw_buf = Buf<uint64_t>();
     J.n = un;
     build_run_index_finish(ctx, rs, nruns, un, J.ix);
     sk_buf = Buf<uint64_t>();

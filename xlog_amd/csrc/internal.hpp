@@ -264,6 +264,11 @@ void rel_free(xlog_hip_rel *r);
 // domain) the passes are exactly those digits of [digit_lo, digit_hi) and the
 // histograms are not read back (a known digit that turns out constant costs a
 // stable copy).
+// Keys sorted by their high word to keys sorted in full, out of place: every
+// run of equal high word is sorted by the low word.  A run longer than 256
+// keys sets *d_long (device) and leaves the output incomplete; the caller then
+// sorts the input in full instead.
+void sort_short_runs(Ctx *ctx, const uint64_t *in, uint64_t n, uint64_t *out, uint64_t *d_long);
 int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **vals, uint32_t **vals_alt,
                    uint64_t n, int digit_lo = 0, int digit_hi = 8, const uint64_t *src = nullptr,
                    uint32_t known_digits = 0);

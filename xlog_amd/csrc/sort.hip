@@ -389,6 +389,110 @@ __global__ __launch_bounds__(BLOCK) void k_onesweep(
     }
 }
 
+// Sort of short runs: keys sorted by their high word, each run of equal high
+// word sorted by the full key (its low word) in place of the low word's radix
+// passes.  A block owns the runs that start in its core of SR_CORE keys and
+// loads the core with SR_MAX keys of halo on both sides.  Every loaded key's
+// run start and end come from a block-wide max-scan of run heads and min-scan
+// of run tails; each key of an owned run then counts the run's smaller
+// keys (earlier equal keys count as smaller, so equal keys keep their order)
+// and that count is its place.  A run longer than SR_MAX keys sets *long_run
+// (its keys are then not placed and the caller sorts the whole input instead).
+constexpr int SR_BLOCK = 256, SR_CORE = 2048, SR_MAX = 256;
+constexpr int SR_LEN = SR_CORE + 2 * SR_MAX, SR_ITEMS = SR_LEN / SR_BLOCK;
+static_assert(SR_LEN % SR_BLOCK == 0, "short-run tile");
+__global__ __launch_bounds__(SR_BLOCK) void k_sort_short_runs(const uint64_t *__restrict__ in, uint64_t n,
+                                                              uint64_t *__restrict__ out, uint64_t *long_run) {
+    __shared__ uint64_t s_k[SR_LEN];
+    __shared__ uint32_t s_lo[SR_LEN];
+    __shared__ uint32_t s_wmax[SR_BLOCK / WAVE], s_wmin[SR_BLOCK / WAVE];
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
+    const uint64_t core_lo = (uint64_t)blockIdx.x * SR_CORE;
+    const uint64_t core_hi = core_lo + SR_CORE < n ? core_lo + SR_CORE : n;
+    const uint64_t lo = core_lo > (uint64_t)SR_MAX ? core_lo - SR_MAX : 0;
+    const uint64_t hi = core_hi + SR_MAX < n ? core_hi + SR_MAX : n;
+    const uint32_t len = (uint32_t)(hi - lo);
+    for (uint32_t i = tid; i < len; i += SR_BLOCK) {
+        const uint64_t k = in[lo + i];
+        s_k[i] = k;
+        s_lo[i] = (uint32_t)k;
+    }
+    __syncthreads();
+    // thread t owns SR_ITEMS consecutive keys: run start = last head at or
+    // before the key, run end = first tail at or after it, plus one
+    const uint32_t b0 = (uint32_t)tid * SR_ITEMS;
+    uint32_t hmax = 0, tmin = 0xFFFFFFFFu;
+    uint32_t st_loc[SR_ITEMS], en_loc[SR_ITEMS];
+#pragma unroll
+    for (int q = 0; q < SR_ITEMS; ++q) {
+        const uint32_t i = b0 + q;
+        const bool head = i < len && (i == 0 || (uint32_t)(s_k[i] >> 32) != (uint32_t)(s_k[i - 1] >> 32));
+        if (head) hmax = i;
+        st_loc[q] = hmax;
+    }
+#pragma unroll
+    for (int q = SR_ITEMS - 1; q >= 0; --q) {
+        const uint32_t i = b0 + q;
+        const bool tail = i < len && (i + 1 == len || (uint32_t)(s_k[i] >> 32) != (uint32_t)(s_k[i + 1] >> 32));
+        if (tail) tmin = i + 1;
+        en_loc[q] = tmin;
+    }
+    // exclusive max-scan of the threads' last heads and min-scan (from the
+    // right) of their first tails over the block
+    uint32_t incl_max = hmax, incl_min = tmin;
+#pragma unroll
+    for (int o = 1; o < WAVE; o <<= 1) {
+        const uint32_t a = __shfl_up(incl_max, o, WAVE);
+        const uint32_t c = __shfl_down(incl_min, o, WAVE);
+        if (lane >= o) incl_max = a > incl_max ? a : incl_max;
+        if (lane + o < WAVE) incl_min = c < incl_min ? c : incl_min;
+    }
+    if (lane == WAVE - 1) s_wmax[wave] = incl_max;
+    if (lane == 0) s_wmin[wave] = incl_min;
+    __syncthreads();
+    uint32_t before = __shfl_up(incl_max, 1, WAVE), after = __shfl_down(incl_min, 1, WAVE);
+    if (lane == 0) before = 0;
+    if (lane == WAVE - 1) after = 0xFFFFFFFFu;
+#pragma unroll
+    for (int w = 0; w < SR_BLOCK / WAVE; ++w) {
+        if (w < wave) before = s_wmax[w] > before ? s_wmax[w] : before;
+        if (w > wave) after = s_wmin[w] < after ? s_wmin[w] : after;
+    }
+    bool longr = false;
+#pragma unroll
+    for (int q = 0; q < SR_ITEMS; ++q) {
+        const uint32_t li = b0 + q;
+        if (li >= len || lo + li < core_lo) continue;
+        const uint32_t st = st_loc[q] > before ? st_loc[q] : before;
+        const uint32_t e = en_loc[q] < after ? en_loc[q] : after;
+        if (e - st > (uint32_t)SR_MAX) {  // a run of more than SR_MAX keys
+            longr = true;
+            continue;
+        }
+        // runs that start before the core (or may start before the loaded
+        // keys) or after it belong to other blocks
+        if (lo + st < core_lo || lo + st >= core_hi) continue;
+        if (e == len && hi < n && (uint32_t)(in[hi] >> 32) == (uint32_t)(s_k[li] >> 32)) {  // continues past the halo
+            longr = true;
+            continue;
+        }
+        // The run shares the high word, so (low word, position) orders it:
+        // one 64-bit compare per key of the run, four loads in flight.
+        const uint64_t mine = ((uint64_t)s_lo[li] << 32) | li;
+        uint32_t r = 0, j = st;
+        for (; j + 4 <= e; j += 4) {
+            uint32_t cj[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) cj[u] = s_lo[j + u];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) r += ((((uint64_t)cj[u] << 32) | (j + u)) < mine) ? 1u : 0u;
+        }
+        for (; j < e; ++j) r += ((((uint64_t)s_lo[j] << 32) | j) < mine) ? 1u : 0u;
+        out[lo + st + r] = s_k[li];
+    }
+    if (__ballot(longr) != 0 && lane == 0) *long_run = 1ull;
+}
+
 __global__ void k_fill_u32(uint32_t *p, uint32_t v, uint64_t n) {
     uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = v;
@@ -469,6 +573,16 @@ static uint32_t pass_capacity(Ctx *ctx) {
 static bool sort_tickets() {
     const char *e = getenv("XLOG_HIP_SORT_TICKETS");
     return e && e[0] == '1';
+}
+
+void sort_short_runs(Ctx *ctx, const uint64_t *in, uint64_t n, uint64_t *out, uint64_t *d_long) {
+    fill_u64(ctx, d_long, 0ull, 1);
+    if (!n) return;
+    const uint64_t blocks = (n + SR_CORE - 1) / SR_CORE;
+    XH_REQUIRE(blocks < (1ull << 31), XLOG_HIP_CAPACITY_OVERFLOW, "short-run sort: input too large");
+    Prof prof(ctx, XLOG_HIP_KERNEL_SORT_RUNS, 16.0 * (double)n);  // reads and writes every key once
+    hipLaunchKernelGGL(k_sort_short_runs, dim3((unsigned)blocks), dim3(SR_BLOCK), 0, ctx->stream, in, n, out, d_long);
+    XH_CHECK_HIP(hipGetLastError());
 }
 
 int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **vals, uint32_t **vals_alt,
