@@ -1,15 +1,18 @@
-"""GPU parity of the dense chain-rule route of the fixpoint (any program whose
-rule bodies are paths of binary relations) against the CPU oracle, which the
-CPU suite pins against boolean-matrix closed forms.  Every program also runs
-on the join route, and both must agree to the tuple, the iteration count and
-every per-iteration delta size."""
+"""GPU parity of the routes that take chain-rule programs (rule bodies that are
+paths of binary relations) against the CPU oracle, which the CPU suite pins
+against boolean-matrix closed forms: the dense bitmap route, the join route,
+and the hash-set route (bodies of up to three atoms, two hops around the delta
+atom).  All must agree to the tuple, the iteration count and every
+per-iteration delta size.  Programs over ids spread across u32 take the
+hash-set route under AUTO."""
 import sys
 
 import numpy as np
 import pytest
 
 import oracle
-from xlog_amd import ROUTE_AUTO, ROUTE_BITMAP, ROUTE_JOIN, XlogError, andersen_plan, datagen, pack, tc_plan
+from xlog_amd import (ROUTE_AUTO, ROUTE_BITMAP, ROUTE_HASH, ROUTE_JOIN, XlogError, andersen_plan, datagen, pack,
+                      tc_plan)
 
 import chain_plans as cp
 
@@ -33,7 +36,7 @@ def _run(p, plan, rels, route, **kw):
     return p.fixpoint(plan, dev, route=route, **kw)
 
 
-def _parity(p, name, plan, rels, idb, routes=(ROUTE_BITMAP, ROUTE_JOIN)):
+def _parity(p, name, plan, rels, idb, routes=(ROUTE_BITMAP, ROUTE_JOIN, ROUTE_HASH)):
     outs_o, it_o, deltas_o = oracle.seminaive(plan, rels)
     for route in routes:
         _note(f"chain {name} route={route}")
@@ -91,7 +94,11 @@ def test_symmetric_closure(provider, n, m, seed):
 def test_four_atom_chain(provider, n, seed):
     a_s, a_d = _graph(n, n, seed)
     b_s, b_d = _graph(n, n // 2, seed + 100)
-    _parity(provider, "quad", cp.quad_plan(), [pack(a_s, a_d), pack(b_s, b_d), None], [2])
+    rels = [pack(a_s, a_d), pack(b_s, b_d), None]
+    _parity(provider, "quad", cp.quad_plan(), rels, [2], routes=(ROUTE_BITMAP, ROUTE_JOIN))
+    with pytest.raises(XlogError) as ex:  # four atoms: three hops
+        _run(provider, cp.quad_plan(), rels, ROUTE_HASH)
+    assert ex.value.status == UNSUPPORTED
 
 
 def test_scrambled_body_order(provider):
@@ -102,10 +109,11 @@ def test_scrambled_body_order(provider):
     b_s, b_d = _graph(600, 500, 14)
     rels = [pack(a_s, a_d), pack(b_s, b_d), None]
     outs_o, it_o, deltas_o = oracle.seminaive(cp.ordered_chain_plan(), rels)
-    outs, st = _run(p, cp.scrambled_chain_plan(), rels, ROUTE_AUTO)
-    assert st["route"] == ROUTE_BITMAP
-    assert np.array_equal(p.download_packed(outs[2]), outs_o[2])
-    assert st["iterations"] == it_o and st["delta_sizes"] == deltas_o
+    for route, taken in ((ROUTE_AUTO, ROUTE_BITMAP), (ROUTE_HASH, ROUTE_HASH)):
+        outs, st = _run(p, cp.scrambled_chain_plan(), rels, route)
+        assert st["route"] == taken
+        assert np.array_equal(p.download_packed(outs[2]), outs_o[2])
+        assert st["iterations"] == it_o and st["delta_sizes"] == deltas_o
     with pytest.raises(XlogError) as ex:
         _run(p, cp.scrambled_chain_plan(), rels, ROUTE_JOIN)
     assert ex.value.status == UNSUPPORTED
@@ -120,7 +128,8 @@ def test_andersen_both_routes(provider, n_vars, n_facts):
 
 def test_domain_edges(provider):
     """Ids at the top of the 2^17 domain (2048-word rows, more stripes than waves), then one id past it:
-    AUTO falls back to the join route and an explicit bitmap request is refused."""
+    AUTO takes the hash-set route (the join route when a join-row limit is set) and an explicit bitmap
+    request is refused."""
     p = provider
     rng = np.random.default_rng(15)
     ids = np.sort(rng.choice(1 << 17, 400, replace=False)).astype(np.uint32)
@@ -132,8 +141,12 @@ def test_domain_edges(provider):
     _parity(p, "symmetric top of domain", cp.symmetric_plan(), [pack(s, d), None], [1])
     big = np.array([1 << 17], np.uint32)
     rels = [pack(np.append(s, big), np.append(d, ids[:1])), pack(hs, hd)]
-    outs, st = _run(p, tc_plan(), rels, ROUTE_AUTO)
-    assert st["route"] == ROUTE_JOIN
+    outs_o, it_o, deltas_o = oracle.seminaive(tc_plan(), rels)
+    for kw, taken in (({}, ROUTE_HASH), ({"max_join_rows": 1 << 40}, ROUTE_JOIN)):
+        outs, st = _run(p, tc_plan(), rels, ROUTE_AUTO, **kw)
+        assert st["route"] == taken
+        assert np.array_equal(p.download_packed(outs[1]), outs_o[1])
+        assert st["iterations"] == it_o and st["delta_sizes"] == deltas_o
     with pytest.raises(XlogError) as ex:
         _run(p, tc_plan(), rels, ROUTE_BITMAP)
     assert ex.value.status == UNSUPPORTED
@@ -153,3 +166,78 @@ def test_chain_route_errors(provider):
     with pytest.raises(XlogError) as ex:
         _run(p, both, [e, e, None], ROUTE_BITMAP)
     assert ex.value.status == UNSUPPORTED
+
+
+def _spread(*cols):
+    """The same relations with every id mapped by the bijection onto u32 that the sparse fixtures use."""
+    return [datagen.sparse_ids(np.asarray(c, np.uint32)) for c in cols]
+
+
+def _sparse_parity(p, name, plan, rels, idb, auto=ROUTE_HASH):
+    outs_o, it_o, deltas_o = oracle.seminaive(plan, rels)
+    for route in (ROUTE_AUTO, ROUTE_HASH, ROUTE_JOIN):
+        _note(f"sparse {name} route={route}")
+        outs, st = _run(p, plan, rels, route)
+        assert st["route"] == (auto if route == ROUTE_AUTO else route)
+        for q in idb:
+            assert np.array_equal(p.download_packed(outs[q]), outs_o[q]), f"{name} route {route} pred {q}"
+            assert outs[q].is_canonical()
+        assert st["iterations"] == it_o
+        assert st["delta_sizes"] == deltas_o
+        if st["route"] == ROUTE_HASH:  # one read-back per iteration, plus set-up
+            assert st["host_waits"] <= 2 * st["iterations"] + 40, st
+
+
+@pytest.mark.parametrize("n,m,seed", [(400, 700, 21), (1200, 1900, 22)])
+def test_sparse_ids_programs(provider, n, m, seed):
+    """Programs over ids spread across u32 (beyond the bitmap route's 2^17) on the hash-set route."""
+    p = provider
+    s, d = _spread(*_graph(n, m, seed))
+    e = pack(s, d)
+    _sparse_parity(p, "nonlinear tc", cp.nonlinear_tc_plan(), [e, None], [1])
+    _sparse_parity(p, "left tc", cp.left_tc_plan(), [e, None], [1])
+    _sparse_parity(p, "parity", cp.parity_plan(), [e, None, None], [1, 2])
+    _sparse_parity(p, "symmetric", cp.symmetric_plan(), [e, None], [1])
+    hs, hd = _spread(*_graph(n, m // 5, seed + 50))
+    _sparse_parity(p, "tc initial head", tc_plan(), [e, pack(hs, hd)], [1])
+
+
+@pytest.mark.parametrize("n,seed", [(600, 23), (4000, 24)])
+def test_sparse_ids_same_generation(provider, n, seed):
+    rng = np.random.default_rng(seed)
+    child = np.arange(1, n, dtype=np.uint32)
+    parent = np.array([rng.integers(max(0, int(c) - 40), int(c)) for c in child], dtype=np.uint32)
+    fs, fd = rng.integers(0, n, n // 4).astype(np.uint32), rng.integers(0, n, n // 4).astype(np.uint32)
+    c2, p2, f2s, f2d = _spread(child, parent, fs, fd)
+    _sparse_parity(provider, "sg up/down", cp.same_generation_plan(), [pack(f2s, f2d), pack(c2, p2), pack(p2, c2), None], [3])
+    _sparse_parity(provider, "sg par backward", cp.same_generation_par_plan(), [pack(f2s, f2d), pack(c2, p2), None], [2])
+
+
+@pytest.mark.parametrize("n_vars,n_facts", [(300, 1000), (3000, 12000)])
+def test_sparse_ids_andersen(provider, n_vars, n_facts):
+    """Andersen's points-to (the three-atom load and store rules: two hops around the delta atom, with
+    the full relation read through its indexes in both directions) over spread ids.  AUTO keeps such
+    rules (two IDB atoms in a three-atom body) on the join route."""
+    f = datagen.andersen(n_vars, n_facts, 1.5, datagen.seed_for(5))
+    rels = [pack(*_spread(*f[k])) for k in ("assign", "addressOf", "load", "store")] + [None]
+    _sparse_parity(provider, f"andersen {n_vars}", andersen_plan(), rels, [4], auto=ROUTE_JOIN)
+
+
+def test_hash_route_programs_rerun(provider, monkeypatch):
+    """A 64-slot table and 100 appends per attempt: every iteration of every head goes through the
+    grow-and-rerun protocol, with several variants sharing one head."""
+    p = provider
+    monkeypatch.setenv("XLOG_HIP_HASH_SLOTS", "64")
+    monkeypatch.setenv("XLOG_HIP_HASH_APPENDS", "100")
+    f = datagen.andersen(400, 1500, 1.5, datagen.seed_for(5))
+    rels = [pack(*f[k]) for k in ("assign", "addressOf", "load", "store")] + [None]
+    outs_o, it_o, deltas_o = oracle.seminaive(andersen_plan(), rels)
+    outs, st = _run(p, andersen_plan(), rels, ROUTE_HASH)
+    assert np.array_equal(p.download_packed(outs[4]), outs_o[4])
+    assert st["iterations"] == it_o and st["delta_sizes"] == deltas_o
+    s, d = _graph(500, 900, 25)
+    outs_o, it_o, deltas_o = oracle.seminaive(cp.parity_plan(), [pack(s, d), None, None])
+    outs, st = _run(p, cp.parity_plan(), [pack(s, d), None, None], ROUTE_HASH)
+    for q in (1, 2):
+        assert np.array_equal(p.download_packed(outs[q]), outs_o[q])
+    assert st["iterations"] == it_o and st["delta_sizes"] == deltas_o

@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 import oracle
-from xlog_amd import ROUTE_BITMAP, ROUTE_JOIN, andersen_plan, datagen, pack, tc_plan
+from xlog_amd import ROUTE_BITMAP, ROUTE_HASH, ROUTE_JOIN, andersen_plan, datagen, pack, tc_plan
 
 pytestmark = pytest.mark.gpu
 FX = json.loads((Path(__file__).parent / "golden" / "fixtures.json").read_text())
@@ -102,6 +102,8 @@ def test_c4_full_transitive_closure(provider, route):
     (ROUTE_BITMAP, "c5_10000_40000"), (ROUTE_JOIN, "c5_10000_40000"),
     (ROUTE_BITMAP, "c5_20000_80000"), (ROUTE_JOIN, "c5_20000_80000"),
     (ROUTE_BITMAP, "c5_40000_160000"),
+    # the hash-set route (two hops around the delta atom, no binary intermediate)
+    (ROUTE_HASH, "c5_2000_8000"), (ROUTE_HASH, "c5_10000_40000"),
 ])
 def test_c5_scaled_andersen_fixture(provider, fixture, route):
     e = FX[fixture]

@@ -106,11 +106,12 @@ def test_hash_route_empty_and_unsupported(provider):
     p = provider
     out, st = _tc(p, [], [], ROUTE_HASH)
     assert out.num_rows() == 0 and st["iterations"] == 1 and st["delta_sizes"] == [0, 0]
-    from xlog_amd import andersen_plan
-    f = datagen.andersen(500, 2000, 1.5, datagen.seed_for(5))
-    rels = [p.create_buffer_from_u32_columns(list(f[k])) for k in ("assign", "addressOf", "load", "store")]
+    # a body of four atoms is beyond the hash route's two hops
+    import chain_plans as cp
+    s, d = datagen.random_digraph(100, 150, 3)
+    e = p.create_buffer_from_u32_columns([np.asarray(s, np.uint32), np.asarray(d, np.uint32)])
     with pytest.raises(XlogError) as ex:
-        p.fixpoint(andersen_plan(), rels + [None], route=ROUTE_HASH)
+        p.fixpoint(cp.quad_plan(), [e, e, None], route=ROUTE_HASH)
     assert ex.value.status == UNSUPPORTED
 
 

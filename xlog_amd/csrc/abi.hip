@@ -1382,6 +1382,16 @@ static xlog_hip_rel *op_project(Ctx *ctx, const xlog_hip_rel *in, const std::vec
     return r;
 }
 
+// a positive integer from the environment, or dflt
+static uint64_t env_u64(const char *name, uint64_t dflt) {
+    const char *e = getenv(name);
+    if (e && *e) {
+        const unsigned long long v = strtoull(e, nullptr, 10);
+        if (v > 0) return v;
+    }
+    return dflt;
+}
+
 // ---------------------------------------------------------------------------
 // semi-naive fixpoint driver (Executor::execute_recursive_scc,
 // crates/xlog-runtime/src/executor/recursive.rs:447-957)
@@ -1634,15 +1644,16 @@ struct Driver {
         return ns == 1;
     }
 
-    uint64_t run(uint64_t max_iter, std::vector<uint64_t> &deltas) {
-        // seed: every rule once against the current store
+    // seed: every rule once against the current store; delta = new \ old,
+    // merged into full
+    void seed(std::vector<uint64_t> &deltas) {
         std::vector<std::vector<std::pair<uint64_t *, uint64_t>>> derived(n_preds);
         for (const Rule &r : rules) {
             const DRel *rel[MAX_BODY];
             for (int j = 0; j < r.nb; ++j) rel[j] = &full[r.b[j].pred];
             eval_body(r, rel, derived[r.head], nullptr);
         }
-        uint64_t seed = 0;
+        uint64_t total = 0;
         for (uint32_t p = 0; p < n_preds; ++p) {
             if (!idb[p]) continue;
             DRel d = finalize(derived[p], full[p]);  // full_new \ full_old
@@ -1652,9 +1663,13 @@ struct Driver {
                 full[p] = m;
             }
             delta[p] = d;
-            seed += d.n;
+            total += d.n;
         }
-        deltas.push_back(seed);
+        deltas.push_back(total);
+    }
+
+    uint64_t run(uint64_t max_iter, std::vector<uint64_t> &deltas) {
+        seed(deltas);
         // count jobs of the next iteration's pre-countable first joins, by (rule, occurrence)
         std::map<std::pair<int, int>, std::unique_ptr<ProbeJob>> pre;
         uint64_t it = 0;
@@ -1734,6 +1749,252 @@ struct Driver {
         throw Error{XLOG_HIP_ITERATION_LIMIT,
                     "Recursive SCC iteration limit (" + std::to_string(max_iter) + ") exceeded"};
     }
+
+    // The loop of run() over device hash sets, for path-shaped rules of at
+    // most three atoms (chains[ri]: rule ri as a path from its first head
+    // variable to its second).  The seed is run()'s.  The full relation of
+    // every IDB predicate also lives in a hash set; an iteration runs one
+    // expand-and-insert pass per variant (hs_path_insert: the delta atom's rows
+    // through the other atoms' run indexes, at most two hops, no intermediate
+    // relation), and the tuples the passes insert are the next delta: new
+    // against R and unique, with no sort, merge-diff or candidate bag.  One
+    // read-back per iteration brings every head's appended count and overflow
+    // flag.  A predicate that some variant reads in full (an IDB atom besides
+    // the delta atom) is sorted into its full relation every iteration, for
+    // the indexes; the others are collected from their set at the end.
+    uint64_t run_hash(uint64_t max_iter, std::vector<uint64_t> &deltas, const std::vector<ChainRule> &chains) {
+        XH_REQUIRE(chains.size() == rules.size(), XLOG_HIP_INVALID_ARG, "hash route: one path per rule");
+        std::vector<bool> indexed(n_preds, false);
+        for (const ChainRule &c : chains) {
+            XH_REQUIRE(c.path.size() >= 1 && c.path.size() <= 3, XLOG_HIP_UNSUPPORTED,
+                       "hash route: rule bodies of 1 to 3 atoms");
+            for (size_t d = 0; d < c.path.size(); ++d) {
+                if (!idb[c.path[d].pred]) continue;
+                for (size_t j = 0; j < c.path.size(); ++j)
+                    if (j != d && idb[c.path[j].pred]) indexed[c.path[j].pred] = true;
+            }
+        }
+        std::vector<HashSet> H(n_preds);
+        std::vector<Buf<uint64_t>> dcur(n_preds);  // the current delta rows (sorted only when indexed)
+        std::vector<uint64_t> dn(n_preds, 0);
+        for (uint32_t p = 0; p < n_preds; ++p) {
+            if (!idb[p]) continue;
+            hs_init(ctx, H[p], env_u64("XLOG_HIP_HASH_SLOTS", std::max<uint64_t>(4 * full[p].n, 1ull << 16)));
+            if (H[p].cap / 2 < full[p].n) hs_grow(ctx, H[p], 4 * full[p].n);
+            if (full[p].n) {
+                hs_insert_all(ctx, H[p], full[p].k, full[p].n);
+                H[p].size = full[p].n;
+            }
+        }
+        struct Var {
+            PathInsertArgs a;
+            bool copy = false;  // one-atom body: the delta rows themselves (swapped when `swap`)
+            bool swap = false;
+            double fanout = 1.0;  // expected head tuples per delta row
+        };
+        // appends allowed per attempt: the expected candidate count, a bound on the novel tuples
+        // (XLOG_HIP_HASH_APPENDS below 2^20 forces small attempts: tests of the rerun path)
+        const uint64_t min_want = env_u64("XLOG_HIP_HASH_APPENDS", 1ull << 20);
+        uint64_t it = 0;
+        // pass 0 is the seed: every rule once, its first path atom reading the whole relation (the
+        // tuples it inserts are T(R) minus R, run()'s seed); pass k > 0 is iteration k
+        for (uint64_t pass = 0;; ++pass) {
+            if (pass) {
+                XH_REQUIRE(it < max_iter, XLOG_HIP_ITERATION_LIMIT,
+                           "Recursive SCC iteration limit (" + std::to_string(max_iter) + ") exceeded");
+                ++it;
+            }
+            // the variants, grouped by head, with their hops at R of the previous pass
+            std::vector<std::vector<Var>> vars(n_preds);
+            for (size_t ri = 0; ri < chains.size(); ++ri) {
+                const std::vector<ChainAtom> &path = chains[ri].path;
+                const int m = (int)path.size();
+                for (int d = 0; d < m; ++d) {
+                    const int q = path[d].pred;
+                    Var v;
+                    if (pass == 0) {
+                        if (d != 0 || full[q].n == 0) continue;
+                        v.a.delta = full[q].k;
+                        v.a.n = full[q].n;
+                    } else {
+                        if (!idb[q] || dn[q] == 0) continue;
+                        v.a.delta = dcur[q].p;
+                        v.a.n = dn[q];
+                    }
+                    v.a.delta_swap = path[d].backward ? 1 : 0;
+                    // a hop through atom j: from x_{j+1} to x_j (left of the delta atom) or from
+                    // x_j to x_{j+1} (right of it); the stored tuple is (x_j, x_{j+1}) unless backward
+                    auto hop = [&](int j, bool left, PathHop &h) {
+                        const bool key_col1 = left != path[j].backward;
+                        const DRel &rel = full[path[j].pred];
+                        if (rel.n == 0) return false;
+                        const JoinIndex &J = index_of(rel, key_col1 ? 1 : 0);
+                        h.table = J.ix.table.p;
+                        h.mask = J.ix.table_mask;
+                        int bits = 0;
+                        while ((1ull << bits) < J.ix.table_mask + 1) ++bits;
+                        h.bits = bits;
+                        h.payload = J.payload.p;
+                        v.fanout *= J.ix.nruns ? (double)J.n / (double)J.ix.nruns : 0.0;
+                        return J.ix.nruns != 0;
+                    };
+                    bool live = true;
+                    if (m == 1) {
+                        v.copy = true;
+                        v.swap = path[0].backward;
+                    } else if (m == 2) {
+                        // d = 0: xb -> x2 (right); d = 1: xa -> x0 (left)
+                        live = hop(d == 0 ? 1 : 0, d == 1, v.a.h1);
+                        v.a.key1 = d == 0 ? 1 : 0;
+                        v.a.out0 = d == 0 ? 0 : 2;
+                        v.a.out1 = d == 0 ? 2 : 1;
+                    } else if (d == 0) {  // xb -> x2 -> x3
+                        live = hop(1, false, v.a.h1) && hop(2, false, v.a.h2);
+                        v.a.key1 = 1;
+                        v.a.key2 = 2;
+                        v.a.out0 = 0;
+                        v.a.out1 = 3;
+                    } else if (d == 1) {  // xa -> x0 and xb -> x3
+                        live = hop(0, true, v.a.h1) && hop(2, false, v.a.h2);
+                        v.a.key1 = 0;
+                        v.a.key2 = 1;
+                        v.a.out0 = 2;
+                        v.a.out1 = 3;
+                    } else {  // xa -> x1 -> x0
+                        live = hop(1, true, v.a.h1) && hop(0, true, v.a.h2);
+                        v.a.key1 = 0;
+                        v.a.key2 = 2;
+                        v.a.out0 = 3;
+                        v.a.out1 = 1;
+                    }
+                    if (live) vars[chains[ri].head].push_back(v);
+                }
+            }
+            std::vector<uint64_t> want(n_preds, 0), appended(n_preds, 0);
+            std::vector<Buf<uint64_t>> out(n_preds);
+            std::vector<uint32_t> todo;
+            for (uint32_t p = 0; p < n_preds; ++p) {
+                if (vars[p].empty()) continue;
+                // the candidates expected, but at most 4x the set and the delta rows (duplicate-heavy
+                // bodies, like the non-linear closure, expand to far more candidates than novel tuples;
+                // the rerun protocol covers an estimate that is too small)
+                double est = 0, rows = 0;
+                for (const Var &v : vars[p]) {
+                    est += (double)v.a.n * v.fanout;
+                    rows += (double)v.a.n;
+                }
+                est = std::min(est * 1.25, 4.0 * ((double)H[p].size + rows));
+                want[p] = min_want < (1ull << 20) ? min_want : std::max<uint64_t>(min_want, (uint64_t)est + 1024);
+                fill_u64(ctx, H[p].flags.p + 1, 0ull, 2);
+                todo.push_back(p);
+            }
+            std::vector<Buf<uint64_t>> swapped;  // one-atom bodies read backward
+            while (!todo.empty()) {
+                for (uint32_t p : todo) {
+                    HashSet &h = H[p];
+                    uint64_t room = h.cap / 2 > h.size + appended[p] ? h.cap / 2 - h.size - appended[p] : 0;
+                    if (room < want[p]) {
+                        // 4x what this step needs: R keeps growing, and every rehash re-inserts all of it
+                        hs_grow(ctx, h, 4 * (h.size + appended[p] + want[p]));
+                        room = h.cap / 2 - h.size - appended[p];
+                    }
+                    const uint64_t limit = appended[p] + std::min(want[p], room);
+                    // every launch appends at most HS_APPEND_SLACK past the limit
+                    const uint64_t need = limit + (uint64_t)vars[p].size() * HS_APPEND_SLACK;
+                    if (out[p].n < need) {
+                        Buf<uint64_t> bigger(ctx, need);
+                        if (appended[p]) copy_d2d(ctx, bigger.p, out[p].p, appended[p]);
+                        out[p] = std::move(bigger);
+                    }
+                    for (const Var &v : vars[p]) {
+                        if (v.copy) {
+                            const uint64_t *rows = v.a.delta;
+                            if (v.swap) {
+                                swapped.emplace_back(ctx, v.a.n);
+                                swap_words(ctx, v.a.delta, v.a.n, swapped.back().p);
+                                rows = swapped.back().p;
+                            }
+                            hs_insert_novel(ctx, h, rows, v.a.n, out[p].p, limit);
+                        } else {
+                            hs_path_insert(ctx, h, v.a, out[p].p, limit);
+                        }
+                    }
+                }
+                // one read-back: every head's overflow flag and appended count
+                Buf<uint64_t> g(ctx, 2 * todo.size());
+                for (size_t t = 0; t < todo.size(); ++t) copy_d2d(ctx, g.p + 2 * t, H[todo[t]].flags.p + 1, 2);
+                ctx->read_scalars(g.p, 2 * todo.size());
+                std::vector<uint32_t> again;
+                for (size_t t = 0; t < todo.size(); ++t) {
+                    const uint32_t p = todo[t];
+                    appended[p] = ctx->host_scalars[2 * t + 1];
+                    if (ctx->host_scalars[2 * t]) {
+                        // the limit or a full table stopped a pass: grow and run the head's passes again;
+                        // the tuples they inserted are found present and are not appended twice
+                        fill_u64(ctx, H[p].flags.p + 1, 0ull, 1);
+                        want[p] *= 4;
+                        again.push_back(p);
+                    }
+                }
+                todo.swap(again);
+            }
+            uint64_t total = 0;
+            for (uint32_t p = 0; p < n_preds; ++p) {
+                if (!idb[p]) continue;
+                total += appended[p];
+                H[p].size += appended[p];
+                dn[p] = appended[p];
+                if (!appended[p]) {
+                    dcur[p] = Buf<uint64_t>();
+                    continue;
+                }
+                if (indexed[p]) {
+                    // sorted: the delta joins R for the next pass's indexes
+                    uint64_t *sd = sort_keys(ctx, out[p].p, appended[p], false, 0, 8, digits);
+                    dcur[p] = Buf<uint64_t>();
+                    dcur[p].ctx = ctx;
+                    dcur[p].p = sd;
+                    dcur[p].n = appended[p];
+                    DRel d;
+                    d.k = sd;
+                    d.n = appended[p];
+                    d.owned = false;
+                    DRel m = merge(full[p], d);
+                    release(full[p]);
+                    full[p] = m;
+                } else {
+                    dcur[p] = std::move(out[p]);
+                }
+            }
+            deltas.push_back(total);
+            if (pass && total == 0) break;
+        }
+        // predicates not kept sorted: their sets, sorted once
+        for (uint32_t p = 0; p < n_preds; ++p) {
+            if (!idb[p] || indexed[p]) continue;
+            DRel f;
+            f.n = H[p].size;
+            if (f.n) {
+                uint64_t *all = static_cast<uint64_t *>(ctx->alloc(f.n * sizeof(uint64_t)));
+                uint64_t got = 0;
+                try {
+                    got = hs_collect(ctx, H[p], all);
+                    XH_REQUIRE(got == f.n, XLOG_HIP_DEVICE_ERROR,
+                               "hash set holds " + std::to_string(got) + " tuples, expected " + std::to_string(f.n));
+                } catch (...) {
+                    ctx->free(all);
+                    throw;
+                }
+                H[p] = HashSet();
+                f.k = sort_keys(ctx, all, got, true, 0, 8, digits);  // consumes all
+                f.owned = true;
+            }
+            f.version = version_counter++;
+            release(full[p]);
+            full[p] = f;
+        }
+        return it;
+    }
 };
 
 // TC plan shape: head(A,B) :- E(A,B).  head(A,C) :- head(A,B), E(B,C).
@@ -1791,6 +2052,13 @@ bool chain_shape(const std::vector<Rule> &rules, std::vector<ChainRule> &out) {
 }
 
 }  // namespace
+
+// a predicate that is the head of some rule
+static bool idb_of(const std::vector<Rule> &rules, int pred) {
+    for (const Rule &r : rules)
+        if (r.head == pred) return true;
+    return false;
+}
 
 // canonical keys of an input relation for the driver
 static DRel canon_drel(Ctx *ctx, const xlog_hip_rel *r) {
@@ -1905,14 +2173,6 @@ static bool run_chain_route(Ctx *ctx, const std::vector<Rule> &rules, uint32_t n
 // includes the final empty iteration; R is sorted once at the end.
 // XLOG_HIP_HASH_SLOTS / XLOG_HIP_HASH_APPENDS override the initial table size
 // and the appends allowed per attempt (tests force the grow-and-rerun path).
-static uint64_t env_u64(const char *name, uint64_t dflt) {
-    const char *e = getenv(name);
-    if (e && *e) {
-        const unsigned long long v = strtoull(e, nullptr, 10);
-        if (v > 0) return v;
-    }
-    return dflt;
-}
 static void tc_fixpoint_hash(Ctx *ctx, const DRel &edges, uint64_t max_iter, uint64_t **res, uint64_t *res_n,
                              uint64_t *iterations, std::vector<uint64_t> &deltas) {
     *res = nullptr;
@@ -2014,8 +2274,12 @@ static void run_fixpoint_impl(Ctx *ctx, const int32_t *plan, uint32_t n_preds, c
         for (const Rule &r : rules) if (r.nb == 1) { E = r.b[0].pred; H = r.head; }
     }
     bool head_empty = tc && (!rels[H] || rels[H]->rows == 0);
-    XH_REQUIRE(route != XLOG_HIP_ROUTE_HASH || (tc && head_empty), XLOG_HIP_UNSUPPORTED,
-               "hash route needs the transitive-closure plan with an empty head");
+    // path-shaped rules of up to three atoms can also run over hash sets (Driver::run_hash)
+    std::vector<ChainRule> paths;
+    bool short_paths = chain_shape(rules, paths);
+    for (const ChainRule &c : paths) short_paths = short_paths && c.path.size() <= 3;
+    XH_REQUIRE(route != XLOG_HIP_ROUTE_HASH || (tc && head_empty) || short_paths, XLOG_HIP_UNSUPPORTED,
+               "hash route needs rule bodies of 1 to 3 atoms forming a path between the head variables");
     uint64_t nv = 0;  // max id + 1 (up to 2^32)
     DRel edges;
     if (tc && head_empty && route != XLOG_HIP_ROUTE_JOIN) {
@@ -2082,10 +2346,26 @@ static void run_fixpoint_impl(Ctx *ctx, const int32_t *plan, uint32_t n_preds, c
         out[H] = n ? rel_adopt(ctx, 2, n, res, nullptr, REL_CANONICAL) : rel_new(ctx, 2, 0);
         out[H]->flags = REL_CANONICAL;
         if (stats) stats->route = XLOG_HIP_ROUTE_BITMAP;
-    } else if (run_chain_route(ctx, rules, n_preds, rels, route, max_iter, out, &iterations, deltas, stats,
-                               edges)) {
+    } else if (route != XLOG_HIP_ROUTE_HASH &&
+               run_chain_route(ctx, rules, n_preds, rels, route, max_iter, out, &iterations, deltas, stats, edges)) {
         if (stats) stats->route = XLOG_HIP_ROUTE_BITMAP;
     } else {
+        if (edges.owned) ctx->free(edges.k);
+        edges = DRel();
+        // Path-shaped plans the bitmap route does not take run over hash sets under AUTO, except (1) when a
+        // join-row limit is set (the limit is defined on the join route's bags) and (2) when a three-atom
+        // rule reads two or more IDB atoms (Andersen's load and store rules): its two-hop expansions then
+        // enumerate every path through the IDB relation's hubs, duplicates included, where the join route
+        // deduplicates the first join's pairs (measured at 10,000 variables: 4.5 s against 1.4 s).
+        bool hub_paths = false;
+        for (const Rule &r : rules) {
+            int n_idb = 0;
+            for (int j = 0; j < r.nb; ++j) n_idb += idb_of(rules, r.b[j].pred) ? 1 : 0;
+            hub_paths = hub_paths || (r.nb == 3 && n_idb >= 2);
+        }
+        const bool use_hash =
+            short_paths && (route == XLOG_HIP_ROUTE_HASH ||
+                            (route == XLOG_HIP_ROUTE_AUTO && !(stats && stats->max_join_rows) && !hub_paths));
         Driver drv{ctx, rules, n_preds, std::vector<bool>(n_preds, false), std::vector<DRel>(n_preds),
                    std::vector<DRel>(n_preds)};
         for (const Rule &r : rules) drv.idb[r.head] = true;
@@ -2108,7 +2388,7 @@ static void run_fixpoint_impl(Ctx *ctx, const int32_t *plan, uint32_t n_preds, c
             drv.digits = nd ? (((1u << nd) - 1u) | (((1u << nd) - 1u) << 4)) : 1u;
         }
         try {
-            iterations = drv.run(max_iter, deltas);
+            iterations = use_hash ? drv.run_hash(max_iter, deltas, paths) : drv.run(max_iter, deltas);
         } catch (const Error &) {
             if (stats) stats->iterations = deltas.empty() ? 0 : deltas.size() - 1;
             throw;
@@ -2131,7 +2411,7 @@ static void run_fixpoint_impl(Ctx *ctx, const int32_t *plan, uint32_t n_preds, c
             r->flags = REL_CANONICAL;
             out[p] = r;
         }
-        if (stats) stats->route = XLOG_HIP_ROUTE_JOIN;
+        if (stats) stats->route = use_hash ? XLOG_HIP_ROUTE_HASH : XLOG_HIP_ROUTE_JOIN;
     }
     XH_CHECK_HIP(hipEventRecord(ctx->ev_b, ctx->stream));
     XH_CHECK_HIP(hipEventSynchronize(ctx->ev_b));

@@ -308,6 +308,163 @@ __global__ __launch_bounds__(HB) void k_hs_join_insert(JoinInsertArgs a, SetView
     }
 }
 
+// One step of a path-shaped rule body over the hash set of its head, for
+// bodies of up to three atoms (two hops besides the delta atom): every delta
+// row (xa, xb) (the delta atom's two path values) is expanded through hop 1
+// (a run of values v1 for xa or xb) and, when the body has a third atom,
+// each level-1 value through hop 2 (a run of values v2 for xa, xb or v1), and
+// the head tuple built from (xa, xb, v1, v2) is inserted; the inserted ones
+// are appended.  Nothing between the levels leaves the wave: level-1 values
+// are expanded 64 at a time (one per lane, found by a search over the wave's
+// run-length prefixes in LDS) and their level-2 runs 64 x HS_U outputs at a
+// time, so the binary intermediate of the first two atoms is never written.
+// The overflow protocol is that of k_hs_join_insert.
+__device__ __forceinline__ uint32_t path_val(int sel, uint32_t xa, uint32_t xb, uint32_t v1, uint32_t v2) {
+    return sel == 0 ? xa : sel == 1 ? xb : sel == 2 ? v1 : v2;
+}
+__device__ __forceinline__ int last_le(const uint64_t *pre, uint64_t o) {
+    int r = 0;
+#pragma unroll
+    for (int step = 32; step > 0; step >>= 1)
+        if (pre[r + step] <= o) r += step;
+    return r;
+}
+
+template <bool TWO>
+__global__ __launch_bounds__(HB) void k_hs_path_insert(PathInsertArgs a, SetView s, uint64_t *__restrict__ out,
+                                                       unsigned long long *count, uint64_t limit,
+                                                       unsigned long long *overflow, unsigned long long *work) {
+    __shared__ uint64_t s_pre1[HB / WAVE][WAVE], s_st1[HB / WAVE][WAVE];
+    __shared__ uint32_t s_xa[HB / WAVE][WAVE], s_xb[HB / WAVE][WAVE];
+    __shared__ uint64_t s_pre2[TWO ? HB / WAVE : 1][WAVE], s_st2[TWO ? HB / WAVE : 1][WAVE];
+    __shared__ uint32_t s_v1[TWO ? HB / WAVE : 1][WAVE], s_ra[TWO ? HB / WAVE : 1][WAVE],
+        s_rb[TWO ? HB / WAVE : 1][WAVE];
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
+    const uint64_t gwave = (uint64_t)blockIdx.x * (HB / WAVE) + (uint64_t)wave;
+    const uint64_t nwaves = (uint64_t)gridDim.x * (HB / WAVE);
+    unsigned long long cand = 0;
+    for (uint64_t rbase = gwave * WAVE; rbase < a.n; rbase += nwaves * WAVE) {
+        const uint64_t i = rbase + lane;
+        uint32_t xa = 0, xb = 0, len1 = 0;
+        uint64_t st1 = 0;
+        if (i < a.n) {
+            const uint64_t row = a.delta[i];
+            xa = a.delta_swap ? (uint32_t)row : (uint32_t)(row >> 32);
+            xb = a.delta_swap ? (uint32_t)(row >> 32) : (uint32_t)row;
+            run_lookup(a.h1.table, a.h1.mask, a.h1.bits, a.key1 ? xb : xa, &st1, &len1);
+        }
+        uint64_t incl = len1;
+#pragma unroll
+        for (int o = 1; o < WAVE; o <<= 1) {
+            const uint64_t t = __shfl_up(incl, o, WAVE);
+            if (lane >= o) incl += t;
+        }
+        const uint64_t total1 = __shfl(incl, WAVE - 1, WAVE);
+        s_pre1[wave][lane] = incl - len1;
+        s_st1[wave][lane] = st1;
+        s_xa[wave][lane] = xa;
+        s_xb[wave][lane] = xb;
+        __builtin_amdgcn_wave_barrier();
+        if constexpr (!TWO) {
+            cand += total1;
+            for (uint64_t ob = 0; ob < total1; ob += (uint64_t)WAVE * HS_U) {
+                uint64_t key[HS_U], h[HS_U];
+                unsigned long long cur[HS_U];
+                bool valid[HS_U], novel[HS_U], full = false;
+#pragma unroll
+                for (int u = 0; u < HS_U; ++u) {
+                    const uint64_t o = ob + (uint64_t)u * WAVE + lane;
+                    valid[u] = o < total1;
+                    const int r = last_le(s_pre1[wave], o);
+                    const uint32_t v1 = valid[u] ? a.h1.payload[s_st1[wave][r] + (o - s_pre1[wave][r])] : 0u;
+                    const uint32_t ra = s_xa[wave][r], rb = s_xb[wave][r];
+                    key[u] = ((uint64_t)path_val(a.out0, ra, rb, v1, 0u) << 32) | path_val(a.out1, ra, rb, v1, 0u);
+                }
+#pragma unroll
+                for (int u = 0; u < HS_U; ++u) {
+                    h[u] = hs_hash(key[u], s.bits);
+                    cur[u] = (valid[u] && key[u] != HS_EMPTY) ? s.slots[h[u]] : 0ull;
+                }
+#pragma unroll
+                for (int u = 0; u < HS_U; ++u) {
+                    const int res = valid[u] ? hs_insert_from(s, key[u], h[u], cur[u]) : 0;
+                    full |= res == 2;
+                    novel[u] = res == 1;
+                }
+                const uint64_t after = wave_append_n(novel, key, out, count, lane);
+                if (after >= limit || any_full(full)) {
+                    if (lane == 0) *overflow = 1ull;
+                    return;
+                }
+            }
+        } else {
+            for (uint64_t o1b = 0; o1b < total1; o1b += WAVE) {
+                // one level-1 value per lane, then its hop-2 run
+                const uint64_t o1 = o1b + lane;
+                const bool valid1 = o1 < total1;
+                const int r = last_le(s_pre1[wave], valid1 ? o1 : 0);
+                const uint32_t ra = s_xa[wave][r], rb = s_xb[wave][r];
+                const uint32_t v1 = valid1 ? a.h1.payload[s_st1[wave][r] + (o1 - s_pre1[wave][r])] : 0u;
+                uint64_t st2 = 0;
+                uint32_t len2 = 0;
+                if (valid1) run_lookup(a.h2.table, a.h2.mask, a.h2.bits, path_val(a.key2, ra, rb, v1, 0u), &st2, &len2);
+                uint64_t incl2 = len2;
+#pragma unroll
+                for (int o = 1; o < WAVE; o <<= 1) {
+                    const uint64_t t = __shfl_up(incl2, o, WAVE);
+                    if (lane >= o) incl2 += t;
+                }
+                const uint64_t total2 = __shfl(incl2, WAVE - 1, WAVE);
+                __builtin_amdgcn_wave_barrier();  // the previous round's readers are done
+                s_pre2[wave][lane] = incl2 - len2;
+                s_st2[wave][lane] = st2;
+                s_v1[wave][lane] = v1;
+                s_ra[wave][lane] = ra;
+                s_rb[wave][lane] = rb;
+                __builtin_amdgcn_wave_barrier();
+                cand += total2;
+                for (uint64_t ob = 0; ob < total2; ob += (uint64_t)WAVE * HS_U) {
+                    uint64_t key[HS_U], h[HS_U];
+                    unsigned long long cur[HS_U];
+                    bool valid[HS_U], novel[HS_U], full = false;
+#pragma unroll
+                    for (int u = 0; u < HS_U; ++u) {
+                        const uint64_t o = ob + (uint64_t)u * WAVE + lane;
+                        valid[u] = o < total2;
+                        const int q = last_le(s_pre2[wave], o);
+                        const uint32_t v2 = valid[u] ? a.h2.payload[s_st2[wave][q] + (o - s_pre2[wave][q])] : 0u;
+                        const uint32_t qa = s_ra[wave][q], qb = s_rb[wave][q], qv = s_v1[wave][q];
+                        key[u] = ((uint64_t)path_val(a.out0, qa, qb, qv, v2) << 32) | path_val(a.out1, qa, qb, qv, v2);
+                    }
+#pragma unroll
+                    for (int u = 0; u < HS_U; ++u) {
+                        h[u] = hs_hash(key[u], s.bits);
+                        cur[u] = (valid[u] && key[u] != HS_EMPTY) ? s.slots[h[u]] : 0ull;
+                    }
+#pragma unroll
+                    for (int u = 0; u < HS_U; ++u) {
+                        const int res = valid[u] ? hs_insert_from(s, key[u], h[u], cur[u]) : 0;
+                        full |= res == 2;
+                        novel[u] = res == 1;
+                    }
+                    const uint64_t after = wave_append_n(novel, key, out, count, lane);
+                    if (after >= limit || any_full(full)) {
+                        if (lane == 0) *overflow = 1ull;
+                        return;
+                    }
+                }
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+    if (work) {
+        // algorithmic bytes: delta row + slot per row; per candidate its value (4 B) + slot word (8 B)
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) cand += __shfl_xor(cand, o, WAVE);
+        if (lane == 0) atomicAdd(work + (blockIdx.x & 63), cand * 12ull);
+    }
+}
+
 __global__ void k_hs_append_allones(const unsigned int *allones, uint64_t *out, uint64_t *count) {
     if (*allones) out[(*count)++] = HS_EMPTY;
 }
@@ -387,6 +544,23 @@ void hs_join_insert(Ctx *ctx, HashSet &h, const uint64_t *delta, uint64_t n, int
     const unsigned grid = grid_for(waves * WAVE, HB, std::min<unsigned>((unsigned)ctx->num_cus * 32, HS_MAX_BLOCKS));
     hipLaunchKernelGGL(k_hs_join_insert, dim3(grid), dim3(HB), 0, ctx->stream, a, view(h), out, cnt, limit, ovf,
                        work);
+    XH_CHECK_HIP(hipGetLastError());
+}
+
+void hs_path_insert(Ctx *ctx, HashSet &h, const PathInsertArgs &a, uint64_t *out, uint64_t limit) {
+    if (!a.n) return;
+    unsigned long long *ovf = reinterpret_cast<unsigned long long *>(h.flags.p + 1);
+    unsigned long long *cnt = reinterpret_cast<unsigned long long *>(h.flags.p + 2);
+    Prof prof(ctx, XLOG_HIP_KERNEL_HASH_INSERT, 24.0 * (double)a.n);
+    unsigned long long *work = prof.work(1.0);
+    const uint64_t waves = (a.n + WAVE - 1) / WAVE;
+    const unsigned grid = grid_for(waves * WAVE, HB, std::min<unsigned>((unsigned)ctx->num_cus * 32, HS_MAX_BLOCKS));
+    if (a.h2.table)
+        hipLaunchKernelGGL(k_hs_path_insert<true>, dim3(grid), dim3(HB), 0, ctx->stream, a, view(h), out, cnt, limit,
+                           ovf, work);
+    else
+        hipLaunchKernelGGL(k_hs_path_insert<false>, dim3(grid), dim3(HB), 0, ctx->stream, a, view(h), out, cnt, limit,
+                           ovf, work);
     XH_CHECK_HIP(hipGetLastError());
 }
 

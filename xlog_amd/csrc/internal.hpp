@@ -412,6 +412,28 @@ void hs_join_insert(Ctx *ctx, HashSet &h, const uint64_t *delta, uint64_t n, int
                     const RunIndex &ix, const uint32_t *payload, uint64_t *out, uint64_t limit);
 // inserts keys[0..n) and appends the novel ones (same protocol)
 void hs_insert_novel(Ctx *ctx, HashSet &h, const uint64_t *keys, uint64_t n, uint64_t *out, uint64_t limit);
+// One step of a path-shaped rule body of two or three atoms, same protocol:
+// every delta row, read as the path values (xa, xb) of the delta atom (the
+// high then low word, swapped when delta_swap), is expanded through hop 1 (the
+// run of xa or xb: values v1) and, when h2.table is set, each v1 through hop
+// 2 (the run of xa, xb or v1: values v2); the head tuple (value out0, value
+// out1) over the selectors 0 = xa, 1 = xb, 2 = v1, 3 = v2 is inserted.
+struct PathHop {
+    const unsigned long long *table = nullptr;  // run index slots (join.hip's build)
+    uint64_t mask = 0;
+    int bits = 0;
+    const uint32_t *payload = nullptr;
+};
+struct PathInsertArgs {
+    const uint64_t *delta = nullptr;
+    uint64_t n = 0;
+    int delta_swap = 0;
+    PathHop h1, h2;
+    int key1 = 0;  // 0: xa, 1: xb
+    int key2 = 0;  // 0: xa, 1: xb, 2: v1
+    int out0 = 0, out1 = 0;
+};
+void hs_path_insert(Ctx *ctx, HashSet &h, const PathInsertArgs &a, uint64_t *out, uint64_t limit);
 // every tuple of the set, unordered, into out (h.size entries); returns the count
 uint64_t hs_collect(Ctx *ctx, const HashSet &h, uint64_t *out);
 // appends past `limit`: one 64-tuple chunk per wave of the insert grid
