@@ -308,9 +308,8 @@ typedef struct {
  * most 2^17 distinct ids (max id + 1) and the bit matrices fit in half the
  * free device memory; otherwise the hash route when every rule body is a path
  * of at most three atoms, no join-row limit is set and no three-atom body
- * reads two IDB atoms (the transitive-closure plan with an empty head takes
- * the hash route's closure kernel); the join route otherwise.  Requesting
- * BITMAP or HASH for a plan or domain it cannot take is UNSUPPORTED. */
+ * reads two IDB atoms; the join route otherwise.  Requesting BITMAP or HASH
+ * for a plan or domain it cannot take is UNSUPPORTED. */
 #define XLOG_HIP_ROUTE_AUTO 0
 #define XLOG_HIP_ROUTE_JOIN 1   /* join -> sort -> dedup -> diff -> merge */
 #define XLOG_HIP_ROUTE_BITMAP 2 /* relations as domain x domain bit matrices, rule bodies as chains of
@@ -321,7 +320,9 @@ typedef struct {
                                    indexes (up to two hops, no intermediate relation: the multiway path
                                    join) and inserts the head tuples, the inserted ones being the next
                                    delta (the sparse factorized delta of provider/fj_delta_sparse.rs:66
-                                   with a persistent table); bodies of 1 to 3 atoms forming a path */
+                                   with a persistent table); bodies of 1 to 3 atoms forming a path.
+                                   Programs whose variants read no IDB relation in full (linear ones)
+                                   queue up to 8 iterations per host read-back */
 
 xlog_hip_status xlog_hip_fixpoint(xlog_hip_ctx *ctx, const int32_t *plan, uint32_t n_preds,
                                   const xlog_hip_rel *const *rels, xlog_hip_rel **out,

@@ -241,3 +241,41 @@ def test_hash_route_programs_rerun(provider, monkeypatch):
     for q in (1, 2):
         assert np.array_equal(p.download_packed(outs[q]), outs_o[q])
     assert st["iterations"] == it_o and st["delta_sizes"] == deltas_o
+
+
+def test_hash_route_queued_steps(provider, monkeypatch):
+    """Linear programs (no IDB atom read in full by a variant) queue several iterations per read-back on
+    the hash-set route: the same relations and deltas as one read-back per iteration, with fewer waits."""
+    p = provider
+    s, d = _spread(*_graph(1500, 1700, 26))
+    for name, plan, rels, idb in (("left tc", cp.left_tc_plan(), [pack(s, d), None], [1]),
+                                  ("parity", cp.parity_plan(), [pack(s, d), None, None], [1, 2])):
+        outs_o, it_o, deltas_o = oracle.seminaive(plan, rels)
+        waits = {}
+        for queue in ("1", "8"):
+            monkeypatch.setenv("XLOG_HIP_HASH_QUEUE", queue)
+            _note(f"queued {name} queue={queue}")
+            outs, st = _run(p, plan, rels, ROUTE_HASH)
+            for q in idb:
+                assert np.array_equal(p.download_packed(outs[q]), outs_o[q]), f"{name} queue {queue} pred {q}"
+            assert st["iterations"] == it_o and st["delta_sizes"] == deltas_o
+            waits[queue] = st["host_waits"]
+        assert it_o > 16 and waits["8"] < waits["1"] - it_o // 2, (name, it_o, waits)
+
+
+def test_hash_route_queued_overflow(provider, monkeypatch):
+    """Queued steps of at most 100 appends each in a 64-slot table: steps overflow inside the queue (the
+    later ones then do nothing), and the half-load budget cuts steps short; each such step is rerun
+    from the host's sizes and the queue resumes."""
+    p = provider
+    monkeypatch.setenv("XLOG_HIP_HASH_SLOTS", "64")
+    monkeypatch.setenv("XLOG_HIP_HASH_APPENDS", "100")
+    s, d = _spread(*_graph(900, 1000, 27))
+    for name, plan, rels, idb in (("left tc", cp.left_tc_plan(), [pack(s, d), None], [1]),
+                                  ("symmetric", cp.symmetric_plan(), [pack(s, d), None], [1])):
+        _note(f"queued overflow {name}")
+        outs_o, it_o, deltas_o = oracle.seminaive(plan, rels)
+        outs, st = _run(p, plan, rels, ROUTE_HASH)
+        for q in idb:
+            assert np.array_equal(p.download_packed(outs[q]), outs_o[q]), name
+        assert st["iterations"] == it_o and st["delta_sizes"] == deltas_o

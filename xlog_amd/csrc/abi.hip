@@ -1752,26 +1752,33 @@ struct Driver {
 
     // The loop of run() over device hash sets, for path-shaped rules of at
     // most three atoms (chains[ri]: rule ri as a path from its first head
-    // variable to its second).  The seed is run()'s.  The full relation of
-    // every IDB predicate also lives in a hash set; an iteration runs one
-    // expand-and-insert pass per variant (hs_path_insert: the delta atom's rows
-    // through the other atoms' run indexes, at most two hops, no intermediate
-    // relation), and the tuples the passes insert are the next delta: new
-    // against R and unique, with no sort, merge-diff or candidate bag.  One
-    // read-back per iteration brings every head's appended count and overflow
-    // flag.  A predicate that some variant reads in full (an IDB atom besides
-    // the delta atom) is sorted into its full relation every iteration, for
-    // the indexes; the others are collected from their set at the end.
+    // variable to its second).  The full relation of every IDB predicate also
+    // lives in a hash set; a pass runs one expand-and-insert launch per
+    // variant (hs_path_insert: the delta atom's rows through the other atoms'
+    // run indexes, at most two hops, no intermediate relation), and the tuples
+    // a head's launches insert are its next delta: new against R and unique,
+    // with no sort, merge-diff or candidate bag.  Pass 0 is the seed (every
+    // rule once, its first path atom reading its whole relation: the tuples it
+    // inserts are T(R) minus R, run()'s seed).  A predicate that some variant
+    // reads in full (an IDB atom besides the delta atom) is sorted into its
+    // full relation after every pass, for the indexes, and every iteration
+    // reads back its sizes.  Programs with no such predicate (linear ones:
+    // every variant reads only EDB relations besides its delta) queue up to
+    // XLOG_HIP_HASH_QUEUE (8) iterations per read-back: each launch reads its
+    // delta's row count on the device, and a step that overflows makes the
+    // later queued steps do nothing and is rerun with the host's sizes.  The
+    // others are collected from their set at the end.
     uint64_t run_hash(uint64_t max_iter, std::vector<uint64_t> &deltas, const std::vector<ChainRule> &chains) {
         XH_REQUIRE(chains.size() == rules.size(), XLOG_HIP_INVALID_ARG, "hash route: one path per rule");
         std::vector<bool> indexed(n_preds, false);
+        bool any_indexed = false;
         for (const ChainRule &c : chains) {
             XH_REQUIRE(c.path.size() >= 1 && c.path.size() <= 3, XLOG_HIP_UNSUPPORTED,
                        "hash route: rule bodies of 1 to 3 atoms");
             for (size_t d = 0; d < c.path.size(); ++d) {
                 if (!idb[c.path[d].pred]) continue;
                 for (size_t j = 0; j < c.path.size(); ++j)
-                    if (j != d && idb[c.path[j].pred]) indexed[c.path[j].pred] = true;
+                    if (j != d && idb[c.path[j].pred]) indexed[c.path[j].pred] = any_indexed = true;
             }
         }
         std::vector<HashSet> H(n_preds);
@@ -1792,86 +1799,75 @@ struct Driver {
             bool swap = false;
             double fanout = 1.0;  // expected head tuples per delta row
         };
+        // The launch arguments of the variant with the delta at path position d of rule ri (rows left
+        // unset), with its hops at the current full relations; false when a hop has no run at all.
+        auto make_var = [&](size_t ri, int d, Var &v) -> bool {
+            const std::vector<ChainAtom> &path = chains[ri].path;
+            const int m = (int)path.size();
+            v = Var();
+            v.a.delta_swap = path[d].backward ? 1 : 0;
+            // a hop through atom j: from x_{j+1} to x_j (left of the delta atom) or from x_j to
+            // x_{j+1} (right of it); the stored tuple is (x_j, x_{j+1}) unless backward
+            auto hop = [&](int j, bool left, PathHop &h) {
+                const bool key_col1 = left != path[j].backward;
+                const DRel &rel = full[path[j].pred];
+                if (rel.n == 0) return false;
+                const JoinIndex &J = index_of(rel, key_col1 ? 1 : 0);
+                h.table = J.ix.table.p;
+                h.mask = J.ix.table_mask;
+                int bits = 0;
+                while ((1ull << bits) < J.ix.table_mask + 1) ++bits;
+                h.bits = bits;
+                h.payload = J.payload.p;
+                v.fanout *= J.ix.nruns ? (double)J.n / (double)J.ix.nruns : 0.0;
+                return J.ix.nruns != 0;
+            };
+            if (m == 1) {
+                v.copy = true;
+                v.swap = path[0].backward;
+                return true;
+            }
+            if (m == 2) {  // d = 0: xb -> x2 (right); d = 1: xa -> x0 (left)
+                v.a.key1 = d == 0 ? 1 : 0;
+                v.a.out0 = d == 0 ? 0 : 2;
+                v.a.out1 = d == 0 ? 2 : 1;
+                return hop(d == 0 ? 1 : 0, d == 1, v.a.h1);
+            }
+            if (d == 0) {  // xb -> x2 -> x3
+                v.a.key1 = 1;
+                v.a.key2 = 2;
+                v.a.out0 = 0;
+                v.a.out1 = 3;
+                return hop(1, false, v.a.h1) && hop(2, false, v.a.h2);
+            }
+            if (d == 1) {  // xa -> x0 and xb -> x3
+                v.a.key1 = 0;
+                v.a.key2 = 1;
+                v.a.out0 = 2;
+                v.a.out1 = 3;
+                return hop(0, true, v.a.h1) && hop(2, false, v.a.h2);
+            }
+            v.a.key1 = 0;  // xa -> x1 -> x0
+            v.a.key2 = 2;
+            v.a.out0 = 3;
+            v.a.out1 = 1;
+            return hop(1, true, v.a.h1) && hop(0, true, v.a.h2);
+        };
+        auto launch = [&](HashSet &h, const Var &v, uint64_t *out, uint64_t limit, unsigned long long *count,
+                          unsigned long long *overflow) {
+            if (v.copy)
+                hs_insert_novel(ctx, h, v.a.delta, v.a.n, out, limit, v.swap ? 1 : 0, count, overflow, &v.a.q);
+            else
+                hs_path_insert(ctx, h, v.a, out, limit, count, overflow);
+        };
         // appends allowed per attempt: the expected candidate count, a bound on the novel tuples
         // (XLOG_HIP_HASH_APPENDS below 2^20 forces small attempts: tests of the rerun path)
         const uint64_t min_want = env_u64("XLOG_HIP_HASH_APPENDS", 1ull << 20);
-        uint64_t it = 0;
-        // pass 0 is the seed: every rule once, its first path atom reading the whole relation (the
-        // tuples it inserts are T(R) minus R, run()'s seed); pass k > 0 is iteration k
-        for (uint64_t pass = 0;; ++pass) {
-            if (pass) {
-                XH_REQUIRE(it < max_iter, XLOG_HIP_ITERATION_LIMIT,
-                           "Recursive SCC iteration limit (" + std::to_string(max_iter) + ") exceeded");
-                ++it;
-            }
-            // the variants, grouped by head, with their hops at R of the previous pass
-            std::vector<std::vector<Var>> vars(n_preds);
-            for (size_t ri = 0; ri < chains.size(); ++ri) {
-                const std::vector<ChainAtom> &path = chains[ri].path;
-                const int m = (int)path.size();
-                for (int d = 0; d < m; ++d) {
-                    const int q = path[d].pred;
-                    Var v;
-                    if (pass == 0) {
-                        if (d != 0 || full[q].n == 0) continue;
-                        v.a.delta = full[q].k;
-                        v.a.n = full[q].n;
-                    } else {
-                        if (!idb[q] || dn[q] == 0) continue;
-                        v.a.delta = dcur[q].p;
-                        v.a.n = dn[q];
-                    }
-                    v.a.delta_swap = path[d].backward ? 1 : 0;
-                    // a hop through atom j: from x_{j+1} to x_j (left of the delta atom) or from
-                    // x_j to x_{j+1} (right of it); the stored tuple is (x_j, x_{j+1}) unless backward
-                    auto hop = [&](int j, bool left, PathHop &h) {
-                        const bool key_col1 = left != path[j].backward;
-                        const DRel &rel = full[path[j].pred];
-                        if (rel.n == 0) return false;
-                        const JoinIndex &J = index_of(rel, key_col1 ? 1 : 0);
-                        h.table = J.ix.table.p;
-                        h.mask = J.ix.table_mask;
-                        int bits = 0;
-                        while ((1ull << bits) < J.ix.table_mask + 1) ++bits;
-                        h.bits = bits;
-                        h.payload = J.payload.p;
-                        v.fanout *= J.ix.nruns ? (double)J.n / (double)J.ix.nruns : 0.0;
-                        return J.ix.nruns != 0;
-                    };
-                    bool live = true;
-                    if (m == 1) {
-                        v.copy = true;
-                        v.swap = path[0].backward;
-                    } else if (m == 2) {
-                        // d = 0: xb -> x2 (right); d = 1: xa -> x0 (left)
-                        live = hop(d == 0 ? 1 : 0, d == 1, v.a.h1);
-                        v.a.key1 = d == 0 ? 1 : 0;
-                        v.a.out0 = d == 0 ? 0 : 2;
-                        v.a.out1 = d == 0 ? 2 : 1;
-                    } else if (d == 0) {  // xb -> x2 -> x3
-                        live = hop(1, false, v.a.h1) && hop(2, false, v.a.h2);
-                        v.a.key1 = 1;
-                        v.a.key2 = 2;
-                        v.a.out0 = 0;
-                        v.a.out1 = 3;
-                    } else if (d == 1) {  // xa -> x0 and xb -> x3
-                        live = hop(0, true, v.a.h1) && hop(2, false, v.a.h2);
-                        v.a.key1 = 0;
-                        v.a.key2 = 1;
-                        v.a.out0 = 2;
-                        v.a.out1 = 3;
-                    } else {  // xa -> x1 -> x0
-                        live = hop(1, true, v.a.h1) && hop(0, true, v.a.h2);
-                        v.a.key1 = 0;
-                        v.a.key2 = 2;
-                        v.a.out0 = 3;
-                        v.a.out1 = 1;
-                    }
-                    if (live) vars[chains[ri].head].push_back(v);
-                }
-            }
-            std::vector<uint64_t> want(n_preds, 0), appended(n_preds, 0);
-            std::vector<Buf<uint64_t>> out(n_preds);
+        // One synchronous pass: every head's variants until none overflows.  appended / out may hold the
+        // appends of a queued step that overflowed (kept: those tuples are in the set already).
+        auto sync_pass = [&](std::vector<std::vector<Var>> &vars, std::vector<uint64_t> &appended,
+                             std::vector<Buf<uint64_t>> &out) {
+            std::vector<uint64_t> want(n_preds, 0);
             std::vector<uint32_t> todo;
             for (uint32_t p = 0; p < n_preds; ++p) {
                 if (vars[p].empty()) continue;
@@ -1885,10 +1881,10 @@ struct Driver {
                 }
                 est = std::min(est * 1.25, 4.0 * ((double)H[p].size + rows));
                 want[p] = min_want < (1ull << 20) ? min_want : std::max<uint64_t>(min_want, (uint64_t)est + 1024);
-                fill_u64(ctx, H[p].flags.p + 1, 0ull, 2);
+                fill_u64(ctx, H[p].flags.p + 1, 0ull, 1);
+                fill_u64(ctx, H[p].flags.p + 2, appended[p], 1);
                 todo.push_back(p);
             }
-            std::vector<Buf<uint64_t>> swapped;  // one-atom bodies read backward
             while (!todo.empty()) {
                 for (uint32_t p : todo) {
                     HashSet &h = H[p];
@@ -1906,19 +1902,7 @@ struct Driver {
                         if (appended[p]) copy_d2d(ctx, bigger.p, out[p].p, appended[p]);
                         out[p] = std::move(bigger);
                     }
-                    for (const Var &v : vars[p]) {
-                        if (v.copy) {
-                            const uint64_t *rows = v.a.delta;
-                            if (v.swap) {
-                                swapped.emplace_back(ctx, v.a.n);
-                                swap_words(ctx, v.a.delta, v.a.n, swapped.back().p);
-                                rows = swapped.back().p;
-                            }
-                            hs_insert_novel(ctx, h, rows, v.a.n, out[p].p, limit);
-                        } else {
-                            hs_path_insert(ctx, h, v.a, out[p].p, limit);
-                        }
-                    }
+                    for (const Var &v : vars[p]) launch(h, v, out[p].p, limit, nullptr, nullptr);
                 }
                 // one read-back: every head's overflow flag and appended count
                 Buf<uint64_t> g(ctx, 2 * todo.size());
@@ -1929,7 +1913,7 @@ struct Driver {
                     const uint32_t p = todo[t];
                     appended[p] = ctx->host_scalars[2 * t + 1];
                     if (ctx->host_scalars[2 * t]) {
-                        // the limit or a full table stopped a pass: grow and run the head's passes again;
+                        // the limit or a full table stopped a launch: grow and run the head's variants again;
                         // the tuples they inserted are found present and are not appended twice
                         fill_u64(ctx, H[p].flags.p + 1, 0ull, 1);
                         want[p] *= 4;
@@ -1938,6 +1922,9 @@ struct Driver {
                 }
                 todo.swap(again);
             }
+        };
+        // a finished pass: the appended tuples become the deltas (sorted into full R where indexed)
+        auto finish_pass = [&](std::vector<uint64_t> &appended, std::vector<Buf<uint64_t>> &out) {
             uint64_t total = 0;
             for (uint32_t p = 0; p < n_preds; ++p) {
                 if (!idb[p]) continue;
@@ -1966,8 +1953,174 @@ struct Driver {
                     dcur[p] = std::move(out[p]);
                 }
             }
+            return total;
+        };
+        // the variants of a synchronous pass over the current deltas (pass 0: the seed)
+        auto pass_vars = [&](bool seed) {
+            std::vector<std::vector<Var>> vars(n_preds);
+            for (size_t ri = 0; ri < chains.size(); ++ri) {
+                const std::vector<ChainAtom> &path = chains[ri].path;
+                for (int d = 0; d < (int)path.size(); ++d) {
+                    const int q = path[d].pred;
+                    if (seed ? (d != 0 || full[q].n == 0) : (!idb[q] || dn[q] == 0)) continue;
+                    Var v;
+                    if (!make_var(ri, d, v)) continue;
+                    v.a.delta = seed ? full[q].k : dcur[q].p;
+                    v.a.n = seed ? full[q].n : dn[q];
+                    vars[chains[ri].head].push_back(v);
+                }
+            }
+            return vars;
+        };
+        {  // pass 0, the seed
+            std::vector<std::vector<Var>> vars = pass_vars(true);
+            std::vector<uint64_t> appended(n_preds, 0);
+            std::vector<Buf<uint64_t>> out(n_preds);
+            sync_pass(vars, appended, out);
+            deltas.push_back(finish_pass(appended, out));
+        }
+        const uint64_t queue_max = any_indexed ? 1 : std::min<uint64_t>(env_u64("XLOG_HIP_HASH_QUEUE", 8), 256);
+        uint64_t queue = queue_max;
+        std::vector<Buf<uint64_t>> spare(n_preds);  // the second delta buffer of the queued steps
+        std::vector<uint64_t> cap(n_preds, 0);
+        uint64_t it = 0;
+        for (;;) {
+            XH_REQUIRE(it < max_iter, XLOG_HIP_ITERATION_LIMIT,
+                       "Recursive SCC iteration limit (" + std::to_string(max_iter) + ") exceeded");
+            uint64_t total_now = 0;
+            for (uint32_t p = 0; p < n_preds; ++p) total_now += idb[p] ? dn[p] : 0;
+            const uint64_t K = std::min<uint64_t>(queue, max_iter - it);
+            if (K >= 2 && total_now) {
+                // ---- K queued steps, one read-back ----
+                std::vector<std::vector<std::pair<size_t, int>>> by_head(n_preds);  // (rule, delta position)
+                std::vector<std::vector<Var>> tmpl(n_preds);
+                for (size_t ri = 0; ri < chains.size(); ++ri)
+                    for (int d = 0; d < (int)chains[ri].path.size(); ++d) {
+                        if (!idb[chains[ri].path[d].pred]) continue;
+                        Var v;
+                        if (!make_var(ri, d, v)) continue;
+                        by_head[chains[ri].head].push_back({ri, d});
+                        tmpl[chains[ri].head].push_back(v);
+                    }
+                // delta buffers: ring[j % 2] holds the delta after step j of the batch (ring[0]: the current one)
+                std::vector<Buf<uint64_t>> ring[2];
+                std::vector<uint64_t> room(n_preds, 0);
+                ring[0].resize(n_preds);
+                ring[1].resize(n_preds);
+                for (uint32_t p = 0; p < n_preds; ++p) {
+                    if (!idb[p]) continue;
+                    // each step's appends: 4x the delta, growing with the deltas seen (a step past it overflows
+                    // and is rerun; XLOG_HIP_HASH_APPENDS below 2^20 fixes it, for tests of that path)
+                    cap[p] = min_want < (1ull << 20) ? min_want : std::max<uint64_t>({cap[p], 4 * dn[p], 1ull << 16});
+                    const uint64_t need = std::max(cap[p] + (uint64_t)tmpl[p].size() * HS_APPEND_SLACK, dn[p]);
+                    if (dcur[p].n >= need) {
+                        ring[0][p] = std::move(dcur[p]);
+                    } else {
+                        ring[0][p] = Buf<uint64_t>(ctx, need);
+                        if (dn[p]) copy_d2d(ctx, ring[0][p].p, dcur[p].p, dn[p]);
+                        dcur[p] = Buf<uint64_t>();
+                    }
+                    ring[1][p] = spare[p].n >= need ? std::move(spare[p]) : Buf<uint64_t>(ctx, need);
+                    HashSet &h = H[p];
+                    // room for two steps' appends at least; the steps' appends together stop at half load
+                    // (QueuedStep::room), and a step cut short by it is one more overflow and a rerun
+                    if (!tmpl[p].empty() && h.cap / 2 < h.size + 2 * cap[p]) hs_grow(ctx, h, 4 * (h.size + 2 * cap[p]));
+                    room[p] = h.cap / 2 > h.size ? h.cap / 2 - h.size : 0;
+                }
+                const uint32_t P = n_preds;
+                Buf<uint64_t> cnt(ctx, (K + 1) * P), ovf(ctx, K + 1);
+                fill_u64(ctx, cnt.p, 0ull, (K + 1) * P);
+                fill_u64(ctx, ovf.p, 0ull, K + 1);
+                unsigned long long *ucnt = reinterpret_cast<unsigned long long *>(cnt.p);
+                unsigned long long *uovf = reinterpret_cast<unsigned long long *>(ovf.p);
+                for (uint64_t j = 1; j <= K; ++j) {
+                    for (uint32_t p = 0; p < n_preds; ++p) {
+                        for (size_t t = 0; t < tmpl[p].size(); ++t) {
+                            Var v = tmpl[p][t];
+                            const int q = chains[by_head[p][t].first].path[by_head[p][t].second].pred;
+                            if (j == 1 && dn[q] == 0) continue;
+                            v.a.delta = ring[(j - 1) % 2][q].p;
+                            v.a.n = j == 1 ? dn[q] : cap[q];
+                            v.a.q.d_n = j == 1 ? nullptr : cnt.p + (j - 1) * P + q;
+                            v.a.q.stop = uovf + 1;
+                            v.a.q.prior = ucnt + P + p;
+                            v.a.q.nprior = (int)(j - 1);
+                            v.a.q.stride = (int)P;
+                            v.a.q.room = room[p];
+                            launch(H[p], v, ring[j % 2][p].p, cap[p], ucnt + j * P + p, uovf + j);
+                        }
+                    }
+                }
+                Buf<uint64_t> g(ctx, K * P + K);
+                copy_d2d(ctx, g.p, cnt.p + P, K * P);
+                copy_d2d(ctx, g.p + K * P, ovf.p + 1, K);
+                ctx->read_scalars(g.p, K * P + K);
+                std::vector<uint64_t> hc(ctx->host_scalars, ctx->host_scalars + K * P + K);
+                uint64_t j0 = 0;  // the first step that overflowed (0: none)
+                bool done = false;
+                uint64_t j = 1;
+                for (; j <= K; ++j) {
+                    if (hc[K * P + j - 1]) {
+                        j0 = j;
+                        break;
+                    }
+                    uint64_t total = 0;
+                    for (uint32_t p = 0; p < n_preds; ++p)
+                        if (idb[p]) {
+                            total += hc[(j - 1) * P + p];
+                            H[p].size += hc[(j - 1) * P + p];
+                            if (min_want >= (1ull << 20)) cap[p] = std::max(cap[p], 2 * hc[(j - 1) * P + p]);
+                        }
+                    ++it;
+                    deltas.push_back(total);
+                    if (total == 0) {
+                        done = true;
+                        break;
+                    }
+                }
+                if (done) break;
+                // the delta of the last complete step becomes the current one
+                const uint64_t last = j0 ? j0 - 1 : K;
+                for (uint32_t p = 0; p < n_preds; ++p) {
+                    if (!idb[p]) continue;
+                    if (last) dn[p] = hc[(last - 1) * P + p];
+                    dcur[p] = std::move(ring[last % 2][p]);
+                    spare[p] = std::move(ring[(last + 1) % 2][p]);
+                }
+                if (!j0) {
+                    queue = std::min<uint64_t>(queue_max, queue * 2);
+                    continue;
+                }
+                // step j0 overflowed: rerun it with the host's sizes, keeping what it appended (in spare)
+                XH_REQUIRE(it < max_iter, XLOG_HIP_ITERATION_LIMIT,
+                           "Recursive SCC iteration limit (" + std::to_string(max_iter) + ") exceeded");
+                ++it;
+                std::vector<std::vector<Var>> vars = pass_vars(false);
+                std::vector<uint64_t> appended(n_preds, 0);
+                std::vector<Buf<uint64_t>> out(n_preds);
+                for (uint32_t p = 0; p < n_preds; ++p) {
+                    if (!idb[p]) continue;
+                    appended[p] = hc[(j0 - 1) * P + p];
+                    out[p] = std::move(spare[p]);
+                }
+                sync_pass(vars, appended, out);
+                for (uint32_t p = 0; p < n_preds; ++p)
+                    if (idb[p] && min_want >= (1ull << 20)) cap[p] = std::max(cap[p], 2 * appended[p]);
+                const uint64_t total = finish_pass(appended, out);
+                deltas.push_back(total);
+                queue = std::max<uint64_t>(2, j0);
+                if (total == 0) break;
+                continue;
+            }
+            // ---- one synchronous iteration ----
+            ++it;
+            std::vector<std::vector<Var>> vars = pass_vars(false);
+            std::vector<uint64_t> appended(n_preds, 0);
+            std::vector<Buf<uint64_t>> out(n_preds);
+            sync_pass(vars, appended, out);
+            const uint64_t total = finish_pass(appended, out);
             deltas.push_back(total);
-            if (pass && total == 0) break;
+            if (total == 0) break;
         }
         // predicates not kept sorted: their sets, sorted once
         for (uint32_t p = 0; p < n_preds; ++p) {
@@ -2163,98 +2316,6 @@ static bool run_chain_route(Ctx *ctx, const std::vector<Rule> &rules, uint32_t n
     return true;
 }
 
-// Transitive closure over the device hash set: the persistent-table form of
-// the reference's sparse factorized delta (fj_delta_sparse_novel_u32_recorded,
-// provider/fj_delta_sparse.rs:66) inside the semi-naive loop of
-// recursive.rs:447-957.  R is the set.  The seed is R = delta_0 = edge; every
-// iteration is one fused pass (expand delta (x, y) through the edges of y,
-// insert (x, z), append the inserted tuples as the next delta) and one
-// read-back of the appended count and the overflow flag.  The iteration count
-// includes the final empty iteration; R is sorted once at the end.
-// XLOG_HIP_HASH_SLOTS / XLOG_HIP_HASH_APPENDS override the initial table size
-// and the appends allowed per attempt (tests force the grow-and-rerun path).
-static void tc_fixpoint_hash(Ctx *ctx, const DRel &edges, uint64_t max_iter, uint64_t **res, uint64_t *res_n,
-                             uint64_t *iterations, std::vector<uint64_t> &deltas) {
-    *res = nullptr;
-    *res_n = 0;
-    deltas.push_back(edges.n);
-    uint64_t it = 0;
-    if (edges.n == 0) {  // the seed and the one empty iteration
-        deltas.push_back(0);
-        *iterations = 1;
-        return;
-    }
-    JoinIndex J;  // edges by source: runs of targets
-    build_join_index(ctx, edges.k, edges.n, 2, 0, true, J);
-    const uint64_t avg_deg = std::max<uint64_t>(1, (edges.n + J.ix.nruns - 1) / std::max<uint64_t>(1, J.ix.nruns));
-    HashSet h;
-    hs_init(ctx, h, env_u64("XLOG_HIP_HASH_SLOTS", std::max<uint64_t>(4 * edges.n, 1ull << 16)));
-    if (h.cap / 2 < edges.n) hs_grow(ctx, h, 4 * edges.n);
-    hs_insert_all(ctx, h, edges.k, edges.n);
-    h.size = edges.n;
-    const uint64_t min_want = env_u64("XLOG_HIP_HASH_APPENDS", 1ull << 20);
-    const uint64_t *cur = edges.k;
-    uint64_t ncur = edges.n;
-    Buf<uint64_t> bufs[2];
-    int nb = 0;
-    for (;;) {
-        XH_REQUIRE(it < max_iter, XLOG_HIP_ITERATION_LIMIT,
-                   "Recursive SCC iteration limit (" + std::to_string(max_iter) + ") exceeded");
-        ++it;
-        Buf<uint64_t> &out = bufs[nb];
-        fill_u64(ctx, h.flags.p + 1, 0ull, 2);  // overflow, appended count
-        // appends allowed per attempt: the expected candidate count (a bound on the novel ones)
-        uint64_t want = std::max<uint64_t>(min_want, ncur * avg_deg + ncur / 4);
-        if (min_want < (1ull << 20)) want = min_want;                          // forced small (tests)
-        uint64_t appended = 0;
-        for (;;) {
-            uint64_t room = h.cap / 2 > h.size + appended ? h.cap / 2 - h.size - appended : 0;
-            if (room < want) {
-                // 4x what this step needs: R keeps growing, and every rehash re-inserts all of it
-                hs_grow(ctx, h, 4 * (h.size + appended + want));
-                room = h.cap / 2 - h.size - appended;
-            }
-            const uint64_t limit = appended + std::min(want, room);
-            if (out.n < limit + HS_APPEND_SLACK) {  // keep the tuples appended by an earlier attempt
-                Buf<uint64_t> bigger(ctx, limit + HS_APPEND_SLACK);
-                if (appended) copy_d2d(ctx, bigger.p, out.p, appended);
-                out = std::move(bigger);
-            }
-            hs_join_insert(ctx, h, cur, ncur, 0, 1, J.ix, J.payload.p, out.p, limit);
-            ctx->read_scalars(h.flags.p + 1, 2);
-            const uint64_t overflow = ctx->host_scalars[0];
-            appended = ctx->host_scalars[1];
-            if (!overflow) break;
-            // the limit or a full table stopped the pass: grow and run it again; the tuples it inserted
-            // are found present and are not appended twice
-            fill_u64(ctx, h.flags.p + 1, 0ull, 1);
-            want *= 4;
-        }
-        h.size += appended;
-        deltas.push_back(appended);
-        if (appended == 0) break;
-        cur = out.p;
-        ncur = appended;
-        nb ^= 1;
-    }
-    *iterations = it;
-    bufs[0] = Buf<uint64_t>();
-    bufs[1] = Buf<uint64_t>();
-    uint64_t *all = static_cast<uint64_t *>(ctx->alloc(h.size * sizeof(uint64_t)));
-    uint64_t got = 0;
-    try {
-        got = hs_collect(ctx, h, all);
-        XH_REQUIRE(got == h.size, XLOG_HIP_DEVICE_ERROR,
-                   "hash set holds " + std::to_string(got) + " tuples, expected " + std::to_string(h.size));
-        h = HashSet();
-    } catch (...) {
-        ctx->free(all);
-        throw;
-    }
-    *res = sort_keys(ctx, all, got, true);  // consumes all
-    *res_n = got;
-}
-
 static void run_fixpoint_impl(Ctx *ctx, const int32_t *plan, uint32_t n_preds, const xlog_hip_rel *const *rels,
                               xlog_hip_rel **out, xlog_hip_fixpoint_stats *stats, std::vector<uint64_t> &deltas) {
     XH_REQUIRE(n_preds >= 1 && n_preds <= 256, XLOG_HIP_INVALID_ARG, "n_preds must be 1..256");
@@ -2278,11 +2339,11 @@ static void run_fixpoint_impl(Ctx *ctx, const int32_t *plan, uint32_t n_preds, c
     std::vector<ChainRule> paths;
     bool short_paths = chain_shape(rules, paths);
     for (const ChainRule &c : paths) short_paths = short_paths && c.path.size() <= 3;
-    XH_REQUIRE(route != XLOG_HIP_ROUTE_HASH || (tc && head_empty) || short_paths, XLOG_HIP_UNSUPPORTED,
+    XH_REQUIRE(route != XLOG_HIP_ROUTE_HASH || short_paths, XLOG_HIP_UNSUPPORTED,
                "hash route needs rule bodies of 1 to 3 atoms forming a path between the head variables");
     uint64_t nv = 0;  // max id + 1 (up to 2^32)
     DRel edges;
-    if (tc && head_empty && route != XLOG_HIP_ROUTE_JOIN) {
+    if (tc && head_empty && route != XLOG_HIP_ROUTE_JOIN && route != XLOG_HIP_ROUTE_HASH) {
         edges = canon_drel(ctx, rels[E]);
         if (edges.n) {
             Buf<unsigned int> mx(ctx, 1);
@@ -2295,22 +2356,7 @@ static void run_fixpoint_impl(Ctx *ctx, const int32_t *plan, uint32_t n_preds, c
     }
     const bool bitmap = tc && head_empty && route != XLOG_HIP_ROUTE_JOIN && route != XLOG_HIP_ROUTE_HASH &&
                         nv <= (1ull << 17);
-    // above the dense domain (or when asked for) the closure runs over the device hash set
-    const bool hashset = tc && head_empty && !bitmap &&
-                         (route == XLOG_HIP_ROUTE_HASH || (route == XLOG_HIP_ROUTE_AUTO && nv > (1ull << 17)));
-    if (hashset) {
-        uint64_t *res = nullptr, n = 0;
-        try {
-            tc_fixpoint_hash(ctx, edges, max_iter, &res, &n, &iterations, deltas);
-        } catch (...) {
-            if (edges.owned) ctx->free(edges.k);
-            throw;
-        }
-        if (edges.owned) ctx->free(edges.k);
-        out[H] = n ? rel_adopt(ctx, 2, n, res, nullptr, REL_CANONICAL) : rel_new(ctx, 2, 0);
-        out[H]->flags = REL_CANONICAL;
-        if (stats) stats->route = XLOG_HIP_ROUTE_HASH;
-    } else if (bitmap) {
+    if (bitmap) {
         // With the head empty, Δ of iteration k is the set of pairs at shortest distance k + 1 whether the
         // step is Δ ∘ edge (the plan as written) or edge ∘ Δ: a shortest path of length k + 2 splits off its
         // last edge or its first edge, and every other derivation lies in R.  So the left-linear chain

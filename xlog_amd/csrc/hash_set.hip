@@ -127,6 +127,21 @@ __device__ __forceinline__ uint64_t wave_append(bool novel, uint64_t key, uint64
 // a full table seen by any lane stops the wave
 __device__ __forceinline__ bool any_full(bool full) { return __ballot(full) != 0ull; }
 
+// A queued step's row count and limit (QueuedStep); false when an earlier
+// step overflowed and this one is to do nothing.  Every thread reads the
+// same words, written by earlier launches, so the answer is uniform.
+__device__ __forceinline__ bool queued_prologue(const QueuedStep &q, uint64_t &n, uint64_t &limit) {
+    uint64_t used = 0;
+    for (int t = 0; t < q.nprior; ++t) {
+        if (q.stop[t]) return false;
+        used += q.prior[(uint64_t)t * q.stride];
+    }
+    if (q.d_n && *q.d_n < n) n = *q.d_n;
+    const uint64_t left = used < q.room ? q.room - used : 0;
+    if (left < limit) limit = left;
+    return true;
+}
+
 // Inserts keys[0..n) (no novelty bookkeeping): the initial full relation, or
 // the keys of an old table being rehashed (old slots; empty ones skipped).
 __global__ void k_hs_insert_all(const uint64_t *__restrict__ keys, uint64_t n, SetView s,
@@ -153,9 +168,13 @@ __global__ void k_hs_insert_all(const uint64_t *__restrict__ keys, uint64_t n, S
 
 // Inserts keys[0..n) and appends the novel ones to out (capacity limit):
 // the generic set-difference-and-merge of a candidate bag.
+// With swap the keys' words are exchanged first; q is a queued step or
+// empty.
 __global__ __launch_bounds__(HB) void k_hs_insert_novel(const uint64_t *__restrict__ keys, uint64_t n, SetView s,
                                                         uint64_t *__restrict__ out, unsigned long long *count,
-                                                        uint64_t limit, unsigned long long *overflow) {
+                                                        uint64_t limit, unsigned long long *overflow, int swap,
+                                                        QueuedStep q) {
+    if (!queued_prologue(q, n, limit)) return;
     const int lane = threadIdx.x & (WAVE - 1);
     const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
     // whole waves step together so that the append's ballot sees every lane
@@ -165,6 +184,7 @@ __global__ __launch_bounds__(HB) void k_hs_insert_novel(const uint64_t *__restri
         uint64_t k = 0;
         if (i < n) {
             k = keys[i];
+            if (swap) k = (k << 32) | (k >> 32);
             const int r = hs_insert(s, k);
             full = r == 2;
             novel = r == 1;
@@ -342,12 +362,14 @@ __global__ __launch_bounds__(HB) void k_hs_path_insert(PathInsertArgs a, SetView
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
     const uint64_t gwave = (uint64_t)blockIdx.x * (HB / WAVE) + (uint64_t)wave;
     const uint64_t nwaves = (uint64_t)gridDim.x * (HB / WAVE);
+    uint64_t n = a.n;
+    if (!queued_prologue(a.q, n, limit)) return;  // an earlier queued step overflowed
     unsigned long long cand = 0;
-    for (uint64_t rbase = gwave * WAVE; rbase < a.n; rbase += nwaves * WAVE) {
+    for (uint64_t rbase = gwave * WAVE; rbase < n; rbase += nwaves * WAVE) {
         const uint64_t i = rbase + lane;
         uint32_t xa = 0, xb = 0, len1 = 0;
         uint64_t st1 = 0;
-        if (i < a.n) {
+        if (i < n) {
             const uint64_t row = a.delta[i];
             xa = a.delta_swap ? (uint32_t)row : (uint32_t)(row >> 32);
             xb = a.delta_swap ? (uint32_t)(row >> 32) : (uint32_t)row;
@@ -547,10 +569,11 @@ void hs_join_insert(Ctx *ctx, HashSet &h, const uint64_t *delta, uint64_t n, int
     XH_CHECK_HIP(hipGetLastError());
 }
 
-void hs_path_insert(Ctx *ctx, HashSet &h, const PathInsertArgs &a, uint64_t *out, uint64_t limit) {
+void hs_path_insert(Ctx *ctx, HashSet &h, const PathInsertArgs &a, uint64_t *out, uint64_t limit,
+                    unsigned long long *count, unsigned long long *overflow) {
     if (!a.n) return;
-    unsigned long long *ovf = reinterpret_cast<unsigned long long *>(h.flags.p + 1);
-    unsigned long long *cnt = reinterpret_cast<unsigned long long *>(h.flags.p + 2);
+    unsigned long long *ovf = overflow ? overflow : reinterpret_cast<unsigned long long *>(h.flags.p + 1);
+    unsigned long long *cnt = count ? count : reinterpret_cast<unsigned long long *>(h.flags.p + 2);
     Prof prof(ctx, XLOG_HIP_KERNEL_HASH_INSERT, 24.0 * (double)a.n);
     unsigned long long *work = prof.work(1.0);
     const uint64_t waves = (a.n + WAVE - 1) / WAVE;
@@ -564,13 +587,14 @@ void hs_path_insert(Ctx *ctx, HashSet &h, const PathInsertArgs &a, uint64_t *out
     XH_CHECK_HIP(hipGetLastError());
 }
 
-void hs_insert_novel(Ctx *ctx, HashSet &h, const uint64_t *keys, uint64_t n, uint64_t *out, uint64_t limit) {
+void hs_insert_novel(Ctx *ctx, HashSet &h, const uint64_t *keys, uint64_t n, uint64_t *out, uint64_t limit,
+                     int swap, unsigned long long *count, unsigned long long *overflow, const QueuedStep *q) {
     if (!n) return;
-    unsigned long long *ovf = reinterpret_cast<unsigned long long *>(h.flags.p + 1);
-    unsigned long long *cnt = reinterpret_cast<unsigned long long *>(h.flags.p + 2);
+    unsigned long long *ovf = overflow ? overflow : reinterpret_cast<unsigned long long *>(h.flags.p + 1);
+    unsigned long long *cnt = count ? count : reinterpret_cast<unsigned long long *>(h.flags.p + 2);
     Prof prof(ctx, XLOG_HIP_KERNEL_HASH_INSERT, 16.0 * (double)n);
     hipLaunchKernelGGL(k_hs_insert_novel, dim3(grid_blocks(ctx, n)), dim3(HB), 0, ctx->stream, keys, n, view(h), out,
-                       cnt, limit, ovf);
+                       cnt, limit, ovf, swap, q ? *q : QueuedStep());
     XH_CHECK_HIP(hipGetLastError());
 }
 

@@ -410,8 +410,27 @@ void hs_grow(Ctx *ctx, HashSet &h, uint64_t min_cap);
 // needs limit + HS_APPEND_SLACK entries.
 void hs_join_insert(Ctx *ctx, HashSet &h, const uint64_t *delta, uint64_t n, int key_hi, int out_carry_hi,
                     const RunIndex &ix, const uint32_t *payload, uint64_t *out, uint64_t limit);
-// inserts keys[0..n) and appends the novel ones (same protocol)
-void hs_insert_novel(Ctx *ctx, HashSet &h, const uint64_t *keys, uint64_t n, uint64_t *out, uint64_t limit);
+// One step of a queue of fixpoint steps launched with no read-back between
+// them: the step's row count is on the device (d_n; the host's n is a bound),
+// stop[0 .. nprior) are the overflow flags of the earlier steps (any one set:
+// the launch does nothing) and prior[t * stride] for t < nprior the tuples
+// this head appended in them.  `room` bounds the appends of all the steps
+// together (the set stays at most half full): the launch's limit is cut to
+// room minus the earlier steps' appends.
+struct QueuedStep {
+    const uint64_t *d_n = nullptr;
+    const unsigned long long *stop = nullptr;
+    const unsigned long long *prior = nullptr;
+    int nprior = 0;
+    int stride = 0;
+    uint64_t room = ~0ull;
+};
+// inserts keys[0..n) and appends the novel ones (same protocol); optionally
+// the keys' words exchanged (swap), the appended count and overflow flag
+// elsewhere than the set's flags, and a queued step
+void hs_insert_novel(Ctx *ctx, HashSet &h, const uint64_t *keys, uint64_t n, uint64_t *out, uint64_t limit,
+                     int swap = 0, unsigned long long *count = nullptr, unsigned long long *overflow = nullptr,
+                     const QueuedStep *q = nullptr);
 // One step of a path-shaped rule body of two or three atoms, same protocol:
 // every delta row, read as the path values (xa, xb) of the delta atom (the
 // high then low word, swapped when delta_swap), is expanded through hop 1 (the
@@ -426,14 +445,16 @@ struct PathHop {
 };
 struct PathInsertArgs {
     const uint64_t *delta = nullptr;
-    uint64_t n = 0;
+    uint64_t n = 0;  // delta rows (a bound in a queued step)
+    QueuedStep q;    // optional: a queued step
     int delta_swap = 0;
     PathHop h1, h2;
     int key1 = 0;  // 0: xa, 1: xb
     int key2 = 0;  // 0: xa, 1: xb, 2: v1
     int out0 = 0, out1 = 0;
 };
-void hs_path_insert(Ctx *ctx, HashSet &h, const PathInsertArgs &a, uint64_t *out, uint64_t limit);
+void hs_path_insert(Ctx *ctx, HashSet &h, const PathInsertArgs &a, uint64_t *out, uint64_t limit,
+                    unsigned long long *count = nullptr, unsigned long long *overflow = nullptr);
 // every tuple of the set, unordered, into out (h.size entries); returns the count
 uint64_t hs_collect(Ctx *ctx, const HashSet &h, uint64_t *out);
 // appends past `limit`: one 64-tuple chunk per wave of the insert grid
