@@ -188,7 +188,13 @@ __global__ void k_col_unsorted(RelView in, int c, uint64_t n, uint32_t *flag) {
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i + 1 < n; i += stride)
         if (col_value(in, c, i) > col_value(in, c, i + 1)) *flag = 1u;
 }
-__global__ void k_max_u32_of_packed(const uint64_t *__restrict__ k, uint64_t n, unsigned int *mx) {
+// The largest word of n packed rows into *mx (atomicMax: *mx starts at 0 or
+// at an earlier maximum).  One atomic per block; launched with at most
+// 1024 blocks of 256 threads (MAX_LAUNCH_1D), so the atomics on the one
+// address stay few.
+__global__ __launch_bounds__(256) void k_max_u32_of_packed(const uint64_t *__restrict__ k, uint64_t n,
+                                                           unsigned int *mx) {
+    __shared__ unsigned int s_m[4];
     uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
     unsigned int m = 0;
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
@@ -198,7 +204,9 @@ __global__ void k_max_u32_of_packed(const uint64_t *__restrict__ k, uint64_t n, 
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) m = max(m, (unsigned)__shfl_xor((int)m, o, 64));
-    if ((threadIdx.x & 63) == 0) atomicMax(mx, m);
+    if ((threadIdx.x & 63) == 0) s_m[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) atomicMax(mx, max(max(s_m[0], s_m[1]), max(s_m[2], s_m[3])));
 }
 __global__ void k_u64_to_u32(const uint64_t *__restrict__ in, uint64_t n, uint32_t *__restrict__ out) {
     uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
@@ -219,6 +227,14 @@ void scan_u64_small(Ctx *ctx, uint64_t *a, uint64_t n, uint64_t *total);
     do {                                                                                                    \
         if ((n) > 0) {                                                                                      \
             hipLaunchKernelGGL(kern, dim3(grid_for((n), 256, 16384)), dim3(256), 0, ctx->stream, __VA_ARGS__); \
+            XH_CHECK_HIP(hipGetLastError());                                                                \
+        }                                                                                                   \
+    } while (0)
+// LAUNCH_1D with at most 1024 blocks (grid-stride reductions into one word)
+#define MAX_LAUNCH_1D(kern, n, ...)                                                                         \
+    do {                                                                                                    \
+        if ((n) > 0) {                                                                                      \
+            hipLaunchKernelGGL(kern, dim3(grid_for((n), 256, 1024)), dim3(256), 0, ctx->stream, __VA_ARGS__);  \
             XH_CHECK_HIP(hipGetLastError());                                                                \
         }                                                                                                   \
     } while (0)
@@ -1069,7 +1085,7 @@ static xlog_hip_rel *op_fj_delta(Ctx *ctx, const xlog_hip_rel *delta, const xlog
         fill_u32(ctx, mx.p, 0u, 1);
         const xlog_hip_rel *rs[3] = {delta, edge, full};
         for (const xlog_hip_rel *r : rs)
-            if (r->rows) LAUNCH_1D(k_max_u32_of_packed, r->rows, r->w[0], r->rows, mx.p);
+            if (r->rows) MAX_LAUNCH_1D(k_max_u32_of_packed, r->rows, r->w[0], r->rows, mx.p);
         uint32_t h = 0;
         XH_CHECK_HIP(hipMemcpyAsync(&h, mx.p, 4, hipMemcpyDeviceToHost, ctx->stream));
         ctx->sync();
@@ -2236,14 +2252,12 @@ static DRel canon_drel(Ctx *ctx, const xlog_hip_rel *r) {
 // The dense chain route (chain_fixpoint) when the plan is made of chain rules
 // over at most 2^17 ids whose bit matrices fit in half the free device
 // memory; false (nothing done) when the join route should run instead, an
-// error when the bitmap route was requested and cannot run.  Consumes `edges`
-// (the canonical edge list of the transitive-closure check, if any).
-static bool run_chain_route(Ctx *ctx, const std::vector<Rule> &rules, uint32_t n_preds,
-                            const xlog_hip_rel *const *rels, uint64_t route, uint64_t max_iter, xlog_hip_rel **out,
-                            uint64_t *iterations, std::vector<uint64_t> &deltas, xlog_hip_fixpoint_stats *stats,
-                            DRel &edges) {
-    if (edges.owned) ctx->free(edges.k);
-    edges = DRel();
+// error when the bitmap route was requested and cannot run.  canon: every
+// predicate's relation, sorted and unique (read, not consumed); domain: the
+// largest id + 1 (0 when every relation is empty).
+static bool run_chain_route(Ctx *ctx, const std::vector<Rule> &rules, uint32_t n_preds, const std::vector<DRel> &canon,
+                            uint64_t domain, uint64_t route, uint64_t max_iter, xlog_hip_rel **out,
+                            uint64_t *iterations, std::vector<uint64_t> &deltas, xlog_hip_fixpoint_stats *stats) {
     std::vector<ChainRule> chains;
     bool chain = route != XLOG_HIP_ROUTE_JOIN && chain_shape(rules, chains);
     XH_REQUIRE(chain || route != XLOG_HIP_ROUTE_BITMAP, XLOG_HIP_UNSUPPORTED,
@@ -2251,43 +2265,20 @@ static bool run_chain_route(Ctx *ctx, const std::vector<Rule> &rules, uint32_t n
     if (!chain) return false;
     std::vector<char> idb(n_preds, 0);
     for (const Rule &r : rules) idb[r.head] = 1;
-    std::vector<DRel> canon(n_preds);
     std::vector<uint64_t *> res;
     auto release = [&]() {
-        for (auto &d : canon)
-            if (d.owned) ctx->free(d.k);
-        canon.clear();
         for (uint64_t *q : res)
             if (q) ctx->free(q);
         res.clear();
     };
     try {
-        for (uint32_t p = 0; p < n_preds; ++p) canon[p] = canon_drel(ctx, rels[p]);
-        uint64_t any = 0;
-        Buf<unsigned int> mx(ctx, 1);
-        fill_u32(ctx, mx.p, 0u, 1);
-        for (uint32_t p = 0; p < n_preds; ++p)
-            if (canon[p].n) {
-                any += canon[p].n;
-                LAUNCH_1D(k_max_u32_of_packed, canon[p].n, canon[p].k, canon[p].n, mx.p);
-            }
-        uint64_t domain = 0;
-        if (any) {
-            XH_CHECK_HIP(hipMemcpyAsync(ctx->host_scalars, mx.p, sizeof(unsigned int), hipMemcpyDeviceToHost,
-                                        ctx->stream));
-            ctx->sync();
-            domain = (uint64_t)*reinterpret_cast<uint32_t *>(ctx->host_scalars) + 1;
-        }
         size_t free_b = 0, total_b = 0;
         XH_CHECK_HIP(hipMemGetInfo(&free_b, &total_b));
         const bool fits = domain >= 1 && domain <= (1ull << 17) &&
                           chain_fixpoint_bytes(chains, idb, (uint32_t)domain) <= (uint64_t)free_b / 2;
         XH_REQUIRE(fits || route != XLOG_HIP_ROUTE_BITMAP, XLOG_HIP_UNSUPPORTED,
                    "bitmap route needs 1..2^17 ids and room for the bit matrices");
-        if (!fits) {
-            release();
-            return false;
-        }
+        if (!fits) return false;
         std::vector<const uint64_t *> keys(n_preds);
         std::vector<uint64_t> rows(n_preds), res_n;
         for (uint32_t p = 0; p < n_preds; ++p) {
@@ -2341,21 +2332,34 @@ static void run_fixpoint_impl(Ctx *ctx, const int32_t *plan, uint32_t n_preds, c
     for (const ChainRule &c : paths) short_paths = short_paths && c.path.size() <= 3;
     XH_REQUIRE(route != XLOG_HIP_ROUTE_HASH || short_paths, XLOG_HIP_UNSUPPORTED,
                "hash route needs rule bodies of 1 to 3 atoms forming a path between the head variables");
-    uint64_t nv = 0;  // max id + 1 (up to 2^32)
-    DRel edges;
-    if (tc && head_empty && route != XLOG_HIP_ROUTE_JOIN && route != XLOG_HIP_ROUTE_HASH) {
-        edges = canon_drel(ctx, rels[E]);
-        if (edges.n) {
-            Buf<unsigned int> mx(ctx, 1);
-            fill_u32(ctx, mx.p, 0u, 1);
-            LAUNCH_1D(k_max_u32_of_packed, edges.n, edges.k, edges.n, mx.p);
-            XH_CHECK_HIP(hipMemcpyAsync(ctx->host_scalars, mx.p, sizeof(unsigned int), hipMemcpyDeviceToHost, ctx->stream));
-            ctx->sync();
-            nv = (uint64_t)*reinterpret_cast<uint32_t *>(ctx->host_scalars) + 1;
+    // every relation sorted and unique once, and the largest id (one read-back) for every route: the bitmap
+    // routes' domain, and the digits the sorts inside the join and hash routes' loops can vary in
+    struct Canon {
+        Ctx *ctx;
+        std::vector<DRel> d;
+        ~Canon() {
+            for (DRel &r : d)
+                if (r.owned) ctx->free(r.k);
+        }
+    } canon{ctx, std::vector<DRel>(n_preds)};
+    uint64_t nv = 0;  // max id + 1 (up to 2^32; 0 when every relation is empty)
+    {
+        Buf<unsigned int> mx(ctx, 2);  // read back as one u64: the maximum in its low half
+        fill_u32(ctx, mx.p, 0u, 2);
+        uint64_t any = 0;
+        for (uint32_t p = 0; p < n_preds; ++p) {
+            canon.d[p] = canon_drel(ctx, rels[p]);
+            any += canon.d[p].n;
+            MAX_LAUNCH_1D(k_max_u32_of_packed, canon.d[p].n, canon.d[p].k, canon.d[p].n, mx.p);
+        }
+        if (any) {
+            ctx->read_scalars(mx.p, 1);
+            nv = (uint64_t)(uint32_t)ctx->host_scalars[0] + 1;
         }
     }
     const bool bitmap = tc && head_empty && route != XLOG_HIP_ROUTE_JOIN && route != XLOG_HIP_ROUTE_HASH &&
                         nv <= (1ull << 17);
+    const DRel &edges = tc ? canon.d[E] : canon.d[0];
     if (bitmap) {
         // With the head empty, Δ of iteration k is the set of pairs at shortest distance k + 1 whether the
         // step is Δ ∘ edge (the plan as written) or edge ∘ Δ: a shortest path of length k + 2 splits off its
@@ -2384,20 +2388,16 @@ static void run_fixpoint_impl(Ctx *ctx, const int32_t *plan, uint32_t n_preds, c
                 n = res_n[H];
             }
         } catch (...) {
-            if (edges.owned) ctx->free(edges.k);
             if (stats) stats->iterations = deltas.empty() ? 0 : deltas.size() - 1;
             throw;
         }
-        if (edges.owned) ctx->free(edges.k);
         out[H] = n ? rel_adopt(ctx, 2, n, res, nullptr, REL_CANONICAL) : rel_new(ctx, 2, 0);
         out[H]->flags = REL_CANONICAL;
         if (stats) stats->route = XLOG_HIP_ROUTE_BITMAP;
     } else if (route != XLOG_HIP_ROUTE_HASH &&
-               run_chain_route(ctx, rules, n_preds, rels, route, max_iter, out, &iterations, deltas, stats, edges)) {
+               run_chain_route(ctx, rules, n_preds, canon.d, nv, route, max_iter, out, &iterations, deltas, stats)) {
         if (stats) stats->route = XLOG_HIP_ROUTE_BITMAP;
     } else {
-        if (edges.owned) ctx->free(edges.k);
-        edges = DRel();
         // Path-shaped plans the bitmap route does not take run over hash sets under AUTO, except (1) when a
         // join-row limit is set (the limit is defined on the join route's bags) and (2) when a three-atom
         // rule reads two or more IDB atoms (Andersen's load and store rules): its two-hop expansions then
@@ -2417,18 +2417,14 @@ static void run_fixpoint_impl(Ctx *ctx, const int32_t *plan, uint32_t n_preds, c
         for (const Rule &r : rules) drv.idb[r.head] = true;
         drv.max_join_rows = stats ? stats->max_join_rows : 0;
         for (uint32_t p = 0; p < n_preds; ++p) {
-            drv.full[p] = canon_drel(ctx, rels[p]);
+            drv.full[p] = canon.d[p];  // the driver owns them now
+            canon.d[p].owned = false;
             drv.full[p].version = drv.version_counter++;
         }
         {
             // Every derived value comes from the inputs, so the largest input id bounds the digits a packed
             // tuple can vary in: sorts inside the loop run those passes without reading histograms back.
-            Buf<unsigned int> mx(ctx, 1);
-            fill_u32(ctx, mx.p, 0u, 1);
-            for (uint32_t p = 0; p < n_preds; ++p)
-                if (drv.full[p].n) LAUNCH_1D(k_max_u32_of_packed, drv.full[p].n, drv.full[p].k, drv.full[p].n, mx.p);
-            ctx->read_scalars(mx.p, 1);
-            const uint32_t maxid = (uint32_t)ctx->host_scalars[0];
+            const uint32_t maxid = nv ? (uint32_t)(nv - 1) : 0u;
             const int bits = maxid ? 32 - __builtin_clz(maxid) : 0;
             const uint32_t nd = (uint32_t)(bits + 7) / 8;  // bytes per column
             drv.digits = nd ? (((1u << nd) - 1u) | (((1u << nd) - 1u) << 4)) : 1u;

@@ -173,8 +173,9 @@ __global__ void k_hs_insert_all(const uint64_t *__restrict__ keys, uint64_t n, S
 __global__ __launch_bounds__(HB) void k_hs_insert_novel(const uint64_t *__restrict__ keys, uint64_t n, SetView s,
                                                         uint64_t *__restrict__ out, unsigned long long *count,
                                                         uint64_t limit, unsigned long long *overflow, int swap,
-                                                        QueuedStep q) {
+                                                        QueuedStep q, unsigned long long *work) {
     if (!queued_prologue(q, n, limit)) return;
+    if (work && blockIdx.x == 0 && threadIdx.x == 0) atomicAdd(work, 16ull * n);  // algorithmic: key + slot
     const int lane = threadIdx.x & (WAVE - 1);
     const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
     // whole waves step together so that the append's ballot sees every lane
@@ -364,6 +365,7 @@ __global__ __launch_bounds__(HB) void k_hs_path_insert(PathInsertArgs a, SetView
     const uint64_t nwaves = (uint64_t)gridDim.x * (HB / WAVE);
     uint64_t n = a.n;
     if (!queued_prologue(a.q, n, limit)) return;  // an earlier queued step overflowed
+    if (work && blockIdx.x == 0 && threadIdx.x == 0) atomicAdd(work, 24ull * n);
     unsigned long long cand = 0;
     for (uint64_t rbase = gwave * WAVE; rbase < n; rbase += nwaves * WAVE) {
         const uint64_t i = rbase + lane;
@@ -480,7 +482,8 @@ __global__ __launch_bounds__(HB) void k_hs_path_insert(PathInsertArgs a, SetView
         __builtin_amdgcn_wave_barrier();
     }
     if (work) {
-        // algorithmic bytes: delta row + slot per row; per candidate its value (4 B) + slot word (8 B)
+        // algorithmic bytes: per candidate its value (4 B) + slot word (8 B); the delta row + run slot per
+        // row (24 B) are added above
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) cand += __shfl_xor(cand, o, WAVE);
         if (lane == 0) atomicAdd(work + (blockIdx.x & 63), cand * 12ull);
@@ -574,7 +577,7 @@ void hs_path_insert(Ctx *ctx, HashSet &h, const PathInsertArgs &a, uint64_t *out
     if (!a.n) return;
     unsigned long long *ovf = overflow ? overflow : reinterpret_cast<unsigned long long *>(h.flags.p + 1);
     unsigned long long *cnt = count ? count : reinterpret_cast<unsigned long long *>(h.flags.p + 2);
-    Prof prof(ctx, XLOG_HIP_KERNEL_HASH_INSERT, 24.0 * (double)a.n);
+    Prof prof(ctx, XLOG_HIP_KERNEL_HASH_INSERT, 0.0);  // bytes counted on the device (the row count may be there)
     unsigned long long *work = prof.work(1.0);
     const uint64_t waves = (a.n + WAVE - 1) / WAVE;
     const unsigned grid = grid_for(waves * WAVE, HB, std::min<unsigned>((unsigned)ctx->num_cus * 32, HS_MAX_BLOCKS));
@@ -592,9 +595,9 @@ void hs_insert_novel(Ctx *ctx, HashSet &h, const uint64_t *keys, uint64_t n, uin
     if (!n) return;
     unsigned long long *ovf = overflow ? overflow : reinterpret_cast<unsigned long long *>(h.flags.p + 1);
     unsigned long long *cnt = count ? count : reinterpret_cast<unsigned long long *>(h.flags.p + 2);
-    Prof prof(ctx, XLOG_HIP_KERNEL_HASH_INSERT, 16.0 * (double)n);
+    Prof prof(ctx, XLOG_HIP_KERNEL_HASH_INSERT, 0.0);  // bytes counted on the device
     hipLaunchKernelGGL(k_hs_insert_novel, dim3(grid_blocks(ctx, n)), dim3(HB), 0, ctx->stream, keys, n, view(h), out,
-                       cnt, limit, ovf, swap, q ? *q : QueuedStep());
+                       cnt, limit, ovf, swap, q ? *q : QueuedStep(), prof.work(1.0));
     XH_CHECK_HIP(hipGetLastError());
 }
 

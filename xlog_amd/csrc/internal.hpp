@@ -133,7 +133,7 @@ struct Ctx {
     void prof_resolve();  // synchronises, folds pending records into the totals
     // device counters that profiled launches add their work units to; read
     // back and cleared by prof_resolve
-    static constexpr int PROF_WORK_SLOTS = 1024;
+    static constexpr int PROF_WORK_SLOTS = 16384;
     // each slot is PROF_WORK_SPREAD counters: a launch's blocks add to counter
     // (block id mod PROF_WORK_SPREAD) so that thousands of blocks do not
     // serialise on one address
