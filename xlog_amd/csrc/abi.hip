@@ -394,6 +394,31 @@ static uint64_t unique_keys(Ctx *ctx, const uint64_t *sorted, uint64_t n, uint64
     return read_count(ctx, cnt.p);
 }
 
+// Sorted unique copy of n keys (the caller's buffer is left as it is): returns
+// the count, *out is a new buffer.  A large input whose high word splits it
+// into short runs gets its unique keys from the fused short-run pass.
+static uint64_t sort_unique_keys(Ctx *ctx, const uint64_t *keys, uint64_t n, uint64_t **out) {
+    if (n >= 2 && n < (1ull << 30)) {
+        uint64_t *a = static_cast<uint64_t *>(ctx->alloc(n * sizeof(uint64_t)));
+        uint64_t *b = static_cast<uint64_t *>(ctx->alloc(n * sizeof(uint64_t)));
+        uint32_t *v0 = nullptr, *v1 = nullptr;
+        SortUnique uq;
+        radix_sort_u64(ctx, &a, &b, &v0, &v1, n, 0, 8, keys, 0, &uq);
+        ctx->free(b);
+        if (uq.done) {
+            *out = a;
+            return uq.count;
+        }
+        const uint64_t c = unique_keys(ctx, a, n, out);
+        ctx->free(a);
+        return c;
+    }
+    uint64_t *s = sort_keys(ctx, const_cast<uint64_t *>(keys), n, false);
+    const uint64_t c = unique_keys(ctx, s, n, out);
+    if (s != keys) ctx->free(s);
+    return c;
+}
+
 // Canonical (sorted, unique) copy of the packed keys of an arity<=2 relation
 // or the relation's own buffer when it is already canonical (borrowed = true).
 struct Canon {
@@ -410,10 +435,8 @@ static void canonical_keys(Ctx *ctx, const xlog_hip_rel *r, Canon &c) {
         c.n = r->rows;
         return;
     }
-    uint64_t *s = sort_keys(ctx, r->w[0], r->rows, false);
     uint64_t *u;
-    c.n = unique_keys(ctx, s, r->rows, &u);
-    if (s != r->w[0]) ctx->free(s);
+    c.n = sort_unique_keys(ctx, r->w[0], r->rows, &u);
     c.owned = u;
     c.k = u;
 }
@@ -500,10 +523,8 @@ static xlog_hip_rel *compact_rel(Ctx *ctx, const xlog_hip_rel *in, const uint8_t
 static xlog_hip_rel *op_dedup_full(Ctx *ctx, const xlog_hip_rel *in) {
     if (in->flags & REL_CANONICAL) return rel_clone(ctx, in);
     if (in->arity <= 2) {
-        uint64_t *s = sort_keys(ctx, in->w[0], in->rows, false);
         uint64_t *u;
-        uint64_t n = unique_keys(ctx, s, in->rows, &u);
-        if (s != in->w[0]) ctx->free(s);
+        const uint64_t n = sort_unique_keys(ctx, in->w[0], in->rows, &u);
         return rel_adopt(ctx, in->arity, n, u, nullptr, REL_CANONICAL);
     }
     std::vector<int> all;
@@ -2240,10 +2261,8 @@ static DRel canon_drel(Ctx *ctx, const xlog_hip_rel *r) {
         d.owned = false;
         return d;
     }
-    uint64_t *s = sort_keys(ctx, r->w[0], r->rows, false);
     uint64_t *u;
-    d.n = unique_keys(ctx, s, r->rows, &u);
-    if (s != r->w[0]) ctx->free(s);
+    d.n = sort_unique_keys(ctx, r->w[0], r->rows, &u);
     d.k = u;
     d.owned = true;
     return d;

@@ -256,8 +256,11 @@ void rel_free(xlog_hip_rel *r);
 // word only).  On return *keys (and *vals) point at whichever of the two
 // buffers holds the result; the other is scratch.  The pass of the lowest
 // digit always runs (it is queued before the histograms are read back); every
-// higher digit that is constant over the input is skipped.  Returns the number
-// of digit passes executed.
+// higher digit that is constant over the input is skipped.  A keys-only sort
+// of the whole key over at least 2^22 keys instead waits for the histograms,
+// and when they predict that the high word leaves runs of a few keys, runs
+// the high word's passes and one sort_short_runs pass (the low word's passes
+// only if some run exceeds 256 keys).  Returns the number of passes executed.
 // With `src` (keys only) the first pass reads src and both buffers are
 // scratch, so an input that must not be modified is never copied first.
 // With known_digits (a bitmask of digits that may vary, e.g. from the value
@@ -269,9 +272,21 @@ void rel_free(xlog_hip_rel *r);
 // keys sets *d_long (device) and leaves the output incomplete; the caller then
 // sorts the input in full instead.
 void sort_short_runs(Ctx *ctx, const uint64_t *in, uint64_t n, uint64_t *out, uint64_t *d_long);
+// With `uq` (a keys-only sort of the whole key) the high-word route, when
+// taken, also deduplicates: *keys then holds the uq->count unique keys and
+// uq->done is set; otherwise *keys holds all n keys, sorted.
+struct SortUnique {
+    bool done = false;
+    uint64_t count = 0;
+};
 int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **vals, uint32_t **vals_alt,
                    uint64_t n, int digit_lo = 0, int digit_hi = 8, const uint64_t *src = nullptr,
-                   uint32_t known_digits = 0);
+                   uint32_t known_digits = 0, SortUnique *uq = nullptr);
+// sort_short_runs fused with the adjacent-compare unique: the unique keys in
+// order to `out`, their count to *d_count (device); a run longer than 256
+// keys sets *d_long and the output is then incomplete.
+void sort_short_runs_unique(Ctx *ctx, const uint64_t *in, uint64_t n, uint64_t *out, uint64_t *d_count,
+                            uint64_t *d_long);
 
 // Stream compaction family (single pass, decoupled look-back).  Each writes
 // the selected keys in input order to `out` and the count to *d_count

@@ -14,11 +14,17 @@
 //      obtained by decoupled look-back, the tile is reordered by digit in
 //      LDS and written out so that consecutive lanes write consecutive
 //      addresses of a digit run.
+//   3. For a large keys-only sort of the whole key whose high word leaves
+//      runs of a few keys (estimated from the histograms), only the high
+//      word's digits take passes; k_sort_short_runs then orders every run of
+//      equal high word by its low word in one more pass (4 + 1 passes over
+//      uniform keys instead of 8).
 // Each pass reads and writes every key exactly once (16 B per key, plus the
 // optional u32 payload).  Tiles go to the XCDs in chunks of consecutive
 // tiles, so that neighbouring tiles share an L2, and a tile only ever waits
 // for tiles of earlier-dispatched blocks.
 #include "internal.hpp"
+#include "short_runs.hpp"
 
 #include <atomic>
 
@@ -390,107 +396,18 @@ __global__ __launch_bounds__(BLOCK) void k_onesweep(
 }
 
 // Sort of short runs: keys sorted by their high word, each run of equal high
-// word sorted by the full key (its low word) in place of the low word's radix
-// passes.  A block owns the runs that start in its core of SR_CORE keys and
-// loads the core with SR_MAX keys of halo on both sides.  Every loaded key's
-// run start and end come from a block-wide max-scan of run heads and min-scan
-// of run tails; each key of an owned run then counts the run's smaller
-// keys (earlier equal keys count as smaller, so equal keys keep their order)
-// and that count is its place.  A run longer than SR_MAX keys sets *long_run
-// (its keys are then not placed and the caller sorts the whole input instead).
+// word sorted by its low word in place of the low word's radix passes (the
+// placement is short_runs_place).  The placed keys sit in LDS at their place
+// and the block's range of places (its runs are contiguous) is written out in
+// one coalesced sweep.  A run longer than SR_MAX keys sets *long_run (its keys
+// are then not placed and the caller sorts the whole input instead).
 constexpr int SR_BLOCK = 256, SR_CORE = 2048, SR_MAX = 256;
-constexpr int SR_LEN = SR_CORE + 2 * SR_MAX, SR_ITEMS = SR_LEN / SR_BLOCK;
-static_assert(SR_LEN % SR_BLOCK == 0, "short-run tile");
+using SrTile = ShortRunTile<SR_BLOCK, SR_CORE, SR_MAX>;
 __global__ __launch_bounds__(SR_BLOCK) void k_sort_short_runs(const uint64_t *__restrict__ in, uint64_t n,
                                                               uint64_t *__restrict__ out, uint64_t *long_run) {
-    __shared__ uint64_t s_k[SR_LEN];
-    __shared__ uint32_t s_lo[SR_LEN];
-    __shared__ uint32_t s_wmax[SR_BLOCK / WAVE], s_wmin[SR_BLOCK / WAVE];
-    const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
-    const uint64_t core_lo = (uint64_t)blockIdx.x * SR_CORE;
-    const uint64_t core_hi = core_lo + SR_CORE < n ? core_lo + SR_CORE : n;
-    const uint64_t lo = core_lo > (uint64_t)SR_MAX ? core_lo - SR_MAX : 0;
-    const uint64_t hi = core_hi + SR_MAX < n ? core_hi + SR_MAX : n;
-    const uint32_t len = (uint32_t)(hi - lo);
-    for (uint32_t i = tid; i < len; i += SR_BLOCK) {
-        const uint64_t k = in[lo + i];
-        s_k[i] = k;
-        s_lo[i] = (uint32_t)k;
-    }
-    __syncthreads();
-    // thread t owns SR_ITEMS consecutive keys: run start = last head at or
-    // before the key, run end = first tail at or after it, plus one
-    const uint32_t b0 = (uint32_t)tid * SR_ITEMS;
-    uint32_t hmax = 0, tmin = 0xFFFFFFFFu;
-    uint32_t st_loc[SR_ITEMS], en_loc[SR_ITEMS];
-#pragma unroll
-    for (int q = 0; q < SR_ITEMS; ++q) {
-        const uint32_t i = b0 + q;
-        const bool head = i < len && (i == 0 || (uint32_t)(s_k[i] >> 32) != (uint32_t)(s_k[i - 1] >> 32));
-        if (head) hmax = i;
-        st_loc[q] = hmax;
-    }
-#pragma unroll
-    for (int q = SR_ITEMS - 1; q >= 0; --q) {
-        const uint32_t i = b0 + q;
-        const bool tail = i < len && (i + 1 == len || (uint32_t)(s_k[i] >> 32) != (uint32_t)(s_k[i + 1] >> 32));
-        if (tail) tmin = i + 1;
-        en_loc[q] = tmin;
-    }
-    // exclusive max-scan of the threads' last heads and min-scan (from the
-    // right) of their first tails over the block
-    uint32_t incl_max = hmax, incl_min = tmin;
-#pragma unroll
-    for (int o = 1; o < WAVE; o <<= 1) {
-        const uint32_t a = __shfl_up(incl_max, o, WAVE);
-        const uint32_t c = __shfl_down(incl_min, o, WAVE);
-        if (lane >= o) incl_max = a > incl_max ? a : incl_max;
-        if (lane + o < WAVE) incl_min = c < incl_min ? c : incl_min;
-    }
-    if (lane == WAVE - 1) s_wmax[wave] = incl_max;
-    if (lane == 0) s_wmin[wave] = incl_min;
-    __syncthreads();
-    uint32_t before = __shfl_up(incl_max, 1, WAVE), after = __shfl_down(incl_min, 1, WAVE);
-    if (lane == 0) before = 0;
-    if (lane == WAVE - 1) after = 0xFFFFFFFFu;
-#pragma unroll
-    for (int w = 0; w < SR_BLOCK / WAVE; ++w) {
-        if (w < wave) before = s_wmax[w] > before ? s_wmax[w] : before;
-        if (w > wave) after = s_wmin[w] < after ? s_wmin[w] : after;
-    }
-    bool longr = false;
-#pragma unroll
-    for (int q = 0; q < SR_ITEMS; ++q) {
-        const uint32_t li = b0 + q;
-        if (li >= len || lo + li < core_lo) continue;
-        const uint32_t st = st_loc[q] > before ? st_loc[q] : before;
-        const uint32_t e = en_loc[q] < after ? en_loc[q] : after;
-        if (e - st > (uint32_t)SR_MAX) {  // a run of more than SR_MAX keys
-            longr = true;
-            continue;
-        }
-        // runs that start before the core (or may start before the loaded
-        // keys) or after it belong to other blocks
-        if (lo + st < core_lo || lo + st >= core_hi) continue;
-        if (e == len && hi < n && (uint32_t)(in[hi] >> 32) == (uint32_t)(s_k[li] >> 32)) {  // continues past the halo
-            longr = true;
-            continue;
-        }
-        // The run shares the high word, so (low word, position) orders it:
-        // one 64-bit compare per key of the run, four loads in flight.
-        const uint64_t mine = ((uint64_t)s_lo[li] << 32) | li;
-        uint32_t r = 0, j = st;
-        for (; j + 4 <= e; j += 4) {
-            uint32_t cj[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) cj[u] = s_lo[j + u];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) r += ((((uint64_t)cj[u] << 32) | (j + u)) < mine) ? 1u : 0u;
-        }
-        for (; j < e; ++j) r += ((((uint64_t)s_lo[j] << 32) | j) < mine) ? 1u : 0u;
-        out[lo + st + r] = s_k[li];
-    }
-    if (__ballot(longr) != 0 && lane == 0) *long_run = 1ull;
+    __shared__ SrTile t;
+    const uint64_t lo = short_runs_place<SR_BLOCK, SR_CORE, SR_MAX>(in, n, (uint64_t)blockIdx.x * SR_CORE, t, long_run);
+    for (uint32_t i = t.pmin + threadIdx.x; i < t.pmax; i += SR_BLOCK) out[lo + i] = ((uint64_t)t.hi[i] << 32) | t.lo[i];
 }
 
 __global__ void k_fill_u32(uint32_t *p, uint32_t v, uint64_t n) {
@@ -575,6 +492,34 @@ static bool sort_tickets() {
     return e && e[0] == '1';
 }
 
+// The high-word route of a full-key sort (keys only, at least
+// HYBRID_MIN_KEYS keys; XLOG_HIP_SORT_HYBRID=0 turns it off, read at each
+// sort): when the high word splits the keys into runs of a few keys, the
+// high word's digit passes and one short-run pass replace the low word's
+// four digit passes.
+constexpr uint64_t HYBRID_MIN_KEYS = 1ull << 22;
+static bool sort_hybrid() {
+    const char *e = getenv("XLOG_HIP_SORT_HYBRID");
+    return !(e && e[0] == '0');
+}
+// From the digit histograms: is a key expected to share its high word with
+// at most a few others?  sum_b h_d[b]^2 / n^2 is the chance that two keys
+// drawn at random agree on digit d; the product over the high word's four
+// digits, as if the digits were independent, estimates the chance that they
+// agree on the whole high word.  Inputs where the estimate is wrong (digits
+// that move together) have longer runs than predicted; a run of more than
+// 256 keys is caught by the short-run pass, and the sort then runs every
+// digit's pass.
+static bool short_high_runs(const uint32_t *h, uint64_t n) {
+    double p = 1.0;
+    for (int d = 4; d < 8; ++d) {
+        double s = 0.0;
+        for (int b = 0; b < 256; ++b) s += (double)h[d * 256 + b] * (double)h[d * 256 + b];
+        p *= s / ((double)n * (double)n);
+    }
+    return (double)(n - 1) * p <= 8.0;
+}
+
 void sort_short_runs(Ctx *ctx, const uint64_t *in, uint64_t n, uint64_t *out, uint64_t *d_long) {
     fill_u64(ctx, d_long, 0ull, 1);
     if (!n) return;
@@ -586,7 +531,8 @@ void sort_short_runs(Ctx *ctx, const uint64_t *in, uint64_t n, uint64_t *out, ui
 }
 
 int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **vals, uint32_t **vals_alt,
-                   uint64_t n, int digit_lo, int digit_hi, const uint64_t *src, uint32_t known_digits) {
+                   uint64_t n, int digit_lo, int digit_hi, const uint64_t *src, uint32_t known_digits,
+                   SortUnique *uq) {
     if (n < 2 || digit_lo >= digit_hi) {
         if (src && n) XH_CHECK_HIP(hipMemcpyAsync(*keys, src, n * 8, hipMemcpyDeviceToDevice, ctx->stream));
         return 0;
@@ -661,21 +607,50 @@ int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **va
     // The pass of the lowest digit is launched before waiting for it (a pass
     // over a constant digit is a stable copy, so it is right either way): the
     // device works on it while the host reads the histograms and queues the
-    // rest, instead of idling through the read-back.
+    // rest, instead of idling through the read-back.  A large full-key sort
+    // waits instead, since its histograms may choose the high-word route.
     uint32_t h_hist[8 * 256];
     static_assert(sizeof(h_hist) <= Ctx::HOST_STAGE_U64 * sizeof(uint64_t), "histograms exceed the staging");
     XH_CHECK_HIP(hipMemcpyAsync(ctx->host_scalars, hist, sizeof(h_hist), hipMemcpyDeviceToHost, ctx->stream));
     XH_CHECK_HIP(hipEventRecord(ctx->ev_read, ctx->stream));
+    const bool hybrid_candidate = !has_val && digit_lo == 0 && digit_hi == 8 && n >= HYBRID_MIN_KEYS && sort_hybrid();
     int first = digit_lo;
-    if (digit_hi - digit_lo >= 2) launch_pass(first++);
+    if (digit_hi - digit_lo >= 2 && !hybrid_candidate) launch_pass(first++);
     ctx->wait_event(ctx->ev_read);
     memcpy(h_hist, ctx->host_scalars, sizeof(h_hist));
-    for (int dgt = first; dgt < digit_hi; ++dgt) {
-        bool trivial = false;
+    auto trivial = [&](int dgt) {
         for (int b = 0; b < 256; ++b)
-            if (h_hist[dgt * 256 + b] == n) { trivial = true; break; }
-        if (!trivial) launch_pass(dgt);
+            if (h_hist[dgt * 256 + b] == n) return true;
+        return false;
+    };
+    if (hybrid_candidate && short_high_runs(h_hist, n)) {
+        // The high word's passes, then every run of equal high word sorted by
+        // its low word in one pass instead of the low word's four passes.
+        for (int dgt = 4; dgt < 8; ++dgt)
+            if (!trivial(dgt)) launch_pass(dgt);
+        if (passes > 0) {
+            Buf<uint64_t> flags(ctx, 2);  // unique count (with uq), long run
+            if (uq) sort_short_runs_unique(ctx, *keys, n, *keys_alt, flags.p, flags.p + 1);
+            else sort_short_runs(ctx, *keys, n, *keys_alt, flags.p + 1);
+            ctx->read_scalars(flags.p, 2);
+            if (ctx->host_scalars[1] == 0) {
+                if (uq) {
+                    uq->done = true;
+                    uq->count = ctx->host_scalars[0];
+                }
+                std::swap(*keys, *keys_alt);
+                return passes + 1;
+            }
+            // a run of more than 256 keys: *keys (the keys sorted by their
+            // high word, intact) takes every digit's pass; any order of the
+            // keys sorts to the same result
+            for (int dgt = 0; dgt < 8; ++dgt)
+                if (!trivial(dgt)) launch_pass(dgt);
+            return passes;
+        }
     }
+    for (int dgt = first; dgt < digit_hi; ++dgt)
+        if (!trivial(dgt)) launch_pass(dgt);
     if (passes == 0 && src) XH_CHECK_HIP(hipMemcpyAsync(*keys, src, n * 8, hipMemcpyDeviceToDevice, ctx->stream));
     return passes;
 }
