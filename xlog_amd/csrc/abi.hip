@@ -221,7 +221,6 @@ uint64_t join_probe_general(Ctx *ctx, const uint64_t *probe, uint64_t n, int pco
                             uint64_t **out1);
 void join_match_flags(Ctx *ctx, const uint64_t *probe, uint64_t n, int pcol, const RunIndex &ix, int want,
                       uint8_t *flags);
-void scan_u64_small(Ctx *ctx, uint64_t *a, uint64_t n, uint64_t *total);
 
 #define LAUNCH_1D(kern, n, ...)                                                                             \
     do {                                                                                                    \

@@ -480,7 +480,6 @@ constexpr uint64_t HS_APPEND_SLACK = 1ull << 21;
 // Returns the row count; out1 is set when the output arity exceeds 2.
 uint64_t nested_loop_join(Ctx *ctx, const uint64_t *l, uint64_t nl, int la, int lk, const uint64_t *r, uint64_t nr,
                           int ra, int rk, uint64_t **out0, uint64_t **out1);
-void scan_u64_small(Ctx *ctx, uint64_t *a, uint64_t n, uint64_t *total);
 
 // One factorized TC delta step over a dense domain (ids < domain): the set
 // {(x, z) : (x, y) in delta, (y, z) in edge, (x, z) not in full} as sorted

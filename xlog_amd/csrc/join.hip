@@ -236,48 +236,6 @@ __global__ __launch_bounds__(JB) void k_probe_count(ProbeArgs a, uint64_t *__res
     }
 }
 
-// single-block exclusive scan of a u64 array; total -> *total.  Each round
-// covers 1024 x 16 elements: a thread sums 16 consecutive ones, the block
-// scans the 1024 sums, and the thread writes its 16 prefixes.
-constexpr int SCAN_SEG = 16;
-__global__ __launch_bounds__(1024) void k_scan_small(uint64_t *a, uint64_t n, uint64_t *total) {
-    __shared__ uint64_t s_w[16];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    uint64_t carry = 0;
-    for (uint64_t base = 0; base < n; base += 1024 * SCAN_SEG) {
-        const uint64_t i0 = base + (uint64_t)tid * SCAN_SEG;
-        uint64_t v[SCAN_SEG], sum = 0;
-#pragma unroll
-        for (int k = 0; k < SCAN_SEG; ++k) {
-            v[k] = i0 + k < n ? a[i0 + k] : 0ull;
-            sum += v[k];
-        }
-        uint64_t x = sum;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            uint64_t t = __shfl_up(x, o, 64);
-            if (lane >= o) x += t;
-        }
-        if (lane == 63) s_w[wave] = x;
-        __syncthreads();
-        uint64_t wpre = 0, tot = 0;
-#pragma unroll
-        for (int w = 0; w < 16; ++w) {
-            if (w < wave) wpre += s_w[w];
-            tot += s_w[w];
-        }
-        uint64_t run = carry + wpre + x - sum;
-#pragma unroll
-        for (int k = 0; k < SCAN_SEG; ++k) {
-            if (i0 + k < n) a[i0 + k] = run;
-            run += v[k];
-        }
-        carry += tot;
-        __syncthreads();  // s_w is rewritten by the next round
-    }
-    if (tid == 0) *total = carry;
-}
-
 // Output spec: up to 4 selected values among v0 = probe.c0, v1 = probe.c1,
 // v2 = build key, v3 = build payload, packed per the relation layout.
 struct OutSpec {
@@ -1046,7 +1004,7 @@ uint64_t nested_loop_join(Ctx *ctx, const uint64_t *l, uint64_t nl, int la, int 
     hipLaunchKernelGGL(k_nlj, dim3(grid), dim3(NLJ_WAVES * WAVE), 0, ctx->stream, l, nl, la, lk, r, nr, ra, rk, off.p,
                        0, spec, nullptr, nullptr);
     XH_CHECK_HIP(hipGetLastError());
-    scan_u64_small(ctx, off.p, nl, off.p + nl);
+    scan_u64_inplace(ctx, off.p, nl, off.p + nl);
     ctx->read_scalars(off.p + nl, 1);
     const uint64_t total = ctx->host_scalars[0];
     if (total == 0) return 0;
@@ -1058,8 +1016,4 @@ uint64_t nested_loop_join(Ctx *ctx, const uint64_t *l, uint64_t nl, int la, int 
     return total;
 }
 
-void scan_u64_small(Ctx *ctx, uint64_t *a, uint64_t n, uint64_t *total) {
-    hipLaunchKernelGGL(k_scan_small, dim3(1), dim3(1024), 0, ctx->stream, a, n, total);
-    XH_CHECK_HIP(hipGetLastError());
-}
 }  // namespace xh

@@ -276,7 +276,7 @@ uint64_t bitmap_emit(Ctx *ctx, const uint64_t *bits, uint32_t nv, uint64_t words
     Buf<uint64_t> rc(ctx, (uint64_t)nv + 1);
     hipLaunchKernelGGL(k_row_counts, dim3(nv), dim3(TB), 0, ctx->stream, bits, words, rc.p);
     XH_CHECK_HIP(hipGetLastError());
-    scan_u64_small(ctx, rc.p, nv, rc.p + nv);
+    scan_u64_inplace(ctx, rc.p, nv, rc.p + nv);
     ctx->read_scalars(rc.p + nv, 1);
     const uint64_t total = ctx->host_scalars[0];
     if (total == 0) return 0;
