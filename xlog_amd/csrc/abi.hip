@@ -396,26 +396,35 @@ static uint64_t unique_keys(Ctx *ctx, const uint64_t *sorted, uint64_t n, uint64
 // Sorted unique copy of n keys (the caller's buffer is left as it is): returns
 // the count, *out is a new buffer.  A large input whose high word splits it
 // into short runs gets its unique keys from the fused short-run pass.
-static uint64_t sort_unique_keys(Ctx *ctx, const uint64_t *keys, uint64_t n, uint64_t **out) {
+static void sort_unique_keys_async(Ctx *ctx, const uint64_t *keys, uint64_t n, uint64_t **out, uint64_t *d_count) {
     if (n >= 2 && n < (1ull << 30)) {
         uint64_t *a = static_cast<uint64_t *>(ctx->alloc(n * sizeof(uint64_t)));
         uint64_t *b = static_cast<uint64_t *>(ctx->alloc(n * sizeof(uint64_t)));
         uint32_t *v0 = nullptr, *v1 = nullptr;
         SortUnique uq;
         radix_sort_u64(ctx, &a, &b, &v0, &v1, n, 0, 8, keys, 0, &uq);
-        ctx->free(b);
         if (uq.done) {
+            ctx->free(b);
             *out = a;
-            return uq.count;
+            fill_u64(ctx, d_count, uq.count, 1);
+            return;
         }
-        const uint64_t c = unique_keys(ctx, a, n, out);
+        select_unique(ctx, a, n, b, d_count);
         ctx->free(a);
-        return c;
+        *out = b;
+        return;
     }
     uint64_t *s = sort_keys(ctx, const_cast<uint64_t *>(keys), n, false);
-    const uint64_t c = unique_keys(ctx, s, n, out);
+    uint64_t *o = static_cast<uint64_t *>(ctx->alloc((n ? n : 1) * sizeof(uint64_t)));
+    select_unique(ctx, s, n, o, d_count);
     if (s != keys) ctx->free(s);
-    return c;
+    *out = o;
+}
+// The same with the count read back (returned).
+static uint64_t sort_unique_keys(Ctx *ctx, const uint64_t *keys, uint64_t n, uint64_t **out) {
+    Buf<uint64_t> cnt(ctx, 1);
+    sort_unique_keys_async(ctx, keys, n, out, cnt.p);
+    return read_count(ctx, cnt.p);
 }
 
 // Canonical (sorted, unique) copy of the packed keys of an arity<=2 relation
@@ -2250,7 +2259,10 @@ static bool idb_of(const std::vector<Rule> &rules, int pred) {
 }
 
 // canonical keys of an input relation for the driver
-static DRel canon_drel(Ctx *ctx, const xlog_hip_rel *r) {
+// Canonical keys of a fixpoint input; for a relation that must be sorted the
+// row count stays on the device (*d_count) and d.n is the input's row count,
+// a bound, until the caller reads it back.
+static DRel canon_drel_async(Ctx *ctx, const xlog_hip_rel *r, uint64_t *d_count) {
     DRel d;
     if (!r || r->rows == 0) return d;
     XH_REQUIRE(r->arity == 2, XLOG_HIP_TYPE_MISMATCH, "fixpoint: every predicate must have arity 2");
@@ -2261,7 +2273,8 @@ static DRel canon_drel(Ctx *ctx, const xlog_hip_rel *r) {
         return d;
     }
     uint64_t *u;
-    d.n = sort_unique_keys(ctx, r->w[0], r->rows, &u);
+    sort_unique_keys_async(ctx, r->w[0], r->rows, &u, d_count);
+    d.n = r->rows;
     d.k = u;
     d.owned = true;
     return d;
@@ -2362,17 +2375,23 @@ static void run_fixpoint_impl(Ctx *ctx, const int32_t *plan, uint32_t n_preds, c
     } canon{ctx, std::vector<DRel>(n_preds)};
     uint64_t nv = 0;  // max id + 1 (up to 2^32; 0 when every relation is empty)
     {
-        Buf<unsigned int> mx(ctx, 2);  // read back as one u64: the maximum in its low half
-        fill_u32(ctx, mx.p, 0u, 2);
+        // one read-back: [0] the largest id (in its low half; an input's ids are its canonical form's), [1 + p]
+        // the canonical row count of relation p
+        Buf<uint64_t> sc(ctx, 1 + (uint64_t)n_preds);
+        fill_u64(ctx, sc.p, 0ull, 1 + (uint64_t)n_preds);
         uint64_t any = 0;
-        for (uint32_t p = 0; p < n_preds; ++p) {
-            canon.d[p] = canon_drel(ctx, rels[p]);
-            any += canon.d[p].n;
-            MAX_LAUNCH_1D(k_max_u32_of_packed, canon.d[p].n, canon.d[p].k, canon.d[p].n, mx.p);
-        }
+        for (uint32_t p = 0; p < n_preds; ++p)
+            if (rels[p] && rels[p]->rows) {
+                any += rels[p]->rows;
+                MAX_LAUNCH_1D(k_max_u32_of_packed, rels[p]->rows, rels[p]->w[0], rels[p]->rows,
+                              reinterpret_cast<unsigned int *>(sc.p));
+            }
+        for (uint32_t p = 0; p < n_preds; ++p) canon.d[p] = canon_drel_async(ctx, rels[p], sc.p + 1 + p);
         if (any) {
-            ctx->read_scalars(mx.p, 1);
+            ctx->read_scalars(sc.p, 1 + (uint64_t)n_preds);
             nv = (uint64_t)(uint32_t)ctx->host_scalars[0] + 1;
+            for (uint32_t p = 0; p < n_preds; ++p)
+                if (canon.d[p].owned) canon.d[p].n = ctx->host_scalars[1 + p];
         }
     }
     const bool bitmap = tc && head_empty && route != XLOG_HIP_ROUTE_JOIN && route != XLOG_HIP_ROUTE_HASH &&

@@ -460,6 +460,31 @@ __global__ void k_pairs_bits_mask(const uint64_t *__restrict__ rows, uint64_t n,
     }
 }
 
+// Seed of a closure whose one exit rule copies an EDB relation E (read
+// forward) into a head that starts empty: R = D = E as whole bit rows, one
+// block per row, the row built in LDS from its CSR adjacency.  Writing every
+// row whole replaces the zero-fills of R and D, and the seed needs neither the
+// candidate matrix nor a finalize pass.
+__global__ __launch_bounds__(FTB) void k_seed_rows(uint32_t words, const uint64_t *__restrict__ row_ptr,
+                                                   const uint32_t *__restrict__ adj, uint64_t *__restrict__ R,
+                                                   uint64_t *__restrict__ D) {
+    extern __shared__ unsigned long long s_row[];  // `words` words
+    const uint32_t x = blockIdx.x;
+    for (uint32_t w = threadIdx.x; w < words; w += FTB) s_row[w] = 0ull;
+    __syncthreads();
+    const uint64_t b = row_ptr[x], e = row_ptr[x + 1];
+    for (uint64_t i = b + threadIdx.x; i < e; i += FTB) {
+        const uint32_t z = adj[i];
+        atomicOr(&s_row[z >> 6], 1ull << (z & 63));
+    }
+    __syncthreads();
+    for (uint32_t w = threadIdx.x; w < words; w += FTB) {
+        const uint64_t v = s_row[w];
+        R[(uint64_t)x * words + w] = v;
+        D[(uint64_t)x * words + w] = v;
+    }
+}
+
 // mask of the non-empty CSR rows, one mask word per thread
 __global__ void k_csr_mask(const uint64_t *__restrict__ row_ptr, uint32_t nv, uint32_t words,
                            uint64_t *__restrict__ mask) {
@@ -675,7 +700,10 @@ struct ChainRun {
 
     void fill0(Buf<uint64_t> &b, uint64_t n) { fill_u64(ctx, b.p, 0ull, n); }
 
-    void setup() {
+    // seed_rows: the seed writes R and D of the one IDB predicate whole
+    // (k_seed_rows), so they are not zero-filled; nor is the candidate matrix
+    // when every product is fused (each writes the rows it marks whole)
+    void setup(bool seed_rows = false) {
         bit.resize(n_preds);
         csr[0].resize(n_preds);
         csr[1].resize(n_preds);
@@ -698,9 +726,13 @@ struct ChainRun {
             if (!idb[p]) continue;
             idb_list.push_back((int)p);
             BitRel &b = bit[p];
-            b.R = Buf<uint64_t>(ctx, cells); fill0(b.R, cells);
-            b.D = Buf<uint64_t>(ctx, cells); fill0(b.D, cells);
-            b.C = Buf<uint64_t>(ctx, cells); fill0(b.C, cells);
+            b.R = Buf<uint64_t>(ctx, cells);
+            b.D = Buf<uint64_t>(ctx, cells);
+            b.C = Buf<uint64_t>(ctx, cells);
+            if (!seed_rows) {
+                fill0(b.R, cells);
+                fill0(b.D, cells);
+            }
             b.rmask = Buf<uint64_t>(ctx, words); fill0(b.rmask, words);
             b.dmask[0] = Buf<uint64_t>(ctx, words); fill0(b.dmask[0], words);
             b.dmask[1] = Buf<uint64_t>(ctx, words); fill0(b.dmask[1], words);
@@ -769,6 +801,8 @@ struct ChainRun {
         }
         counts = Buf<unsigned long long>(ctx, (uint64_t)CHUNK * n_preds * SPREAD);
         totals = Buf<unsigned long long>(ctx, (uint64_t)CHUNK * n_preds);
+        if (!(seed_rows && all_fused()))
+            for (int p : idb_list) fill0(bit[p].C, cells);
     }
 
     enum Use { FULL, DELTA, PREV };  // R, D, or R minus D
@@ -1055,14 +1089,54 @@ void chain_fixpoint(Ctx *ctx, const std::vector<ChainRule> &rules, uint32_t n_pr
     out_n.assign(n_preds, 0);
     const uint32_t words = (domain + 63) / 64;
     ChainRun run{ctx, rules, n_preds, domain, words, (uint64_t)domain * words, idb, keys, rows};
-    run.setup();
-    // seed: every rule once against the initial relations
+    // One IDB predicate H that starts empty and whose one exit rule (no IDB
+    // atom) is a single EDB atom E read forward (transitive closure): the seed
+    // is R = D = E, written whole by k_seed_rows with |E| known on the host.
+    int seed_h = -1, seed_e = -1, n_idb = 0, n_exit = 0;
+    for (uint32_t p = 0; p < n_preds; ++p)
+        if (idb[p]) {
+            ++n_idb;
+            seed_h = (int)p;
+        }
+    for (const ChainRule &r : rules) {
+        bool exit_rule = true;
+        for (const ChainAtom &a : r.path) exit_rule = exit_rule && !idb[a.pred];
+        if (!exit_rule) continue;
+        ++n_exit;
+        if (r.path.size() == 1 && !r.path[0].backward) seed_e = r.path[0].pred;
+    }
+    const bool seed_cand = n_idb == 1 && rows[seed_h] == 0 && n_exit == 1 && seed_e >= 0 && rows[seed_e] > 0;
+    run.setup(seed_cand);
+    // (a head read backward or as R minus D also needs its transposes and P seeded: the general seed)
+    const bool seed_rows =
+        seed_cand && !run.bit[seed_h].trans && !run.bit[seed_h].prev && !run.bit[seed_h].prev_t;
+    if (seed_cand && !seed_rows) {
+        run.fill0(run.bit[seed_h].R, run.cells);
+        run.fill0(run.bit[seed_h].D, run.cells);
+    }
     const std::vector<char> none(n_preds, 0);
     std::vector<uint64_t> sizes;
-    run.begin_iteration(none);
-    for (const ChainRule &r : rules) run.eval_chain(r, -1);
-    run.finalize_all(none);
-    run.read_counts(1, sizes);
+    if (seed_rows) {
+        BitRel &b = run.bit[seed_h];
+        const CsrRel &c = run.csr[0][seed_e];
+        XH_REQUIRE(c.built, XLOG_HIP_INVALID_ARG, "chain bitmap: the exit relation has no CSR");
+        hipLaunchKernelGGL(k_seed_rows, dim3(domain), dim3(FTB), words * sizeof(uint64_t), ctx->stream, words,
+                           c.row_ptr.p, c.adj.p, b.R.p, b.D.p);
+        XH_CHECK_HIP(hipGetLastError());
+        XH_CHECK_HIP(hipMemcpyAsync(b.rmask.p, c.mask.p, words * sizeof(uint64_t), hipMemcpyDeviceToDevice,
+                                    ctx->stream));
+        XH_CHECK_HIP(hipMemcpyAsync(b.dmask[b.dcur ^ 1].p, c.mask.p, words * sizeof(uint64_t),
+                                    hipMemcpyDeviceToDevice, ctx->stream));
+        b.dcur ^= 1;
+        sizes.assign(n_preds, 0);
+        sizes[seed_h] = rows[seed_e];
+    } else {
+        // seed: every rule once against the initial relations
+        run.begin_iteration(none);
+        for (const ChainRule &r : rules) run.eval_chain(r, -1);
+        run.finalize_all(none);
+        run.read_counts(1, sizes);
+    }
     deltas.push_back(run.take_counts(sizes, 0));
     // When every head takes one fused variant per iteration (transitive
     // closure), CHUNK iterations are queued per read-back: an iteration after
