@@ -1204,7 +1204,9 @@ void chain_fixpoint(Ctx *ctx, const std::vector<ChainRule> &rules, uint32_t n_pr
     run.T[0] = Buf<uint64_t>();
     run.T[1] = Buf<uint64_t>();
     for (int p : run.idb_list)
-        out_n[p] = bitmap_emit(ctx, run.bit[p].R.p, domain, words, &out[p], XLOG_HIP_KERNEL_CHAIN_EMIT);
+        // R's bits are its initial rows plus every delta: rcount, with no read-back
+        out_n[p] = bitmap_emit(ctx, run.bit[p].R.p, domain, words, &out[p], XLOG_HIP_KERNEL_CHAIN_EMIT,
+                               run.bit[p].rcount);
 }
 
 }  // namespace xh

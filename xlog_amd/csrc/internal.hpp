@@ -495,7 +495,9 @@ uint64_t fj_delta_step(Ctx *ctx, const uint64_t *delta, uint64_t nd, int delta_x
 void pairs_csr(Ctx *ctx, const uint64_t *pairs, uint64_t m, uint32_t nv, uint64_t *row_ptr, uint32_t *adj);
 // Set bits of an nv x words bitmap as sorted packed (x << 32) | z rows in a
 // new pool buffer *out; returns the row count.
-uint64_t bitmap_emit(Ctx *ctx, const uint64_t *bits, uint32_t nv, uint64_t words, uint64_t **out, int prof_kind);
+// known_total: the number of set bits when the caller knows it (no read-back), else UINT64_MAX
+uint64_t bitmap_emit(Ctx *ctx, const uint64_t *bits, uint32_t nv, uint64_t words, uint64_t **out, int prof_kind,
+                     uint64_t known_total = UINT64_MAX);
 
 // Dense-domain fixpoint of a program whose rules are chains of binary
 // relations: rule r derives head(v0, vk) from path[0](v0, v1), ...,

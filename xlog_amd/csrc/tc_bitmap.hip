@@ -270,15 +270,19 @@ void pairs_csr(Ctx *ctx, const uint64_t *pairs, uint64_t m, uint32_t nv, uint64_
 
 // The set bits of an nv x words bitmap as sorted packed (x << 32) | z rows
 // (row counts, a scan, then one block per row writing at its offset).
-uint64_t bitmap_emit(Ctx *ctx, const uint64_t *bits, uint32_t nv, uint64_t words, uint64_t **out, int prof_kind) {
+uint64_t bitmap_emit(Ctx *ctx, const uint64_t *bits, uint32_t nv, uint64_t words, uint64_t **out, int prof_kind,
+                     uint64_t known_total) {
     *out = nullptr;
-    if (nv == 0) return 0;
+    if (nv == 0 || known_total == 0) return 0;
     Buf<uint64_t> rc(ctx, (uint64_t)nv + 1);
     hipLaunchKernelGGL(k_row_counts, dim3(nv), dim3(TB), 0, ctx->stream, bits, words, rc.p);
     XH_CHECK_HIP(hipGetLastError());
     scan_u64_inplace(ctx, rc.p, nv, rc.p + nv);
-    ctx->read_scalars(rc.p + nv, 1);
-    const uint64_t total = ctx->host_scalars[0];
+    uint64_t total = known_total;
+    if (total == UINT64_MAX) {
+        ctx->read_scalars(rc.p + nv, 1);
+        total = ctx->host_scalars[0];
+    }
     if (total == 0) return 0;
     *out = static_cast<uint64_t *>(ctx->alloc(total * sizeof(uint64_t)));
     Prof prof(ctx, prof_kind, 8.0 * (double)total + 8.0 * (double)nv * (double)words);
