@@ -581,7 +581,15 @@ __global__ __launch_bounds__(MRG_BLOCK) void k_merge(const uint64_t *__restrict_
     const uint64_t d1 = (d0 + MRG_TILE < total) ? d0 + MRG_TILE : total;
     if (tid < 2) s_split[tid] = merge_path(a, na, b, nb, tid == 0 ? d0 : d1);
     __syncthreads();
-    const uint64_t a0 = s_split[0], a1 = s_split[1];
+    // For sorted inputs the splits are monotone and the clamp changes nothing; for inputs that are not
+    // sorted it keeps the tile's ranges inside a and b (and LDS) instead of inverting them.
+    const uint64_t a0 = s_split[0];
+    uint64_t a1 = s_split[1];
+    {
+        const uint64_t lo1 = d1 > nb && d1 - nb > a0 ? d1 - nb : a0;
+        const uint64_t hi1 = a0 + (d1 - d0) < na ? a0 + (d1 - d0) : na;
+        a1 = a1 < lo1 ? lo1 : (a1 > hi1 ? hi1 : a1);
+    }
     const uint32_t la = (uint32_t)(a1 - a0), len = (uint32_t)(d1 - d0), lb = len - la;
     const uint64_t b0 = d0 - a0;
     for (uint32_t i = tid; i < la; i += MRG_BLOCK) s[i] = a[a0 + i];

@@ -4,7 +4,9 @@
 // (crates/xlog-cuda/src/provider/relational.rs:1881-2357, kernels/sort.cu:28-264)
 // with a onesweep design:
 //   1. k_hist8: one read of the keys builds the 256-bin histograms of the
-//      digits the sort uses (all eight for a full-key sort); a digit above
+//      digits the sort uses (all eight for a full-key sort; a large full-key
+//      sort counts the high word's four first and the low word's with a second
+//      read only when it takes a pass over a low digit); a digit above
 //      the lowest whose histogram has a single non-empty bin is constant over
 //      the input and its pass is skipped (the lowest digit's pass is queued
 //      before the histograms reach the host, so it always runs).
@@ -555,19 +557,25 @@ int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **va
     const uint64_t nchunks = (tiles + chunk - 1) / chunk;
     const unsigned grid = (unsigned)(8 * ((nchunks + 7) / 8) * chunk);  // blocks past the last tile exit
 
-    fill_u32(ctx, hist, 0u, 8 * 256);
-    {
+    // A large full-key sort may take the high-word route, whose decision and
+    // passes need only the high word's histograms: they are counted first, and
+    // the low word's only when a pass over a low digit is needed.
+    // (a sort given known_digits takes exactly those passes, so it needs every digit's histogram)
+    const bool hybrid_candidate =
+        !has_val && !known_digits && digit_lo == 0 && digit_hi == 8 && n >= HYBRID_MIN_KEYS && sort_hybrid();
+    auto histograms = [&](const uint64_t *from, int dlo, int dhi) {
         Prof prof(ctx, XLOG_HIP_KERNEL_SORT_HIST, 8.0 * (double)n);  // reads every key once
         // at least 4 rounds per block: every block ends with up to 2048 device-scope atomics, which cost more
         // than the counting when blocks have little to count (2^24 keys: 62 us with one round per block, 47 us
         // with 4, 60 us with 16)
         const unsigned hg = grid_for(n, (unsigned)(HIST_BLOCK * HIST_ITEMS) * 4, (unsigned)ctx->num_cus * 8);
-        hipLaunchKernelGGL(k_hist8, dim3(hg), dim3(HIST_BLOCK), 0, ctx->stream, src ? src : *keys, n, hist, digit_lo,
-                           digit_hi);
-    }
-    XH_CHECK_HIP(hipGetLastError());
-    hipLaunchKernelGGL(k_digit_offsets, dim3(1), dim3(64), 0, ctx->stream, hist, off);
-    XH_CHECK_HIP(hipGetLastError());
+        hipLaunchKernelGGL(k_hist8, dim3(hg), dim3(HIST_BLOCK), 0, ctx->stream, from, n, hist, dlo, dhi);
+        XH_CHECK_HIP(hipGetLastError());
+        hipLaunchKernelGGL(k_digit_offsets, dim3(1), dim3(64), 0, ctx->stream, hist, off);
+        XH_CHECK_HIP(hipGetLastError());
+    };
+    fill_u32(ctx, hist, 0u, 8 * 256);
+    histograms(src ? src : *keys, hybrid_candidate ? 4 : digit_lo, digit_hi);
     int passes = 0;
     int cur = 0;  // status buffer for the next pass
     if (st.dirty[0] == 0) cur = 0; else if (st.dirty[1] == 0) cur = 1; else cur = 0;
@@ -613,7 +621,6 @@ int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **va
     static_assert(sizeof(h_hist) <= Ctx::HOST_STAGE_U64 * sizeof(uint64_t), "histograms exceed the staging");
     XH_CHECK_HIP(hipMemcpyAsync(ctx->host_scalars, hist, sizeof(h_hist), hipMemcpyDeviceToHost, ctx->stream));
     XH_CHECK_HIP(hipEventRecord(ctx->ev_read, ctx->stream));
-    const bool hybrid_candidate = !has_val && digit_lo == 0 && digit_hi == 8 && n >= HYBRID_MIN_KEYS && sort_hybrid();
     int first = digit_lo;
     if (digit_hi - digit_lo >= 2 && !hybrid_candidate) launch_pass(first++);
     ctx->wait_event(ctx->ev_read);
@@ -622,6 +629,14 @@ int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **va
         for (int b = 0; b < 256; ++b)
             if (h_hist[dgt * 256 + b] == n) return true;
         return false;
+    };
+    // the low word's histograms (their counters are still zero) from the same multiset of keys, and back
+    auto low_word_histograms = [&](const uint64_t *from) {
+        histograms(from, 0, 4);
+        XH_CHECK_HIP(hipMemcpyAsync(ctx->host_scalars, hist, sizeof(h_hist), hipMemcpyDeviceToHost, ctx->stream));
+        XH_CHECK_HIP(hipEventRecord(ctx->ev_read, ctx->stream));
+        ctx->wait_event(ctx->ev_read);
+        memcpy(h_hist, ctx->host_scalars, sizeof(h_hist));
     };
     if (hybrid_candidate && short_high_runs(h_hist, n)) {
         // The high word's passes, then every run of equal high word sorted by
@@ -644,11 +659,13 @@ int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **va
             // a run of more than 256 keys: *keys (the keys sorted by their
             // high word, intact) takes every digit's pass; any order of the
             // keys sorts to the same result
+            low_word_histograms(*keys);
             for (int dgt = 0; dgt < 8; ++dgt)
                 if (!trivial(dgt)) launch_pass(dgt);
             return passes;
         }
     }
+    if (hybrid_candidate) low_word_histograms(src ? src : *keys);
     for (int dgt = first; dgt < digit_hi; ++dgt)
         if (!trivial(dgt)) launch_pass(dgt);
     if (passes == 0 && src) XH_CHECK_HIP(hipMemcpyAsync(*keys, src, n * 8, hipMemcpyDeviceToDevice, ctx->stream));
