@@ -396,13 +396,15 @@ static uint64_t unique_keys(Ctx *ctx, const uint64_t *sorted, uint64_t n, uint64
 // Sorted unique copy of n keys (the caller's buffer is left as it is): returns
 // the count, *out is a new buffer.  A large input whose high word splits it
 // into short runs gets its unique keys from the fused short-run pass.
-static void sort_unique_keys_async(Ctx *ctx, const uint64_t *keys, uint64_t n, uint64_t **out, uint64_t *d_count) {
+// known_digits: the digits the keys may vary in (0: unknown, the histograms decide)
+static void sort_unique_keys_async(Ctx *ctx, const uint64_t *keys, uint64_t n, uint64_t **out, uint64_t *d_count,
+                                   uint32_t known_digits = 0) {
     if (n >= 2 && n < (1ull << 30)) {
         uint64_t *a = static_cast<uint64_t *>(ctx->alloc(n * sizeof(uint64_t)));
         uint64_t *b = static_cast<uint64_t *>(ctx->alloc(n * sizeof(uint64_t)));
         uint32_t *v0 = nullptr, *v1 = nullptr;
         SortUnique uq;
-        radix_sort_u64(ctx, &a, &b, &v0, &v1, n, 0, 8, keys, 0, &uq);
+        radix_sort_u64(ctx, &a, &b, &v0, &v1, n, 0, 8, keys, known_digits, &uq);
         if (uq.done) {
             ctx->free(b);
             *out = a;
@@ -414,7 +416,7 @@ static void sort_unique_keys_async(Ctx *ctx, const uint64_t *keys, uint64_t n, u
         *out = b;
         return;
     }
-    uint64_t *s = sort_keys(ctx, const_cast<uint64_t *>(keys), n, false);
+    uint64_t *s = sort_keys(ctx, const_cast<uint64_t *>(keys), n, false, 0, 8, known_digits);
     uint64_t *o = static_cast<uint64_t *>(ctx->alloc((n ? n : 1) * sizeof(uint64_t)));
     select_unique(ctx, s, n, o, d_count);
     if (s != keys) ctx->free(s);
@@ -2262,7 +2264,7 @@ static bool idb_of(const std::vector<Rule> &rules, int pred) {
 // Canonical keys of a fixpoint input; for a relation that must be sorted the
 // row count stays on the device (*d_count) and d.n is the input's row count,
 // a bound, until the caller reads it back.
-static DRel canon_drel_async(Ctx *ctx, const xlog_hip_rel *r, uint64_t *d_count) {
+static DRel canon_drel_async(Ctx *ctx, const xlog_hip_rel *r, uint64_t *d_count, uint32_t known_digits) {
     DRel d;
     if (!r || r->rows == 0) return d;
     XH_REQUIRE(r->arity == 2, XLOG_HIP_TYPE_MISMATCH, "fixpoint: every predicate must have arity 2");
@@ -2273,7 +2275,7 @@ static DRel canon_drel_async(Ctx *ctx, const xlog_hip_rel *r, uint64_t *d_count)
         return d;
     }
     uint64_t *u;
-    sort_unique_keys_async(ctx, r->w[0], r->rows, &u, d_count);
+    sort_unique_keys_async(ctx, r->w[0], r->rows, &u, d_count, known_digits);
     d.n = r->rows;
     d.k = u;
     d.owned = true;
@@ -2363,8 +2365,8 @@ static void run_fixpoint_impl(Ctx *ctx, const int32_t *plan, uint32_t n_preds, c
     for (const ChainRule &c : paths) short_paths = short_paths && c.path.size() <= 3;
     XH_REQUIRE(route != XLOG_HIP_ROUTE_HASH || short_paths, XLOG_HIP_UNSUPPORTED,
                "hash route needs rule bodies of 1 to 3 atoms forming a path between the head variables");
-    // every relation sorted and unique once, and the largest id (one read-back) for every route: the bitmap
-    // routes' domain, and the digits the sorts inside the join and hash routes' loops can vary in
+    // every relation sorted and unique once, and the largest id (read back first) for every route: the bitmap
+    // routes' domain, and the digits the sorts (these and those inside the join and hash routes' loops) vary in
     struct Canon {
         Ctx *ctx;
         std::vector<DRel> d;
@@ -2375,9 +2377,10 @@ static void run_fixpoint_impl(Ctx *ctx, const int32_t *plan, uint32_t n_preds, c
     } canon{ctx, std::vector<DRel>(n_preds)};
     uint64_t nv = 0;  // max id + 1 (up to 2^32; 0 when every relation is empty)
     {
-        // one read-back: [0] the largest id (in its low half; an input's ids are its canonical form's), [1 + p]
-        // the canonical row count of relation p
-        Buf<uint64_t> sc(ctx, 1 + (uint64_t)n_preds);
+        // Two read-backs: the largest id of the raw inputs (an input's ids are its canonical form's), which
+        // gives the digits the sorts can vary in, so that every relation sorts without reading its histograms
+        // back; then the canonical row counts, together.
+        Buf<uint64_t> sc(ctx, 1 + (uint64_t)n_preds);  // [0]: the largest id (low half), [1 + p]: row counts
         fill_u64(ctx, sc.p, 0ull, 1 + (uint64_t)n_preds);
         uint64_t any = 0;
         for (uint32_t p = 0; p < n_preds; ++p)
@@ -2386,12 +2389,20 @@ static void run_fixpoint_impl(Ctx *ctx, const int32_t *plan, uint32_t n_preds, c
                 MAX_LAUNCH_1D(k_max_u32_of_packed, rels[p]->rows, rels[p]->w[0], rels[p]->rows,
                               reinterpret_cast<unsigned int *>(sc.p));
             }
-        for (uint32_t p = 0; p < n_preds; ++p) canon.d[p] = canon_drel_async(ctx, rels[p], sc.p + 1 + p);
         if (any) {
-            ctx->read_scalars(sc.p, 1 + (uint64_t)n_preds);
+            ctx->read_scalars(sc.p, 1);
             nv = (uint64_t)(uint32_t)ctx->host_scalars[0] + 1;
+            // (sorts large enough for the high-word route keep reading their histograms)
+            const uint32_t maxid = (uint32_t)(nv - 1);
+            const int bits = maxid ? 32 - __builtin_clz(maxid) : 0;
+            const uint32_t nd = (uint32_t)(bits + 7) / 8;  // bytes per column
+            const uint32_t digits = nd ? (((1u << nd) - 1u) | (((1u << nd) - 1u) << 4)) : 1u;
             for (uint32_t p = 0; p < n_preds; ++p)
-                if (canon.d[p].owned) canon.d[p].n = ctx->host_scalars[1 + p];
+                canon.d[p] = canon_drel_async(ctx, rels[p], sc.p + 1 + p,
+                                              rels[p] && rels[p]->rows >= (1ull << 22) ? 0u : digits);
+            ctx->read_scalars(sc.p + 1, (uint64_t)n_preds);
+            for (uint32_t p = 0; p < n_preds; ++p)
+                if (canon.d[p].owned) canon.d[p].n = ctx->host_scalars[p];
         }
     }
     const bool bitmap = tc && head_empty && route != XLOG_HIP_ROUTE_JOIN && route != XLOG_HIP_ROUTE_HASH &&
