@@ -699,6 +699,8 @@ struct ChainRun {
     std::vector<int> idb_list;
 
     void fill0(Buf<uint64_t> &b, uint64_t n) { fill_u64(ctx, b.p, 0ull, n); }
+    FillBatch zero{ctx};  // zero-fills gathered into one launch (flushed by setup and begin_iteration)
+    void zero0(Buf<uint64_t> &b, uint64_t n) { zero.add(b.p, n); }
 
     // seed_rows: the seed writes R and D of the one IDB predicate whole
     // (k_seed_rows), so they are not zero-filled; nor is the candidate matrix
@@ -730,28 +732,29 @@ struct ChainRun {
             b.D = Buf<uint64_t>(ctx, cells);
             b.C = Buf<uint64_t>(ctx, cells);
             if (!seed_rows) {
-                fill0(b.R, cells);
-                fill0(b.D, cells);
+                zero0(b.R, cells);
+                zero0(b.D, cells);
             }
-            b.rmask = Buf<uint64_t>(ctx, words); fill0(b.rmask, words);
-            b.dmask[0] = Buf<uint64_t>(ctx, words); fill0(b.dmask[0], words);
-            b.dmask[1] = Buf<uint64_t>(ctx, words); fill0(b.dmask[1], words);
-            b.cmask = Buf<uint64_t>(ctx, words); fill0(b.cmask, words);
+            b.rmask = Buf<uint64_t>(ctx, words); zero0(b.rmask, words);
+            b.dmask[0] = Buf<uint64_t>(ctx, words); zero0(b.dmask[0], words);
+            b.dmask[1] = Buf<uint64_t>(ctx, words); zero0(b.dmask[1], words);
+            b.cmask = Buf<uint64_t>(ctx, words); zero0(b.cmask, words);
             if (b.trans) {
-                b.RT = Buf<uint64_t>(ctx, cells); fill0(b.RT, cells);
-                b.DT = Buf<uint64_t>(ctx, cells); fill0(b.DT, cells);
-                b.rtmask = Buf<uint64_t>(ctx, words); fill0(b.rtmask, words);
-                b.dtmask = Buf<uint64_t>(ctx, words); fill0(b.dtmask, words);
+                b.RT = Buf<uint64_t>(ctx, cells); zero0(b.RT, cells);
+                b.DT = Buf<uint64_t>(ctx, cells); zero0(b.DT, cells);
+                b.rtmask = Buf<uint64_t>(ctx, words); zero0(b.rtmask, words);
+                b.dtmask = Buf<uint64_t>(ctx, words); zero0(b.dtmask, words);
             }
             if (b.prev) {
-                b.P = Buf<uint64_t>(ctx, cells); fill0(b.P, cells);
-                b.pmask = Buf<uint64_t>(ctx, words); fill0(b.pmask, words);
+                b.P = Buf<uint64_t>(ctx, cells); zero0(b.P, cells);
+                b.pmask = Buf<uint64_t>(ctx, words); zero0(b.pmask, words);
             }
             if (b.prev_t) {
-                b.PT = Buf<uint64_t>(ctx, cells); fill0(b.PT, cells);
-                b.ptmask = Buf<uint64_t>(ctx, words); fill0(b.ptmask, words);
+                b.PT = Buf<uint64_t>(ctx, cells); zero0(b.PT, cells);
+                b.ptmask = Buf<uint64_t>(ctx, words); zero0(b.ptmask, words);
             }
             if (rows[p]) {  // initial contents of the head relation (also R minus D: D starts empty)
+                zero.flush();  // the matrices are zero before the rows are OR-ed in
                 const unsigned g = grid_for(rows[p], 256, 4096);
                 hipLaunchKernelGGL(k_pairs_bits_mask, dim3(g), dim3(256), 0, ctx->stream, keys[p], rows[p], 1, words,
                                    b.R.p, b.rmask.p);
@@ -802,7 +805,8 @@ struct ChainRun {
         counts = Buf<unsigned long long>(ctx, (uint64_t)CHUNK * n_preds * SPREAD);
         totals = Buf<unsigned long long>(ctx, (uint64_t)CHUNK * n_preds);
         if (!(seed_rows && all_fused()))
-            for (int p : idb_list) fill0(bit[p].C, cells);
+            for (int p : idb_list) zero0(bit[p].C, cells);
+        zero.flush();
     }
 
     enum Use { FULL, DELTA, PREV };  // R, D, or R minus D
@@ -967,12 +971,19 @@ struct ChainRun {
     // iteration, at the first) and, for every head whose delta a fused product
     // writes, the new delta's row mask (already clear when every iteration is
     // fused: the previous product cleared it).
+    // The new delta's and the candidates' row masks of a non-fused head are
+    // cleared here too (nothing reads them before its finalize), all in one launch.
     void begin_iteration(const std::vector<char> &fused) {
-        if (slot == 0) fill_u64(ctx, reinterpret_cast<uint64_t *>(counts.p), 0ull, (uint64_t)CHUNK * n_preds * SPREAD);
+        if (slot == 0) zero.add(reinterpret_cast<uint64_t *>(counts.p), (uint64_t)CHUNK * n_preds * SPREAD);
         for (int p : idb_list) {
             bit[p].spare_zeroed = false;
-            if (fused[p] && !no_clear) fill_u64(ctx, bit[p].dmask[bit[p].dcur ^ 1].p, 0ull, words);
+            if (fused[p] && !no_clear) zero.add(bit[p].dmask[bit[p].dcur ^ 1].p, words);
+            if (!fused[p]) {
+                zero.add(bit[p].dmask[bit[p].dcur ^ 1].p, words);
+                zero.add(bit[p].cmask.p, words);
+            }
         }
+        zero.flush();
     }
 
     // New deltas of every IDB predicate from its candidates (or, for fused
@@ -996,7 +1007,6 @@ struct ChainRun {
                 }
                 continue;
             }
-            fill_u64(ctx, dnew, 0ull, words);
             const FinalizeArgs fa{b.C.p, b.cmask.p, b.R.p, b.rmask.p, b.D.p, b.dmask[b.dcur].p, dnew, b.P.p,
                                   b.pmask.p, cnt_of(p)};
             {
@@ -1019,7 +1029,6 @@ struct ChainRun {
                                    b.ptmask.p);
                 XH_CHECK_HIP(hipGetLastError());
             }
-            fill_u64(ctx, b.cmask.p, 0ull, words);
             b.dcur ^= 1;
         }
     }

@@ -554,6 +554,18 @@ void select_state_release(Ctx *ctx);
 // SCAN64_EXACT; a caller checks the total before using them.
 constexpr uint64_t SCAN64_EXACT = 1ull << 39;
 void scan_u64_inplace(Ctx *ctx, uint64_t *a, uint64_t n, uint64_t *d_total);
+// Zero-fills gathered into one launch (up to FILL_MAX_RANGES ranges each):
+// add() records a range, flush() launches them in stream order.
+constexpr int FILL_MAX_RANGES = 16;
+struct FillBatch {
+    Ctx *ctx;
+    std::vector<std::pair<uint64_t *, uint64_t>> r;
+    explicit FillBatch(Ctx *c) : ctx(c) {}
+    void add(uint64_t *p, uint64_t n) {
+        if (p && n) r.push_back({p, n});
+    }
+    void flush();
+};
 void fill_u64(Ctx *ctx, uint64_t *p, uint64_t v, uint64_t n);
 void pack_columns(Ctx *ctx, const uint32_t *c0, const uint32_t *c1, uint64_t n, uint64_t *out);
 void unpack_column(Ctx *ctx, const uint64_t *w, int hi, uint64_t n, uint32_t *out);

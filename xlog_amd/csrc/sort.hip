@@ -421,7 +421,35 @@ __global__ void k_fill_u64(uint64_t *p, uint64_t v, uint64_t n) {
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = v;
 }
 
+// Zero-fill of several u64 ranges in one launch: range blockIdx.y, grid-stride
+// over its words (blocks past a short range's end exit at once).
+struct FillRangesArgs {
+    uint64_t *p[FILL_MAX_RANGES];
+    uint64_t n[FILL_MAX_RANGES];
+};
+__global__ void k_fill_ranges(FillRangesArgs a) {
+    uint64_t *p = a.p[blockIdx.y];
+    const uint64_t n = a.n[blockIdx.y], stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = 0ull;
+}
+
 }  // namespace
+
+void FillBatch::flush() {
+    for (size_t b = 0; b < r.size(); b += FILL_MAX_RANGES) {
+        FillRangesArgs a{};
+        const size_t k = std::min<size_t>(FILL_MAX_RANGES, r.size() - b);
+        uint64_t most = 0;
+        for (size_t j = 0; j < k; ++j) {
+            a.p[j] = r[b + j].first;
+            a.n[j] = r[b + j].second;
+            most = std::max(most, a.n[j]);
+        }
+        hipLaunchKernelGGL(k_fill_ranges, dim3(grid_for(most, 256, 4096), (unsigned)k), dim3(256), 0, ctx->stream, a);
+        XH_CHECK_HIP(hipGetLastError());
+    }
+    r.clear();
+}
 
 void fill_u64(Ctx *ctx, uint64_t *p, uint64_t v, uint64_t n) {
     if (!n) return;
