@@ -166,9 +166,12 @@ __global__ __launch_bounds__(TB) void k_row_counts(const uint64_t *__restrict__ 
     if (threadIdx.x == 0) cnt[x] = s;
 }
 
-// emit row x's set bits as (x << 32 | z) starting at off[x]
+// emit row x's set bits as (x << 32 | z) starting at off[x]; positions at or
+// past cap (the allocation: the caller may size it from its own count) are
+// not written
 __global__ __launch_bounds__(TB) void k_emit_rows(const uint64_t *__restrict__ R, uint64_t words,
-                                                  const uint64_t *__restrict__ off, uint64_t *__restrict__ out) {
+                                                  const uint64_t *__restrict__ off, uint64_t *__restrict__ out,
+                                                  uint64_t cap) {
     __shared__ uint64_t s_part[TB / WAVE];
     __shared__ uint64_t s_base;
     __shared__ uint64_t s_word[TB];
@@ -206,8 +209,8 @@ __global__ __launch_bounds__(TB) void k_emit_rows(const uint64_t *__restrict__ R
             const int t = wave * WAVE + j;
             const uint64_t wb = s_word[t];
             if (wb == 0ull) continue;
-            if ((wb >> lane) & 1ull)
-                out[s_woff[t] + (uint64_t)__popcll(wb & lt_mask)] = hi | (uint64_t)((c0 + t) * 64 + lane);
+            const uint64_t pos = s_woff[t] + (uint64_t)__popcll(wb & lt_mask);
+            if (((wb >> lane) & 1ull) && pos < cap) out[pos] = hi | (uint64_t)((c0 + t) * 64 + lane);
         }
         __syncthreads();
         if (tid == 0) s_base += tot;
@@ -286,7 +289,7 @@ uint64_t bitmap_emit(Ctx *ctx, const uint64_t *bits, uint32_t nv, uint64_t words
     if (total == 0) return 0;
     *out = static_cast<uint64_t *>(ctx->alloc(total * sizeof(uint64_t)));
     Prof prof(ctx, prof_kind, 8.0 * (double)total + 8.0 * (double)nv * (double)words);
-    hipLaunchKernelGGL(k_emit_rows, dim3(nv), dim3(TB), 0, ctx->stream, bits, words, rc.p, *out);
+    hipLaunchKernelGGL(k_emit_rows, dim3(nv), dim3(TB), 0, ctx->stream, bits, words, rc.p, *out, total);
     XH_CHECK_HIP(hipGetLastError());
     return total;
 }
