@@ -570,16 +570,27 @@ __device__ __forceinline__ uint64_t merge_path(const uint64_t *a, uint64_t na, c
     return lo;
 }
 
+// split[t] = merge_path at diagonal min(t * MRG_TILE, na + nb), one thread per
+// tile boundary: the binary searches of all tiles run side by side instead of
+// two dependent ~log2(n)-load chains at the start of every merge block
+__global__ void k_merge_partition(const uint64_t *__restrict__ a, uint64_t na, const uint64_t *__restrict__ b,
+                                  uint64_t nb, uint64_t tiles, uint64_t *__restrict__ split) {
+    const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t > tiles) return;
+    const uint64_t total = na + nb, d = t * MRG_TILE < total ? t * MRG_TILE : total;
+    split[t] = merge_path(a, na, b, nb, d);
+}
+
 __global__ __launch_bounds__(MRG_BLOCK) void k_merge(const uint64_t *__restrict__ a, uint64_t na,
                                                      const uint64_t *__restrict__ b, uint64_t nb,
-                                                     uint64_t *__restrict__ out) {
+                                                     const uint64_t *__restrict__ split, uint64_t *__restrict__ out) {
     __shared__ uint64_t s[MRG_TILE];
     __shared__ uint64_t s_split[2];
     const int tid = threadIdx.x;
     const uint64_t total = na + nb;
     const uint64_t d0 = (uint64_t)blockIdx.x * MRG_TILE;
     const uint64_t d1 = (d0 + MRG_TILE < total) ? d0 + MRG_TILE : total;
-    if (tid < 2) s_split[tid] = merge_path(a, na, b, nb, tid == 0 ? d0 : d1);
+    if (tid < 2) s_split[tid] = split[blockIdx.x + tid];
     __syncthreads();
     // For sorted inputs the splits are monotone and the clamp changes nothing; for inputs that are not
     // sorted it keeps the tile's ranges inside a and b (and LDS) instead of inverting them.
@@ -922,8 +933,11 @@ void merge_sorted(Ctx *ctx, const uint64_t *a, uint64_t na, const uint64_t *b, u
     if (!total) return;
     uint64_t tiles = (total + MRG_TILE - 1) / MRG_TILE;
     XH_REQUIRE(tiles < (1ull << 31), XLOG_HIP_CAPACITY_OVERFLOW, "merge: input too large");
+    Buf<uint64_t> split(ctx, tiles + 1);
+    hipLaunchKernelGGL(k_merge_partition, dim3((unsigned)((tiles + 1 + 255) / 256)), dim3(256), 0, ctx->stream, a, na,
+                       b, nb, tiles, split.p);
     Prof prof(ctx, XLOG_HIP_KERNEL_MERGE, 16.0 * (double)total);
-    hipLaunchKernelGGL(k_merge, dim3((unsigned)tiles), dim3(MRG_BLOCK), 0, ctx->stream, a, na, b, nb, out);
+    hipLaunchKernelGGL(k_merge, dim3((unsigned)tiles), dim3(MRG_BLOCK), 0, ctx->stream, a, na, b, nb, split.p, out);
     XH_CHECK_HIP(hipGetLastError());
 }
 
