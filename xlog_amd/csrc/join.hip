@@ -386,21 +386,42 @@ __device__ __forceinline__ uint64_t smj_path(RK rkey, uint64_t nr, LK lkey, uint
     return lo;
 }
 
+// split[t] = smj_path at diagonal min(t * SMJ_TILE, nl + nr), one thread per
+// tile boundary (all tiles' binary searches side by side, not two dependent
+// chains at the start of every lookup block)
+__global__ void k_smj_partition(const uint64_t *__restrict__ l, uint64_t nl, int pcol,
+                                const uint32_t *__restrict__ run_key, uint64_t nr, uint64_t tiles,
+                                uint64_t *__restrict__ split) {
+    const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t > tiles) return;
+    auto lkey_g = [&](uint64_t i) { const uint64_t r = l[i]; return pcol ? (uint32_t)r : (uint32_t)(r >> 32); };
+    auto rkey_g = [&](uint64_t i) { return run_key[i]; };
+    const uint64_t total = nl + nr, d = t * SMJ_TILE < total ? t * SMJ_TILE : total;
+    split[t] = smj_path(rkey_g, nr, lkey_g, nl, d);
+}
+
 __global__ __launch_bounds__(SMJ_BLOCK) void k_smj_lookup(const uint64_t *__restrict__ l, uint64_t nl, int pcol,
                                                           const uint32_t *__restrict__ run_key,
                                                           const uint64_t *__restrict__ run_start, uint64_t nr,
+                                                          const uint64_t *__restrict__ split,
                                                           uint64_t *__restrict__ start, uint32_t *__restrict__ cnt) {
     __shared__ uint32_t s_key[SMJ_TILE];  // the tile's runs, then its left rows
     __shared__ uint64_t s_split[2];
     const int tid = threadIdx.x;
     auto lkey_g = [&](uint64_t i) { const uint64_t r = l[i]; return pcol ? (uint32_t)r : (uint32_t)(r >> 32); };
-    auto rkey_g = [&](uint64_t i) { return run_key[i]; };
     const uint64_t total = nl + nr;
     const uint64_t d0 = (uint64_t)blockIdx.x * SMJ_TILE;
     const uint64_t d1 = d0 + SMJ_TILE < total ? d0 + SMJ_TILE : total;
-    if (tid < 2) s_split[tid] = smj_path(rkey_g, nr, lkey_g, nl, tid == 0 ? d0 : d1);
+    if (tid < 2) s_split[tid] = split[blockIdx.x + tid];
     __syncthreads();
-    const uint64_t r0 = s_split[0], r1 = s_split[1];
+    // (sorted inputs give monotone splits; the clamp keeps a tile's ranges inside both inputs and LDS otherwise)
+    const uint64_t r0 = s_split[0];
+    uint64_t r1 = s_split[1];
+    {
+        const uint64_t lo1 = d1 > nl && d1 - nl > r0 ? d1 - nl : r0;
+        const uint64_t hi1 = r0 + (d1 - d0) < nr ? r0 + (d1 - d0) : nr;
+        r1 = r1 < lo1 ? lo1 : (r1 > hi1 ? hi1 : r1);
+    }
     const uint32_t len = (uint32_t)(d1 - d0), lr = (uint32_t)(r1 - r0), ll = len - lr;
     const uint64_t l0 = d0 - r0;
     for (uint32_t i = tid; i < lr; i += SMJ_BLOCK) s_key[i] = run_key[r0 + i];
@@ -713,8 +734,11 @@ void smj_lookup(Ctx *ctx, const uint64_t *l, uint64_t nl, int pcol, const uint32
     if (nl == 0) return;
     const uint64_t tiles = (nl + nr + SMJ_TILE - 1) / SMJ_TILE;
     XH_REQUIRE(tiles < (1ull << 31), XLOG_HIP_CAPACITY_OVERFLOW, "sort-merge join: input too large");
+    Buf<uint64_t> split(ctx, tiles + 1);
+    hipLaunchKernelGGL(k_smj_partition, dim3((unsigned)((tiles + 1 + 255) / 256)), dim3(256), 0, ctx->stream, l, nl, pcol,
+                       run_key, nr, tiles, split.p);
     hipLaunchKernelGGL(k_smj_lookup, dim3((unsigned)tiles), dim3(SMJ_BLOCK), 0, ctx->stream, l, nl, pcol, run_key,
-                       run_start, nr, start, cnt);
+                       run_start, nr, split.p, start, cnt);
     XH_CHECK_HIP(hipGetLastError());
 }
 
