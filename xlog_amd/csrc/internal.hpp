@@ -18,6 +18,28 @@ namespace xh {
 
 constexpr int WAVE = 64;
 
+// Block-strided copy of n items, st(i, ld(i)) for i in [0, n), with BATCH loads
+// in flight per thread: a plain strided loop waits for each load before its
+// store, so staging a tile costs one memory latency per item a thread copies.
+// Loads past n read item n - 1 (in bounds, results dropped).  Every thread of
+// the block calls it with the same n.
+template <int BLOCK, int BATCH, class Load, class Store>
+__device__ __forceinline__ void batched_copy(uint32_t n, int tid, Load ld, Store st) {
+    for (uint32_t base = 0; base < n; base += (uint32_t)(BLOCK * BATCH)) {
+        decltype(ld(0u)) v[BATCH];
+#pragma unroll
+        for (int q = 0; q < BATCH; ++q) {
+            const uint32_t i = base + (uint32_t)(q * BLOCK + tid);
+            v[q] = ld(i < n ? i : n - 1);
+        }
+#pragma unroll
+        for (int q = 0; q < BATCH; ++q) {
+            const uint32_t i = base + (uint32_t)(q * BLOCK + tid);
+            if (i < n) st(i, v[q]);
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // error plumbing: every entry point returns a status and leaves a message in
 // a thread-local buffer readable through xlog_hip_last_error().

@@ -424,8 +424,9 @@ __global__ __launch_bounds__(SMJ_BLOCK) void k_smj_lookup(const uint64_t *__rest
     }
     const uint32_t len = (uint32_t)(d1 - d0), lr = (uint32_t)(r1 - r0), ll = len - lr;
     const uint64_t l0 = d0 - r0;
-    for (uint32_t i = tid; i < lr; i += SMJ_BLOCK) s_key[i] = run_key[r0 + i];
-    for (uint32_t i = tid; i < ll; i += SMJ_BLOCK) s_key[lr + i] = lkey_g(l0 + i);
+    batched_copy<SMJ_BLOCK, SMJ_ITEMS>(
+        len, tid, [&](uint32_t i) { return i < lr ? run_key[r0 + i] : lkey_g(l0 + (i - lr)); },
+        [&](uint32_t i, uint32_t v) { s_key[i] = v; });
     __syncthreads();
     const uint32_t *sr = s_key, *sl = s_key + lr;
     const uint32_t td = (uint32_t)tid * SMJ_ITEMS;

@@ -305,7 +305,8 @@ struct SelDiff {
         if (!s[2]) return;
         const uint64_t s0 = s[0];
         const uint32_t len = (uint32_t)(s[1] - s0);
-        for (uint32_t i = tid; i < len; i += SEL_WIN_BLOCK) sel_window[i] = b[s0 + i];
+        batched_copy<SEL_WIN_BLOCK, 8>(
+            len, tid, [&](uint32_t i) { return b[s0 + i]; }, [&](uint32_t i, uint64_t v) { sel_window[i] = v; });
     }
     __device__ bool flag(uint64_t idx, uint64_t key, uint64_t prev, const uint64_t *s) const {
         if (UNIQ && idx != 0 && prev == key) return false;
@@ -603,8 +604,9 @@ __global__ __launch_bounds__(MRG_BLOCK) void k_merge(const uint64_t *__restrict_
     }
     const uint32_t la = (uint32_t)(a1 - a0), len = (uint32_t)(d1 - d0), lb = len - la;
     const uint64_t b0 = d0 - a0;
-    for (uint32_t i = tid; i < la; i += MRG_BLOCK) s[i] = a[a0 + i];
-    for (uint32_t i = tid; i < lb; i += MRG_BLOCK) s[la + i] = b[b0 + i];
+    batched_copy<MRG_BLOCK, MRG_ITEMS>(
+        len, tid, [&](uint32_t i) { return i < la ? a[a0 + i] : b[b0 + (i - la)]; },
+        [&](uint32_t i, uint64_t v) { s[i] = v; });
     __syncthreads();
     const uint64_t *sa = s, *sb = s + la;
     uint32_t td = tid * MRG_ITEMS;

@@ -47,11 +47,12 @@ __device__ __forceinline__ uint64_t short_runs_place(const uint64_t *__restrict_
     const uint64_t lo = core_lo > 0 ? core_lo - 1 : 0;
     const uint64_t hi = core_hi + MAXR < n ? core_hi + MAXR : n;
     const uint32_t len = (uint32_t)(hi - lo);
-    for (uint32_t i = tid; i < len; i += BLOCK) {
-        const uint64_t k = in[lo + i];
-        t.hi[i] = (uint32_t)(k >> 32);
-        t.lo[i] = (uint32_t)k;
-    }
+    batched_copy<BLOCK, ITEMS>(
+        len, tid, [&](uint32_t i) { return in[lo + i]; },
+        [&](uint32_t i, uint64_t k) {
+            t.hi[i] = (uint32_t)(k >> 32);
+            t.lo[i] = (uint32_t)k;
+        });
     __syncthreads();
     // thread `tid` owns ITEMS consecutive keys: run start = last head at or
     // before the key, run end = first tail at or after it, plus one (the
