@@ -109,3 +109,14 @@ def test_skewed_high_word_keeps_digit_passes(provider, monkeypatch):
     keys[: n // 2] &= np.uint64(0xFFFFFFFF)
     _note("hybrid sort: skewed high word")
     _check(provider, keys, monkeypatch, want_runs=0, want_passes=8)
+
+
+def test_ticket_order(provider, monkeypatch):
+    """XLOG_HIP_SORT_TICKETS=1: the radix passes and the short-run unique number their tiles by start tickets."""
+    n = N_MIN + 777
+    keys = datagen.dup_tuples(n, 11)
+    _note("hybrid sort: ticket order")
+    monkeypatch.setenv("XLOG_HIP_SORT_TICKETS", "1")
+    got, runs, passes = _dedup_with_route(provider, keys)
+    assert (runs, passes) == (1, 4)
+    assert np.array_equal(got, oracle.sort_dedup(keys))

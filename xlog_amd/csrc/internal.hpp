@@ -301,12 +301,18 @@ struct SortUnique {
     bool done = false;
     uint64_t count = 0;
 };
+// XLOG_HIP_SORT_TICKETS=1 (read at each sort): the radix pass and the
+// short-run unique order their tiles by an atomic start ticket instead of the
+// workgroup index, so that their look-back does not rest on workgroups
+// starting in index order (slower: one device-wide atomic per tile).
+bool sort_tickets();
 int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **vals, uint32_t **vals_alt,
                    uint64_t n, int digit_lo = 0, int digit_hi = 8, const uint64_t *src = nullptr,
                    uint32_t known_digits = 0, SortUnique *uq = nullptr);
 // sort_short_runs fused with the adjacent-compare unique: the unique keys in
 // order to `out`, their count to *d_count (device); a run longer than 256
-// keys sets *d_long and the output is then incomplete.
+// keys sets *d_long and the output is then incomplete.  Its tiles take their
+// order from the workgroup index, like the radix pass, unless sort_tickets().
 void sort_short_runs_unique(Ctx *ctx, const uint64_t *in, uint64_t n, uint64_t *out, uint64_t *d_count,
                             uint64_t *d_long);
 

@@ -661,14 +661,18 @@ __global__ void k_unsorted(const uint64_t *__restrict__ k, uint64_t n, int stric
 }
 
 // Sort of short runs fused with the adjacent-compare unique, for the
-// high-word route of a full-key sort + dedup.  Each tile (in ticket order)
-// places the runs it owns (short_runs_place), keeps a placed key when it
+// high-word route of a full-key sort + dedup.  Each tile places the runs it owns (short_runs_place), keeps a placed key when it
 // differs from the key placed before it (the first place of the tile starts
 // a run, whose high word differs from every earlier key), counts the kept
 // keys, takes its output offset from decoupled look-back over the tiles'
 // counts and writes them there, coalesced.  Reads every key once (plus the
 // 1 + SRU_MAX halo per tile) and writes only the unique keys.  `work`
-// (profiling, optional) counts the written keys.
+// (profiling, optional) counts the written keys.  Tile = workgroup index, so
+// a tile waits only on tiles of lower index, which started before it when
+// workgroups start in index order (the radix pass's condition (1)); with
+// `ticket` the tile is the block's start ticket and the look-back holds
+// without that condition.  On C3 (2^28 keys, 65,536 tiles) the ticket's one
+// device-wide atomic per tile cost 0.09-0.25 ms of 1.67 (two A/B runs).
 constexpr int SRU_BLOCK = 512, SRU_CORE = 4096, SRU_MAX = 256;  // 256 x 2048 measured 10 % slower
 using SruTile = ShortRunTile<SRU_BLOCK, SRU_CORE, SRU_MAX>;
 __global__ __launch_bounds__(SRU_BLOCK) void k_short_runs_unique(const uint64_t *__restrict__ in, uint64_t n,
@@ -683,9 +687,11 @@ __global__ __launch_bounds__(SRU_BLOCK) void k_short_runs_unique(const uint64_t 
     constexpr int IT = SruTile::ITEMS;  // a wave covers WAVE * IT consecutive places
     static_assert(SRU_BLOCK * IT >= SRU_CORE + SRU_MAX, "the waves must cover the placed range");
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
-    if (tid == 0) s_tile = atomicAdd(ticket, 1ull) - ticket_base;
-    __syncthreads();
-    const uint64_t tile = s_tile;
+    if (ticket) {
+        if (tid == 0) s_tile = atomicAdd(ticket, 1ull) - ticket_base;
+        __syncthreads();
+    }
+    const uint64_t tile = ticket ? s_tile : (uint64_t)blockIdx.x;
     short_runs_place<SRU_BLOCK, SRU_CORE, SRU_MAX>(in, n, tile * SRU_CORE, t, long_run);
     const uint32_t pmin = t.pmin, pmax = t.pmax;
     const uint32_t wb = pmin + (uint32_t)wave * (WAVE * IT);
@@ -801,12 +807,13 @@ void sort_short_runs_unique(Ctx *ctx, const uint64_t *in, uint64_t n, uint64_t *
     XH_REQUIRE(tiles < (1ull << 31), XLOG_HIP_CAPACITY_OVERFLOW, "short-run unique: input too large");
     uint64_t tag;
     uint64_t *status = select_status(ctx, tiles, &tag);
-    unsigned long long tb = ctx->take_tickets(1, tiles);
+    unsigned long long *tk = sort_tickets() ? ctx->tickets + 1 : nullptr;
+    const unsigned long long tb = tk ? ctx->take_tickets(1, tiles) : 0ull;
     // algorithmic bytes: every key read once, every unique key written once (counted on the device)
     Prof prof(ctx, XLOG_HIP_KERNEL_SORT_RUNS, 8.0 * (double)n);
     unsigned long long *work = prof.work(8.0);
     hipLaunchKernelGGL(k_short_runs_unique, dim3((unsigned)tiles), dim3(SRU_BLOCK), 0, ctx->stream, in, n, out, d_count,
-                       d_long, status, tag, ctx->tickets + 1, tb, tiles, work);
+                       d_long, status, tag, tk, tb, tiles, work);
     XH_CHECK_HIP(hipGetLastError());
 }
 

@@ -516,8 +516,7 @@ static uint32_t pass_capacity(Ctx *ctx) {
     return (uint32_t)ctx->num_cus * (uint32_t)b;
 }
 
-// XLOG_HIP_SORT_TICKETS=1 selects the ticketed tile order (read at each sort).
-static bool sort_tickets() {
+bool sort_tickets() {
     const char *e = getenv("XLOG_HIP_SORT_TICKETS");
     return e && e[0] == '1';
 }
