@@ -99,12 +99,14 @@ extern __shared__ uint64_t sel_window[];
 // Generic single-pass selection.  Sel supplies:
 //   static constexpr bool kWindow: false, or true for a selection that needs
 //        a window of a second sorted array (then setup runs on all lanes of
-//        wave 0 and stage on every thread, with barriers around both)
+//        wave 0, followed by a barrier)
 //   __device__ void setup(uint64_t tile_first_idx, uint64_t tile_last_idx, uint64_t *smem, int lane)
 //        (thread 0 only unless kWindow)
-//   __device__ void stage(const uint64_t *smem, int tid)          (kWindow only)
 //   __device__ bool flag(uint64_t idx, uint64_t key, uint64_t prev_key, const uint64_t *smem)
 //        (prev_key = in[idx - 1], meaningful for idx > 0)
+//   kWindow selections instead: members<BLOCK, ITEMS>(keys, ...) (every
+//        thread; bit r = key r is in the window) and
+//        flag_member(idx, key, prev_key, member)
 //   __device__ void emit(uint64_t pos, uint64_t idx, uint64_t key)
 // A predicate that also reads the following row declares kNext = true and
 // provides flag_next(idx, key, prev, next); next is 0 past the last row.
@@ -147,8 +149,6 @@ __global__ __launch_bounds__(SelShape<Sel>::block) void k_select(const uint64_t 
             sel.setup(first, last - 1, s_sel, lane);
         }
         __syncthreads();
-        sel.stage(s_sel, tid);
-        __syncthreads();
     }
     const uint64_t wbase = tile * SEL_TILE + (uint64_t)wave * (SEL_ITEMS * WAVE);
     const uint64_t lt_mask = (1ull << lane) - 1ull;
@@ -170,6 +170,8 @@ __global__ __launch_bounds__(SelShape<Sel>::block) void k_select(const uint64_t 
         const uint64_t e = wbase + (uint64_t)SEL_ITEMS * WAVE;
         last_next = e < n ? in[e] : 0ull;
     }
+    uint32_t member = 0;  // window selections: bit r = key r is in the window
+    if constexpr (Sel::kWindow) member = sel.template members<SelShape<Sel>::block, SEL_ITEMS>(k, wbase, n, s_sel, tid, lane);
 #pragma unroll
     for (int r = 0; r < SEL_ITEMS; ++r) {
         uint64_t idx = wbase + (uint64_t)r * WAVE + lane;
@@ -181,6 +183,8 @@ __global__ __launch_bounds__(SelShape<Sel>::block) void k_select(const uint64_t 
             uint64_t down = __shfl_down(k[r], 1, WAVE);
             uint64_t ncarry = (r + 1 < SEL_ITEMS) ? __shfl(k[r + 1 < SEL_ITEMS ? r + 1 : r], 0, WAVE) : last_next;
             f = idx < n && sel.flag_next(idx, k[r], prev, lane < WAVE - 1 ? down : ncarry);
+        } else if constexpr (Sel::kWindow) {
+            f = idx < n && sel.flag_member(idx, k[r], prev, (member >> r) & 1u);
         } else {
             f = idx < n && sel.flag(idx, k[r], prev, s_sel);
         }
@@ -281,9 +285,13 @@ __device__ uint64_t wave_bound(const uint64_t *a, uint64_t lo, uint64_t hi, uint
 
 // unique (optional) and not a member of sorted b.  The tile's window of b
 // (from its first key's lower bound to its last key's upper bound) is found by
-// wave 0; a window of up to WIN_CAP keys is staged in LDS and each key is
-// looked up there in 13 fixed steps, a larger one is searched in HBM.
-constexpr uint32_t WIN_CAP = 8192;  // keys (64 KB of dynamic LDS)
+// wave 0.  A window of at most WIN_STREAM_PER_ROW keys per row of the tile (or
+// of at most WIN_CAP keys) is streamed through LDS in chunks of WIN_CAP keys
+// (one coalesced read of the window; each key is looked up in the chunk whose
+// range holds it, in 13 fixed steps); a larger window is searched in HBM, one
+// binary search per key, so that a small delta never streams a large b.
+constexpr uint32_t WIN_CAP = 8192;             // keys per chunk (64 KB of dynamic LDS)
+constexpr uint64_t WIN_STREAM_PER_ROW = 16;    // streamed window keys per row of the tile, at most
 template <bool UNIQ>
 struct SelDiff {
     static constexpr bool kWindow = true;
@@ -291,37 +299,56 @@ struct SelDiff {
     const uint64_t *b;
     uint64_t nb;
     uint64_t *out;
-    // s[0], s[1]: window [s0, s1) of b; s[2]: 1 when staged in LDS
+    // s[0], s[1]: window [s0, s1) of b; s[2]: 1 when it is streamed through LDS
     __device__ void setup(uint64_t first, uint64_t last, uint64_t *s, int lane) const {
         const uint64_t s0 = wave_bound<false>(b, 0, nb, in[first], lane);
         const uint64_t s1 = wave_bound<true>(b, s0, nb, in[last], lane);
         if (lane == 0) {
             s[0] = s0;
             s[1] = s1;
-            s[2] = s1 - s0 <= WIN_CAP ? 1u : 0u;
+            s[2] = (s1 - s0 <= WIN_CAP || s1 - s0 <= WIN_STREAM_PER_ROW * (last - first + 1)) ? 1u : 0u;
         }
     }
-    __device__ void stage(const uint64_t *s, int tid) const {
-        if (!s[2]) return;
-        const uint64_t s0 = s[0];
-        const uint32_t len = (uint32_t)(s[1] - s0);
-        batched_copy<SEL_WIN_BLOCK, 8>(
-            len, tid, [&](uint32_t i) { return b[s0 + i]; }, [&](uint32_t i, uint64_t v) { sel_window[i] = v; });
-    }
-    __device__ bool flag(uint64_t idx, uint64_t key, uint64_t prev, const uint64_t *s) const {
-        if (UNIQ && idx != 0 && prev == key) return false;
+    // bit r: key k[r] (row wbase + r * WAVE + lane, below n) is in b.  Every
+    // thread of the block calls it (the streamed window has barriers).
+    template <int BLOCK, int ITEMS>
+    __device__ uint32_t members(const uint64_t (&k)[ITEMS], uint64_t wbase, uint64_t n, const uint64_t *s,
+                                int tid, int lane) const {
+        uint32_t m = 0;
         if (s[2]) {
-            // elements of the window below key: binary lifting over <= WIN_CAP entries
-            const uint32_t len = (uint32_t)(s[1] - s[0]);
-            uint32_t pos = 0;
+            for (uint64_t c0 = s[0]; c0 < s[1]; c0 += WIN_CAP) {
+                const uint32_t len = (uint32_t)(s[1] - c0 < WIN_CAP ? s[1] - c0 : WIN_CAP);
+                __syncthreads();  // the previous chunk is no longer read
+                batched_copy<BLOCK, 8>(
+                    len, tid, [&](uint32_t i) { return b[c0 + i]; }, [&](uint32_t i, uint64_t v) { sel_window[i] = v; });
+                __syncthreads();
+                const uint64_t lo_k = sel_window[0], hi_k = sel_window[len - 1];
 #pragma unroll
-            for (uint32_t step = WIN_CAP / 2; step > 0; step >>= 1)
-                if (pos + step <= len && sel_window[pos + step - 1] < key) pos += step;
-            if (pos + 1 <= len && sel_window[pos] < key) ++pos;  // pos counts every entry < key
-            return !(pos < len && sel_window[pos] == key);
+                for (int r = 0; r < ITEMS; ++r) {
+                    const uint64_t key = k[r];
+                    if (wbase + (uint64_t)r * WAVE + lane >= n || key < lo_k || key > hi_k) continue;
+                    // entries of the chunk below key: binary lifting over <= WIN_CAP entries
+                    uint32_t pos = 0;
+#pragma unroll
+                    for (uint32_t step = WIN_CAP / 2; step > 0; step >>= 1)
+                        if (pos + step <= len && sel_window[pos + step - 1] < key) pos += step;
+                    if (pos + 1 <= len && sel_window[pos] < key) ++pos;
+                    if (pos < len && sel_window[pos] == key) m |= 1u << r;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < ITEMS; ++r) {
+                if (wbase + (uint64_t)r * WAVE + lane >= n) continue;
+                const uint64_t p = lower_bound_u64(b, s[0], s[1], k[r]);
+                if (p < s[1] && b[p] == k[r]) m |= 1u << r;
+            }
         }
-        uint64_t p = lower_bound_u64(b, s[0], s[1], key);
-        return !(p < s[1] && b[p] == key);
+        return m;
+    }
+    __device__ bool flag_member(uint64_t idx, uint64_t key, uint64_t prev, bool member) const {
+        if (UNIQ && idx != 0 && prev == key) return false;
+        return !member;
     }
     __device__ void emit(uint64_t pos, uint64_t, uint64_t key) const { out[pos] = key; }
 };
