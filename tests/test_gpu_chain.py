@@ -279,3 +279,33 @@ def test_hash_route_queued_overflow(provider, monkeypatch):
         for q in idb:
             assert np.array_equal(p.download_packed(outs[q]), outs_o[q]), name
         assert st["iterations"] == it_o and st["delta_sizes"] == deltas_o
+
+
+def test_staged_emit(provider, monkeypatch):
+    """The bitmap route's final emit of dense rows stages each group of 64 words in LDS and writes it with
+    line-aligned stores (rows of 8192 tuples or more on average).  A hub graph (every vertex to 0 and back)
+    closes to every pair of its 8,200 vertices (rows of 8,200 tuples, 129-word rows); then programs of the
+    other tests with the staged emit forced on every row size (XLOG_HIP_EMIT_STAGED_ROW=0), including
+    2048-word rows (four chunks of 512 words per row)."""
+    p = provider
+    v = 8200
+    others = np.arange(1, v, dtype=np.uint32)
+    s = np.concatenate([others, np.zeros(v - 1, np.uint32)])
+    d = np.concatenate([np.zeros(v - 1, np.uint32), others])
+    _note("staged emit: hub graph")
+    outs, st = _run(p, tc_plan(), [pack(s, d), None], ROUTE_BITMAP)
+    got = p.download_packed(outs[1])
+    x = np.arange(v, dtype=np.uint64)
+    assert np.array_equal(got, ((x[:, None] << np.uint64(32)) | x[None, :]).ravel())
+    monkeypatch.setenv("XLOG_HIP_EMIT_STAGED_ROW", "0")
+    for n, m, seed in ((300, 600, 1), (1000, 2500, 2)):
+        s, d = _graph(n, m, seed)
+        _parity(p, f"staged emit tc {n}", cp.left_tc_plan(), [pack(s, d), None], [1], routes=(ROUTE_BITMAP,))
+    rng = np.random.default_rng(15)
+    ids = np.sort(rng.choice(1 << 17, 400, replace=False)).astype(np.uint32)
+    ids[-1] = (1 << 17) - 1
+    s, d = ids[rng.integers(0, 400, 900)], ids[rng.integers(0, 400, 900)]
+    _parity(p, "staged emit top of domain", tc_plan(), [pack(s, d), None], [1], routes=(ROUTE_BITMAP,))
+    f = datagen.andersen(400, 1500, 1.5, datagen.seed_for(5))
+    rels = [pack(*f[k]) for k in ("assign", "addressOf", "load", "store")] + [None]
+    _parity(p, "staged emit andersen", andersen_plan(), rels, [4], routes=(ROUTE_BITMAP,))

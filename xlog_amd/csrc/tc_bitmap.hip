@@ -166,10 +166,14 @@ __global__ __launch_bounds__(TB) void k_row_counts(const uint64_t *__restrict__ 
     if (threadIdx.x == 0) cnt[x] = s;
 }
 
-// emit row x's set bits as (x << 32 | z) starting at off[x]; positions at or
-// past cap (the allocation: the caller may size it from its own count) are
-// not written
-__global__ __launch_bounds__(TB) void k_emit_rows(const uint64_t *__restrict__ R, uint64_t words,
+// Both emits write row x's set bits as (x << 32 | z) starting at off[x] (a
+// block per row); positions at or past cap (the allocation: the caller may
+// size it from its own count) are not written.
+//
+// Rows of a few thousand tuples or fewer: each wave stores its words' tuples
+// straight from the bits (lane b stores bit b, so a dense word is one
+// contiguous 512-byte store), TB words per step of the block.
+__global__ __launch_bounds__(TB) void k_emit_rows_direct(const uint64_t *__restrict__ R, uint64_t words,
                                                   const uint64_t *__restrict__ off, uint64_t *__restrict__ out,
                                                   uint64_t cap) {
     __shared__ uint64_t s_part[TB / WAVE];
@@ -215,6 +219,75 @@ __global__ __launch_bounds__(TB) void k_emit_rows(const uint64_t *__restrict__ R
         __syncthreads();
         if (tid == 0) s_base += tot;
         __syncthreads();
+    }
+}
+
+// Dense rows (EMIT_STAGED_ROW tuples or more on average): the row is read in
+// chunks of EMIT_TB words (a block scan of their popcounts gives each word's
+// offset); a group of EMIT_G words is expanded into an LDS buffer (a wave per
+// word, a lane per bit), and the block then writes the group's tuples with
+// stores aligned to 128-byte lines (a word's tuples start at any 8-byte
+// offset, so storing them straight from the expanding wave splits lines).
+// Two buffers, one barrier per group: the expansion of group g + 2 follows
+// the barrier of group g + 1, which every thread passes after writing group g
+// out.
+constexpr int EMIT_TB = 512, EMIT_G = 64;
+constexpr uint64_t EMIT_STAGED_ROW = 8192;
+__global__ __launch_bounds__(EMIT_TB) void k_emit_rows(const uint64_t *__restrict__ R, uint64_t words,
+                                                       const uint64_t *__restrict__ off, uint64_t *__restrict__ out,
+                                                       uint64_t cap) {
+    constexpr int WAVES = EMIT_TB / WAVE, WPG = EMIT_G / WAVES;
+    static_assert(EMIT_TB % EMIT_G == 0 && EMIT_G % WAVES == 0, "groups split evenly over the waves");
+    __shared__ uint64_t s_word[EMIT_TB];
+    __shared__ uint32_t s_woff[EMIT_TB + 1];  // offsets inside the chunk; [EMIT_TB]: the chunk's total
+    __shared__ uint32_t s_part[WAVES];
+    __shared__ uint64_t buf[2][EMIT_G * 64];
+    const uint32_t x = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint64_t *row = R + (uint64_t)x * words;
+    const uint64_t hi = (uint64_t)x << 32;
+    const uint64_t lt_mask = (1ull << lane) - 1ull;
+    uint64_t cbase = off[x];  // output position of the chunk's first tuple
+    int gi = 0;
+    for (uint64_t c0 = 0; c0 < words; c0 += EMIT_TB) {
+        const uint64_t w = c0 + tid;
+        const uint64_t bits = w < words ? row[w] : 0ull;
+        const uint32_t pc = (uint32_t)__popcll(bits);
+        uint32_t incl = pc;
+#pragma unroll
+        for (int o = 1; o < WAVE; o <<= 1) {
+            const uint32_t t = __shfl_up(incl, o, WAVE);
+            if (lane >= o) incl += t;
+        }
+        if (lane == WAVE - 1) s_part[wave] = incl;
+        __syncthreads();
+        uint32_t pre = 0, tot = 0;
+#pragma unroll
+        for (int q = 0; q < WAVES; ++q) {
+            if (q < wave) pre += s_part[q];
+            tot += s_part[q];
+        }
+        s_word[tid] = bits;
+        s_woff[tid] = pre + incl - pc;
+        if (tid == 0) s_woff[EMIT_TB] = tot;
+        __syncthreads();
+        const uint64_t cw = words - c0 < (uint64_t)EMIT_TB ? words - c0 : (uint64_t)EMIT_TB;
+        for (uint32_t g0 = 0; g0 < cw; g0 += EMIT_G, ++gi) {
+            uint64_t *b = buf[gi & 1];
+            const uint32_t gb = s_woff[g0], ge = s_woff[g0 + EMIT_G];
+#pragma unroll
+            for (int j = 0; j < WPG; ++j) {
+                const uint32_t t = g0 + (uint32_t)(wave * WPG + j);
+                const uint64_t wb = s_word[t];
+                if ((wb >> lane) & 1ull)
+                    b[s_woff[t] - gb + (uint32_t)__popcll(wb & lt_mask)] = hi | (uint64_t)((c0 + t) * 64 + lane);
+            }
+            __syncthreads();
+            const uint64_t gs = cbase + gb, gend = cbase + ge;
+            for (uint64_t p = (gs & ~15ull) + (uint64_t)tid; p < gend; p += EMIT_TB)
+                if (p >= gs && p < cap) out[p] = b[p - gs];
+        }
+        cbase += tot;
     }
 }
 
@@ -272,7 +345,8 @@ void pairs_csr(Ctx *ctx, const uint64_t *pairs, uint64_t m, uint32_t nv, uint64_
 }
 
 // The set bits of an nv x words bitmap as sorted packed (x << 32) | z rows
-// (row counts, a scan, then one block per row writing at its offset).
+// (row counts, a scan, then one block per row writing at its offset; rows
+// of EMIT_STAGED_ROW tuples or more on average are staged in LDS).
 uint64_t bitmap_emit(Ctx *ctx, const uint64_t *bits, uint32_t nv, uint64_t words, uint64_t **out, int prof_kind,
                      uint64_t known_total) {
     *out = nullptr;
@@ -289,7 +363,13 @@ uint64_t bitmap_emit(Ctx *ctx, const uint64_t *bits, uint32_t nv, uint64_t words
     if (total == 0) return 0;
     *out = static_cast<uint64_t *>(ctx->alloc(total * sizeof(uint64_t)));
     Prof prof(ctx, prof_kind, 8.0 * (double)total + 8.0 * (double)nv * (double)words);
-    hipLaunchKernelGGL(k_emit_rows, dim3(nv), dim3(TB), 0, ctx->stream, bits, words, rc.p, *out, total);
+    // XLOG_HIP_EMIT_STAGED_ROW (read at each emit) replaces the row size from which the staged emit runs
+    uint64_t staged_row = EMIT_STAGED_ROW;
+    if (const char *e = getenv("XLOG_HIP_EMIT_STAGED_ROW")) staged_row = strtoull(e, nullptr, 10);
+    if (total >= staged_row * nv)
+        hipLaunchKernelGGL(k_emit_rows, dim3(nv), dim3(EMIT_TB), 0, ctx->stream, bits, words, rc.p, *out, total);
+    else
+        hipLaunchKernelGGL(k_emit_rows_direct, dim3(nv), dim3(TB), 0, ctx->stream, bits, words, rc.p, *out, total);
     XH_CHECK_HIP(hipGetLastError());
     return total;
 }
