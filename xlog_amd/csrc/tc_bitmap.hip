@@ -283,9 +283,14 @@ __global__ __launch_bounds__(EMIT_TB) void k_emit_rows(const uint64_t *__restric
                     b[s_woff[t] - gb + (uint32_t)__popcll(wb & lt_mask)] = hi | (uint64_t)((c0 + t) * 64 + lane);
             }
             __syncthreads();
-            const uint64_t gs = cbase + gb, gend = cbase + ge;
-            for (uint64_t p = (gs & ~15ull) + (uint64_t)tid; p < gend; p += EMIT_TB)
-                if (p >= gs && p < cap) out[p] = b[p - gs];
+            // the group's tuples go to [gs, gs + n); o is the 128-byte line holding gs
+            const uint64_t gs = cbase + gb;
+            const uint32_t lead = (uint32_t)(gs & 15u), end = lead + (ge - gb);
+            uint64_t *o = out + (gs - lead);
+            const uint64_t room = cap > gs - lead ? cap - (gs - lead) : 0;  // positions below cap
+            const uint32_t lim = room < (uint64_t)end ? (uint32_t)room : end;
+            for (uint32_t i = (uint32_t)tid; i < lim; i += EMIT_TB)
+                if (i >= lead) o[i] = b[i - lead];
         }
         cbase += tot;
     }
