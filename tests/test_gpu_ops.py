@@ -149,7 +149,10 @@ def test_sort_arity4_and_dedup(provider):
     assert got == [first[k] for k in sorted(first)]
 
 
-@pytest.mark.parametrize("na,nb", [(0, 0), (0, 10), (10, 0), (1000, 1000), (5000, 300000), (300000, 4099)])
+# diff windows: (5000, 300000) searches B in HBM (window above 16 keys per row), (50000, 600000) streams
+# windows of about 10^5 keys through LDS in several 8192-key chunks, the others stream one chunk
+@pytest.mark.parametrize("na,nb", [(0, 0), (0, 10), (10, 0), (1000, 1000), (5000, 300000), (300000, 4099),
+                                   (50000, 600000)])
 def test_union_diff_random(provider, na, nb):
     p = provider
     _note(f"union/diff na={na} nb={nb}")
