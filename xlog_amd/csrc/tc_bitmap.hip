@@ -283,7 +283,7 @@ __global__ __launch_bounds__(EMIT_TB) void k_emit_rows(const uint64_t *__restric
                     b[s_woff[t] - gb + (uint32_t)__popcll(wb & lt_mask)] = hi | (uint64_t)((c0 + t) * 64 + lane);
             }
             __syncthreads();
-            // the group's tuples go to [gs, gs + n); o is the 128-byte line holding gs
+            // the group's tuples go to [gs, gs + ge - gb); o starts at the 128-byte line holding gs
             const uint64_t gs = cbase + gb;
             const uint32_t lead = (uint32_t)(gs & 15u), end = lead + (ge - gb);
             uint64_t *o = out + (gs - lead);
