@@ -139,3 +139,21 @@ def test_ticketed_tile_order(provider, monkeypatch, tiles):
     s = p.sort(p.create_buffer_from_u32_columns([c0, c1, c2]), [2, 0])
     order = np.lexsort((c0, c2))  # stable: by c2, then c0, ties in input order
     assert np.array_equal(p.download_column(s, 1), c1[order])
+
+
+@pytest.mark.parametrize("n", [2, 3, 1000, 1024, 1025, 4097, 8191, 8192, 8193])
+def test_small_sort_unique(provider, n):
+    """Sort + dedup of one tile or less and just past it: random keys, many duplicates, all-equal keys and keys
+    of all ones (the largest u64)."""
+    p = provider
+    _note(f"small sort unique n={n}")
+    rng = np.random.default_rng(n + 5)
+    cases = [rng.integers(0, 1 << 64, size=n, dtype=np.uint64),
+             rng.integers(0, max(2, n // 3), size=n, dtype=np.uint64),
+             np.full(n, 12345, dtype=np.uint64)]
+    top = rng.integers(0, 1 << 64, size=n, dtype=np.uint64)
+    top[rng.choice(n, max(1, n // 4), replace=False)] = np.uint64(0xFFFFFFFFFFFFFFFF)
+    cases.append(top)
+    for keys in cases:
+        got = p.download_packed(p.dedup_full_row(p.create_buffer_from_packed(keys)))
+        assert np.array_equal(got, np.unique(keys))
