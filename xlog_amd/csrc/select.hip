@@ -284,14 +284,19 @@ __device__ uint64_t wave_bound(const uint64_t *a, uint64_t lo, uint64_t hi, uint
 }
 
 // unique (optional) and not a member of sorted b.  The tile's window of b
-// (from its first key's lower bound to its last key's upper bound) is found by
-// wave 0.  A window of at most WIN_STREAM_PER_ROW keys per row of the tile (or
+// (from its first key's lower bound to its last key's upper bound) comes from
+// k_diff_windows, which finds every tile's window at once before the selection
+// (a tile that searched its own would wait on 10 dependent rounds of loads
+// before reading anything), or, for selections of fewer than DIFF_WINDOW_PASS
+// tiles (where the extra launch costs more), is found by the tile's wave 0.
+// A window of at most WIN_STREAM_PER_ROW keys per row of the tile (or
 // of at most WIN_CAP keys) is streamed through LDS in chunks of WIN_CAP keys
 // (one coalesced read of the window; each key is looked up in the chunk whose
 // range holds it, in 13 fixed steps); a larger window is searched in HBM, one
 // binary search per key, so that a small delta never streams a large b.
 constexpr uint32_t WIN_CAP = 8192;             // keys per chunk (64 KB of dynamic LDS)
 constexpr uint64_t WIN_STREAM_PER_ROW = 16;    // streamed window keys per row of the tile, at most
+constexpr uint64_t DIFF_WINDOW_PASS = 256;     // tiles from which the windows come from k_diff_windows
 template <bool UNIQ>
 struct SelDiff {
     static constexpr bool kWindow = true;
@@ -299,10 +304,19 @@ struct SelDiff {
     const uint64_t *b;
     uint64_t nb;
     uint64_t *out;
+    const uint64_t *win;  // [2t], [2t + 1]: window of tile t (nullptr: searched by the tile)
+    uint64_t tile_rows;
     // s[0], s[1]: window [s0, s1) of b; s[2]: 1 when it is streamed through LDS
     __device__ void setup(uint64_t first, uint64_t last, uint64_t *s, int lane) const {
-        const uint64_t s0 = wave_bound<false>(b, 0, nb, in[first], lane);
-        const uint64_t s1 = wave_bound<true>(b, s0, nb, in[last], lane);
+        uint64_t s0, s1;
+        if (win) {
+            const uint64_t t = first / tile_rows;
+            s0 = win[2 * t];
+            s1 = win[2 * t + 1];
+        } else {
+            s0 = wave_bound<false>(b, 0, nb, in[first], lane);
+            s1 = wave_bound<true>(b, s0, nb, in[last], lane);
+        }
         if (lane == 0) {
             s[0] = s0;
             s[1] = s1;
@@ -352,6 +366,23 @@ struct SelDiff {
     }
     __device__ void emit(uint64_t pos, uint64_t, uint64_t key) const { out[pos] = key; }
 };
+
+// win[2t] = lower bound of tile t's first row in b, win[2t + 1] = upper bound
+// of its last row: a wave per tile, 4 tiles per 256-thread block
+__global__ __launch_bounds__(256) void k_diff_windows(const uint64_t *__restrict__ in, uint64_t n,
+                                                      const uint64_t *__restrict__ b, uint64_t nb, uint64_t tile_rows,
+                                                      uint64_t tiles, uint64_t *__restrict__ win) {
+    const int lane = threadIdx.x & (WAVE - 1);
+    const uint64_t t = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= tiles) return;  // wave-uniform
+    const uint64_t first = t * tile_rows, last = (first + tile_rows < n ? first + tile_rows : n) - 1;
+    const uint64_t s0 = wave_bound<false>(b, 0, nb, in[first], lane);
+    const uint64_t s1 = wave_bound<true>(b, s0, nb, in[last], lane);
+    if (lane == 0) {
+        win[2 * t] = s0;
+        win[2 * t + 1] = s1;
+    }
+}
 
 // keys different from one value (the occupied slots of a hash table)
 struct SelNotValue {
@@ -852,8 +883,18 @@ void select_unique_low(Ctx *ctx, const uint64_t *k, uint64_t n, uint64_t *out, u
 }
 void select_unique_diff(Ctx *ctx, const uint64_t *k, uint64_t n, const uint64_t *b, uint64_t nb, uint64_t *out,
                         uint64_t *d_count) {
-    if (nb == 0) { select_unique(ctx, k, n, out, d_count); return; }
-    run_select(ctx, k, n, SelDiff<true>{k, b, nb, out}, d_count);
+    if (nb == 0 || n == 0) { select_unique(ctx, k, n, out, d_count); return; }
+    constexpr uint64_t rows = SelShape<SelDiff<true>>::tile;
+    const uint64_t tiles = (n + rows - 1) / rows;
+    XH_REQUIRE(tiles < (1ull << 31), XLOG_HIP_CAPACITY_OVERFLOW, "select: input too large");
+    Buf<uint64_t> win;
+    if (tiles >= DIFF_WINDOW_PASS) {
+        win = Buf<uint64_t>(ctx, 2 * tiles);
+        hipLaunchKernelGGL(k_diff_windows, dim3((unsigned)((tiles + 3) / 4)), dim3(256), 0, ctx->stream, k, n, b, nb,
+                           rows, tiles, win.p);
+        XH_CHECK_HIP(hipGetLastError());
+    }
+    run_select(ctx, k, n, SelDiff<true>{k, b, nb, out, win.p, rows}, d_count);
 }
 void select_not_value(Ctx *ctx, const uint64_t *k, uint64_t n, uint64_t v, uint64_t *out, uint64_t *d_count) {
     run_select(ctx, k, n, SelNotValue{v, out}, d_count);
