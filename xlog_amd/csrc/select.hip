@@ -368,19 +368,19 @@ struct SelDiff {
 };
 
 // win[2t] = lower bound of tile t's first row in b, win[2t + 1] = upper bound
-// of its last row: a wave per tile, 4 tiles per 256-thread block
+// of its last row: a thread per bound, all of them in flight at once (the top
+// levels of the searches are shared and stay in cache)
 __global__ __launch_bounds__(256) void k_diff_windows(const uint64_t *__restrict__ in, uint64_t n,
                                                       const uint64_t *__restrict__ b, uint64_t nb, uint64_t tile_rows,
                                                       uint64_t tiles, uint64_t *__restrict__ win) {
-    const int lane = threadIdx.x & (WAVE - 1);
-    const uint64_t t = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (t >= tiles) return;  // wave-uniform
-    const uint64_t first = t * tile_rows, last = (first + tile_rows < n ? first + tile_rows : n) - 1;
-    const uint64_t s0 = wave_bound<false>(b, 0, nb, in[first], lane);
-    const uint64_t s1 = wave_bound<true>(b, s0, nb, in[last], lane);
-    if (lane == 0) {
-        win[2 * t] = s0;
-        win[2 * t + 1] = s1;
+    const uint64_t q = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= 2 * tiles) return;
+    const uint64_t t = q >> 1, first = t * tile_rows;
+    if (q & 1) {
+        const uint64_t last = (first + tile_rows < n ? first + tile_rows : n) - 1;
+        win[q] = upper_bound_u64(b, 0, nb, in[last]);
+    } else {
+        win[q] = lower_bound_u64(b, 0, nb, in[first]);
     }
 }
 
@@ -890,8 +890,8 @@ void select_unique_diff(Ctx *ctx, const uint64_t *k, uint64_t n, const uint64_t 
     Buf<uint64_t> win;
     if (tiles >= DIFF_WINDOW_PASS) {
         win = Buf<uint64_t>(ctx, 2 * tiles);
-        hipLaunchKernelGGL(k_diff_windows, dim3((unsigned)((tiles + 3) / 4)), dim3(256), 0, ctx->stream, k, n, b, nb,
-                           rows, tiles, win.p);
+        hipLaunchKernelGGL(k_diff_windows, dim3((unsigned)((2 * tiles + 255) / 256)), dim3(256), 0, ctx->stream, k, n, b,
+                           nb, rows, tiles, win.p);
         XH_CHECK_HIP(hipGetLastError());
     }
     run_select(ctx, k, n, SelDiff<true>{k, b, nb, out, win.p, rows}, d_count);
