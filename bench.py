@@ -14,7 +14,9 @@ With the default workload the same line carries the other configs under
 `configs` (c1: TC on G(1000, 5000); c2: R(a,b) join S(b,c), project, sort +
 dedup at 2^24 rows a side; c3: sort + dedup of 2^28 packed tuples; c5: Andersen
 points-to at 10,000 variables), each with its own timing, roofline and CPU
-baseline.  c1j / c4j force the join route and c1h / c4h the hash-set route;
+baseline.  c5_stated is C5 at its stated 500,000 variables, run once for its outcome
+(the reference's u32 join-row limit trips in the first recursive iteration).
+c1j / c4j force the join route and c1h / c4h the hash-set route;
 tcs / tcs_crit are closures over 2^20 vertices whose ids are spread over u32
 (the hash-set route, AUTO's choice there) and tcs_j is tcs on the join route;
 c2u is the unfused join -> sort -> dedup sequence; copy is the counter
@@ -309,6 +311,12 @@ def measure(name: str, p, steps: int, warmup: int, with_cpu: bool) -> dict:
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": dname,
                 "launches_per_step": d["launches"] / max(1, steps), "avg_launch_ms": round(avg_ms, 4),
                 "algo_bytes_per_launch": bytes_per_launch}
+    # the whole step against the same peak: every instrumented kernel's algorithmic bytes per step over the
+    # uninstrumented wall time of a step (kernels outside the instrumented kinds add bytes not counted here)
+    step_bytes = sum(v["algo_bytes"] for v in prof.values()) / max(1, steps)
+    step_gbs = step_bytes / (ms / 1000.0) / 1e9 if ms > 0 else 0.0
+    step_roofline = {"algo_bytes_per_step": step_bytes, "achieved": round(step_gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(step_gbs / HBM_PEAK_GBS, 4)}
     kernels = {k: {"launches": v["launches"], "total_ms": round(v["total_ms"], 3),
                    "algo_GBps": round(v["algo_bytes"] / (v["total_ms"] / 1000.0) / 1e9, 1) if v["total_ms"] else None}
                for k, v in prof.items() if v["launches"]}
@@ -321,11 +329,12 @@ def measure(name: str, p, steps: int, warmup: int, with_cpu: bool) -> dict:
         result["delta_sizes"] = state["delta_sizes"]
     result.update(extra)
     return {"workload": name, "value": value, "unit": "tuples/s", "value_counts": unit_desc, "ms_per_step": ms,
-            "ms_per_step_with_kernel_events": (tp1 - tp0) * 1000.0 / max(1, steps), "steps": steps, "warmup": warmup, "config": config, "roofline": roofline, "cpu_baseline": cpu,
+            "ms_per_step_with_kernel_events": (tp1 - tp0) * 1000.0 / max(1, steps), "steps": steps, "warmup": warmup,
+            "config": config, "roofline": roofline, "step_roofline": step_roofline, "cpu_baseline": cpu,
             "kernels": kernels, "result": result}
 
 
-def run_c5full(p) -> dict:
+def run_c5full(p, max_join_rows: int = (1 << 32) - 1) -> dict:
     """BASELINE's literal C5 (500,000 variables / 2,000,000 facts) on the join route with the reference's
     u32 join-row limit (relational.rs:4550-4555): the outcome (converged, or the failure with the iteration
     and the bag size that tripped it), plus the size of rule 2's first-iteration output, a lower bound of
@@ -338,11 +347,11 @@ def run_c5full(p) -> dict:
     log(f"c5full inputs generated in {time.perf_counter() - t:.1f}s")
     rels = [p.create_buffer_from_u32_columns(list(f[k])) for k in ("assign", "addressOf", "load", "store")]
     out = {"workload": "c5full: Andersen points-to at 500,000 variables / 2,000,000 facts (BASELINE configs[4])",
-           **cfg, "seed": datagen.seed_for(5), "max_join_rows": (1 << 32) - 1}
+           **cfg, "seed": datagen.seed_for(5), "max_join_rows": max_join_rows}
     p.synchronize()
     t0 = time.perf_counter()
     try:
-        outs, st = p.fixpoint(andersen_plan(), rels + [None], max_join_rows=(1 << 32) - 1)
+        outs, st = p.fixpoint(andersen_plan(), rels + [None], max_join_rows=max_join_rows)
         out.update(outcome="converged", tuples=outs[4].num_rows(), iterations=st["iterations"],
                    delta_sizes=st["delta_sizes"], route=st["route"])
     except XlogError as e:
@@ -351,6 +360,8 @@ def run_c5full(p) -> dict:
                    iterations_reached=st.get("iterations"), delta_sizes=st.get("delta_sizes"), route=st.get("route"))
     p.synchronize()
     out["seconds"] = time.perf_counter() - t0
+    if not max_join_rows:
+        return out
     # rule 2 of the first iteration alone: {(v, o) : assign(v, w), addressOf(w, o)} (the seed delta is addressOf)
     t0 = time.perf_counter()
     r2 = p.join_project_dedup(rels[0], rels[1], 1, 0, [0, 3])
@@ -377,8 +388,10 @@ def main() -> int:
     from xlog_amd import HipKernelProvider
 
     p = HipKernelProvider(0)
-    if args.workload == "c5full":
-        print(json.dumps({"metric": METRIC, "value": None, "n_gpus": 1, "result": run_c5full(p)}))
+    if args.workload in ("c5full", "c5full_nolimit"):
+        # c5full_nolimit: the same without the join-row limit (chunked join steps), for its measured outcome
+        r = run_c5full(p, 0 if args.workload == "c5full_nolimit" else (1 << 32) - 1)
+        print(json.dumps({"metric": METRIC, "value": None, "n_gpus": 1, "result": r}))
         p.close()
         return 0
     head = measure(args.workload, p, args.steps, args.warmup, not args.no_cpu_baseline)
@@ -389,6 +402,9 @@ def main() -> int:
         for name, k, w in (("c1", 20, 3), ("c2", 10, 3), ("c3", 3, 1), ("c5", 5, 2)):
             extras[name] = measure(name, p, k, w, not args.no_cpu_baseline)
             p.trim()
+        # C5 at its stated size: its outcome (the fail-closed join-row limit, as the reference), once
+        extras["c5_stated"] = run_c5full(p)
+        p.trim()
 
     out = {
         "metric": METRIC,
@@ -406,6 +422,7 @@ def main() -> int:
         "data": "synthetic (seeded generators, xlog_amd/csrc/datagen.c)",
         "config": {**head["config"], "value_counts": head["value_counts"], "parallelism": "single GPU"},
         "roofline": head["roofline"],
+        "step_roofline": head["step_roofline"],
         "cpu_baseline": head["cpu_baseline"],
         "kernels": head["kernels"],
         "result": head["result"],

@@ -47,7 +47,7 @@ typedef enum {
 
 typedef struct xlog_hip_ctx xlog_hip_ctx;
 typedef struct xlog_hip_rel xlog_hip_rel;
-/* reusable join index over one key column of a relation (reference JoinIndexV2) */
+/* reusable join index over a key list of a relation (reference JoinIndexV2) */
 typedef struct xlog_hip_join_index xlog_hip_join_index;
 
 /* join kinds (reference JoinType, relational.rs:2926); only INNER is on the path */
@@ -77,6 +77,16 @@ void *xlog_hip_stream(xlog_hip_ctx *ctx);
 xlog_hip_status xlog_hip_memory_stats(xlog_hip_ctx *ctx, uint64_t *in_use, uint64_t *peak, uint64_t *cached);
 /* Return cached device blocks to the driver. */
 xlog_hip_status xlog_hip_trim(xlog_hip_ctx *ctx);
+/* Device memory budget of the context in bytes (0: none, the default)
+ * (reference: MemoryBudget::with_limit(device_bytes), crates/xlog-core/src/config.rs:39-45,
+ * enforced by GpuMemoryManager, crates/xlog-cuda/src/memory.rs:633,756-770, with
+ * abort_on_exceed).  An allocation that would take the bytes held by live
+ * relations and scratch past it fails with XLOG_HIP_OOM ("GPU memory budget
+ * exceeded"), and cached blocks are returned to the driver before the
+ * context's footprint would pass it.  The fixpoint's route choice (AUTO) sizes
+ * the bitmap routes' matrices against it.  Lowering it below the bytes in use
+ * is allowed: later allocations then fail until enough is freed. */
+xlog_hip_status xlog_hip_set_memory_budget(xlog_hip_ctx *ctx, uint64_t device_bytes);
 
 /* ---- relations (CudaBuffer counterpart, memory.rs:1758-1930) ------------- */
 
@@ -181,20 +191,26 @@ xlog_hip_status xlog_hip_hash_join(xlog_hip_ctx *ctx, const xlog_hip_rel *left, 
 xlog_hip_status xlog_hip_hash_join_keys(xlog_hip_ctx *ctx, const xlog_hip_rel *left, const xlog_hip_rel *right,
                                         const uint32_t *left_keys, const uint32_t *right_keys, uint32_t n_keys,
                                         int join_type, xlog_hip_rel **out);
-/* Join index over column right_key of `right`, reused across probes; fails
- * on an empty relation like the reference (build_join_index_v2,
- * relational.rs:3728-3880).  Free it with xlog_hip_join_index_free before its
+/* Join index over the key columns right_keys[0 .. n_keys) of `right`,
+ * reused across probes (reference: build_join_index_v2(right, right_keys),
+ * relational.rs:3728-3880, called with the rule's whole key list by the
+ * executor's persistent-index join, node_dispatch.rs:444-488).  Fails on an
+ * empty relation like the reference, and on one of 2^32 - 1 rows or more
+ * (CAPACITY_OVERFLOW).  Free it with xlog_hip_join_index_free before its
  * context is destroyed. */
-xlog_hip_status xlog_hip_join_index_build(xlog_hip_ctx *ctx, const xlog_hip_rel *right, uint32_t right_key,
-                                          xlog_hip_join_index **out);
-/* xlog_hip_hash_join against a prebuilt index of (right, right_key); the
- * output is that of xlog_hip_hash_join.  max_output > 0 keeps at most that
- * many INNER rows (reference: hash_join_v2_with_index, relational.rs:3882-4000;
- * the reference keeps an unspecified subset, this keeps the first rows in
- * probe-row order). */
+xlog_hip_status xlog_hip_join_index_build(xlog_hip_ctx *ctx, const xlog_hip_rel *right, const uint32_t *right_keys,
+                                          uint32_t n_keys, xlog_hip_join_index **out);
+/* xlog_hip_hash_join_keys against a prebuilt index of (right, right_keys);
+ * the index must have been built over this right relation (same row count)
+ * and exactly these right key columns, else INVALID_ARG
+ * (reference: hash_join_v2_with_index, relational.rs:3882-4000).  The output
+ * is that of xlog_hip_hash_join_keys: INNER rows left ++ right in left-row
+ * order and, per left row, right-row order; max_output > 0 keeps the first
+ * max_output INNER rows of that order (the reference keeps an unspecified
+ * subset); SEMI / ANTI the left rows with / without a match. */
 xlog_hip_status xlog_hip_hash_join_with_index(xlog_hip_ctx *ctx, const xlog_hip_rel *left, const xlog_hip_rel *right,
-                                              uint32_t left_key, uint32_t right_key, int join_type,
-                                              const xlog_hip_join_index *index, uint64_t max_output,
+                                              const uint32_t *left_keys, const uint32_t *right_keys, uint32_t n_keys,
+                                              int join_type, const xlog_hip_join_index *index, uint64_t max_output,
                                               xlog_hip_rel **out);
 void xlog_hip_join_index_free(xlog_hip_join_index *index);
 /* Nested-loop inner join on one key column, left ++ right columns, rows in
@@ -237,12 +253,13 @@ xlog_hip_status xlog_hip_is_sorted(xlog_hip_ctx *ctx, const xlog_hip_rel *rel, u
 xlog_hip_status xlog_hip_exclusive_scan_u32(xlog_hip_ctx *ctx, uint32_t *dev, uint64_t n, uint64_t *total);
 /* xlog_hip_exclusive_scan_u32 without any device allocation.  No counterpart
  * in the reference: it is for callers that cannot allocate device memory
- * (code under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc).  Its scratch (ticket, total, look-back status) lives in a
- * fixed device array of 2 MiB per GPU, held from library load to process
- * exit; n above 2^32 is CAPACITY_OVERFLOW.  All calls on one GPU share that
- * array: calls that overlap on one GPU (two contexts on two threads) race.
- * Synchronises the context stream to read *total. */
+ * (tight serving loops, harnesses that forbid hipMalloc).  Its scratch
+ * (ticket, total, look-back status) lives in a fixed device array of 2 MiB
+ * per GPU, held from library load to process exit; n above 2^32 is
+ * CAPACITY_OVERFLOW.  All calls on one GPU share that array: calls that
+ * overlap on one GPU (two contexts on two threads) race.  It synchronises
+ * the context stream to read *total, so it cannot be recorded into a HIP
+ * graph (stream capture forbids the synchronisation). */
 xlog_hip_status xlog_hip_exclusive_scan_u32_noalloc(xlog_hip_ctx *ctx, uint32_t *dev, uint64_t n, uint64_t *total);
 /* Column roles of one factorized delta step (reference FjDeltaCols,
  * provider/fj_delta.rs:50-84); each pair is {0, 1} in some order. */
@@ -302,6 +319,9 @@ typedef struct {
                                  limit (relational.rs:4550-4555). */
     uint64_t host_waits;      /* out: times the host waited for the device during the fixpoint
                                  (each count or size read-back is one wait) */
+    uint64_t delta_count;     /* out: entries of delta_sizes written (the seed and each completed iteration);
+                                 after a failure inside an iteration, iterations counts that iteration
+                                 and delta_count - 1 the ones completed before it */
 } xlog_hip_fixpoint_stats;
 
 /* AUTO takes the bitmap route when every rule body is a path, there are at

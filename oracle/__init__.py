@@ -17,6 +17,8 @@ Pinning (what checks each function beyond retyping it):
       K_{n,n} closed forms, the reference TC and points-to KATs, and the
       independent naive fixpoint for every other plan.
   or_bfs_tc : brute-force Floyd-Warshall style reachability on tiny graphs.
+  or_chain2_counts : Python sets and lists over the joined rows on small
+      random relations (tests/test_oracle.py).
 """
 from __future__ import annotations
 
@@ -58,6 +60,8 @@ def _load() -> C.CDLL:
     lib.or_join_project.restype = C.c_int64
     lib.or_join_count.argtypes = [P, U64, P, U64, I, I]
     lib.or_join_count.restype = U64
+    lib.or_chain2_counts.argtypes = [P, U64, P, U64, P, U64, P]
+    lib.or_chain2_counts.restype = I
     lib.or_free.argtypes = [P]
     lib.or_free.restype = None
     lib.or_seminaive.argtypes = [P, I, P, P, U64, P, P, C.POINTER(U64), P, U64]
@@ -136,6 +140,19 @@ def join_project(l, r, lk: int, rk: int, oc0: int, oc1: int) -> np.ndarray:
     buf = np.ctypeslib.as_array(C.cast(outp, C.POINTER(C.c_uint64)), shape=(n,)).copy()
     _lib.or_free(outp)
     return buf
+
+
+def chain2_counts(l, a, b) -> dict:
+    """Row counts of head(v, o) :- l(v, w), a(w, p), b(p, o) evaluated left-deep
+    (inputs sorted unique packed rows, ids below 2^28): the first join's bag,
+    its distinct (v, p) pairs, and the second join's bag over those pairs and
+    over the first join's bag."""
+    l, a, b = _u64(l), _u64(a), _u64(b)
+    out = np.zeros(4, np.uint64)
+    rc = _lib.or_chain2_counts(_p(l), len(l), _p(a), len(a), _p(b), len(b), out.ctypes.data)
+    if rc != 0:
+        raise ValueError(f"or_chain2_counts failed ({rc})")
+    return {"bag1": int(out[0]), "set1": int(out[1]), "bag2_over_set1": int(out[2]), "bag2_over_bag1": int(out[3])}
 
 
 def join_count(l, r, lk: int, rk: int) -> int:

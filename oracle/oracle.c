@@ -353,6 +353,54 @@ uint64_t or_join_count(const uint64_t *l, uint64_t nl, const uint64_t *r, uint64
 }
 void or_free(void *p) { free(p); }
 
+/* exported: the row counts of the left-deep two-join body
+ *   head(v, o) :- l(v, w), a(w, p), b(p, o)
+ * evaluated as (l join a on w) projected to (v, p), then joined with b on p
+ * (crates/xlog-logic/src/lower.rs:1795-1850; join output left ++ right,
+ * relational.rs:4417-4625).  l, a, b are sorted unique packed (c0 << 32) | c1
+ * rows; every id must be below 2^28 (-1 otherwise).  out[0] = the first join's
+ * bag, out[1] = its distinct (v, p) pairs, out[2] = the second join's bag over
+ * those distinct pairs, out[3] = the second join's bag over the first join's
+ * bag.  Counting only: a degree array per relation and, per v (l is sorted by
+ * v), a marker array of the p values already seen. */
+int or_chain2_counts(const uint64_t *l, uint64_t nl, const uint64_t *a, uint64_t na, const uint64_t *b, uint64_t nb,
+                     uint64_t *out) {
+    uint32_t mx = 0;
+    for (uint64_t i = 0; i < nl; ++i) { mx = mx > (uint32_t)(l[i] >> 32) ? mx : (uint32_t)(l[i] >> 32);
+                                        mx = mx > (uint32_t)l[i] ? mx : (uint32_t)l[i]; }
+    for (uint64_t i = 0; i < na; ++i) { mx = mx > (uint32_t)(a[i] >> 32) ? mx : (uint32_t)(a[i] >> 32);
+                                        mx = mx > (uint32_t)a[i] ? mx : (uint32_t)a[i]; }
+    for (uint64_t i = 0; i < nb; ++i) { mx = mx > (uint32_t)(b[i] >> 32) ? mx : (uint32_t)(b[i] >> 32);
+                                        mx = mx > (uint32_t)b[i] ? mx : (uint32_t)b[i]; }
+    out[0] = out[1] = out[2] = out[3] = 0;
+    if (mx >= (1u << 28)) return -1;
+    const uint64_t D = (uint64_t)mx + 1;
+    uint64_t *a_start = (uint64_t *)calloc(D + 1, sizeof(uint64_t));  /* CSR of a over w */
+    uint64_t *deg_b = (uint64_t *)calloc(D, sizeof(uint64_t));
+    uint64_t *seen = (uint64_t *)calloc(D, sizeof(uint64_t));         /* 1 + the last v that saw p */
+    if (!a_start || !deg_b || !seen) { free(a_start); free(deg_b); free(seen); return -2; }
+    for (uint64_t i = 0; i < na; ++i) a_start[(a[i] >> 32) + 1]++;
+    for (uint64_t w = 0; w < D; ++w) a_start[w + 1] += a_start[w];
+    for (uint64_t i = 0; i < nb; ++i) deg_b[b[i] >> 32]++;
+    for (uint64_t i = 0; i < nl; ++i) {
+        const uint64_t v = l[i] >> 32, w = (uint32_t)l[i];
+        for (uint64_t j = a_start[w]; j < a_start[w + 1]; ++j) {
+            const uint32_t pv = (uint32_t)a[j];
+            out[0] += 1;
+            out[3] += deg_b[pv];
+            if (seen[pv] != v + 1) {
+                seen[pv] = v + 1;
+                out[1] += 1;
+                out[2] += deg_b[pv];
+            }
+        }
+    }
+    free(a_start);
+    free(deg_b);
+    free(seen);
+    return 0;
+}
+
 /* ------------------------------------------------------------------------ */
 /* program plans: rules over arity-2 predicates with chain bodies            */
 /* ------------------------------------------------------------------------ */

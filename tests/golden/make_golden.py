@@ -11,6 +11,10 @@ c1_closure.npz (the full config-1 closure as a packed 1000x1000 bit matrix).
 (tcs, tcs_crit: G(2^20, m) digraphs, beyond any dense bit-matrix domain).
 --c5 computes the larger Andersen instances (10,000, 20,000 and 40,000 variables; the
 naive fixpoint cross-checks the first two, the third is past its time budget).
+--c5-stated computes, for C5 at its stated 500,000 variables / 2,000,000 facts, the
+row counts of the first recursive iteration's joins in the order the join route
+evaluates them (the seed delta, rule 2's join, and rule 3's two-join body with the
+delta in its first pointsTo atom), which decide where a join-row limit trips.
 """
 from __future__ import annotations
 
@@ -82,11 +86,31 @@ def c5_entry(nv, nf, check_naive=True):
             "digest": oracle.fnv1a64(outs[4]), "checked_against_naive": bool(check_naive)}
 
 
+def c5_stated_entry():
+    """C5 at its stated size, first recursive iteration.  After the seed, pointsTo = delta = addressOf
+    (rule 1; the other rules read pointsTo, still empty).  The join route then evaluates, in rule order,
+    rule 2 (assign join delta on W) and rule 3 with the delta in atom 1: load(V,W) join delta(W,P) projected
+    to (V,P), then joined with pointsTo(P,O) (= addressOf) on P.  The library's join step keeps a first join
+    of more than 2^30 - 1 rows as a sorted set (chunked sort + dedup), so the second join's bag is counted
+    over the distinct (V,P) pairs; the reference keeps the bag (bag2_over_bag1)."""
+    cfg = datagen.C5
+    f = datagen.andersen(cfg["n_vars"], cfg["n_facts"], cfg["alpha"], datagen.seed_for(5))
+    assign, addr, load = (oracle.sort_dedup(pack(*f[k])) for k in ("assign", "addressOf", "load"))
+    r2 = oracle.chain2_counts(assign, addr, np.zeros(0, np.uint64))
+    r3 = oracle.chain2_counts(load, addr, addr)
+    return {"n_vars": cfg["n_vars"], "n_facts": cfg["n_facts"], "alpha": cfg["alpha"],
+            "seed_delta": int(len(addr)), "rule2_bag": r2["bag1"], "rule2_tuples": r2["set1"],
+            "rule3_first_join_bag": r3["bag1"], "rule3_first_join_set": r3["set1"],
+            "rule3_second_join_bag_over_set": r3["bag2_over_set1"],
+            "rule3_second_join_bag_over_bag": r3["bag2_over_bag1"]}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--full", action="store_true")
     ap.add_argument("--sparse", action="store_true")
     ap.add_argument("--c5", action="store_true")
+    ap.add_argument("--c5-stated", action="store_true")
     ap.add_argument("--threads", type=int, default=1)
     args = ap.parse_args()
     oracle.set_threads(args.threads)
@@ -147,6 +171,10 @@ def main():
             fx[f"c5_{nv}_{4 * nv}"] = c5_entry(nv, 4 * nv, check_naive=nv <= 20_000)
             print(f"c5 {nv} {time.time() - t:.0f}s", flush=True)
             path.write_text(json.dumps(fx, indent=1) + "\n")
+    if args.c5_stated:
+        t = time.time()
+        fx["c5_stated"] = c5_stated_entry()
+        print(f"c5 stated {time.time() - t:.0f}s {fx['c5_stated']}", flush=True)
     if args.full:
         t = time.time()
         src, dst = datagen.random_digraph(32768, 3 * 32768, datagen.seed_for(4))

@@ -118,6 +118,125 @@ def test_join_index_max_output_and_errors(provider):
     assert p.hash_join_v2_with_index(empty_left, right, [0], [0], JOIN_INNER, ix).num_rows() == 0
 
 
+def _brute_keys(l_rows, r_rows, lk, rk, kind=JOIN_INNER):
+    """Join on key lists: INNER rows left ++ right in left-row-major, right-row order;
+    SEMI / ANTI the left rows with / without a match, input order."""
+    match = lambda a, b: all(a[x] == b[y] for x, y in zip(lk, rk))
+    if kind == JOIN_INNER:
+        return [tuple(a) + tuple(b) for a in l_rows for b in r_rows if match(a, b)]
+    want = kind == JOIN_SEMI
+    return [tuple(a) for a in l_rows if any(match(a, b) for b in r_rows) == want]
+
+
+def _rel(p, rows, arity):
+    return p.create_buffer_from_u32_columns([[r[c] for r in rows] for c in range(arity)])
+
+
+def test_join_index_reference_key_list_shapes(provider):
+    """The reference builds indexes over five key columns and over two
+    (crates/xlog-cuda/tests/pack_keys_gpu.rs:12-38, 53-65); here the index is
+    also probed and checked against brute force."""
+    p = provider
+    five = [(1, 4, 7, 10, 13), (2, 5, 8, 11, 14), (3, 6, 9, 12, 15)]
+    r5 = _rel(p, five, 5)
+    ix5 = p.build_join_index_v2(r5, [0, 1, 2, 3, 4])
+    probe = [(2, 5, 8, 11, 14), (3, 6, 9, 12, 0), (1, 4, 7, 10, 13), (2, 5, 8, 11, 14), (1, 4, 7, 10, 14)]
+    l5 = _rel(p, probe, 5)
+    keys = [0, 1, 2, 3, 4]
+    for kind in (JOIN_SEMI, JOIN_ANTI):
+        got = p.download_rows(p.hash_join_v2_with_index(l5, r5, keys, keys, kind, ix5))
+        assert got == _brute_keys(probe, five, keys, keys, kind), kind
+    # five key columns with the left's columns permuted, INNER (output arity 3 + 5)
+    l3 = [(10, 7, 4), (11, 8, 5), (10, 7, 5), (12, 9, 6)]
+    ix_perm = p.build_join_index_v2(r5, [3, 2, 1])
+    got = p.download_rows(p.hash_join_v2_with_index(_rel(p, l3, 3), r5, [0, 1, 2], [3, 2, 1], JOIN_INNER, ix_perm))
+    assert got == _brute_keys(l3, five, [0, 1, 2], [3, 2, 1]) == [(10, 7, 4) + five[0], (11, 8, 5) + five[1],
+                                                               (12, 9, 6) + five[2]]
+    two = [(1, 10), (2, 20), (3, 30), (4, 40)]
+    r2 = _rel(p, two, 2)
+    ix2 = p.build_join_index_v2(r2, [0, 1])
+    left = [(1, 10, 7), (1, 20, 8), (4, 40, 9), (3, 30, 1), (4, 40, 2)]
+    got = p.download_rows(p.hash_join_v2_with_index(_rel(p, left, 3), r2, [0, 1], [0, 1], JOIN_INNER, ix2))
+    assert got == _brute_keys(left, two, [0, 1], [0, 1])
+    # the index remembers its key list: another list or another relation is refused
+    with pytest.raises(XlogError) as ex:
+        p.hash_join_v2_with_index(_rel(p, left, 3), r2, [1, 0], [1, 0], JOIN_INNER, ix2)
+    assert ex.value.status == 1
+    with pytest.raises(XlogError) as ex:
+        p.hash_join_v2_with_index(_rel(p, left, 3), r5, [0, 1], [0, 1], JOIN_INNER, ix2)
+    assert ex.value.status == 1
+
+
+@pytest.mark.parametrize("seed", range(5))
+@pytest.mark.parametrize("la,ra,nk", [(3, 3, 2), (2, 2, 2), (4, 3, 3), (2, 4, 2), (4, 4, 4), (1, 5, 1), (3, 2, 1)])
+def test_join_index_key_lists_reused_vs_brute_force(provider, seed, la, ra, nk):
+    """One index over a key list, probed by three left relations with every
+    join type, against brute force (exact row order) and against the
+    one-shot keyed join; max_output keeps a prefix of that order."""
+    p = provider
+    rng = np.random.default_rng(1000 * seed + 100 * la + 10 * ra + nk)
+    rk = [int(x) for x in rng.permutation(ra)[:nk]]
+    vals = int(rng.integers(2, 7))
+    nr = int(rng.integers(1, 250))
+    r_rows = [tuple(int(v) for v in rng.integers(0, vals, ra)) for _ in range(nr)]
+    if seed == 0:  # all-ones key values
+        r_rows = [tuple(0xFFFFFFFF if v == 0 else v for v in row) for row in r_rows]
+    right = _rel(p, r_rows, ra)
+    ix = p.build_join_index_v2(right, rk)
+    for probe in range(3):
+        lk = [int(x) for x in rng.permutation(la)[:nk]]
+        nl = int(rng.integers(0, 250))
+        l_rows = [tuple(int(v) for v in rng.integers(0, vals, la)) for _ in range(nl)]
+        if seed == 0:
+            l_rows = [tuple(0xFFFFFFFF if v == 0 else v for v in row) for row in l_rows]
+        _note(f"join index key list la={la} ra={ra} lk={lk} rk={rk} nl={nl} nr={nr} probe={probe}")
+        left = _rel(p, l_rows, la)
+        for kind in (JOIN_INNER, JOIN_SEMI, JOIN_ANTI):
+            if kind == JOIN_INNER and la + ra > 8:
+                continue
+            exp = _brute_keys(l_rows, r_rows, lk, rk, kind)
+            got = p.hash_join_v2_with_index(left, right, lk, rk, kind, ix)
+            assert got.arity == (la + ra if kind == JOIN_INNER else la)
+            assert p.download_rows(got) == exp, (kind, probe)
+            assert p.download_rows(p.hash_join_v2(left, right, lk, rk, kind)) == exp, (kind, probe)
+            if kind == JOIN_INNER and exp:
+                cap = int(rng.integers(1, len(exp) + 1))
+                t = p.hash_join_v2_with_index(left, right, lk, rk, kind, ix, max_output=cap)
+                assert p.download_rows(t) == exp[:cap]
+    ix.free()
+
+
+def test_join_index_larger_random_key_lists(provider):
+    """Two and three key columns over 200,000-row relations, index reused, against numpy."""
+    p = provider
+    rng = np.random.default_rng(42)
+    n = 200_000
+    r_cols = [rng.integers(0, 60, n, dtype=np.uint32), rng.integers(0, 2000, n, dtype=np.uint32),
+              rng.integers(0, 1 << 32, n, dtype=np.uint64).astype(np.uint32)]
+    right = p.create_buffer_from_u32_columns(r_cols)
+    for rk in ([0, 1], [1, 0, 2]):
+        ix = p.build_join_index_v2(right, rk)
+        for probe in range(2):
+            m = 50_000
+            pick = rng.integers(0, n, m)
+            l_cols = [r_cols[rk[t]][pick].copy() for t in range(len(rk))]
+            l_cols[0][: m // 3] = rng.integers(0, 70, m // 3, dtype=np.uint32)  # some keys absent
+            left = p.create_buffer_from_u32_columns(l_cols)
+            lk = list(range(len(rk)))
+            semi = p.download_rows(p.hash_join_v2_with_index(left, right, lk, rk, JOIN_SEMI, ix))
+            rkeys = set(zip(*[r_cols[c].tolist() for c in rk]))
+            lrows = list(zip(*[c.tolist() for c in l_cols]))
+            assert semi == [r for r in lrows if r in rkeys]
+            anti = p.download_rows(p.hash_join_v2_with_index(left, right, lk, rk, JOIN_ANTI, ix))
+            assert anti == [r for r in lrows if r not in rkeys]
+            inner = p.hash_join_v2_with_index(left, right, lk, rk, JOIN_INNER, ix)
+            cnt = Counter(zip(*[r_cols[c].tolist() for c in rk]))
+            assert inner.num_rows() == sum(cnt[r] for r in lrows)
+            assert Counter(p.download_rows(inner)) == Counter(p.download_rows(
+                p.hash_join_v2(left, right, lk, rk, JOIN_INNER)))
+        ix.free()
+
+
 # ---- nested-loop join (relational.rs:3041-3255) ------------------------------
 @pytest.mark.parametrize("la,ra", [(1, 1), (1, 2), (2, 1), (2, 2)])
 def test_nested_loop_join_brute_force(provider, la, ra):

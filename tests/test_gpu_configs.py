@@ -11,10 +11,11 @@ import numpy as np
 import pytest
 
 import oracle
-from xlog_amd import ROUTE_BITMAP, ROUTE_HASH, ROUTE_JOIN, andersen_plan, datagen, pack, tc_plan
+from xlog_amd import ROUTE_BITMAP, ROUTE_HASH, ROUTE_JOIN, XlogError, andersen_plan, datagen, pack, tc_plan
 
 pytestmark = pytest.mark.gpu
 FX = json.loads((Path(__file__).parent / "golden" / "fixtures.json").read_text())
+CAPACITY_OVERFLOW = 3
 
 
 def _note(msg):
@@ -118,6 +119,44 @@ def test_c5_scaled_andersen_fixture(provider, fixture, route):
     assert st["iterations"] == e["iterations"]
     assert st["delta_sizes"] == e["delta_sizes"]
     assert p.digest(outs[4]) == e["digest"]
+
+
+def test_c5_stated_size_fails_closed_like_the_reference(provider):
+    """C5 at its stated 500,000 variables / 2,000,000 facts with the reference's u32
+    join-row limit.  The reference fails closed there: the 3-atom rules' Free Join
+    declines on its u32 work cap (crates/xlog-cuda/src/provider/fj.rs:557-561,
+    wcoj_dispatch.rs:221-250) and the binary path stops at "Join produced ... rows
+    which exceeds the u32 index limit" (relational.rs:4550-4555).  Here the join
+    route stops at the same limit, in the first recursive iteration, on rule 3's
+    second join, before materialising it; the row count it reports, the seed delta
+    and the earlier joins' sizes are pinned by the oracle's independent count
+    (tests/golden/make_golden.py --c5-stated)."""
+    fx = FX["c5_stated"]
+    limit = (1 << 32) - 1
+    chunk = (1 << 30) - 1  # the join step keeps a larger first join as a sorted set
+    bag = fx["rule3_second_join_bag_over_set"] if fx["rule3_first_join_bag"] > chunk else \
+        fx["rule3_second_join_bag_over_bag"]
+    # the joins before it fit the limit, this one does not (with either reading of its first join)
+    assert fx["rule2_bag"] <= limit and fx["rule3_first_join_bag"] <= limit < bag
+    assert fx["rule3_second_join_bag_over_bag"] > limit
+    _note("c5 stated: generating inputs")
+    f = datagen.andersen(fx["n_vars"], fx["n_facts"], fx["alpha"], datagen.seed_for(5))
+    p = provider
+    rels = [p.create_buffer_from_u32_columns(list(f[k])) for k in ("assign", "addressOf", "load", "store")]
+    _note("c5 stated: fixpoint with the u32 join-row limit")
+    with pytest.raises(XlogError) as ex:
+        p.fixpoint(andersen_plan(), rels + [None], max_join_rows=limit)
+    e = ex.value
+    assert e.status == CAPACITY_OVERFLOW
+    assert f"Join produced {bag} rows which exceeds the row limit {limit}" in e.message
+    assert e.stats["route"] == ROUTE_JOIN
+    assert e.stats["iterations"] == 1  # failed inside the first recursive iteration
+    assert e.stats["delta_sizes"] == [fx["seed_delta"]]
+    # rule 2 of that iteration alone (assign join addressOf), deduplicated: a lower bound of |pointsTo|
+    _note("c5 stated: rule 2 of the first iteration")
+    r2 = p.join_project_dedup(rels[0], rels[1], 1, 0, [0, 3])
+    assert r2.num_rows() == fx["rule2_tuples"]
+    assert r2.num_rows() > fx["seed_delta"]
 
 
 def _fnv_inputs(*arrays):

@@ -102,6 +102,45 @@ def test_hash_route_all_ones_ids(provider):
     assert (st["iterations"], st["delta_sizes"]) == (st_j["iterations"], st_j["delta_sizes"])
 
 
+@pytest.mark.parametrize("plan_name", ["tc", "nonlinear_tc"])
+def test_hash_route_all_ones_in_initial_head(provider, plan_name):
+    """The starting IDB relation holds the all-ones tuple (M, M), which the table
+    keeps in its flag: it must count as present from the start (never re-derived
+    as new, never a duplicate row of an indexed relation), on the linear plan and
+    on the non-linear one whose IDB relation is read through an index."""
+    import chain_plans as cp
+    p = provider
+    M = 0xFFFFFFFF
+    edges = [(M, 5), (5, M), (M, 0), (0, M - 1), (M - 1, 7), (7, 7), (12, M), (9, 12)]
+    head = [(M, M), (3, 9), (M, 0)]
+    plan = tc_plan() if plan_name == "tc" else cp.nonlinear_tc_plan()
+    e = pack(np.array([a for a, _ in edges], np.uint32), np.array([b for _, b in edges], np.uint32))
+    h = pack(np.array([a for a, _ in head], np.uint32), np.array([b for _, b in head], np.uint32))
+    outs_o, it_o, deltas_o = oracle.seminaive(plan, [e, h])
+    assert M * (2 ** 32) + M in set(int(x) for x in outs_o[1])
+    for route in (ROUTE_HASH, ROUTE_JOIN):
+        _note(f"all-ones initial head plan={plan_name} route={route}")
+        dev = [p.create_buffer_from_packed(e), p.create_buffer_from_packed(h)]
+        outs, st = p.fixpoint(plan, dev, route=route)
+        assert st["route"] == route
+        assert np.array_equal(p.download_packed(outs[1]), outs_o[1]), route
+        assert outs[1].is_canonical()
+        assert (st["iterations"], st["delta_sizes"]) == (it_o, deltas_o), route
+
+
+def test_fj_delta_sparse_all_ones_in_full(provider):
+    """The one-step sparse operator over a full relation holding (M, M): that
+    tuple is not novel."""
+    p = provider
+    M = 0xFFFFFFFF
+    delta = p.create_buffer_from_u32_columns([np.array([M, 4], np.uint32), np.array([5, 5], np.uint32)])
+    edge = p.create_buffer_from_u32_columns([np.array([5, 5], np.uint32), np.array([M, 6], np.uint32)])
+    full = p.create_buffer_from_u32_columns([np.array([M, 4], np.uint32), np.array([M, 6], np.uint32)])
+    out = p.fj_delta_sparse_novel_u32_recorded(delta, edge, full, FJ_DELTA_CANONICAL)
+    # candidates (M, M), (M, 6), (4, M), (4, 6); (M, M) and (4, 6) are in full
+    assert p.download_rows(out) == [(4, M), (M, 6)]
+
+
 def test_hash_route_empty_and_unsupported(provider):
     p = provider
     out, st = _tc(p, [], [], ROUTE_HASH)

@@ -170,6 +170,41 @@ def test_union_diff_random(provider, na, nb):
     assert np.array_equal(p.download_packed(p.union_many_gpu(parts + [ra])), oracle.union_sorted(ua, ub))
 
 
+def test_diff_window_pass_regions(provider):
+    """A set difference of 2,200,007 rows: 256 tiles of 8192 rows or more, so every
+    tile's window of B comes from the separate window pass (k_diff_windows).  Three
+    regions of keys give the three ways a tile reads its window: A every 8th key
+    under a dense B (windows of about 65,536 keys, within 16 per row: streamed
+    through LDS in eight 8192-key chunks), A every 32nd key under a dense B
+    (windows of about 262,144 keys, above 16 per row: searched in HBM), and A
+    dense over a sparse B (one chunk); half of the A keys of each region are in B."""
+    p = provider
+    rng = _rng(2200007)
+    n1, n2 = 1_000_003, 600_001
+    n3 = 2_200_007 - n1 - n2
+    base2, base3 = 1 << 26, 1 << 28
+    a1 = np.arange(n1, dtype=np.uint64) * 8
+    b1 = np.arange(n1 * 8, dtype=np.uint64)[rng.random(n1 * 8) < 0.9]
+    a2 = base2 + np.arange(n2, dtype=np.uint64) * 32
+    b2 = base2 + np.arange(n2 * 32, dtype=np.uint64)[rng.random(n2 * 32) < 0.9]
+    a3 = base3 + np.arange(n3, dtype=np.uint64)
+    b3 = base3 + np.sort(rng.choice(n3, n3 // 8, replace=False)).astype(np.uint64)
+    a = np.concatenate([a1, a2, a3])
+    b = np.concatenate([b1, b2, b3])
+    assert len(a) == 2_200_007 and len(a) % 8192
+    ra = p.create_buffer_from_packed(rng.permutation(a))
+    rb = p.create_buffer_from_packed(b)
+    ua, ub = oracle.sort_dedup(a), oracle.sort_dedup(b)
+    exp = oracle.diff_sorted(ua, ub)
+    assert 0 < len(exp) < len(ua)
+    _note(f"diff window pass: |A| {len(ua)} |B| {len(ub)} |A minus B| {len(exp)}")
+    assert np.array_equal(p.download_packed(p.diff_gpu(ra, rb)), exp)
+    # canonical inputs (no re-sort), and the union of the same sets
+    ca, cb = p.dedup_full_row(ra), p.dedup_full_row(rb)
+    assert np.array_equal(p.download_packed(p.diff_gpu(ca, cb)), exp)
+    assert np.array_equal(p.download_packed(p.union_gpu(ca, cb)), oracle.union_sorted(ua, ub))
+
+
 @pytest.mark.parametrize("nl,nr,keys", [(0, 10, 5), (10, 0, 5), (1, 1, 1), (5000, 3000, 100), (200000, 100000, 5000),
                                         (100000, 1000, 3)])
 def test_join_project_random(provider, nl, nr, keys):

@@ -95,6 +95,28 @@ def test_join_vs_nested_loop(seed, lk, rk):
     assert oracle.join_count(l, r, lk, rk) == int((cl * cr).sum())
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_chain2_counts_vs_python(seed):
+    """The two-join body head(v, o) :- l(v, w), a(w, p), b(p, o) counted by the
+    oracle equals the sizes of the joined lists and sets built in Python."""
+    rng = np.random.default_rng(900 + seed)
+    n = int(rng.integers(3, 12))
+
+    def rel(m):
+        return oracle.sort_dedup(pack(rng.integers(0, n, m), rng.integers(0, n, m)))
+    l, a, b = rel(int(rng.integers(0, 60))), rel(int(rng.integers(0, 60))), rel(int(rng.integers(0, 60)))
+    L, A, B = ([(int(x >> 32), int(x & 0xFFFFFFFF)) for x in r] for r in (l, a, b))
+    bag1 = [(v, p) for v, w in L for w2, p in A if w == w2]
+    set1 = set(bag1)
+    got = oracle.chain2_counts(l, a, b)
+    assert got["bag1"] == len(bag1)
+    assert got["set1"] == len(set1)
+    assert got["bag2_over_set1"] == len([1 for v, p in set1 for p2, o in B if p == p2])
+    assert got["bag2_over_bag1"] == len([1 for v, p in bag1 for p2, o in B if p == p2])
+    # the first join's bag is also the plain join count
+    assert got["bag1"] == oracle.join_count(l, a, 1, 0)
+
+
 def test_join_kats():
     for kat in KATS["join_inner_key0"]:
         l, r = rows_to_keys(kat["left"]), rows_to_keys(kat["right"])

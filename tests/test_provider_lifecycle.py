@@ -37,7 +37,7 @@ def test_handles_collected_with_their_provider(monkeypatch):
     monkeypatch.setattr(pv, "_lib", fake)
     p = pv.HipKernelProvider(0)
     rels = [p._rel(C.c_void_p(0x2000 + i)) for i in range(3)]
-    ix = pv.JoinIndex(p, C.c_void_p(0x3000), 0)
+    ix = pv.JoinIndex(p, C.c_void_p(0x3000), [0])
     p._live.add(ix)
     p.cycle = (rels, ix)  # provider -> handles -> provider: one garbage batch
     del rels, ix, p

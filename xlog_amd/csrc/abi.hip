@@ -53,6 +53,11 @@ size_t Pool::round_up(size_t b) {
 }
 void *Pool::alloc(size_t bytes) {
     size_t sz = round_up(bytes);
+    // the budget bounds the live bytes, as the reference's GpuMemoryManager
+    // (crates/xlog-cuda/src/memory.rs:756-770; MemoryBudget::with_limit aborts on exceed)
+    if (budget_ && in_use_ + sz > budget_)
+        throw Error{XLOG_HIP_OOM, "GPU memory budget exceeded: requested " + std::to_string(sz) + " bytes with " +
+                                      std::to_string(in_use_) + " in use, budget " + std::to_string(budget_)};
     auto it = free_.find(sz);
     void *p = nullptr;
     if (it != free_.end()) {
@@ -60,6 +65,7 @@ void *Pool::alloc(size_t bytes) {
         free_.erase(it);
         cached_ -= sz;
     } else {
+        if (budget_ && in_use_ + cached_ + sz > budget_) trim();  // the footprint stays within the budget
         hipError_t e = hipMalloc(&p, sz);
         if (e != hipSuccess) {
             (void)hipGetLastError();
@@ -614,12 +620,25 @@ struct JoinIndex {
     Buf<uint32_t> payload;
     uint64_t n = 0;
 };
+// The build side of a join on a key list, folded into dense ids (see
+// op_join_keys): one sorted unique u64 key array per folding step, in which
+// the probe side's keys are ranked, and the run index over (id << 32) | row.
+struct KeyFold {
+    std::vector<Buf<uint64_t>> dict;
+    std::vector<uint64_t> dict_n;
+    JoinIndex J;
+};
 }  // namespace xh
-// Reusable join index handle of the C ABI (one build, many probes).
+// Reusable join index handle of the C ABI (one build, many probes): one key
+// column of a relation of at most two columns is indexed directly (J, runs of
+// that column's values, payload = the other column); any other key list is
+// folded (F).
 struct xlog_hip_join_index {
     xh::Ctx *ctx = nullptr;
     xh::JoinIndex J;
-    uint32_t arity = 0, key = 0;
+    std::unique_ptr<xh::KeyFold> F;
+    uint32_t arity = 0;
+    std::vector<uint32_t> keys;
     uint64_t rows = 0;
 };
 namespace xh {
@@ -876,10 +895,169 @@ __global__ void k_gather_pairs(RelView L, RelView R, const uint64_t *__restrict_
         put_row(out, arity, v, r);
     }
 }
+// output row r = left row (w[r] >> 32) ++ the right row rebuilt from the
+// left row's key value and the index payload (low word): the direct index
+// over one key column of a right relation of at most two columns
+__global__ void k_gather_left_payload(RelView L, int lk, int r_arity, int rk, const uint64_t *__restrict__ w,
+                                      uint64_t n, RelOut out) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    const int arity = L.arity + r_arity;
+    for (uint64_t r = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; r < n; r += stride) {
+        const uint64_t x = w[r];
+        const uint64_t i = x >> 32;
+        uint32_t v[MAX_ARITY];
+        for (int c = 0; c < L.arity; ++c) v[c] = col_value(L, c, i);
+        const uint32_t key = col_value(L, lk, i);
+        if (r_arity == 1) {
+            v[L.arity] = key;
+        } else {
+            v[L.arity + rk] = key;
+            v[L.arity + 1 - rk] = (uint32_t)x;
+        }
+        put_row(out, arity, v, r);
+    }
+}
+// (column c << 32) | row index
+__global__ void k_key_rows(RelView in, int c, uint64_t n, uint64_t *__restrict__ out) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        out[i] = ((uint64_t)col_value(in, c, i) << 32) | (uint32_t)i;
+}
 }  // namespace
 
-static xlog_hip_rel *op_join_keys(Ctx *ctx, const xlog_hip_rel *l, const xlog_hip_rel *r, const std::vector<int> &lk,
-                                  const std::vector<int> &rk, int type) {
+// The folding steps of a key list of nk columns: step 0 keys by columns
+// (c[0], c[1]) as one u64 (c[0] alone when nk == 1), step s >= 1 by
+// (id of step s - 1, c[s + 1]).
+static size_t fold_steps(size_t nk) { return nk >= 2 ? nk - 1 : 1; }
+static void fold_cols(const std::vector<int> &c, size_t step, int *c0, int *c1) {
+    if (step == 0) {
+        *c0 = c[0];
+        *c1 = c.size() >= 2 ? c[1] : -1;
+    } else {
+        *c0 = -1;
+        *c1 = c[step + 1];
+    }
+}
+
+// The build side's fold over its key columns rk: every step's dictionary
+// (sorted unique keys) and, with runs, the run index over (id << 32) | row
+// (a stable sort, so a run lists its rows in input order).
+static void fold_build(Ctx *ctx, const xlog_hip_rel *r, const std::vector<int> &rk, KeyFold &F, bool runs) {
+    const uint64_t nr = r->rows;
+    Buf<uint32_t> rid(ctx, nr);
+    Buf<uint64_t> rkey(ctx, nr);
+    for (size_t st = 0; st < fold_steps(rk.size()); ++st) {
+        int c0, c1;
+        fold_cols(rk, st, &c0, &c1);
+        LAUNCH_1D(k_fold_key, nr, view_of(r), st == 0 ? nullptr : rid.p, c0, c1, nr, rkey.p);
+        uint64_t *sorted = sort_keys(ctx, rkey.p, nr, false);
+        uint64_t *u = nullptr;
+        uint64_t nu = 0;
+        try {
+            nu = unique_keys(ctx, sorted, nr, &u);
+        } catch (...) {
+            ctx->free(sorted);
+            throw;
+        }
+        ctx->free(sorted);
+        Buf<uint64_t> d;
+        d.ctx = ctx;
+        d.p = u;
+        d.n = nu;
+        F.dict.push_back(std::move(d));
+        F.dict_n.push_back(nu);
+        LAUNCH_1D(k_rank_ids, nr, rkey.p, nr, u, nu, rid.p);
+    }
+    if (!runs) return;
+    Buf<uint64_t> rp(ctx, nr);
+    LAUNCH_1D(k_id_rows, nr, rid.p, nr, rp.p);
+    rid = Buf<uint32_t>();
+    rkey = Buf<uint64_t>();
+    build_join_index(ctx, rp.p, nr, 2, 0, false, F.J);
+}
+
+// The probe side's ids in the build side's dictionaries (KEY_NONE for a key
+// no build row has: it stays KEY_NONE through later steps, since every
+// dictionary key of a later step has a build id, below KEY_NONE, in its high
+// word).
+static void fold_probe(Ctx *ctx, const xlog_hip_rel *l, const std::vector<int> &lk, const KeyFold &F,
+                       Buf<uint32_t> &lid, Buf<uint64_t> &lkey) {
+    const uint64_t nl = l->rows;
+    for (size_t st = 0; st < fold_steps(lk.size()); ++st) {
+        int c0, c1;
+        fold_cols(lk, st, &c0, &c1);
+        LAUNCH_1D(k_fold_key, nl, view_of(l), st == 0 ? nullptr : lid.p, c0, c1, nl, lkey.p);
+        LAUNCH_1D(k_rank_ids, nl, lkey.p, nl, F.dict[st].p, F.dict_n[st], lid.p);
+    }
+}
+
+// The join of non-empty inputs against the fold of r: INNER rows left ++
+// right in left-row-major, right-row order (the first max_output when set),
+// SEMI / ANTI the left rows with / without a match in input order.
+static xlog_hip_rel *keyed_join_probe(Ctx *ctx, const xlog_hip_rel *l, const xlog_hip_rel *r,
+                                      const std::vector<int> &lk, const KeyFold &F, int type, uint64_t max_output) {
+    const uint64_t nl = l->rows;
+    const uint32_t arity = l->arity + r->arity;
+    Buf<uint32_t> lid(ctx, nl);
+    Buf<uint64_t> lkey(ctx, nl);
+    fold_probe(ctx, l, lk, F, lid, lkey);
+    if (type != XLOG_HIP_JOIN_INNER) {
+        Buf<uint8_t> flags(ctx, nl);
+        LAUNCH_1D(k_found_flags, nl, lid.p, nl, type == XLOG_HIP_JOIN_SEMI ? 1 : 0, flags.p);
+        xlog_hip_rel *o = compact_rel(ctx, l, flags.p);
+        if (l->flags & REL_CANONICAL) o->flags = REL_CANONICAL;  // a subset of a sorted set is one
+        return o;
+    }
+    // (id << 32) | row on the probe side (the left keys are no longer needed)
+    LAUNCH_1D(k_id_rows, nl, lid.p, nl, lkey.p);
+    lid = Buf<uint32_t>();
+    const int oc[4] = {1, 3, 0, 0};  // (left row << 32) | right row
+    uint64_t *pairs = nullptr;
+    uint64_t n = join_probe_general(ctx, lkey.p, nl, 0, F.J.ix, F.J.payload.p, 2, oc, &pairs, nullptr);
+    if (n == 0) return rel_new(ctx, arity, 0);
+    Buf<uint64_t> pb;
+    pb.ctx = ctx;
+    pb.p = pairs;
+    if (max_output && n > max_output) n = max_output;
+    std::unique_ptr<xlog_hip_rel, void (*)(xlog_hip_rel *)> o(rel_new(ctx, arity, n), rel_free);
+    o->rows = n;
+    LAUNCH_1D(k_gather_pairs, n, view_of(l), view_of(r), pairs, n, out_of(o.get()));
+    return o.release();
+}
+
+// The join of l (any arity) against the direct index over column rk of a
+// relation of r_arity <= 2 columns: probe words (key << 32) | left row, the
+// right row rebuilt from the key and the payload.
+static xlog_hip_rel *direct_join_wide_left(Ctx *ctx, const xlog_hip_rel *l, uint32_t lk, const JoinIndex &J,
+                                           uint32_t r_arity, uint32_t rk, int type, uint64_t max_output) {
+    const uint64_t nl = l->rows;
+    Buf<uint64_t> probe(ctx, nl);
+    LAUNCH_1D(k_key_rows, nl, view_of(l), (int)lk, nl, probe.p);
+    if (type != XLOG_HIP_JOIN_INNER) {
+        Buf<uint8_t> flags(ctx, nl);
+        join_match_flags(ctx, probe.p, nl, 0, J.ix, type == XLOG_HIP_JOIN_SEMI, flags.p);
+        xlog_hip_rel *o = compact_rel(ctx, l, flags.p);
+        if (l->flags & REL_CANONICAL) o->flags = REL_CANONICAL;
+        return o;
+    }
+    const uint32_t arity = l->arity + r_arity;
+    XH_REQUIRE(arity <= MAX_ARITY, XLOG_HIP_UNSUPPORTED, "join: output arity (left ++ right) above 8");
+    const int oc[4] = {1, 3, 0, 0};  // (left row << 32) | payload
+    uint64_t *w = nullptr;
+    uint64_t n = join_probe_general(ctx, probe.p, nl, 0, J.ix, J.payload.p, 2, oc, &w, nullptr);
+    if (n == 0) return rel_new(ctx, arity, 0);
+    Buf<uint64_t> wb;
+    wb.ctx = ctx;
+    wb.p = w;
+    if (max_output && n > max_output) n = max_output;
+    std::unique_ptr<xlog_hip_rel, void (*)(xlog_hip_rel *)> o(rel_new(ctx, arity, n), rel_free);
+    o->rows = n;
+    LAUNCH_1D(k_gather_left_payload, n, view_of(l), (int)lk, (int)r_arity, (int)rk, w, n, out_of(o.get()));
+    return o.release();
+}
+
+static void check_key_lists(const xlog_hip_rel *l, const xlog_hip_rel *r, const std::vector<int> &lk,
+                            const std::vector<int> &rk, int type) {
     XH_REQUIRE(l && r, XLOG_HIP_INVALID_ARG, "join input is NULL");
     XH_REQUIRE(!lk.empty() && lk.size() == rk.size(), XLOG_HIP_INVALID_ARG,
                "join: key column lists must be non-empty and of equal length");
@@ -888,80 +1066,24 @@ static xlog_hip_rel *op_join_keys(Ctx *ctx, const xlog_hip_rel *l, const xlog_hi
                    "join key column out of range");
     XH_REQUIRE(type == XLOG_HIP_JOIN_INNER || type == XLOG_HIP_JOIN_SEMI || type == XLOG_HIP_JOIN_ANTI,
                XLOG_HIP_INVALID_ARG, "unknown join type");
-    const uint32_t arity = l->arity + r->arity;
-    XH_REQUIRE(type != XLOG_HIP_JOIN_INNER || arity <= MAX_ARITY, XLOG_HIP_UNSUPPORTED,
+    XH_REQUIRE(type != XLOG_HIP_JOIN_INNER || l->arity + r->arity <= MAX_ARITY, XLOG_HIP_UNSUPPORTED,
                "join: output arity (left ++ right) above 8");
     XH_REQUIRE(l->rows < KEY_NONE && r->rows < KEY_NONE, XLOG_HIP_CAPACITY_OVERFLOW,
                "join: more than 2^32 - 2 rows on one side");
-    const uint64_t nl = l->rows, nr = r->rows;
-    if (nl == 0 || nr == 0) {
-        if (type == XLOG_HIP_JOIN_ANTI) return rel_clone(ctx, l);
-        return rel_new(ctx, type == XLOG_HIP_JOIN_INNER ? arity : l->arity, 0);
-    }
-    // fold the key columns into dense ids
-    Buf<uint32_t> rid(ctx, nr), lid(ctx, nl);
-    Buf<uint64_t> rkey(ctx, nr), lkey(ctx, nl);
-    const size_t nk = lk.size();
-    for (size_t t = 0; t < nk;) {
-        const bool first = t == 0;
-        int lc0 = -1, lc1, rc0 = -1, rc1;
-        if (first) {
-            lc0 = lk[0];
-            rc0 = rk[0];
-            lc1 = nk >= 2 ? lk[1] : -1;
-            rc1 = nk >= 2 ? rk[1] : -1;
-            t = nk >= 2 ? 2 : 1;
-        } else {
-            lc1 = lk[t];
-            rc1 = rk[t];
-            ++t;
-        }
-        LAUNCH_1D(k_fold_key, nr, view_of(r), first ? nullptr : rid.p, rc0, rc1, nr, rkey.p);
-        LAUNCH_1D(k_fold_key, nl, view_of(l), first ? nullptr : lid.p, lc0, lc1, nl, lkey.p);
-        uint64_t *s = sort_keys(ctx, rkey.p, nr, false);
-        uint64_t *u = nullptr;
-        uint64_t nu = 0;
-        try {
-            nu = unique_keys(ctx, s, nr, &u);
-        } catch (...) {
-            ctx->free(s);
-            throw;
-        }
-        ctx->free(s);
-        LAUNCH_1D(k_rank_ids, nr, rkey.p, nr, u, nu, rid.p);
-        LAUNCH_1D(k_rank_ids, nl, lkey.p, nl, u, nu, lid.p);
-        ctx->free(u);
-    }
-    rkey = Buf<uint64_t>();
-    if (type != XLOG_HIP_JOIN_INNER) {
-        Buf<uint8_t> flags(ctx, nl);
-        LAUNCH_1D(k_found_flags, nl, lid.p, nl, type == XLOG_HIP_JOIN_SEMI ? 1 : 0, flags.p);
-        xlog_hip_rel *o = compact_rel(ctx, l, flags.p);
-        if (l->flags & REL_CANONICAL) o->flags = REL_CANONICAL;  // a subset of a sorted set is one
-        return o;
-    }
-    // (id << 32) | row on both sides; the run index groups the build rows by id
-    // (stable, so a run lists its rows in input order)
-    Buf<uint64_t> rp(ctx, nr);
-    LAUNCH_1D(k_id_rows, nr, rid.p, nr, rp.p);
-    uint64_t *lp = lkey.p;  // reused: the left keys are no longer needed
-    LAUNCH_1D(k_id_rows, nl, lid.p, nl, lp);
-    rid = Buf<uint32_t>();
-    lid = Buf<uint32_t>();
-    JoinIndex J;
-    build_join_index(ctx, rp.p, nr, 2, 0, false, J);
-    rp = Buf<uint64_t>();
-    const int oc[4] = {1, 3, 0, 0};  // (left row << 32) | right row
-    uint64_t *pairs = nullptr;
-    const uint64_t n = join_probe_general(ctx, lp, nl, 0, J.ix, J.payload.p, 2, oc, &pairs, nullptr);
-    if (n == 0) return rel_new(ctx, arity, 0);
-    Buf<uint64_t> pb;
-    pb.ctx = ctx;
-    pb.p = pairs;
-    std::unique_ptr<xlog_hip_rel, void (*)(xlog_hip_rel *)> o(rel_new(ctx, arity, n), rel_free);
-    o->rows = n;
-    LAUNCH_1D(k_gather_pairs, n, view_of(l), view_of(r), pairs, n, out_of(o.get()));
-    return o.release();
+}
+// The result of a join with an empty side (reference relational.rs:3920-3940).
+static xlog_hip_rel *empty_side_join(Ctx *ctx, const xlog_hip_rel *l, const xlog_hip_rel *r, int type) {
+    if (type == XLOG_HIP_JOIN_ANTI) return rel_clone(ctx, l);
+    return rel_new(ctx, type == XLOG_HIP_JOIN_INNER ? l->arity + r->arity : l->arity, 0);
+}
+
+static xlog_hip_rel *op_join_keys(Ctx *ctx, const xlog_hip_rel *l, const xlog_hip_rel *r, const std::vector<int> &lk,
+                                  const std::vector<int> &rk, int type) {
+    check_key_lists(l, r, lk, rk, type);
+    if (l->rows == 0 || r->rows == 0) return empty_side_join(ctx, l, r, type);
+    KeyFold F;
+    fold_build(ctx, r, rk, F, type == XLOG_HIP_JOIN_INNER);
+    return keyed_join_probe(ctx, l, r, lk, F, type, 0);
 }
 
 static bool column_sorted(Ctx *ctx, const xlog_hip_rel *rel, uint32_t col) {
@@ -1491,6 +1613,7 @@ struct Driver {
     std::vector<DRel> full, delta;
     uint64_t version_counter = 1;
     uint64_t max_join_rows = 0;  // 0: no limit on a body join's bag size
+    uint64_t cur_iter = 0;       // the loop iteration in progress (the reference's counter, recursive.rs:619-620)
     uint32_t digits = 0;         // varying digits of packed tuples over the value domain (0: from the histograms)
     // join-index cache keyed by (relation buffer, column, version)
     struct CacheKey {
@@ -1721,7 +1844,7 @@ struct Driver {
         std::map<std::pair<int, int>, std::unique_ptr<ProbeJob>> pre;
         uint64_t it = 0;
         while (it < max_iter) {
-            ++it;
+            cur_iter = ++it;
             std::vector<std::vector<std::pair<uint64_t *, uint64_t>>> raw(n_preds);
             for (size_t ri = 0; ri < rules.size(); ++ri) {
                 const Rule &r = rules[ri];
@@ -2141,7 +2264,7 @@ struct Driver {
                 // step j0 overflowed: rerun it with the host's sizes, keeping what it appended (in spare)
                 XH_REQUIRE(it < max_iter, XLOG_HIP_ITERATION_LIMIT,
                            "Recursive SCC iteration limit (" + std::to_string(max_iter) + ") exceeded");
-                ++it;
+                cur_iter = ++it;
                 std::vector<std::vector<Var>> vars = pass_vars(false);
                 std::vector<uint64_t> appended(n_preds, 0);
                 std::vector<Buf<uint64_t>> out(n_preds);
@@ -2160,7 +2283,7 @@ struct Driver {
                 continue;
             }
             // ---- one synchronous iteration ----
-            ++it;
+            cur_iter = ++it;
             std::vector<std::vector<Var>> vars = pass_vars(false);
             std::vector<uint64_t> appended(n_preds, 0);
             std::vector<Buf<uint64_t>> out(n_preds);
@@ -2282,6 +2405,14 @@ static DRel canon_drel_async(Ctx *ctx, const xlog_hip_rel *r, uint64_t *d_count,
     return d;
 }
 
+// Device bytes an operation may still take: the free device memory, within
+// the context's budget when one is set.
+static uint64_t device_room(Ctx *ctx) {
+    size_t free_b = 0, total_b = 0;
+    XH_CHECK_HIP(hipMemGetInfo(&free_b, &total_b));
+    return std::min<uint64_t>((uint64_t)free_b + ctx->pool->bytes_cached(), ctx->pool->headroom());
+}
+
 // The dense chain route (chain_fixpoint) when the plan is made of chain rules
 // over at most 2^17 ids whose bit matrices fit in half the free device
 // memory; false (nothing done) when the join route should run instead, an
@@ -2305,10 +2436,8 @@ static bool run_chain_route(Ctx *ctx, const std::vector<Rule> &rules, uint32_t n
         res.clear();
     };
     try {
-        size_t free_b = 0, total_b = 0;
-        XH_CHECK_HIP(hipMemGetInfo(&free_b, &total_b));
         const bool fits = domain >= 1 && domain <= (1ull << 17) &&
-                          chain_fixpoint_bytes(chains, idb, (uint32_t)domain) <= (uint64_t)free_b / 2;
+                          chain_fixpoint_bytes(chains, idb, (uint32_t)domain) <= device_room(ctx) / 2;
         XH_REQUIRE(fits || route != XLOG_HIP_ROUTE_BITMAP, XLOG_HIP_UNSUPPORTED,
                    "bitmap route needs 1..2^17 ids and room for the bit matrices");
         if (!fits) return false;
@@ -2341,7 +2470,8 @@ static bool run_chain_route(Ctx *ctx, const std::vector<Rule> &rules, uint32_t n
 }
 
 static void run_fixpoint_impl(Ctx *ctx, const int32_t *plan, uint32_t n_preds, const xlog_hip_rel *const *rels,
-                              xlog_hip_rel **out, xlog_hip_fixpoint_stats *stats, std::vector<uint64_t> &deltas) {
+                              xlog_hip_rel **out, xlog_hip_fixpoint_stats *stats, std::vector<uint64_t> &deltas,
+                              uint64_t &reached) {
     XH_REQUIRE(n_preds >= 1 && n_preds <= 256, XLOG_HIP_INVALID_ARG, "n_preds must be 1..256");
     XH_REQUIRE(rels && out, XLOG_HIP_INVALID_ARG, "rels / out is NULL");
     std::vector<Rule> rules = parse_plan(plan, n_preds);
@@ -2405,8 +2535,15 @@ static void run_fixpoint_impl(Ctx *ctx, const int32_t *plan, uint32_t n_preds, c
                 if (canon.d[p].owned) canon.d[p].n = ctx->host_scalars[p];
         }
     }
-    const bool bitmap = tc && head_empty && route != XLOG_HIP_ROUTE_JOIN && route != XLOG_HIP_ROUTE_HASH &&
-                        nv <= (1ull << 17);
+    bool bitmap = tc && head_empty && route != XLOG_HIP_ROUTE_JOIN && route != XLOG_HIP_ROUTE_HASH &&
+                  nv <= (1ull << 17);
+    if (bitmap && route == XLOG_HIP_ROUTE_AUTO) {
+        // AUTO leaves it when its bit matrices would take more than half the room (a budget, or a busy device)
+        std::vector<ChainRule> tcc{ChainRule{H, {ChainAtom{E, false}}}, ChainRule{H, {ChainAtom{E, false}, ChainAtom{H, false}}}};
+        std::vector<char> idb1(n_preds, 0);
+        idb1[H] = 1;
+        bitmap = chain_fixpoint_bytes(tcc, idb1, (uint32_t)std::max<uint64_t>(nv, 1)) <= device_room(ctx) / 2;
+    }
     const DRel &edges = tc ? canon.d[E] : canon.d[0];
     if (bitmap) {
         // With the head empty, Δ of iteration k is the set of pairs at shortest distance k + 1 whether the
@@ -2477,10 +2614,11 @@ static void run_fixpoint_impl(Ctx *ctx, const int32_t *plan, uint32_t n_preds, c
             const uint32_t nd = (uint32_t)(bits + 7) / 8;  // bytes per column
             drv.digits = nd ? (((1u << nd) - 1u) | (((1u << nd) - 1u) << 4)) : 1u;
         }
+        if (stats) stats->route = use_hash ? XLOG_HIP_ROUTE_HASH : XLOG_HIP_ROUTE_JOIN;  // also on failure
         try {
             iterations = use_hash ? drv.run_hash(max_iter, deltas, paths) : drv.run(max_iter, deltas);
         } catch (const Error &) {
-            if (stats) stats->iterations = deltas.empty() ? 0 : deltas.size() - 1;
+            reached = drv.cur_iter;
             throw;
         }
         for (uint32_t p = 0; p < n_preds; ++p) {
@@ -2514,6 +2652,7 @@ static void run_fixpoint_impl(Ctx *ctx, const int32_t *plan, uint32_t n_preds, c
         stats->wall_ms = ms;
         if (stats->delta_sizes)
             for (uint64_t i = 0; i < stats->delta_cap && i < deltas.size(); ++i) stats->delta_sizes[i] = deltas[i];
+        stats->delta_count = std::min<uint64_t>(deltas.size(), stats->delta_sizes ? stats->delta_cap : 0);
     }
 }
 
@@ -2523,13 +2662,17 @@ static void run_fixpoint(Ctx *ctx, const int32_t *plan, uint32_t n_preds, const 
                          xlog_hip_rel **out, xlog_hip_fixpoint_stats *stats) {
     const uint64_t waits0 = ctx->host_waits;
     std::vector<uint64_t> deltas;
+    uint64_t reached = 0;  // the iteration a failure happened in (0: set-up or seed), when the route knows it
     try {
-        run_fixpoint_impl(ctx, plan, n_preds, rels, out, stats, deltas);
+        run_fixpoint_impl(ctx, plan, n_preds, rels, out, stats, deltas, reached);
     } catch (...) {
         if (stats) {
-            stats->iterations = deltas.empty() ? 0 : deltas.size() - 1;
+            // the iterations completed, or the one in progress when it failed: the reference's counter is
+            // incremented at the top of each iteration (recursive.rs:619-620)
+            stats->iterations = std::max<uint64_t>(deltas.empty() ? 0 : deltas.size() - 1, reached);
             if (stats->delta_sizes)
                 for (uint64_t i = 0; i < stats->delta_cap && i < deltas.size(); ++i) stats->delta_sizes[i] = deltas[i];
+            stats->delta_count = std::min<uint64_t>(deltas.size(), stats->delta_sizes ? stats->delta_cap : 0);
             stats->host_waits = ctx->host_waits - waits0;
         }
         throw;
@@ -2685,6 +2828,13 @@ xlog_hip_status xlog_hip_memory_stats(xlog_hip_ctx *ctx, uint64_t *in_use, uint6
     });
 }
 xlog_hip_status xlog_hip_trim(xlog_hip_ctx *ctx) { return guarded([&] { C(ctx)->pool->trim(); }); }
+xlog_hip_status xlog_hip_set_memory_budget(xlog_hip_ctx *ctx, uint64_t device_bytes) {
+    return guarded([&] {
+        Ctx *c = C(ctx);
+        c->pool->set_budget((size_t)device_bytes);
+        if (device_bytes && c->pool->bytes_in_use() + c->pool->bytes_cached() > device_bytes) c->pool->trim();
+    });
+}
 
 xlog_hip_status xlog_hip_rel_create_empty(xlog_hip_ctx *ctx, uint32_t arity, xlog_hip_rel **out) {
     return guarded([&] {
@@ -3004,33 +3154,36 @@ xlog_hip_status xlog_hip_hash_join_keys(xlog_hip_ctx *ctx, const xlog_hip_rel *l
             *out = op_join_keys(c, left, right, lk, rk, join_type);
     });
 }
-xlog_hip_status xlog_hip_join_index_build(xlog_hip_ctx *ctx, const xlog_hip_rel *right, uint32_t right_key,
-                                          xlog_hip_join_index **out) {
+xlog_hip_status xlog_hip_join_index_build(xlog_hip_ctx *ctx, const xlog_hip_rel *right, const uint32_t *right_keys,
+                                          uint32_t n_keys, xlog_hip_join_index **out) {
     return guarded([&] {
         Ctx *c = C(ctx);
         OUT_GUARD;
         need_rel(right, "right");
-        XH_REQUIRE(right_key < right->arity, XLOG_HIP_INVALID_ARG, "right key column out of range");
-        XH_REQUIRE(right->arity <= 2, XLOG_HIP_UNSUPPORTED, "join: input arity above 2 is not supported");
+        XH_REQUIRE(n_keys >= 1 && right_keys, XLOG_HIP_INVALID_ARG, "Join requires at least one key column");
+        XH_REQUIRE(n_keys <= MAX_ARITY, XLOG_HIP_INVALID_ARG, "more key columns than columns");
+        for (uint32_t t = 0; t < n_keys; ++t)
+            XH_REQUIRE(right_keys[t] < right->arity, XLOG_HIP_INVALID_ARG, "right key column out of range");
         XH_REQUIRE(right->rows > 0, XLOG_HIP_INVALID_ARG, "cannot build a join index for an empty relation");
-        auto *ix = new xlog_hip_join_index;
+        XH_REQUIRE(right->rows < KEY_NONE, XLOG_HIP_CAPACITY_OVERFLOW, "join: more than 2^32 - 2 rows on one side");
+        std::unique_ptr<xlog_hip_join_index> ix(new xlog_hip_join_index);
         ix->ctx = c;
         ix->arity = right->arity;
-        ix->key = right_key;
+        ix->keys.assign(right_keys, right_keys + n_keys);
         ix->rows = right->rows;
-        try {
-            build_join_index(c, right->w[0], right->rows, right->arity, (int)right_key,
+        if (n_keys == 1 && right->arity <= 2) {
+            build_join_index(c, right->w[0], right->rows, right->arity, (int)right_keys[0],
                              (right->flags & REL_CANONICAL) != 0, ix->J);
-        } catch (...) {
-            delete ix;
-            throw;
+        } else {
+            ix->F.reset(new KeyFold());
+            fold_build(c, right, std::vector<int>(right_keys, right_keys + n_keys), *ix->F, true);
         }
-        *out = ix;
+        *out = ix.release();
     });
 }
 xlog_hip_status xlog_hip_hash_join_with_index(xlog_hip_ctx *ctx, const xlog_hip_rel *left, const xlog_hip_rel *right,
-                                              uint32_t left_key, uint32_t right_key, int join_type,
-                                              const xlog_hip_join_index *index, uint64_t max_output,
+                                              const uint32_t *left_keys, const uint32_t *right_keys, uint32_t n_keys,
+                                              int join_type, const xlog_hip_join_index *index, uint64_t max_output,
                                               xlog_hip_rel **out) {
     return guarded([&] {
         Ctx *c = C(ctx);
@@ -3039,9 +3192,30 @@ xlog_hip_status xlog_hip_hash_join_with_index(xlog_hip_ctx *ctx, const xlog_hip_
         need_rel(right, "right");
         XH_REQUIRE(index, XLOG_HIP_INVALID_ARG, "join index is NULL");
         XH_REQUIRE(index->ctx == c, XLOG_HIP_INVALID_ARG, "join index belongs to another context");
-        XH_REQUIRE(index->arity == right->arity && index->key == right_key && index->rows == right->rows,
-                   XLOG_HIP_INVALID_ARG, "join index was not built over this right relation and key");
-        *out = op_join_indexed(c, left, left_key, index->J, right->arity, right_key, join_type, nullptr, max_output);
+        XH_REQUIRE(n_keys >= 1 && left_keys && right_keys, XLOG_HIP_INVALID_ARG,
+                   "Join requires at least one key column");
+        XH_REQUIRE(n_keys <= MAX_ARITY, XLOG_HIP_INVALID_ARG, "more key columns than columns");
+        std::vector<int> lk(left_keys, left_keys + n_keys), rk(right_keys, right_keys + n_keys);
+        check_key_lists(left, right, lk, rk, join_type);
+        // the index must have been built over this right relation and these key columns (relational.rs:3975-3985)
+        XH_REQUIRE(index->rows == right->rows, XLOG_HIP_INVALID_ARG,
+                   "Join index row count does not match right relation");
+        XH_REQUIRE(index->arity == right->arity &&
+                       std::vector<uint32_t>(right_keys, right_keys + n_keys) == index->keys,
+                   XLOG_HIP_INVALID_ARG, "Join index key columns do not match requested right_keys");
+        if (left->rows == 0) {
+            *out = empty_side_join(c, left, right, join_type);
+            return;
+        }
+        if (index->F) {
+            *out = keyed_join_probe(c, left, right, lk, *index->F, join_type, max_output);
+        } else if (left->arity <= 2) {
+            *out = op_join_indexed(c, left, left_keys[0], index->J, right->arity, right_keys[0], join_type, nullptr,
+                                   max_output);
+        } else {
+            *out = direct_join_wide_left(c, left, left_keys[0], index->J, right->arity, right_keys[0], join_type,
+                                         max_output);
+        }
     });
 }
 void xlog_hip_join_index_free(xlog_hip_join_index *index) { delete index; }

@@ -142,10 +142,12 @@ __device__ __forceinline__ bool queued_prologue(const QueuedStep &q, uint64_t &n
     return true;
 }
 
-// Inserts keys[0..n) (no novelty bookkeeping): the initial full relation, or
-// the keys of an old table being rehashed (old slots; empty ones skipped).
+// Inserts keys[0..n) (no novelty bookkeeping): the initial full relation
+// (rehash = 0: the all-ones key is a tuple and sets its flag), or the slots
+// of an old table being rehashed (rehash = 1: all ones is an empty slot and is
+// skipped; the flag carries over with the table's flags).
 __global__ void k_hs_insert_all(const uint64_t *__restrict__ keys, uint64_t n, SetView s,
-                                unsigned long long *overflow) {
+                                unsigned long long *overflow, int rehash) {
     const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
     for (uint64_t i0 = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i0 < n; i0 += stride * HS_U) {
         uint64_t k[HS_U], h[HS_U];
@@ -153,7 +155,8 @@ __global__ void k_hs_insert_all(const uint64_t *__restrict__ keys, uint64_t n, S
 #pragma unroll
         for (int u = 0; u < HS_U; ++u) {
             const uint64_t i = i0 + (uint64_t)u * stride;
-            k[u] = i < n ? keys[i] : HS_EMPTY;  // an empty old slot, or past the end: nothing to insert
+            k[u] = i < n ? keys[i] : HS_EMPTY;  // past the end: nothing to insert
+            if (i < n && k[u] == HS_EMPTY && !rehash) atomicExch(s.allones, 1u);
         }
 #pragma unroll
         for (int u = 0; u < HS_U; ++u) {
@@ -524,12 +527,14 @@ static unsigned grid_blocks(Ctx *ctx, uint64_t threads) {
     return grid_for(threads, HB, std::min<unsigned>((unsigned)ctx->num_cus * 16, HS_MAX_BLOCKS));
 }
 
-void hs_insert_all(Ctx *ctx, HashSet &h, const uint64_t *keys, uint64_t n) {
+static void insert_all(Ctx *ctx, HashSet &h, const uint64_t *keys, uint64_t n, int rehash) {
     if (!n) return;
     unsigned long long *ovf = reinterpret_cast<unsigned long long *>(h.flags.p + 1);
-    hipLaunchKernelGGL(k_hs_insert_all, dim3(grid_blocks(ctx, n)), dim3(HB), 0, ctx->stream, keys, n, view(h), ovf);
+    hipLaunchKernelGGL(k_hs_insert_all, dim3(grid_blocks(ctx, n)), dim3(HB), 0, ctx->stream, keys, n, view(h), ovf,
+                       rehash);
     XH_CHECK_HIP(hipGetLastError());
 }
+void hs_insert_all(Ctx *ctx, HashSet &h, const uint64_t *keys, uint64_t n) { insert_all(ctx, h, keys, n, 0); }
 
 void hs_grow(Ctx *ctx, HashSet &h, uint64_t min_cap) {
     HashSet g;
@@ -542,7 +547,7 @@ void hs_grow(Ctx *ctx, HashSet &h, uint64_t min_cap) {
     g.slots = Buf<uint64_t>(ctx, g.cap);
     fill_u64(ctx, g.slots.p, HS_EMPTY, g.cap);
     fill_u64(ctx, g.flags.p + 1, 0ull, 1);
-    hs_insert_all(ctx, g, h.slots.p, h.cap);  // skips the empty slots
+    insert_all(ctx, g, h.slots.p, h.cap, 1);  // skips the empty slots
     g.size = h.size;
     h = std::move(g);
 }

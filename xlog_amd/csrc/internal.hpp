@@ -79,13 +79,20 @@ class Pool {
     size_t bytes_in_use() const { return in_use_; }
     size_t bytes_cached() const { return cached_; }
     size_t peak_in_use() const { return peak_; }
+    // Device memory budget (0: none): an allocation that would take the live
+    // bytes past it fails with XLOG_HIP_OOM, and cached blocks are returned to
+    // the driver before the pool's footprint (live + cached) would pass it.
+    void set_budget(size_t bytes) { budget_ = bytes; }
+    size_t budget() const { return budget_; }
+    // bytes the budget still allows (SIZE_MAX without one)
+    size_t headroom() const { return budget_ ? (budget_ > in_use_ ? budget_ - in_use_ : 0) : SIZE_MAX; }
 
   private:
     static size_t round_up(size_t b);
     int device_;
     std::multimap<size_t, void *> free_;  // size class -> block
     std::map<void *, size_t> live_;
-    size_t in_use_ = 0, cached_ = 0, peak_ = 0;
+    size_t in_use_ = 0, cached_ = 0, peak_ = 0, budget_ = 0;
 };
 
 // RAII scratch buffer from the context pool
@@ -441,7 +448,8 @@ struct HashSet {
     uint64_t size = 0;  // tuples held (host bookkeeping)
 };
 void hs_init(Ctx *ctx, HashSet &h, uint64_t min_cap);
-// inserts keys without novelty bookkeeping (flags[1] set on a full table)
+// inserts keys without novelty bookkeeping (flags[1] set on a full table);
+// the all-ones key sets flags[0]
 void hs_insert_all(Ctx *ctx, HashSet &h, const uint64_t *keys, uint64_t n);
 // rehash into a table of at least min_cap slots
 void hs_grow(Ctx *ctx, HashSet &h, uint64_t min_cap);

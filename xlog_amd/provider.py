@@ -54,6 +54,7 @@ class FixpointStats(C.Structure):
         ("wall_ms", C.c_double),
         ("max_join_rows", C.c_uint64),
         ("host_waits", C.c_uint64),
+        ("delta_count", C.c_uint64),
     ]
 
 
@@ -90,6 +91,7 @@ def _load() -> C.CDLL:
         "xlog_hip_stream": (P, [P]),
         "xlog_hip_memory_stats": (I32, [P, C.POINTER(U64), C.POINTER(U64), C.POINTER(U64)]),
         "xlog_hip_trim": (I32, [P]),
+        "xlog_hip_set_memory_budget": (I32, [P, U64]),
         "xlog_hip_rel_create_empty": (I32, [P, U32, PP]),
         "xlog_hip_rel_from_host_columns": (I32, [P, PP, U32, U64, PP]),
         "xlog_hip_rel_from_device_columns": (I32, [P, PP, U32, U64, PP]),
@@ -106,8 +108,8 @@ def _load() -> C.CDLL:
         "xlog_hip_dedup": (I32, [P, P, P, U32, PP]),
         "xlog_hip_dedup_full_row": (I32, [P, P, PP]),
         "xlog_hip_dedup_sorted": (I32, [P, P, P, U32, PP]),
-        "xlog_hip_join_index_build": (I32, [P, P, U32, PP]),
-        "xlog_hip_hash_join_with_index": (I32, [P, P, P, U32, U32, I32, P, U64, PP]),
+        "xlog_hip_join_index_build": (I32, [P, P, P, U32, PP]),
+        "xlog_hip_hash_join_with_index": (I32, [P, P, P, P, P, U32, I32, P, U64, PP]),
         "xlog_hip_join_index_free": (None, [P]),
         "xlog_hip_nested_loop_join": (I32, [P, P, P, U32, U32, PP]),
         "xlog_hip_fj_delta_novel": (I32, [P, P, P, P, C.POINTER(FjDeltaCols), U32, PP]),
@@ -151,7 +153,7 @@ _lib = _load()
 #: exported symbol names the C header declares (checked by the CPU test-suite)
 ABI_SYMBOLS = (
     "xlog_hip_last_error", "xlog_hip_version", "xlog_hip_ctx_create", "xlog_hip_ctx_destroy",
-    "xlog_hip_synchronize", "xlog_hip_stream", "xlog_hip_memory_stats", "xlog_hip_trim",
+    "xlog_hip_synchronize", "xlog_hip_stream", "xlog_hip_memory_stats", "xlog_hip_trim", "xlog_hip_set_memory_budget",
     "xlog_hip_rel_create_empty", "xlog_hip_rel_from_host_columns", "xlog_hip_rel_from_device_columns",
     "xlog_hip_rel_from_host_packed", "xlog_hip_rel_download_column", "xlog_hip_rel_download_packed",
     "xlog_hip_rel_num_rows", "xlog_hip_rel_arity", "xlog_hip_rel_is_canonical", "xlog_hip_rel_device_words",
@@ -287,12 +289,12 @@ class JoinIndex:
     """Reusable join index over one key column (the JoinIndexV2 counterpart,
     relational.rs:3728).  Freed when garbage collected or when its provider closes."""
 
-    __slots__ = ("_h", "_provider", "right_key", "__weakref__")
+    __slots__ = ("_h", "_provider", "right_keys", "__weakref__")
 
-    def __init__(self, provider: "HipKernelProvider", handle: C.c_void_p, right_key: int):
+    def __init__(self, provider: "HipKernelProvider", handle: C.c_void_p, right_keys: Sequence[int]):
         self._provider = provider
         self._h = handle
-        self.right_key = right_key
+        self.right_keys = tuple(right_keys)
 
     @property
     def handle(self) -> C.c_void_p:
@@ -366,6 +368,12 @@ class HipKernelProvider:
 
     def trim(self) -> None:
         _check(_lib.xlog_hip_trim(self.ctx))
+
+    def set_memory_budget(self, device_bytes: int) -> None:
+        """Device memory budget in bytes, 0 for none (MemoryBudget::with_limit,
+        crates/xlog-core/src/config.rs:39-45): an allocation past it raises
+        XlogError with status OOM."""
+        _check(_lib.xlog_hip_set_memory_budget(self.ctx, device_bytes))
 
     # -- kernel timing (HIP events on the context stream) --------------------
     def profile_enable(self, on: bool = True) -> None:
@@ -532,21 +540,25 @@ class HipKernelProvider:
         return self._rel(h)
 
     def build_join_index_v2(self, right: Relation, right_keys: Sequence[int]) -> JoinIndex:
-        if len(right_keys) != 1:
-            raise XlogError(7, "joins on one key column per side are supported")
+        """Reusable index over a key list of the build side (relational.rs:3728-3880)."""
+        if not right_keys:
+            raise XlogError(1, "Join requires at least one key column")
+        rk, _ = _u32_array(right_keys)
         h = C.c_void_p()
-        _check(_lib.xlog_hip_join_index_build(self.ctx, right.handle, right_keys[0], C.byref(h)))
-        ix = JoinIndex(self, h, right_keys[0])
+        _check(_lib.xlog_hip_join_index_build(self.ctx, right.handle, rk, len(right_keys), C.byref(h)))
+        ix = JoinIndex(self, h, right_keys)
         self._live.add(ix)
         return ix
 
     def hash_join_v2_with_index(self, left: Relation, right: Relation, left_keys: Sequence[int],
                                 right_keys: Sequence[int], join_type: int, index: JoinIndex,
                                 max_output: Optional[int] = None) -> Relation:
-        if len(left_keys) != 1 or len(right_keys) != 1:
-            raise XlogError(7, "joins on one key column per side are supported")
+        """hash_join_v2 against an index built over (right, right_keys) (relational.rs:3882-4000)."""
+        if len(left_keys) != len(right_keys) or not left_keys:
+            raise XlogError(1, "key column lists must be non-empty and of equal length")
+        (lk, _), (rk, _) = _u32_array(left_keys), _u32_array(right_keys)
         h = C.c_void_p()
-        _check(_lib.xlog_hip_hash_join_with_index(self.ctx, left.handle, right.handle, left_keys[0], right_keys[0],
+        _check(_lib.xlog_hip_hash_join_with_index(self.ctx, left.handle, right.handle, lk, rk, len(left_keys),
                                                   join_type, index.handle, max_output or 0, C.byref(h)))
         return self._rel(h)
 
@@ -648,11 +660,13 @@ class HipKernelProvider:
         rels = (C.c_void_p * n)(*[r.handle if r is not None else None for r in relations])
         outs = (C.c_void_p * n)()
         trace = (C.c_uint64 * trace_cap)()
-        st = FixpointStats(0, max_iterations, trace, trace_cap, route, 0.0, max_join_rows, 0)
+        st = FixpointStats(0, max_iterations, trace, trace_cap, route, 0.0, max_join_rows, 0, 0)
         status = _lib.xlog_hip_fixpoint(self.ctx, plan_arr, n, rels, outs, C.byref(st))
         stats = {"iterations": st.iterations, "route": int(st.route), "wall_ms": st.wall_ms,
                  "host_waits": st.host_waits}
-        stats["delta_sizes"] = [trace[i] for i in range(min(st.iterations + 1, trace_cap))]
+        # the seed's and every completed iteration's delta size (after a failure inside an iteration,
+        # "iterations" counts that iteration and the list stops before it)
+        stats["delta_sizes"] = [trace[i] for i in range(min(st.delta_count, trace_cap))]
         if status != OK:
             err = XlogError(status, (_lib.xlog_hip_last_error() or b"").decode())
             err.stats = stats
