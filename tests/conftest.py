@@ -1,3 +1,4 @@
+import gc
 import os
 import sys
 from pathlib import Path
@@ -20,3 +21,13 @@ def provider():
     p = HipKernelProvider(0)
     yield p
     p.close()
+
+
+@pytest.fixture(autouse=True)
+def _release_device_relations():
+    """Relation handles free their device memory when collected.  A test whose
+    frame holds a pytest.raises result is in a reference cycle (frame ->
+    exception -> traceback -> frame) that only the cycle collector breaks, so
+    its relations would stay live into later tests: collect after each test."""
+    yield
+    gc.collect()

@@ -4,13 +4,14 @@ GpuMemoryManager, crates/xlog-cuda/src/memory.rs:756-770): an allocation past
 it fails closed with OOM, the context stays usable, and the fixpoint's AUTO
 route choice keeps its bit matrices within it (the result, iteration count
 and delta sizes stay those of the oracle)."""
+import gc
 import sys
 
 import numpy as np
 import pytest
 
 import oracle
-from xlog_amd import ROUTE_AUTO, ROUTE_BITMAP, ROUTE_HASH, XlogError, datagen, pack, tc_plan
+from xlog_amd import ROUTE_AUTO, ROUTE_BITMAP, ROUTE_HASH, ROUTE_JOIN, XlogError, datagen, pack, tc_plan
 
 pytestmark = pytest.mark.gpu
 OOM = 5
@@ -22,13 +23,19 @@ def _note(msg):
 
 
 @pytest.fixture
-def p(provider):
-    """The session's provider, its budget lifted again whatever the test does."""
+def p():
+    """A context of its own: its pool holds nothing of the other tests (the
+    session context keeps per-context look-back state sized by the largest
+    sort it ran), so the budget counts only what these tests allocate."""
+    from xlog_amd import HipKernelProvider
+
+    gc.collect()
+    prov = HipKernelProvider(0)
     try:
-        yield provider
+        yield prov
     finally:
-        provider.set_memory_budget(0)
-        provider.trim()
+        gc.collect()
+        prov.close()
 
 
 def test_budget_refuses_then_recovers(p):
@@ -80,3 +87,39 @@ def test_budget_steers_auto_off_the_bitmap_route(p):
         p.fixpoint(tc_plan(), [p.create_buffer_from_packed(e), None], route=ROUTE_BITMAP)
     assert ex.value.status == OOM
     p.set_memory_budget(0)
+
+
+@pytest.mark.parametrize("where", ["rule2", "rule3_second_join"])
+def test_failed_fixpoint_frees_its_device_memory(p, where):
+    """A fixpoint stopped by the join-row limit (CAPACITY_OVERFLOW, the
+    reference's relational.rs:4550-4555) gives back every block it took.  The
+    limit trips in the first recursive iteration either on rule 2's join or on
+    rule 3's second join, when rule 2's head tuples and rule 3's first join
+    are held (join sizes from the oracle's counts, as for C5 at its stated
+    size)."""
+    from xlog_amd import andersen_plan
+
+    f = datagen.andersen(2000, 8000, 1.5, datagen.seed_for(5))
+    assign, addr, load = (oracle.sort_dedup(pack(*f[k])) for k in ("assign", "addressOf", "load"))
+    r2 = oracle.chain2_counts(assign, addr, np.zeros(0, np.uint64))
+    r3 = oracle.chain2_counts(load, addr, addr)
+    if where == "rule2":
+        limit = r2["bag1"] - 1
+    else:
+        limit = max(r2["bag1"], r3["bag1"])
+        assert r3["bag2_over_bag1"] > limit
+    rels = [p.create_buffer_from_u32_columns(list(f[k])) for k in ("assign", "addressOf", "load", "store")]
+
+    def fail_once():
+        with pytest.raises(XlogError) as ex:
+            p.fixpoint(andersen_plan(), rels + [None], route=ROUTE_JOIN, max_join_rows=limit)
+        assert ex.value.status == 3  # CAPACITY_OVERFLOW
+        assert ex.value.stats["iterations"] == 1
+        del ex
+        gc.collect()
+        return p.memory_stats()["in_use"]
+
+    # the first run also sizes the context's persistent look-back state; the
+    # second must end with exactly the live bytes it started with
+    before = fail_once()
+    assert fail_once() == before

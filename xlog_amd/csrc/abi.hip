@@ -322,6 +322,64 @@ static uint64_t read_count(Ctx *ctx, const uint64_t *d) {
     return ctx->host_scalars[0];
 }
 
+// Owns one pool block until it is released: an error unwinding past the owner
+// gives the block back to the pool.
+struct Owned {
+    Ctx *ctx;
+    uint64_t *p;
+    explicit Owned(Ctx *c, uint64_t *q = nullptr) : ctx(c), p(q) {}
+    Owned(const Owned &) = delete;
+    Owned &operator=(const Owned &) = delete;
+    ~Owned() {
+        if (p) ctx->free(p);
+    }
+    void reset(uint64_t *q = nullptr) {
+        if (p && p != q) ctx->free(p);
+        p = q;
+    }
+    uint64_t *release() {
+        uint64_t *q = p;
+        p = nullptr;
+        return q;
+    }
+};
+static uint64_t *alloc_keys(Ctx *ctx, uint64_t n) {
+    return static_cast<uint64_t *>(ctx->alloc((n ? n : 1) * sizeof(uint64_t)));
+}
+
+// Bags of packed tuples, each an owned pool block (a rule body's head tuples,
+// a join's output): what is still held is freed when an error unwinds past
+// the owner.
+struct Bags {
+    Ctx *ctx;
+    std::vector<std::pair<uint64_t *, uint64_t>> v;
+    explicit Bags(Ctx *c) : ctx(c) {}
+    Bags(Bags &&o) noexcept : ctx(o.ctx), v(std::move(o.v)) { o.v.clear(); }
+    Bags(const Bags &) = delete;
+    Bags &operator=(const Bags &) = delete;
+    ~Bags() { clear(); }
+    void clear() {
+        for (auto &b : v)
+            if (b.first) ctx->free(b.first);
+        v.clear();
+    }
+    void add(Owned &o, uint64_t n) {
+        v.push_back({o.p, n});
+        o.release();
+    }
+    uint64_t rows() const {
+        uint64_t t = 0;
+        for (auto &b : v) t += b.second;
+        return t;
+    }
+};
+static std::vector<Bags> bags_per_pred(Ctx *ctx, uint32_t n) {
+    std::vector<Bags> r;
+    r.reserve(n);
+    for (uint32_t i = 0; i < n; ++i) r.emplace_back(ctx);
+    return r;
+}
+
 // ---------------------------------------------------------------------------
 // sorting helpers
 // ---------------------------------------------------------------------------
@@ -333,34 +391,34 @@ static uint64_t read_count(Ctx *ctx, const uint64_t *d) {
 // the high word only, stable otherwise).
 static uint64_t *sort_keys(Ctx *ctx, uint64_t *keys, uint64_t n, bool keys_owned, int digit_lo = 0,
                            int digit_hi = 8, uint32_t known_digits = 0) {
+    // a consumed input is freed if an error unwinds from here
+    Owned in_guard(ctx, keys_owned ? keys : nullptr);
     if (n < 2) {
-        if (keys_owned || n == 0) return keys;
+        if (keys_owned || n == 0) return in_guard.release();
         uint64_t *c = static_cast<uint64_t *>(ctx->alloc(n * sizeof(uint64_t)));
         copy_d2d(ctx, c, keys, n);
         return c;
     }
     const uint64_t CHUNK = 1ull << 29;
     if (n < (1ull << 30)) {
-        uint64_t *a = keys, *b = static_cast<uint64_t *>(ctx->alloc(n * sizeof(uint64_t)));
+        Owned ga(ctx, keys_owned ? in_guard.release() : alloc_keys(ctx, n));
+        Owned gb(ctx, alloc_keys(ctx, n));
+        uint64_t *a = ga.p, *b = gb.p;
         uint32_t *v0 = nullptr, *v1 = nullptr;
-        if (keys_owned) {
-            radix_sort_u64(ctx, &a, &b, &v0, &v1, n, digit_lo, digit_hi, nullptr, known_digits);
-        } else {
-            // the first pass reads the caller's keys; both ping-pong buffers are ours
-            a = static_cast<uint64_t *>(ctx->alloc(n * sizeof(uint64_t)));
-            radix_sort_u64(ctx, &a, &b, &v0, &v1, n, digit_lo, digit_hi, keys, known_digits);
-        }
+        // without keys_owned the first pass reads the caller's keys; both ping-pong buffers are ours
+        radix_sort_u64(ctx, &a, &b, &v0, &v1, n, digit_lo, digit_hi, keys_owned ? nullptr : keys, known_digits);
+        ga.release();
+        gb.release();
         ctx->free(b);
         return a;
     }
     XH_REQUIRE(digit_lo == 0 && digit_hi == 8, XLOG_HIP_UNSUPPORTED, "partial-key sort above 2^30 keys");
     // chunked: sort pieces of 2^29 then merge pairwise
-    uint64_t *a = keys;
-    if (!keys_owned) {
-        a = static_cast<uint64_t *>(ctx->alloc(n * sizeof(uint64_t)));
-        copy_d2d(ctx, a, keys, n);
-    }
-    uint64_t *b = static_cast<uint64_t *>(ctx->alloc(n * sizeof(uint64_t)));
+    Owned ga(ctx, keys_owned ? in_guard.release() : alloc_keys(ctx, n));
+    uint64_t *a = ga.p;
+    if (!keys_owned) copy_d2d(ctx, a, keys, n);
+    Owned gb(ctx, alloc_keys(ctx, n));
+    uint64_t *b = gb.p;
     std::vector<std::pair<uint64_t, uint64_t>> runs;
     for (uint64_t s = 0; s < n; s += CHUNK) {
         uint64_t len = std::min(CHUNK, n - s);
@@ -386,17 +444,20 @@ static uint64_t *sort_keys(Ctx *ctx, uint64_t *keys, uint64_t n, bool keys_owned
         runs.swap(next);
         std::swap(src, dst);
     }
+    ga.release();
+    gb.release();
     ctx->free(dst);
     return src;
 }
 
 // sorted (any) keys -> unique keys in a new buffer; returns count
 static uint64_t unique_keys(Ctx *ctx, const uint64_t *sorted, uint64_t n, uint64_t **out) {
-    uint64_t *o = static_cast<uint64_t *>(ctx->alloc((n ? n : 1) * sizeof(uint64_t)));
+    Owned o(ctx, alloc_keys(ctx, n));
     Buf<uint64_t> cnt(ctx, 1);
-    select_unique(ctx, sorted, n, o, cnt.p);
-    *out = o;
-    return read_count(ctx, cnt.p);
+    select_unique(ctx, sorted, n, o.p, cnt.p);
+    const uint64_t c = read_count(ctx, cnt.p);
+    *out = o.release();
+    return c;
 }
 
 // Sorted unique copy of n keys (the caller's buffer is left as it is): returns
@@ -406,27 +467,28 @@ static uint64_t unique_keys(Ctx *ctx, const uint64_t *sorted, uint64_t n, uint64
 static void sort_unique_keys_async(Ctx *ctx, const uint64_t *keys, uint64_t n, uint64_t **out, uint64_t *d_count,
                                    uint32_t known_digits = 0) {
     if (n >= 2 && n < (1ull << 30)) {
-        uint64_t *a = static_cast<uint64_t *>(ctx->alloc(n * sizeof(uint64_t)));
-        uint64_t *b = static_cast<uint64_t *>(ctx->alloc(n * sizeof(uint64_t)));
+        Owned ga(ctx, alloc_keys(ctx, n)), gb(ctx, alloc_keys(ctx, n));
+        uint64_t *a = ga.p, *b = gb.p;
         uint32_t *v0 = nullptr, *v1 = nullptr;
         SortUnique uq;
         radix_sort_u64(ctx, &a, &b, &v0, &v1, n, 0, 8, keys, known_digits, &uq);
+        ga.release();
+        gb.release();
+        Owned sorted(ctx, a), other(ctx, b);
         if (uq.done) {
-            ctx->free(b);
-            *out = a;
             fill_u64(ctx, d_count, uq.count, 1);
+            *out = sorted.release();
             return;
         }
         select_unique(ctx, a, n, b, d_count);
-        ctx->free(a);
-        *out = b;
+        *out = other.release();
         return;
     }
     uint64_t *s = sort_keys(ctx, const_cast<uint64_t *>(keys), n, false, 0, 8, known_digits);
-    uint64_t *o = static_cast<uint64_t *>(ctx->alloc((n ? n : 1) * sizeof(uint64_t)));
-    select_unique(ctx, s, n, o, d_count);
-    if (s != keys) ctx->free(s);
-    *out = o;
+    Owned gs(ctx, s != keys ? s : nullptr);
+    Owned o(ctx, alloc_keys(ctx, n));
+    select_unique(ctx, s, n, o.p, d_count);
+    *out = o.release();
 }
 // The same with the count read back (returned).
 static uint64_t sort_unique_keys(Ctx *ctx, const uint64_t *keys, uint64_t n, uint64_t **out) {
@@ -717,41 +779,47 @@ static uint64_t join_emit(Ctx *ctx, ProbeJob &job, const int oc[4], uint64_t **o
                    std::to_string(max_rows));
     if (total <= kChunkRows) {
         uint64_t *o = static_cast<uint64_t *>(ctx->alloc(total * sizeof(uint64_t)));
+        Owned go(ctx, o);
         probe_emit_range(ctx, job, 0, job.tiles, total, 2, oc, o, nullptr);
-        *out = o;
+        *out = go.release();
         return total;
     }
     std::vector<uint64_t> off = probe_tile_offsets(ctx, job);
-    uint64_t *acc = nullptr, acc_n = 0;
+    Owned acc(ctx);
+    uint64_t acc_n = 0;
     for (uint64_t t0 = 0; t0 < job.tiles;) {
         uint64_t t1 = t0 + 1;
         while (t1 < job.tiles && off[t1 + 1] - off[t0] <= kChunkRows) ++t1;
         const uint64_t m = off[t1] - off[t0];
         if (m) {
             uint64_t *b = static_cast<uint64_t *>(ctx->alloc(m * sizeof(uint64_t)));
-            probe_emit_range(ctx, job, t0, t1, m, 2, oc, b, nullptr);
-            uint64_t *s = sort_keys(ctx, b, m, true, 0, 8, digits);  // consumes b
+            {
+                Owned gb(ctx, b);
+                probe_emit_range(ctx, job, t0, t1, m, 2, oc, b, nullptr);
+                gb.release();
+            }
+            Owned srt(ctx, sort_keys(ctx, b, m, true, 0, 8, digits));  // consumes b
             uint64_t *u;
-            uint64_t un = unique_keys(ctx, s, m, &u);
-            ctx->free(s);
-            if (!acc) {
-                acc = u;
+            uint64_t un = unique_keys(ctx, srt.p, m, &u);
+            Owned gu(ctx, u);
+            srt.reset();
+            if (!acc.p) {
+                acc.reset(gu.release());
                 acc_n = un;
             } else {
-                uint64_t *mg = static_cast<uint64_t *>(ctx->alloc((acc_n + un) * sizeof(uint64_t)));
-                merge_sorted(ctx, acc, acc_n, u, un, mg);
-                ctx->free(acc);
-                ctx->free(u);
+                Owned mg(ctx, alloc_keys(ctx, acc_n + un));
+                merge_sorted(ctx, acc.p, acc_n, u, un, mg.p);
+                acc.reset();
+                gu.reset();
                 uint64_t *u2;
-                uint64_t n2 = unique_keys(ctx, mg, acc_n + un, &u2);
-                ctx->free(mg);
-                acc = u2;
+                uint64_t n2 = unique_keys(ctx, mg.p, acc_n + un, &u2);
+                acc.reset(u2);
                 acc_n = n2;
             }
         }
         t0 = t1;
     }
-    *out = acc;
+    *out = acc.release();
     return acc_n;
 }
 static uint64_t join_step(Ctx *ctx, const uint64_t *probe, uint64_t n, int pcol, const JoinIndex &J, const int oc[4],
@@ -1647,8 +1715,7 @@ struct Driver {
 
     // Evaluate a rule body; rel[j] is the relation atom j reads.  Appends the
     // head tuples (bag, packed) to `out` as owned device buffers.
-    void eval_body(const Rule &r, const DRel *const *rel, std::vector<std::pair<uint64_t *, uint64_t>> &out,
-                   ProbeJob *pre) {
+    void eval_body(const Rule &r, const DRel *const *rel, Bags &out, ProbeJob *pre) {
         const Atom &a0 = r.b[0];
         XH_REQUIRE(a0.v[0] != a0.v[1], XLOG_HIP_UNSUPPORTED, "plan: repeated variable inside an atom");
         bool k0 = needed_later(r, 1, a0.v[0]), k1 = needed_later(r, 1, a0.v[1]);
@@ -1657,14 +1724,15 @@ struct Driver {
         int vars[2] = {a0.v[0], a0.v[1]};
         const uint64_t *bk = rel[0]->k;
         uint64_t bn = rel[0]->n;
-        uint64_t *owned = nullptr;
+        Owned owned(ctx);  // the binding when an earlier join of this body made it
         if (bn == 0) return;
         if (r.nb == 1) {
             // head projection of a single atom
             int h0 = (r.hv[0] == vars[0]) ? 0 : (r.hv[0] == vars[1] ? 1 : -1);
             int h1 = (r.hv[1] == vars[0]) ? 0 : (r.hv[1] == vars[1] ? 1 : -1);
             XH_REQUIRE(h0 >= 0 && h1 >= 0, XLOG_HIP_UNSUPPORTED, "plan: head variable not bound by the body");
-            uint64_t *o = static_cast<uint64_t *>(ctx->alloc(bn * sizeof(uint64_t)));
+            Owned go(ctx, static_cast<uint64_t *>(ctx->alloc(bn * sizeof(uint64_t))));
+            uint64_t *o = go.p;
             if (h0 == 0 && h1 == 1) copy_d2d(ctx, o, bk, bn);
             else if (h0 == 1 && h1 == 0) swap_words(ctx, bk, bn, o);
             else {
@@ -1673,7 +1741,7 @@ struct Driver {
                 RelOut bo{{o, nullptr, nullptr, nullptr}};
                 LAUNCH_1D(k_project, bn, bv, bn, s, bo);
             }
-            out.push_back({o, bn});
+            out.add(go, bn);
             return;
         }
         for (int j = 1; j < r.nb; ++j) {
@@ -1723,57 +1791,50 @@ struct Driver {
                     on = join_step(ctx, bk, bn, bpos, J, oc, &o, max_join_rows, digits);
                 }
             }
-            if (owned) ctx->free(owned);
-            owned = o;
+            owned.reset(o);
             bk = o;
             bn = on;
             vars[0] = cand_var[sel[0]];
             vars[1] = cand_var[sel[1]];
-            if (bn == 0) {
-                if (owned) ctx->free(owned);
-                return;
-            }
+            if (bn == 0) return;
         }
-        out.push_back({owned, bn});
+        out.add(owned, bn);
     }
 
     // concat bags, sort, unique, minus full -> new canonical delta.  The count
     // stays on the device (cnt); d.n is the candidate total, a bound on it,
     // until the caller reads the count back.
-    DRel finalize_async(std::vector<std::pair<uint64_t *, uint64_t>> &bags, const DRel &against, Buf<uint64_t> &cnt) {
-        uint64_t total = 0;
-        for (auto &b : bags) total += b.second;
+    DRel finalize_async(Bags &bags, const DRel &against, Buf<uint64_t> &cnt) {
+        const uint64_t total = bags.rows();
         DRel d;
         if (total == 0) {
-            for (auto &b : bags) ctx->free(b.first);
             bags.clear();
             return d;
         }
-        uint64_t *cat;
-        if (bags.size() == 1) {
-            cat = bags[0].first;
+        Owned cat(ctx);
+        if (bags.v.size() == 1) {
+            cat.reset(bags.v[0].first);
+            bags.v.clear();
         } else {
-            cat = static_cast<uint64_t *>(ctx->alloc(total * sizeof(uint64_t)));
+            cat.reset(alloc_keys(ctx, total));
             uint64_t off = 0;
-            for (auto &b : bags) {
-                copy_d2d(ctx, cat + off, b.first, b.second);
+            for (auto &b : bags.v) {
+                copy_d2d(ctx, cat.p + off, b.first, b.second);
                 off += b.second;
-                ctx->free(b.first);
             }
+            bags.clear();
         }
-        bags.clear();
-        uint64_t *s = sort_keys(ctx, cat, total, true, 0, 8, digits);  // consumes cat
-        uint64_t *o = static_cast<uint64_t *>(ctx->alloc(total * sizeof(uint64_t)));
+        Owned srt(ctx, sort_keys(ctx, cat.release(), total, true, 0, 8, digits));  // consumes cat
+        Owned o(ctx, alloc_keys(ctx, total));
         cnt = Buf<uint64_t>(ctx, 1);
-        select_unique_diff(ctx, s, total, against.k, against.n, o, cnt.p);
-        ctx->free(s);
+        select_unique_diff(ctx, srt.p, total, against.k, against.n, o.p, cnt.p);
         d.n = total;
-        d.k = o;
+        d.k = o.release();
         d.owned = true;
         d.version = version_counter++;
         return d;
     }
-    DRel finalize(std::vector<std::pair<uint64_t *, uint64_t>> &bags, const DRel &against) {
+    DRel finalize(Bags &bags, const DRel &against) {
         Buf<uint64_t> cnt;
         DRel d = finalize_async(bags, against, cnt);
         if (d.k) d.n = read_count(ctx, cnt.p);
@@ -1783,10 +1844,11 @@ struct Driver {
     DRel merge(const DRel &a, const DRel &b) {
         DRel m;
         m.n = a.n + b.n;
-        m.k = static_cast<uint64_t *>(ctx->alloc((m.n ? m.n : 1) * sizeof(uint64_t)));
+        Owned k(ctx, alloc_keys(ctx, m.n));
+        merge_sorted(ctx, a.k, a.n, b.k, b.n, k.p);
+        m.k = k.release();
         m.owned = true;
         m.version = version_counter++;
-        merge_sorted(ctx, a.k, a.n, b.k, b.n, m.k);
         return m;
     }
 
@@ -1817,7 +1879,7 @@ struct Driver {
     // seed: every rule once against the current store; delta = new \ old,
     // merged into full
     void seed(std::vector<uint64_t> &deltas) {
-        std::vector<std::vector<std::pair<uint64_t *, uint64_t>>> derived(n_preds);
+        std::vector<Bags> derived = bags_per_pred(ctx, n_preds);
         for (const Rule &r : rules) {
             const DRel *rel[MAX_BODY];
             for (int j = 0; j < r.nb; ++j) rel[j] = &full[r.b[j].pred];
@@ -1827,12 +1889,12 @@ struct Driver {
         for (uint32_t p = 0; p < n_preds; ++p) {
             if (!idb[p]) continue;
             DRel d = finalize(derived[p], full[p]);  // full_new \ full_old
+            delta[p] = d;  // the driver owns it from here
             if (d.n) {
                 DRel m = merge(full[p], d);
                 release(full[p]);
                 full[p] = m;
             }
-            delta[p] = d;
             total += d.n;
         }
         deltas.push_back(total);
@@ -1845,7 +1907,7 @@ struct Driver {
         uint64_t it = 0;
         while (it < max_iter) {
             cur_iter = ++it;
-            std::vector<std::vector<std::pair<uint64_t *, uint64_t>>> raw(n_preds);
+            std::vector<Bags> raw = bags_per_pred(ctx, n_preds);
             for (size_t ri = 0; ri < rules.size(); ++ri) {
                 const Rule &r = rules[ri];
                 for (int occ = 0; occ < r.nb; ++occ) {
