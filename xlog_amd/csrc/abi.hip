@@ -4,6 +4,7 @@
 #include "internal.hpp"
 
 #include <algorithm>
+#include <array>
 #include <chrono>
 #include <cerrno>
 #include <cstdio>
@@ -1629,6 +1630,8 @@ static uint64_t env_u64(const char *name, uint64_t dflt) {
     return dflt;
 }
 
+static uint64_t device_room(Ctx *ctx);
+
 // ---------------------------------------------------------------------------
 // semi-naive fixpoint driver (Executor::execute_recursive_scc,
 // crates/xlog-runtime/src/executor/recursive.rs:447-957)
@@ -1663,6 +1666,98 @@ bool needed_later(const Rule &r, int from, int var) {
     for (int j = from; j < r.nb; ++j)
         if (r.b[j].v[0] == var || r.b[j].v[1] == var) return true;
     return false;
+}
+
+// The join steps of a rule body, left-deep in body order (each atom after
+// the first shares one variable with the running binding, which keeps the two
+// variables a later atom or the head reads).  Step j >= 1 joins binding
+// column bpos with column apos of atom j and keeps candidate values sel[0],
+// sel[1] of (binding 0, binding 1, shared, atom's other); a one-atom body
+// projects its columns head[0], head[1].
+struct JoinPlanStep {
+    int bpos = 0, apos = 0, sel[2] = {0, 0};
+};
+struct BodyPlan {
+    JoinPlanStep step[MAX_BODY];
+    int head[2] = {0, 1};
+};
+BodyPlan plan_body(const Rule &r) {
+    BodyPlan bp;
+    const Atom &a0 = r.b[0];
+    XH_REQUIRE(a0.v[0] != a0.v[1], XLOG_HIP_UNSUPPORTED, "plan: repeated variable inside an atom");
+    bool k0 = needed_later(r, 1, a0.v[0]), k1 = needed_later(r, 1, a0.v[1]);
+    XH_REQUIRE(k0 && k1, XLOG_HIP_UNSUPPORTED, "plan: first atom must bind two live variables");
+    int vars[2] = {a0.v[0], a0.v[1]};
+    if (r.nb == 1) {
+        int h0 = (r.hv[0] == vars[0]) ? 0 : (r.hv[0] == vars[1] ? 1 : -1);
+        int h1 = (r.hv[1] == vars[0]) ? 0 : (r.hv[1] == vars[1] ? 1 : -1);
+        XH_REQUIRE(h0 >= 0 && h1 >= 0, XLOG_HIP_UNSUPPORTED, "plan: head variable not bound by the body");
+        bp.head[0] = h0;
+        bp.head[1] = h1;
+        return bp;
+    }
+    for (int j = 1; j < r.nb; ++j) {
+        const Atom &a = r.b[j];
+        XH_REQUIRE(a.v[0] != a.v[1], XLOG_HIP_UNSUPPORTED, "plan: repeated variable inside an atom");
+        int bpos = -1, apos = -1, nshared = 0;
+        for (int x = 0; x < 2; ++x)
+            for (int y = 0; y < 2; ++y)
+                if (vars[x] == a.v[y]) { bpos = x; apos = y; ++nshared; }
+        XH_REQUIRE(nshared == 1, XLOG_HIP_UNSUPPORTED, "plan: each atom must share exactly one variable");
+        int other = a.v[1 - apos];
+        // candidate values: v0 = binding var 0, v1 = binding var 1, v2 = shared, v3 = other
+        int cand_var[4] = {vars[0], vars[1], a.v[apos], other};
+        int sel[2], ns = 0;
+        if (j == r.nb - 1) {
+            for (int t = 0; t < 2; ++t) {
+                int f = -1;
+                for (int c = 0; c < 4; ++c) if (cand_var[c] == r.hv[t]) { f = c; break; }
+                XH_REQUIRE(f >= 0, XLOG_HIP_UNSUPPORTED, "plan: head variable not bound by the body");
+                sel[ns++] = f;
+            }
+        } else {
+            int seen[4] = {-1, -1, -1, -1}, nseen = 0;
+            for (int c = 0; c < 4; ++c) {
+                int v = cand_var[c];
+                bool dup = false;
+                for (int q = 0; q < nseen; ++q) if (seen[q] == v) dup = true;
+                if (dup) continue;
+                seen[nseen++] = v;
+                if (needed_later(r, j + 1, v)) {
+                    XH_REQUIRE(ns < 2, XLOG_HIP_UNSUPPORTED, "plan: more than two live variables");
+                    sel[ns++] = c;
+                }
+            }
+            XH_REQUIRE(ns == 2, XLOG_HIP_UNSUPPORTED, "plan: intermediate binding must keep two variables");
+        }
+        bp.step[j].bpos = bpos;
+        bp.step[j].apos = apos;
+        bp.step[j].sel[0] = sel[0];
+        bp.step[j].sel[1] = sel[1];
+        vars[0] = cand_var[sel[0]];
+        vars[1] = cand_var[sel[1]];
+    }
+    return bp;
+}
+
+// Scalars of a queue of iterations (Driver::run_queue) live in one device
+// array that is read back at once; word 0 holds the stop flag (0, or the
+// queue position + 1 of the first iteration that could not run within its
+// bounds).  These single-thread kernels check a count against its bound and
+// keep the sums the next launches read.
+__global__ void k_q_check(const uint64_t *a, const uint64_t *b, uint64_t cap, uint32_t *stop, uint32_t code) {
+    const uint64_t v = *a + (b ? *b : 0ull);
+    if (v > cap) atomicCAS(stop, 0u, code);
+}
+__global__ void k_q_add(uint64_t *dst, const uint64_t *a, const uint64_t *b, const uint32_t *stop) {
+    if (*stop) return;
+    *dst = *a + (b ? *b : 0ull);
+}
+__global__ void k_q_sum(uint64_t *dst, const uint64_t *src, uint32_t count, const uint32_t *stop) {
+    if (*stop) return;
+    uint64_t t = 0;
+    for (uint32_t i = 0; i < count; ++i) t += src[i];
+    *dst = t;
 }
 
 // device-resident canonical packed relation
@@ -1715,22 +1810,24 @@ struct Driver {
 
     // Evaluate a rule body; rel[j] is the relation atom j reads.  Appends the
     // head tuples (bag, packed) to `out` as owned device buffers.
-    void eval_body(const Rule &r, const DRel *const *rel, Bags &out, ProbeJob *pre) {
-        const Atom &a0 = r.b[0];
-        XH_REQUIRE(a0.v[0] != a0.v[1], XLOG_HIP_UNSUPPORTED, "plan: repeated variable inside an atom");
-        bool k0 = needed_later(r, 1, a0.v[0]), k1 = needed_later(r, 1, a0.v[1]);
-        XH_REQUIRE(k0 && k1, XLOG_HIP_UNSUPPORTED, "plan: first atom must bind two live variables");
-        // binding: packed (vars[0], vars[1])
-        int vars[2] = {a0.v[0], a0.v[1]};
+    // Rows in and out of every join step of every rule body, from the last
+    // evaluation that ran it: the queued iterations size their bounds from
+    // these ratios.  obs[ri][j] = {left rows, output rows} of step j >= 1.
+    std::vector<std::array<std::pair<uint64_t, uint64_t>, MAX_BODY>> obs;
+    // per predicate: the share of its candidates that were new in its last
+    // iteration with candidates (the queued iterations' delta estimate)
+    std::vector<double> nov;
+
+    // ri >= 0: record the join steps' sizes in obs[ri]
+    void eval_body(const Rule &r, const DRel *const *rel, Bags &out, ProbeJob *pre, int ri = -1) {
+        const BodyPlan bp = plan_body(r);
         const uint64_t *bk = rel[0]->k;
         uint64_t bn = rel[0]->n;
         Owned owned(ctx);  // the binding when an earlier join of this body made it
         if (bn == 0) return;
         if (r.nb == 1) {
             // head projection of a single atom
-            int h0 = (r.hv[0] == vars[0]) ? 0 : (r.hv[0] == vars[1] ? 1 : -1);
-            int h1 = (r.hv[1] == vars[0]) ? 0 : (r.hv[1] == vars[1] ? 1 : -1);
-            XH_REQUIRE(h0 >= 0 && h1 >= 0, XLOG_HIP_UNSUPPORTED, "plan: head variable not bound by the body");
+            const int h0 = bp.head[0], h1 = bp.head[1];
             Owned go(ctx, static_cast<uint64_t *>(ctx->alloc(bn * sizeof(uint64_t))));
             uint64_t *o = go.p;
             if (h0 == 0 && h1 == 1) copy_d2d(ctx, o, bk, bn);
@@ -1745,57 +1842,23 @@ struct Driver {
             return;
         }
         for (int j = 1; j < r.nb; ++j) {
-            const Atom &a = r.b[j];
-            XH_REQUIRE(a.v[0] != a.v[1], XLOG_HIP_UNSUPPORTED, "plan: repeated variable inside an atom");
-            int bpos = -1, apos = -1, nshared = 0;
-            for (int x = 0; x < 2; ++x)
-                for (int y = 0; y < 2; ++y)
-                    if (vars[x] == a.v[y]) { bpos = x; apos = y; ++nshared; }
-            XH_REQUIRE(nshared == 1, XLOG_HIP_UNSUPPORTED, "plan: each atom must share exactly one variable");
-            int other = a.v[1 - apos];
-            // candidate values: v0 = binding var 0, v1 = binding var 1, v2 = shared, v3 = other
-            int cand_var[4] = {vars[0], vars[1], a.v[apos], other};
-            int sel[2], ns = 0;
-            bool last = (j == r.nb - 1);
-            if (last) {
-                for (int t = 0; t < 2; ++t) {
-                    int f = -1;
-                    for (int c = 0; c < 4; ++c) if (cand_var[c] == r.hv[t]) { f = c; break; }
-                    XH_REQUIRE(f >= 0, XLOG_HIP_UNSUPPORTED, "plan: head variable not bound by the body");
-                    sel[ns++] = f;
-                }
-            } else {
-                int seen[4] = {-1, -1, -1, -1}, nseen = 0;
-                for (int c = 0; c < 4; ++c) {
-                    int v = cand_var[c];
-                    bool dup = false;
-                    for (int q = 0; q < nseen; ++q) if (seen[q] == v) dup = true;
-                    if (dup) continue;
-                    seen[nseen++] = v;
-                    if (needed_later(r, j + 1, v)) {
-                        XH_REQUIRE(ns < 2, XLOG_HIP_UNSUPPORTED, "plan: more than two live variables");
-                        sel[ns++] = c;
-                    }
-                }
-                XH_REQUIRE(ns == 2, XLOG_HIP_UNSUPPORTED, "plan: intermediate binding must keep two variables");
-            }
+            const JoinPlanStep &st = bp.step[j];
             const DRel &ar = *rel[j];
             uint64_t *o = nullptr;
             uint64_t on = 0;
             if (ar.n != 0) {
-                int oc[4] = {sel[0], sel[1], 0, 0};
+                int oc[4] = {st.sel[0], st.sel[1], 0, 0};
                 if (j == 1 && pre) {  // the count pass ran with the delta's count still on the device
                     on = join_emit(ctx, *pre, oc, &o, max_join_rows, digits);
                 } else {
-                    const JoinIndex &J = index_of(ar, apos);
-                    on = join_step(ctx, bk, bn, bpos, J, oc, &o, max_join_rows, digits);
+                    const JoinIndex &J = index_of(ar, st.apos);
+                    on = join_step(ctx, bk, bn, st.bpos, J, oc, &o, max_join_rows, digits);
                 }
             }
+            if (ri >= 0 && ri < (int)obs.size()) obs[ri][j] = {bn, on};
             owned.reset(o);
             bk = o;
             bn = on;
-            vars[0] = cand_var[sel[0]];
-            vars[1] = cand_var[sel[1]];
             if (bn == 0) return;
         }
         out.add(owned, bn);
@@ -1879,6 +1942,8 @@ struct Driver {
     // seed: every rule once against the current store; delta = new \ old,
     // merged into full
     void seed(std::vector<uint64_t> &deltas) {
+        obs.assign(rules.size(), {});
+        nov.assign(n_preds, 1.0);
         std::vector<Bags> derived = bags_per_pred(ctx, n_preds);
         for (const Rule &r : rules) {
             const DRel *rel[MAX_BODY];
@@ -1900,8 +1965,444 @@ struct Driver {
         deltas.push_back(total);
     }
 
+    // One iteration with its sizes read back (the variants, Δ' = sort+unique(∪
+    // variants) \ R, R ∪= Δ'); returns the iteration's Δ total.
+    // rs: the rules with the queue's body order (queue_rules), whose join
+    // steps' sizes are recorded for the queue's bounds
+    uint64_t iterate_host(uint64_t it, std::vector<uint64_t> &deltas, const std::vector<Rule> &rs) {
+        cur_iter = it;
+        std::vector<Bags> raw = bags_per_pred(ctx, n_preds);
+        for (size_t ri = 0; ri < rs.size(); ++ri) {
+            const Rule &r = rs[ri];
+            for (int occ = 0; occ < r.nb; ++occ) {
+                int p = r.b[occ].pred;
+                if (!idb[p] || delta[p].n == 0) continue;
+                const DRel *rel[MAX_BODY];
+                for (int j = 0; j < r.nb; ++j) {
+                    int q = r.b[j].pred;
+                    rel[j] = (j == occ) ? &delta[q] : &full[q];
+                }
+                eval_body(r, rel, raw[r.head], nullptr, (int)ri);
+            }
+        }
+        uint64_t total = 0;
+        for (uint32_t p = 0; p < n_preds; ++p) {
+            if (!idb[p]) continue;
+            const uint64_t cand = raw[p].rows();
+            DRel d = finalize(raw[p], full[p]);
+            release(delta[p]);
+            delta[p] = d;
+            total += d.n;
+            if (cand) nov[p] = (double)d.n / (double)cand;
+        }
+        deltas.push_back(total);
+        if (total == 0) return 0;
+        for (uint32_t p = 0; p < n_preds; ++p) {
+            if (!idb[p] || delta[p].n == 0) continue;
+            DRel m = merge(full[p], delta[p]);
+            release(full[p]);
+            full[p] = m;
+        }
+        return total;
+    }
+
+    // ---- queued iterations --------------------------------------------------
+    // A plan whose every recursive rule reads one IDB atom, first, and EDB
+    // atoms after it (transitive closure and other linear programs): each
+    // iteration's variants start from a delta and probe indexes that never
+    // change, so whole iterations can be queued with every row count left on
+    // the device and one read-back per queue.  Each launch of a queued
+    // iteration is sized for a bound the host estimates from the sizes seen so
+    // far (every join step's rows out per row in, and the share of each
+    // head's candidates that were new); a
+    // small check kernel compares each device count with its bound before the
+    // launches that rely on it and, when it is exceeded (or a join passes the
+    // join-row limit or the single-sort size), raises the queue's stop flag
+    // with the iteration's number: every later launch of the queue then
+    // returns at once.  The host takes the iterations before it as they are
+    // and runs that iteration with its sizes read back (iterate_host: the same
+    // operators, which also raise the limit's error), then queues again.
+    // Relations and deltas alternate between two buffers per predicate, so a
+    // stopped iteration never overwrites the state it started from; an
+    // iteration that derives nothing rewrites nothing (its merges are
+    // skipped), so the queued iterations after the fixpoint change nothing.
+    // A rule whose one IDB atom is not first is evaluated from it: the body
+    // starts at that atom and takes, each step, the first remaining atom that
+    // shares a variable with those already joined (same-generation's
+    // sg(X,Y) :- up(X,P), sg(P,Q), down(Q,Y) runs sg, up, down).  The derived
+    // set is the same in any order; only the sizes of intermediate bags
+    // differ, so with a join-row limit (defined on the bags of the body's own
+    // order, relational.rs:4550-4555) only bodies that start with their IDB
+    // atom are queued.  qr receives the rules in the order they run.
+    bool queue_rules(std::vector<Rule> &qr) const {
+        qr = rules;
+        bool any = false;
+        for (Rule &r : qr) {
+            int n_idb = 0, at = -1;
+            for (int j = 0; j < r.nb; ++j)
+                if (idb[r.b[j].pred]) {
+                    ++n_idb;
+                    at = j;
+                }
+            if (n_idb == 0) continue;
+            if (n_idb != 1 || r.nb < 2) return false;
+            if (at != 0) {
+                if (max_join_rows) return false;
+                const Rule orig = r;
+                bool used[MAX_BODY] = {false, false, false, false};
+                std::vector<int> seen{orig.b[at].v[0], orig.b[at].v[1]};
+                r.b[0] = orig.b[at];
+                used[at] = true;
+                for (int pos = 1; pos < orig.nb; ++pos) {
+                    int pick = -1;
+                    for (int j = 0; j < orig.nb && pick < 0; ++j) {
+                        if (used[j]) continue;
+                        for (int v : seen)
+                            if (orig.b[j].v[0] == v || orig.b[j].v[1] == v) pick = j;
+                    }
+                    if (pick < 0) return false;
+                    used[pick] = true;
+                    r.b[pos] = orig.b[pick];
+                    seen.push_back(orig.b[pick].v[0]);
+                    seen.push_back(orig.b[pick].v[1]);
+                }
+            }
+            try {
+                (void)plan_body(r);
+            } catch (const Error &) {
+                return false;  // this order has no left-deep plan: the host loop takes the program
+            }
+            any = true;
+        }
+        return any;
+    }
+
+    struct QVariant {
+        int ri = 0, head = 0, dpred = 0;  // rule, head predicate, delta predicate (atom 0)
+        BodyPlan bp;
+        const JoinIndex *J[MAX_BODY] = {};
+        ProbeJob job[MAX_BODY];
+        Owned tmp[MAX_BODY] = {Owned(nullptr), Owned(nullptr), Owned(nullptr), Owned(nullptr)};
+        uint32_t tot_slot = 0;  // first of its (nb - 1) join-total slots in an iteration's block
+    };
+
+    uint64_t run_queued(uint64_t max_iter, std::vector<uint64_t> &deltas, const std::vector<Rule> &qr) {
+        const uint64_t qmax = std::min<uint64_t>(env_u64("XLOG_HIP_JOIN_QUEUE", 8), 64);
+        std::vector<int> heads, hidx(n_preds, -1);
+        for (uint32_t p = 0; p < n_preds; ++p)
+            if (idb[p]) {
+                hidx[p] = (int)heads.size();
+                heads.push_back((int)p);
+            }
+        uint64_t it = 0;
+        bool host_ran = false;  // the join steps' ratios come from an iteration run from the host first
+        while (it < max_iter) {
+            if (host_ran) {
+                const uint64_t done =
+                    run_queue(std::min<uint64_t>(qmax, max_iter - it), it, heads, hidx, deltas, qr);
+                if (done == ~0ull) return it;  // converged inside the queue (it counts the empty iteration)
+                if (done > 0) continue;
+            }
+            // the first iteration, one whose queue stopped at once, or one for which no queue fits
+            ++it;
+            host_ran = true;
+            if (iterate_host(it, deltas, qr) == 0) return it;
+        }
+        cur_iter = it;
+        throw Error{XLOG_HIP_ITERATION_LIMIT,
+                    "Recursive SCC iteration limit (" + std::to_string(max_iter) + ") exceeded"};
+    }
+
+    // Queues up to qn iterations after iteration `it`.  Returns the number of
+    // iterations it completed (it is advanced by them, deltas extended),
+    // or ~0 when the fixpoint was reached inside the queue.  A stop at queue
+    // position f > 0 leaves the state after iteration it + f; the caller then
+    // continues (the stopped iteration is queued again or run from the host).
+    uint64_t run_queue(uint64_t qn, uint64_t &it, const std::vector<int> &heads, const std::vector<int> &hidx,
+                       std::vector<uint64_t> &deltas, const std::vector<Rule> &qr) {
+        const uint32_t H = (uint32_t)heads.size();
+        // the variants (one per recursive rule, its IDB atom first) and their fixed indexes
+        std::vector<std::unique_ptr<QVariant>> vars;
+        uint32_t tot_words = 0;
+        for (size_t ri = 0; ri < qr.size(); ++ri) {
+            const Rule &r = qr[ri];
+            if (!idb[r.b[0].pred]) continue;
+            bool empty_edb = false;
+            for (int j = 1; j < r.nb; ++j) empty_edb = empty_edb || full[r.b[j].pred].n == 0;
+            if (empty_edb) continue;  // derives nothing, ever
+            std::unique_ptr<QVariant> v(new QVariant());
+            for (auto &o : v->tmp) o.ctx = ctx;
+            v->ri = (int)ri;
+            v->head = r.head;
+            v->dpred = r.b[0].pred;
+            v->bp = plan_body(r);
+            for (int j = 1; j < r.nb; ++j) v->J[j] = &index_of(full[r.b[j].pred], v->bp.step[j].apos);
+            v->tot_slot = 3 * H + 1 + tot_words;
+            tot_words += (uint32_t)(r.nb - 1);
+            vars.push_back(std::move(v));
+        }
+        const uint32_t B = 3 * H + 1 + tot_words;  // words per iteration block
+        auto blk = [&](int64_t k) { return (uint64_t)1 + (uint64_t)(k + 1) * B; };
+        // every block comes back in one read of the pinned staging
+        const uint64_t fit = (Ctx::HOST_STAGE_U64 - 1) / B;  // blocks that fit, the starting one included
+        if (fit < 3) return 0;
+        qn = std::min<uint64_t>(qn, fit - 1);
+
+        // ---- bounds ------------------------------------------------------------
+        // rows out per row in of every join step from its last evaluation (4
+        // when never seen); a head's next delta is its candidates times the
+        // share of them that was new in its last iteration with candidates
+        auto fan = [&](const QVariant &v, int j) {
+            const auto &o = obs[v.ri][j];
+            return o.first ? std::max(1.0 / 64.0, (double)o.second / (double)o.first) : 4.0;
+        };
+        // per-step margin over the estimates and a floor on every bound; tests shrink both
+        // (XLOG_HIP_JOIN_QUEUE_MARGIN_PCT, XLOG_HIP_JOIN_QUEUE_SLACK) to make queues stop
+        const double M = (double)env_u64("XLOG_HIP_JOIN_QUEUE_MARGIN_PCT", 125) / 100.0;
+        const uint64_t SLACK = env_u64("XLOG_HIP_JOIN_QUEUE_SLACK", 4096), SORT_MAX = (1ull << 30) - 1;
+        // Lb[k][h]: bound on the delta iteration k reads; T[k][v][j]: join outputs; Cb[k][h]: candidates;
+        // Rb[k][h]: R after iteration k (Rb[-1] exact: stored at index 0, iteration k at k + 1)
+        std::vector<std::vector<uint64_t>> Lb, Cb, Rb;
+        std::vector<std::vector<std::array<uint64_t, MAX_BODY>>> T;
+        Rb.push_back({});
+        for (int p : heads) Rb[0].push_back(full[p].n);
+        std::vector<uint64_t> cur(H);
+        for (uint32_t h = 0; h < H; ++h) cur[h] = delta[heads[h]].n;  // exact for the first
+        const uint64_t room = device_room(ctx) / 2;
+        uint64_t q = 0;
+        for (; q < qn; ++q) {
+            std::vector<uint64_t> lb = cur, cb(H, 0), rb(H, 0);
+            std::vector<std::array<uint64_t, MAX_BODY>> tv(vars.size());
+            bool fits = true;
+            for (size_t vi = 0; vi < vars.size(); ++vi) {
+                const QVariant &v = *vars[vi];
+                const Rule &r = qr[v.ri];
+                double t = (double)lb[hidx[v.dpred]];
+                for (int j = 1; j < r.nb; ++j) {
+                    t = t * fan(v, j) * M + (double)SLACK;
+                    tv[vi][j] = t > 1e18 ? (uint64_t)1e18 : (uint64_t)t;
+                    fits = fits && tv[vi][j] <= SORT_MAX;
+                }
+                cb[hidx[v.head]] += tv[vi][r.nb - 1];
+            }
+            for (uint32_t h = 0; h < H; ++h) fits = fits && cb[h] <= SORT_MAX;
+            // next deltas, and R after this iteration
+            std::vector<uint64_t> nxt(H);
+            for (uint32_t h = 0; h < H; ++h) {
+                // (a delta never exceeds its head's candidates)
+                const double e = (double)cb[h] * nov[heads[h]];
+                nxt[h] = std::min<uint64_t>(std::max<uint64_t>(e > 1e18 ? (uint64_t)1e18 : (uint64_t)e, SLACK), cb[h]);
+                rb[h] = Rb.back()[h] + nxt[h];
+            }
+            // device bytes of the queue's buffers with this iteration in it
+            uint64_t bytes = 0;
+            for (uint32_t h = 0; h < H; ++h) {
+                uint64_t mc = cb[h], mr = rb[h];
+                for (auto &c : Cb) mc = std::max(mc, c[h]);
+                bytes += 8 * (4 * mc + 2 * mr);
+            }
+            for (size_t vi = 0; vi < vars.size(); ++vi) {
+                const Rule &r = qr[vars[vi]->ri];
+                for (int j = 1; j < r.nb; ++j) {
+                    uint64_t mt = tv[vi][j], ml = j == 1 ? lb[hidx[vars[vi]->dpred]] : tv[vi][j - 1];
+                    for (size_t k = 0; k < T.size(); ++k) {
+                        mt = std::max(mt, T[k][vi][j]);
+                        ml = std::max(ml, j == 1 ? Lb[k][hidx[vars[vi]->dpred]] : T[k][vi][j - 1]);
+                    }
+                    bytes += 12 * ml + (j < r.nb - 1 ? 8 * mt : 0);
+                }
+            }
+            if (!fits || bytes > room) break;
+            Lb.push_back(lb);
+            T.push_back(tv);
+            Cb.push_back(cb);
+            Rb.push_back(rb);
+            cur = nxt;
+        }
+        if (q < 2) return 0;  // a queue of fewer than two iterations gains nothing over the host loop
+        const uint64_t Q = q;
+
+        // ---- buffers -------------------------------------------------------------
+        struct QHead {
+            Owned C, Calt, D[2], R[2];
+            explicit QHead(Ctx *c) : C(c), Calt(c), D{Owned(c), Owned(c)}, R{Owned(c), Owned(c)} {}
+        };
+        std::vector<std::unique_ptr<QHead>> qh;
+        for (uint32_t h = 0; h < H; ++h) {
+            uint64_t mc = 0;
+            for (uint64_t k = 0; k < Q; ++k) mc = std::max(mc, Cb[k][h]);
+            std::unique_ptr<QHead> x(new QHead(ctx));
+            x->C.reset(alloc_keys(ctx, mc));
+            x->Calt.reset(alloc_keys(ctx, mc));
+            x->D[0].reset(alloc_keys(ctx, mc));
+            x->D[1].reset(alloc_keys(ctx, mc));
+            x->R[0].reset(alloc_keys(ctx, Rb[Q][h]));
+            x->R[1].reset(alloc_keys(ctx, Rb[Q][h]));
+            qh.push_back(std::move(x));
+        }
+        for (size_t vi = 0; vi < vars.size(); ++vi) {
+            QVariant &v = *vars[vi];
+            const Rule &r = qr[v.ri];
+            for (int j = 1; j + 1 < r.nb; ++j) {
+                uint64_t mt = 0;
+                for (uint64_t k = 0; k < Q; ++k) mt = std::max(mt, T[k][vi][j]);
+                v.tmp[j].reset(alloc_keys(ctx, mt));
+            }
+        }
+        const uint64_t words = blk((int64_t)Q);  // word 0 (stop) + Q + 1 blocks
+        Buf<uint64_t> qs(ctx, words);
+        fill_u64(ctx, qs.p, 0ull, words);
+        uint32_t *stop = reinterpret_cast<uint32_t *>(qs.p);
+        // block -1: the sizes the queue starts from
+        for (uint32_t h = 0; h < H; ++h) {
+            fill_u64(ctx, qs.p + blk(-1) + h, delta[heads[h]].n, 1);
+            fill_u64(ctx, qs.p + blk(-1) + H + h, full[heads[h]].n, 1);
+        }
+        auto check = [&](const uint64_t *a, const uint64_t *b, uint64_t cap, uint64_t k) {
+            hipLaunchKernelGGL(k_q_check, dim3(1), dim3(1), 0, ctx->stream, a, b, cap, stop, (uint32_t)(k + 1));
+            XH_CHECK_HIP(hipGetLastError());
+        };
+        auto add = [&](uint64_t *dst, const uint64_t *a, const uint64_t *b) {
+            hipLaunchKernelGGL(k_q_add, dim3(1), dim3(1), 0, ctx->stream, dst, a, b, stop);
+            XH_CHECK_HIP(hipGetLastError());
+        };
+
+        // ---- the queue -------------------------------------------------------------
+        cur_iter = it + 1;
+        for (uint64_t k = 0; k < Q; ++k) {
+            uint64_t *bk = qs.p + blk((int64_t)k), *bp = qs.p + blk((int64_t)k - 1);
+            uint64_t *nD = bk, *nR = bk + H, *cbase = bk + 2 * H, *total = bk + 3 * H;
+            const uint64_t *pD = bp, *pR = bp + H;
+            for (uint32_t h = 0; h < H; ++h) fill_u64(ctx, cbase + h, 0ull, 1);
+            // the deltas this iteration reads must fit the bounds its probes are sized for
+            if (k > 0)
+                for (uint32_t h = 0; h < H; ++h) check(pD + h, nullptr, Lb[k][h], k);
+            for (size_t vi = 0; vi < vars.size(); ++vi) {
+                QVariant &v = *vars[vi];
+                const Rule &r = qr[v.ri];
+                const int dh_ = hidx[v.dpred], hh = hidx[v.head];
+                const uint64_t *left = k == 0 ? delta[v.dpred].k : qh[dh_]->D[(k - 1) & 1].p;
+                const uint64_t *d_left = pD + dh_;
+                uint64_t left_bound = Lb[k][dh_];
+                if (k == 0 && !left) left_bound = 0;
+                for (int j = 1; j < r.nb; ++j) {
+                    const JoinPlanStep &st = v.bp.step[j];
+                    ProbeJob &job = v.job[j];
+                    job = ProbeJob();
+                    job.probe = left;
+                    job.pcol = st.bpos;
+                    job.ix = &v.J[j]->ix;
+                    job.payload = v.J[j]->payload.p;
+                    probe_prepare_deferred(ctx, job, left_bound, d_left, stop);
+                    const uint64_t *d_tot = job.toff.p + job.tiles;
+                    const bool last = j == r.nb - 1;
+                    // the output must fit its buffer (and the launches after it their bounds), a join the
+                    // limit, and the candidates one sort
+                    if (last) check(cbase + hh, d_tot, Cb[k][hh], k);
+                    else check(d_tot, nullptr, T[k][vi][j], k);
+                    if (max_join_rows) check(d_tot, nullptr, max_join_rows, k);
+                    const int oc[4] = {st.sel[0], st.sel[1], 0, 0};
+                    uint64_t *out = last ? qh[hh]->C.p : v.tmp[j].p;
+                    probe_emit_dev(ctx, job, d_left, oc, out, last ? cbase + hh : nullptr, stop);
+                    add(bk + v.tot_slot + (j - 1), d_tot, nullptr);
+                    if (last) add(cbase + hh, cbase + hh, d_tot);
+                    left = out;
+                    d_left = d_tot;
+                    left_bound = T[k][vi][j];
+                }
+            }
+            // per head: sort the candidates, keep the unique ones not in R
+            for (uint32_t h = 0; h < H; ++h) {
+                const int p = heads[h];
+                uint64_t *ka = qh[h]->C.p, *kb = qh[h]->Calt.p;
+                radix_sort_dev(ctx, &ka, &kb, Cb[k][h], cbase + h, digits, stop);
+                const uint64_t *rin = k == 0 ? full[p].k : qh[h]->R[(k - 1) & 1].p;
+                if (!rin) rin = qh[h]->R[1].p;  // an empty R read through its device count
+                select_unique_diff_dev(ctx, ka, Cb[k][h], cbase + h, rin, std::max<uint64_t>(Rb[k][h], 1), pR + h,
+                                       qh[h]->D[k & 1].p, nD + h, stop);
+            }
+            hipLaunchKernelGGL(k_q_sum, dim3(1), dim3(1), 0, ctx->stream, total, nD, H, stop);
+            XH_CHECK_HIP(hipGetLastError());
+            // per head: R ∪= Δ' into the other buffer (nothing when the iteration derived nothing)
+            for (uint32_t h = 0; h < H; ++h) {
+                const int p = heads[h];
+                check(pR + h, nD + h, Rb[k + 1][h], k);
+                const uint64_t *rin = k == 0 ? full[p].k : qh[h]->R[(k - 1) & 1].p;
+                if (!rin) rin = qh[h]->R[1].p;
+                merge_sorted_dev(ctx, rin, Rb[k][h], pR + h, qh[h]->D[k & 1].p, Cb[k][h], nD + h,
+                                 qh[h]->R[k & 1].p, total, stop);
+                add(nR + h, pR + h, nD + h);
+            }
+        }
+        ctx->read_scalars(qs.p, words);
+        const uint64_t *hs = ctx->host_scalars;
+        const uint32_t stopped = (uint32_t)hs[0];  // 0, or queue position + 1
+        const uint64_t complete = stopped ? (uint64_t)stopped - 1 : Q;
+
+        // ---- the completed iterations ----------------------------------------------------
+        int64_t last = -1;  // the last completed queue position
+        bool converged = false;
+        for (uint64_t k = 0; k < complete; ++k) {
+            const uint64_t *bk = hs + blk((int64_t)k);
+            const uint64_t *bp = hs + blk((int64_t)k - 1);
+            ++it;
+            uint64_t tot = 0;
+            for (uint32_t h = 0; h < H; ++h) tot += bk[h];
+            deltas.push_back(tot);
+            for (uint32_t h = 0; h < H; ++h)
+                if (bk[2 * H + h]) nov[heads[h]] = (double)bk[h] / (double)bk[2 * H + h];
+            for (auto &vp : vars) {
+                const Rule &r = qr[vp->ri];
+                uint64_t in = bp[hidx[vp->dpred]];
+                for (int j = 1; j < r.nb; ++j) {
+                    const uint64_t o = bk[vp->tot_slot + (j - 1)];
+                    if (in) obs[vp->ri][j] = {in, o};
+                    in = o;
+                }
+            }
+            if (tot == 0) {
+                converged = true;
+                break;
+            }
+            last = (int64_t)k;
+        }
+        // hand the state after the last completed iteration to the driver
+        if (last >= 0) {
+            const uint64_t *bk = hs + blk(last);
+            for (uint32_t h = 0; h < H; ++h) {
+                const int p = heads[h];
+                release(full[p]);
+                full[p].n = bk[H + h];
+                full[p].k = qh[h]->R[last & 1].release();
+                full[p].owned = true;
+                full[p].version = version_counter++;
+            }
+        }
+        if (converged || last >= 0) {
+            // the deltas after the last completed iteration (all empty when converged)
+            const int64_t kd = converged ? (int64_t)(complete > 0 ? std::min<uint64_t>(complete - 1, Q - 1) : 0) : last;
+            const uint64_t *bk = hs + blk(kd);
+            for (uint32_t h = 0; h < H; ++h) {
+                const int p = heads[h];
+                if (converged) {
+                    release(delta[p]);
+                    continue;
+                }
+                release(delta[p]);
+                delta[p].n = bk[h];
+                delta[p].k = qh[h]->D[kd & 1].release();
+                delta[p].owned = true;
+                delta[p].version = version_counter++;
+            }
+        }
+        if (converged) return ~0ull;
+        return (uint64_t)(last + 1);
+    }
+
     uint64_t run(uint64_t max_iter, std::vector<uint64_t> &deltas) {
         seed(deltas);
+        std::vector<Rule> qr;
+        if (env_u64("XLOG_HIP_JOIN_QUEUE", 8) >= 2 && queue_rules(qr)) return run_queued(max_iter, deltas, qr);
         // count jobs of the next iteration's pre-countable first joins, by (rule, occurrence)
         std::map<std::pair<int, int>, std::unique_ptr<ProbeJob>> pre;
         uint64_t it = 0;

@@ -316,6 +316,19 @@ bool sort_tickets();
 int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **vals, uint32_t **vals_alt,
                    uint64_t n, int digit_lo = 0, int digit_hi = 8, const uint64_t *src = nullptr,
                    uint32_t known_digits = 0, SortUnique *uq = nullptr);
+// A keys-only sort of a queued iteration: the key count on the device
+// (*d_n <= n_bound, the bound the launches are sized for), exactly the digit
+// passes of known_digits (no read-back), and the stop flag (a raised flag:
+// nothing is done).  Returns the number of passes: *keys and *keys_alt are
+// swapped once per pass, as in radix_sort_u64.
+// Profiling of a launch sized by bounds: adds wa * min(*d_a, a) + wb *
+// min(*d_b, b) (a device count given as null counts its bound) to the
+// launch's work counter, unless *stop is raised or *skip is zero; nothing
+// without a counter.
+void add_work_rows(Ctx *ctx, unsigned long long *work, const uint64_t *d_a, uint64_t a, uint32_t wa, const uint64_t *d_b,
+                   uint64_t b, uint32_t wb, const uint64_t *skip, const uint32_t *stop);
+int radix_sort_dev(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint64_t n_bound, const uint64_t *d_n,
+                   uint32_t known_digits, const uint32_t *stop);
 // sort_short_runs fused with the adjacent-compare unique: the unique keys in
 // order to `out`, their count to *d_count (device); a run longer than 256
 // keys sets *d_long and the output is then incomplete.  Its tiles take their
@@ -337,6 +350,11 @@ void select_unique(Ctx *ctx, const uint64_t *k, uint64_t n, uint64_t *out, uint6
 void select_unique_low(Ctx *ctx, const uint64_t *k, uint64_t n, uint64_t *out, uint32_t *low, uint64_t *d_count);
 void select_unique_diff(Ctx *ctx, const uint64_t *k, uint64_t n, const uint64_t *b, uint64_t nb,
                         uint64_t *out, uint64_t *d_count);
+// The same with the row counts of k and b on the device (d_n, d_nb; n and nb
+// are then the bounds the launches are sized for; b must be a valid pointer)
+// and the stop flag of a queued iteration (a raised flag: nothing is done).
+void select_unique_diff_dev(Ctx *ctx, const uint64_t *k, uint64_t n, const uint64_t *d_n, const uint64_t *b,
+                            uint64_t nb, const uint64_t *d_nb, uint64_t *out, uint64_t *d_count, const uint32_t *stop);
 void select_flags(Ctx *ctx, const uint64_t *k, const uint8_t *flags, uint64_t n, uint64_t *out,
                   uint64_t *d_count);
 //   not_value:   keep k[i] if k[i] != v
@@ -355,6 +373,11 @@ void scan_u32_inplace_noalloc(Ctx *ctx, uint32_t *a, uint64_t n, uint64_t *total
 
 // Merge of two sorted arrays (stable, a before b on ties) into out[na+nb].
 void merge_sorted(Ctx *ctx, const uint64_t *a, uint64_t na, const uint64_t *b, uint64_t nb, uint64_t *out);
+// The same with device row counts (d_na, d_nb; na and nb are the bounds), a
+// stop flag and a skip word: nothing is written when *stop is raised or
+// *skip is zero.
+void merge_sorted_dev(Ctx *ctx, const uint64_t *a, uint64_t na, const uint64_t *d_na, const uint64_t *b, uint64_t nb,
+                      const uint64_t *d_nb, uint64_t *out, const uint64_t *skip, const uint32_t *stop);
 
 // Sorted-run index over the high word of sorted packed keys (join build):
 // an open-addressing hash table of 16-byte slots mapping key -> (run start,
@@ -422,7 +445,14 @@ uint64_t probe_prepare(Ctx *ctx, ProbeJob &job);
 // The count pass for a probe whose row count is on the device (*d_n <= n_bound),
 // with no read-back; the total lands at job.toff.p[job.tiles].  probe_finish
 // completes the job once the host has read the row count and the total.
-void probe_prepare_deferred(Ctx *ctx, ProbeJob &job, uint64_t n_bound, const uint64_t *d_n);
+void probe_prepare_deferred(Ctx *ctx, ProbeJob &job, uint64_t n_bound, const uint64_t *d_n,
+                            const uint32_t *stop = nullptr);
+// The emit of a deferred probe inside a queued iteration: the probe rows'
+// count on the device (d_n, at most job.n), two-column outputs (oc) written
+// to out + *d_out_base (d_out_base may be null), nothing when *stop is raised.
+// The caller has checked that the total fits the output.
+void probe_emit_dev(Ctx *ctx, const ProbeJob &job, const uint64_t *d_n, const int oc[4], uint64_t *out,
+                    const uint64_t *d_out_base, const uint32_t *stop);
 void probe_finish(ProbeJob &job, uint64_t n, uint64_t total);
 // The count pass alone, lookups recorded, no scan and no read-back; with gsel
 // set and gseg null the group heads count zero until probe_group_fixup gives
@@ -589,7 +619,7 @@ void select_state_release(Ctx *ctx);
 // *d_total (device).  The prefixes are exact while the total is below
 // SCAN64_EXACT; a caller checks the total before using them.
 constexpr uint64_t SCAN64_EXACT = 1ull << 39;
-void scan_u64_inplace(Ctx *ctx, uint64_t *a, uint64_t n, uint64_t *d_total);
+void scan_u64_inplace(Ctx *ctx, uint64_t *a, uint64_t n, uint64_t *d_total, const uint32_t *stop = nullptr);
 // Zero-fills gathered into one launch (up to FILL_MAX_RANGES ranges each):
 // add() records a range, flush() launches them in stream order.
 constexpr int FILL_MAX_RANGES = 16;

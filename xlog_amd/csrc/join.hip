@@ -127,6 +127,11 @@ struct ProbeArgs {
     const uint64_t *d_n;
     // optional profiling counter: the deferred count pass adds its real row count
     unsigned long long *work;
+    // queued iterations: the stop flag (raised: the count writes zero tile
+    // counts, the emit nothing) and the emit's output base on the device
+    // (outputs go to out + *d_out_base)
+    const uint32_t *stop;
+    const uint64_t *d_out_base;
 };
 // set in a row's start when its outputs come from gsrc
 constexpr uint64_t GROUP_BIT = 1ull << 63;
@@ -193,9 +198,13 @@ template <int ITEMS>
 __global__ __launch_bounds__(JB) void k_probe_count(ProbeArgs a, uint64_t *__restrict__ tile_cnt) {
     __shared__ uint64_t s_part[JWAVES];
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
+    if (a.stop && *a.stop) {
+        if (tid == 0) tile_cnt[blockIdx.x] = 0;
+        return;
+    }
     if (a.d_n) {
         // deferred count: the grid covers a bound; tiles past the real rows count zero
-        a.n = *a.d_n;
+        if (*a.d_n < a.n) a.n = *a.d_n;
         if (a.work && blockIdx.x == 0 && tid == 0) atomicAdd(a.work, (unsigned long long)a.n);
         if ((uint64_t)blockIdx.x * tile_rows(ITEMS) >= a.n) {
             if (tid == 0) tile_cnt[blockIdx.x] = 0;
@@ -267,6 +276,16 @@ __global__ __launch_bounds__(JB) void k_probe_emit(ProbeArgs a, const uint64_t *
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
     const uint64_t tile = t0 + blockIdx.x;
     const uint64_t wbase = tile * tile_rows(ITEMS) + (uint64_t)wave * (ITEMS * WAVE);
+    if (a.stop && *a.stop) return;
+    if (a.d_n) {  // the row count on the device: tiles past it emit nothing
+        if (*a.d_n < a.n) a.n = *a.d_n;
+        if (tile * tile_rows(ITEMS) >= a.n) return;
+    }
+    if (a.d_out_base) {
+        const uint64_t ob = *a.d_out_base;
+        out0 += ob;
+        if (out1) out1 += ob;
+    }
 
     // pass 1 over this wave's rows: all ITEMS lookups issued together (their
     // latencies overlap) and kept in registers for the expansion
@@ -569,7 +588,7 @@ uint64_t probe_prepare(Ctx *ctx, ProbeJob &job) {
 // lookups are sized for n_bound; nothing is read back.  probe_finish then
 // takes the row count and the total (read back by the caller together with
 // whatever else it needs: d_total() points at the total).
-void probe_prepare_deferred(Ctx *ctx, ProbeJob &job, uint64_t n_bound, const uint64_t *d_n) {
+void probe_prepare_deferred(Ctx *ctx, ProbeJob &job, uint64_t n_bound, const uint64_t *d_n, const uint32_t *stop) {
     job.items = JITEMS;
     job.n = n_bound;
     job.tiles = (n_bound + tile_rows(job.items) - 1) / tile_rows(job.items);
@@ -582,6 +601,7 @@ void probe_prepare_deferred(Ctx *ctx, ProbeJob &job, uint64_t n_bound, const uin
     }
     ProbeArgs a = probe_args(job);
     a.d_n = d_n;
+    a.stop = stop;
     XH_REQUIRE(!job.pre_cnt && job.record_lookups, XLOG_HIP_INVALID_ARG, "deferred probe: recorded lookups only");
     job.rec_start = Buf<uint64_t>(ctx, n_bound);
     job.rec_cnt = Buf<uint32_t>(ctx, n_bound);
@@ -595,7 +615,25 @@ void probe_prepare_deferred(Ctx *ctx, ProbeJob &job, uint64_t n_bound, const uin
         XH_CHECK_HIP(hipGetLastError());
     }
     // tiles past the real rows hold zero counts
-    scan_u64_inplace(ctx, job.toff.p, job.tiles, job.toff.p + job.tiles);
+    scan_u64_inplace(ctx, job.toff.p, job.tiles, job.toff.p + job.tiles, stop);
+}
+
+void probe_emit_dev(Ctx *ctx, const ProbeJob &job, const uint64_t *d_n, const int oc[4], uint64_t *out,
+                    const uint64_t *d_out_base, const uint32_t *stop) {
+    if (job.n == 0 || job.tiles == 0 || !job.rec_cnt.p) return;  // nothing can match (see probe_prepare_deferred)
+    ProbeArgs a = probe_args(job);
+    a.pre_start = job.rec_start.p;  // the count pass's recorded lookups
+    a.pre_cnt = job.rec_cnt.p;
+    a.d_n = d_n;
+    a.stop = stop;
+    a.d_out_base = d_out_base;
+    OutSpec spec{2, {oc[0], oc[1], oc[2], oc[3]}};
+    // per probe row its record (20 B with the row) and per match 12 B, counted on the device
+    Prof prof(ctx, XLOG_HIP_KERNEL_PROBE_EMIT, 0.0);
+    add_work_rows(ctx, prof.work(1.0), d_n, job.n, 20, job.toff.p + job.tiles, ~0ull, 12, nullptr, stop);
+    hipLaunchKernelGGL(k_probe_emit<JITEMS>, dim3((unsigned)job.tiles), dim3(JB), 0, ctx->stream, a, job.toff.p, 0ull,
+                       spec, out, nullptr);
+    XH_CHECK_HIP(hipGetLastError());
 }
 void probe_finish(ProbeJob &job, uint64_t n, uint64_t total) {
     XH_REQUIRE(total < SCAN64_EXACT, XLOG_HIP_CAPACITY_OVERFLOW, "join probe: " + std::to_string(total) + " output rows");

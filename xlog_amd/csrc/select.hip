@@ -120,7 +120,7 @@ __global__ __launch_bounds__(SelShape<Sel>::block) void k_select(const uint64_t 
                                                       uint64_t *__restrict__ d_count, uint64_t *status,
                                                       uint64_t epoch_tag, unsigned long long *ticket,
                                                       unsigned long long ticket_base, uint64_t ntiles,
-                                                      const uint64_t *d_n) {
+                                                      const uint64_t *d_n, const uint32_t *stop) {
     __shared__ uint64_t s_tile;
     __shared__ uint64_t s_prefix;
     constexpr int SEL_WAVES = SelShape<Sel>::waves;
@@ -128,25 +128,34 @@ __global__ __launch_bounds__(SelShape<Sel>::block) void k_select(const uint64_t 
     __shared__ uint32_t s_wc[SEL_WAVES];
     __shared__ uint64_t s_sel[4];
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
+    // every block takes its ticket, so that the counter stays in step with the
+    // host's base, before a stop raised by an earlier launch of a queued
+    // iteration ends it (the flag cannot change while this kernel runs, so
+    // every block of the grid returns here or none does)
+    if (tid == 0) s_tile = atomicAdd(ticket, 1ull) - ticket_base;
+    if (stop && *stop) return;
     // a row count still on the device replaces the bound the grid was sized
     // for; tiles past it select nothing but keep the look-back chain
     if (d_n) n = *d_n < n ? *d_n : n;
-    if (tid == 0) {
-        uint64_t t = atomicAdd(ticket, 1ull) - ticket_base;
-        s_tile = t;
-        if constexpr (!Sel::kWindow) {
-            uint64_t first = t * SEL_TILE, last = first + SEL_TILE;
+    __syncthreads();
+    const uint64_t tile = s_tile;
+    if constexpr (!Sel::kWindow) {
+        if (tid == 0) {
+            uint64_t first = tile * SEL_TILE, last = first + SEL_TILE;
             if (last > n) last = n;
             if (first < last) sel.setup(first, last - 1, s_sel, 0);
         }
-    }
-    __syncthreads();
-    const uint64_t tile = s_tile;
-    if constexpr (Sel::kWindow) {
+        __syncthreads();
+    } else {
         if (wave == 0) {
             uint64_t first = tile * SEL_TILE, last = first + SEL_TILE;
             if (last > n) last = n;
-            sel.setup(first, last - 1, s_sel, lane);
+            if (first < last) {
+                sel.setup(first, last - 1, s_sel, lane);
+            } else if (lane == 0) {  // a tile past the rows: an empty window
+                s_sel[0] = s_sel[1] = 0;
+                s_sel[2] = 1;
+            }
         }
         __syncthreads();
     }
@@ -306,6 +315,7 @@ struct SelDiff {
     uint64_t *out;
     const uint64_t *win;  // [2t], [2t + 1]: window of tile t (nullptr: searched by the tile)
     uint64_t tile_rows;
+    const uint64_t *d_nb;  // optional: b's row count on the device (nb is then its bound)
     // s[0], s[1]: window [s0, s1) of b; s[2]: 1 when it is streamed through LDS
     __device__ void setup(uint64_t first, uint64_t last, uint64_t *s, int lane) const {
         uint64_t s0, s1;
@@ -314,8 +324,9 @@ struct SelDiff {
             s0 = win[2 * t];
             s1 = win[2 * t + 1];
         } else {
-            s0 = wave_bound<false>(b, 0, nb, in[first], lane);
-            s1 = wave_bound<true>(b, s0, nb, in[last], lane);
+            const uint64_t m = d_nb && *d_nb < nb ? *d_nb : nb;
+            s0 = wave_bound<false>(b, 0, m, in[first], lane);
+            s1 = wave_bound<true>(b, s0, m, in[last], lane);
         }
         if (lane == 0) {
             s[0] = s0;
@@ -372,10 +383,20 @@ struct SelDiff {
 // levels of the searches are shared and stay in cache)
 __global__ __launch_bounds__(256) void k_diff_windows(const uint64_t *__restrict__ in, uint64_t n,
                                                       const uint64_t *__restrict__ b, uint64_t nb, uint64_t tile_rows,
-                                                      uint64_t tiles, uint64_t *__restrict__ win) {
+                                                      uint64_t tiles, uint64_t *__restrict__ win,
+                                                      const uint64_t *d_n, const uint64_t *d_nb,
+                                                      const uint32_t *stop) {
     const uint64_t q = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (q >= 2 * tiles) return;
+    if (stop && *stop) return;
+    // device row counts (queued iterations) replace the bounds the grid was sized for
+    if (d_n && *d_n < n) n = *d_n;
+    if (d_nb && *d_nb < nb) nb = *d_nb;
     const uint64_t t = q >> 1, first = t * tile_rows;
+    if (first >= n) {  // a tile past the rows: an empty window
+        win[q] = 0;
+        return;
+    }
     if (q & 1) {
         const uint64_t last = (first + tile_rows < n ? first + tile_rows : n) - 1;
         win[q] = upper_bound_u64(b, 0, nb, in[last]);
@@ -562,12 +583,13 @@ constexpr uint64_t SCAN64_TILE = (uint64_t)SCAN64_BLOCK * SCAN64_ITEMS;
 __global__ __launch_bounds__(SCAN64_BLOCK) void k_scan_u64(uint64_t *a, uint64_t n, uint64_t *status,
                                                            uint64_t epoch_tag, unsigned long long *ticket,
                                                            unsigned long long ticket_base,
-                                                           unsigned long long *d_total) {
+                                                           unsigned long long *d_total, const uint32_t *stop) {
     __shared__ uint64_t s_tile;
     __shared__ uint64_t s_prefix;
     __shared__ uint64_t s_wsum[SCAN64_BLOCK / WAVE];
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
     if (tid == 0) s_tile = atomicAdd(ticket, 1ull) - ticket_base;
+    if (stop && *stop) return;  // after the ticket (see k_select)
     __syncthreads();
     const uint64_t tile = s_tile;
     const uint64_t base = tile * SCAN64_TILE + (uint64_t)tid * SCAN64_ITEMS;
@@ -632,22 +654,41 @@ __device__ __forceinline__ uint64_t merge_path(const uint64_t *a, uint64_t na, c
 // split[t] = merge_path at diagonal min(t * MRG_TILE, na + nb), one thread per
 // tile boundary: the binary searches of all tiles run side by side instead of
 // two dependent ~log2(n)-load chains at the start of every merge block
+// Queued iterations give the row counts on the device (d_na, d_nb replace the
+// bounds na, nb the grid was sized for), a stop flag, and a skip word: a merge
+// whose *skip is zero writes nothing (an iteration that derived nothing keeps
+// its relation where it is).
+struct MergeDev {
+    const uint64_t *d_na = nullptr, *d_nb = nullptr, *skip = nullptr;
+    const uint32_t *stop = nullptr;
+    __device__ bool off() const { return (stop && *stop) || (skip && *skip == 0); }
+    __device__ void counts(uint64_t &na, uint64_t &nb) const {
+        if (d_na && *d_na < na) na = *d_na;
+        if (d_nb && *d_nb < nb) nb = *d_nb;
+    }
+};
+
 __global__ void k_merge_partition(const uint64_t *__restrict__ a, uint64_t na, const uint64_t *__restrict__ b,
-                                  uint64_t nb, uint64_t tiles, uint64_t *__restrict__ split) {
+                                  uint64_t nb, uint64_t tiles, uint64_t *__restrict__ split, MergeDev dv) {
     const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t > tiles) return;
+    if (t > tiles || dv.off()) return;
+    dv.counts(na, nb);
     const uint64_t total = na + nb, d = t * MRG_TILE < total ? t * MRG_TILE : total;
     split[t] = merge_path(a, na, b, nb, d);
 }
 
 __global__ __launch_bounds__(MRG_BLOCK) void k_merge(const uint64_t *__restrict__ a, uint64_t na,
                                                      const uint64_t *__restrict__ b, uint64_t nb,
-                                                     const uint64_t *__restrict__ split, uint64_t *__restrict__ out) {
+                                                     const uint64_t *__restrict__ split, uint64_t *__restrict__ out,
+                                                     MergeDev dv) {
     __shared__ uint64_t s[MRG_TILE];
     __shared__ uint64_t s_split[2];
     const int tid = threadIdx.x;
+    if (dv.off()) return;
+    dv.counts(na, nb);
     const uint64_t total = na + nb;
     const uint64_t d0 = (uint64_t)blockIdx.x * MRG_TILE;
+    if (d0 >= total) return;  // a tile past the rows (the grid covers the bounds)
     const uint64_t d1 = (d0 + MRG_TILE < total) ? d0 + MRG_TILE : total;
     if (tid < 2) s_split[tid] = split[blockIdx.x + tid];
     __syncthreads();
@@ -689,6 +730,16 @@ __global__ __launch_bounds__(MRG_BLOCK) void k_merge(const uint64_t *__restrict_
         if ((uint32_t)j < cnt) s[td + j] = r[j];
     __syncthreads();
     for (uint32_t i = tid; i < len; i += MRG_BLOCK) out[d0 + i] = s[i];
+}
+
+// profiling of launches sized by bounds: the real row counts (up to two
+// device counts, each clamped to its bound), weighted, added to a work counter
+__global__ void k_work_rows(unsigned long long *work, const uint64_t *d_a, uint64_t a, uint32_t wa, const uint64_t *d_b,
+                            uint64_t b, uint32_t wb, const uint64_t *skip, const uint32_t *stop) {
+    if ((stop && *stop) || (skip && *skip == 0)) return;
+    if (d_a && *d_a < a) a = *d_a;
+    if (d_b && *d_b < b) b = *d_b;
+    atomicAdd(work, (unsigned long long)(a * wa + b * wb));
 }
 
 // ---- helpers --------------------------------------------------------------
@@ -831,12 +882,12 @@ static uint64_t *select_status(Ctx *ctx, uint64_t tiles, uint64_t *epoch_tag) {
     return st.status;
 }
 
-// d_n (optional, not for window selections): the row count on the device,
-// at most n, which is then only the bound the grid is sized for
+// d_n (optional): the row count on the device, at most n, which is then only
+// the bound the grid is sized for.  stop (optional): the stop flag of a queued
+// iteration; a raised flag makes the launch do nothing (*d_count unwritten).
 template <class Sel>
 static void run_select(Ctx *ctx, const uint64_t *in, uint64_t n, const Sel &sel, uint64_t *d_count,
-                       const uint64_t *d_n = nullptr) {
-    XH_REQUIRE(!(d_n && Sel::kWindow), XLOG_HIP_INVALID_ARG, "select: a device row count needs a plain selection");
+                       const uint64_t *d_n = nullptr, const uint32_t *stop = nullptr) {
     if (n == 0) {
         fill_u64(ctx, d_count, 0ull, 1);
         return;
@@ -847,10 +898,12 @@ static void run_select(Ctx *ctx, const uint64_t *in, uint64_t n, const Sel &sel,
     uint64_t tag;
     uint64_t *status = select_status(ctx, tiles, &tag);
     unsigned long long tb = ctx->take_tickets(1, tiles);
-    Prof prof(ctx, XLOG_HIP_KERNEL_SELECT, 8.0 * (double)n);
+    // 8 B per input row; with a device row count, counted on the device
+    Prof prof(ctx, XLOG_HIP_KERNEL_SELECT, d_n ? 0.0 : 8.0 * (double)n);
+    if (d_n) add_work_rows(ctx, prof.work(8.0), d_n, n, 1, nullptr, 0, 0, nullptr, stop);
     const size_t dyn = Sel::kWindow ? (size_t)WIN_CAP * sizeof(uint64_t) : 0;
     hipLaunchKernelGGL(k_select<Sel>, dim3((unsigned)tiles), dim3(SelShape<Sel>::block), dyn, ctx->stream, in, n, sel, d_count,
-                       status, tag, ctx->tickets + 1, tb, tiles, d_n);
+                       status, tag, ctx->tickets + 1, tb, tiles, d_n, stop);
     XH_CHECK_HIP(hipGetLastError());
 }
 
@@ -884,6 +937,23 @@ void select_unique_low(Ctx *ctx, const uint64_t *k, uint64_t n, uint64_t *out, u
 void select_unique_diff(Ctx *ctx, const uint64_t *k, uint64_t n, const uint64_t *b, uint64_t nb, uint64_t *out,
                         uint64_t *d_count) {
     if (nb == 0 || n == 0) { select_unique(ctx, k, n, out, d_count); return; }
+    select_unique_diff_dev(ctx, k, n, nullptr, b, nb, nullptr, out, d_count, nullptr);
+}
+void add_work_rows(Ctx *ctx, unsigned long long *work, const uint64_t *d_a, uint64_t a, uint32_t wa, const uint64_t *d_b,
+                   uint64_t b, uint32_t wb, const uint64_t *skip, const uint32_t *stop) {
+    if (!work) return;
+    hipLaunchKernelGGL(k_work_rows, dim3(1), dim3(1), 0, ctx->stream, work, d_a, a, wa, d_b, b, wb, skip, stop);
+    XH_CHECK_HIP(hipGetLastError());
+}
+
+void select_unique_diff_dev(Ctx *ctx, const uint64_t *k, uint64_t n, const uint64_t *d_n, const uint64_t *b,
+                            uint64_t nb, const uint64_t *d_nb, uint64_t *out, uint64_t *d_count, const uint32_t *stop) {
+    if (n == 0) {
+        fill_u64(ctx, d_count, 0ull, 1);
+        return;
+    }
+    // b may be empty only when its count is on the device (an empty b of
+    // known size takes select_unique): a window search then finds nothing
     constexpr uint64_t rows = SelShape<SelDiff<true>>::tile;
     const uint64_t tiles = (n + rows - 1) / rows;
     XH_REQUIRE(tiles < (1ull << 31), XLOG_HIP_CAPACITY_OVERFLOW, "select: input too large");
@@ -891,10 +961,10 @@ void select_unique_diff(Ctx *ctx, const uint64_t *k, uint64_t n, const uint64_t 
     if (tiles >= DIFF_WINDOW_PASS) {
         win = Buf<uint64_t>(ctx, 2 * tiles);
         hipLaunchKernelGGL(k_diff_windows, dim3((unsigned)((2 * tiles + 255) / 256)), dim3(256), 0, ctx->stream, k, n, b,
-                           nb, rows, tiles, win.p);
+                           nb, rows, tiles, win.p, d_n, d_nb, stop);
         XH_CHECK_HIP(hipGetLastError());
     }
-    run_select(ctx, k, n, SelDiff<true>{k, b, nb, out, win.p, rows}, d_count);
+    run_select(ctx, k, n, SelDiff<true>{k, b, nb, out, win.p, rows, d_nb}, d_count, d_n, stop);
 }
 void select_not_value(Ctx *ctx, const uint64_t *k, uint64_t n, uint64_t v, uint64_t *out, uint64_t *d_count) {
     run_select(ctx, k, n, SelNotValue{v, out}, d_count);
@@ -916,7 +986,7 @@ void select_runs(Ctx *ctx, const uint64_t *k, uint64_t n, uint32_t *run_key, uin
     run_select(ctx, k, n, SelRuns{k, run_key, run_start}, d_count, d_n);
 }
 
-void scan_u64_inplace(Ctx *ctx, uint64_t *a, uint64_t n, uint64_t *d_total) {
+void scan_u64_inplace(Ctx *ctx, uint64_t *a, uint64_t n, uint64_t *d_total, const uint32_t *stop) {
     fill_u64(ctx, d_total, 0ull, 1);
     if (n == 0) return;
     const uint64_t tiles = (n + SCAN64_TILE - 1) / SCAN64_TILE;
@@ -925,7 +995,7 @@ void scan_u64_inplace(Ctx *ctx, uint64_t *a, uint64_t n, uint64_t *d_total) {
     uint64_t *status = select_status(ctx, tiles, &tag);
     unsigned long long tb = ctx->take_tickets(1, tiles);
     hipLaunchKernelGGL(k_scan_u64, dim3((unsigned)tiles), dim3(SCAN64_BLOCK), 0, ctx->stream, a, n, status, tag,
-                       ctx->tickets + 1, tb, reinterpret_cast<unsigned long long *>(d_total));
+                       ctx->tickets + 1, tb, reinterpret_cast<unsigned long long *>(d_total), stop);
     XH_CHECK_HIP(hipGetLastError());
 }
 
@@ -1006,15 +1076,28 @@ void scan_u32_inplace_noalloc(Ctx *ctx, uint32_t *a, uint64_t n, uint64_t *total
 }
 
 void merge_sorted(Ctx *ctx, const uint64_t *a, uint64_t na, const uint64_t *b, uint64_t nb, uint64_t *out) {
+    merge_sorted_dev(ctx, a, na, nullptr, b, nb, nullptr, out, nullptr, nullptr);
+}
+void merge_sorted_dev(Ctx *ctx, const uint64_t *a, uint64_t na, const uint64_t *d_na, const uint64_t *b, uint64_t nb,
+                      const uint64_t *d_nb, uint64_t *out, const uint64_t *skip, const uint32_t *stop) {
     uint64_t total = na + nb;
     if (!total) return;
     uint64_t tiles = (total + MRG_TILE - 1) / MRG_TILE;
     XH_REQUIRE(tiles < (1ull << 31), XLOG_HIP_CAPACITY_OVERFLOW, "merge: input too large");
     Buf<uint64_t> split(ctx, tiles + 1);
+    MergeDev dv;
+    dv.d_na = d_na;
+    dv.d_nb = d_nb;
+    dv.skip = skip;
+    dv.stop = stop;
     hipLaunchKernelGGL(k_merge_partition, dim3((unsigned)((tiles + 1 + 255) / 256)), dim3(256), 0, ctx->stream, a, na,
-                       b, nb, tiles, split.p);
-    Prof prof(ctx, XLOG_HIP_KERNEL_MERGE, 16.0 * (double)total);
-    hipLaunchKernelGGL(k_merge, dim3((unsigned)tiles), dim3(MRG_BLOCK), 0, ctx->stream, a, na, b, nb, split.p, out);
+                       b, nb, tiles, split.p, dv);
+    XH_CHECK_HIP(hipGetLastError());
+    // with device counts the bytes are counted on the device (work: 16 B per output row)
+    const bool dev = d_na || d_nb;
+    Prof prof(ctx, XLOG_HIP_KERNEL_MERGE, dev ? 0.0 : 16.0 * (double)total);
+    if (dev) add_work_rows(ctx, prof.work(16.0), d_na, na, 1, d_nb, nb, 1, skip, stop);
+    hipLaunchKernelGGL(k_merge, dim3((unsigned)tiles), dim3(MRG_BLOCK), 0, ctx->stream, a, na, b, nb, split.p, out, dv);
     XH_CHECK_HIP(hipGetLastError());
 }
 

@@ -84,9 +84,13 @@ __device__ __forceinline__ void st_status(uint32_t *p, uint32_t v) {
 // instead of by every lane on one counter.
 constexpr int HIST_BLOCK = 512, HIST_ITEMS = 8, HIST_COPIES = 4;
 __global__ __launch_bounds__(HIST_BLOCK) void k_hist8(const uint64_t *__restrict__ keys, uint64_t n,
-                                                      uint32_t *__restrict__ ghist, int dlo, int dhi) {
+                                                      uint32_t *__restrict__ ghist, int dlo, int dhi,
+                                                      const uint64_t *d_n, const uint32_t *stop) {
     __shared__ uint32_t h[8 * 256 * HIST_COPIES];
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
+    // queued iterations: the key count on the device (n is its bound) and the stop flag
+    if (stop && *stop) return;
+    if (d_n && *d_n < n) n = *d_n;
     for (int i = tid; i < 8 * 256 * HIST_COPIES; i += HIST_BLOCK) h[i] = 0;
     __syncthreads();
     uint32_t *hs = h + (lane % HIST_COPIES);
@@ -206,7 +210,7 @@ __global__ __launch_bounds__(BLOCK) void k_onesweep(
     const uint64_t *__restrict__ kin, uint64_t *__restrict__ kout, const uint32_t *__restrict__ vin,
     uint32_t *__restrict__ vout, uint64_t n, uint32_t tiles, int shift, const uint32_t *__restrict__ digit_off,
     uint32_t *status, uint32_t *status_next, uint32_t chunk, unsigned long long *ticket,
-    unsigned long long ticket_base) {
+    unsigned long long ticket_base, const uint64_t *d_n, const uint32_t *stop) {
     __shared__ uint32_t s_wcnt[(BLOCK / WAVE)][256];
     __shared__ uint32_t s_ticket;
     __shared__ uint32_t s_gbase[256];
@@ -229,6 +233,16 @@ __global__ __launch_bounds__(BLOCK) void k_onesweep(
     __syncthreads();
     const uint32_t tile = chunk_tile(ticket ? __builtin_amdgcn_readfirstlane(s_ticket) : blockIdx.x, chunk, tiles);
     if (tile == TILE_NONE) return;
+    // Queued iterations: the key count on the device (n and tiles are the
+    // bounds the grid was sized for) and the stop flag.  A tile past the keys,
+    // or any tile of a stopped pass, only clears its slot of the next pass's
+    // status buffer, so that after every pass that buffer is clean over all
+    // `tiles` tiles whatever the device count was.
+    if ((stop && *stop) || (d_n && (uint64_t)tile * (BLOCK * ITEMS) >= *d_n)) {
+        if (digit_thread) status_next[(uint64_t)tile * 256 + d] = 0u;
+        return;
+    }
+    if (d_n && *d_n < n) n = *d_n;
     {  // one tile per block
         const uint64_t wbase =
             (uint64_t)tile * (BLOCK * ITEMS) + (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane(wave) * (ITEMS * WAVE);
@@ -559,6 +573,60 @@ void sort_short_runs(Ctx *ctx, const uint64_t *in, uint64_t n, uint64_t *out, ui
     XH_CHECK_HIP(hipGetLastError());
 }
 
+int radix_sort_dev(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint64_t n_bound, const uint64_t *d_n,
+                   uint32_t known_digits, const uint32_t *stop) {
+    XH_REQUIRE(known_digits, XLOG_HIP_INVALID_ARG, "radix sort with a device count: the digits must be known");
+    XH_REQUIRE(n_bound < (1ull << 30), XLOG_HIP_CAPACITY_OVERFLOW,
+               "radix sort: a single sort call is limited to 2^30 - 1 keys");
+    if (n_bound == 0) return 0;
+    const uint64_t tile_keys = (uint64_t)SORT_BLOCK_K * SORT_ITEMS_K;
+    const uint64_t tiles = (n_bound + tile_keys - 1) / tile_keys;
+    SortState &st = sort_state(ctx, tiles);
+    uint32_t *hist = st.hist, *off = st.hist + 8 * 256;
+    const uint32_t cap = pass_capacity<false, SORT_BLOCK_K, SORT_ITEMS_K>(ctx);
+    uint32_t chunk = cap / 16 < 8 ? (cap / 16 > 0 ? cap / 16 : 1) : 8;
+    if (tiles / 64 < chunk) chunk = tiles / 64 > 0 ? (uint32_t)(tiles / 64) : 1;
+    const uint64_t nchunks = (tiles + chunk - 1) / chunk;
+    const unsigned grid = (unsigned)(8 * ((nchunks + 7) / 8) * chunk);
+    fill_u32(ctx, hist, 0u, 8 * 256);
+    {
+        Prof prof(ctx, XLOG_HIP_KERNEL_SORT_HIST, 0.0);
+        add_work_rows(ctx, prof.work(8.0), d_n, n_bound, 1, nullptr, 0, 0, nullptr, stop);  // reads every key once
+        const unsigned hg = grid_for(n_bound, (unsigned)(HIST_BLOCK * HIST_ITEMS) * 4, (unsigned)ctx->num_cus * 8);
+        hipLaunchKernelGGL(k_hist8, dim3(hg), dim3(HIST_BLOCK), 0, ctx->stream, *keys, n_bound, hist, 0, 8, d_n,
+                           stop);
+        XH_CHECK_HIP(hipGetLastError());
+        hipLaunchKernelGGL(k_digit_offsets, dim3(1), dim3(64), 0, ctx->stream, hist, off);
+        XH_CHECK_HIP(hipGetLastError());
+    }
+    int cur = (st.dirty[0] == 0) ? 0 : (st.dirty[1] == 0 ? 1 : 0);
+    int passes = 0;
+    for (int dgt = 0; dgt < 8; ++dgt) {
+        if (!((known_digits >> dgt) & 1u)) continue;
+        const int nxt = 1 - cur;
+        if (st.dirty[cur]) {
+            fill_u32(ctx, st.status[cur], 0u, st.dirty[cur] * 256);
+            st.dirty[cur] = 0;
+        }
+        Prof prof(ctx, XLOG_HIP_KERNEL_SORT_PASS, 0.0);
+        add_work_rows(ctx, prof.work(16.0), d_n, n_bound, 1, nullptr, 0, 0, nullptr, stop);
+        unsigned long long *tk = sort_tickets() ? ctx->tickets + 2 : nullptr;
+        const unsigned long long tb = tk ? ctx->take_tickets(2, grid) : 0ull;
+        hipLaunchKernelGGL((k_onesweep<false, SORT_BLOCK_K, SORT_ITEMS_K>), dim3(grid), dim3(SORT_BLOCK_K), 0,
+                           ctx->stream, *keys, *keys_alt, nullptr, nullptr, n_bound, (uint32_t)tiles, 8 * dgt,
+                           off + dgt * 256, st.status[cur], st.status[nxt], chunk, tk, tb, d_n, stop);
+        XH_CHECK_HIP(hipGetLastError());
+        // this pass wrote the status of at most `tiles` tiles in cur and cleared
+        // nxt over all `tiles` tiles (stopped and empty tiles included)
+        st.dirty[cur] = tiles;
+        if (st.dirty[nxt] <= tiles) st.dirty[nxt] = 0;
+        std::swap(*keys, *keys_alt);
+        cur = nxt;
+        ++passes;
+    }
+    return passes;
+}
+
 int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **vals, uint32_t **vals_alt,
                    uint64_t n, int digit_lo, int digit_hi, const uint64_t *src, uint32_t known_digits,
                    SortUnique *uq) {
@@ -596,7 +664,8 @@ int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **va
         // than the counting when blocks have little to count (2^24 keys: 62 us with one round per block, 47 us
         // with 4, 60 us with 16)
         const unsigned hg = grid_for(n, (unsigned)(HIST_BLOCK * HIST_ITEMS) * 4, (unsigned)ctx->num_cus * 8);
-        hipLaunchKernelGGL(k_hist8, dim3(hg), dim3(HIST_BLOCK), 0, ctx->stream, from, n, hist, dlo, dhi);
+        hipLaunchKernelGGL(k_hist8, dim3(hg), dim3(HIST_BLOCK), 0, ctx->stream, from, n, hist, dlo, dhi, nullptr,
+                           nullptr);
         XH_CHECK_HIP(hipGetLastError());
         hipLaunchKernelGGL(k_digit_offsets, dim3(1), dim3(64), 0, ctx->stream, hist, off);
         XH_CHECK_HIP(hipGetLastError());
@@ -618,12 +687,12 @@ int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **va
         if (has_val)
             hipLaunchKernelGGL((k_onesweep<true, SORT_BLOCK_V, SORT_ITEMS_V>), dim3(grid), dim3(SORT_BLOCK_V), 0,
                                ctx->stream, *keys, *keys_alt, *vals, *vals_alt, n, (uint32_t)tiles, 8 * dgt,
-                               off + dgt * 256, st.status[cur], st.status[nxt], chunk, tk, tb);
+                               off + dgt * 256, st.status[cur], st.status[nxt], chunk, tk, tb, nullptr, nullptr);
         else
             hipLaunchKernelGGL((k_onesweep<false, SORT_BLOCK_K, SORT_ITEMS_K>), dim3(grid), dim3(SORT_BLOCK_K), 0,
                                ctx->stream, (passes == 0 && src) ? src : *keys, *keys_alt, nullptr, nullptr, n,
                                (uint32_t)tiles, 8 * dgt, off + dgt * 256, st.status[cur], st.status[nxt], chunk,
-                               tk, tb);
+                               tk, tb, nullptr, nullptr);
         XH_CHECK_HIP(hipGetLastError());
         st.dirty[cur] = tiles;
         if (st.dirty[nxt] <= tiles) st.dirty[nxt] = 0;
