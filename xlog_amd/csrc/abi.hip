@@ -1745,19 +1745,48 @@ BodyPlan plan_body(const Rule &r) {
 // queue position + 1 of the first iteration that could not run within its
 // bounds).  These single-thread kernels check a count against its bound and
 // keep the sums the next launches read.
-__global__ void k_q_check(const uint64_t *a, const uint64_t *b, uint64_t cap, uint32_t *stop, uint32_t code) {
-    const uint64_t v = *a + (b ? *b : 0ull);
-    if (v > cap) atomicCAS(stop, 0u, code);
-}
-__global__ void k_q_add(uint64_t *dst, const uint64_t *a, const uint64_t *b, const uint32_t *stop) {
+// After a join step's count: the step's rows must fit its bound (with the
+// rows emitted before it into the same candidate buffer: base_in) and the
+// join-row limit; the count is kept in slot and the next emit's base in
+// base_out.  Runs before the emit, which writes at *base_in.
+struct QStep {
+    const uint64_t *tot;
+    const uint64_t *base_in;
+    uint64_t *base_out;
+    uint64_t *slot;
+    uint64_t cap, limit;
+};
+__global__ void k_q_step(QStep a, uint32_t *stop, uint32_t code) {
     if (*stop) return;
-    *dst = *a + (b ? *b : 0ull);
+    const uint64_t t = *a.tot, b = a.base_in ? *a.base_in : 0ull;
+    if (b + t > a.cap || (a.limit && t > a.limit)) {
+        atomicCAS(stop, 0u, code);
+        return;
+    }
+    *a.slot = t;
+    if (a.base_out) *a.base_out = b + t;
 }
-__global__ void k_q_sum(uint64_t *dst, const uint64_t *src, uint32_t count, const uint32_t *stop) {
+// After the set differences, before the merges: the iteration's delta total,
+// and every head's R after the merge, which must fit its bound.
+constexpr uint32_t QMAX_HEADS = 16;
+struct QEnd {
+    const uint64_t *nD, *pR;
+    uint64_t *nR, *total;
+    uint32_t heads;
+    uint64_t rcap[QMAX_HEADS];
+};
+__global__ void k_q_end(QEnd a, uint32_t *stop, uint32_t code) {
     if (*stop) return;
     uint64_t t = 0;
-    for (uint32_t i = 0; i < count; ++i) t += src[i];
-    *dst = t;
+    for (uint32_t h = 0; h < a.heads; ++h) {
+        t += a.nD[h];
+        if (a.pR[h] + a.nD[h] > a.rcap[h]) {
+            atomicCAS(stop, 0u, code);
+            return;
+        }
+    }
+    *a.total = t;
+    for (uint32_t h = 0; h < a.heads; ++h) a.nR[h] = a.pR[h] + a.nD[h];
 }
 
 // device-resident canonical packed relation
@@ -1778,6 +1807,7 @@ struct Driver {
     uint64_t max_join_rows = 0;  // 0: no limit on a body join's bag size
     uint64_t cur_iter = 0;       // the loop iteration in progress (the reference's counter, recursive.rs:619-620)
     uint32_t digits = 0;         // varying digits of packed tuples over the value domain (0: from the histograms)
+    uint64_t domain = 0;         // largest input id + 1: every derived value is an input value (0: unknown)
     // join-index cache keyed by (relation buffer, column, version)
     struct CacheKey {
         const uint64_t *k; int col; uint64_t version;
@@ -1815,8 +1845,11 @@ struct Driver {
     // these ratios.  obs[ri][j] = {left rows, output rows} of step j >= 1.
     std::vector<std::array<std::pair<uint64_t, uint64_t>, MAX_BODY>> obs;
     // per predicate: the share of its candidates that were new in its last
-    // iteration with candidates (the queued iterations' delta estimate)
+    // iteration with candidates (the queued iterations' delta estimate), and
+    // its last two delta sizes (their ratio predicts the end of a decay)
     std::vector<double> nov;
+    std::vector<std::array<uint64_t, 2>> dlast;
+    void note_delta(uint32_t p, uint64_t n) { dlast[p] = {dlast[p][1], n}; }
 
     // ri >= 0: record the join steps' sizes in obs[ri]
     void eval_body(const Rule &r, const DRel *const *rel, Bags &out, ProbeJob *pre, int ri = -1) {
@@ -1944,6 +1977,7 @@ struct Driver {
     void seed(std::vector<uint64_t> &deltas) {
         obs.assign(rules.size(), {});
         nov.assign(n_preds, 1.0);
+        dlast.assign(n_preds, {0, 0});
         std::vector<Bags> derived = bags_per_pred(ctx, n_preds);
         for (const Rule &r : rules) {
             const DRel *rel[MAX_BODY];
@@ -1955,6 +1989,7 @@ struct Driver {
             if (!idb[p]) continue;
             DRel d = finalize(derived[p], full[p]);  // full_new \ full_old
             delta[p] = d;  // the driver owns it from here
+            note_delta(p, d.n);
             if (d.n) {
                 DRel m = merge(full[p], d);
                 release(full[p]);
@@ -1994,6 +2029,7 @@ struct Driver {
             delta[p] = d;
             total += d.n;
             if (cand) nov[p] = (double)d.n / (double)cand;
+            note_delta(p, d.n);
         }
         deltas.push_back(total);
         if (total == 0) return 0;
@@ -2095,17 +2131,12 @@ struct Driver {
                 heads.push_back((int)p);
             }
         uint64_t it = 0;
-        bool host_ran = false;  // the join steps' ratios come from an iteration run from the host first
         while (it < max_iter) {
-            if (host_ran) {
-                const uint64_t done =
-                    run_queue(std::min<uint64_t>(qmax, max_iter - it), it, heads, hidx, deltas, qr);
-                if (done == ~0ull) return it;  // converged inside the queue (it counts the empty iteration)
-                if (done > 0) continue;
-            }
-            // the first iteration, one whose queue stopped at once, or one for which no queue fits
+            const uint64_t done = run_queue(std::min<uint64_t>(qmax, max_iter - it), it, heads, hidx, deltas, qr);
+            if (done == ~0ull) return it;  // converged inside the queue (it counts the empty iteration)
+            if (done > 0) continue;
+            // an iteration whose queue stopped at once, or one for which no queue fits
             ++it;
-            host_ran = true;
             if (iterate_host(it, deltas, qr) == 0) return it;
         }
         cur_iter = it;
@@ -2137,24 +2168,60 @@ struct Driver {
             v->dpred = r.b[0].pred;
             v->bp = plan_body(r);
             for (int j = 1; j < r.nb; ++j) v->J[j] = &index_of(full[r.b[j].pred], v->bp.step[j].apos);
-            v->tot_slot = 3 * H + 1 + tot_words;
+            v->tot_slot = tot_words;  // offset by the block's header below
             tot_words += (uint32_t)(r.nb - 1);
             vars.push_back(std::move(v));
         }
-        const uint32_t B = 3 * H + 1 + tot_words;  // words per iteration block
+        // words of an iteration's block: nD[H], nR[H], per head its emit bases (one per variant of
+        // the head, then its candidate total), the delta total, the variants' join-step totals
+        std::vector<uint32_t> base_off(H), nvar(H, 0), vbase(vars.size());
+        for (size_t vi = 0; vi < vars.size(); ++vi) vbase[vi] = nvar[hidx[vars[vi]->head]]++;
+        uint32_t words_b = 2 * H;
+        for (uint32_t h = 0; h < H; ++h) {
+            base_off[h] = words_b;
+            words_b += nvar[h] + 1;
+        }
+        const uint32_t total_off = words_b;
+        for (auto &vp : vars) vp->tot_slot += total_off + 1;
+        const uint32_t B = total_off + 1 + tot_words;
         auto blk = [&](int64_t k) { return (uint64_t)1 + (uint64_t)(k + 1) * B; };
+        if (H > QMAX_HEADS) return 0;
         // every block comes back in one read of the pinned staging
         const uint64_t fit = (Ctx::HOST_STAGE_U64 - 1) / B;  // blocks that fit, the starting one included
         if (fit < 3) return 0;
         qn = std::min<uint64_t>(qn, fit - 1);
+        // When every head's delta is shrinking, queue only the iterations the decay predicts until the
+        // deltas run out (the last two sizes' ratio per iteration), and one more that derives nothing:
+        // launches queued past the fixpoint do no work but still cost their dispatch.
+        {
+            bool decaying = true;
+            double left = 0.0, r = 0.0;
+            for (uint32_t h = 0; h < H && decaying; ++h) {
+                const auto &d2 = dlast[heads[h]];
+                if (d2[1] == 0) continue;
+                decaying = d2[0] > 0 && d2[1] < d2[0];
+                if (decaying) {
+                    left += (double)d2[1];
+                    r = std::max(r, (double)d2[1] / (double)d2[0]);
+                }
+            }
+            if (decaying && left > 0.0) {
+                uint64_t k = 1;
+                for (double e = left * r; e >= 0.5 && k < qn; e *= r) ++k;
+                qn = std::min<uint64_t>(qn, k + 1);
+            }
+        }
 
         // ---- bounds ------------------------------------------------------------
         // rows out per row in of every join step from its last evaluation (4
         // when never seen); a head's next delta is its candidates times the
         // share of them that was new in its last iteration with candidates
+        // (before a step has run: the average run length of the index it probes)
         auto fan = [&](const QVariant &v, int j) {
             const auto &o = obs[v.ri][j];
-            return o.first ? std::max(1.0 / 64.0, (double)o.second / (double)o.first) : 4.0;
+            if (o.first) return std::max(1.0 / 64.0, (double)o.second / (double)o.first);
+            const JoinIndex &J = *v.J[j];
+            return J.ix.nruns ? std::max(1.0, (double)J.n / (double)J.ix.nruns) : 1.0;
         };
         // per-step margin over the estimates and a floor on every bound; tests shrink both
         // (XLOG_HIP_JOIN_QUEUE_MARGIN_PCT, XLOG_HIP_JOIN_QUEUE_SLACK) to make queues stop
@@ -2169,30 +2236,37 @@ struct Driver {
         std::vector<uint64_t> cur(H);
         for (uint32_t h = 0; h < H; ++h) cur[h] = delta[heads[h]].n;  // exact for the first
         const uint64_t room = device_room(ctx) / 2;
+        // every derived value is an input value: a head holds at most domain^2 tuples, so its delta is at
+        // most what R leaves of that (the bound of small domains)
+        std::vector<uint64_t> dmax(H, ~0ull);
+        if (domain && domain <= (1ull << 31))
+            for (uint32_t h = 0; h < H; ++h) dmax[h] = domain * domain - std::min(domain * domain, full[heads[h]].n);
         uint64_t q = 0;
         for (; q < qn; ++q) {
             std::vector<uint64_t> lb = cur, cb(H, 0), rb(H, 0);
             std::vector<std::array<uint64_t, MAX_BODY>> tv(vars.size());
-            bool fits = true;
+            // bounds past one sort's size are clamped to it: a larger count stops the queue there and
+            // the host loop (which sorts in pieces) takes that iteration
             for (size_t vi = 0; vi < vars.size(); ++vi) {
                 const QVariant &v = *vars[vi];
                 const Rule &r = qr[v.ri];
                 double t = (double)lb[hidx[v.dpred]];
                 for (int j = 1; j < r.nb; ++j) {
-                    t = t * fan(v, j) * M + (double)SLACK;
-                    tv[vi][j] = t > 1e18 ? (uint64_t)1e18 : (uint64_t)t;
-                    fits = fits && tv[vi][j] <= SORT_MAX;
+                    t = std::min(t * fan(v, j) * M + (double)SLACK, (double)SORT_MAX);
+                    tv[vi][j] = (uint64_t)t;
                 }
                 cb[hidx[v.head]] += tv[vi][r.nb - 1];
             }
-            for (uint32_t h = 0; h < H; ++h) fits = fits && cb[h] <= SORT_MAX;
+            for (uint32_t h = 0; h < H; ++h) cb[h] = std::min(cb[h], SORT_MAX);
             // next deltas, and R after this iteration
             std::vector<uint64_t> nxt(H);
             for (uint32_t h = 0; h < H; ++h) {
                 // (a delta never exceeds its head's candidates)
                 const double e = (double)cb[h] * nov[heads[h]];
                 nxt[h] = std::min<uint64_t>(std::max<uint64_t>(e > 1e18 ? (uint64_t)1e18 : (uint64_t)e, SLACK), cb[h]);
+                nxt[h] = std::min(nxt[h], dmax[h]);
                 rb[h] = Rb.back()[h] + nxt[h];
+                if (dmax[h] != ~0ull) rb[h] = std::min(rb[h], Rb[0][h] + dmax[h]);
             }
             // device bytes of the queue's buffers with this iteration in it
             uint64_t bytes = 0;
@@ -2212,14 +2286,14 @@ struct Driver {
                     bytes += 12 * ml + (j < r.nb - 1 ? 8 * mt : 0);
                 }
             }
-            if (!fits || bytes > room) break;
+            if (bytes > room) break;
             Lb.push_back(lb);
             T.push_back(tv);
             Cb.push_back(cb);
             Rb.push_back(rb);
             cur = nxt;
         }
-        if (q < 2) return 0;  // a queue of fewer than two iterations gains nothing over the host loop
+        if (q < 1) return 0;
         const uint64_t Q = q;
 
         // ---- buffers -------------------------------------------------------------
@@ -2258,25 +2332,13 @@ struct Driver {
             fill_u64(ctx, qs.p + blk(-1) + h, delta[heads[h]].n, 1);
             fill_u64(ctx, qs.p + blk(-1) + H + h, full[heads[h]].n, 1);
         }
-        auto check = [&](const uint64_t *a, const uint64_t *b, uint64_t cap, uint64_t k) {
-            hipLaunchKernelGGL(k_q_check, dim3(1), dim3(1), 0, ctx->stream, a, b, cap, stop, (uint32_t)(k + 1));
-            XH_CHECK_HIP(hipGetLastError());
-        };
-        auto add = [&](uint64_t *dst, const uint64_t *a, const uint64_t *b) {
-            hipLaunchKernelGGL(k_q_add, dim3(1), dim3(1), 0, ctx->stream, dst, a, b, stop);
-            XH_CHECK_HIP(hipGetLastError());
-        };
-
         // ---- the queue -------------------------------------------------------------
         cur_iter = it + 1;
         for (uint64_t k = 0; k < Q; ++k) {
             uint64_t *bk = qs.p + blk((int64_t)k), *bp = qs.p + blk((int64_t)k - 1);
-            uint64_t *nD = bk, *nR = bk + H, *cbase = bk + 2 * H, *total = bk + 3 * H;
+            uint64_t *nD = bk, *nR = bk + H, *total = bk + total_off;
             const uint64_t *pD = bp, *pR = bp + H;
-            for (uint32_t h = 0; h < H; ++h) fill_u64(ctx, cbase + h, 0ull, 1);
-            // the deltas this iteration reads must fit the bounds its probes are sized for
-            if (k > 0)
-                for (uint32_t h = 0; h < H; ++h) check(pD + h, nullptr, Lb[k][h], k);
+            const uint32_t code = (uint32_t)(k + 1);
             for (size_t vi = 0; vi < vars.size(); ++vi) {
                 QVariant &v = *vars[vi];
                 const Rule &r = qr[v.ri];
@@ -2285,6 +2347,7 @@ struct Driver {
                 const uint64_t *d_left = pD + dh_;
                 uint64_t left_bound = Lb[k][dh_];
                 if (k == 0 && !left) left_bound = 0;
+                uint64_t *base_in = bk + base_off[hh] + vbase[vi];
                 for (int j = 1; j < r.nb; ++j) {
                     const JoinPlanStep &st = v.bp.step[j];
                     ProbeJob &job = v.job[j];
@@ -2293,19 +2356,20 @@ struct Driver {
                     job.pcol = st.bpos;
                     job.ix = &v.J[j]->ix;
                     job.payload = v.J[j]->payload.p;
-                    probe_prepare_deferred(ctx, job, left_bound, d_left, stop);
+                    // the first step's count raises the stop flag itself when the delta it reads
+                    // is past the bound its launches are sized for
+                    probe_prepare_deferred(ctx, job, left_bound, d_left, stop, j == 1 ? code : 0u);
                     const uint64_t *d_tot = job.toff.p + job.tiles;
                     const bool last = j == r.nb - 1;
                     // the output must fit its buffer (and the launches after it their bounds), a join the
                     // limit, and the candidates one sort
-                    if (last) check(cbase + hh, d_tot, Cb[k][hh], k);
-                    else check(d_tot, nullptr, T[k][vi][j], k);
-                    if (max_join_rows) check(d_tot, nullptr, max_join_rows, k);
+                    QStep qsd{d_tot, last ? base_in : nullptr, last ? base_in + 1 : nullptr,
+                              bk + v.tot_slot + (j - 1), last ? Cb[k][hh] : T[k][vi][j], max_join_rows};
+                    hipLaunchKernelGGL(k_q_step, dim3(1), dim3(1), 0, ctx->stream, qsd, stop, code);
+                    XH_CHECK_HIP(hipGetLastError());
                     const int oc[4] = {st.sel[0], st.sel[1], 0, 0};
                     uint64_t *out = last ? qh[hh]->C.p : v.tmp[j].p;
-                    probe_emit_dev(ctx, job, d_left, oc, out, last ? cbase + hh : nullptr, stop);
-                    add(bk + v.tot_slot + (j - 1), d_tot, nullptr);
-                    if (last) add(cbase + hh, cbase + hh, d_tot);
+                    probe_emit_dev(ctx, job, d_left, oc, out, last ? base_in : nullptr, stop);
                     left = out;
                     d_left = d_tot;
                     left_bound = T[k][vi][j];
@@ -2314,30 +2378,40 @@ struct Driver {
             // per head: sort the candidates, keep the unique ones not in R
             for (uint32_t h = 0; h < H; ++h) {
                 const int p = heads[h];
+                const uint64_t *d_cand = bk + base_off[h] + nvar[h];
                 uint64_t *ka = qh[h]->C.p, *kb = qh[h]->Calt.p;
-                radix_sort_dev(ctx, &ka, &kb, Cb[k][h], cbase + h, digits, stop);
+                radix_sort_dev(ctx, &ka, &kb, Cb[k][h], d_cand, digits, stop);
                 const uint64_t *rin = k == 0 ? full[p].k : qh[h]->R[(k - 1) & 1].p;
                 if (!rin) rin = qh[h]->R[1].p;  // an empty R read through its device count
-                select_unique_diff_dev(ctx, ka, Cb[k][h], cbase + h, rin, std::max<uint64_t>(Rb[k][h], 1), pR + h,
+                select_unique_diff_dev(ctx, ka, Cb[k][h], d_cand, rin, std::max<uint64_t>(Rb[k][h], 1), pR + h,
                                        qh[h]->D[k & 1].p, nD + h, stop);
             }
-            hipLaunchKernelGGL(k_q_sum, dim3(1), dim3(1), 0, ctx->stream, total, nD, H, stop);
+            // the delta total, R's new sizes within their bounds
+            QEnd qe{nD, pR, nR, total, H, {}};
+            for (uint32_t h = 0; h < H; ++h) qe.rcap[h] = Rb[k + 1][h];
+            hipLaunchKernelGGL(k_q_end, dim3(1), dim3(1), 0, ctx->stream, qe, stop, code);
             XH_CHECK_HIP(hipGetLastError());
             // per head: R ∪= Δ' into the other buffer (nothing when the iteration derived nothing)
             for (uint32_t h = 0; h < H; ++h) {
                 const int p = heads[h];
-                check(pR + h, nD + h, Rb[k + 1][h], k);
                 const uint64_t *rin = k == 0 ? full[p].k : qh[h]->R[(k - 1) & 1].p;
                 if (!rin) rin = qh[h]->R[1].p;
                 merge_sorted_dev(ctx, rin, Rb[k][h], pR + h, qh[h]->D[k & 1].p, Cb[k][h], nD + h,
                                  qh[h]->R[k & 1].p, total, stop);
-                add(nR + h, pR + h, nD + h);
             }
         }
         ctx->read_scalars(qs.p, words);
         const uint64_t *hs = ctx->host_scalars;
         const uint32_t stopped = (uint32_t)hs[0];  // 0, or queue position + 1
         const uint64_t complete = stopped ? (uint64_t)stopped - 1 : Q;
+        if (env_u64("XLOG_HIP_TRACE_QUEUE", 0)) {  // one line per queue on stderr
+            fprintf(stderr, "[xlog_hip] join queue after iteration %llu: %llu queued, %llu complete; delta bounds",
+                    (unsigned long long)it, (unsigned long long)Q, (unsigned long long)complete);
+            for (uint64_t k = 0; k < Q; ++k) fprintf(stderr, " %llu", (unsigned long long)Lb[k][0]);
+            fprintf(stderr, "; deltas");
+            for (uint64_t k = 0; k < complete; ++k) fprintf(stderr, " %llu", (unsigned long long)hs[blk((int64_t)k)]);
+            fprintf(stderr, "\n");
+        }
 
         // ---- the completed iterations ----------------------------------------------------
         int64_t last = -1;  // the last completed queue position
@@ -2349,8 +2423,10 @@ struct Driver {
             uint64_t tot = 0;
             for (uint32_t h = 0; h < H; ++h) tot += bk[h];
             deltas.push_back(tot);
-            for (uint32_t h = 0; h < H; ++h)
-                if (bk[2 * H + h]) nov[heads[h]] = (double)bk[h] / (double)bk[2 * H + h];
+            for (uint32_t h = 0; h < H; ++h) {
+                if (const uint64_t cand = bk[base_off[h] + nvar[h]]) nov[heads[h]] = (double)bk[h] / (double)cand;
+                note_delta(heads[h], bk[h]);
+            }
             for (auto &vp : vars) {
                 const Rule &r = qr[vp->ri];
                 uint64_t in = bp[hidx[vp->dpred]];
@@ -3176,6 +3252,7 @@ static void run_fixpoint_impl(Ctx *ctx, const int32_t *plan, uint32_t n_preds, c
             const int bits = maxid ? 32 - __builtin_clz(maxid) : 0;
             const uint32_t nd = (uint32_t)(bits + 7) / 8;  // bytes per column
             drv.digits = nd ? (((1u << nd) - 1u) | (((1u << nd) - 1u) << 4)) : 1u;
+            drv.domain = nv;
         }
         if (stats) stats->route = use_hash ? XLOG_HIP_ROUTE_HASH : XLOG_HIP_ROUTE_JOIN;  // also on failure
         try {

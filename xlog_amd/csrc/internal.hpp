@@ -321,6 +321,25 @@ int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **va
 // passes of known_digits (no read-back), and the stop flag (a raised flag:
 // nothing is done).  Returns the number of passes: *keys and *keys_alt are
 // swapped once per pass, as in radix_sort_u64.
+// Grid of a launch over `tiles` tiles whose real count is on the device: at
+// most a few blocks per CU, which stride over (or take tickets for) the tiles.
+// Persistent launches that take tickets use counter PERSIST_TICKET_SLOT (the
+// radix pass PERSIST_TICKET_SLOT + 1) with base 0, and the counter two slots
+// further on to count the blocks that are done.  Only the first `parts`
+// blocks (at most one per tile that holds rows) take tickets; the last of
+// them to finish zeroes both counters (persist_done), so each launch finds
+// them at zero.
+constexpr int PERSIST_TICKET_SLOT = 8;
+__device__ __forceinline__ void persist_done(unsigned long long *ticket, uint64_t parts) {
+    if (atomicAdd(ticket + 2, 1ull) == (unsigned long long)(parts - 1)) {
+        ticket[0] = 0ull;
+        ticket[2] = 0ull;
+    }
+}
+inline unsigned persistent_grid(const Ctx *ctx, uint64_t tiles, uint32_t per_cu = 8) {
+    const uint64_t cap = (uint64_t)ctx->num_cus * per_cu;
+    return (unsigned)(tiles < cap ? (tiles ? tiles : 1) : cap);
+}
 // Profiling of a launch sized by bounds: adds wa * min(*d_a, a) + wb *
 // min(*d_b, b) (a device count given as null counts its bound) to the
 // launch's work counter, unless *stop is raised or *skip is zero; nothing
@@ -445,14 +464,16 @@ uint64_t probe_prepare(Ctx *ctx, ProbeJob &job);
 // The count pass for a probe whose row count is on the device (*d_n <= n_bound),
 // with no read-back; the total lands at job.toff.p[job.tiles].  probe_finish
 // completes the job once the host has read the row count and the total.
+// In a queued iteration, stop is the queue's stop flag and stop_code (when
+// non-zero) the code the count raises when *d_n is past n_bound.
 void probe_prepare_deferred(Ctx *ctx, ProbeJob &job, uint64_t n_bound, const uint64_t *d_n,
-                            const uint32_t *stop = nullptr);
+                            uint32_t *stop = nullptr, uint32_t stop_code = 0);
 // The emit of a deferred probe inside a queued iteration: the probe rows'
 // count on the device (d_n, at most job.n), two-column outputs (oc) written
 // to out + *d_out_base (d_out_base may be null), nothing when *stop is raised.
 // The caller has checked that the total fits the output.
 void probe_emit_dev(Ctx *ctx, const ProbeJob &job, const uint64_t *d_n, const int oc[4], uint64_t *out,
-                    const uint64_t *d_out_base, const uint32_t *stop);
+                    const uint64_t *d_out_base, uint32_t *stop);
 void probe_finish(ProbeJob &job, uint64_t n, uint64_t total);
 // The count pass alone, lookups recorded, no scan and no read-back; with gsel
 // set and gseg null the group heads count zero until probe_group_fixup gives

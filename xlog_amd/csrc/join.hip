@@ -129,9 +129,12 @@ struct ProbeArgs {
     unsigned long long *work;
     // queued iterations: the stop flag (raised: the count writes zero tile
     // counts, the emit nothing) and the emit's output base on the device
-    // (outputs go to out + *d_out_base)
-    const uint32_t *stop;
+    // (outputs go to out + *d_out_base).  With stop_code, a count pass whose
+    // device row count is past its bound raises the flag with that code (its
+    // own blocks then count at most the bound: the results are discarded).
+    uint32_t *stop;
     const uint64_t *d_out_base;
+    uint32_t stop_code;
 };
 // set in a row's start when its outputs come from gsrc
 constexpr uint64_t GROUP_BIT = 1ull << 63;
@@ -195,23 +198,9 @@ __device__ __forceinline__ void lookup_batch(const ProbeArgs &a, const uint64_t 
 }
 
 template <int ITEMS>
-__global__ __launch_bounds__(JB) void k_probe_count(ProbeArgs a, uint64_t *__restrict__ tile_cnt) {
-    __shared__ uint64_t s_part[JWAVES];
-    const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
-    if (a.stop && *a.stop) {
-        if (tid == 0) tile_cnt[blockIdx.x] = 0;
-        return;
-    }
-    if (a.d_n) {
-        // deferred count: the grid covers a bound; tiles past the real rows count zero
-        if (*a.d_n < a.n) a.n = *a.d_n;
-        if (a.work && blockIdx.x == 0 && tid == 0) atomicAdd(a.work, (unsigned long long)a.n);
-        if ((uint64_t)blockIdx.x * tile_rows(ITEMS) >= a.n) {
-            if (tid == 0) tile_cnt[blockIdx.x] = 0;
-            return;
-        }
-    }
-    const uint64_t wbase = (uint64_t)blockIdx.x * tile_rows(ITEMS) + (uint64_t)wave * (ITEMS * WAVE);
+__device__ __forceinline__ void probe_count_tile(const ProbeArgs &a, uint64_t tile, uint64_t *__restrict__ tile_cnt,
+                                                 uint64_t *s_part, int tid, int lane, int wave) {
+    const uint64_t wbase = tile * tile_rows(ITEMS) + (uint64_t)wave * (ITEMS * WAVE);
     uint64_t rows[ITEMS];
 #pragma unroll
     for (int r = 0; r < ITEMS; ++r) {
@@ -241,7 +230,33 @@ __global__ __launch_bounds__(JB) void k_probe_count(ProbeArgs a, uint64_t *__res
     if (tid == 0) {
         uint64_t t = 0;
         for (int w = 0; w < JWAVES; ++w) t += s_part[w];
-        tile_cnt[blockIdx.x] = t;
+        tile_cnt[tile] = t;
+    }
+}
+
+// One tile per block, or, with a device row count (a.d_n; a.n is then the
+// bound), a grid of a few blocks per CU striding over the bound's tiles: the
+// tiles past the real rows count zero at the cost of one store each.
+template <int ITEMS>
+__global__ __launch_bounds__(JB) void k_probe_count(ProbeArgs a, uint64_t *__restrict__ tile_cnt) {
+    __shared__ uint64_t s_part[JWAVES];
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
+    if (!a.d_n) {
+        probe_count_tile<ITEMS>(a, blockIdx.x, tile_cnt, s_part, tid, lane, wave);
+        return;
+    }
+    if (a.stop && *a.stop) return;  // a stopped queue: nothing reads these counts
+    const uint64_t bound_tiles = (a.n + tile_rows(ITEMS) - 1) / tile_rows(ITEMS);
+    if (*a.d_n > a.n && a.stop_code && blockIdx.x == 0 && tid == 0) atomicCAS(a.stop, 0u, a.stop_code);
+    if (*a.d_n < a.n) a.n = *a.d_n;
+    if (a.work && blockIdx.x == 0 && tid == 0) atomicAdd(a.work, (unsigned long long)a.n);
+    for (uint64_t t = blockIdx.x; t < bound_tiles; t += gridDim.x) {
+        if (t * tile_rows(ITEMS) >= a.n) {
+            if (tid == 0) tile_cnt[t] = 0;
+            continue;
+        }
+        probe_count_tile<ITEMS>(a, t, tile_cnt, s_part, tid, lane, wave);
+        __syncthreads();  // s_part is reused by the next tile
     }
 }
 
@@ -263,29 +278,23 @@ __device__ __forceinline__ void make_words(const OutSpec &o, const uint32_t v[4]
     else *w1 = 0;
 }
 
-// Emits the outputs of tiles [t0, t0 + gridDim.x); output index 0 is the
-// first output of tile t0.
+// The outputs of one probe tile (k_probe_emit).
+struct EmitSmem {
+    uint64_t wtot[JWAVES];
+    uint64_t ex[JWAVES][WAVE + 1];
+    uint64_t row[JWAVES][WAVE];
+    uint64_t st[JWAVES][WAVE];
+};
 template <int ITEMS>
-__global__ __launch_bounds__(JB) void k_probe_emit(ProbeArgs a, const uint64_t *__restrict__ tile_off, uint64_t t0,
-                                                   OutSpec spec, uint64_t *__restrict__ out0,
-                                                   uint64_t *__restrict__ out1) {
-    __shared__ uint64_t s_wtot[JWAVES];
-    __shared__ uint64_t s_ex[JWAVES][WAVE + 1];
-    __shared__ uint64_t s_row[JWAVES][WAVE];
-    __shared__ uint64_t s_st[JWAVES][WAVE];
-    const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
-    const uint64_t tile = t0 + blockIdx.x;
+__device__ __forceinline__ void probe_emit_tile(const ProbeArgs &a, const uint64_t *__restrict__ tile_off, uint64_t t0,
+                                                uint64_t tile, const OutSpec &spec, uint64_t *__restrict__ out0,
+                                                uint64_t *__restrict__ out1, EmitSmem &sm, int tid, int lane,
+                                                int wave) {
+    uint64_t *s_wtot = sm.wtot;
+    auto &s_ex = sm.ex;
+    auto &s_row = sm.row;
+    auto &s_st = sm.st;
     const uint64_t wbase = tile * tile_rows(ITEMS) + (uint64_t)wave * (ITEMS * WAVE);
-    if (a.stop && *a.stop) return;
-    if (a.d_n) {  // the row count on the device: tiles past it emit nothing
-        if (*a.d_n < a.n) a.n = *a.d_n;
-        if (tile * tile_rows(ITEMS) >= a.n) return;
-    }
-    if (a.d_out_base) {
-        const uint64_t ob = *a.d_out_base;
-        out0 += ob;
-        if (out1) out1 += ob;
-    }
 
     // pass 1 over this wave's rows: all ITEMS lookups issued together (their
     // latencies overlap) and kept in registers for the expansion
@@ -379,6 +388,34 @@ __global__ __launch_bounds__(JB) void k_probe_emit(ProbeArgs a, const uint64_t *
         base += total;
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    }
+}
+
+// Emits the outputs of tiles [t0, t0 + gridDim.x); output index 0 is the
+// first output of tile t0.  With a device row count (a.d_n; a.n is then the
+// bound, t0 is 0) a grid of a few blocks per CU strides over the real tiles;
+// a.d_out_base then offsets the output.
+template <int ITEMS>
+__global__ __launch_bounds__(JB) void k_probe_emit(ProbeArgs a, const uint64_t *__restrict__ tile_off, uint64_t t0,
+                                                   OutSpec spec, uint64_t *__restrict__ out0,
+                                                   uint64_t *__restrict__ out1) {
+    __shared__ EmitSmem sm;
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
+    if (!a.d_n) {
+        probe_emit_tile<ITEMS>(a, tile_off, t0, t0 + blockIdx.x, spec, out0, out1, sm, tid, lane, wave);
+        return;
+    }
+    if (a.stop && *a.stop) return;
+    if (*a.d_n < a.n) a.n = *a.d_n;
+    if (a.d_out_base) {
+        const uint64_t ob = *a.d_out_base;
+        out0 += ob;
+        if (out1) out1 += ob;
+    }
+    const uint64_t tiles = (a.n + tile_rows(ITEMS) - 1) / tile_rows(ITEMS);
+    for (uint64_t t = blockIdx.x; t < tiles; t += gridDim.x) {
+        probe_emit_tile<ITEMS>(a, tile_off, 0, t, spec, out0, out1, sm, tid, lane, wave);
+        __syncthreads();  // the shared arrays are reused by the next tile
     }
 }
 
@@ -588,7 +625,8 @@ uint64_t probe_prepare(Ctx *ctx, ProbeJob &job) {
 // lookups are sized for n_bound; nothing is read back.  probe_finish then
 // takes the row count and the total (read back by the caller together with
 // whatever else it needs: d_total() points at the total).
-void probe_prepare_deferred(Ctx *ctx, ProbeJob &job, uint64_t n_bound, const uint64_t *d_n, const uint32_t *stop) {
+void probe_prepare_deferred(Ctx *ctx, ProbeJob &job, uint64_t n_bound, const uint64_t *d_n, uint32_t *stop,
+                            uint32_t stop_code) {
     job.items = JITEMS;
     job.n = n_bound;
     job.tiles = (n_bound + tile_rows(job.items) - 1) / tile_rows(job.items);
@@ -602,6 +640,7 @@ void probe_prepare_deferred(Ctx *ctx, ProbeJob &job, uint64_t n_bound, const uin
     ProbeArgs a = probe_args(job);
     a.d_n = d_n;
     a.stop = stop;
+    a.stop_code = stop_code;
     XH_REQUIRE(!job.pre_cnt && job.record_lookups, XLOG_HIP_INVALID_ARG, "deferred probe: recorded lookups only");
     job.rec_start = Buf<uint64_t>(ctx, n_bound);
     job.rec_cnt = Buf<uint32_t>(ctx, n_bound);
@@ -610,8 +649,8 @@ void probe_prepare_deferred(Ctx *ctx, ProbeJob &job, uint64_t n_bound, const uin
     {
         Prof prof(ctx, XLOG_HIP_KERNEL_PROBE_COUNT, 0.0);
         a.work = prof.work(36.0);  // 36 B per real row, counted on the device
-        hipLaunchKernelGGL(k_probe_count<JITEMS>, dim3((unsigned)job.tiles), dim3(JB), 0, ctx->stream, a,
-                           job.toff.p);
+        hipLaunchKernelGGL(k_probe_count<JITEMS>, dim3(persistent_grid(ctx, job.tiles, 16)), dim3(JB), 0, ctx->stream,
+                           a, job.toff.p);
         XH_CHECK_HIP(hipGetLastError());
     }
     // tiles past the real rows hold zero counts
@@ -619,7 +658,7 @@ void probe_prepare_deferred(Ctx *ctx, ProbeJob &job, uint64_t n_bound, const uin
 }
 
 void probe_emit_dev(Ctx *ctx, const ProbeJob &job, const uint64_t *d_n, const int oc[4], uint64_t *out,
-                    const uint64_t *d_out_base, const uint32_t *stop) {
+                    const uint64_t *d_out_base, uint32_t *stop) {
     if (job.n == 0 || job.tiles == 0 || !job.rec_cnt.p) return;  // nothing can match (see probe_prepare_deferred)
     ProbeArgs a = probe_args(job);
     a.pre_start = job.rec_start.p;  // the count pass's recorded lookups
@@ -631,8 +670,8 @@ void probe_emit_dev(Ctx *ctx, const ProbeJob &job, const uint64_t *d_n, const in
     // per probe row its record (20 B with the row) and per match 12 B, counted on the device
     Prof prof(ctx, XLOG_HIP_KERNEL_PROBE_EMIT, 0.0);
     add_work_rows(ctx, prof.work(1.0), d_n, job.n, 20, job.toff.p + job.tiles, ~0ull, 12, nullptr, stop);
-    hipLaunchKernelGGL(k_probe_emit<JITEMS>, dim3((unsigned)job.tiles), dim3(JB), 0, ctx->stream, a, job.toff.p, 0ull,
-                       spec, out, nullptr);
+    hipLaunchKernelGGL(k_probe_emit<JITEMS>, dim3(persistent_grid(ctx, job.tiles, 16)), dim3(JB), 0, ctx->stream, a,
+                       job.toff.p, 0ull, spec, out, nullptr);
     XH_CHECK_HIP(hipGetLastError());
 }
 void probe_finish(ProbeJob &job, uint64_t n, uint64_t total) {

@@ -128,17 +128,30 @@ __global__ __launch_bounds__(SelShape<Sel>::block) void k_select(const uint64_t 
     __shared__ uint32_t s_wc[SEL_WAVES];
     __shared__ uint64_t s_sel[4];
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
-    // every block takes its ticket, so that the counter stays in step with the
-    // host's base, before a stop raised by an earlier launch of a queued
-    // iteration ends it (the flag cannot change while this kernel runs, so
-    // every block of the grid returns here or none does)
+    // A row count on the device (d_n; n is then the bound the tiles' scratch
+    // was sized for) makes the launch persistent: a grid of a few blocks per
+    // CU takes tickets from a zeroed counter (ticket_base 0) until they pass
+    // the tiles that hold rows, so its cost follows the real count, not the
+    // bound; the last tile that holds rows (tile 0 when there are none)
+    // writes the count.  Otherwise every block takes one ticket, from the
+    // context's counter.  A stop raised by an earlier launch of a queued
+    // iteration (it cannot change while this kernel runs) ends every block.
+    const bool persist = d_n != nullptr;
+    if (persist) {
+        if (stop && *stop) return;
+        n = *d_n < n ? *d_n : n;
+        const uint64_t used = n ? (n + SEL_TILE - 1) / SEL_TILE : 1;
+        ntiles = used < ntiles ? used : ntiles;
+        if (blockIdx.x >= ntiles) return;  // more blocks than tiles: these take no ticket
+    }
+    for (;;) {
     if (tid == 0) s_tile = atomicAdd(ticket, 1ull) - ticket_base;
-    if (stop && *stop) return;
-    // a row count still on the device replaces the bound the grid was sized
-    // for; tiles past it select nothing but keep the look-back chain
-    if (d_n) n = *d_n < n ? *d_n : n;
     __syncthreads();
     const uint64_t tile = s_tile;
+    if (tile >= ntiles) {
+        if (persist && tid == 0) persist_done(ticket, gridDim.x < ntiles ? gridDim.x : ntiles);
+        return;
+    }
     if constexpr (!Sel::kWindow) {
         if (tid == 0) {
             uint64_t first = tile * SEL_TILE, last = first + SEL_TILE;
@@ -225,6 +238,9 @@ __global__ __launch_bounds__(SelShape<Sel>::block) void k_select(const uint64_t 
         uint64_t m = __ballot(f);
         if (f) sel.emit(pos + (uint64_t)__popcll(m & lt_mask), wbase + (uint64_t)r * WAVE + lane, k[r]);
         pos += (uint64_t)__popcll(m);
+    }
+    if (!persist) return;
+    __syncthreads();  // the next tile reuses the shared words
     }
 }
 
@@ -687,10 +703,13 @@ __global__ __launch_bounds__(MRG_BLOCK) void k_merge(const uint64_t *__restrict_
     if (dv.off()) return;
     dv.counts(na, nb);
     const uint64_t total = na + nb;
-    const uint64_t d0 = (uint64_t)blockIdx.x * MRG_TILE;
-    if (d0 >= total) return;  // a tile past the rows (the grid covers the bounds)
+    // with device counts a grid of a few blocks per CU strides over the real tiles
+    const bool persist = dv.d_na || dv.d_nb;
+    for (uint64_t tile = blockIdx.x;; tile += gridDim.x) {
+    const uint64_t d0 = tile * MRG_TILE;
+    if (d0 >= total) return;
     const uint64_t d1 = (d0 + MRG_TILE < total) ? d0 + MRG_TILE : total;
-    if (tid < 2) s_split[tid] = split[blockIdx.x + tid];
+    if (tid < 2) s_split[tid] = split[tile + tid];
     __syncthreads();
     // For sorted inputs the splits are monotone and the clamp changes nothing; for inputs that are not
     // sorted it keeps the tile's ranges inside a and b (and LDS) instead of inverting them.
@@ -730,6 +749,9 @@ __global__ __launch_bounds__(MRG_BLOCK) void k_merge(const uint64_t *__restrict_
         if ((uint32_t)j < cnt) s[td + j] = r[j];
     __syncthreads();
     for (uint32_t i = tid; i < len; i += MRG_BLOCK) out[d0 + i] = s[i];
+    if (!persist) return;
+    __syncthreads();  // s is reused by the next tile
+    }
 }
 
 // profiling of launches sized by bounds: the real row counts (up to two
@@ -897,13 +919,22 @@ static void run_select(Ctx *ctx, const uint64_t *in, uint64_t n, const Sel &sel,
     XH_REQUIRE(tiles < (1ull << 31), XLOG_HIP_CAPACITY_OVERFLOW, "select: input too large");
     uint64_t tag;
     uint64_t *status = select_status(ctx, tiles, &tag);
-    unsigned long long tb = ctx->take_tickets(1, tiles);
+    // tickets: one per block from the context's counter, or, for a persistent launch (device row
+    // count), from a counter zeroed for it
+    unsigned long long *tk = ctx->tickets + 1, tb = 0;
+    unsigned grid = (unsigned)tiles;
+    if (d_n) {
+        tk = ctx->tickets + PERSIST_TICKET_SLOT;  // at zero: the last launch's last block reset it
+        grid = persistent_grid(ctx, tiles, 8);
+    } else {
+        tb = ctx->take_tickets(1, tiles);
+    }
     // 8 B per input row; with a device row count, counted on the device
     Prof prof(ctx, XLOG_HIP_KERNEL_SELECT, d_n ? 0.0 : 8.0 * (double)n);
     if (d_n) add_work_rows(ctx, prof.work(8.0), d_n, n, 1, nullptr, 0, 0, nullptr, stop);
     const size_t dyn = Sel::kWindow ? (size_t)WIN_CAP * sizeof(uint64_t) : 0;
-    hipLaunchKernelGGL(k_select<Sel>, dim3((unsigned)tiles), dim3(SelShape<Sel>::block), dyn, ctx->stream, in, n, sel, d_count,
-                       status, tag, ctx->tickets + 1, tb, tiles, d_n, stop);
+    hipLaunchKernelGGL(k_select<Sel>, dim3(grid), dim3(SelShape<Sel>::block), dyn, ctx->stream, in, n, sel, d_count,
+                       status, tag, tk, tb, tiles, d_n, stop);
     XH_CHECK_HIP(hipGetLastError());
 }
 
@@ -1097,7 +1128,13 @@ void merge_sorted_dev(Ctx *ctx, const uint64_t *a, uint64_t na, const uint64_t *
     const bool dev = d_na || d_nb;
     Prof prof(ctx, XLOG_HIP_KERNEL_MERGE, dev ? 0.0 : 16.0 * (double)total);
     if (dev) add_work_rows(ctx, prof.work(16.0), d_na, na, 1, d_nb, nb, 1, skip, stop);
-    hipLaunchKernelGGL(k_merge, dim3((unsigned)tiles), dim3(MRG_BLOCK), 0, ctx->stream, a, na, b, nb, split.p, out, dv);
+    static const uint32_t merge_per_cu = [] {
+        const char *e = getenv("XLOG_HIP_MERGE_PER_CU");
+        const unsigned long v = e ? strtoul(e, nullptr, 10) : 0ul;
+        return v ? (uint32_t)v : 32u;
+    }();
+    hipLaunchKernelGGL(k_merge, dim3(dev ? persistent_grid(ctx, tiles, merge_per_cu) : (unsigned)tiles), dim3(MRG_BLOCK), 0,
+                       ctx->stream, a, na, b, nb, split.p, out, dv);
     XH_CHECK_HIP(hipGetLastError());
 }
 

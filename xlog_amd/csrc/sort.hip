@@ -228,22 +228,32 @@ __global__ __launch_bounds__(BLOCK) void k_onesweep(
     // started before it or belong to its own group of 8 * chunk tickets,
     // whatever order the blocks are dispatched in.  Block-uniform, so it (and
     // every per-round bound derived from it) stays in scalar registers.
+    // A key count on the device (d_n: a queued iteration's sort; n and tiles
+    // are then bounds) makes the pass persistent: a grid of at most the blocks
+    // the device holds takes tickets in plain order from a counter zeroed for
+    // the pass (ticket_base 0) until they pass the tiles that hold keys, so a
+    // tile waits only on tiles whose blocks took their tickets before it.  A
+    // stop raised by an earlier launch of the queue ends every block.
+    const bool persist = d_n != nullptr;
+    uint32_t real_tiles = tiles;
+    if (persist) {
+        if (stop && *stop) return;
+        if (*d_n < n) n = *d_n;
+        real_tiles = (uint32_t)((n + (uint64_t)(BLOCK * ITEMS) - 1) / (uint64_t)(BLOCK * ITEMS));
+        if (blockIdx.x >= real_tiles) return;  // more blocks than tiles: these take no ticket
+    }
+    for (;;) {
     if (ticket && tid == 0) s_ticket = (uint32_t)(atomicAdd(ticket, 1ull) - ticket_base);
     for (int i = tid; i < (BLOCK / WAVE) * 256; i += BLOCK) (&s_wcnt[0][0])[i] = 0;
     __syncthreads();
-    const uint32_t tile = chunk_tile(ticket ? __builtin_amdgcn_readfirstlane(s_ticket) : blockIdx.x, chunk, tiles);
-    if (tile == TILE_NONE) return;
-    // Queued iterations: the key count on the device (n and tiles are the
-    // bounds the grid was sized for) and the stop flag.  A tile past the keys,
-    // or any tile of a stopped pass, only clears its slot of the next pass's
-    // status buffer, so that after every pass that buffer is clean over all
-    // `tiles` tiles whatever the device count was.
-    if ((stop && *stop) || (d_n && (uint64_t)tile * (BLOCK * ITEMS) >= *d_n)) {
-        if (digit_thread) status_next[(uint64_t)tile * 256 + d] = 0u;
+    const uint32_t tile = persist ? __builtin_amdgcn_readfirstlane(s_ticket)
+                                  : chunk_tile(ticket ? __builtin_amdgcn_readfirstlane(s_ticket) : blockIdx.x, chunk,
+                                               tiles);
+    if (tile == TILE_NONE || tile >= real_tiles) {
+        if (persist && tid == 0) persist_done(ticket, gridDim.x < real_tiles ? gridDim.x : real_tiles);
         return;
     }
-    if (d_n && *d_n < n) n = *d_n;
-    {  // one tile per block
+    {  // one tile
         const uint64_t wbase =
             (uint64_t)tile * (BLOCK * ITEMS) + (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane(wave) * (ITEMS * WAVE);
         // valid keys of this wave (0..ITEMS*WAVE) and of its round r (0..64)
@@ -408,6 +418,9 @@ __global__ __launch_bounds__(BLOCK) void k_onesweep(
                 if (HAS_VAL) vout[o] = s_vals[i];
             }
         }
+    }
+    if (!persist) return;
+    __syncthreads();  // the shared arrays are reused by the next tile
     }
 }
 
@@ -583,11 +596,10 @@ int radix_sort_dev(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint64_t n_bo
     const uint64_t tiles = (n_bound + tile_keys - 1) / tile_keys;
     SortState &st = sort_state(ctx, tiles);
     uint32_t *hist = st.hist, *off = st.hist + 8 * 256;
+    // persistent passes: at most the blocks the device holds, tickets from a counter zeroed per pass
     const uint32_t cap = pass_capacity<false, SORT_BLOCK_K, SORT_ITEMS_K>(ctx);
-    uint32_t chunk = cap / 16 < 8 ? (cap / 16 > 0 ? cap / 16 : 1) : 8;
-    if (tiles / 64 < chunk) chunk = tiles / 64 > 0 ? (uint32_t)(tiles / 64) : 1;
-    const uint64_t nchunks = (tiles + chunk - 1) / chunk;
-    const unsigned grid = (unsigned)(8 * ((nchunks + 7) / 8) * chunk);
+    const unsigned grid = (unsigned)std::min<uint64_t>(tiles, cap);
+    unsigned long long *tk = ctx->tickets + PERSIST_TICKET_SLOT + 1;
     fill_u32(ctx, hist, 0u, 8 * 256);
     {
         Prof prof(ctx, XLOG_HIP_KERNEL_SORT_HIST, 0.0);
@@ -599,31 +611,30 @@ int radix_sort_dev(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint64_t n_bo
         hipLaunchKernelGGL(k_digit_offsets, dim3(1), dim3(64), 0, ctx->stream, hist, off);
         XH_CHECK_HIP(hipGetLastError());
     }
+    // The first pass reads a status buffer made clean over every tile; each pass clears the entries of
+    // its tiles that hold keys in the next pass's buffer, which is all the next pass reads.  After the
+    // sort neither buffer is known to be clean past those tiles: both are marked dirty over the bound.
     int cur = (st.dirty[0] == 0) ? 0 : (st.dirty[1] == 0 ? 1 : 0);
+    if (st.dirty[cur]) {
+        fill_u32(ctx, st.status[cur], 0u, st.dirty[cur] * 256);
+        st.dirty[cur] = 0;
+    }
     int passes = 0;
     for (int dgt = 0; dgt < 8; ++dgt) {
         if (!((known_digits >> dgt) & 1u)) continue;
         const int nxt = 1 - cur;
-        if (st.dirty[cur]) {
-            fill_u32(ctx, st.status[cur], 0u, st.dirty[cur] * 256);
-            st.dirty[cur] = 0;
-        }
         Prof prof(ctx, XLOG_HIP_KERNEL_SORT_PASS, 0.0);
         add_work_rows(ctx, prof.work(16.0), d_n, n_bound, 1, nullptr, 0, 0, nullptr, stop);
-        unsigned long long *tk = sort_tickets() ? ctx->tickets + 2 : nullptr;
-        const unsigned long long tb = tk ? ctx->take_tickets(2, grid) : 0ull;
         hipLaunchKernelGGL((k_onesweep<false, SORT_BLOCK_K, SORT_ITEMS_K>), dim3(grid), dim3(SORT_BLOCK_K), 0,
                            ctx->stream, *keys, *keys_alt, nullptr, nullptr, n_bound, (uint32_t)tiles, 8 * dgt,
-                           off + dgt * 256, st.status[cur], st.status[nxt], chunk, tk, tb, d_n, stop);
+                           off + dgt * 256, st.status[cur], st.status[nxt], 1u, tk, 0ull, d_n, stop);
         XH_CHECK_HIP(hipGetLastError());
-        // this pass wrote the status of at most `tiles` tiles in cur and cleared
-        // nxt over all `tiles` tiles (stopped and empty tiles included)
-        st.dirty[cur] = tiles;
-        if (st.dirty[nxt] <= tiles) st.dirty[nxt] = 0;
         std::swap(*keys, *keys_alt);
         cur = nxt;
         ++passes;
     }
+    st.dirty[0] = std::max<uint64_t>(st.dirty[0], tiles);
+    st.dirty[1] = std::max<uint64_t>(st.dirty[1], tiles);
     return passes;
 }
 
