@@ -765,6 +765,13 @@ static uint64_t join_chunk_rows() {
     }
     return (1ull << 30) - 1;
 }
+// XLOG_HIP_TRACE=1: one line on stderr per fixpoint iteration, per queue of
+// iterations and per piece of a large join step (progress of long runs).
+static bool trace_on() {
+    const char *e = getenv("XLOG_HIP_TRACE");
+    return e && e[0] == '1';
+}
+
 // The emit side of a join step whose count pass has run (job.total known).
 // digits: the sort's known varying digits (0: from the histograms).
 static uint64_t join_emit(Ctx *ctx, ProbeJob &job, const int oc[4], uint64_t **out, uint64_t max_rows,
@@ -792,6 +799,10 @@ static uint64_t join_emit(Ctx *ctx, ProbeJob &job, const int oc[4], uint64_t **o
         uint64_t t1 = t0 + 1;
         while (t1 < job.tiles && off[t1 + 1] - off[t0] <= kChunkRows) ++t1;
         const uint64_t m = off[t1] - off[t0];
+        if (trace_on())
+            fprintf(stderr, "[xlog_hip] join step of %llu rows: piece of %llu rows from tile %llu of %llu\n",
+                    (unsigned long long)total, (unsigned long long)m, (unsigned long long)t0,
+                    (unsigned long long)job.tiles);
         if (m) {
             uint64_t *b = static_cast<uint64_t *>(ctx->alloc(m * sizeof(uint64_t)));
             {
@@ -2032,6 +2043,8 @@ struct Driver {
             note_delta(p, d.n);
         }
         deltas.push_back(total);
+        if (trace_on()) fprintf(stderr, "[xlog_hip] iteration %llu: delta %llu\n", (unsigned long long)it,
+                                (unsigned long long)total);
         if (total == 0) return 0;
         for (uint32_t p = 0; p < n_preds; ++p) {
             if (!idb[p] || delta[p].n == 0) continue;
@@ -2404,7 +2417,7 @@ struct Driver {
         const uint64_t *hs = ctx->host_scalars;
         const uint32_t stopped = (uint32_t)hs[0];  // 0, or queue position + 1
         const uint64_t complete = stopped ? (uint64_t)stopped - 1 : Q;
-        if (env_u64("XLOG_HIP_TRACE_QUEUE", 0)) {  // one line per queue on stderr
+        if (trace_on()) {
             fprintf(stderr, "[xlog_hip] join queue after iteration %llu: %llu queued, %llu complete; delta bounds",
                     (unsigned long long)it, (unsigned long long)Q, (unsigned long long)complete);
             for (uint64_t k = 0; k < Q; ++k) fprintf(stderr, " %llu", (unsigned long long)Lb[k][0]);
@@ -2547,6 +2560,8 @@ struct Driver {
                 probe_finish(*kv.second, delta[p0].n, ctx->host_scalars[q++]);
             }
             deltas.push_back(total);
+            if (trace_on()) fprintf(stderr, "[xlog_hip] iteration %llu: delta %llu\n", (unsigned long long)it,
+                                    (unsigned long long)total);
             if (total == 0) return it;
             for (uint32_t p = 0; p < n_preds; ++p) {
                 if (!idb[p] || delta[p].n == 0) continue;
