@@ -354,8 +354,14 @@ static uint64_t *alloc_keys(Ctx *ctx, uint64_t n) {
 struct Bags {
     Ctx *ctx;
     std::vector<std::pair<uint64_t *, uint64_t>> v;
+    // per bag: 0, or (its rows grouped by their high word, in ascending order)
+    // a bound on the number of groups
+    std::vector<uint64_t> grouped;
     explicit Bags(Ctx *c) : ctx(c) {}
-    Bags(Bags &&o) noexcept : ctx(o.ctx), v(std::move(o.v)) { o.v.clear(); }
+    Bags(Bags &&o) noexcept : ctx(o.ctx), v(std::move(o.v)), grouped(std::move(o.grouped)) {
+        o.v.clear();
+        o.grouped.clear();
+    }
     Bags(const Bags &) = delete;
     Bags &operator=(const Bags &) = delete;
     ~Bags() { clear(); }
@@ -363,9 +369,11 @@ struct Bags {
         for (auto &b : v)
             if (b.first) ctx->free(b.first);
         v.clear();
+        grouped.clear();
     }
-    void add(Owned &o, uint64_t n) {
+    void add(Owned &o, uint64_t n, uint64_t groups = 0) {
         v.push_back({o.p, n});
+        grouped.push_back(groups);
         o.release();
     }
     uint64_t rows() const {
@@ -1691,6 +1699,10 @@ struct JoinPlanStep {
 struct BodyPlan {
     JoinPlanStep step[MAX_BODY];
     int head[2] = {0, 1};
+    // the body's output keeps the first atom's first column as its high word
+    // (each step keeps binding value 0 first): read from a sorted relation,
+    // it comes out grouped by that column, in ascending order
+    bool grouped = false;
 };
 BodyPlan plan_body(const Rule &r) {
     BodyPlan bp;
@@ -1705,8 +1717,10 @@ BodyPlan plan_body(const Rule &r) {
         XH_REQUIRE(h0 >= 0 && h1 >= 0, XLOG_HIP_UNSUPPORTED, "plan: head variable not bound by the body");
         bp.head[0] = h0;
         bp.head[1] = h1;
+        bp.grouped = h0 == 0;
         return bp;
     }
+    bp.grouped = true;
     for (int j = 1; j < r.nb; ++j) {
         const Atom &a = r.b[j];
         XH_REQUIRE(a.v[0] != a.v[1], XLOG_HIP_UNSUPPORTED, "plan: repeated variable inside an atom");
@@ -1745,6 +1759,7 @@ BodyPlan plan_body(const Rule &r) {
         bp.step[j].apos = apos;
         bp.step[j].sel[0] = sel[0];
         bp.step[j].sel[1] = sel[1];
+        bp.grouped = bp.grouped && sel[0] == 0;
         vars[0] = cand_var[sel[0]];
         vars[1] = cand_var[sel[1]];
     }
@@ -1869,6 +1884,7 @@ struct Driver {
         uint64_t bn = rel[0]->n;
         Owned owned(ctx);  // the binding when an earlier join of this body made it
         if (bn == 0) return;
+        const uint64_t src_rows = bn;
         if (r.nb == 1) {
             // head projection of a single atom
             const int h0 = bp.head[0], h1 = bp.head[1];
@@ -1882,7 +1898,7 @@ struct Driver {
                 RelOut bo{{o, nullptr, nullptr, nullptr}};
                 LAUNCH_1D(k_project, bn, bv, bn, s, bo);
             }
-            out.add(go, bn);
+            out.add(go, bn, bp.grouped ? group_bound(bn) : 0);
             return;
         }
         for (int j = 1; j < r.nb; ++j) {
@@ -1905,8 +1921,18 @@ struct Driver {
             bn = on;
             if (bn == 0) return;
         }
-        out.add(owned, bn);
+        out.add(owned, bn, bp.grouped ? group_bound(src_rows) : 0);
     }
+
+    // Groups of a body's output that keeps the high word of `rows` sorted
+    // source rows: at most one per row and one per value of the domain.
+    uint64_t group_bound(uint64_t rows) const {
+        return std::max<uint64_t>(1, domain ? std::min(rows, domain) : rows);
+    }
+    // A grouped bag whose groups average at most this many rows is sorted by
+    // one short-run pass (runs of more than 256 rows fall back to the digit
+    // passes); with longer groups the digit passes run directly.
+    static constexpr uint64_t SHORT_GROUP_ROWS = 64;
 
     // concat bags, sort, unique, minus full -> new canonical delta.  The count
     // stays on the device (cnt); d.n is the candidate total, a bound on it,
@@ -1919,9 +1945,12 @@ struct Driver {
             return d;
         }
         Owned cat(ctx);
+        const bool grouped = bags.v.size() == 1 && bags.grouped[0] && total < (1ull << 30) && digits &&
+                             total / bags.grouped[0] <= SHORT_GROUP_ROWS;
         if (bags.v.size() == 1) {
             cat.reset(bags.v[0].first);
             bags.v.clear();
+            bags.grouped.clear();
         } else {
             cat.reset(alloc_keys(ctx, total));
             uint64_t off = 0;
@@ -1931,7 +1960,17 @@ struct Driver {
             }
             bags.clear();
         }
-        Owned srt(ctx, sort_keys(ctx, cat.release(), total, true, 0, 8, digits));  // consumes cat
+        Owned srt(ctx);
+        if (grouped) {
+            // one bag grouped by its high word: one short-run pass (the digit passes only if a run is long)
+            Owned alt(ctx, alloc_keys(ctx, total));
+            Buf<uint64_t> sc(ctx, 3);
+            fill_u64(ctx, sc.p + 2, total, 1);
+            sort_grouped_dev(ctx, cat.p, alt.p, total, sc.p + 2, digits, nullptr, sc.p);
+            srt.reset(alt.release());
+        } else {
+            srt.reset(sort_keys(ctx, cat.release(), total, true, 0, 8, digits));  // consumes cat
+        }
         Owned o(ctx, alloc_keys(ctx, total));
         cnt = Buf<uint64_t>(ctx, 1);
         select_unique_diff(ctx, srt.p, total, against.k, against.n, o.p, cnt.p);
@@ -2345,6 +2384,17 @@ struct Driver {
             fill_u64(ctx, qs.p + blk(-1) + h, delta[heads[h]].n, 1);
             fill_u64(ctx, qs.p + blk(-1) + H + h, full[heads[h]].n, 1);
         }
+        // a head whose one variant keeps its delta's first column as the high word gets its candidates
+        // grouped by it, in ascending order: one short-run pass sorts them (sort_grouped_dev)
+        std::vector<char> grouped(H, 0);
+        std::vector<int> gsrc(H, -1);  // the delta predicate of a grouped head's variant
+        for (uint32_t h = 0; h < H; ++h) grouped[h] = nvar[h] == 1;
+        for (auto &vp : vars) {
+            grouped[hidx[vp->head]] &= vp->bp.grouped ? 1 : 0;
+            gsrc[hidx[vp->head]] = hidx[vp->dpred];
+        }
+        Buf<uint64_t> gscratch(ctx, 2 * (uint64_t)H);
+
         // ---- the queue -------------------------------------------------------------
         cur_iter = it + 1;
         for (uint64_t k = 0; k < Q; ++k) {
@@ -2393,7 +2443,10 @@ struct Driver {
                 const int p = heads[h];
                 const uint64_t *d_cand = bk + base_off[h] + nvar[h];
                 uint64_t *ka = qh[h]->C.p, *kb = qh[h]->Calt.p;
-                radix_sort_dev(ctx, &ka, &kb, Cb[k][h], d_cand, digits, stop);
+                // (groups: at most one per delta row read and per domain value)
+                if (grouped[h] && Cb[k][h] / group_bound(std::max<uint64_t>(Lb[k][gsrc[h]], 1)) <= SHORT_GROUP_ROWS)
+                    ka = sort_grouped_dev(ctx, ka, kb, Cb[k][h], d_cand, digits, stop, gscratch.p + 2 * h);
+                else radix_sort_dev(ctx, &ka, &kb, Cb[k][h], d_cand, digits, stop);
                 const uint64_t *rin = k == 0 ? full[p].k : qh[h]->R[(k - 1) & 1].p;
                 if (!rin) rin = qh[h]->R[1].p;  // an empty R read through its device count
                 select_unique_diff_dev(ctx, ka, Cb[k][h], d_cand, rin, std::max<uint64_t>(Rb[k][h], 1), pR + h,

@@ -346,6 +346,14 @@ inline unsigned persistent_grid(const Ctx *ctx, uint64_t tiles, uint32_t per_cu 
 // without a counter.
 void add_work_rows(Ctx *ctx, unsigned long long *work, const uint64_t *d_a, uint64_t a, uint32_t wa, const uint64_t *d_b,
                    uint64_t b, uint32_t wb, const uint64_t *skip, const uint32_t *stop);
+// Sort of keys grouped by their high word (every key of a high word in one
+// run, the runs in ascending order) in a queued iteration: one short-run pass
+// (each run ordered by its low word) from keys to keys_alt; when a run is
+// longer than 256 keys, the digit passes of known_digits run instead (decided
+// on the device, no read-back).  The result is in the returned buffer,
+// keys_alt; keys is overwritten.  scratch: two device words.
+uint64_t *sort_grouped_dev(Ctx *ctx, uint64_t *keys, uint64_t *keys_alt, uint64_t n_bound, const uint64_t *d_n,
+                           uint32_t known_digits, const uint32_t *stop, uint64_t *scratch);
 int radix_sort_dev(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint64_t n_bound, const uint64_t *d_n,
                    uint32_t known_digits, const uint32_t *stop);
 // sort_short_runs fused with the adjacent-compare unique: the unique keys in

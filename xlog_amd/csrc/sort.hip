@@ -438,6 +438,32 @@ __global__ __launch_bounds__(SR_BLOCK) void k_sort_short_runs(const uint64_t *__
     const uint64_t lo = short_runs_place<SR_BLOCK, SR_CORE, SR_MAX>(in, n, (uint64_t)blockIdx.x * SR_CORE, t, long_run);
     for (uint32_t i = t.pmin + threadIdx.x; i < t.pmax; i += SR_BLOCK) out[lo + i] = ((uint64_t)t.hi[i] << 32) | t.lo[i];
 }
+// The same over a key count on the device (n is its bound): a grid of a few
+// blocks per CU strides over the cores; nothing when *stop is raised.
+__global__ __launch_bounds__(SR_BLOCK) void k_sort_short_runs_dev(const uint64_t *__restrict__ in, uint64_t n,
+                                                                  const uint64_t *d_n, uint64_t *__restrict__ out,
+                                                                  uint64_t *long_run, const uint32_t *stop) {
+    __shared__ SrTile t;
+    if (stop && *stop) return;
+    if (*d_n < n) n = *d_n;
+    for (uint64_t core = (uint64_t)blockIdx.x * SR_CORE; core < n; core += (uint64_t)gridDim.x * SR_CORE) {
+        const uint64_t lo = short_runs_place<SR_BLOCK, SR_CORE, SR_MAX>(in, n, core, t, long_run);
+        for (uint32_t i = t.pmin + threadIdx.x; i < t.pmax; i += SR_BLOCK)
+            out[lo + i] = ((uint64_t)t.hi[i] << 32) | t.lo[i];
+        __syncthreads();  // t is reused by the next core
+    }
+}
+// skip = 1 unless the short-run pass found a long run (and the queue runs)
+__global__ void k_fallback_skip(const uint64_t *long_run, const uint32_t *stop, uint32_t *skip) {
+    *skip = ((stop && *stop) || *long_run == 0) ? 1u : 0u;
+}
+__global__ void k_copy_dev(const uint64_t *__restrict__ in, uint64_t n, const uint64_t *d_n, uint64_t *__restrict__ out,
+                           const uint32_t *skip) {
+    if (*skip) return;
+    if (*d_n < n) n = *d_n;
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) out[i] = in[i];
+}
 
 __global__ void k_fill_u32(uint32_t *p, uint32_t v, uint64_t n) {
     uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
@@ -547,6 +573,10 @@ bool sort_tickets() {
     const char *e = getenv("XLOG_HIP_SORT_TICKETS");
     return e && e[0] == '1';
 }
+static bool sort_persist() {
+    const char *e = getenv("XLOG_HIP_SORT_PERSIST");
+    return e && e[0] == '1';
+}
 
 // The high-word route of a full-key sort (keys only, at least
 // HYBRID_MIN_KEYS keys; XLOG_HIP_SORT_HYBRID=0 turns it off, read at each
@@ -584,6 +614,33 @@ void sort_short_runs(Ctx *ctx, const uint64_t *in, uint64_t n, uint64_t *out, ui
     Prof prof(ctx, XLOG_HIP_KERNEL_SORT_RUNS, 16.0 * (double)n);  // reads and writes every key once
     hipLaunchKernelGGL(k_sort_short_runs, dim3((unsigned)blocks), dim3(SR_BLOCK), 0, ctx->stream, in, n, out, d_long);
     XH_CHECK_HIP(hipGetLastError());
+}
+
+uint64_t *sort_grouped_dev(Ctx *ctx, uint64_t *keys, uint64_t *keys_alt, uint64_t n_bound, const uint64_t *d_n,
+                           uint32_t known_digits, const uint32_t *stop, uint64_t *scratch) {
+    if (n_bound == 0) return keys_alt;
+    XH_REQUIRE(n_bound < (1ull << 30), XLOG_HIP_CAPACITY_OVERFLOW, "grouped sort: limited to 2^30 - 1 keys");
+    uint64_t *d_long = scratch;
+    uint32_t *skip = reinterpret_cast<uint32_t *>(scratch + 1);
+    fill_u64(ctx, d_long, 0ull, 1);
+    {
+        Prof prof(ctx, XLOG_HIP_KERNEL_SORT_RUNS, 0.0);
+        add_work_rows(ctx, prof.work(16.0), d_n, n_bound, 1, nullptr, 0, 0, nullptr, stop);  // every key read, written
+        const uint64_t cores = (n_bound + SR_CORE - 1) / SR_CORE;
+        hipLaunchKernelGGL(k_sort_short_runs_dev, dim3(persistent_grid(ctx, cores, 8)), dim3(SR_BLOCK), 0, ctx->stream,
+                           keys, n_bound, d_n, keys_alt, d_long, stop);
+        XH_CHECK_HIP(hipGetLastError());
+    }
+    // a run of more than SR_MAX keys: every digit pass, from the unsorted keys (their buffer is intact)
+    hipLaunchKernelGGL(k_fallback_skip, dim3(1), dim3(1), 0, ctx->stream, d_long, stop, skip);
+    XH_CHECK_HIP(hipGetLastError());
+    uint64_t *a = keys, *b = keys_alt;
+    radix_sort_dev(ctx, &a, &b, n_bound, d_n, known_digits, skip);
+    if (a == keys)  // an even number of passes ends where the keys started: bring the result over
+        hipLaunchKernelGGL(k_copy_dev, dim3(grid_for(n_bound, 256, (unsigned)ctx->num_cus * 8)), dim3(256), 0,
+                           ctx->stream, keys, n_bound, d_n, keys_alt, skip);
+    XH_CHECK_HIP(hipGetLastError());
+    return keys_alt;
 }
 
 int radix_sort_dev(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint64_t n_bound, const uint64_t *d_n,
@@ -694,16 +751,28 @@ int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **va
         }
         Prof prof(ctx, XLOG_HIP_KERNEL_SORT_PASS, (has_val ? 24.0 : 16.0) * (double)n);
         unsigned long long *tk = sort_tickets() ? ctx->tickets + 2 : nullptr;
-        const unsigned long long tb = tk ? ctx->take_tickets(2, grid) : 0ull;
+        unsigned long long tb = tk ? ctx->take_tickets(2, grid) : 0ull;
+        unsigned pgrid = grid;
+        const uint64_t *pn = nullptr;
+        if (sort_persist()) {
+            // persistent: at most the blocks the device holds, tickets in plain order from the self-resetting
+            // counter, the key count from a device word (every tile holds keys, so each pass clears all of
+            // the next pass's `tiles` entries, as the index-ordered pass does)
+            tk = ctx->tickets + PERSIST_TICKET_SLOT + 1;
+            tb = 0;
+            pn = reinterpret_cast<const uint64_t *>(ctx->tickets + 12);
+            fill_u64(ctx, reinterpret_cast<uint64_t *>(ctx->tickets + 12), n, 1);
+            pgrid = (unsigned)std::min<uint64_t>(tiles, cap);
+        }
         if (has_val)
-            hipLaunchKernelGGL((k_onesweep<true, SORT_BLOCK_V, SORT_ITEMS_V>), dim3(grid), dim3(SORT_BLOCK_V), 0,
+            hipLaunchKernelGGL((k_onesweep<true, SORT_BLOCK_V, SORT_ITEMS_V>), dim3(pgrid), dim3(SORT_BLOCK_V), 0,
                                ctx->stream, *keys, *keys_alt, *vals, *vals_alt, n, (uint32_t)tiles, 8 * dgt,
-                               off + dgt * 256, st.status[cur], st.status[nxt], chunk, tk, tb, nullptr, nullptr);
+                               off + dgt * 256, st.status[cur], st.status[nxt], chunk, tk, tb, pn, nullptr);
         else
-            hipLaunchKernelGGL((k_onesweep<false, SORT_BLOCK_K, SORT_ITEMS_K>), dim3(grid), dim3(SORT_BLOCK_K), 0,
+            hipLaunchKernelGGL((k_onesweep<false, SORT_BLOCK_K, SORT_ITEMS_K>), dim3(pgrid), dim3(SORT_BLOCK_K), 0,
                                ctx->stream, (passes == 0 && src) ? src : *keys, *keys_alt, nullptr, nullptr, n,
                                (uint32_t)tiles, 8 * dgt, off + dgt * 256, st.status[cur], st.status[nxt], chunk,
-                               tk, tb, nullptr, nullptr);
+                               tk, tb, pn, nullptr);
         XH_CHECK_HIP(hipGetLastError());
         st.dirty[cur] = tiles;
         if (st.dirty[nxt] <= tiles) st.dirty[nxt] = 0;
