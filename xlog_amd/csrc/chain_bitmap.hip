@@ -508,6 +508,7 @@ struct FinalizeArgs {
     uint64_t *dmask_new;
     uint64_t *P, *pmask;  // R minus D (null when no rule reads it forward)
     unsigned long long *count;
+    unsigned long long *work;  // profiling (or null): bytes of the row words loaded and stored
 };
 
 // Per row x with candidates or an old delta row:
@@ -521,10 +522,11 @@ struct FinalizeArgs {
 template <bool PREV>
 __global__ __launch_bounds__(GW * WAVE) void k_chain_finalize(uint32_t domain, uint32_t words, uint32_t batch,
                                                               FinalizeArgs a) {
-    __shared__ unsigned long long s_cnt[GW];
+    __shared__ unsigned long long s_cnt[GW], s_work[GW];
     const int lane = threadIdx.x & (WAVE - 1);
     const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    unsigned long long cnt = 0;  // per lane
+    unsigned long long cnt = 0;   // per lane
+    unsigned long long moved = 0;  // per lane: words loaded or stored (counted when profiling)
     const uint32_t x0 = (blockIdx.x * GW + wave) * batch;
     if (x0 < domain) {
         const uint32_t nr = domain - x0 < batch ? domain - x0 : batch;
@@ -558,12 +560,21 @@ __global__ __launch_bounds__(GW * WAVE) void k_chain_finalize(uint32_t domain, u
                     const uint32_t w = g0 + lane + 64u * k;
                     if (w >= words) continue;
                     const uint64_t nw = cv[k] & ~rv[k];
+                    // C, and D and P of an old delta row, are read; R under a non-zero C word
+                    moved += (c_on ? 1u : 0u) + (PREV && d_on ? 2u : 0u) + (cv[k] ? 1u : 0u);
                     if (cv[k]) {
                         if (nw) rrow[w] = rv[k] | nw;
                         crow[w] = 0ull;
+                        moved += nw ? 2u : 1u;
                     }
-                    if (PREV && dv[k] && (pv[k] | dv[k]) != pv[k]) a.P[base + w] = pv[k] | dv[k];
-                    if (d_on || nw) drow[w] = nw;
+                    if (PREV && dv[k] && (pv[k] | dv[k]) != pv[k]) {
+                        a.P[base + w] = pv[k] | dv[k];
+                        ++moved;
+                    }
+                    if (d_on || nw) {
+                        drow[w] = nw;
+                        ++moved;
+                    }
                     cnt += (unsigned long long)__popcll(nw);
                     any |= nw != 0ull;
                 }
@@ -579,14 +590,24 @@ __global__ __launch_bounds__(GW * WAVE) void k_chain_finalize(uint32_t domain, u
         }
     }
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) cnt += __shfl_xor(cnt, o, WAVE);
-    if (lane == 0) s_cnt[wave] = cnt;
+    for (int o = 32; o > 0; o >>= 1) {
+        cnt += __shfl_xor(cnt, o, WAVE);
+        moved += __shfl_xor(moved, o, WAVE);
+    }
+    if (lane == 0) {
+        s_cnt[wave] = cnt;
+        s_work[wave] = moved;
+    }
     __syncthreads();
     if (threadIdx.x == 0) {
-        unsigned long long c = 0;
+        unsigned long long c = 0, m = 0;
 #pragma unroll
-        for (int i = 0; i < GW; ++i) c += s_cnt[i];
+        for (int i = 0; i < GW; ++i) {
+            c += s_cnt[i];
+            m += s_work[i];
+        }
         if (c) atomicAdd(&a.count[blockIdx.x & (SPREAD - 1)], c);
+        if (a.work && m) atomicAdd(&a.work[blockIdx.x & (SPREAD - 1)], 8ull * m);
     }
 }
 
@@ -618,12 +639,18 @@ __global__ __launch_bounds__(TT_WAVES * WAVE) void k_transpose_delta(
     uint32_t domain, uint32_t words, const uint64_t *__restrict__ D, const uint64_t *__restrict__ dmask_old,
     const uint64_t *__restrict__ dmask_new, uint64_t *__restrict__ DT, uint64_t *__restrict__ dtmask,
     uint64_t *__restrict__ RT, uint64_t *__restrict__ rtmask, uint64_t *__restrict__ PT,
-    uint64_t *__restrict__ ptmask) {
+    uint64_t *__restrict__ ptmask, unsigned long long *work) {
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
     const uint32_t I = blockIdx.y * TT_WAVES + wave;
     if (I >= words) return;                              // wave-uniform
     if ((dmask_old[I] | dmask_new[I]) == 0ull) return;  // wave-uniform
     const uint32_t J0 = blockIdx.x * TT_COLS;
+    // profiling: D read, D^T written, R^T read and written (and P^T written) for the 64 x TT_COLS tile
+    if (work && lane == 0 && J0 < words) {
+        const uint32_t cols = words - J0 < (uint32_t)TT_COLS ? words - J0 : (uint32_t)TT_COLS;
+        atomicAdd(&work[(blockIdx.x + blockIdx.y) & (SPREAD - 1)],
+                  (unsigned long long)cols * 64ull * 8ull * (PT ? 5ull : 4ull));
+    }
     const uint32_t row = I * 64 + lane;
     uint64_t v[TT_COLS];
 #pragma unroll
@@ -1007,10 +1034,11 @@ struct ChainRun {
                 }
                 continue;
             }
-            const FinalizeArgs fa{b.C.p, b.cmask.p, b.R.p, b.rmask.p, b.D.p, b.dmask[b.dcur].p, dnew, b.P.p,
-                                  b.pmask.p, cnt_of(p)};
+            FinalizeArgs fa{b.C.p, b.cmask.p, b.R.p, b.rmask.p, b.D.p, b.dmask[b.dcur].p, dnew, b.P.p,
+                            b.pmask.p, cnt_of(p), nullptr};
             {
                 Prof prof(ctx, XLOG_HIP_KERNEL_CHAIN_FINALIZE, 0.0);
+                fa.work = prof.work(1.0);  // bytes of the row words moved, counted on the device
                 const uint32_t batch = row_batch(domain), blocks = (domain + GW * batch - 1) / (GW * batch);
                 if (b.prev)
                     hipLaunchKernelGGL((k_chain_finalize<true>), dim3(blocks), dim3(GW * WAVE), 0, ctx->stream, domain,
@@ -1026,7 +1054,7 @@ struct ChainRun {
                 const dim3 g((words + TT_COLS - 1) / TT_COLS, (words + TT_WAVES - 1) / TT_WAVES);
                 hipLaunchKernelGGL(k_transpose_delta, g, dim3(TT_WAVES * WAVE), 0, ctx->stream, domain, words, b.D.p,
                                    b.dmask[b.dcur].p, dnew, b.DT.p, b.dtmask.p, b.RT.p, b.rtmask.p, b.PT.p,
-                                   b.ptmask.p);
+                                   b.ptmask.p, prof.work(1.0));
                 XH_CHECK_HIP(hipGetLastError());
             }
             b.dcur ^= 1;
