@@ -1843,10 +1843,28 @@ struct Driver {
     };
     std::map<CacheKey, std::unique_ptr<JoinIndex>> cache;
 
+    // The queued join route keeps R in two sorted runs: full[p] (the base run)
+    // and small[p], the recent run every delta is merged into (see run_queue).
+    std::vector<DRel> small;
+
     ~Driver() {
         cache.clear();
         for (auto &r : full) if (r.owned) ctx->free(r.k);
         for (auto &r : delta) if (r.owned) ctx->free(r.k);
+        for (auto &r : small) if (r.owned) ctx->free(r.k);
+    }
+    // R of p in one run again: the recent run merged into the base run
+    void compact(uint32_t p) {
+        if (p >= small.size()) return;
+        if (small[p].n) {
+            DRel m = merge(full[p], small[p]);
+            release(full[p]);
+            full[p] = m;
+        }
+        release(small[p]);
+    }
+    void compact_all() {
+        for (uint32_t p = 0; p < small.size(); ++p) compact(p);
     }
 
     const JoinIndex &index_of(const DRel &rel, int col) {
@@ -2182,12 +2200,17 @@ struct Driver {
                 hidx[p] = (int)heads.size();
                 heads.push_back((int)p);
             }
+        small.assign(n_preds, DRel());
         uint64_t it = 0;
         while (it < max_iter) {
             const uint64_t done = run_queue(std::min<uint64_t>(qmax, max_iter - it), it, heads, hidx, deltas, qr);
-            if (done == ~0ull) return it;  // converged inside the queue (it counts the empty iteration)
+            if (done == ~0ull) {  // converged inside the queue (it counts the empty iteration)
+                compact_all();
+                return it;
+            }
             if (done > 0) continue;
-            // an iteration whose queue stopped at once, or one for which no queue fits
+            // an iteration whose queue stopped at once, or one for which no queue fits (one run of R)
+            compact_all();
             ++it;
             if (iterate_host(it, deltas, qr) == 0) return it;
         }
@@ -2204,6 +2227,11 @@ struct Driver {
     uint64_t run_queue(uint64_t qn, uint64_t &it, const std::vector<int> &heads, const std::vector<int> &hidx,
                        std::vector<uint64_t> &deltas, const std::vector<Rule> &qr) {
         const uint32_t H = (uint32_t)heads.size();
+        // R as two sorted runs: the base run full[p] is read, never written, by a queue; the recent run
+        // small[p] takes every delta (merge) and is merged into the base run here once it holds more than a
+        // quarter of it, so the merges of a queue rewrite the recent run instead of all of R
+        for (int p : heads)
+            if (small[p].n > full[p].n / 4) compact((uint32_t)p);
         // the variants (one per recursive rule, its IDB atom first) and their fixed indexes
         std::vector<std::unique_ptr<QVariant>> vars;
         uint32_t tot_words = 0;
@@ -2283,8 +2311,8 @@ struct Driver {
         // Rb[k][h]: R after iteration k (Rb[-1] exact: stored at index 0, iteration k at k + 1)
         std::vector<std::vector<uint64_t>> Lb, Cb, Rb;
         std::vector<std::vector<std::array<uint64_t, MAX_BODY>>> T;
-        Rb.push_back({});
-        for (int p : heads) Rb[0].push_back(full[p].n);
+        Rb.push_back({});  // (bounds of the recent run)
+        for (int p : heads) Rb[0].push_back(small[p].n);
         std::vector<uint64_t> cur(H);
         for (uint32_t h = 0; h < H; ++h) cur[h] = delta[heads[h]].n;  // exact for the first
         const uint64_t room = device_room(ctx) / 2;
@@ -2292,7 +2320,8 @@ struct Driver {
         // most what R leaves of that (the bound of small domains)
         std::vector<uint64_t> dmax(H, ~0ull);
         if (domain && domain <= (1ull << 31))
-            for (uint32_t h = 0; h < H; ++h) dmax[h] = domain * domain - std::min(domain * domain, full[heads[h]].n);
+            for (uint32_t h = 0; h < H; ++h)
+                dmax[h] = domain * domain - std::min(domain * domain, full[heads[h]].n + small[heads[h]].n);
         uint64_t q = 0;
         for (; q < qn; ++q) {
             std::vector<uint64_t> lb = cur, cb(H, 0), rb(H, 0);
@@ -2350,7 +2379,7 @@ struct Driver {
 
         // ---- buffers -------------------------------------------------------------
         struct QHead {
-            Owned C, Calt, D[2], R[2];
+            Owned C, Calt, D[2], R[2];  // R: the recent run, alternating
             explicit QHead(Ctx *c) : C(c), Calt(c), D{Owned(c), Owned(c)}, R{Owned(c), Owned(c)} {}
         };
         std::vector<std::unique_ptr<QHead>> qh;
@@ -2382,7 +2411,7 @@ struct Driver {
         // block -1: the sizes the queue starts from
         for (uint32_t h = 0; h < H; ++h) {
             fill_u64(ctx, qs.p + blk(-1) + h, delta[heads[h]].n, 1);
-            fill_u64(ctx, qs.p + blk(-1) + H + h, full[heads[h]].n, 1);
+            fill_u64(ctx, qs.p + blk(-1) + H + h, small[heads[h]].n, 1);
         }
         // a head whose one variant keeps its delta's first column as the high word gets its candidates
         // grouped by it, in ascending order: one short-run pass sorts them (sort_grouped_dev)
@@ -2394,6 +2423,8 @@ struct Driver {
             gsrc[hidx[vp->head]] = hidx[vp->dpred];
         }
         Buf<uint64_t> gscratch(ctx, 2 * (uint64_t)H);
+        Buf<uint64_t> tcount(ctx, 1);  // the size of an empty base run
+        fill_u64(ctx, tcount.p, 0ull, 1);
 
         // ---- the queue -------------------------------------------------------------
         cur_iter = it + 1;
@@ -2447,10 +2478,13 @@ struct Driver {
                 if (grouped[h] && Cb[k][h] / group_bound(std::max<uint64_t>(Lb[k][gsrc[h]], 1)) <= SHORT_GROUP_ROWS)
                     ka = sort_grouped_dev(ctx, ka, kb, Cb[k][h], d_cand, digits, stop, gscratch.p + 2 * h);
                 else radix_sort_dev(ctx, &ka, &kb, Cb[k][h], d_cand, digits, stop);
-                const uint64_t *rin = k == 0 ? full[p].k : qh[h]->R[(k - 1) & 1].p;
-                if (!rin) rin = qh[h]->R[1].p;  // an empty R read through its device count
-                select_unique_diff_dev(ctx, ka, Cb[k][h], d_cand, rin, std::max<uint64_t>(Rb[k][h], 1), pR + h,
-                                       qh[h]->D[k & 1].p, nD + h, stop);
+                // unique, not in the base run (its size is known) and not in the recent run
+                const uint64_t *big = full[p].k ? full[p].k : qh[h]->R[1].p;
+                const uint64_t *rin = k == 0 ? small[p].k : qh[h]->R[(k - 1) & 1].p;
+                if (!rin) rin = qh[h]->R[1].p;  // an empty run read through its device count
+                select_unique_diff2_dev(ctx, ka, Cb[k][h], d_cand, big, std::max<uint64_t>(full[p].n, 1),
+                                        full[p].n ? nullptr : tcount.p, rin, std::max<uint64_t>(Rb[k][h], 1), pR + h,
+                                        qh[h]->D[k & 1].p, nD + h, stop);
             }
             // the delta total, R's new sizes within their bounds
             QEnd qe{nD, pR, nR, total, H, {}};
@@ -2460,7 +2494,7 @@ struct Driver {
             // per head: R ∪= Δ' into the other buffer (nothing when the iteration derived nothing)
             for (uint32_t h = 0; h < H; ++h) {
                 const int p = heads[h];
-                const uint64_t *rin = k == 0 ? full[p].k : qh[h]->R[(k - 1) & 1].p;
+                const uint64_t *rin = k == 0 ? small[p].k : qh[h]->R[(k - 1) & 1].p;
                 if (!rin) rin = qh[h]->R[1].p;
                 merge_sorted_dev(ctx, rin, Rb[k][h], pR + h, qh[h]->D[k & 1].p, Cb[k][h], nD + h,
                                  qh[h]->R[k & 1].p, total, stop);
@@ -2513,11 +2547,11 @@ struct Driver {
             const uint64_t *bk = hs + blk(last);
             for (uint32_t h = 0; h < H; ++h) {
                 const int p = heads[h];
-                release(full[p]);
-                full[p].n = bk[H + h];
-                full[p].k = qh[h]->R[last & 1].release();
-                full[p].owned = true;
-                full[p].version = version_counter++;
+                release(small[p]);
+                small[p].n = bk[H + h];
+                small[p].k = qh[h]->R[last & 1].release();
+                small[p].owned = true;
+                small[p].version = version_counter++;
             }
         }
         if (converged || last >= 0) {

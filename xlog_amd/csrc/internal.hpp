@@ -382,6 +382,11 @@ void select_unique_diff(Ctx *ctx, const uint64_t *k, uint64_t n, const uint64_t 
 // and the stop flag of a queued iteration (a raised flag: nothing is done).
 void select_unique_diff_dev(Ctx *ctx, const uint64_t *k, uint64_t n, const uint64_t *d_n, const uint64_t *b,
                             uint64_t nb, const uint64_t *d_nb, uint64_t *out, uint64_t *d_count, const uint32_t *stop);
+// The same against two sorted arrays at once (not in b and not in b2; b2's
+// count on the device when d_nb2 is set, nb2 its bound).
+void select_unique_diff2_dev(Ctx *ctx, const uint64_t *k, uint64_t n, const uint64_t *d_n, const uint64_t *b,
+                             uint64_t nb, const uint64_t *d_nb, const uint64_t *b2, uint64_t nb2, const uint64_t *d_nb2,
+                             uint64_t *out, uint64_t *d_count, const uint32_t *stop);
 void select_flags(Ctx *ctx, const uint64_t *k, const uint8_t *flags, uint64_t n, uint64_t *out,
                   uint64_t *d_count);
 //   not_value:   keep k[i] if k[i] != v

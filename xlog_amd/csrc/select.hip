@@ -126,7 +126,7 @@ __global__ __launch_bounds__(SelShape<Sel>::block) void k_select(const uint64_t 
     constexpr int SEL_WAVES = SelShape<Sel>::waves;
     constexpr uint64_t SEL_TILE = SelShape<Sel>::tile;
     __shared__ uint32_t s_wc[SEL_WAVES];
-    __shared__ uint64_t s_sel[4];
+    __shared__ uint64_t s_sel[8];
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
     // A row count on the device (d_n; n is then the bound the tiles' scratch
     // was sized for) makes the launch persistent: a grid of a few blocks per
@@ -165,9 +165,9 @@ __global__ __launch_bounds__(SelShape<Sel>::block) void k_select(const uint64_t 
             if (last > n) last = n;
             if (first < last) {
                 sel.setup(first, last - 1, s_sel, lane);
-            } else if (lane == 0) {  // a tile past the rows: an empty window
-                s_sel[0] = s_sel[1] = 0;
-                s_sel[2] = 1;
+            } else if (lane == 0) {  // a tile past the rows: empty windows
+                s_sel[0] = s_sel[1] = s_sel[3] = s_sel[4] = 0;
+                s_sel[2] = s_sel[5] = 1;
             }
         }
         __syncthreads();
@@ -322,6 +322,99 @@ __device__ uint64_t wave_bound(const uint64_t *a, uint64_t lo, uint64_t hi, uint
 constexpr uint32_t WIN_CAP = 8192;             // keys per chunk (64 KB of dynamic LDS)
 constexpr uint64_t WIN_STREAM_PER_ROW = 16;    // streamed window keys per row of the tile, at most
 constexpr uint64_t DIFF_WINDOW_PASS = 256;     // tiles from which the windows come from k_diff_windows
+// Membership of a tile's keys in the window [s0, s1) of sorted b: streamed
+// through LDS in chunks of WIN_CAP keys, or searched in HBM.  Bit r: key k[r]
+// (row wbase + r * WAVE + lane, below n) is in b.  Every thread of the block
+// calls it (the streamed window has barriers).
+//
+// Each search is binary lifting from the largest power of two not above the
+// window's length (pos = keys below k[r]); a lane runs SEARCH_GROUP of its
+// keys' searches in lockstep, so that their loads are independent and in
+// flight together instead of one chain of dependent loads per key (groups of 4
+// keep the selection at 4 waves per SIMD: 119 VGPRs, none spilled).  The load
+// index is clamped into the window, so every load is in bounds and none is
+// predicated.  In LDS a group whose 4 x 64 keys all fall outside
+// the chunk's range is skipped (a wave-uniform branch).
+constexpr int SEARCH_GROUP = 4;
+template <int BLOCK, int ITEMS>
+__device__ uint32_t window_members(const uint64_t *b, uint64_t s0, uint64_t s1, bool streamed,
+                                   const uint64_t (&k)[ITEMS], uint64_t wbase, uint64_t n, int tid, int lane) {
+    static_assert(ITEMS % SEARCH_GROUP == 0, "search groups split the lane's items");
+    uint32_t m = 0;
+    if (streamed) {
+        for (uint64_t c0 = s0; c0 < s1; c0 += WIN_CAP) {
+            const uint32_t len = (uint32_t)(s1 - c0 < WIN_CAP ? s1 - c0 : WIN_CAP);
+            __syncthreads();  // the previous chunk is no longer read
+            batched_copy<BLOCK, 8>(
+                len, tid, [&](uint32_t i) { return b[c0 + i]; }, [&](uint32_t i, uint64_t v) { sel_window[i] = v; });
+            __syncthreads();
+            const uint64_t lo_k = sel_window[0], hi_k = sel_window[len - 1];
+            const uint32_t top = 1u << (31 - __builtin_clz(len));
+#pragma unroll
+            for (int g = 0; g < ITEMS; g += SEARCH_GROUP) {
+                bool act[SEARCH_GROUP];
+                bool any = false;
+#pragma unroll
+                for (int j = 0; j < SEARCH_GROUP; ++j) {
+                    const uint64_t key = k[g + j];
+                    act[j] = wbase + (uint64_t)(g + j) * WAVE + lane < n && key >= lo_k && key <= hi_k;
+                    any |= act[j];
+                }
+                if (__ballot(any) == 0) continue;
+                uint32_t pos[SEARCH_GROUP];
+#pragma unroll
+                for (int j = 0; j < SEARCH_GROUP; ++j) pos[j] = 0;
+                for (uint32_t step = top; step > 0; step >>= 1) {
+                    uint64_t v[SEARCH_GROUP];
+#pragma unroll
+                    for (int j = 0; j < SEARCH_GROUP; ++j) {
+                        const uint32_t q = pos[j] + step;
+                        v[j] = sel_window[(q <= len ? q : len) - 1];
+                    }
+#pragma unroll
+                    for (int j = 0; j < SEARCH_GROUP; ++j)
+                        if (pos[j] + step <= len && v[j] < k[g + j]) pos[j] += step;
+                }
+#pragma unroll
+                for (int j = 0; j < SEARCH_GROUP; ++j) {
+                    const uint64_t v = sel_window[pos[j] < len ? pos[j] : len - 1];
+                    if (act[j] && pos[j] < len && v == k[g + j]) m |= 1u << (g + j);
+                }
+            }
+        }
+    } else if (s1 > s0) {
+        const uint64_t len = s1 - s0;
+        const uint64_t top = 1ull << (63 - __builtin_clzll(len));
+#pragma unroll
+        for (int g = 0; g < ITEMS; g += SEARCH_GROUP) {
+            uint64_t pos[SEARCH_GROUP];
+#pragma unroll
+            for (int j = 0; j < SEARCH_GROUP; ++j) pos[j] = 0;
+            for (uint64_t step = top; step > 0; step >>= 1) {
+                uint64_t v[SEARCH_GROUP];
+#pragma unroll
+                for (int j = 0; j < SEARCH_GROUP; ++j) {
+                    const uint64_t q = pos[j] + step;
+                    v[j] = b[s0 + (q <= len ? q : len) - 1];
+                }
+#pragma unroll
+                for (int j = 0; j < SEARCH_GROUP; ++j)
+                    if (pos[j] + step <= len && v[j] < k[g + j]) pos[j] += step;
+            }
+#pragma unroll
+            for (int j = 0; j < SEARCH_GROUP; ++j) {
+                const bool valid = wbase + (uint64_t)(g + j) * WAVE + lane < n;
+                if (valid && pos[j] < len && b[s0 + pos[j]] == k[g + j]) m |= 1u << (g + j);
+            }
+        }
+    }
+    return m;
+}
+
+// Unique (optional) and not a member of sorted b, nor of the optional second
+// sorted array b2 (the two runs of a relation kept as a base run and a recent
+// run).  b's windows come from k_diff_windows or the tile's own wave search
+// (above); b2's from the tile's wave search.
 template <bool UNIQ>
 struct SelDiff {
     static constexpr bool kWindow = true;
@@ -332,7 +425,10 @@ struct SelDiff {
     const uint64_t *win;  // [2t], [2t + 1]: window of tile t (nullptr: searched by the tile)
     uint64_t tile_rows;
     const uint64_t *d_nb;  // optional: b's row count on the device (nb is then its bound)
-    // s[0], s[1]: window [s0, s1) of b; s[2]: 1 when it is streamed through LDS
+    const uint64_t *b2 = nullptr;  // optional second array, its bound and device count
+    uint64_t nb2 = 0;
+    const uint64_t *d_nb2 = nullptr;
+    // s[0], s[1]: window [s0, s1) of b; s[2]: 1 when it is streamed through LDS; s[3..5] the same for b2
     __device__ void setup(uint64_t first, uint64_t last, uint64_t *s, int lane) const {
         uint64_t s0, s1;
         if (win) {
@@ -344,46 +440,33 @@ struct SelDiff {
             s0 = wave_bound<false>(b, 0, m, in[first], lane);
             s1 = wave_bound<true>(b, s0, m, in[last], lane);
         }
+        uint64_t t0 = 0, t1 = 0;
+        if (b2) {
+            const uint64_t m2 = d_nb2 && *d_nb2 < nb2 ? *d_nb2 : nb2;
+            t0 = wave_bound<false>(b2, 0, m2, in[first], lane);
+            t1 = wave_bound<true>(b2, t0, m2, in[last], lane);
+        }
         if (lane == 0) {
+            const uint64_t rows = last - first + 1;
             s[0] = s0;
             s[1] = s1;
-            s[2] = (s1 - s0 <= WIN_CAP || s1 - s0 <= WIN_STREAM_PER_ROW * (last - first + 1)) ? 1u : 0u;
+            s[2] = (s1 - s0 <= WIN_CAP || s1 - s0 <= WIN_STREAM_PER_ROW * rows) ? 1u : 0u;
+            s[3] = t0;
+            s[4] = t1;
+            s[5] = (t1 - t0 <= WIN_CAP || t1 - t0 <= WIN_STREAM_PER_ROW * rows) ? 1u : 0u;
         }
     }
-    // bit r: key k[r] (row wbase + r * WAVE + lane, below n) is in b.  Every
-    // thread of the block calls it (the streamed window has barriers).
     template <int BLOCK, int ITEMS>
     __device__ uint32_t members(const uint64_t (&k)[ITEMS], uint64_t wbase, uint64_t n, const uint64_t *s,
                                 int tid, int lane) const {
+        // one loop over the arrays, not two inlined copies: the selection keeps
+        // 4 waves per SIMD (2 blocks per CU beside their LDS windows)
         uint32_t m = 0;
-        if (s[2]) {
-            for (uint64_t c0 = s[0]; c0 < s[1]; c0 += WIN_CAP) {
-                const uint32_t len = (uint32_t)(s[1] - c0 < WIN_CAP ? s[1] - c0 : WIN_CAP);
-                __syncthreads();  // the previous chunk is no longer read
-                batched_copy<BLOCK, 8>(
-                    len, tid, [&](uint32_t i) { return b[c0 + i]; }, [&](uint32_t i, uint64_t v) { sel_window[i] = v; });
-                __syncthreads();
-                const uint64_t lo_k = sel_window[0], hi_k = sel_window[len - 1];
-#pragma unroll
-                for (int r = 0; r < ITEMS; ++r) {
-                    const uint64_t key = k[r];
-                    if (wbase + (uint64_t)r * WAVE + lane >= n || key < lo_k || key > hi_k) continue;
-                    // entries of the chunk below key: binary lifting over <= WIN_CAP entries
-                    uint32_t pos = 0;
-#pragma unroll
-                    for (uint32_t step = WIN_CAP / 2; step > 0; step >>= 1)
-                        if (pos + step <= len && sel_window[pos + step - 1] < key) pos += step;
-                    if (pos + 1 <= len && sel_window[pos] < key) ++pos;
-                    if (pos < len && sel_window[pos] == key) m |= 1u << r;
-                }
-            }
-        } else {
-#pragma unroll
-            for (int r = 0; r < ITEMS; ++r) {
-                if (wbase + (uint64_t)r * WAVE + lane >= n) continue;
-                const uint64_t p = lower_bound_u64(b, s[0], s[1], k[r]);
-                if (p < s[1] && b[p] == k[r]) m |= 1u << r;
-            }
+        const int arrays = b2 ? 2 : 1;
+        for (int a = 0; a < arrays; ++a) {
+            const uint64_t *arr = a ? b2 : b;
+            const uint64_t *w = s + 3 * a;
+            m |= window_members<BLOCK, ITEMS>(arr, w[0], w[1], w[2] != 0, k, wbase, n, tid, lane);
         }
         return m;
     }
@@ -979,6 +1062,11 @@ void add_work_rows(Ctx *ctx, unsigned long long *work, const uint64_t *d_a, uint
 
 void select_unique_diff_dev(Ctx *ctx, const uint64_t *k, uint64_t n, const uint64_t *d_n, const uint64_t *b,
                             uint64_t nb, const uint64_t *d_nb, uint64_t *out, uint64_t *d_count, const uint32_t *stop) {
+    select_unique_diff2_dev(ctx, k, n, d_n, b, nb, d_nb, nullptr, 0, nullptr, out, d_count, stop);
+}
+void select_unique_diff2_dev(Ctx *ctx, const uint64_t *k, uint64_t n, const uint64_t *d_n, const uint64_t *b,
+                             uint64_t nb, const uint64_t *d_nb, const uint64_t *b2, uint64_t nb2, const uint64_t *d_nb2,
+                             uint64_t *out, uint64_t *d_count, const uint32_t *stop) {
     if (n == 0) {
         fill_u64(ctx, d_count, 0ull, 1);
         return;
@@ -995,7 +1083,11 @@ void select_unique_diff_dev(Ctx *ctx, const uint64_t *k, uint64_t n, const uint6
                            nb, rows, tiles, win.p, d_n, d_nb, stop);
         XH_CHECK_HIP(hipGetLastError());
     }
-    run_select(ctx, k, n, SelDiff<true>{k, b, nb, out, win.p, rows, d_nb}, d_count, d_n, stop);
+    SelDiff<true> sel{k, b, nb, out, win.p, rows, d_nb};
+    sel.b2 = b2;
+    sel.nb2 = nb2;
+    sel.d_nb2 = d_nb2;
+    run_select(ctx, k, n, sel, d_count, d_n, stop);
 }
 void select_not_value(Ctx *ctx, const uint64_t *k, uint64_t n, uint64_t v, uint64_t *out, uint64_t *d_count) {
     run_select(ctx, k, n, SelNotValue{v, out}, d_count);
