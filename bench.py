@@ -1,7 +1,7 @@
 """Benchmark of the semi-naive relational core on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--workload c4|c1|c1j|c1h|c2|c2u|c3|c4j|c4h|c5|tcs|tcs_crit|tcs_j|copy|c5full]
+                    [--workload c4|c1|c1j|c1h|c2|c2u|c3|c4j|c4h|c5|c5j|tcs|tcs_crit|tcs_j|copy|c5full]
                     [--no-extra] [--no-cpu-baseline]
 
 Default workload is BASELINE.json configs[3] (C4), the metric's lead quantity:
@@ -16,7 +16,7 @@ dedup at 2^24 rows a side; c3: sort + dedup of 2^28 packed tuples; c5: Andersen
 points-to at 10,000 variables), each with its own timing, roofline and CPU
 baseline.  c5_stated is C5 at its stated 500,000 variables, run once for its outcome
 (the reference's u32 join-row limit trips in the first recursive iteration).
-c1j / c4j force the join route and c1h / c4h the hash-set route;
+c1j / c4j / c5j force the join route and c1h / c4h the hash-set route;
 tcs / tcs_crit are closures over 2^20 vertices whose ids are spread over u32
 (the hash-set route, AUTO's choice there) and tcs_j is tcs on the join route;
 c2u is the unfused join -> sort -> dedup sequence; copy is the counter
@@ -145,19 +145,23 @@ def make_workload(name: str, p):
 
         config = {"workload": "copy: column swap of 2^28 packed rows (16 B/row), counter calibration", "rows": n}
         return step, n, "rows", config, None, state
-    if name == "c5":
+    if name in ("c5", "c5j"):
         # BASELINE's literal C5 (500,000 variables) grows |pointsTo| like V^2 (~10^10 tuples, past the
         # reference's u32 row cap): the bench runs the same generator at 10,000 variables / 40,000 facts
         cfg = dict(datagen.C5, n_vars=10_000, n_facts=40_000)
         f = datagen.andersen(cfg["n_vars"], cfg["n_facts"], cfg["alpha"], datagen.seed_for(5))
         rels = [p.create_buffer_from_u32_columns(list(f[k])) for k in ("assign", "addressOf", "load", "store")]
         state = {}
+        from xlog_amd import ROUTE_AUTO, ROUTE_JOIN
+        route = ROUTE_JOIN if name == "c5j" else ROUTE_AUTO
 
         def step():
-            outs, st = p.fixpoint(andersen_plan(), rels + [None])
+            outs, st = p.fixpoint(andersen_plan(), rels + [None], route=route)
             state["out_rows"] = outs[4].num_rows()
             state["iterations"] = st["iterations"]
             state["delta_sizes"] = st["delta_sizes"]
+            state["route"] = st["route"]
+            state["host_waits"] = st["host_waits"]
 
         def same_sample():
             # the GPU on the instance the CPU baseline runs (5,000 variables), for a like-for-like comparison
@@ -171,8 +175,10 @@ def make_workload(name: str, p):
             p.synchronize()
             return {"gpu_5000_vars_ms": (time.perf_counter() - t) * 1000.0 / 5, "gpu_5000_vars_tuples": outs[4].num_rows()}
 
-        state["_extra"] = same_sample
-        config = {"workload": "c5 scaled: Andersen points-to, 4 rules (literal size infeasible, see DESIGN)", **cfg,
+        if name == "c5":
+            state["_extra"] = same_sample
+        config = {"workload": "c5 scaled: Andersen points-to, 4 rules (literal size infeasible, see DESIGN)"
+                              + (" (join route)" if name == "c5j" else ""), **cfg,
                   "seed": datagen.seed_for(5)}
         return step, None, "pointsTo tuples", config, f, state
     raise SystemExit(f"unknown workload {name}")

@@ -298,9 +298,11 @@ xlog_hip_status xlog_hip_compact(xlog_hip_ctx *ctx, const xlog_hip_rel *in, cons
  *   [n_rules, then per rule: head_pred, hv0, hv1, n_body, (pred, v0, v1) * n_body]
  * over arity-2 predicates 0..n_preds-1; variables are small ints; 1..4 atoms
  * per body.  The join route evaluates bodies left-deep in body order: each
- * atom after the first shares exactly one variable with the running binding,
- * which keeps at most two live variables (crates/xlog-logic/src/lower.rs:
- * 1795-1850).  The bitmap route takes bodies whose atoms form a path from hv0
+ * atom after the first shares one variable with the running binding, which
+ * keeps at most two live variables, or both (a cyclic body such as a
+ * triangle: the binding rows that form a row of the atom are kept), as the
+ * reference's lowering joins on every shared variable (crates/xlog-logic/src/
+ * lower.rs:1795-1850).  The bitmap route takes bodies whose atoms form a path from hv0
  * to hv1 in any order (each atom read forward or with its columns swapped).
  * rels[p] supplies every predicate (EDB facts; IDB initial contents, may be
  * empty).  On success out[p] receives a new canonical relation for every IDB

@@ -402,15 +402,16 @@ int or_chain2_counts(const uint64_t *l, uint64_t nl, const uint64_t *a, uint64_t
 }
 
 /* ------------------------------------------------------------------------ */
-/* program plans: rules over arity-2 predicates with chain bodies            */
+/* program plans: rules over arity-2 predicates, left-deep bodies           */
 /* ------------------------------------------------------------------------ */
 /* Layout of the int32 plan array (shared with the GPU library's plan):
  *   [n_rules, then per rule: head_pred, hv0, hv1, n_body, (pred, v0, v1) * n_body]
  * Variables are small non-negative ints.  Bodies are evaluated left-deep in
  * body order, as lowering produces them (crates/xlog-logic/src/lower.rs:1795-1850):
- * the running binding joins the next atom on their shared variable, and keeps
- * only the variables that a later atom or the head still reads.  A binding
- * holds at most two variables. */
+ * the running binding joins the next atom on their shared variable (or, when
+ * both of the atom's variables are bound, on both: a cyclic body such as a
+ * triangle), and keeps only the variables that a later atom or the head still
+ * reads.  A binding holds at most two variables. */
 
 #define MAX_BODY 4
 typedef struct { int pred, v[2]; } atom_t;
@@ -566,6 +567,39 @@ static int eval_body(const rule_t *r, const uint64_t *const *rel, const uint64_t
         for (int x = 0; x < cur.nv; ++x)
             for (int y = 0; y < 2; ++y)
                 if (cur.vars[x] == a->v[y]) { int dup = 0; for (int z = 0; z < ns; ++z) if (bpos[z] == x) dup = 1; if (!dup) { bpos[ns] = x; apos[ns] = y; ++ns; } }
+        if (ns == 2) {
+            /* both of the atom's variables are bound: an inner join on two keys
+             * (lower.rs compute_join_keys), i.e. the binding rows whose values,
+             * in the atom's column order, form a row of the atom */
+            const int x0 = apos[0] == 0 ? bpos[0] : bpos[1], x1 = apos[0] == 0 ? bpos[1] : bpos[0];
+            uint64_t nr = nrel[j];
+            uint64_t *set = (uint64_t *)malloc((nr ? nr : 1) * sizeof(uint64_t));
+            if (!set) { vec_free(&cur.rows); return -2; }
+            memcpy(set, rel[j], nr * sizeof(uint64_t));
+            nr = or_sort_dedup(set, nr);
+            binding_t nxt = {0};
+            int src[2];
+            for (int x = 0; x < cur.nv; ++x)
+                if (needed_later(r, j + 1, cur.vars[x])) { nxt.vars[nxt.nv] = cur.vars[x]; src[nxt.nv] = x; nxt.nv++; }
+            for (uint64_t i = 0; i < cur.rows.n; ++i) {
+                const uint64_t row = cur.rows.v[i];
+                const uint32_t bv[2] = {(uint32_t)(row >> 32), (uint32_t)row};
+                const uint64_t key = ((uint64_t)bv[x0] << 32) | bv[x1];
+                uint64_t lo = 0, hi = nr;
+                while (lo < hi) { uint64_t m = (lo + hi) / 2; if (set[m] < key) lo = m + 1; else hi = m; }
+                if (lo == nr || set[lo] != key) continue;
+                uint64_t o;
+                if (nxt.nv == 2) o = ((uint64_t)bv[src[0]] << 32) | bv[src[1]];
+                else if (nxt.nv == 1) o = bv[src[0]];
+                else o = 0;
+                if (vec_push(&nxt.rows, o)) { free(set); vec_free(&cur.rows); vec_free(&nxt.rows); return -2; }
+            }
+            free(set);
+            vec_free(&cur.rows);
+            nxt.rows.n = or_sort_dedup(nxt.rows.v, nxt.rows.n);
+            cur = nxt;
+            continue;
+        }
         if (ns != 1) { vec_free(&cur.rows); return -3; }  /* plan shape not supported */
         /* candidate output vars: binding vars ++ atom's non-shared var */
         int allv[3], na = 0;

@@ -4,7 +4,9 @@ include/xlog_hip.h: [n_rules, per rule: head, hv0, hv1, n_body, (pred, v0, v1) *
 Each is a recursive program over binary relations whose rule bodies form a
 path between the head variables, in the style of the reference's recursion
 tests (crates/xlog-integration-tests/tests/real_world_tests.rs) and its
-example programs (examples/xlog/)."""
+example programs (examples/xlog/); the cyclic plans at the end have an atom
+whose two variables are both bound when it is joined (the reference's
+left-deep lowering then joins on both keys, lower.rs build_join_tree)."""
 
 X, Y, Z, P, Q, V, W = 0, 1, 2, 3, 4, 5, 6
 
@@ -67,3 +69,26 @@ def scrambled_chain_plan(a=0, b=1, p=2):
 def ordered_chain_plan(a=0, b=1, p=2):
     """The same program as scrambled_chain_plan with the body in path order."""
     return [2, p, X, Y, 1, a, X, Y, p, X, W, 3, a, X, Y, p, Y, Z, b, Z, W]
+
+
+def triangle_closure_plan(edge=0, r=1):
+    """r(X,Y) :- edge(X,Y).  r(X,Z) :- r(X,Y), edge(Y,Z), edge(Z,X)   (the last atom closes a triangle:
+    both of its variables are bound)."""
+    return [2, r, X, Y, 1, edge, X, Y, r, X, Z, 3, r, X, Y, edge, Y, Z, edge, Z, X]
+
+
+def triangles_plan(edge=0, tri=1):
+    """tri(X,Z) :- edge(X,Y), edge(Y,Z), edge(Z,X)   (non-recursive: one iteration derives nothing)."""
+    return [1, tri, X, Z, 3, edge, X, Y, edge, Y, Z, edge, Z, X]
+
+
+def filtered_tc_plan(a=0, keep=1, b=2, p=3):
+    """p(X,Y) :- a(X,Y).  p(X,Z) :- p(X,Y), keep(Y,X), b(Y,Z)   (a two-key step in the middle, its atom's
+    columns in the reverse of the binding's order)."""
+    return [2, p, X, Y, 1, a, X, Y, p, X, Z, 3, p, X, Y, keep, Y, X, b, Y, Z]
+
+
+def flat_sg_plan(flat=0, par=1, sg=2):
+    """sg(X,Y) :- flat(X,Y).  sg(X,Y) :- par(X,P), sg(P,Q), par(Y,Q), flat(X,Y)   (four atoms, the last a
+    two-key step)."""
+    return [2, sg, X, Y, 1, flat, X, Y, sg, X, Y, 4, par, X, P, sg, P, Q, par, Y, Q, flat, X, Y]

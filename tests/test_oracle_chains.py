@@ -136,3 +136,45 @@ def test_scrambled_body_is_outside_left_deep_evaluation():
     with pytest.raises(RuntimeError) as ex:
         oracle.seminaive(cp.scrambled_chain_plan(), [pack([1], [2]), pack([2], [3]), None])
     assert ex.value.code == -3
+
+
+# Cyclic bodies: an atom whose two variables are both bound is a join on both keys (a filter of the
+# binding), lower.rs build_join_tree / compute_join_keys.
+@pytest.mark.parametrize("n,m,seed", [(30, 120, 21), (90, 700, 22)])
+def test_triangle_closure(n, m, seed):
+    s, d = _graph(n, m, seed)
+    E = _mat(n, s, d)
+    step = lambda R: (E | (_mm(R[0], E) & E.T),)
+    _check(cp.triangle_closure_plan(), [pack(s, d), None], [1], _kleene(step, [np.zeros((n, n), bool)]))
+
+
+@pytest.mark.parametrize("n,m,seed", [(25, 150, 23), (60, 600, 24)])
+def test_triangles(n, m, seed):
+    s, d = _graph(n, m, seed)
+    E = _mat(n, s, d)
+    step = lambda R: (_mm(E, E) & E.T,)
+    _check(cp.triangles_plan(), [pack(s, d), None], [1], _kleene(step, [np.zeros((n, n), bool)]))
+
+
+@pytest.mark.parametrize("n,seed", [(40, 25), (100, 26)])
+def test_filtered_tc(n, seed):
+    a_s, a_d = _graph(n, 3 * n, seed)
+    k_s, k_d = _graph(n, 4 * n, seed + 100)
+    b_s, b_d = _graph(n, 2 * n, seed + 200)
+    A, K, B = _mat(n, a_s, a_d), _mat(n, k_s, k_d), _mat(n, b_s, b_d)
+    step = lambda R: (A | _mm(R[0] & K.T, B),)
+    rels = [pack(a_s, a_d), pack(k_s, k_d), pack(b_s, b_d), None]
+    _check(cp.filtered_tc_plan(), rels, [3], _kleene(step, [np.zeros((n, n), bool)]))
+
+
+@pytest.mark.parametrize("n,seed", [(60, 27), (150, 28)])
+def test_flat_same_generation(n, seed):
+    rng = np.random.default_rng(seed)
+    child = np.arange(1, n, dtype=np.uint32)
+    parent = np.array([rng.integers(max(0, int(c) - 6), int(c)) for c in child], dtype=np.uint32)
+    fs = rng.integers(0, n, 3 * n).astype(np.uint32)
+    fd = rng.integers(0, n, 3 * n).astype(np.uint32)
+    F, P = _mat(n, fs, fd), _mat(n, child, parent)
+    step = lambda R: (F | (_mm(_mm(P, R[0]), P.T) & F),)
+    rels = [pack(fs, fd), pack(child, parent), None]
+    _check(cp.flat_sg_plan(), rels, [2], _kleene(step, [np.zeros((n, n), bool)]))

@@ -228,6 +228,10 @@ uint64_t join_probe_general(Ctx *ctx, const uint64_t *probe, uint64_t n, int pco
                             uint64_t **out1);
 void join_match_flags(Ctx *ctx, const uint64_t *probe, uint64_t n, int pcol, const RunIndex &ix, int want,
                       uint8_t *flags);
+// flags[i] = 1 when row i's (key word pcol, other word) pair is a row of the
+// indexed relation (an index on its first column, payloads ascending per run)
+void join_match2_flags(Ctx *ctx, const uint64_t *probe, uint64_t n, int pcol, const RunIndex &ix,
+                       const uint32_t *payload, uint8_t *flags);
 
 #define LAUNCH_1D(kern, n, ...)                                                                             \
     do {                                                                                                    \
@@ -1692,9 +1696,15 @@ bool needed_later(const Rule &r, int from, int var) {
 // variables a later atom or the head reads).  Step j >= 1 joins binding
 // column bpos with column apos of atom j and keeps candidate values sel[0],
 // sel[1] of (binding 0, binding 1, shared, atom's other); a one-atom body
-// projects its columns head[0], head[1].
+// projects its columns head[0], head[1].  An atom whose two variables are
+// both bound (a cyclic body: the reference's left-deep lowering joins it on
+// both keys, lower.rs build_join_tree / compute_join_keys) is a filter step:
+// the binding rows whose values, in the atom's column order, form a row of
+// the atom (binding column bpos holds the atom's first column); sel then
+// picks among the binding's two values.
 struct JoinPlanStep {
     int bpos = 0, apos = 0, sel[2] = {0, 0};
+    bool filter = false;
 };
 struct BodyPlan {
     JoinPlanStep step[MAX_BODY];
@@ -1728,7 +1738,27 @@ BodyPlan plan_body(const Rule &r) {
         for (int x = 0; x < 2; ++x)
             for (int y = 0; y < 2; ++y)
                 if (vars[x] == a.v[y]) { bpos = x; apos = y; ++nshared; }
-        XH_REQUIRE(nshared == 1, XLOG_HIP_UNSUPPORTED, "plan: each atom must share exactly one variable");
+        XH_REQUIRE(nshared == 1 || nshared == 2, XLOG_HIP_UNSUPPORTED,
+                   "plan: each atom must share a variable with the atoms before it");
+        if (nshared == 2) {
+            JoinPlanStep &st = bp.step[j];
+            st.filter = true;
+            st.apos = 0;  // probed through the atom's index on its first column
+            st.bpos = vars[0] == a.v[0] ? 0 : 1;
+            st.sel[0] = 0;
+            st.sel[1] = 1;
+            if (j == r.nb - 1)
+                for (int t = 0; t < 2; ++t) {
+                    const int f = vars[0] == r.hv[t] ? 0 : (vars[1] == r.hv[t] ? 1 : -1);
+                    XH_REQUIRE(f >= 0, XLOG_HIP_UNSUPPORTED, "plan: head variable not bound by the body");
+                    st.sel[t] = f;
+                }
+            bp.grouped = bp.grouped && st.sel[0] == 0;
+            const int v0 = vars[st.sel[0]], v1 = vars[st.sel[1]];
+            vars[0] = v0;
+            vars[1] = v1;
+            continue;
+        }
         int other = a.v[1 - apos];
         // candidate values: v0 = binding var 0, v1 = binding var 1, v2 = shared, v3 = other
         int cand_var[4] = {vars[0], vars[1], a.v[apos], other};
@@ -1924,7 +1954,9 @@ struct Driver {
             const DRel &ar = *rel[j];
             uint64_t *o = nullptr;
             uint64_t on = 0;
-            if (ar.n != 0) {
+            if (ar.n != 0 && st.filter) {
+                on = filter_step(bk, bn, st, index_of(ar, 0), &o);
+            } else if (ar.n != 0) {
                 int oc[4] = {st.sel[0], st.sel[1], 0, 0};
                 if (j == 1 && pre) {  // the count pass ran with the delta's count still on the device
                     on = join_emit(ctx, *pre, oc, &o, max_join_rows, digits);
@@ -1940,6 +1972,34 @@ struct Driver {
             if (bn == 0) return;
         }
         out.add(owned, bn, bp.grouped ? group_bound(src_rows) : 0);
+    }
+
+    // A filter step (plan_body): the rows of the binding bk whose values, in
+    // the atom's column order, are a row of the atom (J: its index on the
+    // first column, whose payloads ascend inside each run), in their order,
+    // then the binding's two values as sel picks them.
+    uint64_t filter_step(const uint64_t *bk, uint64_t bn, const JoinPlanStep &st, const JoinIndex &J, uint64_t **out) {
+        Buf<uint8_t> flags(ctx, bn);
+        join_match2_flags(ctx, bk, bn, st.bpos, J.ix, J.payload.p, flags.p);
+        Owned kept(ctx, alloc_keys(ctx, bn));
+        Buf<uint64_t> cnt(ctx, 1);
+        select_flags(ctx, bk, flags.p, bn, kept.p, cnt.p);
+        ctx->read_scalars(cnt.p, 1);
+        const uint64_t n = ctx->host_scalars[0];
+        if (n && !(st.sel[0] == 0 && st.sel[1] == 1)) {
+            Owned o(ctx, alloc_keys(ctx, n));
+            if (st.sel[0] == 1 && st.sel[1] == 0) {
+                swap_words(ctx, kept.p, n, o.p);
+            } else {
+                ProjSpec s{2, 2, {st.sel[0], st.sel[1], 0, 0, 0, 0, 0, 0}};
+                RelView bv{{kept.p, nullptr, nullptr, nullptr}, 2};
+                RelOut bo{{o.p, nullptr, nullptr, nullptr}};
+                LAUNCH_1D(k_project, n, bv, n, s, bo);
+            }
+            kept.reset(o.release());
+        }
+        *out = n ? kept.release() : nullptr;
+        return n;
     }
 
     // Groups of a body's output that keeps the high word of `rows` sorted
@@ -2174,7 +2234,9 @@ struct Driver {
                 }
             }
             try {
-                (void)plan_body(r);
+                const BodyPlan bp = plan_body(r);
+                for (int j = 1; j < r.nb; ++j)
+                    if (bp.step[j].filter) return false;  // two-key steps run in the host loop
             } catch (const Error &) {
                 return false;  // this order has no left-deep plan: the host loop takes the program
             }

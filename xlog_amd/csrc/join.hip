@@ -527,6 +527,30 @@ __global__ void k_match_flags(ProbeArgs a, int want, uint8_t *__restrict__ flags
     }
 }
 
+// two keys: the key word found and the other word among the run's payloads
+// (which ascend inside the run: an index on the first column of a sorted
+// relation)
+__global__ void k_match2_flags(ProbeArgs a, uint8_t *__restrict__ flags) {
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.n; i += stride) {
+        const uint64_t row = a.probe[i];
+        const uint32_t key = a.pcol ? (uint32_t)row : (uint32_t)(row >> 32);
+        const uint32_t other = a.pcol ? (uint32_t)(row >> 32) : (uint32_t)row;
+        uint64_t st;
+        uint32_t len;
+        bool found = false;
+        if (lookup_run(a.table, a.mask, a.bits, key, &st, &len)) {
+            uint64_t lo = st, hi = st + len;
+            while (lo < hi) {
+                const uint64_t mid = lo + ((hi - lo) >> 1);
+                if (a.payload[mid] < other) lo = mid + 1; else hi = mid;
+            }
+            found = lo < st + len && a.payload[lo] == other;
+        }
+        flags[i] = (uint8_t)found;
+    }
+}
+
 }  // namespace
 
 // Runs of the high word of sorted keys [0, n), n = *d_n when d_n is set
@@ -804,6 +828,15 @@ void join_match_flags(Ctx *ctx, const uint64_t *probe, uint64_t n, int pcol, con
     ProbeArgs a{probe, n, pcol, ix.table.p, ix.table_mask, table_bits(ix), nullptr, nullptr, nullptr, nullptr,
                 nullptr, nullptr, nullptr, nullptr};
     hipLaunchKernelGGL(k_match_flags, dim3(grid_for(n, 256, 16384)), dim3(256), 0, ctx->stream, a, want, flags);
+    XH_CHECK_HIP(hipGetLastError());
+}
+
+void join_match2_flags(Ctx *ctx, const uint64_t *probe, uint64_t n, int pcol, const RunIndex &ix, const uint32_t *payload,
+                       uint8_t *flags) {
+    if (n == 0) return;
+    ProbeArgs a{probe, n, pcol, ix.table.p, ix.table_mask, table_bits(ix), payload, nullptr, nullptr, nullptr,
+                nullptr, nullptr, nullptr, nullptr};
+    hipLaunchKernelGGL(k_match2_flags, dim3(grid_for(n, 256, 16384)), dim3(256), 0, ctx->stream, a, flags);
     XH_CHECK_HIP(hipGetLastError());
 }
 
