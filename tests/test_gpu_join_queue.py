@@ -1,7 +1,10 @@
 """Queued iterations of the join route: programs whose recursive rules each
 read one IDB atom (transitive closure, left-linear closure, mutual recursion,
 same generation) run several iterations per read-back with every row count on
-the device (libxlog_hip's Driver::run_queue).  Checked against the oracle
+the device (libxlog_hip's Driver::run_queue); so do programs whose rules read
+an IDB relation in full beside the delta (non-linear closure, Andersen, a
+four-atom body with two IDB atoms), whose indexes over R are rebuilt on the
+device at the start of every queued iteration.  Checked against the oracle
 (relations, iteration count, every delta size) with the queue on and off, with
 its bounds shrunk so that queues stop and the stopped iteration runs from the
 host (XLOG_HIP_JOIN_QUEUE_MARGIN_PCT / XLOG_HIP_JOIN_QUEUE_SLACK), at the
@@ -13,7 +16,7 @@ import numpy as np
 import pytest
 
 import oracle
-from xlog_amd import ROUTE_JOIN, XlogError, datagen, pack, tc_plan
+from xlog_amd import ROUTE_JOIN, XlogError, andersen_plan, datagen, pack, tc_plan
 
 import chain_plans as cp
 
@@ -58,6 +61,20 @@ def _programs():
     ]
 
 
+def _nonlinear_programs():
+    s, d = _graph(1500, 2600, 31)
+    f = datagen.andersen(600, 2400, 1.5, datagen.seed_for(5))
+    a_s, a_d = _graph(400, 600, 36)
+    b_s, b_d = _graph(400, 380, 37)
+    ss, sd = (datagen.sparse_ids(x) for x in _graph(1200, 1700, 38))
+    return [
+        ("nonlinear tc", cp.nonlinear_tc_plan(), [pack(s, d), None], [1]),
+        ("andersen", andersen_plan(), [pack(*f[k]) for k in ("assign", "addressOf", "load", "store")] + [None], [4]),
+        ("quad", cp.quad_plan(), [pack(a_s, a_d), pack(b_s, b_d), None], [2]),
+        ("sparse-id nonlinear tc", cp.nonlinear_tc_plan(), [pack(ss, sd), None], [1]),
+    ]
+
+
 def _check(p, name, plan, rels, idb, ref):
     outs_o, it_o, deltas_o = ref
     outs, st = _run(p, plan, rels)
@@ -89,6 +106,25 @@ def test_queued_join_route_matches_oracle(provider, monkeypatch):
         assert waits["8"] <= it // 8 + 12, (name, it, waits)
 
 
+def test_queued_join_route_nonlinear(provider, monkeypatch):
+    """Variants that read an IDB relation in full (through an index rebuilt on the device every queued
+    iteration from R's two runs, by its first or second column): queue on and off give the oracle's
+    relations, iterations and deltas, and the queue takes fewer read-backs."""
+    p = provider
+    for name, plan, rels, idb in _nonlinear_programs():
+        ref = oracle.seminaive(plan, rels)
+        waits = {}
+        for queue in ("1", "8"):
+            monkeypatch.setenv("XLOG_HIP_JOIN_QUEUE", queue)
+            _note(f"join queue {name} queue={queue}")
+            waits[queue] = _check(p, name, plan, rels, idb, ref)["host_waits"]
+        it = ref[1]
+        assert it >= 4, (name, it)
+        # an iteration whose candidates pass one sort (2^30 - 1 keys) still runs from the host, in pieces
+        _note(f"join queue {name}: {it} iterations, host waits {waits}")
+        assert waits["8"] <= waits["1"] // 2, (name, it, waits)
+
+
 @pytest.mark.parametrize("margin,slack", [(50, 16), (90, 64), (100, 1024)])
 def test_queued_join_route_stops_and_resumes(provider, monkeypatch, margin, slack):
     """Bounds below the real sizes: queues stop (a check kernel raises the stop flag, every later launch
@@ -97,7 +133,7 @@ def test_queued_join_route_stops_and_resumes(provider, monkeypatch, margin, slac
     p = provider
     monkeypatch.setenv("XLOG_HIP_JOIN_QUEUE_MARGIN_PCT", str(margin))
     monkeypatch.setenv("XLOG_HIP_JOIN_QUEUE_SLACK", str(slack))
-    for name, plan, rels, idb in _programs():
+    for name, plan, rels, idb in _programs() + _nonlinear_programs():
         _note(f"join queue stops {name} margin={margin} slack={slack}")
         _check(p, name, plan, rels, idb, oracle.seminaive(plan, rels))
 

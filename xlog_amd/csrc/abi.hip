@@ -1663,7 +1663,9 @@ namespace {
 
 constexpr int MAX_BODY = 4;
 struct Atom { int pred, v[2]; };
-struct Rule { int head, hv[2], nb; Atom b[MAX_BODY]; };
+// delta_at >= 0: a variant of a rule (its body reordered to start at the
+// atom that reads the delta): the host loop evaluates only that variant
+struct Rule { int head, hv[2], nb; Atom b[MAX_BODY]; int delta_at = -1; };
 
 std::vector<Rule> parse_plan(const int32_t *plan, uint32_t n_preds) {
     XH_REQUIRE(plan, XLOG_HIP_INVALID_ARG, "plan is NULL");
@@ -1816,6 +1818,7 @@ __global__ void k_q_step(QStep a, uint32_t *stop, uint32_t code) {
     if (*stop) return;
     const uint64_t t = *a.tot, b = a.base_in ? *a.base_in : 0ull;
     if (b + t > a.cap || (a.limit && t > a.limit)) {
+        *a.slot = t;  // the count that did not fit: the host sizes the next queue with it
         atomicCAS(stop, 0u, code);
         return;
     }
@@ -1843,6 +1846,16 @@ __global__ void k_q_end(QEnd a, uint32_t *stop, uint32_t code) {
     }
     *a.total = t;
     for (uint32_t h = 0; h < a.heads; ++h) a.nR[h] = a.pR[h] + a.nD[h];
+}
+
+// The rows of a queued iteration's index over an IDB relation read in full:
+// the base run's (known on the host) and the recent run's (on the device, at
+// most its bound).
+__global__ void k_q_rows(uint64_t *out, uint64_t base, const uint64_t *d_recent, uint64_t recent_bound,
+                         const uint32_t *stop) {
+    if (*stop) return;
+    const uint64_t r = *d_recent;
+    *out = base + (r < recent_bound ? r : recent_bound);
 }
 
 // device-resident canonical packed relation
@@ -1876,6 +1889,7 @@ struct Driver {
     // The queued join route keeps R in two sorted runs: full[p] (the base run)
     // and small[p], the recent run every delta is merged into (see run_queue).
     std::vector<DRel> small;
+    bool q_learned = false;  // the last queue stopped and its counts changed the bounds' inputs
 
     ~Driver() {
         cache.clear();
@@ -2140,6 +2154,7 @@ struct Driver {
             for (int occ = 0; occ < r.nb; ++occ) {
                 int p = r.b[occ].pred;
                 if (!idb[p] || delta[p].n == 0) continue;
+                if (r.delta_at >= 0 && occ != r.delta_at) continue;
                 const DRel *rel[MAX_BODY];
                 for (int j = 0; j < r.nb; ++j) {
                     int q = r.b[j].pred;
@@ -2201,46 +2216,53 @@ struct Driver {
     // order, relational.rs:4550-4555) only bodies that start with their IDB
     // atom are queued.  qr receives the rules in the order they run.
     bool queue_rules(std::vector<Rule> &qr) const {
-        qr = rules;
+        qr.clear();
         bool any = false;
-        for (Rule &r : qr) {
-            int n_idb = 0, at = -1;
-            for (int j = 0; j < r.nb; ++j)
-                if (idb[r.b[j].pred]) {
-                    ++n_idb;
-                    at = j;
-                }
-            if (n_idb == 0) continue;
-            if (n_idb != 1 || r.nb < 2) return false;
-            if (at != 0) {
-                if (max_join_rows) return false;
-                const Rule orig = r;
-                bool used[MAX_BODY] = {false, false, false, false};
-                std::vector<int> seen{orig.b[at].v[0], orig.b[at].v[1]};
-                r.b[0] = orig.b[at];
-                used[at] = true;
-                for (int pos = 1; pos < orig.nb; ++pos) {
-                    int pick = -1;
-                    for (int j = 0; j < orig.nb && pick < 0; ++j) {
-                        if (used[j]) continue;
-                        for (int v : seen)
-                            if (orig.b[j].v[0] == v || orig.b[j].v[1] == v) pick = j;
+        for (const Rule &orig : rules) {
+            std::vector<int> occs;
+            for (int j = 0; j < orig.nb; ++j)
+                if (idb[orig.b[j].pred]) occs.push_back(j);
+            if (occs.empty()) {
+                qr.push_back(orig);  // derives only in the seed
+                continue;
+            }
+            if (orig.nb < 2) return false;
+            // one variant per IDB atom (it reads the delta, the other IDB atoms R), its body
+            // reordered to start there
+            for (int at : occs) {
+                Rule r = orig;
+                if (at != 0) {
+                    // a join-row limit must trip where the unqueued loop's body order trips it
+                    if (max_join_rows) return false;
+                    bool used[MAX_BODY] = {false, false, false, false};
+                    std::vector<int> seen{orig.b[at].v[0], orig.b[at].v[1]};
+                    r.b[0] = orig.b[at];
+                    used[at] = true;
+                    for (int pos = 1; pos < orig.nb; ++pos) {
+                        int pick = -1;
+                        for (int j = 0; j < orig.nb && pick < 0; ++j) {
+                            if (used[j]) continue;
+                            for (int v : seen)
+                                if (orig.b[j].v[0] == v || orig.b[j].v[1] == v) pick = j;
+                        }
+                        if (pick < 0) return false;
+                        used[pick] = true;
+                        r.b[pos] = orig.b[pick];
+                        seen.push_back(orig.b[pick].v[0]);
+                        seen.push_back(orig.b[pick].v[1]);
                     }
-                    if (pick < 0) return false;
-                    used[pick] = true;
-                    r.b[pos] = orig.b[pick];
-                    seen.push_back(orig.b[pick].v[0]);
-                    seen.push_back(orig.b[pick].v[1]);
                 }
+                r.delta_at = 0;
+                try {
+                    const BodyPlan bp = plan_body(r);
+                    for (int j = 1; j < r.nb; ++j)
+                        if (bp.step[j].filter) return false;  // two-key steps run in the host loop
+                } catch (const Error &) {
+                    return false;  // this order has no left-deep plan: the host loop takes the program
+                }
+                qr.push_back(r);
+                any = true;
             }
-            try {
-                const BodyPlan bp = plan_body(r);
-                for (int j = 1; j < r.nb; ++j)
-                    if (bp.step[j].filter) return false;  // two-key steps run in the host loop
-            } catch (const Error &) {
-                return false;  // this order has no left-deep plan: the host loop takes the program
-            }
-            any = true;
         }
         return any;
     }
@@ -2249,6 +2271,7 @@ struct Driver {
         int ri = 0, head = 0, dpred = 0;  // rule, head predicate, delta predicate (atom 0)
         BodyPlan bp;
         const JoinIndex *J[MAX_BODY] = {};
+        int dyn[MAX_BODY] = {-1, -1, -1, -1};  // an IDB atom read in full: its index, rebuilt every iteration
         ProbeJob job[MAX_BODY];
         Owned tmp[MAX_BODY] = {Owned(nullptr), Owned(nullptr), Owned(nullptr), Owned(nullptr)};
         uint32_t tot_slot = 0;  // first of its (nb - 1) join-total slots in an iteration's block
@@ -2263,14 +2286,26 @@ struct Driver {
                 heads.push_back((int)p);
             }
         small.assign(n_preds, DRel());
+        if (obs.size() < qr.size()) obs.resize(qr.size());
         uint64_t it = 0;
+        bool retried = false;
         while (it < max_iter) {
             const uint64_t done = run_queue(std::min<uint64_t>(qmax, max_iter - it), it, heads, hidx, deltas, qr);
             if (done == ~0ull) {  // converged inside the queue (it counts the empty iteration)
                 compact_all();
                 return it;
             }
-            if (done > 0) continue;
+            if (done > 0) {
+                retried = false;
+                continue;
+            }
+            // a queue that stopped in its first iteration is queued once more with the bounds its
+            // counts gave, before the host takes that iteration
+            if (q_learned && !retried) {
+                retried = true;
+                continue;
+            }
+            retried = false;
             // an iteration whose queue stopped at once, or one for which no queue fits (one run of R)
             compact_all();
             ++it;
@@ -2294,14 +2329,35 @@ struct Driver {
         // quarter of it, so the merges of a queue rewrite the recent run instead of all of R
         for (int p : heads)
             if (small[p].n > full[p].n / 4) compact((uint32_t)p);
-        // the variants (one per recursive rule, its IDB atom first) and their fixed indexes
+        // the variants (one per IDB atom of a recursive rule, that atom first), the fixed indexes of
+        // their EDB atoms, and an index per IDB relation (and column) that a variant reads in full,
+        // rebuilt on the device at the start of every iteration from R's two runs
+        struct DynIndex {
+            int pred = 0, apos = 0;
+            JoinIndex J;         // table and payload, sized for the queue's largest R
+            Owned rk, srt, alt;  // R in one run; sorted by its second column when apos = 1
+            Buf<uint32_t> run_key;
+            Buf<uint64_t> run_start, cnt;  // cnt: [0] rows of R, [1] runs
+            uint64_t runs_bound = 0;
+            explicit DynIndex(Ctx *c) : rk(c), srt(c), alt(c) {}
+        };
+        std::vector<std::unique_ptr<DynIndex>> dyns;
+        auto dyn_of = [&](int pred, int apos) {
+            for (size_t i = 0; i < dyns.size(); ++i)
+                if (dyns[i]->pred == pred && dyns[i]->apos == apos) return (int)i;
+            std::unique_ptr<DynIndex> d(new DynIndex(ctx));
+            d->pred = pred;
+            d->apos = apos;
+            dyns.push_back(std::move(d));
+            return (int)dyns.size() - 1;
+        };
         std::vector<std::unique_ptr<QVariant>> vars;
         uint32_t tot_words = 0;
         for (size_t ri = 0; ri < qr.size(); ++ri) {
             const Rule &r = qr[ri];
             if (!idb[r.b[0].pred]) continue;
             bool empty_edb = false;
-            for (int j = 1; j < r.nb; ++j) empty_edb = empty_edb || full[r.b[j].pred].n == 0;
+            for (int j = 1; j < r.nb; ++j) empty_edb = empty_edb || (!idb[r.b[j].pred] && full[r.b[j].pred].n == 0);
             if (empty_edb) continue;  // derives nothing, ever
             std::unique_ptr<QVariant> v(new QVariant());
             for (auto &o : v->tmp) o.ctx = ctx;
@@ -2309,7 +2365,11 @@ struct Driver {
             v->head = r.head;
             v->dpred = r.b[0].pred;
             v->bp = plan_body(r);
-            for (int j = 1; j < r.nb; ++j) v->J[j] = &index_of(full[r.b[j].pred], v->bp.step[j].apos);
+            for (int j = 1; j < r.nb; ++j) {
+                const int q = r.b[j].pred;
+                if (idb[q]) v->dyn[j] = dyn_of(q, v->bp.step[j].apos);
+                else v->J[j] = &index_of(full[q], v->bp.step[j].apos);
+            }
             v->tot_slot = tot_words;  // offset by the block's header below
             tot_words += (uint32_t)(r.nb - 1);
             vars.push_back(std::move(v));
@@ -2362,8 +2422,15 @@ struct Driver {
         auto fan = [&](const QVariant &v, int j) {
             const auto &o = obs[v.ri][j];
             if (o.first) return std::max(1.0 / 64.0, (double)o.second / (double)o.first);
-            const JoinIndex &J = *v.J[j];
-            return J.ix.nruns ? std::max(1.0, (double)J.n / (double)J.ix.nruns) : 1.0;
+            if (v.J[j]) {
+                const JoinIndex &J = *v.J[j];
+                return J.ix.nruns ? std::max(1.0, (double)J.n / (double)J.ix.nruns) : 1.0;
+            }
+            // an IDB relation read in full: its rows per distinct value (at most the domain's)
+            const int q = qr[v.ri].b[j].pred;
+            const double rows = (double)(full[q].n + small[q].n);
+            const double keys = std::max(1.0, std::min(rows, domain ? (double)domain : rows));
+            return std::max(1.0, rows / keys);
         };
         // per-step margin over the estimates and a floor on every bound; tests shrink both
         // (XLOG_HIP_JOIN_QUEUE_MARGIN_PCT, XLOG_HIP_JOIN_QUEUE_SLACK) to make queues stop
@@ -2395,7 +2462,15 @@ struct Driver {
                 const Rule &r = qr[v.ri];
                 double t = (double)lb[hidx[v.dpred]];
                 for (int j = 1; j < r.nb; ++j) {
-                    t = std::min(t * fan(v, j) * M + (double)SLACK, (double)SORT_MAX);
+                    // a step into an IDB relation read in full yields more rows per row as that
+                    // relation grows: its fan scales with R's bound over R at the queue's start
+                    double g = 1.0;
+                    if (v.dyn[j] >= 0) {
+                        const int pq = r.b[j].pred;
+                        const double r0 = (double)std::max<uint64_t>(full[pq].n + small[pq].n, 1);
+                        g = std::max(1.0, (double)(full[pq].n + Rb.back()[hidx[pq]]) / r0);
+                    }
+                    t = std::min(t * fan(v, j) * g * M + (double)SLACK, (double)SORT_MAX);
                     tv[vi][j] = (uint64_t)t;
                 }
                 cb[hidx[v.head]] += tv[vi][r.nb - 1];
@@ -2417,6 +2492,12 @@ struct Driver {
                 uint64_t mc = cb[h], mr = rb[h];
                 for (auto &c : Cb) mc = std::max(mc, c[h]);
                 bytes += 8 * (4 * mc + 2 * mr);
+            }
+            // the per-iteration indexes: R in one run (and sorted by its second column), runs, payloads, table
+            for (auto &dp : dyns) {
+                const uint64_t nr = full[dp->pred].n + Rb.back()[hidx[dp->pred]];
+                const uint64_t keys = std::min(nr, domain ? domain : nr);
+                bytes += nr * (24 + (dp->apos ? 16 : 0)) + 64 * keys;
             }
             for (size_t vi = 0; vi < vars.size(); ++vi) {
                 const Rule &r = qr[vars[vi]->ri];
@@ -2466,6 +2547,27 @@ struct Driver {
                 v.tmp[j].reset(alloc_keys(ctx, mt));
             }
         }
+        for (auto &dp : dyns) {
+            DynIndex &d = *dp;
+            const uint64_t nr = std::max<uint64_t>(full[d.pred].n + Rb[Q - 1][hidx[d.pred]], 1);
+            d.runs_bound = std::min(nr, domain ? domain : nr);
+            d.rk.reset(alloc_keys(ctx, nr));
+            if (d.apos) {
+                d.srt.reset(alloc_keys(ctx, nr));
+                d.alt.reset(alloc_keys(ctx, nr));
+            }
+            d.run_key = Buf<uint32_t>(ctx, nr);
+            d.run_start = Buf<uint64_t>(ctx, nr + 1);
+            d.cnt = Buf<uint64_t>(ctx, 2);
+            fill_u64(ctx, d.cnt.p, 0ull, 2);
+            uint64_t slots = 1024;
+            while (slots < 2 * d.runs_bound) slots <<= 1;
+            d.J.ix.table = Buf<unsigned long long>(ctx, 2 * slots);
+            d.J.ix.table_mask = slots - 1;
+            d.J.ix.nruns = d.runs_bound;
+            d.J.payload = Buf<uint32_t>(ctx, nr);
+            d.J.n = nr;
+        }
         const uint64_t words = blk((int64_t)Q);  // word 0 (stop) + Q + 1 blocks
         Buf<uint64_t> qs(ctx, words);
         fill_u64(ctx, qs.p, 0ull, words);
@@ -2495,6 +2597,28 @@ struct Driver {
             uint64_t *nD = bk, *nR = bk + H, *total = bk + total_off;
             const uint64_t *pD = bp, *pR = bp + H;
             const uint32_t code = (uint32_t)(k + 1);
+            // the indexes over R as it stands after the previous iteration (base run + recent run)
+            for (auto &dp : dyns) {
+                DynIndex &d = *dp;
+                const int p = d.pred, hq = hidx[p];
+                const uint64_t nb_ = Rb[k][hq], nr = full[p].n + nb_;
+                const uint64_t *rin = k == 0 ? small[p].k : qh[hq]->R[(k - 1) & 1].p;
+                if (!rin) rin = qh[hq]->R[1].p;  // an empty run read through its device count
+                hipLaunchKernelGGL(k_q_rows, dim3(1), dim3(1), 0, ctx->stream, d.cnt.p, full[p].n, pR + hq, nb_, stop);
+                XH_CHECK_HIP(hipGetLastError());
+                merge_sorted_dev(ctx, full[p].k ? full[p].k : rin, full[p].n, nullptr, rin, nb_, pR + hq, d.rk.p,
+                                 nullptr, stop);
+                uint64_t *sk = d.rk.p;
+                if (d.apos) {
+                    swap_words(ctx, d.rk.p, nr, d.srt.p);  // over the bound: the rows past the count are not sorted
+                    uint64_t *ka = d.srt.p, *kb = d.alt.p;
+                    radix_sort_dev(ctx, &ka, &kb, nr, d.cnt.p, digits, stop);
+                    sk = ka;
+                }
+                select_runs(ctx, sk, nr, d.run_key.p, d.run_start.p, d.cnt.p + 1, d.cnt.p);
+                run_index_insert_dev(ctx, d.run_key.p, d.run_start.p, d.cnt.p + 1, d.runs_bound, d.cnt.p, d.J.ix, stop);
+                low_words(ctx, sk, nr, d.J.payload.p);
+            }
             for (size_t vi = 0; vi < vars.size(); ++vi) {
                 QVariant &v = *vars[vi];
                 const Rule &r = qr[v.ri];
@@ -2510,8 +2634,9 @@ struct Driver {
                     job = ProbeJob();
                     job.probe = left;
                     job.pcol = st.bpos;
-                    job.ix = &v.J[j]->ix;
-                    job.payload = v.J[j]->payload.p;
+                    const JoinIndex &J = v.J[j] ? *v.J[j] : dyns[v.dyn[j]]->J;
+                    job.ix = &J.ix;
+                    job.payload = J.payload.p;
                     // the first step's count raises the stop flag itself when the delta it reads
                     // is past the bound its launches are sized for
                     probe_prepare_deferred(ctx, job, left_bound, d_left, stop, j == 1 ? code : 0u);
@@ -2631,6 +2756,33 @@ struct Driver {
                 delta[p].k = qh[h]->D[kd & 1].release();
                 delta[p].owned = true;
                 delta[p].version = version_counter++;
+            }
+        }
+        // a stopped iteration's counts up to the stop (join totals, and its deltas when the stop came
+        // after them) size the next queue's bounds
+        q_learned = false;
+        if (stopped && !converged) {
+            const uint64_t *bk = hs + blk((int64_t)complete);
+            const uint64_t *bp = hs + blk((int64_t)complete - 1);
+            for (auto &vp : vars) {
+                const Rule &r = qr[vp->ri];
+                uint64_t in = bp[hidx[vp->dpred]];
+                for (int j = 1; j < r.nb; ++j) {
+                    const uint64_t o = bk[vp->tot_slot + (j - 1)];
+                    if (!o) break;  // the steps after the stop did not run
+                    if (in) {
+                        obs[vp->ri][j] = {in, o};
+                        q_learned = true;
+                    }
+                    in = o;
+                }
+            }
+            for (uint32_t h = 0; h < H; ++h) {
+                const uint64_t cand = bk[base_off[h] + nvar[h]];
+                if (cand && bk[h]) {
+                    nov[heads[h]] = (double)bk[h] / (double)cand;
+                    q_learned = true;
+                }
             }
         }
         if (converged) return ~0ull;

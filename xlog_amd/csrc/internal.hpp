@@ -430,6 +430,12 @@ struct RunScratch {
 void build_run_index_async(Ctx *ctx, const uint64_t *sorted_keys, uint64_t n_bound, const uint64_t *d_n,
                            RunScratch &rs, uint64_t *d_nruns);
 void build_run_index_finish(Ctx *ctx, RunScratch &rs, uint64_t nruns, uint64_t n, RunIndex &ix);
+// The table of a run index whose runs are on the device (select_runs with a
+// device row count: *d_nruns runs, at most runs_bound, over *d_n sorted keys):
+// ix.table holds ix.table_mask + 1 >= 2 * runs_bound slots and is cleared and
+// filled here, with no read-back; a raised stop leaves it cleared.
+void run_index_insert_dev(Ctx *ctx, const uint32_t *run_key, const uint64_t *run_start, const uint64_t *d_nruns,
+                          uint64_t runs_bound, const uint64_t *d_n, RunIndex &ix, const uint32_t *stop);
 // Merge-path lookup of the sort-merge join: for every row of l (sorted by the
 // key word pcol), the start and length of its run among the nr runs of
 // (run_key, run_start[0..nr]) (sorted, distinct keys); length 0 without one.

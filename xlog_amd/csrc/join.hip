@@ -76,6 +76,32 @@ __global__ void k_insert(const uint32_t *__restrict__ run_key, const uint64_t *_
     }
 }
 
+// k_insert for a run list whose count is on the device (*d_nruns, at most
+// runs_bound, which the table was sized for: at most half its slots fill)
+// over sorted keys whose count is *d_n (the last run ends there); a raised
+// stop ends it.
+__global__ void k_insert_dev(const uint32_t *__restrict__ run_key, const uint64_t *__restrict__ run_start,
+                             const uint64_t *d_nruns, uint64_t runs_bound, const uint64_t *d_n,
+                             unsigned long long *table, uint64_t mask, int bits, const uint32_t *stop) {
+    if (stop && *stop) return;
+    const uint64_t nruns = *d_nruns < runs_bound ? *d_nruns : runs_bound, n = *d_n;
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t r = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; r < nruns; r += stride) {
+        const uint32_t key = run_key[r];
+        const uint64_t st = run_start[r], en = r + 1 < nruns ? run_start[r + 1] : n;
+        const unsigned long long v = ((unsigned long long)key << 32) | (unsigned long long)(en - st);
+        uint64_t h = hash_slot(key, bits);
+        for (;;) {
+            unsigned long long old = atomicCAS(&table[2 * h], 0ull, v);
+            if (old == 0ull) {
+                table[2 * h + 1] = st;  // read only by later launches
+                break;
+            }
+            h = (h + 1) & mask;
+        }
+    }
+}
+
 __global__ void k_set_u64(uint64_t *p, uint64_t v) { *p = v; }
 __global__ void k_max_run_len(const uint64_t *__restrict__ run_start, uint64_t nruns, unsigned long long *mx) {
     uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
@@ -587,6 +613,16 @@ void build_run_index_finish(Ctx *ctx, RunScratch &rs, uint64_t nruns, uint64_t n
     if (ix.nruns)
         hipLaunchKernelGGL(k_insert, dim3(grid_for(ix.nruns, 256, 16384)), dim3(256), 0, ctx->stream, rs.run_key.p,
                            rs.run_start.p, ix.nruns, ix.table.p, ix.table_mask, bits);
+    XH_CHECK_HIP(hipGetLastError());
+}
+void run_index_insert_dev(Ctx *ctx, const uint32_t *run_key, const uint64_t *run_start, const uint64_t *d_nruns,
+                          uint64_t runs_bound, const uint64_t *d_n, RunIndex &ix, const uint32_t *stop) {
+    const uint64_t slots = ix.table_mask + 1;
+    XH_REQUIRE(slots >= 2 * runs_bound, XLOG_HIP_INVALID_ARG, "run index: table smaller than twice its runs");
+    fill_u64(ctx, reinterpret_cast<uint64_t *>(ix.table.p), 0ull, 2 * slots);
+    if (!runs_bound) return;
+    hipLaunchKernelGGL(k_insert_dev, dim3(persistent_grid(ctx, (runs_bound + 255) / 256, 8)), dim3(256), 0, ctx->stream,
+                       run_key, run_start, d_nruns, runs_bound, d_n, ix.table.p, ix.table_mask, __builtin_ctzll(slots), stop);
     XH_CHECK_HIP(hipGetLastError());
 }
 void build_run_index(Ctx *ctx, const uint64_t *sorted_keys, uint64_t n, RunIndex &ix) {
