@@ -111,12 +111,13 @@ def test_skewed_high_word_keeps_digit_passes(provider, monkeypatch):
     _check(provider, keys, monkeypatch, want_runs=0, want_passes=8)
 
 
-def test_ticket_order(provider, monkeypatch):
-    """XLOG_HIP_SORT_TICKETS=1: the radix passes and the short-run unique number their tiles by start tickets."""
+def test_index_order(provider, monkeypatch):
+    """XLOG_HIP_SORT_TICKETS=0: the radix passes and the short-run unique take their tiles in workgroup-index
+    order (the default numbers them by start tickets, as every other test here runs)."""
     n = N_MIN + 777
     keys = datagen.dup_tuples(n, 11)
-    _note("hybrid sort: ticket order")
-    monkeypatch.setenv("XLOG_HIP_SORT_TICKETS", "1")
+    _note("hybrid sort: index order")
+    monkeypatch.setenv("XLOG_HIP_SORT_TICKETS", "0")
     got, runs, passes = _dedup_with_route(provider, keys)
     assert (runs, passes) == (1, 4)
     assert np.array_equal(got, oracle.sort_dedup(keys))

@@ -1,9 +1,12 @@
 """GPU parity of the radix sort at every tile-order chunk size.
 
-The digit passes deal tiles to the XCDs in chunks of consecutive tiles
-(xlog_amd/csrc/sort.hip, chunk_tile): 8 tiles per chunk from 512 tiles up, and
-tiles / 64 below that, so sorts of 64-511 tiles run with chunks of 1..7 and a
-last group of blocks partly without a tile.  Keys-only sorts use 8192-key tiles;
+By default the digit passes number their tiles by start tickets; with
+XLOG_HIP_SORT_TICKETS=0 (which the tests of this module take, except
+test_tile_orders, which runs both orders) they deal tiles to the XCDs in chunks
+of consecutive tiles by workgroup index (xlog_amd/csrc/sort.hip, chunk_tile): 8
+tiles per chunk from 512 tiles up, and tiles / 64 below that, so sorts of
+64-511 tiles run with chunks of 1..7 and a last group of blocks partly without
+a tile.  Keys-only sorts use 8192-key tiles;
 sorts that carry a row payload (the keyed sort of arity-3/4 rows, join index
 builds) use 4096-key tiles.  Every size here is checked against numpy: the full
 sort + dedup, a stable sort on one key column, and narrow keys whose constant
@@ -20,6 +23,12 @@ from xlog_amd import pack
 pytestmark = pytest.mark.gpu
 
 TILE_K = 8192  # keys-only tile
+
+
+@pytest.fixture(autouse=True)
+def _index_order(monkeypatch):
+    """The chunked workgroup-index order, whose chunk sizes these tests walk."""
+    monkeypatch.setenv("XLOG_HIP_SORT_TICKETS", "0")
 
 
 def _note(msg):
@@ -120,13 +129,18 @@ def test_stable_sort_column_with_constant_low_byte(provider, n):
     assert np.array_equal(got, pack(c0[order], c1[order]))
 
 
+@pytest.mark.parametrize("order", ["ticket", "index"])
 @pytest.mark.parametrize("tiles", [1, 64, 260, 700, 2100])
-def test_ticketed_tile_order(provider, monkeypatch, tiles):
-    # XLOG_HIP_SORT_TICKETS=1: tiles numbered by start-order tickets (no in-order dispatch assumed)
+def test_tile_orders(provider, monkeypatch, tiles, order):
+    # the default numbers tiles by start-order tickets (no in-order dispatch or co-residency assumed);
+    # XLOG_HIP_SORT_TICKETS=0 takes the workgroup-index order with XCD chunks
     p = provider
-    monkeypatch.setenv("XLOG_HIP_SORT_TICKETS", "1")
+    if order == "index":
+        monkeypatch.setenv("XLOG_HIP_SORT_TICKETS", "0")
+    else:
+        monkeypatch.delenv("XLOG_HIP_SORT_TICKETS", raising=False)
     n = tiles * TILE_K - (tiles * 53) % 3000
-    _note(f"ticketed sort: tiles={tiles} n={n}")
+    _note(f"sort tile order {order}: tiles={tiles} n={n}")
     rng = np.random.default_rng(1000 + tiles)
     keys = rng.integers(0, 1 << 64, size=n, dtype=np.uint64)
     keys[rng.integers(0, n, n // 4)] = keys[rng.integers(0, n, n // 4)]  # duplicates

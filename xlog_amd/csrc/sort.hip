@@ -569,9 +569,15 @@ static uint32_t pass_capacity(Ctx *ctx) {
     return (uint32_t)ctx->num_cus * (uint32_t)b;
 }
 
+// Tiles by start ticket (the default): a block takes its tile from an atomic
+// counter when it starts, so a tile waits only on tiles whose blocks have
+// started, whatever the dispatch order and however few blocks are resident
+// (a GPU shared with other streams).  XLOG_HIP_SORT_TICKETS=0 restores the
+// workgroup-index order with XCD chunks, faster and correct under in-order
+// dispatch with 8 x chunk blocks co-resident (chunk_tile).
 bool sort_tickets() {
     const char *e = getenv("XLOG_HIP_SORT_TICKETS");
-    return e && e[0] == '1';
+    return !(e && e[0] == '0');
 }
 static bool sort_persist() {
     const char *e = getenv("XLOG_HIP_SORT_PERSIST");
@@ -752,6 +758,9 @@ int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **va
         Prof prof(ctx, XLOG_HIP_KERNEL_SORT_PASS, (has_val ? 24.0 : 16.0) * (double)n);
         unsigned long long *tk = sort_tickets() ? ctx->tickets + 2 : nullptr;
         unsigned long long tb = tk ? ctx->take_tickets(2, grid) : 0ull;
+        // tickets go to tiles in plain order (chunk 1: chunk_tile is then the identity), which measured
+        // faster than tickets dealt to XCD chunks
+        const uint32_t pchunk = tk ? 1u : chunk;
         unsigned pgrid = grid;
         const uint64_t *pn = nullptr;
         if (sort_persist()) {
@@ -767,11 +776,11 @@ int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **va
         if (has_val)
             hipLaunchKernelGGL((k_onesweep<true, SORT_BLOCK_V, SORT_ITEMS_V>), dim3(pgrid), dim3(SORT_BLOCK_V), 0,
                                ctx->stream, *keys, *keys_alt, *vals, *vals_alt, n, (uint32_t)tiles, 8 * dgt,
-                               off + dgt * 256, st.status[cur], st.status[nxt], chunk, tk, tb, pn, nullptr);
+                               off + dgt * 256, st.status[cur], st.status[nxt], pchunk, tk, tb, pn, nullptr);
         else
             hipLaunchKernelGGL((k_onesweep<false, SORT_BLOCK_K, SORT_ITEMS_K>), dim3(pgrid), dim3(SORT_BLOCK_K), 0,
                                ctx->stream, (passes == 0 && src) ? src : *keys, *keys_alt, nullptr, nullptr, n,
-                               (uint32_t)tiles, 8 * dgt, off + dgt * 256, st.status[cur], st.status[nxt], chunk,
+                               (uint32_t)tiles, 8 * dgt, off + dgt * 256, st.status[cur], st.status[nxt], pchunk,
                                tk, tb, pn, nullptr);
         XH_CHECK_HIP(hipGetLastError());
         st.dirty[cur] = tiles;
