@@ -263,6 +263,44 @@ def test_hash_route_queued_steps(provider, monkeypatch):
         assert it_o > 16 and waits["8"] < waits["1"] - it_o // 2, (name, it_o, waits)
 
 
+def test_hash_route_queued_indexed(provider, monkeypatch):
+    """Programs whose variants read an IDB relation in full (non-linear closure, Andersen) queue on the
+    hash-set route too: before each queued step the relation's appends of the step before are sorted and
+    merged into it and its indexes rebuilt, all on the device.  The same relations and deltas as one
+    read-back per iteration, with fewer waits; then with 100 appends per step in a 64-slot table, so that
+    queued steps overflow and are rerun from the host."""
+    p = provider
+    s, d = _spread(*_graph(1500, 2600, 28))
+    f = datagen.andersen(800, 3000, 1.5, datagen.seed_for(5))
+    progs = (("nonlinear tc", cp.nonlinear_tc_plan(), [pack(s, d), None], [1]),
+             ("andersen", andersen_plan(), [pack(*f[k]) for k in ("assign", "addressOf", "load", "store")] + [None],
+              [4]))
+    for name, plan, rels, idb in progs:
+        outs_o, it_o, deltas_o = oracle.seminaive(plan, rels)
+        waits = {}
+        for queue in ("1", "8"):
+            monkeypatch.setenv("XLOG_HIP_HASH_QUEUE", queue)
+            _note(f"queued indexed {name} queue={queue}")
+            outs, st = _run(p, plan, rels, ROUTE_HASH)
+            for q in idb:
+                assert np.array_equal(p.download_packed(outs[q]), outs_o[q]), f"{name} queue {queue} pred {q}"
+                assert outs[q].is_canonical()
+            assert st["iterations"] == it_o and st["delta_sizes"] == deltas_o
+            waits[queue] = st["host_waits"]
+        _note(f"queued indexed {name}: {it_o} iterations, host waits {waits}")
+        assert waits["8"] < waits["1"], (name, it_o, waits)
+    monkeypatch.delenv("XLOG_HIP_HASH_QUEUE")
+    monkeypatch.setenv("XLOG_HIP_HASH_SLOTS", "64")
+    monkeypatch.setenv("XLOG_HIP_HASH_APPENDS", "100")
+    for name, plan, rels, idb in progs:
+        _note(f"queued indexed overflow {name}")
+        outs_o, it_o, deltas_o = oracle.seminaive(plan, rels)
+        outs, st = _run(p, plan, rels, ROUTE_HASH)
+        for q in idb:
+            assert np.array_equal(p.download_packed(outs[q]), outs_o[q]), name
+        assert st["iterations"] == it_o and st["delta_sizes"] == deltas_o
+
+
 def test_hash_route_queued_overflow(provider, monkeypatch):
     """Queued steps of at most 100 appends each in a 64-slot table: steps overflow inside the queue (the
     later ones then do nothing), and the half-load budget cuts steps short; each such step is rerun

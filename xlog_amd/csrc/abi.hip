@@ -1858,6 +1858,22 @@ __global__ void k_q_rows(uint64_t *out, uint64_t base, const uint64_t *d_recent,
     *out = base + (r < recent_bound ? r : recent_bound);
 }
 
+// Queued hash-route steps: any of the overflow flags of the steps before
+// this one (which then do nothing) as a stop word, and a relation's rows after
+// a step (its rows before it, on the device, plus the step's appends, at most
+// their bound).
+__global__ void k_any_set(const unsigned long long *flags, uint32_t n, uint32_t *out) {
+    uint32_t a = 0;
+    for (uint32_t i = 0; i < n; ++i) a |= flags[i] != 0ull ? 1u : 0u;
+    *out = a;
+}
+__global__ void k_add_rows(uint64_t *out, const uint64_t *d_a, const uint64_t *d_b, uint64_t b_bound,
+                           const uint32_t *stop) {
+    if (*stop) return;
+    const uint64_t b = *d_b;
+    *out = *d_a + (b < b_bound ? b : b_bound);
+}
+
 // device-resident canonical packed relation
 struct DRel {
     uint64_t *k = nullptr;
@@ -1924,6 +1940,58 @@ struct Driver {
     void drop_index(const DRel &rel) {
         for (auto it = cache.begin(); it != cache.end();)
             if (it->first.k == rel.k) it = cache.erase(it); else ++it;
+    }
+
+    // An index over an IDB relation whose rows are on the device (a queued
+    // iteration's R): rows r[0, cnt[0]) sorted, cnt[0] at most the bound the
+    // buffers are sized for, indexed on column col (the second through a sorted
+    // copy of the rows with their words exchanged): runs, a table for at most
+    // min(bound, domain) runs (every value is below the domain) and payloads,
+    // rebuilt with device counts and no read-back.
+    struct DevIndex {
+        int pred = 0, col = 0;
+        JoinIndex J;
+        Owned srt, alt;
+        Buf<uint32_t> run_key;
+        Buf<uint64_t> run_start, cnt;  // cnt[0]: the rows (written by the caller), cnt[1]: the runs
+        uint64_t runs_bound = 0;
+        explicit DevIndex(Ctx *c) : srt(c), alt(c) {}
+    };
+    void dev_index_alloc(DevIndex &d, uint64_t bound) {
+        const uint64_t nr = std::max<uint64_t>(bound, 1);
+        d.runs_bound = std::min(nr, domain ? domain : nr);
+        if (d.col) {
+            d.srt.reset(alloc_keys(ctx, nr));
+            d.alt.reset(alloc_keys(ctx, nr));
+        }
+        d.run_key = Buf<uint32_t>(ctx, nr);
+        d.run_start = Buf<uint64_t>(ctx, nr + 1);
+        d.cnt = Buf<uint64_t>(ctx, 2);
+        fill_u64(ctx, d.cnt.p, 0ull, 2);
+        uint64_t slots = 1024;
+        while (slots < 2 * d.runs_bound) slots <<= 1;
+        d.J.ix.table = Buf<unsigned long long>(ctx, 2 * slots);
+        d.J.ix.table_mask = slots - 1;
+        d.J.ix.nruns = d.runs_bound;
+        d.J.payload = Buf<uint32_t>(ctx, nr);
+        d.J.n = nr;
+    }
+    // r holds at least nr (<= the allocated bound) rows' room; a raised stop skips the work
+    void dev_index_build(DevIndex &d, const uint64_t *r, uint64_t nr, const uint32_t *stop) {
+        if (nr == 0) {  // no rows yet: an empty table (cnt[1] is still 0)
+            run_index_insert_dev(ctx, d.run_key.p, d.run_start.p, d.cnt.p + 1, 0, d.cnt.p, d.J.ix, stop);
+            return;
+        }
+        const uint64_t *sk = r;
+        if (d.col) {
+            swap_words(ctx, r, nr, d.srt.p);  // over the bound: the rows past the count are not sorted
+            uint64_t *ka = d.srt.p, *kb = d.alt.p;
+            radix_sort_dev(ctx, &ka, &kb, nr, d.cnt.p, digits, stop);
+            sk = ka;
+        }
+        select_runs(ctx, sk, nr, d.run_key.p, d.run_start.p, d.cnt.p + 1, d.cnt.p);
+        run_index_insert_dev(ctx, d.run_key.p, d.run_start.p, d.cnt.p + 1, d.runs_bound, d.cnt.p, d.J.ix, stop);
+        low_words(ctx, sk, nr, d.J.payload.p);
     }
 
     // Evaluate a rule body; rel[j] is the relation atom j reads.  Appends the
@@ -2332,22 +2400,17 @@ struct Driver {
         // the variants (one per IDB atom of a recursive rule, that atom first), the fixed indexes of
         // their EDB atoms, and an index per IDB relation (and column) that a variant reads in full,
         // rebuilt on the device at the start of every iteration from R's two runs
-        struct DynIndex {
-            int pred = 0, apos = 0;
-            JoinIndex J;         // table and payload, sized for the queue's largest R
-            Owned rk, srt, alt;  // R in one run; sorted by its second column when apos = 1
-            Buf<uint32_t> run_key;
-            Buf<uint64_t> run_start, cnt;  // cnt: [0] rows of R, [1] runs
-            uint64_t runs_bound = 0;
-            explicit DynIndex(Ctx *c) : rk(c), srt(c), alt(c) {}
+        struct DynIndex : DevIndex {
+            Owned rk;  // R in one run (base + recent)
+            explicit DynIndex(Ctx *c) : DevIndex(c), rk(c) {}
         };
         std::vector<std::unique_ptr<DynIndex>> dyns;
         auto dyn_of = [&](int pred, int apos) {
             for (size_t i = 0; i < dyns.size(); ++i)
-                if (dyns[i]->pred == pred && dyns[i]->apos == apos) return (int)i;
+                if (dyns[i]->pred == pred && dyns[i]->col == apos) return (int)i;
             std::unique_ptr<DynIndex> d(new DynIndex(ctx));
             d->pred = pred;
-            d->apos = apos;
+            d->col = apos;
             dyns.push_back(std::move(d));
             return (int)dyns.size() - 1;
         };
@@ -2497,7 +2560,7 @@ struct Driver {
             for (auto &dp : dyns) {
                 const uint64_t nr = full[dp->pred].n + Rb.back()[hidx[dp->pred]];
                 const uint64_t keys = std::min(nr, domain ? domain : nr);
-                bytes += nr * (24 + (dp->apos ? 16 : 0)) + 64 * keys;
+                bytes += nr * (24 + (dp->col ? 16 : 0)) + 64 * keys;
             }
             for (size_t vi = 0; vi < vars.size(); ++vi) {
                 const Rule &r = qr[vars[vi]->ri];
@@ -2550,23 +2613,8 @@ struct Driver {
         for (auto &dp : dyns) {
             DynIndex &d = *dp;
             const uint64_t nr = std::max<uint64_t>(full[d.pred].n + Rb[Q - 1][hidx[d.pred]], 1);
-            d.runs_bound = std::min(nr, domain ? domain : nr);
             d.rk.reset(alloc_keys(ctx, nr));
-            if (d.apos) {
-                d.srt.reset(alloc_keys(ctx, nr));
-                d.alt.reset(alloc_keys(ctx, nr));
-            }
-            d.run_key = Buf<uint32_t>(ctx, nr);
-            d.run_start = Buf<uint64_t>(ctx, nr + 1);
-            d.cnt = Buf<uint64_t>(ctx, 2);
-            fill_u64(ctx, d.cnt.p, 0ull, 2);
-            uint64_t slots = 1024;
-            while (slots < 2 * d.runs_bound) slots <<= 1;
-            d.J.ix.table = Buf<unsigned long long>(ctx, 2 * slots);
-            d.J.ix.table_mask = slots - 1;
-            d.J.ix.nruns = d.runs_bound;
-            d.J.payload = Buf<uint32_t>(ctx, nr);
-            d.J.n = nr;
+            dev_index_alloc(d, nr);
         }
         const uint64_t words = blk((int64_t)Q);  // word 0 (stop) + Q + 1 blocks
         Buf<uint64_t> qs(ctx, words);
@@ -2608,16 +2656,7 @@ struct Driver {
                 XH_CHECK_HIP(hipGetLastError());
                 merge_sorted_dev(ctx, full[p].k ? full[p].k : rin, full[p].n, nullptr, rin, nb_, pR + hq, d.rk.p,
                                  nullptr, stop);
-                uint64_t *sk = d.rk.p;
-                if (d.apos) {
-                    swap_words(ctx, d.rk.p, nr, d.srt.p);  // over the bound: the rows past the count are not sorted
-                    uint64_t *ka = d.srt.p, *kb = d.alt.p;
-                    radix_sort_dev(ctx, &ka, &kb, nr, d.cnt.p, digits, stop);
-                    sk = ka;
-                }
-                select_runs(ctx, sk, nr, d.run_key.p, d.run_start.p, d.cnt.p + 1, d.cnt.p);
-                run_index_insert_dev(ctx, d.run_key.p, d.run_start.p, d.cnt.p + 1, d.runs_bound, d.cnt.p, d.J.ix, stop);
-                low_words(ctx, sk, nr, d.J.payload.p);
+                dev_index_build(d, d.rk.p, nr, stop);
             }
             for (size_t vi = 0; vi < vars.size(); ++vi) {
                 QVariant &v = *vars[vi];
@@ -2923,10 +2962,13 @@ struct Driver {
             bool copy = false;  // one-atom body: the delta rows themselves (swapped when `swap`)
             bool swap = false;
             double fanout = 1.0;  // expected head tuples per delta row
+            int hp[2] = {-1, -1}, hc[2] = {0, 0};  // per hop: the predicate and key column it reads
         };
         // The launch arguments of the variant with the delta at path position d of rule ri (rows left
-        // unset), with its hops at the current full relations; false when a hop has no run at all.
-        auto make_var = [&](size_t ri, int d, Var &v) -> bool {
+        // unset), with its hops at the current full relations; false when a hop has no run at all.  In
+        // queued steps (queued) a hop into an indexed predicate is left to the index the queue rebuilds
+        // on the device before every step.
+        auto make_var = [&](size_t ri, int d, Var &v, bool queued = false) -> bool {
             const std::vector<ChainAtom> &path = chains[ri].path;
             const int m = (int)path.size();
             v = Var();
@@ -2935,6 +2977,10 @@ struct Driver {
             // x_{j+1} (right of it); the stored tuple is (x_j, x_{j+1}) unless backward
             auto hop = [&](int j, bool left, PathHop &h) {
                 const bool key_col1 = left != path[j].backward;
+                const int slot = &h == &v.a.h1 ? 0 : 1;
+                v.hp[slot] = path[j].pred;
+                v.hc[slot] = key_col1 ? 1 : 0;
+                if (queued && indexed[path[j].pred]) return true;
                 const DRel &rel = full[path[j].pred];
                 if (rel.n == 0) return false;
                 const JoinIndex &J = index_of(rel, key_col1 ? 1 : 0);
@@ -3104,7 +3150,7 @@ struct Driver {
             sync_pass(vars, appended, out);
             deltas.push_back(finish_pass(appended, out));
         }
-        const uint64_t queue_max = any_indexed ? 1 : std::min<uint64_t>(env_u64("XLOG_HIP_HASH_QUEUE", 8), 256);
+        const uint64_t queue_max = std::min<uint64_t>(env_u64("XLOG_HIP_HASH_QUEUE", 8), 256);
         uint64_t queue = queue_max;
         std::vector<Buf<uint64_t>> spare(n_preds);  // the second delta buffer of the queued steps
         std::vector<uint64_t> cap(n_preds, 0);
@@ -3123,7 +3169,7 @@ struct Driver {
                     for (int d = 0; d < (int)chains[ri].path.size(); ++d) {
                         if (!idb[chains[ri].path[d].pred]) continue;
                         Var v;
-                        if (!make_var(ri, d, v)) continue;
+                        if (!make_var(ri, d, v, true)) continue;
                         by_head[chains[ri].head].push_back({ri, d});
                         tmpl[chains[ri].head].push_back(v);
                     }
@@ -3158,7 +3204,91 @@ struct Driver {
                 fill_u64(ctx, ovf.p, 0ull, K + 1);
                 unsigned long long *ucnt = reinterpret_cast<unsigned long long *>(cnt.p);
                 unsigned long long *uovf = reinterpret_cast<unsigned long long *>(ovf.p);
+                // An indexed predicate's R after step j is R_j = R_{j-1} ∪ (step j's appends): before step
+                // j >= 2 the appends of step j-1 are sorted (in their ring buffer: a permutation of the same
+                // rows) and merged into the other of two buffers, and the indexes that the variants' hops
+                // read are rebuilt from it; after the last step R_K is merged once more.  Every count stays
+                // on the device; a step that overflowed stops all of this (k_any_set).
+                struct QR {
+                    Owned RB[2], srt_alt;
+                    Buf<uint64_t> dR;  // [j]: rows of R_j (R_0: full)
+                    uint64_t bound = 0;
+                    explicit QR(Ctx *c) : RB{Owned(c), Owned(c)}, srt_alt(c) {}
+                };
+                std::vector<std::unique_ptr<QR>> qrel(n_preds);
+                std::vector<std::unique_ptr<DevIndex>> devs;
+                Buf<uint32_t> stp(ctx, 1);
+                fill_u32(ctx, stp.p, 0u, 1);
+                for (uint32_t p = 0; p < n_preds; ++p)
+                    for (size_t t = 0; t < tmpl[p].size(); ++t)
+                        for (int slot = 0; slot < 2; ++slot) {
+                            Var &v = tmpl[p][t];
+                            const int q = v.hp[slot];
+                            if (q < 0 || !indexed[q]) continue;
+                            if (!qrel[q]) {
+                                std::unique_ptr<QR> x(new QR(ctx));
+                                x->bound = full[q].n + K * cap[q];
+                                x->RB[0].reset(alloc_keys(ctx, x->bound));
+                                x->RB[1].reset(alloc_keys(ctx, x->bound));
+                                x->srt_alt.reset(alloc_keys(ctx, cap[q]));
+                                x->dR = Buf<uint64_t>(ctx, K + 1);
+                                fill_u64(ctx, x->dR.p, full[q].n, 1);
+                                qrel[q] = std::move(x);
+                            }
+                            DevIndex *d = nullptr;
+                            for (auto &e : devs)
+                                if (e->pred == q && e->col == v.hc[slot]) d = e.get();
+                            if (!d) {
+                                devs.emplace_back(new DevIndex(ctx));
+                                d = devs.back().get();
+                                d->pred = q;
+                                d->col = v.hc[slot];
+                                dev_index_alloc(*d, qrel[q]->bound);
+                            }
+                            PathHop &h = slot ? v.a.h2 : v.a.h1;
+                            h.table = d->J.ix.table.p;
+                            h.mask = d->J.ix.table_mask;
+                            h.bits = __builtin_ctzll(d->J.ix.table_mask + 1);
+                            h.payload = d->J.payload.p;
+                        }
+                // R_{j-1} and the indexes over it, before step j (j = K + 1: R_K only)
+                auto refresh = [&](uint64_t j) {
+                    if (j >= 2) {
+                        hipLaunchKernelGGL(k_any_set, dim3(1), dim3(1), 0, ctx->stream, uovf + 1, (uint32_t)(j - 1),
+                                           stp.p);
+                        XH_CHECK_HIP(hipGetLastError());
+                    }
+                    for (uint32_t q = 0; q < n_preds; ++q) {
+                        if (!qrel[q]) continue;
+                        QR &x = *qrel[q];
+                        const uint64_t *r = full[q].k;  // R_{j-1}
+                        uint64_t rn = full[q].n;
+                        if (j >= 2) {
+                            // the appends of step j - 1, sorted where they lie; merged with R_{j-2}
+                            uint64_t *ka = ring[(j - 1) % 2][q].p, *kb = x.srt_alt.p;
+                            const uint64_t *dapp = cnt.p + (j - 1) * P + q;
+                            radix_sort_dev(ctx, &ka, &kb, cap[q], dapp, digits, stp.p);
+                            const uint64_t *prev = j == 2 ? full[q].k : x.RB[(j - 2) % 2].p;
+                            const uint64_t prev_n = full[q].n + (j - 2) * cap[q];
+                            uint64_t *dst = x.RB[(j - 1) % 2].p;
+                            merge_sorted_dev(ctx, prev ? prev : ka, prev_n, j == 2 ? nullptr : x.dR.p + (j - 2), ka,
+                                             cap[q], dapp, dst, nullptr, stp.p);
+                            hipLaunchKernelGGL(k_add_rows, dim3(1), dim3(1), 0, ctx->stream, x.dR.p + (j - 1),
+                                               x.dR.p + (j - 2), dapp, cap[q], stp.p);
+                            XH_CHECK_HIP(hipGetLastError());
+                            r = dst;
+                            rn = prev_n + cap[q];
+                        }
+                        if (j > K) continue;
+                        for (auto &e : devs) {
+                            if (e->pred != (int)q) continue;
+                            copy_d2d(ctx, e->cnt.p, x.dR.p + (j - 1), 1);
+                            dev_index_build(*e, r, rn, stp.p);
+                        }
+                    }
+                };
                 for (uint64_t j = 1; j <= K; ++j) {
+                    refresh(j);
                     for (uint32_t p = 0; p < n_preds; ++p) {
                         for (size_t t = 0; t < tmpl[p].size(); ++t) {
                             Var v = tmpl[p][t];
@@ -3176,6 +3306,7 @@ struct Driver {
                         }
                     }
                 }
+                refresh(K + 1);
                 Buf<uint64_t> g(ctx, K * P + K);
                 copy_d2d(ctx, g.p, cnt.p + P, K * P);
                 copy_d2d(ctx, g.p + K * P, ovf.p + 1, K);
@@ -3203,9 +3334,27 @@ struct Driver {
                         break;
                     }
                 }
-                if (done) break;
                 // the delta of the last complete step becomes the current one
                 const uint64_t last = j0 ? j0 - 1 : K;
+                if (trace_on())
+                    fprintf(stderr, "[xlog_hip] hash queue of %llu steps: %llu complete%s%s\n", (unsigned long long)K,
+                            (unsigned long long)(j0 ? j0 - 1 : (done ? j : K)), j0 ? ", one overflowed" : "",
+                            done ? ", converged" : "");
+                // an indexed predicate's R after that step (R_0: full as it was); at convergence R_K, which
+                // the steps after the empty one left unchanged
+                for (uint32_t q = 0; q < n_preds; ++q) {
+                    if (!qrel[q] || last == 0) continue;
+                    uint64_t rn = full[q].n;
+                    for (uint64_t t = 1; t <= last; ++t) rn += hc[(t - 1) * P + q];
+                    DRel m;
+                    m.n = rn;
+                    m.k = qrel[q]->RB[last % 2].release();
+                    m.owned = true;
+                    m.version = version_counter++;
+                    release(full[q]);
+                    full[q] = m;
+                }
+                if (done) break;
                 for (uint32_t p = 0; p < n_preds; ++p) {
                     if (!idb[p]) continue;
                     if (last) dn[p] = hc[(last - 1) * P + p];
