@@ -2923,14 +2923,14 @@ struct Driver {
     // a head's launches insert are its next delta: new against R and unique,
     // with no sort, merge-diff or candidate bag.  Pass 0 is the seed (every
     // rule once, its first path atom reading its whole relation: the tuples it
-    // inserts are T(R) minus R, run()'s seed).  A predicate that some variant
-    // reads in full (an IDB atom besides the delta atom) is sorted into its
-    // full relation after every pass, for the indexes, and every iteration
-    // reads back its sizes.  Programs with no such predicate (linear ones:
-    // every variant reads only EDB relations besides its delta) queue up to
-    // XLOG_HIP_HASH_QUEUE (8) iterations per read-back: each launch reads its
-    // delta's row count on the device, and a step that overflows makes the
-    // later queued steps do nothing and is rerun with the host's sizes.  The
+    // inserts are T(R) minus R, run()'s seed).  Up to XLOG_HIP_HASH_QUEUE (8)
+    // iterations are queued per read-back: each launch reads its delta's row
+    // count on the device, and a step that overflows makes the later queued
+    // steps do nothing and is rerun with the host's sizes.  A predicate that
+    // some variant reads in full (an IDB atom besides the delta atom) is kept
+    // sorted in its full relation for the indexes: a synchronous pass merges
+    // its appends, and before each queued step the appends of the step before
+    // are sorted and merged and the indexes rebuilt on the device.  The
     // others are collected from their set at the end.
     uint64_t run_hash(uint64_t max_iter, std::vector<uint64_t> &deltas, const std::vector<ChainRule> &chains) {
         XH_REQUIRE(chains.size() == rules.size(), XLOG_HIP_INVALID_ARG, "hash route: one path per rule");
