@@ -12,7 +12,15 @@
 // below 8*chunk the same model must be able to deadlock, which shows the
 // watchdog detects it.
 //
-// usage: sort_schedule_sim <trials> <watchdog_seconds> <mode: ok|tight|shuffled>
+// The mode may also name "index": a block runs the tile of its workgroup index
+// (the kernel's default order) instead of its start ticket, and "fallback": the
+// look-back's bounded wait (k_onesweep's spin_limit, here 2 failed polls), after
+// which the waiting tile counts its unpublished predecessor itself (here: takes
+// that tile's count) and walks on.  With the fallback, index order in a
+// shuffled dispatch with too few slots must never stall and still give exact
+// prefixes; without it the same schedule can stall.
+//
+// usage: sort_schedule_sim <trials> <watchdog_seconds> <mode: ok|tight|shuffled, with index / fallback>
 // prints "runs R failures F hangs H"
 #include <atomic>
 #include <chrono>
@@ -35,6 +43,7 @@ struct Run {
     std::vector<std::atomic<int>> done;
     std::vector<uint32_t> cnt, prefix;
     std::atomic<bool> abort{false};
+    int spin_limit = -1;  // >= 0: the bounded wait
     Run(uint32_t t, uint32_t c) : tiles(t), chunk(c), status(t), done(t), cnt(t), prefix(t) {
         for (uint32_t i = 0; i < t; ++i) {
             status[i] = 0;
@@ -55,6 +64,7 @@ struct Run {
         if (t > 0) {
             int64_t j = (int64_t)t - 1;
             bool fin = false;
+            int spins = 0;
             while (!fin) {
                 if (abort) return;
                 uint32_t st[4];
@@ -71,7 +81,16 @@ struct Run {
                     }
                 }
                 j -= used;
-                if (!used) std::this_thread::yield();
+                if (used) {
+                    spins = 0;
+                } else if (spin_limit >= 0 && ++spins > spin_limit) {  // count tile j here
+                    p += cnt[j];
+                    j -= 1;
+                    spins = 0;
+                    fin = j < 0;
+                } else {
+                    std::this_thread::yield();
+                }
             }
             status[t].store(ST_INC | (p + cnt[t]));
         }
@@ -83,8 +102,11 @@ struct Run {
 int main(int argc, char **argv) {
     const int trials = argc > 1 ? atoi(argv[1]) : 40;
     const int watchdog = argc > 2 ? atoi(argv[2]) : 10;
-    const bool tight = argc > 3 && strcmp(argv[3], "tight") == 0;
-    const bool shuffled = argc > 3 && strcmp(argv[3], "shuffled") == 0;
+    const char *mode = argc > 3 ? argv[3] : "ok";
+    const bool tight = strstr(mode, "tight") != nullptr;
+    const bool shuffled = strstr(mode, "shuffled") != nullptr;
+    const bool by_index = strstr(mode, "index") != nullptr;
+    const bool fallback = strstr(mode, "fallback") != nullptr;
     std::mt19937 rng(2024);
     int runs = 0, failures = 0, hangs = 0;
     for (int trial = 0; trial < trials; ++trial) {
@@ -102,6 +124,7 @@ int main(int argc, char **argv) {
         const uint32_t nchunks = (tiles + chunk - 1) / chunk;
         const uint32_t grid = 8 * ((nchunks + 7) / 8) * chunk;
         Run r(tiles, chunk);
+        if (fallback) r.spin_limit = 2;
         std::vector<uint32_t> order(grid);  // dispatch order of the block indices
         for (uint32_t b = 0; b < grid; ++b) order[b] = b;
         if (shuffled) std::shuffle(order.begin(), order.end(), rng);
@@ -126,7 +149,8 @@ int main(int argc, char **argv) {
             lk.unlock();
             th.emplace_back([&, b] {
                 std::mt19937 lr(order[b] * 31u + (uint32_t)trial);
-                const uint32_t t = r.tile_of(ticket.fetch_add(1));  // the kernel's start-order ticket
+                // the kernel's start-order ticket, or the block's own index
+                const uint32_t t = r.tile_of(by_index ? order[b] : ticket.fetch_add(1));
                 if (t != NONE) r.process(t, lr);
                 std::lock_guard<std::mutex> g(mu);
                 --running;

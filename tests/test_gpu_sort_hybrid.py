@@ -111,6 +111,18 @@ def test_skewed_high_word_keeps_digit_passes(provider, monkeypatch):
     _check(provider, keys, monkeypatch, want_runs=0, want_passes=8)
 
 
+def test_lookback_fallback(provider, monkeypatch):
+    """XLOG_HIP_SORT_SPIN=2: a look-back wait of a digit pass on a tile still unpublished after two polls
+    counts that tile's keys itself; the result is the same."""
+    n = N_MIN + 4321
+    keys = datagen.dup_tuples(n, 12)
+    _note("hybrid sort: look-back fallback")
+    monkeypatch.setenv("XLOG_HIP_SORT_SPIN", "2")
+    got, runs, passes = _dedup_with_route(provider, keys)
+    assert (runs, passes) == (1, 4)
+    assert np.array_equal(got, oracle.sort_dedup(keys))
+
+
 def test_index_order(provider, monkeypatch):
     """XLOG_HIP_SORT_TICKETS=0: the radix passes and the short-run unique take their tiles in workgroup-index
     order (the default numbers them by start tickets, as every other test here runs)."""

@@ -1,12 +1,12 @@
 """GPU parity of the radix sort at every tile-order chunk size.
 
-By default the digit passes number their tiles by start tickets; with
-XLOG_HIP_SORT_TICKETS=0 (which the tests of this module take, except
-test_tile_orders, which runs both orders) they deal tiles to the XCDs in chunks
-of consecutive tiles by workgroup index (xlog_amd/csrc/sort.hip, chunk_tile): 8
-tiles per chunk from 512 tiles up, and tiles / 64 below that, so sorts of
-64-511 tiles run with chunks of 1..7 and a last group of blocks partly without
-a tile.  Keys-only sorts use 8192-key tiles;
+The digit passes deal tiles to the XCDs in chunks of consecutive tiles by
+workgroup index (xlog_amd/csrc/sort.hip, chunk_tile): 8 tiles per chunk from
+512 tiles up, and tiles / 64 below that, so sorts of 64-511 tiles run with
+chunks of 1..7 and a last group of blocks partly without a tile.  The tests of
+this module take XLOG_HIP_SORT_TICKETS=0 (the fused short-run unique by
+workgroup index too), except test_tile_orders, which runs every order and the
+look-back's counting fallback.  Keys-only sorts use 8192-key tiles;
 sorts that carry a row payload (the keyed sort of arity-3/4 rows, join index
 builds) use 4096-key tiles.  Every size here is checked against numpy: the full
 sort + dedup, a stable sort on one key column, and narrow keys whose constant
@@ -129,16 +129,24 @@ def test_stable_sort_column_with_constant_low_byte(provider, n):
     assert np.array_equal(got, pack(c0[order], c1[order]))
 
 
-@pytest.mark.parametrize("order", ["ticket", "index"])
+@pytest.mark.parametrize("order", ["default", "ticket", "index", "fallback"])
 @pytest.mark.parametrize("tiles", [1, 64, 260, 700, 2100])
 def test_tile_orders(provider, monkeypatch, tiles, order):
-    # the default numbers tiles by start-order tickets (no in-order dispatch or co-residency assumed);
-    # XLOG_HIP_SORT_TICKETS=0 takes the workgroup-index order with XCD chunks
+    # default: digit passes by workgroup index in XCD chunks with the bounded look-back wait, the fused
+    # short-run unique by start tickets; XLOG_HIP_SORT_TICKETS=1 tickets for both, =0 workgroup index for
+    # both; fallback: XLOG_HIP_SORT_SPIN=0 (up to 64 tiles: every wait on an unpublished tile counts that
+    # tile's keys instead of polling again) or 2 (after two polls; a digit thread reads a whole tile per
+    # count, so this mode is kept to a few hundred tiles)
     p = provider
-    if order == "index":
+    monkeypatch.delenv("XLOG_HIP_SORT_TICKETS", raising=False)
+    if order == "ticket":
+        monkeypatch.setenv("XLOG_HIP_SORT_TICKETS", "1")
+    elif order == "index":
         monkeypatch.setenv("XLOG_HIP_SORT_TICKETS", "0")
-    else:
-        monkeypatch.delenv("XLOG_HIP_SORT_TICKETS", raising=False)
+    elif order == "fallback":
+        if tiles > 260:
+            pytest.skip("the counting fallback reads whole tiles per wait: a few hundred tiles at most")
+        monkeypatch.setenv("XLOG_HIP_SORT_SPIN", "0" if tiles <= 64 else "2")
     n = tiles * TILE_K - (tiles * 53) % 3000
     _note(f"sort tile order {order}: tiles={tiles} n={n}")
     rng = np.random.default_rng(1000 + tiles)

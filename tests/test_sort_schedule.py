@@ -1,6 +1,7 @@
 """CPU check of the radix pass's tile order (xlog_amd/csrc/sort.hip, chunk_tile and
 radix_sort_u64's grid): a threaded model of workgroup dispatch (in index order and
-shuffled) with the kernel's start-order tickets, tile formula and decoupled look-back
+shuffled) with the kernel's start-order tickets or workgroup-index tiles, its tile
+formula and decoupled look-back, with and without the look-back's bounded wait
 (tests/sim/sort_schedule_sim.cpp).
 
 With room for at least 8 * chunk blocks at once (the condition the host sizes
@@ -42,4 +43,19 @@ def test_tile_order_never_stalls_under_any_dispatch_order(sim):
 
 def test_tile_order_can_stall_below_the_condition(sim):
     res, out = _run(sim, 3, 1, "tight")
+    assert res["failures"] == 0 and res["hangs"] >= 1, out
+
+
+def test_index_order_with_bounded_wait_never_stalls(sim):
+    # the default order of the digit passes: workgroup index, shuffled dispatch, too few slots for a chunk
+    # group; the bounded wait counts an unpublished predecessor itself, so every run ends with exact prefixes
+    res, out = _run(sim, 40, 60, "tight-shuffled-index-fallback")
+    assert res == {"runs": 40, "failures": 0, "hangs": 0}, out
+    res, out = _run(sim, 60, 60, "shuffled-index-fallback")
+    assert res == {"runs": 60, "failures": 0, "hangs": 0}, out
+
+
+def test_index_order_without_the_bound_can_stall(sim):
+    # the same schedule with an unbounded wait
+    res, out = _run(sim, 3, 1, "tight-shuffled-index")
     assert res["failures"] == 0 and res["hangs"] >= 1, out

@@ -205,12 +205,30 @@ __device__ __forceinline__ uint32_t chunk_tile(uint32_t b, uint32_t chunk, uint3
     return t < tiles ? (uint32_t)t : TILE_NONE;
 }
 
+// The keys of tile j with digit d: the count tile j publishes, computed by a
+// waiting tile instead (the bounded wait of the look-back, below).
+__device__ uint32_t tile_digit_count(const uint64_t *__restrict__ kin, uint64_t n, uint64_t j, uint64_t tile_keys,
+                                     int shift, uint32_t d) {
+    const uint64_t a = j * tile_keys, b = a + tile_keys < n ? a + tile_keys : n;
+    uint32_t c = 0;
+    for (uint64_t i = a; i < b; ++i) c += (((uint32_t)(kin[i] >> shift) & 255u) == d) ? 1u : 0u;
+    return c;
+}
+
+// The look-back's wait is bounded: a digit thread that finds the tile before
+// the ones it has consumed unpublished for spin_limit polls in a row counts
+// that tile's keys of its digit itself (they are in kin before the pass
+// starts) and walks on.  Its prefix is the one the tile would have published,
+// so the pass needs no assumption on dispatch order or residency: a tile
+// whose predecessor's block has not started (out-of-order dispatch, or fewer
+// co-resident blocks than a chunk group) only costs the waiting tile a read
+// of that predecessor, and under in-order dispatch the bound is never reached.
 template <bool HAS_VAL, int BLOCK, int ITEMS>
 __global__ __launch_bounds__(BLOCK) void k_onesweep(
     const uint64_t *__restrict__ kin, uint64_t *__restrict__ kout, const uint32_t *__restrict__ vin,
     uint32_t *__restrict__ vout, uint64_t n, uint32_t tiles, int shift, const uint32_t *__restrict__ digit_off,
     uint32_t *status, uint32_t *status_next, uint32_t chunk, unsigned long long *ticket,
-    unsigned long long ticket_base, const uint64_t *d_n, const uint32_t *stop) {
+    unsigned long long ticket_base, const uint64_t *d_n, const uint32_t *stop, uint32_t spin_limit) {
     __shared__ uint32_t s_wcnt[(BLOCK / WAVE)][256];
     __shared__ uint32_t s_ticket;
     __shared__ uint32_t s_gbase[256];
@@ -376,6 +394,7 @@ __global__ __launch_bounds__(BLOCK) void k_onesweep(
             if (tile > 0) {
                 int64_t j = (int64_t)tile - 1;
                 bool done = false;
+                uint32_t spins = 0;
                 while (!done) {
                     uint32_t st[SORT_LOOKBACK];
 #pragma unroll
@@ -399,6 +418,14 @@ __global__ __launch_bounds__(BLOCK) void k_onesweep(
 #pragma unroll
                     for (int z = 0; z < SORT_LOOKBACK; ++z) prefix += z < used ? (st[z] & ST_VAL) : 0u;
                     j -= used;
+                    if (used > 0) {
+                        spins = 0;
+                    } else if (++spins > spin_limit) {  // tile j has not published: count it here
+                        prefix += tile_digit_count(kin, n, (uint64_t)j, (uint64_t)(BLOCK * ITEMS), shift, (uint32_t)d);
+                        j -= 1;
+                        spins = 0;
+                        done = j < 0;
+                    }
                 }
                 st_status(my, ST_INC | (prefix + cnt));
             }
@@ -569,15 +596,24 @@ static uint32_t pass_capacity(Ctx *ctx) {
     return (uint32_t)ctx->num_cus * (uint32_t)b;
 }
 
-// Tiles by start ticket (the default): a block takes its tile from an atomic
-// counter when it starts, so a tile waits only on tiles whose blocks have
-// started, whatever the dispatch order and however few blocks are resident
-// (a GPU shared with other streams).  XLOG_HIP_SORT_TICKETS=0 restores the
-// workgroup-index order with XCD chunks, faster and correct under in-order
-// dispatch with 8 x chunk blocks co-resident (chunk_tile).
-bool sort_tickets() {
+// Tile order.  The digit passes take tiles by workgroup index in XCD chunks
+// (chunk_tile) with the bounded look-back wait of k_onesweep, which keeps them
+// correct whatever the dispatch order; XLOG_HIP_SORT_TICKETS=1 numbers their
+// tiles by start tickets instead (plain order, 9-11 % slower per pass).  The
+// fused short-run unique has no such fallback and takes start tickets unless
+// XLOG_HIP_SORT_TICKETS=0 (workgroup-index order: correct only when the
+// workgroups of a launch start in index order).
+static int sort_tickets_env() {
     const char *e = getenv("XLOG_HIP_SORT_TICKETS");
-    return !(e && e[0] == '0');
+    return e && (e[0] == '0' || e[0] == '1') ? e[0] - '0' : -1;
+}
+bool sort_tickets() { return sort_tickets_env() != 0; }
+static bool pass_tickets() { return sort_tickets_env() == 1; }
+// polls of an unpublished predecessor before a digit thread counts it itself
+// (XLOG_HIP_SORT_SPIN; the tests set 0 to take the fallback at every wait)
+static uint32_t sort_spin_limit() {
+    const char *e = getenv("XLOG_HIP_SORT_SPIN");
+    return e && *e ? (uint32_t)strtoul(e, nullptr, 10) : 4096u;
 }
 static bool sort_persist() {
     const char *e = getenv("XLOG_HIP_SORT_PERSIST");
@@ -690,7 +726,7 @@ int radix_sort_dev(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint64_t n_bo
         add_work_rows(ctx, prof.work(16.0), d_n, n_bound, 1, nullptr, 0, 0, nullptr, stop);
         hipLaunchKernelGGL((k_onesweep<false, SORT_BLOCK_K, SORT_ITEMS_K>), dim3(grid), dim3(SORT_BLOCK_K), 0,
                            ctx->stream, *keys, *keys_alt, nullptr, nullptr, n_bound, (uint32_t)tiles, 8 * dgt,
-                           off + dgt * 256, st.status[cur], st.status[nxt], 1u, tk, 0ull, d_n, stop);
+                           off + dgt * 256, st.status[cur], st.status[nxt], 1u, tk, 0ull, d_n, stop, sort_spin_limit());
         XH_CHECK_HIP(hipGetLastError());
         std::swap(*keys, *keys_alt);
         cur = nxt;
@@ -756,7 +792,7 @@ int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **va
             st.dirty[cur] = 0;
         }
         Prof prof(ctx, XLOG_HIP_KERNEL_SORT_PASS, (has_val ? 24.0 : 16.0) * (double)n);
-        unsigned long long *tk = sort_tickets() ? ctx->tickets + 2 : nullptr;
+        unsigned long long *tk = pass_tickets() ? ctx->tickets + 2 : nullptr;
         unsigned long long tb = tk ? ctx->take_tickets(2, grid) : 0ull;
         // tickets go to tiles in plain order (chunk 1: chunk_tile is then the identity), which measured
         // faster than tickets dealt to XCD chunks
@@ -776,12 +812,13 @@ int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **va
         if (has_val)
             hipLaunchKernelGGL((k_onesweep<true, SORT_BLOCK_V, SORT_ITEMS_V>), dim3(pgrid), dim3(SORT_BLOCK_V), 0,
                                ctx->stream, *keys, *keys_alt, *vals, *vals_alt, n, (uint32_t)tiles, 8 * dgt,
-                               off + dgt * 256, st.status[cur], st.status[nxt], pchunk, tk, tb, pn, nullptr);
+                               off + dgt * 256, st.status[cur], st.status[nxt], pchunk, tk, tb, pn, nullptr,
+                               sort_spin_limit());
         else
             hipLaunchKernelGGL((k_onesweep<false, SORT_BLOCK_K, SORT_ITEMS_K>), dim3(pgrid), dim3(SORT_BLOCK_K), 0,
                                ctx->stream, (passes == 0 && src) ? src : *keys, *keys_alt, nullptr, nullptr, n,
                                (uint32_t)tiles, 8 * dgt, off + dgt * 256, st.status[cur], st.status[nxt], pchunk,
-                               tk, tb, pn, nullptr);
+                               tk, tb, pn, nullptr, sort_spin_limit());
         XH_CHECK_HIP(hipGetLastError());
         st.dirty[cur] = tiles;
         if (st.dirty[nxt] <= tiles) st.dirty[nxt] = 0;
