@@ -3,8 +3,12 @@ pins against boolean-matrix closed forms): an atom whose two variables are
 both bound when it is joined is a join on both keys in the reference's
 left-deep lowering (crates/xlog-logic/src/lower.rs build_join_tree /
 compute_join_keys), here a filter step of the join route (a lookup of the row
-in the atom's index on its first column).  Such bodies are not paths, so AUTO
-takes the join route and the bitmap and hash routes decline them."""
+in the atom's index on its first column).  A triangle-shaped body whose head
+drops one variable is evaluated by the generic join instead when that reads
+less (each row of the atom over the head's variables intersects two sorted
+runs; XLOG_HIP_WCOJ=1 / =0 forces it / the left-deep plan): both must give the
+oracle's result.  Such bodies are not paths, so AUTO takes the join route and
+the bitmap and hash routes decline them."""
 import sys
 
 import numpy as np
@@ -35,6 +39,13 @@ def _run(p, plan, rels, route, **kw):
     return p.fixpoint(plan, dev, route=route, **kw)
 
 
+def _wcoj(monkeypatch, mode):
+    if mode == "default":
+        monkeypatch.delenv("XLOG_HIP_WCOJ", raising=False)
+    else:
+        monkeypatch.setenv("XLOG_HIP_WCOJ", mode)
+
+
 def _parity(p, name, plan, rels, idb):
     outs_o, it_o, deltas_o = oracle.seminaive(plan, rels)
     for route in (ROUTE_AUTO, ROUTE_JOIN):
@@ -50,15 +61,19 @@ def _parity(p, name, plan, rels, idb):
     return outs_o
 
 
+@pytest.mark.parametrize("wcoj", ["default", "0", "1"])
 @pytest.mark.parametrize("n,m,seed", [(200, 1500, 41), (2000, 30000, 42)])
-def test_triangle_closure(provider, n, m, seed):
+def test_triangle_closure(provider, monkeypatch, n, m, seed, wcoj):
+    _wcoj(monkeypatch, wcoj)
     s, d = _graph(n, m, seed)
     outs = _parity(provider, "triangle closure", cp.triangle_closure_plan(), [pack(s, d), None], [1])
     assert len(outs[1]) > len(set(zip(s.tolist(), d.tolist())))  # the closing atom derives rows
 
 
+@pytest.mark.parametrize("wcoj", ["default", "0", "1"])
 @pytest.mark.parametrize("n,m,seed", [(300, 4000, 43), (3000, 60000, 44)])
-def test_triangles(provider, n, m, seed):
+def test_triangles(provider, monkeypatch, n, m, seed, wcoj):
+    _wcoj(monkeypatch, wcoj)
     s, d = _graph(n, m, seed)
     outs = _parity(provider, "triangles", cp.triangles_plan(), [pack(s, d), None], [1])
     assert len(outs[1]) > 0
@@ -99,3 +114,62 @@ def test_sparse_ids_and_edges(provider):
             _run(provider, cp.triangle_closure_plan(), [pack(s, d), None], route)
         assert ex.value.status == UNSUPPORTED
         del ex
+
+
+def _brute_triangle(plan, n, s, d):
+    """The single rule of `plan` (three atoms over variables 0..2 of relation 0, head two of them) by brute
+    force over an n x n x n boolean tensor."""
+    head, hv0, hv1, nb = plan[1], plan[2], plan[3], plan[4]
+    E = np.zeros((n, n), dtype=bool)
+    E[s.astype(np.int64), d.astype(np.int64)] = True
+    T = np.ones((n, n, n), dtype=bool)
+    for j in range(nb):
+        _, a, b = plan[5 + 3 * j: 8 + 3 * j]
+        shape = [1, 1, 1]
+        shape[a], shape[b] = n, n
+        M = E if a < b else E.T  # M[i, k] indexed by (min axis, max axis)
+        T &= M.reshape(shape)
+    (w,) = {0, 1, 2} - {hv0, hv1}
+    R = T.any(axis=w)  # axes in increasing order of the remaining variables
+    if hv0 > hv1:
+        R = R.T
+    x, z = np.nonzero(R)
+    return np.sort(pack(x.astype(np.uint32), z.astype(np.uint32)))
+
+
+@pytest.mark.parametrize("wcoj", ["default", "0", "1"])
+def test_triangle_orientations(provider, monkeypatch, wcoj):
+    """Triangle bodies with their atoms in every column orientation and body order (the generic join's index
+    columns and the closing atom's word order follow the atoms), heads over each pair of variables, on a
+    graph with a hub, checked against brute force.  One of them has no left-deep plan (after its first
+    join three variables are live): the generic join is its only evaluation, and with it forced off
+    (XLOG_HIP_WCOJ=0) it is UNSUPPORTED."""
+    _wcoj(monkeypatch, wcoj)
+    X, Y, Z = 0, 1, 2
+    n = 400
+    s, d = _graph(n, 5000, 52)
+    hub = np.arange(1, n, dtype=np.uint32)
+    s = np.concatenate([s, np.zeros(n - 1, np.uint32), hub])
+    d = np.concatenate([d, hub, np.zeros(n - 1, np.uint32)])
+    e = pack(s, d)
+    plans = [
+        ([1, 1, X, Z, 3, 0, Y, X, 0, Z, Y, 0, X, Z], True),   # tri(X,Z) :- e(Y,X), e(Z,Y), e(X,Z)
+        ([1, 1, Z, X, 3, 0, X, Y, 0, Y, Z, 0, Z, X], True),   # the head reversed
+        ([1, 1, X, Y, 3, 0, Z, X, 0, X, Y, 0, Y, Z], False),  # the head drops Z: no left-deep plan
+        ([1, 1, Y, Z, 3, 0, X, Y, 0, Z, X, 0, Y, Z], True),   # the head drops X
+    ]
+    for k, (plan, left_deep) in enumerate(plans):
+        _note(f"triangle orientation {k} wcoj={wcoj}")
+        want = _brute_triangle(plan, n, s, d)
+        if wcoj == "0" and not left_deep:
+            with pytest.raises(XlogError) as ex:
+                _run(provider, plan, [e, None], ROUTE_JOIN)
+            assert ex.value.status == UNSUPPORTED
+            del ex
+            continue
+        outs, st = _run(provider, plan, [e, None], ROUTE_AUTO)
+        assert st["route"] == ROUTE_JOIN
+        assert np.array_equal(provider.download_packed(outs[1]), want), k
+        assert st["iterations"] == 1 and st["delta_sizes"] == [len(want), 0]
+    ss, sd = datagen.sparse_ids(s), datagen.sparse_ids(d)
+    _parity(provider, "sparse triangles", cp.triangles_plan(), [pack(ss, sd), None], [1])

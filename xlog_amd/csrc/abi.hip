@@ -232,6 +232,10 @@ void join_match_flags(Ctx *ctx, const uint64_t *probe, uint64_t n, int pcol, con
 // indexed relation (an index on its first column, payloads ascending per run)
 void join_match2_flags(Ctx *ctx, const uint64_t *probe, uint64_t n, int pcol, const RunIndex &ix,
                        const uint32_t *payload, uint8_t *flags);
+// flags[i] = 1 when mask row i, (u, v) (or (v, u) with mask_swap), has a w in both
+// the run of u in P and the run of v in Q (payloads ascending per run)
+void wcoj_triangle_flags(Ctx *ctx, const uint64_t *mask, uint64_t n, int mask_swap, const RunIndex &P,
+                         const uint32_t *p_payload, const RunIndex &Q, const uint32_t *q_payload, uint8_t *flags);
 
 #define LAUNCH_1D(kern, n, ...)                                                                             \
     do {                                                                                                    \
@@ -1937,6 +1941,20 @@ struct Driver {
         cache[key] = std::move(J);
         return ref;
     }
+    // An index whose payloads ascend inside each run: index_of's on the first
+    // column (the rows are sorted), a second-column index with its payloads
+    // sorted otherwise (cached apart from index_of's)
+    const JoinIndex &sorted_index_of(const DRel &rel, int col) {
+        if (col == 0) return index_of(rel, 0);
+        CacheKey key{rel.k, 2 + col, rel.version};
+        auto it = cache.find(key);
+        if (it != cache.end()) return *it->second;
+        std::unique_ptr<JoinIndex> J(new JoinIndex());
+        build_join_index(ctx, rel.k, rel.n, 2, col, true, *J, true);
+        auto &ref = *J;
+        cache[key] = std::move(J);
+        return ref;
+    }
     void drop_index(const DRel &rel) {
         for (auto it = cache.begin(); it != cache.end();)
             if (it->first.k == rel.k) it = cache.erase(it); else ++it;
@@ -2007,8 +2025,111 @@ struct Driver {
     std::vector<std::array<uint64_t, 2>> dlast;
     void note_delta(uint32_t p, uint64_t n) { dlast[p] = {dlast[p][1], n}; }
 
+    // A triangle-shaped body: three atoms over three variables, every pair of
+    // variables in one atom, the head two of them (u, v).  M is the atom over
+    // (u, v), P the one over (u, w), Q the one over (w, v), where w is the
+    // variable the head drops.  Its tuples are the rows (u, v) of M for which
+    // some w is in both u's run of P and v's run of Q: a worst-case-optimal
+    // (generic-join) evaluation, variable order u, v, w, that never writes the
+    // pairs of the left-deep plan's first join (the reference promotes such
+    // bodies to Free Join, promote.rs:1590-1640; its binary fallback is the
+    // left-deep plan, whose result is the same set).
+    struct Triangle {
+        int m = -1, p = -1, q = -1;
+        int mask_swap = 0;  // M's rows are (v, u)
+        int pcol = 0, qcol = 0;  // the column of u in P and of v in Q
+    };
+    static bool triangle_shape(const Rule &r, Triangle &t) {
+        if (r.nb != 3 || r.hv[0] == r.hv[1]) return false;
+        int vs[6], nv = 0;
+        for (int j = 0; j < 3; ++j) {
+            if (r.b[j].v[0] == r.b[j].v[1]) return false;
+            for (int c = 0; c < 2; ++c) {
+                bool seen = false;
+                for (int k = 0; k < nv; ++k) seen = seen || vs[k] == r.b[j].v[c];
+                if (!seen) vs[nv++] = r.b[j].v[c];
+            }
+        }
+        if (nv != 3) return false;
+        const int u = r.hv[0], v = r.hv[1];
+        int w = -1;
+        bool hu = false, hvv = false;
+        for (int k = 0; k < 3; ++k) {
+            if (vs[k] == u) hu = true;
+            else if (vs[k] == v) hvv = true;
+            else w = vs[k];
+        }
+        if (!hu || !hvv || w < 0) return false;
+        auto over = [](const Atom &a, int x, int y) {
+            return (a.v[0] == x && a.v[1] == y) || (a.v[0] == y && a.v[1] == x);
+        };
+        for (int j = 0; j < 3; ++j) {
+            if (over(r.b[j], u, v)) t.m = j;
+            else if (over(r.b[j], u, w)) t.p = j;
+            else if (over(r.b[j], w, v)) t.q = j;
+        }
+        if (t.m < 0 || t.p < 0 || t.q < 0) return false;
+        t.mask_swap = r.b[t.m].v[0] != u;
+        t.pcol = r.b[t.p].v[0] == u ? 0 : 1;
+        t.qcol = r.b[t.q].v[0] == v ? 0 : 1;
+        return true;
+    }
+    // The generic join when it reads less than the left-deep plan's first join
+    // writes: M's rows (each a lookup and an intersection) against the rows of
+    // atom 0 times the average run of atom 1 on their shared column.
+    // XLOG_HIP_WCOJ=1 / =0 takes it always / never.
+    bool use_triangle(const Rule &r, const DRel *const *rel, const Triangle &t) {
+        const char *e = getenv("XLOG_HIP_WCOJ");
+        if (e && e[0] == '0') return false;
+        if (e && e[0] == '1') return true;
+        if (rel[0]->n == 0 || rel[1]->n == 0 || rel[t.m]->n == 0) return false;
+        int apos = -1;
+        for (int x = 0; x < 2 && apos < 0; ++x)
+            for (int y = 0; y < 2; ++y)
+                if (r.b[0].v[x] == r.b[1].v[y]) apos = y;
+        if (apos < 0) return false;
+        const JoinIndex &J = index_of(*rel[1], apos);
+        const double run = J.ix.nruns ? (double)J.n / (double)J.ix.nruns : 0.0;
+        return (double)rel[0]->n * run > 4.0 * (double)rel[t.m]->n;
+    }
+    void eval_triangle(const DRel *const *rel, const Triangle &t, Bags &out) {
+        const DRel &M = *rel[t.m], &P = *rel[t.p], &Q = *rel[t.q];
+        if (M.n == 0 || P.n == 0 || Q.n == 0) return;
+        const JoinIndex &JP = sorted_index_of(P, t.pcol);
+        const JoinIndex &JQ = sorted_index_of(Q, t.qcol);
+        Buf<uint8_t> flags(ctx, M.n);
+        wcoj_triangle_flags(ctx, M.k, M.n, t.mask_swap, JP.ix, JP.payload.p, JQ.ix, JQ.payload.p, flags.p);
+        Owned kept(ctx, alloc_keys(ctx, M.n));
+        Buf<uint64_t> cnt(ctx, 1);
+        select_flags(ctx, M.k, flags.p, M.n, kept.p, cnt.p);
+        ctx->read_scalars(cnt.p, 1);
+        const uint64_t n = ctx->host_scalars[0];
+        if (n == 0) return;
+        if (t.mask_swap) {  // the head's order, (u, v)
+            Owned o(ctx, alloc_keys(ctx, n));
+            swap_words(ctx, kept.p, n, o.p);
+            kept.reset(o.release());
+        }
+        out.add(kept, n, 0);
+    }
+
     // ri >= 0: record the join steps' sizes in obs[ri]
     void eval_body(const Rule &r, const DRel *const *rel, Bags &out, ProbeJob *pre, int ri = -1) {
+        Triangle tri;
+        if (triangle_shape(r, tri)) {
+            // a triangle whose left-deep plan would keep three variables has only this evaluation
+            bool left_deep = true;
+            try {
+                (void)plan_body(r);
+            } catch (const Error &) {
+                left_deep = false;
+            }
+            const char *e = getenv("XLOG_HIP_WCOJ");
+            if (!(e && e[0] == '0') && (!left_deep || use_triangle(r, rel, tri))) {
+                eval_triangle(rel, tri, out);
+                return;
+            }
+        }
         const BodyPlan bp = plan_body(r);
         const uint64_t *bk = rel[0]->k;
         uint64_t bn = rel[0]->n;

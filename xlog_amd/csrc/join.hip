@@ -577,6 +577,51 @@ __global__ void k_match2_flags(ProbeArgs a, uint8_t *__restrict__ flags) {
     }
 }
 
+// Triangle existence (wcoj_triangle_flags): row i of `mask` holds (u, v), or
+// (v, u) with mask_swap; it is kept when the run of u in P and the run of v in
+// Q share a payload value w.  Both runs' payloads ascend, so the shorter run's
+// values are searched in the longer one, each search starting where the last
+// ended (a value past the longer run's end ends the row).
+__global__ void k_wcoj_triangle(const uint64_t *__restrict__ mask, uint64_t n, int mask_swap,
+                                const unsigned long long *__restrict__ pt, uint64_t pmask, int pbits,
+                                const uint32_t *__restrict__ ppay, const unsigned long long *__restrict__ qt,
+                                uint64_t qmask, int qbits, const uint32_t *__restrict__ qpay,
+                                uint8_t *__restrict__ flags) {
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const uint64_t row = mask[i];
+        const uint32_t u = mask_swap ? (uint32_t)row : (uint32_t)(row >> 32);
+        const uint32_t v = mask_swap ? (uint32_t)(row >> 32) : (uint32_t)row;
+        uint64_t sp = 0, sq = 0;
+        uint32_t lp = 0, lq = 0;
+        bool found = false;
+        if (lookup_run(pt, pmask, pbits, u, &sp, &lp) && lookup_run(qt, qmask, qbits, v, &sq, &lq)) {
+            const uint32_t *a = ppay + sp, *b = qpay + sq;  // a: the shorter run
+            uint32_t la = lp, lb = lq;
+            if (la > lb) {
+                const uint32_t *t = a;
+                a = b;
+                b = t;
+                const uint32_t tl = la;
+                la = lb;
+                lb = tl;
+            }
+            uint32_t lo = 0;
+            for (uint32_t k = 0; k < la && !found; ++k) {
+                const uint32_t x = a[k];
+                uint32_t hi = lb;
+                while (lo < hi) {
+                    const uint32_t mid = lo + ((hi - lo) >> 1);
+                    if (b[mid] < x) lo = mid + 1; else hi = mid;
+                }
+                if (lo == lb) break;
+                found = b[lo] == x;
+            }
+        }
+        flags[i] = (uint8_t)found;
+    }
+}
+
 }  // namespace
 
 // Runs of the high word of sorted keys [0, n), n = *d_n when d_n is set
@@ -867,6 +912,14 @@ void join_match_flags(Ctx *ctx, const uint64_t *probe, uint64_t n, int pcol, con
     XH_CHECK_HIP(hipGetLastError());
 }
 
+void wcoj_triangle_flags(Ctx *ctx, const uint64_t *mask, uint64_t n, int mask_swap, const RunIndex &P,
+                         const uint32_t *p_payload, const RunIndex &Q, const uint32_t *q_payload, uint8_t *flags) {
+    if (n == 0) return;
+    hipLaunchKernelGGL(k_wcoj_triangle, dim3(grid_for(n, 256, 16384)), dim3(256), 0, ctx->stream, mask, n, mask_swap,
+                       P.table.p, P.table_mask, table_bits(P), p_payload, Q.table.p, Q.table_mask, table_bits(Q),
+                       q_payload, flags);
+    XH_CHECK_HIP(hipGetLastError());
+}
 void join_match2_flags(Ctx *ctx, const uint64_t *probe, uint64_t n, int pcol, const RunIndex &ix, const uint32_t *payload,
                        uint8_t *flags) {
     if (n == 0) return;
