@@ -1855,6 +1855,12 @@ __global__ void k_q_end(QEnd a, uint32_t *stop, uint32_t code) {
 // The rows of a queued iteration's index over an IDB relation read in full:
 // the base run's (known on the host) and the recent run's (on the device, at
 // most its bound).
+// A count that must not pass its bound (a buffer written up to the bound):
+// past it, the queue stops at this iteration.
+__global__ void k_q_cap(const uint64_t *d_n, uint64_t bound, uint32_t *stop, uint32_t code) {
+    if (*stop) return;
+    if (*d_n > bound) atomicCAS(stop, 0u, code);
+}
 __global__ void k_q_rows(uint64_t *out, uint64_t base, const uint64_t *d_recent, uint64_t recent_bound,
                          const uint32_t *stop) {
     if (*stop) return;
@@ -2758,6 +2764,22 @@ struct Driver {
         Buf<uint64_t> gscratch(ctx, 2 * (uint64_t)H);
         Buf<uint64_t> tcount(ctx, 1);  // the size of an empty base run
         fill_u64(ctx, tcount.p, 0ull, 1);
+        // a grouped head over a domain of at most 2^17 values takes the group bitmaps instead of the sort and
+        // the set difference (XLOG_HIP_GROUP_BITMAP=0: never): its groups' keys and starts
+        const char *gbe = getenv("XLOG_HIP_GROUP_BITMAP");
+        const bool gb_on = !(gbe && gbe[0] == '0') && domain && domain <= (1ull << 17);
+        std::vector<Buf<uint32_t>> gkey(H);
+        std::vector<Buf<uint64_t>> gstart(H);
+        std::vector<uint64_t> gbound(H, 0);
+        Buf<uint64_t> gcount(ctx, H);
+        for (uint32_t h = 0; h < H && gb_on; ++h) {
+            if (!grouped[h]) continue;
+            uint64_t mc = 0;
+            for (uint64_t k = 0; k < Q; ++k) mc = std::max(mc, Cb[k][h]);
+            gbound[h] = std::max<uint64_t>(std::min<uint64_t>(mc, domain), 1);
+            gkey[h] = Buf<uint32_t>(ctx, gbound[h]);
+            gstart[h] = Buf<uint64_t>(ctx, gbound[h]);
+        }
 
         // ---- the queue -------------------------------------------------------------
         cur_iter = it + 1;
@@ -2821,14 +2843,25 @@ struct Driver {
                 const int p = heads[h];
                 const uint64_t *d_cand = bk + base_off[h] + nvar[h];
                 uint64_t *ka = qh[h]->C.p, *kb = qh[h]->Calt.p;
+                const uint64_t *big = full[p].k ? full[p].k : qh[h]->R[1].p;
+                const uint64_t *rin = k == 0 ? small[p].k : qh[h]->R[(k - 1) & 1].p;
+                if (!rin) rin = qh[h]->R[1].p;  // an empty run read through its device count
+                if (gbound[h]) {
+                    // per group (one high word, its runs listed), the new values by two LDS bitmaps, then
+                    // the groups compacted in order; more groups than the domain stop the queue
+                    select_runs(ctx, ka, Cb[k][h], gkey[h].p, gstart[h].p, gcount.p + h, d_cand, stop, gbound[h]);
+                    hipLaunchKernelGGL(k_q_cap, dim3(1), dim3(1), 0, ctx->stream, gcount.p + h, gbound[h], stop, code);
+                    XH_CHECK_HIP(hipGetLastError());
+                    group_bitmap_diff_dev(ctx, ka, Cb[k][h], d_cand, gkey[h].p, gstart[h].p, gbound[h], gcount.p + h,
+                                          big, full[p].n, rin, Rb[k][h], pR + h, (uint32_t)domain, ~0ull, kb, stop);
+                    select_not_value(ctx, kb, Cb[k][h], ~0ull, qh[h]->D[k & 1].p, nD + h, d_cand, stop);
+                    continue;
+                }
                 // (groups: at most one per delta row read and per domain value)
                 if (grouped[h] && Cb[k][h] / group_bound(std::max<uint64_t>(Lb[k][gsrc[h]], 1)) <= SHORT_GROUP_ROWS)
                     ka = sort_grouped_dev(ctx, ka, kb, Cb[k][h], d_cand, digits, stop, gscratch.p + 2 * h);
                 else radix_sort_dev(ctx, &ka, &kb, Cb[k][h], d_cand, digits, stop);
                 // unique, not in the base run (its size is known) and not in the recent run
-                const uint64_t *big = full[p].k ? full[p].k : qh[h]->R[1].p;
-                const uint64_t *rin = k == 0 ? small[p].k : qh[h]->R[(k - 1) & 1].p;
-                if (!rin) rin = qh[h]->R[1].p;  // an empty run read through its device count
                 select_unique_diff2_dev(ctx, ka, Cb[k][h], d_cand, big, std::max<uint64_t>(full[p].n, 1),
                                         full[p].n ? nullptr : tcount.p, rin, std::max<uint64_t>(Rb[k][h], 1), pR + h,
                                         qh[h]->D[k & 1].p, nD + h, stop);

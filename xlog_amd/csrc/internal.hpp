@@ -390,7 +390,21 @@ void select_unique_diff2_dev(Ctx *ctx, const uint64_t *k, uint64_t n, const uint
 void select_flags(Ctx *ctx, const uint64_t *k, const uint8_t *flags, uint64_t n, uint64_t *out,
                   uint64_t *d_count);
 //   not_value:   keep k[i] if k[i] != v
-void select_not_value(Ctx *ctx, const uint64_t *k, uint64_t n, uint64_t v, uint64_t *out, uint64_t *d_count);
+void select_not_value(Ctx *ctx, const uint64_t *k, uint64_t n, uint64_t v, uint64_t *out, uint64_t *d_count,
+                      const uint64_t *d_n = nullptr, const uint32_t *stop = nullptr);
+// Sorted unique difference of grouped candidates over a domain of at most
+// 2^17 values (every low word below `domain`): the candidates (count
+// *d_cand <= cand_bound) come in groups of one high word, listed by
+// select_runs (*d_nruns <= runs_bound); R is a sorted base run of nbase rows
+// and a sorted recent run (*d_nrecent <= recent_bound).  Each group's values
+// that are not in R go, ascending, to slots from the group's first position,
+// the rest of its positions get `hole`; compacting the slots
+// (select_not_value) gives the sorted new rows.
+void group_bitmap_diff_dev(Ctx *ctx, const uint64_t *cand, uint64_t cand_bound, const uint64_t *d_cand,
+                           const uint32_t *run_key, const uint64_t *run_start, uint64_t runs_bound,
+                           const uint64_t *d_nruns, const uint64_t *base, uint64_t nbase, const uint64_t *recent,
+                           uint64_t recent_bound, const uint64_t *d_nrecent, uint32_t domain, uint64_t hole,
+                           uint64_t *slots, const uint32_t *stop);
 
 // In-place exclusive scan of u32 values (prefixes wrap modulo 2^32); the
 // exact u64 sum goes to *d_total (device).  One pass, decoupled look-back.
@@ -644,8 +658,10 @@ inline unsigned grid_for(uint64_t n, unsigned block, unsigned cap) {
     return (unsigned)g;
 }
 void fill_u32(Ctx *ctx, uint32_t *p, uint32_t v, uint64_t n);
+// (cap: runs past it are counted in *d_count but not written)
 void select_runs(Ctx *ctx, const uint64_t *k, uint64_t n, uint32_t *run_key, uint64_t *run_start,
-                 uint64_t *d_count, const uint64_t *d_n = nullptr);
+                 uint64_t *d_count, const uint64_t *d_n = nullptr, const uint32_t *stop = nullptr,
+                 uint64_t cap = ~0ull);
 // Keys sorted by their high word: rows sharing it with a neighbour (key,
 // position), then among those the group heads (key; gsel[position] = group
 // number; hpos, when set, receives each head's position).

@@ -514,6 +514,93 @@ struct SelNotValue {
     __device__ void emit(uint64_t pos, uint64_t, uint64_t key) const { out[pos] = key; }
 };
 
+// Grouped candidates over a small value domain (every low word below
+// 32 * words), each group one run of equal high word x (select_runs): a block
+// marks the group's low words in an LDS bitmap and x's rows of R (a base run of
+// known size and a recent run counted on the device; found by four wave
+// searches) in a second one, and writes the values set in the first and not in
+// the second, ascending, from the group's first position; the group's other
+// positions get `hole`.  Every group is unique and sorted and has none of R's
+// rows; compacted (select_not_value), the groups give the sorted delta.
+constexpr int GB_BLOCK = 512;
+__global__ __launch_bounds__(GB_BLOCK) void k_group_bitmap_diff(
+    const uint64_t *__restrict__ cand, const uint64_t *d_cand, uint64_t cand_bound,
+    const uint32_t *__restrict__ run_key, const uint64_t *__restrict__ run_start, const uint64_t *d_nruns,
+    uint64_t runs_bound, const uint64_t *__restrict__ base, uint64_t nbase, const uint64_t *__restrict__ recent,
+    const uint64_t *d_nrecent, uint64_t recent_bound, uint32_t words, uint64_t hole, uint64_t *__restrict__ slots,
+    const uint32_t *stop) {
+    extern __shared__ uint32_t gb_bits[];  // [0, words): the group's values, [words, 2 words): R's
+    __shared__ uint64_t s_rng[4];
+    __shared__ uint32_t s_wsum[GB_BLOCK / WAVE];
+    if (stop && *stop) return;
+    const uint64_t n = *d_cand < cand_bound ? *d_cand : cand_bound;
+    const uint64_t nruns = *d_nruns < runs_bound ? *d_nruns : runs_bound;
+    const uint64_t nrec = *d_nrecent < recent_bound ? *d_nrecent : recent_bound;
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
+    const uint32_t limit = 32u * words;
+    uint32_t *cb = gb_bits, *rb = gb_bits + words;
+    for (uint64_t g = blockIdx.x; g < nruns; g += gridDim.x) {
+        const uint32_t x = run_key[g];
+        const uint64_t st = run_start[g], en = g + 1 < nruns ? run_start[g + 1] : n;
+        for (uint32_t w = (uint32_t)tid; w < 2 * words; w += GB_BLOCK) gb_bits[w] = 0u;
+        if (wave < 4) {  // x's rows: [x << 32, (x + 1) << 32) in the base run (waves 0, 1) and the recent run
+            const uint64_t *a = wave < 2 ? base : recent;
+            const uint64_t an = wave < 2 ? nbase : nrec;
+            const uint64_t key = ((uint64_t)x + (uint64_t)(wave & 1)) << 32;
+            const uint64_t pos = an ? wave_bound<false>(a, 0, an, key, lane) : 0ull;
+            if (lane == 0) s_rng[wave] = pos;
+        }
+        __syncthreads();
+        for (uint64_t i = st + (uint64_t)tid; i < en; i += GB_BLOCK) {
+            const uint32_t z = (uint32_t)cand[i];
+            if (z < limit) atomicOr(&cb[z >> 5], 1u << (z & 31u));
+        }
+        for (uint64_t i = s_rng[0] + (uint64_t)tid; i < s_rng[1]; i += GB_BLOCK) {
+            const uint32_t z = (uint32_t)base[i];
+            if (z < limit) atomicOr(&rb[z >> 5], 1u << (z & 31u));
+        }
+        for (uint64_t i = s_rng[2] + (uint64_t)tid; i < s_rng[3]; i += GB_BLOCK) {
+            const uint32_t z = (uint32_t)recent[i];
+            if (z < limit) atomicOr(&rb[z >> 5], 1u << (z & 31u));
+        }
+        __syncthreads();
+        // thread t takes words [t * per, (t + 1) * per): its new values' count, a block scan, then the values
+        const uint32_t per = (words + GB_BLOCK - 1) / GB_BLOCK;
+        uint32_t cnt = 0;
+        for (uint32_t k = 0; k < per; ++k) {
+            const uint32_t w = (uint32_t)tid * per + k;
+            if (w < words) cnt += (uint32_t)__popc(cb[w] & ~rb[w]);
+        }
+        uint32_t incl = cnt;
+#pragma unroll
+        for (int o = 1; o < WAVE; o <<= 1) {
+            const uint32_t t = __shfl_up(incl, o, WAVE);
+            if (lane >= o) incl += t;
+        }
+        if (lane == WAVE - 1) s_wsum[wave] = incl;
+        __syncthreads();
+        uint32_t pre = incl - cnt, total = 0;
+#pragma unroll
+        for (int q = 0; q < GB_BLOCK / WAVE; ++q) {
+            if (q < wave) pre += s_wsum[q];
+            total += s_wsum[q];
+        }
+        uint64_t pos = st + pre;
+        const uint64_t hi = (uint64_t)x << 32;
+        for (uint32_t k = 0; k < per; ++k) {
+            const uint32_t w = (uint32_t)tid * per + k;
+            if (w >= words) break;
+            uint32_t bits = cb[w] & ~rb[w];
+            while (bits) {
+                slots[pos++] = hi | (uint64_t)(w * 32u + (uint32_t)__builtin_ctz(bits));
+                bits &= bits - 1u;
+            }
+        }
+        for (uint64_t i = st + total + (uint64_t)tid; i < en; i += GB_BLOCK) slots[i] = hole;
+        __syncthreads();  // the bitmaps and s_rng are reused by the next group
+    }
+}
+
 struct SelFlags {
     const uint8_t *flags;
     uint64_t *out;
@@ -566,12 +653,14 @@ struct SelRuns {
     const uint64_t *in;
     uint32_t *run_key;
     uint64_t *run_start;
+    uint64_t cap = ~0ull;  // runs past it are counted, not written
     static constexpr bool kWindow = false;
     __device__ void setup(uint64_t, uint64_t, uint64_t *, int) const {}
     __device__ bool flag(uint64_t idx, uint64_t key, uint64_t prev, const uint64_t *) const {
         return idx == 0 || (prev >> 32) != (key >> 32);
     }
     __device__ void emit(uint64_t pos, uint64_t idx, uint64_t key) const {
+        if (pos >= cap) return;
         run_key[pos] = (uint32_t)(key >> 32);
         run_start[pos] = idx;
     }
@@ -1089,8 +1178,25 @@ void select_unique_diff2_dev(Ctx *ctx, const uint64_t *k, uint64_t n, const uint
     sel.d_nb2 = d_nb2;
     run_select(ctx, k, n, sel, d_count, d_n, stop);
 }
-void select_not_value(Ctx *ctx, const uint64_t *k, uint64_t n, uint64_t v, uint64_t *out, uint64_t *d_count) {
-    run_select(ctx, k, n, SelNotValue{v, out}, d_count);
+void select_not_value(Ctx *ctx, const uint64_t *k, uint64_t n, uint64_t v, uint64_t *out, uint64_t *d_count,
+                      const uint64_t *d_n, const uint32_t *stop) {
+    run_select(ctx, k, n, SelNotValue{v, out}, d_count, d_n, stop);
+}
+void group_bitmap_diff_dev(Ctx *ctx, const uint64_t *cand, uint64_t cand_bound, const uint64_t *d_cand,
+                           const uint32_t *run_key, const uint64_t *run_start, uint64_t runs_bound,
+                           const uint64_t *d_nruns, const uint64_t *base, uint64_t nbase, const uint64_t *recent,
+                           uint64_t recent_bound, const uint64_t *d_nrecent, uint32_t domain, uint64_t hole,
+                           uint64_t *slots, const uint32_t *stop) {
+    if (cand_bound == 0 || runs_bound == 0) return;
+    const uint32_t words = (domain + 31u) / 32u;
+    XH_REQUIRE(words >= 1 && words <= 4096, XLOG_HIP_INVALID_ARG, "group bitmap difference: domain above 2^17");
+    // the groups' and R's bytes, counted on the device (8 B per candidate read and per slot written)
+    Prof prof(ctx, XLOG_HIP_KERNEL_SELECT, 0.0);
+    add_work_rows(ctx, prof.work(16.0), d_cand, cand_bound, 1, nullptr, 0, 0, nullptr, stop);
+    hipLaunchKernelGGL(k_group_bitmap_diff, dim3(persistent_grid(ctx, runs_bound, 4)), dim3(GB_BLOCK),
+                       2 * words * sizeof(uint32_t), ctx->stream, cand, d_cand, cand_bound, run_key, run_start,
+                       d_nruns, runs_bound, base, nbase, recent, d_nrecent, recent_bound, words, hole, slots, stop);
+    XH_CHECK_HIP(hipGetLastError());
 }
 void select_flags(Ctx *ctx, const uint64_t *k, const uint8_t *flags, uint64_t n, uint64_t *out, uint64_t *d_count) {
     run_select(ctx, k, n, SelFlags{flags, out}, d_count);
@@ -1105,8 +1211,10 @@ void select_group_heads(Ctx *ctx, const uint64_t *mkeys, uint64_t nm, const uint
     run_select(ctx, mkeys, nm, SelGroupHeads{mpos, hkeys, gsel, hpos}, d_count, d_n);
 }
 void select_runs(Ctx *ctx, const uint64_t *k, uint64_t n, uint32_t *run_key, uint64_t *run_start, uint64_t *d_count,
-                 const uint64_t *d_n) {
-    run_select(ctx, k, n, SelRuns{k, run_key, run_start}, d_count, d_n);
+                 const uint64_t *d_n, const uint32_t *stop, uint64_t cap) {
+    SelRuns sel{k, run_key, run_start};
+    sel.cap = cap;
+    run_select(ctx, k, n, sel, d_count, d_n, stop);
 }
 
 void scan_u64_inplace(Ctx *ctx, uint64_t *a, uint64_t n, uint64_t *d_total, const uint32_t *stop) {
