@@ -2768,7 +2768,7 @@ struct Driver {
         // the set difference (XLOG_HIP_GROUP_BITMAP=0: never): its groups' keys and starts
         const char *gbe = getenv("XLOG_HIP_GROUP_BITMAP");
         const bool gb_on = !(gbe && gbe[0] == '0') && domain && domain <= (1ull << 17);
-        std::vector<Buf<uint32_t>> gkey(H);
+        std::vector<Buf<uint32_t>> gkey(H), rbits(H);
         std::vector<Buf<uint64_t>> gstart(H);
         std::vector<uint64_t> gbound(H, 0);
         Buf<uint64_t> gcount(ctx, H);
@@ -2779,6 +2779,16 @@ struct Driver {
             gbound[h] = std::max<uint64_t>(std::min<uint64_t>(mc, domain), 1);
             gkey[h] = Buf<uint32_t>(ctx, gbound[h]);
             gstart[h] = Buf<uint64_t>(ctx, gbound[h]);
+            // R as a bit matrix for the queue (domain^2 / 8 bytes, when that is at most an eighth of the room
+            // left): each iteration then reads a group's row of bits instead of its rows of R, and adds its
+            // new values to it
+            const uint64_t words = (domain + 31) / 32, cells = domain * words;
+            if (4 * cells <= device_room(ctx) / 8) {
+                const int p = heads[h];
+                rbits[h] = Buf<uint32_t>(ctx, cells);
+                rows_to_bits(ctx, full[p].k ? full[p].k : gstart[h].p, full[p].n, small[p].k ? small[p].k : gstart[h].p,
+                             small[p].n, (uint32_t)domain, rbits[h].p);
+            }
         }
 
         // ---- the queue -------------------------------------------------------------
@@ -2853,7 +2863,8 @@ struct Driver {
                     hipLaunchKernelGGL(k_q_cap, dim3(1), dim3(1), 0, ctx->stream, gcount.p + h, gbound[h], stop, code);
                     XH_CHECK_HIP(hipGetLastError());
                     group_bitmap_diff_dev(ctx, ka, Cb[k][h], d_cand, gkey[h].p, gstart[h].p, gbound[h], gcount.p + h,
-                                          big, full[p].n, rin, Rb[k][h], pR + h, (uint32_t)domain, ~0ull, kb, stop);
+                                          big, full[p].n, rin, Rb[k][h], pR + h, (uint32_t)domain, ~0ull, kb,
+                                          rbits[h].p, stop);
                     select_not_value(ctx, kb, Cb[k][h], ~0ull, qh[h]->D[k & 1].p, nD + h, d_cand, stop);
                     continue;
                 }

@@ -522,13 +522,52 @@ struct SelNotValue {
 // the second, ascending, from the group's first position; the group's other
 // positions get `hole`.  Every group is unique and sorted and has none of R's
 // rows; compacted (select_not_value), the groups give the sorted delta.
+// With rbits (R as a bit matrix, `words` words per row) x's row is read from
+// it instead, and rewritten with the group's values added (R after the
+// iteration); each row belongs to one group, so no two blocks share a row.
 constexpr int GB_BLOCK = 512;
+// x's rows of R (base and recent runs, as above) into an LDS bitmap; every thread calls it
+__device__ void rows_to_lds_bits(uint32_t x, const uint64_t *__restrict__ base, uint64_t nbase,
+                                 const uint64_t *__restrict__ recent, uint64_t nrec, uint32_t limit, uint32_t *rb,
+                                 uint64_t *s_rng, int tid, int lane, int wave) {
+    if (wave < 4) {  // x's rows: [x << 32, (x + 1) << 32) in the base run (waves 0, 1) and the recent run
+        const uint64_t *a = wave < 2 ? base : recent;
+        const uint64_t an = wave < 2 ? nbase : nrec;
+        const uint64_t key = ((uint64_t)x + (uint64_t)(wave & 1)) << 32;
+        const uint64_t pos = an ? wave_bound<false>(a, 0, an, key, lane) : 0ull;
+        if (lane == 0) s_rng[wave] = pos;
+    }
+    __syncthreads();
+    for (uint64_t i = s_rng[0] + (uint64_t)tid; i < s_rng[1]; i += GB_BLOCK) {
+        const uint32_t z = (uint32_t)base[i];
+        if (z < limit) atomicOr(&rb[z >> 5], 1u << (z & 31u));
+    }
+    for (uint64_t i = s_rng[2] + (uint64_t)tid; i < s_rng[3]; i += GB_BLOCK) {
+        const uint32_t z = (uint32_t)recent[i];
+        if (z < limit) atomicOr(&rb[z >> 5], 1u << (z & 31u));
+    }
+}
+// R as a bit matrix (rows 0 .. domain - 1, `words` words each), from its runs
+__global__ __launch_bounds__(GB_BLOCK) void k_rows_to_bits(const uint64_t *__restrict__ base, uint64_t nbase,
+                                                           const uint64_t *__restrict__ recent, uint64_t nrec,
+                                                           uint32_t domain, uint32_t words, uint32_t *__restrict__ bits) {
+    extern __shared__ uint32_t gb_bits[];
+    __shared__ uint64_t s_rng[4];
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
+    for (uint32_t x = blockIdx.x; x < domain; x += gridDim.x) {
+        for (uint32_t w = (uint32_t)tid; w < words; w += GB_BLOCK) gb_bits[w] = 0u;
+        rows_to_lds_bits(x, base, nbase, recent, nrec, 32u * words, gb_bits, s_rng, tid, lane, wave);
+        __syncthreads();
+        for (uint32_t w = (uint32_t)tid; w < words; w += GB_BLOCK) bits[(uint64_t)x * words + w] = gb_bits[w];
+        __syncthreads();
+    }
+}
 __global__ __launch_bounds__(GB_BLOCK) void k_group_bitmap_diff(
     const uint64_t *__restrict__ cand, const uint64_t *d_cand, uint64_t cand_bound,
     const uint32_t *__restrict__ run_key, const uint64_t *__restrict__ run_start, const uint64_t *d_nruns,
     uint64_t runs_bound, const uint64_t *__restrict__ base, uint64_t nbase, const uint64_t *__restrict__ recent,
     const uint64_t *d_nrecent, uint64_t recent_bound, uint32_t words, uint64_t hole, uint64_t *__restrict__ slots,
-    const uint32_t *stop) {
+    uint32_t *rbits, const uint32_t *stop) {
     extern __shared__ uint32_t gb_bits[];  // [0, words): the group's values, [words, 2 words): R's
     __shared__ uint64_t s_rng[4];
     __shared__ uint32_t s_wsum[GB_BLOCK / WAVE];
@@ -542,28 +581,20 @@ __global__ __launch_bounds__(GB_BLOCK) void k_group_bitmap_diff(
     for (uint64_t g = blockIdx.x; g < nruns; g += gridDim.x) {
         const uint32_t x = run_key[g];
         const uint64_t st = run_start[g], en = g + 1 < nruns ? run_start[g + 1] : n;
-        for (uint32_t w = (uint32_t)tid; w < 2 * words; w += GB_BLOCK) gb_bits[w] = 0u;
-        if (wave < 4) {  // x's rows: [x << 32, (x + 1) << 32) in the base run (waves 0, 1) and the recent run
-            const uint64_t *a = wave < 2 ? base : recent;
-            const uint64_t an = wave < 2 ? nbase : nrec;
-            const uint64_t key = ((uint64_t)x + (uint64_t)(wave & 1)) << 32;
-            const uint64_t pos = an ? wave_bound<false>(a, 0, an, key, lane) : 0ull;
-            if (lane == 0) s_rng[wave] = pos;
+        uint32_t *row = rbits ? rbits + (uint64_t)x * words : nullptr;
+        for (uint32_t w = (uint32_t)tid; w < words; w += GB_BLOCK) {
+            cb[w] = 0u;
+            rb[w] = row ? row[w] : 0u;
         }
+        if (!row) rows_to_lds_bits(x, base, nbase, recent, nrec, limit, rb, s_rng, tid, lane, wave);
         __syncthreads();
         for (uint64_t i = st + (uint64_t)tid; i < en; i += GB_BLOCK) {
             const uint32_t z = (uint32_t)cand[i];
             if (z < limit) atomicOr(&cb[z >> 5], 1u << (z & 31u));
         }
-        for (uint64_t i = s_rng[0] + (uint64_t)tid; i < s_rng[1]; i += GB_BLOCK) {
-            const uint32_t z = (uint32_t)base[i];
-            if (z < limit) atomicOr(&rb[z >> 5], 1u << (z & 31u));
-        }
-        for (uint64_t i = s_rng[2] + (uint64_t)tid; i < s_rng[3]; i += GB_BLOCK) {
-            const uint32_t z = (uint32_t)recent[i];
-            if (z < limit) atomicOr(&rb[z >> 5], 1u << (z & 31u));
-        }
         __syncthreads();
+        if (row)  // R after this iteration: its row with the group's values added
+            for (uint32_t w = (uint32_t)tid; w < words; w += GB_BLOCK) row[w] = rb[w] | cb[w];
         // thread t takes words [t * per, (t + 1) * per): its new values' count, a block scan, then the values
         const uint32_t per = (words + GB_BLOCK - 1) / GB_BLOCK;
         uint32_t cnt = 0;
@@ -1182,11 +1213,19 @@ void select_not_value(Ctx *ctx, const uint64_t *k, uint64_t n, uint64_t v, uint6
                       const uint64_t *d_n, const uint32_t *stop) {
     run_select(ctx, k, n, SelNotValue{v, out}, d_count, d_n, stop);
 }
+void rows_to_bits(Ctx *ctx, const uint64_t *base, uint64_t nbase, const uint64_t *recent, uint64_t nrec,
+                  uint32_t domain, uint32_t *bits) {
+    const uint32_t words = (domain + 31u) / 32u;
+    XH_REQUIRE(words >= 1 && words <= 4096, XLOG_HIP_INVALID_ARG, "bit matrix: domain above 2^17");
+    hipLaunchKernelGGL(k_rows_to_bits, dim3(persistent_grid(ctx, domain, 4)), dim3(GB_BLOCK), words * sizeof(uint32_t),
+                       ctx->stream, base, nbase, recent, nrec, domain, words, bits);
+    XH_CHECK_HIP(hipGetLastError());
+}
 void group_bitmap_diff_dev(Ctx *ctx, const uint64_t *cand, uint64_t cand_bound, const uint64_t *d_cand,
                            const uint32_t *run_key, const uint64_t *run_start, uint64_t runs_bound,
                            const uint64_t *d_nruns, const uint64_t *base, uint64_t nbase, const uint64_t *recent,
                            uint64_t recent_bound, const uint64_t *d_nrecent, uint32_t domain, uint64_t hole,
-                           uint64_t *slots, const uint32_t *stop) {
+                           uint64_t *slots, uint32_t *rbits, const uint32_t *stop) {
     if (cand_bound == 0 || runs_bound == 0) return;
     const uint32_t words = (domain + 31u) / 32u;
     XH_REQUIRE(words >= 1 && words <= 4096, XLOG_HIP_INVALID_ARG, "group bitmap difference: domain above 2^17");
@@ -1195,7 +1234,8 @@ void group_bitmap_diff_dev(Ctx *ctx, const uint64_t *cand, uint64_t cand_bound, 
     add_work_rows(ctx, prof.work(16.0), d_cand, cand_bound, 1, nullptr, 0, 0, nullptr, stop);
     hipLaunchKernelGGL(k_group_bitmap_diff, dim3(persistent_grid(ctx, runs_bound, 4)), dim3(GB_BLOCK),
                        2 * words * sizeof(uint32_t), ctx->stream, cand, d_cand, cand_bound, run_key, run_start,
-                       d_nruns, runs_bound, base, nbase, recent, d_nrecent, recent_bound, words, hole, slots, stop);
+                       d_nruns, runs_bound, base, nbase, recent, d_nrecent, recent_bound, words, hole, slots, rbits,
+                       stop);
     XH_CHECK_HIP(hipGetLastError());
 }
 void select_flags(Ctx *ctx, const uint64_t *k, const uint8_t *flags, uint64_t n, uint64_t *out, uint64_t *d_count) {
