@@ -138,6 +138,30 @@ def test_queued_join_route_stops_and_resumes(provider, monkeypatch, margin, slac
         _check(p, name, plan, rels, idb, oracle.seminaive(plan, rels))
 
 
+@pytest.mark.parametrize("mode", ["0", "1", "2", "3"])
+def test_queued_join_route_group_bitmap_modes(provider, monkeypatch, mode):
+    """Grouped heads over a small domain find their new rows by per-group LDS bitmaps.
+    XLOG_HIP_GROUP_BITMAP: 0 sort + set difference instead; 1 R's rows read from its two runs; 2 from R
+    as a bit matrix that every iteration brings up to date, the runs merged as before; 3 (the default)
+    R kept only in the matrix during a queue by heads that no index reads in full, its new rows emitted
+    and merged once at the queue's end, the matrix kept between queues while R is unchanged.  Each mode
+    with the queue's own bounds and with bounds shrunk so that queues stop and host iterations come
+    between them (the matrix is then rebuilt); every result is the oracle's."""
+    p = provider
+    monkeypatch.setenv("XLOG_HIP_GROUP_BITMAP", mode)
+    for name, plan, rels, idb in _programs() + _nonlinear_programs():
+        ref = oracle.seminaive(plan, rels)
+        for stops in (False, True):
+            if stops:
+                monkeypatch.setenv("XLOG_HIP_JOIN_QUEUE_MARGIN_PCT", "50")
+                monkeypatch.setenv("XLOG_HIP_JOIN_QUEUE_SLACK", "16")
+            else:
+                monkeypatch.delenv("XLOG_HIP_JOIN_QUEUE_MARGIN_PCT", raising=False)
+                monkeypatch.delenv("XLOG_HIP_JOIN_QUEUE_SLACK", raising=False)
+            _note(f"join queue group bitmap mode={mode} {name} stops={stops}")
+            _check(p, name, plan, rels, idb, ref)
+
+
 def test_queued_join_route_small_and_empty(provider):
     """Edge cases: no edges, one edge, a cycle (the last iterations derive nothing), a head with
     initial contents, and an iteration limit reached inside a queue."""

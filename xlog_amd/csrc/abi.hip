@@ -1916,6 +1916,25 @@ struct Driver {
     // and small[p], the recent run every delta is merged into (see run_queue).
     std::vector<DRel> small;
     bool q_learned = false;  // the last queue stopped and its counts changed the bounds' inputs
+    // R of a head as a bit matrix (domain rows of ceil(domain / 64) u64 words) for the queue's group
+    // bitmaps: m[cur] holds R as it stood when full[p] and small[p] had versions vfull and vsmall;
+    // m[cur ^ 1] and `start` are the queue's working copies
+    struct BitR {
+        Buf<uint64_t> m[2], start;
+        int cur = 0;
+        uint64_t vfull = 0, vsmall = 0, domain = 0;
+        bool valid = false;
+    };
+    std::vector<BitR> bitr;
+    bool bitr_current(uint32_t p) const {
+        return p < bitr.size() && bitr[p].valid && bitr[p].vfull == full[p].version &&
+               bitr[p].vsmall == small[p].version;
+    }
+    void bitr_stamp(uint32_t p) {
+        bitr[p].valid = true;
+        bitr[p].vfull = full[p].version;
+        bitr[p].vsmall = small[p].version;
+    }
 
     ~Driver() {
         cache.clear();
@@ -1926,12 +1945,14 @@ struct Driver {
     // R of p in one run again: the recent run merged into the base run
     void compact(uint32_t p) {
         if (p >= small.size()) return;
+        const bool bits = bitr_current(p);
         if (small[p].n) {
             DRel m = merge(full[p], small[p]);
             release(full[p]);
             full[p] = m;
         }
         release(small[p]);
+        if (bits) bitr_stamp(p);  // the same rows
     }
     void compact_all() {
         for (uint32_t p = 0; p < small.size(); ++p) compact(p);
@@ -2481,6 +2502,8 @@ struct Driver {
                 heads.push_back((int)p);
             }
         small.assign(n_preds, DRel());
+        bitr.clear();
+        bitr.resize(n_preds);
         if (obs.size() < qr.size()) obs.resize(qr.size());
         uint64_t it = 0;
         bool retried = false;
@@ -2578,6 +2601,55 @@ struct Driver {
         const uint32_t B = total_off + 1 + tot_words;
         auto blk = [&](int64_t k) { return (uint64_t)1 + (uint64_t)(k + 1) * B; };
         if (H > QMAX_HEADS) return 0;
+        // a head whose one variant keeps its delta's first column as the high word gets its candidates
+        // grouped by it, in ascending order: one short-run pass sorts them (sort_grouped_dev)
+        std::vector<char> grouped(H, 0);
+        std::vector<int> gsrc(H, -1);  // the delta predicate of a grouped head's variant
+        for (uint32_t h = 0; h < H; ++h) grouped[h] = nvar[h] == 1;
+        for (auto &vp : vars) {
+            grouped[hidx[vp->head]] &= vp->bp.grouped ? 1 : 0;
+            gsrc[hidx[vp->head]] = hidx[vp->dpred];
+        }
+        // A grouped head over a domain of at most 2^17 values takes the group bitmaps instead of the sort
+        // and the set difference, reading R's rows from R as a bit matrix (domain^2 / 8 bytes, three copies,
+        // when that is at most an eighth of the room left) that each iteration brings up to date.  Such a
+        // head that no index of the queue reads in full keeps R only in the matrix while the queue runs (no
+        // merges): the queue's new rows are emitted from it at the end and merged into the recent run once.
+        // XLOG_HIP_GROUP_BITMAP: 0 never; 1 group bitmaps over R's runs (no matrix); 2 the matrix with R's
+        // runs merged every iteration; unset or 3 all of it.
+        const uint64_t gb_mode = env_u64("XLOG_HIP_GROUP_BITMAP", 3);
+        const bool gb_on = gb_mode != 0 && domain && domain <= (1ull << 17);
+        const uint32_t bw = (uint32_t)((domain + 63) / 64);
+        const uint64_t cells = domain * bw;
+        std::vector<char> mh(H, 0), bm(H, 0);  // R as a bit matrix; R only as the matrix
+        for (uint32_t h = 0; h < H && gb_on && gb_mode >= 2; ++h) {
+            if (!grouped[h]) continue;
+            const int p = heads[h];
+            BitR &b = bitr[p];
+            if (b.domain != domain) b = BitR();
+            if (!b.m[0].p) {
+                if (24 * cells > device_room(ctx) / 8) continue;
+                b.m[0] = Buf<uint64_t>(ctx, cells);
+                b.m[1] = Buf<uint64_t>(ctx, cells);
+                b.start = Buf<uint64_t>(ctx, cells);
+                b.domain = domain;
+            }
+            if (!bitr_current((uint32_t)p)) {
+                b.cur = 0;
+                rows_to_bits(ctx, full[p].k ? full[p].k : b.start.p, full[p].n, small[p].k ? small[p].k : b.start.p,
+                             small[p].n, (uint32_t)domain, b.m[0].p);
+                bitr_stamp((uint32_t)p);
+            }
+            // the other copy starts equal (each iteration writes it from the current one), and the rows at
+            // the queue's start are kept for the emit
+            XH_CHECK_HIP(hipMemcpyAsync(b.m[b.cur ^ 1].p, b.m[b.cur].p, cells * sizeof(uint64_t),
+                                        hipMemcpyDeviceToDevice, ctx->stream));
+            XH_CHECK_HIP(hipMemcpyAsync(b.start.p, b.m[b.cur].p, cells * sizeof(uint64_t), hipMemcpyDeviceToDevice,
+                                        ctx->stream));
+            mh[h] = 1;
+            bm[h] = gb_mode >= 3;
+            for (auto &dp : dyns) bm[h] &= dp->pred != p;
+        }
         // every block comes back in one read of the pinned staging
         const uint64_t fit = (Ctx::HOST_STAGE_U64 - 1) / B;  // blocks that fit, the starting one included
         if (fit < 3) return 0;
@@ -2679,7 +2751,7 @@ struct Driver {
             // device bytes of the queue's buffers with this iteration in it
             uint64_t bytes = 0;
             for (uint32_t h = 0; h < H; ++h) {
-                uint64_t mc = cb[h], mr = rb[h];
+                uint64_t mc = cb[h], mr = bm[h] ? 0 : rb[h];
                 for (auto &c : Cb) mc = std::max(mc, c[h]);
                 bytes += 8 * (4 * mc + 2 * mr);
             }
@@ -2724,8 +2796,8 @@ struct Driver {
             x->Calt.reset(alloc_keys(ctx, mc));
             x->D[0].reset(alloc_keys(ctx, mc));
             x->D[1].reset(alloc_keys(ctx, mc));
-            x->R[0].reset(alloc_keys(ctx, Rb[Q][h]));
-            x->R[1].reset(alloc_keys(ctx, Rb[Q][h]));
+            x->R[0].reset(alloc_keys(ctx, bm[h] ? 1 : Rb[Q][h]));  // (R only as the matrix: not written)
+            x->R[1].reset(alloc_keys(ctx, bm[h] ? 1 : Rb[Q][h]));
             qh.push_back(std::move(x));
         }
         for (size_t vi = 0; vi < vars.size(); ++vi) {
@@ -2752,26 +2824,15 @@ struct Driver {
             fill_u64(ctx, qs.p + blk(-1) + h, delta[heads[h]].n, 1);
             fill_u64(ctx, qs.p + blk(-1) + H + h, small[heads[h]].n, 1);
         }
-        // a head whose one variant keeps its delta's first column as the high word gets its candidates
-        // grouped by it, in ascending order: one short-run pass sorts them (sort_grouped_dev)
-        std::vector<char> grouped(H, 0);
-        std::vector<int> gsrc(H, -1);  // the delta predicate of a grouped head's variant
-        for (uint32_t h = 0; h < H; ++h) grouped[h] = nvar[h] == 1;
-        for (auto &vp : vars) {
-            grouped[hidx[vp->head]] &= vp->bp.grouped ? 1 : 0;
-            gsrc[hidx[vp->head]] = hidx[vp->dpred];
-        }
         Buf<uint64_t> gscratch(ctx, 2 * (uint64_t)H);
         Buf<uint64_t> tcount(ctx, 1);  // the size of an empty base run
         fill_u64(ctx, tcount.p, 0ull, 1);
-        // a grouped head over a domain of at most 2^17 values takes the group bitmaps instead of the sort and
-        // the set difference (XLOG_HIP_GROUP_BITMAP=0: never): its groups' keys and starts
-        const char *gbe = getenv("XLOG_HIP_GROUP_BITMAP");
-        const bool gb_on = !(gbe && gbe[0] == '0') && domain && domain <= (1ull << 17);
-        std::vector<Buf<uint32_t>> gkey(H), rbits(H);
+        // the group bitmaps' groups: keys and starts
+        std::vector<Buf<uint32_t>> gkey(H);
         std::vector<Buf<uint64_t>> gstart(H);
         std::vector<uint64_t> gbound(H, 0);
         Buf<uint64_t> gcount(ctx, H);
+        fill_u64(ctx, gcount.p, 0ull, H);
         for (uint32_t h = 0; h < H && gb_on; ++h) {
             if (!grouped[h]) continue;
             uint64_t mc = 0;
@@ -2779,17 +2840,10 @@ struct Driver {
             gbound[h] = std::max<uint64_t>(std::min<uint64_t>(mc, domain), 1);
             gkey[h] = Buf<uint32_t>(ctx, gbound[h]);
             gstart[h] = Buf<uint64_t>(ctx, gbound[h]);
-            // R as a bit matrix for the queue (domain^2 / 8 bytes, when that is at most an eighth of the room
-            // left): each iteration then reads a group's row of bits instead of its rows of R, and adds its
-            // new values to it
-            const uint64_t words = (domain + 31) / 32, cells = domain * words;
-            if (4 * cells <= device_room(ctx) / 8) {
-                const int p = heads[h];
-                rbits[h] = Buf<uint32_t>(ctx, cells);
-                rows_to_bits(ctx, full[p].k ? full[p].k : gstart[h].p, full[p].n, small[p].k ? small[p].k : gstart[h].p,
-                             small[p].n, (uint32_t)domain, rbits[h].p);
-            }
         }
+        // iteration k reads R's matrix M(k) and writes M(k + 1) (the two copies alternate): a stopped
+        // iteration leaves M(k), R after the last completed one, as it was
+        auto mat = [&](uint32_t h, uint64_t k) { BitR &b = bitr[heads[h]]; return b.m[(b.cur + k) & 1].p; };
 
         // ---- the queue -------------------------------------------------------------
         cur_iter = it + 1;
@@ -2858,13 +2912,18 @@ struct Driver {
                 if (!rin) rin = qh[h]->R[1].p;  // an empty run read through its device count
                 if (gbound[h]) {
                     // per group (one high word, its runs listed), the new values by two LDS bitmaps, then
-                    // the groups compacted in order; more groups than the domain stop the queue
+                    // the groups compacted in order; more groups than the domain stop the queue.  M(k + 1)
+                    // first takes the rows of the previous iteration's groups (it holds R before them), then
+                    // the group kernel writes this iteration's groups' rows into it
+                    if (mh[h] && k > 0)
+                        copy_group_rows(ctx, gkey[h].p, gcount.p + h, gbound[h], (uint32_t)domain, mat(h, k),
+                                        mat(h, k + 1), stop);
                     select_runs(ctx, ka, Cb[k][h], gkey[h].p, gstart[h].p, gcount.p + h, d_cand, stop, gbound[h]);
                     hipLaunchKernelGGL(k_q_cap, dim3(1), dim3(1), 0, ctx->stream, gcount.p + h, gbound[h], stop, code);
                     XH_CHECK_HIP(hipGetLastError());
                     group_bitmap_diff_dev(ctx, ka, Cb[k][h], d_cand, gkey[h].p, gstart[h].p, gbound[h], gcount.p + h,
                                           big, full[p].n, rin, Rb[k][h], pR + h, (uint32_t)domain, ~0ull, kb,
-                                          rbits[h].p, stop);
+                                          mh[h] ? mat(h, k) : nullptr, mh[h] ? mat(h, k + 1) : nullptr, stop);
                     select_not_value(ctx, kb, Cb[k][h], ~0ull, qh[h]->D[k & 1].p, nD + h, d_cand, stop);
                     continue;
                 }
@@ -2879,11 +2938,12 @@ struct Driver {
             }
             // the delta total, R's new sizes within their bounds
             QEnd qe{nD, pR, nR, total, H, {}};
-            for (uint32_t h = 0; h < H; ++h) qe.rcap[h] = Rb[k + 1][h];
+            for (uint32_t h = 0; h < H; ++h) qe.rcap[h] = bm[h] ? ~0ull : Rb[k + 1][h];
             hipLaunchKernelGGL(k_q_end, dim3(1), dim3(1), 0, ctx->stream, qe, stop, code);
             XH_CHECK_HIP(hipGetLastError());
             // per head: R ∪= Δ' into the other buffer (nothing when the iteration derived nothing)
             for (uint32_t h = 0; h < H; ++h) {
+                if (bm[h]) continue;
                 const int p = heads[h];
                 const uint64_t *rin = k == 0 ? small[p].k : qh[h]->R[(k - 1) & 1].p;
                 if (!rin) rin = qh[h]->R[1].p;
@@ -2938,11 +2998,32 @@ struct Driver {
             const uint64_t *bk = hs + blk(last);
             for (uint32_t h = 0; h < H; ++h) {
                 const int p = heads[h];
-                release(small[p]);
-                small[p].n = bk[H + h];
-                small[p].k = qh[h]->R[last & 1].release();
-                small[p].owned = true;
-                small[p].version = version_counter++;
+                if (bm[h]) {
+                    // the queue's new rows: R's matrix after the last completed iteration less its rows at
+                    // the start, emitted in order and merged into the recent run
+                    const uint64_t added = bk[H + h] - small[p].n;
+                    if (added) {
+                        bits_andnot(ctx, mat(h, (uint64_t)last + 1), bitr[p].start.p, cells);
+                        DRel add;
+                        add.n = bitmap_emit(ctx, bitr[p].start.p, (uint32_t)domain, bw, &add.k, XLOG_HIP_KERNEL_MERGE,
+                                            added);
+                        add.owned = true;
+                        DRel m = merge(small[p], add);
+                        release(small[p]);
+                        release(add);
+                        small[p] = m;
+                    }
+                } else {
+                    release(small[p]);
+                    small[p].n = bk[H + h];
+                    small[p].k = qh[h]->R[last & 1].release();
+                    small[p].owned = true;
+                    small[p].version = version_counter++;
+                }
+                if (mh[h]) {
+                    bitr[p].cur = (bitr[p].cur + (int)(last + 1)) & 1;
+                    bitr_stamp((uint32_t)p);
+                }
             }
         }
         if (converged || last >= 0) {

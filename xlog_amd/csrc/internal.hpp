@@ -399,19 +399,26 @@ void select_not_value(Ctx *ctx, const uint64_t *k, uint64_t n, uint64_t v, uint6
 // and a sorted recent run (*d_nrecent <= recent_bound).  Each group's values
 // that are not in R go, ascending, to slots from the group's first position,
 // the rest of its positions get `hole`; compacting the slots
-// (select_not_value) gives the sorted new rows.  With rbits (R as a bit
-// matrix, rows_to_bits) R's rows come from it, and it is updated to R after
-// the iteration.
+// (select_not_value) gives the sorted new rows.  With rin (R as a bit
+// matrix, rows_to_bits) R's rows come from it, and rout receives the rows of
+// the groups with their values added (R after the iteration; the caller
+// copies the other rows).
 void group_bitmap_diff_dev(Ctx *ctx, const uint64_t *cand, uint64_t cand_bound, const uint64_t *d_cand,
                            const uint32_t *run_key, const uint64_t *run_start, uint64_t runs_bound,
                            const uint64_t *d_nruns, const uint64_t *base, uint64_t nbase, const uint64_t *recent,
                            uint64_t recent_bound, const uint64_t *d_nrecent, uint32_t domain, uint64_t hole,
-                           uint64_t *slots, uint32_t *rbits, const uint32_t *stop);
+                           uint64_t *slots, const uint64_t *rin, uint64_t *rout, const uint32_t *stop);
 // R (a sorted base run of nbase rows and a sorted recent run of nrec rows,
 // every value below `domain` <= 2^17) as a bit matrix: domain rows of
-// ceil(domain / 32) u32 words.
+// ceil(domain / 64) u64 words (bitmap_emit's layout).
 void rows_to_bits(Ctx *ctx, const uint64_t *base, uint64_t nbase, const uint64_t *recent, uint64_t nrec,
-                  uint32_t domain, uint32_t *bits);
+                  uint32_t domain, uint64_t *bits);
+// Rows run_key[0 .. *d_n) (at most bound) of a bit matrix over `domain`
+// values copied from src to dst (nothing once *stop is set).
+void copy_group_rows(Ctx *ctx, const uint32_t *run_key, const uint64_t *d_n, uint64_t bound, uint32_t domain,
+                     const uint64_t *src, uint64_t *dst, const uint32_t *stop);
+// s = a & ~s over n u64 words (the bits a sets that s does not)
+void bits_andnot(Ctx *ctx, const uint64_t *a, uint64_t *s, uint64_t n);
 
 // In-place exclusive scan of u32 values (prefixes wrap modulo 2^32); the
 // exact u64 sum goes to *d_total (device).  One pass, decoupled look-back.

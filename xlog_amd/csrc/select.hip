@@ -515,21 +515,22 @@ struct SelNotValue {
 };
 
 // Grouped candidates over a small value domain (every low word below
-// 32 * words), each group one run of equal high word x (select_runs): a block
-// marks the group's low words in an LDS bitmap and x's rows of R (a base run of
-// known size and a recent run counted on the device; found by four wave
-// searches) in a second one, and writes the values set in the first and not in
-// the second, ascending, from the group's first position; the group's other
-// positions get `hole`.  Every group is unique and sorted and has none of R's
-// rows; compacted (select_not_value), the groups give the sorted delta.
-// With rbits (R as a bit matrix, `words` words per row) x's row is read from
-// it instead, and rewritten with the group's values added (R after the
-// iteration); each row belongs to one group, so no two blocks share a row.
+// 64 * words), each group one run of equal high word x (select_runs): a block
+// marks the group's low words in an LDS bitmap and x's row of R in a second
+// one, and writes the values set in the first and not in the second,
+// ascending, from the group's first position; the group's other positions
+// get `hole`.  Every group is unique and sorted and has none of R's rows;
+// compacted (select_not_value), the groups give the sorted delta.  x's row of
+// R comes from R's runs (a base run of known size and a recent run counted on
+// the device; found by four wave searches) or, with rin, from R as a bit
+// matrix (`words` u64 words per row), and then R after the iteration, the row
+// with the group's values added, goes to the same row of rout (each row
+// belongs to one group; rows without a group are copied by the caller).
 constexpr int GB_BLOCK = 512;
-// x's rows of R (base and recent runs, as above) into an LDS bitmap; every thread calls it
+// x's rows of R (base and recent runs) into an LDS bitmap; every thread calls it
 __device__ void rows_to_lds_bits(uint32_t x, const uint64_t *__restrict__ base, uint64_t nbase,
-                                 const uint64_t *__restrict__ recent, uint64_t nrec, uint32_t limit, uint32_t *rb,
-                                 uint64_t *s_rng, int tid, int lane, int wave) {
+                                 const uint64_t *__restrict__ recent, uint64_t nrec, uint32_t limit,
+                                 unsigned long long *rb, uint64_t *s_rng, int tid, int lane, int wave) {
     if (wave < 4) {  // x's rows: [x << 32, (x + 1) << 32) in the base run (waves 0, 1) and the recent run
         const uint64_t *a = wave < 2 ? base : recent;
         const uint64_t an = wave < 2 ? nbase : nrec;
@@ -540,23 +541,23 @@ __device__ void rows_to_lds_bits(uint32_t x, const uint64_t *__restrict__ base, 
     __syncthreads();
     for (uint64_t i = s_rng[0] + (uint64_t)tid; i < s_rng[1]; i += GB_BLOCK) {
         const uint32_t z = (uint32_t)base[i];
-        if (z < limit) atomicOr(&rb[z >> 5], 1u << (z & 31u));
+        if (z < limit) atomicOr(&rb[z >> 6], 1ull << (z & 63u));
     }
     for (uint64_t i = s_rng[2] + (uint64_t)tid; i < s_rng[3]; i += GB_BLOCK) {
         const uint32_t z = (uint32_t)recent[i];
-        if (z < limit) atomicOr(&rb[z >> 5], 1u << (z & 31u));
+        if (z < limit) atomicOr(&rb[z >> 6], 1ull << (z & 63u));
     }
 }
-// R as a bit matrix (rows 0 .. domain - 1, `words` words each), from its runs
+// R as a bit matrix (rows 0 .. domain - 1, `words` u64 words each), from its runs
 __global__ __launch_bounds__(GB_BLOCK) void k_rows_to_bits(const uint64_t *__restrict__ base, uint64_t nbase,
                                                            const uint64_t *__restrict__ recent, uint64_t nrec,
-                                                           uint32_t domain, uint32_t words, uint32_t *__restrict__ bits) {
-    extern __shared__ uint32_t gb_bits[];
+                                                           uint32_t domain, uint32_t words, uint64_t *__restrict__ bits) {
+    extern __shared__ unsigned long long gb_bits[];
     __shared__ uint64_t s_rng[4];
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
     for (uint32_t x = blockIdx.x; x < domain; x += gridDim.x) {
-        for (uint32_t w = (uint32_t)tid; w < words; w += GB_BLOCK) gb_bits[w] = 0u;
-        rows_to_lds_bits(x, base, nbase, recent, nrec, 32u * words, gb_bits, s_rng, tid, lane, wave);
+        for (uint32_t w = (uint32_t)tid; w < words; w += GB_BLOCK) gb_bits[w] = 0ull;
+        rows_to_lds_bits(x, base, nbase, recent, nrec, 64u * words, gb_bits, s_rng, tid, lane, wave);
         __syncthreads();
         for (uint32_t w = (uint32_t)tid; w < words; w += GB_BLOCK) bits[(uint64_t)x * words + w] = gb_bits[w];
         __syncthreads();
@@ -567,8 +568,8 @@ __global__ __launch_bounds__(GB_BLOCK) void k_group_bitmap_diff(
     const uint32_t *__restrict__ run_key, const uint64_t *__restrict__ run_start, const uint64_t *d_nruns,
     uint64_t runs_bound, const uint64_t *__restrict__ base, uint64_t nbase, const uint64_t *__restrict__ recent,
     const uint64_t *d_nrecent, uint64_t recent_bound, uint32_t words, uint64_t hole, uint64_t *__restrict__ slots,
-    uint32_t *rbits, const uint32_t *stop) {
-    extern __shared__ uint32_t gb_bits[];  // [0, words): the group's values, [words, 2 words): R's
+    const uint64_t *__restrict__ rin, uint64_t *__restrict__ rout, const uint32_t *stop) {
+    extern __shared__ unsigned long long gb_bits[];  // [0, words): the group's values, [words, 2 words): R's
     __shared__ uint64_t s_rng[4];
     __shared__ uint32_t s_wsum[GB_BLOCK / WAVE];
     if (stop && *stop) return;
@@ -576,31 +577,30 @@ __global__ __launch_bounds__(GB_BLOCK) void k_group_bitmap_diff(
     const uint64_t nruns = *d_nruns < runs_bound ? *d_nruns : runs_bound;
     const uint64_t nrec = *d_nrecent < recent_bound ? *d_nrecent : recent_bound;
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
-    const uint32_t limit = 32u * words;
-    uint32_t *cb = gb_bits, *rb = gb_bits + words;
+    const uint32_t limit = 64u * words;
+    unsigned long long *cb = gb_bits, *rb = gb_bits + words;
     for (uint64_t g = blockIdx.x; g < nruns; g += gridDim.x) {
         const uint32_t x = run_key[g];
         const uint64_t st = run_start[g], en = g + 1 < nruns ? run_start[g + 1] : n;
-        uint32_t *row = rbits ? rbits + (uint64_t)x * words : nullptr;
         for (uint32_t w = (uint32_t)tid; w < words; w += GB_BLOCK) {
-            cb[w] = 0u;
-            rb[w] = row ? row[w] : 0u;
+            cb[w] = 0ull;
+            rb[w] = rin ? rin[(uint64_t)x * words + w] : 0ull;
         }
-        if (!row) rows_to_lds_bits(x, base, nbase, recent, nrec, limit, rb, s_rng, tid, lane, wave);
+        if (!rin) rows_to_lds_bits(x, base, nbase, recent, nrec, limit, rb, s_rng, tid, lane, wave);
         __syncthreads();
         for (uint64_t i = st + (uint64_t)tid; i < en; i += GB_BLOCK) {
             const uint32_t z = (uint32_t)cand[i];
-            if (z < limit) atomicOr(&cb[z >> 5], 1u << (z & 31u));
+            if (z < limit) atomicOr(&cb[z >> 6], 1ull << (z & 63u));
         }
         __syncthreads();
-        if (row)  // R after this iteration: its row with the group's values added
-            for (uint32_t w = (uint32_t)tid; w < words; w += GB_BLOCK) row[w] = rb[w] | cb[w];
+        if (rout)  // R after this iteration: the row with the group's values added
+            for (uint32_t w = (uint32_t)tid; w < words; w += GB_BLOCK) rout[(uint64_t)x * words + w] = rb[w] | cb[w];
         // thread t takes words [t * per, (t + 1) * per): its new values' count, a block scan, then the values
         const uint32_t per = (words + GB_BLOCK - 1) / GB_BLOCK;
         uint32_t cnt = 0;
         for (uint32_t k = 0; k < per; ++k) {
             const uint32_t w = (uint32_t)tid * per + k;
-            if (w < words) cnt += (uint32_t)__popc(cb[w] & ~rb[w]);
+            if (w < words) cnt += (uint32_t)__popcll(cb[w] & ~rb[w]);
         }
         uint32_t incl = cnt;
 #pragma unroll
@@ -621,10 +621,10 @@ __global__ __launch_bounds__(GB_BLOCK) void k_group_bitmap_diff(
         for (uint32_t k = 0; k < per; ++k) {
             const uint32_t w = (uint32_t)tid * per + k;
             if (w >= words) break;
-            uint32_t bits = cb[w] & ~rb[w];
+            unsigned long long bits = cb[w] & ~rb[w];
             while (bits) {
-                slots[pos++] = hi | (uint64_t)(w * 32u + (uint32_t)__builtin_ctz(bits));
-                bits &= bits - 1u;
+                slots[pos++] = hi | (uint64_t)(w * 64u + (uint32_t)__builtin_ctzll(bits));
+                bits &= bits - 1ull;
             }
         }
         for (uint64_t i = st + total + (uint64_t)tid; i < en; i += GB_BLOCK) slots[i] = hole;
@@ -1214,10 +1214,10 @@ void select_not_value(Ctx *ctx, const uint64_t *k, uint64_t n, uint64_t v, uint6
     run_select(ctx, k, n, SelNotValue{v, out}, d_count, d_n, stop);
 }
 void rows_to_bits(Ctx *ctx, const uint64_t *base, uint64_t nbase, const uint64_t *recent, uint64_t nrec,
-                  uint32_t domain, uint32_t *bits) {
-    const uint32_t words = (domain + 31u) / 32u;
-    XH_REQUIRE(words >= 1 && words <= 4096, XLOG_HIP_INVALID_ARG, "bit matrix: domain above 2^17");
-    hipLaunchKernelGGL(k_rows_to_bits, dim3(persistent_grid(ctx, domain, 4)), dim3(GB_BLOCK), words * sizeof(uint32_t),
+                  uint32_t domain, uint64_t *bits) {
+    const uint32_t words = (domain + 63u) / 64u;
+    XH_REQUIRE(words >= 1 && words <= 2048, XLOG_HIP_INVALID_ARG, "bit matrix: domain above 2^17");
+    hipLaunchKernelGGL(k_rows_to_bits, dim3(persistent_grid(ctx, domain, 4)), dim3(GB_BLOCK), words * sizeof(uint64_t),
                        ctx->stream, base, nbase, recent, nrec, domain, words, bits);
     XH_CHECK_HIP(hipGetLastError());
 }
@@ -1225,17 +1225,50 @@ void group_bitmap_diff_dev(Ctx *ctx, const uint64_t *cand, uint64_t cand_bound, 
                            const uint32_t *run_key, const uint64_t *run_start, uint64_t runs_bound,
                            const uint64_t *d_nruns, const uint64_t *base, uint64_t nbase, const uint64_t *recent,
                            uint64_t recent_bound, const uint64_t *d_nrecent, uint32_t domain, uint64_t hole,
-                           uint64_t *slots, uint32_t *rbits, const uint32_t *stop) {
+                           uint64_t *slots, const uint64_t *rin, uint64_t *rout, const uint32_t *stop) {
     if (cand_bound == 0 || runs_bound == 0) return;
-    const uint32_t words = (domain + 31u) / 32u;
-    XH_REQUIRE(words >= 1 && words <= 4096, XLOG_HIP_INVALID_ARG, "group bitmap difference: domain above 2^17");
+    const uint32_t words = (domain + 63u) / 64u;
+    XH_REQUIRE(words >= 1 && words <= 2048, XLOG_HIP_INVALID_ARG, "group bitmap difference: domain above 2^17");
     // the groups' and R's bytes, counted on the device (8 B per candidate read and per slot written)
     Prof prof(ctx, XLOG_HIP_KERNEL_SELECT, 0.0);
     add_work_rows(ctx, prof.work(16.0), d_cand, cand_bound, 1, nullptr, 0, 0, nullptr, stop);
     hipLaunchKernelGGL(k_group_bitmap_diff, dim3(persistent_grid(ctx, runs_bound, 4)), dim3(GB_BLOCK),
-                       2 * words * sizeof(uint32_t), ctx->stream, cand, d_cand, cand_bound, run_key, run_start,
-                       d_nruns, runs_bound, base, nbase, recent, d_nrecent, recent_bound, words, hole, slots, rbits,
+                       2 * words * sizeof(uint64_t), ctx->stream, cand, d_cand, cand_bound, run_key, run_start,
+                       d_nruns, runs_bound, base, nbase, recent, d_nrecent, recent_bound, words, hole, slots, rin, rout,
                        stop);
+    XH_CHECK_HIP(hipGetLastError());
+}
+// Rows run_key[0 .. *d_n) (at most bound) of one bit matrix copied to another
+// (`words` u64 words per row): a block per row.
+__global__ __launch_bounds__(256) void k_copy_group_rows(const uint32_t *__restrict__ run_key, const uint64_t *d_n,
+                                                         uint64_t bound, uint32_t words,
+                                                         const uint64_t *__restrict__ src, uint64_t *__restrict__ dst,
+                                                         const uint32_t *stop) {
+    if (stop && *stop) return;
+    const uint64_t n = *d_n < bound ? *d_n : bound;
+    for (uint64_t g = blockIdx.x; g < n; g += gridDim.x) {
+        const uint64_t row = (uint64_t)run_key[g] * words;
+        for (uint32_t w = threadIdx.x; w < words; w += blockDim.x) dst[row + w] = src[row + w];
+    }
+}
+void copy_group_rows(Ctx *ctx, const uint32_t *run_key, const uint64_t *d_n, uint64_t bound, uint32_t domain,
+                     const uint64_t *src, uint64_t *dst, const uint32_t *stop) {
+    if (bound == 0) return;
+    const uint32_t words = (domain + 63u) / 64u;
+    Prof prof(ctx, XLOG_HIP_KERNEL_MERGE, 0.0);
+    hipLaunchKernelGGL(k_copy_group_rows, dim3(persistent_grid(ctx, bound, 8)), dim3(256), 0, ctx->stream, run_key,
+                       d_n, bound, words, src, dst, stop);
+    XH_CHECK_HIP(hipGetLastError());
+}
+// s = a & ~s over n words
+__global__ void k_bits_andnot(const uint64_t *__restrict__ a, uint64_t *__restrict__ s, uint64_t n) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+        s[i] = a[i] & ~s[i];
+}
+void bits_andnot(Ctx *ctx, const uint64_t *a, uint64_t *s, uint64_t n) {
+    if (n == 0) return;
+    Prof prof(ctx, XLOG_HIP_KERNEL_MERGE, 24.0 * (double)n);
+    hipLaunchKernelGGL(k_bits_andnot, dim3(grid_for(n, 256, 8192)), dim3(256), 0, ctx->stream, a, s, n);
     XH_CHECK_HIP(hipGetLastError());
 }
 void select_flags(Ctx *ctx, const uint64_t *k, const uint8_t *flags, uint64_t n, uint64_t *out, uint64_t *d_count) {
