@@ -143,10 +143,10 @@ def test_queued_join_route_group_bitmap_modes(provider, monkeypatch, mode):
     """Grouped heads over a small domain find their new rows by per-group LDS bitmaps.
     XLOG_HIP_GROUP_BITMAP: 0 sort + set difference instead; 1 R's rows read from its two runs; 2 from R
     as a bit matrix that every iteration brings up to date, the runs merged as before; 3 (the default)
-    R kept only in the matrix during a queue by heads that no index reads in full, its new rows emitted
-    and merged once at the queue's end, the matrix kept between queues while R is unchanged.  Each mode
-    with the queue's own bounds and with bounds shrunk so that queues stop and host iterations come
-    between them (the matrix is then rebuilt); every result is the oracle's."""
+    R kept only in the matrix, from queue to queue, by heads that no index reads in full, and written
+    back to R's runs when a host iteration or the end of the fixpoint reads them.  Each mode with the
+    queue's own bounds and with bounds shrunk so that queues stop and host iterations come between them
+    (R's runs written back, the matrix rebuilt after the host iteration); every result is the oracle's."""
     p = provider
     monkeypatch.setenv("XLOG_HIP_GROUP_BITMAP", mode)
     for name, plan, rels, idb in _programs() + _nonlinear_programs():

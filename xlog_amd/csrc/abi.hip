@@ -1917,13 +1917,15 @@ struct Driver {
     std::vector<DRel> small;
     bool q_learned = false;  // the last queue stopped and its counts changed the bounds' inputs
     // R of a head as a bit matrix (domain rows of ceil(domain / 64) u64 words) for the queue's group
-    // bitmaps: m[cur] holds R as it stood when full[p] and small[p] had versions vfull and vsmall;
-    // m[cur ^ 1] and `start` are the queue's working copies
+    // bitmaps: m[cur] holds R as it stood when full[p] and small[p] had versions vfull and vsmall, or,
+    // with `lags`, R of `rows` rows while full[p] and small[p] still hold R as it was then (a queue that
+    // kept R only in the matrix adds its rows there; bitr_settle writes them back); m[cur ^ 1] is the
+    // queue's working copy
     struct BitR {
-        Buf<uint64_t> m[2], start;
+        Buf<uint64_t> m[2];
         int cur = 0;
-        uint64_t vfull = 0, vsmall = 0, domain = 0;
-        bool valid = false;
+        uint64_t vfull = 0, vsmall = 0, domain = 0, rows = 0;
+        bool valid = false, lags = false;
     };
     std::vector<BitR> bitr;
     bool bitr_current(uint32_t p) const {
@@ -1934,6 +1936,29 @@ struct Driver {
         bitr[p].valid = true;
         bitr[p].vfull = full[p].version;
         bitr[p].vsmall = small[p].version;
+    }
+    // R's rows, and those past the base run (the recent run's, or what the matrix holds past the base run)
+    uint64_t r_rows(int p) const {
+        return (size_t)p < bitr.size() && bitr[p].lags ? bitr[p].rows : full[p].n + small[p].n;
+    }
+    uint64_t recent_rows(int p) const { return r_rows(p) - full[p].n; }
+    // R's runs brought up to the matrix: R emitted from it in order as one base run
+    void bitr_settle(uint32_t p) {
+        if (p >= bitr.size() || !bitr[p].lags) return;
+        BitR &b = bitr[p];
+        DRel r;
+        r.n = bitmap_emit(ctx, b.m[b.cur].p, (uint32_t)b.domain, (b.domain + 63) / 64, &r.k, XLOG_HIP_KERNEL_MERGE,
+                          b.rows);
+        r.owned = r.k != nullptr;
+        r.version = version_counter++;
+        release(full[p]);
+        release(small[p]);
+        full[p] = r;
+        b.lags = false;
+        bitr_stamp(p);
+    }
+    void bitr_settle_all() {
+        for (uint32_t p = 0; p < bitr.size(); ++p) bitr_settle(p);
     }
 
     ~Driver() {
@@ -2510,6 +2535,7 @@ struct Driver {
         while (it < max_iter) {
             const uint64_t done = run_queue(std::min<uint64_t>(qmax, max_iter - it), it, heads, hidx, deltas, qr);
             if (done == ~0ull) {  // converged inside the queue (it counts the empty iteration)
+                bitr_settle_all();
                 compact_all();
                 return it;
             }
@@ -2525,11 +2551,13 @@ struct Driver {
             }
             retried = false;
             // an iteration whose queue stopped at once, or one for which no queue fits (one run of R)
+            bitr_settle_all();
             compact_all();
             ++it;
             if (iterate_host(it, deltas, qr) == 0) return it;
         }
         cur_iter = it;
+        bitr_settle_all();
         throw Error{XLOG_HIP_ITERATION_LIMIT,
                     "Recursive SCC iteration limit (" + std::to_string(max_iter) + ") exceeded"};
     }
@@ -2546,7 +2574,7 @@ struct Driver {
         // small[p] takes every delta (merge) and is merged into the base run here once it holds more than a
         // quarter of it, so the merges of a queue rewrite the recent run instead of all of R
         for (int p : heads)
-            if (small[p].n > full[p].n / 4) compact((uint32_t)p);
+            if (!bitr[p].lags && small[p].n > full[p].n / 4) compact((uint32_t)p);
         // the variants (one per IDB atom of a recursive rule, that atom first), the fixed indexes of
         // their EDB atoms, and an index per IDB relation (and column) that a variant reads in full,
         // rebuilt on the device at the start of every iteration from R's two runs
@@ -2611,10 +2639,10 @@ struct Driver {
             gsrc[hidx[vp->head]] = hidx[vp->dpred];
         }
         // A grouped head over a domain of at most 2^17 values takes the group bitmaps instead of the sort
-        // and the set difference, reading R's rows from R as a bit matrix (domain^2 / 8 bytes, three copies,
+        // and the set difference, reading R's rows from R as a bit matrix (domain^2 / 8 bytes, two copies,
         // when that is at most an eighth of the room left) that each iteration brings up to date.  Such a
-        // head that no index of the queue reads in full keeps R only in the matrix while the queue runs (no
-        // merges): the queue's new rows are emitted from it at the end and merged into the recent run once.
+        // head that no index of the queue reads in full keeps R only in the matrix (no merges), from queue
+        // to queue, until a host iteration or the end of the fixpoint needs R's runs (bitr_settle).
         // XLOG_HIP_GROUP_BITMAP: 0 never; 1 group bitmaps over R's runs (no matrix); 2 the matrix with R's
         // runs merged every iteration; unset or 3 all of it.
         const uint64_t gb_mode = env_u64("XLOG_HIP_GROUP_BITMAP", 3);
@@ -2628,28 +2656,26 @@ struct Driver {
             BitR &b = bitr[p];
             if (b.domain != domain) b = BitR();
             if (!b.m[0].p) {
-                if (24 * cells > device_room(ctx) / 8) continue;
+                if (16 * cells > device_room(ctx) / 8) continue;
                 b.m[0] = Buf<uint64_t>(ctx, cells);
                 b.m[1] = Buf<uint64_t>(ctx, cells);
-                b.start = Buf<uint64_t>(ctx, cells);
                 b.domain = domain;
             }
             if (!bitr_current((uint32_t)p)) {
                 b.cur = 0;
-                rows_to_bits(ctx, full[p].k ? full[p].k : b.start.p, full[p].n, small[p].k ? small[p].k : b.start.p,
+                rows_to_bits(ctx, full[p].k ? full[p].k : b.m[1].p, full[p].n, small[p].k ? small[p].k : b.m[1].p,
                              small[p].n, (uint32_t)domain, b.m[0].p);
                 bitr_stamp((uint32_t)p);
             }
-            // the other copy starts equal (each iteration writes it from the current one), and the rows at
-            // the queue's start are kept for the emit
+            // the other copy starts equal (each iteration writes it from the current one)
             XH_CHECK_HIP(hipMemcpyAsync(b.m[b.cur ^ 1].p, b.m[b.cur].p, cells * sizeof(uint64_t),
                                         hipMemcpyDeviceToDevice, ctx->stream));
-            XH_CHECK_HIP(hipMemcpyAsync(b.start.p, b.m[b.cur].p, cells * sizeof(uint64_t), hipMemcpyDeviceToDevice,
-                                        ctx->stream));
             mh[h] = 1;
             bm[h] = gb_mode >= 3;
             for (auto &dp : dyns) bm[h] &= dp->pred != p;
         }
+        for (uint32_t h = 0; h < H; ++h)
+            if (!bm[h]) bitr_settle((uint32_t)heads[h]);  // this queue reads or merges R's runs
         // every block comes back in one read of the pinned staging
         const uint64_t fit = (Ctx::HOST_STAGE_U64 - 1) / B;  // blocks that fit, the starting one included
         if (fit < 3) return 0;
@@ -2690,7 +2716,7 @@ struct Driver {
             }
             // an IDB relation read in full: its rows per distinct value (at most the domain's)
             const int q = qr[v.ri].b[j].pred;
-            const double rows = (double)(full[q].n + small[q].n);
+            const double rows = (double)r_rows(q);
             const double keys = std::max(1.0, std::min(rows, domain ? (double)domain : rows));
             return std::max(1.0, rows / keys);
         };
@@ -2703,7 +2729,7 @@ struct Driver {
         std::vector<std::vector<uint64_t>> Lb, Cb, Rb;
         std::vector<std::vector<std::array<uint64_t, MAX_BODY>>> T;
         Rb.push_back({});  // (bounds of the recent run)
-        for (int p : heads) Rb[0].push_back(small[p].n);
+        for (int p : heads) Rb[0].push_back(recent_rows(p));
         std::vector<uint64_t> cur(H);
         for (uint32_t h = 0; h < H; ++h) cur[h] = delta[heads[h]].n;  // exact for the first
         const uint64_t room = device_room(ctx) / 2;
@@ -2712,7 +2738,7 @@ struct Driver {
         std::vector<uint64_t> dmax(H, ~0ull);
         if (domain && domain <= (1ull << 31))
             for (uint32_t h = 0; h < H; ++h)
-                dmax[h] = domain * domain - std::min(domain * domain, full[heads[h]].n + small[heads[h]].n);
+                dmax[h] = domain * domain - std::min(domain * domain, r_rows(heads[h]));
         uint64_t q = 0;
         for (; q < qn; ++q) {
             std::vector<uint64_t> lb = cur, cb(H, 0), rb(H, 0);
@@ -2729,7 +2755,7 @@ struct Driver {
                     double g = 1.0;
                     if (v.dyn[j] >= 0) {
                         const int pq = r.b[j].pred;
-                        const double r0 = (double)std::max<uint64_t>(full[pq].n + small[pq].n, 1);
+                        const double r0 = (double)std::max<uint64_t>(r_rows(pq), 1);
                         g = std::max(1.0, (double)(full[pq].n + Rb.back()[hidx[pq]]) / r0);
                     }
                     t = std::min(t * fan(v, j) * g * M + (double)SLACK, (double)SORT_MAX);
@@ -2822,7 +2848,7 @@ struct Driver {
         // block -1: the sizes the queue starts from
         for (uint32_t h = 0; h < H; ++h) {
             fill_u64(ctx, qs.p + blk(-1) + h, delta[heads[h]].n, 1);
-            fill_u64(ctx, qs.p + blk(-1) + H + h, small[heads[h]].n, 1);
+            fill_u64(ctx, qs.p + blk(-1) + H + h, recent_rows(heads[h]), 1);
         }
         Buf<uint64_t> gscratch(ctx, 2 * (uint64_t)H);
         Buf<uint64_t> tcount(ctx, 1);  // the size of an empty base run
@@ -2999,20 +3025,9 @@ struct Driver {
             for (uint32_t h = 0; h < H; ++h) {
                 const int p = heads[h];
                 if (bm[h]) {
-                    // the queue's new rows: R's matrix after the last completed iteration less its rows at
-                    // the start, emitted in order and merged into the recent run
-                    const uint64_t added = bk[H + h] - small[p].n;
-                    if (added) {
-                        bits_andnot(ctx, mat(h, (uint64_t)last + 1), bitr[p].start.p, cells);
-                        DRel add;
-                        add.n = bitmap_emit(ctx, bitr[p].start.p, (uint32_t)domain, bw, &add.k, XLOG_HIP_KERNEL_MERGE,
-                                            added);
-                        add.owned = true;
-                        DRel m = merge(small[p], add);
-                        release(small[p]);
-                        release(add);
-                        small[p] = m;
-                    }
+                    // R stays in the matrix (its runs lag it until bitr_settle)
+                    bitr[p].rows = r_rows(p) + (bk[H + h] - recent_rows(p));
+                    bitr[p].lags = true;
                 } else {
                     release(small[p]);
                     small[p].n = bk[H + h];

@@ -417,8 +417,6 @@ void rows_to_bits(Ctx *ctx, const uint64_t *base, uint64_t nbase, const uint64_t
 // values copied from src to dst (nothing once *stop is set).
 void copy_group_rows(Ctx *ctx, const uint32_t *run_key, const uint64_t *d_n, uint64_t bound, uint32_t domain,
                      const uint64_t *src, uint64_t *dst, const uint32_t *stop);
-// s = a & ~s over n u64 words (the bits a sets that s does not)
-void bits_andnot(Ctx *ctx, const uint64_t *a, uint64_t *s, uint64_t n);
 
 // In-place exclusive scan of u32 values (prefixes wrap modulo 2^32); the
 // exact u64 sum goes to *d_total (device).  One pass, decoupled look-back.

@@ -1260,17 +1260,6 @@ void copy_group_rows(Ctx *ctx, const uint32_t *run_key, const uint64_t *d_n, uin
                        d_n, bound, words, src, dst, stop);
     XH_CHECK_HIP(hipGetLastError());
 }
-// s = a & ~s over n words
-__global__ void k_bits_andnot(const uint64_t *__restrict__ a, uint64_t *__restrict__ s, uint64_t n) {
-    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
-        s[i] = a[i] & ~s[i];
-}
-void bits_andnot(Ctx *ctx, const uint64_t *a, uint64_t *s, uint64_t n) {
-    if (n == 0) return;
-    Prof prof(ctx, XLOG_HIP_KERNEL_MERGE, 24.0 * (double)n);
-    hipLaunchKernelGGL(k_bits_andnot, dim3(grid_for(n, 256, 8192)), dim3(256), 0, ctx->stream, a, s, n);
-    XH_CHECK_HIP(hipGetLastError());
-}
 void select_flags(Ctx *ctx, const uint64_t *k, const uint8_t *flags, uint64_t n, uint64_t *out, uint64_t *d_count) {
     run_select(ctx, k, n, SelFlags{flags, out}, d_count);
 }
