@@ -138,17 +138,22 @@ def test_queued_join_route_stops_and_resumes(provider, monkeypatch, margin, slac
         _check(p, name, plan, rels, idb, oracle.seminaive(plan, rels))
 
 
-@pytest.mark.parametrize("mode", ["0", "1", "2", "3"])
-def test_queued_join_route_group_bitmap_modes(provider, monkeypatch, mode):
+@pytest.mark.parametrize("mode,filt", [("0", "1"), ("1", "1"), ("2", "1"), ("3", "1"), ("3", "0"), ("0", "0")])
+def test_queued_join_route_group_bitmap_modes(provider, monkeypatch, mode, filt):
     """Grouped heads over a small domain find their new rows by per-group LDS bitmaps.
     XLOG_HIP_GROUP_BITMAP: 0 sort + set difference instead; 1 R's rows read from its two runs; 2 from R
     as a bit matrix that every iteration brings up to date, the runs merged as before; 3 (the default)
     R kept only in the matrix, from queue to queue, by heads that no index reads in full, and written
-    back to R's runs when a host iteration or the end of the fixpoint reads them.  Each mode with the
-    queue's own bounds and with bounds shrunk so that queues stop and host iterations come between them
-    (R's runs written back, the matrix rebuilt after the host iteration); every result is the oracle's."""
+    back to R's runs when a host iteration or the end of the fixpoint reads them.  Heads whose
+    candidates are not grouped (left-linear closure, same generation, the non-linear programs) filter
+    their join outputs against R's matrix and the outputs already taken, and every step before a last
+    one drops repeated outputs (XLOG_HIP_JOIN_FILTER=0: sort + set difference instead).  Each setting
+    with the queue's own bounds and with bounds shrunk so that queues stop and host iterations come
+    between them (R's runs written back, the matrix rebuilt after the host iteration); every result is
+    the oracle's."""
     p = provider
     monkeypatch.setenv("XLOG_HIP_GROUP_BITMAP", mode)
+    monkeypatch.setenv("XLOG_HIP_JOIN_FILTER", filt)
     for name, plan, rels, idb in _programs() + _nonlinear_programs():
         ref = oracle.seminaive(plan, rels)
         for stops in (False, True):
@@ -158,7 +163,7 @@ def test_queued_join_route_group_bitmap_modes(provider, monkeypatch, mode):
             else:
                 monkeypatch.delenv("XLOG_HIP_JOIN_QUEUE_MARGIN_PCT", raising=False)
                 monkeypatch.delenv("XLOG_HIP_JOIN_QUEUE_SLACK", raising=False)
-            _note(f"join queue group bitmap mode={mode} {name} stops={stops}")
+            _note(f"join queue group bitmap mode={mode} filter={filt} {name} stops={stops}")
             _check(p, name, plan, rels, idb, ref)
 
 

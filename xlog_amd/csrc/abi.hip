@@ -1829,6 +1829,30 @@ __global__ void k_q_step(QStep a, uint32_t *stop, uint32_t code) {
     *a.slot = t;
     if (a.base_out) *a.base_out = b + t;
 }
+// A filtered join step (its outputs appended at *taken): before the emit, the
+// bag within the join-row limit and the count before it; after, its outputs
+// (the count's growth) in its slot, and the count within the buffer.
+struct QFilt {
+    const uint64_t *bag;
+    uint64_t *taken, *before, *slot;
+    uint64_t limit, cap;
+};
+__global__ void k_q_fstart(QFilt a, uint32_t *stop, uint32_t code) {
+    if (*stop) return;
+    const uint64_t t = *a.bag;
+    if (a.limit && t > a.limit) {
+        *a.slot = t;
+        atomicCAS(stop, 0u, code);
+        return;
+    }
+    *a.before = *a.taken;
+}
+__global__ void k_q_fend(QFilt a, uint32_t *stop, uint32_t code) {
+    if (*stop) return;
+    const uint64_t t = *a.taken;
+    *a.slot = t - *a.before;
+    if (t > a.cap) atomicCAS(stop, 0u, code);
+}
 // After the set differences, before the merges: the iteration's delta total,
 // and every head's R after the merge, which must fit its bound.
 constexpr uint32_t QMAX_HEADS = 16;
@@ -2649,9 +2673,23 @@ struct Driver {
         const bool gb_on = gb_mode != 0 && domain && domain <= (1ull << 17);
         const uint32_t bw = (uint32_t)((domain + 63) / 64);
         const uint64_t cells = domain * bw;
-        std::vector<char> mh(H, 0), bm(H, 0);  // R as a bit matrix; R only as the matrix
-        for (uint32_t h = 0; h < H && gb_on && gb_mode >= 2; ++h) {
-            if (!grouped[h]) continue;
+        // A head whose candidates are not grouped, over a domain whose bit matrix takes at most 128 MiB,
+        // filters its join outputs as they are emitted (XLOG_HIP_JOIN_FILTER=0: never): an output already in
+        // R (R's bit matrix, kept like the group bitmaps') or already emitted in the iteration (a bit matrix
+        // of the outputs taken, claimed by atomic OR) is dropped, so the candidates are the new rows, each
+        // once, and sorted they are the delta.  Every join step before a last one drops its repeated
+        // outputs the same way.  (The bags are still counted for the join-row limit.)
+        bool filt_on = env_u64("XLOG_HIP_JOIN_FILTER", 1) != 0 && domain && cells * 8 <= (128ull << 20);
+        if (filt_on) {  // (R's two copies and the outputs taken per filtered head, one per step before a last)
+            uint64_t nm = 0;
+            for (uint32_t h = 0; h < H; ++h) nm += grouped[h] ? 0 : 3;
+            for (auto &vp : vars) nm += (uint64_t)(qr[vp->ri].nb - 2);
+            filt_on = nm * cells * 8 <= device_room(ctx) / 8;
+        }
+        std::vector<char> mh(H, 0), bm(H, 0), fh(H, 0);  // R as a bit matrix; R only as the matrix; filtered
+        for (uint32_t h = 0; h < H; ++h) {
+            const bool g = grouped[h] && gb_on && gb_mode >= 2, f = !grouped[h] && filt_on;
+            if (!g && !f) continue;
             const int p = heads[h];
             BitR &b = bitr[p];
             if (b.domain != domain) b = BitR();
@@ -2671,7 +2709,8 @@ struct Driver {
             XH_CHECK_HIP(hipMemcpyAsync(b.m[b.cur ^ 1].p, b.m[b.cur].p, cells * sizeof(uint64_t),
                                         hipMemcpyDeviceToDevice, ctx->stream));
             mh[h] = 1;
-            bm[h] = gb_mode >= 3;
+            fh[h] = f;
+            bm[h] = f || gb_mode >= 3;
             for (auto &dp : dyns) bm[h] &= dp->pred != p;
         }
         for (uint32_t h = 0; h < H; ++h)
@@ -2759,6 +2798,9 @@ struct Driver {
                         g = std::max(1.0, (double)(full[pq].n + Rb.back()[hidx[pq]]) / r0);
                     }
                     t = std::min(t * fan(v, j) * g * M + (double)SLACK, (double)SORT_MAX);
+                    // filtered outputs are distinct pairs of the domain (and a last step's not in R)
+                    if (filt_on && (j < r.nb - 1 || fh[hidx[v.head]]))
+                        t = std::min(t, (double)(j < r.nb - 1 ? domain * domain : std::max<uint64_t>(dmax[hidx[v.head]], 1)));
                     tv[vi][j] = (uint64_t)t;
                 }
                 cb[hidx[v.head]] += tv[vi][r.nb - 1];
@@ -2870,6 +2912,23 @@ struct Driver {
         // iteration k reads R's matrix M(k) and writes M(k + 1) (the two copies alternate): a stopped
         // iteration leaves M(k), R after the last completed one, as it was
         auto mat = [&](uint32_t h, uint64_t k) { BitR &b = bitr[heads[h]]; return b.m[(b.cur + k) & 1].p; };
+        // the filters' bit matrices of the outputs taken (zero here; after every iteration the rows taken
+        // clear their words again) and their counters, per iteration, variant and step: [0] the outputs
+        // taken by a step before the last, [1] the count before the step
+        std::vector<Buf<uint64_t>> seen_h(H);
+        std::vector<std::array<Buf<uint64_t>, MAX_BODY>> seen_s(vars.size());
+        for (uint32_t h = 0; h < H; ++h)
+            if (fh[h]) {
+                seen_h[h] = Buf<uint64_t>(ctx, cells);
+                fill_u64(ctx, seen_h[h].p, 0ull, cells);
+            }
+        for (size_t vi = 0; vi < vars.size() && filt_on; ++vi)
+            for (int j = 1; j + 1 < qr[vars[vi]->ri].nb; ++j) {
+                seen_s[vi][j] = Buf<uint64_t>(ctx, cells);
+                fill_u64(ctx, seen_s[vi][j].p, 0ull, cells);
+            }
+        Buf<uint64_t> fcnt(ctx, Q * vars.size() * MAX_BODY * 2);
+        fill_u64(ctx, fcnt.p, 0ull, Q * vars.size() * MAX_BODY * 2);
 
         // ---- the queue -------------------------------------------------------------
         cur_iter = it + 1;
@@ -2914,19 +2973,40 @@ struct Driver {
                     probe_prepare_deferred(ctx, job, left_bound, d_left, stop, j == 1 ? code : 0u);
                     const uint64_t *d_tot = job.toff.p + job.tiles;
                     const bool last = j == r.nb - 1;
-                    // the output must fit its buffer (and the launches after it their bounds), a join the
-                    // limit, and the candidates one sort
-                    QStep qsd{d_tot, last ? base_in : nullptr, last ? base_in + 1 : nullptr,
-                              bk + v.tot_slot + (j - 1), last ? Cb[k][hh] : T[k][vi][j], max_join_rows};
-                    hipLaunchKernelGGL(k_q_step, dim3(1), dim3(1), 0, ctx->stream, qsd, stop, code);
-                    XH_CHECK_HIP(hipGetLastError());
                     const int oc[4] = {st.sel[0], st.sel[1], 0, 0};
                     uint64_t *out = last ? qh[hh]->C.p : v.tmp[j].p;
-                    probe_emit_dev(ctx, job, d_left, oc, out, last ? base_in : nullptr, stop);
+                    if (filt_on && (!last || fh[hh])) {
+                        // the bag within the join-row limit; its outputs filtered and appended (a last step's
+                        // to the head's candidates), within their buffer
+                        uint64_t *fc = fcnt.p + ((k * vars.size() + vi) * MAX_BODY + (uint64_t)j) * 2;
+                        uint64_t *taken = last ? bk + base_off[hh] + nvar[hh] : fc;
+                        const uint64_t cap = last ? Cb[k][hh] : T[k][vi][j];
+                        QFilt qf{d_tot, taken, fc + 1, bk + v.tot_slot + (j - 1), max_join_rows, cap};
+                        hipLaunchKernelGGL(k_q_fstart, dim3(1), dim3(1), 0, ctx->stream, qf, stop, code);
+                        XH_CHECK_HIP(hipGetLastError());
+                        const EmitFilter ef{last ? mat(hh, k) : nullptr, last ? seen_h[hh].p : seen_s[vi][j].p, taken,
+                                            cap, bw};
+                        probe_emit_dev(ctx, job, d_left, oc, out, nullptr, stop, &ef);
+                        hipLaunchKernelGGL(k_q_fend, dim3(1), dim3(1), 0, ctx->stream, qf, stop, code);
+                        XH_CHECK_HIP(hipGetLastError());
+                        d_left = taken;
+                    } else {
+                        // the output must fit its buffer (and the launches after it their bounds), a join the
+                        // limit, and the candidates one sort
+                        QStep qsd{d_tot, last ? base_in : nullptr, last ? base_in + 1 : nullptr,
+                                  bk + v.tot_slot + (j - 1), last ? Cb[k][hh] : T[k][vi][j], max_join_rows};
+                        hipLaunchKernelGGL(k_q_step, dim3(1), dim3(1), 0, ctx->stream, qsd, stop, code);
+                        XH_CHECK_HIP(hipGetLastError());
+                        probe_emit_dev(ctx, job, d_left, oc, out, last ? base_in : nullptr, stop);
+                        d_left = d_tot;
+                    }
                     left = out;
-                    d_left = d_tot;
                     left_bound = T[k][vi][j];
                 }
+                // the filtered steps' outputs clear the bits they took
+                for (int j = 1; j + 1 < r.nb && filt_on; ++j)
+                    rows_bits(ctx, v.tmp[j].p, fcnt.p + ((k * vars.size() + vi) * MAX_BODY + (uint64_t)j) * 2,
+                              T[k][vi][j], bw, seen_s[vi][j].p, true, stop);
             }
             // per head: sort the candidates, keep the unique ones not in R
             for (uint32_t h = 0; h < H; ++h) {
@@ -2936,6 +3016,18 @@ struct Driver {
                 const uint64_t *big = full[p].k ? full[p].k : qh[h]->R[1].p;
                 const uint64_t *rin = k == 0 ? small[p].k : qh[h]->R[(k - 1) & 1].p;
                 if (!rin) rin = qh[h]->R[1].p;  // an empty run read through its device count
+                if (fh[h]) {
+                    // the candidates are the new rows, each once: sorted, they are the delta.  They clear
+                    // the bits they took, and R's matrix for the next iteration, M(k + 1) (R before the
+                    // previous iteration), takes the previous delta and this one
+                    radix_sort_dev(ctx, &ka, &kb, Cb[k][h], d_cand, digits, stop);
+                    select_not_value(ctx, ka, Cb[k][h], ~0ull, qh[h]->D[k & 1].p, nD + h, d_cand, stop);
+                    rows_bits(ctx, qh[h]->D[k & 1].p, nD + h, Cb[k][h], bw, seen_h[h].p, true, stop);
+                    if (k > 0)
+                        rows_bits(ctx, qh[h]->D[(k - 1) & 1].p, pD + h, Cb[k - 1][h], bw, mat(h, k + 1), false, stop);
+                    rows_bits(ctx, qh[h]->D[k & 1].p, nD + h, Cb[k][h], bw, mat(h, k + 1), false, stop);
+                    continue;
+                }
                 if (gbound[h]) {
                     // per group (one high word, its runs listed), the new values by two LDS bitmaps, then
                     // the groups compacted in order; more groups than the domain stop the queue.  M(k + 1)

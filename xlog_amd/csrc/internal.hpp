@@ -417,6 +417,11 @@ void rows_to_bits(Ctx *ctx, const uint64_t *base, uint64_t nbase, const uint64_t
 // values copied from src to dst (nothing once *stop is set).
 void copy_group_rows(Ctx *ctx, const uint32_t *run_key, const uint64_t *d_n, uint64_t bound, uint32_t domain,
                      const uint64_t *src, uint64_t *dst, const uint32_t *stop);
+// The bits of packed rows (x << 32) | z, rows[0 .. *d_n) (at most bound), in a
+// bit matrix of `words` u64 words per row: set (atomic OR), or, with clear,
+// every word that holds one of them zeroed (nothing once *stop is set).
+void rows_bits(Ctx *ctx, const uint64_t *rows, const uint64_t *d_n, uint64_t bound, uint32_t words, uint64_t *bits,
+               bool clear, const uint32_t *stop);
 
 // In-place exclusive scan of u32 values (prefixes wrap modulo 2^32); the
 // exact u64 sum goes to *d_total (device).  One pass, decoupled look-back.
@@ -517,8 +522,20 @@ void probe_prepare_deferred(Ctx *ctx, ProbeJob &job, uint64_t n_bound, const uin
 // count on the device (d_n, at most job.n), two-column outputs (oc) written
 // to out + *d_out_base (d_out_base may be null), nothing when *stop is raised.
 // The caller has checked that the total fits the output.
+// With a filter (two-column outputs of ids below 64 * words): an output
+// already in R (bit set in rbits, a bit matrix of `words` u64 words per row;
+// may be null) or already taken (bit set in seen, which the emit sets) is
+// dropped, the others are appended in no set order at out[*count] (*count
+// advanced; positions at or past cap are counted and not written).
+struct EmitFilter {
+    const uint64_t *rbits;
+    uint64_t *seen;
+    uint64_t *count;
+    uint64_t cap;
+    uint32_t words;
+};
 void probe_emit_dev(Ctx *ctx, const ProbeJob &job, const uint64_t *d_n, const int oc[4], uint64_t *out,
-                    const uint64_t *d_out_base, uint32_t *stop);
+                    const uint64_t *d_out_base, uint32_t *stop, const EmitFilter *filter = nullptr);
 void probe_finish(ProbeJob &job, uint64_t n, uint64_t total);
 // The count pass alone, lookups recorded, no scan and no read-back; with gsel
 // set and gseg null the group heads count zero until probe_group_fixup gives

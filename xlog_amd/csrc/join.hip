@@ -161,6 +161,15 @@ struct ProbeArgs {
     uint32_t *stop;
     const uint64_t *d_out_base;
     uint32_t stop_code;
+    // optional output filter (EmitFilter), for two-column outputs of ids below 64 * fwords: an output
+    // (x, z) is dropped when bit z of row x is set in fr (R's bit matrix, may be null) or in fseen (the
+    // outputs already taken: the bit is claimed by an atomic OR); the others are appended to out0 at
+    // positions taken from *fcount (positions at or past fcap are counted, not written)
+    const uint64_t *fr;
+    unsigned long long *fseen;
+    unsigned long long *fcount;
+    uint64_t fcap;
+    uint32_t fwords;
 };
 // set in a row's start when its outputs come from gsrc
 constexpr uint64_t GROUP_BIT = 1ull << 63;
@@ -304,6 +313,32 @@ __device__ __forceinline__ void make_words(const OutSpec &o, const uint32_t v[4]
     else *w1 = 0;
 }
 
+// One output per lane through the filter (lanes with live = false only take
+// part in the wave's append): the wave's kept outputs take consecutive
+// positions from one atomic add.
+__device__ __forceinline__ void filter_append(const ProbeArgs &a, bool live, uint64_t w, uint64_t *__restrict__ out,
+                                              int lane) {
+    bool keep = false;
+    if (live) {
+        const uint64_t x = w >> 32;
+        const uint32_t z = (uint32_t)w;
+        const uint64_t idx = x * a.fwords + (z >> 6);
+        const unsigned long long m = 1ull << (z & 63u);
+        // (a plain read first: a bit once set stays set, so only a clear bit needs the atomic)
+        if (!(a.fr && (a.fr[idx] & m)) && !(a.fseen[idx] & m)) keep = !(atomicOr(&a.fseen[idx], m) & m);
+    }
+    const uint64_t bal = __ballot(keep);
+    if (!bal) return;
+    const int leader = __ffsll((unsigned long long)bal) - 1;
+    unsigned long long base = 0;
+    if (lane == leader) base = atomicAdd(a.fcount, (unsigned long long)__popcll(bal));
+    base = __shfl(base, leader, WAVE);
+    if (keep) {
+        const uint64_t pos = base + (uint64_t)__popcll(bal & ((1ull << lane) - 1ull));
+        if (pos < a.fcap) out[pos] = w;
+    }
+}
+
 // The outputs of one probe tile (k_probe_emit).
 struct EmitSmem {
     uint64_t wtot[JWAVES];
@@ -311,7 +346,7 @@ struct EmitSmem {
     uint64_t row[JWAVES][WAVE];
     uint64_t st[JWAVES][WAVE];
 };
-template <int ITEMS>
+template <int ITEMS, bool FILT = false>
 __device__ __forceinline__ void probe_emit_tile(const ProbeArgs &a, const uint64_t *__restrict__ tile_off, uint64_t t0,
                                                 uint64_t tile, const OutSpec &spec, uint64_t *__restrict__ out0,
                                                 uint64_t *__restrict__ out1, EmitSmem &sm, int tid, int lane,
@@ -391,6 +426,23 @@ __device__ __forceinline__ void probe_emit_tile(const ProbeArgs &a, const uint64
                 pay[u] = (live && !grp && a.payload) ? a.payload[bpos[u]] : 0u;
                 gw[u] = (live && grp) ? a.gsrc[bpos[u] & ~GROUP_BIT] : 0ull;
             }
+            if (FILT) {  // filtered two-column outputs, appended
+#pragma unroll
+                for (int u = 0; u < EMIT_UNROLL; ++u) {
+                    const uint64_t j = j0 + (uint64_t)u * WAVE;
+                    uint64_t w0 = 0, w1;
+                    if (j < total) {
+                        uint32_t v[4];
+                        v[0] = (uint32_t)(prow[u] >> 32);
+                        v[1] = (uint32_t)prow[u];
+                        v[2] = a.pcol ? (uint32_t)prow[u] : (uint32_t)(prow[u] >> 32);
+                        v[3] = pay[u];
+                        make_words(spec, v, &w0, &w1);
+                    }
+                    filter_append(a, j < total, w0, out0, lane);
+                }
+                continue;
+            }
 #pragma unroll
             for (int u = 0; u < EMIT_UNROLL; ++u) {
                 const uint64_t j = j0 + (uint64_t)u * WAVE;
@@ -421,14 +473,14 @@ __device__ __forceinline__ void probe_emit_tile(const ProbeArgs &a, const uint64
 // first output of tile t0.  With a device row count (a.d_n; a.n is then the
 // bound, t0 is 0) a grid of a few blocks per CU strides over the real tiles;
 // a.d_out_base then offsets the output.
-template <int ITEMS>
+template <int ITEMS, bool FILT = false>
 __global__ __launch_bounds__(JB) void k_probe_emit(ProbeArgs a, const uint64_t *__restrict__ tile_off, uint64_t t0,
                                                    OutSpec spec, uint64_t *__restrict__ out0,
                                                    uint64_t *__restrict__ out1) {
     __shared__ EmitSmem sm;
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
     if (!a.d_n) {
-        probe_emit_tile<ITEMS>(a, tile_off, t0, t0 + blockIdx.x, spec, out0, out1, sm, tid, lane, wave);
+        probe_emit_tile<ITEMS, FILT>(a, tile_off, t0, t0 + blockIdx.x, spec, out0, out1, sm, tid, lane, wave);
         return;
     }
     if (a.stop && *a.stop) return;
@@ -440,7 +492,7 @@ __global__ __launch_bounds__(JB) void k_probe_emit(ProbeArgs a, const uint64_t *
     }
     const uint64_t tiles = (a.n + tile_rows(ITEMS) - 1) / tile_rows(ITEMS);
     for (uint64_t t = blockIdx.x; t < tiles; t += gridDim.x) {
-        probe_emit_tile<ITEMS>(a, tile_off, 0, t, spec, out0, out1, sm, tid, lane, wave);
+        probe_emit_tile<ITEMS, FILT>(a, tile_off, 0, t, spec, out0, out1, sm, tid, lane, wave);
         __syncthreads();  // the shared arrays are reused by the next tile
     }
 }
@@ -763,7 +815,7 @@ void probe_prepare_deferred(Ctx *ctx, ProbeJob &job, uint64_t n_bound, const uin
 }
 
 void probe_emit_dev(Ctx *ctx, const ProbeJob &job, const uint64_t *d_n, const int oc[4], uint64_t *out,
-                    const uint64_t *d_out_base, uint32_t *stop) {
+                    const uint64_t *d_out_base, uint32_t *stop, const EmitFilter *filter) {
     if (job.n == 0 || job.tiles == 0 || !job.rec_cnt.p) return;  // nothing can match (see probe_prepare_deferred)
     ProbeArgs a = probe_args(job);
     a.pre_start = job.rec_start.p;  // the count pass's recorded lookups
@@ -771,12 +823,25 @@ void probe_emit_dev(Ctx *ctx, const ProbeJob &job, const uint64_t *d_n, const in
     a.d_n = d_n;
     a.stop = stop;
     a.d_out_base = d_out_base;
+    if (filter) {
+        XH_REQUIRE(!d_out_base && filter->seen && filter->count && filter->words, XLOG_HIP_INVALID_ARG,
+                   "filtered probe emit: appended output only");
+        a.fr = filter->rbits;
+        a.fseen = reinterpret_cast<unsigned long long *>(filter->seen);
+        a.fcount = reinterpret_cast<unsigned long long *>(filter->count);
+        a.fcap = filter->cap;
+        a.fwords = filter->words;
+    }
     OutSpec spec{2, {oc[0], oc[1], oc[2], oc[3]}};
     // per probe row its record (20 B with the row) and per match 12 B, counted on the device
     Prof prof(ctx, XLOG_HIP_KERNEL_PROBE_EMIT, 0.0);
     add_work_rows(ctx, prof.work(1.0), d_n, job.n, 20, job.toff.p + job.tiles, ~0ull, 12, nullptr, stop);
-    hipLaunchKernelGGL(k_probe_emit<JITEMS>, dim3(persistent_grid(ctx, job.tiles, 16)), dim3(JB), 0, ctx->stream, a,
-                       job.toff.p, 0ull, spec, out, nullptr);
+    if (filter)
+        hipLaunchKernelGGL((k_probe_emit<JITEMS, true>), dim3(persistent_grid(ctx, job.tiles, 16)), dim3(JB), 0,
+                           ctx->stream, a, job.toff.p, 0ull, spec, out, nullptr);
+    else
+        hipLaunchKernelGGL(k_probe_emit<JITEMS>, dim3(persistent_grid(ctx, job.tiles, 16)), dim3(JB), 0, ctx->stream,
+                           a, job.toff.p, 0ull, spec, out, nullptr);
     XH_CHECK_HIP(hipGetLastError());
 }
 void probe_finish(ProbeJob &job, uint64_t n, uint64_t total) {

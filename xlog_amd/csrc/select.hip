@@ -1260,6 +1260,25 @@ void copy_group_rows(Ctx *ctx, const uint32_t *run_key, const uint64_t *d_n, uin
                        d_n, bound, words, src, dst, stop);
     XH_CHECK_HIP(hipGetLastError());
 }
+__global__ void k_rows_bits(const uint64_t *__restrict__ rows, const uint64_t *d_n, uint64_t bound, uint32_t words,
+                            unsigned long long *__restrict__ bits, int clear, const uint32_t *stop) {
+    if (stop && *stop) return;
+    const uint64_t n = *d_n < bound ? *d_n : bound;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x) {
+        const uint64_t w = rows[i];
+        const uint64_t idx = (w >> 32) * words + ((uint32_t)w >> 6);
+        if (clear) bits[idx] = 0ull;
+        else atomicOr(&bits[idx], 1ull << ((uint32_t)w & 63u));
+    }
+}
+void rows_bits(Ctx *ctx, const uint64_t *rows, const uint64_t *d_n, uint64_t bound, uint32_t words, uint64_t *bits,
+               bool clear, const uint32_t *stop) {
+    if (bound == 0) return;
+    Prof prof(ctx, XLOG_HIP_KERNEL_SELECT, 0.0);
+    hipLaunchKernelGGL(k_rows_bits, dim3(grid_for(bound, 256, 2048)), dim3(256), 0, ctx->stream, rows, d_n, bound,
+                       words, reinterpret_cast<unsigned long long *>(bits), clear ? 1 : 0, stop);
+    XH_CHECK_HIP(hipGetLastError());
+}
 void select_flags(Ctx *ctx, const uint64_t *k, const uint8_t *flags, uint64_t n, uint64_t *out, uint64_t *d_count) {
     run_select(ctx, k, n, SelFlags{flags, out}, d_count);
 }
