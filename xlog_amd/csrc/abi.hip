@@ -2798,9 +2798,14 @@ struct Driver {
                         g = std::max(1.0, (double)(full[pq].n + Rb.back()[hidx[pq]]) / r0);
                     }
                     t = std::min(t * fan(v, j) * g * M + (double)SLACK, (double)SORT_MAX);
-                    // filtered outputs are distinct pairs of the domain (and a last step's not in R)
-                    if (filt_on && (j < r.nb - 1 || fh[hidx[v.head]]))
-                        t = std::min(t, (double)(j < r.nb - 1 ? domain * domain : std::max<uint64_t>(dmax[hidx[v.head]], 1)));
+                    // filtered outputs are distinct pairs of the domain (and a last step's not in R); a
+                    // filtered step not yet seen takes that bound when its buffer is small beside the room
+                    if (filt_on && (j < r.nb - 1 || fh[hidx[v.head]])) {
+                        const double cap = (double)(j < r.nb - 1 ? domain * domain
+                                                                 : std::max<uint64_t>(dmax[hidx[v.head]], 1));
+                        t = obs[v.ri][j].first == 0 && 8.0 * cap * (double)MAX_BODY <= (double)room / 16.0
+                                ? cap : std::min(t, cap);
+                    }
                     tv[vi][j] = (uint64_t)t;
                 }
                 cb[hidx[v.head]] += tv[vi][r.nb - 1];
@@ -2810,7 +2815,7 @@ struct Driver {
             std::vector<uint64_t> nxt(H);
             for (uint32_t h = 0; h < H; ++h) {
                 // (a delta never exceeds its head's candidates)
-                const double e = (double)cb[h] * nov[heads[h]];
+                const double e = (double)cb[h] * (fh[h] ? 1.0 : nov[heads[h]]);  // (filtered: all new)
                 nxt[h] = std::min<uint64_t>(std::max<uint64_t>(e > 1e18 ? (uint64_t)1e18 : (uint64_t)e, SLACK), cb[h]);
                 nxt[h] = std::min(nxt[h], dmax[h]);
                 rb[h] = Rb.back()[h] + nxt[h];
