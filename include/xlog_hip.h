@@ -373,7 +373,8 @@ xlog_hip_status xlog_hip_fixpoint_tc(xlog_hip_ctx *ctx, const xlog_hip_rel *edge
 #define XLOG_HIP_KERNEL_CHAIN_EMIT 10    /* dense chain-rule final emit */
 #define XLOG_HIP_KERNEL_HASH_INSERT 11   /* sparse delta step: expand + hash-set insert */
 #define XLOG_HIP_KERNEL_SORT_RUNS 12     /* sort of short runs by the low word */
-#define XLOG_HIP_KERNEL_KINDS 13
+#define XLOG_HIP_KERNEL_SORT_SEGMENTS 13 /* on-chip sort of top-16-bit segments */
+#define XLOG_HIP_KERNEL_KINDS 14
 xlog_hip_status xlog_hip_profile_enable(xlog_hip_ctx *ctx, int on);
 xlog_hip_status xlog_hip_profile_reset(xlog_hip_ctx *ctx);
 xlog_hip_status xlog_hip_profile_read(xlog_hip_ctx *ctx, uint32_t kind, uint64_t *launches, double *total_ms,

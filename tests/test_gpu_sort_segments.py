@@ -1,0 +1,193 @@
+"""GPU parity of the segment route of the radix sort.
+
+A keys-only sort of the whole key over at least 2^26 keys (XLOG_HIP_SORT_SEG_MIN
+lowers the bound so that these tests take the route at 2^22 keys) whose
+histograms of digits 6 and 7 predict segments of at most 0.85 x 5,120 keys
+(xlog_amd/csrc/sort.hip, segment_route) takes two digit passes, which order
+the keys by their top 16 bits, then sorts every segment of equal top 16 bits on
+chip (select.hip, k_seg_sort: one counting pass through LDS over the 2,048
+bins of bits 37..47, every bin ranked by the whole key, and the unique keys
+written at an offset from decoupled look-back, for sort + dedup).  A segment of
+more than 5,120 keys, or a bin of more than 256 keys that are not all equal,
+makes the sort run every digit's pass instead.  Each case is checked against numpy (sort) and the oracle
+(sort + dedup); the route it took is read from the kernel profile."""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from xlog_amd import datagen
+
+pytestmark = pytest.mark.gpu
+
+N = 1 << 22
+U64 = np.uint64
+
+
+def _note(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _route(p, fn):
+    p.profile_reset()
+    p.profile_enable(True)
+    try:
+        out = fn()
+        prof = p.profile_read()
+    finally:
+        p.profile_enable(False)
+    return out, prof["sort_segments"]["launches"], prof["sort_pass"]["launches"], prof["sort_runs"]["launches"]
+
+
+def _check(p, keys, want_segments, want_passes, want_runs=0):
+    """dedup_full_row against the oracle and the full-key sort against numpy, both with the expected route."""
+    exp = oracle.sort_dedup(keys)
+    got, segs, passes, runs = _route(p, lambda: p.download_packed(p.dedup_full_row(p.create_buffer_from_packed(keys))))
+    assert np.array_equal(got, exp)
+    assert (segs, passes, runs) == (want_segments, want_passes, want_runs)
+    srt, segs, passes, runs = _route(
+        p, lambda: p.download_packed(p.sort(p.create_buffer_from_packed(keys), [0, 1])))
+    assert np.array_equal(srt, np.sort(keys))
+    assert (segs, passes, runs) == (want_segments, want_passes, want_runs)
+
+
+@pytest.fixture
+def seg_min(monkeypatch):
+    monkeypatch.setenv("XLOG_HIP_SORT_SEG_MIN", str(N))
+
+
+@pytest.mark.parametrize("n", [N, N + 12345, 3 * N - 7])
+def test_uniform_keys_take_segment_route(provider, seg_min, n):
+    """Uniform 64-bit keys: two digit passes and one segment pass."""
+    _note(f"segment sort: uniform n={n}")
+    keys = np.random.default_rng(n).integers(0, 1 << 64, size=n, dtype=U64)
+    _check(provider, keys, 1, 2)
+
+
+def test_c3_shaped_duplicates(provider, seg_min):
+    """C3's generator (30 % exact duplicates) at 2^23 tuples."""
+    n = 2 * N
+    _note(f"segment sort: c3-shaped n={n}")
+    _check(provider, datagen.dup_tuples(n, datagen.seed_for(3)), 1, 2)
+
+
+def test_default_bound_takes_route_at_2_26(provider):
+    """Without the override the route starts at 2^26 keys (C3-shaped tuples)."""
+    n = 1 << 26
+    _note(f"segment sort: default bound n={n}")
+    keys = datagen.dup_tuples(n, 26)
+    got, segs, passes, runs = _route(
+        provider, lambda: provider.download_packed(provider.dedup_full_row(provider.create_buffer_from_packed(keys))))
+    assert (segs, passes, runs) == (1, 2, 0)
+    assert np.array_equal(got, oracle.sort_dedup(keys))
+
+
+def test_constant_middle_bits(provider, seg_min):
+    """Bits 32..47 constant: every segment is one bin (about 64 keys) ranked by the whole key."""
+    rng = np.random.default_rng(3247)
+    top = rng.integers(0, 1 << 16, size=N, dtype=U64)
+    keys = (top << U64(48)) | (U64(0xABCD) << U64(32)) | rng.integers(0, 1 << 32, size=N, dtype=U64)
+    _note("segment sort: constant bits 32..47")
+    _check(provider, keys, 1, 2)
+
+
+def test_one_constant_middle_digit(provider, seg_min):
+    """Bits 40..47 constant: the bins of bits 37..47 use 8 of their 2,048 values (bins of about 8 keys)."""
+    rng = np.random.default_rng(4047)
+    keys = rng.integers(0, 1 << 64, size=N, dtype=U64)
+    keys = (keys & ~(U64(0xFF) << U64(40))) | (U64(0x5A) << U64(40))
+    _note("segment sort: constant bits 40..47")
+    _check(provider, keys, 1, 2)
+
+
+def test_runs_of_exactly_256(provider, seg_min):
+    """2^14 high words with distinct bits 37..63, each carrying exactly 256 keys: the longest bins (keys that
+    share bits 37..63) the segment pass ranks; segments hold a few of them, within capacity."""
+    rng = np.random.default_rng(256)
+    top = rng.permutation(np.unique(rng.integers(0, 1 << 27, size=N // 128, dtype=U64)))[: N // 256]
+    hi = (top << U64(5)) | rng.integers(0, 32, size=len(top), dtype=U64)
+    keys = (np.repeat(hi, 256) << U64(32)) | rng.integers(0, 1 << 32, size=N, dtype=U64)
+    rng.shuffle(keys)
+    _note("segment sort: runs of 256")
+    _check(provider, keys, 1, 2)
+
+
+def test_long_bin_of_equal_keys(provider, seg_min):
+    """One key repeated 3,000 times: a bin above 256 keys whose keys are all equal stays on the route."""
+    rng = np.random.default_rng(3000)
+    keys = rng.integers(0, 1 << 64, size=N, dtype=U64)
+    keys[rng.choice(N, 3000, replace=False)] = U64(0x0123456789ABCDEF)
+    _note("segment sort: 3,000 equal keys")
+    _check(provider, keys, 1, 2)
+
+
+def test_run_of_257_falls_back(provider, seg_min):
+    """One high word carries 257 keys (not all equal): the segment pass flags its bin and every digit takes its
+    pass."""
+    rng = np.random.default_rng(257)
+    keys = rng.integers(0, 1 << 64, size=N + 1, dtype=U64)
+    keys[rng.choice(N + 1, 257, replace=False)] = (U64(0xDEADBEEF) << U64(32)) | rng.integers(
+        0, 1 << 32, size=257, dtype=U64)
+    _note("segment sort: a run of 257")
+    _check(provider, keys, 1, 2 + 8)
+
+
+@pytest.mark.parametrize("extra", [5120 - 64, 5121])
+def test_segment_at_capacity(provider, seg_min, extra):
+    """One top-16-bit value carries about `extra` + 64 keys: 5,120 keys are sorted on chip, more fall back."""
+    rng = np.random.default_rng(extra)
+    keys = rng.integers(0, 1 << 64, size=N, dtype=U64)
+    top = U64(0x1234)
+    have = int(np.count_nonzero((keys >> U64(48)) == top))
+    idx = rng.choice(np.flatnonzero((keys >> U64(48)) != top), extra + 64 - have, replace=False)
+    keys[idx] = (top << U64(48)) | rng.integers(0, 1 << 48, size=len(idx), dtype=U64)
+    size = int(np.count_nonzero((keys >> U64(48)) == top))
+    _note(f"segment sort: a segment of {size} keys")
+    _check(provider, keys, 1, 2 if size <= 5120 else 2 + 8)
+
+
+def test_correlated_top_digits_fall_back(provider, seg_min):
+    """Top 16 bits x * 0x0101: each digit looks uniform (estimate 64 keys per segment), the 256 segments hold
+    n / 256 keys each: every segment is above capacity and the sort runs every digit."""
+    rng = np.random.default_rng(77)
+    x = rng.integers(0, 256, size=N + 3, dtype=U64)
+    keys = ((x * U64(0x0101)) << U64(48)) | rng.integers(0, 1 << 48, size=N + 3, dtype=U64)
+    _note("segment sort: correlated top digits")
+    _check(provider, keys, 1, 2 + 8)
+
+
+def test_skewed_top_bits_keep_other_routes(provider, seg_min):
+    """Half the keys below 2^48: the estimate rules the segment route out before any pass."""
+    rng = np.random.default_rng(5)
+    keys = rng.integers(0, 1 << 64, size=N + 5, dtype=U64)
+    keys[: (N + 5) // 2] &= U64((1 << 48) - 1)
+    _note("segment sort: skewed top bits")
+    exp = oracle.sort_dedup(keys)
+    got, segs, _, _ = _route(provider, lambda: provider.download_packed(
+        provider.dedup_full_row(provider.create_buffer_from_packed(keys))))
+    assert segs == 0
+    assert np.array_equal(got, exp)
+
+
+def test_index_order(provider, seg_min, monkeypatch):
+    """XLOG_HIP_SORT_TICKETS=0: the segment unique takes its segments in workgroup-index order."""
+    keys = datagen.dup_tuples(N + 777, 11)
+    monkeypatch.setenv("XLOG_HIP_SORT_TICKETS", "0")
+    _note("segment sort: index order")
+    got, segs, passes, _ = _route(provider, lambda: provider.download_packed(
+        provider.dedup_full_row(provider.create_buffer_from_packed(keys))))
+    assert (segs, passes) == (1, 2)
+    assert np.array_equal(got, oracle.sort_dedup(keys))
+
+
+def test_route_off_matches(provider, seg_min, monkeypatch):
+    """XLOG_HIP_SORT_SEGMENTS=0 turns the route off; the result is the same."""
+    keys = datagen.dup_tuples(N + 99, 12)
+    on = provider.download_packed(provider.dedup_full_row(provider.create_buffer_from_packed(keys)))
+    monkeypatch.setenv("XLOG_HIP_SORT_SEGMENTS", "0")
+    off, segs, _, _ = _route(provider, lambda: provider.download_packed(
+        provider.dedup_full_row(provider.create_buffer_from_packed(keys))))
+    assert segs == 0
+    assert np.array_equal(on, off)

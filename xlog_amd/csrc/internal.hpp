@@ -362,6 +362,15 @@ int radix_sort_dev(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint64_t n_bo
 // order from the workgroup index, like the radix pass, unless sort_tickets().
 void sort_short_runs_unique(Ctx *ctx, const uint64_t *in, uint64_t n, uint64_t *out, uint64_t *d_count,
                             uint64_t *d_long);
+// Segment route of a large full-key sort: `in` holds n keys ordered by their
+// top 16 bits; every segment (the keys of one top-16-bit value) is sorted by
+// the rest of the key on chip, one block per segment.  With d_count the unique
+// keys go to `out` in order and their count to *d_count (device); without it
+// all n keys go to `out`, sorted.  A segment of more than SORT_SEGMENT_MAX keys,
+// or more than 256 keys that share bits 37..63 and are not all equal, sets
+// *d_long and the output is then incomplete.
+constexpr uint64_t SORT_SEGMENT_MAX = 5120;
+void sort_segments(Ctx *ctx, const uint64_t *in, uint64_t n, uint64_t *out, uint64_t *d_count, uint64_t *d_long);
 
 // Stream compaction family (single pass, decoupled look-back).  Each writes
 // the selected keys in input order to `out` and the count to *d_count

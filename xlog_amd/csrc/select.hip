@@ -1070,6 +1070,231 @@ __global__ __launch_bounds__(SRU_BLOCK) void k_short_runs_unique(const uint64_t 
     }
 }
 
+// Segment sort of a large full-key sort whose keys two digit passes have
+// ordered by their top 16 bits: the keys of one top-16-bit value (a segment,
+// about n / 65,536 keys of uniform input) are sorted by the rest of the key on
+// chip, one block per segment.  This is the hybrid radix sort of Stehle and
+// Jacobsen ("A Memory Bandwidth-Efficient Hybrid Radix Sort on GPUs", SIGMOD
+// 2017): global digit passes until every bucket fits on chip, then one on-chip
+// sort per bucket.  The sort is of whole keys only, so equal keys need no
+// stable order, and one counting pass places the segment: each key takes a
+// slot of its bin of bits 37..47 by an LDS atomic (2,048 bins, about two keys
+// each for uniform keys), the bins' starts come from a block scan, and every
+// key is then ranked inside its bin by the whole key (the bin is the run of
+// keys that share bits 37..63).  The segment is written at its place (sort), or
+// its unique keys at an offset from decoupled look-back over the segments'
+// counts (sort + unique).  A segment of more than SEG_MAX keys, or a bin of
+// more than SEG_RUN_MAX keys that are not all equal, raises *long_run: the
+// block then counts zero and writes nothing, and the caller sorts the keys by
+// every digit instead.
+constexpr int SEG_BLOCK = 512, SEG_ITEMS = 10, SEG_MAX = SEG_BLOCK * SEG_ITEMS, SEG_RUN_MAX = 256;
+constexpr int SEG_WAVES = SEG_BLOCK / WAVE;
+constexpr int SEG_BIN_BITS = 11, SEG_BINS = 1 << SEG_BIN_BITS, SEG_BIN_SHIFT = 48 - SEG_BIN_BITS;
+constexpr uint32_t SEG_COUNT = 1u << 16;
+static_assert((uint64_t)SEG_MAX == SORT_SEGMENT_MAX, "segment capacity");
+static_assert(SEG_BINS % SEG_BLOCK == 0, "bins per thread");
+
+// bounds[s] = index of the first key whose top 16 bits are at least s (keys
+// ordered by their top 16 bits); bounds[65536] = n
+__global__ void k_seg_bounds(const uint64_t *__restrict__ keys, uint64_t n, uint64_t *__restrict__ bounds) {
+    const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s > SEG_COUNT) return;
+    uint64_t lo = 0, hi = n;
+    if (s == SEG_COUNT) {
+        lo = n;
+    } else {
+        const uint64_t target = (uint64_t)s << 48;
+        while (lo < hi) {
+            const uint64_t mid = (lo + hi) >> 1;
+            if (keys[mid] < target) lo = mid + 1;
+            else hi = mid;
+        }
+    }
+    bounds[s] = lo;
+}
+
+struct SegSmem {
+    uint32_t hi[SEG_MAX], lo[SEG_MAX];  // the segment's keys (high and low words) at their place
+    uint32_t bin[SEG_BINS];             // key counts, then the bins' starts
+    uint32_t wsum[SEG_WAVES];
+    uint32_t wc[SEG_WAVES];
+    uint64_t prefix;
+    uint32_t tile;
+    uint32_t bad;
+};
+
+// One block per segment: block index, or (UNIQUE with `ticket`) the block's
+// start ticket, so that a segment's look-back waits only on segments whose
+// blocks started before it.  UNIQUE: the unique keys go to out at their
+// offset and their total to *d_count; otherwise the segment's keys go to out
+// at the segment's place.
+template <bool UNIQUE>
+__global__ __launch_bounds__(SEG_BLOCK) __attribute__((amdgpu_waves_per_eu(6))) void k_seg_sort(const uint64_t *__restrict__ in,
+                                                        const uint64_t *__restrict__ bounds, uint64_t *__restrict__ out,
+                                                        uint64_t *d_count, uint64_t *long_run, uint64_t *status,
+                                                        uint64_t epoch_tag, unsigned long long *ticket,
+                                                        unsigned long long ticket_base, unsigned long long *work) {
+    __shared__ SegSmem sm;
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
+    constexpr int BPT = SEG_BINS / SEG_BLOCK;  // consecutive bins per thread in the scan
+#pragma unroll
+    for (int q = 0; q < BPT; ++q) sm.bin[tid * BPT + q] = 0u;
+    if (tid == 0) {
+        sm.bad = 0;
+        if (UNIQUE && ticket) sm.tile = (uint32_t)(atomicAdd(ticket, 1ull) - ticket_base);
+    }
+    __syncthreads();
+    const uint32_t seg = (UNIQUE && ticket) ? __builtin_amdgcn_readfirstlane(sm.tile) : blockIdx.x;
+    const uint64_t a = bounds[seg], b = bounds[seg + 1];
+    const bool too_big = b - a > (uint64_t)SEG_MAX;
+    const uint32_t len = too_big ? 0u : (uint32_t)(b - a);
+    if (too_big && tid == 0) *long_run = 1ull;
+
+    // the segment's keys in registers (key r of a thread: tid + r * SEG_BLOCK),
+    // each with its slot in its bin
+    uint64_t k[SEG_ITEMS];
+    uint32_t slot[SEG_ITEMS];
+#pragma unroll
+    for (int r = 0; r < SEG_ITEMS; ++r) {
+        const uint32_t p = (uint32_t)(tid + r * SEG_BLOCK);
+        k[r] = p < len ? in[a + p] : 0ull;
+    }
+#pragma unroll
+    for (int r = 0; r < SEG_ITEMS; ++r) {
+        const uint32_t p = (uint32_t)(tid + r * SEG_BLOCK);
+        slot[r] = p < len ? atomicAdd(&sm.bin[(uint32_t)(k[r] >> SEG_BIN_SHIFT) & (SEG_BINS - 1)], 1u) : 0u;
+    }
+    __syncthreads();
+    // exclusive scan of the bin counts: BPT consecutive bins per thread, then waves
+    uint32_t c[BPT], run = 0;
+#pragma unroll
+    for (int q = 0; q < BPT; ++q) {
+        c[q] = sm.bin[tid * BPT + q];
+        run += c[q];
+    }
+    uint32_t incl = run;
+#pragma unroll
+    for (int o = 1; o < WAVE; o <<= 1) {
+        const uint32_t t = __shfl_up(incl, o, WAVE);
+        if (lane >= o) incl += t;
+    }
+    if (lane == WAVE - 1) sm.wsum[wave] = incl;
+    __syncthreads();
+    uint32_t start = incl - run;
+#pragma unroll
+    for (int w = 0; w < SEG_WAVES; ++w)
+        if (w < wave) start += sm.wsum[w];
+#pragma unroll
+    for (int q = 0; q < BPT; ++q) {
+        sm.bin[tid * BPT + q] = start;
+        start += c[q];
+    }
+    __syncthreads();
+    // scatter to the bins: slot r of bin b goes to place start(b) + r
+    uint32_t place[SEG_ITEMS];
+#pragma unroll
+    for (int r = 0; r < SEG_ITEMS; ++r) {
+        const uint32_t p = (uint32_t)(tid + r * SEG_BLOCK);
+        place[r] = 0u;
+        if (p < len) {
+            place[r] = sm.bin[(uint32_t)(k[r] >> SEG_BIN_SHIFT) & (SEG_BINS - 1)] + slot[r];
+            sm.hi[place[r]] = (uint32_t)(k[r] >> 32);
+            sm.lo[place[r]] = (uint32_t)k[r];
+        }
+    }
+    __syncthreads();
+    // rank inside the bin (the run of keys that share bits 37..63) by (key,
+    // place): the key's place in the segment; `moved` marks keys whose place
+    // changes
+    bool longr = false;
+    uint32_t moved = 0;
+#pragma unroll
+    for (int r = 0; r < SEG_ITEMS; ++r) {
+        const uint32_t p = (uint32_t)(tid + r * SEG_BLOCK);
+        if (p >= len) continue;
+        const uint32_t bn = (uint32_t)(k[r] >> SEG_BIN_SHIFT) & (SEG_BINS - 1);
+        const uint32_t st = sm.bin[bn], en = bn + 1 < (uint32_t)SEG_BINS ? sm.bin[bn + 1] : len;
+        if (en - st < 2) continue;
+        if (en - st > (uint32_t)SEG_RUN_MAX) {
+            // a long bin is left as it is when all its keys are equal (any order is sorted)
+            if ((((uint64_t)sm.hi[st] << 32) | sm.lo[st]) != k[r]) longr = true;
+            continue;
+        }
+        uint32_t rk = 0;
+        for (uint32_t j = st; j < en; ++j) {
+            const uint64_t kj = ((uint64_t)sm.hi[j] << 32) | sm.lo[j];
+            rk += (kj < k[r] || (kj == k[r] && j < place[r])) ? 1u : 0u;
+        }
+        if (st + rk != place[r]) {
+            place[r] = st + rk;
+            moved |= 1u << r;
+        }
+    }
+    if (__ballot(longr) != 0 && lane == 0) {
+        sm.bad = 1u;
+        *long_run = 1ull;
+    }
+    __syncthreads();  // every rank has read the bins; sm.bad is final
+    const bool bad = sm.bad != 0u;
+    if (!bad) {
+#pragma unroll
+        for (int r = 0; r < SEG_ITEMS; ++r) {
+            if (!((moved >> r) & 1u)) continue;
+            sm.hi[place[r]] = (uint32_t)(k[r] >> 32);
+            sm.lo[place[r]] = (uint32_t)k[r];
+        }
+    }
+    __syncthreads();
+    const uint32_t wbase = (uint32_t)wave * (SEG_ITEMS * WAVE);
+    const uint32_t n_out = bad ? 0u : len;
+    if (!UNIQUE) {
+        for (uint32_t i = tid; i < n_out; i += SEG_BLOCK) out[a + i] = ((uint64_t)sm.hi[i] << 32) | sm.lo[i];
+        return;
+    }
+    // unique keys: a key differing from the one before it (the segment's first
+    // key has top 16 bits no earlier segment has), counted per wave over
+    // consecutive places
+    uint32_t fl = 0, wc = 0;
+#pragma unroll
+    for (int r = 0; r < SEG_ITEMS; ++r) {
+        const uint32_t i = wbase + (uint32_t)(r * WAVE + lane);
+        const bool f = i < n_out && (i == 0 || sm.hi[i] != sm.hi[i - 1] || sm.lo[i] != sm.lo[i - 1]);
+        if (f) fl |= 1u << r;
+        wc += (uint32_t)__popcll(__ballot(f));
+    }
+    if (lane == 0) sm.wc[wave] = wc;
+    __syncthreads();
+    uint64_t tile_cnt = 0, wpre = 0;
+#pragma unroll
+    for (int w = 0; w < SEG_WAVES; ++w) {
+        if (w < wave) wpre += sm.wc[w];
+        tile_cnt += sm.wc[w];
+    }
+    if (wave == 0) {
+        if (tid == 0) lb_store(status + seg, epoch_tag | (seg == 0 ? LB_INC : 0ull) | tile_cnt);
+        const uint64_t prefix = seg ? lookback_wave(status, seg, epoch_tag, lane) : 0ull;
+        if (tid == 0) {
+            if (seg) lb_store(status + seg, epoch_tag | LB_INC | (prefix + tile_cnt));
+            sm.prefix = prefix;
+            if (seg == SEG_COUNT - 1) *d_count = prefix + tile_cnt;
+            if (work && tile_cnt) atomicAdd(&work[blockIdx.x & (Ctx::PROF_WORK_SPREAD - 1)], tile_cnt);
+        }
+    }
+    __syncthreads();
+    const uint64_t lt_mask = (1ull << lane) - 1ull;
+    uint64_t pos = sm.prefix + wpre;
+#pragma unroll
+    for (int r = 0; r < SEG_ITEMS; ++r) {
+        const bool f = (fl >> r) & 1u;
+        const uint64_t m = __ballot(f);
+        if (f) {
+            const uint32_t i = wbase + (uint32_t)(r * WAVE + lane);
+            out[pos + (uint64_t)__popcll(m & lt_mask)] = ((uint64_t)sm.hi[i] << 32) | sm.lo[i];
+        }
+        pos += (uint64_t)__popcll(m);
+    }
+}
+
 }  // namespace
 
 // ---- host wrappers ----------------------------------------------------------
@@ -1159,6 +1384,33 @@ void sort_short_runs_unique(Ctx *ctx, const uint64_t *in, uint64_t n, uint64_t *
     unsigned long long *work = prof.work(8.0);
     hipLaunchKernelGGL(k_short_runs_unique, dim3((unsigned)tiles), dim3(SRU_BLOCK), 0, ctx->stream, in, n, out, d_count,
                        d_long, status, tag, tk, tb, tiles, work);
+    XH_CHECK_HIP(hipGetLastError());
+}
+
+void sort_segments(Ctx *ctx, const uint64_t *in, uint64_t n, uint64_t *out, uint64_t *d_count, uint64_t *d_long) {
+    fill_u64(ctx, d_long, 0ull, 1);
+    if (n == 0) {
+        if (d_count) fill_u64(ctx, d_count, 0ull, 1);
+        return;
+    }
+    Buf<uint64_t> bounds(ctx, SEG_COUNT + 1);
+    hipLaunchKernelGGL(k_seg_bounds, dim3((SEG_COUNT + 1 + 255) / 256), dim3(256), 0, ctx->stream, in, n, bounds.p);
+    XH_CHECK_HIP(hipGetLastError());
+    if (d_count) {
+        uint64_t tag;
+        uint64_t *status = select_status(ctx, SEG_COUNT, &tag);
+        unsigned long long *tk = sort_tickets() ? ctx->tickets + 1 : nullptr;
+        const unsigned long long tb = tk ? ctx->take_tickets(1, SEG_COUNT) : 0ull;
+        // algorithmic bytes: every key read once, every unique key written once (counted on the device)
+        Prof prof(ctx, XLOG_HIP_KERNEL_SORT_SEGMENTS, 8.0 * (double)n);
+        unsigned long long *work = prof.work(8.0);
+        hipLaunchKernelGGL(k_seg_sort<true>, dim3(SEG_COUNT), dim3(SEG_BLOCK), 0, ctx->stream, in, bounds.p, out,
+                           d_count, d_long, status, tag, tk, tb, work);
+    } else {
+        Prof prof(ctx, XLOG_HIP_KERNEL_SORT_SEGMENTS, 16.0 * (double)n);  // every key read and written once
+        hipLaunchKernelGGL(k_seg_sort<false>, dim3(SEG_COUNT), dim3(SEG_BLOCK), 0, ctx->stream, in, bounds.p, out,
+                           nullptr, d_long, nullptr, 0ull, nullptr, 0ull, nullptr);
+    }
     XH_CHECK_HIP(hipGetLastError());
 }
 

@@ -648,6 +648,29 @@ static bool short_high_runs(const uint32_t *h, uint64_t n) {
     return (double)(n - 1) * p <= 8.0;
 }
 
+// The segment route of a large full-key sort (keys only, at least
+// XLOG_HIP_SORT_SEG_MIN keys, default 2^26; XLOG_HIP_SORT_SEGMENTS=0 turns it
+// off, both read at each sort): two digit passes order the keys by their top
+// 16 bits and one on-chip sort per segment (sort_segments) replaces the other
+// six digits' passes.  From the histograms of digits 6 and 7: the largest
+// segment, as if the two digits were independent, is max h6 * max h7 / n; the
+// route is taken when that leaves room below the on-chip capacity (a segment
+// above it is caught by the segment pass, and the sort then runs every
+// digit's pass).
+static bool segment_route(const uint32_t *h, uint64_t n) {
+    const char *off = getenv("XLOG_HIP_SORT_SEGMENTS");
+    if (off && off[0] == '0') return false;
+    const char *e = getenv("XLOG_HIP_SORT_SEG_MIN");
+    const uint64_t min_keys = e && *e ? strtoull(e, nullptr, 10) : (1ull << 26);
+    if (n < min_keys) return false;
+    uint32_t m6 = 0, m7 = 0;
+    for (int b = 0; b < 256; ++b) {
+        m6 = std::max(m6, h[6 * 256 + b]);
+        m7 = std::max(m7, h[7 * 256 + b]);
+    }
+    return (double)m6 * (double)m7 / (double)n <= 0.85 * (double)SORT_SEGMENT_MAX;
+}
+
 void sort_short_runs(Ctx *ctx, const uint64_t *in, uint64_t n, uint64_t *out, uint64_t *d_long) {
     fill_u64(ctx, d_long, 0ull, 1);
     if (!n) return;
@@ -860,6 +883,28 @@ int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **va
         ctx->wait_event(ctx->ev_read);
         memcpy(h_hist, ctx->host_scalars, sizeof(h_hist));
     };
+    if (hybrid_candidate && segment_route(h_hist, n)) {
+        // Digits 6 and 7, then every segment of equal top 16 bits sorted on chip.
+        for (int dgt = 6; dgt < 8; ++dgt)
+            if (!trivial(dgt)) launch_pass(dgt);
+        Buf<uint64_t> flags(ctx, 2);  // unique count (with uq), long segment or run
+        sort_segments(ctx, (passes == 0 && src) ? src : *keys, n, *keys_alt, uq ? flags.p : nullptr, flags.p + 1);
+        ctx->read_scalars(flags.p, 2);
+        if (ctx->host_scalars[1] == 0) {
+            if (uq) {
+                uq->done = true;
+                uq->count = ctx->host_scalars[0];
+            }
+            std::swap(*keys, *keys_alt);
+            return passes + 1;
+        }
+        // a segment above the on-chip capacity or a long run of unequal keys:
+        // every digit's pass, from the keys as they are (any order sorts alike)
+        low_word_histograms((passes == 0 && src) ? src : *keys);
+        for (int dgt = 0; dgt < 8; ++dgt)
+            if (!trivial(dgt)) launch_pass(dgt);
+        return passes;
+    }
     if (hybrid_candidate && short_high_runs(h_hist, n)) {
         // The high word's passes, then every run of equal high word sorted by
         // its low word in one pass instead of the low word's four passes.

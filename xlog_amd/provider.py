@@ -173,6 +173,7 @@ ABI_SYMBOLS = (
 KERNEL_KINDS = {
     "sort_pass": 0, "sort_hist": 1, "select": 2, "merge": 3, "probe_count": 4, "probe_emit": 5, "tc_step": 6,
     "tc_emit": 7, "chain_product": 8, "chain_finalize": 9, "chain_emit": 10, "hash_insert": 11, "sort_runs": 12,
+    "sort_segments": 13,
 }
 
 
