@@ -5,8 +5,8 @@ lowers the bound so that these tests take the route at 2^22 keys) whose
 histograms of digits 6 and 7 predict segments of at most 0.85 x 5,120 keys
 (xlog_amd/csrc/sort.hip, segment_route) takes two digit passes, which order
 the keys by their top 16 bits, then sorts every segment of equal top 16 bits on
-chip (select.hip, k_seg_sort: one counting pass through LDS over the 2,048
-bins of bits 37..47, every bin ranked by the whole key, and the unique keys
+chip (select.hip, k_seg_sort: one counting pass through LDS over the 4,096
+bins of bits 36..47, every bin ranked by the whole key, and the unique keys
 written at an offset from decoupled look-back, for sort + dedup).  A segment of
 more than 5,120 keys, or a bin of more than 256 keys that are not all equal,
 makes the sort run every digit's pass instead.  Each case is checked against numpy (sort) and the oracle
@@ -94,7 +94,7 @@ def test_constant_middle_bits(provider, seg_min):
 
 
 def test_one_constant_middle_digit(provider, seg_min):
-    """Bits 40..47 constant: the bins of bits 37..47 use 8 of their 2,048 values (bins of about 8 keys)."""
+    """Bits 40..47 constant: the bins of bits 36..47 use 16 of their 4,096 values (bins of about 4 keys)."""
     rng = np.random.default_rng(4047)
     keys = rng.integers(0, 1 << 64, size=N, dtype=U64)
     keys = (keys & ~(U64(0xFF) << U64(40))) | (U64(0x5A) << U64(40))
@@ -103,11 +103,11 @@ def test_one_constant_middle_digit(provider, seg_min):
 
 
 def test_runs_of_exactly_256(provider, seg_min):
-    """2^14 high words with distinct bits 37..63, each carrying exactly 256 keys: the longest bins (keys that
-    share bits 37..63) the segment pass ranks; segments hold a few of them, within capacity."""
+    """2^14 high words with distinct bits 36..63, each carrying exactly 256 keys: the longest bins (keys that
+    share bits 36..63) the segment pass ranks; segments hold a few of them, within capacity."""
     rng = np.random.default_rng(256)
-    top = rng.permutation(np.unique(rng.integers(0, 1 << 27, size=N // 128, dtype=U64)))[: N // 256]
-    hi = (top << U64(5)) | rng.integers(0, 32, size=len(top), dtype=U64)
+    top = rng.permutation(np.unique(rng.integers(0, 1 << 28, size=N // 128, dtype=U64)))[: N // 256]
+    hi = (top << U64(4)) | rng.integers(0, 16, size=len(top), dtype=U64)
     keys = (np.repeat(hi, 256) << U64(32)) | rng.integers(0, 1 << 32, size=N, dtype=U64)
     rng.shuffle(keys)
     _note("segment sort: runs of 256")

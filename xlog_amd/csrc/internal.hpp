@@ -367,7 +367,7 @@ void sort_short_runs_unique(Ctx *ctx, const uint64_t *in, uint64_t n, uint64_t *
 // the rest of the key on chip, one block per segment.  With d_count the unique
 // keys go to `out` in order and their count to *d_count (device); without it
 // all n keys go to `out`, sorted.  A segment of more than SORT_SEGMENT_MAX keys,
-// or more than 256 keys that share bits 37..63 and are not all equal, sets
+// or more than 256 keys that share bits 36..63 and are not all equal, sets
 // *d_long and the output is then incomplete.
 constexpr uint64_t SORT_SEGMENT_MAX = 5120;
 void sort_segments(Ctx *ctx, const uint64_t *in, uint64_t n, uint64_t *out, uint64_t *d_count, uint64_t *d_long);

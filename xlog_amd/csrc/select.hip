@@ -1078,18 +1078,18 @@ __global__ __launch_bounds__(SRU_BLOCK) void k_short_runs_unique(const uint64_t 
 // 2017): global digit passes until every bucket fits on chip, then one on-chip
 // sort per bucket.  The sort is of whole keys only, so equal keys need no
 // stable order, and one counting pass places the segment: each key takes a
-// slot of its bin of bits 37..47 by an LDS atomic (2,048 bins, about two keys
+// slot of its bin of bits 36..47 by an LDS atomic (4,096 bins, about one key
 // each for uniform keys), the bins' starts come from a block scan, and every
 // key is then ranked inside its bin by the whole key (the bin is the run of
-// keys that share bits 37..63).  The segment is written at its place (sort), or
+// keys that share bits 36..63).  The segment is written at its place (sort), or
 // its unique keys at an offset from decoupled look-back over the segments'
 // counts (sort + unique).  A segment of more than SEG_MAX keys, or a bin of
 // more than SEG_RUN_MAX keys that are not all equal, raises *long_run: the
 // block then counts zero and writes nothing, and the caller sorts the keys by
 // every digit instead.
-constexpr int SEG_BLOCK = 512, SEG_ITEMS = 10, SEG_MAX = SEG_BLOCK * SEG_ITEMS, SEG_RUN_MAX = 256;
+constexpr int SEG_BLOCK = 1024, SEG_ITEMS = 5, SEG_MAX = SEG_BLOCK * SEG_ITEMS, SEG_RUN_MAX = 256, SEG_RANK_BATCH = 4;
 constexpr int SEG_WAVES = SEG_BLOCK / WAVE;
-constexpr int SEG_BIN_BITS = 11, SEG_BINS = 1 << SEG_BIN_BITS, SEG_BIN_SHIFT = 48 - SEG_BIN_BITS;
+constexpr int SEG_BIN_BITS = 12, SEG_BINS = 1 << SEG_BIN_BITS, SEG_BIN_SHIFT = 48 - SEG_BIN_BITS;
 constexpr uint32_t SEG_COUNT = 1u << 16;
 static_assert((uint64_t)SEG_MAX == SORT_SEGMENT_MAX, "segment capacity");
 static_assert(SEG_BINS % SEG_BLOCK == 0, "bins per thread");
@@ -1116,6 +1116,7 @@ __global__ void k_seg_bounds(const uint64_t *__restrict__ keys, uint64_t n, uint
 struct SegSmem {
     uint32_t hi[SEG_MAX], lo[SEG_MAX];  // the segment's keys (high and low words) at their place
     uint32_t bin[SEG_BINS];             // key counts, then the bins' starts
+    uint8_t uf[SEG_MAX];                // 1 at the place of the first of every group of equal keys
     uint32_t wsum[SEG_WAVES];
     uint32_t wc[SEG_WAVES];
     uint64_t prefix;
@@ -1129,7 +1130,7 @@ struct SegSmem {
 // offset and their total to *d_count; otherwise the segment's keys go to out
 // at the segment's place.
 template <bool UNIQUE>
-__global__ __launch_bounds__(SEG_BLOCK) __attribute__((amdgpu_waves_per_eu(6))) void k_seg_sort(const uint64_t *__restrict__ in,
+__global__ __launch_bounds__(SEG_BLOCK) __attribute__((amdgpu_waves_per_eu(8))) void k_seg_sort(const uint64_t *__restrict__ in,
                                                         const uint64_t *__restrict__ bounds, uint64_t *__restrict__ out,
                                                         uint64_t *d_count, uint64_t *long_run, uint64_t *status,
                                                         uint64_t epoch_tag, unsigned long long *ticket,
@@ -1203,42 +1204,85 @@ __global__ __launch_bounds__(SEG_BLOCK) __attribute__((amdgpu_waves_per_eu(6))) 
         }
     }
     __syncthreads();
-    // rank inside the bin (the run of keys that share bits 37..63) by (key,
+    // rank inside the bin (the run of keys that share bits 36..63) by (key,
     // place): the key's place in the segment; `moved` marks keys whose place
-    // changes
+    // changes and `uniq` the first of every group of equal keys.  Every key's
+    // bin bounds are read first, and a bin's first SEG_RANK_BATCH keys are
+    // loaded together (most bins hold fewer).
     bool longr = false;
-    uint32_t moved = 0;
+    uint32_t moved = 0, uniq = 0;
+    uint32_t bst[SEG_ITEMS], bln[SEG_ITEMS];
 #pragma unroll
     for (int r = 0; r < SEG_ITEMS; ++r) {
         const uint32_t p = (uint32_t)(tid + r * SEG_BLOCK);
-        if (p >= len) continue;
         const uint32_t bn = (uint32_t)(k[r] >> SEG_BIN_SHIFT) & (SEG_BINS - 1);
-        const uint32_t st = sm.bin[bn], en = bn + 1 < (uint32_t)SEG_BINS ? sm.bin[bn + 1] : len;
-        if (en - st < 2) continue;
-        if (en - st > (uint32_t)SEG_RUN_MAX) {
-            // a long bin is left as it is when all its keys are equal (any order is sorted)
+        bst[r] = p < len ? sm.bin[bn] : 0u;
+        bln[r] = p < len ? (bn + 1 < (uint32_t)SEG_BINS ? sm.bin[bn + 1] : len) - bst[r] : 0u;
+    }
+#pragma unroll
+    for (int r = 0; r < SEG_ITEMS; ++r) {
+        const uint32_t st = bst[r], ln = bln[r];
+        if (ln < 2) {
+            if (ln == 1) uniq |= 1u << r;
+            continue;
+        }
+        if (ln > (uint32_t)SEG_RUN_MAX) {
+            // a long bin is left as it is when all its keys are equal (any
+            // order is sorted); the key at its start stands for them
             if ((((uint64_t)sm.hi[st] << 32) | sm.lo[st]) != k[r]) longr = true;
+            else if (place[r] == st) uniq |= 1u << r;
             continue;
         }
         uint32_t rk = 0;
-        for (uint32_t j = st; j < en; ++j) {
-            const uint64_t kj = ((uint64_t)sm.hi[j] << 32) | sm.lo[j];
-            rk += (kj < k[r] || (kj == k[r] && j < place[r])) ? 1u : 0u;
+        bool eq_before = false;
+        uint64_t kj[SEG_RANK_BATCH];
+#pragma unroll
+        for (int u = 0; u < SEG_RANK_BATCH; ++u) {
+            const uint32_t j = st + ((uint32_t)u < ln ? (uint32_t)u : ln - 1);
+            kj[u] = ((uint64_t)sm.hi[j] << 32) | sm.lo[j];
         }
+#pragma unroll
+        for (int u = 0; u < SEG_RANK_BATCH; ++u) {
+            const bool in = (uint32_t)u < ln, before = st + u < place[r];
+            rk += (in && (kj[u] < k[r] || (kj[u] == k[r] && before))) ? 1u : 0u;
+            eq_before |= in && kj[u] == k[r] && before;
+        }
+        for (uint32_t j = st + SEG_RANK_BATCH; j < st + ln; ++j) {
+            const uint64_t x = ((uint64_t)sm.hi[j] << 32) | sm.lo[j];
+            rk += (x < k[r] || (x == k[r] && j < place[r])) ? 1u : 0u;
+            eq_before |= x == k[r] && j < place[r];
+        }
+        if (!eq_before) uniq |= 1u << r;
         if (st + rk != place[r]) {
             place[r] = st + rk;
             moved |= 1u << r;
         }
     }
+    uint32_t wu = 0;
+    if (UNIQUE) {
+#pragma unroll
+        for (int r = 0; r < SEG_ITEMS; ++r) wu += (uint32_t)__popcll(__ballot((uniq >> r) & 1u));
+    }
+    if (lane == 0) sm.wc[wave] = wu;
     if (__ballot(longr) != 0 && lane == 0) {
         sm.bad = 1u;
         *long_run = 1ull;
     }
-    __syncthreads();  // every rank has read the bins; sm.bad is final
+    __syncthreads();  // every rank has read the bins; sm.bad and the counts are final
     const bool bad = sm.bad != 0u;
+    uint64_t tile_cnt = 0;
+    if (UNIQUE) {
+#pragma unroll
+        for (int w = 0; w < SEG_WAVES; ++w) tile_cnt += sm.wc[w];
+        if (bad) tile_cnt = 0;
+        // the segment's count is known: published before its keys are placed
+        if (tid == 0) lb_store(status + seg, epoch_tag | (seg == 0 ? LB_INC : 0ull) | tile_cnt);
+    }
     if (!bad) {
 #pragma unroll
         for (int r = 0; r < SEG_ITEMS; ++r) {
+            const uint32_t p = (uint32_t)(tid + r * SEG_BLOCK);
+            if (UNIQUE && p < len) sm.uf[place[r]] = (uint8_t)((uniq >> r) & 1u);
             if (!((moved >> r) & 1u)) continue;
             sm.hi[place[r]] = (uint32_t)(k[r] >> 32);
             sm.lo[place[r]] = (uint32_t)k[r];
@@ -1251,27 +1295,22 @@ __global__ __launch_bounds__(SEG_BLOCK) __attribute__((amdgpu_waves_per_eu(6))) 
         for (uint32_t i = tid; i < n_out; i += SEG_BLOCK) out[a + i] = ((uint64_t)sm.hi[i] << 32) | sm.lo[i];
         return;
     }
-    // unique keys: a key differing from the one before it (the segment's first
-    // key has top 16 bits no earlier segment has), counted per wave over
-    // consecutive places
+    // the unique keys in place order, counted per wave over consecutive places
     uint32_t fl = 0, wc = 0;
 #pragma unroll
     for (int r = 0; r < SEG_ITEMS; ++r) {
         const uint32_t i = wbase + (uint32_t)(r * WAVE + lane);
-        const bool f = i < n_out && (i == 0 || sm.hi[i] != sm.hi[i - 1] || sm.lo[i] != sm.lo[i - 1]);
+        const bool f = i < n_out && sm.uf[i] != 0;
         if (f) fl |= 1u << r;
         wc += (uint32_t)__popcll(__ballot(f));
     }
     if (lane == 0) sm.wc[wave] = wc;
     __syncthreads();
-    uint64_t tile_cnt = 0, wpre = 0;
+    uint64_t wpre = 0;
 #pragma unroll
-    for (int w = 0; w < SEG_WAVES; ++w) {
+    for (int w = 0; w < SEG_WAVES; ++w)
         if (w < wave) wpre += sm.wc[w];
-        tile_cnt += sm.wc[w];
-    }
     if (wave == 0) {
-        if (tid == 0) lb_store(status + seg, epoch_tag | (seg == 0 ? LB_INC : 0ull) | tile_cnt);
         const uint64_t prefix = seg ? lookback_wave(status, seg, epoch_tag, lane) : 0ull;
         if (tid == 0) {
             if (seg) lb_store(status + seg, epoch_tag | LB_INC | (prefix + tile_cnt));
