@@ -22,6 +22,13 @@ pytestmark = pytest.mark.gpu
 N_MIN = 1 << 22  # smallest sort that may take the route
 
 
+@pytest.fixture(autouse=True)
+def _no_segment_route(monkeypatch):
+    """These sorts would take the segment route (tests/test_gpu_sort_segments.py); it is switched off so
+    that the high-word route is the one under test."""
+    monkeypatch.setenv("XLOG_HIP_SORT_SEGMENTS", "0")
+
+
 def _note(msg):
     print(msg, flush=True)
     sys.stdout.flush()

@@ -407,7 +407,8 @@ static std::vector<Bags> bags_per_pred(Ctx *ctx, uint32_t n) {
 // digit_lo / digit_hi restrict the sort to 8-bit digits [lo, hi) (4..8 = by
 // the high word only, stable otherwise).
 static uint64_t *sort_keys(Ctx *ctx, uint64_t *keys, uint64_t n, bool keys_owned, int digit_lo = 0,
-                           int digit_hi = 8, uint32_t known_digits = 0) {
+                           int digit_hi = 8, uint32_t known_digits = 0, bool *whole = nullptr) {
+    if (whole) *whole = false;
     // a consumed input is freed if an error unwinds from here
     Owned in_guard(ctx, keys_owned ? keys : nullptr);
     if (n < 2) {
@@ -423,7 +424,8 @@ static uint64_t *sort_keys(Ctx *ctx, uint64_t *keys, uint64_t n, bool keys_owned
         uint64_t *a = ga.p, *b = gb.p;
         uint32_t *v0 = nullptr, *v1 = nullptr;
         // without keys_owned the first pass reads the caller's keys; both ping-pong buffers are ours
-        radix_sort_u64(ctx, &a, &b, &v0, &v1, n, digit_lo, digit_hi, keys_owned ? nullptr : keys, known_digits);
+        radix_sort_u64(ctx, &a, &b, &v0, &v1, n, digit_lo, digit_hi, keys_owned ? nullptr : keys, known_digits,
+                       nullptr, whole);
         ga.release();
         gb.release();
         ctx->free(b);
@@ -1478,13 +1480,15 @@ static xlog_hip_rel *op_join_project_dedup(Ctx *ctx, const xlog_hip_rel *l, cons
     // 1. probe keys (out column << 32 | join key), ordered by the out column
     Buf<uint64_t> lk_buf;  // owns the sorted probe keys
     lk_buf.ctx = ctx;
+    //    (or by the whole key, when the segment route of many keys does that in fewer passes)
+    bool whole = false;
     if (l->arity == 2 && out_cols[0] == 0 && lk == 1) {
         // the rows are already (out column << 32 | join key): the sort reads them directly
-        lk_buf.p = sort_keys(ctx, l->w[0], n, false, 4, 8);
+        lk_buf.p = sort_keys(ctx, l->w[0], n, false, 4, 8, 0, &whole);
     } else {
         lk_buf.p = static_cast<uint64_t *>(ctx->alloc(n * sizeof(uint64_t)));
         left_keys(ctx, l->w[0], n, (int)l->arity, out_cols[0], (int)lk, lk_buf.p);
-        lk_buf.p = sort_keys(ctx, lk_buf.p, n, true, 4, 8);
+        lk_buf.p = sort_keys(ctx, lk_buf.p, n, true, 4, 8, 0, &whole);
     }
     const uint64_t *lkeys = lk_buf.p;
     // 2. build rows as (key << 32 | payload), sorted and unique, so that a probe
@@ -1502,15 +1506,20 @@ static xlog_hip_rel *op_join_project_dedup(Ctx *ctx, const xlog_hip_rel *l, cons
         fill_u64(ctx, cnt.p + 4, 0ull, 1);
     } else {
         if (rk == 0) {
-            kw_buf.p = sort_keys(ctx, r->w[0], nr, false, 4, 8);
+            kw_buf.p = sort_keys(ctx, r->w[0], nr, false, 4, 8, 0, &whole);
         } else {
             kw_buf.p = static_cast<uint64_t *>(ctx->alloc(nr * sizeof(uint64_t)));
             swap_words(ctx, r->w[0], nr, kw_buf.p);
-            kw_buf.p = sort_keys(ctx, kw_buf.p, nr, true, 4, 8);
+            kw_buf.p = sort_keys(ctx, kw_buf.p, nr, true, 4, 8, 0, &whole);
         }
-        sk_buf = Buf<uint64_t>(ctx, nr);
-        sort_short_runs(ctx, kw_buf.p, nr, sk_buf.p, cnt.p + 4);
-        sk = sk_buf.p;
+        if (whole) {  // the segment route ordered the build rows by the whole key
+            fill_u64(ctx, cnt.p + 4, 0ull, 1);
+            sk = kw_buf.p;
+        } else {
+            sk_buf = Buf<uint64_t>(ctx, nr);
+            sort_short_runs(ctx, kw_buf.p, nr, sk_buf.p, cnt.p + 4);
+            sk = sk_buf.p;
+        }
     }
     Buf<uint64_t> ub;
     JoinIndex J;

@@ -313,9 +313,12 @@ struct SortUnique {
 // workgroup index, so that their look-back does not rest on workgroups
 // starting in index order (slower: one device-wide atomic per tile).
 bool sort_tickets();
+// With `whole` (a keys-only sort of the high word, digits 4..7, of at least
+// 2^22 keys) the sort may order the keys by the whole key instead, through the
+// segment route; *whole tells whether it did.
 int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **vals, uint32_t **vals_alt,
                    uint64_t n, int digit_lo = 0, int digit_hi = 8, const uint64_t *src = nullptr,
-                   uint32_t known_digits = 0, SortUnique *uq = nullptr);
+                   uint32_t known_digits = 0, SortUnique *uq = nullptr, bool *whole = nullptr);
 // A keys-only sort of a queued iteration: the key count on the device
 // (*d_n <= n_bound, the bound the launches are sized for), exactly the digit
 // passes of known_digits (no read-back), and the stop flag (a raised flag:
@@ -363,14 +366,16 @@ int radix_sort_dev(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint64_t n_bo
 void sort_short_runs_unique(Ctx *ctx, const uint64_t *in, uint64_t n, uint64_t *out, uint64_t *d_count,
                             uint64_t *d_long);
 // Segment route of a large full-key sort: `in` holds n keys ordered by their
-// top 16 bits; every segment (the keys of one top-16-bit value) is sorted by
-// the rest of the key on chip, one block per segment.  With d_count the unique
-// keys go to `out` in order and their count to *d_count (device); without it
-// all n keys go to `out`, sorted.  A segment of more than SORT_SEGMENT_MAX keys,
-// or more than 256 keys that share bits 36..63 and are not all equal, sets
+// top 16 bits; a segment is the keys of 2^gshift consecutive top-16-bit values
+// (gshift in [0, 8]), and every segment is sorted by the rest of the key on
+// chip, one block per segment.  With d_count the unique keys go to `out` in
+// order and their count to *d_count (device); without it all n keys go to
+// `out`, sorted.  A segment of more than SORT_SEGMENT_MAX keys, or more than
+// 256 keys that share bits 36 + gshift .. 63 and are not all equal, sets
 // *d_long and the output is then incomplete.
 constexpr uint64_t SORT_SEGMENT_MAX = 5120;
-void sort_segments(Ctx *ctx, const uint64_t *in, uint64_t n, uint64_t *out, uint64_t *d_count, uint64_t *d_long);
+void sort_top_segments(Ctx *ctx, const uint64_t *in, uint64_t n, uint64_t *out, uint64_t *d_count, uint64_t *d_long,
+                       int gshift);
 
 // Stream compaction family (single pass, decoupled look-back).  Each writes
 // the selected keys in input order to `out` and the count to *d_count

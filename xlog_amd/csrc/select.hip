@@ -1089,21 +1089,23 @@ __global__ __launch_bounds__(SRU_BLOCK) void k_short_runs_unique(const uint64_t 
 // every digit instead.
 constexpr int SEG_BLOCK = 1024, SEG_ITEMS = 5, SEG_MAX = SEG_BLOCK * SEG_ITEMS, SEG_RUN_MAX = 256, SEG_RANK_BATCH = 4;
 constexpr int SEG_WAVES = SEG_BLOCK / WAVE;
-constexpr int SEG_BIN_BITS = 12, SEG_BINS = 1 << SEG_BIN_BITS, SEG_BIN_SHIFT = 48 - SEG_BIN_BITS;
-constexpr uint32_t SEG_COUNT = 1u << 16;
+constexpr int SEG_BIN_BITS = 12, SEG_BINS = 1 << SEG_BIN_BITS;
+constexpr uint32_t SEG_COUNT = 1u << 16;  // top-16-bit values
 static_assert((uint64_t)SEG_MAX == SORT_SEGMENT_MAX, "segment capacity");
 static_assert(SEG_BINS % SEG_BLOCK == 0, "bins per thread");
 
-// bounds[s] = index of the first key whose top 16 bits are at least s (keys
-// ordered by their top 16 bits); bounds[65536] = n
-__global__ void k_seg_bounds(const uint64_t *__restrict__ keys, uint64_t n, uint64_t *__restrict__ bounds) {
+// A segment is the keys of 2^gshift consecutive top-16-bit values (their bits
+// 48 + gshift and up agree): bounds[s] = index of the first key of segment s
+// or a later one (keys ordered by their top 16 bits), bounds[nseg] = n.
+__global__ void k_seg_bounds(const uint64_t *__restrict__ keys, uint64_t n, uint32_t nseg, int gshift,
+                             uint64_t *__restrict__ bounds) {
     const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
-    if (s > SEG_COUNT) return;
+    if (s > nseg) return;
     uint64_t lo = 0, hi = n;
-    if (s == SEG_COUNT) {
+    if (s == nseg) {
         lo = n;
     } else {
-        const uint64_t target = (uint64_t)s << 48;
+        const uint64_t target = (uint64_t)s << (48 + gshift);
         while (lo < hi) {
             const uint64_t mid = (lo + hi) >> 1;
             if (keys[mid] < target) lo = mid + 1;
@@ -1134,8 +1136,11 @@ __global__ __launch_bounds__(SEG_BLOCK) __attribute__((amdgpu_waves_per_eu(8))) 
                                                         const uint64_t *__restrict__ bounds, uint64_t *__restrict__ out,
                                                         uint64_t *d_count, uint64_t *long_run, uint64_t *status,
                                                         uint64_t epoch_tag, unsigned long long *ticket,
-                                                        unsigned long long ticket_base, unsigned long long *work) {
+                                                        unsigned long long ticket_base, uint32_t nseg, int gshift,
+                                                        unsigned long long *work) {
     __shared__ SegSmem sm;
+    // the bins take the 12 bits below the segment's own (bits 36 + gshift .. 47 + gshift)
+    const int bin_shift = 48 - SEG_BIN_BITS + gshift;
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
     constexpr int BPT = SEG_BINS / SEG_BLOCK;  // consecutive bins per thread in the scan
 #pragma unroll
@@ -1163,7 +1168,7 @@ __global__ __launch_bounds__(SEG_BLOCK) __attribute__((amdgpu_waves_per_eu(8))) 
 #pragma unroll
     for (int r = 0; r < SEG_ITEMS; ++r) {
         const uint32_t p = (uint32_t)(tid + r * SEG_BLOCK);
-        slot[r] = p < len ? atomicAdd(&sm.bin[(uint32_t)(k[r] >> SEG_BIN_SHIFT) & (SEG_BINS - 1)], 1u) : 0u;
+        slot[r] = p < len ? atomicAdd(&sm.bin[(uint32_t)(k[r] >> bin_shift) & (SEG_BINS - 1)], 1u) : 0u;
     }
     __syncthreads();
     // exclusive scan of the bin counts: BPT consecutive bins per thread, then waves
@@ -1198,7 +1203,7 @@ __global__ __launch_bounds__(SEG_BLOCK) __attribute__((amdgpu_waves_per_eu(8))) 
         const uint32_t p = (uint32_t)(tid + r * SEG_BLOCK);
         place[r] = 0u;
         if (p < len) {
-            place[r] = sm.bin[(uint32_t)(k[r] >> SEG_BIN_SHIFT) & (SEG_BINS - 1)] + slot[r];
+            place[r] = sm.bin[(uint32_t)(k[r] >> bin_shift) & (SEG_BINS - 1)] + slot[r];
             sm.hi[place[r]] = (uint32_t)(k[r] >> 32);
             sm.lo[place[r]] = (uint32_t)k[r];
         }
@@ -1215,7 +1220,7 @@ __global__ __launch_bounds__(SEG_BLOCK) __attribute__((amdgpu_waves_per_eu(8))) 
 #pragma unroll
     for (int r = 0; r < SEG_ITEMS; ++r) {
         const uint32_t p = (uint32_t)(tid + r * SEG_BLOCK);
-        const uint32_t bn = (uint32_t)(k[r] >> SEG_BIN_SHIFT) & (SEG_BINS - 1);
+        const uint32_t bn = (uint32_t)(k[r] >> bin_shift) & (SEG_BINS - 1);
         bst[r] = p < len ? sm.bin[bn] : 0u;
         bln[r] = p < len ? (bn + 1 < (uint32_t)SEG_BINS ? sm.bin[bn + 1] : len) - bst[r] : 0u;
     }
@@ -1315,7 +1320,7 @@ __global__ __launch_bounds__(SEG_BLOCK) __attribute__((amdgpu_waves_per_eu(8))) 
         if (tid == 0) {
             if (seg) lb_store(status + seg, epoch_tag | LB_INC | (prefix + tile_cnt));
             sm.prefix = prefix;
-            if (seg == SEG_COUNT - 1) *d_count = prefix + tile_cnt;
+            if (seg == nseg - 1) *d_count = prefix + tile_cnt;
             if (work && tile_cnt) atomicAdd(&work[blockIdx.x & (Ctx::PROF_WORK_SPREAD - 1)], tile_cnt);
         }
     }
@@ -1426,29 +1431,33 @@ void sort_short_runs_unique(Ctx *ctx, const uint64_t *in, uint64_t n, uint64_t *
     XH_CHECK_HIP(hipGetLastError());
 }
 
-void sort_segments(Ctx *ctx, const uint64_t *in, uint64_t n, uint64_t *out, uint64_t *d_count, uint64_t *d_long) {
+void sort_top_segments(Ctx *ctx, const uint64_t *in, uint64_t n, uint64_t *out, uint64_t *d_count, uint64_t *d_long,
+                       int gshift) {
+    XH_REQUIRE(gshift >= 0 && gshift <= 8, XLOG_HIP_INVALID_ARG, "segment sort: group shift outside [0, 8]");
     fill_u64(ctx, d_long, 0ull, 1);
     if (n == 0) {
         if (d_count) fill_u64(ctx, d_count, 0ull, 1);
         return;
     }
-    Buf<uint64_t> bounds(ctx, SEG_COUNT + 1);
-    hipLaunchKernelGGL(k_seg_bounds, dim3((SEG_COUNT + 1 + 255) / 256), dim3(256), 0, ctx->stream, in, n, bounds.p);
+    const uint32_t nseg = SEG_COUNT >> gshift;
+    Buf<uint64_t> bounds(ctx, nseg + 1);
+    hipLaunchKernelGGL(k_seg_bounds, dim3((nseg + 1 + 255) / 256), dim3(256), 0, ctx->stream, in, n, nseg, gshift,
+                       bounds.p);
     XH_CHECK_HIP(hipGetLastError());
     if (d_count) {
         uint64_t tag;
-        uint64_t *status = select_status(ctx, SEG_COUNT, &tag);
+        uint64_t *status = select_status(ctx, nseg, &tag);
         unsigned long long *tk = sort_tickets() ? ctx->tickets + 1 : nullptr;
-        const unsigned long long tb = tk ? ctx->take_tickets(1, SEG_COUNT) : 0ull;
+        const unsigned long long tb = tk ? ctx->take_tickets(1, nseg) : 0ull;
         // algorithmic bytes: every key read once, every unique key written once (counted on the device)
         Prof prof(ctx, XLOG_HIP_KERNEL_SORT_SEGMENTS, 8.0 * (double)n);
         unsigned long long *work = prof.work(8.0);
-        hipLaunchKernelGGL(k_seg_sort<true>, dim3(SEG_COUNT), dim3(SEG_BLOCK), 0, ctx->stream, in, bounds.p, out,
-                           d_count, d_long, status, tag, tk, tb, work);
+        hipLaunchKernelGGL(k_seg_sort<true>, dim3(nseg), dim3(SEG_BLOCK), 0, ctx->stream, in, bounds.p, out,
+                           d_count, d_long, status, tag, tk, tb, nseg, gshift, work);
     } else {
         Prof prof(ctx, XLOG_HIP_KERNEL_SORT_SEGMENTS, 16.0 * (double)n);  // every key read and written once
-        hipLaunchKernelGGL(k_seg_sort<false>, dim3(SEG_COUNT), dim3(SEG_BLOCK), 0, ctx->stream, in, bounds.p, out,
-                           nullptr, d_long, nullptr, 0ull, nullptr, 0ull, nullptr);
+        hipLaunchKernelGGL(k_seg_sort<false>, dim3(nseg), dim3(SEG_BLOCK), 0, ctx->stream, in, bounds.p, out,
+                           nullptr, d_long, nullptr, 0ull, nullptr, 0ull, nseg, gshift, nullptr);
     }
     XH_CHECK_HIP(hipGetLastError());
 }

@@ -649,25 +649,38 @@ static bool short_high_runs(const uint32_t *h, uint64_t n) {
 }
 
 // The segment route of a large full-key sort (keys only, at least
-// XLOG_HIP_SORT_SEG_MIN keys, default 2^26; XLOG_HIP_SORT_SEGMENTS=0 turns it
-// off, both read at each sort): two digit passes order the keys by their top
-// 16 bits and one on-chip sort per segment (sort_segments) replaces the other
-// six digits' passes.  From the histograms of digits 6 and 7: the largest
-// segment, as if the two digits were independent, is max h6 * max h7 / n; the
-// route is taken when that leaves room below the on-chip capacity (a segment
-// above it is caught by the segment pass, and the sort then runs every
-// digit's pass).
-static bool segment_route(const uint32_t *h, uint64_t n) {
+// XLOG_HIP_SORT_SEG_MIN keys, default 2^22), or of a sort of the high word
+// whose caller accepts the whole key's order: two digit passes order the keys
+// by their top 16 bits and one on-chip sort per segment (sort_top_segments)
+// replaces the other digits' passes.  A segment is the keys of 2^gshift
+// consecutive top-16-bit values, gshift the largest (at most 6) that keeps
+// segments at 4,096 keys or fewer on average (0 at 2^28 keys, 4 at 2^24, 6
+// at 2^22).  From the histograms of digits 6 and 7: the largest
+// segment, as if the two digits were independent, is max h7 * (max over
+// 2^gshift consecutive digit-6 values of their count) / n; the route is taken
+// when that leaves room below the on-chip capacity (a segment above it is
+// caught by the segment pass, and the sort then runs every digit's pass).
+// XLOG_HIP_SORT_SEGMENTS=0 turns the route off and XLOG_HIP_SORT_SEG_GSHIFT
+// fixes gshift (tests), both read at each sort.
+static bool segment_route(const uint32_t *h, uint64_t n, int *gshift) {
     const char *off = getenv("XLOG_HIP_SORT_SEGMENTS");
     if (off && off[0] == '0') return false;
     const char *e = getenv("XLOG_HIP_SORT_SEG_MIN");
-    const uint64_t min_keys = e && *e ? strtoull(e, nullptr, 10) : (1ull << 26);
+    const uint64_t min_keys = e && *e ? strtoull(e, nullptr, 10) : (1ull << 22);
     if (n < min_keys) return false;
-    uint32_t m6 = 0, m7 = 0;
-    for (int b = 0; b < 256; ++b) {
-        m6 = std::max(m6, h[6 * 256 + b]);
-        m7 = std::max(m7, h[7 * 256 + b]);
+    int g = 0;
+    while (g < 6 && (n << (g + 1)) <= 4096ull * 65536ull) ++g;
+    const char *fg = getenv("XLOG_HIP_SORT_SEG_GSHIFT");  // a fixed segment width (tests)
+    if (fg && *fg) g = std::min(6, std::max(0, atoi(fg)));
+    uint32_t m7 = 0;
+    uint64_t m6 = 0;
+    for (int b = 0; b < 256; ++b) m7 = std::max(m7, h[7 * 256 + b]);
+    for (int j = 0; j < (256 >> g); ++j) {
+        uint64_t c = 0;
+        for (int b = j << g; b < ((j + 1) << g); ++b) c += h[6 * 256 + b];
+        m6 = std::max(m6, c);
     }
+    *gshift = g;
     return (double)m6 * (double)m7 / (double)n <= 0.85 * (double)SORT_SEGMENT_MAX;
 }
 
@@ -762,7 +775,8 @@ int radix_sort_dev(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint64_t n_bo
 
 int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **vals, uint32_t **vals_alt,
                    uint64_t n, int digit_lo, int digit_hi, const uint64_t *src, uint32_t known_digits,
-                   SortUnique *uq) {
+                   SortUnique *uq, bool *whole) {
+    if (whole) *whole = false;
     if (n < 2 || digit_lo >= digit_hi) {
         if (src && n) XH_CHECK_HIP(hipMemcpyAsync(*keys, src, n * 8, hipMemcpyDeviceToDevice, ctx->stream));
         return 0;
@@ -791,6 +805,9 @@ int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **va
     // (a sort given known_digits takes exactly those passes, so it needs every digit's histogram)
     const bool hybrid_candidate =
         !has_val && !known_digits && digit_lo == 0 && digit_hi == 8 && n >= HYBRID_MIN_KEYS && sort_hybrid();
+    // a sort of the high word that may order the keys by the whole key instead (the segment route)
+    const bool word_candidate = whole && !has_val && !known_digits && digit_lo == 4 && digit_hi == 8 &&
+                                n >= HYBRID_MIN_KEYS && sort_hybrid();
     auto histograms = [&](const uint64_t *from, int dlo, int dhi) {
         Prof prof(ctx, XLOG_HIP_KERNEL_SORT_HIST, 8.0 * (double)n);  // reads every key once
         // at least 4 rounds per block: every block ends with up to 2048 device-scope atomics, which cost more
@@ -867,7 +884,7 @@ int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **va
     XH_CHECK_HIP(hipMemcpyAsync(ctx->host_scalars, hist, sizeof(h_hist), hipMemcpyDeviceToHost, ctx->stream));
     XH_CHECK_HIP(hipEventRecord(ctx->ev_read, ctx->stream));
     int first = digit_lo;
-    if (digit_hi - digit_lo >= 2 && !hybrid_candidate) launch_pass(first++);
+    if (digit_hi - digit_lo >= 2 && !hybrid_candidate && !word_candidate) launch_pass(first++);
     ctx->wait_event(ctx->ev_read);
     memcpy(h_hist, ctx->host_scalars, sizeof(h_hist));
     auto trivial = [&](int dgt) {
@@ -883,12 +900,14 @@ int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **va
         ctx->wait_event(ctx->ev_read);
         memcpy(h_hist, ctx->host_scalars, sizeof(h_hist));
     };
-    if (hybrid_candidate && segment_route(h_hist, n)) {
-        // Digits 6 and 7, then every segment of equal top 16 bits sorted on chip.
+    int gshift = 0;
+    if ((hybrid_candidate || word_candidate) && segment_route(h_hist, n, &gshift)) {
+        // The top two digits, then every segment sorted on chip.
         for (int dgt = 6; dgt < 8; ++dgt)
             if (!trivial(dgt)) launch_pass(dgt);
         Buf<uint64_t> flags(ctx, 2);  // unique count (with uq), long segment or run
-        sort_segments(ctx, (passes == 0 && src) ? src : *keys, n, *keys_alt, uq ? flags.p : nullptr, flags.p + 1);
+        sort_top_segments(ctx, (passes == 0 && src) ? src : *keys, n, *keys_alt, uq ? flags.p : nullptr,
+                          flags.p + 1, gshift);
         ctx->read_scalars(flags.p, 2);
         if (ctx->host_scalars[1] == 0) {
             if (uq) {
@@ -896,10 +915,17 @@ int radix_sort_u64(Ctx *ctx, uint64_t **keys, uint64_t **keys_alt, uint32_t **va
                 uq->count = ctx->host_scalars[0];
             }
             std::swap(*keys, *keys_alt);
+            if (whole) *whole = true;
             return passes + 1;
         }
         // a segment above the on-chip capacity or a long run of unequal keys:
-        // every digit's pass, from the keys as they are (any order sorts alike)
+        // every digit's pass of the sort, from the keys as they are (any order
+        // sorts alike)
+        if (word_candidate) {
+            for (int dgt = 4; dgt < 8; ++dgt)
+                if (!trivial(dgt)) launch_pass(dgt);
+            return passes;
+        }
         low_word_histograms((passes == 0 && src) ? src : *keys);
         for (int dgt = 0; dgt < 8; ++dgt)
             if (!trivial(dgt)) launch_pass(dgt);
