@@ -20,7 +20,7 @@ BUILD = ROOT / "_build" / "xlog_amd"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 HIP_SOURCES = ["sort.hip", "select.hip", "join.hip", "tc_bitmap.hip", "chain_bitmap.hip", "hash_set.hip", "arrow_ipc.cpp",
-               "abi.hip"]
+               "abi.hip", "fixpoint.hip"]
 HIP_FLAGS = [
     "--offload-arch=gfx950",
     "-O3",
