@@ -1116,7 +1116,7 @@ __global__ void k_seg_bounds(const uint64_t *__restrict__ keys, uint64_t n, uint
 }
 
 struct SegSmem {
-    uint32_t hi[SEG_MAX], lo[SEG_MAX];  // the segment's keys (high and low words) at their place
+    uint64_t key[SEG_MAX];              // the segment's keys at their place
     uint32_t bin[SEG_BINS];             // key counts, then the bins' starts
     uint8_t uf[SEG_MAX];                // 1 at the place of the first of every group of equal keys
     uint32_t wsum[SEG_WAVES];
@@ -1204,8 +1204,7 @@ __global__ __launch_bounds__(SEG_BLOCK) __attribute__((amdgpu_waves_per_eu(8))) 
         place[r] = 0u;
         if (p < len) {
             place[r] = sm.bin[(uint32_t)(k[r] >> bin_shift) & (SEG_BINS - 1)] + slot[r];
-            sm.hi[place[r]] = (uint32_t)(k[r] >> 32);
-            sm.lo[place[r]] = (uint32_t)k[r];
+            sm.key[place[r]] = k[r];
         }
     }
     __syncthreads();
@@ -1234,7 +1233,7 @@ __global__ __launch_bounds__(SEG_BLOCK) __attribute__((amdgpu_waves_per_eu(8))) 
         if (ln > (uint32_t)SEG_RUN_MAX) {
             // a long bin is left as it is when all its keys are equal (any
             // order is sorted); the key at its start stands for them
-            if ((((uint64_t)sm.hi[st] << 32) | sm.lo[st]) != k[r]) longr = true;
+            if (sm.key[st] != k[r]) longr = true;
             else if (place[r] == st) uniq |= 1u << r;
             continue;
         }
@@ -1244,7 +1243,7 @@ __global__ __launch_bounds__(SEG_BLOCK) __attribute__((amdgpu_waves_per_eu(8))) 
 #pragma unroll
         for (int u = 0; u < SEG_RANK_BATCH; ++u) {
             const uint32_t j = st + ((uint32_t)u < ln ? (uint32_t)u : ln - 1);
-            kj[u] = ((uint64_t)sm.hi[j] << 32) | sm.lo[j];
+            kj[u] = sm.key[j];
         }
 #pragma unroll
         for (int u = 0; u < SEG_RANK_BATCH; ++u) {
@@ -1253,7 +1252,7 @@ __global__ __launch_bounds__(SEG_BLOCK) __attribute__((amdgpu_waves_per_eu(8))) 
             eq_before |= in && kj[u] == k[r] && before;
         }
         for (uint32_t j = st + SEG_RANK_BATCH; j < st + ln; ++j) {
-            const uint64_t x = ((uint64_t)sm.hi[j] << 32) | sm.lo[j];
+            const uint64_t x = sm.key[j];
             rk += (x < k[r] || (x == k[r] && j < place[r])) ? 1u : 0u;
             eq_before |= x == k[r] && j < place[r];
         }
@@ -1289,15 +1288,14 @@ __global__ __launch_bounds__(SEG_BLOCK) __attribute__((amdgpu_waves_per_eu(8))) 
             const uint32_t p = (uint32_t)(tid + r * SEG_BLOCK);
             if (UNIQUE && p < len) sm.uf[place[r]] = (uint8_t)((uniq >> r) & 1u);
             if (!((moved >> r) & 1u)) continue;
-            sm.hi[place[r]] = (uint32_t)(k[r] >> 32);
-            sm.lo[place[r]] = (uint32_t)k[r];
+            sm.key[place[r]] = k[r];
         }
     }
     __syncthreads();
     const uint32_t wbase = (uint32_t)wave * (SEG_ITEMS * WAVE);
     const uint32_t n_out = bad ? 0u : len;
     if (!UNIQUE) {
-        for (uint32_t i = tid; i < n_out; i += SEG_BLOCK) out[a + i] = ((uint64_t)sm.hi[i] << 32) | sm.lo[i];
+        for (uint32_t i = tid; i < n_out; i += SEG_BLOCK) out[a + i] = sm.key[i];
         return;
     }
     // the unique keys in place order, counted per wave over consecutive places
@@ -1333,7 +1331,7 @@ __global__ __launch_bounds__(SEG_BLOCK) __attribute__((amdgpu_waves_per_eu(8))) 
         const uint64_t m = __ballot(f);
         if (f) {
             const uint32_t i = wbase + (uint32_t)(r * WAVE + lane);
-            out[pos + (uint64_t)__popcll(m & lt_mask)] = ((uint64_t)sm.hi[i] << 32) | sm.lo[i];
+            out[pos + (uint64_t)__popcll(m & lt_mask)] = sm.key[i];
         }
         pos += (uint64_t)__popcll(m);
     }
