@@ -1070,23 +1070,25 @@ __global__ __launch_bounds__(SRU_BLOCK) void k_short_runs_unique(const uint64_t 
     }
 }
 
-// Segment sort of a large full-key sort whose keys two digit passes have
-// ordered by their top 16 bits: the keys of one top-16-bit value (a segment,
-// about n / 65,536 keys of uniform input) are sorted by the rest of the key on
-// chip, one block per segment.  This is the hybrid radix sort of Stehle and
-// Jacobsen ("A Memory Bandwidth-Efficient Hybrid Radix Sort on GPUs", SIGMOD
-// 2017): global digit passes until every bucket fits on chip, then one on-chip
-// sort per bucket.  The sort is of whole keys only, so equal keys need no
-// stable order, and one counting pass places the segment: each key takes a
-// slot of its bin of bits 36..47 by an LDS atomic (4,096 bins, about one key
-// each for uniform keys), the bins' starts come from a block scan, and every
-// key is then ranked inside its bin by the whole key (the bin is the run of
-// keys that share bits 36..63).  The segment is written at its place (sort), or
-// its unique keys at an offset from decoupled look-back over the segments'
-// counts (sort + unique).  A segment of more than SEG_MAX keys, or a bin of
-// more than SEG_RUN_MAX keys that are not all equal, raises *long_run: the
-// block then counts zero and writes nothing, and the caller sorts the keys by
-// every digit instead.
+// Segment sort of a large keys-only sort whose keys two digit passes have
+// ordered by their top 16 bits: a segment is the keys of 2^gshift consecutive
+// top-16-bit values (gshift chosen by the caller for about 4,096 keys per
+// segment of uniform input), and every segment is sorted by the rest of the key
+// on chip, one 1024-thread block per segment (two per CU).  This is the hybrid
+// radix sort of Stehle and Jacobsen ("A Memory Bandwidth-Efficient Hybrid
+// Radix Sort on GPUs", SIGMOD 2017): global digit passes until every bucket
+// fits on chip, then one on-chip sort per bucket.  The sort is of whole keys
+// only, so equal keys need no stable order, and one counting pass places the
+// segment: each key takes a slot of its bin of the 12 bits below the segment's
+// (bits 36 + gshift .. 47 + gshift, 4,096 bins, about one key each for uniform
+// keys) by an LDS atomic, the bins' starts come from a block scan, and every
+// key is then ranked inside its bin by the whole key (a bin is the run of keys
+// that agree from bit 36 + gshift up).  The segment is written at its place
+// (sort), or its unique keys at an offset from decoupled look-back over the
+// segments' counts (sort + unique).  A segment of more than SEG_MAX keys, or a
+// bin of more than SEG_RUN_MAX keys that are not all equal, raises *long_run:
+// the block then counts zero and writes nothing, and the caller sorts the keys
+// by every digit instead.
 constexpr int SEG_BLOCK = 1024, SEG_ITEMS = 5, SEG_MAX = SEG_BLOCK * SEG_ITEMS, SEG_RUN_MAX = 256, SEG_RANK_BATCH = 4;
 constexpr int SEG_WAVES = SEG_BLOCK / WAVE;
 constexpr int SEG_BIN_BITS = 12, SEG_BINS = 1 << SEG_BIN_BITS;
